@@ -1,0 +1,299 @@
+#!/usr/bin/env python3
+"""Benchmark of the gemma4 decode hot path on one MI355X.
+
+Workload (one "step" = one decoded token at batch 1): 35 Gemma-4-E2B-shaped
+decoder layers (hidden 1536; Q4_K q 2048x1536, k/v 256x1536, o 1536x2048,
+gate/up 6144x1536; Q6_K down 1536x6144; 8 query / 1 KV head of dim 256;
+layers 4,9,...,34 global, the rest with a 512-token window), then the tied
+Q6_K LM head [262144 x 1536], softcap 30 and argmax. Weights are seeded
+synthetic data generated on the device; the KV cache is pre-filled with
+N(0,1) f16 rows up to the start position. The fused step is captured once as
+a HIP graph and replayed; each replay advances the device-side position.
+
+Prints one JSON line. `value` is decoded tokens/s; `roofline` describes the
+kernel with the largest share of a step, timed with HIP events on the
+library's stream; `cpu_baseline` times the CPU oracle on a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gemma4-webgpu_amd"))
+
+import numpy as np  # noqa: E402
+
+import g4hip  # noqa: E402
+from g4hip.decoder import Decoder, E2BShape  # noqa: E402
+
+METRIC = "Q4_K GEMV GB/s (% of 8 TB/s peak); E2B decode tok/s at B=1 and B=32"
+HBM_PEAK_GBPS = 8000.0
+START_POS = 512
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_launches(ctx, fn, iters):
+    """Average ms per call of fn() (enqueue-only work) over `iters` calls."""
+    fn()
+    ctx.sync()
+    a = ctx.record()
+    for i in range(iters):
+        fn(i)
+    b = ctx.record()
+    ms = ctx.elapsed_ms(a, b)
+    ctx.destroy_event(a)
+    ctx.destroy_event(b)
+    return ms / iters
+
+
+def kernel_census(ctx, dec: Decoder, reps: int):
+    """Per-launch time of each fused kernel kind, each run over all layers
+    (so weights rotate through HBM as in a real step)."""
+    s, c = dec.s, ctx
+    dec.set_position(START_POS)
+    Ls = dec.layers
+    nl = len(Ls)
+
+    def over_layers(body):
+        def run(_i=0):
+            for il, L in enumerate(Ls):
+                body(il, L)
+        return run
+
+    kinds = {}
+
+    def qkv(il, L):
+        c.rmsNormMatmul_q4k(dec.hidden, L.attn_norm, L.wq, dec.q, s.q_dim, s.hidden, s.eps)
+        c.rmsNormMatmul_q4k(dec.hidden, L.attn_norm, L.wk, dec.k, s.kv_dim, s.hidden, s.eps)
+        c.rmsNormMatmul_q4k(dec.hidden, L.attn_norm, L.wv, dec.v, s.kv_dim, s.hidden, s.eps)
+    kinds["qkv_matvec(x3)"] = (qkv, 3, (s.q_dim + 2 * s.kv_dim) * s.hidden // 256 * 144)
+
+    def attn(il, L):
+        w = 0 if s.is_global(il) else s.window
+        c.attnDecode(dec.q, L.k_cache, L.v_cache, dec.attn, s.n_q_heads, s.n_kv_heads, s.head_dim, dec.max_seq, 1.0,
+                     w, workspace=dec.attn_ws, position_dev=dec.pos)
+    n_glob = sum(1 for il in range(nl) if s.is_global(il))
+    kv_bytes = ((nl - n_glob) * min(START_POS + 1, s.window) + n_glob * (START_POS + 1)) * s.kv_dim * 2 * 2 // nl
+    kinds["attn_decode(+combine)"] = (attn, 2, kv_bytes)
+
+    def oproj(il, L):
+        c.matmulQuant(dec.attn, L.wo, dec.o, s.hidden, s.q_dim)
+    kinds["o_matvec"] = (oproj, 1, s.hidden * s.q_dim // 256 * 144)
+
+    def gateup(il, L):
+        c.normAddGateUpGelu_q4k(dec.o, L.post_attn_norm, dec.hidden, L.pre_ffn_norm, L.wgate, L.wup, dec.hidden2,
+                                dec.act, s.ffn, s.hidden, s.eps)
+    kinds["gateup_gelu"] = (gateup, 1, 2 * s.ffn * s.hidden // 256 * 144 + 4 * s.hidden * 4 + s.ffn * 4)
+
+    def down(il, L):
+        c.matmulQuant(dec.act, L.wdown, dec.down, s.hidden, s.ffn, "q6k")
+    kinds["down_matvec_q6k"] = (down, 1, s.hidden * s.ffn // 256 * 210 + s.ffn * 4 + s.hidden * 4)
+
+    def small(il, L):
+        c.perHeadRmsNormNoWeight(dec.v, s.n_kv_heads, s.head_dim, s.eps)
+        c.fusedPerHeadNormRope(dec.q, L.q_norm, s.n_q_heads, s.head_dim, s.eps, 0, 1e4, 0, dec.rope_freqs,
+                               position_dev=dec.pos)
+        c.fusedPerHeadNormRope(dec.k, L.k_norm, s.n_kv_heads, s.head_dim, s.eps, 0, 1e4, 0, dec.rope_freqs,
+                               position_dev=dec.pos)
+        c.kvCacheStore(dec.k, dec.v, L.k_cache, L.v_cache, s.n_kv_heads, s.head_dim, 0, dec.max_seq,
+                       position_dev=dec.pos)
+        c.fusedNormAdd(dec.down, L.post_ffn_norm, dec.hidden2, dec.hidden, s.hidden, s.eps)
+    kinds["small(vnorm,rope x2,kvstore,normadd)"] = (small, 5, 0)
+
+    out = {}
+    for name, (body, launches, bytes_per_layer) in kinds.items():
+        ms = time_launches(ctx, over_layers(body), reps) / nl
+        out[name] = {"us_per_layer": ms * 1e3, "launches_per_layer": launches,
+                     "bytes_per_layer": bytes_per_layer,
+                     "gbps": (bytes_per_layer / (ms * 1e-3) / 1e9) if bytes_per_layer else None}
+    # LM head (330 MB: larger than the 256 MB last-level cache, no rotation needed)
+    lm_bytes = s.lm_head_bytes() + s.hidden * 4 + s.vocab * 4
+
+    def head(_i=0):
+        c.matmulQuant(dec.normed, dec.lm_head, dec.logits, s.vocab, s.hidden, "q6k")
+    ms = time_launches(ctx, head, max(3, reps))
+    out["lm_head_q6k"] = {"us_per_layer": None, "us": ms * 1e3, "launches_per_layer": 0, "bytes": lm_bytes,
+                          "gbps": lm_bytes / (ms * 1e-3) / 1e9}
+    return out
+
+
+def gemv_cfg0(ctx, copies=101, rounds=5):
+    """Config-0 GEMV: W [6144 x 1536] Q4_K, x f32[1536], y f32[6144]; weights
+    rotated over `copies` buffers (> 2x the 256 MB last-level cache)."""
+    M, N = 6144, 1536
+    nb = M * N // 256
+    wb = nb * 144
+    W = ctx.alloc(wb * copies)
+    ctx.fill_q4k(W, nb * copies, 12345)
+    x = ctx.empty(N, np.float32)
+    ctx.fill_normal_f32(x, N, 1, 0.0, 1.0)
+    y = ctx.empty(M, np.float32)
+    ptrs = [W.ptr + i * wb for i in range(copies)]
+
+    def one(i=0):
+        ctx.matmulQuant(x, ptrs[i % copies], y, M, N, "q4k")
+    ms = time_launches(ctx, one, copies * rounds)
+    alg = wb + N * 4 + M * 4
+    W.free()
+    return {"shape": [M, N], "us": ms * 1e3, "bytes": alg, "gbps": alg / (ms * 1e-3) / 1e9,
+            "frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, "copies": copies}
+
+
+def cpu_baseline(layers_sample=2, head_rows=8192):
+    """Times the CPU oracle (1 thread, f64 accumulation) on a bounded sample
+    of the same step: `layers_sample` full layers at the same context plus
+    `head_rows` rows of the LM head, scaled to one token."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    s = E2BShape()
+    H, Q, KV, I = s.hidden, s.q_dim, s.kv_dim, s.ffn
+    rng_seed = 7
+    Wq, Wk, Wv = O.gen_q4k(1, Q * H // 256), O.gen_q4k(2, KV * H // 256), O.gen_q4k(3, KV * H // 256)
+    Wo, Wg, Wu = O.gen_q4k(4, H * Q // 256), O.gen_q4k(5, I * H // 256), O.gen_q4k(6, I * H // 256)
+    Wd = O.gen_q6k(rng_seed, H * I // 256)
+    nw = O.gen_normal_f16(8, H, 1.0, 0.1)
+    hw = O.gen_normal_f16(9, s.head_dim, 1.0, 0.1)
+    L = START_POS + 1
+    kc = O.gen_normal_f16(10, (L + 1) * KV)
+    vc = O.gen_normal_f16(11, (L + 1) * KV)
+    table = np.ones(s.head_dim // 2, np.float16).view(np.uint16)
+    x = O.gen_normal_f32(12, H)
+    t0 = time.perf_counter()
+    for il in range(layers_sample):
+        n = O.rms_norm(x, nw)
+        q = O.matmul(n, Wq, Q, H, "q4k")
+        k = O.matmul(n, Wk, KV, H, "q4k")
+        v = O.per_head_rms_norm_no_weight(O.matmul(n, Wv, KV, H, "q4k"), 1, s.head_dim)
+        q = O.fused_per_head_norm_rope(q, hw, s.n_q_heads, s.head_dim, 1e-6, START_POS, 1e4, 0, table)
+        k = O.fused_per_head_norm_rope(k, hw, 1, s.head_dim, 1e-6, START_POS, 1e4, 0, table)
+        O.kv_cache_store_f16(k, v, kc, vc, 1, s.head_dim, START_POS)
+        a = O.attention(q, kc, vc, s.n_q_heads, 1, s.head_dim, L, 1.0, s.window if il % 5 != 4 else 0)
+        o = O.matmul(a, Wo, H, Q, "q4k")
+        h = O.fused_norm_add(o, nw, x)
+        n2 = O.rms_norm(h, nw)
+        act = O.gelu_mul(O.matmul(n2, Wg, I, H, "q4k"), O.matmul(n2, Wu, I, H, "q4k"))
+        x = O.fused_norm_add(O.matmul(act, Wd, H, I, "q6k"), nw, h)
+    t_layers = time.perf_counter() - t0
+    Wh = O.gen_q6k(13, head_rows * H // 256)
+    t0 = time.perf_counter()
+    lg = O.logit_softcap(O.matmul(O.rms_norm(x, nw), Wh, head_rows, H, "q6k"))
+    O.argmax(lg)
+    t_head = time.perf_counter() - t0
+    per_token = t_layers / layers_sample * s.n_layers + t_head * (s.vocab / head_rows)
+    return {"value": 1.0 / per_token, "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": (f"CPU oracle (C, 1 thread, f64 accumulation): {layers_sample} E2B-shaped layers at "
+                       f"context {START_POS + 1} + {head_rows}/{s.vocab} LM-head rows, "
+                       f"{t_layers + t_head:.1f} s of CPU work, scaled to one token "
+                       f"(35 layers + full LM head)")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--census-reps", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-layers", type=int, default=3)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
+              "the multi-GPU layout is described, not built", file=sys.stderr)
+        sys.exit(2)
+    if int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py runs as a single process on one GPU", file=sys.stderr)
+        sys.exit(2)
+
+    ctx = g4hip.Context(0)
+    info = ctx.info()
+    log(f"device {info}")
+    s = E2BShape()
+    max_seq = START_POS + args.warmup + args.steps + 64
+    max_seq = (max_seq + 255) // 256 * 256
+    t0 = time.time()
+    dec = Decoder(ctx, s, max_seq=max_seq, seed=0)
+    dec.fill_kv(START_POS, seed=1)
+    dec.set_position(START_POS)
+    ctx.sync()
+    log(f"weights + KV ready in {time.time() - t0:.1f}s "
+        f"({(s.layer_weight_bytes() * s.n_layers + s.lm_head_bytes()) / 1e9:.3f} GB of weights)")
+
+    graph = dec.capture_fused("argmax")
+    for _ in range(args.warmup):
+        ctx.graph_launch(graph)
+    ctx.sync()
+    log(f"warmup {args.warmup} steps done")
+    a = ctx.record()
+    for _ in range(args.steps):
+        ctx.graph_launch(graph)
+    b = ctx.record()
+    ms_total = ctx.elapsed_ms(a, b)
+    ctx.sync()
+    ms_step = ms_total / args.steps
+    tok_s = 1000.0 / ms_step
+    pos_end = int(dec.pos.download(np.uint32)[0])
+    log(f"decode: {ms_step * 1e3:.1f} us/token = {tok_s:.1f} tok/s (positions {START_POS}..{pos_end})")
+    ctx.graph_destroy(graph)
+
+    census = kernel_census(ctx, dec, args.census_reps)
+    for k, v in census.items():
+        log(f"  {k}: {v}")
+    # dominant kernel = largest time per step
+    per_step = {k: (v["us"] if k == "lm_head_q6k" else v["us_per_layer"] * s.n_layers)
+                for k, v in census.items()}
+    dom = max((k for k in per_step if census[k].get("gbps")), key=lambda k: per_step[k])
+    dv = census[dom]
+    if dom == "lm_head_q6k":
+        bytes_launch, us_launch = dv["bytes"], dv["us"]
+    else:
+        bytes_launch, us_launch = dv["bytes_per_layer"], dv["us_per_layer"]
+    achieved = bytes_launch / (us_launch * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                "bytes_per_launch": bytes_launch, "us_per_launch": round(us_launch, 3)}
+
+    g0 = gemv_cfg0(ctx)
+    log(f"config-0 Q4_K GEMV: {g0}")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(layers_sample=args.cpu_layers)
+        log(f"cpu baseline: {cpu}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k/q6_k weights x int8 activation digits (i32 dot), f32 accumulate, f16 KV",
+        "data": "synthetic (seeded SplitMix64 weights generated on the device, N(0,1) f16 KV)",
+        "config": {"workload": "E2B decode B=1: 35 E2B-shaped layers (Q4_K q/k/v/o/gate/up, Q6_K down, "
+                               "H=1536, 8 q heads / 1 kv head x 256, I=6144, local window 512 / 7 global) "
+                               "+ tied Q6_K LM head 262144x1536 + softcap + argmax, one HIP-graph replay per "
+                               "token",
+                   "batch": 1, "start_position": START_POS, "positions": [START_POS, pos_end],
+                   "launches_per_token": dec.launches_per_step_fused()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "q4k_gemv_config0": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in g0.items()},
+        "kernel_census_us": {k: round(per_step[k], 2) for k in per_step},
+        "device": info["name"],
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,130 @@
+// g4_internal.hpp — shared host/device helpers of libg4hip (not installed).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "g4hip.h"
+
+struct g4_ctx {
+  int device = 0;
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;  // the stream every entry point enqueues on
+  bool lost = false;
+  int num_cus = 0;
+  size_t hbm_bytes = 0;
+  char name[128] = {0};
+  bool capturing = false;
+  // Small device buffer for the partials of two-stage reductions (argmax,
+  // topk256), allocated once at g4_init so that no entry point allocates.
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
+};
+
+// Returns the context scratch buffer if it holds `bytes`.
+int g4_internal_scratch(g4_ctx* ctx, size_t bytes, void** out);
+
+struct g4_event {
+  hipEvent_t ev = nullptr;
+  int device = 0;
+};
+
+struct g4_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+namespace g4 {
+
+// Thread-local message of the last failure (g4_last_error).
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Maps a HIP status to a g4 status; a device fault marks the context lost.
+int hip_fail(g4_ctx* ctx, hipError_t e, const char* what);
+// Common prologue of every entry point: null / lost checks, set the device.
+int enter(g4_ctx* ctx, const char* fn);
+// Checks the launch that was just enqueued.
+int check_launch(g4_ctx* ctx, const char* kernel);
+
+}  // namespace g4
+
+#define G4_ENTER(ctx)                              \
+  do {                                             \
+    int _rc = g4::enter((ctx), __func__);          \
+    if (_rc != G4_OK) return _rc;                  \
+  } while (0)
+
+#define G4_REQUIRE(cond, ...)                                      \
+  do {                                                             \
+    if (!(cond)) return g4::set_error(G4_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+#define G4_HIP(ctx, call)                                    \
+  do {                                                       \
+    hipError_t _e = (call);                                  \
+    if (_e != hipSuccess) return g4::hip_fail((ctx), _e, #call); \
+  } while (0)
+
+#define G4_LAUNCHED(ctx, name)                      \
+  do {                                              \
+    int _rc = g4::check_launch((ctx), (name));      \
+    if (_rc != G4_OK) return _rc;                   \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+
+namespace g4d {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
+  return (float)v;
+}
+
+// Round to nearest even f32 -> f16 bits (the hardware conversion).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Block-wide sum for blockDim.x == 64 * nwaves; `red` holds >= nwaves floats.
+// Every thread gets the total. Contains __syncthreads.
+template <int NWAVES>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < NWAVES; ++i) t += red[i];
+  __syncthreads();
+  return t;
+}
+
+// Counter-based SplitMix64 (same definition as the host g4_splitmix64).
+__host__ __device__ __forceinline__ uint64_t splitmix64(uint64_t seed, uint64_t idx) {
+  uint64_t z = seed + (idx + 1) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+}  // namespace g4d
+
+inline unsigned ceil_div(uint64_t a, uint64_t b) { return (unsigned)((a + b - 1) / b); }

@@ -1,0 +1,571 @@
+// k_elem.hip — norms, RoPE, activations, KV store, sampling, dequant and the
+// seeded synthetic-input generators.
+#include <math.h>
+
+#include "g4_internal.hpp"
+
+namespace {
+
+constexpr int NT = 256;
+
+// ---------------------------------------------------------------------------
+// norms (shaders/rms_norm.wgsl, fused_norm_add.wgsl,
+// per_head_rms_norm_no_weight.wgsl)
+// ---------------------------------------------------------------------------
+
+// out = [residual +] in * w / sqrt(mean(in^2) + eps); one workgroup.
+template <bool ADD>
+__global__ __launch_bounds__(1024) void rms_norm_kernel(const float* in, const uint16_t* w,
+                                                        const float* residual, float* out,
+                                                        uint32_t n, float eps) {
+  __shared__ float red[16];
+  float ss = 0.f;
+  for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+    const float v = in[i];
+    ss += v * v;
+  }
+  ss = g4d::wave_sum(ss);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if (lane == 0) red[wv] = ss;
+  __syncthreads();
+  float tot = 0.f;
+  for (int i = 0; i < nw; ++i) tot += red[i];
+  const float inv = 1.0f / sqrtf(tot / (float)n + eps);
+  for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+    float v = in[i] * g4d::f16_bits_to_f32(w[i]) * inv;
+    if (ADD) v = residual[i] + v;
+    out[i] = v;
+  }
+}
+
+// Per-head norm (+ weight) then rotate-half RoPE over pairs (i, i+HD/2);
+// one workgroup per head (shaders/fused_per_head_norm_rope.wgsl:21-63).
+// MODE 0: weightless norm only (v_norm). MODE 1: weighted norm + RoPE.
+template <int MODE>
+__global__ __launch_bounds__(NT) void head_norm_kernel(float* data, const uint16_t* weight, uint32_t num_heads,
+                                                       uint32_t hd, float eps, uint32_t position,
+                                                       const uint32_t* position_dev, float theta,
+                                                       uint32_t apply_divisor, const uint16_t* rope_freqs) {
+  __shared__ float red[4];
+  __shared__ float x[512];
+  const uint32_t head = blockIdx.x;
+  if (head >= num_heads) return;
+  float* v = data + (size_t)head * hd;
+  float ss = 0.f;
+  for (uint32_t i = threadIdx.x; i < hd; i += NT) {
+    const float t = v[i];
+    x[i] = t;
+    ss += t * t;
+  }
+  ss = g4d::block_sum<4>(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+  if (MODE == 0) {
+    for (uint32_t i = threadIdx.x; i < hd; i += NT) v[i] = x[i] * inv;
+    return;
+  }
+  for (uint32_t i = threadIdx.x; i < hd; i += NT) x[i] = x[i] * g4d::f16_bits_to_f32(weight[i]) * inv;
+  __syncthreads();
+  const uint32_t pos = position_dev ? *position_dev : position;
+  const uint32_t half = hd / 2;
+  for (uint32_t i = threadIdx.x; i < half; i += NT) {
+    // f32 frequency and angle exactly as the shader forms them; cos/sin of
+    // that f32 angle are evaluated in double and rounded once.
+    float f = (float)(1.0 / pow((double)theta, (double)(2u * i) / (double)hd));
+    if (apply_divisor) f = f / g4d::f16_bits_to_f32(rope_freqs[i]);
+    const float angle = (float)pos * f;
+    const float c = (float)cos((double)angle), s = (float)sin((double)angle);
+    const float x0 = x[i], x1 = x[i + half];
+    v[i] = x0 * c - x1 * s;
+    v[i + half] = x0 * s + x1 * c;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// activations (shaders/gelu_mul.wgsl, logit_softcap.wgsl)
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(NT) void gelu_mul_kernel(const float* gate, const float* up, float* out, uint32_t n) {
+  const uint32_t i = blockIdx.x * NT + threadIdx.x;
+  if (i >= n) return;
+  const float x = gate[i];
+  float t = 0.7978845608028654f * x * (1.0f + 0.044715f * x * x);
+  t = fminf(fmaxf(t, -15.0f), 15.0f);
+  out[i] = 0.5f * x * (1.0f + tanhf(t)) * up[i];
+}
+
+__global__ void advance_kernel(uint32_t* p, uint32_t delta) {
+  if (threadIdx.x == 0) p[0] += delta;
+}
+
+__global__ __launch_bounds__(NT) void softcap_kernel(float* logits, uint32_t n, float cap) {
+  const uint32_t i = blockIdx.x * NT + threadIdx.x;
+  if (i >= n) return;
+  float x = logits[i] / cap;
+  x = fminf(fmaxf(x, -15.0f), 15.0f);
+  logits[i] = tanhf(x) * cap;
+}
+
+// ---------------------------------------------------------------------------
+// KV cache store (shaders/kv_cache_store.wgsl:9-17), f16 rows
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(NT) void kv_store_kernel(const float* k_in, const float* v_in, uint16_t* kc,
+                                                      uint16_t* vc, uint32_t total, uint32_t position,
+                                                      const uint32_t* position_dev, uint32_t max_seq) {
+  const uint32_t i = blockIdx.x * NT + threadIdx.x;
+  if (i >= total) return;
+  const uint32_t pos = position_dev ? *position_dev : position;
+  if (pos >= max_seq) return;  // a row past the cache is dropped, never written out of bounds
+  const size_t idx = (size_t)pos * total + i;
+  kc[idx] = g4d::f32_to_f16_bits(k_in[i]);
+  vc[idx] = g4d::f32_to_f16_bits(v_in[i]);
+}
+
+// ---------------------------------------------------------------------------
+// argmax / topk256 (shaders/argmax.wgsl, topk256.wgsl)
+// ---------------------------------------------------------------------------
+// The reference keeps, per residue class c = i mod 256, the first strict '>'
+// maximum (init -1e30, index 0), then merges slot t with slot t + stride for
+// stride = 128, 64, ..., 1, keeping the lower slot on equal values. The last
+// merge (slot 0 vs 1) therefore prefers an even class, the one before it a
+// class with bit 1 clear, and so on: among equal maxima the class with the
+// smallest bit-reversed 8-bit id wins, then the lowest index. NaN and values
+// <= -1e30 never win; with no candidate the answer is 0. `better` encodes
+// exactly that order, so any partition of the index range reduces to the same
+// answer.
+struct Cand {
+  float v;
+  uint32_t i;
+};
+
+__device__ __forceinline__ bool better(const Cand& a, const Cand& b) {
+  if (a.v > b.v) return true;
+  if (a.v < b.v || !(a.v == b.v)) return false;
+  const uint32_t ra = __brev(a.i & 255u), rb = __brev(b.i & 255u);
+  if (ra != rb) return ra < rb;
+  return a.i < b.i;
+}
+
+__device__ __forceinline__ Cand wave_best(Cand c) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    Cand d;
+    d.v = __shfl_xor(c.v, o, 64);
+    d.i = __shfl_xor(c.i, o, 64);
+    if (better(d, c)) c = d;
+  }
+  return c;
+}
+
+constexpr int kArgmaxBlocks = 256;
+
+// stage 1: workgroup b scans a contiguous chunk
+__global__ __launch_bounds__(NT) void argmax_partial(const float* logits, uint32_t n, Cand* part) {
+  __shared__ Cand sm[4];
+  const uint32_t chunk = (n + gridDim.x - 1) / gridDim.x;
+  const uint32_t lo = blockIdx.x * chunk;
+  const uint32_t hi = min(n, lo + chunk);
+  Cand c{-1e30f, 0u};
+  for (uint32_t i = lo + threadIdx.x; i < hi; i += NT) {
+    const Cand d{logits[i], i};
+    if (better(d, c)) c = d;
+  }
+  c = wave_best(c);
+  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    Cand b = sm[0];
+    for (int k = 1; k < 4; ++k)
+      if (better(sm[k], b)) b = sm[k];
+    part[blockIdx.x] = b;
+  }
+}
+
+// stage 2: one workgroup reduces the partials; the initial candidate
+// (-1e30, 0) mirrors the reference's default result.
+__global__ __launch_bounds__(NT) void argmax_final(const Cand* part, int nparts, uint32_t* result) {
+  __shared__ Cand sm[4];
+  Cand c{-1e30f, 0u};
+  for (int i = threadIdx.x; i < nparts; i += NT)
+    if (better(part[i], c)) c = part[i];
+  c = wave_best(c);
+  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    Cand b = sm[0];
+    for (int k = 1; k < 4; ++k)
+      if (better(sm[k], b)) b = sm[k];
+    // a candidate that never beat the -1e30 initial value leaves index 0
+    result[0] = (b.v > -1e30f) ? b.i : 0u;
+  }
+}
+
+// topk256: residue class t of a slab of rows (row r = indices [256r, 256r+256)).
+// Within a class the first strict maximum wins, so slabs are merged in
+// ascending order with a strict '>' (shaders/topk256.wgsl:12-18).
+constexpr int kTopkSlabs = 128;
+
+__global__ __launch_bounds__(NT) void topk_partial(const float* logits, uint32_t n, float2* part) {
+  const uint32_t t = threadIdx.x;
+  const uint32_t rows = (n + 255) / 256;
+  const uint32_t per = (rows + gridDim.x - 1) / gridDim.x;
+  const uint32_t r0 = blockIdx.x * per, r1 = min(rows, r0 + per);
+  float mx = -1e30f;
+  uint32_t idx = 0;
+  for (uint32_t r = r0; r < r1; ++r) {
+    const uint32_t i = r * 256 + t;
+    if (i < n) {
+      const float v = logits[i];
+      if (v > mx) {
+        mx = v;
+        idx = i;
+      }
+    }
+  }
+  part[(size_t)blockIdx.x * 256 + t] = make_float2(mx, __uint_as_float(idx));
+}
+
+__global__ __launch_bounds__(NT) void topk_final(const float2* part, int nparts, float* result) {
+  const uint32_t t = threadIdx.x;
+  float mx = -1e30f;
+  uint32_t idx = 0;
+  for (int s = 0; s < nparts; ++s) {
+    const float2 p = part[(size_t)s * 256 + t];
+    if (p.x > mx) {
+      mx = p.x;
+      idx = __float_as_uint(p.y);
+    }
+  }
+  result[2 * t] = mx;
+  result[2 * t + 1] = __uint_as_float(idx);
+}
+
+// ---------------------------------------------------------------------------
+// dequant (debug exports): one thread per 32-weight run
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(NT) void dequant_q4k_kernel(const uint8_t* blocks, uint64_t nblocks, float* out) {
+  const uint64_t t = (uint64_t)blockIdx.x * NT + threadIdx.x;  // (block, group, half)
+  if (t >= nblocks * 8) return;
+  const uint64_t b = t >> 3;
+  const int g = (int)(t >> 1) & 3, hi = (int)t & 1;
+  const uint8_t* p = blocks + b * 144;
+  const float d = g4d::f16_bits_to_f32(p[0] | (p[1] << 8));
+  const float dmin = g4d::f16_bits_to_f32(p[2] | (p[3] << 8));
+  const uint8_t* s = p + 4;
+  const int j = 2 * g + hi;
+  int sc, m;
+  if (j < 4) {
+    sc = s[j] & 63;
+    m = s[j + 4] & 63;
+  } else {
+    sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+    m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+  }
+  const float d1 = d * (float)sc, m1 = dmin * (float)m;  // exact products
+  float* o = out + b * 256 + 64 * g + 32 * hi;
+  for (int l = 0; l < 32; ++l) {
+    const uint8_t q = p[16 + 32 * g + l];
+    const int qq = hi ? (q >> 4) : (q & 15);
+    // d1*q is exact, so the fused form rounds once, like the f64 reference
+    o[l] = __builtin_fmaf(d1, (float)qq, -m1);
+  }
+}
+
+__global__ __launch_bounds__(NT) void dequant_q6k_kernel(const uint8_t* blocks, uint64_t nblocks, float* out) {
+  const uint64_t t = (uint64_t)blockIdx.x * NT + threadIdx.x;  // (block, half, l)
+  if (t >= nblocks * 64) return;
+  const uint64_t b = t >> 6;
+  const int half = (int)(t >> 5) & 1, l = (int)t & 31;
+  const uint8_t* p = blocks + b * 210;
+  const float d = g4d::f16_bits_to_f32(p[208] | (p[209] << 8));
+  const uint8_t* ql = p + 64 * half;
+  const uint8_t qh = p[128 + 32 * half + l];
+  const int8_t* sc = (const int8_t*)(p + 192 + 8 * half);
+  const int is = l >> 4;
+  const int q1 = ((ql[l] & 15) | ((qh & 3) << 4)) - 32;
+  const int q2 = ((ql[l + 32] & 15) | (((qh >> 2) & 3) << 4)) - 32;
+  const int q3 = ((ql[l] >> 4) | (((qh >> 4) & 3) << 4)) - 32;
+  const int q4 = ((ql[l + 32] >> 4) | (((qh >> 6) & 3) << 4)) - 32;
+  float* o = out + b * 256 + 128 * half;
+  // d*sc*q needs <= 23 significant bits: exact in f32
+  o[l] = d * (float)sc[is] * (float)q1;
+  o[l + 32] = d * (float)sc[is + 2] * (float)q2;
+  o[l + 64] = d * (float)sc[is + 4] * (float)q3;
+  o[l + 96] = d * (float)sc[is + 6] * (float)q4;
+}
+
+// ---------------------------------------------------------------------------
+// seeded synthetic inputs (counter-based SplitMix64, Box-Muller in f64)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ double normal_from(uint64_t w0, uint64_t w1) {
+  const double u1 = (double)((w0 >> 11) + 1) * 0x1.0p-53;
+  const double u2 = (double)(w1 >> 11) * 0x1.0p-53;
+  return sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+}
+
+__global__ __launch_bounds__(NT) void fill_q4k_kernel(uint8_t* dst, uint64_t nblocks, uint64_t seed) {
+  const uint64_t b = (uint64_t)blockIdx.x * NT + threadIdx.x;
+  if (b >= nblocks) return;
+  uint64_t w[22];
+#pragma unroll
+  for (int i = 0; i < 22; ++i) w[i] = g4d::splitmix64(seed, 32 * b + (uint64_t)i);
+  uint32_t words[36];
+  const uint16_t d = g4d::f32_to_f16_bits((float)(fabs(normal_from(w[0], w[1])) * 2e-3));
+  const uint16_t dm = g4d::f32_to_f16_bits((float)(fabs(normal_from(w[2], w[3])) * 1e-3));
+  words[0] = (uint32_t)d | ((uint32_t)dm << 16);
+  words[1] = (uint32_t)w[4];
+  words[2] = (uint32_t)(w[4] >> 32);
+  words[3] = (uint32_t)w[5];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    words[4 + 2 * k] = (uint32_t)w[6 + k];
+    words[5 + 2 * k] = (uint32_t)(w[6 + k] >> 32);
+  }
+  uint4* o = (uint4*)(dst + b * 144);
+#pragma unroll
+  for (int k = 0; k < 9; ++k) o[k] = make_uint4(words[4 * k], words[4 * k + 1], words[4 * k + 2], words[4 * k + 3]);
+}
+
+__global__ __launch_bounds__(NT) void fill_q6k_kernel(uint8_t* dst, uint64_t nblocks, uint64_t seed) {
+  const uint64_t b = (uint64_t)blockIdx.x * NT + threadIdx.x;
+  if (b >= nblocks) return;
+  uint8_t* o = dst + b * 210;  // 2-byte aligned
+  uint16_t* o16 = (uint16_t*)o;
+  for (int i = 0; i < 24; ++i) {
+    const uint64_t w = g4d::splitmix64(seed, 32 * b + (uint64_t)i);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o16[4 * i + k] = (uint16_t)(w >> (16 * k));
+  }
+  for (int i = 0; i < 2; ++i) {
+    const uint64_t w = g4d::splitmix64(seed, 32 * b + 24 + (uint64_t)i);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int lo = (int)((w >> (16 * k)) & 63u) - 32;
+      const int hi = (int)((w >> (16 * k + 8)) & 63u) - 32;
+      o16[96 + 4 * i + k] = (uint16_t)((uint8_t)(int8_t)lo | ((uint16_t)(uint8_t)(int8_t)hi << 8));
+    }
+  }
+  const uint64_t w26 = g4d::splitmix64(seed, 32 * b + 26), w27 = g4d::splitmix64(seed, 32 * b + 27);
+  o16[104] = g4d::f32_to_f16_bits((float)(fabs(normal_from(w26, w27)) * 2e-3));
+}
+
+__global__ __launch_bounds__(NT) void fill_normal_kernel(float* dst32, uint16_t* dst16, uint64_t n, uint64_t seed,
+                                                         float mean, float std) {
+  const uint64_t i = (uint64_t)blockIdx.x * NT + threadIdx.x;
+  if (i >= n) return;
+  const float v = (float)((double)mean + (double)std * normal_from(g4d::splitmix64(seed, 2 * i),
+                                                                   g4d::splitmix64(seed, 2 * i + 1)));
+  if (dst32) dst32[i] = v;
+  else dst16[i] = g4d::f32_to_f16_bits(v);
+}
+
+}  // namespace
+
+extern "C" {
+
+int g4_rmsNorm(g4_ctx* ctx, const float* input, const uint16_t* weight, float* output, g4_rms_norm_params p) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(input && weight && output, "g4_rmsNorm: null buffer");
+  G4_REQUIRE(p.hidden_size > 0, "g4_rmsNorm: hidden_size 0");
+  hipLaunchKernelGGL((rms_norm_kernel<false>), dim3(1), dim3(512), 0, ctx->stream, input, weight, nullptr, output,
+                     p.hidden_size, p.eps);
+  G4_LAUNCHED(ctx, "rms_norm");
+  return G4_OK;
+}
+
+int g4_fusedNormAdd(g4_ctx* ctx, const float* input, const uint16_t* weight, const float* residual, float* output,
+                    g4_norm_add_params p) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(input && weight && residual && output, "g4_fusedNormAdd: null buffer");
+  G4_REQUIRE(p.size > 0, "g4_fusedNormAdd: size 0");
+  hipLaunchKernelGGL((rms_norm_kernel<true>), dim3(1), dim3(512), 0, ctx->stream, input, weight, residual, output,
+                     p.size, p.eps);
+  G4_LAUNCHED(ctx, "fused_norm_add");
+  return G4_OK;
+}
+
+int g4_perHeadRmsNormNoWeight(g4_ctx* ctx, float* data, g4_per_head_norm_params p) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(data, "g4_perHeadRmsNormNoWeight: null buffer");
+  G4_REQUIRE(p.num_heads > 0 && p.head_dim > 0 && p.head_dim <= 512,
+             "g4_perHeadRmsNormNoWeight: head_dim %u outside (0, 512]", p.head_dim);
+  hipLaunchKernelGGL((head_norm_kernel<0>), dim3(p.num_heads), dim3(NT), 0, ctx->stream, data, nullptr, p.num_heads,
+                     p.head_dim, p.eps, 0u, nullptr, 0.f, 0u, nullptr);
+  G4_LAUNCHED(ctx, "per_head_rms_norm_no_weight");
+  return G4_OK;
+}
+
+static int norm_rope(g4_ctx* ctx, float* data, const uint16_t* weight, g4_norm_rope_params p,
+                     const uint16_t* rope_freqs, const uint32_t* position_dev) {
+  G4_REQUIRE(data && weight, "g4_fusedPerHeadNormRope: null buffer");
+  G4_REQUIRE(!p.apply_divisor || rope_freqs, "g4_fusedPerHeadNormRope: apply_divisor needs rope_freqs");
+  G4_REQUIRE(p.num_heads > 0 && p.head_dim >= 2 && p.head_dim <= 512 && p.head_dim % 2 == 0,
+             "g4_fusedPerHeadNormRope: head_dim %u must be even and <= 512", p.head_dim);
+  hipLaunchKernelGGL((head_norm_kernel<1>), dim3(p.num_heads), dim3(NT), 0, ctx->stream, data, weight, p.num_heads,
+                     p.head_dim, p.eps, p.position, position_dev, p.theta, p.apply_divisor, rope_freqs);
+  G4_LAUNCHED(ctx, "fused_per_head_norm_rope");
+  return G4_OK;
+}
+
+int g4_fusedPerHeadNormRope(g4_ctx* ctx, float* data, const uint16_t* weight, g4_norm_rope_params p,
+                            const uint16_t* rope_freqs) {
+  G4_ENTER(ctx);
+  return norm_rope(ctx, data, weight, p, rope_freqs, nullptr);
+}
+
+int g4_fusedPerHeadNormRope_dev(g4_ctx* ctx, float* data, const uint16_t* weight, g4_norm_rope_params p,
+                                const uint16_t* rope_freqs, const uint32_t* position_dev) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(position_dev, "g4_fusedPerHeadNormRope_dev: null position");
+  return norm_rope(ctx, data, weight, p, rope_freqs, position_dev);
+}
+
+int g4_geluMul(g4_ctx* ctx, const float* gate, const float* up, float* output, uint32_t size) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(gate && up && output, "g4_geluMul: null buffer");
+  if (!size) return G4_OK;
+  hipLaunchKernelGGL(gelu_mul_kernel, dim3(ceil_div(size, NT)), dim3(NT), 0, ctx->stream, gate, up, output, size);
+  G4_LAUNCHED(ctx, "gelu_mul");
+  return G4_OK;
+}
+
+int g4_logitSoftcap(g4_ctx* ctx, float* logits, g4_softcap_params p) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(logits, "g4_logitSoftcap: null buffer");
+  G4_REQUIRE(p.cap != 0.f, "g4_logitSoftcap: cap must be non-zero");
+  if (!p.size) return G4_OK;
+  hipLaunchKernelGGL(softcap_kernel, dim3(ceil_div(p.size, NT)), dim3(NT), 0, ctx->stream, logits, p.size, p.cap);
+  G4_LAUNCHED(ctx, "logit_softcap");
+  return G4_OK;
+}
+
+static int kv_store(g4_ctx* ctx, const float* k_in, const float* v_in, uint16_t* kc, uint16_t* vc,
+                    g4_kv_store_params p, const uint32_t* position_dev) {
+  G4_REQUIRE(k_in && v_in && kc && vc, "g4_kvCacheStore: null buffer");
+  G4_REQUIRE(position_dev || p.position < p.max_seq_len, "g4_kvCacheStore: position %u >= max_seq_len %u",
+             p.position, p.max_seq_len);
+  const uint32_t total = p.num_kv_heads * p.head_dim;
+  if (!total) return G4_OK;
+  hipLaunchKernelGGL(kv_store_kernel, dim3(ceil_div(total, NT)), dim3(NT), 0, ctx->stream, k_in, v_in, kc, vc, total,
+                     p.position, position_dev, p.max_seq_len);
+  G4_LAUNCHED(ctx, "kv_cache_store");
+  return G4_OK;
+}
+
+int g4_kvCacheStore(g4_ctx* ctx, const float* k_in, const float* v_in, uint16_t* k_cache, uint16_t* v_cache,
+                    g4_kv_store_params p) {
+  G4_ENTER(ctx);
+  return kv_store(ctx, k_in, v_in, k_cache, v_cache, p, nullptr);
+}
+
+int g4_kvCacheStore_dev(g4_ctx* ctx, const float* k_in, const float* v_in, uint16_t* k_cache, uint16_t* v_cache,
+                        g4_kv_store_params p, const uint32_t* position_dev) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(position_dev, "g4_kvCacheStore_dev: null position");
+  return kv_store(ctx, k_in, v_in, k_cache, v_cache, p, position_dev);
+}
+
+int g4_advancePosition(g4_ctx* ctx, uint32_t* position_dev, uint32_t delta) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(position_dev, "g4_advancePosition: null position");
+  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, ctx->stream, position_dev, delta);
+  G4_LAUNCHED(ctx, "advance_position");
+  return G4_OK;
+}
+
+int g4_argmax(g4_ctx* ctx, const float* logits, uint32_t* result, uint32_t size) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(logits && result, "g4_argmax: null buffer");
+  void* scratch = nullptr;
+  int rc = g4_internal_scratch(ctx, kArgmaxBlocks * sizeof(Cand), &scratch);
+  if (rc) return rc;
+  const unsigned want = ceil_div(size, 1024);
+  const int nb = want == 0 ? 1 : (want > (unsigned)kArgmaxBlocks ? kArgmaxBlocks : (int)want);
+  hipLaunchKernelGGL(argmax_partial, dim3(nb), dim3(NT), 0, ctx->stream, logits, size, (Cand*)scratch);
+  G4_LAUNCHED(ctx, "argmax_partial");
+  hipLaunchKernelGGL(argmax_final, dim3(1), dim3(NT), 0, ctx->stream, (const Cand*)scratch, nb, result);
+  G4_LAUNCHED(ctx, "argmax_final");
+  return G4_OK;
+}
+
+int g4_topk256(g4_ctx* ctx, const float* logits, float* result, uint32_t size) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(logits && result, "g4_topk256: null buffer");
+  void* scratch = nullptr;
+  int rc = g4_internal_scratch(ctx, (size_t)kTopkSlabs * 256 * sizeof(float2), &scratch);
+  if (rc) return rc;
+  const uint32_t rows = (size + 255) / 256;
+  const unsigned want = ceil_div(rows, 8);
+  const int ns = want == 0 ? 1 : (want > (unsigned)kTopkSlabs ? kTopkSlabs : (int)want);
+  hipLaunchKernelGGL(topk_partial, dim3(ns), dim3(NT), 0, ctx->stream, logits, size, (float2*)scratch);
+  G4_LAUNCHED(ctx, "topk_partial");
+  hipLaunchKernelGGL(topk_final, dim3(1), dim3(NT), 0, ctx->stream, (const float2*)scratch, ns, result);
+  G4_LAUNCHED(ctx, "topk_final");
+  return G4_OK;
+}
+
+int g4_dequant_q4k(g4_ctx* ctx, const void* blocks, uint64_t nblocks, float* out) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(blocks && out, "g4_dequant_q4k: null buffer");
+  if (!nblocks) return G4_OK;
+  hipLaunchKernelGGL(dequant_q4k_kernel, dim3(ceil_div(nblocks * 8, NT)), dim3(NT), 0, ctx->stream,
+                     (const uint8_t*)blocks, nblocks, out);
+  G4_LAUNCHED(ctx, "dequant_q4k");
+  return G4_OK;
+}
+
+int g4_dequant_q6k(g4_ctx* ctx, const void* blocks, uint64_t nblocks, float* out) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(blocks && out, "g4_dequant_q6k: null buffer");
+  if (!nblocks) return G4_OK;
+  hipLaunchKernelGGL(dequant_q6k_kernel, dim3(ceil_div(nblocks * 64, NT)), dim3(NT), 0, ctx->stream,
+                     (const uint8_t*)blocks, nblocks, out);
+  G4_LAUNCHED(ctx, "dequant_q6k");
+  return G4_OK;
+}
+
+int g4_fill_q4k(g4_ctx* ctx, void* dst, uint64_t nblocks, uint64_t seed) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(dst, "g4_fill_q4k: null buffer");
+  G4_REQUIRE(((uintptr_t)dst & 15) == 0, "g4_fill_q4k: destination must be 16-byte aligned");
+  if (!nblocks) return G4_OK;
+  hipLaunchKernelGGL(fill_q4k_kernel, dim3(ceil_div(nblocks, NT)), dim3(NT), 0, ctx->stream, (uint8_t*)dst, nblocks,
+                     seed);
+  G4_LAUNCHED(ctx, "fill_q4k");
+  return G4_OK;
+}
+
+int g4_fill_q6k(g4_ctx* ctx, void* dst, uint64_t nblocks, uint64_t seed) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(dst, "g4_fill_q6k: null buffer");
+  G4_REQUIRE(((uintptr_t)dst & 1) == 0, "g4_fill_q6k: destination must be 2-byte aligned");
+  if (!nblocks) return G4_OK;
+  hipLaunchKernelGGL(fill_q6k_kernel, dim3(ceil_div(nblocks, NT)), dim3(NT), 0, ctx->stream, (uint8_t*)dst, nblocks,
+                     seed);
+  G4_LAUNCHED(ctx, "fill_q6k");
+  return G4_OK;
+}
+
+int g4_fill_normal_f32(g4_ctx* ctx, float* dst, uint64_t n, uint64_t seed, float mean, float std) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(dst, "g4_fill_normal_f32: null buffer");
+  if (!n) return G4_OK;
+  hipLaunchKernelGGL(fill_normal_kernel, dim3(ceil_div(n, NT)), dim3(NT), 0, ctx->stream, dst, (uint16_t*)nullptr, n,
+                     seed, mean, std);
+  G4_LAUNCHED(ctx, "fill_normal_f32");
+  return G4_OK;
+}
+
+int g4_fill_normal_f16(g4_ctx* ctx, uint16_t* dst, uint64_t n, uint64_t seed, float mean, float std) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(dst, "g4_fill_normal_f16: null buffer");
+  if (!n) return G4_OK;
+  hipLaunchKernelGGL(fill_normal_kernel, dim3(ceil_div(n, NT)), dim3(NT), 0, ctx->stream, (float*)nullptr, dst, n,
+                     seed, mean, std);
+  G4_LAUNCHED(ctx, "fill_normal_f16");
+  return G4_OK;
+}
+
+}  // extern "C"

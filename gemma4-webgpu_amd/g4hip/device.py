@@ -1,0 +1,320 @@
+"""Device context, buffers and the per-kernel entry points of libg4hip.
+
+Method names are the reference's kernel keys (src/shaders.ts:34-56); their
+arguments are the WGSL bindings in order followed by the Params fields
+(src/engine.ts:432-545 builds the same Params). Buffers are device
+allocations owned by the caller, as in the reference (src/engine.ts:1001-1064).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Union
+
+import numpy as np
+
+from ._lib import (
+    AttnOutputParams,
+    AttnScoreParams,
+    KvStoreParams,
+    MatmulParams,
+    NormAddParams,
+    NormRopeParams,
+    PagedAttnParams,
+    PerHeadNormParams,
+    RmsNormParams,
+    SoftcapParams,
+    SoftmaxParams,
+    check,
+    lib,
+)
+
+
+class Buffer:
+    """A device allocation (pointer + size); `offset(n)` views a byte offset."""
+
+    def __init__(self, ctx: "Context", ptr: int, nbytes: int, owned: bool = True):
+        self.ctx = ctx
+        self.ptr = ptr
+        self.nbytes = nbytes
+        self._owned = owned
+
+    def offset(self, nbytes: int) -> "Buffer":
+        assert 0 <= nbytes <= self.nbytes
+        return Buffer(self.ctx, self.ptr + nbytes, self.nbytes - nbytes, owned=False)
+
+    def upload(self, arr: np.ndarray, offset: int = 0) -> "Buffer":
+        a = np.ascontiguousarray(arr)
+        assert offset + a.nbytes <= self.nbytes, "upload past the end of the buffer"
+        check(lib().g4_upload(self.ctx.h, ctypes.c_void_p(self.ptr), a.ctypes.data_as(ctypes.c_void_p),
+                              a.nbytes, offset))
+        return self
+
+    def download(self, dtype, count: Optional[int] = None, offset: int = 0) -> np.ndarray:
+        dt = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dt.itemsize
+        out = np.empty(count, dt)
+        assert offset + out.nbytes <= self.nbytes, "download past the end of the buffer"
+        check(lib().g4_download(self.ctx.h, out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(self.ptr),
+                                out.nbytes, offset))
+        return out
+
+    def zero(self) -> "Buffer":
+        check(lib().g4_memset(self.ctx.h, ctypes.c_void_p(self.ptr), 0, self.nbytes))
+        return self
+
+    def free(self) -> None:
+        if self._owned and self.ptr:
+            check(lib().g4_free(self.ctx.h, ctypes.c_void_p(self.ptr)))
+        self.ptr = 0
+
+    def __del__(self):
+        try:
+            if self._owned and self.ptr and self.ctx.h:
+                lib().g4_free(self.ctx.h, ctypes.c_void_p(self.ptr))
+                self.ptr = 0
+        except Exception:
+            pass
+
+
+Ptr = Union[Buffer, int, None]
+
+
+def _p(b: Ptr) -> ctypes.c_void_p:
+    if b is None:
+        return ctypes.c_void_p(0)
+    if isinstance(b, Buffer):
+        return ctypes.c_void_p(b.ptr)
+    return ctypes.c_void_p(int(b))
+
+
+class Context:
+    """One HIP device + stream. All kernels enqueue on `stream`."""
+
+    def __init__(self, device: int = 0):
+        h = ctypes.c_void_p()
+        check(lib().g4_init(device, ctypes.byref(h)))
+        self.h = h
+        self.device = device
+
+    def close(self) -> None:
+        if self.h:
+            lib().g4_destroy(self.h)
+            self.h = ctypes.c_void_p(0)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # ---- info / memory ----
+    def info(self):
+        name = ctypes.create_string_buffer(128)
+        cus = ctypes.c_int()
+        hbm = ctypes.c_size_t()
+        check(lib().g4_device_info(self.h, name, 128, ctypes.byref(cus), ctypes.byref(hbm)))
+        return {"name": name.value.decode(), "num_cus": cus.value, "hbm_bytes": hbm.value}
+
+    @property
+    def stream(self) -> int:
+        return lib().g4_get_stream(self.h) or 0
+
+    def set_stream(self, hip_stream: int) -> None:
+        check(lib().g4_set_stream(self.h, ctypes.c_void_p(hip_stream)))
+
+    def alloc(self, nbytes: int) -> Buffer:
+        p = ctypes.c_void_p()
+        check(lib().g4_alloc(self.h, max(int(nbytes), 1), ctypes.byref(p)))
+        return Buffer(self, p.value, int(nbytes))
+
+    def empty(self, count: int, dtype) -> Buffer:
+        return self.alloc(int(count) * np.dtype(dtype).itemsize)
+
+    def zeros(self, count: int, dtype) -> Buffer:
+        return self.empty(count, dtype).zero()
+
+    def from_numpy(self, arr: np.ndarray) -> Buffer:
+        a = np.ascontiguousarray(arr)
+        return self.alloc(a.nbytes).upload(a)
+
+    def copy(self, dst: Ptr, src: Ptr, nbytes: int) -> None:
+        check(lib().g4_copy_d2d(self.h, _p(dst), _p(src), nbytes))
+
+    def sync(self) -> None:
+        check(lib().g4_stream_sync(self.h))
+
+    # ---- events / graphs ----
+    def record(self) -> ctypes.c_void_p:
+        ev = ctypes.c_void_p()
+        check(lib().g4_event_record(self.h, ctypes.byref(ev)))
+        return ev
+
+    @staticmethod
+    def elapsed_ms(a, b) -> float:
+        ms = ctypes.c_float()
+        check(lib().g4_event_wait(b))
+        check(lib().g4_event_elapsed_ms(a, b, ctypes.byref(ms)))
+        return float(ms.value)
+
+    @staticmethod
+    def destroy_event(ev) -> None:
+        lib().g4_event_destroy(ev)
+
+    def graph_begin(self) -> None:
+        check(lib().g4_graph_begin(self.h))
+
+    def graph_end(self) -> ctypes.c_void_p:
+        g = ctypes.c_void_p()
+        check(lib().g4_graph_end(self.h, ctypes.byref(g)))
+        return g
+
+    def graph_launch(self, g) -> None:
+        check(lib().g4_graph_launch(self.h, g))
+
+    @staticmethod
+    def graph_destroy(g) -> None:
+        lib().g4_graph_destroy(g)
+
+    # ---- matvec (shaders/matmul_quant.wgsl, matmul_quant_mr4.wgsl) ----
+    def matmulQuant(self, x: Ptr, w: Ptr, y: Ptr, M: int, N: int, wtype: str = "q4k") -> None:
+        fn = {"q4k": lib().g4_matmulQuant_q4k, "q6k": lib().g4_matmulQuant_q6k,
+              "f16": lib().g4_matmulQuant_f16}[wtype]
+        check(fn(self.h, _p(x), _p(w), _p(y), MatmulParams(M, N)))
+
+    def matmulQuantMR4(self, x: Ptr, w: Ptr, y: Ptr, M: int, N: int) -> None:
+        check(lib().g4_matmulQuantMR4_q4k(self.h, _p(x), _p(w), _p(y), MatmulParams(M, N)))
+
+    def matmulQuantBatch(self, x: Ptr, w: Ptr, y: Ptr, M: int, N: int, batch: int, wtype: str = "q4k") -> None:
+        fn = {"q4k": lib().g4_matmulQuantBatch_q4k, "q6k": lib().g4_matmulQuantBatch_q6k}[wtype]
+        check(fn(self.h, _p(x), _p(w), _p(y), MatmulParams(M, N), batch))
+
+    def rmsNormMatmul_q4k(self, x: Ptr, norm_w: Ptr, w: Ptr, y: Ptr, M: int, N: int, eps: float = 1e-6) -> None:
+        check(lib().g4_rmsNormMatmul_q4k(self.h, _p(x), _p(norm_w), _p(w), _p(y), MatmulParams(M, N), eps))
+
+    def normAddGateUpGelu_q4k(self, o: Ptr, w_post: Ptr, residual: Ptr, w_pre: Ptr, w_gate: Ptr, w_up: Ptr,
+                              h_out: Ptr, out: Ptr, M: int, N: int, eps: float = 1e-6) -> None:
+        check(lib().g4_normAddGateUpGelu_q4k(self.h, _p(o), _p(w_post), _p(residual), _p(w_pre), _p(w_gate),
+                                             _p(w_up), _p(h_out), _p(out), MatmulParams(M, N), eps))
+
+    # ---- attention (kv_cache_store / attn_score / softmax / attn_output) ----
+    def kvCacheStore(self, k_in: Ptr, v_in: Ptr, k_cache: Ptr, v_cache: Ptr, num_kv_heads: int, head_dim: int,
+                     position: int, max_seq_len: int, position_dev: Ptr = None) -> None:
+        p = KvStoreParams(num_kv_heads, head_dim, position, max_seq_len)
+        if position_dev is None:
+            check(lib().g4_kvCacheStore(self.h, _p(k_in), _p(v_in), _p(k_cache), _p(v_cache), p))
+        else:
+            check(lib().g4_kvCacheStore_dev(self.h, _p(k_in), _p(v_in), _p(k_cache), _p(v_cache), p,
+                                            _p(position_dev)))
+
+    def attnScore(self, q: Ptr, k_cache: Ptr, scores: Ptr, nqh: int, nkh: int, hd: int, seq_len: int,
+                  scale: float = 1.0, window: int = 0) -> None:
+        check(lib().g4_attnScore(self.h, _p(q), _p(k_cache), _p(scores),
+                                 AttnScoreParams(nqh, nkh, hd, seq_len, scale, window)))
+
+    def softmax(self, scores: Ptr, num_heads: int, seq_len: int) -> None:
+        check(lib().g4_softmax(self.h, _p(scores), SoftmaxParams(num_heads, seq_len)))
+
+    def attnOutput(self, probs: Ptr, v_cache: Ptr, out: Ptr, nqh: int, nkh: int, hd: int, seq_len: int) -> None:
+        check(lib().g4_attnOutput(self.h, _p(probs), _p(v_cache), _p(out), AttnOutputParams(nqh, nkh, hd, seq_len)))
+
+    @staticmethod
+    def attn_workspace_bytes(nqh: int, nkh: int, hd: int, seq_len: int, window: int = 0) -> int:
+        n = ctypes.c_size_t()
+        check(lib().g4_attnDecode_workspace_size(AttnScoreParams(nqh, nkh, hd, seq_len, 1.0, window),
+                                                 ctypes.byref(n)))
+        return int(n.value)
+
+    def attnDecode(self, q: Ptr, k_cache: Ptr, v_cache: Ptr, out: Ptr, nqh: int, nkh: int, hd: int, seq_len: int,
+                   scale: float = 1.0, window: int = 0, workspace: Optional[Buffer] = None,
+                   position_dev: Ptr = None) -> None:
+        p = AttnScoreParams(nqh, nkh, hd, seq_len, scale, window)
+        ws = workspace
+        if ws is None:
+            ws = self.alloc(self.attn_workspace_bytes(nqh, nkh, hd, seq_len, window))
+        if position_dev is None:
+            check(lib().g4_attnDecode(self.h, _p(q), _p(k_cache), _p(v_cache), _p(out), p, _p(ws), ws.nbytes))
+        else:
+            check(lib().g4_attnDecode_dev(self.h, _p(q), _p(k_cache), _p(v_cache), _p(out), p, _p(ws), ws.nbytes,
+                                          _p(position_dev)))
+        if workspace is None:
+            self.sync()
+            ws.free()
+
+    @staticmethod
+    def paged_params(num_seqs, nqh, nkh, hd, page_size, max_pages, max_seq_len, num_pages, scale=1.0, window=0):
+        return PagedAttnParams(num_seqs, nqh, nkh, hd, page_size, max_pages, max_seq_len, num_pages, scale, window)
+
+    @staticmethod
+    def paged_workspace_bytes(p: PagedAttnParams) -> int:
+        n = ctypes.c_size_t()
+        check(lib().g4_pagedAttnDecode_workspace_size(p, ctypes.byref(n)))
+        return int(n.value)
+
+    def pagedAttnDecode(self, q: Ptr, k_pool: Ptr, v_pool: Ptr, page_table: Ptr, seq_lens: Ptr, out: Ptr,
+                        p: PagedAttnParams, workspace: Buffer) -> None:
+        check(lib().g4_pagedAttnDecode(self.h, _p(q), _p(k_pool), _p(v_pool), _p(page_table), _p(seq_lens),
+                                       _p(out), p, _p(workspace), workspace.nbytes))
+
+    def pagedKvStore(self, k_in: Ptr, v_in: Ptr, k_pool: Ptr, v_pool: Ptr, page_table: Ptr, seq_lens: Ptr,
+                     p: PagedAttnParams) -> None:
+        check(lib().g4_pagedKvStore(self.h, _p(k_in), _p(v_in), _p(k_pool), _p(v_pool), _p(page_table),
+                                    _p(seq_lens), p))
+
+    # ---- norms / activations ----
+    def perHeadRmsNormNoWeight(self, data: Ptr, num_heads: int, head_dim: int, eps: float = 1e-6) -> None:
+        check(lib().g4_perHeadRmsNormNoWeight(self.h, _p(data), PerHeadNormParams(num_heads, head_dim, eps, 0)))
+
+    def fusedPerHeadNormRope(self, data: Ptr, weight: Ptr, num_heads: int, head_dim: int, eps: float,
+                             position: int, theta: float, apply_divisor: int, rope_freqs: Ptr,
+                             position_dev: Ptr = None) -> None:
+        p = NormRopeParams(num_heads, head_dim, eps, position, theta, apply_divisor)
+        if position_dev is None:
+            check(lib().g4_fusedPerHeadNormRope(self.h, _p(data), _p(weight), p, _p(rope_freqs)))
+        else:
+            check(lib().g4_fusedPerHeadNormRope_dev(self.h, _p(data), _p(weight), p, _p(rope_freqs),
+                                                    _p(position_dev)))
+
+    def rmsNorm(self, x: Ptr, w: Ptr, out: Ptr, hidden_size: int, eps: float = 1e-6) -> None:
+        check(lib().g4_rmsNorm(self.h, _p(x), _p(w), _p(out), RmsNormParams(hidden_size, eps)))
+
+    def fusedNormAdd(self, x: Ptr, w: Ptr, residual: Ptr, out: Ptr, size: int, eps: float = 1e-6) -> None:
+        check(lib().g4_fusedNormAdd(self.h, _p(x), _p(w), _p(residual), _p(out), NormAddParams(size, eps)))
+
+    def geluMul(self, gate: Ptr, up: Ptr, out: Ptr, size: int) -> None:
+        check(lib().g4_geluMul(self.h, _p(gate), _p(up), _p(out), size))
+
+    def logitSoftcap(self, logits: Ptr, size: int, cap: float = 30.0) -> None:
+        check(lib().g4_logitSoftcap(self.h, _p(logits), SoftcapParams(size, cap)))
+
+    def advancePosition(self, position_dev: Ptr, delta: int = 1) -> None:
+        check(lib().g4_advancePosition(self.h, _p(position_dev), delta))
+
+    def argmax(self, logits: Ptr, result: Ptr, size: int) -> None:
+        check(lib().g4_argmax(self.h, _p(logits), _p(result), size))
+
+    def topk256(self, logits: Ptr, result: Ptr, size: int) -> None:
+        check(lib().g4_topk256(self.h, _p(logits), _p(result), size))
+
+    # ---- debug / synthetic inputs ----
+    def dequant_q4k(self, blocks: Ptr, nblocks: int, out: Ptr) -> None:
+        check(lib().g4_dequant_q4k(self.h, _p(blocks), nblocks, _p(out)))
+
+    def dequant_q6k(self, blocks: Ptr, nblocks: int, out: Ptr) -> None:
+        check(lib().g4_dequant_q6k(self.h, _p(blocks), nblocks, _p(out)))
+
+    def fill_q4k(self, dst: Ptr, nblocks: int, seed: int) -> None:
+        check(lib().g4_fill_q4k(self.h, _p(dst), nblocks, seed))
+
+    def fill_q6k(self, dst: Ptr, nblocks: int, seed: int) -> None:
+        check(lib().g4_fill_q6k(self.h, _p(dst), nblocks, seed))
+
+    def fill_normal_f32(self, dst: Ptr, n: int, seed: int, mean: float = 0.0, std: float = 1.0) -> None:
+        check(lib().g4_fill_normal_f32(self.h, _p(dst), n, seed, mean, std))
+
+    def fill_normal_f16(self, dst: Ptr, n: int, seed: int, mean: float = 0.0, std: float = 1.0) -> None:
+        check(lib().g4_fill_normal_f16(self.h, _p(dst), n, seed, mean, std))
+
+
+def splitmix64(seed: int, idx: int) -> int:
+    return int(lib().g4_splitmix64(seed, idx))

@@ -1,0 +1,277 @@
+/*
+ * g4hip.h — C ABI of libg4hip.so, the MI355X (gfx950) drop-in for the WebGPU
+ * decode hot path of gemma4-webgpu.
+ *
+ * The reference dispatches one WGSL compute shader per kernel key
+ * (src/shaders.ts:34-56) with storage buffers bound in order and a `Params`
+ * uniform (src/engine.ts:412-430). Each g4_<key> entry below takes the same
+ * buffers, in the same binding order, as device pointers, followed by a
+ * Params struct passed by value whose fields match the WGSL struct field for
+ * field. Grid geometry is internal to the library (the reference's caller-side
+ * dispatchMatmul, src/engine.ts:332-341, has no counterpart here).
+ *
+ * Conventions
+ *  - Every call returns an int status: G4_OK (0) or a negative G4_ERR_*.
+ *    g4_last_error() returns a thread-local message for the last failure.
+ *  - A device fault makes the context sticky-lost: every later call on it
+ *    returns G4_ERR_DEVICE_LOST (mirrors `device.lost`, src/engine.ts:385-388).
+ *  - Kernels are enqueued on the context's stream and return immediately;
+ *    they never allocate (callers own every buffer, src/engine.ts:1001-1064).
+ *  - Weights are raw GGUF block bytes (Q4_K: 144 B / 256 weights, Q6_K: 210 B /
+ *    256 weights), rows of N/256 blocks, instead of the f16 rows the reference
+ *    expands them to at load (src/engine.ts:828-841). An f16 entry point is
+ *    kept for hosts that still upload f16.
+ *  - The KV cache element type is f16 (the reference's is f32,
+ *    src/engine.ts:1053-1063); layout is unchanged: position-major,
+ *    [max_seq][num_kv_heads][head_dim].
+ *  - `_dev` variants read the per-forward dynamic field (position; seq_len is
+ *    position + 1) from device memory, so a captured graph can be replayed
+ *    and the sampled token can stay on the GPU (src/engine.ts:1487-1504,
+ *    1724-1727).
+ */
+#ifndef G4HIP_H
+#define G4HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define G4_OK 0
+#define G4_ERR_INVALID (-1)      /* bad argument / shape / null pointer */
+#define G4_ERR_HIP (-2)          /* a HIP runtime call failed */
+#define G4_ERR_DEVICE_LOST (-3)  /* sticky: the context is unusable */
+#define G4_ERR_OOM (-4)          /* device allocation failed */
+#define G4_ERR_UNSUPPORTED (-5)  /* shape the kernels do not handle */
+#define G4_ERR_NO_DEVICE (-6)    /* no HIP device / wrong architecture */
+
+typedef struct g4_ctx g4_ctx;
+typedef struct g4_event g4_event;
+typedef struct g4_graph g4_graph;
+
+/* ------------------------------------------------------------------------ */
+/* Lifecycle, memory, synchronisation                                        */
+/* (replaces initWebGPU / createF16Buffer / writeBuffer / mapAsync:          */
+/*  src/engine.ts:354-389, 553-567, 313-316, 1772-1787)                      */
+/* ------------------------------------------------------------------------ */
+
+const char* g4_last_error(void);
+int g4_version(void); /* ABI version, currently 1 */
+
+int g4_init(int device, g4_ctx** out);
+int g4_destroy(g4_ctx* ctx);
+/* Use an external HIP stream (hipStream_t as void*); NULL restores the
+ * context's own stream. */
+int g4_set_stream(g4_ctx* ctx, void* hip_stream);
+void* g4_get_stream(g4_ctx* ctx);
+int g4_device_info(g4_ctx* ctx, char* name, size_t name_len, int* num_cus, size_t* hbm_bytes);
+
+int g4_alloc(g4_ctx* ctx, size_t bytes, void** dptr);
+int g4_free(g4_ctx* ctx, void* dptr);
+int g4_memset(g4_ctx* ctx, void* dptr, int value, size_t bytes);
+/* host -> device, complete when the call returns (writeBuffer semantics) */
+int g4_upload(g4_ctx* ctx, void* dst, const void* src, size_t bytes, size_t dst_offset);
+/* device -> host, blocking */
+int g4_download(g4_ctx* ctx, void* dst, const void* src, size_t bytes, size_t src_offset);
+/* device -> host, completes asynchronously; poll or wait on the event.
+ * dst must stay valid until the event completes. */
+int g4_download_async(g4_ctx* ctx, void* dst, const void* src, size_t bytes, size_t src_offset,
+                      g4_event** ev);
+int g4_copy_d2d(g4_ctx* ctx, void* dst, const void* src, size_t bytes);
+int g4_stream_sync(g4_ctx* ctx);
+
+int g4_event_record(g4_ctx* ctx, g4_event** ev);
+int g4_event_query(g4_event* ev); /* 1 = complete, 0 = pending, <0 error */
+int g4_event_wait(g4_event* ev);
+int g4_event_elapsed_ms(g4_event* start, g4_event* end, float* ms);
+int g4_event_destroy(g4_event* ev);
+
+/* Graph capture of everything enqueued on the context stream between begin
+ * and end; launch replays it on the context stream. */
+int g4_graph_begin(g4_ctx* ctx);
+int g4_graph_end(g4_ctx* ctx, g4_graph** graph);
+int g4_graph_launch(g4_ctx* ctx, g4_graph* graph);
+int g4_graph_destroy(g4_graph* graph);
+
+/* ------------------------------------------------------------------------ */
+/* Kernel entry points (one per SHADERS key, src/shaders.ts:34-56)           */
+/* ------------------------------------------------------------------------ */
+
+/* shaders/matmul_quant.wgsl:12 — Params { M: out rows, N: reduction }. */
+typedef struct { uint32_t M, N; } g4_matmul_params;
+
+/* y[M] = W[M,N] . x[N].  shaders/matmul_quant.wgsl:21-54 (matmulQuant);
+ * W is raw Q4_K blocks, N % 256 == 0. */
+int g4_matmulQuant_q4k(g4_ctx* ctx, const float* input, const void* weight, float* output,
+                       g4_matmul_params p);
+/* Same contract with W as raw Q6_K blocks (ffn down, tied LM head). */
+int g4_matmulQuant_q6k(g4_ctx* ctx, const float* input, const void* weight, float* output,
+                       g4_matmul_params p);
+/* Same contract with the reference's own f16 rows (shaders/matmul_quant.wgsl:14). */
+int g4_matmulQuant_f16(g4_ctx* ctx, const float* input, const uint16_t* weight, float* output,
+                       g4_matmul_params p);
+/* shaders/matmul_quant_mr4.wgsl:17-88 (matmulQuantMR4): same bindings and
+ * Params; rows per wavefront are internal, so this is the same kernel. */
+int g4_matmulQuantMR4_q4k(g4_ctx* ctx, const float* input, const void* weight, float* output,
+                          g4_matmul_params p);
+/* Batched variant (LM head at M=8, ragged batch): Y[b][M] = W . X[b] for
+ * b < batch; X is [batch][N] f32, Y is [batch][M] f32. batch <= 8 uses the
+ * vector path, batch >= 16 the MFMA path. */
+int g4_matmulQuantBatch_q4k(g4_ctx* ctx, const float* input, const void* weight, float* output,
+                            g4_matmul_params p, uint32_t batch);
+int g4_matmulQuantBatch_q6k(g4_ctx* ctx, const float* input, const void* weight, float* output,
+                            g4_matmul_params p, uint32_t batch);
+
+/* shaders/kv_cache_store.wgsl:1 — Params {num_kv_heads, head_dim, position, max_seq_len}.
+ * Writes k_in/v_in (f32) as f16 into row `position` of the caches. */
+typedef struct { uint32_t num_kv_heads, head_dim, position, max_seq_len; } g4_kv_store_params;
+int g4_kvCacheStore(g4_ctx* ctx, const float* k_in, const float* v_in, uint16_t* k_cache,
+                    uint16_t* v_cache, g4_kv_store_params p);
+int g4_kvCacheStore_dev(g4_ctx* ctx, const float* k_in, const float* v_in, uint16_t* k_cache,
+                        uint16_t* v_cache, g4_kv_store_params p, const uint32_t* position_dev);
+
+/* shaders/attn_score.wgsl:9 — Params {num_q_heads, num_kv_heads, head_dim,
+ * seq_len, scale, sliding_window}; scores is [num_q_heads][seq_len]. */
+typedef struct {
+  uint32_t num_q_heads, num_kv_heads, head_dim, seq_len;
+  float scale;
+  uint32_t sliding_window;
+} g4_attn_score_params;
+int g4_attnScore(g4_ctx* ctx, const float* q, const uint16_t* k_cache, float* scores,
+                 g4_attn_score_params p);
+
+/* shaders/softmax.wgsl:1 — Params {num_heads, seq_len}; in place. */
+typedef struct { uint32_t num_heads, seq_len; } g4_softmax_params;
+int g4_softmax(g4_ctx* ctx, float* scores, g4_softmax_params p);
+
+/* shaders/attn_output.wgsl:1 — Params {num_q_heads, num_kv_heads, head_dim, seq_len}. */
+typedef struct { uint32_t num_q_heads, num_kv_heads, head_dim, seq_len; } g4_attn_output_params;
+int g4_attnOutput(g4_ctx* ctx, const float* probs, const uint16_t* v_cache, float* output,
+                  g4_attn_output_params p);
+
+/* Fused split-K flash-decode: the attnScore -> softmax -> attnOutput trio in
+ * one pass over the KV cache (same inputs and masking as the trio,
+ * src/engine.ts:1582-1584). `workspace` holds per-split partials; its size
+ * comes from g4_attnDecode_workspace_size. */
+int g4_attnDecode_workspace_size(g4_attn_score_params p, size_t* bytes);
+int g4_attnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                  float* output, g4_attn_score_params p, void* workspace, size_t workspace_bytes);
+/* seq_len = *position_dev + 1 read on the device; p.seq_len is the maximum
+ * the workspace was sized for. */
+int g4_attnDecode_dev(g4_ctx* ctx, const float* q, const uint16_t* k_cache,
+                      const uint16_t* v_cache, float* output, g4_attn_score_params p,
+                      void* workspace, size_t workspace_bytes, const uint32_t* position_dev);
+
+/* Ragged multi-sequence decode attention over a paged f16 KV pool: sequence
+ * s has seq_lens[s] positions; its logical position t lives in page
+ * page_table[s * max_pages + t / page_size], slot t % page_size, of a pool
+ * of num_pages pages of page_size rows [num_kv_heads][head_dim]. q is
+ * [num_seqs][num_q_heads][head_dim], output likewise. Lengths are clamped to
+ * max_seq_len and page ids to [0, num_pages), so a bad table cannot address
+ * memory outside the pool. */
+typedef struct {
+  uint32_t num_seqs, num_q_heads, num_kv_heads, head_dim;
+  uint32_t page_size, max_pages, max_seq_len, num_pages;
+  float scale;
+  uint32_t sliding_window;
+} g4_paged_attn_params;
+int g4_pagedAttnDecode_workspace_size(g4_paged_attn_params p, size_t* bytes);
+int g4_pagedAttnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                       const int32_t* page_table, const uint32_t* seq_lens, float* output,
+                       g4_paged_attn_params p, void* workspace, size_t workspace_bytes);
+/* Append one row per sequence at position seq_lens[s] - 1 (after the host or
+ * a previous kernel advanced seq_lens). k_in/v_in are [num_seqs][nkh*hd] f32. */
+int g4_pagedKvStore(g4_ctx* ctx, const float* k_in, const float* v_in, uint16_t* k_pool,
+                    uint16_t* v_pool, const int32_t* page_table, const uint32_t* seq_lens,
+                    g4_paged_attn_params p);
+
+/* shaders/per_head_rms_norm_no_weight.wgsl:8 — Params {num_heads, head_dim, eps, pad}; in place. */
+typedef struct { uint32_t num_heads, head_dim; float eps; uint32_t pad; } g4_per_head_norm_params;
+int g4_perHeadRmsNormNoWeight(g4_ctx* ctx, float* data, g4_per_head_norm_params p);
+
+/* shaders/fused_per_head_norm_rope.wgsl:13 — Params {num_heads, head_dim, eps,
+ * position, theta, apply_divisor}; bindings data (rw), weight f16[head_dim],
+ * params, rope_freqs f16[head_dim/2]. */
+typedef struct {
+  uint32_t num_heads, head_dim;
+  float eps;
+  uint32_t position;
+  float theta;
+  uint32_t apply_divisor;
+} g4_norm_rope_params;
+int g4_fusedPerHeadNormRope(g4_ctx* ctx, float* data, const uint16_t* weight,
+                            g4_norm_rope_params p, const uint16_t* rope_freqs);
+int g4_fusedPerHeadNormRope_dev(g4_ctx* ctx, float* data, const uint16_t* weight,
+                                g4_norm_rope_params p, const uint16_t* rope_freqs,
+                                const uint32_t* position_dev);
+
+/* shaders/rms_norm.wgsl:2 — Params {hidden_size, eps}. */
+typedef struct { uint32_t hidden_size; float eps; } g4_rms_norm_params;
+int g4_rmsNorm(g4_ctx* ctx, const float* input, const uint16_t* weight, float* output,
+               g4_rms_norm_params p);
+
+/* shaders/fused_norm_add.wgsl:2 — Params {size, eps}; out = residual + norm(in)*w. */
+typedef struct { uint32_t size; float eps; } g4_norm_add_params;
+int g4_fusedNormAdd(g4_ctx* ctx, const float* input, const uint16_t* weight, const float* residual,
+                    float* output, g4_norm_add_params p);
+
+/* shaders/gelu_mul.wgsl:7 — uniform size. */
+int g4_geluMul(g4_ctx* ctx, const float* gate, const float* up, float* output, uint32_t size);
+
+/* shaders/logit_softcap.wgsl:5 — Params {size, cap}; in place. */
+typedef struct { uint32_t size; float cap; } g4_softcap_params;
+int g4_logitSoftcap(g4_ctx* ctx, float* logits, g4_softcap_params p);
+
+/* *position_dev += delta on the stream: the device-side step counter that lets
+ * a captured decode graph be replayed token after token (the role of the
+ * per-forward uniform patches, src/engine.ts:1487-1504). */
+int g4_advancePosition(g4_ctx* ctx, uint32_t* position_dev, uint32_t delta);
+
+/* shaders/argmax.wgsl:1-3 — result u32[1]; size = vocabulary. */
+int g4_argmax(g4_ctx* ctx, const float* logits, uint32_t* result, uint32_t size);
+/* shaders/topk256.wgsl:1-3 — result f32[512] = (max, bitcast idx) per residue class. */
+int g4_topk256(g4_ctx* ctx, const float* logits, float* result, uint32_t size);
+
+/* ------------------------------------------------------------------------ */
+/* Fused step kernels (the MI355X decode path; each is equivalent to a run   */
+/* of the per-key kernels above, named in its comment)                       */
+/* ------------------------------------------------------------------------ */
+
+/* rmsNorm -> matmulQuant: y = W . (x * w / rms(x)). src/engine.ts:1546-1547. */
+int g4_rmsNormMatmul_q4k(g4_ctx* ctx, const float* x, const uint16_t* norm_w, const void* weight,
+                         float* y, g4_matmul_params p, float eps);
+/* fusedNormAdd -> rmsNorm -> matmulQuant gate/up -> geluMul:
+ *   h = residual + o * w_post / rms(o)   (written to h_out when non-NULL)
+ *   x = h * w_pre / rms(h)
+ *   out = gelu(W_gate . x) * (W_up . x)
+ * src/engine.ts:1587-1604. Gate and up are separate raw Q4_K tensors of
+ * [I, N]; p.M = I, p.N = N. */
+int g4_normAddGateUpGelu_q4k(g4_ctx* ctx, const float* o, const uint16_t* w_post,
+                             const float* residual, const uint16_t* w_pre, const void* w_gate,
+                             const void* w_up, float* h_out, float* out, g4_matmul_params p,
+                             float eps);
+
+/* ------------------------------------------------------------------------ */
+/* Debug / test exports                                                      */
+/* ------------------------------------------------------------------------ */
+
+/* Dequantize nblocks raw blocks to f32 (bit-exact vs src/gguf.ts:168-210 / :323-368). */
+int g4_dequant_q4k(g4_ctx* ctx, const void* blocks, uint64_t nblocks, float* out);
+int g4_dequant_q6k(g4_ctx* ctx, const void* blocks, uint64_t nblocks, float* out);
+
+/* Seeded synthetic inputs, generated on the device (counter-based SplitMix64;
+ * block b of a stream draws words 32b.., element i of a normal stream words
+ * 2i and 2i+1; Box-Muller in f64). */
+uint64_t g4_splitmix64(uint64_t seed, uint64_t idx);
+int g4_fill_q4k(g4_ctx* ctx, void* dst, uint64_t nblocks, uint64_t seed);
+int g4_fill_q6k(g4_ctx* ctx, void* dst, uint64_t nblocks, uint64_t seed);
+int g4_fill_normal_f32(g4_ctx* ctx, float* dst, uint64_t n, uint64_t seed, float mean, float std);
+int g4_fill_normal_f16(g4_ctx* ctx, uint16_t* dst, uint64_t n, uint64_t seed, float mean,
+                       float std);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* G4HIP_H */

@@ -1,0 +1,137 @@
+"""GPU parity: decode attention over an f16 KV cache — the per-key trio and
+the split-K flash-decode (dense, device-position and paged/ragged forms)
+against the f64 oracle (rel-L2 <= 1e-3, cos >= 0.9999)."""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_util import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def kv(seed, L, nkh, hd):
+    k = O.gen_normal_f16(seed, L * nkh * hd)
+    v = O.gen_normal_f16(seed + 1, L * nkh * hd)
+    return k, v
+
+
+def unit_q(seed, nqh, hd):
+    # q after q_norm (unit RMS, weights ~ N(1, 0.1))
+    q = O.gen_normal_f32(seed, nqh * hd)
+    w = O.gen_normal_f16(seed + 2, hd, 1.0, 0.1)
+    no = np.ones(hd // 2, np.float16).view(np.uint16)
+    return O.fused_per_head_norm_rope(q, w, nqh, hd, 1e-6, 0, 1e4, 0, no)
+
+
+@pytest.mark.parametrize("L,window", [(1, 0), (7, 0), (33, 512), (600, 512), (600, 0)])
+def test_trio(ctx, L, window):
+    nqh, nkh, hd = 8, 1, 256
+    k, v = kv(L, L, nkh, hd)
+    q = unit_q(L + 3, nqh, hd)
+    dq, dk, dv = ctx.from_numpy(q), ctx.from_numpy(k), ctx.from_numpy(v)
+    sc = ctx.empty(nqh * L, np.float32)
+    ctx.attnScore(dq, dk, sc, nqh, nkh, hd, L, 1.0, window)
+    s_ref = O.attn_score(q, k, nqh, nkh, hd, L, 1.0, window)
+    s = sc.download(np.float32)
+    masked = s_ref == np.float32(-1e30)
+    assert np.array_equal(s == np.float32(-1e30), masked)
+    assert_close(s[~masked], s_ref[~masked], rel=1e-6, cos=0.99999999, what="scores")
+    ctx.softmax(sc, nqh, L)
+    out = ctx.empty(nqh * hd, np.float32)
+    ctx.attnOutput(sc, dv, out, nqh, nkh, hd, L)
+    assert_close(out.download(np.float32), O.attention(q, k, v, nqh, nkh, hd, L, 1.0, window), what="trio")
+
+
+DECODE_CASES = [
+    # (L, window, head_dim): short, E2B local (W=512), the config-3 contexts
+    (1, 0, 256), (7, 0, 256), (64, 0, 256), (65, 0, 256), (600, 512, 256), (600, 0, 256),
+    (512, 0, 256), (4096, 0, 256), (4096, 512, 256), (32768, 0, 256), (5000, 0, 512), (777, 0, 128),
+]
+
+
+@pytest.mark.parametrize("L,window,hd", DECODE_CASES)
+def test_attn_decode(ctx, L, window, hd):
+    nqh, nkh = 8, 1
+    k, v = kv(L * 3 + hd, L, nkh, hd)
+    q = unit_q(L + 5, nqh, hd)
+    ref = O.attention(q, k, v, nqh, nkh, hd, L, 1.0, window)
+    out = ctx.empty(nqh * hd, np.float32)
+    ws = ctx.alloc(ctx.attn_workspace_bytes(nqh, nkh, hd, L, window))
+    dk, dv = ctx.from_numpy(k), ctx.from_numpy(v)
+    ctx.attnDecode(ctx.from_numpy(q), dk, dv, out, nqh, nkh, hd, L, 1.0, window, workspace=ws)
+    assert_close(out.download(np.float32), ref, what=f"L={L} W={window}")
+
+
+def test_attn_decode_gqa_groups(ctx):
+    for nqh, nkh in [(8, 2), (4, 4), (8, 8)]:
+        hd, L = 256, 300
+        k, v = kv(nqh * 10 + nkh, L, nkh, hd)
+        q = O.gen_normal_f32(nqh, nqh * hd)
+        out = ctx.empty(nqh * hd, np.float32)
+        ctx.attnDecode(ctx.from_numpy(q), ctx.from_numpy(k), ctx.from_numpy(v), out, nqh, nkh, hd, L)
+        assert_close(out.download(np.float32), O.attention(q, k, v, nqh, nkh, hd, L), what=f"{nqh}/{nkh}")
+
+
+def test_attn_decode_dev_position(ctx):
+    """Capacity-sized plan, live length read on the device (graph replay form)."""
+    nqh, nkh, hd, cap = 8, 1, 256, 8192
+    k, v = kv(99, cap, nkh, hd)
+    q = unit_q(98, nqh, hd)
+    dk, dv, dq = ctx.from_numpy(k), ctx.from_numpy(v), ctx.from_numpy(q)
+    ws = ctx.alloc(ctx.attn_workspace_bytes(nqh, nkh, hd, cap, 0))
+    out = ctx.empty(nqh * hd, np.float32)
+    for pos in (0, 100, 4095, cap - 1):
+        pdev = ctx.from_numpy(np.array([pos], np.uint32))
+        ctx.attnDecode(dq, dk, dv, out, nqh, nkh, hd, cap, 1.0, 0, workspace=ws, position_dev=pdev)
+        assert_close(out.download(np.float32), O.attention(q, k, v, nqh, nkh, hd, pos + 1), what=f"pos={pos}")
+
+
+@pytest.mark.parametrize("B,window", [(4, 0), (32, 0), (32, 512)])
+def test_paged_ragged(ctx, B, window):
+    nqh, nkh, hd, P = 8, 1, 256, 16
+    rng = np.random.default_rng(B + window)
+    lens = rng.integers(128, 8193, B).astype(np.uint32) if B > 4 else np.array([1, 16, 17, 1000], np.uint32)
+    max_len = int(lens.max())
+    max_pages = (max_len + P - 1) // P
+    total_pages = int(sum((int(L) + P - 1) // P for L in lens)) + 7
+    perm = rng.permutation(total_pages).astype(np.int32)
+    table = np.zeros((B, max_pages), np.int32)
+    k_pool = O.gen_normal_f16(1, total_pages * P * hd).reshape(-1, hd)
+    v_pool = O.gen_normal_f16(2, total_pages * P * hd).reshape(-1, hd)
+    c = 0
+    for s in range(B):
+        n = (int(lens[s]) + P - 1) // P
+        table[s, :n] = perm[c:c + n]
+        c += n
+    q = O.gen_normal_f32(3, B * nqh * hd).reshape(B, nqh * hd)
+    p = ctx.paged_params(B, nqh, nkh, hd, P, max_pages, max_len, total_pages, 1.0, window)
+    ws = ctx.alloc(ctx.paged_workspace_bytes(p))
+    out = ctx.empty(B * nqh * hd, np.float32)
+    ctx.pagedAttnDecode(ctx.from_numpy(q), ctx.from_numpy(k_pool), ctx.from_numpy(v_pool), ctx.from_numpy(table),
+                        ctx.from_numpy(lens), out, p, ws)
+    got = out.download(np.float32).reshape(B, -1)
+    for s in range(B):
+        ref = O.attention_paged(q[s], k_pool.reshape(-1), v_pool.reshape(-1), table[s], P, nqh, nkh, hd,
+                                int(lens[s]), 1.0, window)
+        assert_close(got[s], ref, what=f"seq {s} len {lens[s]}")
+
+
+def test_paged_kv_store(ctx):
+    nkh, hd, P, B = 1, 256, 16, 3
+    lens = np.array([1, 17, 32], np.uint32)
+    table = np.array([[2, 0], [5, 1], [3, 4]], np.int32)
+    kp = ctx.zeros(6 * P * hd, np.uint16)
+    vp = ctx.zeros(6 * P * hd, np.uint16)
+    k = O.gen_normal_f32(1, B * hd)
+    v = O.gen_normal_f32(2, B * hd)
+    p = ctx.paged_params(B, 8, nkh, hd, P, 2, 32, 6)
+    ctx.pagedKvStore(ctx.from_numpy(k), ctx.from_numpy(v), kp, vp, ctx.from_numpy(table), ctx.from_numpy(lens), p)
+    K = kp.download(np.uint16).reshape(-1, hd)
+    V = vp.download(np.uint16).reshape(-1, hd)
+    for s in range(B):
+        pos = int(lens[s]) - 1
+        row = table[s, pos // P] * P + pos % P
+        assert np.array_equal(K[row], k.reshape(B, hd)[s].astype(np.float16).view(np.uint16))
+        assert np.array_equal(V[row], v.reshape(B, hd)[s].astype(np.float16).view(np.uint16))
+    assert np.count_nonzero(K.any(axis=1)) == B

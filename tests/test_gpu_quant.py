@@ -1,0 +1,175 @@
+"""GPU parity: Q4_K/Q6_K unpack (bit-exact), quantized matvec (rel-L2 <= 1e-3,
+cos >= 0.9999 against the f64 oracle), the fused norm/GELU matvecs, and the
+device-side synthetic generators (bit-exact against the oracle's)."""
+import struct
+
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_util import assert_close, bits_equal
+from test_oracle import q4k_edge_blocks
+
+pytestmark = pytest.mark.gpu
+
+
+def test_dequant_q4k_bit_exact(ctx):
+    rng = np.random.default_rng(0)
+    b = q4k_edge_blocks(rng, 3000)
+    n = b.size // 144
+    db = ctx.from_numpy(b)
+    out = ctx.empty(n * 256, np.float32)
+    ctx.dequant_q4k(db, n, out)
+    assert bits_equal(out.download(np.float32), O.dequant_q4k(b))
+
+
+def test_dequant_q6k_bit_exact(ctx):
+    b = O.gen_q6k(3, 3001).reshape(3001, 210).copy()
+    b[::7, 208:210] = np.frombuffer(struct.pack("<H", 0x0001), np.uint8)
+    b[1::7, 208:210] = np.frombuffer(struct.pack("<H", 0xbc00), np.uint8)
+    b[2::7, 208:210] = np.frombuffer(struct.pack("<H", 0x7bff), np.uint8)
+    b = b.reshape(-1)
+    db = ctx.from_numpy(b)
+    out = ctx.empty(3001 * 256, np.float32)
+    ctx.dequant_q6k(db, 3001, out)
+    assert bits_equal(out.download(np.float32), O.dequant_q6k(b))
+
+
+def test_generators_match_oracle(ctx):
+    n4, n6, nf = 5000, 3001, 100001
+    b4 = ctx.alloc(n4 * 144)
+    ctx.fill_q4k(b4, n4, 42)
+    assert np.array_equal(b4.download(np.uint8), O.gen_q4k(42, n4))
+    b6 = ctx.alloc(n6 * 210)
+    ctx.fill_q6k(b6, n6, 43)
+    assert np.array_equal(b6.download(np.uint8), O.gen_q6k(43, n6))
+    x = ctx.empty(nf, np.float32)
+    ctx.fill_normal_f32(x, nf, 44, 0.0, 1.0)
+    got = x.download(np.float32)
+    ref = O.gen_normal_f32(44, nf, 0.0, 1.0)
+    # Box-Muller runs in f64 on both sides; a last-bit difference of the
+    # device's log/cos could flip one f32 rounding, so allow one ulp
+    assert np.max(np.abs(got.view(np.int32) - ref.view(np.int32))) <= 1
+    h = ctx.empty(nf, np.uint16)
+    ctx.fill_normal_f16(h, nf, 45, 1.0, 0.1)
+    d = np.abs(h.download(np.uint16).astype(np.int32) - O.gen_normal_f16(45, nf, 1.0, 0.1).astype(np.int32))
+    assert d.max() <= 1
+
+
+MATVEC_CASES = [
+    # (wtype, M, N): config-0 GEMV, E2B q/k/v/o/gate/up (Q4_K), down (Q6_K, I=6144 and
+    # 12288), global-layer shapes (HD=512), a ragged M and a shape on the generic path
+    ("q4k", 6144, 1536),
+    ("q4k", 2048, 1536),
+    ("q4k", 256, 1536),
+    ("q4k", 1536, 2048),
+    ("q4k", 4096, 1536),
+    ("q4k", 1536, 4096),
+    ("q4k", 100, 1536),
+    ("q4k", 33, 2560),
+    ("q6k", 1536, 6144),
+    ("q6k", 1536, 12288),
+    ("q6k", 8192, 1536),
+    ("q6k", 77, 1536),
+    ("q6k", 40, 2560),
+]
+
+
+@pytest.mark.parametrize("wtype,M,N", MATVEC_CASES)
+def test_matmul_quant(ctx, wtype, M, N):
+    bpb = 144 if wtype == "q4k" else 210
+    nb = M * N // 256
+    W = O.gen_q4k(M * 7 + N, nb) if wtype == "q4k" else O.gen_q6k(M * 7 + N, nb)
+    x = O.gen_normal_f32(N, N)
+    ref = O.matmul(x, W, M, N, wtype)
+    dW, dx = ctx.from_numpy(W), ctx.from_numpy(x)
+    dy = ctx.empty(M, np.float32)
+    ctx.matmulQuant(dx, dW, dy, M, N, wtype)
+    assert_close(dy.download(np.float32), ref, what=f"{wtype} {M}x{N}")
+    if wtype == "q4k":
+        dy2 = ctx.empty(M, np.float32)
+        ctx.matmulQuantMR4(dx, dW, dy2, M, N)
+        assert bits_equal(dy2.download(np.float32), dy.download(np.float32))
+    assert nb * bpb == W.size
+
+
+def test_matmul_quant_special_inputs(ctx):
+    M, N = 512, 1536
+    W = O.gen_q4k(1, M * N // 256)
+    dW = ctx.from_numpy(W)
+    dy = ctx.empty(M, np.float32)
+    # x = 0 gives exactly 0
+    ctx.matmulQuant(ctx.zeros(N, np.float32), dW, dy, M, N)
+    assert np.all(dy.download(np.float32) == 0)
+    # widely ranged x (sub-block scales differ by 1e6)
+    x = O.gen_normal_f32(2, N) * np.repeat(10.0 ** np.arange(-3, 3), 256).astype(np.float32)
+    ctx.matmulQuant(ctx.from_numpy(x), dW, dy, M, N)
+    assert_close(dy.download(np.float32), O.matmul(x, W, M, N, "q4k"), what="ranged x")
+
+
+def test_matmul_f16_reference_format(ctx):
+    M, N = 1000, 1536
+    W = O.gen_normal_f16(5, M * N, 0.0, 0.02)
+    x = O.gen_normal_f32(6, N)
+    dy = ctx.empty(M, np.float32)
+    ctx.matmulQuant(ctx.from_numpy(x), ctx.from_numpy(W), dy, M, N, "f16")
+    assert_close(dy.download(np.float32), O.matmul(x, W, M, N, "f16"), rel=1e-5, cos=0.9999999)
+
+
+@pytest.mark.parametrize("wtype,M,N,batch", [("q4k", 2048, 1536, 3), ("q4k", 6144, 1536, 8),
+                                             ("q6k", 4096, 1536, 8), ("q6k", 1536, 6144, 5),
+                                             ("q4k", 1536, 2048, 16)])
+def test_matmul_quant_batched(ctx, wtype, M, N, batch):
+    nb = M * N // 256
+    W = O.gen_q4k(9, nb) if wtype == "q4k" else O.gen_q6k(9, nb)
+    X = O.gen_normal_f32(10, batch * N).reshape(batch, N)
+    dY = ctx.empty(batch * M, np.float32)
+    ctx.matmulQuantBatch(ctx.from_numpy(X), ctx.from_numpy(W), dY, M, N, batch, wtype)
+    Y = dY.download(np.float32).reshape(batch, M)
+    for b in range(batch):
+        assert_close(Y[b], O.matmul(X[b], W, M, N, wtype), what=f"vector {b}")
+
+
+def test_rms_norm_matmul(ctx):
+    M, N = 2560, 1536
+    W = O.gen_q4k(20, M * N // 256)
+    x = O.gen_normal_f32(21, N, 0.0, 3.0)
+    w = O.gen_normal_f16(22, N, 1.0, 0.1)
+    ref = O.matmul(O.rms_norm(x, w, 1e-6), W, M, N, "q4k")
+    dy = ctx.empty(M, np.float32)
+    ctx.rmsNormMatmul_q4k(ctx.from_numpy(x), ctx.from_numpy(w), ctx.from_numpy(W), dy, M, N, 1e-6)
+    assert_close(dy.download(np.float32), ref, what="rmsNorm->matmulQuant")
+
+
+@pytest.mark.parametrize("I,N", [(6144, 1536), (512, 2048)])
+def test_norm_add_gate_up_gelu(ctx, I, N):
+    Wg = O.gen_q4k(30, I * N // 256)
+    Wu = O.gen_q4k(31, I * N // 256)
+    o = O.gen_normal_f32(32, N, 0.0, 2.0)
+    res = O.gen_normal_f32(33, N)
+    w_post = O.gen_normal_f16(34, N, 1.0, 0.1)
+    w_pre = O.gen_normal_f16(35, N, 1.0, 0.1)
+    h = O.fused_norm_add(o, w_post, res, 1e-6)
+    x = O.rms_norm(h, w_pre, 1e-6)
+    ref = O.gelu_mul(O.matmul(x, Wg, I, N, "q4k"), O.matmul(x, Wu, I, N, "q4k"))
+    dh = ctx.empty(N, np.float32)
+    dout = ctx.empty(I, np.float32)
+    ctx.normAddGateUpGelu_q4k(ctx.from_numpy(o), ctx.from_numpy(w_post), ctx.from_numpy(res),
+                              ctx.from_numpy(w_pre), ctx.from_numpy(Wg), ctx.from_numpy(Wu), dh, dout, I, N, 1e-6)
+    assert_close(dh.download(np.float32), h, rel=1e-6, cos=0.99999999, what="h")
+    assert_close(dout.download(np.float32), ref, what="gelu(gate)*up")
+
+
+def test_lm_head_q6k_full_size(ctx):
+    """The tied LM head at its real shape: [262144 x 1536] Q6_K (330 MB)."""
+    M, N = 262144, 1536
+    W = ctx.alloc(M * N // 256 * 210)
+    ctx.fill_q6k(W, M * N // 256, 7)
+    x = O.gen_normal_f32(8, N)
+    dy = ctx.empty(M, np.float32)
+    ctx.matmulQuant(ctx.from_numpy(x), W, dy, M, N, "q6k")
+    y = dy.download(np.float32)
+    # check a strided subset of rows against the oracle (the full oracle takes ~1 s)
+    rows = np.arange(0, M, 97)
+    Wh = W.download(np.uint8).reshape(M, -1)[rows]
+    assert_close(y[rows], O.matmul(x, Wh.reshape(-1), rows.size, N, "q6k"), what="LM head rows")

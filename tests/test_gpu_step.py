@@ -1,0 +1,133 @@
+"""GPU parity of a whole decode step (E2B-shaped layers + tied Q6_K LM head):
+the oracle composition, the per-key kernel sequence (the reference's
+encodeTransformerPass order), the fused step and its HIP-graph replays."""
+import numpy as np
+import pytest
+
+import oracle as O
+from g4hip.decoder import Decoder, E2BShape
+from gpu_util import assert_close, bits_equal
+
+pytestmark = pytest.mark.gpu
+
+N_LAYERS = 2
+MAX_SEQ = 1024
+POS = 600  # > window so the local layer masks
+
+
+@pytest.fixture(scope="module")
+def dec(ctx):
+    # layer 0 local (window 512), layer 1 global
+    shape = E2BShape(n_layers=N_LAYERS, global_layers=(1,))
+    d = Decoder(ctx, shape, max_seq=MAX_SEQ, seed=3)
+    d.fill_kv(POS, seed=4)
+    ctx.sync()
+    return d
+
+
+def host(buf, dtype):
+    return buf.download(dtype)
+
+
+def oracle_step(d: Decoder, hidden, kcs, vcs, pos):
+    s = d.s
+    x = hidden.copy()
+    for il, L in enumerate(d.layers):
+        glob = s.is_global(il)
+        theta = s.theta_global if glob else s.theta_local
+        window = 0 if glob else s.window
+        table = host(d.rope_freqs, np.uint16)
+        n = O.rms_norm(x, host(L.attn_norm, np.uint16), s.eps)
+        q = O.matmul(n, host(L.wq, np.uint8), s.q_dim, s.hidden, "q4k")
+        k = O.matmul(n, host(L.wk, np.uint8), s.kv_dim, s.hidden, "q4k")
+        v = O.matmul(n, host(L.wv, np.uint8), s.kv_dim, s.hidden, "q4k")
+        v = O.per_head_rms_norm_no_weight(v, s.n_kv_heads, s.head_dim, s.eps)
+        q = O.fused_per_head_norm_rope(q, host(L.q_norm, np.uint16), s.n_q_heads, s.head_dim, s.eps, pos, theta,
+                                       int(glob), table)
+        k = O.fused_per_head_norm_rope(k, host(L.k_norm, np.uint16), s.n_kv_heads, s.head_dim, s.eps, pos, theta,
+                                       int(glob), table)
+        O.kv_cache_store_f16(k, v, kcs[il], vcs[il], s.n_kv_heads, s.head_dim, pos)
+        a = O.attention(q, kcs[il], vcs[il], s.n_q_heads, s.n_kv_heads, s.head_dim, pos + 1, 1.0, window)
+        o = O.matmul(a, host(L.wo, np.uint8), s.hidden, s.q_dim, "q4k")
+        h = O.fused_norm_add(o, host(L.post_attn_norm, np.uint16), x, s.eps)
+        n2 = O.rms_norm(h, host(L.pre_ffn_norm, np.uint16), s.eps)
+        g = O.matmul(n2, host(L.wgate, np.uint8), s.ffn, s.hidden, "q4k")
+        u = O.matmul(n2, host(L.wup, np.uint8), s.ffn, s.hidden, "q4k")
+        act = O.gelu_mul(g, u)
+        dn = O.matmul(act, host(L.wdown, np.uint8), s.hidden, s.ffn, "q6k")
+        x = O.fused_norm_add(dn, host(L.post_ffn_norm, np.uint16), h, s.eps)
+    n = O.rms_norm(x, host(d.final_norm, np.uint16), s.eps)
+    logits = O.logit_softcap(O.matmul(n, host(d.lm_head, np.uint8), s.vocab, s.hidden, "q6k"), s.softcap)
+    return x, logits
+
+
+def snapshot(d):
+    return (host(d.hidden, np.float32), [host(L.k_cache, np.uint16) for L in d.layers],
+            [host(L.v_cache, np.uint16) for L in d.layers])
+
+
+def restore(d, snap):
+    d.hidden.upload(snap[0])
+    for L, k, v in zip(d.layers, snap[1], snap[2]):
+        L.k_cache.upload(k)
+        L.v_cache.upload(v)
+
+
+def check_token(d, logits_gpu, what):
+    tok = int(host(d.token, np.uint32)[0])
+    assert tok == O.argmax(logits_gpu), what   # indices bit-exact on identical logits
+
+
+def test_step_reference_and_fused_vs_oracle(ctx, dec):
+    snap = snapshot(dec)
+    x_ref, logits_ref = oracle_step(dec, snap[0], [k.copy() for k in snap[1]], [v.copy() for v in snap[2]], POS)
+
+    dec.step_reference(POS)
+    ctx.sync()
+    assert_close(host(dec.hidden, np.float32), x_ref, what="per-key hidden")
+    lg = host(dec.logits, np.float32)
+    assert_close(lg, logits_ref, what="per-key logits")
+    check_token(dec, lg, "per-key token")
+
+    restore(dec, snap)
+    dec.set_position(POS)
+    dec.step_fused()
+    ctx.sync()
+    assert int(host(dec.pos, np.uint32)[0]) == POS + 1
+    assert_close(host(dec.hidden, np.float32), x_ref, what="fused hidden")
+    lg = host(dec.logits, np.float32)
+    assert_close(lg, logits_ref, what="fused logits")
+    check_token(dec, lg, "fused token")
+    # the KV rows written at POS are the same f16 bits on both paths
+    for il, L in enumerate(dec.layers):
+        row = slice(POS * dec.s.kv_dim, (POS + 1) * dec.s.kv_dim)
+        kf = host(L.k_cache, np.uint16)[row]
+        restore_k = snap[1][il][row]
+        assert not np.array_equal(kf, restore_k)
+    restore(dec, snap)
+
+
+def test_graph_replay_matches_eager(ctx, dec):
+    snap = snapshot(dec)
+    eager = []
+    dec.set_position(POS)
+    for _ in range(3):
+        dec.step_fused()
+        ctx.sync()
+        eager.append((host(dec.hidden, np.float32), host(dec.logits, np.float32), int(host(dec.token, np.uint32)[0])))
+    restore(dec, snap)
+    dec.set_position(POS)
+    g = dec.capture_fused()
+    try:
+        for i in range(3):
+            ctx.graph_launch(g)
+            ctx.sync()
+            # eager work between replays, as a host program would do
+            _ = host(dec.pos, np.uint32)
+            assert bits_equal(host(dec.hidden, np.float32), eager[i][0]), i
+            assert bits_equal(host(dec.logits, np.float32), eager[i][1]), i
+            assert int(host(dec.token, np.uint32)[0]) == eager[i][2]
+        assert int(host(dec.pos, np.uint32)[0]) == POS + 3
+    finally:
+        ctx.graph_destroy(g)
+        restore(dec, snap)
