@@ -52,73 +52,68 @@ def time_launches(ctx, fn, iters):
 
 
 def kernel_census(ctx, dec: Decoder, reps: int):
-    """Per-launch time of each fused kernel kind, each run over all layers
-    (so weights rotate through HBM as in a real step)."""
+    """Average duration of each kernel of the fused step. Each kind is
+    captured as a graph of its launches over all 35 layers (so weights rotate
+    through HBM as in a real step, and no host launch overhead is timed),
+    replayed `reps` times between HIP events on the library's stream.
+    Algorithmic bytes: weights + activations read/written by one launch."""
     s, c = dec.s, ctx
     dec.set_position(START_POS)
     Ls = dec.layers
     nl = len(Ls)
+    H, Q, KV, I, V = s.hidden, s.q_dim, s.kv_dim, s.ffn, s.vocab
+    q4 = lambda M, N: M * N // 256 * 144  # noqa: E731
+    q6 = lambda M, N: M * N // 256 * 210  # noqa: E731
+    n_glob = sum(1 for il in range(nl) if s.is_global(il))
+    L_loc, L_glob = min(START_POS + 1, s.window), START_POS + 1
+    kv_avg = ((nl - n_glob) * L_loc + n_glob * L_glob) * KV * 2 * 2 // nl  # f16 K + V rows read
 
-    def over_layers(body):
-        def run(_i=0):
+    kinds = {
+        # name: (per-layer body, launches per body, algorithmic bytes per launch)
+        "qkv_normadd_matvec": (
+            lambda il, L: c.normAddMatmulSegments(
+                "q4k", dec.down, L.post_ffn_norm, dec.hidden2, L.attn_norm, dec.hidden, [L.wq, L.wk, L.wv],
+                [dec.q, dec.k, dec.v], [Q, KV, KV], H, s.eps),
+            1, q4(Q + 2 * KV, H) + 5 * H * 4 + (Q + 2 * KV) * 4),
+        "attn_fused": (
+            lambda il, L: c.attnDecodeFused(dec.q, dec.k, dec.v, L.q_norm, L.k_norm, dec.rope_freqs, L.k_cache,
+                                            L.v_cache, dec.attn, dec.attn_params[il], dec.attn_ws, dec.pos),
+            1, kv_avg + (Q + 2 * KV) * 4 + Q * 4),
+        "o_matvec": (
+            lambda il, L: c.matmulQuant(dec.attn, L.wo, dec.o, H, Q),
+            1, q4(H, Q) + Q * 4 + H * 4),
+        "gateup_gelu": (
+            lambda il, L: c.normAddGateUpGelu_q4k(dec.o, L.post_attn_norm, dec.hidden, L.pre_ffn_norm, L.wgate,
+                                                  L.wup, dec.hidden2, dec.act, I, H, s.eps),
+            1, 2 * q4(I, H) + 4 * H * 4 + I * 4),
+        "down_matvec_q6k": (
+            lambda il, L: c.matmulQuant(dec.act, L.wdown, dec.down, H, I, "q6k"),
+            1, q6(H, I) + I * 4 + H * 4),
+    }
+    out = {}
+    for name, (body, launches, nbytes) in kinds.items():
+        ctx.graph_begin()
+        try:
             for il, L in enumerate(Ls):
                 body(il, L)
-        return run
-
-    kinds = {}
-
-    def qkv(il, L):
-        c.rmsNormMatmul_q4k(dec.hidden, L.attn_norm, L.wq, dec.q, s.q_dim, s.hidden, s.eps)
-        c.rmsNormMatmul_q4k(dec.hidden, L.attn_norm, L.wk, dec.k, s.kv_dim, s.hidden, s.eps)
-        c.rmsNormMatmul_q4k(dec.hidden, L.attn_norm, L.wv, dec.v, s.kv_dim, s.hidden, s.eps)
-    kinds["qkv_matvec(x3)"] = (qkv, 3, (s.q_dim + 2 * s.kv_dim) * s.hidden // 256 * 144)
-
-    def attn(il, L):
-        w = 0 if s.is_global(il) else s.window
-        c.attnDecode(dec.q, L.k_cache, L.v_cache, dec.attn, s.n_q_heads, s.n_kv_heads, s.head_dim, dec.max_seq, 1.0,
-                     w, workspace=dec.attn_ws, position_dev=dec.pos)
-    n_glob = sum(1 for il in range(nl) if s.is_global(il))
-    kv_bytes = ((nl - n_glob) * min(START_POS + 1, s.window) + n_glob * (START_POS + 1)) * s.kv_dim * 2 * 2 // nl
-    kinds["attn_decode(+combine)"] = (attn, 2, kv_bytes)
-
-    def oproj(il, L):
-        c.matmulQuant(dec.attn, L.wo, dec.o, s.hidden, s.q_dim)
-    kinds["o_matvec"] = (oproj, 1, s.hidden * s.q_dim // 256 * 144)
-
-    def gateup(il, L):
-        c.normAddGateUpGelu_q4k(dec.o, L.post_attn_norm, dec.hidden, L.pre_ffn_norm, L.wgate, L.wup, dec.hidden2,
-                                dec.act, s.ffn, s.hidden, s.eps)
-    kinds["gateup_gelu"] = (gateup, 1, 2 * s.ffn * s.hidden // 256 * 144 + 4 * s.hidden * 4 + s.ffn * 4)
-
-    def down(il, L):
-        c.matmulQuant(dec.act, L.wdown, dec.down, s.hidden, s.ffn, "q6k")
-    kinds["down_matvec_q6k"] = (down, 1, s.hidden * s.ffn // 256 * 210 + s.ffn * 4 + s.hidden * 4)
-
-    def small(il, L):
-        c.perHeadRmsNormNoWeight(dec.v, s.n_kv_heads, s.head_dim, s.eps)
-        c.fusedPerHeadNormRope(dec.q, L.q_norm, s.n_q_heads, s.head_dim, s.eps, 0, 1e4, 0, dec.rope_freqs,
-                               position_dev=dec.pos)
-        c.fusedPerHeadNormRope(dec.k, L.k_norm, s.n_kv_heads, s.head_dim, s.eps, 0, 1e4, 0, dec.rope_freqs,
-                               position_dev=dec.pos)
-        c.kvCacheStore(dec.k, dec.v, L.k_cache, L.v_cache, s.n_kv_heads, s.head_dim, 0, dec.max_seq,
-                       position_dev=dec.pos)
-        c.fusedNormAdd(dec.down, L.post_ffn_norm, dec.hidden2, dec.hidden, s.hidden, s.eps)
-    kinds["small(vnorm,rope x2,kvstore,normadd)"] = (small, 5, 0)
-
-    out = {}
-    for name, (body, launches, bytes_per_layer) in kinds.items():
-        ms = time_launches(ctx, over_layers(body), reps) / nl
-        out[name] = {"us_per_layer": ms * 1e3, "launches_per_layer": launches,
-                     "bytes_per_layer": bytes_per_layer,
-                     "gbps": (bytes_per_layer / (ms * 1e-3) / 1e9) if bytes_per_layer else None}
-    # LM head (330 MB: larger than the 256 MB last-level cache, no rotation needed)
-    lm_bytes = s.lm_head_bytes() + s.hidden * 4 + s.vocab * 4
-
-    def head(_i=0):
-        c.matmulQuant(dec.normed, dec.lm_head, dec.logits, s.vocab, s.hidden, "q6k")
-    ms = time_launches(ctx, head, max(3, reps))
-    out["lm_head_q6k"] = {"us_per_layer": None, "us": ms * 1e3, "launches_per_layer": 0, "bytes": lm_bytes,
-                          "gbps": lm_bytes / (ms * 1e-3) / 1e9}
+        finally:
+            g = ctx.graph_end()
+        us = time_launches(ctx, lambda _i=0: ctx.graph_launch(g), reps) * 1e3 / nl
+        ctx.graph_destroy(g)
+        out[name] = {"us": us, "per_step": nl, "bytes": nbytes, "gbps": nbytes / (us * 1e-6) / 1e9}
+    # LM head with the final norm-add and softcap (330 MB: larger than the
+    # 256 MB last-level cache, so no rotation is needed)
+    last = Ls[-1]
+    ctx.graph_begin()
+    try:
+        c.normAddMatmulSegments("q6k", dec.down, last.post_ffn_norm, dec.hidden2, dec.final_norm, dec.hidden,
+                                [dec.lm_head], [dec.logits], [V], H, s.eps, softcap=s.softcap)
+    finally:
+        g = ctx.graph_end()
+    us = time_launches(ctx, lambda _i=0: ctx.graph_launch(g), max(5, reps)) * 1e3
+    ctx.graph_destroy(g)
+    nbytes = s.lm_head_bytes() + 5 * H * 4 + V * 4
+    out["lm_head_q6k_softcap"] = {"us": us, "per_step": 1, "bytes": nbytes, "gbps": nbytes / (us * 1e-6) / 1e9}
     return out
 
 
@@ -201,6 +196,11 @@ def main():
     ap.add_argument("--census-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=3)
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the step kernels directly instead of replaying a captured graph "
+                         "(for profilers that do not follow graph launches)")
+    ap.add_argument("--no-census", action="store_true")
+    ap.add_argument("--no-gemv0", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
@@ -224,41 +224,48 @@ def main():
     log(f"weights + KV ready in {time.time() - t0:.1f}s "
         f"({(s.layer_weight_bytes() * s.n_layers + s.lm_head_bytes()) / 1e9:.3f} GB of weights)")
 
-    graph = dec.capture_fused("argmax")
+    if args.eager:
+        def step():
+            dec.step_fused("argmax")
+    else:
+        graph = dec.capture_fused("argmax")
+
+        def step():
+            ctx.graph_launch(graph)
     for _ in range(args.warmup):
-        ctx.graph_launch(graph)
+        step()
     ctx.sync()
     log(f"warmup {args.warmup} steps done")
     a = ctx.record()
     for _ in range(args.steps):
-        ctx.graph_launch(graph)
+        step()
     b = ctx.record()
     ms_total = ctx.elapsed_ms(a, b)
     ctx.sync()
     ms_step = ms_total / args.steps
     tok_s = 1000.0 / ms_step
     pos_end = int(dec.pos.download(np.uint32)[0])
-    log(f"decode: {ms_step * 1e3:.1f} us/token = {tok_s:.1f} tok/s (positions {START_POS}..{pos_end})")
-    ctx.graph_destroy(graph)
+    log(f"decode ({'eager' if args.eager else 'graph'}): {ms_step * 1e3:.1f} us/token = {tok_s:.1f} tok/s "
+        f"(positions {START_POS}..{pos_end})")
+    if not args.eager:
+        ctx.graph_destroy(graph)
 
+    if args.no_census:
+        print(json.dumps({"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": ms_step}), flush=True)
+        return
     census = kernel_census(ctx, dec, args.census_reps)
     for k, v in census.items():
         log(f"  {k}: {v}")
     # dominant kernel = largest time per step
-    per_step = {k: (v["us"] if k == "lm_head_q6k" else v["us_per_layer"] * s.n_layers)
-                for k, v in census.items()}
-    dom = max((k for k in per_step if census[k].get("gbps")), key=lambda k: per_step[k])
-    dv = census[dom]
-    if dom == "lm_head_q6k":
-        bytes_launch, us_launch = dv["bytes"], dv["us"]
-    else:
-        bytes_launch, us_launch = dv["bytes_per_layer"], dv["us_per_layer"]
+    per_step = {k: v["us"] * v["per_step"] for k, v in census.items()}
+    dom = max(per_step, key=lambda k: per_step[k])
+    bytes_launch, us_launch = census[dom]["bytes"], census[dom]["us"]
     achieved = bytes_launch / (us_launch * 1e-6) / 1e9
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
                 "bytes_per_launch": bytes_launch, "us_per_launch": round(us_launch, 3)}
 
-    g0 = gemv_cfg0(ctx)
+    g0 = {} if args.no_gemv0 else gemv_cfg0(ctx)
     log(f"config-0 Q4_K GEMV: {g0}")
 
     cpu = None

@@ -1,15 +1,19 @@
 // k_attn.hip — GQA decode attention over an f16 KV cache.
 //
-// Two forms of the same computation (shaders/attn_score.wgsl,
-// shaders/softmax.wgsl, shaders/attn_output.wgsl; scale 1.0, sliding window
-// W masks positions < seq_len - W):
+// Forms of the same computation (shaders/attn_score.wgsl, shaders/softmax.wgsl,
+// shaders/attn_output.wgsl; scale 1.0, sliding window W masks positions
+// < seq_len - W):
 //  * the per-key trio attnScore -> softmax -> attnOutput, kept so that every
 //    reference kernel has a drop-in (scores round-trip through HBM);
-//  * split-K flash-decode: workgroup (split, kv head[, sequence]) streams a
-//    chunk of K/V rows once for all G = NQH/NKH query heads of that KV head,
-//    keeps a running (max, sum, o) per head, and a combine kernel merges the
-//    splits with a log-sum-exp rescale. The paged form addresses rows through
-//    a per-sequence page table (ragged multi-sequence batches).
+//  * split-K flash-decode: workgroup (split, kv head[, sequence]) loads a
+//    32/64-row chunk of K/V once for all G = NQH/NKH query heads of that KV
+//    head and writes a (max, sum, o) partial per head; a merge kernel
+//    combines the splits with a log-sum-exp rescale. The paged form addresses
+//    rows through a per-sequence page table (ragged multi-sequence batches).
+//  * the fused decode form additionally applies q_norm/k_norm + RoPE and the
+//    weightless v_norm and stores the current K/V row
+//    (src/engine.ts:1562-1584: perHeadRmsNormNoWeight, fusedPerHeadNormRope
+//    q/k, kvCacheStore, attnScore, softmax, attnOutput in two launches).
 #include <math.h>
 
 #include "g4_internal.hpp"
@@ -72,8 +76,7 @@ __global__ __launch_bounds__(NT) void softmax_kernel(float* scores, uint32_t num
   for (uint32_t i = threadIdx.x; i < seq_len; i += NT) s[i] = s[i] * inv;
 }
 
-// Thread per (head, d); the position loop is split across blockIdx.y slabs
-// whose partial sums are added in a fixed order by the last pass.
+// Thread per (head, d): sum over positions of p * V.
 __global__ __launch_bounds__(NT) void attn_output_kernel(const float* probs, const uint16_t* vc, float* out,
                                                          uint32_t nqh, uint32_t nkh, uint32_t hd,
                                                          uint32_t seq_len) {
@@ -99,41 +102,76 @@ __global__ __launch_bounds__(NT) void attn_output_kernel(const float* probs, con
 // ---------------------------------------------------------------------------
 // split-K flash-decode
 // ---------------------------------------------------------------------------
+//
+// Workgroup (split, kv head, sequence) owns P = 32*CP consecutive positions
+// of the window and issues every K and V load of its chunk before any other
+// work, so the chunk costs one memory round trip:
+//   K: thread t reads row (t/8) of each 32-row block, slice t%8 (HD/8 halves);
+//   V: thread t reads column(s) of every row of the chunk (one f16 per row for
+//      head_dim 256; head_dim 512 reads two adjacent columns, 128 splits the
+//      rows between two threads per column).
+// Scores are reduced over the 8 slice lanes, the chunk's softmax statistics
+// are formed in LDS, and each thread accumulates o for its own columns, so no
+// cross-wave reduction is needed. A partial (m, l, o) per (split, head) goes
+// to the workspace and attn_merge_kernel combines the splits.
 
 struct AttnArgs {
-  const float* q;            // [num_seqs][nqh][hd]
+  const float* q;            // [num_seqs][nqh][hd] (fused form: raw q projection)
   const uint16_t* kc;        // cache [max_seq][nkh][hd] or pool [rows][nkh][hd]
+  uint16_t* vc_w;            // fused form: written at the current row
+  uint16_t* kc_w;
   const uint16_t* vc;
   const int32_t* page_table; // paged: [num_seqs][max_pages]
   uint32_t page_size, max_pages, num_pages;
   const uint32_t* seq_lens;  // paged: per sequence
-  const uint32_t* pos_dev;   // dense dev variant: seq_len = *pos_dev + 1
-  uint32_t seq_len;          // dense: the length (host variant) or the cache capacity (dev variant)
-  uint32_t cap;              // positions addressable (lengths are clamped to it)
+  const uint32_t* pos_dev;   // dense dev forms: seq_len = *pos_dev + 1
+  uint32_t seq_len;          // dense: the length (host form) or the cache capacity (dev forms)
+  uint32_t cap;              // lengths are clamped to it
   uint32_t nqh, nkh;
   float scale;
   uint32_t window;
-  uint32_t chunk;            // positions per split (multiple of the pass size)
+  uint32_t chunk;            // positions per split (= 32 * CP)
   uint32_t nsplit;           // splits per (sequence, kv head)
-  float* ws;                 // partials
+  float* ws;                 // partials: m, l, o
+  // fused form
+  const float* k_in;         // [nkh][hd] raw k projection
+  const float* v_in;         // [nkh][hd] raw v projection
+  const uint16_t* q_w;       // q_norm weight f16[hd]
+  const uint16_t* k_w;       // k_norm weight f16[hd]
+  const uint16_t* rope_freqs;
+  float theta;
+  uint32_t apply_divisor;
+  float eps;
 };
 
-// workspace: m, l then o, indexed by (seq, kvh, split, head-in-group)
-__host__ __device__ inline size_t ws_floats(uint32_t num_seqs, uint32_t nkh, uint32_t nsplit, uint32_t G,
-                                           uint32_t hd) {
-  return (size_t)num_seqs * nkh * nsplit * G * (hd + 2);
+__host__ __device__ inline size_t ws_bytes(uint32_t num_seqs, uint32_t nkh, uint32_t nsplit, uint32_t G,
+                                          uint32_t hd) {
+  return (size_t)num_seqs * nkh * nsplit * G * (hd + 2) * sizeof(float);
 }
 
-template <int G, int HD, int PPL, bool PAGED>
-__global__ __launch_bounds__(NT) void attn_split_kernel(AttnArgs a) {
-  constexpr int CH = 64 * PPL;             // positions per pass
-  constexpr int DPL = HD / 4;              // halves of a row per lane in the score phase
-  constexpr int QS = HD + HD / 16;         // padded q row (4 floats of pad per 64)
-  constexpr int DPV = HD / 64;             // dims per lane in the PV phase
+template <int HD>
+struct VMap {  // V columns / row groups per thread
+  static constexpr int VD = HD >= 512 ? HD / 256 : 1;   // adjacent columns per thread
+  static constexpr int VG = HD >= 256 ? 1 : 256 / HD;   // threads sharing a column (row groups)
+};
+
+template <int G, int HD, int CP, bool PAGED, bool FUSE>
+__global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
+  constexpr int P = 32 * CP;        // positions of a chunk
+  constexpr int KS = HD / 8;        // halves of a K row per slice lane
+  constexpr int KW = KS / 8;        // 16-byte words per slice
+  constexpr int QS = HD + 32;       // padded q row: 4 floats after each of the 8 slices
+  constexpr int VD = VMap<HD>::VD;
+  constexpr int VG = VMap<HD>::VG;
+  constexpr int VR = P / VG;        // rows of V per thread
+  static_assert(KS % 8 == 0 && VD <= 2, "layout");
   __shared__ __align__(16) float q_s[G * QS];
-  __shared__ __align__(16) float p_s[CH * G];      // [pos][head]
-  __shared__ __align__(16) float o_s[2 * G * HD];  // cross-wave fold
-  __shared__ float stat_s[2 * G];                  // pass max / sum per head
+  __shared__ __align__(16) float p_s[P * G];     // scores, then probabilities [pos][head]
+  __shared__ float stat_s[2 * G];
+  __shared__ float2 cs_s[FUSE ? HD / 2 : 1];
+  __shared__ float cur_s[FUSE ? 2 * HD : 1];     // current row: k (roped), v; f16-rounded
+  __shared__ float red_s[4 * (G + 2)];
+  __shared__ float o_s[VG > 1 ? G * HD : 1];
 
   const uint32_t split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -147,9 +185,9 @@ __global__ __launch_bounds__(NT) void attn_split_kernel(AttnArgs a) {
   const size_t part = (((size_t)seq * a.nkh + kvh) * a.nsplit + split) * G;
   const size_t nparts = (size_t)gridDim.z * a.nkh * a.nsplit * G;
   float* ws_m = a.ws;
-  float* ws_l = a.ws + nparts;
-  float* ws_o = a.ws + 2 * nparts;
-  if (b0 >= b1) {
+  float* ws_l = ws_m + nparts;
+  float* ws_o = ws_m + 2 * nparts;
+  if (b0 >= b1) {  // a split past the live length
     if (tid < G) {
       ws_m[part + tid] = -INFINITY;
       ws_l[part + tid] = 0.f;
@@ -157,217 +195,284 @@ __global__ __launch_bounds__(NT) void attn_split_kernel(AttnArgs a) {
     return;
   }
 
-  // stage q (G heads of this kv head) with a 16-byte pad every 64 floats
-  const float* qg = a.q + ((size_t)seq * a.nqh + (size_t)kvh * G) * HD;
-  for (int i = tid; i < G * HD; i += NT) {
-    const int h = i / HD, d = i % HD;
-    q_s[h * QS + d + (d >> 6) * 4] = qg[i];
-  }
-
-  auto row_ptr = [&](const uint16_t* base, uint32_t pos) -> const uint16_t* {
-    size_t row;
+  auto row_of = [&](uint32_t pos) -> size_t {
     if (PAGED) {
       int32_t pg = a.page_table[(size_t)seq * a.max_pages + pos / a.page_size];
       pg = pg < 0 ? 0 : (pg >= (int32_t)a.num_pages ? (int32_t)a.num_pages - 1 : pg);
-      row = (size_t)pg * a.page_size + pos % a.page_size;
-    } else {
-      row = pos;
+      return (size_t)pg * a.page_size + pos % a.page_size;
     }
-    return base + (row * a.nkh + kvh) * HD;
+    return pos;
   };
 
-  float m_run[G], l_run[G];
-  float o[G][DPV];
+  // ---- issue every K and V load of the chunk ----
+  const int ks = tid & 7;  // K slice
+  uint4 kraw[CP][KW];
+#pragma unroll
+  for (int c = 0; c < CP; ++c) {
+    const uint32_t pos = b0 + (uint32_t)(c * 32 + (tid >> 3));
+    if (pos < b1) {
+      const uint4* kp = (const uint4*)(a.kc + (row_of(pos) * a.nkh + kvh) * HD + ks * KS);
+#pragma unroll
+      for (int j = 0; j < KW; ++j) kraw[c][j] = kp[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < KW; ++j) kraw[c][j] = make_uint4(0, 0, 0, 0);
+    }
+  }
+  const int vcol = (tid % (HD / VD)) * VD;  // first column of this thread
+  const int vgrp = tid / (HD / VD);         // row group (VG > 1 only)
+  uint32_t vraw[VR];                        // VD f16 values per row (VD == 2: packed)
+#pragma unroll
+  for (int r = 0; r < VR; ++r) {
+    const uint32_t pos = b0 + (uint32_t)(r * VG + vgrp);
+    if (pos < b1) {
+      const uint16_t* vp = a.vc + (row_of(pos) * a.nkh + kvh) * HD + vcol;
+      vraw[r] = VD == 2 ? *(const uint32_t*)vp : (uint32_t)*vp;
+    } else {
+      vraw[r] = 0;
+    }
+  }
+
+  // ---- q for the G heads of this kv head -> q_s (slice-padded) ----
+  auto qidx = [](int h, int d) { return h * QS + d + (d / KS) * 4; };
+  const float* qg = a.q + ((size_t)seq * a.nqh + (size_t)kvh * G) * HD;
+  if constexpr (FUSE) {
+    const uint32_t pos = L - 1;  // the position being decoded
+    // RoPE for this position: frequency and angle in f32 as
+    // shaders/fused_per_head_norm_rope.wgsl:50-55 forms them; cos/sin in f64.
+    for (int i = tid; i < HD / 2; i += NT) {
+      float f = (float)(1.0 / pow((double)a.theta, (double)(2 * i) / (double)HD));
+      if (a.apply_divisor) f = f / g4d::f16_bits_to_f32(a.rope_freqs[i]);
+      const float ang = (float)pos * f;
+      cs_s[i] = make_float2((float)cos((double)ang), (float)sin((double)ang));
+    }
+    static_assert((G * HD) % NT == 0 && HD >= 256, "fused form: whole q heads per thread stride");
+    constexpr int QE = G * HD / NT;  // raw q elements per thread (t + 256k)
+    constexpr int KE = (HD + NT - 1) / NT;
+    const bool owner = b1 == L;      // this chunk holds the current position
+    float qv[QE], kx[KE], vx[KE];
+    float ss[G + 2];
+#pragma unroll
+    for (int h = 0; h < G + 2; ++h) ss[h] = 0.f;
+#pragma unroll
+    for (int k = 0; k < QE; ++k) {
+      const int i = tid + k * NT;
+      qv[k] = qg[i];
+      ss[i / HD] += qv[k] * qv[k];
+    }
+#pragma unroll
+    for (int k = 0; k < KE; ++k) {
+      const int i = tid + k * NT;
+      kx[k] = (owner && i < HD) ? a.k_in[(size_t)kvh * HD + i] : 0.f;
+      vx[k] = (owner && i < HD) ? a.v_in[(size_t)kvh * HD + i] : 0.f;
+      ss[G] += kx[k] * kx[k];
+      ss[G + 1] += vx[k] * vx[k];
+    }
+#pragma unroll
+    for (int h = 0; h < G + 2; ++h) {
+      const float t = g4d::wave_sum(ss[h]);
+      if (lane == 0) red_s[w * (G + 2) + h] = t;
+    }
+    __syncthreads();
+    float inv[G + 2];
+#pragma unroll
+    for (int h = 0; h < G + 2; ++h) {
+      const float tot = red_s[h] + red_s[(G + 2) + h] + red_s[2 * (G + 2) + h] + red_s[3 * (G + 2) + h];
+      inv[h] = 1.0f / sqrtf(tot / (float)HD + a.eps);
+    }
+#pragma unroll
+    for (int k = 0; k < QE; ++k) {
+      const int i = tid + k * NT, h = i / HD, d = i % HD;
+      q_s[qidx(h, d)] = qv[k] * g4d::f16_bits_to_f32(a.q_w[d]) * inv[h];
+    }
+    if (owner) {
+#pragma unroll
+      for (int k = 0; k < KE; ++k) {
+        const int i = tid + k * NT;
+        if (i < HD) {
+          cur_s[i] = kx[k] * g4d::f16_bits_to_f32(a.k_w[i]) * inv[G];
+          const uint16_t vb = g4d::f32_to_f16_bits(vx[k] * inv[G + 1]);
+          cur_s[HD + i] = g4d::f16_bits_to_f32(vb);
+          a.vc_w[(row_of(pos) * a.nkh + kvh) * HD + i] = vb;
+        }
+      }
+    }
+    __syncthreads();
+    // rotate-half over pairs (i, i + HD/2): the G q heads, and k in the owner
+    for (int j = tid; j < (G + (owner ? 1 : 0)) * HD / 2; j += NT) {
+      const int h = j / (HD / 2), i = j % (HD / 2);
+      const float2 cs = cs_s[i];
+      if (h < G) {
+        float* p0 = q_s + qidx(h, i);
+        float* p1 = q_s + qidx(h, i + HD / 2);
+        const float x0 = *p0, x1 = *p1;
+        *p0 = x0 * cs.x - x1 * cs.y;
+        *p1 = x0 * cs.y + x1 * cs.x;
+      } else {
+        const float x0 = cur_s[i], x1 = cur_s[i + HD / 2];
+        const uint16_t k0 = g4d::f32_to_f16_bits(x0 * cs.x - x1 * cs.y);
+        const uint16_t k1 = g4d::f32_to_f16_bits(x0 * cs.y + x1 * cs.x);
+        uint16_t* kdst = a.kc_w + (row_of(pos) * a.nkh + kvh) * HD;
+        kdst[i] = k0;
+        kdst[i + HD / 2] = k1;
+        cur_s[i] = g4d::f16_bits_to_f32(k0);  // as the cache row will read back
+        cur_s[i + HD / 2] = g4d::f16_bits_to_f32(k1);
+      }
+    }
+    __syncthreads();
+    // the current row was loaded from the cache before it was written: take it from LDS
+    if (owner) {
+      const uint32_t pc = pos - b0;
+#pragma unroll
+      for (int c = 0; c < CP; ++c) {
+        if ((uint32_t)(c * 32 + (tid >> 3)) == pc) {
+#pragma unroll
+          for (int j = 0; j < KW; ++j) {
+            uint32_t wd[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int d = ks * KS + 8 * j + 2 * e;
+              wd[e] = (uint32_t)g4d::f32_to_f16_bits(cur_s[d]) | ((uint32_t)g4d::f32_to_f16_bits(cur_s[d + 1]) << 16);
+            }
+            kraw[c][j] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < VR; ++r) {
+        if ((uint32_t)(r * VG + vgrp) == pc) {
+          const uint32_t v0 = g4d::f32_to_f16_bits(cur_s[HD + vcol]);
+          vraw[r] = VD == 2 ? (v0 | ((uint32_t)g4d::f32_to_f16_bits(cur_s[HD + vcol + 1]) << 16)) : v0;
+        }
+      }
+    }
+  } else {
+    for (int i = tid; i < G * HD; i += NT) q_s[qidx(i / HD, i % HD)] = qg[i];
+    __syncthreads();
+  }
+
+  // ---- scores: slice lanes (8 per row) ----
+#pragma unroll
+  for (int c = 0; c < CP; ++c) {
+    float acc[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) acc[h] = 0.f;
+#pragma unroll
+    for (int j = 0; j < KW; ++j) {
+      const uint32_t wd[4] = {kraw[c][j].x, kraw[c][j].y, kraw[c][j].z, kraw[c][j].w};
+      float kf[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kf[2 * e] = g4d::f16_bits_to_f32(wd[e] & 0xffffu);
+        kf[2 * e + 1] = g4d::f16_bits_to_f32(wd[e] >> 16);
+      }
+      const int d0 = ks * KS + 8 * j;
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float4 q0 = *(const float4*)(q_s + qidx(h, d0));
+        const float4 q1 = *(const float4*)(q_s + qidx(h, d0 + 4));
+        acc[h] += q0.x * kf[0] + q0.y * kf[1] + q0.z * kf[2] + q0.w * kf[3];
+        acc[h] += q1.x * kf[4] + q1.y * kf[5] + q1.z * kf[6] + q1.w * kf[7];
+      }
+    }
+    const uint32_t pos = b0 + (uint32_t)(c * 32 + (tid >> 3));
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float v = acc[h];
+      v += __shfl_xor(v, 1, 64);
+      v += __shfl_xor(v, 2, 64);
+      v += __shfl_xor(v, 4, 64);
+      acc[h] = pos < b1 ? v * a.scale : -INFINITY;
+    }
+    if (ks == 0) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) p_s[(c * 32 + (tid >> 3)) * G + h] = acc[h];
+    }
+  }
+  __syncthreads();
+
+  // ---- chunk softmax statistics per head ----
+  constexpr int SL = (NT / G) < 64 ? (NT / G) : 64;
+  if (tid < G * SL) {
+    const int h = tid / SL, sl = tid % SL;
+    float mx = -INFINITY;
+    for (int i = sl; i < P; i += SL) mx = fmaxf(mx, p_s[i * G + h]);
+#pragma unroll
+    for (int off = SL / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    float sum = 0.f;
+    for (int i = sl; i < P; i += SL) {
+      const float e = expf(p_s[i * G + h] - mx);  // rows past the chunk: exp(-inf) = 0
+      p_s[i * G + h] = e;
+      sum += e;
+    }
+#pragma unroll
+    for (int off = SL / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    if (sl == 0) {
+      stat_s[h] = mx;
+      stat_s[G + h] = sum;
+    }
+  }
+  __syncthreads();
+
+  // ---- o for this thread's columns over the chunk's rows ----
+  float o[G][VD];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int j = 0; j < VD; ++j) o[h][j] = 0.f;
+#pragma unroll
+  for (int r = 0; r < VR; ++r) {
+    const int pi = r * VG + vgrp;
+    float vf[VD];
+    vf[0] = g4d::f16_bits_to_f32(vraw[r] & 0xffffu);
+    if constexpr (VD == 2) vf[1] = g4d::f16_bits_to_f32(vraw[r] >> 16);
+    const float4* pp = (const float4*)(p_s + pi * G);
+    float pv[G];
+#pragma unroll
+    for (int h4 = 0; h4 < G / 4; ++h4) {
+      const float4 t = pp[h4];
+      pv[4 * h4] = t.x; pv[4 * h4 + 1] = t.y; pv[4 * h4 + 2] = t.z; pv[4 * h4 + 3] = t.w;
+    }
+    if constexpr (G % 4 != 0) {
+#pragma unroll
+      for (int h = (G / 4) * 4; h < G; ++h) pv[h] = p_s[pi * G + h];
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int j = 0; j < VD; ++j) o[h][j] += pv[h] * vf[j];
+  }
+  if constexpr (VG > 1) {  // head_dim 128: two row groups per column
+    if (vgrp == 1) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) o_s[h * HD + vcol] = o[h][0];
+    }
+    __syncthreads();
+    if (vgrp != 0) return;
+#pragma unroll
+    for (int h = 0; h < G; ++h) o[h][0] += o_s[h * HD + vcol];
+  }
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    m_run[h] = -INFINITY;
-    l_run[h] = 0.f;
+    float* dst = ws_o + (part + h) * HD + vcol;
 #pragma unroll
-    for (int j = 0; j < DPV; ++j) o[h][j] = 0.f;
+    for (int j = 0; j < VD; ++j) dst[j] = o[h][j];
   }
-  __syncthreads();
-
-  const int qd = lane & 3;   // quarter of the head dimension
-  const int pl = lane >> 2;  // position slot within the wave
-  for (uint32_t pass0 = b0; pass0 < b1; pass0 += CH) {
-    // ---- scores: lane = (position, quarter); PPL positions per lane ----
-    float acc[PPL][G];
-    uint32_t pos[PPL];
-    bool valid[PPL];
-#pragma unroll
-    for (int j = 0; j < PPL; ++j) {
-      pos[j] = pass0 + (uint32_t)(j * 64 + w * 16 + pl);
-      valid[j] = pos[j] < b1;
-#pragma unroll
-      for (int h = 0; h < G; ++h) acc[j][h] = 0.f;
-    }
-#pragma unroll
-    for (int db = 0; db < DPL / 32; ++db) {
-      float kf[PPL][32];
-#pragma unroll
-      for (int j = 0; j < PPL; ++j) {
-        if (valid[j]) {
-          const uint4* kp = (const uint4*)(row_ptr(a.kc, pos[j]) + qd * DPL + db * 32);
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const uint4 t = kp[c];
-            const uint32_t wd[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              kf[j][8 * c + 2 * i] = g4d::f16_bits_to_f32(wd[i] & 0xffffu);
-              kf[j][8 * c + 2 * i + 1] = g4d::f16_bits_to_f32(wd[i] >> 16);
-            }
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 32; ++i) kf[j][i] = 0.f;
-        }
-      }
-      const int dbase = qd * DPL + db * 32;
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float* qr = q_s + h * QS + dbase + (dbase >> 6) * 4;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const float4 qv = *(const float4*)(qr + 4 * c);
-#pragma unroll
-          for (int j = 0; j < PPL; ++j) {
-            acc[j][h] += qv.x * kf[j][4 * c] + qv.y * kf[j][4 * c + 1];
-            acc[j][h] += qv.z * kf[j][4 * c + 2] + qv.w * kf[j][4 * c + 3];
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < PPL; ++j) {
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        float v = acc[j][h];
-        v += __shfl_xor(v, 1, 64);
-        v += __shfl_xor(v, 2, 64);
-        acc[j][h] = valid[j] ? v * a.scale : -INFINITY;
-      }
-      if (qd == 0) {
-        const int pi = j * 64 + w * 16 + pl;
-#pragma unroll
-        for (int h = 0; h < G; ++h) p_s[pi * G + h] = acc[j][h];
-      }
-    }
-    __syncthreads();
-    // ---- pass max per head, online rescale, probabilities ----
-    // thread -> (head, slot): G heads x SL slots over CH positions; SL <= 64
-    // so a head's slots sit in one wave and whole waves are idle or busy.
-    constexpr int SL = (NT / G) < 64 ? (NT / G) : 64;
-    if (tid < G * SL) {
-      const int h = tid / SL, sl = tid % SL;
-      float mx = -INFINITY;
-      for (int i = sl; i < CH; i += SL) mx = fmaxf(mx, p_s[i * G + h]);
-#pragma unroll
-      for (int off = SL / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-      if (sl == 0) stat_s[h] = mx;
-    }
-    __syncthreads();
-    float alpha[G];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float m_new = fmaxf(m_run[h], stat_s[h]);
-      alpha[h] = expf(m_run[h] - m_new);  // 0 on the first pass (m_run = -inf)
-      m_run[h] = m_new;
-    }
-    if (tid < G * SL) {
-      const int h = tid / SL, sl = tid % SL;
-      float sum = 0.f;
-      for (int i = sl; i < CH; i += SL) {
-        const float e = expf(p_s[i * G + h] - m_run[h]);  // masked: exp(-inf) = 0
-        p_s[i * G + h] = e;
-        sum += e;
-      }
-#pragma unroll
-      for (int off = SL / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-      if (sl == 0) stat_s[G + h] = sum;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      l_run[h] = l_run[h] * alpha[h] + stat_s[G + h];
-#pragma unroll
-      for (int j = 0; j < DPV; ++j) o[h][j] *= alpha[h];
-    }
-    // ---- PV: lane owns DPV dims, wave w takes positions w, w+4, ... ----
-    const int npos = (b1 - pass0) < (uint32_t)CH ? (int)(b1 - pass0) : CH;
-    for (int i = w; i < npos; i += 4) {
-      const uint16_t* vp = row_ptr(a.vc, pass0 + (uint32_t)i) + lane * DPV;
-      float vf[DPV];
-      if constexpr (DPV == 4) {
-        const uint2 t = *(const uint2*)vp;
-        vf[0] = g4d::f16_bits_to_f32(t.x & 0xffffu);
-        vf[1] = g4d::f16_bits_to_f32(t.x >> 16);
-        vf[2] = g4d::f16_bits_to_f32(t.y & 0xffffu);
-        vf[3] = g4d::f16_bits_to_f32(t.y >> 16);
-      } else {
-#pragma unroll
-        for (int c = 0; c < DPV / 8; ++c) {
-          const uint4 t = *(const uint4*)(vp + 8 * c);
-          const uint32_t wd[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            vf[8 * c + 2 * k] = g4d::f16_bits_to_f32(wd[k] & 0xffffu);
-            vf[8 * c + 2 * k + 1] = g4d::f16_bits_to_f32(wd[k] >> 16);
-          }
-        }
-      }
-      const float* pp = p_s + i * G;
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float pv = pp[h];
-#pragma unroll
-        for (int j = 0; j < DPV; ++j) o[h][j] += pv * vf[j];
-      }
-    }
-    __syncthreads();  // p_s is rewritten by the next pass
-  }
-
-  // ---- fold the 4 waves' o (fixed order: (w2+w0) + (w3+w1), then + ) ----
-  if (w >= 2) {
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int j = 0; j < DPV; ++j) o_s[((w - 2) * G + h) * HD + lane * DPV + j] = o[h][j];
-  }
-  __syncthreads();
-  if (w < 2) {
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int j = 0; j < DPV; ++j) o[h][j] += o_s[(w * G + h) * HD + lane * DPV + j];
-  }
-  __syncthreads();
-  if (w == 1) {
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int j = 0; j < DPV; ++j) o_s[h * HD + lane * DPV + j] = o[h][j];
-  }
-  __syncthreads();
-  if (w == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float* dst = ws_o + (part + h) * HD + lane * DPV;
-#pragma unroll
-      for (int j = 0; j < DPV; ++j) dst[j] = o[h][j] + o_s[h * HD + lane * DPV + j];
-    }
-    if (lane < G) {
-      ws_m[part + lane] = m_run[lane];
-      ws_l[part + lane] = l_run[lane];
-    }
+  if (tid < G) {
+    ws_m[part + tid] = stat_s[tid];
+    ws_l[part + tid] = stat_s[G + tid];
   }
 }
 
-// Merge the splits of one (sequence, query head): O = sum_s o_s e^(m_s - M) /
-// sum_s l_s e^(m_s - M); empty splits (l = 0) are skipped.
-__global__ __launch_bounds__(NT) void attn_combine_kernel(const float* ws, float* out, uint32_t nqh, uint32_t nkh,
-                                                          uint32_t G, uint32_t hd, uint32_t nsplit,
-                                                          uint32_t num_seqs) {
+// Merge the splits of one (sequence, query head):
+// O = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M); empty splits (l = 0) drop out.
+// The per-split weights are formed in parallel first, then every thread
+// streams its columns of all splits with independent loads.
+__global__ __launch_bounds__(NT) void attn_merge_kernel(const float* ws, float* out, uint32_t nqh, uint32_t nkh,
+                                                        uint32_t G, uint32_t hd, uint32_t nsplit,
+                                                        uint32_t num_seqs) {
+  __shared__ float wgt_s[1024];
+  __shared__ float red_s[8];
   const uint32_t hq = blockIdx.x, seq = blockIdx.y;
   const uint32_t kvh = hq / G, h = hq % G;
   const size_t nparts = (size_t)num_seqs * nkh * nsplit * G;
@@ -375,26 +480,39 @@ __global__ __launch_bounds__(NT) void attn_combine_kernel(const float* ws, float
   const float* ws_l = ws + nparts;
   const float* ws_o = ws + 2 * nparts;
   const size_t base = ((size_t)seq * nkh + kvh) * nsplit * G + h;
-  float M = -INFINITY;
-  for (uint32_t s = 0; s < nsplit; ++s)
-    if (ws_l[base + (size_t)s * G] > 0.f) M = fmaxf(M, ws_m[base + (size_t)s * G]);
-  float Lsum = 0.f;
-  float acc0 = 0.f, acc1 = 0.f;
-  const uint32_t d0 = threadIdx.x, d1 = threadIdx.x + NT;
-  for (uint32_t s = 0; s < nsplit; ++s) {
-    const size_t pi = base + (size_t)s * G;
-    const float l = ws_l[pi];
-    if (!(l > 0.f)) continue;
-    const float wgt = expf(ws_m[pi] - M);
-    Lsum += l * wgt;
-    const float* op = ws_o + pi * hd;
-    if (d0 < hd) acc0 += op[d0] * wgt;
-    if (d1 < hd) acc1 += op[d1] * wgt;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // global max over live splits
+  float mx = -INFINITY;
+  for (uint32_t s = tid; s < nsplit; s += NT) {
+    const float l = ws_l[base + (size_t)s * G];
+    if (l > 0.f) mx = fmaxf(mx, ws_m[base + (size_t)s * G]);
   }
-  const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
+  mx = g4d::wave_max(mx);
+  if (lane == 0) red_s[w] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red_s[0], red_s[1]), fmaxf(red_s[2], red_s[3]));
+  __syncthreads();
+  float lsum = 0.f;
+  for (uint32_t s = tid; s < nsplit; s += NT) {
+    const float l = ws_l[base + (size_t)s * G];
+    const float wt = l > 0.f ? expf(ws_m[base + (size_t)s * G] - M) : 0.f;
+    if (s < 1024) wgt_s[s] = wt;
+    lsum += l * wt;
+  }
+  lsum = g4d::block_sum<4>(lsum, red_s);
+  const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
   float* dst = out + ((size_t)seq * nqh + hq) * hd;
-  if (d0 < hd) dst[d0] = acc0 * inv;
-  if (d1 < hd) dst[d1] = acc1 * inv;
+  for (uint32_t d = tid; d < hd; d += NT) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    uint32_t s = 0;
+    for (; s + 4 <= nsplit; s += 4) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        acc[u] += ws_o[(base + (size_t)(s + u) * G) * hd + d] * wgt_s[s + u];
+    }
+    for (; s < nsplit; ++s) acc[0] += ws_o[(base + (size_t)s * G) * hd + d] * wgt_s[s];
+    dst[d] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) * inv;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -419,28 +537,25 @@ __global__ __launch_bounds__(NT) void paged_store_kernel(const float* k_in, cons
 }
 
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 
+constexpr uint32_t kMaxSplits = 1024;  // merge kernel limit; 64 * 1024 = 65536 positions
+
 struct SplitPlan {
-  int ppl;
-  uint32_t chunk;
+  int cp;           // 32-position blocks per split (1 or 2)
+  uint32_t chunk;   // positions per split
   uint32_t nsplit;
 };
 
-// Pass size 64 (one position per lane) up to 64 splits, then 128-position
-// passes with as many passes per split as keep the grid near 256 splits.
+// 32-position splits up to 16K positions (at most 512 splits), 64-position
+// splits beyond.
 SplitPlan plan_splits(uint32_t l_eff) {
   SplitPlan p;
   if (l_eff == 0) l_eff = 1;
-  if (l_eff <= 64 * 64) {
-    p.ppl = 1;
-    p.chunk = 64;
-  } else {
-    p.ppl = 2;
-    const uint32_t passes = ceil_div(ceil_div(l_eff, 128), 256);
-    p.chunk = 128 * passes;
-  }
+  p.cp = l_eff <= 16384 ? 1 : 2;
+  p.chunk = 32u * (uint32_t)p.cp;
   p.nsplit = ceil_div(l_eff, p.chunk);
   return p;
 }
@@ -449,31 +564,41 @@ uint32_t eff_len(uint32_t seq_len, uint32_t window) {
   return (window != 0 && seq_len > window) ? window : seq_len;
 }
 
-template <int G, int HD, bool PAGED>
-int launch_split_hd(g4_ctx* ctx, const AttnArgs& a, int ppl, dim3 grid) {
-  if (ppl == 1) hipLaunchKernelGGL((attn_split_kernel<G, HD, 1, PAGED>), grid, dim3(NT), 0, ctx->stream, a);
-  else hipLaunchKernelGGL((attn_split_kernel<G, HD, 2, PAGED>), grid, dim3(NT), 0, ctx->stream, a);
-  G4_LAUNCHED(ctx, "attn_split");
+template <int G, int HD, bool PAGED, bool FUSE>
+int launch_hd(g4_ctx* ctx, const AttnArgs& a, int cp, dim3 grid) {
+  if (cp == 1) hipLaunchKernelGGL((attn_kernel<G, HD, 1, PAGED, FUSE>), grid, dim3(NT), 0, ctx->stream, a);
+  else hipLaunchKernelGGL((attn_kernel<G, HD, 2, PAGED, FUSE>), grid, dim3(NT), 0, ctx->stream, a);
+  G4_LAUNCHED(ctx, "attn_decode");
   return G4_OK;
 }
 
-template <bool PAGED>
-int launch_split(g4_ctx* ctx, const AttnArgs& a, uint32_t G, uint32_t hd, int ppl, dim3 grid) {
+template <bool PAGED, bool FUSE>
+int launch_attn(g4_ctx* ctx, const AttnArgs& a, uint32_t G, uint32_t hd, int cp, dim3 grid) {
 #define G4_ATTN_CASE(g, h) \
-  if (G == g && hd == h) return launch_split_hd<g, h, PAGED>(ctx, a, ppl, grid);
+  if (G == g && hd == h) return launch_hd<g, h, PAGED, FUSE>(ctx, a, cp, grid);
   G4_ATTN_CASE(8, 256)
   G4_ATTN_CASE(8, 512)
-  G4_ATTN_CASE(8, 128)
-  G4_ATTN_CASE(4, 256)
-  G4_ATTN_CASE(4, 512)
-  G4_ATTN_CASE(4, 128)
-  G4_ATTN_CASE(2, 256)
-  G4_ATTN_CASE(2, 128)
-  G4_ATTN_CASE(1, 256)
-  G4_ATTN_CASE(1, 128)
+  if constexpr (!FUSE) {
+    G4_ATTN_CASE(8, 128)
+    G4_ATTN_CASE(4, 256)
+    G4_ATTN_CASE(4, 512)
+    G4_ATTN_CASE(4, 128)
+    G4_ATTN_CASE(2, 256)
+    G4_ATTN_CASE(2, 128)
+    G4_ATTN_CASE(1, 256)
+    G4_ATTN_CASE(1, 128)
+  }
 #undef G4_ATTN_CASE
   return g4::set_error(G4_ERR_UNSUPPORTED, "attention: %u query heads per kv head with head_dim %u not built", G,
                        hd);
+}
+
+int merge(g4_ctx* ctx, const AttnArgs& a, float* out, const SplitPlan& sp, uint32_t num_seqs, uint32_t G,
+          uint32_t hd) {
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(a.nqh, num_seqs), dim3(NT), 0, ctx->stream, (const float*)a.ws, out,
+                     a.nqh, a.nkh, G, hd, sp.nsplit, num_seqs);
+  G4_LAUNCHED(ctx, "attn_merge");
+  return G4_OK;
 }
 
 int check_heads(const char* fn, uint32_t nqh, uint32_t nkh, uint32_t hd) {
@@ -483,37 +608,51 @@ int check_heads(const char* fn, uint32_t nqh, uint32_t nkh, uint32_t hd) {
   return G4_OK;
 }
 
-int dense_decode(g4_ctx* ctx, const char* fn, const float* q, const uint16_t* kc, const uint16_t* vc, float* out,
-                 g4_attn_score_params p, void* ws, size_t ws_bytes, const uint32_t* pos_dev) {
-  G4_REQUIRE(q && kc && vc && out && ws, "%s: null buffer", fn);
-  G4_REQUIRE(((uintptr_t)kc & 15) == 0 && ((uintptr_t)vc & 15) == 0, "%s: KV caches must be 16-byte aligned", fn);
-  int rc = check_heads(fn, p.num_q_heads, p.num_kv_heads, p.head_dim);
-  if (rc) return rc;
-  G4_REQUIRE(p.seq_len > 0, "%s: seq_len must be >= 1", fn);
-  const uint32_t G = p.num_q_heads / p.num_kv_heads;
-  const SplitPlan sp = plan_splits(eff_len(p.seq_len, p.sliding_window));
-  const size_t need = ws_floats(1, p.num_kv_heads, sp.nsplit, G, p.head_dim) * sizeof(float);
-  G4_REQUIRE(ws_bytes >= need, "%s: workspace %zu bytes < %zu required", fn, ws_bytes, need);
+int check_plan(const char* fn, const SplitPlan& sp) {
+  G4_REQUIRE(sp.nsplit <= kMaxSplits, "%s: %u positions exceed the %u-position limit of one decode call", fn,
+             sp.nsplit * sp.chunk, kMaxSplits * 64);
+  return G4_OK;
+}
+
+AttnArgs dense_args(const float* q, const uint16_t* kc, const uint16_t* vc, uint32_t nqh, uint32_t nkh,
+                    uint32_t seq_len, float scale, uint32_t window, const SplitPlan& sp, void* ws,
+                    const uint32_t* pos_dev) {
   AttnArgs a{};
   a.q = q;
   a.kc = kc;
   a.vc = vc;
   a.pos_dev = pos_dev;
-  a.seq_len = p.seq_len;
-  a.cap = p.seq_len;
-  a.nqh = p.num_q_heads;
-  a.nkh = p.num_kv_heads;
-  a.scale = p.scale;
-  a.window = p.sliding_window;
+  a.seq_len = seq_len;
+  a.cap = seq_len;
+  a.nqh = nqh;
+  a.nkh = nkh;
+  a.scale = scale;
+  a.window = window;
   a.chunk = sp.chunk;
   a.nsplit = sp.nsplit;
   a.ws = (float*)ws;
-  rc = launch_split<false>(ctx, a, G, p.head_dim, sp.ppl, dim3(sp.nsplit, p.num_kv_heads, 1));
+  return a;
+}
+
+int dense_decode(g4_ctx* ctx, const char* fn, const float* q, const uint16_t* kc, const uint16_t* vc, float* out,
+                 g4_attn_score_params p, void* ws, size_t ws_len, const uint32_t* pos_dev) {
+  G4_REQUIRE(q && kc && vc && out && ws, "%s: null buffer", fn);
+  G4_REQUIRE(((uintptr_t)kc & 15) == 0 && ((uintptr_t)vc & 15) == 0 && ((uintptr_t)ws & 15) == 0,
+             "%s: KV caches and workspace must be 16-byte aligned", fn);
+  int rc = check_heads(fn, p.num_q_heads, p.num_kv_heads, p.head_dim);
   if (rc) return rc;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(p.num_q_heads, 1), dim3(NT), 0, ctx->stream, (const float*)ws, out,
-                     p.num_q_heads, p.num_kv_heads, G, p.head_dim, sp.nsplit, 1u);
-  G4_LAUNCHED(ctx, "attn_combine");
-  return G4_OK;
+  G4_REQUIRE(p.seq_len > 0, "%s: seq_len must be >= 1", fn);
+  const uint32_t G = p.num_q_heads / p.num_kv_heads;
+  const SplitPlan sp = plan_splits(eff_len(p.seq_len, p.sliding_window));
+  rc = check_plan(fn, sp);
+  if (rc) return rc;
+  const size_t need = ws_bytes(1, p.num_kv_heads, sp.nsplit, G, p.head_dim);
+  G4_REQUIRE(ws_len >= need, "%s: workspace %zu bytes < %zu required", fn, ws_len, need);
+  const AttnArgs a = dense_args(q, kc, vc, p.num_q_heads, p.num_kv_heads, p.seq_len, p.scale, p.sliding_window,
+                                sp, ws, pos_dev);
+  rc = launch_attn<false, false>(ctx, a, G, p.head_dim, sp.cp, dim3(sp.nsplit, p.num_kv_heads, 1));
+  if (rc) return rc;
+  return merge(ctx, a, out, sp, 1, G, p.head_dim);
 }
 
 }  // namespace
@@ -555,7 +694,9 @@ int g4_attnDecode_workspace_size(g4_attn_score_params p, size_t* bytes) {
   int rc = check_heads(__func__, p.num_q_heads, p.num_kv_heads, p.head_dim);
   if (rc) return rc;
   const SplitPlan sp = plan_splits(eff_len(p.seq_len, p.sliding_window));
-  *bytes = ws_floats(1, p.num_kv_heads, sp.nsplit, p.num_q_heads / p.num_kv_heads, p.head_dim) * sizeof(float);
+  rc = check_plan(__func__, sp);
+  if (rc) return rc;
+  *bytes = ws_bytes(1, p.num_kv_heads, sp.nsplit, p.num_q_heads / p.num_kv_heads, p.head_dim);
   return G4_OK;
 }
 
@@ -574,13 +715,65 @@ int g4_attnDecode_dev(g4_ctx* ctx, const float* q, const uint16_t* k_cache, cons
   return dense_decode(ctx, __func__, q, k_cache, v_cache, output, p, workspace, workspace_bytes, position_dev);
 }
 
+int g4_attnDecodeFused_workspace_size(g4_attn_fused_params p, size_t* bytes) {
+  G4_REQUIRE(bytes, "g4_attnDecodeFused_workspace_size: null out");
+  int rc = check_heads(__func__, p.num_q_heads, p.num_kv_heads, p.head_dim);
+  if (rc) return rc;
+  const SplitPlan sp = plan_splits(eff_len(p.max_seq_len, p.sliding_window));
+  rc = check_plan(__func__, sp);
+  if (rc) return rc;
+  *bytes = ws_bytes(1, p.num_kv_heads, sp.nsplit, p.num_q_heads / p.num_kv_heads, p.head_dim);
+  return G4_OK;
+}
+
+int g4_attnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float* v_raw,
+                       const uint16_t* q_norm_w, const uint16_t* k_norm_w, const uint16_t* rope_freqs,
+                       uint16_t* k_cache, uint16_t* v_cache, float* output, g4_attn_fused_params p, void* workspace,
+                       size_t workspace_bytes, const uint32_t* position_dev) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(q_raw && k_raw && v_raw && q_norm_w && k_norm_w && k_cache && v_cache && output && workspace &&
+                 position_dev,
+             "g4_attnDecodeFused: null buffer");
+  G4_REQUIRE(!p.apply_divisor || rope_freqs, "g4_attnDecodeFused: apply_divisor needs rope_freqs");
+  G4_REQUIRE(((uintptr_t)k_cache & 15) == 0 && ((uintptr_t)v_cache & 15) == 0 && ((uintptr_t)workspace & 15) == 0,
+             "g4_attnDecodeFused: KV caches and workspace must be 16-byte aligned");
+  int rc = check_heads(__func__, p.num_q_heads, p.num_kv_heads, p.head_dim);
+  if (rc) return rc;
+  G4_REQUIRE(p.max_seq_len > 0, "g4_attnDecodeFused: max_seq_len must be >= 1");
+  const uint32_t G = p.num_q_heads / p.num_kv_heads;
+  G4_REQUIRE(G == 8 && (p.head_dim == 256 || p.head_dim == 512),
+             "g4_attnDecodeFused: built for 8 query heads per kv head and head_dim 256/512");
+  const SplitPlan sp = plan_splits(eff_len(p.max_seq_len, p.sliding_window));
+  rc = check_plan(__func__, sp);
+  if (rc) return rc;
+  const size_t need = ws_bytes(1, p.num_kv_heads, sp.nsplit, G, p.head_dim);
+  G4_REQUIRE(workspace_bytes >= need, "g4_attnDecodeFused: workspace %zu bytes < %zu required", workspace_bytes,
+             need);
+  AttnArgs a = dense_args(q_raw, k_cache, v_cache, p.num_q_heads, p.num_kv_heads, p.max_seq_len, p.scale,
+                          p.sliding_window, sp, workspace, position_dev);
+  a.kc_w = k_cache;
+  a.vc_w = v_cache;
+  a.k_in = k_raw;
+  a.v_in = v_raw;
+  a.q_w = q_norm_w;
+  a.k_w = k_norm_w;
+  a.rope_freqs = rope_freqs;
+  a.theta = p.theta;
+  a.apply_divisor = p.apply_divisor;
+  a.eps = p.eps;
+  rc = launch_attn<false, true>(ctx, a, G, p.head_dim, sp.cp, dim3(sp.nsplit, p.num_kv_heads, 1));
+  if (rc) return rc;
+  return merge(ctx, a, output, sp, 1, G, p.head_dim);
+}
+
 int g4_pagedAttnDecode_workspace_size(g4_paged_attn_params p, size_t* bytes) {
   G4_REQUIRE(bytes, "g4_pagedAttnDecode_workspace_size: null out");
   int rc = check_heads(__func__, p.num_q_heads, p.num_kv_heads, p.head_dim);
   if (rc) return rc;
   const SplitPlan sp = plan_splits(eff_len(p.max_seq_len, p.sliding_window));
-  *bytes = ws_floats(p.num_seqs, p.num_kv_heads, sp.nsplit, p.num_q_heads / p.num_kv_heads, p.head_dim) *
-           sizeof(float);
+  rc = check_plan(__func__, sp);
+  if (rc) return rc;
+  *bytes = ws_bytes(p.num_seqs, p.num_kv_heads, sp.nsplit, p.num_q_heads / p.num_kv_heads, p.head_dim);
   return G4_OK;
 }
 
@@ -590,8 +783,8 @@ int g4_pagedAttnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_pool, cons
   G4_ENTER(ctx);
   G4_REQUIRE(q && k_pool && v_pool && page_table && seq_lens && output && workspace,
              "g4_pagedAttnDecode: null buffer");
-  G4_REQUIRE(((uintptr_t)k_pool & 15) == 0 && ((uintptr_t)v_pool & 15) == 0,
-             "g4_pagedAttnDecode: KV pools must be 16-byte aligned");
+  G4_REQUIRE(((uintptr_t)k_pool & 15) == 0 && ((uintptr_t)v_pool & 15) == 0 && ((uintptr_t)workspace & 15) == 0,
+             "g4_pagedAttnDecode: KV pools and workspace must be 16-byte aligned");
   int rc = check_heads(__func__, p.num_q_heads, p.num_kv_heads, p.head_dim);
   if (rc) return rc;
   G4_REQUIRE(p.num_seqs > 0 && p.page_size > 0 && p.max_pages > 0 && p.num_pages > 0,
@@ -601,7 +794,9 @@ int g4_pagedAttnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_pool, cons
              p.page_size);
   const uint32_t G = p.num_q_heads / p.num_kv_heads;
   const SplitPlan sp = plan_splits(eff_len(p.max_seq_len, p.sliding_window));
-  const size_t need = ws_floats(p.num_seqs, p.num_kv_heads, sp.nsplit, G, p.head_dim) * sizeof(float);
+  rc = check_plan(__func__, sp);
+  if (rc) return rc;
+  const size_t need = ws_bytes(p.num_seqs, p.num_kv_heads, sp.nsplit, G, p.head_dim);
   G4_REQUIRE(workspace_bytes >= need, "g4_pagedAttnDecode: workspace %zu bytes < %zu required", workspace_bytes,
              need);
   AttnArgs a{};
@@ -621,13 +816,9 @@ int g4_pagedAttnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_pool, cons
   a.chunk = sp.chunk;
   a.nsplit = sp.nsplit;
   a.ws = (float*)workspace;
-  rc = launch_split<true>(ctx, a, G, p.head_dim, sp.ppl, dim3(sp.nsplit, p.num_kv_heads, p.num_seqs));
+  rc = launch_attn<true, false>(ctx, a, G, p.head_dim, sp.cp, dim3(sp.nsplit, p.num_kv_heads, p.num_seqs));
   if (rc) return rc;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(p.num_q_heads, p.num_seqs), dim3(NT), 0, ctx->stream,
-                     (const float*)workspace, output, p.num_q_heads, p.num_kv_heads, G, p.head_dim, sp.nsplit,
-                     p.num_seqs);
-  G4_LAUNCHED(ctx, "attn_combine");
-  return G4_OK;
+  return merge(ctx, a, output, sp, p.num_seqs, G, p.head_dim);
 }
 
 int g4_pagedKvStore(g4_ctx* ctx, const float* k_in, const float* v_in, uint16_t* k_pool, uint16_t* v_pool,

@@ -17,6 +17,7 @@ from ._lib import (  # noqa: F401
     AttnScoreParams,
     SoftmaxParams,
     AttnOutputParams,
+    AttnFusedParams,
     PagedAttnParams,
     PerHeadNormParams,
     NormRopeParams,

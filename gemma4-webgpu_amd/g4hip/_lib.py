@@ -50,6 +50,13 @@ class AttnOutputParams(ctypes.Structure):  # shaders/attn_output.wgsl:1
                 ("head_dim", ctypes.c_uint32), ("seq_len", ctypes.c_uint32)]
 
 
+class AttnFusedParams(ctypes.Structure):
+    _fields_ = [("num_q_heads", ctypes.c_uint32), ("num_kv_heads", ctypes.c_uint32),
+                ("head_dim", ctypes.c_uint32), ("max_seq_len", ctypes.c_uint32),
+                ("scale", ctypes.c_float), ("sliding_window", ctypes.c_uint32),
+                ("eps", ctypes.c_float), ("theta", ctypes.c_float), ("apply_divisor", ctypes.c_uint32)]
+
+
 class PagedAttnParams(ctypes.Structure):
     _fields_ = [("num_seqs", ctypes.c_uint32), ("num_q_heads", ctypes.c_uint32),
                 ("num_kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
@@ -129,6 +136,8 @@ SIGNATURES = {
     "g4_attnDecode_workspace_size": (_I, [AttnScoreParams, ctypes.POINTER(_SZ)]),
     "g4_attnDecode": (_I, [_P, _P, _P, _P, _P, AttnScoreParams, _P, _SZ]),
     "g4_attnDecode_dev": (_I, [_P, _P, _P, _P, _P, AttnScoreParams, _P, _SZ, _P]),
+    "g4_attnDecodeFused_workspace_size": (_I, [AttnFusedParams, ctypes.POINTER(_SZ)]),
+    "g4_attnDecodeFused": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, AttnFusedParams, _P, _SZ, _P]),
     "g4_pagedAttnDecode_workspace_size": (_I, [PagedAttnParams, ctypes.POINTER(_SZ)]),
     "g4_pagedAttnDecode": (_I, [_P, _P, _P, _P, _P, _P, _P, PagedAttnParams, _P, _SZ]),
     "g4_pagedKvStore": (_I, [_P, _P, _P, _P, _P, _P, _P, PagedAttnParams]),
@@ -144,6 +153,8 @@ SIGNATURES = {
     "g4_topk256": (_I, [_P, _P, _P, _U32]),
     "g4_rmsNormMatmul_q4k": (_I, [_P, _P, _P, _P, _P, MatmulParams, _F]),
     "g4_normAddGateUpGelu_q4k": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, MatmulParams, _F]),
+    "g4_normAddMatmulSegments": (_I, [_P, _I, _P, _P, _P, _P, _P, ctypes.POINTER(_P),
+                                      ctypes.POINTER(_P), ctypes.POINTER(_U32), _I, _U32, _F, _F]),
     "g4_dequant_q4k": (_I, [_P, _P, _U64, _P]),
     "g4_dequant_q6k": (_I, [_P, _P, _U64, _P]),
     "g4_splitmix64": (_U64, [_U64, _U64]),

@@ -137,9 +137,17 @@ class Decoder:
         self.token = ctx.zeros(1, np.uint32)
         self.topk = ctx.empty(512, f32)
         self.pos = ctx.zeros(1, np.uint32)
-        ws = max(ctx.attn_workspace_bytes(s.n_q_heads, s.n_kv_heads, s.head_dim, max_seq, w)
-                 for w in (0, s.window))
-        self.attn_ws = ctx.alloc(ws)
+        self.attn_params = []
+        for il in range(s.n_layers):
+            glob = s.is_global(il)
+            self.attn_params.append(ctx.attn_fused_params(
+                s.n_q_heads, s.n_kv_heads, s.head_dim, max_seq, 0 if glob else s.window, s.eps,
+                s.theta_global if glob else s.theta_local, int(glob)))
+        ws = max(max(ctx.attn_workspace_bytes(s.n_q_heads, s.n_kv_heads, s.head_dim, max_seq, w)
+                     for w in (0, s.window)),
+                 max(ctx.attn_fused_workspace_bytes(p) for p in self.attn_params))
+        # split-K partials + arrival counters; zeroed once, the kernels keep the counters zeroed
+        self.attn_ws = ctx.zeros(ws, np.uint8)
         ctx.fill_normal_f32(self.hidden, s.hidden, self._seed(), 0.0, 1.0)
         ctx.sync()
 
@@ -220,30 +228,46 @@ class Decoder:
 
     # ---- the fused MI355X step ----------------------------------------------
     def step_fused(self, sample: str = "argmax", advance: bool = True) -> None:
-        """One token at position *pos (device), then pos += 1 on the device."""
+        """One token at position *pos (device), then pos += 1 on the device.
+
+        Five launches per layer:
+          1. [post-FFN norm-add of the previous layer ->] attn rmsNorm -> q/k/v matvecs
+          2. q/k norm + RoPE, v_norm, KV row store, split-K attention (+ merge)
+          3. o matvec
+          4. post-attn norm-add -> pre-FFN rmsNorm -> gate/up matvecs -> GELU product
+          5. down matvec (Q6_K)
+        then the last post-FFN norm-add + final rmsNorm + LM head + softcap in
+        one launch, and the argmax.
+        """
         c, s = self.ctx, self.s
         for il, L in enumerate(self.layers):
-            glob = s.is_global(il)
-            theta = s.theta_global if glob else s.theta_local
-            window = 0 if glob else s.window
-            c.rmsNormMatmul_q4k(self.hidden, L.attn_norm, L.wq, self.q, s.q_dim, s.hidden, s.eps)
-            c.rmsNormMatmul_q4k(self.hidden, L.attn_norm, L.wk, self.k, s.kv_dim, s.hidden, s.eps)
-            c.rmsNormMatmul_q4k(self.hidden, L.attn_norm, L.wv, self.v, s.kv_dim, s.hidden, s.eps)
-            c.perHeadRmsNormNoWeight(self.v, s.n_kv_heads, s.head_dim, s.eps)
-            c.fusedPerHeadNormRope(self.q, L.q_norm, s.n_q_heads, s.head_dim, s.eps, 0, theta, int(glob),
-                                   self.rope_freqs, position_dev=self.pos)
-            c.fusedPerHeadNormRope(self.k, L.k_norm, s.n_kv_heads, s.head_dim, s.eps, 0, theta, int(glob),
-                                   self.rope_freqs, position_dev=self.pos)
-            c.kvCacheStore(self.k, self.v, L.k_cache, L.v_cache, s.n_kv_heads, s.head_dim, 0, self.max_seq,
-                           position_dev=self.pos)
-            c.attnDecode(self.q, L.k_cache, L.v_cache, self.attn, s.n_q_heads, s.n_kv_heads, s.head_dim,
-                         self.max_seq, 1.0, window, workspace=self.attn_ws, position_dev=self.pos)
+            outs = [self.q, self.k, self.v]
+            ws = [L.wq, L.wk, L.wv]
+            rows = [s.q_dim, s.kv_dim, s.kv_dim]
+            if il == 0:
+                c.normAddMatmulSegments("q4k", self.hidden, L.attn_norm, None, None, None, ws, outs, rows,
+                                        s.hidden, s.eps)
+            else:
+                prev = self.layers[il - 1]
+                c.normAddMatmulSegments("q4k", self.down, prev.post_ffn_norm, self.hidden2, L.attn_norm,
+                                        self.hidden, ws, outs, rows, s.hidden, s.eps)
+            c.attnDecodeFused(self.q, self.k, self.v, L.q_norm, L.k_norm, self.rope_freqs, L.k_cache, L.v_cache,
+                              self.attn, self.attn_params[il], self.attn_ws, self.pos)
             c.matmulQuant(self.attn, L.wo, self.o, s.hidden, s.q_dim)
             c.normAddGateUpGelu_q4k(self.o, L.post_attn_norm, self.hidden, L.pre_ffn_norm, L.wgate, L.wup,
                                     self.hidden2, self.act, s.ffn, s.hidden, s.eps)
             c.matmulQuant(self.act, L.wdown, self.down, s.hidden, s.ffn, "q6k")
-            c.fusedNormAdd(self.down, L.post_ffn_norm, self.hidden2, self.hidden, s.hidden, s.eps)
-        self._head(sample)
+        last = self.layers[-1]
+        if self.lm_head is not None:
+            c.normAddMatmulSegments("q6k", self.down, last.post_ffn_norm, self.hidden2, self.final_norm,
+                                    self.hidden, [self.lm_head], [self.logits], [s.vocab], s.hidden, s.eps,
+                                    softcap=s.softcap)
+            if sample == "argmax":
+                c.argmax(self.logits, self.token, s.vocab)
+            else:
+                c.topk256(self.logits, self.topk, s.vocab)
+        else:
+            c.fusedNormAdd(self.down, last.post_ffn_norm, self.hidden2, self.hidden, s.hidden, s.eps)
         if advance:
             c.advancePosition(self.pos, 1)
 
@@ -256,4 +280,7 @@ class Decoder:
         return g
 
     def launches_per_step_fused(self) -> int:
-        return 13 * self.s.n_layers + (5 if self.lm_head is not None else 0) + 1
+        """Kernel launches of step_fused: 5 per layer (plus the attention merge
+        kernel when the split count is too large to merge in-kernel), the head
+        (1), argmax (2) and the position advance (1)."""
+        return 5 * self.s.n_layers + (3 if self.lm_head is not None else 1) + 1

@@ -13,6 +13,7 @@ from typing import Optional, Union
 import numpy as np
 
 from ._lib import (
+    AttnFusedParams,
     AttnOutputParams,
     AttnScoreParams,
     KvStoreParams,
@@ -197,6 +198,16 @@ class Context:
         check(lib().g4_normAddGateUpGelu_q4k(self.h, _p(o), _p(w_post), _p(residual), _p(w_pre), _p(w_gate),
                                              _p(w_up), _p(h_out), _p(out), MatmulParams(M, N), eps))
 
+    def normAddMatmulSegments(self, wtype: str, x: Ptr, w1: Ptr, residual: Ptr, w2: Ptr, h_out: Ptr,
+                              weights, outputs, rows, N: int, eps: float = 1e-6, softcap: float = 0.0) -> None:
+        """[residual + norm(x)*w1 ->] norm(.)*w -> y_i = W_i . x' for up to 4 matrices."""
+        n = len(weights)
+        W = (ctypes.c_void_p * n)(*[_p(w).value for w in weights])
+        Y = (ctypes.c_void_p * n)(*[_p(y).value for y in outputs])
+        R = (ctypes.c_uint32 * n)(*rows)
+        check(lib().g4_normAddMatmulSegments(self.h, {"q4k": 0, "q6k": 1}[wtype], _p(x), _p(w1), _p(residual),
+                                             _p(w2), _p(h_out), W, Y, R, n, N, eps, softcap))
+
     # ---- attention (kv_cache_store / attn_score / softmax / attn_output) ----
     def kvCacheStore(self, k_in: Ptr, v_in: Ptr, k_cache: Ptr, v_cache: Ptr, num_kv_heads: int, head_dim: int,
                      position: int, max_seq_len: int, position_dev: Ptr = None) -> None:
@@ -230,8 +241,8 @@ class Context:
                    position_dev: Ptr = None) -> None:
         p = AttnScoreParams(nqh, nkh, hd, seq_len, scale, window)
         ws = workspace
-        if ws is None:
-            ws = self.alloc(self.attn_workspace_bytes(nqh, nkh, hd, seq_len, window))
+        if ws is None:  # a fresh workspace must start zeroed (arrival counters)
+            ws = self.zeros(self.attn_workspace_bytes(nqh, nkh, hd, seq_len, window), np.uint8)
         if position_dev is None:
             check(lib().g4_attnDecode(self.h, _p(q), _p(k_cache), _p(v_cache), _p(out), p, _p(ws), ws.nbytes))
         else:
@@ -240,6 +251,25 @@ class Context:
         if workspace is None:
             self.sync()
             ws.free()
+
+    @staticmethod
+    def attn_fused_params(nqh, nkh, hd, max_seq_len, window=0, eps=1e-6, theta=1e4, apply_divisor=0,
+                          scale=1.0) -> AttnFusedParams:
+        return AttnFusedParams(nqh, nkh, hd, max_seq_len, scale, window, eps, theta, apply_divisor)
+
+    @staticmethod
+    def attn_fused_workspace_bytes(p: AttnFusedParams) -> int:
+        n = ctypes.c_size_t()
+        check(lib().g4_attnDecodeFused_workspace_size(p, ctypes.byref(n)))
+        return int(n.value)
+
+    def attnDecodeFused(self, q_raw: Ptr, k_raw: Ptr, v_raw: Ptr, q_norm_w: Ptr, k_norm_w: Ptr, rope_freqs: Ptr,
+                        k_cache: Ptr, v_cache: Ptr, out: Ptr, p: AttnFusedParams, workspace: Buffer,
+                        position_dev: Ptr) -> None:
+        """q/k norm + RoPE, v_norm, KV row store at *position_dev and decode attention in one launch."""
+        check(lib().g4_attnDecodeFused(self.h, _p(q_raw), _p(k_raw), _p(v_raw), _p(q_norm_w), _p(k_norm_w),
+                                       _p(rope_freqs), _p(k_cache), _p(v_cache), _p(out), p, _p(workspace),
+                                       workspace.nbytes, _p(position_dev)))
 
     @staticmethod
     def paged_params(num_seqs, nqh, nkh, hd, page_size, max_pages, max_seq_len, num_pages, scale=1.0, window=0):

@@ -153,8 +153,10 @@ int g4_attnOutput(g4_ctx* ctx, const float* probs, const uint16_t* v_cache, floa
 
 /* Fused split-K flash-decode: the attnScore -> softmax -> attnOutput trio in
  * one pass over the KV cache (same inputs and masking as the trio,
- * src/engine.ts:1582-1584). `workspace` holds per-split partials; its size
- * comes from g4_attnDecode_workspace_size. */
+ * src/engine.ts:1582-1584). `workspace` holds per-split partials and arrival
+ * counters; its size comes from g4_attnDecode_workspace_size. It must be
+ * zeroed once before its first use (g4_memset); the kernels leave it zeroed.
+ * Calls that share a workspace must not overlap. */
 int g4_attnDecode_workspace_size(g4_attn_score_params p, size_t* bytes);
 int g4_attnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                   float* output, g4_attn_score_params p, void* workspace, size_t workspace_bytes);
@@ -163,6 +165,26 @@ int g4_attnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_cache, const ui
 int g4_attnDecode_dev(g4_ctx* ctx, const float* q, const uint16_t* k_cache,
                       const uint16_t* v_cache, float* output, g4_attn_score_params p,
                       void* workspace, size_t workspace_bytes, const uint32_t* position_dev);
+
+/* The per-layer attention block of a decode step in one launch
+ * (src/engine.ts:1562-1584): q_norm + RoPE on the raw q projection, k_norm +
+ * RoPE on k and the weightless v_norm on v, the K/V row stored (f16) at
+ * position *position_dev, then split-K decode attention over positions
+ * [0, *position_dev] with the window. q_raw is [num_q_heads][head_dim] and is
+ * not modified; k_raw/v_raw are [num_kv_heads][head_dim]; caches hold
+ * max_seq_len rows. Workspace rules as for g4_attnDecode. */
+typedef struct {
+  uint32_t num_q_heads, num_kv_heads, head_dim, max_seq_len;
+  float scale;
+  uint32_t sliding_window;
+  float eps, theta;
+  uint32_t apply_divisor;
+} g4_attn_fused_params;
+int g4_attnDecodeFused_workspace_size(g4_attn_fused_params p, size_t* bytes);
+int g4_attnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float* v_raw,
+                       const uint16_t* q_norm_w, const uint16_t* k_norm_w, const uint16_t* rope_freqs,
+                       uint16_t* k_cache, uint16_t* v_cache, float* output, g4_attn_fused_params p,
+                       void* workspace, size_t workspace_bytes, const uint32_t* position_dev);
 
 /* Ragged multi-sequence decode attention over a paged f16 KV pool: sequence
  * s has seq_lens[s] positions; its logical position t lives in page
@@ -252,6 +274,21 @@ int g4_normAddGateUpGelu_q4k(g4_ctx* ctx, const float* o, const uint16_t* w_post
                              const float* residual, const uint16_t* w_pre, const void* w_gate,
                              const void* w_up, float* h_out, float* out, g4_matmul_params p,
                              float eps);
+
+/* [fusedNormAdd ->] rmsNorm -> matmulQuant over up to 4 matrices that share
+ * the input (src/engine.ts:1546-1554 for q/k/v, :1606 + :1621-1625 + :1686-1701
+ * for the post-FFN add, final norm, LM head and softcap):
+ *   residual == NULL:  x' = x * w1 / rms(x)
+ *   residual != NULL:  h = residual + x * w1 / rms(x)   (written to h_out if non-NULL)
+ *                      x' = h * w2 / rms(h)
+ *   outputs[i] = weights[i] . x'  (rows[i] x N), then tanh(y/cap)*cap if
+ *   softcap_cap != 0.
+ * wtype 0 = Q4_K, 1 = Q6_K; N <= 8192; norm weights are f16[N]. */
+int g4_normAddMatmulSegments(g4_ctx* ctx, int wtype, const float* x, const uint16_t* w1,
+                             const float* residual, const uint16_t* w2, float* h_out,
+                             const void* const* weights, float* const* outputs,
+                             const uint32_t* rows, int nseg, uint32_t N, float eps,
+                             float softcap_cap);
 
 /* ------------------------------------------------------------------------ */
 /* Debug / test exports                                                      */

@@ -69,8 +69,8 @@ def test_error_paths_without_device():
     assert L.g4_attnDecode_workspace_size(bad, ctypes.byref(size)) == -1
     good = g4hip.AttnScoreParams(8, 1, 256, 32768, 1.0, 0)
     assert L.g4_attnDecode_workspace_size(good, ctypes.byref(size)) == 0
-    # 256 splits x 8 heads x (256 + 2) floats
-    assert size.value == 256 * 8 * 258 * 4
+    # 32768 positions in 64-position splits: 512 splits x 8 heads x (256 + 2) floats
+    assert size.value == 512 * 8 * 258 * 4
 
 
 def test_init_without_gpu_fails_cleanly():

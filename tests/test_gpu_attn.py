@@ -57,7 +57,7 @@ def test_attn_decode(ctx, L, window, hd):
     q = unit_q(L + 5, nqh, hd)
     ref = O.attention(q, k, v, nqh, nkh, hd, L, 1.0, window)
     out = ctx.empty(nqh * hd, np.float32)
-    ws = ctx.alloc(ctx.attn_workspace_bytes(nqh, nkh, hd, L, window))
+    ws = ctx.zeros(ctx.attn_workspace_bytes(nqh, nkh, hd, L, window), np.uint8)
     dk, dv = ctx.from_numpy(k), ctx.from_numpy(v)
     ctx.attnDecode(ctx.from_numpy(q), dk, dv, out, nqh, nkh, hd, L, 1.0, window, workspace=ws)
     assert_close(out.download(np.float32), ref, what=f"L={L} W={window}")
@@ -79,7 +79,7 @@ def test_attn_decode_dev_position(ctx):
     k, v = kv(99, cap, nkh, hd)
     q = unit_q(98, nqh, hd)
     dk, dv, dq = ctx.from_numpy(k), ctx.from_numpy(v), ctx.from_numpy(q)
-    ws = ctx.alloc(ctx.attn_workspace_bytes(nqh, nkh, hd, cap, 0))
+    ws = ctx.zeros(ctx.attn_workspace_bytes(nqh, nkh, hd, cap, 0), np.uint8)
     out = ctx.empty(nqh * hd, np.float32)
     for pos in (0, 100, 4095, cap - 1):
         pdev = ctx.from_numpy(np.array([pos], np.uint32))
@@ -106,7 +106,7 @@ def test_paged_ragged(ctx, B, window):
         c += n
     q = O.gen_normal_f32(3, B * nqh * hd).reshape(B, nqh * hd)
     p = ctx.paged_params(B, nqh, nkh, hd, P, max_pages, max_len, total_pages, 1.0, window)
-    ws = ctx.alloc(ctx.paged_workspace_bytes(p))
+    ws = ctx.zeros(ctx.paged_workspace_bytes(p), np.uint8)
     out = ctx.empty(B * nqh * hd, np.float32)
     ctx.pagedAttnDecode(ctx.from_numpy(q), ctx.from_numpy(k_pool), ctx.from_numpy(v_pool), ctx.from_numpy(table),
                         ctx.from_numpy(lens), out, p, ws)
@@ -135,3 +135,56 @@ def test_paged_kv_store(ctx):
         assert np.array_equal(K[row], k.reshape(B, hd)[s].astype(np.float16).view(np.uint16))
         assert np.array_equal(V[row], v.reshape(B, hd)[s].astype(np.float16).view(np.uint16))
     assert np.count_nonzero(K.any(axis=1)) == B
+
+
+FUSED_CASES = [
+    # (position, window, head_dim, theta, apply_divisor): local layer (W=512,
+    # theta 1e4), global layer (proportional table), short and long positions
+    (0, 512, 256, 1e4, 0),
+    (14, 512, 256, 1e4, 0),
+    (700, 512, 256, 1e4, 0),
+    (700, 0, 256, 1e6, 1),
+    (3000, 0, 256, 1e6, 1),
+    (900, 0, 512, 1e6, 1),
+]
+
+
+@pytest.mark.parametrize("pos,window,hd,theta,div", FUSED_CASES)
+def test_attn_decode_fused(ctx, pos, window, hd, theta, div):
+    """norm + RoPE on q/k, v_norm, KV store and attention in one launch equals
+    the reference's per-key sequence restated by the oracle."""
+    nqh, nkh, cap = 8, 1, 4096
+    k, v = kv(pos + 11, cap, nkh, hd)
+    qr = O.gen_normal_f32(pos + 1, nqh * hd, 0.0, 3.0)
+    kr = O.gen_normal_f32(pos + 2, nkh * hd, 0.0, 3.0)
+    vr = O.gen_normal_f32(pos + 3, nkh * hd, 0.0, 60.0)
+    qw = O.gen_normal_f16(pos + 4, hd, 1.0, 0.1)
+    kw = O.gen_normal_f16(pos + 5, hd, 1.0, 0.1)
+    table = np.where(np.arange(hd // 2) < hd // 8, 1.0, np.inf).astype(np.float16).view(np.uint16)
+    # oracle: the reference's per-key order (src/engine.ts:1562-1584)
+    vq = O.per_head_rms_norm_no_weight(vr, nkh, hd, 1e-6)
+    q = O.fused_per_head_norm_rope(qr, qw, nqh, hd, 1e-6, pos, theta, div, table)
+    kk = O.fused_per_head_norm_rope(kr, kw, nkh, hd, 1e-6, pos, theta, div, table)
+    k_ref, v_ref = k.copy(), v.copy()
+    O.kv_cache_store_f16(kk, vq, k_ref, v_ref, nkh, hd, pos)
+    ref = O.attention(q, k_ref, v_ref, nqh, nkh, hd, pos + 1, 1.0, window)
+    p = ctx.attn_fused_params(nqh, nkh, hd, cap, window, 1e-6, theta, div)
+    ws = ctx.zeros(ctx.attn_fused_workspace_bytes(p), np.uint8)
+    dk, dv = ctx.from_numpy(k), ctx.from_numpy(v)
+    out = ctx.empty(nqh * hd, np.float32)
+    dq = ctx.from_numpy(qr)
+    pdev = ctx.from_numpy(np.array([pos], np.uint32))
+    for rep in range(2):  # the arrival counters must be left zeroed for the next call
+        ctx.attnDecodeFused(dq, ctx.from_numpy(kr), ctx.from_numpy(vr), ctx.from_numpy(qw), ctx.from_numpy(kw),
+                            ctx.from_numpy(table), dk, dv, out, p, ws, pdev)
+        assert_close(out.download(np.float32), ref, what=f"fused pos={pos} rep={rep}")
+    # the stored row: within an f16 rounding of the oracle's (the norm's f32
+    # rounding differs from the oracle's f64 one); no other row touched
+    kc, vc = dk.download(np.uint16).reshape(cap, hd), dv.download(np.uint16).reshape(cap, hd)
+    assert np.max(np.abs(vc[pos].astype(np.int32) - v_ref.reshape(cap, hd)[pos].astype(np.int32))) <= 1
+    assert np.max(np.abs(kc[pos].view(np.float16).astype(np.float32) -
+                         k_ref.reshape(cap, hd)[pos].view(np.float16).astype(np.float32))) <= 2e-3
+    other = np.arange(cap) != pos
+    assert np.array_equal(kc[other], k.reshape(cap, hd)[other])
+    assert np.array_equal(vc[other], v.reshape(cap, hd)[other])
+    assert np.array_equal(qr, dq.download(np.float32))   # q_raw is not modified

@@ -35,14 +35,30 @@ def test_dequant_q6k_bit_exact(ctx):
     assert bits_equal(out.download(np.float32), O.dequant_q6k(b))
 
 
+def _f16_ulps(a, b):
+    return np.abs(a.astype(np.int32) - b.astype(np.int32))
+
+
 def test_generators_match_oracle(ctx):
+    """Integer fields (scales, quants) are bit-exact; the f16 super-scales come
+    from f64 Box-Muller (log, cos), whose last bit may differ between the
+    device math library and the host libm, so they may differ by one f16 ulp
+    in rare blocks."""
     n4, n6, nf = 5000, 3001, 100001
     b4 = ctx.alloc(n4 * 144)
     ctx.fill_q4k(b4, n4, 42)
-    assert np.array_equal(b4.download(np.uint8), O.gen_q4k(42, n4))
+    got, ref = b4.download(np.uint8).reshape(n4, 144), O.gen_q4k(42, n4).reshape(n4, 144)
+    assert np.array_equal(got[:, 4:], ref[:, 4:])
+    dd = _f16_ulps(got[:, :4].copy().view(np.uint16), ref[:, :4].copy().view(np.uint16))
+    print(f"q4k d/dmin differing: {np.count_nonzero(dd)} of {2 * n4}", flush=True)
+    assert dd.max() <= 1 and np.count_nonzero(dd) <= 0.001 * 2 * n4
     b6 = ctx.alloc(n6 * 210)
     ctx.fill_q6k(b6, n6, 43)
-    assert np.array_equal(b6.download(np.uint8), O.gen_q6k(43, n6))
+    got, ref = b6.download(np.uint8).reshape(n6, 210), O.gen_q6k(43, n6).reshape(n6, 210)
+    assert np.array_equal(got[:, :208], ref[:, :208])
+    dd = _f16_ulps(got[:, 208:].copy().view(np.uint16), ref[:, 208:].copy().view(np.uint16))
+    print(f"q6k d differing: {np.count_nonzero(dd)} of {n6}", flush=True)
+    assert dd.max() <= 1 and np.count_nonzero(dd) <= 0.001 * n6
     x = ctx.empty(nf, np.float32)
     ctx.fill_normal_f32(x, nf, 44, 0.0, 1.0)
     got = x.download(np.float32)
@@ -173,3 +189,53 @@ def test_lm_head_q6k_full_size(ctx):
     rows = np.arange(0, M, 97)
     Wh = W.download(np.uint8).reshape(M, -1)[rows]
     assert_close(y[rows], O.matmul(x, Wh.reshape(-1), rows.size, N, "q6k"), what="LM head rows")
+
+
+@pytest.mark.parametrize("mode", ["norm", "normadd"])
+def test_norm_add_matmul_segments_qkv(ctx, mode):
+    """q/k/v projections in one launch, with the RMSNorm (and, between layers,
+    the post-FFN residual add) in the prologue."""
+    N = 1536
+    segs = [(2048, 40), (256, 41), (256, 42)]
+    Ws = [O.gen_q4k(s, M * N // 256) for M, s in segs]
+    x = O.gen_normal_f32(43, N, 0.0, 2.0)
+    res = O.gen_normal_f32(44, N)
+    w1 = O.gen_normal_f16(45, N, 1.0, 0.1)
+    w2 = O.gen_normal_f16(46, N, 1.0, 0.1)
+    if mode == "norm":
+        xn = O.rms_norm(x, w1, 1e-6)
+    else:
+        h = O.fused_norm_add(x, w1, res, 1e-6)
+        xn = O.rms_norm(h, w2, 1e-6)
+    outs = [ctx.empty(M, np.float32) for M, _ in segs]
+    dh = ctx.empty(N, np.float32)
+    ctx.normAddMatmulSegments("q4k", ctx.from_numpy(x), ctx.from_numpy(w1),
+                              ctx.from_numpy(res) if mode == "normadd" else None,
+                              ctx.from_numpy(w2) if mode == "normadd" else None,
+                              dh if mode == "normadd" else None,
+                              [ctx.from_numpy(W) for W in Ws], outs, [M for M, _ in segs], N)
+    for (M, _), W, o in zip(segs, Ws, outs):
+        assert_close(o.download(np.float32), O.matmul(xn, W, M, N, "q4k"), what=f"{mode} M={M}")
+    if mode == "normadd":
+        assert_close(dh.download(np.float32), h, rel=1e-6, cos=0.99999999, what="h_out")
+
+
+def test_norm_add_matmul_q6k_softcap(ctx):
+    """post-FFN add + final norm + tied Q6_K LM head + softcap in one launch."""
+    M, N = 20000, 1536
+    W = O.gen_q6k(50, M * N // 256)
+    x = O.gen_normal_f32(51, N, 0.0, 2.0)
+    res = O.gen_normal_f32(52, N, 0.0, 5.0)
+    w1 = O.gen_normal_f16(53, N, 1.0, 0.1)
+    w2 = O.gen_normal_f16(54, N, 1.0, 0.1)
+    h = O.fused_norm_add(x, w1, res, 1e-6)
+    # scale the final-norm weight 20x so that logits reach the softcap's knee
+    w2s = (w2.view(np.float16).astype(np.float32) * 20).astype(np.float16).view(np.uint16)
+    ref = O.logit_softcap(O.matmul(O.rms_norm(h, w2s, 1e-6), W, M, N, "q6k"), 30.0)
+    y = ctx.empty(M, np.float32)
+    dh = ctx.empty(N, np.float32)
+    ctx.normAddMatmulSegments("q6k", ctx.from_numpy(x), ctx.from_numpy(w1), ctx.from_numpy(res),
+                              ctx.from_numpy(w2s), dh, [ctx.from_numpy(W)], [y], [M], N, 1e-6, softcap=30.0)
+    got = y.download(np.float32)
+    assert np.max(np.abs(got)) <= 30.0 and np.max(np.abs(ref)) > 20.0
+    assert_close(got, ref, what="lm head + softcap")
