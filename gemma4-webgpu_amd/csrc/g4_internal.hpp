@@ -15,6 +15,7 @@ struct g4_ctx {
   bool lost = false;
   int num_cus = 0;
   size_t hbm_bytes = 0;
+  size_t lds_max = 65536;  // LDS bytes one workgroup may use (160 KB on gfx950)
   char name[128] = {0};
   bool capturing = false;
   // Small device buffer for the partials of two-stage reductions (argmax,

@@ -100,6 +100,7 @@ int g4_init(int device, g4_ctx** out) {
   ctx->device = device;
   ctx->num_cus = prop.multiProcessorCount;
   ctx->hbm_bytes = prop.totalGlobalMem;
+  ctx->lds_max = prop.sharedMemPerBlock;
   snprintf(ctx->name, sizeof(ctx->name), "%s (%s)", prop.name, prop.gcnArchName);
   e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
   if (e != hipSuccess) {

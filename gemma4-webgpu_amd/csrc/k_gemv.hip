@@ -39,8 +39,6 @@ constexpr size_t kMaxLds = 65536; // LDS bytes one workgroup may claim
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
 
 __device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *(const uint4*)p; }
-__device__ __forceinline__ u32x4a ld16a4(const uint8_t* p) { return *(const u32x4a*)p; }
-__device__ __forceinline__ uint32_t ld4(const uint8_t* p) { return *(const uint32_t*)p; }
 
 __device__ __forceinline__ int plane_off(uint32_t e) { return (int)((e >> 8) * XSTRIDE + (e & 255)); }
 
@@ -59,7 +57,7 @@ struct XView {
   __device__ int plane_bytes() const { return (int)(K / 256) * XSTRIDE; }
 };
 
-__host__ __device__ inline size_t xview_bytes(uint32_t K, int NV) {
+__host__ __device__ constexpr size_t xview_bytes(uint32_t K, int NV) {
   const size_t nb = K / 256;
   size_t b = 2 * (size_t)NV * nb * XSTRIDE;
   b += 2 * (size_t)NV * (K / 32) * sizeof(float);
@@ -247,84 +245,87 @@ __device__ __forceinline__ int dot8(const uint32_t* q, const uint32_t* x) {
   return acc;
 }
 
-struct Q4Unit {
-  uint4 hd, q0, q1;
-};
-
-__device__ __forceinline__ void q4_load(const uint8_t* blk, int g, Q4Unit& q) {
-  q.hd = ld16(blk);
-  q.q0 = ld16(blk + 16 + 32 * g);
-  q.q1 = ld16(blk + 32 + 32 * g);
-}
-
-__device__ __forceinline__ void q4_zero(Q4Unit& q) { q.hd = q.q0 = q.q1 = make_uint4(0, 0, 0, 0); }
-
-// 16 bytes at a 2-byte aligned address: an aligned 16-byte load plus the next
-// dword, funnel-shifted by the misalignment (0 or 2 bytes).
-struct Piece {
-  u32x4a a;
-  uint32_t e;
-  uint32_t sh;
-};
-
-__device__ __forceinline__ Piece ld_piece(const uint8_t* p) {
-  const uintptr_t ad = (uintptr_t)p;
-  const uint8_t* p4 = (const uint8_t*)(ad & ~(uintptr_t)3);
-  Piece r;
-  r.a = ld16a4(p4);
-  r.e = ld4(p4 + 16);
-  r.sh = (uint32_t)(ad & 3);
-  return r;
-}
-
-__device__ __forceinline__ void piece_words(const Piece& p, uint32_t (&w)[4]) {
-  w[0] = __builtin_amdgcn_alignbyte(p.a.y, p.a.x, p.sh);
-  w[1] = __builtin_amdgcn_alignbyte(p.a.z, p.a.y, p.sh);
-  w[2] = __builtin_amdgcn_alignbyte(p.a.w, p.a.z, p.sh);
-  w[3] = __builtin_amdgcn_alignbyte(p.e, p.a.w, p.sh);
-}
-
-struct Q6Unit {
-  Piece A, B, H;
-  int sc[4];
-  uint32_t d;
-};
-
-// Q6_K unit u of a block: h = u >> 1, l0 = 16 (u & 1): ql[64h+l0..], ql[64h+32+l0..],
-// qh[32h+l0..] (16 bytes each), scales sc[8h + (u&1) + 2k], d.
-__device__ __forceinline__ void q6_load(const uint8_t* blk, int u, Q6Unit& q) {
-  const int h = u >> 1, l0 = (u & 1) * 16;
-  q.A = ld_piece(blk + 64 * h + l0);
-  q.B = ld_piece(blk + 64 * h + 32 + l0);
-  q.H = ld_piece(blk + 128 + 32 * h + l0);
-  const int8_t* sc = (const int8_t*)(blk + 192 + 8 * h + (u & 1));
-#pragma unroll
-  for (int k = 0; k < 4; ++k) q.sc[k] = sc[2 * k];
-  q.d = *(const uint16_t*)(blk + 208);
-}
-
-__device__ __forceinline__ void q6_zero(Q6Unit& q) {
-  q.A.a = q.B.a = q.H.a = u32x4a{0, 0, 0, 0};
-  q.A.e = q.B.e = q.H.e = 0;
-  q.A.sh = q.B.sh = q.H.sh = 0;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) q.sc[k] = 0;
-  q.d = 0;
-}
-
+// The weight bytes of a workgroup's row tile are one contiguous range. They
+// are streamed with coalesced 16-byte loads (lane i of the workgroup takes
+// bytes 16i, 16i + 16*NT, ...) into registers, then written to LDS, where
+// each lane picks the pieces of the blocks it multiplies.
 template <int QT>
-struct UnitOf;
-template <> struct UnitOf<0> { using T = Q4Unit; static constexpr int BYTES = 144; };
-template <> struct UnitOf<1> { using T = Q6Unit; static constexpr int BYTES = 210; };
+struct BlockOf;
+template <> struct BlockOf<0> { static constexpr int BYTES = 144; };
+template <> struct BlockOf<1> { static constexpr int BYTES = 210; };
 
-// partial dot of one unit with vector v
-__device__ __forceinline__ float q4_part(const XView& xv, const Q4Unit& q, int g, uint32_t b, int v) {
-  const float d = g4d::f16_bits_to_f32(q.hd.x & 0xffffu);
-  const float dmin = g4d::f16_bits_to_f32(q.hd.x >> 16);
+// A wave's share of a tile: R rows x BPR blocks, 4 lanes per block, 16
+// blocks per step (the last step may be partial). A workgroup tile is the
+// NW*R consecutive rows of its waves.
+template <int QT, int BPR, int R>
+struct Tile {
+  static constexpr int BYTES = BlockOf<QT>::BYTES;
+  static constexpr int NB = R * BPR;
+  static constexpr int IT = (NB + 15) / 16;
+  static constexpr int ROWS_WG = R * NW;
+  static constexpr uint32_t WAVE_B = (uint32_t)NB * BYTES;  // R rows
+  static constexpr uint32_t WG_B = NW * WAVE_B;             // ROWS_WG rows
+  static_assert(WG_B == (uint32_t)ROWS_WG * BPR * BYTES, "a tile is ROWS_WG whole rows");
+  static constexpr int LPT = (int)((WG_B + 16 * NT - 1) / (16 * NT));  // 16-byte loads per thread
+  static constexpr uint32_t LDS_B = (WG_B + 15) / 16 * 16;
+};
+
+template <int LPT>
+struct Stage {
+  u32x4a r[LPT];
+};
+
+// Tail of a range whose length is not a multiple of 16 (Q6_K: even lengths).
+__device__ __forceinline__ u32x4a ld_tail(const uint8_t* p, uint32_t n) {
+  uint32_t w[4] = {0, 0, 0, 0};
+  for (uint32_t j = 0; 2 * j < n; ++j) w[j >> 1] |= (uint32_t)((const uint16_t*)p)[j] << (16 * (j & 1));
+  return u32x4a{w[0], w[1], w[2], w[3]};
+}
+
+// Issues the loads of bytes [0, nbytes) of a tile starting at src (4-byte aligned).
+template <class T>
+__device__ __forceinline__ void stage_load(const uint8_t* src, uint32_t nbytes, Stage<T::LPT>& st) {
+#pragma unroll
+  for (int i = 0; i < T::LPT; ++i) {
+    const uint32_t off = (uint32_t)(i * NT + threadIdx.x) * 16u;
+    if (off + 16 <= nbytes) st.r[i] = *(const u32x4a*)(src + off);
+    else if (off < nbytes) st.r[i] = ld_tail(src + off, nbytes - off);
+    else st.r[i] = u32x4a{0, 0, 0, 0};
+  }
+}
+
+template <class T>
+__device__ __forceinline__ void stage_store(uint8_t* lds, const Stage<T::LPT>& st) {
+#pragma unroll
+  for (int i = 0; i < T::LPT; ++i) {
+    const uint32_t off = (uint32_t)(i * NT + threadIdx.x) * 16u;
+    if (off < T::LDS_B) *(u32x4a*)(lds + off) = st.r[i];
+  }
+}
+
+// 16 bytes at a 2-byte aligned LDS address, from five aligned dwords.
+__device__ __forceinline__ void lds_piece(const uint8_t* p, uint32_t (&w)[4]) {
+  const uintptr_t ad = (uintptr_t)p;
+  const uint32_t* p4 = (const uint32_t*)(ad & ~(uintptr_t)3);
+  const uint32_t sh = (uint32_t)(ad & 3);
+  const uint32_t a0 = p4[0], a1 = p4[1], a2 = p4[2], a3 = p4[3], a4 = p4[4];
+  w[0] = __builtin_amdgcn_alignbyte(a1, a0, sh);
+  w[1] = __builtin_amdgcn_alignbyte(a2, a1, sh);
+  w[2] = __builtin_amdgcn_alignbyte(a3, a2, sh);
+  w[3] = __builtin_amdgcn_alignbyte(a4, a3, sh);
+}
+
+// partial dot of quarter g of the Q4_K block at blk (LDS) with vector v
+__device__ __forceinline__ float q4_part(const XView& xv, const uint8_t* blk, int g, uint32_t b, int v) {
+  const uint4 hd = *(const uint4*)blk;
+  const uint4 q0 = *(const uint4*)(blk + 16 + 32 * g);
+  const uint4 q1 = *(const uint4*)(blk + 32 + 32 * g);
+  const float d = g4d::f16_bits_to_f32(hd.x & 0xffffu);
+  const float dmin = g4d::f16_bits_to_f32(hd.x >> 16);
   float sc_lo, sc_hi, m_lo, m_hi;
-  q4k_scales(q.hd.y, q.hd.z, q.hd.w, g, sc_lo, sc_hi, m_lo, m_hi);
+  q4k_scales(hd.y, hd.z, hd.w, g, sc_lo, sc_hi, m_lo, m_hi);
   uint32_t nl[8], nh[8];
-  const uint32_t qa[8] = {q.q0.x, q.q0.y, q.q0.z, q.q0.w, q.q1.x, q.q1.y, q.q1.z, q.q1.w};
+  const uint32_t qa[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     nl[k] = qa[k] & 0x0f0f0f0fu;
@@ -350,12 +351,17 @@ __device__ __forceinline__ float q4_part(const XView& xv, const Q4Unit& q, int g
   return part;
 }
 
-__device__ __forceinline__ float q6_part(const XView& xv, const Q6Unit& qu, int u, uint32_t b, int v) {
+// Q6_K quarter u of the block at blk (LDS): h = u >> 1, l0 = 16 (u & 1):
+// ql[64h+l0..], ql[64h+32+l0..], qh[32h+l0..] (16 bytes each), scales
+// sc[8h + (u&1) + 2k], d.
+__device__ __forceinline__ float q6_part(const XView& xv, const uint8_t* blk, int u, uint32_t b, int v) {
   const int h = u >> 1, l0 = (u & 1) * 16;
   uint32_t A[4], B[4], H[4];
-  piece_words(qu.A, A);
-  piece_words(qu.B, B);
-  piece_words(qu.H, H);
+  lds_piece(blk + 64 * h + l0, A);
+  lds_piece(blk + 64 * h + 32 + l0, B);
+  lds_piece(blk + 128 + 32 * h + l0, H);
+  const int8_t* scp = (const int8_t*)(blk + 192 + 8 * h + (u & 1));
+  const float dd = g4d::f16_bits_to_f32(*(const uint16_t*)(blk + 208));
   // run k covers elements 128h + 32k + l0 + [0,16) (src/gguf.ts:344-361)
   uint32_t q[4][4];
 #pragma unroll
@@ -383,58 +389,31 @@ __device__ __forceinline__ float q6_part(const XView& xv, const Q6Unit& qu, int 
     al = __builtin_amdgcn_sdot4((int)q[k][3], (int)tl.w, al, false);
     const int2 c = xv.c16[v * (xv.K / 16) + e / 16];
     const int I = (ah - c.x) * 256 + (al - c.y);
-    part += (float)qu.sc[k] * xv.s[v * (xv.K / 32) + e / 32] * (float)I;
+    part += (float)scp[2 * k] * xv.s[v * (xv.K / 32) + e / 32] * (float)I;
   }
-  return part * g4d::f16_bits_to_f32(qu.d);
+  return part * dd;
 }
 
-// A wave's tile: R rows x BPR blocks, 4 lanes per block, 16 blocks per step;
-// the last step may be partial.
-template <int BPR, int R>
-struct Tile {
-  static constexpr int NB = R * BPR;
-  static constexpr int IT = (NB + 15) / 16;
-  static constexpr int ROWS_WG = R * NW;
-};
-
-template <int QT, int BPR, int R>
-__device__ __forceinline__ void tile_load(const uint8_t* W, uint32_t M, uint32_t row0,
-                                          typename UnitOf<QT>::T (&un)[Tile<BPR, R>::IT]) {
-  using T = Tile<BPR, R>;
-  const int lane = threadIdx.x & 63;
-  const int u = lane & 3, bl = lane >> 2;
-#pragma unroll
-  for (int it = 0; it < T::IT; ++it) {
-    const int fb = it * 16 + bl;
-    const bool ok = fb < T::NB && row0 + (uint32_t)(fb / BPR) < M;
-    const uint8_t* blk = W + ((size_t)row0 * BPR + fb) * UnitOf<QT>::BYTES;
-    if constexpr (QT == 0) {
-      if (ok) q4_load(blk, u, un[it]);
-      else q4_zero(un[it]);
-    } else {
-      if (ok) q6_load(blk, u, un[it]);
-      else q6_zero(un[it]);
-    }
-  }
-}
-
+// Multiplies the wave's R rows (at wl in LDS) with the NV activation vectors.
 template <int QT, int BPR, int R, int NV>
-__device__ __forceinline__ void tile_compute(const XView& xv, const typename UnitOf<QT>::T (&un)[Tile<BPR, R>::IT],
-                                             float (&acc)[NV * R]) {
-  using T = Tile<BPR, R>;
+__device__ __forceinline__ void tile_compute(const XView& xv, const uint8_t* wl, float (&acc)[NV * R]) {
+  using T = Tile<QT, BPR, R>;
   const int lane = threadIdx.x & 63;
   const int u = lane & 3, bl = lane >> 2;
 #pragma unroll
   for (int it = 0; it < T::IT; ++it) {
     const int fb = it * 16 + bl;
-    const int r = fb / BPR;
-    const uint32_t b = (uint32_t)(fb % BPR);
+    const bool live = fb < T::NB;
+    const int fbc = live ? fb : T::NB - 1;  // idle lanes of a partial step read a valid block
+    const int r = fbc / BPR;
+    const uint32_t b = (uint32_t)(fbc % BPR);
+    const uint8_t* blk = wl + fbc * T::BYTES;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       float part;
-      if constexpr (QT == 0) part = q4_part(xv, un[it], u, b, v);
-      else part = q6_part(xv, un[it], u, b, v);
-      if (fb >= T::NB) part = 0.f;
+      if constexpr (QT == 0) part = q4_part(xv, blk, u, b, v);
+      else part = q6_part(xv, blk, u, b, v);
+      if (!live) part = 0.f;
       // rows a lane can touch at this step are known at compile time
 #pragma unroll
       for (int rr = (it * 16) / BPR; rr <= (it * 16 + 15) / BPR && rr < R; ++rr)
@@ -492,9 +471,23 @@ struct GemvSegs {
 // EPI: 0 = store y, 1 = store softcap(y) (shaders/logit_softcap.wgsl).
 // A workgroup walks `rep` consecutive tiles of NW*R rows with one activation
 // prologue, loading the next tile's weights while it computes the current one.
+// LDS layout of a workgroup: activation digits, then the weight tile(s).
+__host__ __device__ constexpr size_t align16(size_t b) { return (b + 15) / 16 * 16; }
+
+template <int QT, int BPR, int R>
+__device__ __forceinline__ uint32_t tile_bytes(uint32_t M, uint32_t t) {
+  using T = Tile<QT, BPR, R>;
+  const uint64_t total = (uint64_t)M * BPR * T::BYTES;
+  const uint64_t o = (uint64_t)t * T::WG_B;
+  return o >= total ? 0u : (uint32_t)min((uint64_t)T::WG_B, total - o);
+}
+
+// EPI: 0 = store y, 1 = store softcap(y) (shaders/logit_softcap.wgsl).
+// A workgroup walks `rep` consecutive tiles of NW*R rows with one activation
+// prologue; the next tile's loads are in flight while it computes the current one.
 template <int QT, int BPR, int R, int NV, int PRO, int EPI>
 __global__ __launch_bounds__(NT) void gemv_kernel(GemvSegs segs, ProArgs pa, uint32_t ldy, float cap) {
-  using T = Tile<BPR, R>;
+  using T = Tile<QT, BPR, R>;
   constexpr int K = BPR * 256;
   extern __shared__ __align__(16) uint8_t smem[];
   int si = 0;
@@ -505,35 +498,34 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvSegs segs, ProArgs pa, uin
   const uint32_t tiles = (sg.M + T::ROWS_WG - 1) / T::ROWS_WG;
   const uint32_t tb = (blockIdx.x - sg.wg_begin) * segs.rep;
   const uint32_t te = min(tiles, tb + segs.rep);
-  const uint32_t wrow = (threadIdx.x >> 6) * R;  // this wave's first row in a tile
+  const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
 
   XRegs<NV, K> xr;
   pro_load<NV, K, PRO>(xr, pa);
   __builtin_amdgcn_sched_barrier(0);
-  typename UnitOf<QT>::T un[T::IT];
-  tile_load<QT, BPR, R>(sg.W, sg.M, tb * T::ROWS_WG + wrow, un);
+  Stage<T::LPT> st;
+  stage_load<T>(sg.W + (size_t)tb * T::WG_B, tile_bytes<QT, BPR, R>(sg.M, tb), st);
   const XView xv = carve(smem, K, NV);
+  uint8_t* wl = smem + align16(xview_bytes(K, NV));
   pro_finish<NV, K, PRO>(xr, xv, pa);
 
   for (uint32_t t = tb; t < te; ++t) {
-    const uint32_t row0 = t * T::ROWS_WG + wrow;
-    typename UnitOf<QT>::T nx[T::IT];
-    if (t + 1 < te) tile_load<QT, BPR, R>(sg.W, sg.M, row0 + T::ROWS_WG, nx);
+    if (t != tb) __syncthreads();  // every wave is done with the previous tile
+    stage_store<T>(wl, st);
+    __syncthreads();
+    if (t + 1 < te) stage_load<T>(sg.W + (size_t)(t + 1) * T::WG_B, tile_bytes<QT, BPR, R>(sg.M, t + 1), st);
     float acc[NV * R];
 #pragma unroll
     for (int i = 0; i < NV * R; ++i) acc[i] = 0.f;
-    tile_compute<QT, BPR, R, NV>(xv, un, acc);
+    tile_compute<QT, BPR, R, NV>(xv, wl + wave * T::WAVE_B, acc);
     const float y = wave_fold<NV * R>(acc);
     constexpr int G = 64 / (NV * R);
+    const uint32_t row0 = t * T::ROWS_WG + wave * R;
     if ((lane % G) == 0) {
       const int idx = lane / G;
       const int vec = idx / R, rr = idx % R;
       if (row0 + rr < sg.M) sg.Y[(size_t)vec * ldy + row0 + rr] = EPI == 1 ? softcap(y, cap) : y;
-    }
-    if (t + 1 < te) {
-#pragma unroll
-      for (int i = 0; i < T::IT; ++i) un[i] = nx[i];
     }
   }
 }
@@ -549,29 +541,36 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 template <int BPR, int R, int PRO>
 __global__ __launch_bounds__(NT) void gateup_kernel(const uint8_t* Wg, const uint8_t* Wu, float* out, uint32_t M,
                                                     ProArgs pa) {
-  using T = Tile<BPR, R>;
+  using T = Tile<0, BPR, R>;
   constexpr int K = BPR * 256;
   extern __shared__ __align__(16) uint8_t smem[];
-  const uint32_t row0 = (blockIdx.x * NW + (threadIdx.x >> 6)) * R;
+  const uint32_t t = blockIdx.x;
+  const int wave = threadIdx.x >> 6;
   XRegs<1, K> xr;
   pro_load<1, K, PRO>(xr, pa);
   __builtin_amdgcn_sched_barrier(0);
-  Q4Unit ug[T::IT], uu[T::IT];
-  tile_load<0, BPR, R>(Wg, M, row0, ug);
-  tile_load<0, BPR, R>(Wu, M, row0, uu);
+  const uint32_t nb = tile_bytes<0, BPR, R>(M, t);
+  Stage<T::LPT> sg, su;
+  stage_load<T>(Wg + (size_t)t * T::WG_B, nb, sg);
+  stage_load<T>(Wu + (size_t)t * T::WG_B, nb, su);
   const XView xv = carve(smem, K, 1);
+  uint8_t* wg_l = smem + align16(xview_bytes(K, 1));
+  uint8_t* wu_l = wg_l + T::LDS_B;
   pro_finish<1, K, PRO>(xr, xv, pa);
+  stage_store<T>(wg_l, sg);
+  stage_store<T>(wu_l, su);
+  __syncthreads();
   float ag[R], au[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) ag[i] = au[i] = 0.f;
-  tile_compute<0, BPR, R, 1>(xv, ug, ag);
-  tile_compute<0, BPR, R, 1>(xv, uu, au);
+  tile_compute<0, BPR, R, 1>(xv, wg_l + wave * T::WAVE_B, ag);
+  tile_compute<0, BPR, R, 1>(xv, wu_l + wave * T::WAVE_B, au);
   const float vg = wave_fold<R>(ag);
   const float vu = wave_fold<R>(au);
   const int lane = threadIdx.x & 63;
   constexpr int G = 64 / R;
   if ((lane % G) == 0) {
-    const uint32_t row = row0 + lane / G;
+    const uint32_t row = t * T::ROWS_WG + wave * R + lane / G;
     if (row < M) out[row] = gelu_tanh(vg) * vu;
   }
 }
@@ -698,6 +697,25 @@ struct LaunchReq {
 
 constexpr uint32_t kMaxGemvWgs = 2048;  // beyond this a workgroup walks several row tiles
 
+// Workgroups above 64 KB of LDS must be allowed per kernel.
+int claim_lds(const void* kern, g4_ctx* ctx, size_t lds) {
+  if (lds > ctx->lds_max)
+    return g4::set_error(G4_ERR_UNSUPPORTED, "gemv: %zu bytes of LDS exceed the %zu-byte workgroup limit", lds,
+                         ctx->lds_max);
+  if (lds > kMaxLds) {
+    const hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return g4::hip_fail(ctx, e, "hipFuncSetAttribute");
+  }
+  return G4_OK;
+}
+
+// LDS bytes of a plain gemv workgroup (host-side mirror of the kernel layout).
+size_t gemv_lds(int qt, uint32_t N, int nv) {
+  const uint32_t bpr = N / 256;
+  const int R = bpr >= 12 ? 1 : (bpr >= 6 ? 2 : 4);
+  return align16(xview_bytes(N, nv)) + align16((size_t)R * NW * bpr * (qt ? 210 : 144));
+}
+
 template <int QT, int BPR, int NV, int PRO, int EPI>
 int launch_fixed(g4_ctx* ctx, const LaunchReq& q) {
   constexpr int R = RowsFor<BPR>::R;
@@ -714,7 +732,9 @@ int launch_fixed(g4_ctx* ctx, const LaunchReq& q) {
   }
   sg.n = q.nseg;
   if (wgs == 0) return G4_OK;
-  const size_t lds = xview_bytes(BPR * 256, NV);
+  const size_t lds = align16(xview_bytes(BPR * 256, NV)) + Tile<QT, BPR, R>::LDS_B;
+  int rc = claim_lds((const void*)gemv_kernel<QT, BPR, R, NV, PRO, EPI>, ctx, lds);
+  if (rc) return rc;
   hipLaunchKernelGGL((gemv_kernel<QT, BPR, R, NV, PRO, EPI>), dim3(wgs), dim3(NT), lds, ctx->stream, sg, q.pa,
                      q.ldy, q.cap);
   G4_LAUNCHED(ctx, "gemv");
@@ -791,7 +811,7 @@ int matmul_quant(g4_ctx* ctx, const char* fn, int qt, const float* in, const voi
     return G4_OK;
   }
   int nv_max = 8;
-  while (nv_max > 1 && xview_bytes(p.N, nv_max) > kMaxLds) nv_max >>= 1;
+  while (nv_max > 1 && gemv_lds(qt, p.N, nv_max) > ctx->lds_max) nv_max >>= 1;
   uint32_t done = 0;
   while (done < batch) {
     const uint32_t left = batch - done;
@@ -811,8 +831,10 @@ template <int BPR, int PRO>
 int launch_gateup(g4_ctx* ctx, const uint8_t* wg, const uint8_t* wu, float* out, uint32_t M, const ProArgs& pa) {
   constexpr int R = RowsFor<BPR>::R;
   const dim3 grid(ceil_div(M, R * NW));
-  hipLaunchKernelGGL((gateup_kernel<BPR, R, PRO>), grid, dim3(NT), xview_bytes(BPR * 256, 1), ctx->stream, wg, wu,
-                     out, M, pa);
+  const size_t lds = align16(xview_bytes(BPR * 256, 1)) + 2 * Tile<0, BPR, R>::LDS_B;
+  int rc = claim_lds((const void*)gateup_kernel<BPR, R, PRO>, ctx, lds);
+  if (rc) return rc;
+  hipLaunchKernelGGL((gateup_kernel<BPR, R, PRO>), grid, dim3(NT), lds, ctx->stream, wg, wu, out, M, pa);
   G4_LAUNCHED(ctx, "gateup");
   return G4_OK;
 }
