@@ -275,40 +275,47 @@ struct Stage {
   u32x4a r[LPT];
 };
 
-// Tail of a range whose length is not a multiple of 16 (Q6_K: even lengths).
-__device__ __forceinline__ u32x4a ld_tail(const uint8_t* p, uint32_t n) {
-  uint32_t w[4] = {0, 0, 0, 0};
-  for (uint32_t j = 0; 2 * j < n; ++j) w[j >> 1] |= (uint32_t)((const uint16_t*)p)[j] << (16 * (j & 1));
-  return u32x4a{w[0], w[1], w[2], w[3]};
+// Chunk i of a tile of nbytes (nbytes >= 16) is read from and stored to the
+// same offset: 16*i, or for the last, partial chunk (and lanes past the end)
+// the 16 bytes that end the tile, which overlap the chunk before them with
+// identical bytes. The loaded values are only stored, never computed on, and
+// the load sits under no branch: any arithmetic on them (or a branch around
+// a load) lets the compiler move a wait for the whole weight stream into the
+// activation prologue.
+__device__ __forceinline__ uint32_t chunk_off(uint32_t off, uint32_t nbytes) {
+  return off + 16 <= nbytes ? off : nbytes - 16;
 }
 
 // Issues the loads of bytes [0, nbytes) of a tile starting at src (4-byte aligned).
 template <class T>
 __device__ __forceinline__ void stage_load(const uint8_t* src, uint32_t nbytes, Stage<T::LPT>& st) {
 #pragma unroll
-  for (int i = 0; i < T::LPT; ++i) {
-    const uint32_t off = (uint32_t)(i * NT + threadIdx.x) * 16u;
-    if (off + 16 <= nbytes) st.r[i] = *(const u32x4a*)(src + off);
-    else if (off < nbytes) st.r[i] = ld_tail(src + off, nbytes - off);
-    else st.r[i] = u32x4a{0, 0, 0, 0};
-  }
+  for (int i = 0; i < T::LPT; ++i)
+    st.r[i] = *(const u32x4a*)(src + chunk_off((uint32_t)(i * NT + threadIdx.x) * 16u, nbytes));
 }
 
 template <class T>
-__device__ __forceinline__ void stage_store(uint8_t* lds, const Stage<T::LPT>& st) {
+__device__ __forceinline__ void stage_store(uint8_t* lds, uint32_t nbytes, const Stage<T::LPT>& st) {
 #pragma unroll
   for (int i = 0; i < T::LPT; ++i) {
     const uint32_t off = (uint32_t)(i * NT + threadIdx.x) * 16u;
-    if (off < T::LDS_B) *(u32x4a*)(lds + off) = st.r[i];
+    if (off < T::LDS_B) *(u32x4a*)(lds + chunk_off(off, nbytes)) = st.r[i];
   }
 }
 
-// 16 bytes at a 2-byte aligned LDS address, from five aligned dwords.
+// 16 bytes at a 2-byte aligned LDS address, from three 8-byte aligned
+// reads (wider reads at a weaker alignment stall the LDS pipeline). The
+// aligned address is derived from p by pointer arithmetic: a round trip
+// through an integer would lose the LDS address space and turn the reads
+// into flat loads, which also wait on every global load in flight.
 __device__ __forceinline__ void lds_piece(const uint8_t* p, uint32_t (&w)[4]) {
-  const uintptr_t ad = (uintptr_t)p;
-  const uint32_t* p4 = (const uint32_t*)(ad & ~(uintptr_t)3);
-  const uint32_t sh = (uint32_t)(ad & 3);
-  const uint32_t a0 = p4[0], a1 = p4[1], a2 = p4[2], a3 = p4[3], a4 = p4[4];
+  const uint32_t mis = (uint32_t)(uintptr_t)p & 7u;
+  const uint2* p8 = (const uint2*)(p - mis);
+  const uint2 b0 = p8[0], b1 = p8[1], b2 = p8[2];
+  const bool hi = (mis & 4) != 0;  // skip one dword
+  const uint32_t sh = mis & 3;
+  const uint32_t a0 = hi ? b0.y : b0.x, a1 = hi ? b1.x : b0.y, a2 = hi ? b1.y : b1.x;
+  const uint32_t a3 = hi ? b2.x : b1.y, a4 = hi ? b2.y : b2.x;
   w[0] = __builtin_amdgcn_alignbyte(a1, a0, sh);
   w[1] = __builtin_amdgcn_alignbyte(a2, a1, sh);
   w[2] = __builtin_amdgcn_alignbyte(a3, a2, sh);
@@ -505,16 +512,21 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvSegs segs, ProArgs pa, uin
   pro_load<NV, K, PRO>(xr, pa);
   __builtin_amdgcn_sched_barrier(0);
   Stage<T::LPT> st;
-  stage_load<T>(sg.W + (size_t)tb * T::WG_B, tile_bytes<QT, BPR, R>(sg.M, tb), st);
+  uint32_t nb = tile_bytes<QT, BPR, R>(sg.M, tb);
+  stage_load<T>(sg.W + (size_t)tb * T::WG_B, nb, st);
+  __builtin_amdgcn_sched_barrier(0);
   const XView xv = carve(smem, K, NV);
   uint8_t* wl = smem + align16(xview_bytes(K, NV));
   pro_finish<NV, K, PRO>(xr, xv, pa);
 
   for (uint32_t t = tb; t < te; ++t) {
     if (t != tb) __syncthreads();  // every wave is done with the previous tile
-    stage_store<T>(wl, st);
+    stage_store<T>(wl, nb, st);
     __syncthreads();
-    if (t + 1 < te) stage_load<T>(sg.W + (size_t)(t + 1) * T::WG_B, tile_bytes<QT, BPR, R>(sg.M, t + 1), st);
+    if (t + 1 < te) {
+      nb = tile_bytes<QT, BPR, R>(sg.M, t + 1);
+      stage_load<T>(sg.W + (size_t)(t + 1) * T::WG_B, nb, st);
+    }
     float acc[NV * R];
 #pragma unroll
     for (int i = 0; i < NV * R; ++i) acc[i] = 0.f;
@@ -538,40 +550,386 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return 0.5f * x * (1.0f + tanhf(t));
 }
 
-template <int BPR, int R, int PRO>
-__global__ __launch_bounds__(NT) void gateup_kernel(const uint8_t* Wg, const uint8_t* Wu, float* out, uint32_t M,
-                                                    ProArgs pa) {
-  using T = Tile<0, BPR, R>;
-  constexpr int K = BPR * 256;
-  extern __shared__ __align__(16) uint8_t smem[];
-  const uint32_t t = blockIdx.x;
-  const int wave = threadIdx.x >> 6;
-  XRegs<1, K> xr;
-  pro_load<1, K, PRO>(xr, pa);
-  __builtin_amdgcn_sched_barrier(0);
-  const uint32_t nb = tile_bytes<0, BPR, R>(M, t);
-  Stage<T::LPT> sg, su;
-  stage_load<T>(Wg + (size_t)t * T::WG_B, nb, sg);
-  stage_load<T>(Wu + (size_t)t * T::WG_B, nb, su);
-  const XView xv = carve(smem, K, 1);
-  uint8_t* wg_l = smem + align16(xview_bytes(K, 1));
-  uint8_t* wu_l = wg_l + T::LDS_B;
-  pro_finish<1, K, PRO>(xr, xv, pa);
-  stage_store<T>(wg_l, sg);
-  stage_store<T>(wu_l, su);
-  __syncthreads();
-  float ag[R], au[R];
+// ---------------------------------------------------------------------------
+// M=1 matvec with register-resident activation digits
+// ---------------------------------------------------------------------------
+//
+// Thread (slot, unit): unit u = 4b + g is one quarter of super-block b, i.e.
+// 64 weights of every row. The thread holds the digits of those 64
+// activations in registers for the whole launch and multiplies them with the
+// matching quarter of the row its slot owns in each tile, reading the
+// weight bytes from the tile staged in LDS. Per-row partials meet in an LDS
+// buffer, where a group of lanes per row adds them up. The digits are
+// computed once per workgroup from coalesced loads, eight lanes per 32-element
+// sub-block exchanging their maxima and sums through DPP.
+
+// NWV waves per workgroup; a tile is one row per slot.
+template <int BPR, int NWV>
+struct MvGeom {
+  static constexpr int U = 4 * BPR;                // units per row
+  static constexpr int NTH = 64 * NWV;             // threads per workgroup
+  static constexpr int SLOTS = NTH / U;            // rows in flight
+  static constexpr int NSB = BPR * 8;              // 32-element sub-blocks
+  static_assert(SLOTS >= 1 && SLOTS * U == NTH, "slots tile the workgroup exactly");
+};
+
+template <int QT, int BPR, int NWV>
+struct MvTile {
+  using G = MvGeom<BPR, NWV>;
+  static constexpr int BYTES = BlockOf<QT>::BYTES;
+  static constexpr int TR = G::SLOTS;             // rows per tile
+  static constexpr uint32_t RB = BPR * BYTES;     // bytes per row
+  static constexpr uint32_t TB = TR * RB;         // bytes per tile
+  static constexpr int LPT = (int)((TB + 16 * G::NTH - 1) / (16 * G::NTH));
+  static constexpr uint32_t LDS_T = (TB + 15) / 16 * 16;
+  static constexpr int RS = G::U + 4;             // reduction row stride (floats)
+  // a row's U partials are added by RG lanes of one wave, U / RG each
+  static constexpr int RG = (G::U & -G::U) < 64 ? (G::U & -G::U) : 64;
+  static_assert(G::U % RG == 0 && 64 % RG == 0, "reduction groups stay inside a wave");
+};
+
+// LDS layout: digits | sub-block scales | sums | 16-run offsets | block-sum slots | reductions | tiles
+template <int BPR>
+struct MvX {
+  static constexpr int K = BPR * 256;
+  static constexpr int NSB = BPR * 8;
+  static constexpr size_t HI = 0, LO = K, S = 2 * (size_t)K, SUM = S + 4 * NSB, C16 = SUM + 4 * NSB,
+                          RED8 = C16 + 16 * NSB, END = RED8 + 64;
+};
+
+template <int QT, int BPR, int NWV, int NMAT>
+__host__ __device__ constexpr size_t mv_lds_bytes() {
+  using T = MvTile<QT, BPR, NWV>;
+  return align16(MvX<BPR>::END) + NMAT * align16((size_t)T::TR * T::RS * 4) + NMAT * (size_t)T::LDS_T;
+}
+
+template <class T, int NTH>
+__device__ __forceinline__ void mv_stage_load(const uint8_t* src, uint32_t nbytes, Stage<T::LPT>& st) {
 #pragma unroll
-  for (int i = 0; i < R; ++i) ag[i] = au[i] = 0.f;
-  tile_compute<0, BPR, R, 1>(xv, wg_l + wave * T::WAVE_B, ag);
-  tile_compute<0, BPR, R, 1>(xv, wu_l + wave * T::WAVE_B, au);
-  const float vg = wave_fold<R>(ag);
-  const float vu = wave_fold<R>(au);
+  for (int i = 0; i < T::LPT; ++i)
+    st.r[i] = *(const u32x4a*)(src + chunk_off((uint32_t)(i * NTH + threadIdx.x) * 16u, nbytes));
+}
+
+template <class T, int NTH>
+__device__ __forceinline__ void mv_stage_store(uint8_t* lds, uint32_t nbytes, const Stage<T::LPT>& st) {
+#pragma unroll
+  for (int i = 0; i < T::LPT; ++i) {
+    const uint32_t off = (uint32_t)(i * NTH + threadIdx.x) * 16u;
+    if (off < T::LDS_T) *(u32x4a*)(lds + chunk_off(off, nbytes)) = st.r[i];
+  }
+}
+
+template <int QT, int BPR, int NWV>
+__device__ __forceinline__ uint32_t mv_tile_bytes(uint32_t M, uint32_t t) {
+  using T = MvTile<QT, BPR, NWV>;
+  const uint64_t total = (uint64_t)M * T::RB;
+  const uint64_t o = (uint64_t)t * T::TB;
+  return o >= total ? 0u : (uint32_t)min((uint64_t)T::TB, total - o);
+}
+
+// DPP lane exchanges inside a row of 16 lanes (VALU, no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dppi(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+constexpr int kDppXor1 = 0xb1;      // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4e;      // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within 8 lanes
+
+// Activation registers of one thread: the float4 at element 4*tid + 4*NTH*p.
+// Eight consecutive lanes hold one 32-element sub-block.
+template <int BPR, int NWV, int PRO>
+struct MvPro {
+  static constexpr int K = BPR * 256;
+  static constexpr int NTH = MvGeom<BPR, NWV>::NTH;
+  static constexpr int XP = (K + 4 * NTH - 1) / (4 * NTH);
+  float4 x[XP];
+  float4 r[PRO == 2 ? XP : 1];
+  uint2 w1[PRO >= 1 ? XP : 1];
+  uint2 w2[PRO == 2 ? XP : 1];
+  // Every workgroup reads the whole vector; starting each one at a different
+  // sub-block spreads these broadcast reads over the L2 channels instead of
+  // all workgroups asking for the same lines at the same moment.
+  __device__ static int rot() { return (int)((blockIdx.x * 37u) % (uint32_t)(K / 32)) * 32; }
+  __device__ static int slot(int p) { return 4 * (int)threadIdx.x + 4 * NTH * p; }
+  __device__ static bool live(int p) { return slot(p) < K; }
+  // element held at round p (valid when live(p))
+  __device__ static int elem(int p) {
+    const int f = slot(p) + rot();
+    return f >= K ? f - K : f;
+  }
+};
+
+template <int BPR, int NWV, int PRO>
+__device__ __forceinline__ void mv_pro_load(MvPro<BPR, NWV, PRO>& P, const ProArgs& a) {
+  using PP = MvPro<BPR, NWV, PRO>;
+  // Unconditional loads (see chunk_off). Lanes past K read element 0 again;
+  // they form whole 8-lane sub-block groups whose digits are never stored,
+  // and their squares are masked out of the norms.
+#pragma unroll
+  for (int p = 0; p < PP::XP; ++p) {
+    const int fc = PP::live(p) ? PP::elem(p) : 0;
+    P.x[p] = *(const float4*)(a.x + fc);
+    if constexpr (PRO >= 1) P.w1[p] = *(const uint2*)(a.w1 + fc);
+    if constexpr (PRO == 2) {
+      P.r[p] = *(const float4*)(a.residual + fc);
+      P.w2[p] = *(const uint2*)(a.w2 + fc);
+    }
+  }
+}
+
+// Normalises (PRO 1/2) and digitises the activations into LDS, then barrier.
+template <int BPR, int NWV, int PRO>
+__device__ __forceinline__ void mv_pro_finish(MvPro<BPR, NWV, PRO>& P, uint8_t* smem, const ProArgs& a) {
+  using PP = MvPro<BPR, NWV, PRO>;
+  using X = MvX<BPR>;
+  float* red8 = (float*)(smem + X::RED8);
+  if constexpr (PRO >= 1) {
+    float ss = 0.f;
+#pragma unroll
+    for (int p = 0; p < PP::XP; ++p) {
+      const float q = sumsq(P.x[p]);
+      ss += PP::live(p) ? q : 0.f;
+    }
+    ss = g4d::block_sum<NWV>(ss, red8);
+    const float inv1 = 1.0f / sqrtf(ss / (float)X::K + a.eps);
+    if constexpr (PRO == 1) {
+#pragma unroll
+      for (int p = 0; p < PP::XP; ++p) P.x[p] = mul_w(P.x[p], P.w1[p], inv1);
+    } else {
+      float ss2 = 0.f;
+#pragma unroll
+      for (int p = 0; p < PP::XP; ++p) {
+        const float4 t = mul_w(P.x[p], P.w1[p], inv1);
+        const float4 h = make_float4(P.r[p].x + t.x, P.r[p].y + t.y, P.r[p].z + t.z, P.r[p].w + t.w);
+        P.x[p] = h;
+        const float q = sumsq(h);
+        ss2 += PP::live(p) ? q : 0.f;
+        if (a.h_out && blockIdx.x == 0 && PP::live(p)) *(float4*)(a.h_out + PP::elem(p)) = h;
+      }
+      ss2 = g4d::block_sum<NWV>(ss2, red8);
+      const float inv2 = 1.0f / sqrtf(ss2 / (float)X::K + a.eps);
+#pragma unroll
+      for (int p = 0; p < PP::XP; ++p) P.x[p] = mul_w(P.x[p], P.w2[p], inv2);
+    }
+  }
   const int lane = threadIdx.x & 63;
-  constexpr int G = 64 / R;
-  if ((lane % G) == 0) {
-    const uint32_t row = t * T::ROWS_WG + wave * R + lane / G;
-    if (row < M) out[row] = gelu_tanh(vg) * vu;
+#pragma unroll
+  for (int p = 0; p < PP::XP; ++p) {
+    const int f = PP::elem(p);
+    const bool lv = PP::live(p);
+    const float4 v = P.x[p];
+    float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    float sm = (v.x + v.y) + (v.z + v.w);
+    am = fmaxf(am, dpp<kDppXor1>(am));
+    sm += dpp<kDppXor1>(sm);
+    am = fmaxf(am, dpp<kDppXor2>(am));
+    sm += dpp<kDppXor2>(sm);
+    am = fmaxf(am, dpp<kDppHalfMirror>(am));
+    sm += dpp<kDppHalfMirror>(sm);
+    const float inv = am > 0.f ? XQ / am : 0.f;
+    const float xs[4] = {v.x, v.y, v.z, v.w};
+    uint32_t ph = 0, pl = 0;
+    int shi = 0, slo = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int q = (int)__builtin_rintf(xs[e] * inv);
+      const int lo = ((q + 128) & 255) - 128;
+      const int hi = (q - lo) >> 8;
+      shi += hi;
+      slo += lo;
+      ph |= (uint32_t)(hi & 255) << (8 * e);
+      pl |= (uint32_t)(lo & 255) << (8 * e);
+    }
+    shi += dppi<kDppXor1>(shi);
+    slo += dppi<kDppXor1>(slo);
+    shi += dppi<kDppXor2>(shi);
+    slo += dppi<kDppXor2>(slo);
+    if (lv) {
+      *(uint32_t*)(smem + X::HI + f) = ph;
+      *(uint32_t*)(smem + X::LO + f) = pl;
+      if ((lane & 7) == 0) {
+        ((float*)(smem + X::S))[f / 32] = am * (1.0f / XQ);
+        ((float*)(smem + X::SUM))[f / 32] = sm;
+      }
+      if ((lane & 3) == 0) ((int2*)(smem + X::C16))[f / 16] = make_int2(32 * shi, 32 * slo);
+    }
+  }
+  __syncthreads();
+}
+
+// Digits and constants of one unit, held in registers.
+template <int QT>
+struct MvUnit {
+  uint32_t hi[16], lo[16];
+  float s[4];   // Q4_K: s[0..1] scales of sub-blocks 2u, 2u+1, s[2..3] their sums; Q6_K: scale of run k
+  int2 c[4];    // Q6_K: 32*sum(hi), 32*sum(lo) of run k
+};
+
+template <int QT, int BPR>
+__device__ __forceinline__ void mv_unit_load(MvUnit<QT>& X, const uint8_t* smem, int u) {
+  using XL = MvX<BPR>;
+  const float* s = (const float*)(smem + XL::S);
+  if constexpr (QT == 0) {
+    // elements [64u, 64u + 64): low nibbles -> sub-block 2u, high nibbles -> 2u + 1
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint4 th = *(const uint4*)(smem + XL::HI + 64 * u + 16 * c);
+      const uint4 tl = *(const uint4*)(smem + XL::LO + 64 * u + 16 * c);
+      X.hi[4 * c] = th.x; X.hi[4 * c + 1] = th.y; X.hi[4 * c + 2] = th.z; X.hi[4 * c + 3] = th.w;
+      X.lo[4 * c] = tl.x; X.lo[4 * c + 1] = tl.y; X.lo[4 * c + 2] = tl.z; X.lo[4 * c + 3] = tl.w;
+    }
+    const float* sum = (const float*)(smem + XL::SUM);
+    X.s[0] = s[2 * u];
+    X.s[1] = s[2 * u + 1];
+    X.s[2] = sum[2 * u];
+    X.s[3] = sum[2 * u + 1];
+  } else {
+    // runs k = 0..3 at element 256b + 128h + 32k + l0 (src/gguf.ts:344-361)
+    const int b = u >> 2, g = u & 3, h = g >> 1, l0 = 16 * (g & 1);
+    const int4* c16 = (const int4*)(smem + XL::C16);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int e = 256 * b + 128 * h + 32 * k + l0;
+      const uint4 th = *(const uint4*)(smem + XL::HI + e);
+      const uint4 tl = *(const uint4*)(smem + XL::LO + e);
+      X.hi[4 * k] = th.x; X.hi[4 * k + 1] = th.y; X.hi[4 * k + 2] = th.z; X.hi[4 * k + 3] = th.w;
+      X.lo[4 * k] = tl.x; X.lo[4 * k + 1] = tl.y; X.lo[4 * k + 2] = tl.z; X.lo[4 * k + 3] = tl.w;
+      X.s[k] = s[e / 32];
+      const int4 cc = c16[e / 32];
+      X.c[k] = (l0 == 0) ? make_int2(cc.x, cc.y) : make_int2(cc.z, cc.w);
+    }
+  }
+}
+
+// Dot product of unit u of one row (block at blk in LDS) with the resident digits.
+template <int QT>
+__device__ __forceinline__ float mv_unit_dot(const MvUnit<QT>& X, const uint8_t* blk, int g) {
+  if constexpr (QT == 0) {
+    const uint4 hd = *(const uint4*)blk;
+    const uint4 q0 = *(const uint4*)(blk + 16 + 32 * g);
+    const uint4 q1 = *(const uint4*)(blk + 32 + 32 * g);
+    float sc_lo, sc_hi, m_lo, m_hi;
+    q4k_scales(hd.y, hd.z, hd.w, g, sc_lo, sc_hi, m_lo, m_hi);
+    const uint32_t qa[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    int ah0 = 0, al0 = 0, ah1 = 0, al1 = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t nl = qa[k] & 0x0f0f0f0fu, nh = (qa[k] >> 4) & 0x0f0f0f0fu;
+      ah0 = __builtin_amdgcn_sdot4((int)nl, (int)X.hi[k], ah0, false);
+      al0 = __builtin_amdgcn_sdot4((int)nl, (int)X.lo[k], al0, false);
+      ah1 = __builtin_amdgcn_sdot4((int)nh, (int)X.hi[8 + k], ah1, false);
+      al1 = __builtin_amdgcn_sdot4((int)nh, (int)X.lo[8 + k], al1, false);
+    }
+    const float d = g4d::f16_bits_to_f32(hd.x & 0xffffu);
+    const float dmin = g4d::f16_bits_to_f32(hd.x >> 16);
+    const float i0 = (float)(ah0 * 256 + al0), i1 = (float)(ah1 * 256 + al1);
+    return d * (sc_lo * X.s[0] * i0 + sc_hi * X.s[1] * i1) - dmin * (m_lo * X.s[2] + m_hi * X.s[3]);
+  } else {
+    const int h = g >> 1, l0 = 16 * (g & 1);
+    uint32_t A[4], B[4], H[4];
+    lds_piece(blk + 64 * h + l0, A);
+    lds_piece(blk + 64 * h + 32 + l0, B);
+    lds_piece(blk + 128 + 32 * h + l0, H);
+    const int8_t* scp = (const int8_t*)(blk + 192 + 8 * h + (g & 1));
+    const float dd = g4d::f16_bits_to_f32(*(const uint16_t*)(blk + 208));
+    float part = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      int ah = 0, al = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t q;
+        if (k == 0) q = (A[j] & 0x0f0f0f0fu) | ((H[j] << 4) & 0x30303030u);
+        else if (k == 1) q = (B[j] & 0x0f0f0f0fu) | ((H[j] << 2) & 0x30303030u);
+        else if (k == 2) q = ((A[j] >> 4) & 0x0f0f0f0fu) | (H[j] & 0x30303030u);
+        else q = ((B[j] >> 4) & 0x0f0f0f0fu) | ((H[j] >> 2) & 0x30303030u);
+        ah = __builtin_amdgcn_sdot4((int)q, (int)X.hi[4 * k + j], ah, false);
+        al = __builtin_amdgcn_sdot4((int)q, (int)X.lo[4 * k + j], al, false);
+      }
+      const int I = (ah - X.c[k].x) * 256 + (al - X.c[k].y);
+      part += (float)scp[2 * k] * X.s[k] * (float)I;
+    }
+    return part * dd;
+  }
+}
+
+// NMAT = 1: y, or softcap(y) when cap > 0 (shaders/logit_softcap.wgsl), for
+// each segment's rows. NMAT = 2: gate/up pair, out = gelu(gate) * up
+// (shaders/gelu_mul.wgsl:10-16).
+template <int QT, int BPR, int NWV, int PRO, int NMAT>
+__global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8_t* w_up, ProArgs pa, float cap) {
+  using G = MvGeom<BPR, NWV>;
+  using T = MvTile<QT, BPR, NWV>;
+  constexpr int NTH = G::NTH;
+  extern __shared__ __align__(16) uint8_t smem[];
+  int si = 0;
+#pragma unroll
+  for (int i = 1; i < 4; ++i)
+    if (i < segs.n && blockIdx.x >= segs.s[i].wg_begin) si = i;
+  const GemvSeg sg = segs.s[si];
+  const uint8_t* W[2] = {sg.W, w_up};
+  const uint32_t tiles = (sg.M + T::TR - 1) / T::TR;
+  const uint32_t tb = (blockIdx.x - sg.wg_begin) * segs.rep;
+  const uint32_t te = min(tiles, tb + segs.rep);
+  const int tid = threadIdx.x;
+  const int slot = tid / G::U, u = tid % G::U;
+  float* red = (float*)(smem + align16(MvX<BPR>::END));
+  uint8_t* tl = smem + align16(MvX<BPR>::END) + NMAT * align16((size_t)T::TR * T::RS * 4);
+
+  MvPro<BPR, NWV, PRO> P;
+  mv_pro_load<BPR, NWV, PRO>(P, pa);
+  __builtin_amdgcn_sched_barrier(0);
+  Stage<T::LPT> st[NMAT];
+  uint32_t nb = mv_tile_bytes<QT, BPR, NWV>(sg.M, tb);
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m) mv_stage_load<T, NTH>(W[m] + (size_t)tb * T::TB, nb, st[m]);
+  __builtin_amdgcn_sched_barrier(0);  // every weight load is issued before the activations are used
+  mv_pro_finish<BPR, NWV, PRO>(P, smem, pa);
+  MvUnit<QT> X;
+  mv_unit_load<QT, BPR>(X, smem, u);
+
+  for (uint32_t t = tb; t < te; ++t) {
+    __syncthreads();  // digits read (first tile) / previous tile reduced
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m) mv_stage_store<T, NTH>(tl + m * T::LDS_T, nb, st[m]);
+    __syncthreads();
+    if (t + 1 < te) {
+      nb = mv_tile_bytes<QT, BPR, NWV>(sg.M, t + 1);
+#pragma unroll
+      for (int m = 0; m < NMAT; ++m) mv_stage_load<T, NTH>(W[m] + (size_t)(t + 1) * T::TB, nb, st[m]);
+    }
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m) {
+      const uint8_t* blk = tl + m * T::LDS_T + slot * T::RB + (u >> 2) * T::BYTES;
+      red[m * T::TR * T::RS + slot * T::RS + u] = mv_unit_dot<QT>(X, blk, u & 3);
+    }
+    __syncthreads();
+    const int gl = tid % T::RG;
+    for (int r = tid / T::RG; r < T::TR; r += NTH / T::RG) {  // uniform within a group
+      float y[NMAT];
+#pragma unroll
+      for (int m = 0; m < NMAT; ++m) {
+        const float* rr = red + m * T::TR * T::RS + r * T::RS + gl;
+        float a = rr[0];
+#pragma unroll
+        for (int v = 1; v < G::U / T::RG; ++v) a += rr[v * T::RG];
+#pragma unroll
+        for (int o = T::RG / 2; o > 0; o >>= 1) a += __shfl_xor(a, o, 64);
+        y[m] = a;
+      }
+      const uint32_t row = t * T::TR + r;
+      if (gl == 0 && row < sg.M) {
+        float v;
+        if constexpr (NMAT == 2) v = gelu_tanh(y[0]) * y[1];
+        else v = cap > 0.f ? softcap(y[0], cap) : y[0];
+        sg.Y[row] = v;
+      }
+    }
   }
 }
 
@@ -756,13 +1114,11 @@ int launch_bpr(g4_ctx* ctx, const LaunchReq& q) {
   }
 }
 
+// Batched activations (NV > 1): staged tiles, digits read from LDS per block.
 template <int QT>
 int launch_qt(g4_ctx* ctx, const LaunchReq& q) {
-  if (q.pro == 1) return q.epi ? launch_bpr<QT, 1, 1, 1>(ctx, q) : launch_bpr<QT, 1, 1, 0>(ctx, q);
-  if (q.pro == 2) return q.epi ? launch_bpr<QT, 1, 2, 1>(ctx, q) : launch_bpr<QT, 1, 2, 0>(ctx, q);
-  if (q.epi) return q.nv == 1 ? launch_bpr<QT, 1, 0, 1>(ctx, q) : G4_ERR_UNSUPPORTED;
+  if (q.pro != 0 || q.epi != 0) return G4_ERR_UNSUPPORTED;
   switch (q.nv) {
-    case 1: return launch_bpr<QT, 1, 0, 0>(ctx, q);
     case 2: return launch_bpr<QT, 2, 0, 0>(ctx, q);
     case 4: return launch_bpr<QT, 4, 0, 0>(ctx, q);
     case 8: return launch_bpr<QT, 8, 0, 0>(ctx, q);
@@ -770,7 +1126,92 @@ int launch_qt(g4_ctx* ctx, const LaunchReq& q) {
   }
 }
 
-int launch_gemv(g4_ctx* ctx, const LaunchReq& q) { return q.qt == 0 ? launch_qt<0>(ctx, q) : launch_qt<1>(ctx, q); }
+// One activation vector: register-resident digits (mv_kernel). Each
+// workgroup digitises the whole activation vector and walks its tiles one row
+// per slot; more waves per workgroup shorten both serial phases. The launch
+// takes the widest workgroup that still leaves kMvMinWgs tiles; matrices
+// larger than two workgroups per CU are walked tile by tile.
+constexpr uint32_t kMvMinWgs = 160;
+
+template <int QT, int BPR, int NWV, int PRO, int NMAT>
+int mv_launch(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
+  using T = MvTile<QT, BPR, NWV>;
+  GemvSegs sg{};
+  uint32_t tiles = 0;
+  for (int i = 0; i < q.nseg; ++i) tiles += ceil_div(q.segs[i].M, T::TR);
+  sg.rep = ceil_div(tiles, 2u * (uint32_t)ctx->num_cus);
+  uint32_t wgs = 0;
+  for (int i = 0; i < q.nseg; ++i) {
+    sg.s[i] = q.segs[i];
+    sg.s[i].wg_begin = wgs;
+    wgs += ceil_div(ceil_div(q.segs[i].M, T::TR), sg.rep);
+  }
+  sg.n = q.nseg;
+  if (wgs == 0) return G4_OK;
+  const size_t lds = mv_lds_bytes<QT, BPR, NWV, NMAT>();
+  int rc = claim_lds((const void*)mv_kernel<QT, BPR, NWV, PRO, NMAT>, ctx, lds);
+  if (rc) return rc;
+  hipLaunchKernelGGL((mv_kernel<QT, BPR, NWV, PRO, NMAT>), dim3(wgs), dim3(64 * NWV), lds, ctx->stream, sg, w_up,
+                     q.pa, q.epi ? q.cap : 0.f);
+  G4_LAUNCHED(ctx, "mv");
+  return G4_OK;
+}
+
+// workgroup widths in waves for a row of BPR super-blocks (slots must tile it)
+template <int BPR> struct MvWaves { static constexpr int A = 12, B = 6, C = 3; };
+template <> struct MvWaves<32> { static constexpr int A = 12, B = 6, C = 4; };
+
+template <int QT, int BPR, int PRO, int NMAT>
+int mv_rows(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
+  using Wv = MvWaves<BPR>;
+  auto tiles = [&](uint32_t slots) {
+    uint32_t t = 0;
+    for (int i = 0; i < q.nseg; ++i) t += ceil_div(q.segs[i].M, slots);
+    return t;
+  };
+  if (tiles(MvGeom<BPR, Wv::A>::SLOTS) >= kMvMinWgs) return mv_launch<QT, BPR, Wv::A, PRO, NMAT>(ctx, q, w_up);
+  if (tiles(MvGeom<BPR, Wv::B>::SLOTS) >= kMvMinWgs) return mv_launch<QT, BPR, Wv::B, PRO, NMAT>(ctx, q, w_up);
+  return mv_launch<QT, BPR, Wv::C, PRO, NMAT>(ctx, q, w_up);
+}
+
+template <int QT, int PRO, int NMAT>
+int mv_bpr(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
+  if constexpr (PRO != 0) {
+    // the normalising prologues serve the hidden vector (1536 or 2048 wide)
+    switch (q.N / 256) {
+      case 6: return mv_rows<QT, 6, PRO, NMAT>(ctx, q, w_up);
+      case 8: return mv_rows<QT, 8, PRO, NMAT>(ctx, q, w_up);
+      default: return G4_ERR_UNSUPPORTED;
+    }
+  } else {
+    switch (q.N / 256) {
+      case 4: return mv_rows<QT, 4, PRO, NMAT>(ctx, q, w_up);
+      case 6: return mv_rows<QT, 6, PRO, NMAT>(ctx, q, w_up);
+      case 8: return mv_rows<QT, 8, PRO, NMAT>(ctx, q, w_up);
+      case 12: return mv_rows<QT, 12, PRO, NMAT>(ctx, q, w_up);
+      case 16: return mv_rows<QT, 16, PRO, NMAT>(ctx, q, w_up);
+      case 24: return mv_rows<QT, 24, PRO, NMAT>(ctx, q, w_up);
+      case 32: return mv_rows<QT, 32, PRO, NMAT>(ctx, q, w_up);
+      case 48: return mv_rows<QT, 48, PRO, NMAT>(ctx, q, w_up);
+      default: return G4_ERR_UNSUPPORTED;
+    }
+  }
+}
+
+template <int QT>
+int launch_mv(g4_ctx* ctx, const LaunchReq& q) {
+  switch (q.pro) {
+    case 0: return mv_bpr<QT, 0, 1>(ctx, q, nullptr);
+    case 1: return mv_bpr<QT, 1, 1>(ctx, q, nullptr);
+    case 2: return mv_bpr<QT, 2, 1>(ctx, q, nullptr);
+    default: return G4_ERR_UNSUPPORTED;
+  }
+}
+
+int launch_gemv(g4_ctx* ctx, const LaunchReq& q) {
+  if (q.nv == 1) return q.qt == 0 ? launch_mv<0>(ctx, q) : launch_mv<1>(ctx, q);
+  return q.qt == 0 ? launch_qt<0>(ctx, q) : launch_qt<1>(ctx, q);
+}
 
 bool supported_bpr(uint32_t bpr) {
   return bpr == 4 || bpr == 6 || bpr == 8 || bpr == 12 || bpr == 16 || bpr == 24 || bpr == 32 || bpr == 48;
@@ -829,14 +1270,9 @@ int matmul_quant(g4_ctx* ctx, const char* fn, int qt, const float* in, const voi
 
 template <int BPR, int PRO>
 int launch_gateup(g4_ctx* ctx, const uint8_t* wg, const uint8_t* wu, float* out, uint32_t M, const ProArgs& pa) {
-  constexpr int R = RowsFor<BPR>::R;
-  const dim3 grid(ceil_div(M, R * NW));
-  const size_t lds = align16(xview_bytes(BPR * 256, 1)) + 2 * Tile<0, BPR, R>::LDS_B;
-  int rc = claim_lds((const void*)gateup_kernel<BPR, R, PRO>, ctx, lds);
-  if (rc) return rc;
-  hipLaunchKernelGGL((gateup_kernel<BPR, R, PRO>), grid, dim3(NT), lds, ctx->stream, wg, wu, out, M, pa);
-  G4_LAUNCHED(ctx, "gateup");
-  return G4_OK;
+  const GemvSeg seg{wg, out, M, 0};
+  const LaunchReq q{0, &seg, 1, BPR * 256, 1, PRO, 0, 0.f, pa, M};
+  return mv_rows<0, BPR, PRO, 2>(ctx, q, wu);
 }
 
 }  // namespace
@@ -887,7 +1323,7 @@ int g4_rmsNormMatmul_q4k(g4_ctx* ctx, const float* x, const uint16_t* norm_w, co
   rc = check_w(__func__, 0, weight);
   if (rc) return rc;
   G4_REQUIRE(norm_w && ((uintptr_t)norm_w & 7) == 0, "g4_rmsNormMatmul_q4k: norm weight null or not 8-byte aligned");
-  G4_REQUIRE(supported_bpr(p.N / 256) && p.N <= 8192, "g4_rmsNormMatmul_q4k: N=%u unsupported", p.N);
+  G4_REQUIRE(p.N == 1536 || p.N == 2048, "g4_rmsNormMatmul_q4k: N=%u unsupported (1536 or 2048)", p.N);
   GemvSeg s{(const uint8_t*)weight, y, p.M, 0};
   LaunchReq q{0, &s, 1, p.N, 1, 1, 0, 0.f, ProArgs{x, norm_w, nullptr, nullptr, nullptr, eps}, p.M};
   return launch_gemv(ctx, q);
@@ -911,8 +1347,8 @@ int g4_normAddGateUpGelu_q4k(g4_ctx* ctx, const float* o, const uint16_t* w_post
   switch (p.N / 256) {
     case 6: return launch_gateup<6, 2>(ctx, wg, wu, out, p.M, pa);
     case 8: return launch_gateup<8, 2>(ctx, wg, wu, out, p.M, pa);
-    case 16: return launch_gateup<16, 2>(ctx, wg, wu, out, p.M, pa);
-    default: return g4::set_error(G4_ERR_UNSUPPORTED, "g4_normAddGateUpGelu_q4k: N=%u unsupported", p.N);
+    default:
+      return g4::set_error(G4_ERR_UNSUPPORTED, "g4_normAddGateUpGelu_q4k: N=%u unsupported (1536 or 2048)", p.N);
   }
 }
 
@@ -924,8 +1360,7 @@ int g4_normAddMatmulSegments(g4_ctx* ctx, int wtype, const float* x, const uint1
   G4_REQUIRE(nseg >= 1 && nseg <= 4, "g4_normAddMatmulSegments: 1..4 segments");
   G4_REQUIRE(x && w1 && weights && outputs && rows, "g4_normAddMatmulSegments: null buffer");
   G4_REQUIRE(!residual == !w2, "g4_normAddMatmulSegments: residual and w2 go together");
-  G4_REQUIRE(N % 256 == 0 && supported_bpr(N / 256) && N <= 8192, "g4_normAddMatmulSegments: N=%u unsupported",
-             N);
+  G4_REQUIRE(N == 1536 || N == 2048, "g4_normAddMatmulSegments: N=%u unsupported (1536 or 2048)", N);
   G4_REQUIRE(((uintptr_t)x & 15) == 0 && (!residual || ((uintptr_t)residual & 15) == 0) &&
                  (!h_out || ((uintptr_t)h_out & 15) == 0),
              "g4_normAddMatmulSegments: activations must be 16-byte aligned");

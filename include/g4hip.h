@@ -261,7 +261,8 @@ int g4_topk256(g4_ctx* ctx, const float* logits, float* result, uint32_t size);
 /* of the per-key kernels above, named in its comment)                       */
 /* ------------------------------------------------------------------------ */
 
-/* rmsNorm -> matmulQuant: y = W . (x * w / rms(x)). src/engine.ts:1546-1547. */
+/* rmsNorm -> matmulQuant: y = W . (x * w / rms(x)). src/engine.ts:1546-1547.
+ * p.N (the hidden width) is 1536 or 2048. */
 int g4_rmsNormMatmul_q4k(g4_ctx* ctx, const float* x, const uint16_t* norm_w, const void* weight,
                          float* y, g4_matmul_params p, float eps);
 /* fusedNormAdd -> rmsNorm -> matmulQuant gate/up -> geluMul:
@@ -269,7 +270,7 @@ int g4_rmsNormMatmul_q4k(g4_ctx* ctx, const float* x, const uint16_t* norm_w, co
  *   x = h * w_pre / rms(h)
  *   out = gelu(W_gate . x) * (W_up . x)
  * src/engine.ts:1587-1604. Gate and up are separate raw Q4_K tensors of
- * [I, N]; p.M = I, p.N = N. */
+ * [I, N]; p.M = I, p.N = N (the hidden width, 1536 or 2048). */
 int g4_normAddGateUpGelu_q4k(g4_ctx* ctx, const float* o, const uint16_t* w_post,
                              const float* residual, const uint16_t* w_pre, const void* w_gate,
                              const void* w_up, float* h_out, float* out, g4_matmul_params p,
@@ -283,7 +284,8 @@ int g4_normAddGateUpGelu_q4k(g4_ctx* ctx, const float* o, const uint16_t* w_post
  *                      x' = h * w2 / rms(h)
  *   outputs[i] = weights[i] . x'  (rows[i] x N), then tanh(y/cap)*cap if
  *   softcap_cap != 0.
- * wtype 0 = Q4_K, 1 = Q6_K; N <= 8192; norm weights are f16[N]. */
+ * wtype 0 = Q4_K, 1 = Q6_K; N (the hidden width) is 1536 or 2048; norm
+ * weights are f16[N]. */
 int g4_normAddMatmulSegments(g4_ctx* ctx, int wtype, const float* x, const uint16_t* w1,
                              const float* residual, const uint16_t* w2, float* h_out,
                              const void* const* weights, float* const* outputs,
