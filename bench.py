@@ -117,6 +117,19 @@ def kernel_census(ctx, dec: Decoder, reps: int):
     return out
 
 
+def measured_traffic(kind):
+    """HBM bytes per launch of a census kind, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (scaled by the copy calibration), or None
+    when that summary does not cover the kind."""
+    path = os.path.join(ROOT, "profiles", "decode_b1_e2b_hbm_traffic.json")
+    try:
+        with open(path) as f:
+            entry = json.load(f)["entries"].get(kind)
+    except (OSError, ValueError, KeyError):
+        return None
+    return None if entry is None else entry["bytes_per_launch"]
+
+
 def gemv_cfg0(ctx, copies=101, rounds=5):
     """Config-0 GEMV: W [6144 x 1536] Q4_K, x f32[1536], y f32[6144]; weights
     rotated over `copies` buffers (> 2x the 256 MB last-level cache)."""
@@ -139,53 +152,54 @@ def gemv_cfg0(ctx, copies=101, rounds=5):
             "frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, "copies": copies}
 
 
-def cpu_baseline(layers_sample=2, head_rows=8192):
-    """Times the CPU oracle (1 thread, f64 accumulation) on a bounded sample
-    of the same step: `layers_sample` full layers at the same context plus
-    `head_rows` rows of the LM head, scaled to one token."""
+def cpu_baseline(tokens=5):
+    """Times the CPU oracle (plain C, 1 thread, f64 accumulation) on `tokens`
+    whole decode steps of the same workload: 35 E2B-shaped layers at context
+    START_POS + 1 (local layers windowed, every fifth global) plus the full
+    262144-row Q6_K LM head, softcap and argmax. One set of layer weights is
+    reused for all layers (the cost does not depend on the values); weight
+    generation is outside the timed region."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
     s = E2BShape()
     H, Q, KV, I = s.hidden, s.q_dim, s.kv_dim, s.ffn
-    rng_seed = 7
     Wq, Wk, Wv = O.gen_q4k(1, Q * H // 256), O.gen_q4k(2, KV * H // 256), O.gen_q4k(3, KV * H // 256)
     Wo, Wg, Wu = O.gen_q4k(4, H * Q // 256), O.gen_q4k(5, I * H // 256), O.gen_q4k(6, I * H // 256)
-    Wd = O.gen_q6k(rng_seed, H * I // 256)
+    Wd = O.gen_q6k(7, H * I // 256)
+    Wh = O.gen_q6k(13, s.vocab * H // 256)
     nw = O.gen_normal_f16(8, H, 1.0, 0.1)
     hw = O.gen_normal_f16(9, s.head_dim, 1.0, 0.1)
     L = START_POS + 1
     kc = O.gen_normal_f16(10, (L + 1) * KV)
     vc = O.gen_normal_f16(11, (L + 1) * KV)
     table = np.ones(s.head_dim // 2, np.float16).view(np.uint16)
-    x = O.gen_normal_f32(12, H)
+    x0 = O.gen_normal_f32(12, H)
     t0 = time.perf_counter()
-    for il in range(layers_sample):
-        n = O.rms_norm(x, nw)
-        q = O.matmul(n, Wq, Q, H, "q4k")
-        k = O.matmul(n, Wk, KV, H, "q4k")
-        v = O.per_head_rms_norm_no_weight(O.matmul(n, Wv, KV, H, "q4k"), 1, s.head_dim)
-        q = O.fused_per_head_norm_rope(q, hw, s.n_q_heads, s.head_dim, 1e-6, START_POS, 1e4, 0, table)
-        k = O.fused_per_head_norm_rope(k, hw, 1, s.head_dim, 1e-6, START_POS, 1e4, 0, table)
-        O.kv_cache_store_f16(k, v, kc, vc, 1, s.head_dim, START_POS)
-        a = O.attention(q, kc, vc, s.n_q_heads, 1, s.head_dim, L, 1.0, s.window if il % 5 != 4 else 0)
-        o = O.matmul(a, Wo, H, Q, "q4k")
-        h = O.fused_norm_add(o, nw, x)
-        n2 = O.rms_norm(h, nw)
-        act = O.gelu_mul(O.matmul(n2, Wg, I, H, "q4k"), O.matmul(n2, Wu, I, H, "q4k"))
-        x = O.fused_norm_add(O.matmul(act, Wd, H, I, "q6k"), nw, h)
-    t_layers = time.perf_counter() - t0
-    Wh = O.gen_q6k(13, head_rows * H // 256)
-    t0 = time.perf_counter()
-    lg = O.logit_softcap(O.matmul(O.rms_norm(x, nw), Wh, head_rows, H, "q6k"))
-    O.argmax(lg)
-    t_head = time.perf_counter() - t0
-    per_token = t_layers / layers_sample * s.n_layers + t_head * (s.vocab / head_rows)
-    return {"value": 1.0 / per_token, "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": (f"CPU oracle (C, 1 thread, f64 accumulation): {layers_sample} E2B-shaped layers at "
-                       f"context {START_POS + 1} + {head_rows}/{s.vocab} LM-head rows, "
-                       f"{t_layers + t_head:.1f} s of CPU work, scaled to one token "
-                       f"(35 layers + full LM head)")}
+    for _ in range(tokens):
+        x = x0
+        for il in range(s.n_layers):
+            glob = s.is_global(il)
+            theta = 1e6 if glob else 1e4
+            n = O.rms_norm(x, nw)
+            q = O.matmul(n, Wq, Q, H, "q4k")
+            k = O.matmul(n, Wk, KV, H, "q4k")
+            v = O.per_head_rms_norm_no_weight(O.matmul(n, Wv, KV, H, "q4k"), 1, s.head_dim)
+            q = O.fused_per_head_norm_rope(q, hw, s.n_q_heads, s.head_dim, 1e-6, START_POS, theta, 0, table)
+            k = O.fused_per_head_norm_rope(k, hw, 1, s.head_dim, 1e-6, START_POS, theta, 0, table)
+            O.kv_cache_store_f16(k, v, kc, vc, 1, s.head_dim, START_POS)
+            a = O.attention(q, kc, vc, s.n_q_heads, 1, s.head_dim, L, 1.0, 0 if glob else s.window)
+            h = O.fused_norm_add(O.matmul(a, Wo, H, Q, "q4k"), nw, x)
+            n2 = O.rms_norm(h, nw)
+            act = O.gelu_mul(O.matmul(n2, Wg, I, H, "q4k"), O.matmul(n2, Wu, I, H, "q4k"))
+            x = O.fused_norm_add(O.matmul(act, Wd, H, I, "q6k"), nw, h)
+        lg = O.logit_softcap(O.matmul(O.rms_norm(x, nw), Wh, s.vocab, H, "q6k"))
+        O.argmax(lg)
+    t = time.perf_counter() - t0
+    return {"value": tokens / t, "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": (f"CPU oracle (plain C, 1 thread, f64 accumulation): {tokens} whole decode steps "
+                       f"(35 E2B-shaped layers at context {L} + full 262144-row Q6_K LM head + softcap "
+                       f"+ argmax), {t:.1f} s of CPU work")}
 
 
 def main():
@@ -195,7 +209,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--census-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-layers", type=int, default=3)
+    ap.add_argument("--cpu-tokens", type=int, default=5)
     ap.add_argument("--eager", action="store_true",
                     help="launch the step kernels directly instead of replaying a captured graph "
                          "(for profilers that do not follow graph launches)")
@@ -262,7 +276,7 @@ def main():
     bytes_launch, us_launch = census[dom]["bytes"], census[dom]["us"]
     achieved = bytes_launch / (us_launch * 1e-6) / 1e9
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(dom),
                 "bytes_per_launch": bytes_launch, "us_per_launch": round(us_launch, 3)}
 
     g0 = {} if args.no_gemv0 else gemv_cfg0(ctx)
@@ -270,7 +284,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(layers_sample=args.cpu_layers)
+        cpu = cpu_baseline(tokens=args.cpu_tokens)
         log(f"cpu baseline: {cpu}")
 
     line = {

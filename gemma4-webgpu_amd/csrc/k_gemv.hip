@@ -594,7 +594,7 @@ struct MvX {
   static constexpr int K = BPR * 256;
   static constexpr int NSB = BPR * 8;
   static constexpr size_t HI = 0, LO = K, S = 2 * (size_t)K, SUM = S + 4 * NSB, C16 = SUM + 4 * NSB,
-                          RED8 = C16 + 16 * NSB, END = RED8 + 64;
+                          RED8 = C16 + 16 * NSB, END = RED8 + 128;  // two block sums of up to 16 waves
 };
 
 template <int QT, int BPR, int NWV, int NMAT>
@@ -639,6 +639,31 @@ __device__ __forceinline__ int dppi(int v) {
 constexpr int kDppXor1 = 0xb1;      // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4e;      // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within 8 lanes
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within 16 lanes
+
+// Sum over the wave: DPP inside each 16-lane row, then the four row sums.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  const int iv = __float_as_int(v);
+  return (__int_as_float(__builtin_amdgcn_readlane(iv, 0)) + __int_as_float(__builtin_amdgcn_readlane(iv, 16))) +
+         (__int_as_float(__builtin_amdgcn_readlane(iv, 32)) + __int_as_float(__builtin_amdgcn_readlane(iv, 48)));
+}
+
+// Sum over the workgroup with one barrier; `red` holds NWV floats not reused
+// by another sum before the next barrier.
+template <int NWV>
+__device__ __forceinline__ float block_sum_1(float v, float* red) {
+  v = wave_sum_dpp(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < NWV; ++i) t += red[i];
+  return t;
+}
 
 // Activation registers of one thread: the float4 at element 4*tid + 4*NTH*p.
 // Eight consecutive lanes hold one 32-element sub-block.
@@ -695,7 +720,7 @@ __device__ __forceinline__ void mv_pro_finish(MvPro<BPR, NWV, PRO>& P, uint8_t* 
       const float q = sumsq(P.x[p]);
       ss += PP::live(p) ? q : 0.f;
     }
-    ss = g4d::block_sum<NWV>(ss, red8);
+    ss = block_sum_1<NWV>(ss, red8);
     const float inv1 = 1.0f / sqrtf(ss / (float)X::K + a.eps);
     if constexpr (PRO == 1) {
 #pragma unroll
@@ -711,7 +736,7 @@ __device__ __forceinline__ void mv_pro_finish(MvPro<BPR, NWV, PRO>& P, uint8_t* 
         ss2 += PP::live(p) ? q : 0.f;
         if (a.h_out && blockIdx.x == 0 && PP::live(p)) *(float4*)(a.h_out + PP::elem(p)) = h;
       }
-      ss2 = g4d::block_sum<NWV>(ss2, red8);
+      ss2 = block_sum_1<NWV>(ss2, red8 + 16);
       const float inv2 = 1.0f / sqrtf(ss2 / (float)X::K + a.eps);
 #pragma unroll
       for (int p = 0; p < PP::XP; ++p) P.x[p] = mul_w(P.x[p], P.w2[p], inv2);
@@ -883,6 +908,12 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
 
   MvPro<BPR, NWV, PRO> P;
   mv_pro_load<BPR, NWV, PRO>(P, pa);
+  // Requests leave a CU in issue order across its waves: every wave's
+  // activation loads go out before any wave's weight loads, or the last
+  // waves' activations queue behind the first waves' weight tiles. A bare
+  // s_barrier orders the issue without waiting for any load.
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
   Stage<T::LPT> st[NMAT];
   uint32_t nb = mv_tile_bytes<QT, BPR, NWV>(sg.M, tb);
