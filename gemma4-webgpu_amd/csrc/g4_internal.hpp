@@ -103,11 +103,54 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// DPP lane exchanges inside a row of 16 lanes (VALU; no LDS round trip as
+// __shfl_xor's ds_bpermute has).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dppi(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+constexpr int kDppXor1 = 0xb1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4e;         // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within 8 lanes
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within 16 lanes
+
+// Sum / max over each aligned group of 8 lanes; every lane gets its group's value.
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  return v + dpp<kDppHalfMirror>(v);
+}
+__device__ __forceinline__ float max8(float v) {
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  return fmaxf(v, dpp<kDppHalfMirror>(v));
+}
+// ... over each 16-lane row
+__device__ __forceinline__ float sum16(float v) { v = sum8(v); return v + dpp<kDppMirror>(v); }
+__device__ __forceinline__ float max16(float v) { v = max8(v); return fmaxf(v, dpp<kDppMirror>(v)); }
+
+__device__ __forceinline__ float lane_value(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+// Wave-wide sum / max, wave-uniform result.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = sum16(v);
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = max16(v);
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+
 // Block-wide sum for blockDim.x == 64 * nwaves; `red` holds >= nwaves floats.
 // Every thread gets the total. Contains __syncthreads.
 template <int NWAVES>
 __device__ __forceinline__ float block_sum(float v, float* red) {
-  v = wave_sum(v);
+  v = wave_sum_dpp(v);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   if (lane == 0) red[w] = v;
   __syncthreads();

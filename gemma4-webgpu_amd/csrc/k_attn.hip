@@ -155,6 +155,30 @@ struct VMap {  // V columns / row groups per thread
   static constexpr int VG = HD >= 256 ? 1 : 256 / HD;   // threads sharing a column (row groups)
 };
 
+// Group-of-SL-lanes reductions (SL = 32 or 64, aligned inside a wave): every
+// lane gets its group's value.
+template <int SL>
+__device__ __forceinline__ float group_max(float v) {
+  v = g4d::max16(v);
+  const float a0 = g4d::lane_value(v, 0), a1 = g4d::lane_value(v, 16);
+  const float a2 = g4d::lane_value(v, 32), a3 = g4d::lane_value(v, 48);
+  if constexpr (SL == 64) return fmaxf(fmaxf(a0, a1), fmaxf(a2, a3));
+  return (threadIdx.x & 32) ? fmaxf(a2, a3) : fmaxf(a0, a1);
+}
+template <int SL>
+__device__ __forceinline__ float group_sum(float v) {
+  v = g4d::sum16(v);
+  const float a0 = g4d::lane_value(v, 0), a1 = g4d::lane_value(v, 16);
+  const float a2 = g4d::lane_value(v, 32), a3 = g4d::lane_value(v, 48);
+  if constexpr (SL == 64) return (a0 + a1) + (a2 + a3);
+  return (threadIdx.x & 32) ? a2 + a3 : a0 + a1;
+}
+
+// Order of work: every load this workgroup needs is issued before any result
+// is used, the query side first (all waves, then one s_barrier), then the K
+// and V rows of the chunk. Loads are unconditional at clamped positions (rows
+// past the chunk are masked in the scores), so no branch or loop surrounds a
+// load: the compiler then waits for exactly the loads each step consumes.
 template <int G, int HD, int CP, bool PAGED, bool FUSE>
 __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
   constexpr int P = 32 * CP;        // positions of a chunk
@@ -164,6 +188,8 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
   constexpr int VD = VMap<HD>::VD;
   constexpr int VG = VMap<HD>::VG;
   constexpr int VR = P / VG;        // rows of V per thread
+  constexpr int QE = (G * HD + NT - 1) / NT;  // q elements per thread (t + NT k)
+  constexpr int KE = (HD + NT - 1) / NT;      // k / v elements per thread (fused form)
   static_assert(KS % 8 == 0 && VD <= 2, "layout");
   __shared__ __align__(16) float q_s[G * QS];
   __shared__ __align__(16) float p_s[P * G];     // scores, then probabilities [pos][head]
@@ -174,7 +200,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
   __shared__ float o_s[VG > 1 ? G * HD : 1];
 
   const uint32_t split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, w = tid >> 6;
   uint32_t L;
   if (PAGED) L = a.seq_lens[seq];
   else L = a.pos_dev ? *a.pos_dev + 1 : a.seq_len;
@@ -187,7 +213,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
   float* ws_m = a.ws;
   float* ws_l = ws_m + nparts;
   float* ws_o = ws_m + 2 * nparts;
-  if (b0 >= b1) {  // a split past the live length
+  if (b0 >= b1) {  // a split past the live length (uniform over the workgroup)
     if (tid < G) {
       ws_m[part + tid] = -INFINITY;
       ws_l[part + tid] = 0.f;
@@ -204,74 +230,86 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
     return pos;
   };
 
-  // ---- issue every K and V load of the chunk ----
+  // ---- 1. query-side loads ----
+  const float* qg = a.q + ((size_t)seq * a.nqh + (size_t)kvh * G) * HD;
+  float qv[QE];
+#pragma unroll
+  for (int k = 0; k < QE; ++k) {
+    const int i = tid + k * NT;
+    qv[k] = qg[i < G * HD ? i : 0];
+  }
+  float kx[FUSE ? KE : 1], vx[FUSE ? KE : 1], kwt[FUSE ? KE : 1], qwt[FUSE ? QE : 1];
+  uint16_t rfb = 0;
+  if constexpr (FUSE) {
+#pragma unroll
+    for (int k = 0; k < KE; ++k) {
+      const int i = tid + k * NT, ic = i < HD ? i : 0;
+      kx[k] = a.k_in[(size_t)kvh * HD + ic];
+      vx[k] = a.v_in[(size_t)kvh * HD + ic];
+      kwt[k] = g4d::f16_bits_to_f32(a.k_w[ic]);
+    }
+#pragma unroll
+    for (int k = 0; k < QE; ++k) qwt[k] = g4d::f16_bits_to_f32(a.q_w[(tid + k * NT) % HD]);
+    rfb = a.rope_freqs[tid < HD / 2 ? tid : 0];  // valid even without the divisor (host passes q_w)
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();  // every wave's query loads are out before any K/V load
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- 2. the chunk's K and V rows ----
   const int ks = tid & 7;  // K slice
   uint4 kraw[CP][KW];
 #pragma unroll
   for (int c = 0; c < CP; ++c) {
-    const uint32_t pos = b0 + (uint32_t)(c * 32 + (tid >> 3));
-    if (pos < b1) {
-      const uint4* kp = (const uint4*)(a.kc + (row_of(pos) * a.nkh + kvh) * HD + ks * KS);
+    const uint32_t pos = min(b0 + (uint32_t)(c * 32 + (tid >> 3)), b1 - 1);
+    const uint4* kp = (const uint4*)(a.kc + (row_of(pos) * a.nkh + kvh) * HD + ks * KS);
 #pragma unroll
-      for (int j = 0; j < KW; ++j) kraw[c][j] = kp[j];
-    } else {
-#pragma unroll
-      for (int j = 0; j < KW; ++j) kraw[c][j] = make_uint4(0, 0, 0, 0);
-    }
+    for (int j = 0; j < KW; ++j) kraw[c][j] = kp[j];
   }
   const int vcol = (tid % (HD / VD)) * VD;  // first column of this thread
   const int vgrp = tid / (HD / VD);         // row group (VG > 1 only)
   uint32_t vraw[VR];                        // VD f16 values per row (VD == 2: packed)
 #pragma unroll
   for (int r = 0; r < VR; ++r) {
-    const uint32_t pos = b0 + (uint32_t)(r * VG + vgrp);
-    if (pos < b1) {
-      const uint16_t* vp = a.vc + (row_of(pos) * a.nkh + kvh) * HD + vcol;
-      vraw[r] = VD == 2 ? *(const uint32_t*)vp : (uint32_t)*vp;
-    } else {
-      vraw[r] = 0;
-    }
+    const uint32_t pos = min(b0 + (uint32_t)(r * VG + vgrp), b1 - 1);
+    const uint16_t* vp = a.vc + (row_of(pos) * a.nkh + kvh) * HD + vcol;
+    vraw[r] = VD == 2 ? *(const uint32_t*)vp : (uint32_t)*vp;
   }
+  __builtin_amdgcn_sched_barrier(0);
 
-  // ---- q for the G heads of this kv head -> q_s (slice-padded) ----
+  // ---- 3. q (fused: per-head RMSNorm + RoPE, and this position's k/v row) ----
   auto qidx = [](int h, int d) { return h * QS + d + (d / KS) * 4; };
-  const float* qg = a.q + ((size_t)seq * a.nqh + (size_t)kvh * G) * HD;
   if constexpr (FUSE) {
     const uint32_t pos = L - 1;  // the position being decoded
-    // RoPE for this position: frequency and angle in f32 as
-    // shaders/fused_per_head_norm_rope.wgsl:50-55 forms them; cos/sin in f64.
-    for (int i = tid; i < HD / 2; i += NT) {
-      float f = (float)(1.0 / pow((double)a.theta, (double)(2 * i) / (double)HD));
-      if (a.apply_divisor) f = f / g4d::f16_bits_to_f32(a.rope_freqs[i]);
+    // RoPE for this position: the frequency is the correctly rounded f32 of
+    // 1/theta^(2i/HD) and the angle the f32 product, as
+    // shaders/fused_per_head_norm_rope.wgsl:50-55 forms them; cos/sin of that
+    // angle in f32 (within 2 ulp of the rounded exact values).
+    if (tid < HD / 2) {
+      float f = (float)(1.0 / pow((double)a.theta, (double)(2 * tid) / (double)HD));
+      if (a.apply_divisor) f = f / g4d::f16_bits_to_f32(rfb);
       const float ang = (float)pos * f;
-      cs_s[i] = make_float2((float)cos((double)ang), (float)sin((double)ang));
+      float sn, cn;
+      sincosf(ang, &sn, &cn);
+      cs_s[tid] = make_float2(cn, sn);
     }
     static_assert((G * HD) % NT == 0 && HD >= 256, "fused form: whole q heads per thread stride");
-    constexpr int QE = G * HD / NT;  // raw q elements per thread (t + 256k)
-    constexpr int KE = (HD + NT - 1) / NT;
-    const bool owner = b1 == L;      // this chunk holds the current position
-    float qv[QE], kx[KE], vx[KE];
+    const bool owner = b1 == L;  // this chunk holds the current position
     float ss[G + 2];
 #pragma unroll
     for (int h = 0; h < G + 2; ++h) ss[h] = 0.f;
 #pragma unroll
-    for (int k = 0; k < QE; ++k) {
-      const int i = tid + k * NT;
-      qv[k] = qg[i];
-      ss[i / HD] += qv[k] * qv[k];
-    }
+    for (int k = 0; k < QE; ++k) ss[(tid + k * NT) / HD] += qv[k] * qv[k];
 #pragma unroll
     for (int k = 0; k < KE; ++k) {
-      const int i = tid + k * NT;
-      kx[k] = (owner && i < HD) ? a.k_in[(size_t)kvh * HD + i] : 0.f;
-      vx[k] = (owner && i < HD) ? a.v_in[(size_t)kvh * HD + i] : 0.f;
-      ss[G] += kx[k] * kx[k];
-      ss[G + 1] += vx[k] * vx[k];
+      const bool in = tid + k * NT < HD;
+      ss[G] += in ? kx[k] * kx[k] : 0.f;
+      ss[G + 1] += in ? vx[k] * vx[k] : 0.f;
     }
 #pragma unroll
     for (int h = 0; h < G + 2; ++h) {
-      const float t = g4d::wave_sum(ss[h]);
-      if (lane == 0) red_s[w * (G + 2) + h] = t;
+      const float t = g4d::wave_sum_dpp(ss[h]);
+      if ((tid & 63) == 0) red_s[w * (G + 2) + h] = t;
     }
     __syncthreads();
     float inv[G + 2];
@@ -283,14 +321,14 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int k = 0; k < QE; ++k) {
       const int i = tid + k * NT, h = i / HD, d = i % HD;
-      q_s[qidx(h, d)] = qv[k] * g4d::f16_bits_to_f32(a.q_w[d]) * inv[h];
+      q_s[qidx(h, d)] = qv[k] * qwt[k] * inv[h];
     }
     if (owner) {
 #pragma unroll
       for (int k = 0; k < KE; ++k) {
         const int i = tid + k * NT;
         if (i < HD) {
-          cur_s[i] = kx[k] * g4d::f16_bits_to_f32(a.k_w[i]) * inv[G];
+          cur_s[i] = kx[k] * kwt[k] * inv[G];
           const uint16_t vb = g4d::f32_to_f16_bits(vx[k] * inv[G + 1]);
           cur_s[HD + i] = g4d::f16_bits_to_f32(vb);
           a.vc_w[(row_of(pos) * a.nkh + kvh) * HD + i] = vb;
@@ -347,11 +385,15 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
       }
     }
   } else {
-    for (int i = tid; i < G * HD; i += NT) q_s[qidx(i / HD, i % HD)] = qg[i];
+#pragma unroll
+    for (int k = 0; k < QE; ++k) {
+      const int i = tid + k * NT;
+      if (i < G * HD) q_s[qidx(i / HD, i % HD)] = qv[k];
+    }
     __syncthreads();
   }
 
-  // ---- scores: slice lanes (8 per row) ----
+  // ---- 4. scores: 8 slice lanes per row ----
 #pragma unroll
   for (int c = 0; c < CP; ++c) {
     float acc[G];
@@ -378,10 +420,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
     const uint32_t pos = b0 + (uint32_t)(c * 32 + (tid >> 3));
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      float v = acc[h];
-      v += __shfl_xor(v, 1, 64);
-      v += __shfl_xor(v, 2, 64);
-      v += __shfl_xor(v, 4, 64);
+      const float v = g4d::sum8(acc[h]);
       acc[h] = pos < b1 ? v * a.scale : -INFINITY;
     }
     if (ks == 0) {
@@ -391,22 +430,23 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
   }
   __syncthreads();
 
-  // ---- chunk softmax statistics per head ----
+  // ---- 5. chunk softmax statistics per head ----
   constexpr int SL = (NT / G) < 64 ? (NT / G) : 64;
+  static_assert(SL == 32 || SL == 64, "head groups of 32 or 64 lanes");
   if (tid < G * SL) {
     const int h = tid / SL, sl = tid % SL;
     float mx = -INFINITY;
-    for (int i = sl; i < P; i += SL) mx = fmaxf(mx, p_s[i * G + h]);
 #pragma unroll
-    for (int off = SL / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    for (int i = sl; i < P; i += SL) mx = fmaxf(mx, p_s[i * G + h]);
+    mx = group_max<SL>(mx);
     float sum = 0.f;
+#pragma unroll
     for (int i = sl; i < P; i += SL) {
       const float e = expf(p_s[i * G + h] - mx);  // rows past the chunk: exp(-inf) = 0
       p_s[i * G + h] = e;
       sum += e;
     }
-#pragma unroll
-    for (int off = SL / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    sum = group_sum<SL>(sum);
     if (sl == 0) {
       stat_s[h] = mx;
       stat_s[G + h] = sum;
@@ -414,7 +454,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
   }
   __syncthreads();
 
-  // ---- o for this thread's columns over the chunk's rows ----
+  // ---- 6. o for this thread's columns over the chunk's rows ----
   float o[G][VD];
 #pragma unroll
   for (int h = 0; h < G; ++h)
@@ -465,14 +505,18 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
 }
 
 // Merge the splits of one (sequence, query head):
-// O = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M); empty splits (l = 0) drop out.
-// The per-split weights are formed in parallel first, then every thread
-// streams its columns of all splits with independent loads.
-__global__ __launch_bounds__(NT) void attn_merge_kernel(const float* ws, float* out, uint32_t nqh, uint32_t nkh,
-                                                        uint32_t G, uint32_t hd, uint32_t nsplit,
-                                                        uint32_t num_seqs) {
-  __shared__ float wgt_s[1024];
-  __shared__ float red_s[8];
+// O = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M); empty splits (l = 0)
+// drop out. MG thread groups of HD threads each take MS splits per pass with
+// every load of the pass issued first (unconditional, clamped index); passes
+// combine online and the groups combine through LDS at the end.
+constexpr int MS = 16;
+
+template <int HD>
+__global__ __launch_bounds__(1024) void attn_merge_kernel(const float* ws, float* out, uint32_t nqh, uint32_t nkh,
+                                                          uint32_t G, uint32_t nsplit, uint32_t num_seqs) {
+  constexpr int MG = 1024 / HD;  // split groups (thread g*HD + d owns column d of group g)
+  __shared__ float gm_s[MG], gl_s[MG];
+  __shared__ float go_s[MG > 1 ? (MG - 1) * HD : 1];
   const uint32_t hq = blockIdx.x, seq = blockIdx.y;
   const uint32_t kvh = hq / G, h = hq % G;
   const size_t nparts = (size_t)num_seqs * nkh * nsplit * G;
@@ -480,39 +524,50 @@ __global__ __launch_bounds__(NT) void attn_merge_kernel(const float* ws, float* 
   const float* ws_l = ws + nparts;
   const float* ws_o = ws + 2 * nparts;
   const size_t base = ((size_t)seq * nkh + kvh) * nsplit * G + h;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  // global max over live splits
-  float mx = -INFINITY;
-  for (uint32_t s = tid; s < nsplit; s += NT) {
-    const float l = ws_l[base + (size_t)s * G];
-    if (l > 0.f) mx = fmaxf(mx, ws_m[base + (size_t)s * G]);
-  }
-  mx = g4d::wave_max(mx);
-  if (lane == 0) red_s[w] = mx;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(red_s[0], red_s[1]), fmaxf(red_s[2], red_s[3]));
-  __syncthreads();
-  float lsum = 0.f;
-  for (uint32_t s = tid; s < nsplit; s += NT) {
-    const float l = ws_l[base + (size_t)s * G];
-    const float wt = l > 0.f ? expf(ws_m[base + (size_t)s * G] - M) : 0.f;
-    if (s < 1024) wgt_s[s] = wt;
-    lsum += l * wt;
-  }
-  lsum = g4d::block_sum<4>(lsum, red_s);
-  const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
-  float* dst = out + ((size_t)seq * nqh + hq) * hd;
-  for (uint32_t d = tid; d < hd; d += NT) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    uint32_t s = 0;
-    for (; s + 4 <= nsplit; s += 4) {
+  const uint32_t tid = threadIdx.x, d = tid % HD, grp = tid / HD;
+  float M = -INFINITY, Ls = 0.f, acc = 0.f;
+  for (uint32_t s0 = grp * MS; s0 < nsplit; s0 += MG * MS) {
+    float mm[MS], ll[MS], oo[MS];
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        acc[u] += ws_o[(base + (size_t)(s + u) * G) * hd + d] * wgt_s[s + u];
+    for (int u = 0; u < MS; ++u) {
+      const size_t ps = base + (size_t)min(s0 + u, nsplit - 1) * G;
+      mm[u] = ws_m[ps];
+      ll[u] = ws_l[ps];
+      oo[u] = ws_o[ps * HD + d];
     }
-    for (; s < nsplit; ++s) acc[0] += ws_o[(base + (size_t)s * G) * hd + d] * wgt_s[s];
-    dst[d] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) * inv;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < MS; ++u) mx = fmaxf(mx, (s0 + u < nsplit && ll[u] > 0.f) ? mm[u] : -INFINITY);
+    const float nM = fmaxf(M, mx);
+    const float sc = nM == -INFINITY || M == -INFINITY ? 0.f : expf(M - nM);
+    acc *= sc;
+    Ls *= sc;
+#pragma unroll
+    for (int u = 0; u < MS; ++u) {
+      const float wt = (s0 + u < nsplit && ll[u] > 0.f) ? expf(mm[u] - nM) : 0.f;
+      acc += wt * oo[u];
+      Ls += wt * ll[u];
+    }
+    M = nM;
   }
+  if (d == 0) {
+    gm_s[grp] = M;
+    gl_s[grp] = Ls;
+  }
+  if (grp > 0) go_s[(grp - 1) * HD + d] = acc;
+  __syncthreads();
+  if (grp != 0) return;
+  float TM = -INFINITY;
+#pragma unroll
+  for (int g = 0; g < MG; ++g) TM = fmaxf(TM, gm_s[g]);
+  float tl = 0.f, to = 0.f;
+#pragma unroll
+  for (int g = 0; g < MG; ++g) {
+    const float wg = gm_s[g] == -INFINITY ? 0.f : expf(gm_s[g] - TM);
+    tl += wg * gl_s[g];
+    to += wg * (g == 0 ? acc : go_s[(g - 1) * HD + d]);
+  }
+  out[((size_t)seq * nqh + hq) * HD + d] = tl > 0.f ? to / tl : 0.f;
 }
 
 // ---------------------------------------------------------------------------
@@ -595,8 +650,21 @@ int launch_attn(g4_ctx* ctx, const AttnArgs& a, uint32_t G, uint32_t hd, int cp,
 
 int merge(g4_ctx* ctx, const AttnArgs& a, float* out, const SplitPlan& sp, uint32_t num_seqs, uint32_t G,
           uint32_t hd) {
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(a.nqh, num_seqs), dim3(NT), 0, ctx->stream, (const float*)a.ws, out,
-                     a.nqh, a.nkh, G, hd, sp.nsplit, num_seqs);
+  const dim3 mg(a.nqh, num_seqs);
+  switch (hd) {
+    case 128:
+      hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(1024), 0, ctx->stream, (const float*)a.ws, out, a.nqh, a.nkh,
+                         G, sp.nsplit, num_seqs);
+      break;
+    case 256:
+      hipLaunchKernelGGL(attn_merge_kernel<256>, mg, dim3(1024), 0, ctx->stream, (const float*)a.ws, out, a.nqh, a.nkh,
+                         G, sp.nsplit, num_seqs);
+      break;
+    default:
+      hipLaunchKernelGGL(attn_merge_kernel<512>, mg, dim3(1024), 0, ctx->stream, (const float*)a.ws, out, a.nqh, a.nkh,
+                         G, sp.nsplit, num_seqs);
+      break;
+  }
   G4_LAUNCHED(ctx, "attn_merge");
   return G4_OK;
 }
@@ -757,7 +825,9 @@ int g4_attnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw, cons
   a.v_in = v_raw;
   a.q_w = q_norm_w;
   a.k_w = k_norm_w;
-  a.rope_freqs = rope_freqs;
+  // the kernel reads the table unconditionally; without the divisor any
+  // valid buffer of >= head_dim/2 halves serves (the value is unused)
+  a.rope_freqs = rope_freqs ? rope_freqs : q_norm_w;
   a.theta = p.theta;
   a.apply_divisor = p.apply_divisor;
   a.eps = p.eps;

@@ -627,30 +627,12 @@ __device__ __forceinline__ uint32_t mv_tile_bytes(uint32_t M, uint32_t t) {
   return o >= total ? 0u : (uint32_t)min((uint64_t)T::TB, total - o);
 }
 
-// DPP lane exchanges inside a row of 16 lanes (VALU, no LDS round trip).
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-template <int CTRL>
-__device__ __forceinline__ int dppi(int v) {
-  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
-}
-constexpr int kDppXor1 = 0xb1;      // quad_perm [1,0,3,2]
-constexpr int kDppXor2 = 0x4e;      // quad_perm [2,3,0,1]
-constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within 8 lanes
-constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within 16 lanes
-
-// Sum over the wave: DPP inside each 16-lane row, then the four row sums.
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-  v += dpp<kDppXor1>(v);
-  v += dpp<kDppXor2>(v);
-  v += dpp<kDppHalfMirror>(v);
-  v += dpp<kDppMirror>(v);
-  const int iv = __float_as_int(v);
-  return (__int_as_float(__builtin_amdgcn_readlane(iv, 0)) + __int_as_float(__builtin_amdgcn_readlane(iv, 16))) +
-         (__int_as_float(__builtin_amdgcn_readlane(iv, 32)) + __int_as_float(__builtin_amdgcn_readlane(iv, 48)));
-}
+using g4d::dpp;
+using g4d::dppi;
+using g4d::kDppXor1;
+using g4d::kDppXor2;
+using g4d::kDppHalfMirror;
+using g4d::wave_sum_dpp;
 
 // Sum over the workgroup with one barrier; `red` holds NWV floats not reused
 // by another sum before the next barrier.
