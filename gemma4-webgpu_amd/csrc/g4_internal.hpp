@@ -18,14 +18,19 @@ struct g4_ctx {
   size_t lds_max = 65536;  // LDS bytes one workgroup may use (160 KB on gfx950)
   char name[128] = {0};
   bool capturing = false;
-  // Small device buffer for the partials of two-stage reductions (argmax,
-  // topk256), allocated once at g4_init so that no entry point allocates.
+  // Device buffer for the partials of two-stage reductions (argmax, topk256)
+  // and the activation digits of batched matmuls, allocated once at g4_init
+  // so that no entry point allocates. Calls use it in stream order.
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
 };
 
 // Returns the context scratch buffer if it holds `bytes`.
 int g4_internal_scratch(g4_ctx* ctx, size_t bytes, void** out);
+
+// Matrix-core matmul of `batch` activation vectors (k_batch.hip).
+int g4_internal_batch_matmul(g4_ctx* ctx, const char* fn, int qt, const float* x, const void* w, float* y,
+                             uint32_t M, uint32_t N, uint32_t batch);
 
 struct g4_event {
   hipEvent_t ev = nullptr;

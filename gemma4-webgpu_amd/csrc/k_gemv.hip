@@ -1264,6 +1264,7 @@ int matmul_quant(g4_ctx* ctx, const char* fn, int qt, const float* in, const voi
     G4_LAUNCHED(ctx, fn);
     return G4_OK;
   }
+  if (batch >= 16 && batch <= 64) return g4_internal_batch_matmul(ctx, fn, qt, in, w, out, p.M, p.N, batch);
   int nv_max = 8;
   while (nv_max > 1 && gemv_lds(qt, p.N, nv_max) > ctx->lds_max) nv_max >>= 1;
   uint32_t done = 0;

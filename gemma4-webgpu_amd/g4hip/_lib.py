@@ -155,6 +155,8 @@ SIGNATURES = {
     "g4_normAddGateUpGelu_q4k": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, MatmulParams, _F]),
     "g4_normAddMatmulSegments": (_I, [_P, _I, _P, _P, _P, _P, _P, ctypes.POINTER(_P),
                                       ctypes.POINTER(_P), ctypes.POINTER(_U32), _I, _U32, _F, _F]),
+    "g4_normAddMatmulSegmentsBatch": (_I, [_P, _I, _P, _P, _P, _P, _P, ctypes.POINTER(_P),
+                                           ctypes.POINTER(_P), ctypes.POINTER(_U32), _I, _U32, _F, _F, _U32]),
     "g4_dequant_q4k": (_I, [_P, _P, _U64, _P]),
     "g4_dequant_q6k": (_I, [_P, _P, _U64, _P]),
     "g4_splitmix64": (_U64, [_U64, _U64]),

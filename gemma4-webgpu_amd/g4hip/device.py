@@ -208,6 +208,18 @@ class Context:
         check(lib().g4_normAddMatmulSegments(self.h, {"q4k": 0, "q6k": 1}[wtype], _p(x), _p(w1), _p(residual),
                                              _p(w2), _p(h_out), W, Y, R, n, N, eps, softcap))
 
+    def normAddMatmulSegmentsBatch(self, wtype: str, x: Ptr, w1: Ptr, residual: Ptr, w2: Ptr, h_out: Ptr,
+                                   weights, outputs, rows, N: int, batch: int, eps: float = 1e-6,
+                                   softcap: float = 0.0) -> None:
+        """normAddMatmulSegments over `batch` vectors: x [batch][N] -> outputs[i] [batch][rows[i]]."""
+        n = len(weights)
+        W = (ctypes.c_void_p * n)(*[_p(w).value for w in weights])
+        Y = (ctypes.c_void_p * n)(*[_p(y).value for y in outputs])
+        R = (ctypes.c_uint32 * n)(*rows)
+        check(lib().g4_normAddMatmulSegmentsBatch(self.h, {"q4k": 0, "q6k": 1}[wtype], _p(x), _p(w1),
+                                                  _p(residual), _p(w2), _p(h_out), W, Y, R, n, N, eps, softcap,
+                                                  batch))
+
     # ---- attention (kv_cache_store / attn_score / softmax / attn_output) ----
     def kvCacheStore(self, k_in: Ptr, v_in: Ptr, k_cache: Ptr, v_cache: Ptr, num_kv_heads: int, head_dim: int,
                      position: int, max_seq_len: int, position_dev: Ptr = None) -> None:

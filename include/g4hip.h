@@ -292,6 +292,17 @@ int g4_normAddMatmulSegments(g4_ctx* ctx, int wtype, const float* x, const uint1
                              const uint32_t* rows, int nseg, uint32_t N, float eps,
                              float softcap_cap);
 
+/* The same over `batch` activation vectors at once (ragged multi-sequence
+ * decode: src/engine.ts:1546-1554 run once per sequence). x, residual and
+ * h_out are [batch][N]; outputs[i] is [batch][rows[i]]. w1 == NULL skips the
+ * norms (plain matmul). 1 <= batch <= 64. Runs on the matrix cores; the
+ * activation digits live in the context scratch between its two launches. */
+int g4_normAddMatmulSegmentsBatch(g4_ctx* ctx, int wtype, const float* x, const uint16_t* w1,
+                                  const float* residual, const uint16_t* w2, float* h_out,
+                                  const void* const* weights, float* const* outputs,
+                                  const uint32_t* rows, int nseg, uint32_t N, float eps,
+                                  float softcap_cap, uint32_t batch);
+
 /* ------------------------------------------------------------------------ */
 /* Debug / test exports                                                      */
 /* ------------------------------------------------------------------------ */

@@ -1,0 +1,97 @@
+"""GPU parity of the matrix-core matmul over many activation vectors (ragged
+multi-sequence decode): every vector of the batch against the f64 oracle's
+matvec (rel-L2 <= 1e-3, cos >= 0.9999), with the norm prologues, several
+matrices per launch and the softcap epilogue."""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_util import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(wtype, seed, M, N):
+    nb = M * N // 256
+    return O.gen_q4k(seed, nb) if wtype == "q4k" else O.gen_q6k(seed, nb)
+
+
+@pytest.mark.parametrize("wtype,M,N,batch", [
+    ("q4k", 2048, 1536, 32),   # E2B q projection at B=32
+    ("q4k", 1536, 2048, 16),   # o projection
+    ("q4k", 6144, 1536, 64),   # gate/up at B=64
+    ("q4k", 100, 1536, 17),    # ragged rows and batch
+    ("q6k", 1536, 6144, 32),   # down projection
+    ("q6k", 1000, 1536, 33),   # LM-head-like K, ragged
+    ("q6k", 777, 12288, 16),   # wide FFN down, rows not a multiple of 16
+])
+def test_batched_matmul_matches_oracle(ctx, wtype, M, N, batch):
+    W = _weights(wtype, 60, M, N)
+    X = O.gen_normal_f32(61, batch * N, 0.0, 1.5).reshape(batch, N)
+    X[batch // 2] *= 40.0  # one vector with a very different scale
+    dY = ctx.empty(batch * M, np.float32)
+    ctx.matmulQuantBatch(ctx.from_numpy(X), ctx.from_numpy(W), dY, M, N, batch, wtype)
+    Y = dY.download(np.float32).reshape(batch, M)
+    for b in range(batch):
+        assert_close(Y[b], O.matmul(X[b], W, M, N, wtype), what=f"{wtype} {M}x{N} vector {b}")
+
+
+@pytest.mark.parametrize("mode", ["plain", "norm", "normadd"])
+def test_batched_segments_with_prologues(ctx, mode):
+    """q/k/v of 32 sequences in one launch, with the per-sequence RMSNorm (or
+    residual add + RMSNorm) prologue."""
+    N, B = 1536, 32
+    segs = [(2048, 70), (256, 71), (256, 72)]
+    Ws = [O.gen_q4k(s, M * N // 256) for M, s in segs]
+    X = O.gen_normal_f32(73, B * N, 0.0, 2.0).reshape(B, N)
+    R = O.gen_normal_f32(74, B * N).reshape(B, N)
+    w1 = O.gen_normal_f16(75, N, 1.0, 0.1)
+    w2 = O.gen_normal_f16(76, N, 1.0, 0.1)
+    outs = [ctx.empty(B * M, np.float32) for M, _ in segs]
+    dh = ctx.empty(B * N, np.float32)
+    ctx.normAddMatmulSegmentsBatch(
+        "q4k", ctx.from_numpy(X), ctx.from_numpy(w1) if mode != "plain" else None,
+        ctx.from_numpy(R) if mode == "normadd" else None, ctx.from_numpy(w2) if mode == "normadd" else None,
+        dh if mode == "normadd" else None, [ctx.from_numpy(W) for W in Ws], outs, [M for M, _ in segs], N, B)
+    H = dh.download(np.float32).reshape(B, N)
+    for b in range(B):
+        if mode == "plain":
+            xn = X[b]
+        elif mode == "norm":
+            xn = O.rms_norm(X[b], w1, 1e-6)
+        else:
+            h = O.fused_norm_add(X[b], w1, R[b], 1e-6)
+            assert_close(H[b], h, rel=1e-6, cos=0.99999999, what=f"h_out {b}")
+            xn = O.rms_norm(h, w2, 1e-6)
+        for (M, _), W, o in zip(segs, Ws, outs):
+            got = o.download(np.float32).reshape(B, M)[b]
+            assert_close(got, O.matmul(xn, W, M, N, "q4k"), what=f"{mode} seq {b} M={M}")
+
+
+def test_batched_lm_head_softcap(ctx):
+    """Final norm-add + tied Q6_K LM head + softcap for 16 sequences."""
+    M, N, B = 8192, 1536, 16
+    W = O.gen_q6k(80, M * N // 256)
+    X = O.gen_normal_f32(81, B * N, 0.0, 2.0).reshape(B, N)
+    R = O.gen_normal_f32(82, B * N, 0.0, 5.0).reshape(B, N)
+    w1 = O.gen_normal_f16(83, N, 1.0, 0.1)
+    w2 = (O.gen_normal_f16(84, N, 1.0, 0.1).view(np.float16).astype(np.float32) * 20).astype(np.float16)
+    w2 = w2.view(np.uint16)
+    dY = ctx.empty(B * M, np.float32)
+    ctx.normAddMatmulSegmentsBatch("q6k", ctx.from_numpy(X), ctx.from_numpy(w1), ctx.from_numpy(R),
+                                   ctx.from_numpy(w2), None, [ctx.from_numpy(W)], [dY], [M], N, B, softcap=30.0)
+    Y = dY.download(np.float32).reshape(B, M)
+    assert np.max(np.abs(Y)) <= 30.0
+    for b in range(B):
+        h = O.fused_norm_add(X[b], w1, R[b], 1e-6)
+        ref = O.logit_softcap(O.matmul(O.rms_norm(h, w2, 1e-6), W, M, N, "q6k"), 30.0)
+        assert_close(Y[b], ref, what=f"lm head seq {b}")
+
+
+def test_batched_matmul_rejects_bad_shapes(ctx):
+    W = O.gen_q4k(90, 64 * 1536 // 256)
+    X = O.gen_normal_f32(91, 65 * 1536)
+    dY = ctx.empty(65 * 64, np.float32)
+    with pytest.raises(Exception, match="batch 65"):
+        ctx.normAddMatmulSegmentsBatch("q4k", ctx.from_numpy(X), None, None, None, None, [ctx.from_numpy(W)],
+                                       [dY], [64], 1536, 65)
