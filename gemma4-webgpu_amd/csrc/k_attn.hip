@@ -134,8 +134,8 @@ struct AttnArgs {
   uint32_t nsplit;           // splits per (sequence, kv head)
   float* ws;                 // partials: m, l, o
   // fused form
-  const float* k_in;         // [nkh][hd] raw k projection
-  const float* v_in;         // [nkh][hd] raw v projection
+  const float* k_in;         // [num_seqs][nkh][hd] raw k projection
+  const float* v_in;         // [num_seqs][nkh][hd] raw v projection
   const uint16_t* q_w;       // q_norm weight f16[hd]
   const uint16_t* k_w;       // k_norm weight f16[hd]
   const uint16_t* rope_freqs;
@@ -244,8 +244,8 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int k = 0; k < KE; ++k) {
       const int i = tid + k * NT, ic = i < HD ? i : 0;
-      kx[k] = a.k_in[(size_t)kvh * HD + ic];
-      vx[k] = a.v_in[(size_t)kvh * HD + ic];
+      kx[k] = a.k_in[((size_t)seq * a.nkh + kvh) * HD + ic];
+      vx[k] = a.v_in[((size_t)seq * a.nkh + kvh) * HD + ic];
       kwt[k] = g4d::f16_bits_to_f32(a.k_w[ic]);
     }
 #pragma unroll
@@ -295,6 +295,19 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
     }
     static_assert((G * HD) % NT == 0 && HD >= 256, "fused form: whole q heads per thread stride");
     const bool owner = b1 == L;  // this chunk holds the current position
+    // Where the row is written. Paged: the page id must be in the pool and
+    // the length unclamped; otherwise nothing is stored (the attention still
+    // uses the row), as g4_pagedKvStore does for a bad table entry.
+    bool store = true;
+    size_t srow = pos;
+    if constexpr (PAGED) {
+      const uint32_t lr = a.seq_lens[seq];
+      const int32_t pg = a.page_table[(size_t)seq * a.max_pages + pos / a.page_size];
+      store = lr <= a.cap && pg >= 0 && pg < (int32_t)a.num_pages;
+      srow = (size_t)(store ? pg : 0) * a.page_size + pos % a.page_size;
+    }
+    uint16_t* kdst = a.kc_w + (srow * a.nkh + kvh) * HD;
+    uint16_t* vdst = a.vc_w + (srow * a.nkh + kvh) * HD;
     float ss[G + 2];
 #pragma unroll
     for (int h = 0; h < G + 2; ++h) ss[h] = 0.f;
@@ -331,7 +344,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
           cur_s[i] = kx[k] * kwt[k] * inv[G];
           const uint16_t vb = g4d::f32_to_f16_bits(vx[k] * inv[G + 1]);
           cur_s[HD + i] = g4d::f16_bits_to_f32(vb);
-          a.vc_w[(row_of(pos) * a.nkh + kvh) * HD + i] = vb;
+          if (store) vdst[i] = vb;
         }
       }
     }
@@ -350,9 +363,10 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
         const float x0 = cur_s[i], x1 = cur_s[i + HD / 2];
         const uint16_t k0 = g4d::f32_to_f16_bits(x0 * cs.x - x1 * cs.y);
         const uint16_t k1 = g4d::f32_to_f16_bits(x0 * cs.y + x1 * cs.x);
-        uint16_t* kdst = a.kc_w + (row_of(pos) * a.nkh + kvh) * HD;
-        kdst[i] = k0;
-        kdst[i + HD / 2] = k1;
+        if (store) {
+          kdst[i] = k0;
+          kdst[i + HD / 2] = k1;
+        }
         cur_s[i] = g4d::f16_bits_to_f32(k0);  // as the cache row will read back
         cur_s[i + HD / 2] = g4d::f16_bits_to_f32(k1);
       }
@@ -723,6 +737,58 @@ int dense_decode(g4_ctx* ctx, const char* fn, const float* q, const uint16_t* kc
   return merge(ctx, a, out, sp, 1, G, p.head_dim);
 }
 
+g4_paged_attn_params fused_attn_part(const g4_paged_attn_fused_params& f) {
+  g4_paged_attn_params p{};
+  p.num_seqs = f.num_seqs;
+  p.num_q_heads = f.num_q_heads;
+  p.num_kv_heads = f.num_kv_heads;
+  p.head_dim = f.head_dim;
+  p.page_size = f.page_size;
+  p.max_pages = f.max_pages;
+  p.max_seq_len = f.max_seq_len;
+  p.num_pages = f.num_pages;
+  p.scale = f.scale;
+  p.sliding_window = f.sliding_window;
+  return p;
+}
+
+// Shape checks and the kernel arguments shared by the paged entry points.
+int paged_setup(const char* fn, const uint16_t* k_pool, const uint16_t* v_pool, const int32_t* page_table,
+                const uint32_t* seq_lens, const g4_paged_attn_params& p, void* ws, size_t ws_len, AttnArgs& a,
+                SplitPlan& sp) {
+  G4_REQUIRE(((uintptr_t)k_pool & 15) == 0 && ((uintptr_t)v_pool & 15) == 0 && ((uintptr_t)ws & 15) == 0,
+             "%s: KV pools and workspace must be 16-byte aligned", fn);
+  int rc = check_heads(fn, p.num_q_heads, p.num_kv_heads, p.head_dim);
+  if (rc) return rc;
+  G4_REQUIRE(p.num_seqs > 0 && p.page_size > 0 && p.max_pages > 0 && p.num_pages > 0,
+             "%s: empty batch or pages", fn);
+  G4_REQUIRE(p.num_seqs <= 65535, "%s: %u sequences exceed the grid limit 65535", fn, p.num_seqs);
+  G4_REQUIRE(p.max_seq_len > 0 && (uint64_t)p.max_seq_len <= (uint64_t)p.page_size * p.max_pages,
+             "%s: max_seq_len %u exceeds the page table (%u x %u)", fn, p.max_seq_len, p.max_pages, p.page_size);
+  sp = plan_splits(eff_len(p.max_seq_len, p.sliding_window));
+  rc = check_plan(fn, sp);
+  if (rc) return rc;
+  const size_t need = ws_bytes(p.num_seqs, p.num_kv_heads, sp.nsplit, p.num_q_heads / p.num_kv_heads, p.head_dim);
+  G4_REQUIRE(ws_len >= need, "%s: workspace %zu bytes < %zu required", fn, ws_len, need);
+  a = AttnArgs{};
+  a.kc = k_pool;
+  a.vc = v_pool;
+  a.page_table = page_table;
+  a.page_size = p.page_size;
+  a.max_pages = p.max_pages;
+  a.num_pages = p.num_pages;
+  a.cap = p.max_seq_len;
+  a.seq_lens = seq_lens;
+  a.nqh = p.num_q_heads;
+  a.nkh = p.num_kv_heads;
+  a.scale = p.scale;
+  a.window = p.sliding_window;
+  a.chunk = sp.chunk;
+  a.nsplit = sp.nsplit;
+  a.ws = (float*)ws;
+  return G4_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -853,40 +919,50 @@ int g4_pagedAttnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_pool, cons
   G4_ENTER(ctx);
   G4_REQUIRE(q && k_pool && v_pool && page_table && seq_lens && output && workspace,
              "g4_pagedAttnDecode: null buffer");
-  G4_REQUIRE(((uintptr_t)k_pool & 15) == 0 && ((uintptr_t)v_pool & 15) == 0 && ((uintptr_t)workspace & 15) == 0,
-             "g4_pagedAttnDecode: KV pools and workspace must be 16-byte aligned");
-  int rc = check_heads(__func__, p.num_q_heads, p.num_kv_heads, p.head_dim);
-  if (rc) return rc;
-  G4_REQUIRE(p.num_seqs > 0 && p.page_size > 0 && p.max_pages > 0 && p.num_pages > 0,
-             "g4_pagedAttnDecode: empty batch or pages");
-  G4_REQUIRE(p.max_seq_len > 0 && p.max_seq_len <= p.page_size * p.max_pages,
-             "g4_pagedAttnDecode: max_seq_len %u exceeds the page table (%u x %u)", p.max_seq_len, p.max_pages,
-             p.page_size);
-  const uint32_t G = p.num_q_heads / p.num_kv_heads;
-  const SplitPlan sp = plan_splits(eff_len(p.max_seq_len, p.sliding_window));
-  rc = check_plan(__func__, sp);
-  if (rc) return rc;
-  const size_t need = ws_bytes(p.num_seqs, p.num_kv_heads, sp.nsplit, G, p.head_dim);
-  G4_REQUIRE(workspace_bytes >= need, "g4_pagedAttnDecode: workspace %zu bytes < %zu required", workspace_bytes,
-             need);
   AttnArgs a{};
+  SplitPlan sp{};
+  int rc = paged_setup(__func__, k_pool, v_pool, page_table, seq_lens, p, workspace, workspace_bytes, a, sp);
+  if (rc) return rc;
   a.q = q;
-  a.kc = k_pool;
-  a.vc = v_pool;
-  a.page_table = page_table;
-  a.page_size = p.page_size;
-  a.max_pages = p.max_pages;
-  a.num_pages = p.num_pages;
-  a.cap = p.max_seq_len;
-  a.seq_lens = seq_lens;
-  a.nqh = p.num_q_heads;
-  a.nkh = p.num_kv_heads;
-  a.scale = p.scale;
-  a.window = p.sliding_window;
-  a.chunk = sp.chunk;
-  a.nsplit = sp.nsplit;
-  a.ws = (float*)workspace;
-  rc = launch_attn<true, false>(ctx, a, G, p.head_dim, sp.cp, dim3(sp.nsplit, p.num_kv_heads, p.num_seqs));
+  rc = launch_attn<true, false>(ctx, a, p.num_q_heads / p.num_kv_heads, p.head_dim, sp.cp,
+                                dim3(sp.nsplit, p.num_kv_heads, p.num_seqs));
+  if (rc) return rc;
+  return merge(ctx, a, output, sp, p.num_seqs, p.num_q_heads / p.num_kv_heads, p.head_dim);
+}
+
+int g4_pagedAttnDecodeFused_workspace_size(g4_paged_attn_fused_params p, size_t* bytes) {
+  return g4_pagedAttnDecode_workspace_size(fused_attn_part(p), bytes);
+}
+
+int g4_pagedAttnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float* v_raw,
+                            const uint16_t* q_norm_w, const uint16_t* k_norm_w, const uint16_t* rope_freqs,
+                            uint16_t* k_pool, uint16_t* v_pool, const int32_t* page_table, const uint32_t* seq_lens,
+                            float* output, g4_paged_attn_fused_params p, void* workspace, size_t workspace_bytes) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(q_raw && k_raw && v_raw && q_norm_w && k_norm_w && k_pool && v_pool && page_table && seq_lens &&
+                 output && workspace,
+             "g4_pagedAttnDecodeFused: null buffer");
+  G4_REQUIRE(!p.apply_divisor || rope_freqs, "g4_pagedAttnDecodeFused: apply_divisor needs rope_freqs");
+  const g4_paged_attn_params ap = fused_attn_part(p);
+  AttnArgs a{};
+  SplitPlan sp{};
+  int rc = paged_setup(__func__, k_pool, v_pool, page_table, seq_lens, ap, workspace, workspace_bytes, a, sp);
+  if (rc) return rc;
+  const uint32_t G = p.num_q_heads / p.num_kv_heads;
+  G4_REQUIRE(G == 8 && (p.head_dim == 256 || p.head_dim == 512),
+             "g4_pagedAttnDecodeFused: built for 8 query heads per kv head and head_dim 256/512");
+  a.q = q_raw;
+  a.kc_w = k_pool;
+  a.vc_w = v_pool;
+  a.k_in = k_raw;
+  a.v_in = v_raw;
+  a.q_w = q_norm_w;
+  a.k_w = k_norm_w;
+  a.rope_freqs = rope_freqs ? rope_freqs : q_norm_w;  // read unconditionally, used only with the divisor
+  a.theta = p.theta;
+  a.apply_divisor = p.apply_divisor;
+  a.eps = p.eps;
+  rc = launch_attn<true, true>(ctx, a, G, p.head_dim, sp.cp, dim3(sp.nsplit, p.num_kv_heads, p.num_seqs));
   if (rc) return rc;
   return merge(ctx, a, output, sp, p.num_seqs, G, p.head_dim);
 }

@@ -2,6 +2,8 @@
 // seeded synthetic-input generators.
 #include <math.h>
 
+#include <algorithm>
+
 #include "g4_internal.hpp"
 
 namespace {
@@ -97,6 +99,11 @@ __global__ void advance_kernel(uint32_t* p, uint32_t delta) {
   if (threadIdx.x == 0) p[0] += delta;
 }
 
+__global__ __launch_bounds__(NT) void advance_many_kernel(uint32_t* p, uint32_t n, uint32_t delta) {
+  const uint32_t i = blockIdx.x * NT + threadIdx.x;
+  if (i < n) p[i] += delta;
+}
+
 __global__ __launch_bounds__(NT) void softcap_kernel(float* logits, uint32_t n, float cap) {
   const uint32_t i = blockIdx.x * NT + threadIdx.x;
   if (i >= n) return;
@@ -159,9 +166,11 @@ __device__ __forceinline__ Cand wave_best(Cand c) {
 
 constexpr int kArgmaxBlocks = 256;
 
-// stage 1: workgroup b scans a contiguous chunk
+// stage 1: workgroup (b, r) scans a contiguous chunk of row r
 __global__ __launch_bounds__(NT) void argmax_partial(const float* logits, uint32_t n, Cand* part) {
   __shared__ Cand sm[4];
+  logits += (size_t)blockIdx.y * n;
+  part += (size_t)blockIdx.y * gridDim.x;
   const uint32_t chunk = (n + gridDim.x - 1) / gridDim.x;
   const uint32_t lo = blockIdx.x * chunk;
   const uint32_t hi = min(n, lo + chunk);
@@ -181,10 +190,11 @@ __global__ __launch_bounds__(NT) void argmax_partial(const float* logits, uint32
   }
 }
 
-// stage 2: one workgroup reduces the partials; the initial candidate
+// stage 2: workgroup r reduces row r's partials; the initial candidate
 // (-1e30, 0) mirrors the reference's default result.
 __global__ __launch_bounds__(NT) void argmax_final(const Cand* part, int nparts, uint32_t* result) {
   __shared__ Cand sm[4];
+  part += (size_t)blockIdx.x * nparts;
   Cand c{-1e30f, 0u};
   for (int i = threadIdx.x; i < nparts; i += NT)
     if (better(part[i], c)) c = part[i];
@@ -196,7 +206,7 @@ __global__ __launch_bounds__(NT) void argmax_final(const Cand* part, int nparts,
     for (int k = 1; k < 4; ++k)
       if (better(sm[k], b)) b = sm[k];
     // a candidate that never beat the -1e30 initial value leaves index 0
-    result[0] = (b.v > -1e30f) ? b.i : 0u;
+    result[blockIdx.x] = (b.v > -1e30f) ? b.i : 0u;
   }
 }
 
@@ -207,6 +217,8 @@ constexpr int kTopkSlabs = 128;
 
 __global__ __launch_bounds__(NT) void topk_partial(const float* logits, uint32_t n, float2* part) {
   const uint32_t t = threadIdx.x;
+  logits += (size_t)blockIdx.y * n;
+  part += (size_t)blockIdx.y * gridDim.x * 256;
   const uint32_t rows = (n + 255) / 256;
   const uint32_t per = (rows + gridDim.x - 1) / gridDim.x;
   const uint32_t r0 = blockIdx.x * per, r1 = min(rows, r0 + per);
@@ -227,6 +239,8 @@ __global__ __launch_bounds__(NT) void topk_partial(const float* logits, uint32_t
 
 __global__ __launch_bounds__(NT) void topk_final(const float2* part, int nparts, float* result) {
   const uint32_t t = threadIdx.x;
+  part += (size_t)blockIdx.x * nparts * 256;
+  result += (size_t)blockIdx.x * 512;
   float mx = -1e30f;
   uint32_t idx = 0;
   for (int s = 0; s < nparts; ++s) {
@@ -475,35 +489,56 @@ int g4_advancePosition(g4_ctx* ctx, uint32_t* position_dev, uint32_t delta) {
   return G4_OK;
 }
 
-int g4_argmax(g4_ctx* ctx, const float* logits, uint32_t* result, uint32_t size) {
+int g4_advanceSeqLens(g4_ctx* ctx, uint32_t* seq_lens, uint32_t num_seqs, uint32_t delta) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(seq_lens, "g4_advanceSeqLens: null buffer");
+  if (!num_seqs) return G4_OK;
+  hipLaunchKernelGGL(advance_many_kernel, dim3(ceil_div(num_seqs, NT)), dim3(NT), 0, ctx->stream, seq_lens, num_seqs,
+                     delta);
+  G4_LAUNCHED(ctx, "advance_seq_lens");
+  return G4_OK;
+}
+
+int g4_argmaxBatch(g4_ctx* ctx, const float* logits, uint32_t* result, uint32_t size, uint32_t batch) {
   G4_ENTER(ctx);
   G4_REQUIRE(logits && result, "g4_argmax: null buffer");
+  G4_REQUIRE(batch >= 1 && batch <= 1024, "g4_argmaxBatch: batch %u not in 1..1024", batch);
+  // about 4096 workgroups in all, at most kArgmaxBlocks per row
+  const unsigned want = ceil_div(size, 1024), cap = std::max(1u, 4096u / batch);
+  const int nb = want == 0 ? 1 : (int)std::min({want, (unsigned)kArgmaxBlocks, cap});
   void* scratch = nullptr;
-  int rc = g4_internal_scratch(ctx, kArgmaxBlocks * sizeof(Cand), &scratch);
+  int rc = g4_internal_scratch(ctx, (size_t)batch * nb * sizeof(Cand), &scratch);
   if (rc) return rc;
-  const unsigned want = ceil_div(size, 1024);
-  const int nb = want == 0 ? 1 : (want > (unsigned)kArgmaxBlocks ? kArgmaxBlocks : (int)want);
-  hipLaunchKernelGGL(argmax_partial, dim3(nb), dim3(NT), 0, ctx->stream, logits, size, (Cand*)scratch);
+  hipLaunchKernelGGL(argmax_partial, dim3(nb, batch), dim3(NT), 0, ctx->stream, logits, size, (Cand*)scratch);
   G4_LAUNCHED(ctx, "argmax_partial");
-  hipLaunchKernelGGL(argmax_final, dim3(1), dim3(NT), 0, ctx->stream, (const Cand*)scratch, nb, result);
+  hipLaunchKernelGGL(argmax_final, dim3(batch), dim3(NT), 0, ctx->stream, (const Cand*)scratch, nb, result);
   G4_LAUNCHED(ctx, "argmax_final");
   return G4_OK;
 }
 
-int g4_topk256(g4_ctx* ctx, const float* logits, float* result, uint32_t size) {
+int g4_argmax(g4_ctx* ctx, const float* logits, uint32_t* result, uint32_t size) {
+  return g4_argmaxBatch(ctx, logits, result, size, 1);
+}
+
+int g4_topk256Batch(g4_ctx* ctx, const float* logits, float* result, uint32_t size, uint32_t batch) {
   G4_ENTER(ctx);
   G4_REQUIRE(logits && result, "g4_topk256: null buffer");
-  void* scratch = nullptr;
-  int rc = g4_internal_scratch(ctx, (size_t)kTopkSlabs * 256 * sizeof(float2), &scratch);
-  if (rc) return rc;
+  G4_REQUIRE(batch >= 1 && batch <= 1024, "g4_topk256Batch: batch %u not in 1..1024", batch);
   const uint32_t rows = (size + 255) / 256;
-  const unsigned want = ceil_div(rows, 8);
-  const int ns = want == 0 ? 1 : (want > (unsigned)kTopkSlabs ? kTopkSlabs : (int)want);
-  hipLaunchKernelGGL(topk_partial, dim3(ns), dim3(NT), 0, ctx->stream, logits, size, (float2*)scratch);
+  const unsigned want = ceil_div(rows, 8), cap = std::max(1u, 1024u / batch);
+  const int ns = want == 0 ? 1 : (int)std::min({want, (unsigned)kTopkSlabs, cap});
+  void* scratch = nullptr;
+  int rc = g4_internal_scratch(ctx, (size_t)batch * ns * 256 * sizeof(float2), &scratch);
+  if (rc) return rc;
+  hipLaunchKernelGGL(topk_partial, dim3(ns, batch), dim3(NT), 0, ctx->stream, logits, size, (float2*)scratch);
   G4_LAUNCHED(ctx, "topk_partial");
-  hipLaunchKernelGGL(topk_final, dim3(1), dim3(NT), 0, ctx->stream, (const float2*)scratch, ns, result);
+  hipLaunchKernelGGL(topk_final, dim3(batch), dim3(NT), 0, ctx->stream, (const float2*)scratch, ns, result);
   G4_LAUNCHED(ctx, "topk_final");
   return G4_OK;
+}
+
+int g4_topk256(g4_ctx* ctx, const float* logits, float* result, uint32_t size) {
+  return g4_topk256Batch(ctx, logits, result, size, 1);
 }
 
 int g4_dequant_q4k(g4_ctx* ctx, const void* blocks, uint64_t nblocks, float* out) {

@@ -65,6 +65,11 @@ class PagedAttnParams(ctypes.Structure):
                 ("scale", ctypes.c_float), ("sliding_window", ctypes.c_uint32)]
 
 
+class PagedAttnFusedParams(ctypes.Structure):
+    _fields_ = PagedAttnParams._fields_ + [("eps", ctypes.c_float), ("theta", ctypes.c_float),
+                                           ("apply_divisor", ctypes.c_uint32)]
+
+
 class PerHeadNormParams(ctypes.Structure):  # shaders/per_head_rms_norm_no_weight.wgsl:8
     _fields_ = [("num_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
                 ("eps", ctypes.c_float), ("pad", ctypes.c_uint32)]
@@ -141,6 +146,10 @@ SIGNATURES = {
     "g4_pagedAttnDecode_workspace_size": (_I, [PagedAttnParams, ctypes.POINTER(_SZ)]),
     "g4_pagedAttnDecode": (_I, [_P, _P, _P, _P, _P, _P, _P, PagedAttnParams, _P, _SZ]),
     "g4_pagedKvStore": (_I, [_P, _P, _P, _P, _P, _P, _P, PagedAttnParams]),
+    "g4_pagedAttnDecodeFused_workspace_size": (_I, [PagedAttnFusedParams, ctypes.POINTER(_SZ)]),
+    "g4_pagedAttnDecodeFused": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, PagedAttnFusedParams, _P,
+                                     _SZ]),
+    "g4_advanceSeqLens": (_I, [_P, _P, _U32, _U32]),
     "g4_perHeadRmsNormNoWeight": (_I, [_P, _P, PerHeadNormParams]),
     "g4_fusedPerHeadNormRope": (_I, [_P, _P, _P, NormRopeParams, _P]),
     "g4_fusedPerHeadNormRope_dev": (_I, [_P, _P, _P, NormRopeParams, _P, _P]),
@@ -151,6 +160,8 @@ SIGNATURES = {
     "g4_advancePosition": (_I, [_P, _P, _U32]),
     "g4_argmax": (_I, [_P, _P, _P, _U32]),
     "g4_topk256": (_I, [_P, _P, _P, _U32]),
+    "g4_argmaxBatch": (_I, [_P, _P, _P, _U32, _U32]),
+    "g4_topk256Batch": (_I, [_P, _P, _P, _U32, _U32]),
     "g4_rmsNormMatmul_q4k": (_I, [_P, _P, _P, _P, _P, MatmulParams, _F]),
     "g4_normAddGateUpGelu_q4k": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, MatmulParams, _F]),
     "g4_normAddMatmulSegments": (_I, [_P, _I, _P, _P, _P, _P, _P, ctypes.POINTER(_P),

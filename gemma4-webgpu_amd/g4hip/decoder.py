@@ -17,6 +17,12 @@ decode step in either of two forms:
   flash-decode) and reads the position from device memory, so the whole step
   can be captured once in a HIP graph and replayed token after token.
 
+``BatchDecoder`` runs the same layers for many sequences at once (ragged
+continuous-batching decode): every matmul takes all sequences' activation
+vectors through the matrix-core kernel (each weight tile read once per
+step), and attention reads each sequence's K/V from a paged f16 pool
+through a per-sequence page table.
+
 Shapes follow the layer the benchmark is quoted on: hidden 1536, 8 query heads
 and 1 KV head of dim 256, FFN 6144 (Q4_K q/k/v/o/gate/up, Q6_K down), tied
 Q6_K LM head [262144 x 1536], softcap 30; layers {4,9,...,34} attend globally
@@ -92,33 +98,69 @@ class LayerWeights:
     v_cache: Buffer
 
 
-class Decoder:
-    def __init__(self, ctx: Context, shape: Optional[E2BShape] = None, max_seq: int = 4096, seed: int = 0,
-                 n_layers: Optional[int] = None, lm_head: bool = True):
+class _SyntheticModel:
+    """Seeded synthetic E2B-shaped weights, generated on the device. Each
+    layer's k_cache / v_cache is whatever `kv(il)` returns (dense caches or
+    paged pools)."""
+
+    def _build_weights(self, ctx: Context, shape: Optional[E2BShape], n_layers: Optional[int], seed: int,
+                       lm_head: bool, kv) -> None:
         self.ctx = ctx
         self.s = shape or E2BShape()
         if n_layers is not None:
             self.s.n_layers = n_layers
-        self.max_seq = max_seq
         self.seed = seed
         s = self.s
         self._tid = 0
         self.layers: List[LayerWeights] = []
         for il in range(s.n_layers):
+            kc, vc = kv(il)
             self.layers.append(LayerWeights(
                 wq=self._q4k(s.q_dim, s.hidden), wk=self._q4k(s.kv_dim, s.hidden), wv=self._q4k(s.kv_dim, s.hidden),
                 wo=self._q4k(s.hidden, s.q_dim), wgate=self._q4k(s.ffn, s.hidden), wup=self._q4k(s.ffn, s.hidden),
                 wdown=self._q6k(s.hidden, s.ffn),
                 attn_norm=self._f16(s.hidden), post_attn_norm=self._f16(s.hidden), pre_ffn_norm=self._f16(s.hidden),
                 post_ffn_norm=self._f16(s.hidden), q_norm=self._f16(s.head_dim), k_norm=self._f16(s.head_dim),
-                k_cache=ctx.zeros(max_seq * s.kv_dim, np.uint16), v_cache=ctx.zeros(max_seq * s.kv_dim, np.uint16)))
+                k_cache=kc, v_cache=vc))
         self.final_norm = self._f16(s.hidden)
         self.lm_head = self._q6k(s.vocab, s.hidden) if lm_head else None
         # proportional RoPE divisor table: 1.0 on the first quarter of the pairs,
         # 1e30 (+Inf in f16) after (src/engine.ts:522-537)
         half = s.head_dim // 2
-        table = np.where(np.arange(half) < half // 4, 1.0, 1e30).astype(np.float16)
+        table = np.where(np.arange(half) < half // 4, 1.0, np.inf).astype(np.float16)
         self.rope_freqs = ctx.from_numpy(table.view(np.uint16))
+
+    # ---- synthetic weights -------------------------------------------------
+    def _seed(self) -> int:
+        self._tid += 1
+        return splitmix64(self.seed, self._tid)
+
+    def _q4k(self, M: int, N: int) -> Buffer:
+        nb = M * N // 256
+        b = self.ctx.alloc(nb * Q4K_BYTES)
+        self.ctx.fill_q4k(b, nb, self._seed())
+        return b
+
+    def _q6k(self, M: int, N: int) -> Buffer:
+        nb = M * N // 256
+        b = self.ctx.alloc(nb * Q6K_BYTES)
+        self.ctx.fill_q6k(b, nb, self._seed())
+        return b
+
+    def _f16(self, n: int) -> Buffer:
+        b = self.ctx.empty(n, np.uint16)
+        self.ctx.fill_normal_f16(b, n, self._seed(), 1.0, 0.1)
+        return b
+
+
+class Decoder(_SyntheticModel):
+    def __init__(self, ctx: Context, shape: Optional[E2BShape] = None, max_seq: int = 4096, seed: int = 0,
+                 n_layers: Optional[int] = None, lm_head: bool = True):
+        self.max_seq = max_seq
+        kvn = max_seq * (shape or E2BShape()).kv_dim
+        self._build_weights(ctx, shape, n_layers, seed, lm_head,
+                            lambda il: (ctx.zeros(kvn, np.uint16), ctx.zeros(kvn, np.uint16)))
+        s = self.s
         f32 = np.float32
         self.hidden = ctx.empty(s.hidden, f32)
         self.hidden2 = ctx.empty(s.hidden, f32)
@@ -150,28 +192,6 @@ class Decoder:
         self.attn_ws = ctx.zeros(ws, np.uint8)
         ctx.fill_normal_f32(self.hidden, s.hidden, self._seed(), 0.0, 1.0)
         ctx.sync()
-
-    # ---- synthetic weights -------------------------------------------------
-    def _seed(self) -> int:
-        self._tid += 1
-        return splitmix64(self.seed, self._tid)
-
-    def _q4k(self, M: int, N: int) -> Buffer:
-        nb = M * N // 256
-        b = self.ctx.alloc(nb * Q4K_BYTES)
-        self.ctx.fill_q4k(b, nb, self._seed())
-        return b
-
-    def _q6k(self, M: int, N: int) -> Buffer:
-        nb = M * N // 256
-        b = self.ctx.alloc(nb * Q6K_BYTES)
-        self.ctx.fill_q6k(b, nb, self._seed())
-        return b
-
-    def _f16(self, n: int) -> Buffer:
-        b = self.ctx.empty(n, np.uint16)
-        self.ctx.fill_normal_f16(b, n, self._seed(), 1.0, 0.1)
-        return b
 
     def fill_kv(self, length: int, seed: int = 1) -> None:
         """Synthetic cached K/V ~ N(0,1) for positions [0, length)."""
@@ -284,3 +304,157 @@ class Decoder:
         kernel when the split count is too large to merge in-kernel), the head
         (1), argmax (2) and the position advance (1)."""
         return 5 * self.s.n_layers + (3 if self.lm_head is not None else 1) + 1
+
+
+class BatchDecoder(_SyntheticModel):
+    """Ragged multi-sequence decode: `num_seqs` sequences with their own cached
+    lengths share one set of weights and, per layer, one paged f16 K/V pool.
+
+    Pages are handed out on the host when the decoder is built: sequence i
+    owns ceil((context_lens[i] + reserve) / page_size) pages, taken from a
+    shuffled free list so that a sequence's pages are scattered over the
+    pool, as they are after a serving loop has run a while. `seq_lens` holds
+    every sequence's length on the device; a step appends one token to each
+    sequence (seq_lens += 1) and may be captured once and replayed while the
+    reserve lasts.
+    """
+
+    def __init__(self, ctx: Context, context_lens, shape: Optional[E2BShape] = None, page_size: int = 16,
+                 reserve: int = 64, seed: int = 0, n_layers: Optional[int] = None, lm_head: bool = True,
+                 page_seed: int = 7):
+        lens = np.asarray(context_lens, dtype=np.int64)
+        if lens.ndim != 1 or lens.size == 0 or lens.size > 64 or np.any(lens < 0):
+            raise ValueError("context_lens: 1..64 non-negative lengths")
+        s0 = shape or E2BShape()
+        self.B = int(lens.size)
+        self.page_size = page_size
+        self.max_seq = int(lens.max()) + reserve
+        self.max_pages = -(-self.max_seq // page_size)
+        per_seq = [-(-(int(L) + reserve) // page_size) for L in lens]
+        self.num_pages = int(sum(per_seq))
+        order = np.random.default_rng(page_seed).permutation(self.num_pages).astype(np.int32)
+        table = np.full((self.B, self.max_pages), -1, np.int32)
+        at = 0
+        for i, n in enumerate(per_seq):
+            table[i, :n] = order[at:at + n]
+            at += n
+        self.page_table_host = table
+        self.lens_host = lens.astype(np.uint32)
+        pool = self.num_pages * page_size * s0.kv_dim
+        self._build_weights(ctx, shape, n_layers, seed, lm_head,
+                            lambda il: (ctx.zeros(pool, np.uint16), ctx.zeros(pool, np.uint16)))
+        s, B, f32 = self.s, self.B, np.float32
+        self.page_table = ctx.from_numpy(table)
+        self.seq_lens = ctx.from_numpy(self.lens_host)
+        self.hidden = ctx.empty(B * s.hidden, f32)
+        self.hidden2 = ctx.empty(B * s.hidden, f32)
+        self.q = ctx.empty(B * s.q_dim, f32)
+        self.k = ctx.empty(B * s.kv_dim, f32)
+        self.v = ctx.empty(B * s.kv_dim, f32)
+        self.attn = ctx.empty(B * s.q_dim, f32)
+        self.o = ctx.empty(B * s.hidden, f32)
+        self.gate = ctx.empty(B * s.ffn, f32)
+        self.up = ctx.empty(B * s.ffn, f32)
+        self.act = ctx.empty(B * s.ffn, f32)
+        self.down = ctx.empty(B * s.hidden, f32)
+        self.logits = ctx.empty(B * s.vocab, f32) if lm_head else None
+        self.tokens = ctx.zeros(B, np.uint32)
+        self.topk = ctx.empty(B * 512, f32)
+        self.attn_params = []
+        for il in range(s.n_layers):
+            glob = s.is_global(il)
+            self.attn_params.append(ctx.paged_fused_params(
+                B, s.n_q_heads, s.n_kv_heads, s.head_dim, page_size, self.max_pages, self.max_seq, self.num_pages,
+                0 if glob else s.window, s.eps, s.theta_global if glob else s.theta_local, int(glob)))
+        self.attn_ws = ctx.zeros(max(ctx.paged_fused_workspace_bytes(p) for p in self.attn_params), np.uint8)
+        ctx.fill_normal_f32(self.hidden, B * s.hidden, self._seed(), 0.0, 1.0)
+        ctx.sync()
+
+    def fill_kv(self, seed: int = 1) -> None:
+        """Synthetic cached K/V ~ N(0,1) over every page of every pool."""
+        n = self.num_pages * self.page_size * self.s.kv_dim
+        for il, L in enumerate(self.layers):
+            self.ctx.fill_normal_f16(L.k_cache, n, splitmix64(seed, 2 * il), 0.0, 1.0)
+            self.ctx.fill_normal_f16(L.v_cache, n, splitmix64(seed, 2 * il + 1), 0.0, 1.0)
+
+    def set_lengths(self, lens) -> None:
+        lens = np.asarray(lens, dtype=np.uint32)
+        if lens.shape != (self.B,) or int(lens.max()) >= self.max_seq:
+            raise ValueError("set_lengths: one length per sequence, below the reserved capacity")
+        self.lens_host = lens
+        self.seq_lens.upload(lens)
+
+    def pool_row(self, seq: int, pos: int) -> int:
+        """Pool row of sequence `seq`'s logical position `pos`."""
+        return int(self.page_table_host[seq, pos // self.page_size]) * self.page_size + pos % self.page_size
+
+    def kv_bytes_per_step(self) -> int:
+        """K/V bytes one step reads: every sequence's window in every layer
+        (lengths after the step's append)."""
+        s, total = self.s, 0
+        for il in range(s.n_layers):
+            for L in self.lens_host:
+                n = int(L) + 1
+                if not s.is_global(il):
+                    n = min(n, s.window)
+                total += n * 2 * s.kv_dim * 2
+        return total
+
+    def step(self, sample: str = "argmax") -> None:
+        """One token for every sequence. Six launches per layer:
+          1. [post-FFN norm-add of the previous layer ->] attn rmsNorm -> q/k/v
+          2. per sequence: q/k norm + RoPE, v_norm, K/V append, paged split-K attention (+ merge)
+          3. o projection
+          4. post-attn norm-add -> pre-FFN rmsNorm -> gate/up
+          5. GELU product
+          6. down projection (Q6_K)
+        then the last norm-add + final rmsNorm + LM head + softcap, and the
+        per-sequence argmax (or top-k 256)."""
+        c, s, B = self.ctx, self.s, self.B
+        c.advanceSeqLens(self.seq_lens, B, 1)
+        for il, L in enumerate(self.layers):
+            ws = [L.wq, L.wk, L.wv]
+            outs = [self.q, self.k, self.v]
+            rows = [s.q_dim, s.kv_dim, s.kv_dim]
+            if il == 0:
+                c.normAddMatmulSegmentsBatch("q4k", self.hidden, L.attn_norm, None, None, None, ws, outs, rows,
+                                             s.hidden, B, s.eps)
+            else:
+                prev = self.layers[il - 1]
+                c.normAddMatmulSegmentsBatch("q4k", self.down, prev.post_ffn_norm, self.hidden2, L.attn_norm,
+                                             self.hidden, ws, outs, rows, s.hidden, B, s.eps)
+            c.pagedAttnDecodeFused(self.q, self.k, self.v, L.q_norm, L.k_norm, self.rope_freqs, L.k_cache,
+                                   L.v_cache, self.page_table, self.seq_lens, self.attn, self.attn_params[il],
+                                   self.attn_ws)
+            c.matmulQuantBatch(self.attn, L.wo, self.o, s.hidden, s.q_dim, B)
+            c.normAddMatmulSegmentsBatch("q4k", self.o, L.post_attn_norm, self.hidden, L.pre_ffn_norm,
+                                         self.hidden2, [L.wgate, L.wup], [self.gate, self.up], [s.ffn, s.ffn],
+                                         s.hidden, B, s.eps)
+            c.geluMul(self.gate, self.up, self.act, B * s.ffn)
+            c.matmulQuantBatch(self.act, L.wdown, self.down, s.hidden, s.ffn, B, "q6k")
+        last = self.layers[-1]
+        if self.lm_head is not None:
+            c.normAddMatmulSegmentsBatch("q6k", self.down, last.post_ffn_norm, self.hidden2, self.final_norm,
+                                         self.hidden, [self.lm_head], [self.logits], [s.vocab], s.hidden, B, s.eps,
+                                         softcap=s.softcap)
+            if sample == "argmax":
+                c.argmaxBatch(self.logits, self.tokens, s.vocab, B)
+            else:
+                c.topk256Batch(self.logits, self.topk, s.vocab, B)
+        else:
+            row = 4 * s.hidden
+            for i in range(B):
+                c.fusedNormAdd(self.down.offset(i * row), last.post_ffn_norm, self.hidden2.offset(i * row),
+                               self.hidden.offset(i * row), s.hidden, s.eps)
+        self.lens_host = self.lens_host + 1
+
+    def capture(self, sample: str = "argmax"):
+        """The step as a HIP graph; each replay appends one token per sequence."""
+        lens = self.lens_host.copy()
+        self.ctx.graph_begin()
+        try:
+            self.step(sample)
+        finally:
+            g = self.ctx.graph_end()
+        self.lens_host = lens  # capture enqueues nothing
+        return g

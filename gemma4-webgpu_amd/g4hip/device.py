@@ -20,6 +20,7 @@ from ._lib import (
     MatmulParams,
     NormAddParams,
     NormRopeParams,
+    PagedAttnFusedParams,
     PagedAttnParams,
     PerHeadNormParams,
     RmsNormParams,
@@ -303,6 +304,29 @@ class Context:
         check(lib().g4_pagedKvStore(self.h, _p(k_in), _p(v_in), _p(k_pool), _p(v_pool), _p(page_table),
                                     _p(seq_lens), p))
 
+    @staticmethod
+    def paged_fused_params(num_seqs, nqh, nkh, hd, page_size, max_pages, max_seq_len, num_pages, window, eps,
+                           theta, apply_divisor, scale=1.0):
+        return PagedAttnFusedParams(num_seqs, nqh, nkh, hd, page_size, max_pages, max_seq_len, num_pages, scale,
+                                    window, eps, theta, apply_divisor)
+
+    @staticmethod
+    def paged_fused_workspace_bytes(p: PagedAttnFusedParams) -> int:
+        n = ctypes.c_size_t()
+        check(lib().g4_pagedAttnDecodeFused_workspace_size(p, ctypes.byref(n)))
+        return int(n.value)
+
+    def pagedAttnDecodeFused(self, q_raw: Ptr, k_raw: Ptr, v_raw: Ptr, q_norm_w: Ptr, k_norm_w: Ptr,
+                             rope_freqs: Ptr, k_pool: Ptr, v_pool: Ptr, page_table: Ptr, seq_lens: Ptr, out: Ptr,
+                             p: PagedAttnFusedParams, workspace: Buffer) -> None:
+        """Per sequence: q/k norm + RoPE, v_norm, KV row store into the pool page and decode attention."""
+        check(lib().g4_pagedAttnDecodeFused(self.h, _p(q_raw), _p(k_raw), _p(v_raw), _p(q_norm_w), _p(k_norm_w),
+                                            _p(rope_freqs), _p(k_pool), _p(v_pool), _p(page_table), _p(seq_lens),
+                                            _p(out), p, _p(workspace), workspace.nbytes))
+
+    def advanceSeqLens(self, seq_lens: Ptr, num_seqs: int, delta: int = 1) -> None:
+        check(lib().g4_advanceSeqLens(self.h, _p(seq_lens), num_seqs, delta))
+
     # ---- norms / activations ----
     def perHeadRmsNormNoWeight(self, data: Ptr, num_heads: int, head_dim: int, eps: float = 1e-6) -> None:
         check(lib().g4_perHeadRmsNormNoWeight(self.h, _p(data), PerHeadNormParams(num_heads, head_dim, eps, 0)))
@@ -337,6 +361,12 @@ class Context:
 
     def topk256(self, logits: Ptr, result: Ptr, size: int) -> None:
         check(lib().g4_topk256(self.h, _p(logits), _p(result), size))
+
+    def argmaxBatch(self, logits: Ptr, result: Ptr, size: int, batch: int) -> None:
+        check(lib().g4_argmaxBatch(self.h, _p(logits), _p(result), size, batch))
+
+    def topk256Batch(self, logits: Ptr, result: Ptr, size: int, batch: int) -> None:
+        check(lib().g4_topk256Batch(self.h, _p(logits), _p(result), size, batch))
 
     # ---- debug / synthetic inputs ----
     def dequant_q4k(self, blocks: Ptr, nblocks: int, out: Ptr) -> None:

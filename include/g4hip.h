@@ -203,6 +203,33 @@ int g4_pagedAttnDecode_workspace_size(g4_paged_attn_params p, size_t* bytes);
 int g4_pagedAttnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
                        const int32_t* page_table, const uint32_t* seq_lens, float* output,
                        g4_paged_attn_params p, void* workspace, size_t workspace_bytes);
+/* The per-layer attention block of a multi-sequence decode step in one launch
+ * (per sequence, the block src/engine.ts:1562-1584 runs for one token):
+ * sequence s decodes position seq_lens[s] - 1 (seq_lens already advanced,
+ * g4_advanceSeqLens). q_norm + RoPE on q_raw [num_seqs][num_q_heads][head_dim]
+ * (not modified), k_norm + RoPE on k_raw and the weightless v_norm on v_raw
+ * ([num_seqs][num_kv_heads][head_dim]), the f16 K/V row stored in the pool
+ * page the table names (a page id outside [0, num_pages) stores nothing),
+ * then split-K decode attention over the sequence's window. The workspace is
+ * sized by g4_pagedAttnDecodeFused_workspace_size; calls that share it must
+ * not overlap. */
+typedef struct {
+  uint32_t num_seqs, num_q_heads, num_kv_heads, head_dim;
+  uint32_t page_size, max_pages, max_seq_len, num_pages;
+  float scale;
+  uint32_t sliding_window;
+  float eps, theta;
+  uint32_t apply_divisor;
+} g4_paged_attn_fused_params;
+int g4_pagedAttnDecodeFused_workspace_size(g4_paged_attn_fused_params p, size_t* bytes);
+int g4_pagedAttnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float* v_raw,
+                            const uint16_t* q_norm_w, const uint16_t* k_norm_w, const uint16_t* rope_freqs,
+                            uint16_t* k_pool, uint16_t* v_pool, const int32_t* page_table,
+                            const uint32_t* seq_lens, float* output, g4_paged_attn_fused_params p,
+                            void* workspace, size_t workspace_bytes);
+/* seq_lens[s] += delta for s < num_seqs, on the stream (the device-side
+ * length counters a captured multi-sequence step replays with). */
+int g4_advanceSeqLens(g4_ctx* ctx, uint32_t* seq_lens, uint32_t num_seqs, uint32_t delta);
 /* Append one row per sequence at position seq_lens[s] - 1 (after the host or
  * a previous kernel advanced seq_lens). k_in/v_in are [num_seqs][nkh*hd] f32. */
 int g4_pagedKvStore(g4_ctx* ctx, const float* k_in, const float* v_in, uint16_t* k_pool,
@@ -255,6 +282,11 @@ int g4_advancePosition(g4_ctx* ctx, uint32_t* position_dev, uint32_t delta);
 int g4_argmax(g4_ctx* ctx, const float* logits, uint32_t* result, uint32_t size);
 /* shaders/topk256.wgsl:1-3 — result f32[512] = (max, bitcast idx) per residue class. */
 int g4_topk256(g4_ctx* ctx, const float* logits, float* result, uint32_t size);
+/* The same per row of `batch` rows of `size` logits each (sampling at M > 1):
+ * result[r] is row r's argmax / result[512 r .. 512 r + 511] its top-k pairs,
+ * each equal to what the one-row call returns for that row. batch <= 1024. */
+int g4_argmaxBatch(g4_ctx* ctx, const float* logits, uint32_t* result, uint32_t size, uint32_t batch);
+int g4_topk256Batch(g4_ctx* ctx, const float* logits, float* result, uint32_t size, uint32_t batch);
 
 /* ------------------------------------------------------------------------ */
 /* Fused step kernels (the MI355X decode path; each is equivalent to a run   */

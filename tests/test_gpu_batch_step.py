@@ -1,0 +1,196 @@
+"""GPU parity of the ragged multi-sequence decode step.
+
+* The paged attention block on identical inputs: per sequence bit-identical
+  to the single-sequence fused kernel over a dense copy of its pages, within
+  rel-L2 1e-3 of the oracle, K/V rows appended only where the table says.
+* The whole step: every sequence against the oracle's single-sequence step on
+  its own dense caches. Attention at scale 1.0 over N(0,1) keys has scores
+  with a standard deviation near 16, so where two positions' scores are
+  within a fraction of a unit the softmax weights amplify the ~1e-5 relative
+  difference of the int8-activation q/k/v projections roughly 100-fold; the
+  composed step is therefore held to rel-L2 1e-2 and cosine 0.9999 (each
+  kernel meets 1e-3 on its own inputs in the stage-wise tests).
+* HIP-graph replays equal eager steps bit for bit."""
+import numpy as np
+import pytest
+
+import oracle as O
+from decode_oracle import HostModel
+from g4hip.decoder import BatchDecoder, E2BShape
+from gpu_util import assert_close, bits_equal
+
+pytestmark = pytest.mark.gpu
+
+# lengths cover: the first token, page edges (15/16/17), the window edge
+# (511/512/513) and beyond it, and a long global context
+LENS = [0, 1, 15, 16, 17, 31, 300, 511, 512, 513, 530, 700, 1000, 5, 64, 100, 255, 256]
+
+
+@pytest.fixture(scope="module")
+def bdec(ctx):
+    # layer 0 local (window 512), layer 1 global; a smaller vocabulary keeps the oracle quick
+    shape = E2BShape(n_layers=2, global_layers=(1,), vocab=16384)
+    d = BatchDecoder(ctx, LENS, shape, seed=11, reserve=8)
+    d.fill_kv(seed=12)
+    ctx.sync()
+    return d
+
+
+def _pools(d):
+    return [(L.k_cache.download(np.uint16), L.v_cache.download(np.uint16)) for L in d.layers]
+
+
+def _restore(d, hidden, pools, lens):
+    d.hidden.upload(hidden)
+    for L, (k, v) in zip(d.layers, pools):
+        L.k_cache.upload(k)
+        L.v_cache.upload(v)
+    d.set_lengths(lens)
+
+
+def _dense(d, pool, seq, n):
+    """Sequence `seq`'s first n rows gathered from a pool, as a dense cache
+    with one spare row."""
+    kv = d.s.kv_dim
+    P = pool.reshape(-1, kv)
+    out = np.zeros((n + 1, kv), np.uint16)
+    for t in range(n):
+        out[t] = P[d.pool_row(seq, t)]
+    return out.reshape(-1)
+
+
+STEP_REL = 1e-2
+
+
+def test_paged_attention_block_matches_dense_and_oracle(ctx, bdec):
+    d, s, B = bdec, bdec.s, bdec.B
+    kv, table = s.kv_dim, d.rope_freqs.download(np.uint16)
+    rng = np.random.default_rng(21)
+    Q = rng.normal(0, 2, (B, s.q_dim)).astype(np.float32)
+    K = rng.normal(0, 2, (B, kv)).astype(np.float32)
+    V = rng.normal(0, 2, (B, kv)).astype(np.float32)
+    d.q.upload(Q)
+    d.k.upload(K)
+    d.v.upload(V)
+    for il, L in enumerate(d.layers):
+        glob = s.is_global(il)
+        theta = s.theta_global if glob else s.theta_local
+        window = 0 if glob else s.window
+        k0 = L.k_cache.download(np.uint16)
+        v0 = L.v_cache.download(np.uint16)
+        d.set_lengths(np.array(LENS, np.uint32) + 1)  # the step's advance already applied
+        ctx.pagedAttnDecodeFused(d.q, d.k, d.v, L.q_norm, L.k_norm, d.rope_freqs, L.k_cache, L.v_cache,
+                                 d.page_table, d.seq_lens, d.attn, d.attn_params[il], d.attn_ws)
+        A = d.attn.download(np.float32).reshape(B, -1)
+        k1 = L.k_cache.download(np.uint16).reshape(-1, kv)
+        v1 = L.v_cache.download(np.uint16).reshape(-1, kv)
+        qn, kn = L.q_norm.download(np.uint16), L.k_norm.download(np.uint16)
+        for b, pos in enumerate(LENS):
+            # dense copy of the sequence's pages, then the single-sequence kernel
+            kc, vc = _dense(d, k0, b, pos), _dense(d, v0, b, pos)
+            kdev, vdev = ctx.from_numpy(kc), ctx.from_numpy(vc)
+            ap = ctx.attn_fused_params(s.n_q_heads, s.n_kv_heads, s.head_dim, pos + 1, window, s.eps, theta,
+                                       int(glob))
+            ws = ctx.zeros(ctx.attn_fused_workspace_bytes(ap), np.uint8)
+            out = ctx.empty(s.q_dim, np.float32)
+            ctx.attnDecodeFused(ctx.from_numpy(Q[b]), ctx.from_numpy(K[b]), ctx.from_numpy(V[b]), L.q_norm,
+                                L.k_norm, d.rope_freqs, kdev, vdev, out, ap, ws,
+                                ctx.from_numpy(np.array([pos], np.uint32)))
+            assert bits_equal(A[b], out.download(np.float32)), (il, b)
+            r = d.pool_row(b, pos)
+            kd = kdev.download(np.uint16).reshape(-1, kv)
+            vd = vdev.download(np.uint16).reshape(-1, kv)
+            assert np.array_equal(k1[r], kd[pos]) and np.array_equal(v1[r], vd[pos]), (il, b)
+            # the oracle on the same inputs
+            q = O.fused_per_head_norm_rope(Q[b], qn, s.n_q_heads, s.head_dim, s.eps, pos, theta, int(glob), table)
+            k = O.fused_per_head_norm_rope(K[b], kn, s.n_kv_heads, s.head_dim, s.eps, pos, theta, int(glob), table)
+            v = O.per_head_rms_norm_no_weight(V[b], s.n_kv_heads, s.head_dim, s.eps)
+            O.kv_cache_store_f16(k, v, kc, vc, s.n_kv_heads, s.head_dim, pos)
+            a = O.attention(q, kc, vc, s.n_q_heads, s.n_kv_heads, s.head_dim, pos + 1, 1.0, window)
+            assert_close(A[b], a, what=f"layer {il} seq {b} len {pos}")
+            for got, want in ((k1[r], kc.reshape(-1, kv)[pos]), (v1[r], vc.reshape(-1, kv)[pos])):
+                g16, w16 = got.view(np.float16).astype(np.float32), want.view(np.float16).astype(np.float32)
+                assert np.all(np.abs(g16 - w16) <= 2.0 ** -10 * np.maximum(np.abs(w16), 2.0 ** -14)), (il, b)
+        written = {d.pool_row(b, pos) for b, pos in enumerate(LENS)}
+        for before, after in ((k0, k1), (v0, v1)):
+            diff = np.nonzero(np.any(before.reshape(-1, kv) != after, axis=1))[0]
+            assert set(diff.tolist()) <= written
+        L.k_cache.upload(k0)
+        L.v_cache.upload(v0)
+    d.set_lengths(np.array(LENS, np.uint32))
+
+
+def test_batch_step_matches_oracle_per_sequence(ctx, bdec):
+    d, s, B = bdec, bdec.s, bdec.B
+    hm = HostModel(d)
+    hidden0 = d.hidden.download(np.float32).reshape(B, s.hidden)
+    pools0 = _pools(d)
+    lens0 = d.lens_host.copy()
+
+    d.step()
+    ctx.sync()
+    assert np.array_equal(d.seq_lens.download(np.uint32), lens0 + 1)
+    H = d.hidden.download(np.float32).reshape(B, s.hidden)
+    LG = d.logits.download(np.float32).reshape(B, s.vocab)
+    TOK = d.tokens.download(np.uint32)
+    pools1 = _pools(d)
+    kv = s.kv_dim
+    for b, L in enumerate(LENS):
+        kcs = [_dense(d, k, b, L) for k, _ in pools0]
+        vcs = [_dense(d, v, b, L) for _, v in pools0]
+        x, logits = hm.step(hidden0[b], kcs, vcs, L)
+        assert_close(H[b], x, rel=STEP_REL, what=f"hidden seq {b} len {L}")
+        assert_close(LG[b], logits, rel=STEP_REL, what=f"logits seq {b} len {L}")
+        assert TOK[b] == O.argmax(LG[b]), b
+        r = d.pool_row(b, L)
+        for il in range(s.n_layers):
+            for got, ref, nm in ((pools1[il][0], kcs[il], "k"), (pools1[il][1], vcs[il], "v")):
+                row = got.reshape(-1, kv)[r].view(np.float16).astype(np.float32)
+                want = ref.reshape(-1, kv)[L].view(np.float16).astype(np.float32)
+                assert_close(row, want, rel=STEP_REL, what=f"{nm} row seq {b} layer {il}")
+    # nothing but the appended rows changed in the pools
+    written = sorted(d.pool_row(b, L) for b, L in enumerate(LENS))
+    for il in range(s.n_layers):
+        for before, after in ((pools0[il][0], pools1[il][0]), (pools0[il][1], pools1[il][1])):
+            diff = np.nonzero(np.any(before.reshape(-1, kv) != after.reshape(-1, kv), axis=1))[0]
+            assert set(diff.tolist()) <= set(written)
+    _restore(d, hidden0.reshape(-1), pools0, lens0)
+
+
+def test_batch_graph_replay_matches_eager(ctx, bdec):
+    d, B = bdec, bdec.B
+    hidden0 = d.hidden.download(np.float32)
+    pools0 = _pools(d)
+    lens0 = d.lens_host.copy()
+    eager = []
+    for _ in range(3):
+        d.step()
+        ctx.sync()
+        eager.append((d.hidden.download(np.float32), d.logits.download(np.float32), d.tokens.download(np.uint32)))
+    _restore(d, hidden0, pools0, lens0)
+    g = d.capture()
+    try:
+        for i in range(3):
+            ctx.graph_launch(g)
+            ctx.sync()
+            _ = d.seq_lens.download(np.uint32)  # eager work between replays
+            assert bits_equal(d.hidden.download(np.float32), eager[i][0]), i
+            assert bits_equal(d.logits.download(np.float32), eager[i][1]), i
+            assert np.array_equal(d.tokens.download(np.uint32), eager[i][2]), i
+        assert np.array_equal(d.seq_lens.download(np.uint32), lens0 + 3)
+    finally:
+        ctx.graph_destroy(g)
+        _restore(d, hidden0, pools0, lens0)
+
+
+def test_paged_fused_rejects_bad_shapes(ctx, bdec):
+    d = bdec
+    p = d.attn_params[0]
+    bad = ctx.paged_fused_params(d.B, 8, 1, 256, 16, 2, 64, d.num_pages, 0, 1e-6, 1e4, 0)
+    with pytest.raises(Exception, match="exceeds the page table"):
+        ctx.pagedAttnDecodeFused(d.q, d.k, d.v, d.layers[0].q_norm, d.layers[0].k_norm, None, d.layers[0].k_cache,
+                                 d.layers[0].v_cache, d.page_table, d.seq_lens, d.attn, bad, d.attn_ws)
+    small = ctx.zeros(16, np.uint8)
+    with pytest.raises(Exception, match="workspace"):
+        ctx.pagedAttnDecodeFused(d.q, d.k, d.v, d.layers[0].q_norm, d.layers[0].k_norm, None, d.layers[0].k_cache,
+                                 d.layers[0].v_cache, d.page_table, d.seq_lens, d.attn, p, small)

@@ -49,7 +49,7 @@ def test_fused_per_head_norm_rope(ctx, nh, hd, pos, theta, div):
     x = O.gen_normal_f32(pos + hd, nh * hd, 0.0, 2.0)
     w = O.gen_normal_f16(pos + 1, hd, 1.0, 0.1)
     # real E2B table: 1.0 for the first quarter of the pairs, 1e30 (-> +Inf in f16) after
-    table = np.where(np.arange(hd // 2) < hd // 8, 1.0, 1e30).astype(np.float16).view(np.uint16)
+    table = np.where(np.arange(hd // 2) < hd // 8, 1.0, np.inf).astype(np.float16).view(np.uint16)
     ref = O.fused_per_head_norm_rope(x, w, nh, hd, 1e-6, pos, theta, div, table)
     d = ctx.from_numpy(x)
     ctx.fusedPerHeadNormRope(d, ctx.from_numpy(w), nh, hd, 1e-6, pos, theta, div, ctx.from_numpy(table))
@@ -140,3 +140,22 @@ def test_argmax_topk_ties_and_specials(ctx):
         a, t = _argmax_topk(ctx, x)
         assert a == O.argmax(x) == _rule_argmax(x), trial
         assert bits_equal(t, O.topk256(x)), trial
+
+
+@pytest.mark.parametrize("size,batch", [(262144, 8), (262144, 32), (1000, 5), (257, 64)])
+def test_argmax_topk_batch_rows(ctx, size, batch):
+    """Sampling over many rows: each row's result equals the one-row rule."""
+    rng = np.random.default_rng(size + batch)
+    X = rng.integers(-3, 4, (batch, size)).astype(np.float32)
+    X[1::3, rng.integers(0, size, 5)] = np.nan
+    X[2] = -np.inf
+    d = ctx.from_numpy(X)
+    r = ctx.zeros(batch, np.uint32)
+    t = ctx.empty(batch * 512, np.float32)
+    ctx.argmaxBatch(d, r, size, batch)
+    ctx.topk256Batch(d, t, size, batch)
+    R = r.download(np.uint32)
+    T = t.download(np.float32).reshape(batch, 512)
+    for b in range(batch):
+        assert R[b] == O.argmax(X[b]), b
+        assert bits_equal(T[b], O.topk256(X[b])), b

@@ -5,6 +5,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+from decode_oracle import HostModel
 from g4hip.decoder import Decoder, E2BShape
 from gpu_util import assert_close, bits_equal
 
@@ -30,35 +31,7 @@ def host(buf, dtype):
 
 
 def oracle_step(d: Decoder, hidden, kcs, vcs, pos):
-    s = d.s
-    x = hidden.copy()
-    for il, L in enumerate(d.layers):
-        glob = s.is_global(il)
-        theta = s.theta_global if glob else s.theta_local
-        window = 0 if glob else s.window
-        table = host(d.rope_freqs, np.uint16)
-        n = O.rms_norm(x, host(L.attn_norm, np.uint16), s.eps)
-        q = O.matmul(n, host(L.wq, np.uint8), s.q_dim, s.hidden, "q4k")
-        k = O.matmul(n, host(L.wk, np.uint8), s.kv_dim, s.hidden, "q4k")
-        v = O.matmul(n, host(L.wv, np.uint8), s.kv_dim, s.hidden, "q4k")
-        v = O.per_head_rms_norm_no_weight(v, s.n_kv_heads, s.head_dim, s.eps)
-        q = O.fused_per_head_norm_rope(q, host(L.q_norm, np.uint16), s.n_q_heads, s.head_dim, s.eps, pos, theta,
-                                       int(glob), table)
-        k = O.fused_per_head_norm_rope(k, host(L.k_norm, np.uint16), s.n_kv_heads, s.head_dim, s.eps, pos, theta,
-                                       int(glob), table)
-        O.kv_cache_store_f16(k, v, kcs[il], vcs[il], s.n_kv_heads, s.head_dim, pos)
-        a = O.attention(q, kcs[il], vcs[il], s.n_q_heads, s.n_kv_heads, s.head_dim, pos + 1, 1.0, window)
-        o = O.matmul(a, host(L.wo, np.uint8), s.hidden, s.q_dim, "q4k")
-        h = O.fused_norm_add(o, host(L.post_attn_norm, np.uint16), x, s.eps)
-        n2 = O.rms_norm(h, host(L.pre_ffn_norm, np.uint16), s.eps)
-        g = O.matmul(n2, host(L.wgate, np.uint8), s.ffn, s.hidden, "q4k")
-        u = O.matmul(n2, host(L.wup, np.uint8), s.ffn, s.hidden, "q4k")
-        act = O.gelu_mul(g, u)
-        dn = O.matmul(act, host(L.wdown, np.uint8), s.hidden, s.ffn, "q6k")
-        x = O.fused_norm_add(dn, host(L.post_ffn_norm, np.uint16), h, s.eps)
-    n = O.rms_norm(x, host(d.final_norm, np.uint16), s.eps)
-    logits = O.logit_softcap(O.matmul(n, host(d.lm_head, np.uint8), s.vocab, s.hidden, "q6k"), s.softcap)
-    return x, logits
+    return HostModel(d).step(hidden, kcs, vcs, pos)
 
 
 def snapshot(d):
