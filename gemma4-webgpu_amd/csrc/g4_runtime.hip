@@ -11,7 +11,7 @@
 
 namespace {
 thread_local char g_err[512] = "";
-constexpr size_t kScratchBytes = 4u << 20;  // reduction partials; activation digits of batched matmuls
+constexpr size_t kScratchBytes = 16u << 20;  // reduction partials; operand blocks of batched matmuls
 
 bool is_fatal(hipError_t e) {
   switch (e) {

@@ -585,6 +585,122 @@ __global__ __launch_bounds__(1024) void attn_merge_kernel(const float* ws, float
 }
 
 // ---------------------------------------------------------------------------
+// paged prologue (multi-sequence step): per sequence, the q/k/v projections
+// (sums of split-K partials, added in chunk order) through q_norm + RoPE,
+// k_norm + RoPE and the weightless v_norm, the f16 K/V row appended to the
+// pool (src/engine.ts:1556-1570 per sequence). Workgroup (head, sequence):
+// heads [0, nqh) are query heads, [nqh, nqh + nkh) the K/V heads; thread t
+// owns the RoPE pair (t, t + hd/2).
+// ---------------------------------------------------------------------------
+struct ProArgs {
+  const float* q;  // [nparts][num_seqs][nqh * hd]
+  const float* k;  // [nparts][num_seqs][nkh * hd]
+  const float* v;
+  uint32_t nparts, num_seqs, nqh, nkh, hd;
+  const uint16_t* q_w;
+  const uint16_t* k_w;
+  const uint16_t* rope_freqs;
+  float theta;
+  uint32_t apply_divisor;
+  float eps;
+  float* q_out;  // [num_seqs][nqh * hd]
+  uint16_t* kp;
+  uint16_t* vp;
+  const int32_t* page_table;
+  const uint32_t* seq_lens;
+  uint32_t page_size, max_pages, num_pages, cap;
+};
+
+// Elements i0 and i1 summed over the n partials in chunk order; the loads of
+// up to 8 chunks are issued together.
+__device__ __forceinline__ float2 sum_parts2(const float* base, size_t stride, uint32_t n, uint32_t i0,
+                                             uint32_t i1) {
+  float a = 0.f, b = 0.f;
+  for (uint32_t c0 = 0; c0 < n; c0 += 8) {
+    float ta[8], tb[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const size_t c = min(c0 + (uint32_t)i, n - 1);
+      ta[i] = base[c * stride + i0];
+      tb[i] = base[c * stride + i1];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (c0 + i < n) {
+        a += ta[i];
+        b += tb[i];
+      }
+  }
+  return make_float2(a, b);
+}
+
+__global__ __launch_bounds__(NT) void attn_prologue_kernel(ProArgs a) {
+  __shared__ float red[8];
+  const uint32_t head = blockIdx.x, seq = blockIdx.y;
+  const uint32_t t = threadIdx.x, half = a.hd / 2;
+  const bool on = t < half;
+  const uint32_t tc = on ? t : 0;
+  const bool is_q = head < a.nqh;
+  const uint32_t kvh = is_q ? 0 : head - a.nqh;
+  const uint32_t L = a.seq_lens[seq];
+  const uint32_t Lc = min(L, a.cap);
+  const uint32_t pos = Lc > 0 ? Lc - 1 : 0;
+  float2 x, y = make_float2(0.f, 0.f);
+  if (is_q) {
+    const size_t stride = (size_t)a.num_seqs * a.nqh * a.hd;
+    const float* b = a.q + ((size_t)seq * a.nqh + head) * a.hd;
+    x = sum_parts2(b, stride, a.nparts, tc, tc + half);
+  } else {
+    const size_t stride = (size_t)a.num_seqs * a.nkh * a.hd;
+    const size_t off = ((size_t)seq * a.nkh + kvh) * a.hd;
+    x = sum_parts2(a.k + off, stride, a.nparts, tc, tc + half);
+    y = sum_parts2(a.v + off, stride, a.nparts, tc, tc + half);
+  }
+  if (!on) x = y = make_float2(0.f, 0.f);
+  // sums of squares: x in red[0..3], y in red[4..7]
+  const float sx = g4d::wave_sum_dpp(x.x * x.x + x.y * x.y);
+  const float sy = g4d::wave_sum_dpp(y.x * y.x + y.y * y.y);
+  if ((t & 63) == 0) {
+    red[t >> 6] = sx;
+    red[4 + (t >> 6)] = sy;
+  }
+  __syncthreads();
+  const float tx = (red[0] + red[1]) + (red[2] + red[3]);
+  const float ty = (red[4] + red[5]) + (red[6] + red[7]);
+  const float invx = 1.0f / sqrtf(tx / (float)a.hd + a.eps);
+  const float invy = 1.0f / sqrtf(ty / (float)a.hd + a.eps);
+  if (!on) return;
+  const uint16_t* wn = is_q ? a.q_w : a.k_w;
+  float x0 = x.x * g4d::f16_bits_to_f32(wn[t]) * invx;
+  float x1 = x.y * g4d::f16_bits_to_f32(wn[t + half]) * invx;
+  // RoPE as shaders/fused_per_head_norm_rope.wgsl:50-55 forms frequency and
+  // angle; cos/sin of the f32 angle in f32
+  float f = (float)(1.0 / pow((double)a.theta, (double)(2 * t) / (double)a.hd));
+  if (a.apply_divisor) f = f / g4d::f16_bits_to_f32(a.rope_freqs[t]);
+  const float ang = (float)pos * f;
+  float sn, cn;
+  sincosf(ang, &sn, &cn);
+  const float r0 = x0 * cn - x1 * sn, r1 = x0 * sn + x1 * cn;
+  if (is_q) {
+    float* o = a.q_out + ((size_t)seq * a.nqh + head) * a.hd;
+    o[t] = r0;
+    o[t + half] = r1;
+    return;
+  }
+  // append at pos when the length is in range and the page id is in the pool
+  if (L == 0 || L > a.cap) return;
+  const int32_t pg = a.page_table[(size_t)seq * a.max_pages + pos / a.page_size];
+  if (pg < 0 || pg >= (int32_t)a.num_pages) return;
+  const size_t row = ((size_t)pg * a.page_size + pos % a.page_size) * a.nkh + kvh;
+  uint16_t* kd = a.kp + row * a.hd;
+  uint16_t* vd = a.vp + row * a.hd;
+  kd[t] = g4d::f32_to_f16_bits(r0);
+  kd[t + half] = g4d::f32_to_f16_bits(r1);
+  vd[t] = g4d::f32_to_f16_bits(y.x * invy);
+  vd[t + half] = g4d::f32_to_f16_bits(y.y * invy);
+}
+
+// ---------------------------------------------------------------------------
 // paged KV append: row for position seq_lens[s]-1 of each sequence
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(NT) void paged_store_kernel(const float* k_in, const float* v_in, uint16_t* kp,
@@ -965,6 +1081,53 @@ int g4_pagedAttnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw,
   rc = launch_attn<true, true>(ctx, a, G, p.head_dim, sp.cp, dim3(sp.nsplit, p.num_kv_heads, p.num_seqs));
   if (rc) return rc;
   return merge(ctx, a, output, sp, p.num_seqs, G, p.head_dim);
+}
+
+int g4_pagedAttnPrologue(g4_ctx* ctx, const float* q_parts, const float* k_parts, const float* v_parts,
+                         uint32_t nparts, const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                         const uint16_t* rope_freqs, float* q_out, uint16_t* k_pool, uint16_t* v_pool,
+                         const int32_t* page_table, const uint32_t* seq_lens, g4_paged_attn_fused_params p) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(q_parts && k_parts && v_parts && q_norm_w && k_norm_w && q_out && k_pool && v_pool && page_table &&
+                 seq_lens && nparts >= 1,
+             "g4_pagedAttnPrologue: null buffer or no parts");
+  G4_REQUIRE(!p.apply_divisor || rope_freqs, "g4_pagedAttnPrologue: apply_divisor needs rope_freqs");
+  G4_REQUIRE(p.num_seqs > 0 && p.num_seqs <= 65535 && p.num_q_heads > 0 && p.num_kv_heads > 0,
+             "g4_pagedAttnPrologue: empty batch or heads");
+  G4_REQUIRE(p.head_dim >= 2 && p.head_dim <= 2 * NT && p.head_dim % 2 == 0,
+             "g4_pagedAttnPrologue: head_dim %u must be even and <= %d", p.head_dim, 2 * NT);
+  G4_REQUIRE(p.page_size > 0 && p.max_pages > 0 && p.num_pages > 0 && p.max_seq_len > 0 &&
+                 (uint64_t)p.max_seq_len <= (uint64_t)p.page_size * p.max_pages,
+             "g4_pagedAttnPrologue: max_seq_len %u exceeds the page table (%u x %u)", p.max_seq_len, p.max_pages,
+             p.page_size);
+  ProArgs a{};
+  a.q = q_parts;
+  a.k = k_parts;
+  a.v = v_parts;
+  a.nparts = nparts;
+  a.num_seqs = p.num_seqs;
+  a.nqh = p.num_q_heads;
+  a.nkh = p.num_kv_heads;
+  a.hd = p.head_dim;
+  a.q_w = q_norm_w;
+  a.k_w = k_norm_w;
+  a.rope_freqs = rope_freqs ? rope_freqs : q_norm_w;
+  a.theta = p.theta;
+  a.apply_divisor = p.apply_divisor;
+  a.eps = p.eps;
+  a.q_out = q_out;
+  a.kp = k_pool;
+  a.vp = v_pool;
+  a.page_table = page_table;
+  a.seq_lens = seq_lens;
+  a.page_size = p.page_size;
+  a.max_pages = p.max_pages;
+  a.num_pages = p.num_pages;
+  a.cap = p.max_seq_len;
+  hipLaunchKernelGGL(attn_prologue_kernel, dim3(p.num_q_heads + p.num_kv_heads, p.num_seqs), dim3(NT), 0,
+                     ctx->stream, a);
+  G4_LAUNCHED(ctx, "attn_prologue");
+  return G4_OK;
 }
 
 int g4_pagedKvStore(g4_ctx* ctx, const float* k_in, const float* v_in, uint16_t* k_pool, uint16_t* v_pool,

@@ -1,57 +1,89 @@
-// k_batch.hip — quantized matmul for several activation vectors (ragged
+// k_batch.hip — quantized matmul for many activation vectors (ragged
 // multi-sequence decode) on the gfx950 matrix cores.
 //
-// Y[v][m] = sum_k W[m,k] X[v][k] for B vectors (src/engine.ts runs the
+// Y[v][m] = sum_k W[m,k] X[v][k] for B <= 64 vectors (src/engine.ts runs the
 // per-token matmulQuant of shaders/matmul_quant.wgsl:21-54 once per sequence;
 // here one launch serves all sequences, so each weight byte is read once).
 //
-//  * quant_kernel turns the B activation vectors into two-digit int8 form
-//    (x ~= s * (256*hi + lo) per 32-element sub-block, s = max|x| / 32512),
-//    optionally after RMSNorm or residual-add + RMSNorm, into the context
-//    scratch buffer. Layout: for sub-block sb, vector v and 8-element group q,
-//    16 bytes [hi x8][lo x8] at ((sb*Bp + v)*4 + q)*16; (s, sum) as a float2
-//    at [sb*Bp + v]. Bp = 16, 32 or 64 (the MFMA column tiles of a launch).
-//  * mm_kernel: a workgroup owns 16 rows; its waves split K by whole
-//    super-blocks. Per 32-element sub-block a wave runs
-//    v_mfma_i32_16x16x32_i8 with A = 16 rows x 32 weight codes and B = 32
-//    digits x 16 vectors (once for hi, once for lo), so the integer products
-//    are exact and the sub-block's scales are applied once per output in
-//    f32. Q6_K's two 16-element runs of a sub-block sit in lane groups {0,1}
-//    and {2,3} of the A operand; two MFMAs with the other half zeroed give
-//    each run its own scale. Wave partials meet in LDS.
+//  * mmf_kernel: a workgroup (4 waves) owns 64 rows (16 per wave) and a chunk
+//    of kc super-blocks (256 k each). For each super-block it reads the f32
+//    activations of all vectors and builds the MFMA operands in LDS, shared
+//    by the four waves: x * 2^e as an f16 pair x_hi + x_lo (2^e a power of
+//    two that puts the vector's largest |x| in the super-block in
+//    [2^13, 2^14)) and the 32-element sub-block sums as three f16 parts (for
+//    the Q4_K min term).
+//  * The sub-block scale is folded into the weight operand: each lane turns
+//    its 8 weight codes c into f16 sc * q with one byte permutation and one
+//    or two packed f16 operations per pair (c | 0x6400 is the f16 1024 + c),
+//    exact for Q4_K (sc * q <= 945) and for Q6_K whenever |sc * q| <= 2048
+//    (larger products round once, relative error <= 2^-12).
+//    v_mfma_f32_16x16x32_f16 against x_hi and x_lo accumulates a whole
+//    super-block in the matrix core; the row's d (for Q4_K also dmin times
+//    the min-term MFMA) and the vector's 2^-e are applied once per
+//    super-block in f32. The next super-block's activations and weights are
+//    in flight while the current one is multiplied.
+//  * Matrices too small to fill the chip split K into ksplit chunks. Each
+//    chunk's products land as partial sums [ksplit][B][M]; whoever reads them
+//    next (bprep_kernel, reduce_kernel or the attention prologue) adds the
+//    chunks in order, so results do not depend on timing and no workgroup
+//    waits for another.
+//  * The gate/up pair form gives each workgroup 32 rows of both matrices and
+//    writes gelu(gate) * up.
+//  * bprep_kernel applies RMSNorm or residual-add + RMSNorm per vector to the
+//    (summed) input of a matmul.
 #include "g4_internal.hpp"
 
 namespace {
 
-constexpr float XQ = 32512.0f;  // |v| <= 32512 keeps both digits in [-128, 127]
-constexpr int QNT = 256;        // quant_kernel threads
-
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x3a __attribute__((ext_vector_type(3), aligned(4)));
-typedef int int4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // native vector: stays in registers
+
+constexpr int PNT = 256;   // prep threads
+constexpr int MNT = 256;   // matmul threads (4 waves)
+constexpr int PMAX = 12;   // partials added per pass of the prep loads
 
 // Vectors are padded to the 16, 32 or 64 columns of the MFMA tiles a launch uses.
 __host__ __device__ constexpr uint32_t pad_batch(uint32_t b) { return b <= 16 ? 16 : (b <= 32 ? 32 : 64); }
 
-struct DigitBuf {
-  uint8_t* dq;  // [K/32][Bp][4][16] hi/lo bytes
-  float2* ds;   // [K/32][Bp] (scale, sum)
-  uint32_t Bp;
+// LDS operand block of one super-block for NTV tiles of 16 vectors:
+//   main  [t][s][h][lane] 16 B: f16 x 8 of vector 16t + lane%16 at
+//         k = 32s + 8(lane/16) .. +7; h = 0: x_hi, 1: x_lo
+//   sums  [t][lane] 16 B: f16 slots 8(lane/16) .. +7 of vector 16t + lane%16;
+//         slot j is part j%4 of the sum over sub-block j/4 of x * 2^(e-6)
+//         (parts 0..2, part 3 zero)
+//   scale [t][16] f32: 2^-e per vector
+struct Ops {
+  static constexpr uint32_t MAIN_T = 8 * 2 * 1024;
+  __host__ __device__ static constexpr uint32_t sums_off(int ntv) { return (uint32_t)ntv * MAIN_T; }
+  __host__ __device__ static constexpr uint32_t scale_off(int ntv) { return (uint32_t)ntv * (MAIN_T + 1024); }
+  __host__ __device__ static constexpr uint32_t bytes(int ntv) { return (uint32_t)ntv * (MAIN_T + 1024 + 64); }
 };
 
-__host__ inline size_t digit_bytes(uint32_t K, uint32_t Bp) {
-  return (size_t)2 * K * Bp + (size_t)(K / 32) * Bp * sizeof(float2);
+__device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
+  h2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
-// Prologue modes (as the one-vector matvec): 0 = x; 1 = x * w1 / rms(x);
-// 2 = h = residual + x * w1 / rms(x) (written to h_out), x' = h * w2 / rms(h).
-struct QuantArgs {
-  const float* x;  // [B][K]
+// ---------------------------------------------------------------------------
+// per-vector prologue: out = x' where x = sum of the nparts partials and
+//   PRO 0: x' = x;  PRO 1: x' = x * w1 / rms(x);
+//   PRO 2: h = residual + x * w1 / rms(x) (written to h_out), x' = h * w2 / rms(h)
+// (src/engine.ts:1545 rmsNorm, :1606-1607 fusedNormAdd + rmsNorm)
+// ---------------------------------------------------------------------------
+struct BPrepArgs {
+  const float* x;  // [nparts][B][K]
+  uint32_t nparts;
+  uint32_t B;
   const uint16_t* w1;
   const float* residual;  // [B][K]
   const uint16_t* w2;
   float* h_out;  // [B][K]
+  float* out;    // [B][K]
   float eps;
-  DigitBuf d;
 };
 
 __device__ __forceinline__ float4 mulw(float4 x, uint2 w, float s) {
@@ -59,20 +91,25 @@ __device__ __forceinline__ float4 mulw(float4 x, uint2 w, float s) {
                      x.z * g4d::f16_bits_to_f32(w.y & 0xffffu) * s, x.w * g4d::f16_bits_to_f32(w.y >> 16) * s);
 }
 __device__ __forceinline__ float sq4(float4 v) { return (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w); }
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
 
-// One workgroup per vector; thread t holds the float4 at element 4t + 1024p.
+// One workgroup per vector; thread t holds the float4s at 4t + 1024p. The
+// partials are read PMAX at a time, all loads of a pass issued together.
 template <int BPR, int PRO>
-__global__ __launch_bounds__(QNT) void quant_kernel(QuantArgs a) {
+__global__ __launch_bounds__(PNT) void bprep_kernel(BPrepArgs a) {
   constexpr int K = BPR * 256;
-  constexpr int XP = (K + 4 * QNT - 1) / (4 * QNT);
-  __shared__ float red[2 * (QNT / 64)];
+  constexpr int XP = (K + 4 * PNT - 1) / (4 * PNT);
+  __shared__ float red[2 * (PNT / 64)];
   const uint32_t v = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const size_t vstride = (size_t)a.B * K;
   float4 x[XP], r[PRO == 2 ? XP : 1];
   uint2 w1[PRO >= 1 ? XP : 1], w2[PRO == 2 ? XP : 1];
 #pragma unroll
-  for (int p = 0; p < XP; ++p) {  // unconditional loads at clamped offsets
-    const int f = 4 * tid + 4 * QNT * p, fc = f < K ? f : 0;
+  for (int p = 0; p < XP; ++p) {
+    const int f = 4 * tid + 4 * PNT * p, fc = f < K ? f : 0;
     x[p] = *(const float4*)(a.x + (size_t)v * K + fc);
     if constexpr (PRO >= 1) w1[p] = *(const uint2*)(a.w1 + fc);
     if constexpr (PRO == 2) {
@@ -80,16 +117,33 @@ __global__ __launch_bounds__(QNT) void quant_kernel(QuantArgs a) {
       w2[p] = *(const uint2*)(a.w2 + fc);
     }
   }
+  for (uint32_t c0 = 1; c0 < a.nparts; c0 += PMAX) {  // chunks 1.. in order
+    float4 t[PMAX][XP];
+#pragma unroll
+    for (int i = 0; i < PMAX; ++i) {
+      const uint32_t c = min(c0 + i, a.nparts - 1);
+#pragma unroll
+      for (int p = 0; p < XP; ++p) {
+        const int f = 4 * tid + 4 * PNT * p, fc = f < K ? f : 0;
+        t[i][p] = *(const float4*)(a.x + c * vstride + (size_t)v * K + fc);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PMAX; ++i)
+      if (c0 + i < a.nparts)
+#pragma unroll
+        for (int p = 0; p < XP; ++p) x[p] = add4(x[p], t[i][p]);
+  }
   if constexpr (PRO >= 1) {
     float ss = 0.f;
 #pragma unroll
-    for (int p = 0; p < XP; ++p) ss += (4 * tid + 4 * QNT * p < K) ? sq4(x[p]) : 0.f;
+    for (int p = 0; p < XP; ++p) ss += (4 * tid + 4 * PNT * p < K) ? sq4(x[p]) : 0.f;
     ss = g4d::wave_sum_dpp(ss);
-    if (lane == 0) red[tid >> 6] = ss;
+    if (lane == 0) red[w] = ss;
     __syncthreads();
     float t1 = 0.f;
 #pragma unroll
-    for (int i = 0; i < QNT / 64; ++i) t1 += red[i];
+    for (int i = 0; i < PNT / 64; ++i) t1 += red[i];
     const float inv1 = 1.0f / sqrtf(t1 / (float)K + a.eps);
     if constexpr (PRO == 1) {
 #pragma unroll
@@ -98,18 +152,17 @@ __global__ __launch_bounds__(QNT) void quant_kernel(QuantArgs a) {
       float ss2 = 0.f;
 #pragma unroll
       for (int p = 0; p < XP; ++p) {
-        const int f = 4 * tid + 4 * QNT * p;
-        const float4 t = mulw(x[p], w1[p], inv1);
-        x[p] = make_float4(r[p].x + t.x, r[p].y + t.y, r[p].z + t.z, r[p].w + t.w);
+        const int f = 4 * tid + 4 * PNT * p;
+        x[p] = add4(r[p], mulw(x[p], w1[p], inv1));
         ss2 += f < K ? sq4(x[p]) : 0.f;
         if (a.h_out && f < K) *(float4*)(a.h_out + (size_t)v * K + f) = x[p];
       }
       ss2 = g4d::wave_sum_dpp(ss2);
-      if (lane == 0) red[QNT / 64 + (tid >> 6)] = ss2;
+      if (lane == 0) red[PNT / 64 + w] = ss2;
       __syncthreads();
       float t2 = 0.f;
 #pragma unroll
-      for (int i = 0; i < QNT / 64; ++i) t2 += red[QNT / 64 + i];
+      for (int i = 0; i < PNT / 64; ++i) t2 += red[PNT / 64 + i];
       const float inv2 = 1.0f / sqrtf(t2 / (float)K + a.eps);
 #pragma unroll
       for (int p = 0; p < XP; ++p) x[p] = mulw(x[p], w2[p], inv2);
@@ -117,31 +170,20 @@ __global__ __launch_bounds__(QNT) void quant_kernel(QuantArgs a) {
   }
 #pragma unroll
   for (int p = 0; p < XP; ++p) {
-    const int f = 4 * tid + 4 * QNT * p;
-    const float4 xv = x[p];
-    float am = fmaxf(fmaxf(fabsf(xv.x), fabsf(xv.y)), fmaxf(fabsf(xv.z), fabsf(xv.w)));
-    float sm = (xv.x + xv.y) + (xv.z + xv.w);
-    am = g4d::max8(am);
-    sm = g4d::sum8(sm);
-    const float inv = am > 0.f ? XQ / am : 0.f;
-    const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
-    uint32_t ph = 0, pl = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int q = (int)__builtin_rintf(xs[e] * inv);
-      const int lo = ((q + 128) & 255) - 128;
-      const int hi = (q - lo) >> 8;
-      ph |= (uint32_t)(hi & 255) << (8 * e);
-      pl |= (uint32_t)(lo & 255) << (8 * e);
-    }
-    if (f < K) {
-      const uint32_t sb = (uint32_t)f / 32, e = (uint32_t)f % 32;
-      uint8_t* dst = a.d.dq + (((size_t)sb * a.d.Bp + v) * 4 + e / 8) * 16 + (e % 8);
-      *(uint32_t*)dst = ph;
-      *(uint32_t*)(dst + 8) = pl;
-      if ((lane & 7) == 0) a.d.ds[(size_t)sb * a.d.Bp + v] = make_float2(am * (1.0f / XQ), sm);
-    }
+    const int f = 4 * tid + 4 * PNT * p;
+    if (f < K) *(float4*)(a.out + (size_t)v * K + f) = x[p];
   }
+}
+
+// Y[v][m] = epilogue(sum_c part[c][v][m]) for a split-K matmul (in chunk order).
+__global__ __launch_bounds__(PNT) void reduce_kernel(const float* part, float* Y, uint32_t n, uint32_t nparts,
+                                                     float cap) {
+  const uint32_t i = blockIdx.x * PNT + threadIdx.x;
+  if (i >= n) return;
+  float y = part[i];
+  for (uint32_t c = 1; c < nparts; ++c) y += part[(size_t)c * n + i];
+  if (cap > 0.f) y = tanhf(fminf(fmaxf(y / cap, -15.0f), 15.0f)) * cap;
+  Y[i] = y;
 }
 
 // ---------------------------------------------------------------------------
@@ -149,30 +191,24 @@ __global__ __launch_bounds__(QNT) void quant_kernel(QuantArgs a) {
 // ---------------------------------------------------------------------------
 
 template <int QT>
-struct MmBlock;
-template <> struct MmBlock<0> { static constexpr int BYTES = 144; };
-template <> struct MmBlock<1> { static constexpr int BYTES = 210; };
-
-// Super-blocks per wave and waves per workgroup for a row of BPR blocks.
-template <int BPR>
-struct MmGeom {
-  static constexpr int BPW = (BPR + 15) / 16;
-  static constexpr int NWK = BPR / BPW;
-  static_assert(NWK * BPW == BPR && NWK <= 16, "whole blocks per wave");
-};
+struct Blk;
+template <> struct Blk<0> { static constexpr int BYTES = 144; };
+template <> struct Blk<1> { static constexpr int BYTES = 210; };
 
 struct MmSeg {
   const uint8_t* W;
-  float* Y;  // [B][M]
+  float* Y;  // ksplit == 1: [B][M]; else the partials [ksplit][B][M]
   uint32_t M;
-  uint32_t wg_begin;
+  uint32_t g_begin;  // first row group of the segment
 };
 struct MmArgs {
   MmSeg s[4];
   int n;
   uint32_t B;
-  float cap;  // softcap when > 0
-  DigitBuf d;
+  float cap;       // softcap when > 0 (ksplit == 1)
+  const float* x;  // [B][K] activations
+  uint32_t K;
+  uint32_t ksplit, kc;  // K in ksplit chunks of kc super-blocks
 };
 
 // 8 bytes at a 2-byte aligned address: three aligned dwords, funnel-shifted.
@@ -183,211 +219,356 @@ __device__ __forceinline__ uint2 ld8_a2(const uint8_t* p) {
   return make_uint2(__builtin_amdgcn_alignbyte(w.y, w.x, sh), __builtin_amdgcn_alignbyte(w.z, w.y, sh));
 }
 
-__device__ __forceinline__ long as_long(uint2 v) { return (long)(((uint64_t)v.y << 32) | v.x); }
+// Weight registers of one 16-row tile and super-block. A side (row lane%16,
+// k-group q = lane/16): codes and sub-block scales; D side (rows 4q + i): d
+// (Q4_K: d | dmin << 16).
+template <int QT>
+struct WRegs;
+template <> struct WRegs<0> {
+  uint2 qs[4];
+  uint4 hdr;
+  uint32_t dd[4];
+};
+template <> struct WRegs<1> {
+  uint2 ql[4], qh[2];
+  uint4 sc;
+  uint32_t dd[4];
+};
 
-// Q6_K codes minus 32 as signed bytes: c in [0,63] -> c - 32 in two's complement.
-__device__ __forceinline__ uint32_t q6_signed(uint32_t c) {
-  const uint32_t t = c ^ 0x20202020u;
-  const uint32_t neg = t & 0x20202020u;  // bit 5 set <=> c < 32
-  return t | (neg << 1) | (neg << 2);
+template <int BPR>
+__device__ __forceinline__ void load_w(WRegs<0>& r, const uint8_t* W, uint32_t M, uint32_t rbase, uint32_t kb,
+                                       int l) {
+  constexpr int BY = 144;
+  const int q = l >> 4;
+  const uint32_t ra = min(rbase + (uint32_t)(l & 15), M - 1);
+  const uint8_t* blk = W + ((size_t)ra * BPR + kb) * BY;
+  r.hdr = *(const uint4*)blk;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) r.qs[g] = *(const uint2*)(blk + 16 + 32 * g + 8 * q);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t rd = min(rbase + 4u * q + i, M - 1);
+    r.dd[i] = *(const uint32_t*)(W + ((size_t)rd * BPR + kb) * BY);
+  }
 }
 
-template <int QT, int BPR, int NTV>
-__global__ __launch_bounds__(64 * MmGeom<BPR>::NWK) void mm_kernel(MmArgs a) {
-  using Gm = MmGeom<BPR>;
-  constexpr int BPW = Gm::BPW, NWK = Gm::NWK, BY = MmBlock<QT>::BYTES;
-  constexpr int SBW = 8 * BPW;  // sub-blocks per wave
-  __shared__ float part[NWK][16][16 * NTV];
-
-  int si = 0;
+template <int BPR>
+__device__ __forceinline__ void load_w(WRegs<1>& r, const uint8_t* W, uint32_t M, uint32_t rbase, uint32_t kb,
+                                       int l) {
+  constexpr int BY = 210;
+  const int q = l >> 4;
+  const uint32_t ra = min(rbase + (uint32_t)(l & 15), M - 1);
+  const uint8_t* blk = W + ((size_t)ra * BPR + kb) * BY;
 #pragma unroll
-  for (int i = 1; i < 4; ++i)
-    if (i < a.n && blockIdx.x >= a.s[i].wg_begin) si = i;
-  const MmSeg sg = a.s[si];
-  const uint32_t row0 = (blockIdx.x - sg.wg_begin) * 16;
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int ra = l & 15, qa = l >> 4;   // A row / C column, k-group
-  const uint32_t arow = min(row0 + (uint32_t)ra, sg.M - 1);
-  const uint32_t b0 = (uint32_t)w * BPW;  // first super-block of this wave
-  const uint8_t* wa = sg.W + ((size_t)arow * BPR + b0) * BY;
-  const uint32_t Bp = a.d.Bp;
-
-  // ---- every load of this wave, issued first ----
-  // A-side weight pieces (row arow, group qa)
-  uint2 qs[BPW][QT == 0 ? 4 : 6];
-#pragma unroll
-  for (int i = 0; i < BPW; ++i) {
-    const uint8_t* blk = wa + (size_t)i * BY;
-    if constexpr (QT == 0) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) qs[i][g] = *(const uint2*)(blk + 16 + 32 * g + 8 * qa);
-    } else {
-      // ql[64h + 32c + 8qa..+8] (c = k' & 1) and qh[32h + 8qa..+8]
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        qs[i][2 * h] = ld8_a2(blk + 64 * h + 8 * qa);
-        qs[i][2 * h + 1] = ld8_a2(blk + 64 * h + 32 + 8 * qa);
-        qs[i][4 + h] = ld8_a2(blk + 128 + 32 * h + 8 * qa);
-      }
-    }
+  for (int h = 0; h < 2; ++h) {
+    r.ql[2 * h] = ld8_a2(blk + 64 * h + 8 * q);
+    r.ql[2 * h + 1] = ld8_a2(blk + 64 * h + 32 + 8 * q);
+    r.qh[h] = ld8_a2(blk + 128 + 32 * h + 8 * q);
   }
-  // C-side scale data of rows row0 + 4qa + r
-  uint4 hd[BPW][4];  // Q4_K: header; Q6_K: sc[16] as 4 dwords (x..w)
-  uint32_t dq6[BPW][4];
+  // sc[16] at bytes 192..207 from aligned dwords inside the 210-byte block:
+  // four from the dword holding byte 192 and a fifth (bytes 206..209) that is
+  // only needed when the block is 2 mod 4
+  const uintptr_t ad = (uintptr_t)(blk + 192);
+  const uint32_t sh = (uint32_t)(ad & 3);
+  const uint32_t* p4 = (const uint32_t*)(blk + 192 - sh);
+  const uint32_t x0 = p4[0], x1 = p4[1], x2 = p4[2], x3 = p4[3];
+  const uint32_t x4 = *(const uint32_t*)((const uint8_t*)p4 + 12 + 2 * sh);
+  r.sc = make_uint4(__builtin_amdgcn_alignbyte(x1, x0, sh), __builtin_amdgcn_alignbyte(x2, x1, sh),
+                    __builtin_amdgcn_alignbyte(x3, x2, sh), __builtin_amdgcn_alignbyte(x4, x3, sh));
 #pragma unroll
-  for (int i = 0; i < BPW; ++i)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const uint32_t crow = min(row0 + 4 * qa + r, sg.M - 1);
-      const uint8_t* blk = sg.W + ((size_t)crow * BPR + b0 + i) * BY;
-      if constexpr (QT == 0) {
-        hd[i][r] = *(const uint4*)blk;
-      } else {
-        // sc[16] at bytes 192..207 from aligned dwords that stay inside the
-        // 210-byte block: four from the dword holding byte 192, and a fifth
-        // only needed (and only read past them) when the block is 2 mod 4
-        const uintptr_t ad = (uintptr_t)(blk + 192);
-        const uint32_t sh = (uint32_t)(ad & 3);
-        const uint32_t* p4 = (const uint32_t*)(blk + 192 - sh);
-        const uint32_t x0 = p4[0], x1 = p4[1], x2 = p4[2], x3 = p4[3];
-        const uint32_t x4 = *(const uint32_t*)((const uint8_t*)p4 + 12 + 2 * sh);  // +16 when sh == 2
-        hd[i][r] = make_uint4(__builtin_amdgcn_alignbyte(x1, x0, sh), __builtin_amdgcn_alignbyte(x2, x1, sh),
-                              __builtin_amdgcn_alignbyte(x3, x2, sh), __builtin_amdgcn_alignbyte(x4, x3, sh));
-        dq6[i][r] = *(const uint16_t*)(blk + 208);
-      }
-    }
-  // B-side digits and scales of this wave's sub-blocks
-  uint4 dg[SBW][NTV];
-  float2 sc2[SBW][NTV];
-#pragma unroll
-  for (int s = 0; s < SBW; ++s)
-#pragma unroll
-    for (int t = 0; t < NTV; ++t) {
-      const size_t sb = (size_t)b0 * 8 + s;
-      dg[s][t] = *(const uint4*)(a.d.dq + ((sb * Bp + 16 * t + ra) * 4 + qa) * 16);
-      sc2[s][t] = a.d.ds[sb * Bp + 16 * t + ra];
-    }
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t rd = min(rbase + 4u * q + i, M - 1);
+    r.dd[i] = *(const uint16_t*)(W + ((size_t)rd * BPR + kb) * BY + 208);
+  }
+}
 
-  // ---- sub-block products ----
-  float acc[NTV][4];
-#pragma unroll
-  for (int t = 0; t < NTV; ++t)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[t][r] = 0.f;
+// f16 pairs (1024 + b_i, 1024 + b_j) from two bytes of `codes`: v_perm_b32
+// takes selector bytes 0-3 from its second operand and 4-7 from its first.
+__device__ __forceinline__ h2 biased_pair(uint32_t codes, uint32_t sel) {
+  return __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, codes, sel));
+}
+constexpr uint32_t kSel01 = 0x04010400u, kSel23 = 0x04030402u;
 
+__device__ __forceinline__ h8 cat(h2 a, h2 b, h2 c, h2 d) { return h8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y}; }
+
+// Q4_K 6-bit scale and min of sub-block j (src/gguf.ts:175-182).
+__device__ __forceinline__ void q4k_sc_mn(const uint4& hdr, int j, uint32_t& sc, uint32_t& mn) {
+  const int sh = 8 * (j & 3);
+  if (j < 4) {
+    sc = (hdr.y >> sh) & 63u;
+    mn = (hdr.z >> sh) & 63u;
+  } else {
+    sc = ((hdr.w >> sh) & 15u) | (((hdr.y >> sh) >> 6 & 3u) << 4);
+    mn = ((hdr.w >> sh) >> 4 & 15u) | (((hdr.z >> sh) >> 6 & 3u) << 4);
+  }
+}
+
+// Weight operand of sub-block s: 8 f16 values sc * q of row lane%16, k = 8q .. 8q+7.
+__device__ __forceinline__ h8 a_operand(const WRegs<0>& r, int s, int) {
+  const uint2 raw = r.qs[s >> 1];
+  const uint32_t c0 = (s & 1) ? (raw.x >> 4) & 0x0f0f0f0fu : raw.x & 0x0f0f0f0fu;
+  const uint32_t c1 = (s & 1) ? (raw.y >> 4) & 0x0f0f0f0fu : raw.y & 0x0f0f0f0fu;
+  uint32_t sc, mn;
+  q4k_sc_mn(r.hdr, s, sc, mn);
+  const _Float16 f = (_Float16)(float)sc;
+  const _Float16 fb = (_Float16)(-1024.0f * (float)sc);  // exact: sc <= 63
+  const h2 mul = {f, f}, bias = {fb, fb};
+  // (1024 + c) * sc - 1024 * sc = c * sc, one rounding of an exact value
+  return cat(__builtin_elementwise_fma(biased_pair(c0, kSel01), mul, bias),
+             __builtin_elementwise_fma(biased_pair(c0, kSel23), mul, bias),
+             __builtin_elementwise_fma(biased_pair(c1, kSel01), mul, bias),
+             __builtin_elementwise_fma(biased_pair(c1, kSel23), mul, bias));
+}
+
+// Q6_K sub-block s: half h = s/4, run pair k' = s%4 (src/gguf.ts:344-361);
+// this lane's 8 codes lie in run q/2 of the sub-block.
+__device__ __forceinline__ h8 a_operand(const WRegs<1>& r, int s, int q) {
+  const int h = s >> 2, kp = s & 3;
+  const uint2 ql = r.ql[2 * h + (kp & 1)];
+  const uint2 qh = r.qh[h];
+  const uint32_t lo0 = kp < 2 ? (ql.x & 0x0f0f0f0fu) : ((ql.x >> 4) & 0x0f0f0f0fu);
+  const uint32_t lo1 = kp < 2 ? (ql.y & 0x0f0f0f0fu) : ((ql.y >> 4) & 0x0f0f0f0fu);
+  const uint32_t c0 = lo0 | (((qh.x >> (2 * kp)) & 0x03030303u) << 4);
+  const uint32_t c1 = lo1 | (((qh.y >> (2 * kp)) & 0x03030303u) << 4);
+  const int is = 8 * h + 2 * kp + (q >> 1);
+  const uint32_t wd = (is < 4) ? r.sc.x : (is < 8) ? r.sc.y : (is < 12) ? r.sc.z : r.sc.w;
+  const int scv = (int)(int8_t)((wd >> (8 * (is & 3))) & 0xffu);
+  const _Float16 f = (_Float16)(float)scv;
+  const h2 mul = {f, f};
+  const h2 off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+  // (1024 + c) - 1056 = c - 32 exactly, then one rounding of (c - 32) * sc
+  return cat((biased_pair(c0, kSel01) + off) * mul, (biased_pair(c0, kSel23) + off) * mul,
+             (biased_pair(c1, kSel01) + off) * mul, (biased_pair(c1, kSel23) + off) * mul);
+}
+
+// Min operand of a Q4_K super-block: slots 8q .. 8q+3 hold the min of
+// sub-block 2q, slots 8q+4 .. +7 that of sub-block 2q+1.
+__device__ __forceinline__ h8 min_operand(const WRegs<0>& r, int q) {
+  uint32_t sc0, m0, sc1, m1;
+  q4k_sc_mn(r.hdr, 2 * q, sc0, m0);
+  q4k_sc_mn(r.hdr, 2 * q + 1, sc1, m1);
+  const _Float16 a = (_Float16)(float)m0, b = (_Float16)(float)m1;
+  return h8{a, a, a, a, b, b, b, b};
+}
+
+// Activations of one super-block: item (v, s) = vector v, sub-block s,
+// item = tid + MNT * u, v = item / 8, s = item % 8; 8 float4 per item.
+template <int NTV>
+struct Raw {
+  static constexpr int IPT = NTV >= 2 ? NTV / 2 : 1;  // items per thread (Bp * 8 / MNT, at least 1)
+  float4 x[IPT][8];
+};
+
+template <int NTV>
+__device__ __forceinline__ void raw_load(Raw<NTV>& r, const float* x, uint32_t B, uint32_t K, uint32_t kb, int tid) {
 #pragma unroll
-  for (int i = 0; i < BPW; ++i) {
-    float d[4], dm[4];
-    if constexpr (QT == 0) {
+  for (int u = 0; u < Raw<NTV>::IPT; ++u) {
+    const uint32_t it = (uint32_t)(tid + MNT * u), v = it >> 3, s = it & 7;
+    const uint32_t vc = v < B ? v : 0;  // padded vectors: read vector 0, zeroed at the store
+    const float4* src = (const float4*)(x + (size_t)vc * K + kb * 256 + 32 * s);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        d[r] = g4d::f16_bits_to_f32(hd[i][r].x & 0xffffu);
-        dm[r] = g4d::f16_bits_to_f32(hd[i][r].x >> 16);
-      }
-    } else {
+    for (int j = 0; j < 8; ++j) r.x[u][j] = src[j];
+  }
+}
+
+// Operand block of the super-block into LDS (see Ops).
+template <int NTV>
+__device__ __forceinline__ void raw_store(const Raw<NTV>& r, uint8_t* lds, uint32_t B, int tid) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) d[r] = g4d::f16_bits_to_f32(dq6[i][r]);
-    }
+  for (int u = 0; u < Raw<NTV>::IPT; ++u) {
+    const uint32_t it = (uint32_t)(tid + MNT * u), v = it >> 3, s = it & 7;
+    const bool live = v < B;
+    float xs[32];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int s = i * 8 + j;
-      if constexpr (QT == 0) {
-        // sub-block j = low (even j) or high (odd j) nibbles of qs group j/2
-        const uint2 raw = qs[i][j / 2];
-        const uint2 codes = (j & 1) ? make_uint2((raw.x >> 4) & 0x0f0f0f0fu, (raw.y >> 4) & 0x0f0f0f0fu)
-                                    : make_uint2(raw.x & 0x0f0f0f0fu, raw.y & 0x0f0f0f0fu);
-        const long av = as_long(codes);
-        float scr[4], mnr[4];
+      xs[4 * j] = live ? r.x[u][j].x : 0.f;
+      xs[4 * j + 1] = live ? r.x[u][j].y : 0.f;
+      xs[4 * j + 2] = live ? r.x[u][j].z : 0.f;
+      xs[4 * j + 3] = live ? r.x[u][j].w : 0.f;
+    }
+    float am = 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          // scale / min of sub-block j (src/gguf.ts:175-182)
-          const uint32_t S0 = hd[i][r].y, S1 = hd[i][r].z, S2 = hd[i][r].w;
-          const int sh = 8 * (j & 3);
-          uint32_t scv, mv;
-          if (j < 4) {
-            scv = (S0 >> sh) & 63u;
-            mv = (S1 >> sh) & 63u;
-          } else {
-            scv = ((S2 >> sh) & 15u) | (((S0 >> sh) >> 6 & 3u) << 4);
-            mv = ((S2 >> sh) >> 4 & 15u) | (((S1 >> sh) >> 6 & 3u) << 4);
-          }
-          scr[r] = d[r] * (float)scv;
-          mnr[r] = dm[r] * (float)mv;
-        }
+    for (int e = 0; e < 32; ++e) am = fmaxf(am, fabsf(xs[e]));
+    am = g4d::max8(am);  // the 8 sub-blocks of vector v sit in 8 consecutive lanes
+    int ex = 0;
+    (void)frexpf(am, &ex);
+    const int k = am > 0.f ? min(max(14 - ex, -120), 120) : 0;
+    const float sc = ldexpf(1.0f, k);
+    float sum = 0.f;
 #pragma unroll
-        for (int t = 0; t < NTV; ++t) {
-          const int4v z = {0, 0, 0, 0};
-          const int4v ch = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, as_long(make_uint2(dg[s][t].x, dg[s][t].y)), z,
-                                                                  0, 0, 0);
-          const int4v cl = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, as_long(make_uint2(dg[s][t].z, dg[s][t].w)), z,
-                                                                  0, 0, 0);
-          const float2 ss = sc2[s][t];
+    for (int e = 0; e < 32; ++e) {
+      xs[e] *= sc;
+      sum += xs[e];
+    }
+    if (v >= 16u * NTV) continue;  // items past the padded batch (NTV == 1 only)
+    const uint32_t t = v >> 4, c = v & 15;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int I = ch[r] * 256 + cl[r];
-            acc[t][r] += scr[r] * ss.x * (float)I - mnr[r] * ss.y;
-          }
-        }
-      } else {
-        // sub-block j: half h = j / 4, run pair k' = j % 4 (src/gguf.ts:344-361)
-        const int h = j / 4, kp = j % 4;
-        const uint2 ql = qs[i][2 * h + (kp & 1)];
-        const uint2 qh = qs[i][4 + h];
-        const uint32_t lo0 = kp < 2 ? (ql.x & 0x0f0f0f0fu) : ((ql.x >> 4) & 0x0f0f0f0fu);
-        const uint32_t lo1 = kp < 2 ? (ql.y & 0x0f0f0f0fu) : ((ql.y >> 4) & 0x0f0f0f0fu);
-        const uint32_t hb0 = ((qh.x >> (2 * kp)) & 0x03030303u) << 4;
-        const uint32_t hb1 = ((qh.y >> (2 * kp)) & 0x03030303u) << 4;
-        const uint2 codes = make_uint2(q6_signed(lo0 | hb0), q6_signed(lo1 | hb1));
-        const bool first = qa < 2;  // lanes of the sub-block's first 16-element run
-        const long a0 = first ? as_long(codes) : 0l;
-        const long a1 = first ? 0l : as_long(codes);
-        int sca[4], scb[4];
+    for (int q = 0; q < 4; ++q) {
+      uint32_t hw[4], lw[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          // sc[8h + 2k' + (0|1)] as signed bytes
-          const int is = 8 * h + 2 * kp;
-          const uint32_t wd = (is < 4) ? hd[i][r].x : (is < 8) ? hd[i][r].y : (is < 12) ? hd[i][r].z : hd[i][r].w;
-          sca[r] = (int)(int8_t)((wd >> (8 * (is & 3))) & 0xffu);
-          scb[r] = (int)(int8_t)((wd >> (8 * ((is + 1) & 3))) & 0xffu);
-        }
+      for (int e = 0; e < 4; ++e) {
+        const float a0 = xs[8 * q + 2 * e], a1 = xs[8 * q + 2 * e + 1];
+        const _Float16 h0 = (_Float16)a0, h1 = (_Float16)a1;
+        hw[e] = pack_h2(h0, h1);
+        lw[e] = pack_h2((_Float16)(a0 - (float)h0), (_Float16)(a1 - (float)h1));
+      }
+      uint8_t* slot = lds + t * Ops::MAIN_T + s * 2048 + (c + 16u * q) * 16;
+      *(u32x4*)slot = u32x4{hw[0], hw[1], hw[2], hw[3]};
+      *(u32x4*)(slot + 1024) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+    }
+    sum *= 0.015625f;  // * 2^-6
+    const _Float16 p0 = (_Float16)sum;
+    const float r1 = sum - (float)p0;
+    const _Float16 p1 = (_Float16)r1;
+    const _Float16 p2 = (_Float16)(r1 - (float)p1);
+    *(u32x2*)(lds + Ops::sums_off(NTV) + t * 1024 + (c + 16u * (s >> 1)) * 16 + (s & 1) * 8) =
+        u32x2{pack_h2(p0, p1), pack_h2(p2, (_Float16)0.f)};
+    if (s == 0) *(float*)(lds + Ops::scale_off(NTV) + t * 64 + c * 4) = ldexpf(1.0f, -k);
+  }
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {  // shaders/gelu_mul.wgsl:10-16
+  float t = 0.7978845608028654f * x * (1.0f + 0.044715f * x * x);
+  t = fminf(fmaxf(t, -15.0f), 15.0f);
+  return 0.5f * x * (1.0f + tanhf(t));
+}
+
+__device__ __forceinline__ float epilogue(float y, float cap) {
+  if (cap > 0.f) {
+    const float t = fminf(fmaxf(y / cap, -15.0f), 15.0f);
+    return tanhf(t) * cap;
+  }
+  return y;
+}
+
+// MODE 0: a row group is 64 rows of one segment. MODE 1 (gate/up): segments
+// 0 and 1 have the same rows; a row group is 32 rows of both, waves 0-1 gate,
+// waves 2-3 up, and the output (segment 0's Y) is gelu(gate) * up.
+template <int QT, int BPR, int NTV, int MODE>
+__global__ __launch_bounds__(MNT) void mmf_kernel(MmArgs a) {
+  __shared__ __align__(16) uint8_t lds[Ops::bytes(NTV)];
+
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q = l >> 4;
+  const uint32_t g = blockIdx.x / a.ksplit, chunk = blockIdx.x % a.ksplit;
+  int si = 0;
+  uint32_t rbase;
+  const uint8_t* W;
+  uint32_t M;
+  if constexpr (MODE == 0) {
 #pragma unroll
-        for (int t = 0; t < NTV; ++t) {
-          const int4v z = {0, 0, 0, 0};
-          const long bh = as_long(make_uint2(dg[s][t].x, dg[s][t].y));
-          const long bl = as_long(make_uint2(dg[s][t].z, dg[s][t].w));
-          const int4v ah = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bh, z, 0, 0, 0);
-          const int4v al = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bl, z, 0, 0, 0);
-          const int4v bh2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bh, z, 0, 0, 0);
-          const int4v bl2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bl, z, 0, 0, 0);
-          const float sx = sc2[s][t].x;
+    for (int i = 1; i < 4; ++i)
+      if (i < a.n && g >= a.s[i].g_begin) si = i;
+    W = a.s[si].W;
+    M = a.s[si].M;
+    rbase = (g - a.s[si].g_begin) * 64 + 16u * w;
+  } else {
+    W = a.s[w >> 1].W;
+    M = a.s[0].M;
+    rbase = g * 32 + 16u * (w & 1);
+  }
+  const uint32_t kb0 = chunk * a.kc;
+
+  Raw<NTV> raw;
+  WRegs<QT> wr, wn;
+  raw_load<NTV>(raw, a.x, a.B, a.K, kb0, tid);
+  load_w<BPR>(wr, W, M, rbase, kb0, l);
+  raw_store<NTV>(raw, lds, a.B, tid);
+  __syncthreads();
+
+  f4 acc[NTV];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int I = (ah[r] * 256 + al[r]) * sca[r] + (bh2[r] * 256 + bl2[r]) * scb[r];
-            acc[t][r] += d[r] * sx * (float)I;
-          }
+  for (int t = 0; t < NTV; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+  const u32x4* lv = (const u32x4*)lds;
+
+  for (uint32_t j = 0; j < a.kc; ++j) {
+    const bool more = j + 1 < a.kc;
+    const uint32_t kn = kb0 + j + (more ? 1u : 0u);
+    raw_load<NTV>(raw, a.x, a.B, a.K, kn, tid);  // the next block is in flight during this one
+    load_w<BPR>(wn, W, M, rbase, kn, l);
+
+    f4 C[NTV], Cm[NTV];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const h8 A = a_operand(wr, s, q);
+#pragma unroll
+      for (int t = 0; t < NTV; ++t) {
+        const u32x4 bh = lv[(t * Ops::MAIN_T + s * 2048) / 16 + l];
+        const u32x4 bl = lv[(t * Ops::MAIN_T + s * 2048 + 1024) / 16 + l];
+        const f4 z = s == 0 ? f4{0.f, 0.f, 0.f, 0.f} : C[t];
+        C[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bh), z, 0, 0, 0);
+        C[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bl), C[t], 0, 0, 0);
+      }
+    }
+    if constexpr (QT == 0) {
+      const h8 Am = min_operand(wr, q);
+#pragma unroll
+      for (int t = 0; t < NTV; ++t) {
+        const u32x4 bm = lv[(Ops::sums_off(NTV) + t * 1024) / 16 + l];
+        Cm[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Am, __builtin_bit_cast(h8, bm), f4{0.f, 0.f, 0.f, 0.f}, 0,
+                                                        0, 0);
+      }
+    }
+    const float* scl = (const float*)(lds + Ops::scale_off(NTV));
+#pragma unroll
+    for (int t = 0; t < NTV; ++t) {
+      const float fs = scl[t * 16 + (l & 15)];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (QT == 0) {
+          const float d = g4d::f16_bits_to_f32(wr.dd[i] & 0xffffu);
+          const float dm = g4d::f16_bits_to_f32(wr.dd[i] >> 16) * 64.0f;
+          acc[t][i] += fs * (d * C[t][i] - dm * Cm[t][i]);
+        } else {
+          acc[t][i] += fs * g4d::f16_bits_to_f32(wr.dd[i]) * C[t][i];
         }
       }
     }
+    __syncthreads();  // every wave is done with this block's operands
+    if (more) {
+      raw_store<NTV>(raw, lds, a.B, tid);
+      __syncthreads();
+    }
+    wr = wn;
   }
 
-  // ---- wave partials -> LDS -> rows ----
+  // ---- outputs: lane (q, c) holds rows rbase + 4q + i of vectors 16t + c ----
+  if constexpr (MODE == 1) {
+    // the up waves hand their sums to the gate waves through LDS
+    f4* xfer = (f4*)lds;
+    if (w >= 2) {
 #pragma unroll
-  for (int t = 0; t < NTV; ++t)
+      for (int t = 0; t < NTV; ++t) xfer[((w - 2) * NTV + t) * 64 + l] = acc[t];
+    }
+    __syncthreads();
+    if (w < 2) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) part[w][4 * qa + r][16 * t + ra] = acc[t][r];
-  __syncthreads();
-  for (int o = threadIdx.x; o < 16 * 16 * NTV; o += 64 * NWK) {
-    const int rr = o / (16 * NTV), vv = o % (16 * NTV);
-    float y = 0.f;
+      for (int t = 0; t < NTV; ++t) {
+        const f4 up = xfer[(w * NTV + t) * 64 + l];
+        const uint32_t v = 16u * t + (l & 15);
 #pragma unroll
-    for (int ww = 0; ww < NWK; ++ww) y += part[ww][rr][vv];
-    const uint32_t row = row0 + rr;
-    if (row < sg.M && (uint32_t)vv < a.B) {
-      if (a.cap > 0.f) {
-        const float t = fminf(fmaxf(y / a.cap, -15.0f), 15.0f);
-        y = tanhf(t) * a.cap;
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t row = rbase + 4u * q + i;
+          if (row < M && v < a.B) a.s[0].Y[(size_t)v * M + row] = gelu_tanh(acc[t][i]) * up[i];
+        }
       }
-      sg.Y[(size_t)vv * sg.M + row] = y;
+    }
+    return;
+  }
+  float* Y = a.s[si].Y + (size_t)chunk * a.B * M;
+  const float cap = a.ksplit == 1 ? a.cap : 0.f;
+#pragma unroll
+  for (int t = 0; t < NTV; ++t) {
+    const uint32_t v = 16u * t + (l & 15);
+    const uint32_t row = rbase + 4u * q;
+    if (v >= a.B) continue;
+    float* dst = Y + (size_t)v * M + row;
+    if ((M & 3) == 0 && row + 3 < M) {
+      *(f4*)dst = f4{epilogue(acc[t][0], cap), epilogue(acc[t][1], cap), epilogue(acc[t][2], cap),
+                     epilogue(acc[t][3], cap)};
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (row + i < M) dst[i] = epilogue(acc[t][i], cap);
     }
   }
 }
@@ -397,90 +578,177 @@ __global__ __launch_bounds__(64 * MmGeom<BPR>::NWK) void mm_kernel(MmArgs a) {
 // ---------------------------------------------------------------------------
 
 template <int BPR>
-int quant_bpr(g4_ctx* ctx, int pro, const QuantArgs& q, uint32_t B) {
-  const dim3 grid(B);
-  if (pro == 0) hipLaunchKernelGGL((quant_kernel<BPR, 0>), grid, dim3(QNT), 0, ctx->stream, q);
-  else if (pro == 1) hipLaunchKernelGGL((quant_kernel<BPR, 1>), grid, dim3(QNT), 0, ctx->stream, q);
-  else hipLaunchKernelGGL((quant_kernel<BPR, 2>), grid, dim3(QNT), 0, ctx->stream, q);
-  G4_LAUNCHED(ctx, "quant");
+int bprep_bpr(g4_ctx* ctx, int pro, const BPrepArgs& p) {
+  const dim3 grid(p.B);
+  if (pro == 0) hipLaunchKernelGGL((bprep_kernel<BPR, 0>), grid, dim3(PNT), 0, ctx->stream, p);
+  else if (pro == 1) hipLaunchKernelGGL((bprep_kernel<BPR, 1>), grid, dim3(PNT), 0, ctx->stream, p);
+  else hipLaunchKernelGGL((bprep_kernel<BPR, 2>), grid, dim3(PNT), 0, ctx->stream, p);
+  G4_LAUNCHED(ctx, "batch_prep");
   return G4_OK;
 }
 
-template <int QT, int BPR, int NTV>
-int mm_launch(g4_ctx* ctx, MmArgs& a) {
-  uint32_t wgs = 0;
-  for (int i = 0; i < a.n; ++i) {
-    a.s[i].wg_begin = wgs;
-    wgs += ceil_div(a.s[i].M, 16);
+int bprep_launch(g4_ctx* ctx, uint32_t N, int pro, const BPrepArgs& p) {
+  switch (N / 256) {
+    case 6: return bprep_bpr<6>(ctx, pro, p);
+    case 8: return bprep_bpr<8>(ctx, pro, p);
+    default: return G4_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((mm_kernel<QT, BPR, NTV>), dim3(wgs), dim3(64 * MmGeom<BPR>::NWK), 0, ctx->stream, a);
+}
+
+bool mm_supported(uint32_t bpr) {
+  return bpr == 4 || bpr == 6 || bpr == 8 || bpr == 12 || bpr == 16 || bpr == 24 || bpr == 32 || bpr == 48;
+}
+
+template <int QT, int BPR, int NTV, int MODE>
+int mm_launch(g4_ctx* ctx, const MmArgs& a, uint32_t groups) {
+  hipLaunchKernelGGL((mmf_kernel<QT, BPR, NTV, MODE>), dim3(groups * a.ksplit), dim3(MNT), 0, ctx->stream, a);
   G4_LAUNCHED(ctx, "mm");
   return G4_OK;
 }
 
-template <int QT, int BPR>
-int mm_ntv(g4_ctx* ctx, MmArgs& a) {  // Bp == 16 * NTV
-  if (a.d.Bp == 16) return mm_launch<QT, BPR, 1>(ctx, a);
-  if (a.d.Bp == 32) return mm_launch<QT, BPR, 2>(ctx, a);
-  return mm_launch<QT, BPR, 4>(ctx, a);
+template <int QT, int BPR, int MODE>
+int mm_ntv(g4_ctx* ctx, const MmArgs& a, uint32_t groups) {
+  const uint32_t Bp = pad_batch(a.B);
+  if (Bp == 16) return mm_launch<QT, BPR, 1, MODE>(ctx, a, groups);
+  if (Bp == 32) return mm_launch<QT, BPR, 2, MODE>(ctx, a, groups);
+  return mm_launch<QT, BPR, 4, MODE>(ctx, a, groups);
 }
-
-bool mm_supported(uint32_t bpr) { return bpr == 4 || bpr == 6 || bpr == 8 || bpr == 12 || bpr == 16 || bpr == 24 || bpr == 32 || bpr == 48; }
 
 template <int QT>
-int mm_bpr(g4_ctx* ctx, uint32_t N, MmArgs& a) {
+int mm_bpr(g4_ctx* ctx, uint32_t N, const MmArgs& a, uint32_t groups) {
   switch (N / 256) {
-    case 4: return mm_ntv<QT, 4>(ctx, a);
-    case 6: return mm_ntv<QT, 6>(ctx, a);
-    case 8: return mm_ntv<QT, 8>(ctx, a);
-    case 12: return mm_ntv<QT, 12>(ctx, a);
-    case 16: return mm_ntv<QT, 16>(ctx, a);
-    case 24: return mm_ntv<QT, 24>(ctx, a);
-    case 32: return mm_ntv<QT, 32>(ctx, a);
-    case 48: return mm_ntv<QT, 48>(ctx, a);
+    case 4: return mm_ntv<QT, 4, 0>(ctx, a, groups);
+    case 6: return mm_ntv<QT, 6, 0>(ctx, a, groups);
+    case 8: return mm_ntv<QT, 8, 0>(ctx, a, groups);
+    case 12: return mm_ntv<QT, 12, 0>(ctx, a, groups);
+    case 16: return mm_ntv<QT, 16, 0>(ctx, a, groups);
+    case 24: return mm_ntv<QT, 24, 0>(ctx, a, groups);
+    case 32: return mm_ntv<QT, 32, 0>(ctx, a, groups);
+    case 48: return mm_ntv<QT, 48, 0>(ctx, a, groups);
     default: return G4_ERR_UNSUPPORTED;
   }
 }
 
-int quant_launch(g4_ctx* ctx, uint32_t N, int pro, const QuantArgs& q, uint32_t B) {
-  switch (N / 256) {
-    case 4: return quant_bpr<4>(ctx, pro, q, B);
-    case 6: return quant_bpr<6>(ctx, pro, q, B);
-    case 8: return quant_bpr<8>(ctx, pro, q, B);
-    case 12: return quant_bpr<12>(ctx, 0, q, B);
-    case 16: return quant_bpr<16>(ctx, 0, q, B);
-    case 24: return quant_bpr<24>(ctx, 0, q, B);
-    case 32: return quant_bpr<32>(ctx, 0, q, B);
-    case 48: return quant_bpr<48>(ctx, 0, q, B);
-    default: return G4_ERR_UNSUPPORTED;
+// Smallest divisor of bpr (at most max_split) that gives about one workgroup per CU.
+uint32_t pick_ksplit(const g4_ctx* ctx, uint32_t groups, uint32_t bpr, uint32_t max_split) {
+  const uint32_t want = (uint32_t)(ctx->num_cus > 0 ? ctx->num_cus : 256) * 15 / 16;
+  uint32_t best = 1;
+  for (uint32_t d = 1; d <= bpr && d <= max_split; ++d) {
+    if (bpr % d) continue;
+    best = d;
+    if (groups * d >= want) break;
   }
+  return best;
 }
 
-// Digits of B vectors into the context scratch, then one matmul launch over
-// up to four matrices sharing the input.
-int batch_matmul(g4_ctx* ctx, const char* fn, int qt, int pro, const QuantArgs& q0, const uint8_t* const* W,
-                 float* const* Y, const uint32_t* rows, int nseg, uint32_t N, uint32_t B, float cap) {
+int check_x(const char* fn, const float* x, uint32_t N, uint32_t B) {
   G4_REQUIRE(B >= 1 && B <= 64, "%s: batch %u outside 1..64", fn, B);
   G4_REQUIRE(N % 256 == 0 && mm_supported(N / 256), "%s: N=%u unsupported", fn, N);
-  G4_REQUIRE(pro == 0 || N == 1536 || N == 2048, "%s: normalising prologue needs N 1536 or 2048", fn);
-  const uint32_t Bp = pad_batch(B);
-  void* scratch = nullptr;
-  int rc = g4_internal_scratch(ctx, digit_bytes(N, Bp), &scratch);
-  if (rc) return rc;
-  QuantArgs q = q0;
-  q.d.dq = (uint8_t*)scratch;
-  q.d.ds = (float2*)((uint8_t*)scratch + (size_t)2 * N * Bp);
-  q.d.Bp = Bp;
-  rc = quant_launch(ctx, N, pro, q, B);
-  if (rc) return rc;
+  G4_REQUIRE(x && ((uintptr_t)x & 15) == 0, "%s: activations must be non-null and 16-byte aligned", fn);
+  return G4_OK;
+}
+
+// One matmul launch over up to four matrices sharing the input x [B][N] (or
+// the gate/up pair). ksplit > 1 leaves partial sums in Y[i] [ksplit][B][rows[i]].
+int mm_run(g4_ctx* ctx, const char* fn, int qt, const float* x, const uint8_t* const* W, float* const* Y,
+           const uint32_t* rows, int nseg, uint32_t N, uint32_t B, float cap, bool gelu, uint32_t ksplit) {
+  const uint32_t bpr = N / 256;
+  uint32_t groups = 0;
   MmArgs a{};
-  for (int i = 0; i < nseg; ++i) a.s[i] = MmSeg{W[i], Y[i], rows[i], 0};
+  for (int i = 0; i < nseg; ++i) {
+    a.s[i] = MmSeg{W[i], Y[i], rows[i], groups};
+    if (!gelu) groups += ceil_div(rows[i], 64);
+  }
+  if (gelu) groups = ceil_div(rows[0], 32);
   a.n = nseg;
   a.B = B;
   a.cap = cap;
-  a.d = q.d;
-  rc = qt == 0 ? mm_bpr<0>(ctx, N, a) : mm_bpr<1>(ctx, N, a);
+  a.x = x;
+  a.K = N;
+  a.ksplit = ksplit;
+  a.kc = bpr / ksplit;
+  int rc;
+  if (gelu) {
+    switch (bpr) {
+      case 6: rc = mm_ntv<0, 6, 1>(ctx, a, groups); break;
+      case 8: rc = mm_ntv<0, 8, 1>(ctx, a, groups); break;
+      default: rc = G4_ERR_UNSUPPORTED;
+    }
+  } else {
+    rc = qt == 0 ? mm_bpr<0>(ctx, N, a, groups) : mm_bpr<1>(ctx, N, a, groups);
+  }
   return rc == G4_ERR_UNSUPPORTED ? g4::set_error(rc, "%s: unsupported shape", fn) : rc;
+}
+
+uint32_t total_groups(const uint32_t* rows, int nseg) {
+  uint32_t g = 0;
+  for (int i = 0; i < nseg; ++i) g += ceil_div(rows[i], 64);
+  return g;
+}
+
+// Complete products: [prologue ->] matmul [-> ordered reduction], all
+// intermediates in the context scratch.
+int batch_matmul(g4_ctx* ctx, const char* fn, int qt, int pro, const BPrepArgs& p0, const uint8_t* const* W,
+                 float* const* Y, const uint32_t* rows, int nseg, uint32_t N, uint32_t B, float cap, bool gelu) {
+  int rc = check_x(fn, p0.x, N, B);
+  if (rc) return rc;
+  G4_REQUIRE(pro == 0 || N == 1536 || N == 2048, "%s: normalising prologue needs N 1536 or 2048", fn);
+  const uint32_t bpr = N / 256;
+  const uint32_t ksplit = gelu ? 1 : pick_ksplit(ctx, total_groups(rows, nseg), bpr, bpr);
+  const size_t xbytes = pro ? (size_t)B * N * sizeof(float) : 0;
+  size_t part_off[4] = {0, 0, 0, 0}, part_bytes = 0;
+  if (ksplit > 1)
+    for (int i = 0; i < nseg; ++i) {
+      part_off[i] = xbytes + part_bytes;
+      part_bytes += (size_t)ksplit * B * rows[i] * sizeof(float);
+    }
+  void* scratch = nullptr;
+  rc = g4_internal_scratch(ctx, xbytes + part_bytes, &scratch);
+  if (rc) return rc;
+  const float* x = p0.x;
+  if (pro) {
+    BPrepArgs p = p0;
+    p.nparts = 1;
+    p.B = B;
+    p.out = (float*)scratch;
+    rc = bprep_launch(ctx, N, pro, p);
+    if (rc) return rc == G4_ERR_UNSUPPORTED ? g4::set_error(rc, "%s: unsupported shape", fn) : rc;
+    x = p.out;
+  }
+  float* dst[4];
+  for (int i = 0; i < nseg; ++i) dst[i] = ksplit > 1 ? (float*)((uint8_t*)scratch + part_off[i]) : Y[i];
+  rc = mm_run(ctx, fn, qt, x, W, dst, rows, nseg, N, B, cap, gelu, ksplit);
+  if (rc || ksplit == 1) return rc;
+  for (int i = 0; i < nseg; ++i) {
+    const uint32_t n = B * rows[i];
+    hipLaunchKernelGGL(reduce_kernel, dim3(ceil_div(n, PNT)), dim3(PNT), 0, ctx->stream, dst[i], Y[i], n, ksplit,
+                       cap);
+    G4_LAUNCHED(ctx, "mm_reduce");
+  }
+  return G4_OK;
+}
+
+int check_norms(const char* fn, const uint16_t* w1, const float* residual, const uint16_t* w2,
+                const float* h_out) {
+  G4_REQUIRE(!residual == !w2, "%s: residual and w2 go together", fn);
+  G4_REQUIRE((!residual || ((uintptr_t)residual & 15) == 0) && (!h_out || ((uintptr_t)h_out & 15) == 0),
+             "%s: activations must be 16-byte aligned", fn);
+  G4_REQUIRE((!w1 || ((uintptr_t)w1 & 7) == 0) && (!w2 || ((uintptr_t)w2 & 7) == 0),
+             "%s: norm weights must be 8-byte aligned", fn);
+  return G4_OK;
+}
+
+int check_weights(const char* fn, int wtype, const void* const* weights, float* const* outputs,
+                  const uint32_t* rows, int nseg) {
+  G4_REQUIRE(wtype == 0 || wtype == 1, "%s: wtype must be 0 (Q4_K) or 1 (Q6_K)", fn);
+  G4_REQUIRE(nseg >= 1 && nseg <= 4, "%s: 1..4 segments", fn);
+  G4_REQUIRE(weights && outputs && rows, "%s: null buffer", fn);
+  for (int i = 0; i < nseg; ++i) {
+    G4_REQUIRE(weights[i] && outputs[i] && rows[i] > 0, "%s: segment %d empty", fn, i);
+    G4_REQUIRE(((uintptr_t)weights[i] & (wtype == 0 ? 15 : 3)) == 0,
+               "%s: weights misaligned (Q4_K 16 B, Q6_K 4 B)", fn);
+  }
+  return G4_OK;
 }
 
 }  // namespace
@@ -488,11 +756,12 @@ int batch_matmul(g4_ctx* ctx, const char* fn, int qt, int pro, const QuantArgs& 
 // Used by k_gemv.hip's batched entry points for batch >= 16.
 int g4_internal_batch_matmul(g4_ctx* ctx, const char* fn, int qt, const float* x, const void* w, float* y,
                              uint32_t M, uint32_t N, uint32_t batch) {
-  const QuantArgs q{x, nullptr, nullptr, nullptr, nullptr, 0.f, DigitBuf{}};
+  BPrepArgs p{};
+  p.x = x;
   const uint8_t* W[1] = {(const uint8_t*)w};
   float* Y[1] = {y};
   const uint32_t rows[1] = {M};
-  return batch_matmul(ctx, fn, qt, 0, q, W, Y, rows, 1, N, batch, 0.f);
+  return batch_matmul(ctx, fn, qt, 0, p, W, Y, rows, 1, N, batch, 0.f, false);
 }
 
 extern "C" {
@@ -502,27 +771,86 @@ int g4_normAddMatmulSegmentsBatch(g4_ctx* ctx, int wtype, const float* x, const 
                                   const void* const* weights, float* const* outputs, const uint32_t* rows, int nseg,
                                   uint32_t N, float eps, float softcap_cap, uint32_t batch) {
   G4_ENTER(ctx);
-  G4_REQUIRE(wtype == 0 || wtype == 1, "g4_normAddMatmulSegmentsBatch: wtype must be 0 (Q4_K) or 1 (Q6_K)");
-  G4_REQUIRE(nseg >= 1 && nseg <= 4, "g4_normAddMatmulSegmentsBatch: 1..4 segments");
-  G4_REQUIRE(x && weights && outputs && rows, "g4_normAddMatmulSegmentsBatch: null buffer");
-  G4_REQUIRE(!residual == !w2, "g4_normAddMatmulSegmentsBatch: residual and w2 go together");
-  G4_REQUIRE(((uintptr_t)x & 15) == 0 && (!residual || ((uintptr_t)residual & 15) == 0) &&
-                 (!h_out || ((uintptr_t)h_out & 15) == 0),
-             "g4_normAddMatmulSegmentsBatch: activations must be 16-byte aligned");
-  G4_REQUIRE((!w1 || ((uintptr_t)w1 & 7) == 0) && (!w2 || ((uintptr_t)w2 & 7) == 0),
-             "g4_normAddMatmulSegmentsBatch: norm weights must be 8-byte aligned");
+  int rc = check_weights(__func__, wtype, weights, outputs, rows, nseg);
+  if (!rc) rc = check_norms(__func__, w1, residual, w2, h_out);
+  if (rc) return rc;
   const uint8_t* W[4];
   float* Y[4];
   for (int i = 0; i < nseg; ++i) {
-    G4_REQUIRE(weights[i] && outputs[i] && rows[i] > 0, "g4_normAddMatmulSegmentsBatch: segment %d empty", i);
-    G4_REQUIRE(((uintptr_t)weights[i] & (wtype == 0 ? 15 : 3)) == 0,
-               "g4_normAddMatmulSegmentsBatch: weights misaligned (Q4_K 16 B, Q6_K 4 B)");
     W[i] = (const uint8_t*)weights[i];
     Y[i] = outputs[i];
   }
   const int pro = !w1 ? 0 : (residual ? 2 : 1);
-  const QuantArgs q{x, w1, residual, w2, h_out, eps, DigitBuf{}};
-  return batch_matmul(ctx, __func__, wtype, pro, q, W, Y, rows, nseg, N, batch, softcap_cap);
+  const BPrepArgs p{x, 1, batch, w1, residual, w2, h_out, nullptr, eps};
+  return batch_matmul(ctx, __func__, wtype, pro, p, W, Y, rows, nseg, N, batch, softcap_cap, false);
+}
+
+int g4_normAddGateUpGeluBatch(g4_ctx* ctx, const float* o, const uint16_t* w_post, const float* residual,
+                              const uint16_t* w_pre, const void* w_gate, const void* w_up, float* h_out, float* out,
+                              g4_matmul_params p, float eps, uint32_t batch) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(o && w_post && residual && w_pre && w_gate && w_up && out, "g4_normAddGateUpGeluBatch: null buffer");
+  G4_REQUIRE(p.M > 0 && (p.N == 1536 || p.N == 2048), "g4_normAddGateUpGeluBatch: N=%u must be 1536 or 2048",
+             p.N);
+  G4_REQUIRE(((uintptr_t)w_gate & 15) == 0 && ((uintptr_t)w_up & 15) == 0,
+             "g4_normAddGateUpGeluBatch: weights must be 16-byte aligned");
+  int rc = check_norms(__func__, w_post, residual, w_pre, h_out);
+  if (rc) return rc;
+  const uint8_t* W[2] = {(const uint8_t*)w_gate, (const uint8_t*)w_up};
+  float* Y[2] = {out, out};
+  const uint32_t rows[2] = {p.M, p.M};
+  const BPrepArgs pa{o, 1, batch, w_post, residual, w_pre, h_out, nullptr, eps};
+  return batch_matmul(ctx, __func__, 0, 2, pa, W, Y, rows, 2, p.N, batch, 0.f, true);
+}
+
+int g4_batchPrep(g4_ctx* ctx, const float* x, uint32_t nparts, const uint16_t* w1, const float* residual,
+                 const uint16_t* w2, float* h_out, float* out, uint32_t N, uint32_t batch, float eps) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(x && out && nparts >= 1, "g4_batchPrep: null buffer or no parts");
+  G4_REQUIRE(batch >= 1 && batch <= 65535, "g4_batchPrep: batch %u outside 1..65535", batch);
+  G4_REQUIRE(N == 1536 || N == 2048, "g4_batchPrep: N=%u must be 1536 or 2048", N);
+  G4_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 15) == 0, "g4_batchPrep: buffers must be 16-byte aligned");
+  G4_REQUIRE(w1 || !residual, "g4_batchPrep: residual needs w1");
+  int rc = check_norms(__func__, w1, residual, w2, h_out);
+  if (rc) return rc;
+  const int pro = !w1 ? 0 : (residual ? 2 : 1);
+  const BPrepArgs p{x, nparts, batch, w1, residual, w2, h_out, out, eps};
+  return bprep_launch(ctx, N, pro, p);
+}
+
+int g4_matmulSegmentsBatchPartial(g4_ctx* ctx, int wtype, const float* x, const void* const* weights,
+                                  float* const* outputs, const uint32_t* rows, int nseg, uint32_t N,
+                                  uint32_t batch, uint32_t max_ksplit, uint32_t* ksplit) {
+  G4_ENTER(ctx);
+  int rc = check_weights(__func__, wtype, weights, outputs, rows, nseg);
+  if (!rc) rc = check_x(__func__, x, N, batch);
+  if (rc) return rc;
+  G4_REQUIRE(ksplit && max_ksplit >= 1, "g4_matmulSegmentsBatchPartial: null ksplit or max_ksplit 0");
+  const uint8_t* W[4];
+  float* Y[4];
+  for (int i = 0; i < nseg; ++i) {
+    W[i] = (const uint8_t*)weights[i];
+    Y[i] = outputs[i];
+  }
+  const uint32_t ks = pick_ksplit(ctx, total_groups(rows, nseg), N / 256, max_ksplit);
+  rc = mm_run(ctx, __func__, wtype, x, W, Y, rows, nseg, N, batch, 0.f, false, ks);
+  if (rc == G4_OK) *ksplit = ks;
+  return rc;
+}
+
+int g4_gateUpGeluBatch(g4_ctx* ctx, const float* x, const void* w_gate, const void* w_up, float* out,
+                       g4_matmul_params p, uint32_t batch) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(w_gate && w_up && out && p.M > 0, "g4_gateUpGeluBatch: null buffer or empty");
+  G4_REQUIRE(p.N == 1536 || p.N == 2048, "g4_gateUpGeluBatch: N=%u must be 1536 or 2048", p.N);
+  G4_REQUIRE(((uintptr_t)w_gate & 15) == 0 && ((uintptr_t)w_up & 15) == 0,
+             "g4_gateUpGeluBatch: weights must be 16-byte aligned");
+  int rc = check_x(__func__, x, p.N, batch);
+  if (rc) return rc;
+  const uint8_t* W[2] = {(const uint8_t*)w_gate, (const uint8_t*)w_up};
+  float* Y[2] = {out, out};
+  const uint32_t rows[2] = {p.M, p.M};
+  return mm_run(ctx, __func__, 0, x, W, Y, rows, 2, p.N, batch, 0.f, true, 1);
 }
 
 }  // extern "C"

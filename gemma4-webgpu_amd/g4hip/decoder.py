@@ -317,6 +317,11 @@ class BatchDecoder(_SyntheticModel):
     every sequence's length on the device; a step appends one token to each
     sequence (seq_lens += 1) and may be captured once and replayed while the
     reserve lasts.
+
+    The split-K matmuls leave their chunks' partial sums in per-purpose
+    buffers; the next launch adds them in chunk order (the per-vector norm
+    prologue, or the attention prologue), so no launch waits on another's
+    workgroups and the step is deterministic.
     """
 
     def __init__(self, ctx: Context, context_lens, shape: Optional[E2BShape] = None, page_size: int = 16,
@@ -348,25 +353,32 @@ class BatchDecoder(_SyntheticModel):
         self.seq_lens = ctx.from_numpy(self.lens_host)
         self.hidden = ctx.empty(B * s.hidden, f32)
         self.hidden2 = ctx.empty(B * s.hidden, f32)
-        self.q = ctx.empty(B * s.q_dim, f32)
-        self.k = ctx.empty(B * s.kv_dim, f32)
-        self.v = ctx.empty(B * s.kv_dim, f32)
+        self.xn = ctx.empty(B * s.hidden, f32)        # normalised input of the next matmul
+        self.ks_h = s.hidden // 256                    # most K chunks of a matmul over the hidden width
+        self.ks_q = s.q_dim // 256
+        self.ks_f = s.ffn // 256
+        self.q_parts = ctx.empty(self.ks_h * B * s.q_dim, f32)
+        self.k_parts = ctx.empty(self.ks_h * B * s.kv_dim, f32)
+        self.v_parts = ctx.empty(self.ks_h * B * s.kv_dim, f32)
+        self.q = ctx.empty(B * s.q_dim, f32)           # q after q_norm + RoPE
         self.attn = ctx.empty(B * s.q_dim, f32)
-        self.o = ctx.empty(B * s.hidden, f32)
-        self.gate = ctx.empty(B * s.ffn, f32)
-        self.up = ctx.empty(B * s.ffn, f32)
+        self.o_parts = ctx.empty(self.ks_q * B * s.hidden, f32)
         self.act = ctx.empty(B * s.ffn, f32)
-        self.down = ctx.empty(B * s.hidden, f32)
+        self.down_parts = ctx.empty(self.ks_f * B * s.hidden, f32)
         self.logits = ctx.empty(B * s.vocab, f32) if lm_head else None
         self.tokens = ctx.zeros(B, np.uint32)
         self.topk = ctx.empty(B * 512, f32)
-        self.attn_params = []
+        self.pro_params, self.attn_params = [], []
         for il in range(s.n_layers):
             glob = s.is_global(il)
-            self.attn_params.append(ctx.paged_fused_params(
+            window = 0 if glob else s.window
+            self.pro_params.append(ctx.paged_fused_params(
                 B, s.n_q_heads, s.n_kv_heads, s.head_dim, page_size, self.max_pages, self.max_seq, self.num_pages,
-                0 if glob else s.window, s.eps, s.theta_global if glob else s.theta_local, int(glob)))
-        self.attn_ws = ctx.zeros(max(ctx.paged_fused_workspace_bytes(p) for p in self.attn_params), np.uint8)
+                window, s.eps, s.theta_global if glob else s.theta_local, int(glob)))
+            self.attn_params.append(ctx.paged_params(
+                B, s.n_q_heads, s.n_kv_heads, s.head_dim, page_size, self.max_pages, self.max_seq, self.num_pages,
+                1.0, window))
+        self.attn_ws = ctx.zeros(max(ctx.paged_workspace_bytes(p) for p in self.attn_params), np.uint8)
         ctx.fill_normal_f32(self.hidden, B * s.hidden, self._seed(), 0.0, 1.0)
         ctx.sync()
 
@@ -401,51 +413,51 @@ class BatchDecoder(_SyntheticModel):
         return total
 
     def step(self, sample: str = "argmax") -> None:
-        """One token for every sequence. Six launches per layer:
-          1. [post-FFN norm-add of the previous layer ->] attn rmsNorm -> q/k/v
-          2. per sequence: q/k norm + RoPE, v_norm, K/V append, paged split-K attention (+ merge)
-          3. o projection
-          4. post-attn norm-add -> pre-FFN rmsNorm -> gate/up
-          5. GELU product
-          6. down projection (Q6_K)
-        then the last norm-add + final rmsNorm + LM head + softcap, and the
+        """One token for every sequence. Per layer:
+          1. [sum of the previous down chunks -> post-FFN norm-add ->] attn rmsNorm
+          2. q/k/v projections (split-K partial sums)
+          3. attention prologue: q/k norm + RoPE, v_norm, K/V append into the pages
+          4. paged split-K attention (+ merge)
+          5. o projection (partial sums)
+          6. post-attn norm-add -> pre-FFN rmsNorm
+          7. gate/up -> GELU product
+          8. down projection (Q6_K, partial sums)
+        then the last norm-add + final rmsNorm, the LM head + softcap, and the
         per-sequence argmax (or top-k 256)."""
         c, s, B = self.ctx, self.s, self.B
+        H = s.hidden
         c.advanceSeqLens(self.seq_lens, B, 1)
+        nd = 0
         for il, L in enumerate(self.layers):
-            ws = [L.wq, L.wk, L.wv]
-            outs = [self.q, self.k, self.v]
-            rows = [s.q_dim, s.kv_dim, s.kv_dim]
             if il == 0:
-                c.normAddMatmulSegmentsBatch("q4k", self.hidden, L.attn_norm, None, None, None, ws, outs, rows,
-                                             s.hidden, B, s.eps)
+                c.batchPrep(self.hidden, 1, L.attn_norm, None, None, None, self.xn, H, B, s.eps)
             else:
                 prev = self.layers[il - 1]
-                c.normAddMatmulSegmentsBatch("q4k", self.down, prev.post_ffn_norm, self.hidden2, L.attn_norm,
-                                             self.hidden, ws, outs, rows, s.hidden, B, s.eps)
-            c.pagedAttnDecodeFused(self.q, self.k, self.v, L.q_norm, L.k_norm, self.rope_freqs, L.k_cache,
-                                   L.v_cache, self.page_table, self.seq_lens, self.attn, self.attn_params[il],
-                                   self.attn_ws)
-            c.matmulQuantBatch(self.attn, L.wo, self.o, s.hidden, s.q_dim, B)
-            c.normAddMatmulSegmentsBatch("q4k", self.o, L.post_attn_norm, self.hidden, L.pre_ffn_norm,
-                                         self.hidden2, [L.wgate, L.wup], [self.gate, self.up], [s.ffn, s.ffn],
-                                         s.hidden, B, s.eps)
-            c.geluMul(self.gate, self.up, self.act, B * s.ffn)
-            c.matmulQuantBatch(self.act, L.wdown, self.down, s.hidden, s.ffn, B, "q6k")
+                c.batchPrep(self.down_parts, nd, prev.post_ffn_norm, self.hidden2, L.attn_norm, self.hidden,
+                            self.xn, H, B, s.eps)
+            nq = c.matmulSegmentsBatchPartial("q4k", self.xn, [L.wq, L.wk, L.wv],
+                                              [self.q_parts, self.k_parts, self.v_parts],
+                                              [s.q_dim, s.kv_dim, s.kv_dim], H, B, self.ks_h)
+            c.pagedAttnPrologue(self.q_parts, self.k_parts, self.v_parts, nq, L.q_norm, L.k_norm, self.rope_freqs,
+                                self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.pro_params[il])
+            c.pagedAttnDecode(self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.attn,
+                              self.attn_params[il], self.attn_ws)
+            no = c.matmulSegmentsBatchPartial("q4k", self.attn, [L.wo], [self.o_parts], [H], s.q_dim, B, self.ks_q)
+            c.batchPrep(self.o_parts, no, L.post_attn_norm, self.hidden, L.pre_ffn_norm, self.hidden2, self.xn, H, B,
+                        s.eps)
+            c.gateUpGeluBatch(self.xn, L.wgate, L.wup, self.act, s.ffn, H, B)
+            nd = c.matmulSegmentsBatchPartial("q6k", self.act, [L.wdown], [self.down_parts], [H], s.ffn, B,
+                                              self.ks_f)
         last = self.layers[-1]
+        c.batchPrep(self.down_parts, nd, last.post_ffn_norm, self.hidden2, self.final_norm, self.hidden, self.xn, H,
+                    B, s.eps)
         if self.lm_head is not None:
-            c.normAddMatmulSegmentsBatch("q6k", self.down, last.post_ffn_norm, self.hidden2, self.final_norm,
-                                         self.hidden, [self.lm_head], [self.logits], [s.vocab], s.hidden, B, s.eps,
-                                         softcap=s.softcap)
+            c.normAddMatmulSegmentsBatch("q6k", self.xn, None, None, None, None, [self.lm_head], [self.logits],
+                                         [s.vocab], H, B, s.eps, softcap=s.softcap)
             if sample == "argmax":
                 c.argmaxBatch(self.logits, self.tokens, s.vocab, B)
             else:
                 c.topk256Batch(self.logits, self.topk, s.vocab, B)
-        else:
-            row = 4 * s.hidden
-            for i in range(B):
-                c.fusedNormAdd(self.down.offset(i * row), last.post_ffn_norm, self.hidden2.offset(i * row),
-                               self.hidden.offset(i * row), s.hidden, s.eps)
         self.lens_host = self.lens_host + 1
 
     def capture(self, sample: str = "argmax"):

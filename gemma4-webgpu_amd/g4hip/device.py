@@ -221,6 +221,34 @@ class Context:
                                                   _p(residual), _p(w2), _p(h_out), W, Y, R, n, N, eps, softcap,
                                                   batch))
 
+    def normAddGateUpGeluBatch(self, o: Ptr, w_post: Ptr, residual: Ptr, w_pre: Ptr, w_gate: Ptr, w_up: Ptr,
+                               h_out: Ptr, out: Ptr, M: int, N: int, batch: int, eps: float = 1e-6) -> None:
+        """normAddGateUpGelu_q4k over `batch` vectors: o/residual/h_out [batch][N], out [batch][M]."""
+        check(lib().g4_normAddGateUpGeluBatch(self.h, _p(o), _p(w_post), _p(residual), _p(w_pre), _p(w_gate),
+                                              _p(w_up), _p(h_out), _p(out), MatmulParams(M, N), eps, batch))
+
+    def matmulSegmentsBatchPartial(self, wtype: str, x: Ptr, weights, outputs, rows, N: int, batch: int,
+                                   max_ksplit: int) -> int:
+        """x [batch][N] times each weight; outputs[i] gets [ksplit][batch][rows[i]] partial sums.
+        Returns ksplit (<= max_ksplit)."""
+        n = len(weights)
+        W = (ctypes.c_void_p * n)(*[_p(w).value for w in weights])
+        Y = (ctypes.c_void_p * n)(*[_p(y).value for y in outputs])
+        R = (ctypes.c_uint32 * n)(*rows)
+        ks = ctypes.c_uint32(0)
+        check(lib().g4_matmulSegmentsBatchPartial(self.h, {"q4k": 0, "q6k": 1}[wtype], _p(x), W, Y, R, n, N, batch,
+                                                  max_ksplit, ctypes.byref(ks)))
+        return int(ks.value)
+
+    def batchPrep(self, x_parts: Ptr, nparts: int, w1: Ptr, residual: Ptr, w2: Ptr, h_out: Ptr, out: Ptr, N: int,
+                  batch: int, eps: float = 1e-6) -> None:
+        """out = prologue(sum of nparts chunks of x_parts) per vector (rmsNorm / fusedNormAdd + rmsNorm)."""
+        check(lib().g4_batchPrep(self.h, _p(x_parts), nparts, _p(w1), _p(residual), _p(w2), _p(h_out), _p(out), N,
+                                 batch, eps))
+
+    def gateUpGeluBatch(self, x: Ptr, w_gate: Ptr, w_up: Ptr, out: Ptr, M: int, N: int, batch: int) -> None:
+        check(lib().g4_gateUpGeluBatch(self.h, _p(x), _p(w_gate), _p(w_up), _p(out), MatmulParams(M, N), batch))
+
     # ---- attention (kv_cache_store / attn_score / softmax / attn_output) ----
     def kvCacheStore(self, k_in: Ptr, v_in: Ptr, k_cache: Ptr, v_cache: Ptr, num_kv_heads: int, head_dim: int,
                      position: int, max_seq_len: int, position_dev: Ptr = None) -> None:
@@ -323,6 +351,14 @@ class Context:
         check(lib().g4_pagedAttnDecodeFused(self.h, _p(q_raw), _p(k_raw), _p(v_raw), _p(q_norm_w), _p(k_norm_w),
                                             _p(rope_freqs), _p(k_pool), _p(v_pool), _p(page_table), _p(seq_lens),
                                             _p(out), p, _p(workspace), workspace.nbytes))
+
+    def pagedAttnPrologue(self, q_parts: Ptr, k_parts: Ptr, v_parts: Ptr, nparts: int, q_norm_w: Ptr, k_norm_w: Ptr,
+                          rope_freqs: Ptr, q_out: Ptr, k_pool: Ptr, v_pool: Ptr, page_table: Ptr, seq_lens: Ptr,
+                          p: PagedAttnFusedParams) -> None:
+        """Per sequence: q_norm + RoPE into q_out, K/V row (k_norm + RoPE, v_norm) appended to the pool."""
+        check(lib().g4_pagedAttnPrologue(self.h, _p(q_parts), _p(k_parts), _p(v_parts), nparts, _p(q_norm_w),
+                                         _p(k_norm_w), _p(rope_freqs), _p(q_out), _p(k_pool), _p(v_pool),
+                                         _p(page_table), _p(seq_lens), p))
 
     def advanceSeqLens(self, seq_lens: Ptr, num_seqs: int, delta: int = 1) -> None:
         check(lib().g4_advanceSeqLens(self.h, _p(seq_lens), num_seqs, delta))

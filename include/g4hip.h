@@ -227,6 +227,18 @@ int g4_pagedAttnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw,
                             uint16_t* k_pool, uint16_t* v_pool, const int32_t* page_table,
                             const uint32_t* seq_lens, float* output, g4_paged_attn_fused_params p,
                             void* workspace, size_t workspace_bytes);
+/* The same block before the attention, as a launch of its own over the
+ * split-K partial sums of the q/k/v projections (q_parts [nparts][num_seqs]
+ * [num_q_heads*head_dim], k_parts / v_parts [nparts][num_seqs]
+ * [num_kv_heads*head_dim], added in chunk order): q_out [num_seqs]
+ * [num_q_heads][head_dim] receives q after q_norm + RoPE, and the f16 K/V
+ * row is appended to the pool as g4_pagedAttnDecodeFused does;
+ * g4_pagedAttnDecode then attends. p.scale and p.sliding_window are unused. */
+int g4_pagedAttnPrologue(g4_ctx* ctx, const float* q_parts, const float* k_parts,
+                         const float* v_parts, uint32_t nparts, const uint16_t* q_norm_w,
+                         const uint16_t* k_norm_w, const uint16_t* rope_freqs, float* q_out,
+                         uint16_t* k_pool, uint16_t* v_pool, const int32_t* page_table,
+                         const uint32_t* seq_lens, g4_paged_attn_fused_params p);
 /* seq_lens[s] += delta for s < num_seqs, on the stream (the device-side
  * length counters a captured multi-sequence step replays with). */
 int g4_advanceSeqLens(g4_ctx* ctx, uint32_t* seq_lens, uint32_t num_seqs, uint32_t delta);
@@ -328,12 +340,42 @@ int g4_normAddMatmulSegments(g4_ctx* ctx, int wtype, const float* x, const uint1
  * decode: src/engine.ts:1546-1554 run once per sequence). x, residual and
  * h_out are [batch][N]; outputs[i] is [batch][rows[i]]. w1 == NULL skips the
  * norms (plain matmul). 1 <= batch <= 64. Runs on the matrix cores; the
- * activation digits live in the context scratch between its two launches. */
+ * activation operands live in the context scratch between its two launches. */
 int g4_normAddMatmulSegmentsBatch(g4_ctx* ctx, int wtype, const float* x, const uint16_t* w1,
                                   const float* residual, const uint16_t* w2, float* h_out,
                                   const void* const* weights, float* const* outputs,
                                   const uint32_t* rows, int nseg, uint32_t N, float eps,
                                   float softcap_cap, uint32_t batch);
+/* g4_normAddGateUpGelu_q4k over `batch` vectors (1..64): o, residual, h_out
+ * are [batch][N], out is [batch][p.M]. */
+int g4_normAddGateUpGeluBatch(g4_ctx* ctx, const float* o, const uint16_t* w_post,
+                              const float* residual, const uint16_t* w_pre, const void* w_gate,
+                              const void* w_up, float* h_out, float* out, g4_matmul_params p,
+                              float eps, uint32_t batch);
+
+/* The pieces of a multi-sequence step, for callers that chain them without
+ * an intermediate reduction (src/engine.ts:1545-1625 per sequence, for many
+ * sequences at once):
+ *
+ * g4_matmulSegmentsBatchPartial: x [batch][N] f32 times up to 4 matrices on
+ * the matrix cores, K split into *ksplit <= max_ksplit chunks (chosen to fill
+ * the device); outputs[i] receives [*ksplit][batch][rows[i]] partial sums
+ * (one chunk each) and must hold max_ksplit * batch * rows[i] floats. The
+ * consumer adds the chunks in order: g4_batchPrep, g4_pagedAttnPrologue. */
+int g4_matmulSegmentsBatchPartial(g4_ctx* ctx, int wtype, const float* x,
+                                  const void* const* weights, float* const* outputs,
+                                  const uint32_t* rows, int nseg, uint32_t N, uint32_t batch,
+                                  uint32_t max_ksplit, uint32_t* ksplit);
+/* x = the sum of the nparts chunks of x_parts [nparts][batch][N]; then
+ * w1 == NULL: out = x; residual == NULL: out = x * w1 / rms(x) (rmsNorm);
+ * else h = residual + x * w1 / rms(x) (written to h_out when non-NULL) and
+ * out = h * w2 / rms(h) (fusedNormAdd -> rmsNorm). N is 1536 or 2048. */
+int g4_batchPrep(g4_ctx* ctx, const float* x_parts, uint32_t nparts, const uint16_t* w1,
+                 const float* residual, const uint16_t* w2, float* h_out, float* out, uint32_t N,
+                 uint32_t batch, float eps);
+/* out = gelu(W_gate . x) * (W_up . x) for x [batch][p.N] (already normalised). */
+int g4_gateUpGeluBatch(g4_ctx* ctx, const float* x, const void* w_gate, const void* w_up,
+                       float* out, g4_matmul_params p, uint32_t batch);
 
 /* ------------------------------------------------------------------------ */
 /* Debug / test exports                                                      */

@@ -95,3 +95,72 @@ def test_batched_matmul_rejects_bad_shapes(ctx):
     with pytest.raises(Exception, match="batch 65"):
         ctx.normAddMatmulSegmentsBatch("q4k", ctx.from_numpy(X), None, None, None, None, [ctx.from_numpy(W)],
                                        [dY], [64], 1536, 65)
+
+
+@pytest.mark.parametrize("B", [5, 32, 64])
+def test_batched_gate_up_gelu(ctx, B):
+    """Post-attention norm-add + pre-FFN norm + gate/up + GELU product for B
+    sequences in one launch."""
+    M, N = 6144, 1536
+    Wg = O.gen_q4k(100, M * N // 256)
+    Wu = O.gen_q4k(101, M * N // 256)
+    X = O.gen_normal_f32(102, B * N, 0.0, 2.0).reshape(B, N)
+    R = O.gen_normal_f32(103, B * N).reshape(B, N)
+    w1 = O.gen_normal_f16(104, N, 1.0, 0.1)
+    w2 = O.gen_normal_f16(105, N, 1.0, 0.1)
+    dh = ctx.empty(B * N, np.float32)
+    dA = ctx.empty(B * M, np.float32)
+    ctx.normAddGateUpGeluBatch(ctx.from_numpy(X), ctx.from_numpy(w1), ctx.from_numpy(R), ctx.from_numpy(w2),
+                               ctx.from_numpy(Wg), ctx.from_numpy(Wu), dh, dA, M, N, B)
+    H = dh.download(np.float32).reshape(B, N)
+    A = dA.download(np.float32).reshape(B, M)
+    for b in range(B):
+        h = O.fused_norm_add(X[b], w1, R[b], 1e-6)
+        assert_close(H[b], h, rel=1e-6, cos=0.99999999, what=f"h_out {b}")
+        xn = O.rms_norm(h, w2, 1e-6)
+        ref = O.gelu_mul(O.matmul(xn, Wg, M, N, "q4k"), O.matmul(xn, Wu, M, N, "q4k"))
+        assert_close(A[b], ref, what=f"gelu(gate)*up seq {b}")
+
+
+@pytest.mark.parametrize("B", [3, 32])
+def test_batch_prep_adds_partials_then_norms(ctx, B):
+    """fusedNormAdd -> rmsNorm over x given as 3 chunks added in order."""
+    N = 1536
+    X = O.gen_normal_f32(110, 3 * B * N, 0.0, 1.0).reshape(3, B, N)
+    R = O.gen_normal_f32(111, B * N).reshape(B, N)
+    w1 = O.gen_normal_f16(112, N, 1.0, 0.1)
+    w2 = O.gen_normal_f16(113, N, 1.0, 0.1)
+    dh, dout = ctx.empty(B * N, np.float32), ctx.empty(B * N, np.float32)
+    ctx.batchPrep(ctx.from_numpy(X), 3, ctx.from_numpy(w1), ctx.from_numpy(R), ctx.from_numpy(w2), dh, dout, N, B)
+    H, Y = dh.download(np.float32).reshape(B, N), dout.download(np.float32).reshape(B, N)
+    S = (X[0] + X[1]) + X[2]  # f32, chunk order
+    for b in range(B):
+        h = O.fused_norm_add(S[b], w1, R[b], 1e-6)
+        assert_close(H[b], h, rel=1e-6, cos=0.99999999, what=f"h {b}")
+        assert_close(Y[b], O.rms_norm(h, w2, 1e-6), rel=1e-6, cos=0.99999999, what=f"x' {b}")
+    ctx.batchPrep(ctx.from_numpy(X), 1, ctx.from_numpy(w1), None, None, None, dout, N, B)
+    Y = dout.download(np.float32).reshape(B, N)
+    for b in range(B):
+        assert_close(Y[b], O.rms_norm(X[0][b], w1, 1e-6), rel=1e-6, cos=0.99999999, what=f"norm {b}")
+
+
+@pytest.mark.parametrize("wtype,segs,N,B,max_ks", [
+    ("q4k", (2048, 256, 256), 1536, 32, 6),   # q/k/v
+    ("q4k", (1536,), 2048, 17, 8),            # o
+    ("q6k", (1536,), 6144, 32, 24),           # down
+    ("q6k", (1536,), 6144, 64, 1),            # no split allowed
+])
+def test_matmul_partials_add_up(ctx, wtype, segs, N, B, max_ks):
+    Ws = [_weights(wtype, 120 + i, M, N) for i, M in enumerate(segs)]
+    X = O.gen_normal_f32(125, B * N, 0.0, 1.5).reshape(B, N)
+    outs = [ctx.empty(max_ks * B * M, np.float32) for M in segs]
+    ks = ctx.matmulSegmentsBatchPartial(wtype, ctx.from_numpy(X), [ctx.from_numpy(W) for W in Ws], outs,
+                                        list(segs), N, B, max_ks)
+    assert 1 <= ks <= max_ks and (N // 256) % ks == 0
+    for M, W, o in zip(segs, Ws, outs):
+        P = o.download(np.float32)[:ks * B * M].reshape(ks, B, M)
+        Y = P[0].copy()
+        for c in range(1, ks):
+            Y += P[c]
+        for b in range(B):
+            assert_close(Y[b], O.matmul(X[b], W, M, N, wtype), what=f"{wtype} M={M} vector {b} ({ks} chunks)")

@@ -69,9 +69,7 @@ def test_paged_attention_block_matches_dense_and_oracle(ctx, bdec):
     Q = rng.normal(0, 2, (B, s.q_dim)).astype(np.float32)
     K = rng.normal(0, 2, (B, kv)).astype(np.float32)
     V = rng.normal(0, 2, (B, kv)).astype(np.float32)
-    d.q.upload(Q)
-    d.k.upload(K)
-    d.v.upload(V)
+    dq, dk, dv = ctx.from_numpy(Q), ctx.from_numpy(K), ctx.from_numpy(V)
     for il, L in enumerate(d.layers):
         glob = s.is_global(il)
         theta = s.theta_global if glob else s.theta_local
@@ -79,8 +77,8 @@ def test_paged_attention_block_matches_dense_and_oracle(ctx, bdec):
         k0 = L.k_cache.download(np.uint16)
         v0 = L.v_cache.download(np.uint16)
         d.set_lengths(np.array(LENS, np.uint32) + 1)  # the step's advance already applied
-        ctx.pagedAttnDecodeFused(d.q, d.k, d.v, L.q_norm, L.k_norm, d.rope_freqs, L.k_cache, L.v_cache,
-                                 d.page_table, d.seq_lens, d.attn, d.attn_params[il], d.attn_ws)
+        ctx.pagedAttnDecodeFused(dq, dk, dv, L.q_norm, L.k_norm, d.rope_freqs, L.k_cache, L.v_cache,
+                                 d.page_table, d.seq_lens, d.attn, d.pro_params[il], d.attn_ws)
         A = d.attn.download(np.float32).reshape(B, -1)
         k1 = L.k_cache.download(np.uint16).reshape(-1, kv)
         v1 = L.v_cache.download(np.uint16).reshape(-1, kv)
@@ -115,6 +113,56 @@ def test_paged_attention_block_matches_dense_and_oracle(ctx, bdec):
         for before, after in ((k0, k1), (v0, v1)):
             diff = np.nonzero(np.any(before.reshape(-1, kv) != after, axis=1))[0]
             assert set(diff.tolist()) <= written
+        L.k_cache.upload(k0)
+        L.v_cache.upload(v0)
+    d.set_lengths(np.array(LENS, np.uint32))
+
+
+def test_prologue_then_paged_decode_matches_fused_and_oracle(ctx, bdec):
+    """The step's attention path (prologue over split-K partial sums, then the
+    paged decode) against the one-launch fused block and the oracle."""
+    d, s, B = bdec, bdec.s, bdec.B
+    kv, table = s.kv_dim, d.rope_freqs.download(np.uint16)
+    rng = np.random.default_rng(31)
+    Q = rng.normal(0, 2, (B, s.q_dim)).astype(np.float32)
+    K = rng.normal(0, 2, (B, kv)).astype(np.float32)
+    V = rng.normal(0, 2, (B, kv)).astype(np.float32)
+    # two chunks whose in-order sum is exactly Q (K, V)
+    parts = [ctx.from_numpy(np.concatenate([0.5 * A, 0.5 * A])) for A in (Q, K, V)]
+    dq, dk, dv = ctx.from_numpy(Q), ctx.from_numpy(K), ctx.from_numpy(V)
+    for il, L in enumerate(d.layers):
+        glob = s.is_global(il)
+        theta = s.theta_global if glob else s.theta_local
+        window = 0 if glob else s.window
+        k0, v0 = L.k_cache.download(np.uint16), L.v_cache.download(np.uint16)
+        d.set_lengths(np.array(LENS, np.uint32) + 1)
+        ctx.pagedAttnDecodeFused(dq, dk, dv, L.q_norm, L.k_norm, d.rope_freqs, L.k_cache, L.v_cache, d.page_table,
+                                 d.seq_lens, d.attn, d.pro_params[il], d.attn_ws)
+        A_fused = d.attn.download(np.float32).reshape(B, -1)
+        kf, vf = L.k_cache.download(np.uint16).reshape(-1, kv), L.v_cache.download(np.uint16).reshape(-1, kv)
+        L.k_cache.upload(k0)
+        L.v_cache.upload(v0)
+        ctx.pagedAttnPrologue(parts[0], parts[1], parts[2], 2, L.q_norm, L.k_norm, d.rope_freqs, d.q, L.k_cache,
+                              L.v_cache, d.page_table, d.seq_lens, d.pro_params[il])
+        ctx.pagedAttnDecode(d.q, L.k_cache, L.v_cache, d.page_table, d.seq_lens, d.attn, d.attn_params[il],
+                            d.attn_ws)
+        A = d.attn.download(np.float32).reshape(B, -1)
+        QR = d.q.download(np.float32).reshape(B, -1)
+        kp, vp = L.k_cache.download(np.uint16).reshape(-1, kv), L.v_cache.download(np.uint16).reshape(-1, kv)
+        qn, kn = L.q_norm.download(np.uint16), L.k_norm.download(np.uint16)
+        for b, pos in enumerate(LENS):
+            q = O.fused_per_head_norm_rope(Q[b], qn, s.n_q_heads, s.head_dim, s.eps, pos, theta, int(glob), table)
+            assert_close(QR[b], q, rel=1e-5, cos=0.9999999, what=f"roped q layer {il} seq {b}")
+            r = d.pool_row(b, pos)
+            for got, want in ((kp[r], kf[r]), (vp[r], vf[r])):  # the fused block's f16 rows, to 1 ulp
+                g16, w16 = got.view(np.float16).astype(np.float32), want.view(np.float16).astype(np.float32)
+                assert np.all(np.abs(g16 - w16) <= 2.0 ** -10 * np.maximum(np.abs(w16), 2.0 ** -14)), (il, b)
+            kc, vc = _dense(d, k0, b, pos), _dense(d, v0, b, pos)
+            kc.reshape(-1, kv)[pos] = kp[r]
+            vc.reshape(-1, kv)[pos] = vp[r]
+            a = O.attention(q, kc, vc, s.n_q_heads, s.n_kv_heads, s.head_dim, pos + 1, 1.0, window)
+            assert_close(A[b], a, what=f"attention layer {il} seq {b} len {pos}")
+            assert_close(A[b], A_fused[b], what=f"vs fused layer {il} seq {b}")
         L.k_cache.upload(k0)
         L.v_cache.upload(v0)
     d.set_lengths(np.array(LENS, np.uint32))
@@ -185,12 +233,12 @@ def test_batch_graph_replay_matches_eager(ctx, bdec):
 
 def test_paged_fused_rejects_bad_shapes(ctx, bdec):
     d = bdec
-    p = d.attn_params[0]
+    p = d.pro_params[0]
     bad = ctx.paged_fused_params(d.B, 8, 1, 256, 16, 2, 64, d.num_pages, 0, 1e-6, 1e4, 0)
     with pytest.raises(Exception, match="exceeds the page table"):
-        ctx.pagedAttnDecodeFused(d.q, d.k, d.v, d.layers[0].q_norm, d.layers[0].k_norm, None, d.layers[0].k_cache,
+        ctx.pagedAttnDecodeFused(d.q, d.q, d.q, d.layers[0].q_norm, d.layers[0].k_norm, None, d.layers[0].k_cache,
                                  d.layers[0].v_cache, d.page_table, d.seq_lens, d.attn, bad, d.attn_ws)
     small = ctx.zeros(16, np.uint8)
     with pytest.raises(Exception, match="workspace"):
-        ctx.pagedAttnDecodeFused(d.q, d.k, d.v, d.layers[0].q_norm, d.layers[0].k_norm, None, d.layers[0].k_cache,
+        ctx.pagedAttnDecodeFused(d.q, d.q, d.q, d.layers[0].q_norm, d.layers[0].k_norm, None, d.layers[0].k_cache,
                                  d.layers[0].v_cache, d.page_table, d.seq_lens, d.attn, p, small)
