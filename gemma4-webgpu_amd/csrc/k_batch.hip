@@ -30,7 +30,10 @@
 //  * The gate/up pair form gives each workgroup 32 rows of both matrices and
 //    writes gelu(gate) * up.
 //  * bprep_kernel applies RMSNorm or residual-add + RMSNorm per vector to the
-//    (summed) input of a matmul.
+//    (summed) input of a matmul and can also write the operand blocks of the
+//    matmul that follows, so that its workgroups copy them instead of each
+//    building them again (the LM head's 4096 workgroups read the same
+//    activations).
 #include "g4_internal.hpp"
 
 namespace {
@@ -84,6 +87,8 @@ struct BPrepArgs {
   float* h_out;  // [B][K]
   float* out;    // [B][K]
   float eps;
+  uint8_t* ops;  // optional: operand blocks [K/256][Ops::bytes(ntv)]
+  int ntv;
 };
 
 __device__ __forceinline__ float4 mulw(float4 x, uint2 w, float s) {
@@ -173,6 +178,49 @@ __global__ __launch_bounds__(PNT) void bprep_kernel(BPrepArgs a) {
     const int f = 4 * tid + 4 * PNT * p;
     if (f < K) *(float4*)(a.out + (size_t)v * K + f) = x[p];
   }
+  if (!a.ops) return;
+  // operand blocks: wave w of pass p holds super-block 4p + w, lanes 8j .. 8j+7 its sub-block j
+  const uint32_t sblk = Ops::bytes(a.ntv);
+  const uint32_t t = v / 16, c = v % 16;
+  const int s = lane >> 3;        // sub-block within the super-block
+  const int kk = (lane & 7) * 4;  // first element within the sub-block
+  const int q = kk >> 3;          // 8-element group
+#pragma unroll
+  for (int p = 0; p < XP; ++p) {
+    const uint32_t sb = 4u * p + w;  // uniform over the wave
+    if (sb >= (uint32_t)BPR) break;
+    const float4 xv = x[p];
+    float am = fmaxf(fmaxf(fabsf(xv.x), fabsf(xv.y)), fmaxf(fabsf(xv.z), fabsf(xv.w)));
+    am = g4d::wave_max_dpp(am);
+    int ex = 0;
+    (void)frexpf(am, &ex);
+    const int k = am > 0.f ? min(max(14 - ex, -120), 120) : 0;
+    const float sc = ldexpf(1.0f, k);
+    const float xs[4] = {xv.x * sc, xv.y * sc, xv.z * sc, xv.w * sc};
+    _Float16 hi[4], lo[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      hi[e] = (_Float16)xs[e];
+      lo[e] = (_Float16)(xs[e] - (float)hi[e]);
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sum += xs[e];
+    sum = g4d::sum8(sum) * 0.015625f;  // * 2^-6
+    uint8_t* base = a.ops + (size_t)sb * sblk;
+    uint8_t* mp = base + t * Ops::MAIN_T + s * 2048 + (c + 16u * q) * 16 + (kk & 7) * 2;
+    *(uint2*)mp = make_uint2(pack_h2(hi[0], hi[1]), pack_h2(hi[2], hi[3]));
+    *(uint2*)(mp + 1024) = make_uint2(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));
+    if ((lane & 7) == 0) {
+      const _Float16 p0 = (_Float16)sum;
+      const float r1 = sum - (float)p0;
+      const _Float16 p1 = (_Float16)r1;
+      const _Float16 p2 = (_Float16)(r1 - (float)p1);
+      *(uint2*)(base + Ops::sums_off(a.ntv) + t * 1024 + (c + 16u * (uint32_t)(s >> 1)) * 16 + (s & 1) * 8) =
+          make_uint2(pack_h2(p0, p1), pack_h2(p2, (_Float16)0.f));
+    }
+    if (lane == 0) *(float*)(base + Ops::scale_off(a.ntv) + t * 64 + c * 4) = ldexpf(1.0f, -k);
+  }
 }
 
 // Y[v][m] = epilogue(sum_c part[c][v][m]) for a split-K matmul (in chunk order).
@@ -206,7 +254,8 @@ struct MmArgs {
   int n;
   uint32_t B;
   float cap;       // softcap when > 0 (ksplit == 1)
-  const float* x;  // [B][K] activations
+  const float* x;        // [B][K] activations
+  const uint8_t* ops;    // OPS: their operand blocks [K/256][Ops::bytes(NTV)]
   uint32_t K;
   uint32_t ksplit, kc;  // K in ksplit chunks of kc super-blocks
 };
@@ -427,6 +476,48 @@ __device__ __forceinline__ void raw_store(const Raw<NTV>& r, uint8_t* lds, uint3
   }
 }
 
+// Prebuilt operand block copy, global -> registers -> LDS: N 16-byte pieces,
+// piece tid + MNT*i per thread; pieces past N go to the sink slot at N.
+template <int NCP, uint32_t N>
+__device__ __forceinline__ void cp_load(u32x4 (&cp)[NCP], const u32x4* src, int tid) {
+#pragma unroll
+  for (int i = 0; i < NCP; ++i) {
+    const uint32_t e = (uint32_t)(tid + MNT * i);
+    cp[i] = src[e < N ? e : 0];
+  }
+}
+template <int NCP, uint32_t N>
+__device__ __forceinline__ void cp_store(const u32x4 (&cp)[NCP], u32x4* lds, int tid) {
+#pragma unroll
+  for (int i = 0; i < NCP; ++i) {
+    const uint32_t e = (uint32_t)(tid + MNT * i);
+    lds[e < N ? e : N] = cp[i];
+  }
+}
+
+// The operand source of one launch: built from f32 activations (OPS false)
+// or copied from blocks a prep launch built (OPS true).
+template <int NTV, bool OPS>
+struct OpSrc;
+template <int NTV>
+struct OpSrc<NTV, false> {
+  Raw<NTV> r;
+  __device__ __forceinline__ void load(const MmArgs& a, uint32_t kb, int tid) { raw_load<NTV>(r, a.x, a.B, a.K, kb, tid); }
+  __device__ __forceinline__ void store(uint8_t* lds, const MmArgs& a, int tid) { raw_store<NTV>(r, lds, a.B, tid); }
+};
+template <int NTV>
+struct OpSrc<NTV, true> {
+  static constexpr uint32_t NPC = Ops::bytes(NTV) / 16;
+  static constexpr int NCP = (int)((NPC + MNT - 1) / MNT);
+  u32x4 cp[NCP];
+  __device__ __forceinline__ void load(const MmArgs& a, uint32_t kb, int tid) {
+    cp_load<NCP, NPC>(cp, (const u32x4*)a.ops + (size_t)kb * NPC, tid);
+  }
+  __device__ __forceinline__ void store(uint8_t* lds, const MmArgs&, int tid) {
+    cp_store<NCP, NPC>(cp, (u32x4*)lds, tid);
+  }
+};
+
 __device__ __forceinline__ float gelu_tanh(float x) {  // shaders/gelu_mul.wgsl:10-16
   float t = 0.7978845608028654f * x * (1.0f + 0.044715f * x * x);
   t = fminf(fmaxf(t, -15.0f), 15.0f);
@@ -444,9 +535,9 @@ __device__ __forceinline__ float epilogue(float y, float cap) {
 // MODE 0: a row group is 64 rows of one segment. MODE 1 (gate/up): segments
 // 0 and 1 have the same rows; a row group is 32 rows of both, waves 0-1 gate,
 // waves 2-3 up, and the output (segment 0's Y) is gelu(gate) * up.
-template <int QT, int BPR, int NTV, int MODE>
+template <int QT, int BPR, int NTV, int MODE, bool OPS>
 __global__ __launch_bounds__(MNT) void mmf_kernel(MmArgs a) {
-  __shared__ __align__(16) uint8_t lds[Ops::bytes(NTV)];
+  __shared__ __align__(16) uint8_t lds[Ops::bytes(NTV) + 16];  // + the copy's sink slot
 
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q = l >> 4;
   const uint32_t g = blockIdx.x / a.ksplit, chunk = blockIdx.x % a.ksplit;
@@ -468,11 +559,11 @@ __global__ __launch_bounds__(MNT) void mmf_kernel(MmArgs a) {
   }
   const uint32_t kb0 = chunk * a.kc;
 
-  Raw<NTV> raw;
+  OpSrc<NTV, OPS> src;
   WRegs<QT> wr, wn;
-  raw_load<NTV>(raw, a.x, a.B, a.K, kb0, tid);
+  src.load(a, kb0, tid);
   load_w<BPR>(wr, W, M, rbase, kb0, l);
-  raw_store<NTV>(raw, lds, a.B, tid);
+  src.store(lds, a, tid);
   __syncthreads();
 
   f4 acc[NTV];
@@ -483,7 +574,7 @@ __global__ __launch_bounds__(MNT) void mmf_kernel(MmArgs a) {
   for (uint32_t j = 0; j < a.kc; ++j) {
     const bool more = j + 1 < a.kc;
     const uint32_t kn = kb0 + j + (more ? 1u : 0u);
-    raw_load<NTV>(raw, a.x, a.B, a.K, kn, tid);  // the next block is in flight during this one
+    src.load(a, kn, tid);  // the next block is in flight during this one
     load_w<BPR>(wn, W, M, rbase, kn, l);
 
     f4 C[NTV], Cm[NTV];
@@ -525,7 +616,7 @@ __global__ __launch_bounds__(MNT) void mmf_kernel(MmArgs a) {
     }
     __syncthreads();  // every wave is done with this block's operands
     if (more) {
-      raw_store<NTV>(raw, lds, a.B, tid);
+      src.store(lds, a, tid);
       __syncthreads();
     }
     wr = wn;
@@ -599,19 +690,31 @@ bool mm_supported(uint32_t bpr) {
   return bpr == 4 || bpr == 6 || bpr == 8 || bpr == 12 || bpr == 16 || bpr == 24 || bpr == 32 || bpr == 48;
 }
 
-template <int QT, int BPR, int NTV, int MODE>
+template <int QT, int BPR, int NTV, int MODE, bool OPS>
 int mm_launch(g4_ctx* ctx, const MmArgs& a, uint32_t groups) {
-  hipLaunchKernelGGL((mmf_kernel<QT, BPR, NTV, MODE>), dim3(groups * a.ksplit), dim3(MNT), 0, ctx->stream, a);
+  hipLaunchKernelGGL((mmf_kernel<QT, BPR, NTV, MODE, OPS>), dim3(groups * a.ksplit), dim3(MNT), 0, ctx->stream, a);
   G4_LAUNCHED(ctx, "mm");
   return G4_OK;
 }
 
+// Prebuilt operands come from the norm prologue, whose widths are 1536 and 2048.
+template <int BPR>
+constexpr bool ops_width() { return BPR == 6 || BPR == 8; }
+
 template <int QT, int BPR, int MODE>
 int mm_ntv(g4_ctx* ctx, const MmArgs& a, uint32_t groups) {
   const uint32_t Bp = pad_batch(a.B);
-  if (Bp == 16) return mm_launch<QT, BPR, 1, MODE>(ctx, a, groups);
-  if (Bp == 32) return mm_launch<QT, BPR, 2, MODE>(ctx, a, groups);
-  return mm_launch<QT, BPR, 4, MODE>(ctx, a, groups);
+  if constexpr (ops_width<BPR>()) {
+    if (a.ops) {
+      if (Bp == 16) return mm_launch<QT, BPR, 1, MODE, true>(ctx, a, groups);
+      if (Bp == 32) return mm_launch<QT, BPR, 2, MODE, true>(ctx, a, groups);
+      return mm_launch<QT, BPR, 4, MODE, true>(ctx, a, groups);
+    }
+  }
+  if (a.ops) return G4_ERR_UNSUPPORTED;
+  if (Bp == 16) return mm_launch<QT, BPR, 1, MODE, false>(ctx, a, groups);
+  if (Bp == 32) return mm_launch<QT, BPR, 2, MODE, false>(ctx, a, groups);
+  return mm_launch<QT, BPR, 4, MODE, false>(ctx, a, groups);
 }
 
 template <int QT>
@@ -650,8 +753,9 @@ int check_x(const char* fn, const float* x, uint32_t N, uint32_t B) {
 
 // One matmul launch over up to four matrices sharing the input x [B][N] (or
 // the gate/up pair). ksplit > 1 leaves partial sums in Y[i] [ksplit][B][rows[i]].
-int mm_run(g4_ctx* ctx, const char* fn, int qt, const float* x, const uint8_t* const* W, float* const* Y,
-           const uint32_t* rows, int nseg, uint32_t N, uint32_t B, float cap, bool gelu, uint32_t ksplit) {
+int mm_run(g4_ctx* ctx, const char* fn, int qt, const float* x, const uint8_t* ops, const uint8_t* const* W,
+           float* const* Y, const uint32_t* rows, int nseg, uint32_t N, uint32_t B, float cap, bool gelu,
+           uint32_t ksplit) {
   const uint32_t bpr = N / 256;
   uint32_t groups = 0;
   MmArgs a{};
@@ -664,6 +768,7 @@ int mm_run(g4_ctx* ctx, const char* fn, int qt, const float* x, const uint8_t* c
   a.B = B;
   a.cap = cap;
   a.x = x;
+  a.ops = ops;
   a.K = N;
   a.ksplit = ksplit;
   a.kc = bpr / ksplit;
@@ -695,7 +800,8 @@ int batch_matmul(g4_ctx* ctx, const char* fn, int qt, int pro, const BPrepArgs& 
   G4_REQUIRE(pro == 0 || N == 1536 || N == 2048, "%s: normalising prologue needs N 1536 or 2048", fn);
   const uint32_t bpr = N / 256;
   const uint32_t ksplit = gelu ? 1 : pick_ksplit(ctx, total_groups(rows, nseg), bpr, bpr);
-  const size_t xbytes = pro ? (size_t)B * N * sizeof(float) : 0;
+  const uint32_t ntv = pad_batch(B) / 16;
+  const size_t xbytes = pro ? (size_t)B * N * sizeof(float) + (size_t)bpr * Ops::bytes((int)ntv) : 0;
   size_t part_off[4] = {0, 0, 0, 0}, part_bytes = 0;
   if (ksplit > 1)
     for (int i = 0; i < nseg; ++i) {
@@ -706,18 +812,22 @@ int batch_matmul(g4_ctx* ctx, const char* fn, int qt, int pro, const BPrepArgs& 
   rc = g4_internal_scratch(ctx, xbytes + part_bytes, &scratch);
   if (rc) return rc;
   const float* x = p0.x;
+  const uint8_t* ops = nullptr;
   if (pro) {
     BPrepArgs p = p0;
     p.nparts = 1;
     p.B = B;
     p.out = (float*)scratch;
+    p.ops = (uint8_t*)scratch + (size_t)B * N * sizeof(float);
+    p.ntv = (int)ntv;
     rc = bprep_launch(ctx, N, pro, p);
     if (rc) return rc == G4_ERR_UNSUPPORTED ? g4::set_error(rc, "%s: unsupported shape", fn) : rc;
     x = p.out;
+    ops = p.ops;
   }
   float* dst[4];
   for (int i = 0; i < nseg; ++i) dst[i] = ksplit > 1 ? (float*)((uint8_t*)scratch + part_off[i]) : Y[i];
-  rc = mm_run(ctx, fn, qt, x, W, dst, rows, nseg, N, B, cap, gelu, ksplit);
+  rc = mm_run(ctx, fn, qt, x, ops, W, dst, rows, nseg, N, B, cap, gelu, ksplit);
   if (rc || ksplit == 1) return rc;
   for (int i = 0; i < nseg; ++i) {
     const uint32_t n = B * rows[i];
@@ -781,7 +891,7 @@ int g4_normAddMatmulSegmentsBatch(g4_ctx* ctx, int wtype, const float* x, const 
     Y[i] = outputs[i];
   }
   const int pro = !w1 ? 0 : (residual ? 2 : 1);
-  const BPrepArgs p{x, 1, batch, w1, residual, w2, h_out, nullptr, eps};
+  const BPrepArgs p{x, 1, batch, w1, residual, w2, h_out, nullptr, eps, nullptr, 0};
   return batch_matmul(ctx, __func__, wtype, pro, p, W, Y, rows, nseg, N, batch, softcap_cap, false);
 }
 
@@ -799,33 +909,44 @@ int g4_normAddGateUpGeluBatch(g4_ctx* ctx, const float* o, const uint16_t* w_pos
   const uint8_t* W[2] = {(const uint8_t*)w_gate, (const uint8_t*)w_up};
   float* Y[2] = {out, out};
   const uint32_t rows[2] = {p.M, p.M};
-  const BPrepArgs pa{o, 1, batch, w_post, residual, w_pre, h_out, nullptr, eps};
+  const BPrepArgs pa{o, 1, batch, w_post, residual, w_pre, h_out, nullptr, eps, nullptr, 0};
   return batch_matmul(ctx, __func__, 0, 2, pa, W, Y, rows, 2, p.N, batch, 0.f, true);
 }
 
+int g4_batchOperandBytes(uint32_t N, uint32_t batch, size_t* bytes) {
+  G4_REQUIRE(bytes && N % 256 == 0 && batch >= 1 && batch <= 64, "g4_batchOperandBytes: bad shape");
+  *bytes = (size_t)(N / 256) * Ops::bytes((int)(pad_batch(batch) / 16));
+  return G4_OK;
+}
+
 int g4_batchPrep(g4_ctx* ctx, const float* x, uint32_t nparts, const uint16_t* w1, const float* residual,
-                 const uint16_t* w2, float* h_out, float* out, uint32_t N, uint32_t batch, float eps) {
+                 const uint16_t* w2, float* h_out, float* out, void* ops, uint32_t N, uint32_t batch, float eps) {
   G4_ENTER(ctx);
   G4_REQUIRE(x && out && nparts >= 1, "g4_batchPrep: null buffer or no parts");
-  G4_REQUIRE(batch >= 1 && batch <= 65535, "g4_batchPrep: batch %u outside 1..65535", batch);
+  G4_REQUIRE(batch >= 1 && batch <= (ops ? 64u : 65535u), "g4_batchPrep: batch %u out of range", batch);
   G4_REQUIRE(N == 1536 || N == 2048, "g4_batchPrep: N=%u must be 1536 or 2048", N);
-  G4_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 15) == 0, "g4_batchPrep: buffers must be 16-byte aligned");
+  G4_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)ops & 15) == 0,
+             "g4_batchPrep: buffers must be 16-byte aligned");
   G4_REQUIRE(w1 || !residual, "g4_batchPrep: residual needs w1");
   int rc = check_norms(__func__, w1, residual, w2, h_out);
   if (rc) return rc;
   const int pro = !w1 ? 0 : (residual ? 2 : 1);
-  const BPrepArgs p{x, nparts, batch, w1, residual, w2, h_out, out, eps};
+  const BPrepArgs p{x, nparts, batch, w1, residual, w2, h_out, out, eps, (uint8_t*)ops,
+                    (int)(pad_batch(batch) / 16)};
   return bprep_launch(ctx, N, pro, p);
 }
 
-int g4_matmulSegmentsBatchPartial(g4_ctx* ctx, int wtype, const float* x, const void* const* weights,
-                                  float* const* outputs, const uint32_t* rows, int nseg, uint32_t N,
-                                  uint32_t batch, uint32_t max_ksplit, uint32_t* ksplit) {
+int g4_matmulSegmentsBatchPartial(g4_ctx* ctx, int wtype, const float* x, const void* ops,
+                                  const void* const* weights, float* const* outputs, const uint32_t* rows, int nseg,
+                                  uint32_t N, uint32_t batch, uint32_t max_ksplit, float softcap_cap,
+                                  uint32_t* ksplit) {
   G4_ENTER(ctx);
   int rc = check_weights(__func__, wtype, weights, outputs, rows, nseg);
   if (!rc) rc = check_x(__func__, x, N, batch);
   if (rc) return rc;
   G4_REQUIRE(ksplit && max_ksplit >= 1, "g4_matmulSegmentsBatchPartial: null ksplit or max_ksplit 0");
+  G4_REQUIRE(softcap_cap <= 0.f || max_ksplit == 1, "g4_matmulSegmentsBatchPartial: softcap needs max_ksplit 1");
+  G4_REQUIRE(!ops || ((uintptr_t)ops & 15) == 0, "g4_matmulSegmentsBatchPartial: operands must be 16-byte aligned");
   const uint8_t* W[4];
   float* Y[4];
   for (int i = 0; i < nseg; ++i) {
@@ -833,24 +954,24 @@ int g4_matmulSegmentsBatchPartial(g4_ctx* ctx, int wtype, const float* x, const 
     Y[i] = outputs[i];
   }
   const uint32_t ks = pick_ksplit(ctx, total_groups(rows, nseg), N / 256, max_ksplit);
-  rc = mm_run(ctx, __func__, wtype, x, W, Y, rows, nseg, N, batch, 0.f, false, ks);
+  rc = mm_run(ctx, __func__, wtype, x, (const uint8_t*)ops, W, Y, rows, nseg, N, batch, softcap_cap, false, ks);
   if (rc == G4_OK) *ksplit = ks;
   return rc;
 }
 
-int g4_gateUpGeluBatch(g4_ctx* ctx, const float* x, const void* w_gate, const void* w_up, float* out,
-                       g4_matmul_params p, uint32_t batch) {
+int g4_gateUpGeluBatch(g4_ctx* ctx, const float* x, const void* ops, const void* w_gate, const void* w_up,
+                       float* out, g4_matmul_params p, uint32_t batch) {
   G4_ENTER(ctx);
   G4_REQUIRE(w_gate && w_up && out && p.M > 0, "g4_gateUpGeluBatch: null buffer or empty");
   G4_REQUIRE(p.N == 1536 || p.N == 2048, "g4_gateUpGeluBatch: N=%u must be 1536 or 2048", p.N);
-  G4_REQUIRE(((uintptr_t)w_gate & 15) == 0 && ((uintptr_t)w_up & 15) == 0,
-             "g4_gateUpGeluBatch: weights must be 16-byte aligned");
+  G4_REQUIRE(((uintptr_t)w_gate & 15) == 0 && ((uintptr_t)w_up & 15) == 0 && ((uintptr_t)ops & 15) == 0,
+             "g4_gateUpGeluBatch: weights and operands must be 16-byte aligned");
   int rc = check_x(__func__, x, p.N, batch);
   if (rc) return rc;
   const uint8_t* W[2] = {(const uint8_t*)w_gate, (const uint8_t*)w_up};
   float* Y[2] = {out, out};
   const uint32_t rows[2] = {p.M, p.M};
-  return mm_run(ctx, __func__, 0, x, W, Y, rows, 2, p.N, batch, 0.f, true, 1);
+  return mm_run(ctx, __func__, 0, x, (const uint8_t*)ops, W, Y, rows, 2, p.N, batch, 0.f, true, 1);
 }
 
 }  // extern "C"

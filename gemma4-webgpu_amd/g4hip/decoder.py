@@ -354,6 +354,7 @@ class BatchDecoder(_SyntheticModel):
         self.hidden = ctx.empty(B * s.hidden, f32)
         self.hidden2 = ctx.empty(B * s.hidden, f32)
         self.xn = ctx.empty(B * s.hidden, f32)        # normalised input of the next matmul
+        self.xops = ctx.empty(ctx.batch_operand_bytes(s.hidden, B), np.uint8)  # its operand blocks
         self.ks_h = s.hidden // 256                    # most K chunks of a matmul over the hidden width
         self.ks_q = s.q_dim // 256
         self.ks_f = s.ffn // 256
@@ -430,30 +431,30 @@ class BatchDecoder(_SyntheticModel):
         nd = 0
         for il, L in enumerate(self.layers):
             if il == 0:
-                c.batchPrep(self.hidden, 1, L.attn_norm, None, None, None, self.xn, H, B, s.eps)
+                c.batchPrep(self.hidden, 1, L.attn_norm, None, None, None, self.xn, H, B, s.eps, ops=self.xops)
             else:
                 prev = self.layers[il - 1]
                 c.batchPrep(self.down_parts, nd, prev.post_ffn_norm, self.hidden2, L.attn_norm, self.hidden,
-                            self.xn, H, B, s.eps)
+                            self.xn, H, B, s.eps, ops=self.xops)
             nq = c.matmulSegmentsBatchPartial("q4k", self.xn, [L.wq, L.wk, L.wv],
                                               [self.q_parts, self.k_parts, self.v_parts],
-                                              [s.q_dim, s.kv_dim, s.kv_dim], H, B, self.ks_h)
+                                              [s.q_dim, s.kv_dim, s.kv_dim], H, B, self.ks_h, ops=self.xops)
             c.pagedAttnPrologue(self.q_parts, self.k_parts, self.v_parts, nq, L.q_norm, L.k_norm, self.rope_freqs,
                                 self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.pro_params[il])
             c.pagedAttnDecode(self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.attn,
                               self.attn_params[il], self.attn_ws)
             no = c.matmulSegmentsBatchPartial("q4k", self.attn, [L.wo], [self.o_parts], [H], s.q_dim, B, self.ks_q)
             c.batchPrep(self.o_parts, no, L.post_attn_norm, self.hidden, L.pre_ffn_norm, self.hidden2, self.xn, H, B,
-                        s.eps)
-            c.gateUpGeluBatch(self.xn, L.wgate, L.wup, self.act, s.ffn, H, B)
+                        s.eps, ops=self.xops)
+            c.gateUpGeluBatch(self.xn, L.wgate, L.wup, self.act, s.ffn, H, B, ops=self.xops)
             nd = c.matmulSegmentsBatchPartial("q6k", self.act, [L.wdown], [self.down_parts], [H], s.ffn, B,
                                               self.ks_f)
         last = self.layers[-1]
         c.batchPrep(self.down_parts, nd, last.post_ffn_norm, self.hidden2, self.final_norm, self.hidden, self.xn, H,
-                    B, s.eps)
+                    B, s.eps, ops=self.xops)
         if self.lm_head is not None:
-            c.normAddMatmulSegmentsBatch("q6k", self.xn, None, None, None, None, [self.lm_head], [self.logits],
-                                         [s.vocab], H, B, s.eps, softcap=s.softcap)
+            c.matmulSegmentsBatchPartial("q6k", self.xn, [self.lm_head], [self.logits], [s.vocab], H, B, 1,
+                                         ops=self.xops, softcap=s.softcap)
             if sample == "argmax":
                 c.argmaxBatch(self.logits, self.tokens, s.vocab, B)
             else:

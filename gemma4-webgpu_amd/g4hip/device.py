@@ -228,26 +228,35 @@ class Context:
                                               _p(w_up), _p(h_out), _p(out), MatmulParams(M, N), eps, batch))
 
     def matmulSegmentsBatchPartial(self, wtype: str, x: Ptr, weights, outputs, rows, N: int, batch: int,
-                                   max_ksplit: int) -> int:
-        """x [batch][N] times each weight; outputs[i] gets [ksplit][batch][rows[i]] partial sums.
-        Returns ksplit (<= max_ksplit)."""
+                                   max_ksplit: int, ops: Ptr = None, softcap: float = 0.0) -> int:
+        """x [batch][N] (and its operand blocks `ops`, or None) times each weight; outputs[i] gets
+        [ksplit][batch][rows[i]] partial sums. Returns ksplit (<= max_ksplit)."""
         n = len(weights)
         W = (ctypes.c_void_p * n)(*[_p(w).value for w in weights])
         Y = (ctypes.c_void_p * n)(*[_p(y).value for y in outputs])
         R = (ctypes.c_uint32 * n)(*rows)
         ks = ctypes.c_uint32(0)
-        check(lib().g4_matmulSegmentsBatchPartial(self.h, {"q4k": 0, "q6k": 1}[wtype], _p(x), W, Y, R, n, N, batch,
-                                                  max_ksplit, ctypes.byref(ks)))
+        check(lib().g4_matmulSegmentsBatchPartial(self.h, {"q4k": 0, "q6k": 1}[wtype], _p(x), _p(ops), W, Y, R, n,
+                                                  N, batch, max_ksplit, softcap, ctypes.byref(ks)))
         return int(ks.value)
 
-    def batchPrep(self, x_parts: Ptr, nparts: int, w1: Ptr, residual: Ptr, w2: Ptr, h_out: Ptr, out: Ptr, N: int,
-                  batch: int, eps: float = 1e-6) -> None:
-        """out = prologue(sum of nparts chunks of x_parts) per vector (rmsNorm / fusedNormAdd + rmsNorm)."""
-        check(lib().g4_batchPrep(self.h, _p(x_parts), nparts, _p(w1), _p(residual), _p(w2), _p(h_out), _p(out), N,
-                                 batch, eps))
+    @staticmethod
+    def batch_operand_bytes(N: int, batch: int) -> int:
+        n = ctypes.c_size_t()
+        check(lib().g4_batchOperandBytes(N, batch, ctypes.byref(n)))
+        return int(n.value)
 
-    def gateUpGeluBatch(self, x: Ptr, w_gate: Ptr, w_up: Ptr, out: Ptr, M: int, N: int, batch: int) -> None:
-        check(lib().g4_gateUpGeluBatch(self.h, _p(x), _p(w_gate), _p(w_up), _p(out), MatmulParams(M, N), batch))
+    def batchPrep(self, x_parts: Ptr, nparts: int, w1: Ptr, residual: Ptr, w2: Ptr, h_out: Ptr, out: Ptr, N: int,
+                  batch: int, eps: float = 1e-6, ops: Ptr = None) -> None:
+        """out = prologue(sum of nparts chunks of x_parts) per vector (rmsNorm / fusedNormAdd + rmsNorm);
+        `ops` (optional) receives the matrix-core operand blocks of out."""
+        check(lib().g4_batchPrep(self.h, _p(x_parts), nparts, _p(w1), _p(residual), _p(w2), _p(h_out), _p(out),
+                                 _p(ops), N, batch, eps))
+
+    def gateUpGeluBatch(self, x: Ptr, w_gate: Ptr, w_up: Ptr, out: Ptr, M: int, N: int, batch: int,
+                        ops: Ptr = None) -> None:
+        check(lib().g4_gateUpGeluBatch(self.h, _p(x), _p(ops), _p(w_gate), _p(w_up), _p(out), MatmulParams(M, N),
+                                       batch))
 
     # ---- attention (kv_cache_store / attn_score / softmax / attn_output) ----
     def kvCacheStore(self, k_in: Ptr, v_in: Ptr, k_cache: Ptr, v_cache: Ptr, num_kv_heads: int, head_dim: int,

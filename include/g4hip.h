@@ -355,27 +355,35 @@ int g4_normAddGateUpGeluBatch(g4_ctx* ctx, const float* o, const uint16_t* w_pos
 
 /* The pieces of a multi-sequence step, for callers that chain them without
  * an intermediate reduction (src/engine.ts:1545-1625 per sequence, for many
- * sequences at once):
+ * sequences at once).
  *
- * g4_matmulSegmentsBatchPartial: x [batch][N] f32 times up to 4 matrices on
- * the matrix cores, K split into *ksplit <= max_ksplit chunks (chosen to fill
- * the device); outputs[i] receives [*ksplit][batch][rows[i]] partial sums
- * (one chunk each) and must hold max_ksplit * batch * rows[i] floats. The
- * consumer adds the chunks in order: g4_batchPrep, g4_pagedAttnPrologue. */
-int g4_matmulSegmentsBatchPartial(g4_ctx* ctx, int wtype, const float* x,
+ * g4_batchPrep: x = the sum of the nparts chunks of x_parts
+ * [nparts][batch][N] (added in chunk order); then w1 == NULL: out = x;
+ * residual == NULL: out = x * w1 / rms(x) (rmsNorm); else
+ * h = residual + x * w1 / rms(x) (written to h_out when non-NULL) and
+ * out = h * w2 / rms(h) (fusedNormAdd -> rmsNorm). N is 1536 or 2048. When
+ * `ops` is non-NULL (batch <= 64) it also receives the matrix-core operand
+ * blocks of `out` (g4_batchOperandBytes bytes), which the matmul entries
+ * below take so that their workgroups need not rebuild them from `out`. */
+int g4_batchOperandBytes(uint32_t N, uint32_t batch, size_t* bytes);
+int g4_batchPrep(g4_ctx* ctx, const float* x_parts, uint32_t nparts, const uint16_t* w1,
+                 const float* residual, const uint16_t* w2, float* h_out, float* out, void* ops,
+                 uint32_t N, uint32_t batch, float eps);
+/* x [batch][N] f32 (with `ops` from g4_batchPrep of the same x, or NULL)
+ * times up to 4 matrices on the matrix cores, K split into
+ * *ksplit <= max_ksplit chunks (chosen to fill the device); outputs[i]
+ * receives [*ksplit][batch][rows[i]] partial sums (one chunk each) and must
+ * hold max_ksplit * batch * rows[i] floats. The consumer adds the chunks in
+ * order: g4_batchPrep, g4_pagedAttnPrologue. softcap_cap > 0 (tanh softcap
+ * of the outputs) needs max_ksplit == 1. */
+int g4_matmulSegmentsBatchPartial(g4_ctx* ctx, int wtype, const float* x, const void* ops,
                                   const void* const* weights, float* const* outputs,
                                   const uint32_t* rows, int nseg, uint32_t N, uint32_t batch,
-                                  uint32_t max_ksplit, uint32_t* ksplit);
-/* x = the sum of the nparts chunks of x_parts [nparts][batch][N]; then
- * w1 == NULL: out = x; residual == NULL: out = x * w1 / rms(x) (rmsNorm);
- * else h = residual + x * w1 / rms(x) (written to h_out when non-NULL) and
- * out = h * w2 / rms(h) (fusedNormAdd -> rmsNorm). N is 1536 or 2048. */
-int g4_batchPrep(g4_ctx* ctx, const float* x_parts, uint32_t nparts, const uint16_t* w1,
-                 const float* residual, const uint16_t* w2, float* h_out, float* out, uint32_t N,
-                 uint32_t batch, float eps);
-/* out = gelu(W_gate . x) * (W_up . x) for x [batch][p.N] (already normalised). */
-int g4_gateUpGeluBatch(g4_ctx* ctx, const float* x, const void* w_gate, const void* w_up,
-                       float* out, g4_matmul_params p, uint32_t batch);
+                                  uint32_t max_ksplit, float softcap_cap, uint32_t* ksplit);
+/* out = gelu(W_gate . x) * (W_up . x) for x [batch][p.N] (already
+ * normalised; `ops` as above). */
+int g4_gateUpGeluBatch(g4_ctx* ctx, const float* x, const void* ops, const void* w_gate,
+                       const void* w_up, float* out, g4_matmul_params p, uint32_t batch);
 
 /* ------------------------------------------------------------------------ */
 /* Debug / test exports                                                      */

@@ -132,6 +132,15 @@ def test_batch_prep_adds_partials_then_norms(ctx, B):
     w2 = O.gen_normal_f16(113, N, 1.0, 0.1)
     dh, dout = ctx.empty(B * N, np.float32), ctx.empty(B * N, np.float32)
     ctx.batchPrep(ctx.from_numpy(X), 3, ctx.from_numpy(w1), ctx.from_numpy(R), ctx.from_numpy(w2), dh, dout, N, B)
+    # the same with operand blocks, then a matmul that takes them: equal to the one that rebuilds them
+    dops = ctx.empty(ctx.batch_operand_bytes(N, B), np.uint8)
+    ctx.batchPrep(ctx.from_numpy(X), 3, ctx.from_numpy(w1), ctx.from_numpy(R), ctx.from_numpy(w2), None, dout, N, B,
+                  ops=dops)
+    Wm = O.gen_q4k(114, 512 * N // 256)
+    y1, y2 = ctx.empty(B * 512, np.float32), ctx.empty(B * 512, np.float32)
+    ctx.matmulSegmentsBatchPartial("q4k", dout, [ctx.from_numpy(Wm)], [y1], [512], N, B, 1)
+    ctx.matmulSegmentsBatchPartial("q4k", dout, [ctx.from_numpy(Wm)], [y2], [512], N, B, 1, ops=dops)
+    assert_close(y2.download(np.float32), y1.download(np.float32), rel=1e-6, cos=0.99999999, what="ops vs rebuilt")
     H, Y = dh.download(np.float32).reshape(B, N), dout.download(np.float32).reshape(B, N)
     S = (X[0] + X[1]) + X[2]  # f32, chunk order
     for b in range(B):
