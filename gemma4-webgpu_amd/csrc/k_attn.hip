@@ -16,6 +16,8 @@
 //    q/k, kvCacheStore, attnScore, softmax, attnOutput in two launches).
 #include <math.h>
 
+#include <algorithm>
+
 #include "g4_internal.hpp"
 
 namespace {
@@ -525,9 +527,26 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
 // combine online and the groups combine through LDS at the end.
 constexpr int MS = 16;
 
+// Live length of a sequence's attention window (as attn_kernel forms it).
+struct LenArgs {
+  const uint32_t* seq_lens;  // paged
+  const uint32_t* pos_dev;   // dense dev forms
+  uint32_t seq_len;          // dense host form
+  uint32_t cap, window;
+};
+__device__ __forceinline__ void live_window(const LenArgs& a, uint32_t seq, uint32_t& start, uint32_t& n) {
+  uint32_t L = a.seq_lens ? a.seq_lens[seq] : (a.pos_dev ? *a.pos_dev + 1 : a.seq_len);
+  L = min(L, a.cap);
+  start = (a.window != 0 && L > a.window) ? L - a.window : 0;
+  n = L - start;
+}
+
+// Splits past ceil(n / chunk) of a sequence are never read: the matrix-core
+// kernel does not launch workgroups for them.
 template <int HD>
 __global__ __launch_bounds__(1024) void attn_merge_kernel(const float* ws, float* out, uint32_t nqh, uint32_t nkh,
-                                                          uint32_t G, uint32_t nsplit, uint32_t num_seqs) {
+                                                          uint32_t G, uint32_t nsplit, uint32_t num_seqs,
+                                                          LenArgs la, uint32_t chunk) {
   constexpr int MG = 1024 / HD;  // split groups (thread g*HD + d owns column d of group g)
   __shared__ float gm_s[MG], gl_s[MG];
   __shared__ float go_s[MG > 1 ? (MG - 1) * HD : 1];
@@ -539,6 +558,9 @@ __global__ __launch_bounds__(1024) void attn_merge_kernel(const float* ws, float
   const float* ws_o = ws + 2 * nparts;
   const size_t base = ((size_t)seq * nkh + kvh) * nsplit * G + h;
   const uint32_t tid = threadIdx.x, d = tid % HD, grp = tid / HD;
+  uint32_t wstart, n;
+  live_window(la, seq, wstart, n);
+  nsplit = min(nsplit, (n + chunk - 1) / chunk);
   float M = -INFINITY, Ls = 0.f, acc = 0.f;
   for (uint32_t s0 = grp * MS; s0 < nsplit; s0 += MG * MS) {
     float mm[MS], ll[MS], oo[MS];
@@ -582,6 +604,260 @@ __global__ __launch_bounds__(1024) void attn_merge_kernel(const float* ws, float
     to += wg * (g == 0 ? acc : go_s[(g - 1) * HD + d]);
   }
   out[((size_t)seq * nqh + hq) * HD + d] = tl > 0.f ? to / tl : 0.f;
+}
+
+// ---------------------------------------------------------------------------
+// matrix-core split-K decode attention: 8 query heads per KV head, head_dim 256
+// ---------------------------------------------------------------------------
+//
+// Workgroup = (chunk of 64 * nstep consecutive positions of one sequence's
+// window, KV head); workgroups are numbered over the sequences' live chunks
+// only. Each step stages 64 positions of K and V in LDS (rows padded to
+// 528 B so that the 16 rows an MFMA operand reads fall on different banks)
+// while the next step's rows are loaded; wave w takes positions
+// 16w .. 16w+15 of the step:
+//  * scores: v_mfma_f32_16x16x32_f16 with A = 16 K rows x 32 dims and
+//    B = 16 columns holding q_hi (columns 0-7) and q_lo (8-15) of the 8 heads,
+//    so S[pos][h] = D[pos][h] + D[pos][h + 8] (one DPP row rotate by 8).
+//  * online softmax per head over the wave's positions (running m, l).
+//  * PV: v_mfma_f32_16x16x16_f16 with A = rows (p_hi | p_lo) x 16 positions,
+//    which is exactly the layout the score MFMA left p in, and B = 4
+//    positions x 16 dims of V; 16 dim tiles.
+// At the end the four waves' (m, l, o) are combined in LDS and one partial
+// per head is written for attn_merge_kernel.
+typedef _Float16 mh8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mh4 __attribute__((ext_vector_type(4)));
+typedef float mf4 __attribute__((ext_vector_type(4)));
+typedef uint32_t mu4 __attribute__((ext_vector_type(4)));
+
+constexpr int MQ_STEP = 64;  // positions per step
+constexpr int MQ_RS = 264;   // LDS row stride in halves (528 B)
+constexpr int MQ_G = 8, MQ_HD = 256;
+constexpr int kDppRor8 = 0x128;  // row_ror:8 within 16 lanes
+
+struct MqArgs {
+  const float* q;  // [num_seqs][nqh][256]
+  const uint16_t* kc;
+  const uint16_t* vc;
+  const int32_t* page_table;  // paged: [num_seqs][max_pages]
+  uint32_t page_size, max_pages, num_pages;
+  LenArgs len;
+  uint32_t num_seqs, nqh, nkh;
+  float scale;
+  uint32_t nstep;       // steps per workgroup
+  uint32_t max_chunks;  // partial slots per (sequence, KV head)
+  float* ws;
+};
+
+template <bool PAGED>
+__global__ __launch_bounds__(NT, 2) void mq_attn_kernel(MqArgs a) {
+  __shared__ __align__(16) _Float16 kt[MQ_STEP * MQ_RS];
+  __shared__ __align__(16) _Float16 vt[MQ_STEP * MQ_RS];
+  __shared__ uint32_t s_seq, s_chunk;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q = l >> 4, c = l & 15;
+  const uint32_t kvh = blockIdx.y;
+  const uint32_t CH = MQ_STEP * a.nstep;
+
+  // ---- this workgroup's (sequence, chunk) in the order of live chunks ----
+  if (w == 0) {
+    uint32_t nch = 0;
+    if ((uint32_t)l < a.num_seqs) {
+      uint32_t st, n;
+      live_window(a.len, (uint32_t)l, st, n);
+      nch = (n + CH - 1) / CH;
+    }
+    uint32_t incl = nch;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t t = __shfl_up(incl, o, 64);
+      if (l >= o) incl += t;
+    }
+    const unsigned long long hit = __ballot(incl > blockIdx.x);
+    const int sq = hit ? __ffsll(hit) - 1 : 0;
+    const uint32_t before = __shfl(incl - nch, sq, 64);
+    if (l == 0) {
+      s_seq = hit ? (uint32_t)sq : 0xffffffffu;
+      s_chunk = blockIdx.x - before;
+    }
+  }
+  __syncthreads();
+  const uint32_t seq = s_seq;
+  if (seq == 0xffffffffu) return;  // past the last live chunk (uniform)
+  const uint32_t chunk = s_chunk;
+  uint32_t wstart, n;
+  live_window(a.len, seq, wstart, n);
+  const uint32_t c0 = chunk * CH;          // chunk start within the window
+  const uint32_t cend = min(n, c0 + CH);   // > c0
+  const uint32_t last = wstart + cend - 1; // last live position of the chunk
+  const uint32_t nst = (cend - c0 + MQ_STEP - 1) / MQ_STEP;
+
+  auto row_of = [&](uint32_t pos) -> size_t {
+    if constexpr (PAGED) {
+      int32_t pg = a.page_table[(size_t)seq * a.max_pages + pos / a.page_size];
+      pg = pg < 0 ? 0 : (pg >= (int32_t)a.num_pages ? (int32_t)a.num_pages - 1 : pg);
+      return (size_t)pg * a.page_size + pos % a.page_size;
+    }
+    return pos;
+  };
+  // K (pieces 0-7) and V (8-15) of one step: piece tid + 256i covers row
+  // (tid + 256i) / 32 % 64, dims 8 * (tid % 32) .. +7; rows past the chunk
+  // repeat its last live position (masked in the scores)
+  mu4 pf[16];
+  auto load_step = [&](uint32_t st) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t pc = (uint32_t)tid + 256u * (uint32_t)(i & 7);
+      const uint32_t r = pc >> 5, col = (pc & 31) * 8;
+      const uint32_t pos = min(wstart + c0 + st * MQ_STEP + r, last);
+      const uint16_t* base = i < 8 ? a.kc : a.vc;
+      pf[i] = *(const mu4*)(base + (row_of(pos) * a.nkh + kvh) * MQ_HD + col);
+    }
+  };
+  auto store_step = [&]() {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t pc = (uint32_t)tid + 256u * (uint32_t)(i & 7);
+      const uint32_t r = pc >> 5, col = (pc & 31) * 8;
+      _Float16* dst = (i < 8 ? kt : vt) + r * MQ_RS + col;
+      *(mu4*)dst = pf[i];
+    }
+  };
+
+  load_step(0);
+  // q as the scores' B operand: column c = (part c/8, head c%8), dims 32j + 8q .. +7
+  const float* qg = a.q + ((size_t)seq * a.nqh + kvh * MQ_G + (c & 7)) * MQ_HD;
+  float4 qr[16];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    qr[2 * j] = *(const float4*)(qg + 32 * j + 8 * q);
+    qr[2 * j + 1] = *(const float4*)(qg + 32 * j + 8 * q + 4);
+  }
+  mh8 qb[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float xs[8] = {qr[2 * j].x, qr[2 * j].y, qr[2 * j].z, qr[2 * j].w,
+                         qr[2 * j + 1].x, qr[2 * j + 1].y, qr[2 * j + 1].z, qr[2 * j + 1].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const _Float16 hi = (_Float16)xs[e];
+      qb[j][e] = c < 8 ? hi : (_Float16)(xs[e] - (float)hi);
+    }
+  }
+  store_step();
+  __syncthreads();
+
+  mf4 O[16];
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) O[dt] = mf4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;  // of head c % 8
+
+  for (uint32_t st = 0; st < nst; ++st) {
+    const bool more = st + 1 < nst;
+    load_step(more ? st + 1 : st);  // the next step's rows are in flight during this one
+
+    // ---- scores of the wave's 16 positions ----
+    mf4 S = mf4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const mh8 A = *(const mh8*)(kt + (16 * w + c) * MQ_RS + 32 * j + 8 * q);
+      S = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, qb[j], S, 0, 0, 0);
+    }
+    float sc[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = S[i] + g4d::dpp<kDppRor8>(S[i]);  // q_hi + q_lo columns
+      const uint32_t off = c0 + st * MQ_STEP + 16u * w + 4u * q + i;
+      sc[i] = off < cend ? v * a.scale : -INFINITY;
+      mx = fmaxf(mx, sc[i]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = m_new == -INFINITY ? 1.f : expf(m_run - m_new);
+    float p[4], ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = sc[i] == -INFINITY ? 0.f : expf(sc[i] - m_new);
+      ps += p[i];
+    }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+    // rows of O held here: 4q + i = (part, head 4(q&1) + i)
+    float ar[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a0 = g4d::lane_value(alpha, i), a1 = g4d::lane_value(alpha, 4 + i);
+      ar[i] = (q & 1) ? a1 : a0;
+    }
+    mh4 P;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const _Float16 hi = (_Float16)p[i];
+      P[i] = c < 8 ? hi : (_Float16)(p[i] - (float)hi);
+    }
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) {
+      mh4 Bv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Bv[i] = vt[(16 * w + 4 * q + i) * MQ_RS + 16 * dt + c];
+      mf4 o = O[dt];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] *= ar[i];
+      O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(P, Bv, o, 0, 0, 0);
+    }
+    __syncthreads();  // every wave is done with this step's rows
+    if (more) {
+      store_step();
+      __syncthreads();
+    }
+  }
+
+  // ---- combine the hi and lo rows, then the four waves ----
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) O[dt][i] += __shfl_xor(O[dt][i], 32, 64);
+  float* ow = (float*)kt;                 // [4 waves][8 heads][256]
+  float* mw = (float*)vt;                 // [4][8]
+  float* lw = mw + 32;                    // [4][8]
+  if (q < 2) {
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ow[(w * MQ_G + 4 * q + i) * MQ_HD + 16 * dt + c] = O[dt][i];
+  }
+  if (q == 0 && c < MQ_G) {
+    mw[w * MQ_G + c] = m_run;
+    lw[w * MQ_G + c] = l_run;
+  }
+  __syncthreads();
+  const size_t part = (((size_t)seq * a.nkh + kvh) * a.max_chunks + chunk) * MQ_G;
+  const size_t nparts = (size_t)a.num_seqs * a.nkh * a.max_chunks * MQ_G;
+  float* ws_m = a.ws;
+  float* ws_l = ws_m + nparts;
+  float* ws_o = ws_m + 2 * nparts;
+#pragma unroll
+  for (int h = 0; h < MQ_G; ++h) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, mw[ww * MQ_G + h]);
+    float L = 0.f, o = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float m = mw[ww * MQ_G + h];
+      const float wt = m == -INFINITY ? 0.f : expf(m - M);
+      L += wt * lw[ww * MQ_G + h];
+      o += wt * ow[(ww * MQ_G + h) * MQ_HD + tid];
+    }
+    ws_o[(part + h) * MQ_HD + tid] = o;
+    if (tid == 0) {
+      ws_m[part + h] = M;
+      ws_l[part + h] = L;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -778,25 +1054,71 @@ int launch_attn(g4_ctx* ctx, const AttnArgs& a, uint32_t G, uint32_t hd, int cp,
                        hd);
 }
 
-int merge(g4_ctx* ctx, const AttnArgs& a, float* out, const SplitPlan& sp, uint32_t num_seqs, uint32_t G,
-          uint32_t hd) {
-  const dim3 mg(a.nqh, num_seqs);
+LenArgs len_args(const AttnArgs& a) { return LenArgs{a.seq_lens, a.pos_dev, a.seq_len, a.cap, a.window}; }
+
+int merge_launch(g4_ctx* ctx, const float* ws, float* out, uint32_t nqh, uint32_t nkh, uint32_t G, uint32_t hd,
+                 uint32_t nsplit, uint32_t num_seqs, const LenArgs& la, uint32_t chunk) {
+  const dim3 mg(nqh, num_seqs);
   switch (hd) {
     case 128:
-      hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(1024), 0, ctx->stream, (const float*)a.ws, out, a.nqh, a.nkh,
-                         G, sp.nsplit, num_seqs);
+      hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(1024), 0, ctx->stream, ws, out, nqh, nkh, G, nsplit,
+                         num_seqs, la, chunk);
       break;
     case 256:
-      hipLaunchKernelGGL(attn_merge_kernel<256>, mg, dim3(1024), 0, ctx->stream, (const float*)a.ws, out, a.nqh, a.nkh,
-                         G, sp.nsplit, num_seqs);
+      hipLaunchKernelGGL(attn_merge_kernel<256>, mg, dim3(1024), 0, ctx->stream, ws, out, nqh, nkh, G, nsplit,
+                         num_seqs, la, chunk);
       break;
     default:
-      hipLaunchKernelGGL(attn_merge_kernel<512>, mg, dim3(1024), 0, ctx->stream, (const float*)a.ws, out, a.nqh, a.nkh,
-                         G, sp.nsplit, num_seqs);
+      hipLaunchKernelGGL(attn_merge_kernel<512>, mg, dim3(1024), 0, ctx->stream, ws, out, nqh, nkh, G, nsplit,
+                         num_seqs, la, chunk);
       break;
   }
   G4_LAUNCHED(ctx, "attn_merge");
   return G4_OK;
+}
+
+int merge(g4_ctx* ctx, const AttnArgs& a, float* out, const SplitPlan& sp, uint32_t num_seqs, uint32_t G,
+          uint32_t hd) {
+  return merge_launch(ctx, a.ws, out, a.nqh, a.nkh, G, hd, sp.nsplit, num_seqs, len_args(a), sp.chunk);
+}
+
+// The matrix-core kernel serves 8 query heads per KV head at head_dim 256 and
+// up to 64 sequences (its chunk numbering runs in one wave).
+bool mq_fits(uint32_t G, uint32_t hd, uint32_t num_seqs) { return G == 8 && hd == 256 && num_seqs <= 64; }
+
+// Steps per workgroup from the largest window, sized for about four
+// workgroups per CU when every sequence is that long.
+int mq_decode(g4_ctx* ctx, const char* fn, const AttnArgs& base, bool paged, uint32_t num_seqs, float* out,
+              size_t ws_len) {
+  const uint32_t eff = eff_len(base.cap, base.window);
+  const uint64_t cus = ctx->num_cus > 0 ? (uint64_t)ctx->num_cus : 256;
+  const uint64_t want = ((uint64_t)num_seqs * eff + 64 * 4 * cus - 1) / (64 * 4 * cus);
+  const uint32_t nstep = (uint32_t)std::min<uint64_t>(std::max<uint64_t>(want, 1), 16);
+  const uint32_t chunk = MQ_STEP * nstep;
+  const uint32_t max_chunks = ceil_div(eff == 0 ? 1 : eff, chunk);
+  const size_t need = ws_bytes(num_seqs, base.nkh, max_chunks, MQ_G, MQ_HD);
+  G4_REQUIRE(ws_len >= need, "%s: workspace %zu bytes < %zu required", fn, ws_len, need);
+  MqArgs m{};
+  m.q = base.q;
+  m.kc = base.kc;
+  m.vc = base.vc;
+  m.page_table = base.page_table;
+  m.page_size = base.page_size;
+  m.max_pages = base.max_pages;
+  m.num_pages = base.num_pages;
+  m.len = len_args(base);
+  m.num_seqs = num_seqs;
+  m.nqh = base.nqh;
+  m.nkh = base.nkh;
+  m.scale = base.scale;
+  m.nstep = nstep;
+  m.max_chunks = max_chunks;
+  m.ws = base.ws;
+  const dim3 grid(num_seqs * max_chunks, base.nkh);
+  if (paged) hipLaunchKernelGGL(mq_attn_kernel<true>, grid, dim3(NT), 0, ctx->stream, m);
+  else hipLaunchKernelGGL(mq_attn_kernel<false>, grid, dim3(NT), 0, ctx->stream, m);
+  G4_LAUNCHED(ctx, "attn_decode_mfma");
+  return merge_launch(ctx, base.ws, out, base.nqh, base.nkh, MQ_G, MQ_HD, max_chunks, num_seqs, m.len, chunk);
 }
 
 int check_heads(const char* fn, uint32_t nqh, uint32_t nkh, uint32_t hd) {
@@ -848,6 +1170,7 @@ int dense_decode(g4_ctx* ctx, const char* fn, const float* q, const uint16_t* kc
   G4_REQUIRE(ws_len >= need, "%s: workspace %zu bytes < %zu required", fn, ws_len, need);
   const AttnArgs a = dense_args(q, kc, vc, p.num_q_heads, p.num_kv_heads, p.seq_len, p.scale, p.sliding_window,
                                 sp, ws, pos_dev);
+  if (mq_fits(G, p.head_dim, 1)) return mq_decode(ctx, fn, a, false, 1, out, ws_len);
   rc = launch_attn<false, false>(ctx, a, G, p.head_dim, sp.cp, dim3(sp.nsplit, p.num_kv_heads, 1));
   if (rc) return rc;
   return merge(ctx, a, out, sp, 1, G, p.head_dim);
@@ -1040,6 +1363,8 @@ int g4_pagedAttnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_pool, cons
   int rc = paged_setup(__func__, k_pool, v_pool, page_table, seq_lens, p, workspace, workspace_bytes, a, sp);
   if (rc) return rc;
   a.q = q;
+  if (mq_fits(p.num_q_heads / p.num_kv_heads, p.head_dim, p.num_seqs))
+    return mq_decode(ctx, __func__, a, true, p.num_seqs, output, workspace_bytes);
   rc = launch_attn<true, false>(ctx, a, p.num_q_heads / p.num_kv_heads, p.head_dim, sp.cp,
                                 dim3(sp.nsplit, p.num_kv_heads, p.num_seqs));
   if (rc) return rc;
