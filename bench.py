@@ -10,6 +10,11 @@ synthetic data generated on the device; the KV cache is pre-filled with
 N(0,1) f16 rows up to the start position. The fused step is captured once as
 a HIP graph and replayed; each replay advances the device-side position.
 
+The ragged multi-sequence step (B sequences with context lengths ~ U(128,
+8192) in a paged f16 pool of 16-token pages, every projection on the
+matrix-core kernel) is timed the same way at B = 32 and swept over B = 1, 8
+and 64; those figures go in `batch_decode` (aggregate tokens/s).
+
 Prints one JSON line. `value` is decoded tokens/s; `roofline` describes the
 kernel with the largest share of a step, timed with HIP events on the
 library's stream; `cpu_baseline` times the CPU oracle on a bounded sample.
@@ -26,7 +31,7 @@ sys.path.insert(0, os.path.join(ROOT, "gemma4-webgpu_amd"))
 import numpy as np  # noqa: E402
 
 import g4hip  # noqa: E402
-from g4hip.decoder import Decoder, E2BShape  # noqa: E402
+from g4hip.decoder import BatchDecoder, Decoder, E2BShape  # noqa: E402
 
 METRIC = "Q4_K GEMV GB/s (% of 8 TB/s peak); E2B decode tok/s at B=1 and B=32"
 HBM_PEAK_GBPS = 8000.0
@@ -152,6 +157,172 @@ def gemv_cfg0(ctx, copies=101, rounds=5):
             "frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, "copies": copies}
 
 
+def graph_us(ctx, body, reps):
+    """Average us of one replay of a graph holding body()'s launches."""
+    ctx.graph_begin()
+    try:
+        body()
+    finally:
+        g = ctx.graph_end()
+    ms = time_launches(ctx, lambda _i=0: ctx.graph_launch(g), reps)
+    ctx.graph_destroy(g)
+    return ms * 1e3
+
+
+def attention_cfg3(ctx, reps=3):
+    """Decode attention alone: 8 query heads, 1 KV head, head_dim 256, f16
+    K/V ~ N(0,1), one sequence, contexts 512 / 4096 / 32768, globally (no
+    window) and with the 512-position window. Every launch of a replay reads a
+    different window of a 302 MB K/V region (more than the 256 MB last-level
+    cache). Algorithmic bytes: L_eff * 1024 (f16 K and V rows) + q + output."""
+    nqh, nkh, hd, P = 8, 1, 256, 288 * 1024
+    k = ctx.empty(P * hd, np.uint16)
+    v = ctx.empty(P * hd, np.uint16)
+    ctx.fill_normal_f16(k, P * hd, 31, 0.0, 1.0)
+    ctx.fill_normal_f16(v, P * hd, 32, 0.0, 1.0)
+    q = ctx.empty(nqh * hd, np.float32)
+    ctx.fill_normal_f32(q, nqh * hd, 33, 0.0, 1.0)
+    out = ctx.empty(nqh * hd, np.float32)
+    res = {}
+    for L in (512, 4096, 32768):
+        for window in (0, 512):
+            if window and L <= window:
+                continue
+            ws = ctx.zeros(ctx.attn_workspace_bytes(nqh, nkh, hd, L, window), np.uint8)
+            n_rot = P // L
+
+            def body():
+                for r in range(n_rot):
+                    off = r * L * hd * 2
+                    ctx.attnDecode(q, k.offset(off), v.offset(off), out, nqh, nkh, hd, L, 1.0, window, workspace=ws)
+            us = graph_us(ctx, body, reps) / n_rot
+            l_eff = min(L, window) if window else L
+            nbytes = l_eff * 1024 + 2 * nqh * hd * 4
+            res[f"ctx{L}_{'window512' if window else 'global'}"] = {
+                "us": round(us, 2), "bytes": nbytes, "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+    k.free()
+    v.free()
+    return res
+
+
+def lm_head_sampling(ctx, reps=10):
+    """Tied Q6_K LM head [262144 x 1536] + softcap 30 + argmax and top-k 256,
+    at M = 1 and M = 8 hidden vectors ~ N(0,1) (the 330 MB matrix exceeds the
+    last-level cache, so replays stream it from HBM)."""
+    V, H = 262144, 1536
+    nb = V * H // 256
+    W = ctx.alloc(nb * 210)
+    ctx.fill_q6k(W, nb, 41)
+    res = {}
+    for M in (1, 8):
+        x = ctx.empty(M * H, np.float32)
+        ctx.fill_normal_f32(x, M * H, 42, 0.0, 1.0)
+        lg = ctx.empty(M * V, np.float32)
+        tok = ctx.empty(M, np.uint32)
+        tk = ctx.empty(M * 512, np.float32)
+
+        def head():
+            if M == 1:
+                ctx.matmulQuant(x, W, lg, V, H, "q6k")
+                ctx.logitSoftcap(lg, V, 30.0)
+            else:
+                ctx.normAddMatmulSegmentsBatch("q6k", x, None, None, None, None, [W], [lg], [V], H, M,
+                                               softcap=30.0)
+        us_head = graph_us(ctx, head, reps)
+        us_arg = graph_us(ctx, lambda: ctx.argmaxBatch(lg, tok, V, M), reps)
+        us_topk = graph_us(ctx, lambda: ctx.topk256Batch(lg, tk, V, M), reps)
+        nbytes = nb * 210 + M * H * 4 + M * V * 4
+        res[f"M={M}"] = {"head_softcap_us": round(us_head, 2), "argmax_us": round(us_arg, 2),
+                         "topk256_us": round(us_topk, 2), "head_bytes": nbytes,
+                         "head_gbps": round(nbytes / (us_head * 1e-6) / 1e9, 1)}
+    W.free()
+    return res
+
+
+def batch_census(ctx, bd, reps=10):
+    """Average us per launch kind of the ragged step, each kind captured over
+    all 35 layers (weights rotate through HBM as in the step)."""
+    c, s, B = ctx, bd.s, bd.B
+    H, Q, KV, I = s.hidden, s.q_dim, s.kv_dim, s.ffn
+    Ls = bd.layers
+    kinds = {
+        "prep_attn": lambda il, L: c.batchPrep(bd.down_parts, bd.ks_f // 2, L.post_ffn_norm, bd.hidden2, L.attn_norm,
+                                               bd.hidden, bd.xn, H, B, s.eps, ops=bd.xops),
+        "qkv": lambda il, L: c.matmulSegmentsBatchPartial("q4k", bd.xn, [L.wq, L.wk, L.wv],
+                                                          [bd.q_parts, bd.k_parts, bd.v_parts], [Q, KV, KV], H, B,
+                                                          bd.ks_h, ops=bd.xops),
+        "attn_prologue": lambda il, L: c.pagedAttnPrologue(bd.q_parts, bd.k_parts, bd.v_parts, bd.ks_h, L.q_norm,
+                                                           L.k_norm, bd.rope_freqs, bd.q, L.k_cache, L.v_cache,
+                                                           bd.page_table, bd.seq_lens, bd.pro_params[il]),
+        "attn_global": lambda il, L: (c.pagedAttnDecode(bd.q, L.k_cache, L.v_cache, bd.page_table, bd.seq_lens,
+                                                        bd.attn, bd.attn_params[il], bd.attn_ws)
+                                      if s.is_global(il) else "skip"),
+        "attn_window512": lambda il, L: (c.pagedAttnDecode(bd.q, L.k_cache, L.v_cache, bd.page_table, bd.seq_lens,
+                                                           bd.attn, bd.attn_params[il], bd.attn_ws)
+                                         if not s.is_global(il) else "skip"),
+        "o": lambda il, L: c.matmulSegmentsBatchPartial("q4k", bd.attn, [L.wo], [bd.o_parts], [H], Q, B, bd.ks_q),
+        "prep_ffn": lambda il, L: c.batchPrep(bd.o_parts, bd.ks_q, L.post_attn_norm, bd.hidden, L.pre_ffn_norm,
+                                              bd.hidden2, bd.xn, H, B, s.eps, ops=bd.xops),
+        "gate_up_gelu": lambda il, L: c.gateUpGeluBatch(bd.xn, L.wgate, L.wup, bd.act, I, H, B, ops=bd.xops),
+        "down": lambda il, L: c.matmulSegmentsBatchPartial("q6k", bd.act, [L.wdown], [bd.down_parts], [H], I, B,
+                                                           bd.ks_f),
+    }
+    out = {}
+    for name, body in kinds.items():
+        n = [0]
+
+        def run(body=body):
+            for il, L in enumerate(Ls):
+                if body(il, L) != "skip":
+                    n[0] += 1
+        us = graph_us(ctx, run, reps)
+        out[name] = {"us_per_launch": round(us / n[0], 2), "per_step_us": round(us, 1), "launches": n[0]}
+    us = graph_us(ctx, lambda: c.matmulSegmentsBatchPartial("q6k", bd.xn, [bd.lm_head], [bd.logits], [s.vocab], H,
+                                                            B, 1, ops=bd.xops, softcap=s.softcap), max(3, reps // 2))
+    out["lm_head_softcap"] = {"us_per_launch": round(us, 2), "per_step_us": round(us, 1), "launches": 1}
+    return out
+
+
+def batch_decode(ctx, B, steps, warmup, seed=0, census=False):
+    """Aggregate tok/s of the ragged B-sequence step replayed as a HIP graph.
+    Context lengths ~ U(128, 8192) (seeded); each replay appends one token
+    to every sequence. HBM bytes per step: all weights once, plus every
+    sequence's K/V window in every layer."""
+    lens = np.random.default_rng(1000 + B).integers(128, 8193, B)
+    t0 = time.time()
+    bd = BatchDecoder(ctx, lens, E2BShape(), reserve=warmup + steps + 8, seed=seed)
+    bd.fill_kv(seed=1)
+    ctx.sync()
+    s = bd.s
+    kv_bytes = bd.kv_bytes_per_step()
+    w_bytes = s.layer_weight_bytes() * s.n_layers + s.lm_head_bytes()
+    log(f"B={B}: decoder ready in {time.time() - t0:.1f}s, {bd.num_pages} pages, mean context {lens.mean():.0f}")
+    g = bd.capture("argmax")
+    for _ in range(warmup):
+        ctx.graph_launch(g)
+    ctx.sync()
+    a = ctx.record()
+    for _ in range(steps):
+        ctx.graph_launch(g)
+    b = ctx.record()
+    ms = ctx.elapsed_ms(a, b) / steps
+    ctx.sync()
+    final = bd.seq_lens.download(np.uint32)
+    ok = bool(np.array_equal(final, lens + warmup + steps))
+    ctx.graph_destroy(g)
+    cens = batch_census(ctx, bd) if census else None
+    del bd
+    res = {"B": B, "tok_s": round(B * 1000.0 / ms, 1), "ms_per_step": round(ms, 4),
+           "mean_context": round(float(lens.mean()), 1), "min_context": int(lens.min()),
+           "max_context": int(lens.max()), "kv_bytes_per_step": kv_bytes, "weight_bytes_per_step": w_bytes,
+           "hbm_gbps_alg": round((kv_bytes + w_bytes) / (ms * 1e-3) / 1e9, 1), "lengths_advanced": ok}
+    if cens is not None:
+        res["census_us"] = cens
+    log(f"B={B}: {res}")
+    return res
+
+
 def cpu_baseline(tokens=5):
     """Times the CPU oracle (plain C, 1 thread, f64 accumulation) on `tokens`
     whole decode steps of the same workload: 35 E2B-shaped layers at context
@@ -215,6 +386,10 @@ def main():
                          "(for profilers that do not follow graph launches)")
     ap.add_argument("--no-census", action="store_true")
     ap.add_argument("--no-gemv0", action="store_true")
+    ap.add_argument("--batch-steps", type=int, default=30)
+    ap.add_argument("--batch-warmup", type=int, default=5)
+    ap.add_argument("--batch-sweep", default="1,8,32,64",
+                    help="comma-separated batch sizes of the ragged step ('' to skip)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
@@ -264,8 +439,13 @@ def main():
     if not args.eager:
         ctx.graph_destroy(graph)
 
+    batch = {}
+    for B in [int(b) for b in args.batch_sweep.split(",") if b.strip()]:
+        batch[f"B={B}"] = batch_decode(ctx, B, args.batch_steps, args.batch_warmup, census=(B == 32 and not
+                                                                                              args.no_census))
     if args.no_census:
-        print(json.dumps({"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": ms_step}), flush=True)
+        print(json.dumps({"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": ms_step,
+                          "batch_decode": batch}), flush=True)
         return
     census = kernel_census(ctx, dec, args.census_reps)
     for k, v in census.items():
@@ -281,6 +461,10 @@ def main():
 
     g0 = {} if args.no_gemv0 else gemv_cfg0(ctx)
     log(f"config-0 Q4_K GEMV: {g0}")
+    attn3 = attention_cfg3(ctx)
+    log(f"decode attention: {attn3}")
+    head = lm_head_sampling(ctx)
+    log(f"LM head + sampling: {head}")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -310,6 +494,9 @@ def main():
         "cpu_baseline": cpu,
         "q4k_gemv_config0": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in g0.items()},
         "kernel_census_us": {k: round(per_step[k], 2) for k in per_step},
+        "batch_decode": batch,
+        "attention_decode": attn3,
+        "lm_head_sampling": head,
         "device": info["name"],
     }
     print(json.dumps(line), flush=True)

@@ -860,6 +860,340 @@ __global__ __launch_bounds__(NT, 2) void mq_attn_kernel(MqArgs a) {
   }
 }
 
+// Fused single-sequence form over a dense cache (the one-token decode step),
+// the whole attention block of src/engine.ts:1556-1584 in one launch:
+//  * every workgroup applies q_norm + RoPE to q once, cooperatively (thread t
+//    owns head t / 32 and the RoPE pairs (d, d + 128), d = 4 (t % 32) + 0..3),
+//    and stages the MFMA B operand (q hi / lo columns) in LDS;
+//  * the workgroup that owns the current position forms that position's K/V
+//    row (k_norm + RoPE, weightless v_norm), writes it to the caches and
+//    patches it into its LDS tile;
+//  * each workgroup writes one (m, l, o) partial per head; the last one to
+//    arrive (arrival counter per KV head, reset for the next call) merges
+//    the chunks in chunk order.
+// With one sequence the grid is a few dozen workgroups, so latency is the
+// instruction count of one wave's path: the per-thread work outside the
+// MFMA loop is kept to a handful of vector operations.
+struct MqfArgs {
+  const float* q_raw;  // [nqh][256]
+  const float* k_raw;  // [nkh][256]
+  const float* v_raw;
+  const uint16_t* q_w;
+  const uint16_t* k_w;
+  const uint16_t* rope_freqs;
+  float theta;
+  uint32_t apply_divisor;
+  float eps;
+  uint16_t* kc;  // [cap][nkh][256]
+  uint16_t* vc;
+  const uint32_t* pos_dev;
+  uint32_t cap, nqh, nkh;
+  float scale;
+  uint32_t window;
+  uint32_t nstep, max_chunks;
+  float* ws;      // partials [nkh][max_chunks][8] (m, l, o)
+  uint32_t* cnt;  // [nkh] arrivals, zero between calls
+  float* out;     // [nqh][256]
+};
+
+constexpr int MQF_QS = 264;  // LDS stride of a q column (halves)
+
+__global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
+  // K and V tiles; after the last step, the waves' o rows [4 waves][256 dims][16 rows]
+  __shared__ __align__(16) _Float16 kvt[2 * MQ_STEP * MQ_RS];
+  __shared__ __align__(16) _Float16 qs[16 * MQF_QS];  // B operand: column c = head c % 8, hi (c < 8) / lo
+  __shared__ float2 cs_s[MQ_HD / 2];
+  __shared__ float red_s[8];
+  __shared__ float kn_s[MQ_HD];
+  __shared__ __align__(16) uint16_t cur_s[2 * MQ_HD];  // the current row: k (roped), v; f16
+  __shared__ float ml_s[2 * 4 * MQ_G];                 // per (wave, head) m, then l
+  __shared__ __align__(16) float wt_s[4 * MQ_G];       // per (wave, head) weight
+  __shared__ uint32_t s_last;
+  _Float16* const kt = kvt;
+  _Float16* const vt = kvt + MQ_STEP * MQ_RS;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q = l >> 4, c = l & 15;
+  const uint32_t kvh = blockIdx.y, chunk = blockIdx.x;
+  const uint32_t CH = MQ_STEP * a.nstep;
+  const uint32_t L = min(*a.pos_dev + 1, a.cap);
+  const uint32_t pos = L - 1;  // the position being decoded
+  const uint32_t wstart = (a.window != 0 && L > a.window) ? L - a.window : 0;
+  const uint32_t n = L - wstart;
+  const uint32_t nch = (n + CH - 1) / CH;
+  if (chunk >= nch) return;  // (uniform) past the live chunks
+  const uint32_t c0 = chunk * CH, cend = min(n, c0 + CH), last = wstart + cend - 1;
+  const uint32_t nst = (cend - c0 + MQ_STEP - 1) / MQ_STEP;
+  const bool owner = cend == n;  // this chunk ends at the current position
+  // thread -> (head, 4 dims of each RoPE half) for q, the partial and the merge
+  const int th = tid >> 5, td = 4 * (tid & 31);
+
+  mu4 pf[16];
+  auto load_step = [&](uint32_t st) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t pc = (uint32_t)tid + 256u * (uint32_t)(i & 7);
+      const uint32_t r = pc >> 5, col = (pc & 31) * 8;
+      const uint32_t p = min(wstart + c0 + st * MQ_STEP + r, last);
+      const uint16_t* base = i < 8 ? a.kc : a.vc;
+      pf[i] = *(const mu4*)(base + ((size_t)p * a.nkh + kvh) * MQ_HD + col);
+    }
+  };
+  auto store_step = [&]() {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t pc = (uint32_t)tid + 256u * (uint32_t)(i & 7);
+      const uint32_t r = pc >> 5, col = (pc & 31) * 8;
+      *(mu4*)((i < 8 ? kt : vt) + r * MQ_RS + col) = pf[i];
+    }
+  };
+  // the owner's last step: rows from the current position on (the clamped
+  // rows repeat it) take the row formed here, not the cache's stale one
+  auto patch = [&](uint32_t st) {
+    const uint32_t r0 = last - (wstart + c0 + st * MQ_STEP);
+    for (uint32_t e = (uint32_t)tid; e < (MQ_STEP - r0) * 32; e += NT) {
+      const uint32_t r = r0 + e / 32, col = (e % 32) * 8;
+      *(mu4*)(kt + r * MQ_RS + col) = *(const mu4*)(cur_s + col);
+      *(mu4*)(vt + r * MQ_RS + col) = *(const mu4*)(cur_s + MQ_HD + col);
+    }
+  };
+
+  // ---- every load of the prologue, then the first step's rows ----
+  const float* qg = a.q_raw + (size_t)(kvh * MQ_G + th) * MQ_HD + td;
+  const float4 q0 = *(const float4*)qg, q1 = *(const float4*)(qg + MQ_HD / 2);
+  const uint2 w0 = *(const uint2*)(a.q_w + td), w1 = *(const uint2*)(a.q_w + MQ_HD / 2 + td);
+  const float kx = a.k_raw[(size_t)kvh * MQ_HD + tid], vx = a.v_raw[(size_t)kvh * MQ_HD + tid];
+  const float kw = g4d::f16_bits_to_f32(a.k_w[tid]);
+  const uint16_t rfb = a.rope_freqs[tid & (MQ_HD / 2 - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  load_step(0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // RoPE of this position: frequency and angle as
+  // shaders/fused_per_head_norm_rope.wgsl:50-55 form them, cos/sin in f32
+  if (tid < MQ_HD / 2) {
+    float f = (float)(1.0 / pow((double)a.theta, (double)(2 * tid) / (double)MQ_HD));
+    if (a.apply_divisor) f = f / g4d::f16_bits_to_f32(rfb);
+    const float ang = (float)pos * f;
+    float sn, cn;
+    sincosf(ang, &sn, &cn);
+    cs_s[tid] = make_float2(cn, sn);
+  }
+  const float sk = g4d::wave_sum_dpp(kx * kx), sv = g4d::wave_sum_dpp(vx * vx);
+  if (l == 0) {
+    red_s[w] = sk;
+    red_s[4 + w] = sv;
+  }
+  // q: the head's sum of squares over its 32 threads (two DPP rows)
+  float qss = (q0.x * q0.x + q0.y * q0.y) + (q0.z * q0.z + q0.w * q0.w) + (q1.x * q1.x + q1.y * q1.y) +
+              (q1.z * q1.z + q1.w * q1.w);
+  qss = g4d::sum16(qss);
+  qss += __shfl_xor(qss, 16, 64);
+  const float invq = 1.0f / sqrtf(qss / (float)MQ_HD + a.eps);
+  __syncthreads();
+  const float invk = 1.0f / sqrtf(((red_s[0] + red_s[1]) + (red_s[2] + red_s[3])) / (float)MQ_HD + a.eps);
+  const float invv = 1.0f / sqrtf(((red_s[4] + red_s[5]) + (red_s[6] + red_s[7])) / (float)MQ_HD + a.eps);
+  kn_s[tid] = kx * kw * invk;
+  cur_s[MQ_HD + tid] = g4d::f32_to_f16_bits(vx * invv);
+  {
+    const float x0[4] = {q0.x, q0.y, q0.z, q0.w}, x1[4] = {q1.x, q1.y, q1.z, q1.w};
+    const uint32_t wa[4] = {w0.x & 0xffffu, w0.x >> 16, w0.y & 0xffffu, w0.y >> 16};
+    const uint32_t wb[4] = {w1.x & 0xffffu, w1.x >> 16, w1.y & 0xffffu, w1.y >> 16};
+    mh4 h0, l0, h1, l1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float2 cs = cs_s[td + e];
+      const float y0 = x0[e] * g4d::f16_bits_to_f32(wa[e]) * invq;
+      const float y1 = x1[e] * g4d::f16_bits_to_f32(wb[e]) * invq;
+      const float r0 = y0 * cs.x - y1 * cs.y, r1 = y0 * cs.y + y1 * cs.x;
+      h0[e] = (_Float16)r0;
+      l0[e] = (_Float16)(r0 - (float)h0[e]);
+      h1[e] = (_Float16)r1;
+      l1[e] = (_Float16)(r1 - (float)h1[e]);
+    }
+    *(mh4*)(qs + th * MQF_QS + td) = h0;
+    *(mh4*)(qs + (th + 8) * MQF_QS + td) = l0;
+    *(mh4*)(qs + th * MQF_QS + MQ_HD / 2 + td) = h1;
+    *(mh4*)(qs + (th + 8) * MQF_QS + MQ_HD / 2 + td) = l1;
+  }
+  __syncthreads();
+  if (tid < MQ_HD / 2) {
+    const float2 cs = cs_s[tid];
+    const float x0 = kn_s[tid], x1 = kn_s[tid + MQ_HD / 2];
+    cur_s[tid] = g4d::f32_to_f16_bits(x0 * cs.x - x1 * cs.y);
+    cur_s[tid + MQ_HD / 2] = g4d::f32_to_f16_bits(x0 * cs.y + x1 * cs.x);
+  }
+  store_step();
+  __syncthreads();
+  if (owner) {
+    a.kc[((size_t)pos * a.nkh + kvh) * MQ_HD + tid] = cur_s[tid];
+    a.vc[((size_t)pos * a.nkh + kvh) * MQ_HD + tid] = cur_s[MQ_HD + tid];
+    if (nst == 1) patch(0);
+  }
+  mh8 qb[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) qb[j] = *(const mh8*)(qs + c * MQF_QS + 32 * j + 8 * q);
+  __syncthreads();
+
+  mf4 O[16];
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) O[dt] = mf4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;  // of head c % 8
+
+  for (uint32_t st = 0; st < nst; ++st) {
+    const bool more = st + 1 < nst;
+    if (more) load_step(st + 1);
+    mf4 S = mf4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const mh8 A = *(const mh8*)(kt + (16 * w + c) * MQ_RS + 32 * j + 8 * q);
+      S = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, qb[j], S, 0, 0, 0);
+    }
+    float sc[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = S[i] + g4d::dpp<kDppRor8>(S[i]);
+      const uint32_t off = c0 + st * MQ_STEP + 16u * w + 4u * q + i;
+      sc[i] = off < cend ? v * a.scale : -INFINITY;
+      mx = fmaxf(mx, sc[i]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = m_new == -INFINITY ? 1.f : expf(m_run - m_new);
+    float p[4], ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = sc[i] == -INFINITY ? 0.f : expf(sc[i] - m_new);
+      ps += p[i];
+    }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+    float ar[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a0 = g4d::lane_value(alpha, i), a1 = g4d::lane_value(alpha, 4 + i);
+      ar[i] = (q & 1) ? a1 : a0;
+    }
+    mh4 P;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const _Float16 hi = (_Float16)p[i];
+      P[i] = c < 8 ? hi : (_Float16)(p[i] - (float)hi);
+    }
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) {
+      mh4 Bv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Bv[i] = vt[(16 * w + 4 * q + i) * MQ_RS + 16 * dt + c];
+      mf4 o = O[dt];
+      if (st > 0) {  // (uniform) the first step's O is zero
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] *= ar[i];
+      }
+      O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(P, Bv, o, 0, 0, 0);
+    }
+    __syncthreads();
+    if (more) {
+      store_step();
+      if (owner && st + 2 == nst) {  // (uniform) the patched rows are stored rows: order the two writes
+        __syncthreads();
+        patch(st + 1);
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---- the four waves, then this chunk's partial ----
+  // O row 4q + i of lane (q, c) is head (4q + i) % 8 (the p_hi rows for
+  // q < 2, the p_lo rows for q >= 2) at dim 16 dt + c.
+  float* ow = (float*)kvt;
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) *(mf4*)(ow + ((w * MQ_HD) + 16 * dt + c) * 16 + 4 * q) = O[dt];
+  if (q == 0 && c < MQ_G) {
+    ml_s[w * MQ_G + c] = m_run;
+    ml_s[4 * MQ_G + w * MQ_G + c] = l_run;
+  }
+  __syncthreads();
+  const size_t nparts = (size_t)a.nkh * a.max_chunks * MQ_G;
+  float* ws_m = a.ws;
+  float* ws_l = ws_m + nparts;
+  float* ws_o = ws_m + 2 * nparts;
+  const size_t part0 = ((size_t)kvh * a.max_chunks + chunk) * MQ_G;
+  if (tid < MQ_G) {  // thread h: the head's weight per wave and the chunk's (m, l)
+    float m4[4], M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      m4[ww] = ml_s[ww * MQ_G + tid];
+      M = fmaxf(M, m4[ww]);
+    }
+    float Ls = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float wt = m4[ww] == -INFINITY ? 0.f : expf(m4[ww] - M);
+      wt_s[ww * MQ_G + tid] = wt;
+      Ls += wt * ml_s[4 * MQ_G + ww * MQ_G + tid];
+    }
+    ws_m[part0 + tid] = M;
+    ws_l[part0 + tid] = Ls;
+  }
+  __syncthreads();
+  {  // thread = dim: o[h] = sum over waves of wt * (hi row + lo row)
+    float o[MQ_G];
+#pragma unroll
+    for (int h = 0; h < MQ_G; ++h) o[h] = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float* r = ow + (ww * MQ_HD + tid) * 16;
+      const mf4 h03 = *(const mf4*)r, h47 = *(const mf4*)(r + 4), l03 = *(const mf4*)(r + 8),
+                l47 = *(const mf4*)(r + 12);
+      const mf4 w03 = *(const mf4*)(wt_s + ww * MQ_G), w47 = *(const mf4*)(wt_s + ww * MQ_G + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[i] += w03[i] * (h03[i] + l03[i]);
+        o[4 + i] += w47[i] * (h47[i] + l47[i]);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < MQ_G; ++h) ws_o[(part0 + h) * MQ_HD + tid] = o[h];
+  }
+
+  // ---- the last workgroup of this KV head merges the chunks in order ----
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) s_last = atomicAdd(&a.cnt[kvh], 1u) == nch - 1 ? 1u : 0u;
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  // thread (head th, dims td.. and td + 128..): one pass in chunk order with
+  // a running maximum
+  float M = -INFINITY, Ls = 0.f;
+  float4 o0 = make_float4(0.f, 0.f, 0.f, 0.f), o1 = o0;
+  const size_t pb = (size_t)kvh * a.max_chunks * MQ_G + th;
+#pragma unroll 4
+  for (uint32_t s2 = 0; s2 < nch; ++s2) {
+    const size_t pp = pb + (size_t)s2 * MQ_G;
+    const float m = ws_m[pp], lv = ws_l[pp];
+    const float4 a0 = *(const float4*)(ws_o + pp * MQ_HD + td);
+    const float4 a1 = *(const float4*)(ws_o + pp * MQ_HD + MQ_HD / 2 + td);
+    const float Mn = fmaxf(M, m);
+    const float fo = M == -INFINITY ? 0.f : expf(M - Mn);
+    const float fn = m == -INFINITY ? 0.f : expf(m - Mn);
+    Ls = Ls * fo + lv * fn;
+    o0.x = o0.x * fo + a0.x * fn; o0.y = o0.y * fo + a0.y * fn;
+    o0.z = o0.z * fo + a0.z * fn; o0.w = o0.w * fo + a0.w * fn;
+    o1.x = o1.x * fo + a1.x * fn; o1.y = o1.y * fo + a1.y * fn;
+    o1.z = o1.z * fo + a1.z * fn; o1.w = o1.w * fo + a1.w * fn;
+    M = Mn;
+  }
+  const float li = Ls > 0.f ? 1.0f / Ls : 0.f;
+  float* dst = a.out + ((size_t)kvh * MQ_G + th) * MQ_HD + td;
+  *(float4*)dst = make_float4(o0.x * li, o0.y * li, o0.z * li, o0.w * li);
+  *(float4*)(dst + MQ_HD / 2) = make_float4(o1.x * li, o1.y * li, o1.z * li, o1.w * li);
+  if (tid == 0) atomicExch(&a.cnt[kvh], 0u);
+}
+
 // ---------------------------------------------------------------------------
 // paged prologue (multi-sequence step): per sequence, the q/k/v projections
 // (sums of split-K partials, added in chunk order) through q_norm + RoPE,
@@ -1052,6 +1386,24 @@ int launch_attn(g4_ctx* ctx, const AttnArgs& a, uint32_t G, uint32_t hd, int cp,
 #undef G4_ATTN_CASE
   return g4::set_error(G4_ERR_UNSUPPORTED, "attention: %u query heads per kv head with head_dim %u not built", G,
                        hd);
+}
+
+// Fused single-sequence plan: at most 64 chunks (the last workgroup merges
+// them in one wave). The arrival counters sit in the first kMqfCnt bytes of
+// the workspace, at the same place whatever the plan, so that layers of
+// different windows can share one workspace; the partials follow.
+constexpr size_t kMqfCnt = 256;
+struct MqfPlan {
+  uint32_t nstep, max_chunks;
+  size_t bytes;
+};
+MqfPlan mqf_plan(const g4_attn_fused_params& p) {
+  MqfPlan m{};
+  const uint32_t eff = std::max(eff_len(p.max_seq_len, p.sliding_window), 1u);
+  m.nstep = std::min(16u, std::max(1u, ceil_div(eff, MQ_STEP * 64)));
+  m.max_chunks = ceil_div(eff, MQ_STEP * m.nstep);
+  m.bytes = kMqfCnt + ws_bytes(1, p.num_kv_heads, m.max_chunks, MQ_G, MQ_HD);
+  return m;
 }
 
 LenArgs len_args(const AttnArgs& a) { return LenArgs{a.seq_lens, a.pos_dev, a.seq_len, a.cap, a.window}; }
@@ -1295,7 +1647,8 @@ int g4_attnDecodeFused_workspace_size(g4_attn_fused_params p, size_t* bytes) {
   const SplitPlan sp = plan_splits(eff_len(p.max_seq_len, p.sliding_window));
   rc = check_plan(__func__, sp);
   if (rc) return rc;
-  *bytes = ws_bytes(1, p.num_kv_heads, sp.nsplit, p.num_q_heads / p.num_kv_heads, p.head_dim);
+  const size_t old = ws_bytes(1, p.num_kv_heads, sp.nsplit, p.num_q_heads / p.num_kv_heads, p.head_dim);
+  *bytes = std::max(old, mqf_plan(p).bytes);
   return G4_OK;
 }
 
@@ -1316,6 +1669,38 @@ int g4_attnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw, cons
   const uint32_t G = p.num_q_heads / p.num_kv_heads;
   G4_REQUIRE(G == 8 && (p.head_dim == 256 || p.head_dim == 512),
              "g4_attnDecodeFused: built for 8 query heads per kv head and head_dim 256/512");
+  if (p.head_dim == MQ_HD && p.num_kv_heads <= kMqfCnt / sizeof(uint32_t) && ((uintptr_t)q_norm_w & 15) == 0 &&
+      eff_len(p.max_seq_len, p.sliding_window) <= 65536) {
+    const MqfPlan mp = mqf_plan(p);
+    G4_REQUIRE(workspace_bytes >= mp.bytes, "g4_attnDecodeFused: workspace %zu bytes < %zu required",
+               workspace_bytes, mp.bytes);
+    MqfArgs m{};
+    m.q_raw = q_raw;
+    m.k_raw = k_raw;
+    m.v_raw = v_raw;
+    m.q_w = q_norm_w;
+    m.k_w = k_norm_w;
+    m.rope_freqs = rope_freqs ? rope_freqs : q_norm_w;  // read unconditionally, used only with the divisor
+    m.theta = p.theta;
+    m.apply_divisor = p.apply_divisor;
+    m.eps = p.eps;
+    m.kc = k_cache;
+    m.vc = v_cache;
+    m.pos_dev = position_dev;
+    m.cap = p.max_seq_len;
+    m.nqh = p.num_q_heads;
+    m.nkh = p.num_kv_heads;
+    m.scale = p.scale;
+    m.window = p.sliding_window;
+    m.nstep = mp.nstep;
+    m.max_chunks = mp.max_chunks;
+    m.ws = (float*)((uint8_t*)workspace + kMqfCnt);
+    m.cnt = (uint32_t*)workspace;
+    m.out = output;
+    hipLaunchKernelGGL(mqf_kernel, dim3(mp.max_chunks, p.num_kv_heads), dim3(NT), 0, ctx->stream, m);
+    G4_LAUNCHED(ctx, "attn_decode_fused_mfma");
+    return G4_OK;
+  }
   const SplitPlan sp = plan_splits(eff_len(p.max_seq_len, p.sliding_window));
   rc = check_plan(__func__, sp);
   if (rc) return rc;

@@ -291,7 +291,7 @@ class Context:
                    position_dev: Ptr = None) -> None:
         p = AttnScoreParams(nqh, nkh, hd, seq_len, scale, window)
         ws = workspace
-        if ws is None:  # a fresh workspace must start zeroed (arrival counters)
+        if ws is None:
             ws = self.zeros(self.attn_workspace_bytes(nqh, nkh, hd, seq_len, window), np.uint8)
         if position_dev is None:
             check(lib().g4_attnDecode(self.h, _p(q), _p(k_cache), _p(v_cache), _p(out), p, _p(ws), ws.nbytes))

@@ -153,10 +153,9 @@ int g4_attnOutput(g4_ctx* ctx, const float* probs, const uint16_t* v_cache, floa
 
 /* Fused split-K flash-decode: the attnScore -> softmax -> attnOutput trio in
  * one pass over the KV cache (same inputs and masking as the trio,
- * src/engine.ts:1582-1584). `workspace` holds per-split partials and arrival
- * counters; its size comes from g4_attnDecode_workspace_size. It must be
- * zeroed once before its first use (g4_memset); the kernels leave it zeroed.
- * Calls that share a workspace must not overlap. */
+ * src/engine.ts:1582-1584). `workspace` holds the per-split partials; its
+ * size comes from g4_attnDecode_workspace_size. Calls that share a workspace
+ * must not overlap. */
 int g4_attnDecode_workspace_size(g4_attn_score_params p, size_t* bytes);
 int g4_attnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                   float* output, g4_attn_score_params p, void* workspace, size_t workspace_bytes);
@@ -172,7 +171,12 @@ int g4_attnDecode_dev(g4_ctx* ctx, const float* q, const uint16_t* k_cache,
  * position *position_dev, then split-K decode attention over positions
  * [0, *position_dev] with the window. q_raw is [num_q_heads][head_dim] and is
  * not modified; k_raw/v_raw are [num_kv_heads][head_dim]; caches hold
- * max_seq_len rows. Workspace rules as for g4_attnDecode. */
+ * max_seq_len rows. The workspace (g4_attnDecodeFused_workspace_size bytes)
+ * keeps arrival counters in its first 256 bytes and partials after them: it
+ * must be zeroed (g4_memset) before its first use, every call leaves the
+ * counters zero, and one workspace may serve calls of different windows and
+ * lengths (the layers of a step) as long as they do not overlap and no other
+ * entry point writes into it in between. */
 typedef struct {
   uint32_t num_q_heads, num_kv_heads, head_dim, max_seq_len;
   float scale;

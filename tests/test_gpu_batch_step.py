@@ -94,11 +94,14 @@ def test_paged_attention_block_matches_dense_and_oracle(ctx, bdec):
             ctx.attnDecodeFused(ctx.from_numpy(Q[b]), ctx.from_numpy(K[b]), ctx.from_numpy(V[b]), L.q_norm,
                                 L.k_norm, d.rope_freqs, kdev, vdev, out, ap, ws,
                                 ctx.from_numpy(np.array([pos], np.uint32)))
-            assert bits_equal(A[b], out.download(np.float32)), (il, b)
+            # the single-sequence kernel merges its chunks in another order and
+            # sums the norms' squares in another order: f32 rounding apart
+            assert_close(A[b], out.download(np.float32), rel=1e-5, cos=0.9999999, what=f"dense {il} {b}")
             r = d.pool_row(b, pos)
             kd = kdev.download(np.uint16).reshape(-1, kv)
             vd = vdev.download(np.uint16).reshape(-1, kv)
-            assert np.array_equal(k1[r], kd[pos]) and np.array_equal(v1[r], vd[pos]), (il, b)
+            for got, want in ((k1[r], kd[pos]), (v1[r], vd[pos])):
+                assert np.max(np.abs(got.astype(np.int32) - want.astype(np.int32))) <= 1, (il, b)
             # the oracle on the same inputs
             q = O.fused_per_head_norm_rope(Q[b], qn, s.n_q_heads, s.head_dim, s.eps, pos, theta, int(glob), table)
             k = O.fused_per_head_norm_rope(K[b], kn, s.n_kv_heads, s.head_dim, s.eps, pos, theta, int(glob), table)
