@@ -170,11 +170,13 @@ def graph_us(ctx, body, reps):
 
 
 def attention_cfg3(ctx, reps=3):
-    """Decode attention alone: 8 query heads, 1 KV head, head_dim 256, f16
-    K/V ~ N(0,1), one sequence, contexts 512 / 4096 / 32768, globally (no
-    window) and with the 512-position window. Every launch of a replay reads a
-    different window of a 302 MB K/V region (more than the 256 MB last-level
-    cache). Algorithmic bytes: L_eff * 1024 (f16 K and V rows) + q + output."""
+    """Decode attention: 8 query heads, 1 KV head, head_dim 256, f16 K/V ~
+    N(0,1), one sequence, contexts 512 / 4096 / 32768, globally (no window)
+    and with the 512-position window; `us` is attention alone (normed q in),
+    `fused_block_us` the whole block (q/k norm + RoPE, v_norm, KV store,
+    attention) in its one launch. Every launch of a replay reads a different
+    window of a 302 MB K/V region (more than the 256 MB last-level cache).
+    Algorithmic bytes: L_eff * 1024 (f16 K and V rows) + q + output."""
     nqh, nkh, hd, P = 8, 1, 256, 288 * 1024
     k = ctx.empty(P * hd, np.uint16)
     v = ctx.empty(P * hd, np.uint16)
@@ -183,6 +185,16 @@ def attention_cfg3(ctx, reps=3):
     q = ctx.empty(nqh * hd, np.float32)
     ctx.fill_normal_f32(q, nqh * hd, 33, 0.0, 1.0)
     out = ctx.empty(nqh * hd, np.float32)
+    # the whole block: raw q/k/v, norm weights ~ N(1, 0.1), proportional RoPE table
+    k_raw = ctx.empty(nkh * hd, np.float32)
+    v_raw = ctx.empty(nkh * hd, np.float32)
+    ctx.fill_normal_f32(k_raw, nkh * hd, 34, 0.0, 1.0)
+    ctx.fill_normal_f32(v_raw, nkh * hd, 35, 0.0, 1.0)
+    q_w = ctx.empty(hd, np.uint16)
+    k_w = ctx.empty(hd, np.uint16)
+    ctx.fill_normal_f16(q_w, hd, 36, 1.0, 0.1)
+    ctx.fill_normal_f16(k_w, hd, 37, 1.0, 0.1)
+    table = ctx.from_numpy(np.where(np.arange(hd // 2) < hd // 8, 1.0, np.inf).astype(np.float16).view(np.uint16))
     res = {}
     for L in (512, 4096, 32768):
         for window in (0, 512):
@@ -196,13 +208,29 @@ def attention_cfg3(ctx, reps=3):
                     off = r * L * hd * 2
                     ctx.attnDecode(q, k.offset(off), v.offset(off), out, nqh, nkh, hd, L, 1.0, window, workspace=ws)
             us = graph_us(ctx, body, reps) / n_rot
+            # fused block: q_norm + RoPE, k_norm + RoPE, v_norm, KV store at
+            # position L - 1, attention (theta 1e6 global, 1e4 local)
+            glob = window == 0
+            fp = ctx.attn_fused_params(nqh, nkh, hd, L, window, 1e-6, 1e6 if glob else 1e4, int(glob))
+            fws = ctx.zeros(ctx.attn_fused_workspace_bytes(fp), np.uint8)
+            pdev = ctx.from_numpy(np.array([L - 1], np.uint32))
+
+            def fused():
+                for r in range(n_rot):
+                    off = r * L * hd * 2
+                    ctx.attnDecodeFused(q, k_raw, v_raw, q_w, k_w, table, k.offset(off), v.offset(off), out, fp, fws,
+                                        pdev)
+            us_f = graph_us(ctx, fused, reps) / n_rot
             l_eff = min(L, window) if window else L
             nbytes = l_eff * 1024 + 2 * nqh * hd * 4
             res[f"ctx{L}_{'window512' if window else 'global'}"] = {
                 "us": round(us, 2), "bytes": nbytes, "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
-                "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
-    k.free()
-    v.free()
+                "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                "fused_block_us": round(us_f, 2), "fused_block_gbps": round(nbytes / (us_f * 1e-6) / 1e9, 1)}
+            fws.free()
+            ws.free()
+    for b in (k, v, k_raw, v_raw, q_w, k_w, table):
+        b.free()
     return res
 
 

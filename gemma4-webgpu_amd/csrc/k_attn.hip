@@ -891,12 +891,39 @@ struct MqfArgs {
   float scale;
   uint32_t window;
   uint32_t nstep, max_chunks;
-  float* ws;      // partials [nkh][max_chunks][8] (m, l, o)
-  uint32_t* cnt;  // [nkh] arrivals, zero between calls
+  float* ws;      // chunk partials [nkh][max_chunks][8] (m, l, o)
+  float* ws1;     // group partials [nkh][MQF_FAN][8] (m, l, o)
+  uint32_t* cnt;  // [nkh][MQF_CNT] arrivals (groups, then the top), zero between calls
   float* out;     // [nqh][256]
 };
 
 constexpr int MQF_QS = 264;  // LDS stride of a q column (halves)
+
+// Device-scope (agent) loads and stores through a buffer resource: written
+// through / read past the XCD-local L2, so they are coherent across XCDs
+// without a write-back or invalidation of the whole L2. Offsets in bytes.
+typedef float mqf_f4 __attribute__((ext_vector_type(4)));
+constexpr int kScDevice = 16;  // cache policy operand: sc1 (device scope)
+// Merge tree: chunk partials are merged in groups of up to MQF_FAN by the
+// last workgroup of each group to arrive; with more than one group, the last
+// group merger merges the group partials. Two levels: MQF_FAN^2 chunks.
+constexpr uint32_t MQF_FAN = 16, MQF_CNT = 32;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(float* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void st_dev(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, kScDevice);
+}
+__device__ __forceinline__ void st_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off, const float4& v) {
+  __builtin_amdgcn_raw_buffer_store_b128(mqf_f4{v.x, v.y, v.z, v.w}, r, off, 0, kScDevice);
+}
+__device__ __forceinline__ float ld_dev(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kScDevice));
+}
+__device__ __forceinline__ float4 ld_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const mqf_f4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kScDevice);
+  return make_float4(v.x, v.y, v.z, v.w);
+}
 
 __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
   // K and V tiles; after the last step, the waves' o rows [4 waves][256 dims][16 rows]
@@ -1117,9 +1144,8 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
   }
   __syncthreads();
   const size_t nparts = (size_t)a.nkh * a.max_chunks * MQ_G;
-  float* ws_m = a.ws;
-  float* ws_l = ws_m + nparts;
-  float* ws_o = ws_m + 2 * nparts;
+  // chunk partials: m [nparts], l [nparts], o [nparts][256] (f32)
+  const __amdgpu_buffer_rsrc_t r0 = dev_rsrc(a.ws, (uint32_t)(nparts * (MQ_HD + 2) * sizeof(float)));
   const size_t part0 = ((size_t)kvh * a.max_chunks + chunk) * MQ_G;
   if (tid < MQ_G) {  // thread h: the head's weight per wave and the chunk's (m, l)
     float m4[4], M = -INFINITY;
@@ -1135,8 +1161,8 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
       wt_s[ww * MQ_G + tid] = wt;
       Ls += wt * ml_s[4 * MQ_G + ww * MQ_G + tid];
     }
-    ws_m[part0 + tid] = M;
-    ws_l[part0 + tid] = Ls;
+    st_dev(r0, (uint32_t)(part0 + tid) * 4u, M);
+    st_dev(r0, (uint32_t)(nparts + part0 + tid) * 4u, Ls);
   }
   __syncthreads();
   {  // thread = dim: o[h] = sum over waves of wt * (hi row + lo row)
@@ -1156,42 +1182,81 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
       }
     }
 #pragma unroll
-    for (int h = 0; h < MQ_G; ++h) ws_o[(part0 + h) * MQ_HD + tid] = o[h];
+    for (int h = 0; h < MQ_G; ++h) st_dev(r0, (uint32_t)(2 * nparts + (part0 + h) * MQ_HD + tid) * 4u, o[h]);
   }
 
-  // ---- the last workgroup of this KV head merges the chunks in order ----
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = atomicAdd(&a.cnt[kvh], 1u) == nch - 1 ? 1u : 0u;
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  // thread (head th, dims td.. and td + 128..): one pass in chunk order with
-  // a running maximum
-  float M = -INFINITY, Ls = 0.f;
-  float4 o0 = make_float4(0.f, 0.f, 0.f, 0.f), o1 = o0;
-  const size_t pb = (size_t)kvh * a.max_chunks * MQ_G + th;
+  // ---- merge tree: the last arriver of each group merges it in chunk order ----
+  // thread (head th, dims td.. and td + 128..): one pass with a running maximum
+  auto merge = [&](__amdgpu_buffer_rsrc_t r, size_t stride, size_t first, uint32_t count, float& M, float& Ls,
+                   float4& o0, float4& o1) {
+    M = -INFINITY;
+    Ls = 0.f;
+    o0 = make_float4(0.f, 0.f, 0.f, 0.f);
+    o1 = o0;
 #pragma unroll 4
-  for (uint32_t s2 = 0; s2 < nch; ++s2) {
-    const size_t pp = pb + (size_t)s2 * MQ_G;
-    const float m = ws_m[pp], lv = ws_l[pp];
-    const float4 a0 = *(const float4*)(ws_o + pp * MQ_HD + td);
-    const float4 a1 = *(const float4*)(ws_o + pp * MQ_HD + MQ_HD / 2 + td);
-    const float Mn = fmaxf(M, m);
-    const float fo = M == -INFINITY ? 0.f : expf(M - Mn);
-    const float fn = m == -INFINITY ? 0.f : expf(m - Mn);
-    Ls = Ls * fo + lv * fn;
-    o0.x = o0.x * fo + a0.x * fn; o0.y = o0.y * fo + a0.y * fn;
-    o0.z = o0.z * fo + a0.z * fn; o0.w = o0.w * fo + a0.w * fn;
-    o1.x = o1.x * fo + a1.x * fn; o1.y = o1.y * fo + a1.y * fn;
-    o1.z = o1.z * fo + a1.z * fn; o1.w = o1.w * fo + a1.w * fn;
-    M = Mn;
+    for (uint32_t s2 = 0; s2 < count; ++s2) {
+      const size_t pp = first + (size_t)s2 * MQ_G + th;
+      const float m = ld_dev(r, (uint32_t)pp * 4u), lv = ld_dev(r, (uint32_t)(stride + pp) * 4u);
+      const uint32_t ob = (uint32_t)(2 * stride + pp * MQ_HD + td) * 4u;
+      const float4 a0 = ld_dev4(r, ob);
+      const float4 a1 = ld_dev4(r, ob + MQ_HD / 2 * 4u);
+      const float Mn = fmaxf(M, m);
+      const float fo = M == -INFINITY ? 0.f : expf(M - Mn);
+      const float fn = m == -INFINITY ? 0.f : expf(m - Mn);
+      Ls = Ls * fo + lv * fn;
+      o0.x = o0.x * fo + a0.x * fn; o0.y = o0.y * fo + a0.y * fn;
+      o0.z = o0.z * fo + a0.z * fn; o0.w = o0.w * fo + a0.w * fn;
+      o1.x = o1.x * fo + a1.x * fn; o1.y = o1.y * fo + a1.y * fn;
+      o1.z = o1.z * fo + a1.z * fn; o1.w = o1.w * fo + a1.w * fn;
+      M = Mn;
+    }
+  };
+  // The partials are written and read with device-scope accesses (written
+  // through / read past the XCD-local L2), so an arrival needs only its own
+  // stores complete, not a write-back or invalidation of the whole L2.
+  auto arrive = [&](uint32_t* c, uint32_t fanin) -> bool {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);  // every store of this thread has completed
+    __syncthreads();
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == fanin - 1 ? 1u : 0u;
+    __syncthreads();
+    if (!s_last) return false;
+    if (tid == 0) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // all arrivals are in
+    return true;
+  };
+  auto write_out = [&](float Ls, const float4& o0, const float4& o1) {
+    const float li = Ls > 0.f ? 1.0f / Ls : 0.f;
+    float* dst = a.out + ((size_t)kvh * MQ_G + th) * MQ_HD + td;
+    *(float4*)dst = make_float4(o0.x * li, o0.y * li, o0.z * li, o0.w * li);
+    *(float4*)(dst + MQ_HD / 2) = make_float4(o1.x * li, o1.y * li, o1.z * li, o1.w * li);
+  };
+  uint32_t* cnt = a.cnt + (size_t)kvh * MQF_CNT;
+  const uint32_t ng = (nch + MQF_FAN - 1) / MQF_FAN, g = chunk / MQF_FAN;
+  if (!arrive(cnt + g, min(MQF_FAN, nch - g * MQF_FAN))) return;
+  float M, Ls;
+  float4 o0, o1;
+  merge(r0, nparts, ((size_t)kvh * a.max_chunks + g * MQF_FAN) * MQ_G,
+        min(MQF_FAN, nch - g * MQF_FAN), M, Ls, o0, o1);
+  if (ng == 1) {
+    write_out(Ls, o0, o1);
+    return;
   }
-  const float li = Ls > 0.f ? 1.0f / Ls : 0.f;
-  float* dst = a.out + ((size_t)kvh * MQ_G + th) * MQ_HD + td;
-  *(float4*)dst = make_float4(o0.x * li, o0.y * li, o0.z * li, o0.w * li);
-  *(float4*)(dst + MQ_HD / 2) = make_float4(o1.x * li, o1.y * li, o1.z * li, o1.w * li);
-  if (tid == 0) atomicExch(&a.cnt[kvh], 0u);
+  const size_t nparts1 = (size_t)a.nkh * MQF_FAN * MQ_G;
+  const __amdgpu_buffer_rsrc_t r1 = dev_rsrc(a.ws1, (uint32_t)(nparts1 * (MQ_HD + 2) * sizeof(float)));
+  {
+    const size_t pp = ((size_t)kvh * MQF_FAN + g) * MQ_G + th;
+    if ((tid & 31) == 0) {
+      st_dev(r1, (uint32_t)pp * 4u, M);
+      st_dev(r1, (uint32_t)(nparts1 + pp) * 4u, Ls);
+    }
+    const uint32_t ob = (uint32_t)(2 * nparts1 + pp * MQ_HD + td) * 4u;
+    st_dev4(r1, ob, o0);
+    st_dev4(r1, ob + MQ_HD / 2 * 4u, o1);
+  }
+  if (!arrive(cnt + MQF_CNT - 1, ng)) return;
+  merge(r1, nparts1, (size_t)kvh * MQF_FAN * MQ_G, ng, M, Ls, o0, o1);
+  write_out(Ls, o0, o1);
 }
 
 // ---------------------------------------------------------------------------
@@ -1388,21 +1453,25 @@ int launch_attn(g4_ctx* ctx, const AttnArgs& a, uint32_t G, uint32_t hd, int cp,
                        hd);
 }
 
-// Fused single-sequence plan: at most 64 chunks (the last workgroup merges
-// them in one wave). The arrival counters sit in the first kMqfCnt bytes of
-// the workspace, at the same place whatever the plan, so that layers of
-// different windows can share one workspace; the partials follow.
-constexpr size_t kMqfCnt = 256;
+// Fused single-sequence plan: one 64-position step per workgroup up to
+// MQF_FAN^2 chunks (so a long context is read by as many CUs as it has
+// chunks), more steps beyond. The arrival counters sit in the first kMqfCnt
+// bytes of the workspace, at the same place whatever the plan, so that
+// layers of different windows can share one workspace; the chunk partials
+// follow, then the group partials.
+constexpr uint32_t kMqfMaxKvHeads = 64;
+constexpr size_t kMqfCnt = (size_t)kMqfMaxKvHeads * MQF_CNT * sizeof(uint32_t);
 struct MqfPlan {
   uint32_t nstep, max_chunks;
-  size_t bytes;
+  size_t bytes_ws0, bytes;
 };
 MqfPlan mqf_plan(const g4_attn_fused_params& p) {
   MqfPlan m{};
   const uint32_t eff = std::max(eff_len(p.max_seq_len, p.sliding_window), 1u);
-  m.nstep = std::min(16u, std::max(1u, ceil_div(eff, MQ_STEP * 64)));
+  m.nstep = std::max(1u, ceil_div(eff, MQ_STEP * MQF_FAN * MQF_FAN));
   m.max_chunks = ceil_div(eff, MQ_STEP * m.nstep);
-  m.bytes = kMqfCnt + ws_bytes(1, p.num_kv_heads, m.max_chunks, MQ_G, MQ_HD);
+  m.bytes_ws0 = ws_bytes(1, p.num_kv_heads, m.max_chunks, MQ_G, MQ_HD);
+  m.bytes = kMqfCnt + m.bytes_ws0 + ws_bytes(1, p.num_kv_heads, MQF_FAN, MQ_G, MQ_HD);
   return m;
 }
 
@@ -1669,8 +1738,8 @@ int g4_attnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw, cons
   const uint32_t G = p.num_q_heads / p.num_kv_heads;
   G4_REQUIRE(G == 8 && (p.head_dim == 256 || p.head_dim == 512),
              "g4_attnDecodeFused: built for 8 query heads per kv head and head_dim 256/512");
-  if (p.head_dim == MQ_HD && p.num_kv_heads <= kMqfCnt / sizeof(uint32_t) && ((uintptr_t)q_norm_w & 15) == 0 &&
-      eff_len(p.max_seq_len, p.sliding_window) <= 65536) {
+  if (p.head_dim == MQ_HD && p.num_kv_heads <= kMqfMaxKvHeads && ((uintptr_t)q_norm_w & 15) == 0 &&
+      eff_len(p.max_seq_len, p.sliding_window) <= 4 * MQ_STEP * MQF_FAN * MQF_FAN) {
     const MqfPlan mp = mqf_plan(p);
     G4_REQUIRE(workspace_bytes >= mp.bytes, "g4_attnDecodeFused: workspace %zu bytes < %zu required",
                workspace_bytes, mp.bytes);
@@ -1695,6 +1764,7 @@ int g4_attnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw, cons
     m.nstep = mp.nstep;
     m.max_chunks = mp.max_chunks;
     m.ws = (float*)((uint8_t*)workspace + kMqfCnt);
+    m.ws1 = (float*)((uint8_t*)workspace + kMqfCnt + mp.bytes_ws0);
     m.cnt = (uint32_t*)workspace;
     m.out = output;
     hipLaunchKernelGGL(mqf_kernel, dim3(mp.max_chunks, p.num_kv_heads), dim3(NT), 0, ctx->stream, m);

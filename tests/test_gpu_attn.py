@@ -146,6 +146,10 @@ FUSED_CASES = [
     (700, 0, 256, 1e6, 1),
     (3000, 0, 256, 1e6, 1),
     (900, 0, 512, 1e6, 1),
+    # long contexts: chunk partials merged in groups, then the groups
+    (20000, 0, 256, 1e6, 1),
+    (32767, 0, 256, 1e6, 1),
+    (32767, 512, 256, 1e4, 0),
 ]
 
 
@@ -153,7 +157,8 @@ FUSED_CASES = [
 def test_attn_decode_fused(ctx, pos, window, hd, theta, div):
     """norm + RoPE on q/k, v_norm, KV store and attention in one launch equals
     the reference's per-key sequence restated by the oracle."""
-    nqh, nkh, cap = 8, 1, 4096
+    nqh, nkh = 8, 1
+    cap = 4096 if pos < 4096 else 32768
     k, v = kv(pos + 11, cap, nkh, hd)
     qr = O.gen_normal_f32(pos + 1, nqh * hd, 0.0, 3.0)
     kr = O.gen_normal_f32(pos + 2, nkh * hd, 0.0, 3.0)
