@@ -172,7 +172,7 @@ int g4_attnDecode_dev(g4_ctx* ctx, const float* q, const uint16_t* k_cache,
  * [0, *position_dev] with the window. q_raw is [num_q_heads][head_dim] and is
  * not modified; k_raw/v_raw are [num_kv_heads][head_dim]; caches hold
  * max_seq_len rows. The workspace (g4_attnDecodeFused_workspace_size bytes)
- * keeps arrival counters in its first 256 bytes and partials after them: it
+ * keeps arrival counters in its first 8 KB and partials after them: it
  * must be zeroed (g4_memset) before its first use, every call leaves the
  * counters zero, and one workspace may serve calls of different windows and
  * lengths (the layers of a step) as long as they do not overlap and no other
