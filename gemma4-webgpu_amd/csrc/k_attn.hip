@@ -1716,8 +1716,10 @@ int g4_attnDecodeFused_workspace_size(g4_attn_fused_params p, size_t* bytes) {
   const SplitPlan sp = plan_splits(eff_len(p.max_seq_len, p.sliding_window));
   rc = check_plan(__func__, sp);
   if (rc) return rc;
+  // both forms keep the first kMqfCnt bytes for the one-launch form's
+  // counters, so layers of either form can share a workspace
   const size_t old = ws_bytes(1, p.num_kv_heads, sp.nsplit, p.num_q_heads / p.num_kv_heads, p.head_dim);
-  *bytes = std::max(old, mqf_plan(p).bytes);
+  *bytes = std::max(kMqfCnt + old, mqf_plan(p).bytes);
   return G4_OK;
 }
 
@@ -1774,11 +1776,11 @@ int g4_attnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw, cons
   const SplitPlan sp = plan_splits(eff_len(p.max_seq_len, p.sliding_window));
   rc = check_plan(__func__, sp);
   if (rc) return rc;
-  const size_t need = ws_bytes(1, p.num_kv_heads, sp.nsplit, G, p.head_dim);
+  const size_t need = kMqfCnt + ws_bytes(1, p.num_kv_heads, sp.nsplit, G, p.head_dim);
   G4_REQUIRE(workspace_bytes >= need, "g4_attnDecodeFused: workspace %zu bytes < %zu required", workspace_bytes,
              need);
   AttnArgs a = dense_args(q_raw, k_cache, v_cache, p.num_q_heads, p.num_kv_heads, p.max_seq_len, p.scale,
-                          p.sliding_window, sp, workspace, position_dev);
+                          p.sliding_window, sp, (uint8_t*)workspace + kMqfCnt, position_dev);
   a.kc_w = k_cache;
   a.vc_w = v_cache;
   a.k_in = k_raw;

@@ -153,10 +153,7 @@ FUSED_CASES = [
 ]
 
 
-@pytest.mark.parametrize("pos,window,hd,theta,div", FUSED_CASES)
-def test_attn_decode_fused(ctx, pos, window, hd, theta, div):
-    """norm + RoPE on q/k, v_norm, KV store and attention in one launch equals
-    the reference's per-key sequence restated by the oracle."""
+def _fused_inputs(pos, window, hd, theta, div):
     nqh, nkh = 8, 1
     cap = 4096 if pos < 4096 else 32768
     k, v = kv(pos + 11, cap, nkh, hd)
@@ -173,18 +170,29 @@ def test_attn_decode_fused(ctx, pos, window, hd, theta, div):
     k_ref, v_ref = k.copy(), v.copy()
     O.kv_cache_store_f16(kk, vq, k_ref, v_ref, nkh, hd, pos)
     ref = O.attention(q, k_ref, v_ref, nqh, nkh, hd, pos + 1, 1.0, window)
+    return dict(nqh=nqh, nkh=nkh, cap=cap, k=k, v=v, qr=qr, kr=kr, vr=vr, qw=qw, kw=kw, table=table,
+                k_ref=k_ref, v_ref=v_ref, ref=ref)
+
+
+@pytest.mark.parametrize("pos,window,hd,theta,div", FUSED_CASES)
+def test_attn_decode_fused(ctx, pos, window, hd, theta, div):
+    """norm + RoPE on q/k, v_norm, KV store and attention in one launch equals
+    the reference's per-key sequence restated by the oracle."""
+    c = _fused_inputs(pos, window, hd, theta, div)
+    nqh, nkh, cap = c["nqh"], c["nkh"], c["cap"]
     p = ctx.attn_fused_params(nqh, nkh, hd, cap, window, 1e-6, theta, div)
     ws = ctx.zeros(ctx.attn_fused_workspace_bytes(p), np.uint8)
-    dk, dv = ctx.from_numpy(k), ctx.from_numpy(v)
+    dk, dv = ctx.from_numpy(c["k"]), ctx.from_numpy(c["v"])
     out = ctx.empty(nqh * hd, np.float32)
-    dq = ctx.from_numpy(qr)
+    dq = ctx.from_numpy(c["qr"])
     pdev = ctx.from_numpy(np.array([pos], np.uint32))
     for rep in range(2):  # the arrival counters must be left zeroed for the next call
-        ctx.attnDecodeFused(dq, ctx.from_numpy(kr), ctx.from_numpy(vr), ctx.from_numpy(qw), ctx.from_numpy(kw),
-                            ctx.from_numpy(table), dk, dv, out, p, ws, pdev)
-        assert_close(out.download(np.float32), ref, what=f"fused pos={pos} rep={rep}")
+        ctx.attnDecodeFused(dq, ctx.from_numpy(c["kr"]), ctx.from_numpy(c["vr"]), ctx.from_numpy(c["qw"]),
+                            ctx.from_numpy(c["kw"]), ctx.from_numpy(c["table"]), dk, dv, out, p, ws, pdev)
+        assert_close(out.download(np.float32), c["ref"], what=f"fused pos={pos} rep={rep}")
     # the stored row: within an f16 rounding of the oracle's (the norm's f32
     # rounding differs from the oracle's f64 one); no other row touched
+    k, v, k_ref, v_ref = c["k"], c["v"], c["k_ref"], c["v_ref"]
     kc, vc = dk.download(np.uint16).reshape(cap, hd), dv.download(np.uint16).reshape(cap, hd)
     assert np.max(np.abs(vc[pos].astype(np.int32) - v_ref.reshape(cap, hd)[pos].astype(np.int32))) <= 1
     assert np.max(np.abs(kc[pos].view(np.float16).astype(np.float32) -
@@ -192,4 +200,28 @@ def test_attn_decode_fused(ctx, pos, window, hd, theta, div):
     other = np.arange(cap) != pos
     assert np.array_equal(kc[other], k.reshape(cap, hd)[other])
     assert np.array_equal(vc[other], v.reshape(cap, hd)[other])
-    assert np.array_equal(qr, dq.download(np.float32))   # q_raw is not modified
+    assert np.array_equal(c["qr"], dq.download(np.float32))   # q_raw is not modified
+
+
+def test_attn_decode_fused_shared_workspace(ctx):
+    """Layers of different windows, lengths and head sizes (the one-launch
+    form and the two-launch form) share one workspace, as a decode step's
+    layers do, over two rounds."""
+    cases = [(700, 0, 256, 1e6, 1), (900, 0, 512, 1e6, 1), (3000, 512, 256, 1e4, 0), (3000, 0, 256, 1e6, 1),
+             (20, 512, 256, 1e4, 0)]
+    prepared = []
+    need = 0
+    for pos, window, hd, theta, div in cases:
+        c = _fused_inputs(pos, window, hd, theta, div)
+        p = ctx.attn_fused_params(c["nqh"], c["nkh"], hd, c["cap"], window, 1e-6, theta, div)
+        need = max(need, ctx.attn_fused_workspace_bytes(p))
+        dev = {n: ctx.from_numpy(c[n]) for n in ("qr", "kr", "vr", "qw", "kw", "table")}
+        prepared.append((pos, hd, c, p, dev))
+    ws = ctx.zeros(need, np.uint8)
+    for rnd in range(2):
+        for pos, hd, c, p, dev in prepared:
+            dk, dv = ctx.from_numpy(c["k"]), ctx.from_numpy(c["v"])
+            out = ctx.empty(c["nqh"] * hd, np.float32)
+            ctx.attnDecodeFused(dev["qr"], dev["kr"], dev["vr"], dev["qw"], dev["kw"], dev["table"], dk, dv, out, p,
+                                ws, ctx.from_numpy(np.array([pos], np.uint32)))
+            assert_close(out.download(np.float32), c["ref"], what=f"shared ws round {rnd} pos={pos} hd={hd}")
