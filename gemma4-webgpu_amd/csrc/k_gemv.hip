@@ -1141,10 +1141,13 @@ int launch_qt(g4_ctx* ctx, const LaunchReq& q) {
 
 // One activation vector: register-resident digits (mv_kernel). Each
 // workgroup digitises the whole activation vector and walks its tiles one row
-// per slot; more waves per workgroup shorten both serial phases. The launch
-// takes the widest workgroup that still leaves kMvMinWgs tiles; matrices
-// larger than two workgroups per CU are walked tile by tile.
-constexpr uint32_t kMvMinWgs = 160;
+// per slot; more waves per workgroup shorten both serial phases. A CU streams
+// its tile at a limited rate (measured: a workgroup's weights arrive in time
+// proportional to its bytes), so the launch takes the widest workgroup that
+// still gives every CU a tile (kMvFullWgs), else the widest of at least
+// 6 waves that leaves kMvMinWgs tiles; matrices larger than two workgroups
+// per CU are walked tile by tile.
+constexpr uint32_t kMvFullWgs = 240, kMvMinWgs = 160;
 
 template <int QT, int BPR, int NWV, int PRO, int NMAT>
 int mv_launch(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
@@ -1171,8 +1174,8 @@ int mv_launch(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
 }
 
 // workgroup widths in waves for a row of BPR super-blocks (slots must tile it)
-template <int BPR> struct MvWaves { static constexpr int A = 12, B = 6, C = 3; };
-template <> struct MvWaves<32> { static constexpr int A = 12, B = 6, C = 4; };
+template <int BPR> struct MvWaves { static constexpr int A = 12, B = 9, C = 6, D = 3; };
+template <> struct MvWaves<32> { static constexpr int A = 12, B = 8, C = 6, D = 4; };
 
 template <int QT, int BPR, int PRO, int NMAT>
 int mv_rows(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
@@ -1182,9 +1185,10 @@ int mv_rows(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
     for (int i = 0; i < q.nseg; ++i) t += ceil_div(q.segs[i].M, slots);
     return t;
   };
-  if (tiles(MvGeom<BPR, Wv::A>::SLOTS) >= kMvMinWgs) return mv_launch<QT, BPR, Wv::A, PRO, NMAT>(ctx, q, w_up);
-  if (tiles(MvGeom<BPR, Wv::B>::SLOTS) >= kMvMinWgs) return mv_launch<QT, BPR, Wv::B, PRO, NMAT>(ctx, q, w_up);
-  return mv_launch<QT, BPR, Wv::C, PRO, NMAT>(ctx, q, w_up);
+  if (tiles(MvGeom<BPR, Wv::A>::SLOTS) >= kMvFullWgs) return mv_launch<QT, BPR, Wv::A, PRO, NMAT>(ctx, q, w_up);
+  if (tiles(MvGeom<BPR, Wv::B>::SLOTS) >= kMvFullWgs) return mv_launch<QT, BPR, Wv::B, PRO, NMAT>(ctx, q, w_up);
+  if (tiles(MvGeom<BPR, Wv::C>::SLOTS) >= kMvMinWgs) return mv_launch<QT, BPR, Wv::C, PRO, NMAT>(ctx, q, w_up);
+  return mv_launch<QT, BPR, Wv::D, PRO, NMAT>(ctx, q, w_up);
 }
 
 template <int QT, int PRO, int NMAT>
