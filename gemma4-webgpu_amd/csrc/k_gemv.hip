@@ -594,13 +594,14 @@ struct MvX {
   static constexpr int K = BPR * 256;
   static constexpr int NSB = BPR * 8;
   static constexpr size_t HI = 0, LO = K, S = 2 * (size_t)K, SUM = S + 4 * NSB, C16 = SUM + 4 * NSB,
-                          RED8 = C16 + 16 * NSB, END = RED8 + 128;  // two block sums of up to 16 waves
+                          RED8 = C16 + 16 * NSB, END = RED8 + 256;  // a 4-wide block sum of up to 16 waves
 };
 
 template <int QT, int BPR, int NWV, int NMAT>
 __host__ __device__ constexpr size_t mv_lds_bytes() {
   using T = MvTile<QT, BPR, NWV>;
-  return align16(MvX<BPR>::END) + NMAT * align16((size_t)T::TR * T::RS * 4) + NMAT * (size_t)T::LDS_T;
+  // Q4_K rows are read straight into registers (no staged tile)
+  return align16(MvX<BPR>::END) + NMAT * align16((size_t)T::TR * T::RS * 4) + (QT == 0 ? 0 : NMAT * (size_t)T::LDS_T);
 }
 
 template <class T, int NTH>
@@ -644,6 +645,28 @@ __device__ __forceinline__ float block_sum_1(float v, float* red) {
   float t = 0.f;
 #pragma unroll
   for (int i = 0; i < NWV; ++i) t += red[i];
+  return t;
+}
+
+// Four block-wide sums at once (one barrier); `red` holds >= 4 * NWV floats,
+// 16-byte aligned.
+template <int NWV>
+__device__ __forceinline__ float4 block_sum_4(float4 v, float* red) {
+  v.x = wave_sum_dpp(v.x);
+  v.y = wave_sum_dpp(v.y);
+  v.z = wave_sum_dpp(v.z);
+  v.w = wave_sum_dpp(v.w);
+  if ((threadIdx.x & 63) == 0) *(float4*)(red + 4 * (threadIdx.x >> 6)) = v;
+  __syncthreads();
+  float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < NWV; ++i) {
+    const float4 r = *(const float4*)(red + 4 * i);
+    t.x += r.x;
+    t.y += r.y;
+    t.z += r.z;
+    t.w += r.w;
+  }
   return t;
 }
 
@@ -695,7 +718,7 @@ __device__ __forceinline__ void mv_pro_finish(MvPro<BPR, NWV, PRO>& P, uint8_t* 
   using PP = MvPro<BPR, NWV, PRO>;
   using X = MvX<BPR>;
   float* red8 = (float*)(smem + X::RED8);
-  if constexpr (PRO >= 1) {
+  if constexpr (PRO == 1) {
     float ss = 0.f;
 #pragma unroll
     for (int p = 0; p < PP::XP; ++p) {
@@ -704,24 +727,37 @@ __device__ __forceinline__ void mv_pro_finish(MvPro<BPR, NWV, PRO>& P, uint8_t* 
     }
     ss = block_sum_1<NWV>(ss, red8);
     const float inv1 = 1.0f / sqrtf(ss / (float)X::K + a.eps);
-    if constexpr (PRO == 1) {
 #pragma unroll
-      for (int p = 0; p < PP::XP; ++p) P.x[p] = mul_w(P.x[p], P.w1[p], inv1);
-    } else {
-      float ss2 = 0.f;
+    for (int p = 0; p < PP::XP; ++p) P.x[p] = mul_w(P.x[p], P.w1[p], inv1);
+  } else if constexpr (PRO == 2) {
+    // h = r + t, t = (o * w1) * inv1. Both norms come out of one block
+    // reduction: sum(o^2), and sum(h^2) expanded as
+    // sum(r^2) + 2 inv1 sum(r (o w1)) + inv1^2 sum((o w1)^2).
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 ow[PP::XP];
 #pragma unroll
-      for (int p = 0; p < PP::XP; ++p) {
-        const float4 t = mul_w(P.x[p], P.w1[p], inv1);
-        const float4 h = make_float4(P.r[p].x + t.x, P.r[p].y + t.y, P.r[p].z + t.z, P.r[p].w + t.w);
-        P.x[p] = h;
-        const float q = sumsq(h);
-        ss2 += PP::live(p) ? q : 0.f;
-        if (a.h_out && blockIdx.x == 0 && PP::live(p)) *(float4*)(a.h_out + PP::elem(p)) = h;
-      }
-      ss2 = block_sum_1<NWV>(ss2, red8 + 16);
-      const float inv2 = 1.0f / sqrtf(ss2 / (float)X::K + a.eps);
+    for (int p = 0; p < PP::XP; ++p) {
+      ow[p] = mul_w(P.x[p], P.w1[p], 1.0f);
+      const float4 o = P.x[p], r = P.r[p], t = ow[p];
+      const float so = sumsq(o), sr = sumsq(r), st = sumsq(t);
+      const float rt = (r.x * t.x + r.y * t.y) + (r.z * t.z + r.w * t.w);
+      const bool lv = PP::live(p);
+      acc.x += lv ? so : 0.f;
+      acc.y += lv ? sr : 0.f;
+      acc.z += lv ? rt : 0.f;
+      acc.w += lv ? st : 0.f;
+    }
+    acc = block_sum_4<NWV>(acc, red8);
+    const float inv1 = 1.0f / sqrtf(acc.x / (float)X::K + a.eps);
+    const float ss2 = fmaxf(acc.y + 2.0f * inv1 * acc.z + inv1 * inv1 * acc.w, 0.f);
+    const float inv2 = 1.0f / sqrtf(ss2 / (float)X::K + a.eps);
 #pragma unroll
-      for (int p = 0; p < PP::XP; ++p) P.x[p] = mul_w(P.x[p], P.w2[p], inv2);
+    for (int p = 0; p < PP::XP; ++p) {
+      const float4 t = ow[p];
+      const float4 h = make_float4(P.r[p].x + t.x * inv1, P.r[p].y + t.y * inv1, P.r[p].z + t.z * inv1,
+                                   P.r[p].w + t.w * inv1);
+      if (a.h_out && blockIdx.x == 0 && PP::live(p)) *(float4*)(a.h_out + PP::elem(p)) = h;
+      P.x[p] = mul_w(h, P.w2[p], inv2);
     }
   }
   const int lane = threadIdx.x & 63;
@@ -865,6 +901,65 @@ __device__ __forceinline__ float mv_unit_dot(const MvUnit<QT>& X, const uint8_t*
   }
 }
 
+// Q4_K: the 48 bytes unit g of one row-block needs (header, two 16-byte
+// quant runs) are 16-byte aligned in global memory (144-byte blocks), so
+// each thread loads its own unit straight into registers: no LDS staging and
+// no workgroup barrier between the weights' arrival and the products.
+struct Q4Unit {
+  u32x4a hd, q0, q1;
+};
+__device__ __forceinline__ void q4_unit_load(Q4Unit& w, const uint8_t* blk, int g) {
+  w.hd = *(const u32x4a*)blk;
+  w.q0 = *(const u32x4a*)(blk + 16 + 32 * g);
+  w.q1 = *(const u32x4a*)(blk + 32 + 32 * g);
+}
+__device__ __forceinline__ float q4_unit_dot(const MvUnit<0>& X, const Q4Unit& w, int g) {
+  float sc_lo, sc_hi, m_lo, m_hi;
+  q4k_scales(w.hd[1], w.hd[2], w.hd[3], g, sc_lo, sc_hi, m_lo, m_hi);
+  const uint32_t qa[8] = {w.q0[0], w.q0[1], w.q0[2], w.q0[3], w.q1[0], w.q1[1], w.q1[2], w.q1[3]};
+  int ah0 = 0, al0 = 0, ah1 = 0, al1 = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t nl = qa[k] & 0x0f0f0f0fu, nh = (qa[k] >> 4) & 0x0f0f0f0fu;
+    ah0 = __builtin_amdgcn_sdot4((int)nl, (int)X.hi[k], ah0, false);
+    al0 = __builtin_amdgcn_sdot4((int)nl, (int)X.lo[k], al0, false);
+    ah1 = __builtin_amdgcn_sdot4((int)nh, (int)X.hi[8 + k], ah1, false);
+    al1 = __builtin_amdgcn_sdot4((int)nh, (int)X.lo[8 + k], al1, false);
+  }
+  const float d = g4d::f16_bits_to_f32(w.hd[0] & 0xffffu);
+  const float dmin = g4d::f16_bits_to_f32(w.hd[0] >> 16);
+  const float i0 = (float)(ah0 * 256 + al0), i1 = (float)(ah1 * 256 + al1);
+  return d * (sc_lo * X.s[0] * i0 + sc_hi * X.s[1] * i1) - dmin * (m_lo * X.s[2] + m_hi * X.s[3]);
+}
+
+// Adds each row's U unit partials (RG lanes per row, then a butterfly) and
+// stores the tile's rows: y, softcap(y), or gelu(gate) * up for a pair.
+template <class T, int NTH, int NMAT>
+__device__ __forceinline__ void mv_reduce_store(const float* red, const GemvSeg& sg, uint32_t t, int tid, float cap) {
+  constexpr int U = NTH / T::TR;
+  const int gl = tid % T::RG;
+  for (int r = tid / T::RG; r < T::TR; r += NTH / T::RG) {  // uniform within a group
+    float y[NMAT];
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m) {
+      const float* rr = red + m * T::TR * T::RS + r * T::RS + gl;
+      float a = rr[0];
+#pragma unroll
+      for (int v = 1; v < U / T::RG; ++v) a += rr[v * T::RG];
+#pragma unroll
+      for (int o = T::RG / 2; o > 0; o >>= 1) a += __shfl_xor(a, o, 64);
+      y[m] = a;
+    }
+    const uint32_t row = t * T::TR + r;
+    if (gl == 0 && row < sg.M) {
+      float v;
+      if constexpr (NMAT == 2) v = gelu_tanh(y[0]) * y[1];
+      else v = cap > 0.f ? softcap(y[0], cap) : y[0];
+      sg.Y[row] = v;
+    }
+  }
+}
+
 // NMAT = 1: y, or softcap(y) when cap > 0 (shaders/logit_softcap.wgsl), for
 // each segment's rows. NMAT = 2: gate/up pair, out = gelu(gate) * up
 // (shaders/gelu_mul.wgsl:10-16).
@@ -897,51 +992,58 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
-  Stage<T::LPT> st[NMAT];
-  uint32_t nb = mv_tile_bytes<QT, BPR, NWV>(sg.M, tb);
+  if constexpr (QT == 0) {
+    // Q4_K: each thread's unit straight from global memory into registers;
+    // rows past M (a partial last tile) read row M - 1 and are not stored
+    Q4Unit wu[NMAT];
+    auto unit_ptr = [&](int m, uint32_t t) {
+      const uint32_t row = min(t * (uint32_t)T::TR + (uint32_t)slot, sg.M - 1);
+      return W[m] + (size_t)row * T::RB + (size_t)(u >> 2) * T::BYTES;
+    };
 #pragma unroll
-  for (int m = 0; m < NMAT; ++m) mv_stage_load<T, NTH>(W[m] + (size_t)tb * T::TB, nb, st[m]);
-  __builtin_amdgcn_sched_barrier(0);  // every weight load is issued before the activations are used
-  mv_pro_finish<BPR, NWV, PRO>(P, smem, pa);
-  MvUnit<QT> X;
-  mv_unit_load<QT, BPR>(X, smem, u);
+    for (int m = 0; m < NMAT; ++m) q4_unit_load(wu[m], unit_ptr(m, tb), u & 3);
+    __builtin_amdgcn_sched_barrier(0);  // every weight load is issued before the activations are used
+    mv_pro_finish<BPR, NWV, PRO>(P, smem, pa);
+    MvUnit<QT> X;
+    mv_unit_load<QT, BPR>(X, smem, u);
+    for (uint32_t t = tb; t < te; ++t) {
+#pragma unroll
+      for (int m = 0; m < NMAT; ++m) red[m * T::TR * T::RS + slot * T::RS + u] = q4_unit_dot(X, wu[m], u & 3);
+      if (t + 1 < te) {
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) q4_unit_load(wu[m], unit_ptr(m, t + 1), u & 3);
+      }
+      __syncthreads();
+      mv_reduce_store<T, NTH, NMAT>(red, sg, t, tid, cap);
+      __syncthreads();  // the reduction buffer is reused by the next tile
+    }
+  } else {
+    Stage<T::LPT> st[NMAT];
+    uint32_t nb = mv_tile_bytes<QT, BPR, NWV>(sg.M, tb);
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m) mv_stage_load<T, NTH>(W[m] + (size_t)tb * T::TB, nb, st[m]);
+    __builtin_amdgcn_sched_barrier(0);  // every weight load is issued before the activations are used
+    mv_pro_finish<BPR, NWV, PRO>(P, smem, pa);
+    MvUnit<QT> X;
+    mv_unit_load<QT, BPR>(X, smem, u);
 
-  for (uint32_t t = tb; t < te; ++t) {
-    __syncthreads();  // digits read (first tile) / previous tile reduced
+    for (uint32_t t = tb; t < te; ++t) {
+      __syncthreads();  // digits read (first tile) / previous tile reduced
 #pragma unroll
-    for (int m = 0; m < NMAT; ++m) mv_stage_store<T, NTH>(tl + m * T::LDS_T, nb, st[m]);
-    __syncthreads();
-    if (t + 1 < te) {
-      nb = mv_tile_bytes<QT, BPR, NWV>(sg.M, t + 1);
+      for (int m = 0; m < NMAT; ++m) mv_stage_store<T, NTH>(tl + m * T::LDS_T, nb, st[m]);
+      __syncthreads();
+      if (t + 1 < te) {
+        nb = mv_tile_bytes<QT, BPR, NWV>(sg.M, t + 1);
 #pragma unroll
-      for (int m = 0; m < NMAT; ++m) mv_stage_load<T, NTH>(W[m] + (size_t)(t + 1) * T::TB, nb, st[m]);
-    }
-#pragma unroll
-    for (int m = 0; m < NMAT; ++m) {
-      const uint8_t* blk = tl + m * T::LDS_T + slot * T::RB + (u >> 2) * T::BYTES;
-      red[m * T::TR * T::RS + slot * T::RS + u] = mv_unit_dot<QT>(X, blk, u & 3);
-    }
-    __syncthreads();
-    const int gl = tid % T::RG;
-    for (int r = tid / T::RG; r < T::TR; r += NTH / T::RG) {  // uniform within a group
-      float y[NMAT];
+        for (int m = 0; m < NMAT; ++m) mv_stage_load<T, NTH>(W[m] + (size_t)(t + 1) * T::TB, nb, st[m]);
+      }
 #pragma unroll
       for (int m = 0; m < NMAT; ++m) {
-        const float* rr = red + m * T::TR * T::RS + r * T::RS + gl;
-        float a = rr[0];
-#pragma unroll
-        for (int v = 1; v < G::U / T::RG; ++v) a += rr[v * T::RG];
-#pragma unroll
-        for (int o = T::RG / 2; o > 0; o >>= 1) a += __shfl_xor(a, o, 64);
-        y[m] = a;
+        const uint8_t* blk = tl + m * T::LDS_T + slot * T::RB + (u >> 2) * T::BYTES;
+        red[m * T::TR * T::RS + slot * T::RS + u] = mv_unit_dot<QT>(X, blk, u & 3);
       }
-      const uint32_t row = t * T::TR + r;
-      if (gl == 0 && row < sg.M) {
-        float v;
-        if constexpr (NMAT == 2) v = gelu_tanh(y[0]) * y[1];
-        else v = cap > 0.f ? softcap(y[0], cap) : y[0];
-        sg.Y[row] = v;
-      }
+      __syncthreads();
+      mv_reduce_store<T, NTH, NMAT>(red, sg, t, tid, cap);
     }
   }
 }
