@@ -28,6 +28,8 @@
 //    per launch (q/k/v), gate/up pairs with the GELU product epilogue.
 #include "g4_internal.hpp"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int NW = 4;             // wavefronts per workgroup
@@ -597,11 +599,12 @@ struct MvX {
                           RED8 = C16 + 16 * NSB, END = RED8 + 256;  // a 4-wide block sum of up to 16 waves
 };
 
+// A workgroup with one tile reads its weight units straight into registers;
+// one that walks several tiles stages them through LDS (`staged`).
 template <int QT, int BPR, int NWV, int NMAT>
-__host__ __device__ constexpr size_t mv_lds_bytes() {
+__host__ __device__ constexpr size_t mv_lds_bytes(bool staged) {
   using T = MvTile<QT, BPR, NWV>;
-  // Q4_K rows are read straight into registers (no staged tile)
-  return align16(MvX<BPR>::END) + NMAT * align16((size_t)T::TR * T::RS * 4) + (QT == 0 ? 0 : NMAT * (size_t)T::LDS_T);
+  return align16(MvX<BPR>::END) + NMAT * align16((size_t)T::TR * T::RS * 4) + (staged ? NMAT * (size_t)T::LDS_T : 0);
 }
 
 template <class T, int NTH>
@@ -637,11 +640,21 @@ using g4d::wave_sum_dpp;
 
 // Sum over the workgroup with one barrier; `red` holds NWV floats not reused
 // by another sum before the next barrier.
+// Workgroup barrier that orders LDS accesses only: it waits for the wave's
+// LDS operations, not for its global loads and stores in flight (a plain
+// __syncthreads also waits for every outstanding load, prefetched weights
+// included, whenever a global store precedes it).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <int NWV>
 __device__ __forceinline__ float block_sum_1(float v, float* red) {
   v = wave_sum_dpp(v);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
+  lds_barrier();
   float t = 0.f;
 #pragma unroll
   for (int i = 0; i < NWV; ++i) t += red[i];
@@ -657,7 +670,7 @@ __device__ __forceinline__ float4 block_sum_4(float4 v, float* red) {
   v.z = wave_sum_dpp(v.z);
   v.w = wave_sum_dpp(v.w);
   if ((threadIdx.x & 63) == 0) *(float4*)(red + 4 * (threadIdx.x >> 6)) = v;
-  __syncthreads();
+  lds_barrier();
   float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int i = 0; i < NWV; ++i) {
@@ -802,7 +815,7 @@ __device__ __forceinline__ void mv_pro_finish(MvPro<BPR, NWV, PRO>& P, uint8_t* 
       if ((lane & 3) == 0) ((int2*)(smem + X::C16))[f / 16] = make_int2(32 * shi, 32 * slo);
     }
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // Digits and constants of one unit, held in registers.
@@ -932,6 +945,72 @@ __device__ __forceinline__ float q4_unit_dot(const MvUnit<0>& X, const Q4Unit& w
   return d * (sc_lo * X.s[0] * i0 + sc_hi * X.s[1] * i1) - dmin * (m_lo * X.s[2] + m_hi * X.s[3]);
 }
 
+// Q6_K: blocks are 210 bytes, so a block starts 4-byte aligned (even block)
+// or 2 bytes past a dword (odd block; rows start dword-aligned). Each 16-byte
+// run is read as five aligned dwords and shifted into place (the fifth dword
+// stays inside the block: runs end at byte 192 at most); the four scales of
+// the unit and d are read as single bytes / one half, which never leaves the
+// block either.
+struct Q6Unit {
+  u32x4a a4, b4, h4;
+  uint32_t a1, b1, h1, sh;
+  uint32_t s0, s1, s2, s3;  // the unit's four int8 scales, as loaded (zero-extended)
+  uint32_t d;
+};
+__device__ __forceinline__ void q6_unit_load(Q6Unit& w, const uint8_t* blk, int g) {
+  const int h = g >> 1, l0 = 16 * (g & 1);
+  w.sh = (uint32_t)(uintptr_t)blk & 3u;
+  const uint8_t* ba = blk - w.sh;
+  w.a4 = *(const u32x4a*)(ba + 64 * h + l0);
+  w.a1 = *(const uint32_t*)(ba + 64 * h + l0 + 16);
+  w.b4 = *(const u32x4a*)(ba + 64 * h + 32 + l0);
+  w.b1 = *(const uint32_t*)(ba + 64 * h + 32 + l0 + 16);
+  w.h4 = *(const u32x4a*)(ba + 128 + 32 * h + l0);
+  w.h1 = *(const uint32_t*)(ba + 128 + 32 * h + l0 + 16);
+  // raw bytes only: any arithmetic on a loaded value here would make the
+  // compiler wait for it where it is loaded (for the prefetched tile too)
+  const uint8_t* scp = blk + 192 + 8 * h + (g & 1);
+  w.s0 = scp[0];
+  w.s1 = scp[2];
+  w.s2 = scp[4];
+  w.s3 = scp[6];
+  w.d = *(const uint16_t*)(blk + 208);
+}
+__device__ __forceinline__ void q6_run(const u32x4a& v4, uint32_t v1, uint32_t sh, uint32_t (&o)[4]) {
+  o[0] = __builtin_amdgcn_alignbyte(v4[1], v4[0], sh);
+  o[1] = __builtin_amdgcn_alignbyte(v4[2], v4[1], sh);
+  o[2] = __builtin_amdgcn_alignbyte(v4[3], v4[2], sh);
+  o[3] = __builtin_amdgcn_alignbyte(v1, v4[3], sh);
+}
+__device__ __forceinline__ float q6_unit_dot(const MvUnit<1>& X, const Q6Unit& w) {
+  uint32_t A[4], B[4], H[4];
+  q6_run(w.a4, w.a1, w.sh, A);
+  q6_run(w.b4, w.b1, w.sh, B);
+  q6_run(w.h4, w.h1, w.sh, H);
+  // the empty asm pins the byte extraction here, after the loads' wait
+  uint32_t r0 = w.s0, r1 = w.s1, r2 = w.s2, r3 = w.s3, rd = w.d;
+  asm volatile("" : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3), "+v"(rd));
+  const int32_t scs[4] = {(int32_t)(int8_t)r0, (int32_t)(int8_t)r1, (int32_t)(int8_t)r2, (int32_t)(int8_t)r3};
+  float part = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    int ah = 0, al = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t q;
+      if (k == 0) q = (A[j] & 0x0f0f0f0fu) | ((H[j] << 4) & 0x30303030u);
+      else if (k == 1) q = (B[j] & 0x0f0f0f0fu) | ((H[j] << 2) & 0x30303030u);
+      else if (k == 2) q = ((A[j] >> 4) & 0x0f0f0f0fu) | (H[j] & 0x30303030u);
+      else q = ((B[j] >> 4) & 0x0f0f0f0fu) | ((H[j] >> 2) & 0x30303030u);
+      ah = __builtin_amdgcn_sdot4((int)q, (int)X.hi[4 * k + j], ah, false);
+      al = __builtin_amdgcn_sdot4((int)q, (int)X.lo[4 * k + j], al, false);
+    }
+    const int I = (ah - X.c[k].x) * 256 + (al - X.c[k].y);
+    part += (float)scs[k] * X.s[k] * (float)I;
+  }
+  return part * g4d::f16_bits_to_f32(rd);
+}
+
 // Adds each row's U unit partials (RG lanes per row, then a butterfly) and
 // stores the tile's rows: y, softcap(y), or gelu(gate) * up for a pair.
 template <class T, int NTH, int NMAT>
@@ -981,7 +1060,6 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
   const int tid = threadIdx.x;
   const int slot = tid / G::U, u = tid % G::U;
   float* red = (float*)(smem + align16(MvX<BPR>::END));
-  uint8_t* tl = smem + align16(MvX<BPR>::END) + NMAT * align16((size_t)T::TR * T::RS * 4);
 
   MvPro<BPR, NWV, PRO> P;
   mv_pro_load<BPR, NWV, PRO>(P, pa);
@@ -992,59 +1070,63 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (QT == 0) {
-    // Q4_K: each thread's unit straight from global memory into registers;
-    // rows past M (a partial last tile) read row M - 1 and are not stored
-    Q4Unit wu[NMAT];
-    auto unit_ptr = [&](int m, uint32_t t) {
-      const uint32_t row = min(t * (uint32_t)T::TR + (uint32_t)slot, sg.M - 1);
-      return W[m] + (size_t)row * T::RB + (size_t)(u >> 2) * T::BYTES;
-    };
+  // each thread's unit straight from global memory into registers; rows
+  // past M (a partial last tile) read row M - 1 and are not stored
+  if (te - tb == 1) {
+    // one tile: each thread's unit straight from global memory into
+    // registers; rows past M (a partial tile) read row M - 1, not stored
+    using WU = typename std::conditional<QT == 0, Q4Unit, Q6Unit>::type;
+    WU wu[NMAT];
 #pragma unroll
-    for (int m = 0; m < NMAT; ++m) q4_unit_load(wu[m], unit_ptr(m, tb), u & 3);
+    for (int m = 0; m < NMAT; ++m) {
+      const uint32_t row = min(tb * (uint32_t)T::TR + (uint32_t)slot, sg.M - 1);
+      const uint8_t* blk = W[m] + (size_t)row * T::RB + (size_t)(u >> 2) * T::BYTES;
+      if constexpr (QT == 0) q4_unit_load(wu[m], blk, u & 3);
+      else q6_unit_load(wu[m], blk, u & 3);
+    }
     __builtin_amdgcn_sched_barrier(0);  // every weight load is issued before the activations are used
     mv_pro_finish<BPR, NWV, PRO>(P, smem, pa);
     MvUnit<QT> X;
     mv_unit_load<QT, BPR>(X, smem, u);
-    for (uint32_t t = tb; t < te; ++t) {
 #pragma unroll
-      for (int m = 0; m < NMAT; ++m) red[m * T::TR * T::RS + slot * T::RS + u] = q4_unit_dot(X, wu[m], u & 3);
-      if (t + 1 < te) {
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m) q4_unit_load(wu[m], unit_ptr(m, t + 1), u & 3);
-      }
-      __syncthreads();
-      mv_reduce_store<T, NTH, NMAT>(red, sg, t, tid, cap);
-      __syncthreads();  // the reduction buffer is reused by the next tile
+    for (int m = 0; m < NMAT; ++m) {
+      float v;
+      if constexpr (QT == 0) v = q4_unit_dot(X, wu[m], u & 3);
+      else v = q6_unit_dot(X, wu[m]);
+      red[m * T::TR * T::RS + slot * T::RS + u] = v;
     }
-  } else {
-    Stage<T::LPT> st[NMAT];
-    uint32_t nb = mv_tile_bytes<QT, BPR, NWV>(sg.M, tb);
+    lds_barrier();
+    mv_reduce_store<T, NTH, NMAT>(red, sg, tb, tid, cap);
+    return;
+  }
+  // several tiles: coalesced loads of the next tile into registers while
+  // this one is multiplied out of LDS
+  uint8_t* tl = smem + align16(MvX<BPR>::END) + NMAT * align16((size_t)T::TR * T::RS * 4);
+  Stage<T::LPT> st[NMAT];
+  uint32_t nb = mv_tile_bytes<QT, BPR, NWV>(sg.M, tb);
 #pragma unroll
-    for (int m = 0; m < NMAT; ++m) mv_stage_load<T, NTH>(W[m] + (size_t)tb * T::TB, nb, st[m]);
-    __builtin_amdgcn_sched_barrier(0);  // every weight load is issued before the activations are used
-    mv_pro_finish<BPR, NWV, PRO>(P, smem, pa);
-    MvUnit<QT> X;
-    mv_unit_load<QT, BPR>(X, smem, u);
-
-    for (uint32_t t = tb; t < te; ++t) {
-      __syncthreads();  // digits read (first tile) / previous tile reduced
+  for (int m = 0; m < NMAT; ++m) mv_stage_load<T, NTH>(W[m] + (size_t)tb * T::TB, nb, st[m]);
+  __builtin_amdgcn_sched_barrier(0);  // every weight load is issued before the activations are used
+  mv_pro_finish<BPR, NWV, PRO>(P, smem, pa);
+  MvUnit<QT> X;
+  mv_unit_load<QT, BPR>(X, smem, u);
+  for (uint32_t t = tb; t < te; ++t) {
+    __syncthreads();  // digits read (first tile) / previous tile reduced
 #pragma unroll
-      for (int m = 0; m < NMAT; ++m) mv_stage_store<T, NTH>(tl + m * T::LDS_T, nb, st[m]);
-      __syncthreads();
-      if (t + 1 < te) {
-        nb = mv_tile_bytes<QT, BPR, NWV>(sg.M, t + 1);
+    for (int m = 0; m < NMAT; ++m) mv_stage_store<T, NTH>(tl + m * T::LDS_T, nb, st[m]);
+    __syncthreads();
+    if (t + 1 < te) {
+      nb = mv_tile_bytes<QT, BPR, NWV>(sg.M, t + 1);
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m) mv_stage_load<T, NTH>(W[m] + (size_t)(t + 1) * T::TB, nb, st[m]);
-      }
-#pragma unroll
-      for (int m = 0; m < NMAT; ++m) {
-        const uint8_t* blk = tl + m * T::LDS_T + slot * T::RB + (u >> 2) * T::BYTES;
-        red[m * T::TR * T::RS + slot * T::RS + u] = mv_unit_dot<QT>(X, blk, u & 3);
-      }
-      __syncthreads();
-      mv_reduce_store<T, NTH, NMAT>(red, sg, t, tid, cap);
+      for (int m = 0; m < NMAT; ++m) mv_stage_load<T, NTH>(W[m] + (size_t)(t + 1) * T::TB, nb, st[m]);
     }
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m) {
+      const uint8_t* blk = tl + m * T::LDS_T + slot * T::RB + (u >> 2) * T::BYTES;
+      red[m * T::TR * T::RS + slot * T::RS + u] = mv_unit_dot<QT>(X, blk, u & 3);
+    }
+    __syncthreads();
+    mv_reduce_store<T, NTH, NMAT>(red, sg, t, tid, cap);
   }
 }
 
@@ -1266,7 +1348,7 @@ int mv_launch(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
   }
   sg.n = q.nseg;
   if (wgs == 0) return G4_OK;
-  const size_t lds = mv_lds_bytes<QT, BPR, NWV, NMAT>();
+  const size_t lds = mv_lds_bytes<QT, BPR, NWV, NMAT>(sg.rep > 1);
   int rc = claim_lds((const void*)mv_kernel<QT, BPR, NWV, PRO, NMAT>, ctx, lds);
   if (rc) return rc;
   hipLaunchKernelGGL((mv_kernel<QT, BPR, NWV, PRO, NMAT>), dim3(wgs), dim3(64 * NWV), lds, ctx->stream, sg, w_up,
