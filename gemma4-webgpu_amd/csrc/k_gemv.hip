@@ -921,10 +921,21 @@ __device__ __forceinline__ float mv_unit_dot(const MvUnit<QT>& X, const uint8_t*
 struct Q4Unit {
   u32x4a hd, q0, q1;
 };
-__device__ __forceinline__ void q4_unit_load(Q4Unit& w, const uint8_t* blk, int g) {
-  w.hd = *(const u32x4a*)blk;
-  w.q0 = *(const u32x4a*)(blk + 16 + 32 * g);
-  w.q1 = *(const u32x4a*)(blk + 32 + 32 * g);
+// Weight units are read through a buffer resource over the matrix, with a
+// cache policy per kernel shape: POL 2 (non-temporal) measured faster for
+// the one-matrix Q4_K launches (o, q/k/v: 0.3 us each), slower where
+// neighbouring threads re-read a line (Q6_K runs, the gate/up pair).
+typedef uint32_t bu4 __attribute__((ext_vector_type(4)));
+template <int POL>
+__device__ __forceinline__ u32x4a bl16(__amdgpu_buffer_rsrc_t r, uint32_t o) {
+  const bu4 v = __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, POL);
+  return u32x4a{v[0], v[1], v[2], v[3]};
+}
+template <int POL>
+__device__ __forceinline__ void q4_unit_load(Q4Unit& w, __amdgpu_buffer_rsrc_t r, uint32_t o, int g) {
+  w.hd = bl16<POL>(r, o);
+  w.q0 = bl16<POL>(r, o + 16 + 32 * g);
+  w.q1 = bl16<POL>(r, o + 32 + 32 * g);
 }
 __device__ __forceinline__ float q4_unit_dot(const MvUnit<0>& X, const Q4Unit& w, int g) {
   float sc_lo, sc_hi, m_lo, m_hi;
@@ -957,16 +968,18 @@ struct Q6Unit {
   uint32_t s0, s1, s2, s3;  // the unit's four int8 scales, as loaded (zero-extended)
   uint32_t d;
 };
-__device__ __forceinline__ void q6_unit_load(Q6Unit& w, const uint8_t* blk, int g) {
+template <int POL>
+__device__ __forceinline__ void q6_unit_load(Q6Unit& w, __amdgpu_buffer_rsrc_t r, uint32_t o, const uint8_t* blk,
+                                             int g) {
   const int h = g >> 1, l0 = 16 * (g & 1);
   w.sh = (uint32_t)(uintptr_t)blk & 3u;
-  const uint8_t* ba = blk - w.sh;
-  w.a4 = *(const u32x4a*)(ba + 64 * h + l0);
-  w.a1 = *(const uint32_t*)(ba + 64 * h + l0 + 16);
-  w.b4 = *(const u32x4a*)(ba + 64 * h + 32 + l0);
-  w.b1 = *(const uint32_t*)(ba + 64 * h + 32 + l0 + 16);
-  w.h4 = *(const u32x4a*)(ba + 128 + 32 * h + l0);
-  w.h1 = *(const uint32_t*)(ba + 128 + 32 * h + l0 + 16);
+  const uint32_t oa = o - w.sh;  // the dword at or before the block
+  w.a4 = bl16<POL>(r, oa + 64 * h + l0);
+  w.a1 = __builtin_amdgcn_raw_buffer_load_b32(r, oa + 64 * h + l0 + 16, 0, POL);
+  w.b4 = bl16<POL>(r, oa + 64 * h + 32 + l0);
+  w.b1 = __builtin_amdgcn_raw_buffer_load_b32(r, oa + 64 * h + 32 + l0 + 16, 0, POL);
+  w.h4 = bl16<POL>(r, oa + 128 + 32 * h + l0);
+  w.h1 = __builtin_amdgcn_raw_buffer_load_b32(r, oa + 128 + 32 * h + l0 + 16, 0, POL);
   // raw bytes only: any arithmetic on a loaded value here would make the
   // compiler wait for it where it is loaded (for the prefetched tile too)
   const uint8_t* scp = blk + 192 + 8 * h + (g & 1);
@@ -1079,10 +1092,15 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
     WU wu[NMAT];
 #pragma unroll
     for (int m = 0; m < NMAT; ++m) {
+      constexpr int POL = (QT == 0 && NMAT == 1) ? 2 : 0;
       const uint32_t row = min(tb * (uint32_t)T::TR + (uint32_t)slot, sg.M - 1);
-      const uint8_t* blk = W[m] + (size_t)row * T::RB + (size_t)(u >> 2) * T::BYTES;
-      if constexpr (QT == 0) q4_unit_load(wu[m], blk, u & 3);
-      else q6_unit_load(wu[m], blk, u & 3);
+      const uint32_t off = row * T::RB + (uint32_t)(u >> 2) * T::BYTES;
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc((void*)W[m], (short)0,
+                                            (int)(uint32_t)min((uint64_t)sg.M * T::RB, (uint64_t)0xffffffffu),
+                                            0x00020000);
+      if constexpr (QT == 0) q4_unit_load<POL>(wu[m], rs, off, u & 3);
+      else q6_unit_load<POL>(wu[m], rs, off, W[m] + off, u & 3);
     }
     __builtin_amdgcn_sched_barrier(0);  // every weight load is issued before the activations are used
     mv_pro_finish<BPR, NWV, PRO>(P, smem, pa);
