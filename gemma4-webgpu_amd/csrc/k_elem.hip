@@ -191,8 +191,11 @@ __global__ __launch_bounds__(NT) void argmax_partial(const float* logits, uint32
 }
 
 // stage 2: workgroup r reduces row r's partials; the initial candidate
-// (-1e30, 0) mirrors the reference's default result.
-__global__ __launch_bounds__(NT) void argmax_final(const Cand* part, int nparts, uint32_t* result) {
+// (-1e30, 0) mirrors the reference's default result. With `adv` non-null it
+// also adds `delta` to adv[r] (the row's position: a captured decode step
+// then needs no separate advance launch).
+__global__ __launch_bounds__(NT) void argmax_final(const Cand* part, int nparts, uint32_t* result, uint32_t* adv,
+                                                  uint32_t delta) {
   __shared__ Cand sm[4];
   part += (size_t)blockIdx.x * nparts;
   Cand c{-1e30f, 0u};
@@ -207,6 +210,7 @@ __global__ __launch_bounds__(NT) void argmax_final(const Cand* part, int nparts,
       if (better(sm[k], b)) b = sm[k];
     // a candidate that never beat the -1e30 initial value leaves index 0
     result[blockIdx.x] = (b.v > -1e30f) ? b.i : 0u;
+    if (adv) adv[blockIdx.x] += delta;
   }
 }
 
@@ -499,10 +503,11 @@ int g4_advanceSeqLens(g4_ctx* ctx, uint32_t* seq_lens, uint32_t num_seqs, uint32
   return G4_OK;
 }
 
-int g4_argmaxBatch(g4_ctx* ctx, const float* logits, uint32_t* result, uint32_t size, uint32_t batch) {
-  G4_ENTER(ctx);
-  G4_REQUIRE(logits && result, "g4_argmax: null buffer");
-  G4_REQUIRE(batch >= 1 && batch <= 1024, "g4_argmaxBatch: batch %u not in 1..1024", batch);
+namespace {
+int argmax_launch(g4_ctx* ctx, const char* fn, const float* logits, uint32_t* result, uint32_t size,
+                  uint32_t batch, uint32_t* adv, uint32_t delta) {
+  G4_REQUIRE(logits && result, "%s: null buffer", fn);
+  G4_REQUIRE(batch >= 1 && batch <= 1024, "%s: batch %u not in 1..1024", fn, batch);
   // about 4096 workgroups in all, at most kArgmaxBlocks per row
   const unsigned want = ceil_div(size, 1024), cap = std::max(1u, 4096u / batch);
   const int nb = want == 0 ? 1 : (int)std::min({want, (unsigned)kArgmaxBlocks, cap});
@@ -511,9 +516,23 @@ int g4_argmaxBatch(g4_ctx* ctx, const float* logits, uint32_t* result, uint32_t 
   if (rc) return rc;
   hipLaunchKernelGGL(argmax_partial, dim3(nb, batch), dim3(NT), 0, ctx->stream, logits, size, (Cand*)scratch);
   G4_LAUNCHED(ctx, "argmax_partial");
-  hipLaunchKernelGGL(argmax_final, dim3(batch), dim3(NT), 0, ctx->stream, (const Cand*)scratch, nb, result);
+  hipLaunchKernelGGL(argmax_final, dim3(batch), dim3(NT), 0, ctx->stream, (const Cand*)scratch, nb, result, adv,
+                     delta);
   G4_LAUNCHED(ctx, "argmax_final");
   return G4_OK;
+}
+}  // namespace
+
+int g4_argmaxBatch(g4_ctx* ctx, const float* logits, uint32_t* result, uint32_t size, uint32_t batch) {
+  G4_ENTER(ctx);
+  return argmax_launch(ctx, __func__, logits, result, size, batch, nullptr, 0);
+}
+
+int g4_argmaxAdvance(g4_ctx* ctx, const float* logits, uint32_t* result, uint32_t size, uint32_t batch,
+                     uint32_t* positions, uint32_t delta) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(positions, "g4_argmaxAdvance: null positions");
+  return argmax_launch(ctx, __func__, logits, result, size, batch, positions, delta);
 }
 
 int g4_argmax(g4_ctx* ctx, const float* logits, uint32_t* result, uint32_t size) {

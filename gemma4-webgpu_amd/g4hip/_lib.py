@@ -161,6 +161,7 @@ SIGNATURES = {
     "g4_argmax": (_I, [_P, _P, _P, _U32]),
     "g4_topk256": (_I, [_P, _P, _P, _U32]),
     "g4_argmaxBatch": (_I, [_P, _P, _P, _U32, _U32]),
+    "g4_argmaxAdvance": (_I, [_P, _P, _P, _U32, _U32, _P, _U32]),
     "g4_topk256Batch": (_I, [_P, _P, _P, _U32, _U32]),
     "g4_rmsNormMatmul_q4k": (_I, [_P, _P, _P, _P, _P, MatmulParams, _F]),
     "g4_normAddGateUpGelu_q4k": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, MatmulParams, _F]),

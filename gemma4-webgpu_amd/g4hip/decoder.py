@@ -282,6 +282,9 @@ class Decoder(_SyntheticModel):
             c.normAddMatmulSegments("q6k", self.down, last.post_ffn_norm, self.hidden2, self.final_norm,
                                     self.hidden, [self.lm_head], [self.logits], [s.vocab], s.hidden, s.eps,
                                     softcap=s.softcap)
+            if sample == "argmax" and advance:
+                c.argmaxAdvance(self.logits, self.token, s.vocab, 1, self.pos, 1)
+                return
             if sample == "argmax":
                 c.argmax(self.logits, self.token, s.vocab)
             else:
@@ -300,10 +303,9 @@ class Decoder(_SyntheticModel):
         return g
 
     def launches_per_step_fused(self) -> int:
-        """Kernel launches of step_fused: 5 per layer (plus the attention merge
-        kernel when the split count is too large to merge in-kernel), the head
-        (1), argmax (2) and the position advance (1)."""
-        return 5 * self.s.n_layers + (3 if self.lm_head is not None else 1) + 1
+        """Kernel launches of step_fused with argmax sampling: 5 per layer, the
+        head (1) and the argmax that also advances the position (1)."""
+        return 5 * self.s.n_layers + 2
 
 
 class BatchDecoder(_SyntheticModel):

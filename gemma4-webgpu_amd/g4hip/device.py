@@ -410,6 +410,10 @@ class Context:
     def argmaxBatch(self, logits: Ptr, result: Ptr, size: int, batch: int) -> None:
         check(lib().g4_argmaxBatch(self.h, _p(logits), _p(result), size, batch))
 
+    def argmaxAdvance(self, logits: Ptr, result: Ptr, size: int, batch: int, positions: Ptr, delta: int = 1) -> None:
+        """argmaxBatch, then positions[r] += delta for each row, in one launch."""
+        check(lib().g4_argmaxAdvance(self.h, _p(logits), _p(result), size, batch, _p(positions), delta))
+
     def topk256Batch(self, logits: Ptr, result: Ptr, size: int, batch: int) -> None:
         check(lib().g4_topk256Batch(self.h, _p(logits), _p(result), size, batch))
 

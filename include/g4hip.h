@@ -303,6 +303,12 @@ int g4_topk256(g4_ctx* ctx, const float* logits, float* result, uint32_t size);
  * each equal to what the one-row call returns for that row. batch <= 1024. */
 int g4_argmaxBatch(g4_ctx* ctx, const float* logits, uint32_t* result, uint32_t size, uint32_t batch);
 int g4_topk256Batch(g4_ctx* ctx, const float* logits, float* result, uint32_t size, uint32_t batch);
+/* g4_argmaxBatch, then positions[r] += delta for every row, in the same
+ * launch: the greedy sample (shaders/argmax.wgsl) and the position step the
+ * host takes after it (src/engine.ts:1724-1727) at the end of a captured
+ * decode step. */
+int g4_argmaxAdvance(g4_ctx* ctx, const float* logits, uint32_t* result, uint32_t size, uint32_t batch,
+                     uint32_t* positions, uint32_t delta);
 
 /* ------------------------------------------------------------------------ */
 /* Fused step kernels (the MI355X decode path; each is equivalent to a run   */

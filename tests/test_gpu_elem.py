@@ -159,3 +159,21 @@ def test_argmax_topk_batch_rows(ctx, size, batch):
     for b in range(batch):
         assert R[b] == O.argmax(X[b]), b
         assert bits_equal(T[b], O.topk256(X[b])), b
+
+
+@pytest.mark.parametrize("size,batch", [(262144, 1), (1000, 7), (4097, 32)])
+def test_argmax_advance(ctx, size, batch):
+    """Each row's argmax (the one-row rule, ties included) and
+    positions[r] += delta, over three calls in a row."""
+    rng = np.random.default_rng(size * 3 + batch)
+    pos0 = rng.integers(0, 1000, batch).astype(np.uint32)
+    p = ctx.from_numpy(pos0)
+    r = ctx.zeros(batch, np.uint32)
+    for call in range(3):
+        X = rng.integers(-3, 4, (batch, size)).astype(np.float32)
+        X[::2, rng.integers(0, size, 3)] = np.nan
+        ctx.argmaxAdvance(ctx.from_numpy(X), r, size, batch, p, 2)
+        R = r.download(np.uint32)
+        for b in range(batch):
+            assert R[b] == O.argmax(X[b]), (call, b)
+        assert np.array_equal(p.download(np.uint32), pos0 + 2 * (call + 1)), call
