@@ -28,6 +28,12 @@ struct g4_ctx {
 // Returns the context scratch buffer if it holds `bytes`.
 int g4_internal_scratch(g4_ctx* ctx, size_t bytes, void** out);
 
+// Second argmax stage (k_elem.hip): reduces `nparts` (value, index)
+// candidates per row, writes the winning index of row r to result[r] and,
+// with `adv` non-null, adds `delta` to adv[r].
+int g4_internal_argmax_final(g4_ctx* ctx, const void* parts, int nparts, uint32_t batch, uint32_t* result,
+                             uint32_t* adv, uint32_t delta);
+
 // Matrix-core matmul of `batch` activation vectors (k_batch.hip).
 int g4_internal_batch_matmul(g4_ctx* ctx, const char* fn, int qt, const float* x, const void* w, float* y,
                              uint32_t M, uint32_t N, uint32_t batch);
@@ -164,6 +170,39 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   for (int i = 0; i < NWAVES; ++i) t += red[i];
   __syncthreads();
   return t;
+}
+
+// argmax candidates (shaders/argmax.wgsl:12-33). The reference keeps, per
+// residue class c = i mod 256, the first strict '>' maximum (init -1e30,
+// index 0), then merges slot t with slot t + stride for stride = 128, 64,
+// ..., 1, keeping the lower slot on equal values. The last merge (slot 0 vs
+// 1) therefore prefers an even class, the one before it a class with bit 1
+// clear, and so on: among equal maxima the class with the smallest
+// bit-reversed 8-bit id wins, then the lowest index. NaN and values <= -1e30
+// never win; with no candidate the answer is 0. `better` encodes exactly that
+// order, so any partition of the index range reduces to the same answer.
+struct Cand {
+  float v;
+  uint32_t i;
+};
+
+__device__ __forceinline__ bool better(const Cand& a, const Cand& b) {
+  if (a.v > b.v) return true;
+  if (a.v < b.v || !(a.v == b.v)) return false;
+  const uint32_t ra = __brev(a.i & 255u), rb = __brev(b.i & 255u);
+  if (ra != rb) return ra < rb;
+  return a.i < b.i;
+}
+
+__device__ __forceinline__ Cand wave_best(Cand c) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    Cand d;
+    d.v = __shfl_xor(c.v, o, 64);
+    d.i = __shfl_xor(c.i, o, 64);
+    if (better(d, c)) c = d;
+  }
+  return c;
 }
 
 // Counter-based SplitMix64 (same definition as the host g4_splitmix64).

@@ -131,38 +131,11 @@ __global__ __launch_bounds__(NT) void kv_store_kernel(const float* k_in, const f
 // ---------------------------------------------------------------------------
 // argmax / topk256 (shaders/argmax.wgsl, topk256.wgsl)
 // ---------------------------------------------------------------------------
-// The reference keeps, per residue class c = i mod 256, the first strict '>'
-// maximum (init -1e30, index 0), then merges slot t with slot t + stride for
-// stride = 128, 64, ..., 1, keeping the lower slot on equal values. The last
-// merge (slot 0 vs 1) therefore prefers an even class, the one before it a
-// class with bit 1 clear, and so on: among equal maxima the class with the
-// smallest bit-reversed 8-bit id wins, then the lowest index. NaN and values
-// <= -1e30 never win; with no candidate the answer is 0. `better` encodes
-// exactly that order, so any partition of the index range reduces to the same
-// answer.
-struct Cand {
-  float v;
-  uint32_t i;
-};
-
-__device__ __forceinline__ bool better(const Cand& a, const Cand& b) {
-  if (a.v > b.v) return true;
-  if (a.v < b.v || !(a.v == b.v)) return false;
-  const uint32_t ra = __brev(a.i & 255u), rb = __brev(b.i & 255u);
-  if (ra != rb) return ra < rb;
-  return a.i < b.i;
-}
-
-__device__ __forceinline__ Cand wave_best(Cand c) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    Cand d;
-    d.v = __shfl_xor(c.v, o, 64);
-    d.i = __shfl_xor(c.i, o, 64);
-    if (better(d, c)) c = d;
-  }
-  return c;
-}
+// The candidate order (g4d::Cand, g4d::better) reproduces the reference's
+// per-residue scan and tree merge; see g4_internal.hpp.
+using g4d::Cand;
+using g4d::better;
+using g4d::wave_best;
 
 constexpr int kArgmaxBlocks = 256;
 
@@ -516,10 +489,7 @@ int argmax_launch(g4_ctx* ctx, const char* fn, const float* logits, uint32_t* re
   if (rc) return rc;
   hipLaunchKernelGGL(argmax_partial, dim3(nb, batch), dim3(NT), 0, ctx->stream, logits, size, (Cand*)scratch);
   G4_LAUNCHED(ctx, "argmax_partial");
-  hipLaunchKernelGGL(argmax_final, dim3(batch), dim3(NT), 0, ctx->stream, (const Cand*)scratch, nb, result, adv,
-                     delta);
-  G4_LAUNCHED(ctx, "argmax_final");
-  return G4_OK;
+  return g4_internal_argmax_final(ctx, scratch, nb, batch, result, adv, delta);
 }
 }  // namespace
 
@@ -623,3 +593,11 @@ int g4_fill_normal_f16(g4_ctx* ctx, uint16_t* dst, uint64_t n, uint64_t seed, fl
 }
 
 }  // extern "C"
+
+int g4_internal_argmax_final(g4_ctx* ctx, const void* parts, int nparts, uint32_t batch, uint32_t* result,
+                             uint32_t* adv, uint32_t delta) {
+  hipLaunchKernelGGL(argmax_final, dim3(batch), dim3(NT), 0, ctx->stream, (const Cand*)parts, nparts, result, adv,
+                     delta);
+  G4_LAUNCHED(ctx, "argmax_final");
+  return G4_OK;
+}

@@ -474,7 +474,8 @@ struct GemvSeg {
 struct GemvSegs {
   GemvSeg s[4];
   int n;
-  uint32_t rep;  // consecutive row tiles per workgroup
+  uint32_t rep;     // consecutive row tiles per workgroup
+  g4d::Cand* amx;   // mv_kernel, one matrix: per-workgroup argmax candidate of the stored rows, or null
 };
 
 // EPI: 0 = store y, 1 = store softcap(y) (shaders/logit_softcap.wgsl).
@@ -1027,7 +1028,8 @@ __device__ __forceinline__ float q6_unit_dot(const MvUnit<1>& X, const Q6Unit& w
 // Adds each row's U unit partials (RG lanes per row, then a butterfly) and
 // stores the tile's rows: y, softcap(y), or gelu(gate) * up for a pair.
 template <class T, int NTH, int NMAT>
-__device__ __forceinline__ void mv_reduce_store(const float* red, const GemvSeg& sg, uint32_t t, int tid, float cap) {
+__device__ __forceinline__ void mv_reduce_store(const float* red, const GemvSeg& sg, uint32_t t, int tid, float cap,
+                                                bool track, g4d::Cand& best) {
   constexpr int U = NTH / T::TR;
   const int gl = tid % T::RG;
   for (int r = tid / T::RG; r < T::TR; r += NTH / T::RG) {  // uniform within a group
@@ -1048,12 +1050,34 @@ __device__ __forceinline__ void mv_reduce_store(const float* red, const GemvSeg&
       if constexpr (NMAT == 2) v = gelu_tanh(y[0]) * y[1];
       else v = cap > 0.f ? softcap(y[0], cap) : y[0];
       sg.Y[row] = v;
+      if constexpr (NMAT == 1) {
+        const g4d::Cand d{v, row};
+        if (track && g4d::better(d, best)) best = d;
+      }
     }
   }
 }
 
+// The workgroup's best candidate over the rows it stored (argmax stage 1 run
+// as the matvec's epilogue: the logits are not read back); `sm` holds NWV
+// candidates not otherwise in use.
+template <int NWV>
+__device__ __forceinline__ void mv_argmax_partial(g4d::Cand c, g4d::Cand* sm, g4d::Cand* dst) {
+  c = g4d::wave_best(c);
+  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = c;
+  lds_barrier();
+  if (threadIdx.x == 0) {
+    g4d::Cand b = sm[0];
+#pragma unroll
+    for (int k = 1; k < NWV; ++k)
+      if (g4d::better(sm[k], b)) b = sm[k];
+    *dst = b;
+  }
+}
+
 // NMAT = 1: y, or softcap(y) when cap > 0 (shaders/logit_softcap.wgsl), for
-// each segment's rows. NMAT = 2: gate/up pair, out = gelu(gate) * up
+// each segment's rows; with `segs.amx`, also the workgroup's argmax candidate
+// (shaders/argmax.wgsl order) in segs.amx[blockIdx.x]. NMAT = 2: gate/up pair, out = gelu(gate) * up
 // (shaders/gelu_mul.wgsl:10-16).
 template <int QT, int BPR, int NWV, int PRO, int NMAT>
 __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8_t* w_up, ProArgs pa, float cap) {
@@ -1114,7 +1138,10 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
       red[m * T::TR * T::RS + slot * T::RS + u] = v;
     }
     lds_barrier();
-    mv_reduce_store<T, NTH, NMAT>(red, sg, tb, tid, cap);
+    g4d::Cand best{-1e30f, 0u};
+    mv_reduce_store<T, NTH, NMAT>(red, sg, tb, tid, cap, segs.amx != nullptr, best);
+    if constexpr (NMAT == 1)
+      if (segs.amx) mv_argmax_partial<NWV>(best, (g4d::Cand*)(smem + MvX<BPR>::RED8), segs.amx + blockIdx.x);
     return;
   }
   // several tiles: coalesced loads of the next tile into registers while
@@ -1128,6 +1155,7 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
   mv_pro_finish<BPR, NWV, PRO>(P, smem, pa);
   MvUnit<QT> X;
   mv_unit_load<QT, BPR>(X, smem, u);
+  g4d::Cand best{-1e30f, 0u};
   for (uint32_t t = tb; t < te; ++t) {
     __syncthreads();  // digits read (first tile) / previous tile reduced
 #pragma unroll
@@ -1144,8 +1172,10 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
       red[m * T::TR * T::RS + slot * T::RS + u] = mv_unit_dot<QT>(X, blk, u & 3);
     }
     __syncthreads();
-    mv_reduce_store<T, NTH, NMAT>(red, sg, t, tid, cap);
+    mv_reduce_store<T, NTH, NMAT>(red, sg, t, tid, cap, segs.amx != nullptr, best);
   }
+  if constexpr (NMAT == 1)
+    if (segs.amx) mv_argmax_partial<NWV>(best, (g4d::Cand*)(smem + MvX<BPR>::RED8), segs.amx + blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1266,6 +1296,9 @@ struct LaunchReq {
   float cap;
   ProArgs pa;
   uint32_t ldy;
+  g4d::Cand* amx = nullptr;     // one-vector launches: per-workgroup argmax candidates (see GemvSegs)
+  uint32_t amx_cap = 0;         // candidates `amx` holds
+  uint32_t* wgs_out = nullptr;  // receives the workgroup count
 };
 
 constexpr uint32_t kMaxGemvWgs = 2048;  // beyond this a workgroup walks several row tiles
@@ -1365,7 +1398,11 @@ int mv_launch(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
     wgs += ceil_div(ceil_div(q.segs[i].M, T::TR), sg.rep);
   }
   sg.n = q.nseg;
+  sg.amx = q.amx;
+  if (q.wgs_out) *q.wgs_out = wgs;
   if (wgs == 0) return G4_OK;
+  if (q.amx && wgs > q.amx_cap)
+    return g4::set_error(G4_ERR_UNSUPPORTED, "matvec: %u workgroups exceed the %u argmax candidates", wgs, q.amx_cap);
   const size_t lds = mv_lds_bytes<QT, BPR, NWV, NMAT>(sg.rep > 1);
   int rc = claim_lds((const void*)mv_kernel<QT, BPR, NWV, PRO, NMAT>, ctx, lds);
   if (rc) return rc;
@@ -1597,6 +1634,37 @@ int g4_normAddMatmulSegments(g4_ctx* ctx, int wtype, const float* x, const uint1
   LaunchReq q{wtype, segs, nseg, N, 1, pro, softcap_cap != 0.f ? 1 : 0, softcap_cap,
               ProArgs{x, w1, residual, w2, h_out, eps}, 0};
   return launch_gemv(ctx, q);
+}
+
+int g4_normAddMatmulArgmax(g4_ctx* ctx, int wtype, const float* x, const uint16_t* w1, const float* residual,
+                           const uint16_t* w2, float* h_out, const void* weight, float* logits, uint32_t rows,
+                           uint32_t N, float eps, float softcap_cap, uint32_t* result, uint32_t* positions,
+                           uint32_t delta) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(wtype == 0 || wtype == 1, "g4_normAddMatmulArgmax: wtype must be 0 (Q4_K) or 1 (Q6_K)");
+  G4_REQUIRE(x && w1 && weight && logits && result && rows > 0, "g4_normAddMatmulArgmax: null buffer or no rows");
+  G4_REQUIRE(!residual == !w2, "g4_normAddMatmulArgmax: residual and w2 go together");
+  G4_REQUIRE(N == 1536 || N == 2048, "g4_normAddMatmulArgmax: N=%u unsupported (1536 or 2048)", N);
+  G4_REQUIRE(((uintptr_t)x & 15) == 0 && (!residual || ((uintptr_t)residual & 15) == 0) &&
+                 (!h_out || ((uintptr_t)h_out & 15) == 0),
+             "g4_normAddMatmulArgmax: activations must be 16-byte aligned");
+  G4_REQUIRE(((uintptr_t)w1 & 7) == 0 && ((uintptr_t)w2 & 7) == 0,
+             "g4_normAddMatmulArgmax: norm weights must be 8-byte aligned");
+  int rc = check_w(__func__, wtype, weight);
+  if (rc) return rc;
+  // one candidate per workgroup: at most two workgroups per CU for a matrix
+  // walked tile by tile, one per tile below that
+  const size_t max_parts = 2 * (size_t)ctx->num_cus;
+  void* parts = nullptr;
+  rc = g4_internal_scratch(ctx, max_parts * sizeof(g4d::Cand), &parts);
+  if (rc) return rc;
+  GemvSeg seg{(const uint8_t*)weight, logits, rows, 0};
+  uint32_t wgs = 0;
+  LaunchReq q{wtype, &seg, 1, N, 1, residual ? 2 : 1, softcap_cap != 0.f ? 1 : 0, softcap_cap,
+              ProArgs{x, w1, residual, w2, h_out, eps}, 0, (g4d::Cand*)parts, (uint32_t)max_parts, &wgs};
+  rc = launch_gemv(ctx, q);
+  if (rc) return rc;  // (N is 1536 or 2048: every failure here sets its own message)
+  return g4_internal_argmax_final(ctx, parts, (int)wgs, 1, result, positions, delta);
 }
 
 }  // extern "C"

@@ -257,7 +257,9 @@ class Decoder(_SyntheticModel):
           4. post-attn norm-add -> pre-FFN rmsNorm -> gate/up matvecs -> GELU product
           5. down matvec (Q6_K)
         then the last post-FFN norm-add + final rmsNorm + LM head + softcap in
-        one launch, and the argmax.
+        one launch; with argmax sampling its workgroups also leave their
+        argmax candidates, which a one-workgroup launch reduces to the token
+        (and advances the position).
         """
         c, s = self.ctx, self.s
         for il, L in enumerate(self.layers):
@@ -279,16 +281,15 @@ class Decoder(_SyntheticModel):
             c.matmulQuant(self.act, L.wdown, self.down, s.hidden, s.ffn, "q6k")
         last = self.layers[-1]
         if self.lm_head is not None:
+            if sample == "argmax":
+                c.normAddMatmulArgmax("q6k", self.down, last.post_ffn_norm, self.hidden2, self.final_norm,
+                                      self.hidden, self.lm_head, self.logits, s.vocab, s.hidden, self.token, s.eps,
+                                      softcap=s.softcap, positions=self.pos if advance else None, delta=1)
+                return
             c.normAddMatmulSegments("q6k", self.down, last.post_ffn_norm, self.hidden2, self.final_norm,
                                     self.hidden, [self.lm_head], [self.logits], [s.vocab], s.hidden, s.eps,
                                     softcap=s.softcap)
-            if sample == "argmax" and advance:
-                c.argmaxAdvance(self.logits, self.token, s.vocab, 1, self.pos, 1)
-                return
-            if sample == "argmax":
-                c.argmax(self.logits, self.token, s.vocab)
-            else:
-                c.topk256(self.logits, self.topk, s.vocab)
+            c.topk256(self.logits, self.topk, s.vocab)
         else:
             c.fusedNormAdd(self.down, last.post_ffn_norm, self.hidden2, self.hidden, s.hidden, s.eps)
         if advance:
@@ -304,7 +305,8 @@ class Decoder(_SyntheticModel):
 
     def launches_per_step_fused(self) -> int:
         """Kernel launches of step_fused with argmax sampling: 5 per layer, the
-        head (1) and the argmax that also advances the position (1)."""
+        head with its argmax candidates (1) and their reduction, which also
+        advances the position (1)."""
         return 5 * self.s.n_layers + 2
 
 

@@ -209,6 +209,15 @@ class Context:
         check(lib().g4_normAddMatmulSegments(self.h, {"q4k": 0, "q6k": 1}[wtype], _p(x), _p(w1), _p(residual),
                                              _p(w2), _p(h_out), W, Y, R, n, N, eps, softcap))
 
+    def normAddMatmulArgmax(self, wtype: str, x: Ptr, w1: Ptr, residual: Ptr, w2: Ptr, h_out: Ptr, weight: Ptr,
+                            logits: Ptr, rows: int, N: int, result: Ptr, eps: float = 1e-6, softcap: float = 0.0,
+                            positions: Ptr = None, delta: int = 1) -> None:
+        """normAddMatmulSegments over one matrix into `logits`, and *result = argmax(logits) (reference ties
+        and NaN rule) from the matvec's own per-workgroup candidates; *positions += delta when given."""
+        check(lib().g4_normAddMatmulArgmax(self.h, {"q4k": 0, "q6k": 1}[wtype], _p(x), _p(w1), _p(residual),
+                                           _p(w2), _p(h_out), _p(weight), _p(logits), rows, N, eps, softcap,
+                                           _p(result), _p(positions), delta))
+
     def normAddMatmulSegmentsBatch(self, wtype: str, x: Ptr, w1: Ptr, residual: Ptr, w2: Ptr, h_out: Ptr,
                                    weights, outputs, rows, N: int, batch: int, eps: float = 1e-6,
                                    softcap: float = 0.0) -> None:
@@ -411,7 +420,7 @@ class Context:
         check(lib().g4_argmaxBatch(self.h, _p(logits), _p(result), size, batch))
 
     def argmaxAdvance(self, logits: Ptr, result: Ptr, size: int, batch: int, positions: Ptr, delta: int = 1) -> None:
-        """argmaxBatch, then positions[r] += delta for each row, in one launch."""
+        """argmaxBatch, then positions[r] += delta for each row (done by the reduction's final stage)."""
         check(lib().g4_argmaxAdvance(self.h, _p(logits), _p(result), size, batch, _p(positions), delta))
 
     def topk256Batch(self, logits: Ptr, result: Ptr, size: int, batch: int) -> None:

@@ -345,6 +345,19 @@ int g4_normAddMatmulSegments(g4_ctx* ctx, int wtype, const float* x, const uint1
                              const void* const* weights, float* const* outputs,
                              const uint32_t* rows, int nseg, uint32_t N, float eps,
                              float softcap_cap);
+/* The LM head with greedy sampling in two launches: g4_normAddMatmulSegments
+ * over one matrix (logits[rows], softcapped when softcap_cap != 0), whose
+ * workgroups also keep the argmax candidate of the rows they store, then the
+ * reduction of those candidates: *result = g4_argmax(logits, rows), ties
+ * and NaN as shaders/argmax.wgsl:12-33, without reading the logits back;
+ * with `positions` non-NULL, *positions += delta (the GPU-written position
+ * of src/engine.ts:1724-1727). Replaces src/engine.ts:1686-1717 (final norm,
+ * LM head, softcap, argmax). */
+int g4_normAddMatmulArgmax(g4_ctx* ctx, int wtype, const float* x, const uint16_t* w1,
+                           const float* residual, const uint16_t* w2, float* h_out,
+                           const void* weight, float* logits, uint32_t rows, uint32_t N, float eps,
+                           float softcap_cap, uint32_t* result, uint32_t* positions,
+                           uint32_t delta);
 
 /* The same over `batch` activation vectors at once (ragged multi-sequence
  * decode: src/engine.ts:1546-1554 run once per sequence). x, residual and

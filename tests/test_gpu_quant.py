@@ -239,3 +239,54 @@ def test_norm_add_matmul_q6k_softcap(ctx):
     got = y.download(np.float32)
     assert np.max(np.abs(got)) <= 30.0 and np.max(np.abs(ref)) > 20.0
     assert_close(got, ref, what="lm head + softcap")
+
+
+@pytest.mark.parametrize("M,scale,specials", [(20000, 20.0, False), (3000, 20.0, False), (20000, 2000.0, False),
+                                              (3000, 2000.0, True), (262144, 20.0, False)])
+def test_norm_add_matmul_argmax(ctx, M, scale, specials):
+    """LM head + softcap with the argmax taken from the matvec's own per-workgroup
+    candidates: the logits are those of normAddMatmulSegments bit for bit, and the
+    index is the reference rule's argmax of them (ties and NaN included). A
+    2000x final-norm weight drives many logits to exactly 30.0 (tanh saturates),
+    so the residue tie order decides; NaN block scales make NaN rows, kept as
+    NaN logits by running that case without the softcap (whose clamp maps NaN
+    to -cap)."""
+    N = 1536
+    W = O.gen_q6k(60, M * N // 256).reshape(M, -1).copy()
+    if specials:
+        W[5::97, 208:210] = np.frombuffer(struct.pack("<H", 0x7e00), np.uint8)  # d = NaN
+    W = W.reshape(-1)
+    x = O.gen_normal_f32(61, N, 0.0, 2.0)
+    res = O.gen_normal_f32(62, N, 0.0, 5.0)
+    w1 = O.gen_normal_f16(63, N, 1.0, 0.1)
+    w2 = O.gen_normal_f16(64, N, 1.0, 0.1)
+    w2s = (w2.view(np.float16).astype(np.float32) * scale).astype(np.float16).view(np.uint16)
+    cap = 0.0 if specials else 30.0
+    dx, dw1, dres, dw2, dW = (ctx.from_numpy(a) for a in (x, w1, res, w2s, W))
+    y_ref = ctx.empty(M, np.float32)
+    ctx.normAddMatmulSegments("q6k", dx, dw1, dres, dw2, None, [dW], [y_ref], [M], N, 1e-6, softcap=cap)
+    want = y_ref.download(np.float32)
+    y = ctx.empty(M, np.float32)
+    dh = ctx.empty(N, np.float32)
+    r = ctx.zeros(1, np.uint32)
+    pos0 = np.array([77], np.uint32)
+    p = ctx.from_numpy(pos0)
+    for call in range(2):
+        ctx.normAddMatmulArgmax("q6k", dx, dw1, dres, dw2, dh, dW, y, M, N, r, 1e-6, softcap=cap,
+                                positions=p, delta=3)
+        got = y.download(np.float32)
+        assert bits_equal(got, want), call
+        idx = int(r.download(np.uint32)[0])
+        assert idx == O.argmax(got), (call, idx, O.argmax(got))
+        assert p.download(np.uint32)[0] == 77 + 3 * (call + 1)
+    if scale > 100 and not specials:
+        assert np.count_nonzero(got == np.float32(30.0)) > 8
+    if specials:
+        assert np.isnan(got).any()
+    assert_close(dh.download(np.float32), O.fused_norm_add(x, w1, res, 1e-6), rel=1e-6, cos=0.99999999,
+                 what="h_out")
+    # no positions: the index only
+    r2 = ctx.zeros(1, np.uint32)
+    ctx.normAddMatmulArgmax("q6k", dx, dw1, dres, dw2, None, dW, y, M, N, r2, 1e-6, softcap=cap)
+    assert int(r2.download(np.uint32)[0]) == idx
+    assert p.download(np.uint32)[0] == 77 + 6
