@@ -684,13 +684,21 @@ __device__ __forceinline__ float4 block_sum_4(float4 v, float* red) {
   return t;
 }
 
-// Activation registers of one thread: the float4 at element 4*tid + 4*NTH*p.
-// Eight consecutive lanes hold one 32-element sub-block.
+// Activation registers of one prologue thread: the float4 at element
+// 4*tid + 4*PTH*p. Eight consecutive lanes hold one 32-element sub-block.
+// Only the first PW waves (one per SIMD) load, normalise and digitise the
+// vector; the others go straight to the barrier that publishes the digits.
+// A SIMD issues one wave64 VALU instruction per 4 cycles whichever wave it
+// comes from, and the prologue's per-wave part (block sums, the norm
+// scalars) is the same in every wave that runs it, so spreading the vector
+// over all waves only multiplies that part on the SIMDs holding two or
+// three of them.
 template <int BPR, int NWV, int PRO>
 struct MvPro {
   static constexpr int K = BPR * 256;
-  static constexpr int NTH = MvGeom<BPR, NWV>::NTH;
-  static constexpr int XP = (K + 4 * NTH - 1) / (4 * NTH);
+  static constexpr int PW = NWV >= 4 ? 4 : NWV;  // prologue waves
+  static constexpr int PTH = 64 * PW;
+  static constexpr int XP = (K + 4 * PTH - 1) / (4 * PTH);
   float4 x[XP];
   float4 r[PRO == 2 ? XP : 1];
   uint2 w1[PRO >= 1 ? XP : 1];
@@ -699,7 +707,8 @@ struct MvPro {
   // sub-block spreads these broadcast reads over the L2 channels instead of
   // all workgroups asking for the same lines at the same moment.
   __device__ static int rot() { return (int)((blockIdx.x * 37u) % (uint32_t)(K / 32)) * 32; }
-  __device__ static int slot(int p) { return 4 * (int)threadIdx.x + 4 * NTH * p; }
+  __device__ static bool active() { return (int)threadIdx.x < PTH; }  // (wave-uniform)
+  __device__ static int slot(int p) { return 4 * (int)threadIdx.x + 4 * PTH * p; }
   __device__ static bool live(int p) { return slot(p) < K; }
   // element held at round p (valid when live(p))
   __device__ static int elem(int p) {
@@ -711,6 +720,7 @@ struct MvPro {
 template <int BPR, int NWV, int PRO>
 __device__ __forceinline__ void mv_pro_load(MvPro<BPR, NWV, PRO>& P, const ProArgs& a) {
   using PP = MvPro<BPR, NWV, PRO>;
+  if (!PP::active()) return;
   // Unconditional loads (see chunk_off). Lanes past K read element 0 again;
   // they form whole 8-lane sub-block groups whose digits are never stored,
   // and their squares are masked out of the norms.
@@ -726,54 +736,12 @@ __device__ __forceinline__ void mv_pro_load(MvPro<BPR, NWV, PRO>& P, const ProAr
   }
 }
 
-// Normalises (PRO 1/2) and digitises the activations into LDS, then barrier.
+// The prologue waves' activations as 8-bit digit pairs, per-sub-block scales,
+// sums and 16-run digit sums in LDS.
 template <int BPR, int NWV, int PRO>
-__device__ __forceinline__ void mv_pro_finish(MvPro<BPR, NWV, PRO>& P, uint8_t* smem, const ProArgs& a) {
+__device__ __forceinline__ void mv_digitize(const MvPro<BPR, NWV, PRO>& P, uint8_t* smem) {
   using PP = MvPro<BPR, NWV, PRO>;
   using X = MvX<BPR>;
-  float* red8 = (float*)(smem + X::RED8);
-  if constexpr (PRO == 1) {
-    float ss = 0.f;
-#pragma unroll
-    for (int p = 0; p < PP::XP; ++p) {
-      const float q = sumsq(P.x[p]);
-      ss += PP::live(p) ? q : 0.f;
-    }
-    ss = block_sum_1<NWV>(ss, red8);
-    const float inv1 = 1.0f / sqrtf(ss / (float)X::K + a.eps);
-#pragma unroll
-    for (int p = 0; p < PP::XP; ++p) P.x[p] = mul_w(P.x[p], P.w1[p], inv1);
-  } else if constexpr (PRO == 2) {
-    // h = r + t, t = (o * w1) * inv1. Both norms come out of one block
-    // reduction: sum(o^2), and sum(h^2) expanded as
-    // sum(r^2) + 2 inv1 sum(r (o w1)) + inv1^2 sum((o w1)^2).
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 ow[PP::XP];
-#pragma unroll
-    for (int p = 0; p < PP::XP; ++p) {
-      ow[p] = mul_w(P.x[p], P.w1[p], 1.0f);
-      const float4 o = P.x[p], r = P.r[p], t = ow[p];
-      const float so = sumsq(o), sr = sumsq(r), st = sumsq(t);
-      const float rt = (r.x * t.x + r.y * t.y) + (r.z * t.z + r.w * t.w);
-      const bool lv = PP::live(p);
-      acc.x += lv ? so : 0.f;
-      acc.y += lv ? sr : 0.f;
-      acc.z += lv ? rt : 0.f;
-      acc.w += lv ? st : 0.f;
-    }
-    acc = block_sum_4<NWV>(acc, red8);
-    const float inv1 = 1.0f / sqrtf(acc.x / (float)X::K + a.eps);
-    const float ss2 = fmaxf(acc.y + 2.0f * inv1 * acc.z + inv1 * inv1 * acc.w, 0.f);
-    const float inv2 = 1.0f / sqrtf(ss2 / (float)X::K + a.eps);
-#pragma unroll
-    for (int p = 0; p < PP::XP; ++p) {
-      const float4 t = ow[p];
-      const float4 h = make_float4(P.r[p].x + t.x * inv1, P.r[p].y + t.y * inv1, P.r[p].z + t.z * inv1,
-                                   P.r[p].w + t.w * inv1);
-      if (a.h_out && blockIdx.x == 0 && PP::live(p)) *(float4*)(a.h_out + PP::elem(p)) = h;
-      P.x[p] = mul_w(h, P.w2[p], inv2);
-    }
-  }
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int p = 0; p < PP::XP; ++p) {
@@ -788,7 +756,9 @@ __device__ __forceinline__ void mv_pro_finish(MvPro<BPR, NWV, PRO>& P, uint8_t* 
     sm += dpp<kDppXor2>(sm);
     am = fmaxf(am, dpp<kDppHalfMirror>(am));
     sm += dpp<kDppHalfMirror>(sm);
-    const float inv = am > 0.f ? XQ / am : 0.f;
+    // hardware reciprocal (1 ulp): |x * inv| stays below XQ + 0.01, so the
+    // rounded digits keep |q| <= XQ
+    const float inv = am > 0.f ? XQ * __builtin_amdgcn_rcpf(am) : 0.f;
     const float xs[4] = {v.x, v.y, v.z, v.w};
     uint32_t ph = 0, pl = 0;
     int shi = 0, slo = 0;
@@ -816,6 +786,94 @@ __device__ __forceinline__ void mv_pro_finish(MvPro<BPR, NWV, PRO>& P, uint8_t* 
       if ((lane & 3) == 0) ((int2*)(smem + X::C16))[f / 16] = make_int2(32 * shi, 32 * slo);
     }
   }
+}
+
+// 1 / sqrt(ss / K + eps) with the hardware reciprocal square root (1 ulp).
+template <int K>
+__device__ __forceinline__ float mv_inv_rms(float ss, float eps) {
+  return __builtin_amdgcn_rsqf(ss * (1.0f / (float)K) + eps);
+}
+
+// Normalises (PRO 1/2) and digitises the activations into LDS, then barrier.
+// Every wave of the workgroup calls it (it holds the barriers); only the
+// prologue waves compute.
+template <int BPR, int NWV, int PRO>
+__device__ __forceinline__ void mv_pro_finish(MvPro<BPR, NWV, PRO>& P, uint8_t* smem, const ProArgs& a) {
+  using PP = MvPro<BPR, NWV, PRO>;
+  using X = MvX<BPR>;
+  float* red8 = (float*)(smem + X::RED8);
+  const bool act = PP::active();
+  const int wv = (int)threadIdx.x >> 6;
+  if constexpr (PRO == 1) {
+    if (act) {
+      float ss = 0.f;
+#pragma unroll
+      for (int p = 0; p < PP::XP; ++p) {
+        const float q = sumsq(P.x[p]);
+        ss += PP::live(p) ? q : 0.f;
+      }
+      ss = wave_sum_dpp(ss);
+      if ((threadIdx.x & 63) == 0) red8[wv] = ss;
+    }
+    lds_barrier();
+    if (act) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < PP::PW; ++i) ss += red8[i];
+      const float inv1 = mv_inv_rms<X::K>(ss, a.eps);
+#pragma unroll
+      for (int p = 0; p < PP::XP; ++p) P.x[p] = mul_w(P.x[p], P.w1[p], inv1);
+    }
+  } else if constexpr (PRO == 2) {
+    // h = r + t, t = (o * w1) * inv1. Both norms come out of one block
+    // reduction: sum(o^2), and sum(h^2) expanded as
+    // sum(r^2) + 2 inv1 sum(r (o w1)) + inv1^2 sum((o w1)^2).
+    float4 ow[PP::XP];
+    if (act) {
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int p = 0; p < PP::XP; ++p) {
+        ow[p] = mul_w(P.x[p], P.w1[p], 1.0f);
+        const float4 o = P.x[p], r = P.r[p], t = ow[p];
+        const float so = sumsq(o), sr = sumsq(r), st = sumsq(t);
+        const float rt = (r.x * t.x + r.y * t.y) + (r.z * t.z + r.w * t.w);
+        const bool lv = PP::live(p);
+        acc.x += lv ? so : 0.f;
+        acc.y += lv ? sr : 0.f;
+        acc.z += lv ? rt : 0.f;
+        acc.w += lv ? st : 0.f;
+      }
+      acc.x = wave_sum_dpp(acc.x);
+      acc.y = wave_sum_dpp(acc.y);
+      acc.z = wave_sum_dpp(acc.z);
+      acc.w = wave_sum_dpp(acc.w);
+      if ((threadIdx.x & 63) == 0) *(float4*)(red8 + 4 * wv) = acc;
+    }
+    lds_barrier();
+    if (act) {
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int i = 0; i < PP::PW; ++i) {
+        const float4 r = *(const float4*)(red8 + 4 * i);
+        acc.x += r.x;
+        acc.y += r.y;
+        acc.z += r.z;
+        acc.w += r.w;
+      }
+      const float inv1 = mv_inv_rms<X::K>(acc.x, a.eps);
+      const float ss2 = fmaxf(acc.y + 2.0f * inv1 * acc.z + inv1 * inv1 * acc.w, 0.f);
+      const float inv2 = mv_inv_rms<X::K>(ss2, a.eps);
+#pragma unroll
+      for (int p = 0; p < PP::XP; ++p) {
+        const float4 t = ow[p];
+        const float4 h = make_float4(P.r[p].x + t.x * inv1, P.r[p].y + t.y * inv1, P.r[p].z + t.z * inv1,
+                                     P.r[p].w + t.w * inv1);
+        if (a.h_out && blockIdx.x == 0 && PP::live(p)) *(float4*)(a.h_out + PP::elem(p)) = h;
+        P.x[p] = mul_w(h, P.w2[p], inv2);
+      }
+    }
+  }
+  if (act) mv_digitize<BPR, NWV, PRO>(P, smem);
   lds_barrier();
 }
 
@@ -1076,9 +1134,9 @@ __device__ __forceinline__ void mv_argmax_partial(g4d::Cand c, g4d::Cand* sm, g4
 }
 
 // NMAT = 1: y, or softcap(y) when cap > 0 (shaders/logit_softcap.wgsl), for
-// each segment's rows; with `segs.amx`, also the workgroup's argmax candidate
-// (shaders/argmax.wgsl order) in segs.amx[blockIdx.x]. NMAT = 2: gate/up pair, out = gelu(gate) * up
-// (shaders/gelu_mul.wgsl:10-16).
+// each segment's rows; with `segs.amx`, also the workgroup's argmax
+// candidate (shaders/argmax.wgsl order) in segs.amx[blockIdx.x]. NMAT = 2:
+// gate/up pair, out = gelu(gate) * up (shaders/gelu_mul.wgsl:10-16).
 template <int QT, int BPR, int NWV, int PRO, int NMAT>
 __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8_t* w_up, ProArgs pa, float cap) {
   using G = MvGeom<BPR, NWV>;
