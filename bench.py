@@ -409,6 +409,8 @@ def main():
     ap.add_argument("--census-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=5)
+    ap.add_argument("--no-warm", action="store_true",
+                    help="attention launches do not read the next matvecs' weights into L2")
     ap.add_argument("--eager", action="store_true",
                     help="launch the step kernels directly instead of replaying a captured graph "
                          "(for profilers that do not follow graph launches)")
@@ -443,9 +445,9 @@ def main():
 
     if args.eager:
         def step():
-            dec.step_fused("argmax")
+            dec.step_fused("argmax", warm=not args.no_warm)
     else:
-        graph = dec.capture_fused("argmax")
+        graph = dec.capture_fused("argmax", warm=not args.no_warm)
 
         def step():
             ctx.graph_launch(graph)

@@ -874,6 +874,10 @@ __global__ __launch_bounds__(NT, 2) void mq_attn_kernel(MqArgs a) {
 // With one sequence the grid is a few dozen workgroups, so latency is the
 // instruction count of one wave's path: the per-thread work outside the
 // MFMA loop is kept to a handful of vector operations.
+constexpr int kMaxWarm = 4;
+// Dynamic LDS a warming launch adds to each workgroup's static ~75 KB: past
+// half of the CU's 160 KB, so one workgroup per CU (unused otherwise).
+constexpr size_t kWarmLds = 16384;
 struct MqfArgs {
   const float* q_raw;  // [nqh][256]
   const float* k_raw;  // [nkh][256]
@@ -895,6 +899,13 @@ struct MqfArgs {
   float* ws1;     // group partials [nkh][MQF_FAN][8] (m, l, o)
   uint32_t* cnt;  // [nkh][MQF_CNT] arrivals (groups, then the top), zero between calls
   float* out;     // [nqh][256]
+  // L2 warming: workgroups max_chunks.. of row 0 read the weights of the
+  // launches that follow (see mqf_warm)
+  const uint8_t* wbase[kMaxWarm];
+  uint32_t wtotal[kMaxWarm];  // bytes of the matrix (reads past it return 0)
+  uint32_t wwgb[kMaxWarm];    // bytes each consuming workgroup reads
+  uint32_t wnwg[kMaxWarm];    // consuming workgroups
+  uint32_t nwarm_regions, nwarm;  // regions; warming workgroups (a multiple of 8)
 };
 
 constexpr int MQF_QS = 264;  // LDS stride of a q column (halves)
@@ -925,7 +936,60 @@ __device__ __forceinline__ float4 ld_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off
   return make_float4(v.x, v.y, v.z, v.w);
 }
 
+// Brings the weights of the launches that follow into the L2 of the XCD
+// that will read them. Workgroups are dispatched to the 8 XCDs in turn
+// (linear id mod 8), in this launch and in the consuming ones, so consuming
+// workgroup j reads through the L2 of XCD j % 8: warming workgroup p (at
+// linear id max_chunks + p, XCD c) reads the tiles of consuming workgroups
+// j = c + 8 (p / 8 + R i), R = nwarm / 8. These workgroups run on the CUs
+// the attention leaves idle; the loads go through a buffer resource sized to
+// each matrix, so a partial last tile reads zeros past its end.
+__device__ __forceinline__ void mqf_warm(const MqfArgs& a) {
+  const uint32_t p = blockIdx.x - a.max_chunks;
+  const uint32_t c = blockIdx.x & 7u, r = p >> 3, R = a.nwarm >> 3;
+  const uint32_t t = threadIdx.x;
+  // regions past nwarm_regions have no records (their loads return 0)
+  __amdgpu_buffer_rsrc_t rs[kMaxWarm];
+  uint32_t wgb[kMaxWarm], nwg[kMaxWarm], maxwg = 0;
+#pragma unroll
+  for (int g = 0; g < kMaxWarm; ++g) {
+    const bool on = (uint32_t)g < a.nwarm_regions;
+    rs[g] = __builtin_amdgcn_make_buffer_rsrc((void*)a.wbase[g], (short)0, on ? (int)a.wtotal[g] : 0, 0x00020000);
+    wgb[g] = on ? a.wwgb[g] : 0u;
+    nwg[g] = on ? a.wnwg[g] : 0u;
+    maxwg = max(maxwg, nwg[g]);
+  }
+  constexpr uint32_t kStep = 64u * NT * 8u;  // bytes one round of 8 loads covers
+  uint32_t acc = 0;
+  // one region's round at a time, the workgroups' first rounds staggered:
+  // a burst of every region at once queued ahead of the attention's own
+  // memory traffic and slowed it by 1 us
+  for (uint32_t k = 0; k < (p & 3u); ++k) __builtin_amdgcn_s_sleep(16);
+  for (uint32_t j = c + 8u * r; j < maxwg; j += 8u * R) {
+#pragma unroll
+    for (int g = 0; g < kMaxWarm; ++g) {
+      for (uint32_t o = 0; o < wgb[g]; o += kStep) {
+        uint32_t v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          // one dword per 64-byte line brings the line into the cache
+          const uint32_t off = o + (64u * NT) * (uint32_t)k + 64u * t;
+          const bool in = j < nwg[g] && off < wgb[g];
+          v[k] = __builtin_amdgcn_raw_buffer_load_b32(rs[g], in ? j * wgb[g] + off : 0xfffffff0u, 0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc ^= v[k];
+      }
+    }
+  }
+  asm volatile("" ::"v"(acc));
+}
+
 __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
+  if (blockIdx.x >= a.max_chunks) {  // (uniform) L2 warming workgroups
+    if (blockIdx.y == 0) mqf_warm(a);
+    return;
+  }
   // K and V tiles; after the last step, the waves' o rows [4 waves][256 dims][16 rows]
   __shared__ __align__(16) _Float16 kvt[2 * MQ_STEP * MQ_RS];
   __shared__ __align__(16) _Float16 qs[16 * MQF_QS];  // B operand: column c = head c % 8, hi (c < 8) / lo
@@ -1727,10 +1791,27 @@ int g4_attnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw, cons
                        const uint16_t* q_norm_w, const uint16_t* k_norm_w, const uint16_t* rope_freqs,
                        uint16_t* k_cache, uint16_t* v_cache, float* output, g4_attn_fused_params p, void* workspace,
                        size_t workspace_bytes, const uint32_t* position_dev) {
+  return g4_attnDecodeFusedWarm(ctx, q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs, k_cache, v_cache, output, p,
+                                workspace, workspace_bytes, position_dev, nullptr, 0);
+}
+
+int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float* v_raw,
+                           const uint16_t* q_norm_w, const uint16_t* k_norm_w, const uint16_t* rope_freqs,
+                           uint16_t* k_cache, uint16_t* v_cache, float* output, g4_attn_fused_params p,
+                           void* workspace, size_t workspace_bytes, const uint32_t* position_dev,
+                           const g4_warm_region* regions, int nregions) {
   G4_ENTER(ctx);
   G4_REQUIRE(q_raw && k_raw && v_raw && q_norm_w && k_norm_w && k_cache && v_cache && output && workspace &&
                  position_dev,
              "g4_attnDecodeFused: null buffer");
+  G4_REQUIRE(nregions >= 0 && nregions <= kMaxWarm && (nregions == 0 || regions),
+             "g4_attnDecodeFusedWarm: 0..%d warm regions", kMaxWarm);
+  for (int i = 0; i < nregions; ++i) {
+    const g4_warm_region& r = regions[i];
+    G4_REQUIRE(r.base && r.total_bytes > 0 && r.total_bytes <= 0xffffffffull && r.wg_bytes > 0 && r.nwgs > 0 &&
+                   r.wg_bytes * (uint64_t)r.nwgs <= 0xffffffffull,
+               "g4_attnDecodeFusedWarm: region %d empty or beyond 4 GiB", i);
+  }
   G4_REQUIRE(!p.apply_divisor || rope_freqs, "g4_attnDecodeFused: apply_divisor needs rope_freqs");
   G4_REQUIRE(((uintptr_t)k_cache & 15) == 0 && ((uintptr_t)v_cache & 15) == 0 && ((uintptr_t)workspace & 15) == 0,
              "g4_attnDecodeFused: KV caches and workspace must be 16-byte aligned");
@@ -1769,7 +1850,22 @@ int g4_attnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw, cons
     m.ws1 = (float*)((uint8_t*)workspace + kMqfCnt + mp.bytes_ws0);
     m.cnt = (uint32_t*)workspace;
     m.out = output;
-    hipLaunchKernelGGL(mqf_kernel, dim3(mp.max_chunks, p.num_kv_heads), dim3(NT), 0, ctx->stream, m);
+    // warming workgroups on the CUs the attention leaves idle, a multiple
+    // of 8 so that every XCD gets as many. A launch that warms asks for
+    // kWarmLds more LDS per workgroup, so no two of its workgroups share a
+    // CU: a warming workgroup next to an attention one slowed it by 1 us.
+    const uint32_t busy = mp.max_chunks * p.num_kv_heads;
+    const uint32_t idle = (uint32_t)ctx->num_cus > busy ? (uint32_t)ctx->num_cus - busy : 0u;
+    m.nwarm = nregions ? idle / 8u * 8u : 0u;
+    m.nwarm_regions = m.nwarm ? (uint32_t)nregions : 0u;
+    for (int i = 0; i < (int)m.nwarm_regions; ++i) {
+      m.wbase[i] = (const uint8_t*)regions[i].base;
+      m.wtotal[i] = (uint32_t)regions[i].total_bytes;
+      m.wwgb[i] = (uint32_t)regions[i].wg_bytes;
+      m.wnwg[i] = regions[i].nwgs;
+    }
+    hipLaunchKernelGGL(mqf_kernel, dim3(mp.max_chunks + m.nwarm, p.num_kv_heads), dim3(NT),
+                       m.nwarm ? kWarmLds : 0, ctx->stream, m);
     G4_LAUNCHED(ctx, "attn_decode_fused_mfma");
     return G4_OK;
   }

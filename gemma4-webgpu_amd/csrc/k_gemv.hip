@@ -1445,6 +1445,7 @@ constexpr uint32_t kMvFullWgs = 240, kMvMinWgs = 160;
 template <int QT, int BPR, int NWV, int PRO, int NMAT>
 int mv_launch(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
   using T = MvTile<QT, BPR, NWV>;
+  static_assert(T::TR == 16 * NWV / BPR, "mv_pick / mv_shape compute the tile rows as 16 NWV / BPR");
   GemvSegs sg{};
   uint32_t tiles = 0;
   for (int i = 0; i < q.nseg; ++i) tiles += ceil_div(q.segs[i].M, T::TR);
@@ -1471,20 +1472,37 @@ int mv_launch(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
 }
 
 // workgroup widths in waves for a row of BPR super-blocks (slots must tile it)
-template <int BPR> struct MvWaves { static constexpr int A = 12, B = 9, C = 6, D = 3; };
-template <> struct MvWaves<32> { static constexpr int A = 12, B = 8, C = 6, D = 4; };
+struct MvWaveSet {
+  int A, B, C, D;
+};
+constexpr MvWaveSet mv_waves(uint32_t bpr) { return bpr == 32 ? MvWaveSet{12, 8, 6, 4} : MvWaveSet{12, 9, 6, 3}; }
+template <int BPR> struct MvWaves {
+  static constexpr int A = mv_waves(BPR).A, B = mv_waves(BPR).B, C = mv_waves(BPR).C, D = mv_waves(BPR).D;
+};
+
+// The workgroup width of a one-vector launch over row segments of
+// 256*bpr-wide rows (the rule stated above kMvFullWgs).
+int mv_pick(uint32_t bpr, const GemvSeg* segs, int nseg) {
+  const MvWaveSet w = mv_waves(bpr);
+  auto tiles = [&](int nwv) {
+    const uint32_t slots = (uint32_t)(16 * nwv) / bpr;  // 64 nwv threads over 4 bpr units per row
+    uint32_t t = 0;
+    for (int i = 0; i < nseg; ++i) t += ceil_div(segs[i].M, slots);
+    return t;
+  };
+  if (tiles(w.A) >= kMvFullWgs) return w.A;
+  if (tiles(w.B) >= kMvFullWgs) return w.B;
+  if (tiles(w.C) >= kMvMinWgs) return w.C;
+  return w.D;
+}
 
 template <int QT, int BPR, int PRO, int NMAT>
 int mv_rows(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
   using Wv = MvWaves<BPR>;
-  auto tiles = [&](uint32_t slots) {
-    uint32_t t = 0;
-    for (int i = 0; i < q.nseg; ++i) t += ceil_div(q.segs[i].M, slots);
-    return t;
-  };
-  if (tiles(MvGeom<BPR, Wv::A>::SLOTS) >= kMvFullWgs) return mv_launch<QT, BPR, Wv::A, PRO, NMAT>(ctx, q, w_up);
-  if (tiles(MvGeom<BPR, Wv::B>::SLOTS) >= kMvFullWgs) return mv_launch<QT, BPR, Wv::B, PRO, NMAT>(ctx, q, w_up);
-  if (tiles(MvGeom<BPR, Wv::C>::SLOTS) >= kMvMinWgs) return mv_launch<QT, BPR, Wv::C, PRO, NMAT>(ctx, q, w_up);
+  const int nwv = mv_pick(BPR, q.segs, q.nseg);
+  if (nwv == Wv::A) return mv_launch<QT, BPR, Wv::A, PRO, NMAT>(ctx, q, w_up);
+  if (nwv == Wv::B) return mv_launch<QT, BPR, Wv::B, PRO, NMAT>(ctx, q, w_up);
+  if (nwv == Wv::C) return mv_launch<QT, BPR, Wv::C, PRO, NMAT>(ctx, q, w_up);
   return mv_launch<QT, BPR, Wv::D, PRO, NMAT>(ctx, q, w_up);
 }
 
@@ -1590,9 +1608,43 @@ int launch_gateup(g4_ctx* ctx, const uint8_t* wg, const uint8_t* wu, float* out,
   return mv_rows<0, BPR, PRO, 2>(ctx, q, wu);
 }
 
+// The one-vector launch's geometry for W [M x 256*bpr] (mv_rows, then
+// mv_launch): the workgroup width, the rows a tile holds, the tiles a
+// workgroup walks and the workgroup count.
+struct MvShape {
+  int nwv;
+  uint32_t rows_per_tile, rep, wgs;
+};
+MvShape mv_shape(const g4_ctx* ctx, uint32_t M, uint32_t bpr) {
+  const GemvSeg seg{nullptr, nullptr, M, 0};
+  MvShape s{};
+  s.nwv = mv_pick(bpr, &seg, 1);
+  s.rows_per_tile = (uint32_t)(16 * s.nwv) / bpr;
+  const uint32_t t = ceil_div(M, s.rows_per_tile);
+  s.rep = ceil_div(t, 2u * (uint32_t)ctx->num_cus);  // as mv_launch
+  s.wgs = ceil_div(t, s.rep);
+  return s;
+}
+
 }  // namespace
 
 extern "C" {
+
+int g4_matmulWarmRegion(g4_ctx* ctx, int wtype, uint32_t M, uint32_t N, const void* weight, g4_warm_region* out) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(out && weight && M > 0, "g4_matmulWarmRegion: null buffer or no rows");
+  G4_REQUIRE(wtype == 0 || wtype == 1, "g4_matmulWarmRegion: wtype must be 0 (Q4_K) or 1 (Q6_K)");
+  G4_REQUIRE(N % 256 == 0 && supported_bpr(N / 256), "g4_matmulWarmRegion: N=%u has no one-vector launch", N);
+  const uint32_t bpr = N / 256;
+  const MvShape sh = mv_shape(ctx, M, bpr);
+  const uint64_t row_bytes = (uint64_t)bpr * (wtype ? 210 : 144);
+  out->base = weight;
+  out->total_bytes = (uint64_t)M * row_bytes;
+  out->wg_bytes = (uint64_t)sh.rep * sh.rows_per_tile * row_bytes;
+  out->nwgs = sh.wgs;
+  out->reserved = 0;
+  return G4_OK;
+}
 
 int g4_matmulQuant_q4k(g4_ctx* ctx, const float* input, const void* weight, float* output, g4_matmul_params p) {
   return matmul_quant(ctx, __func__, 0, input, weight, output, p, 1);

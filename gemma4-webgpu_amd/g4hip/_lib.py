@@ -50,6 +50,11 @@ class AttnOutputParams(ctypes.Structure):  # shaders/attn_output.wgsl:1
                 ("head_dim", ctypes.c_uint32), ("seq_len", ctypes.c_uint32)]
 
 
+class WarmRegion(ctypes.Structure):  # g4_warm_region
+    _fields_ = [("base", ctypes.c_void_p), ("total_bytes", ctypes.c_uint64), ("wg_bytes", ctypes.c_uint64),
+                ("nwgs", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
 class AttnFusedParams(ctypes.Structure):
     _fields_ = [("num_q_heads", ctypes.c_uint32), ("num_kv_heads", ctypes.c_uint32),
                 ("head_dim", ctypes.c_uint32), ("max_seq_len", ctypes.c_uint32),
@@ -143,6 +148,9 @@ SIGNATURES = {
     "g4_attnDecode_dev": (_I, [_P, _P, _P, _P, _P, AttnScoreParams, _P, _SZ, _P]),
     "g4_attnDecodeFused_workspace_size": (_I, [AttnFusedParams, ctypes.POINTER(_SZ)]),
     "g4_attnDecodeFused": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, AttnFusedParams, _P, _SZ, _P]),
+    "g4_attnDecodeFusedWarm": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, AttnFusedParams, _P, _SZ, _P,
+                                    ctypes.POINTER(WarmRegion), _I]),
+    "g4_matmulWarmRegion": (_I, [_P, _I, _U32, _U32, _P, ctypes.POINTER(WarmRegion)]),
     "g4_pagedAttnDecode_workspace_size": (_I, [PagedAttnParams, ctypes.POINTER(_SZ)]),
     "g4_pagedAttnDecode": (_I, [_P, _P, _P, _P, _P, _P, _P, PagedAttnParams, _P, _SZ]),
     "g4_pagedKvStore": (_I, [_P, _P, _P, _P, _P, _P, _P, PagedAttnParams]),

@@ -190,6 +190,12 @@ class Decoder(_SyntheticModel):
                  max(ctx.attn_fused_workspace_bytes(p) for p in self.attn_params))
         # split-K partials + arrival counters; zeroed once, the kernels keep the counters zeroed
         self.attn_ws = ctx.zeros(ws, np.uint8)
+        # weights of the gate/up and down launches that follow each attention
+        # launch, read into the L2 caches by that launch (the o projection's
+        # 1.8 MB arrive in time on their own: measured no faster from L2)
+        self.warm = [[ctx.matmulWarmRegion("q4k", s.ffn, s.hidden, L.wgate),
+                      ctx.matmulWarmRegion("q4k", s.ffn, s.hidden, L.wup),
+                      ctx.matmulWarmRegion("q6k", s.hidden, s.ffn, L.wdown)] for L in self.layers]
         ctx.fill_normal_f32(self.hidden, s.hidden, self._seed(), 0.0, 1.0)
         ctx.sync()
 
@@ -247,7 +253,7 @@ class Decoder(_SyntheticModel):
             c.topk256(self.logits, self.topk, s.vocab)
 
     # ---- the fused MI355X step ----------------------------------------------
-    def step_fused(self, sample: str = "argmax", advance: bool = True) -> None:
+    def step_fused(self, sample: str = "argmax", advance: bool = True, warm: bool = True) -> None:
         """One token at position *pos (device), then pos += 1 on the device.
 
         Five launches per layer:
@@ -259,7 +265,9 @@ class Decoder(_SyntheticModel):
         then the last post-FFN norm-add + final rmsNorm + LM head + softcap in
         one launch; with argmax sampling its workgroups also leave their
         argmax candidates, which a one-workgroup launch reduces to the token
-        (and advances the position).
+        (and advances the position). With `warm`, each attention launch also
+        reads the gate/up and down weights of its layer into the L2 caches
+        (on the CUs the attention leaves idle).
         """
         c, s = self.ctx, self.s
         for il, L in enumerate(self.layers):
@@ -273,8 +281,13 @@ class Decoder(_SyntheticModel):
                 prev = self.layers[il - 1]
                 c.normAddMatmulSegments("q4k", self.down, prev.post_ffn_norm, self.hidden2, L.attn_norm,
                                         self.hidden, ws, outs, rows, s.hidden, s.eps)
-            c.attnDecodeFused(self.q, self.k, self.v, L.q_norm, L.k_norm, self.rope_freqs, L.k_cache, L.v_cache,
-                              self.attn, self.attn_params[il], self.attn_ws, self.pos)
+            if warm:
+                c.attnDecodeFusedWarm(self.q, self.k, self.v, L.q_norm, L.k_norm, self.rope_freqs, L.k_cache,
+                                      L.v_cache, self.attn, self.attn_params[il], self.attn_ws, self.pos,
+                                      self.warm[il])
+            else:
+                c.attnDecodeFused(self.q, self.k, self.v, L.q_norm, L.k_norm, self.rope_freqs, L.k_cache,
+                                  L.v_cache, self.attn, self.attn_params[il], self.attn_ws, self.pos)
             c.matmulQuant(self.attn, L.wo, self.o, s.hidden, s.q_dim)
             c.normAddGateUpGelu_q4k(self.o, L.post_attn_norm, self.hidden, L.pre_ffn_norm, L.wgate, L.wup,
                                     self.hidden2, self.act, s.ffn, s.hidden, s.eps)
@@ -295,10 +308,10 @@ class Decoder(_SyntheticModel):
         if advance:
             c.advancePosition(self.pos, 1)
 
-    def capture_fused(self, sample: str = "argmax"):
+    def capture_fused(self, sample: str = "argmax", warm: bool = True):
         self.ctx.graph_begin()
         try:
-            self.step_fused(sample)
+            self.step_fused(sample, warm=warm)
         finally:
             g = self.ctx.graph_end()
         return g

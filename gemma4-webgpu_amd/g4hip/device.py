@@ -20,6 +20,7 @@ from ._lib import (
     MatmulParams,
     NormAddParams,
     NormRopeParams,
+    WarmRegion,
     PagedAttnFusedParams,
     PagedAttnParams,
     PerHeadNormParams,
@@ -329,6 +330,23 @@ class Context:
         check(lib().g4_attnDecodeFused(self.h, _p(q_raw), _p(k_raw), _p(v_raw), _p(q_norm_w), _p(k_norm_w),
                                        _p(rope_freqs), _p(k_cache), _p(v_cache), _p(out), p, _p(workspace),
                                        workspace.nbytes, _p(position_dev)))
+
+    def matmulWarmRegion(self, wtype: str, M: int, N: int, weight: Ptr) -> WarmRegion:
+        """The bytes each workgroup of the one-vector matvec launch over W [M x N] reads."""
+        r = WarmRegion()
+        check(lib().g4_matmulWarmRegion(self.h, {"q4k": 0, "q6k": 1}[wtype], M, N, _p(weight), ctypes.byref(r)))
+        return r
+
+    def attnDecodeFusedWarm(self, q_raw: Ptr, k_raw: Ptr, v_raw: Ptr, q_norm_w: Ptr, k_norm_w: Ptr,
+                            rope_freqs: Ptr, k_cache: Ptr, v_cache: Ptr, out: Ptr, p: AttnFusedParams,
+                            workspace: Buffer, position_dev: Ptr, regions) -> None:
+        """attnDecodeFused whose launch also reads `regions` (WarmRegion list, <= 4) into the L2 caches
+        the matvecs that follow will read them through."""
+        n = len(regions)
+        arr = (WarmRegion * max(n, 1))(*regions)
+        check(lib().g4_attnDecodeFusedWarm(self.h, _p(q_raw), _p(k_raw), _p(v_raw), _p(q_norm_w), _p(k_norm_w),
+                                           _p(rope_freqs), _p(k_cache), _p(v_cache), _p(out), p, _p(workspace),
+                                           workspace.nbytes, _p(position_dev), arr, n))
 
     @staticmethod
     def paged_params(num_seqs, nqh, nkh, hd, page_size, max_pages, max_seq_len, num_pages, scale=1.0, window=0):

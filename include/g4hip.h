@@ -190,6 +190,33 @@ int g4_attnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw, cons
                        uint16_t* k_cache, uint16_t* v_cache, float* output, g4_attn_fused_params p,
                        void* workspace, size_t workspace_bytes, const uint32_t* position_dev);
 
+/* L2 warming (an MI355X scheduling aid with no counterpart in the
+ * reference, for hosts that issue a fixed launch sequence such as the decode
+ * step). A one-vector matvec launch over W [M x N] has workgroup j read the
+ * bytes [j * wg_bytes, (j + 1) * wg_bytes) of W (of each matrix of a gate/up
+ * pair); g4_matmulWarmRegion describes that for the launch
+ * g4_matmulQuant_* / g4_normAddGateUpGelu_q4k would make. */
+typedef struct {
+  const void* base;
+  uint64_t total_bytes; /* bytes of the matrix; at most 4 GiB - 1 */
+  uint64_t wg_bytes;
+  uint32_t nwgs;
+  uint32_t reserved;
+} g4_warm_region;
+int g4_matmulWarmRegion(g4_ctx* ctx, int wtype, uint32_t M, uint32_t N, const void* weight,
+                        g4_warm_region* out);
+/* g4_attnDecodeFused, whose launch also reads up to 4 regions (the weights
+ * of the matvecs that follow it) into the L2 cache of the XCD each
+ * consuming workgroup will run on, using the CUs the attention leaves idle.
+ * Results are those of g4_attnDecodeFused; only where the weights come from
+ * changes. */
+int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float* v_raw,
+                           const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                           const uint16_t* rope_freqs, uint16_t* k_cache, uint16_t* v_cache,
+                           float* output, g4_attn_fused_params p, void* workspace,
+                           size_t workspace_bytes, const uint32_t* position_dev,
+                           const g4_warm_region* regions, int nregions);
+
 /* Ragged multi-sequence decode attention over a paged f16 KV pool: sequence
  * s has seq_lens[s] positions; its logical position t lives in page
  * page_table[s * max_pages + t / page_size], slot t % page_size, of a pool

@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from gpu_util import assert_close
+from gpu_util import assert_close, bits_equal
 
 pytestmark = pytest.mark.gpu
 
@@ -225,3 +225,46 @@ def test_attn_decode_fused_shared_workspace(ctx):
             ctx.attnDecodeFused(dev["qr"], dev["kr"], dev["vr"], dev["qw"], dev["kw"], dev["table"], dk, dv, out, p,
                                 ws, ctx.from_numpy(np.array([pos], np.uint32)))
             assert_close(out.download(np.float32), c["ref"], what=f"shared ws round {rnd} pos={pos} hd={hd}")
+
+
+@pytest.mark.parametrize("pos,window", [(700, 512), (3000, 0), (20, 512)])
+def test_attn_decode_fused_warm_matches(ctx, pos, window):
+    """The launch that also reads the following matvecs' weights into the L2
+    caches computes exactly what the plain one does (output and caches bit for
+    bit); the warm regions describe the matvec launches' own tiling, with
+    sizes that are not multiples of a tile (a partial last tile reads past no
+    matrix end)."""
+    hd, theta, div = 256, (1e6 if window == 0 else 1e4), int(window == 0)
+    c = _fused_inputs(pos, window, hd, theta, div)
+    p = ctx.attn_fused_params(c["nqh"], c["nkh"], hd, c["cap"], window, 1e-6, theta, div)
+    ws = ctx.zeros(ctx.attn_fused_workspace_bytes(p), np.uint8)
+    dev = {n: ctx.from_numpy(c[n]) for n in ("qr", "kr", "vr", "qw", "kw", "table")}
+    shapes = [("q4k", 1536, 2048), ("q4k", 6144, 1536), ("q4k", 1000, 1536), ("q6k", 1537, 6144)]
+    mats, regions = [], []
+    for wt, M, N in shapes:
+        nb = M * N // 256
+        w = ctx.alloc(nb * (144 if wt == "q4k" else 210))
+        (ctx.fill_q4k if wt == "q4k" else ctx.fill_q6k)(w, nb, M + N)
+        r = ctx.matmulWarmRegion(wt, M, N, w)
+        assert r.total_bytes == nb * (144 if wt == "q4k" else 210)
+        assert r.nwgs >= 1 and r.wg_bytes * r.nwgs >= r.total_bytes
+        assert r.wg_bytes * (r.nwgs - 1) < r.total_bytes  # every workgroup has rows
+        mats.append(w)
+        regions.append(r)
+    outs = []
+    for warm in (False, True, True):
+        dk, dv = ctx.from_numpy(c["k"]), ctx.from_numpy(c["v"])
+        out = ctx.empty(c["nqh"] * hd, np.float32)
+        args = (dev["qr"], dev["kr"], dev["vr"], dev["qw"], dev["kw"], dev["table"], dk, dv, out, p, ws,
+                ctx.from_numpy(np.array([pos], np.uint32)))
+        if warm:
+            ctx.attnDecodeFusedWarm(*args, regions)
+        else:
+            ctx.attnDecodeFused(*args)
+        outs.append((out.download(np.float32), dk.download(np.uint16), dv.download(np.uint16)))
+    for o in outs[1:]:
+        for a, b in zip(outs[0], o):
+            assert bits_equal(a, b)
+    assert_close(outs[0][0], c["ref"], what=f"warm pos={pos}")
+    for w in mats:
+        w.free()
