@@ -126,7 +126,8 @@ __device__ __forceinline__ void digits4(const XView& xv, int vec, uint32_t e, fl
 // Prologue modes: 0 = x from global; 1 = x * w / rms(x) (shaders/rms_norm.wgsl);
 // 2 = h = residual + o * w1 / rms(o); x = h * w2 / rms(h)
 // (shaders/fused_norm_add.wgsl then shaders/rms_norm.wgsl); h is written to
-// h_out by workgroup 0 when h_out is non-null.
+// h_out by workgroup 0 when h_out is non-null; 3 (one-vector matvec, Q6_K)
+// = x already digitised by the launch that produced it (MvD8 block at x).
 struct ProArgs {
   const float* x;         // [NV][K] (mode 2: o)
   const uint16_t* w1;
@@ -476,6 +477,7 @@ struct GemvSegs {
   int n;
   uint32_t rep;     // consecutive row tiles per workgroup
   g4d::Cand* amx;   // mv_kernel, one matrix: per-workgroup argmax candidate of the stored rows, or null
+  uint8_t* d8;      // mv_kernel, gate/up pair: the outputs also as an MvD8 block (K = rows), or null
 };
 
 // EPI: 0 = store y, 1 = store softcap(y) (shaders/logit_softcap.wgsl).
@@ -600,12 +602,32 @@ struct MvX {
                           RED8 = C16 + 16 * NSB, END = RED8 + 256;  // a 4-wide block sum of up to 16 waves
 };
 
+// Pre-digitised activations ("D8"), the same bytes in global memory and in
+// LDS: the two digit planes, then one scale per 8 elements, then 32 x the
+// digit sums of each 8 (the Q6_K -32 offset term). A producer that holds 8
+// consecutive outputs in one wave (the gate/up launch's GELU rows) writes
+// them, so the consumer (the down matvec) skips the per-element prologue.
+template <int BPR>
+struct MvD8 {
+  static constexpr int K = BPR * 256;
+  static constexpr size_t HI = 0, LO = K, S = 2 * (size_t)K, C = S + 4 * (size_t)(K / 8), BYTES = C + 8 * (size_t)(K / 8);
+};
+__host__ __device__ constexpr size_t d8_bytes(uint32_t K) { return 2 * (size_t)K + 12 * (size_t)(K / 8); }
+
+// End of the activation area (and its block-sum slots) for a prologue mode.
+template <int BPR, int PRO>
+struct MvXA {
+  static constexpr size_t RED8 = PRO == 3 ? align16(MvD8<BPR>::BYTES) : MvX<BPR>::RED8;
+  static constexpr size_t END = RED8 + 256;
+};
+
 // A workgroup with one tile reads its weight units straight into registers;
 // one that walks several tiles stages them through LDS (`staged`).
-template <int QT, int BPR, int NWV, int NMAT>
+template <int QT, int BPR, int NWV, int PRO, int NMAT>
 __host__ __device__ constexpr size_t mv_lds_bytes(bool staged) {
   using T = MvTile<QT, BPR, NWV>;
-  return align16(MvX<BPR>::END) + NMAT * align16((size_t)T::TR * T::RS * 4) + (staged ? NMAT * (size_t)T::LDS_T : 0);
+  return align16(MvXA<BPR, PRO>::END) + NMAT * align16((size_t)T::TR * T::RS * 4) +
+         (staged ? NMAT * (size_t)T::LDS_T : 0);
 }
 
 template <class T, int NTH>
@@ -1083,11 +1105,91 @@ __device__ __forceinline__ float q6_unit_dot(const MvUnit<1>& X, const Q6Unit& w
   return part * g4d::f16_bits_to_f32(rd);
 }
 
+// Q6_K unit against D8 digits: each 16-element run (one int8 scale) is two
+// 8-element groups, each with its own activation scale and offset.
+struct MvUnit8 {
+  uint32_t hi[16], lo[16];
+  float s[8];
+  int2 c[8];
+};
+template <int BPR>
+__device__ __forceinline__ void mv_unit_load8(MvUnit8& X, const uint8_t* smem, int u) {
+  using D = MvD8<BPR>;
+  const int b = u >> 2, g = u & 3, h = g >> 1, l0 = 16 * (g & 1);
+  const float* sc = (const float*)(smem + D::S);
+  const int2* cc = (const int2*)(smem + D::C);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int e = 256 * b + 128 * h + 32 * k + l0;  // run k (src/gguf.ts:344-361)
+    const uint4 th = *(const uint4*)(smem + D::HI + e);
+    const uint4 tl = *(const uint4*)(smem + D::LO + e);
+    X.hi[4 * k] = th.x; X.hi[4 * k + 1] = th.y; X.hi[4 * k + 2] = th.z; X.hi[4 * k + 3] = th.w;
+    X.lo[4 * k] = tl.x; X.lo[4 * k + 1] = tl.y; X.lo[4 * k + 2] = tl.z; X.lo[4 * k + 3] = tl.w;
+    const float2 s2 = *(const float2*)(sc + e / 8);
+    const int4 c2 = *(const int4*)(cc + e / 8);
+    X.s[2 * k] = s2.x;
+    X.s[2 * k + 1] = s2.y;
+    X.c[2 * k] = make_int2(c2.x, c2.y);
+    X.c[2 * k + 1] = make_int2(c2.z, c2.w);
+  }
+}
+__device__ __forceinline__ float q6_unit_dot8(const MvUnit8& X, const Q6Unit& w) {
+  uint32_t A[4], B[4], H[4];
+  q6_run(w.a4, w.a1, w.sh, A);
+  q6_run(w.b4, w.b1, w.sh, B);
+  q6_run(w.h4, w.h1, w.sh, H);
+  uint32_t r0 = w.s0, r1 = w.s1, r2 = w.s2, r3 = w.s3, rd = w.d;
+  asm volatile("" : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3), "+v"(rd));
+  const int32_t scs[4] = {(int32_t)(int8_t)r0, (int32_t)(int8_t)r1, (int32_t)(int8_t)r2, (int32_t)(int8_t)r3};
+  float part = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    int ah[2] = {0, 0}, al[2] = {0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t q;
+      if (k == 0) q = (A[j] & 0x0f0f0f0fu) | ((H[j] << 4) & 0x30303030u);
+      else if (k == 1) q = (B[j] & 0x0f0f0f0fu) | ((H[j] << 2) & 0x30303030u);
+      else if (k == 2) q = ((A[j] >> 4) & 0x0f0f0f0fu) | (H[j] & 0x30303030u);
+      else q = ((B[j] >> 4) & 0x0f0f0f0fu) | ((H[j] >> 2) & 0x30303030u);
+      ah[j >> 1] = __builtin_amdgcn_sdot4((int)q, (int)X.hi[4 * k + j], ah[j >> 1], false);
+      al[j >> 1] = __builtin_amdgcn_sdot4((int)q, (int)X.lo[4 * k + j], al[j >> 1], false);
+    }
+    const int I0 = (ah[0] - X.c[2 * k].x) * 256 + (al[0] - X.c[2 * k].y);
+    const int I1 = (ah[1] - X.c[2 * k + 1].x) * 256 + (al[1] - X.c[2 * k + 1].y);
+    part += (float)scs[k] * (X.s[2 * k] * (float)I0 + X.s[2 * k + 1] * (float)I1);
+  }
+  return part * g4d::f16_bits_to_f32(rd);
+}
+
+// D8 digits of a gate/up launch's GELU outputs: the 8 rows of a group are
+// the 8 rows one wave reduces (8 lanes each, the first of them at lanes 0,
+// 8, ..., 56), so the group's maximum and digit sums are wave reductions
+// (DPP, no LDS round trip; the digit sums are integers below 2^11, exact in
+// f32). `real`: this lane stores a row (the other lanes and rows past the
+// output carry 0). Every lane of the wave calls it.
+__device__ __forceinline__ void mv_d8_group(float v, bool real, uint32_t row, uint32_t K, uint8_t* d8) {
+  const float am = g4d::wave_max_dpp(real ? fabsf(v) : 0.f);
+  const float inv = am > 0.f ? XQ * __builtin_amdgcn_rcpf(am) : 0.f;
+  const int q = real ? (int)__builtin_rintf(v * inv) : 0;
+  const int lo = ((q + 128) & 255) - 128;
+  const int hi = (q - lo) >> 8;
+  const int shi = (int)g4d::wave_sum_dpp((float)hi), slo = (int)g4d::wave_sum_dpp((float)lo);
+  if (real) {
+    d8[row] = (uint8_t)(hi & 255);
+    d8[K + row] = (uint8_t)(lo & 255);
+  }
+  if (real && (threadIdx.x & 63) == 0) {  // the group's first row
+    ((float*)(d8 + 2 * (size_t)K))[row / 8] = am * (1.0f / XQ);
+    ((int2*)(d8 + 2 * (size_t)K + 4 * (size_t)(K / 8)))[row / 8] = make_int2(32 * shi, 32 * slo);
+  }
+}
+
 // Adds each row's U unit partials (RG lanes per row, then a butterfly) and
 // stores the tile's rows: y, softcap(y), or gelu(gate) * up for a pair.
 template <class T, int NTH, int NMAT>
 __device__ __forceinline__ void mv_reduce_store(const float* red, const GemvSeg& sg, uint32_t t, int tid, float cap,
-                                                bool track, g4d::Cand& best) {
+                                                bool track, g4d::Cand& best, uint8_t* d8 = nullptr) {
   constexpr int U = NTH / T::TR;
   const int gl = tid % T::RG;
   for (int r = tid / T::RG; r < T::TR; r += NTH / T::RG) {  // uniform within a group
@@ -1103,15 +1205,19 @@ __device__ __forceinline__ void mv_reduce_store(const float* red, const GemvSeg&
       y[m] = a;
     }
     const uint32_t row = t * T::TR + r;
-    if (gl == 0 && row < sg.M) {
-      float v;
-      if constexpr (NMAT == 2) v = gelu_tanh(y[0]) * y[1];
-      else v = cap > 0.f ? softcap(y[0], cap) : y[0];
+    const bool real = gl == 0 && row < sg.M;
+    if constexpr (NMAT == 2) {
+      const float v = gelu_tanh(y[0]) * y[1];
+      if (real) sg.Y[row] = v;
+      // (uniform) every lane of the group's wave is in this iteration: 8
+      // rows x 8 lanes fill it, and TR is a multiple of 8 (host-checked)
+      if constexpr (T::RG == 8)
+        if (d8) mv_d8_group(v, real, row, sg.M, d8);
+    } else if (real) {
+      const float v = cap > 0.f ? softcap(y[0], cap) : y[0];
       sg.Y[row] = v;
-      if constexpr (NMAT == 1) {
-        const g4d::Cand d{v, row};
-        if (track && g4d::better(d, best)) best = d;
-      }
+      const g4d::Cand d{v, row};
+      if (track && g4d::better(d, best)) best = d;
     }
   }
 }
@@ -1142,6 +1248,7 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
   using G = MvGeom<BPR, NWV>;
   using T = MvTile<QT, BPR, NWV>;
   constexpr int NTH = G::NTH;
+  static_assert(PRO != 3 || (QT == 1 && NMAT == 1), "D8 input: one Q6_K matrix");
   extern __shared__ __align__(16) uint8_t smem[];
   int si = 0;
 #pragma unroll
@@ -1154,10 +1261,20 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
   const uint32_t te = min(tiles, tb + segs.rep);
   const int tid = threadIdx.x;
   const int slot = tid / G::U, u = tid % G::U;
-  float* red = (float*)(smem + align16(MvX<BPR>::END));
+  float* red = (float*)(smem + align16(MvXA<BPR, PRO>::END));
+  uint8_t* const d8 = NMAT == 2 ? segs.d8 : nullptr;
 
-  MvPro<BPR, NWV, PRO> P;
-  mv_pro_load<BPR, NWV, PRO>(P, pa);
+  MvPro<BPR, NWV, PRO == 3 ? 0 : PRO> P;
+  // D8 input: the block's 16-byte chunks, a few per thread, copied to LDS as is
+  constexpr int DN = (int)((MvD8<BPR>::BYTES + 15) / 16), DL = (DN + NTH - 1) / NTH;
+  u32x4a dg[PRO == 3 ? DL : 1];
+  if constexpr (PRO == 3) {
+#pragma unroll
+    for (int i = 0; i < DL; ++i)
+      dg[i] = *(const u32x4a*)((const uint8_t*)pa.x + 16 * min(tid + i * NTH, DN - 1));
+  } else {
+    mv_pro_load<BPR, NWV, PRO>(P, pa);
+  }
   // Requests leave a CU in issue order across its waves: every wave's
   // activation loads go out before any wave's weight loads, or the last
   // waves' activations queue behind the first waves' weight tiles. A bare
@@ -1165,9 +1282,7 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
-  // each thread's unit straight from global memory into registers; rows
-  // past M (a partial last tile) read row M - 1 and are not stored
-  if (te - tb == 1) {
+  if (PRO == 3 || te - tb == 1) {  // (a D8-input launch has one tile per workgroup: host-checked)
     // one tile: each thread's unit straight from global memory into
     // registers; rows past M (a partial tile) read row M - 1, not stored
     using WU = typename std::conditional<QT == 0, Q4Unit, Q6Unit>::type;
@@ -1185,55 +1300,69 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
       else q6_unit_load<POL>(wu[m], rs, off, W[m] + off, u & 3);
     }
     __builtin_amdgcn_sched_barrier(0);  // every weight load is issued before the activations are used
-    mv_pro_finish<BPR, NWV, PRO>(P, smem, pa);
-    MvUnit<QT> X;
-    mv_unit_load<QT, BPR>(X, smem, u);
+    if constexpr (PRO == 3) {
 #pragma unroll
-    for (int m = 0; m < NMAT; ++m) {
-      float v;
-      if constexpr (QT == 0) v = q4_unit_dot(X, wu[m], u & 3);
-      else v = q6_unit_dot(X, wu[m]);
-      red[m * T::TR * T::RS + slot * T::RS + u] = v;
+      for (int i = 0; i < DL; ++i)
+        if (tid + i * NTH < DN) *(u32x4a*)(smem + 16 * (tid + i * NTH)) = dg[i];
+      lds_barrier();
+      MvUnit8 X;
+      mv_unit_load8<BPR>(X, smem, u);
+      red[slot * T::RS + u] = q6_unit_dot8(X, wu[0]);
+    } else {
+      mv_pro_finish<BPR, NWV, PRO>(P, smem, pa);
+      MvUnit<QT> X;
+      mv_unit_load<QT, BPR>(X, smem, u);
+#pragma unroll
+      for (int m = 0; m < NMAT; ++m) {
+        float v;
+        if constexpr (QT == 0) v = q4_unit_dot(X, wu[m], u & 3);
+        else v = q6_unit_dot(X, wu[m]);
+        red[m * T::TR * T::RS + slot * T::RS + u] = v;
+      }
     }
     lds_barrier();
     g4d::Cand best{-1e30f, 0u};
-    mv_reduce_store<T, NTH, NMAT>(red, sg, tb, tid, cap, segs.amx != nullptr, best);
+    mv_reduce_store<T, NTH, NMAT>(red, sg, tb, tid, cap, segs.amx != nullptr, best, d8);
     if constexpr (NMAT == 1)
-      if (segs.amx) mv_argmax_partial<NWV>(best, (g4d::Cand*)(smem + MvX<BPR>::RED8), segs.amx + blockIdx.x);
+      if (segs.amx)
+        mv_argmax_partial<NWV>(best, (g4d::Cand*)(smem + MvXA<BPR, PRO>::RED8), segs.amx + blockIdx.x);
     return;
   }
-  // several tiles: coalesced loads of the next tile into registers while
-  // this one is multiplied out of LDS
-  uint8_t* tl = smem + align16(MvX<BPR>::END) + NMAT * align16((size_t)T::TR * T::RS * 4);
-  Stage<T::LPT> st[NMAT];
-  uint32_t nb = mv_tile_bytes<QT, BPR, NWV>(sg.M, tb);
+  if constexpr (PRO != 3) {
+    // several tiles: coalesced loads of the next tile into registers while
+    // this one is multiplied out of LDS
+    uint8_t* tl = smem + align16(MvXA<BPR, PRO>::END) + NMAT * align16((size_t)T::TR * T::RS * 4);
+    Stage<T::LPT> st[NMAT];
+    uint32_t nb = mv_tile_bytes<QT, BPR, NWV>(sg.M, tb);
 #pragma unroll
-  for (int m = 0; m < NMAT; ++m) mv_stage_load<T, NTH>(W[m] + (size_t)tb * T::TB, nb, st[m]);
-  __builtin_amdgcn_sched_barrier(0);  // every weight load is issued before the activations are used
-  mv_pro_finish<BPR, NWV, PRO>(P, smem, pa);
-  MvUnit<QT> X;
-  mv_unit_load<QT, BPR>(X, smem, u);
-  g4d::Cand best{-1e30f, 0u};
-  for (uint32_t t = tb; t < te; ++t) {
-    __syncthreads();  // digits read (first tile) / previous tile reduced
+    for (int m = 0; m < NMAT; ++m) mv_stage_load<T, NTH>(W[m] + (size_t)tb * T::TB, nb, st[m]);
+    __builtin_amdgcn_sched_barrier(0);  // every weight load is issued before the activations are used
+    mv_pro_finish<BPR, NWV, PRO>(P, smem, pa);
+    MvUnit<QT> X;
+    mv_unit_load<QT, BPR>(X, smem, u);
+    g4d::Cand best{-1e30f, 0u};
+    for (uint32_t t = tb; t < te; ++t) {
+      __syncthreads();  // digits read (first tile) / previous tile reduced
 #pragma unroll
-    for (int m = 0; m < NMAT; ++m) mv_stage_store<T, NTH>(tl + m * T::LDS_T, nb, st[m]);
-    __syncthreads();
-    if (t + 1 < te) {
-      nb = mv_tile_bytes<QT, BPR, NWV>(sg.M, t + 1);
+      for (int m = 0; m < NMAT; ++m) mv_stage_store<T, NTH>(tl + m * T::LDS_T, nb, st[m]);
+      __syncthreads();
+      if (t + 1 < te) {
+        nb = mv_tile_bytes<QT, BPR, NWV>(sg.M, t + 1);
 #pragma unroll
-      for (int m = 0; m < NMAT; ++m) mv_stage_load<T, NTH>(W[m] + (size_t)(t + 1) * T::TB, nb, st[m]);
+        for (int m = 0; m < NMAT; ++m) mv_stage_load<T, NTH>(W[m] + (size_t)(t + 1) * T::TB, nb, st[m]);
+      }
+#pragma unroll
+      for (int m = 0; m < NMAT; ++m) {
+        const uint8_t* blk = tl + m * T::LDS_T + slot * T::RB + (u >> 2) * T::BYTES;
+        red[m * T::TR * T::RS + slot * T::RS + u] = mv_unit_dot<QT>(X, blk, u & 3);
+      }
+      __syncthreads();
+      mv_reduce_store<T, NTH, NMAT>(red, sg, t, tid, cap, segs.amx != nullptr, best, d8);
     }
-#pragma unroll
-    for (int m = 0; m < NMAT; ++m) {
-      const uint8_t* blk = tl + m * T::LDS_T + slot * T::RB + (u >> 2) * T::BYTES;
-      red[m * T::TR * T::RS + slot * T::RS + u] = mv_unit_dot<QT>(X, blk, u & 3);
-    }
-    __syncthreads();
-    mv_reduce_store<T, NTH, NMAT>(red, sg, t, tid, cap, segs.amx != nullptr, best);
+    if constexpr (NMAT == 1)
+      if (segs.amx)
+        mv_argmax_partial<NWV>(best, (g4d::Cand*)(smem + MvXA<BPR, PRO>::RED8), segs.amx + blockIdx.x);
   }
-  if constexpr (NMAT == 1)
-    if (segs.amx) mv_argmax_partial<NWV>(best, (g4d::Cand*)(smem + MvX<BPR>::RED8), segs.amx + blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1357,6 +1486,7 @@ struct LaunchReq {
   g4d::Cand* amx = nullptr;     // one-vector launches: per-workgroup argmax candidates (see GemvSegs)
   uint32_t amx_cap = 0;         // candidates `amx` holds
   uint32_t* wgs_out = nullptr;  // receives the workgroup count
+  uint8_t* d8 = nullptr;        // gate/up pair: also write the outputs as an MvD8 block
 };
 
 constexpr uint32_t kMaxGemvWgs = 2048;  // beyond this a workgroup walks several row tiles
@@ -1458,11 +1588,14 @@ int mv_launch(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
   }
   sg.n = q.nseg;
   sg.amx = q.amx;
+  sg.d8 = q.d8;
+  if (PRO == 3 && sg.rep != 1)
+    return g4::set_error(G4_ERR_UNSUPPORTED, "matvec: digit input needs one tile per workgroup (%u rows)", q.segs[0].M);
   if (q.wgs_out) *q.wgs_out = wgs;
   if (wgs == 0) return G4_OK;
   if (q.amx && wgs > q.amx_cap)
     return g4::set_error(G4_ERR_UNSUPPORTED, "matvec: %u workgroups exceed the %u argmax candidates", wgs, q.amx_cap);
-  const size_t lds = mv_lds_bytes<QT, BPR, NWV, NMAT>(sg.rep > 1);
+  const size_t lds = mv_lds_bytes<QT, BPR, NWV, PRO, NMAT>(sg.rep > 1);
   int rc = claim_lds((const void*)mv_kernel<QT, BPR, NWV, PRO, NMAT>, ctx, lds);
   if (rc) return rc;
   hipLaunchKernelGGL((mv_kernel<QT, BPR, NWV, PRO, NMAT>), dim3(wgs), dim3(64 * NWV), lds, ctx->stream, sg, w_up,
@@ -1508,7 +1641,14 @@ int mv_rows(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
 
 template <int QT, int PRO, int NMAT>
 int mv_bpr(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
-  if constexpr (PRO != 0) {
+  if constexpr (PRO == 3) {
+    // digits come from a GELU product: the FFN width (6144 or 12288)
+    switch (q.N / 256) {
+      case 24: return mv_rows<QT, 24, PRO, NMAT>(ctx, q, w_up);
+      case 48: return mv_rows<QT, 48, PRO, NMAT>(ctx, q, w_up);
+      default: return G4_ERR_UNSUPPORTED;
+    }
+  } else if constexpr (PRO != 0) {
     // the normalising prologues serve the hidden vector (1536 or 2048 wide)
     switch (q.N / 256) {
       case 6: return mv_rows<QT, 6, PRO, NMAT>(ctx, q, w_up);
@@ -1536,6 +1676,9 @@ int launch_mv(g4_ctx* ctx, const LaunchReq& q) {
     case 0: return mv_bpr<QT, 0, 1>(ctx, q, nullptr);
     case 1: return mv_bpr<QT, 1, 1>(ctx, q, nullptr);
     case 2: return mv_bpr<QT, 2, 1>(ctx, q, nullptr);
+    case 3:
+      if constexpr (QT == 1) return mv_bpr<QT, 3, 1>(ctx, q, nullptr);
+      return G4_ERR_UNSUPPORTED;
     default: return G4_ERR_UNSUPPORTED;
   }
 }
@@ -1602,9 +1745,11 @@ int matmul_quant(g4_ctx* ctx, const char* fn, int qt, const float* in, const voi
 }
 
 template <int BPR, int PRO>
-int launch_gateup(g4_ctx* ctx, const uint8_t* wg, const uint8_t* wu, float* out, uint32_t M, const ProArgs& pa) {
+int launch_gateup(g4_ctx* ctx, const uint8_t* wg, const uint8_t* wu, float* out, uint32_t M, const ProArgs& pa,
+                  uint8_t* d8 = nullptr) {
   const GemvSeg seg{wg, out, M, 0};
-  const LaunchReq q{0, &seg, 1, BPR * 256, 1, PRO, 0, 0.f, pa, M};
+  LaunchReq q{0, &seg, 1, BPR * 256, 1, PRO, 0, 0.f, pa, M};
+  q.d8 = d8;
   return mv_rows<0, BPR, PRO, 2>(ctx, q, wu);
 }
 
@@ -1717,6 +1862,44 @@ int g4_normAddGateUpGelu_q4k(g4_ctx* ctx, const float* o, const uint16_t* w_post
     default:
       return g4::set_error(G4_ERR_UNSUPPORTED, "g4_normAddGateUpGelu_q4k: N=%u unsupported (1536 or 2048)", p.N);
   }
+}
+
+int g4_digitsBytes(uint32_t K, size_t* bytes) {
+  G4_REQUIRE(bytes && K > 0 && K % 256 == 0, "g4_digitsBytes: K=%u must be a positive multiple of 256", K);
+  *bytes = d8_bytes(K);
+  return G4_OK;
+}
+
+int g4_normAddGateUpGeluDigits_q4k(g4_ctx* ctx, const float* o, const uint16_t* w_post, const float* residual,
+                                   const uint16_t* w_pre, const void* w_gate, const void* w_up, float* h_out,
+                                   float* out, void* digits, g4_matmul_params p, float eps) {
+  G4_ENTER(ctx);
+  int rc = check_mm(__func__, o, w_gate, out, p);
+  if (rc) return rc;
+  G4_REQUIRE(w_post && residual && w_pre && w_up && digits, "g4_normAddGateUpGeluDigits_q4k: null buffer");
+  G4_REQUIRE(p.N == 1536, "g4_normAddGateUpGeluDigits_q4k: N=%u unsupported (1536)", p.N);
+  G4_REQUIRE(p.M % 256 == 0, "g4_normAddGateUpGeluDigits_q4k: M=%u must be a multiple of 256", p.M);
+  G4_REQUIRE(((uintptr_t)w_post & 7) == 0 && ((uintptr_t)w_pre & 7) == 0,
+             "g4_normAddGateUpGeluDigits_q4k: norm weights must be 8-byte aligned");
+  G4_REQUIRE(((uintptr_t)w_gate & 15) == 0 && ((uintptr_t)w_up & 15) == 0 && ((uintptr_t)residual & 15) == 0 &&
+                 ((uintptr_t)digits & 15) == 0 && (!h_out || ((uintptr_t)h_out & 15) == 0),
+             "g4_normAddGateUpGeluDigits_q4k: weights, residual, h_out and digits must be 16-byte aligned");
+  const ProArgs pa{o, w_post, residual, w_pre, h_out, eps};
+  return launch_gateup<6, 2>(ctx, (const uint8_t*)w_gate, (const uint8_t*)w_up, out, p.M, pa, (uint8_t*)digits);
+}
+
+int g4_matmulQuantDigits_q6k(g4_ctx* ctx, const void* digits, const void* weight, float* output,
+                             g4_matmul_params p) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(digits && weight && output && p.M > 0, "g4_matmulQuantDigits_q6k: null buffer or no rows");
+  G4_REQUIRE(p.N == 6144 || p.N == 12288, "g4_matmulQuantDigits_q6k: N=%u unsupported (6144 or 12288)", p.N);
+  G4_REQUIRE(((uintptr_t)digits & 15) == 0, "g4_matmulQuantDigits_q6k: digits must be 16-byte aligned");
+  int rc = check_w(__func__, 1, weight);
+  if (rc) return rc;
+  GemvSeg s{(const uint8_t*)weight, output, p.M, 0};
+  LaunchReq q{1, &s, 1, p.N, 1, 3, 0, 0.f, ProArgs{(const float*)digits, nullptr, nullptr, nullptr, nullptr, 0.f},
+              p.M};
+  return launch_gemv(ctx, q);
 }
 
 int g4_normAddMatmulSegments(g4_ctx* ctx, int wtype, const float* x, const uint16_t* w1, const float* residual,

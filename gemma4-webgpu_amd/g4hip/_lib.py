@@ -175,6 +175,9 @@ SIGNATURES = {
     "g4_normAddGateUpGelu_q4k": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, MatmulParams, _F]),
     "g4_normAddMatmulSegments": (_I, [_P, _I, _P, _P, _P, _P, _P, ctypes.POINTER(_P),
                                       ctypes.POINTER(_P), ctypes.POINTER(_U32), _I, _U32, _F, _F]),
+    "g4_digitsBytes": (_I, [_U32, ctypes.POINTER(_SZ)]),
+    "g4_normAddGateUpGeluDigits_q4k": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, MatmulParams, _F]),
+    "g4_matmulQuantDigits_q6k": (_I, [_P, _P, _P, _P, MatmulParams]),
     "g4_normAddMatmulArgmax": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, _F, _F, _P, _P, _U32]),
     "g4_matmulSegmentsBatchPartial": (_I, [_P, _I, _P, _P, ctypes.POINTER(_P), ctypes.POINTER(_P),
                                            ctypes.POINTER(_U32), _I, _U32, _U32, _U32, _F,

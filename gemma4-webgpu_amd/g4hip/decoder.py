@@ -173,6 +173,7 @@ class Decoder(_SyntheticModel):
         self.gate = ctx.empty(s.ffn, f32)
         self.up = ctx.empty(s.ffn, f32)
         self.act = ctx.empty(s.ffn, f32)
+        self.act_digits = ctx.empty(ctx.digits_bytes(s.ffn), np.uint8)  # `act` as the down launch reads it
         self.down = ctx.empty(s.hidden, f32)
         self.logits = ctx.empty(s.vocab, f32)
         self.scores = ctx.empty(s.n_q_heads * max_seq, f32)
@@ -261,7 +262,8 @@ class Decoder(_SyntheticModel):
           2. q/k norm + RoPE, v_norm, KV row store, split-K attention (+ merge)
           3. o matvec
           4. post-attn norm-add -> pre-FFN rmsNorm -> gate/up matvecs -> GELU product
-          5. down matvec (Q6_K)
+             (also written as the digit block the down launch reads)
+          5. down matvec (Q6_K) over those digits
         then the last post-FFN norm-add + final rmsNorm + LM head + softcap in
         one launch; with argmax sampling its workgroups also leave their
         argmax candidates, which a one-workgroup launch reduces to the token
@@ -289,9 +291,9 @@ class Decoder(_SyntheticModel):
                 c.attnDecodeFused(self.q, self.k, self.v, L.q_norm, L.k_norm, self.rope_freqs, L.k_cache,
                                   L.v_cache, self.attn, self.attn_params[il], self.attn_ws, self.pos)
             c.matmulQuant(self.attn, L.wo, self.o, s.hidden, s.q_dim)
-            c.normAddGateUpGelu_q4k(self.o, L.post_attn_norm, self.hidden, L.pre_ffn_norm, L.wgate, L.wup,
-                                    self.hidden2, self.act, s.ffn, s.hidden, s.eps)
-            c.matmulQuant(self.act, L.wdown, self.down, s.hidden, s.ffn, "q6k")
+            c.normAddGateUpGeluDigits_q4k(self.o, L.post_attn_norm, self.hidden, L.pre_ffn_norm, L.wgate, L.wup,
+                                          self.hidden2, self.act, self.act_digits, s.ffn, s.hidden, s.eps)
+            c.matmulQuantDigits_q6k(self.act_digits, L.wdown, self.down, s.hidden, s.ffn)
         last = self.layers[-1]
         if self.lm_head is not None:
             if sample == "argmax":

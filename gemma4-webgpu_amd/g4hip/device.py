@@ -210,6 +210,22 @@ class Context:
         check(lib().g4_normAddMatmulSegments(self.h, {"q4k": 0, "q6k": 1}[wtype], _p(x), _p(w1), _p(residual),
                                              _p(w2), _p(h_out), W, Y, R, n, N, eps, softcap))
 
+    def digits_bytes(self, K: int) -> int:
+        n = ctypes.c_size_t(0)
+        check(lib().g4_digitsBytes(K, ctypes.byref(n)))
+        return int(n.value)
+
+    def normAddGateUpGeluDigits_q4k(self, o: Ptr, w_post: Ptr, residual: Ptr, w_pre: Ptr, w_gate: Ptr, w_up: Ptr,
+                                    h_out: Ptr, out: Ptr, digits: Ptr, M: int, N: int, eps: float = 1e-6) -> None:
+        """normAddGateUpGelu_q4k that also writes `out` as a digit block for matmulQuantDigits_q6k."""
+        check(lib().g4_normAddGateUpGeluDigits_q4k(self.h, _p(o), _p(w_post), _p(residual), _p(w_pre), _p(w_gate),
+                                                   _p(w_up), _p(h_out), _p(out), _p(digits), MatmulParams(M, N),
+                                                   eps))
+
+    def matmulQuantDigits_q6k(self, digits: Ptr, weight: Ptr, out: Ptr, M: int, N: int) -> None:
+        """y[M] = W[M, N] . x with x given as the digit block a gate/up launch wrote."""
+        check(lib().g4_matmulQuantDigits_q6k(self.h, _p(digits), _p(weight), _p(out), MatmulParams(M, N)))
+
     def normAddMatmulArgmax(self, wtype: str, x: Ptr, w1: Ptr, residual: Ptr, w2: Ptr, h_out: Ptr, weight: Ptr,
                             logits: Ptr, rows: int, N: int, result: Ptr, eps: float = 1e-6, softcap: float = 0.0,
                             positions: Ptr = None, delta: int = 1) -> None:

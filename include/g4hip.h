@@ -357,6 +357,23 @@ int g4_normAddGateUpGelu_q4k(g4_ctx* ctx, const float* o, const uint16_t* w_post
                              const void* w_up, float* h_out, float* out, g4_matmul_params p,
                              float eps);
 
+/* The FFN of g4_normAddGateUpGelu_q4k and the down projection with the
+ * activation handed over pre-digitised (an MI355X form of the gelu_mul ->
+ * matmulQuant down hand-off, src/engine.ts:1604-1605; no reference
+ * counterpart for the digit block itself). The gate/up launch also writes
+ * its outputs as a digit block (two 8-bit digit planes, a scale per 8
+ * elements and the digit sums: g4_digitsBytes(K) bytes, K = the FFN width),
+ * and the down launch reads that block instead of digitising the f32
+ * vector itself. g4_normAddGateUpGeluDigits_q4k: p.N = 1536, p.M a multiple
+ * of 256; g4_matmulQuantDigits_q6k: p.N (= the FFN width) 6144 or 12288. */
+int g4_digitsBytes(uint32_t K, size_t* bytes);
+int g4_normAddGateUpGeluDigits_q4k(g4_ctx* ctx, const float* o, const uint16_t* w_post,
+                                   const float* residual, const uint16_t* w_pre,
+                                   const void* w_gate, const void* w_up, float* h_out, float* out,
+                                   void* digits, g4_matmul_params p, float eps);
+int g4_matmulQuantDigits_q6k(g4_ctx* ctx, const void* digits, const void* weight, float* output,
+                             g4_matmul_params p);
+
 /* [fusedNormAdd ->] rmsNorm -> matmulQuant over up to 4 matrices that share
  * the input (src/engine.ts:1546-1554 for q/k/v, :1606 + :1621-1625 + :1686-1701
  * for the post-FFN add, final norm, LM head and softcap):

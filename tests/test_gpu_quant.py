@@ -290,3 +290,67 @@ def test_norm_add_matmul_argmax(ctx, M, scale, specials):
     ctx.normAddMatmulArgmax("q6k", dx, dw1, dres, dw2, None, dW, y, M, N, r2, 1e-6, softcap=cap)
     assert int(r2.download(np.uint32)[0]) == idx
     assert p.download(np.uint32)[0] == 77 + 6
+
+
+def _check_digit_block(blk, x):
+    """The digit block a gate/up launch writes for its outputs x: per 8
+    elements, x ~ s * (256 hi + lo) to within one digit step (the scale is
+    max|x| / 32512 over the 8), |256 hi + lo| <= 32512, and the offsets are
+    32 x the digit sums."""
+    K = x.size
+    hi = blk[:K].view(np.int8).astype(np.int64)
+    lo = blk[K:2 * K].view(np.int8).astype(np.int64)
+    s = blk[2 * K:2 * K + 4 * (K // 8)].view(np.float32)
+    c = blk[2 * K + 4 * (K // 8):2 * K + 12 * (K // 8)].view(np.int32).reshape(-1, 2)
+    g = x.reshape(-1, 8).astype(np.float64)
+    am = np.abs(g).max(axis=1)
+    assert np.allclose(s, am / 32512.0, rtol=1e-6, atol=0)
+    q = (256 * hi + lo).reshape(-1, 8)
+    assert np.abs(q).max() <= 32512
+    rec = s.astype(np.float64)[:, None] * q
+    assert np.all(np.abs(rec - g) <= 1.0001 * s.astype(np.float64)[:, None])
+    assert np.array_equal(c[:, 0], 32 * hi.reshape(-1, 8).sum(axis=1))
+    assert np.array_equal(c[:, 1], 32 * lo.reshape(-1, 8).sum(axis=1))
+
+
+@pytest.mark.parametrize("I", [6144, 12288])
+def test_gate_up_digits_then_down(ctx, I):
+    """The FFN with the GELU product handed to the down projection as digits:
+    the f32 product equals normAddGateUpGelu_q4k's bit for bit, the digit
+    block restates it (per-8 scales, digit sums), and the down matvec over
+    the digits matches the oracle's down projection of the f32 product."""
+    N = 1536
+    Wg = O.gen_q4k(40, I * N // 256)
+    Wu = O.gen_q4k(41, I * N // 256)
+    Wd = O.gen_q6k(42, N * I // 256)
+    o = O.gen_normal_f32(43, N, 0.0, 2.0)
+    res = O.gen_normal_f32(44, N)
+    w_post = O.gen_normal_f16(45, N, 1.0, 0.1)
+    w_pre = O.gen_normal_f16(46, N, 1.0, 0.1)
+    args = [ctx.from_numpy(a) for a in (o, w_post, res, w_pre, Wg, Wu)]
+    ref_out = ctx.empty(I, np.float32)
+    ctx.normAddGateUpGelu_q4k(*args, ctx.empty(N, np.float32), ref_out, I, N, 1e-6)
+    out = ctx.empty(I, np.float32)
+    dig = ctx.zeros(ctx.digits_bytes(I), np.uint8)
+    dW = ctx.from_numpy(Wd)
+    y = ctx.empty(N, np.float32)
+    for rep in range(2):
+        ctx.normAddGateUpGeluDigits_q4k(*args, ctx.empty(N, np.float32), out, dig, I, N, 1e-6)
+        x = out.download(np.float32)
+        assert bits_equal(x, ref_out.download(np.float32))
+        _check_digit_block(dig.download(np.uint8), x)
+        ctx.matmulQuantDigits_q6k(dig, dW, y, N, I)
+        assert_close(y.download(np.float32), O.matmul(x, Wd, N, I, "q6k"), what=f"down over digits I={I}")
+
+
+def test_digit_entries_reject_bad_shapes(ctx):
+    """Shapes the digit hand-off does not cover fail with an error, not a launch."""
+    N, I = 2048, 6144
+    z = ctx.zeros(I * 8, np.float32)
+    dig = ctx.zeros(ctx.digits_bytes(I), np.uint8)
+    with pytest.raises(RuntimeError):  # hidden width 2048: 32 lanes reduce a row, no 8-row groups in a wave
+        ctx.normAddGateUpGeluDigits_q4k(z, z, z, z, z, z, None, z, dig, I, N, 1e-6)
+    with pytest.raises(RuntimeError):  # FFN width not covered
+        ctx.matmulQuantDigits_q6k(dig, z, z, 1536, 4096)
+    with pytest.raises(RuntimeError):
+        ctx.digits_bytes(100)
