@@ -61,7 +61,11 @@ def kernel_census(ctx, dec: Decoder, reps: int):
     captured as a graph of its launches over all 35 layers (so weights rotate
     through HBM as in a real step, and no host launch overhead is timed),
     replayed `reps` times between HIP events on the library's stream.
-    Algorithmic bytes: weights + activations read/written by one launch."""
+    Algorithmic bytes: weights + activations read/written by one launch.
+    The attention is timed without the L2 warming the step's attention
+    launches also do (the warming reads the next matvecs' weights, which
+    those matvecs' own launches are charged for), and the matvecs with cold
+    weights."""
     s, c = dec.s, ctx
     dec.set_position(START_POS)
     Ls = dec.layers
@@ -72,6 +76,7 @@ def kernel_census(ctx, dec: Decoder, reps: int):
     n_glob = sum(1 for il in range(nl) if s.is_global(il))
     L_loc, L_glob = min(START_POS + 1, s.window), START_POS + 1
     kv_avg = ((nl - n_glob) * L_loc + n_glob * L_glob) * KV * 2 * 2 // nl  # f16 K + V rows read
+    dig = ctx.digits_bytes(I)  # the GELU product as the down launch's digit block
 
     kinds = {
         # name: (per-layer body, launches per body, algorithmic bytes per launch)
@@ -88,12 +93,13 @@ def kernel_census(ctx, dec: Decoder, reps: int):
             lambda il, L: c.matmulQuant(dec.attn, L.wo, dec.o, H, Q),
             1, q4(H, Q) + Q * 4 + H * 4),
         "gateup_gelu": (
-            lambda il, L: c.normAddGateUpGelu_q4k(dec.o, L.post_attn_norm, dec.hidden, L.pre_ffn_norm, L.wgate,
-                                                  L.wup, dec.hidden2, dec.act, I, H, s.eps),
-            1, 2 * q4(I, H) + 4 * H * 4 + I * 4),
+            lambda il, L: c.normAddGateUpGeluDigits_q4k(dec.o, L.post_attn_norm, dec.hidden, L.pre_ffn_norm,
+                                                        L.wgate, L.wup, dec.hidden2, dec.act, dec.act_digits, I, H,
+                                                        s.eps),
+            1, 2 * q4(I, H) + 4 * H * 4 + I * 4 + dig),
         "down_matvec_q6k": (
-            lambda il, L: c.matmulQuant(dec.act, L.wdown, dec.down, H, I, "q6k"),
-            1, q6(H, I) + I * 4 + H * 4),
+            lambda il, L: c.matmulQuantDigits_q6k(dec.act_digits, L.wdown, dec.down, H, I),
+            1, q6(H, I) + dig + H * 4),
     }
     out = {}
     for name, (body, launches, nbytes) in kinds.items():
@@ -106,19 +112,21 @@ def kernel_census(ctx, dec: Decoder, reps: int):
         us = time_launches(ctx, lambda _i=0: ctx.graph_launch(g), reps) * 1e3 / nl
         ctx.graph_destroy(g)
         out[name] = {"us": us, "per_step": nl, "bytes": nbytes, "gbps": nbytes / (us * 1e-6) / 1e9}
-    # LM head with the final norm-add and softcap (330 MB: larger than the
+    # LM head with the final norm-add, softcap and the argmax candidates,
+    # then their reduction, as the step runs them (330 MB: larger than the
     # 256 MB last-level cache, so no rotation is needed)
     last = Ls[-1]
     ctx.graph_begin()
     try:
-        c.normAddMatmulSegments("q6k", dec.down, last.post_ffn_norm, dec.hidden2, dec.final_norm, dec.hidden,
-                                [dec.lm_head], [dec.logits], [V], H, s.eps, softcap=s.softcap)
+        c.normAddMatmulArgmax("q6k", dec.down, last.post_ffn_norm, dec.hidden2, dec.final_norm, dec.hidden,
+                              dec.lm_head, dec.logits, V, H, dec.token, s.eps, softcap=s.softcap)
     finally:
         g = ctx.graph_end()
     us = time_launches(ctx, lambda _i=0: ctx.graph_launch(g), max(5, reps)) * 1e3
     ctx.graph_destroy(g)
     nbytes = s.lm_head_bytes() + 5 * H * 4 + V * 4
-    out["lm_head_q6k_softcap"] = {"us": us, "per_step": 1, "bytes": nbytes, "gbps": nbytes / (us * 1e-6) / 1e9}
+    out["lm_head_q6k_softcap_argmax"] = {"us": us, "per_step": 1, "launches": 2, "bytes": nbytes,
+                                         "gbps": nbytes / (us * 1e-6) / 1e9}
     return out
 
 
