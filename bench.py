@@ -423,6 +423,8 @@ def main():
                     help="launch the step kernels directly instead of replaying a captured graph "
                          "(for profilers that do not follow graph launches)")
     ap.add_argument("--no-census", action="store_true")
+    ap.add_argument("--census-only", action="store_true",
+                    help="time only the per-kernel census of the B=1 step (the launches a profiler should see)")
     ap.add_argument("--no-gemv0", action="store_true")
     ap.add_argument("--batch-steps", type=int, default=30)
     ap.add_argument("--batch-warmup", type=int, default=5)
@@ -451,6 +453,10 @@ def main():
     log(f"weights + KV ready in {time.time() - t0:.1f}s "
         f"({(s.layer_weight_bytes() * s.n_layers + s.lm_head_bytes()) / 1e9:.3f} GB of weights)")
 
+    if args.census_only:
+        census = kernel_census(ctx, dec, args.census_reps)
+        print(json.dumps({"kernel_census": census}), flush=True)
+        return
     if args.eager:
         def step():
             dec.step_fused("argmax", warm=not args.no_warm)
