@@ -181,6 +181,22 @@ __device__ __forceinline__ float group_sum(float v) {
 // and V rows of the chunk. Loads are unconditional at clamped positions (rows
 // past the chunk are masked in the scores), so no branch or loop surrounds a
 // load: the compiler then waits for exactly the loads each step consumes.
+// RoPE of position `pos` for the pair (i, i + hd/2): the frequency is the
+// correctly rounded f32 of 1/theta^(2i/hd) (divided in f32 by the f16
+// divisor when apply_divisor), the angle the f32 product, as
+// shaders/fused_per_head_norm_rope.wgsl:50-55 forms them; cos/sin of that
+// angle in f32 (within 2 ulp of the rounded exact values). The table kernel
+// and the in-launch path share it, so a precomputed table is bit-identical.
+__device__ __forceinline__ float2 rope_cos_sin(float theta, uint32_t apply_divisor, uint16_t divisor_bits, uint32_t i,
+                                               uint32_t hd, uint32_t pos) {
+  float f = (float)(1.0 / pow((double)theta, (double)(2 * i) / (double)hd));
+  if (apply_divisor) f = f / g4d::f16_bits_to_f32(divisor_bits);
+  const float ang = (float)pos * f;
+  float sn, cn;
+  sincosf(ang, &sn, &cn);
+  return make_float2(cn, sn);
+}
+
 template <int G, int HD, int CP, bool PAGED, bool FUSE>
 __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
   constexpr int P = 32 * CP;        // positions of a chunk
@@ -287,14 +303,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
     // 1/theta^(2i/HD) and the angle the f32 product, as
     // shaders/fused_per_head_norm_rope.wgsl:50-55 forms them; cos/sin of that
     // angle in f32 (within 2 ulp of the rounded exact values).
-    if (tid < HD / 2) {
-      float f = (float)(1.0 / pow((double)a.theta, (double)(2 * tid) / (double)HD));
-      if (a.apply_divisor) f = f / g4d::f16_bits_to_f32(rfb);
-      const float ang = (float)pos * f;
-      float sn, cn;
-      sincosf(ang, &sn, &cn);
-      cs_s[tid] = make_float2(cn, sn);
-    }
+    if (tid < HD / 2) cs_s[tid] = rope_cos_sin(a.theta, a.apply_divisor, rfb, tid, HD, pos);
     static_assert((G * HD) % NT == 0 && HD >= 256, "fused form: whole q heads per thread stride");
     const bool owner = b1 == L;  // this chunk holds the current position
     // Where the row is written. Paged: the page id must be in the pool and
@@ -906,6 +915,7 @@ struct MqfArgs {
   uint32_t wwgb[kMaxWarm];    // bytes each consuming workgroup reads
   uint32_t wnwg[kMaxWarm];    // consuming workgroups
   uint32_t nwarm_regions, nwarm;  // regions; warming workgroups (a multiple of 8)
+  const float2* rope_cs;          // [cap][128] (cos, sin) of every position (g4_ropeTable), or null
 };
 
 constexpr int MQF_QS = 264;  // LDS stride of a q column (halves)
@@ -1054,20 +1064,16 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
   const float kx = a.k_raw[(size_t)kvh * MQ_HD + tid], vx = a.v_raw[(size_t)kvh * MQ_HD + tid];
   const float kw = g4d::f16_bits_to_f32(a.k_w[tid]);
   const uint16_t rfb = a.rope_freqs[tid & (MQ_HD / 2 - 1)];
+  const float2 cst =
+      a.rope_cs ? a.rope_cs[(size_t)pos * (MQ_HD / 2) + (tid & (MQ_HD / 2 - 1))] : make_float2(1.f, 0.f);
   __builtin_amdgcn_sched_barrier(0);
   load_step(0);
   __builtin_amdgcn_sched_barrier(0);
 
-  // RoPE of this position: frequency and angle as
-  // shaders/fused_per_head_norm_rope.wgsl:50-55 form them, cos/sin in f32
-  if (tid < MQ_HD / 2) {
-    float f = (float)(1.0 / pow((double)a.theta, (double)(2 * tid) / (double)MQ_HD));
-    if (a.apply_divisor) f = f / g4d::f16_bits_to_f32(rfb);
-    const float ang = (float)pos * f;
-    float sn, cn;
-    sincosf(ang, &sn, &cn);
-    cs_s[tid] = make_float2(cn, sn);
-  }
+  // RoPE of this position (rope_cos_sin), from the table when there is one:
+  // the frequency's f64 pow and a large-argument sincos are some 380 VALU
+  // instructions of the prologue's critical path
+  if (tid < MQ_HD / 2) cs_s[tid] = a.rope_cs ? cst : rope_cos_sin(a.theta, a.apply_divisor, rfb, tid, MQ_HD, pos);
   const float sk = g4d::wave_sum_dpp(kx * kx), sv = g4d::wave_sum_dpp(vx * vx);
   if (l == 0) {
     red_s[w] = sk;
@@ -1321,6 +1327,16 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
   if (!arrive(cnt + MQF_CNT - 1, ng)) return;
   merge(r1, nparts1, (size_t)kvh * MQF_FAN * MQ_G, ng, M, Ls, o0, o1);
   write_out(Ls, o0, o1);
+}
+
+// RoPE table: (cos, sin) of every position and pair, rope_cos_sin's values.
+__global__ __launch_bounds__(NT) void rope_table_kernel(float2* out, float theta, uint32_t apply_divisor,
+                                                        const uint16_t* rope_freqs, uint32_t hd, uint32_t rows) {
+  const uint32_t half = hd / 2;
+  const size_t e = (size_t)blockIdx.x * NT + threadIdx.x;
+  if (e >= (size_t)rows * half) return;
+  const uint32_t i = (uint32_t)(e % half), pos = (uint32_t)(e / half);
+  out[e] = rope_cos_sin(theta, apply_divisor, apply_divisor ? rope_freqs[i] : (uint16_t)0, i, hd, pos);
 }
 
 // ---------------------------------------------------------------------------
@@ -1773,6 +1789,20 @@ int g4_attnDecode_dev(g4_ctx* ctx, const float* q, const uint16_t* k_cache, cons
   return dense_decode(ctx, __func__, q, k_cache, v_cache, output, p, workspace, workspace_bytes, position_dev);
 }
 
+int g4_ropeTable(g4_ctx* ctx, float theta, uint32_t apply_divisor, const uint16_t* rope_freqs, uint32_t head_dim,
+                 uint32_t rows, float* table) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(table && rows > 0 && head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 1024,
+             "g4_ropeTable: null table or bad shape (rows %u, head_dim %u)", rows, head_dim);
+  G4_REQUIRE(!apply_divisor || rope_freqs, "g4_ropeTable: apply_divisor needs rope_freqs");
+  G4_REQUIRE(((uintptr_t)table & 7) == 0, "g4_ropeTable: table must be 8-byte aligned");
+  const size_t n = (size_t)rows * (head_dim / 2);
+  hipLaunchKernelGGL(rope_table_kernel, dim3(ceil_div(n, NT)), dim3(NT), 0, ctx->stream, (float2*)table, theta,
+                     apply_divisor, rope_freqs, head_dim, rows);
+  G4_LAUNCHED(ctx, "rope_table");
+  return G4_OK;
+}
+
 int g4_attnDecodeFused_workspace_size(g4_attn_fused_params p, size_t* bytes) {
   G4_REQUIRE(bytes, "g4_attnDecodeFused_workspace_size: null out");
   int rc = check_heads(__func__, p.num_q_heads, p.num_kv_heads, p.head_dim);
@@ -1792,14 +1822,14 @@ int g4_attnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw, cons
                        uint16_t* k_cache, uint16_t* v_cache, float* output, g4_attn_fused_params p, void* workspace,
                        size_t workspace_bytes, const uint32_t* position_dev) {
   return g4_attnDecodeFusedWarm(ctx, q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs, k_cache, v_cache, output, p,
-                                workspace, workspace_bytes, position_dev, nullptr, 0);
+                                workspace, workspace_bytes, position_dev, nullptr, 0, nullptr);
 }
 
 int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float* v_raw,
                            const uint16_t* q_norm_w, const uint16_t* k_norm_w, const uint16_t* rope_freqs,
                            uint16_t* k_cache, uint16_t* v_cache, float* output, g4_attn_fused_params p,
                            void* workspace, size_t workspace_bytes, const uint32_t* position_dev,
-                           const g4_warm_region* regions, int nregions) {
+                           const g4_warm_region* regions, int nregions, const float* rope_cs) {
   G4_ENTER(ctx);
   G4_REQUIRE(q_raw && k_raw && v_raw && q_norm_w && k_norm_w && k_cache && v_cache && output && workspace &&
                  position_dev,
@@ -1850,6 +1880,7 @@ int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, 
     m.ws1 = (float*)((uint8_t*)workspace + kMqfCnt + mp.bytes_ws0);
     m.cnt = (uint32_t*)workspace;
     m.out = output;
+    m.rope_cs = (const float2*)rope_cs;
     // warming workgroups on the CUs the attention leaves idle, a multiple
     // of 8 so that every XCD gets as many. A launch that warms asks for
     // kWarmLds more LDS per workgroup, so no two of its workgroups share a
@@ -1869,6 +1900,7 @@ int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, 
     G4_LAUNCHED(ctx, "attn_decode_fused_mfma");
     return G4_OK;
   }
+  // (the two-launch form computes the RoPE per call: a table is not needed)
   const SplitPlan sp = plan_splits(eff_len(p.max_seq_len, p.sliding_window));
   rc = check_plan(__func__, sp);
   if (rc) return rc;

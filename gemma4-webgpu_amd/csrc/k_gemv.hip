@@ -1243,7 +1243,11 @@ __device__ __forceinline__ void mv_argmax_partial(g4d::Cand c, g4d::Cand* sm, g4
 // each segment's rows; with `segs.amx`, also the workgroup's argmax
 // candidate (shaders/argmax.wgsl order) in segs.amx[blockIdx.x]. NMAT = 2:
 // gate/up pair, out = gelu(gate) * up (shaders/gelu_mul.wgsl:10-16).
-template <int QT, int BPR, int NWV, int PRO, int NMAT>
+// STAGED: every workgroup walks several tiles (rep > 1: matrices past two
+// tiles per CU, the LM head); the other instances hold the one-tile path
+// only. (Bounding the staged instance to two 12-wave workgroups per CU,
+// 80 VGPRs, spilled the tile loop to scratch: 199 us instead of 82.)
+template <int QT, int BPR, int NWV, int PRO, int NMAT, bool STAGED>
 __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8_t* w_up, ProArgs pa, float cap) {
   using G = MvGeom<BPR, NWV>;
   using T = MvTile<QT, BPR, NWV>;
@@ -1282,7 +1286,7 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
-  if (PRO == 3 || te - tb == 1) {  // (a D8-input launch has one tile per workgroup: host-checked)
+  if constexpr (!STAGED) {  // one tile per workgroup (host-checked)
     // one tile: each thread's unit straight from global memory into
     // registers; rows past M (a partial tile) read row M - 1, not stored
     using WU = typename std::conditional<QT == 0, Q4Unit, Q6Unit>::type;
@@ -1328,7 +1332,7 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
         mv_argmax_partial<NWV>(best, (g4d::Cand*)(smem + MvXA<BPR, PRO>::RED8), segs.amx + blockIdx.x);
     return;
   }
-  if constexpr (PRO != 3) {
+  if constexpr (STAGED && PRO != 3) {
     // several tiles: coalesced loads of the next tile into registers while
     // this one is multiplied out of LDS
     uint8_t* tl = smem + align16(MvXA<BPR, PRO>::END) + NMAT * align16((size_t)T::TR * T::RS * 4);
@@ -1596,10 +1600,24 @@ int mv_launch(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
   if (q.amx && wgs > q.amx_cap)
     return g4::set_error(G4_ERR_UNSUPPORTED, "matvec: %u workgroups exceed the %u argmax candidates", wgs, q.amx_cap);
   const size_t lds = mv_lds_bytes<QT, BPR, NWV, PRO, NMAT>(sg.rep > 1);
-  int rc = claim_lds((const void*)mv_kernel<QT, BPR, NWV, PRO, NMAT>, ctx, lds);
+  // rep > 1 means more than 2 * num_cus tiles of the widest workgroup, which
+  // mv_pick chooses for at least kMvFullWgs tiles: only the 12-wave
+  // instances walk tiles
+  if constexpr (NWV == 12 && PRO != 3) {
+    if (sg.rep > 1) {
+      int rc = claim_lds((const void*)mv_kernel<QT, BPR, NWV, PRO, NMAT, true>, ctx, lds);
+      if (rc) return rc;
+      hipLaunchKernelGGL((mv_kernel<QT, BPR, NWV, PRO, NMAT, true>), dim3(wgs), dim3(64 * NWV), lds, ctx->stream,
+                         sg, w_up, q.pa, q.epi ? q.cap : 0.f);
+      G4_LAUNCHED(ctx, "mv");
+      return G4_OK;
+    }
+  }
+  if (sg.rep > 1) return g4::set_error(G4_ERR_UNSUPPORTED, "matvec: %d-wave workgroups do not walk tiles", NWV);
+  int rc = claim_lds((const void*)mv_kernel<QT, BPR, NWV, PRO, NMAT, false>, ctx, lds);
   if (rc) return rc;
-  hipLaunchKernelGGL((mv_kernel<QT, BPR, NWV, PRO, NMAT>), dim3(wgs), dim3(64 * NWV), lds, ctx->stream, sg, w_up,
-                     q.pa, q.epi ? q.cap : 0.f);
+  hipLaunchKernelGGL((mv_kernel<QT, BPR, NWV, PRO, NMAT, false>), dim3(wgs), dim3(64 * NWV), lds, ctx->stream, sg,
+                     w_up, q.pa, q.epi ? q.cap : 0.f);
   G4_LAUNCHED(ctx, "mv");
   return G4_OK;
 }

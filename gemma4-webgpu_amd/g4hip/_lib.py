@@ -149,7 +149,8 @@ SIGNATURES = {
     "g4_attnDecodeFused_workspace_size": (_I, [AttnFusedParams, ctypes.POINTER(_SZ)]),
     "g4_attnDecodeFused": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, AttnFusedParams, _P, _SZ, _P]),
     "g4_attnDecodeFusedWarm": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, AttnFusedParams, _P, _SZ, _P,
-                                    ctypes.POINTER(WarmRegion), _I]),
+                                    ctypes.POINTER(WarmRegion), _I, _P]),
+    "g4_ropeTable": (_I, [_P, _F, _U32, _P, _U32, _U32, _P]),
     "g4_matmulWarmRegion": (_I, [_P, _I, _U32, _U32, _P, ctypes.POINTER(WarmRegion)]),
     "g4_pagedAttnDecode_workspace_size": (_I, [PagedAttnParams, ctypes.POINTER(_SZ)]),
     "g4_pagedAttnDecode": (_I, [_P, _P, _P, _P, _P, _P, _P, PagedAttnParams, _P, _SZ]),

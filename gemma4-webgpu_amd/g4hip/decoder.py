@@ -194,6 +194,13 @@ class Decoder(_SyntheticModel):
         # weights of the gate/up and down launches that follow each attention
         # launch, read into the L2 caches by that launch (the o projection's
         # 1.8 MB arrive in time on their own: measured no faster from L2)
+        # RoPE (cos, sin) of every position, one table per (theta, divisor)
+        self.rope_cs = {}
+        for glob in (False, True):
+            t = ctx.empty(max_seq * s.head_dim, f32)
+            ctx.ropeTable(s.theta_global if glob else s.theta_local, int(glob), self.rope_freqs, s.head_dim, max_seq,
+                          t)
+            self.rope_cs[glob] = t
         self.warm = [[ctx.matmulWarmRegion("q4k", s.ffn, s.hidden, L.wgate),
                       ctx.matmulWarmRegion("q4k", s.ffn, s.hidden, L.wup),
                       ctx.matmulWarmRegion("q6k", s.hidden, s.ffn, L.wdown)] for L in self.layers]
@@ -259,7 +266,8 @@ class Decoder(_SyntheticModel):
 
         Five launches per layer:
           1. [post-FFN norm-add of the previous layer ->] attn rmsNorm -> q/k/v matvecs
-          2. q/k norm + RoPE, v_norm, KV row store, split-K attention (+ merge)
+          2. q/k norm + RoPE (cos/sin from the per-theta table), v_norm, KV row
+             store, split-K attention (+ merge)
           3. o matvec
           4. post-attn norm-add -> pre-FFN rmsNorm -> gate/up matvecs -> GELU product
              (also written as the digit block the down launch reads)
@@ -283,13 +291,9 @@ class Decoder(_SyntheticModel):
                 prev = self.layers[il - 1]
                 c.normAddMatmulSegments("q4k", self.down, prev.post_ffn_norm, self.hidden2, L.attn_norm,
                                         self.hidden, ws, outs, rows, s.hidden, s.eps)
-            if warm:
-                c.attnDecodeFusedWarm(self.q, self.k, self.v, L.q_norm, L.k_norm, self.rope_freqs, L.k_cache,
-                                      L.v_cache, self.attn, self.attn_params[il], self.attn_ws, self.pos,
-                                      self.warm[il])
-            else:
-                c.attnDecodeFused(self.q, self.k, self.v, L.q_norm, L.k_norm, self.rope_freqs, L.k_cache,
-                                  L.v_cache, self.attn, self.attn_params[il], self.attn_ws, self.pos)
+            c.attnDecodeFusedWarm(self.q, self.k, self.v, L.q_norm, L.k_norm, self.rope_freqs, L.k_cache,
+                                  L.v_cache, self.attn, self.attn_params[il], self.attn_ws, self.pos,
+                                  self.warm[il] if warm else [], self.rope_cs[s.is_global(il)])
             c.matmulQuant(self.attn, L.wo, self.o, s.hidden, s.q_dim)
             c.normAddGateUpGeluDigits_q4k(self.o, L.post_attn_norm, self.hidden, L.pre_ffn_norm, L.wgate, L.wup,
                                           self.hidden2, self.act, self.act_digits, s.ffn, s.hidden, s.eps)

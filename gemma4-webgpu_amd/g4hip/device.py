@@ -355,14 +355,20 @@ class Context:
 
     def attnDecodeFusedWarm(self, q_raw: Ptr, k_raw: Ptr, v_raw: Ptr, q_norm_w: Ptr, k_norm_w: Ptr,
                             rope_freqs: Ptr, k_cache: Ptr, v_cache: Ptr, out: Ptr, p: AttnFusedParams,
-                            workspace: Buffer, position_dev: Ptr, regions) -> None:
+                            workspace: Buffer, position_dev: Ptr, regions, rope_cs: Ptr = None) -> None:
         """attnDecodeFused whose launch also reads `regions` (WarmRegion list, <= 4) into the L2 caches
-        the matvecs that follow will read them through."""
+        the matvecs that follow will read them through, taking the RoPE cos/sin from `rope_cs`
+        (ropeTable) when given."""
         n = len(regions)
         arr = (WarmRegion * max(n, 1))(*regions)
         check(lib().g4_attnDecodeFusedWarm(self.h, _p(q_raw), _p(k_raw), _p(v_raw), _p(q_norm_w), _p(k_norm_w),
                                            _p(rope_freqs), _p(k_cache), _p(v_cache), _p(out), p, _p(workspace),
-                                           workspace.nbytes, _p(position_dev), arr, n))
+                                           workspace.nbytes, _p(position_dev), arr, n, _p(rope_cs)))
+
+    def ropeTable(self, theta: float, apply_divisor: int, rope_freqs: Ptr, head_dim: int, rows: int,
+                  table: Ptr) -> None:
+        """table[t][i] = (cos, sin) of position t's RoPE angle for pair i (rows x head_dim/2 float2)."""
+        check(lib().g4_ropeTable(self.h, theta, apply_divisor, _p(rope_freqs), head_dim, rows, _p(table)))
 
     @staticmethod
     def paged_params(num_seqs, nqh, nkh, hd, page_size, max_pages, max_seq_len, num_pages, scale=1.0, window=0):

@@ -207,15 +207,26 @@ int g4_matmulWarmRegion(g4_ctx* ctx, int wtype, uint32_t M, uint32_t N, const vo
                         g4_warm_region* out);
 /* g4_attnDecodeFused, whose launch also reads up to 4 regions (the weights
  * of the matvecs that follow it) into the L2 cache of the XCD each
- * consuming workgroup will run on, using the CUs the attention leaves idle.
- * Results are those of g4_attnDecodeFused; only where the weights come from
- * changes. */
+ * consuming workgroup will run on, using the CUs the attention leaves idle,
+ * and, with rope_cs non-NULL, takes the RoPE cos/sin of the position from a
+ * table g4_ropeTable wrote for this theta / divisor with at least
+ * max_seq_len rows (the per-call frequency pow and sincos cost the
+ * prologue about 0.6 us). Results are those of g4_attnDecodeFused, bit for
+ * bit. */
 int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float* v_raw,
                            const uint16_t* q_norm_w, const uint16_t* k_norm_w,
                            const uint16_t* rope_freqs, uint16_t* k_cache, uint16_t* v_cache,
                            float* output, g4_attn_fused_params p, void* workspace,
                            size_t workspace_bytes, const uint32_t* position_dev,
-                           const g4_warm_region* regions, int nregions);
+                           const g4_warm_region* regions, int nregions, const float* rope_cs);
+/* RoPE table of shaders/fused_per_head_norm_rope.wgsl:50-55: for position
+ * t < rows and pair i < head_dim/2, table[2 (t head_dim/2 + i)] = cos and
+ * [.. + 1] = sin of t * freq_i, freq_i = 1/theta^(2i/head_dim) (divided by
+ * rope_freqs[i] when apply_divisor), the values the fused attention
+ * computes per call. An MI355X aid with no reference counterpart (the
+ * reference recomputes them in every fusedPerHeadNormRope dispatch). */
+int g4_ropeTable(g4_ctx* ctx, float theta, uint32_t apply_divisor, const uint16_t* rope_freqs,
+                 uint32_t head_dim, uint32_t rows, float* table);
 
 /* Ragged multi-sequence decode attention over a paged f16 KV pool: sequence
  * s has seq_lens[s] positions; its logical position t lives in page

@@ -230,10 +230,10 @@ def test_attn_decode_fused_shared_workspace(ctx):
 @pytest.mark.parametrize("pos,window", [(700, 512), (3000, 0), (20, 512)])
 def test_attn_decode_fused_warm_matches(ctx, pos, window):
     """The launch that also reads the following matvecs' weights into the L2
-    caches computes exactly what the plain one does (output and caches bit for
-    bit); the warm regions describe the matvec launches' own tiling, with
-    sizes that are not multiples of a tile (a partial last tile reads past no
-    matrix end)."""
+    caches and takes the RoPE cos/sin from a precomputed table computes
+    exactly what the plain one does (output and caches bit for bit); the warm
+    regions describe the matvec launches' own tiling, with sizes that are
+    not multiples of a tile (a partial last tile reads past no matrix end)."""
     hd, theta, div = 256, (1e6 if window == 0 else 1e4), int(window == 0)
     c = _fused_inputs(pos, window, hd, theta, div)
     p = ctx.attn_fused_params(c["nqh"], c["nkh"], hd, c["cap"], window, 1e-6, theta, div)
@@ -251,14 +251,16 @@ def test_attn_decode_fused_warm_matches(ctx, pos, window):
         assert r.wg_bytes * (r.nwgs - 1) < r.total_bytes  # every workgroup has rows
         mats.append(w)
         regions.append(r)
+    rope = ctx.empty(c["cap"] * hd, np.float32)
+    ctx.ropeTable(theta, div, dev["table"], hd, c["cap"], rope)
     outs = []
     for warm in (False, True, True):
         dk, dv = ctx.from_numpy(c["k"]), ctx.from_numpy(c["v"])
         out = ctx.empty(c["nqh"] * hd, np.float32)
         args = (dev["qr"], dev["kr"], dev["vr"], dev["qw"], dev["kw"], dev["table"], dk, dv, out, p, ws,
                 ctx.from_numpy(np.array([pos], np.uint32)))
-        if warm:
-            ctx.attnDecodeFusedWarm(*args, regions)
+        if warm:  # L2 warming and the RoPE table
+            ctx.attnDecodeFusedWarm(*args, regions, rope)
         else:
             ctx.attnDecodeFused(*args)
         outs.append((out.download(np.float32), dk.download(np.uint16), dv.download(np.uint16)))
@@ -268,3 +270,25 @@ def test_attn_decode_fused_warm_matches(ctx, pos, window):
     assert_close(outs[0][0], c["ref"], what=f"warm pos={pos}")
     for w in mats:
         w.free()
+
+
+@pytest.mark.parametrize("theta,div,hd", [(1e4, 0, 256), (1e6, 1, 256), (1e6, 1, 512)])
+def test_rope_table(ctx, theta, div, hd):
+    """ropeTable: cos/sin of t * freq_i with freq_i the f32 of 1/theta^(2i/hd)
+    (divided by the f16 divisor), the angle an f32 product
+    (shaders/fused_per_head_norm_rope.wgsl:50-55), against f64 cos/sin of the
+    same f32 angle; positions up to 32767 (large angles)."""
+    rows = 32768
+    half = hd // 2
+    table = np.where(np.arange(half) < hd // 8, 1.0, np.inf).astype(np.float16)
+    out = ctx.empty(rows * hd, np.float32)
+    ctx.ropeTable(theta, div, ctx.from_numpy(table.view(np.uint16)), hd, rows, out)
+    got = out.download(np.float32).reshape(rows, half, 2)
+    i = np.arange(half)
+    f = (1.0 / np.power(np.float64(theta), 2.0 * i / hd)).astype(np.float32)
+    if div:
+        f = (f / table.astype(np.float32)).astype(np.float32)
+    t = np.arange(rows, dtype=np.float32)[:, None]
+    ang = (t * f[None, :]).astype(np.float32).astype(np.float64)
+    assert np.max(np.abs(got[..., 0] - np.cos(ang))) < 1e-6
+    assert np.max(np.abs(got[..., 1] - np.sin(ang))) < 1e-6
