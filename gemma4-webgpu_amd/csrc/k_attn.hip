@@ -995,6 +995,12 @@ __device__ __forceinline__ void mqf_warm(const MqfArgs& a) {
   asm volatile("" ::"v"(acc));
 }
 
+// exp(x) = 2^(x log2 e) on the hardware exp2 (v_exp_f32, 1 ulp): the
+// softmax and merge weights are exponents of differences <= 0, where the
+// product's rounding (|x| ulp of log2 e) stays below 1e-5 relative; a
+// library expf is some 15 instructions on the merge's critical path.
+__device__ __forceinline__ float mq_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504f); }
+
 __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
   if (blockIdx.x >= a.max_chunks) {  // (uniform) L2 warming workgroups
     if (blockIdx.y == 0) mqf_warm(a);
@@ -1084,10 +1090,12 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
               (q1.z * q1.z + q1.w * q1.w);
   qss = g4d::sum16(qss);
   qss += __shfl_xor(qss, 16, 64);
-  const float invq = 1.0f / sqrtf(qss / (float)MQ_HD + a.eps);
+  const float invq = __builtin_amdgcn_rsqf(qss * (1.0f / (float)MQ_HD) + a.eps);
   __syncthreads();
-  const float invk = 1.0f / sqrtf(((red_s[0] + red_s[1]) + (red_s[2] + red_s[3])) / (float)MQ_HD + a.eps);
-  const float invv = 1.0f / sqrtf(((red_s[4] + red_s[5]) + (red_s[6] + red_s[7])) / (float)MQ_HD + a.eps);
+  const float invk =
+      __builtin_amdgcn_rsqf(((red_s[0] + red_s[1]) + (red_s[2] + red_s[3])) * (1.0f / (float)MQ_HD) + a.eps);
+  const float invv =
+      __builtin_amdgcn_rsqf(((red_s[4] + red_s[5]) + (red_s[6] + red_s[7])) * (1.0f / (float)MQ_HD) + a.eps);
   kn_s[tid] = kx * kw * invk;
   cur_s[MQ_HD + tid] = g4d::f32_to_f16_bits(vx * invv);
   {
@@ -1156,11 +1164,11 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m_run, mx);
-    const float alpha = m_new == -INFINITY ? 1.f : expf(m_run - m_new);
+    const float alpha = m_new == -INFINITY ? 1.f : mq_exp(m_run - m_new);
     float p[4], ps = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      p[i] = sc[i] == -INFINITY ? 0.f : expf(sc[i] - m_new);
+      p[i] = sc[i] == -INFINITY ? 0.f : mq_exp(sc[i] - m_new);
       ps += p[i];
     }
     ps += __shfl_xor(ps, 16, 64);
@@ -1227,7 +1235,7 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
     float Ls = 0.f;
 #pragma unroll
     for (int ww = 0; ww < 4; ++ww) {
-      const float wt = m4[ww] == -INFINITY ? 0.f : expf(m4[ww] - M);
+      const float wt = m4[ww] == -INFINITY ? 0.f : mq_exp(m4[ww] - M);
       wt_s[ww * MQ_G + tid] = wt;
       Ls += wt * ml_s[4 * MQ_G + ww * MQ_G + tid];
     }
@@ -1271,8 +1279,8 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
       const float4 a0 = ld_dev4(r, ob);
       const float4 a1 = ld_dev4(r, ob + MQ_HD / 2 * 4u);
       const float Mn = fmaxf(M, m);
-      const float fo = M == -INFINITY ? 0.f : expf(M - Mn);
-      const float fn = m == -INFINITY ? 0.f : expf(m - Mn);
+      const float fo = M == -INFINITY ? 0.f : mq_exp(M - Mn);
+      const float fn = m == -INFINITY ? 0.f : mq_exp(m - Mn);
       Ls = Ls * fo + lv * fn;
       o0.x = o0.x * fo + a0.x * fn; o0.y = o0.y * fo + a0.y * fn;
       o0.z = o0.z * fo + a0.z * fn; o0.w = o0.w * fo + a0.w * fn;
