@@ -181,6 +181,12 @@ __device__ __forceinline__ float group_sum(float v) {
 // and V rows of the chunk. Loads are unconditional at clamped positions (rows
 // past the chunk are masked in the scores), so no branch or loop surrounds a
 // load: the compiler then waits for exactly the loads each step consumes.
+// exp(x) = 2^(x log2 e) on the hardware exp2 (v_exp_f32, 1 ulp): the
+// softmax and merge weights are exponents of differences <= 0, where the
+// product's rounding (|x| ulp of log2 e) stays below 1e-5 relative; a
+// library expf is some 15 instructions on the merge's critical path.
+__device__ __forceinline__ float mq_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504f); }
+
 // RoPE of position `pos` for the pair (i, i + hd/2): the frequency is the
 // correctly rounded f32 of 1/theta^(2i/hd) (divided in f32 by the f16
 // divisor when apply_divisor), the angle the f32 product, as
@@ -467,7 +473,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
     float sum = 0.f;
 #pragma unroll
     for (int i = sl; i < P; i += SL) {
-      const float e = expf(p_s[i * G + h] - mx);  // rows past the chunk: exp(-inf) = 0
+      const float e = mq_exp(p_s[i * G + h] - mx);  // rows past the chunk: exp(-inf) = 0
       p_s[i * G + h] = e;
       sum += e;
     }
@@ -584,12 +590,12 @@ __global__ __launch_bounds__(1024) void attn_merge_kernel(const float* ws, float
 #pragma unroll
     for (int u = 0; u < MS; ++u) mx = fmaxf(mx, (s0 + u < nsplit && ll[u] > 0.f) ? mm[u] : -INFINITY);
     const float nM = fmaxf(M, mx);
-    const float sc = nM == -INFINITY || M == -INFINITY ? 0.f : expf(M - nM);
+    const float sc = nM == -INFINITY || M == -INFINITY ? 0.f : mq_exp(M - nM);
     acc *= sc;
     Ls *= sc;
 #pragma unroll
     for (int u = 0; u < MS; ++u) {
-      const float wt = (s0 + u < nsplit && ll[u] > 0.f) ? expf(mm[u] - nM) : 0.f;
+      const float wt = (s0 + u < nsplit && ll[u] > 0.f) ? mq_exp(mm[u] - nM) : 0.f;
       acc += wt * oo[u];
       Ls += wt * ll[u];
     }
@@ -608,7 +614,7 @@ __global__ __launch_bounds__(1024) void attn_merge_kernel(const float* ws, float
   float tl = 0.f, to = 0.f;
 #pragma unroll
   for (int g = 0; g < MG; ++g) {
-    const float wg = gm_s[g] == -INFINITY ? 0.f : expf(gm_s[g] - TM);
+    const float wg = gm_s[g] == -INFINITY ? 0.f : mq_exp(gm_s[g] - TM);
     tl += wg * gl_s[g];
     to += wg * (g == 0 ? acc : go_s[(g - 1) * HD + d]);
   }
@@ -783,11 +789,11 @@ __global__ __launch_bounds__(NT, 2) void mq_attn_kernel(MqArgs a) {
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m_run, mx);
-    const float alpha = m_new == -INFINITY ? 1.f : expf(m_run - m_new);
+    const float alpha = m_new == -INFINITY ? 1.f : mq_exp(m_run - m_new);
     float p[4], ps = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      p[i] = sc[i] == -INFINITY ? 0.f : expf(sc[i] - m_new);
+      p[i] = sc[i] == -INFINITY ? 0.f : mq_exp(sc[i] - m_new);
       ps += p[i];
     }
     ps += __shfl_xor(ps, 16, 64);
@@ -857,7 +863,7 @@ __global__ __launch_bounds__(NT, 2) void mq_attn_kernel(MqArgs a) {
 #pragma unroll
     for (int ww = 0; ww < 4; ++ww) {
       const float m = mw[ww * MQ_G + h];
-      const float wt = m == -INFINITY ? 0.f : expf(m - M);
+      const float wt = m == -INFINITY ? 0.f : mq_exp(m - M);
       L += wt * lw[ww * MQ_G + h];
       o += wt * ow[(ww * MQ_G + h) * MQ_HD + tid];
     }
@@ -994,12 +1000,6 @@ __device__ __forceinline__ void mqf_warm(const MqfArgs& a) {
   }
   asm volatile("" ::"v"(acc));
 }
-
-// exp(x) = 2^(x log2 e) on the hardware exp2 (v_exp_f32, 1 ulp): the
-// softmax and merge weights are exponents of differences <= 0, where the
-// product's rounding (|x| ulp of log2 e) stays below 1e-5 relative; a
-// library expf is some 15 instructions on the merge's critical path.
-__device__ __forceinline__ float mq_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504f); }
 
 __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
   if (blockIdx.x >= a.max_chunks) {  // (uniform) L2 warming workgroups
@@ -1372,6 +1372,7 @@ struct ProArgs {
   const int32_t* page_table;
   const uint32_t* seq_lens;
   uint32_t page_size, max_pages, num_pages, cap;
+  const float2* rope_cs;  // [cap][hd/2] (cos, sin) of every position (g4_ropeTable), or null
 };
 
 // Elements i0 and i1 summed over the n partials in chunk order; the loads of
@@ -1430,19 +1431,16 @@ __global__ __launch_bounds__(NT) void attn_prologue_kernel(ProArgs a) {
   __syncthreads();
   const float tx = (red[0] + red[1]) + (red[2] + red[3]);
   const float ty = (red[4] + red[5]) + (red[6] + red[7]);
-  const float invx = 1.0f / sqrtf(tx / (float)a.hd + a.eps);
-  const float invy = 1.0f / sqrtf(ty / (float)a.hd + a.eps);
+  const float invx = __builtin_amdgcn_rsqf(tx * (1.0f / (float)a.hd) + a.eps);
+  const float invy = __builtin_amdgcn_rsqf(ty * (1.0f / (float)a.hd) + a.eps);
   if (!on) return;
   const uint16_t* wn = is_q ? a.q_w : a.k_w;
   float x0 = x.x * g4d::f16_bits_to_f32(wn[t]) * invx;
   float x1 = x.y * g4d::f16_bits_to_f32(wn[t + half]) * invx;
-  // RoPE as shaders/fused_per_head_norm_rope.wgsl:50-55 forms frequency and
-  // angle; cos/sin of the f32 angle in f32
-  float f = (float)(1.0 / pow((double)a.theta, (double)(2 * t) / (double)a.hd));
-  if (a.apply_divisor) f = f / g4d::f16_bits_to_f32(a.rope_freqs[t]);
-  const float ang = (float)pos * f;
-  float sn, cn;
-  sincosf(ang, &sn, &cn);
+  // RoPE (rope_cos_sin), from the table when there is one
+  const float2 cs = a.rope_cs ? a.rope_cs[(size_t)pos * half + t]
+                              : rope_cos_sin(a.theta, a.apply_divisor, a.rope_freqs[t], t, a.hd, pos);
+  const float cn = cs.x, sn = cs.y;
   const float r0 = x0 * cn - x1 * sn, r1 = x0 * sn + x1 * cn;
   if (is_q) {
     float* o = a.q_out + ((size_t)seq * a.nqh + head) * a.hd;
@@ -2004,11 +2002,13 @@ int g4_pagedAttnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw,
 int g4_pagedAttnPrologue(g4_ctx* ctx, const float* q_parts, const float* k_parts, const float* v_parts,
                          uint32_t nparts, const uint16_t* q_norm_w, const uint16_t* k_norm_w,
                          const uint16_t* rope_freqs, float* q_out, uint16_t* k_pool, uint16_t* v_pool,
-                         const int32_t* page_table, const uint32_t* seq_lens, g4_paged_attn_fused_params p) {
+                         const int32_t* page_table, const uint32_t* seq_lens, g4_paged_attn_fused_params p,
+                         const float* rope_cs) {
   G4_ENTER(ctx);
   G4_REQUIRE(q_parts && k_parts && v_parts && q_norm_w && k_norm_w && q_out && k_pool && v_pool && page_table &&
                  seq_lens && nparts >= 1,
              "g4_pagedAttnPrologue: null buffer or no parts");
+  G4_REQUIRE(((uintptr_t)rope_cs & 7) == 0, "g4_pagedAttnPrologue: rope_cs must be 8-byte aligned");
   G4_REQUIRE(!p.apply_divisor || rope_freqs, "g4_pagedAttnPrologue: apply_divisor needs rope_freqs");
   G4_REQUIRE(p.num_seqs > 0 && p.num_seqs <= 65535 && p.num_q_heads > 0 && p.num_kv_heads > 0,
              "g4_pagedAttnPrologue: empty batch or heads");
@@ -2042,6 +2042,7 @@ int g4_pagedAttnPrologue(g4_ctx* ctx, const float* q_parts, const float* k_parts
   a.max_pages = p.max_pages;
   a.num_pages = p.num_pages;
   a.cap = p.max_seq_len;
+  a.rope_cs = (const float2*)rope_cs;
   hipLaunchKernelGGL(attn_prologue_kernel, dim3(p.num_q_heads + p.num_kv_heads, p.num_seqs), dim3(NT), 0,
                      ctx->stream, a);
   G4_LAUNCHED(ctx, "attn_prologue");

@@ -147,6 +147,16 @@ class _SyntheticModel:
         self.ctx.fill_q6k(b, nb, self._seed())
         return b
 
+    def _rope_tables(self, rows: int) -> dict:
+        """RoPE (cos, sin) of positions [0, rows), one table per layer kind: {is_global: table}."""
+        s, out = self.s, {}
+        for glob in (False, True):
+            t = self.ctx.empty(rows * s.head_dim, np.float32)
+            self.ctx.ropeTable(s.theta_global if glob else s.theta_local, int(glob), self.rope_freqs, s.head_dim,
+                               rows, t)
+            out[glob] = t
+        return out
+
     def _f16(self, n: int) -> Buffer:
         b = self.ctx.empty(n, np.uint16)
         self.ctx.fill_normal_f16(b, n, self._seed(), 1.0, 0.1)
@@ -194,13 +204,7 @@ class Decoder(_SyntheticModel):
         # weights of the gate/up and down launches that follow each attention
         # launch, read into the L2 caches by that launch (the o projection's
         # 1.8 MB arrive in time on their own: measured no faster from L2)
-        # RoPE (cos, sin) of every position, one table per (theta, divisor)
-        self.rope_cs = {}
-        for glob in (False, True):
-            t = ctx.empty(max_seq * s.head_dim, f32)
-            ctx.ropeTable(s.theta_global if glob else s.theta_local, int(glob), self.rope_freqs, s.head_dim, max_seq,
-                          t)
-            self.rope_cs[glob] = t
+        self.rope_cs = self._rope_tables(max_seq)
         self.warm = [[ctx.matmulWarmRegion("q4k", s.ffn, s.hidden, L.wgate),
                       ctx.matmulWarmRegion("q4k", s.ffn, s.hidden, L.wup),
                       ctx.matmulWarmRegion("q6k", s.hidden, s.ffn, L.wdown)] for L in self.layers]
@@ -403,6 +407,7 @@ class BatchDecoder(_SyntheticModel):
                 B, s.n_q_heads, s.n_kv_heads, s.head_dim, page_size, self.max_pages, self.max_seq, self.num_pages,
                 1.0, window))
         self.attn_ws = ctx.zeros(max(ctx.paged_workspace_bytes(p) for p in self.attn_params), np.uint8)
+        self.rope_cs = self._rope_tables(self.max_seq)
         ctx.fill_normal_f32(self.hidden, B * s.hidden, self._seed(), 0.0, 1.0)
         ctx.sync()
 
@@ -463,7 +468,8 @@ class BatchDecoder(_SyntheticModel):
                                               [self.q_parts, self.k_parts, self.v_parts],
                                               [s.q_dim, s.kv_dim, s.kv_dim], H, B, self.ks_h, ops=self.xops)
             c.pagedAttnPrologue(self.q_parts, self.k_parts, self.v_parts, nq, L.q_norm, L.k_norm, self.rope_freqs,
-                                self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.pro_params[il])
+                                self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.pro_params[il],
+                                self.rope_cs[s.is_global(il)])
             c.pagedAttnDecode(self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.attn,
                               self.attn_params[il], self.attn_ws)
             no = c.matmulSegmentsBatchPartial("q4k", self.attn, [L.wo], [self.o_parts], [H], s.q_dim, B, self.ks_q)

@@ -412,11 +412,12 @@ class Context:
 
     def pagedAttnPrologue(self, q_parts: Ptr, k_parts: Ptr, v_parts: Ptr, nparts: int, q_norm_w: Ptr, k_norm_w: Ptr,
                           rope_freqs: Ptr, q_out: Ptr, k_pool: Ptr, v_pool: Ptr, page_table: Ptr, seq_lens: Ptr,
-                          p: PagedAttnFusedParams) -> None:
-        """Per sequence: q_norm + RoPE into q_out, K/V row (k_norm + RoPE, v_norm) appended to the pool."""
+                          p: PagedAttnFusedParams, rope_cs: Ptr = None) -> None:
+        """Per sequence: q_norm + RoPE into q_out, K/V row (k_norm + RoPE, v_norm) appended to the pool
+        (RoPE cos/sin from the ropeTable `rope_cs` when given)."""
         check(lib().g4_pagedAttnPrologue(self.h, _p(q_parts), _p(k_parts), _p(v_parts), nparts, _p(q_norm_w),
                                          _p(k_norm_w), _p(rope_freqs), _p(q_out), _p(k_pool), _p(v_pool),
-                                         _p(page_table), _p(seq_lens), p))
+                                         _p(page_table), _p(seq_lens), p, _p(rope_cs)))
 
     def advanceSeqLens(self, seq_lens: Ptr, num_seqs: int, delta: int = 1) -> None:
         check(lib().g4_advanceSeqLens(self.h, _p(seq_lens), num_seqs, delta))

@@ -275,12 +275,16 @@ int g4_pagedAttnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw,
  * [num_kv_heads*head_dim], added in chunk order): q_out [num_seqs]
  * [num_q_heads][head_dim] receives q after q_norm + RoPE, and the f16 K/V
  * row is appended to the pool as g4_pagedAttnDecodeFused does;
- * g4_pagedAttnDecode then attends. p.scale and p.sliding_window are unused. */
+ * g4_pagedAttnDecode then attends. p.scale and p.sliding_window are unused.
+ * rope_cs: a g4_ropeTable table for p.theta / p.apply_divisor with at least
+ * p.max_seq_len rows, or NULL to compute the RoPE angles per call (same
+ * values). */
 int g4_pagedAttnPrologue(g4_ctx* ctx, const float* q_parts, const float* k_parts,
                          const float* v_parts, uint32_t nparts, const uint16_t* q_norm_w,
                          const uint16_t* k_norm_w, const uint16_t* rope_freqs, float* q_out,
                          uint16_t* k_pool, uint16_t* v_pool, const int32_t* page_table,
-                         const uint32_t* seq_lens, g4_paged_attn_fused_params p);
+                         const uint32_t* seq_lens, g4_paged_attn_fused_params p,
+                         const float* rope_cs);
 /* seq_lens[s] += delta for s < num_seqs, on the stream (the device-side
  * length counters a captured multi-sequence step replays with). */
 int g4_advanceSeqLens(g4_ctx* ctx, uint32_t* seq_lens, uint32_t num_seqs, uint32_t delta);
