@@ -291,7 +291,7 @@ def batch_census(ctx, bd, reps=10):
         "attn_prologue": lambda il, L: c.pagedAttnPrologue(bd.q_parts, bd.k_parts, bd.v_parts, bd.ks_h, L.q_norm,
                                                            L.k_norm, bd.rope_freqs, bd.q, L.k_cache, L.v_cache,
                                                            bd.page_table, bd.seq_lens, bd.pro_params[il],
-                                                           bd.rope_cs[bd.s.is_global(il)]),
+                                                           bd.rope_cs[bd.s.is_global(il)], bd.rope_rows),
         "attn_global": lambda il, L: (c.pagedAttnDecode(bd.q, L.k_cache, L.v_cache, bd.page_table, bd.seq_lens,
                                                         bd.attn, bd.attn_params[il], bd.attn_ws)
                                       if s.is_global(il) else "skip"),

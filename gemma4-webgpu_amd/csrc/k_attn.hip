@@ -1828,15 +1828,18 @@ int g4_attnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw, cons
                        uint16_t* k_cache, uint16_t* v_cache, float* output, g4_attn_fused_params p, void* workspace,
                        size_t workspace_bytes, const uint32_t* position_dev) {
   return g4_attnDecodeFusedWarm(ctx, q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs, k_cache, v_cache, output, p,
-                                workspace, workspace_bytes, position_dev, nullptr, 0, nullptr);
+                                workspace, workspace_bytes, position_dev, nullptr, 0, nullptr, 0);
 }
 
 int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float* v_raw,
                            const uint16_t* q_norm_w, const uint16_t* k_norm_w, const uint16_t* rope_freqs,
                            uint16_t* k_cache, uint16_t* v_cache, float* output, g4_attn_fused_params p,
                            void* workspace, size_t workspace_bytes, const uint32_t* position_dev,
-                           const g4_warm_region* regions, int nregions, const float* rope_cs) {
+                           const g4_warm_region* regions, int nregions, const float* rope_cs,
+                           uint32_t rope_rows) {
   G4_ENTER(ctx);
+  G4_REQUIRE(!rope_cs || rope_rows >= p.max_seq_len, "g4_attnDecodeFusedWarm: RoPE table of %u rows < max_seq_len %u",
+             rope_rows, p.max_seq_len);
   G4_REQUIRE(q_raw && k_raw && v_raw && q_norm_w && k_norm_w && k_cache && v_cache && output && workspace &&
                  position_dev,
              "g4_attnDecodeFused: null buffer");
@@ -1844,9 +1847,10 @@ int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, 
              "g4_attnDecodeFusedWarm: 0..%d warm regions", kMaxWarm);
   for (int i = 0; i < nregions; ++i) {
     const g4_warm_region& r = regions[i];
-    G4_REQUIRE(r.base && r.total_bytes > 0 && r.total_bytes <= 0xffffffffull && r.wg_bytes > 0 && r.nwgs > 0 &&
-                   r.wg_bytes * (uint64_t)r.nwgs <= 0xffffffffull,
-               "g4_attnDecodeFusedWarm: region %d empty or beyond 4 GiB", i);
+    // (below 4 GiB - 4 KiB: the kernel's out-of-range reads use offset 0xfffffff0)
+    G4_REQUIRE(r.base && r.total_bytes > 0 && r.total_bytes <= 0xfffff000ull && r.wg_bytes > 0 && r.nwgs > 0 &&
+                   r.wg_bytes * (uint64_t)r.nwgs <= 0xfffff000ull,
+               "g4_attnDecodeFusedWarm: region %d empty or beyond 4 GiB - 4 KiB", i);
   }
   G4_REQUIRE(!p.apply_divisor || rope_freqs, "g4_attnDecodeFused: apply_divisor needs rope_freqs");
   G4_REQUIRE(((uintptr_t)k_cache & 15) == 0 && ((uintptr_t)v_cache & 15) == 0 && ((uintptr_t)workspace & 15) == 0,
@@ -2003,8 +2007,10 @@ int g4_pagedAttnPrologue(g4_ctx* ctx, const float* q_parts, const float* k_parts
                          uint32_t nparts, const uint16_t* q_norm_w, const uint16_t* k_norm_w,
                          const uint16_t* rope_freqs, float* q_out, uint16_t* k_pool, uint16_t* v_pool,
                          const int32_t* page_table, const uint32_t* seq_lens, g4_paged_attn_fused_params p,
-                         const float* rope_cs) {
+                         const float* rope_cs, uint32_t rope_rows) {
   G4_ENTER(ctx);
+  G4_REQUIRE(!rope_cs || rope_rows >= p.max_seq_len, "g4_pagedAttnPrologue: RoPE table of %u rows < max_seq_len %u",
+             rope_rows, p.max_seq_len);
   G4_REQUIRE(q_parts && k_parts && v_parts && q_norm_w && k_norm_w && q_out && k_pool && v_pool && page_table &&
                  seq_lens && nparts >= 1,
              "g4_pagedAttnPrologue: null buffer or no parts");

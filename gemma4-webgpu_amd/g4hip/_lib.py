@@ -149,7 +149,7 @@ SIGNATURES = {
     "g4_attnDecodeFused_workspace_size": (_I, [AttnFusedParams, ctypes.POINTER(_SZ)]),
     "g4_attnDecodeFused": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, AttnFusedParams, _P, _SZ, _P]),
     "g4_attnDecodeFusedWarm": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, AttnFusedParams, _P, _SZ, _P,
-                                    ctypes.POINTER(WarmRegion), _I, _P]),
+                                    ctypes.POINTER(WarmRegion), _I, _P, _U32]),
     "g4_ropeTable": (_I, [_P, _F, _U32, _P, _U32, _U32, _P]),
     "g4_matmulWarmRegion": (_I, [_P, _I, _U32, _U32, _P, ctypes.POINTER(WarmRegion)]),
     "g4_pagedAttnDecode_workspace_size": (_I, [PagedAttnParams, ctypes.POINTER(_SZ)]),
@@ -187,7 +187,7 @@ SIGNATURES = {
     "g4_batchPrep": (_I, [_P, _P, _U32, _P, _P, _P, _P, _P, _P, _U32, _U32, _F]),
     "g4_gateUpGeluBatch": (_I, [_P, _P, _P, _P, _P, _P, MatmulParams, _U32]),
     "g4_pagedAttnPrologue": (_I, [_P, _P, _P, _P, _U32, _P, _P, _P, _P, _P, _P, _P, _P, PagedAttnFusedParams,
-                                  _P]),
+                                  _P, _U32]),
     "g4_normAddGateUpGeluBatch": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, MatmulParams, _F, _U32]),
     "g4_normAddMatmulSegmentsBatch": (_I, [_P, _I, _P, _P, _P, _P, _P, ctypes.POINTER(_P),
                                            ctypes.POINTER(_P), ctypes.POINTER(_U32), _I, _U32, _F, _F, _U32]),

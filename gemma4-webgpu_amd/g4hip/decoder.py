@@ -150,6 +150,7 @@ class _SyntheticModel:
     def _rope_tables(self, rows: int) -> dict:
         """RoPE (cos, sin) of positions [0, rows), one table per layer kind: {is_global: table}."""
         s, out = self.s, {}
+        self.rope_rows = rows
         for glob in (False, True):
             t = self.ctx.empty(rows * s.head_dim, np.float32)
             self.ctx.ropeTable(s.theta_global if glob else s.theta_local, int(glob), self.rope_freqs, s.head_dim,
@@ -297,7 +298,7 @@ class Decoder(_SyntheticModel):
                                         self.hidden, ws, outs, rows, s.hidden, s.eps)
             c.attnDecodeFusedWarm(self.q, self.k, self.v, L.q_norm, L.k_norm, self.rope_freqs, L.k_cache,
                                   L.v_cache, self.attn, self.attn_params[il], self.attn_ws, self.pos,
-                                  self.warm[il] if warm else [], self.rope_cs[s.is_global(il)])
+                                  self.warm[il] if warm else [], self.rope_cs[s.is_global(il)], self.rope_rows)
             c.matmulQuant(self.attn, L.wo, self.o, s.hidden, s.q_dim)
             c.normAddGateUpGeluDigits_q4k(self.o, L.post_attn_norm, self.hidden, L.pre_ffn_norm, L.wgate, L.wup,
                                           self.hidden2, self.act, self.act_digits, s.ffn, s.hidden, s.eps)
@@ -469,7 +470,7 @@ class BatchDecoder(_SyntheticModel):
                                               [s.q_dim, s.kv_dim, s.kv_dim], H, B, self.ks_h, ops=self.xops)
             c.pagedAttnPrologue(self.q_parts, self.k_parts, self.v_parts, nq, L.q_norm, L.k_norm, self.rope_freqs,
                                 self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.pro_params[il],
-                                self.rope_cs[s.is_global(il)])
+                                self.rope_cs[s.is_global(il)], self.rope_rows)
             c.pagedAttnDecode(self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.attn,
                               self.attn_params[il], self.attn_ws)
             no = c.matmulSegmentsBatchPartial("q4k", self.attn, [L.wo], [self.o_parts], [H], s.q_dim, B, self.ks_q)

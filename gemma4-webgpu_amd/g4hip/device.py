@@ -355,7 +355,8 @@ class Context:
 
     def attnDecodeFusedWarm(self, q_raw: Ptr, k_raw: Ptr, v_raw: Ptr, q_norm_w: Ptr, k_norm_w: Ptr,
                             rope_freqs: Ptr, k_cache: Ptr, v_cache: Ptr, out: Ptr, p: AttnFusedParams,
-                            workspace: Buffer, position_dev: Ptr, regions, rope_cs: Ptr = None) -> None:
+                            workspace: Buffer, position_dev: Ptr, regions, rope_cs: Ptr = None,
+                            rope_rows: int = 0) -> None:
         """attnDecodeFused whose launch also reads `regions` (WarmRegion list, <= 4) into the L2 caches
         the matvecs that follow will read them through, taking the RoPE cos/sin from `rope_cs`
         (ropeTable) when given."""
@@ -363,7 +364,7 @@ class Context:
         arr = (WarmRegion * max(n, 1))(*regions)
         check(lib().g4_attnDecodeFusedWarm(self.h, _p(q_raw), _p(k_raw), _p(v_raw), _p(q_norm_w), _p(k_norm_w),
                                            _p(rope_freqs), _p(k_cache), _p(v_cache), _p(out), p, _p(workspace),
-                                           workspace.nbytes, _p(position_dev), arr, n, _p(rope_cs)))
+                                           workspace.nbytes, _p(position_dev), arr, n, _p(rope_cs), rope_rows))
 
     def ropeTable(self, theta: float, apply_divisor: int, rope_freqs: Ptr, head_dim: int, rows: int,
                   table: Ptr) -> None:
@@ -412,12 +413,12 @@ class Context:
 
     def pagedAttnPrologue(self, q_parts: Ptr, k_parts: Ptr, v_parts: Ptr, nparts: int, q_norm_w: Ptr, k_norm_w: Ptr,
                           rope_freqs: Ptr, q_out: Ptr, k_pool: Ptr, v_pool: Ptr, page_table: Ptr, seq_lens: Ptr,
-                          p: PagedAttnFusedParams, rope_cs: Ptr = None) -> None:
+                          p: PagedAttnFusedParams, rope_cs: Ptr = None, rope_rows: int = 0) -> None:
         """Per sequence: q_norm + RoPE into q_out, K/V row (k_norm + RoPE, v_norm) appended to the pool
         (RoPE cos/sin from the ropeTable `rope_cs` when given)."""
         check(lib().g4_pagedAttnPrologue(self.h, _p(q_parts), _p(k_parts), _p(v_parts), nparts, _p(q_norm_w),
                                          _p(k_norm_w), _p(rope_freqs), _p(q_out), _p(k_pool), _p(v_pool),
-                                         _p(page_table), _p(seq_lens), p, _p(rope_cs)))
+                                         _p(page_table), _p(seq_lens), p, _p(rope_cs), rope_rows))
 
     def advanceSeqLens(self, seq_lens: Ptr, num_seqs: int, delta: int = 1) -> None:
         check(lib().g4_advanceSeqLens(self.h, _p(seq_lens), num_seqs, delta))

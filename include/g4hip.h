@@ -209,16 +209,16 @@ int g4_matmulWarmRegion(g4_ctx* ctx, int wtype, uint32_t M, uint32_t N, const vo
  * of the matvecs that follow it) into the L2 cache of the XCD each
  * consuming workgroup will run on, using the CUs the attention leaves idle,
  * and, with rope_cs non-NULL, takes the RoPE cos/sin of the position from a
- * table g4_ropeTable wrote for this theta / divisor with at least
- * max_seq_len rows (the per-call frequency pow and sincos cost the
- * prologue about 0.6 us). Results are those of g4_attnDecodeFused, bit for
- * bit. */
+ * table g4_ropeTable wrote for this theta / divisor, of rope_rows >=
+ * max_seq_len rows (the per-call frequency pow and sincos cost the prologue
+ * about 0.3 us). Results are those of g4_attnDecodeFused, bit for bit. */
 int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float* v_raw,
                            const uint16_t* q_norm_w, const uint16_t* k_norm_w,
                            const uint16_t* rope_freqs, uint16_t* k_cache, uint16_t* v_cache,
                            float* output, g4_attn_fused_params p, void* workspace,
                            size_t workspace_bytes, const uint32_t* position_dev,
-                           const g4_warm_region* regions, int nregions, const float* rope_cs);
+                           const g4_warm_region* regions, int nregions, const float* rope_cs,
+                           uint32_t rope_rows);
 /* RoPE table of shaders/fused_per_head_norm_rope.wgsl:50-55: for position
  * t < rows and pair i < head_dim/2, table[2 (t head_dim/2 + i)] = cos and
  * [.. + 1] = sin of t * freq_i, freq_i = 1/theta^(2i/head_dim) (divided by
@@ -276,15 +276,15 @@ int g4_pagedAttnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw,
  * [num_q_heads][head_dim] receives q after q_norm + RoPE, and the f16 K/V
  * row is appended to the pool as g4_pagedAttnDecodeFused does;
  * g4_pagedAttnDecode then attends. p.scale and p.sliding_window are unused.
- * rope_cs: a g4_ropeTable table for p.theta / p.apply_divisor with at least
- * p.max_seq_len rows, or NULL to compute the RoPE angles per call (same
- * values). */
+ * rope_cs: a g4_ropeTable table for p.theta / p.apply_divisor of
+ * rope_rows >= p.max_seq_len rows, or NULL to compute the RoPE angles per
+ * call (same values). */
 int g4_pagedAttnPrologue(g4_ctx* ctx, const float* q_parts, const float* k_parts,
                          const float* v_parts, uint32_t nparts, const uint16_t* q_norm_w,
                          const uint16_t* k_norm_w, const uint16_t* rope_freqs, float* q_out,
                          uint16_t* k_pool, uint16_t* v_pool, const int32_t* page_table,
                          const uint32_t* seq_lens, g4_paged_attn_fused_params p,
-                         const float* rope_cs);
+                         const float* rope_cs, uint32_t rope_rows);
 /* seq_lens[s] += delta for s < num_seqs, on the stream (the device-side
  * length counters a captured multi-sequence step replays with). */
 int g4_advanceSeqLens(g4_ctx* ctx, uint32_t* seq_lens, uint32_t num_seqs, uint32_t delta);

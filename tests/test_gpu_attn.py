@@ -260,7 +260,7 @@ def test_attn_decode_fused_warm_matches(ctx, pos, window):
         args = (dev["qr"], dev["kr"], dev["vr"], dev["qw"], dev["kw"], dev["table"], dk, dv, out, p, ws,
                 ctx.from_numpy(np.array([pos], np.uint32)))
         if warm:  # L2 warming and the RoPE table
-            ctx.attnDecodeFusedWarm(*args, regions, rope)
+            ctx.attnDecodeFusedWarm(*args, regions, rope, c["cap"])
         else:
             ctx.attnDecodeFused(*args)
         outs.append((out.download(np.float32), dk.download(np.uint16), dv.download(np.uint16)))
@@ -268,6 +268,8 @@ def test_attn_decode_fused_warm_matches(ctx, pos, window):
         for a, b in zip(outs[0], o):
             assert bits_equal(a, b)
     assert_close(outs[0][0], c["ref"], what=f"warm pos={pos}")
+    with pytest.raises(RuntimeError):  # a table shorter than the cache
+        ctx.attnDecodeFusedWarm(*args, regions, rope, c["cap"] - 1)
     for w in mats:
         w.free()
 
