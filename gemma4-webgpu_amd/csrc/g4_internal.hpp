@@ -194,15 +194,28 @@ __device__ __forceinline__ bool better(const Cand& a, const Cand& b) {
   return a.i < b.i;
 }
 
+// The wave's best candidate, wave-uniform (every lane active): DPP steps
+// inside each 16-lane row, then the four rows' winners by readlane (no
+// ds_bpermute round trips).
+template <int CTRL>
+__device__ __forceinline__ void cand_step(Cand& c) {
+  Cand d;
+  d.v = dpp<CTRL>(c.v);
+  d.i = (uint32_t)dppi<CTRL>((int)c.i);
+  if (better(d, c)) c = d;
+}
 __device__ __forceinline__ Cand wave_best(Cand c) {
+  cand_step<kDppXor1>(c);
+  cand_step<kDppXor2>(c);
+  cand_step<kDppHalfMirror>(c);
+  cand_step<kDppMirror>(c);
+  Cand b{lane_value(c.v, 0), (uint32_t)__builtin_amdgcn_readlane((int)c.i, 0)};
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    Cand d;
-    d.v = __shfl_xor(c.v, o, 64);
-    d.i = __shfl_xor(c.i, o, 64);
-    if (better(d, c)) c = d;
+  for (int r = 16; r < 64; r += 16) {
+    const Cand d{lane_value(c.v, r), (uint32_t)__builtin_amdgcn_readlane((int)c.i, r)};
+    if (better(d, b)) b = d;
   }
-  return c;
+  return b;
 }
 
 // Counter-based SplitMix64 (same definition as the host g4_splitmix64).

@@ -167,22 +167,29 @@ __global__ __launch_bounds__(NT) void argmax_partial(const float* logits, uint32
 // (-1e30, 0) mirrors the reference's default result. With `adv` non-null it
 // also adds `delta` to adv[r] (the row's position: a captured decode step
 // then needs no separate advance launch).
-__global__ __launch_bounds__(NT) void argmax_final(const Cand* part, int nparts, uint32_t* result, uint32_t* adv,
-                                                  uint32_t delta) {
-  __shared__ Cand sm[4];
+// One wave per row: its lanes issue the loads of 8 candidates each before
+// comparing any (one memory round trip per 512 candidates), then the wave
+// reduction; no LDS, no barrier.
+constexpr int kFinalLoads = 8;
+__global__ __launch_bounds__(64) void argmax_final(const Cand* part, int nparts, uint32_t* result, uint32_t* adv,
+                                                   uint32_t delta) {
   part += (size_t)blockIdx.x * nparts;
   Cand c{-1e30f, 0u};
-  for (int i = threadIdx.x; i < nparts; i += NT)
-    if (better(part[i], c)) c = part[i];
+  for (int i0 = 0; i0 < nparts; i0 += 64 * kFinalLoads) {
+    Cand d[kFinalLoads];
+#pragma unroll
+    for (int k = 0; k < kFinalLoads; ++k) {
+      const int i = i0 + 64 * k + (int)threadIdx.x;
+      d[k] = i < nparts ? part[i] : Cand{-1e30f, 0u};
+    }
+#pragma unroll
+    for (int k = 0; k < kFinalLoads; ++k)
+      if (better(d[k], c)) c = d[k];
+  }
   c = wave_best(c);
-  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = c;
-  __syncthreads();
   if (threadIdx.x == 0) {
-    Cand b = sm[0];
-    for (int k = 1; k < 4; ++k)
-      if (better(sm[k], b)) b = sm[k];
     // a candidate that never beat the -1e30 initial value leaves index 0
-    result[blockIdx.x] = (b.v > -1e30f) ? b.i : 0u;
+    result[blockIdx.x] = (c.v > -1e30f) ? c.i : 0u;
     if (adv) adv[blockIdx.x] += delta;
   }
 }
@@ -596,7 +603,7 @@ int g4_fill_normal_f16(g4_ctx* ctx, uint16_t* dst, uint64_t n, uint64_t seed, fl
 
 int g4_internal_argmax_final(g4_ctx* ctx, const void* parts, int nparts, uint32_t batch, uint32_t* result,
                              uint32_t* adv, uint32_t delta) {
-  hipLaunchKernelGGL(argmax_final, dim3(batch), dim3(NT), 0, ctx->stream, (const Cand*)parts, nparts, result, adv,
+  hipLaunchKernelGGL(argmax_final, dim3(batch), dim3(64), 0, ctx->stream, (const Cand*)parts, nparts, result, adv,
                      delta);
   G4_LAUNCHED(ctx, "argmax_final");
   return G4_OK;
