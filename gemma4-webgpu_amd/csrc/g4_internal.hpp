@@ -144,6 +144,38 @@ __device__ __forceinline__ float max8(float v) {
 __device__ __forceinline__ float sum16(float v) { v = sum8(v); return v + dpp<kDppMirror>(v); }
 __device__ __forceinline__ float max16(float v) { v = max8(v); return fmaxf(v, dpp<kDppMirror>(v)); }
 
+// Combine with lane l ^ 16 / l ^ 32 through the gfx950 row / half-wave
+// swaps (v_permlane16_swap / v_permlane32_swap on two copies of v give, in
+// every lane, the pair's lower and upper values): VALU, no ds_bpermute.
+__device__ __forceinline__ float xsum16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xmax16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xsum32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xmax32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Sum over each aligned group of RG lanes (RG a power of two <= 64); every
+// lane of the group gets it.
+template <int RG>
+__device__ __forceinline__ float group_sum(float a) {
+  if constexpr (RG >= 2) a += dpp<kDppXor1>(a);
+  if constexpr (RG >= 4) a += dpp<kDppXor2>(a);
+  if constexpr (RG >= 8) a += dpp<kDppHalfMirror>(a);
+  if constexpr (RG >= 16) a += dpp<kDppMirror>(a);
+  if constexpr (RG >= 32) a = xsum16(a);
+  if constexpr (RG >= 64) a = xsum32(a);
+  return a;
+}
+
 __device__ __forceinline__ float lane_value(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }

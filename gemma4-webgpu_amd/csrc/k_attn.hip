@@ -786,8 +786,8 @@ __global__ __launch_bounds__(NT, 2) void mq_attn_kernel(MqArgs a) {
       sc[i] = off < cend ? v * a.scale : -INFINITY;
       mx = fmaxf(mx, sc[i]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = g4d::xmax16(mx);
+    mx = g4d::xmax32(mx);
     const float m_new = fmaxf(m_run, mx);
     const float alpha = m_new == -INFINITY ? 1.f : mq_exp(m_run - m_new);
     float p[4], ps = 0.f;
@@ -796,8 +796,8 @@ __global__ __launch_bounds__(NT, 2) void mq_attn_kernel(MqArgs a) {
       p[i] = sc[i] == -INFINITY ? 0.f : mq_exp(sc[i] - m_new);
       ps += p[i];
     }
-    ps += __shfl_xor(ps, 16, 64);
-    ps += __shfl_xor(ps, 32, 64);
+    ps = g4d::xsum16(ps);
+    ps = g4d::xsum32(ps);
     l_run = l_run * alpha + ps;
     m_run = m_new;
     // rows of O held here: 4q + i = (part, head 4(q&1) + i)
@@ -834,7 +834,7 @@ __global__ __launch_bounds__(NT, 2) void mq_attn_kernel(MqArgs a) {
 #pragma unroll
   for (int dt = 0; dt < 16; ++dt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) O[dt][i] += __shfl_xor(O[dt][i], 32, 64);
+    for (int i = 0; i < 4; ++i) O[dt][i] = g4d::xsum32(O[dt][i]);
   float* ow = (float*)kt;                 // [4 waves][8 heads][256]
   float* mw = (float*)vt;                 // [4][8]
   float* lw = mw + 32;                    // [4][8]
@@ -1089,7 +1089,7 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
   float qss = (q0.x * q0.x + q0.y * q0.y) + (q0.z * q0.z + q0.w * q0.w) + (q1.x * q1.x + q1.y * q1.y) +
               (q1.z * q1.z + q1.w * q1.w);
   qss = g4d::sum16(qss);
-  qss += __shfl_xor(qss, 16, 64);
+  qss = g4d::xsum16(qss);
   const float invq = __builtin_amdgcn_rsqf(qss * (1.0f / (float)MQ_HD) + a.eps);
   __syncthreads();
   const float invk =
@@ -1161,8 +1161,8 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
       sc[i] = off < cend ? v * a.scale : -INFINITY;
       mx = fmaxf(mx, sc[i]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = g4d::xmax16(mx);
+    mx = g4d::xmax32(mx);
     const float m_new = fmaxf(m_run, mx);
     const float alpha = m_new == -INFINITY ? 1.f : mq_exp(m_run - m_new);
     float p[4], ps = 0.f;
@@ -1171,8 +1171,8 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
       p[i] = sc[i] == -INFINITY ? 0.f : mq_exp(sc[i] - m_new);
       ps += p[i];
     }
-    ps += __shfl_xor(ps, 16, 64);
-    ps += __shfl_xor(ps, 32, 64);
+    ps = g4d::xsum16(ps);
+    ps = g4d::xsum32(ps);
     l_run = l_run * alpha + ps;
     m_run = m_new;
     float ar[4];

@@ -1200,9 +1200,7 @@ __device__ __forceinline__ void mv_reduce_store(const float* red, const GemvSeg&
       float a = rr[0];
 #pragma unroll
       for (int v = 1; v < U / T::RG; ++v) a += rr[v * T::RG];
-#pragma unroll
-      for (int o = T::RG / 2; o > 0; o >>= 1) a += __shfl_xor(a, o, 64);
-      y[m] = a;
+      y[m] = g4d::group_sum<T::RG>(a);
     }
     const uint32_t row = t * T::TR + r;
     const bool real = gl == 0 && row < sg.M;
