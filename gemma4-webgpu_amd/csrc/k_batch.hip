@@ -47,7 +47,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // native vector: s
 
 constexpr int PNT = 256;   // prep threads
 constexpr int MNT = 256;   // matmul threads (4 waves)
-constexpr int PMAX = 12;   // partials added per pass of the prep loads
+constexpr int PMAX = 12;   // partials added per pass of the prep loads (24 measured
+                           // slower: passes over fewer chunks load clamped copies)
 
 // Vectors are padded to the 16, 32 or 64 columns of the MFMA tiles a launch uses.
 __host__ __device__ constexpr uint32_t pad_batch(uint32_t b) { return b <= 16 ? 16 : (b <= 32 ? 32 : 64); }
@@ -149,7 +150,7 @@ __global__ __launch_bounds__(PNT) void bprep_kernel(BPrepArgs a) {
     float t1 = 0.f;
 #pragma unroll
     for (int i = 0; i < PNT / 64; ++i) t1 += red[i];
-    const float inv1 = 1.0f / sqrtf(t1 / (float)K + a.eps);
+    const float inv1 = __builtin_amdgcn_rsqf(t1 * (1.0f / (float)K) + a.eps);
     if constexpr (PRO == 1) {
 #pragma unroll
       for (int p = 0; p < XP; ++p) x[p] = mulw(x[p], w1[p], inv1);
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(PNT) void bprep_kernel(BPrepArgs a) {
       float t2 = 0.f;
 #pragma unroll
       for (int i = 0; i < PNT / 64; ++i) t2 += red[PNT / 64 + i];
-      const float inv2 = 1.0f / sqrtf(t2 / (float)K + a.eps);
+      const float inv2 = __builtin_amdgcn_rsqf(t2 * (1.0f / (float)K) + a.eps);
 #pragma unroll
       for (int p = 0; p < XP; ++p) x[p] = mulw(x[p], w2[p], inv2);
     }
