@@ -429,6 +429,66 @@ int g4_geluMul(g4_ctx* ctx, const float* gate, const float* up, float* output, u
   return G4_OK;
 }
 
+// shaders/embedding_lookup.wgsl:9-13: one thread per hidden element; the row is
+// token * H, scaled by sqrt(H) in f32. The f16 row is read 8 halves (16 B) per
+// thread when H is a multiple of 8 and the table 16-byte aligned, else one.
+__global__ __launch_bounds__(NT) void embedding_lookup_kernel(const uint16_t* __restrict__ emb, uint32_t rows,
+                                                              float* __restrict__ out, uint32_t H, uint32_t token,
+                                                              const uint32_t* __restrict__ token_dev, int vec8) {
+  const uint32_t tok = token_dev ? *token_dev : token;
+  const float scale = sqrtf(static_cast<float>(H));
+  const uint32_t t = blockIdx.x * NT + threadIdx.x;
+  if (vec8) {
+    const uint32_t i = t * 8;
+    if (i >= H) return;
+    float v[8];
+    if (tok < rows) {
+      const uint4 w = *reinterpret_cast<const uint4*>(emb + static_cast<size_t>(tok) * H + i);
+      const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[2 * j] = g4d::f16_bits_to_f32(u[j] & 0xffffu) * scale;
+        v[2 * j + 1] = g4d::f16_bits_to_f32(u[j] >> 16) * scale;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = 0.f;
+    }
+    *reinterpret_cast<float4*>(out + i) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(out + i + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+    if (t >= H) return;
+    out[t] = tok < rows ? g4d::f16_bits_to_f32(emb[static_cast<size_t>(tok) * H + t]) * scale : 0.f;
+  }
+}
+
+static int embedding_lookup(g4_ctx* ctx, const uint16_t* emb, uint32_t rows, float* out, g4_embedding_params p,
+                            const uint32_t* token_dev) {
+  G4_REQUIRE(emb && out, "g4_embeddingLookup: null buffer");
+  if (!p.hidden_size) return G4_OK;
+  const int vec8 = p.hidden_size % 8 == 0 && reinterpret_cast<uintptr_t>(emb) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  const uint32_t threads = vec8 ? p.hidden_size / 8 : p.hidden_size;
+  hipLaunchKernelGGL(embedding_lookup_kernel, dim3(ceil_div(threads, NT)), dim3(NT), 0, ctx->stream, emb, rows, out,
+                     p.hidden_size, p.token_id, token_dev, vec8);
+  G4_LAUNCHED(ctx, "embedding_lookup");
+  return G4_OK;
+}
+
+int g4_embeddingLookup(g4_ctx* ctx, const uint16_t* embedding, uint32_t num_rows, float* output,
+                       g4_embedding_params p) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(p.token_id < num_rows, "g4_embeddingLookup: token_id %u >= num_rows %u", p.token_id, num_rows);
+  return embedding_lookup(ctx, embedding, num_rows, output, p, nullptr);
+}
+
+int g4_embeddingLookup_dev(g4_ctx* ctx, const uint16_t* embedding, uint32_t num_rows, float* output,
+                           g4_embedding_params p, const uint32_t* token_dev) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(token_dev, "g4_embeddingLookup_dev: null token");
+  return embedding_lookup(ctx, embedding, num_rows, output, p, token_dev);
+}
+
 int g4_logitSoftcap(g4_ctx* ctx, float* logits, g4_softcap_params p) {
   G4_ENTER(ctx);
   G4_REQUIRE(logits, "g4_logitSoftcap: null buffer");

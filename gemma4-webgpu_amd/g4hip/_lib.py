@@ -98,6 +98,10 @@ class SoftcapParams(ctypes.Structure):  # shaders/logit_softcap.wgsl:5
     _fields_ = [("size", ctypes.c_uint32), ("cap", ctypes.c_float)]
 
 
+class EmbeddingParams(ctypes.Structure):  # shaders/embedding_lookup.wgsl:2
+    _fields_ = [("hidden_size", ctypes.c_uint32), ("token_id", ctypes.c_uint32)]
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _U32 = ctypes.c_uint32
@@ -166,6 +170,8 @@ SIGNATURES = {
     "g4_fusedNormAdd": (_I, [_P, _P, _P, _P, _P, NormAddParams]),
     "g4_geluMul": (_I, [_P, _P, _P, _P, _U32]),
     "g4_logitSoftcap": (_I, [_P, _P, SoftcapParams]),
+    "g4_embeddingLookup": (_I, [_P, _P, _U32, _P, EmbeddingParams]),
+    "g4_embeddingLookup_dev": (_I, [_P, _P, _U32, _P, EmbeddingParams, _P]),
     "g4_advancePosition": (_I, [_P, _P, _U32]),
     "g4_argmax": (_I, [_P, _P, _P, _U32]),
     "g4_topk256": (_I, [_P, _P, _P, _U32]),

@@ -26,6 +26,7 @@ from ._lib import (
     PerHeadNormParams,
     RmsNormParams,
     SoftcapParams,
+    EmbeddingParams,
     SoftmaxParams,
     check,
     lib,
@@ -448,6 +449,15 @@ class Context:
 
     def logitSoftcap(self, logits: Ptr, size: int, cap: float = 30.0) -> None:
         check(lib().g4_logitSoftcap(self.h, _p(logits), SoftcapParams(size, cap)))
+
+    def embeddingLookup(self, embedding: Ptr, num_rows: int, out: Ptr, hidden_size: int, token_id: int = 0,
+                        token_dev: Ptr = None) -> None:
+        """shaders/embedding_lookup.wgsl: out = f32(embedding[token row]) * sqrt(hidden_size)."""
+        p = EmbeddingParams(hidden_size, token_id)
+        if token_dev is None:
+            check(lib().g4_embeddingLookup(self.h, _p(embedding), num_rows, _p(out), p))
+        else:
+            check(lib().g4_embeddingLookup_dev(self.h, _p(embedding), num_rows, _p(out), p, _p(token_dev)))
 
     def advancePosition(self, position_dev: Ptr, delta: int = 1) -> None:
         check(lib().g4_advancePosition(self.h, _p(position_dev), delta))

@@ -331,6 +331,20 @@ int g4_geluMul(g4_ctx* ctx, const float* gate, const float* up, float* output, u
 typedef struct { uint32_t size; float cap; } g4_softcap_params;
 int g4_logitSoftcap(g4_ctx* ctx, float* logits, g4_softcap_params p);
 
+/* shaders/embedding_lookup.wgsl:2,12 — Params {hidden_size, token_id};
+ * out[i] = f32(embedding[token_id * hidden_size + i]) * sqrt(f32(hidden_size)),
+ * the first dispatch of a forward (src/engine.ts:1488,1511-1514). `embedding`
+ * is the f16 table [num_rows][hidden_size]; num_rows bounds token_id (the
+ * shader has no bound): a token_id >= num_rows is G4_ERR_ARG. */
+typedef struct { uint32_t hidden_size; uint32_t token_id; } g4_embedding_params;
+int g4_embeddingLookup(g4_ctx* ctx, const uint16_t* embedding, uint32_t num_rows, float* output,
+                       g4_embedding_params p);
+/* As g4_embeddingLookup with the token read from device memory (the argmax
+ * result that the reference copies into this uniform, src/engine.ts:1724-1727);
+ * p.token_id is ignored. A device token >= num_rows writes a zero row. */
+int g4_embeddingLookup_dev(g4_ctx* ctx, const uint16_t* embedding, uint32_t num_rows, float* output,
+                           g4_embedding_params p, const uint32_t* token_dev);
+
 /* *position_dev += delta on the stream: the device-side step counter that lets
  * a captured decode graph be replayed token after token (the role of the
  * per-forward uniform patches, src/engine.ts:1487-1504). */

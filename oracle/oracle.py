@@ -267,6 +267,17 @@ def attention_paged(q, k_pool, v_pool, page_table, page_size, nqh, nkh, hd, seq_
     return out
 
 
+def embedding_lookup(table_f16, hidden_size, token_id):
+    """shaders/embedding_lookup.wgsl:9-13: f32(table[token_id * H + i]) * sqrt(f32(H)).
+
+    Pinned in tests against a float64 product rounded once to f32 (exact here:
+    an 11-bit by 24-bit significand product fits in 53 bits) and against
+    perfect-square H, where sqrt(H) is exact and each output is f16 * integer.
+    """
+    t = np.ascontiguousarray(table_f16, dtype=np.float16).reshape(-1, hidden_size)
+    return t[token_id].astype(np.float32) * np.sqrt(np.float32(hidden_size))
+
+
 def logit_softcap(logits, cap=30.0):
     x = _c(logits, np.float32).copy()
     lib().g4o_logit_softcap(_p(x), x.size, cap)

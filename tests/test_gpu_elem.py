@@ -177,3 +177,24 @@ def test_argmax_advance(ctx, size, batch):
         for b in range(batch):
             assert R[b] == O.argmax(X[b]), (call, b)
         assert np.array_equal(p.download(np.uint32), pos0 + 2 * (call + 1)), call
+
+
+def test_embedding_lookup(ctx):
+    """shaders/embedding_lookup.wgsl: E2B's H = 1536 (vector path), an odd H
+    (scalar path), host and device token ids, and an out-of-range device token."""
+    rng = np.random.default_rng(11)
+    for H, rows in ((1536, 97), (250, 13)):
+        table = (rng.standard_normal((rows, H)) * 0.05).astype(np.float16)
+        d_tab = ctx.from_numpy(table.view(np.uint16))
+        out = ctx.empty(H, np.float32)
+        for tok in (0, rows // 2, rows - 1):
+            ctx.embeddingLookup(d_tab, rows, out, H, tok)
+            assert bits_equal(out.download(np.float32), O.embedding_lookup(table, H, tok))
+            tdev = ctx.from_numpy(np.array([tok], np.uint32))
+            ctx.embeddingLookup(d_tab, rows, out, H, 0, token_dev=tdev)
+            assert bits_equal(out.download(np.float32), O.embedding_lookup(table, H, tok))
+        tdev = ctx.from_numpy(np.array([rows], np.uint32))
+        ctx.embeddingLookup(d_tab, rows, out, H, 0, token_dev=tdev)
+        assert not out.download(np.float32).any()
+        with pytest.raises(Exception):
+            ctx.embeddingLookup(d_tab, rows, out, H, rows)

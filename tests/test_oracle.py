@@ -490,3 +490,23 @@ def test_generators_distribution():
     assert s6.min() == -32 and s6.max() == 31
     x = O.gen_normal_f32(3, 200000)
     assert abs(x.mean()) < 0.01 and abs(x.std() - 1) < 0.01
+
+
+def test_embedding_lookup_pinned():
+    """shaders/embedding_lookup.wgsl:12 pinned two ways: for H = 1536 against one
+    rounding of the exact float64 product (11- by 24-bit significands fit in 53
+    bits), and for the perfect square H = 256 where sqrt(H) = 16 exactly."""
+    rng = np.random.default_rng(7)
+    for H in (1536, 256):
+        table = (rng.standard_normal((5, H)) * 0.05).astype(np.float16)
+        table[3, :4] = [np.inf, -0.0, 6.1e-5, 65504]
+        for tok in (0, 3, 4):
+            got = O.embedding_lookup(table, H, tok)
+            s = np.float32(np.sqrt(np.float64(H)))  # sqrt correctly rounded to f32
+            want = (table[tok].astype(np.float64) * np.float64(s)).astype(np.float32)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+            if H == 256:
+                assert np.array_equal(got, table[tok].astype(np.float32) * 16)
+    # the row index, not the column, selects the token
+    t = np.arange(4 * 16, dtype=np.float16).reshape(4, 16)
+    assert O.embedding_lookup(t, 16, 2)[0] == 32 * 4
