@@ -62,7 +62,8 @@ def kernel_census(ctx, dec: Decoder, reps: int):
     through HBM as in a real step, and no host launch overhead is timed),
     replayed `reps` times between HIP events on the library's stream.
     Algorithmic bytes: weights + activations read/written by one launch.
-    The attention is timed without the L2 warming the step's attention
+    The attention is timed as the step runs it (RoPE cos/sin from the
+    per-theta table) but without the L2 warming the step's attention
     launches also do (the warming reads the next matvecs' weights, which
     those matvecs' own launches are charged for), and the matvecs with cold
     weights."""
@@ -86,8 +87,9 @@ def kernel_census(ctx, dec: Decoder, reps: int):
                 [dec.q, dec.k, dec.v], [Q, KV, KV], H, s.eps),
             1, q4(Q + 2 * KV, H) + 5 * H * 4 + (Q + 2 * KV) * 4),
         "attn_fused": (
-            lambda il, L: c.attnDecodeFused(dec.q, dec.k, dec.v, L.q_norm, L.k_norm, dec.rope_freqs, L.k_cache,
-                                            L.v_cache, dec.attn, dec.attn_params[il], dec.attn_ws, dec.pos),
+            lambda il, L: c.attnDecodeFusedWarm(dec.q, dec.k, dec.v, L.q_norm, L.k_norm, dec.rope_freqs, L.k_cache,
+                                                L.v_cache, dec.attn, dec.attn_params[il], dec.attn_ws, dec.pos, [],
+                                                dec.rope_cs[s.is_global(il)], dec.rope_rows),
             1, kv_avg + (Q + 2 * KV) * 4 + Q * 4),
         "o_matvec": (
             lambda il, L: c.matmulQuant(dec.attn, L.wo, dec.o, H, Q),

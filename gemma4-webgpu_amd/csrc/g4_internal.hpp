@@ -34,6 +34,10 @@ int g4_internal_scratch(g4_ctx* ctx, size_t bytes, void** out);
 int g4_internal_argmax_final(g4_ctx* ctx, const void* parts, int nparts, uint32_t batch, uint32_t* result,
                              uint32_t* adv, uint32_t delta);
 
+// Weight values through the matrix-core operands (k_batch.hip; the path 2
+// of g4_dequantPath).
+int g4_internal_operand_values(g4_ctx* ctx, int wtype, const void* blocks, uint64_t nblocks, float* out);
+
 // Matrix-core matmul of `batch` activation vectors (k_batch.hip).
 int g4_internal_batch_matmul(g4_ctx* ctx, const char* fn, int qt, const float* x, const void* w, float* y,
                              uint32_t M, uint32_t N, uint32_t batch);

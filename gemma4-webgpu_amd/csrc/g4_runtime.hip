@@ -162,8 +162,15 @@ int g4_free(g4_ctx* ctx, void* dptr) {
   return G4_OK;
 }
 
+// Calls that would put a memset node into a captured graph (such nodes have
+// given wrong results on replays after the first) or synchronise inside a
+// capture are refused while g4_graph_begin/end capture the stream.
+#define G4_NOT_CAPTURING(ctx, fn) \
+  G4_REQUIRE(!(ctx)->capturing, fn ": not allowed while a graph is being captured")
+
 int g4_memset(g4_ctx* ctx, void* dptr, int value, size_t bytes) {
   G4_ENTER(ctx);
+  G4_NOT_CAPTURING(ctx, "g4_memset");
   G4_REQUIRE(dptr || bytes == 0, "g4_memset: null pointer");
   if (bytes) G4_HIP(ctx, hipMemsetAsync(dptr, value, bytes, ctx->stream));
   return G4_OK;
@@ -171,6 +178,7 @@ int g4_memset(g4_ctx* ctx, void* dptr, int value, size_t bytes) {
 
 int g4_upload(g4_ctx* ctx, void* dst, const void* src, size_t bytes, size_t dst_offset) {
   G4_ENTER(ctx);
+  G4_NOT_CAPTURING(ctx, "g4_upload");
   G4_REQUIRE((dst && src) || bytes == 0, "g4_upload: null pointer");
   if (!bytes) return G4_OK;
   G4_HIP(ctx, hipMemcpyAsync((char*)dst + dst_offset, src, bytes, hipMemcpyHostToDevice,
@@ -181,6 +189,7 @@ int g4_upload(g4_ctx* ctx, void* dst, const void* src, size_t bytes, size_t dst_
 
 int g4_download(g4_ctx* ctx, void* dst, const void* src, size_t bytes, size_t src_offset) {
   G4_ENTER(ctx);
+  G4_NOT_CAPTURING(ctx, "g4_download");
   G4_REQUIRE((dst && src) || bytes == 0, "g4_download: null pointer");
   if (!bytes) return G4_OK;
   G4_HIP(ctx, hipMemcpyAsync(dst, (const char*)src + src_offset, bytes, hipMemcpyDeviceToHost,
@@ -192,6 +201,7 @@ int g4_download(g4_ctx* ctx, void* dst, const void* src, size_t bytes, size_t sr
 int g4_download_async(g4_ctx* ctx, void* dst, const void* src, size_t bytes, size_t src_offset,
                       g4_event** ev) {
   G4_ENTER(ctx);
+  G4_NOT_CAPTURING(ctx, "g4_download_async");
   G4_REQUIRE(dst && src && ev, "g4_download_async: null pointer");
   *ev = nullptr;
   if (bytes)
@@ -209,6 +219,7 @@ int g4_copy_d2d(g4_ctx* ctx, void* dst, const void* src, size_t bytes) {
 
 int g4_stream_sync(g4_ctx* ctx) {
   G4_ENTER(ctx);
+  G4_NOT_CAPTURING(ctx, "g4_stream_sync");
   G4_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return G4_OK;
 }

@@ -29,11 +29,20 @@ constexpr float kMasked = -1e30f;
 // the trio
 // ---------------------------------------------------------------------------
 
+// seq_len of a trio launch: the Params value, or with pos_dev (the _dev
+// entries) *pos_dev + 1 read on the device, at most the Params value (the
+// maximum the grid and the scores buffer were sized for).
+__device__ __forceinline__ uint32_t trio_len(uint32_t seq_len, const uint32_t* pos_dev) {
+  return pos_dev ? min(*pos_dev + 1u, seq_len) : seq_len;
+}
+
 // One wave per position: lanes stride the head dimension (coalesced row
 // reads), one wave reduction per query head.
 __global__ __launch_bounds__(NT) void attn_score_kernel(const float* q, const uint16_t* kc, float* scores,
                                                         uint32_t nqh, uint32_t nkh, uint32_t hd,
-                                                        uint32_t seq_len, float scale, uint32_t window) {
+                                                        uint32_t max_len, float scale, uint32_t window,
+                                                        const uint32_t* pos_dev) {
+  const uint32_t seq_len = trio_len(max_len, pos_dev);
   const int lane = threadIdx.x & 63;
   const uint32_t pos = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (pos >= seq_len) return;
@@ -55,7 +64,9 @@ __global__ __launch_bounds__(NT) void attn_score_kernel(const float* q, const ui
 }
 
 // One workgroup per head: max (init -1e30), exp, sum, normalise.
-__global__ __launch_bounds__(NT) void softmax_kernel(float* scores, uint32_t num_heads, uint32_t seq_len) {
+__global__ __launch_bounds__(NT) void softmax_kernel(float* scores, uint32_t num_heads, uint32_t max_len,
+                                                     const uint32_t* pos_dev) {
+  const uint32_t seq_len = trio_len(max_len, pos_dev);
   __shared__ float red[4];
   const uint32_t h = blockIdx.x;
   if (h >= num_heads) return;
@@ -81,7 +92,8 @@ __global__ __launch_bounds__(NT) void softmax_kernel(float* scores, uint32_t num
 // Thread per (head, d): sum over positions of p * V.
 __global__ __launch_bounds__(NT) void attn_output_kernel(const float* probs, const uint16_t* vc, float* out,
                                                          uint32_t nqh, uint32_t nkh, uint32_t hd,
-                                                         uint32_t seq_len) {
+                                                         uint32_t max_len, const uint32_t* pos_dev) {
+  const uint32_t seq_len = trio_len(max_len, pos_dev);
   const uint32_t idx = blockIdx.x * NT + threadIdx.x;
   if (idx >= nqh * hd) return;
   const uint32_t h = idx / hd, d = idx % hd;
@@ -1739,34 +1751,47 @@ int paged_setup(const char* fn, const uint16_t* k_pool, const uint16_t* v_pool, 
 
 extern "C" {
 
-int g4_attnScore(g4_ctx* ctx, const float* q, const uint16_t* k_cache, float* scores, g4_attn_score_params p) {
+int g4_attnScore_dev(g4_ctx* ctx, const float* q, const uint16_t* k_cache, float* scores, g4_attn_score_params p,
+                     const uint32_t* position_dev) {
   G4_ENTER(ctx);
   G4_REQUIRE(q && k_cache && scores, "g4_attnScore: null buffer");
   G4_REQUIRE(p.num_q_heads > 0 && p.num_kv_heads > 0 && p.head_dim > 0, "g4_attnScore: empty shape");
   if (!p.seq_len) return G4_OK;
   hipLaunchKernelGGL(attn_score_kernel, dim3(ceil_div(p.seq_len, 4)), dim3(NT), 0, ctx->stream, q, k_cache, scores,
-                     p.num_q_heads, p.num_kv_heads, p.head_dim, p.seq_len, p.scale, p.sliding_window);
+                     p.num_q_heads, p.num_kv_heads, p.head_dim, p.seq_len, p.scale, p.sliding_window, position_dev);
   G4_LAUNCHED(ctx, "attn_score");
   return G4_OK;
 }
 
-int g4_softmax(g4_ctx* ctx, float* scores, g4_softmax_params p) {
+int g4_attnScore(g4_ctx* ctx, const float* q, const uint16_t* k_cache, float* scores, g4_attn_score_params p) {
+  return g4_attnScore_dev(ctx, q, k_cache, scores, p, nullptr);
+}
+
+int g4_softmax_dev(g4_ctx* ctx, float* scores, g4_softmax_params p, const uint32_t* position_dev) {
   G4_ENTER(ctx);
   G4_REQUIRE(scores, "g4_softmax: null buffer");
   if (!p.num_heads || !p.seq_len) return G4_OK;
-  hipLaunchKernelGGL(softmax_kernel, dim3(p.num_heads), dim3(NT), 0, ctx->stream, scores, p.num_heads, p.seq_len);
+  hipLaunchKernelGGL(softmax_kernel, dim3(p.num_heads), dim3(NT), 0, ctx->stream, scores, p.num_heads, p.seq_len,
+                     position_dev);
   G4_LAUNCHED(ctx, "softmax");
   return G4_OK;
 }
 
-int g4_attnOutput(g4_ctx* ctx, const float* probs, const uint16_t* v_cache, float* output, g4_attn_output_params p) {
+int g4_softmax(g4_ctx* ctx, float* scores, g4_softmax_params p) { return g4_softmax_dev(ctx, scores, p, nullptr); }
+
+int g4_attnOutput_dev(g4_ctx* ctx, const float* probs, const uint16_t* v_cache, float* output,
+                      g4_attn_output_params p, const uint32_t* position_dev) {
   G4_ENTER(ctx);
   G4_REQUIRE(probs && v_cache && output, "g4_attnOutput: null buffer");
   G4_REQUIRE(p.num_q_heads > 0 && p.num_kv_heads > 0 && p.head_dim > 0, "g4_attnOutput: empty shape");
   hipLaunchKernelGGL(attn_output_kernel, dim3(ceil_div(p.num_q_heads * p.head_dim, NT)), dim3(NT), 0, ctx->stream,
-                     probs, v_cache, output, p.num_q_heads, p.num_kv_heads, p.head_dim, p.seq_len);
+                     probs, v_cache, output, p.num_q_heads, p.num_kv_heads, p.head_dim, p.seq_len, position_dev);
   G4_LAUNCHED(ctx, "attn_output");
   return G4_OK;
+}
+
+int g4_attnOutput(g4_ctx* ctx, const float* probs, const uint16_t* v_cache, float* output, g4_attn_output_params p) {
+  return g4_attnOutput_dev(ctx, probs, v_cache, output, p, nullptr);
 }
 
 int g4_attnDecode_workspace_size(g4_attn_score_params p, size_t* bytes) {

@@ -666,6 +666,42 @@ __global__ __launch_bounds__(MNT) void mmf_kernel(MmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Unpack check of the matrix-core operands (path 2 of the test export
+// g4_dequantPath): one wave per 16 blocks, each block a one-block row, lanes
+// as in mmf_kernel (row l % 16, k-group q = l / 16) with the weights read by
+// load_w. Element 32s + 8q + i of a block gets Q4_K: d * A[i] - dmin * m_s,
+// Q6_K: d * A[i], where A = a_operand(s) (f16 sc * q) and m_s the min
+// operand of sub-block s; d * A and dmin * m are exact in f32, so for Q4_K
+// the value is the reference's (src/gguf.ts:184-209) and for Q6_K it is d
+// times the f16 rounding of sc * (q - 32).
+// ---------------------------------------------------------------------------
+template <int QT>
+__global__ __launch_bounds__(64) void operand_check_kernel(const uint8_t* W, uint32_t nblocks, float* out) {
+  const int l = threadIdx.x, q = l >> 4;
+  const uint32_t rbase = blockIdx.x * 16u;
+  WRegs<QT> wr;
+  load_w<1>(wr, W, nblocks, rbase, 0, l);
+  const uint32_t row = rbase + (uint32_t)(l & 15);
+  if (row >= nblocks) return;
+  float* o = out + (size_t)row * 256;
+  float d, dmin = 0.f;
+  if constexpr (QT == 0) {
+    d = g4d::f16_bits_to_f32(wr.hdr.x & 0xffffu);
+    dmin = g4d::f16_bits_to_f32(wr.hdr.x >> 16);
+  } else {
+    d = g4d::f16_bits_to_f32(*(const uint16_t*)(W + (size_t)row * Blk<QT>::BYTES + 208));
+  }
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const h8 A = a_operand(wr, s, q);
+    float mn = 0.f;
+    if constexpr (QT == 0) mn = (float)min_operand(wr, s >> 1)[(s & 1) * 4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[32 * s + 8 * q + i] = d * (float)A[i] - dmin * mn;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host
 // ---------------------------------------------------------------------------
 
@@ -873,6 +909,18 @@ int g4_internal_batch_matmul(g4_ctx* ctx, const char* fn, int qt, const float* x
   float* Y[1] = {y};
   const uint32_t rows[1] = {M};
   return batch_matmul(ctx, fn, qt, 0, p, W, Y, rows, 1, N, batch, 0.f, false);
+}
+
+int g4_internal_operand_values(g4_ctx* ctx, int wtype, const void* blocks, uint64_t nblocks, float* out) {
+  G4_REQUIRE(nblocks < (1ull << 32), "g4_dequantPath: path 2 takes fewer than 2^32 blocks");
+  const uint32_t nb = (uint32_t)nblocks;
+  const dim3 grid((nb + 15) / 16);
+  if (wtype == 0)
+    hipLaunchKernelGGL(operand_check_kernel<0>, grid, dim3(64), 0, ctx->stream, (const uint8_t*)blocks, nb, out);
+  else
+    hipLaunchKernelGGL(operand_check_kernel<1>, grid, dim3(64), 0, ctx->stream, (const uint8_t*)blocks, nb, out);
+  G4_LAUNCHED(ctx, "operand_check");
+  return G4_OK;
 }
 
 extern "C" {

@@ -239,61 +239,6 @@ __global__ __launch_bounds__(NT) void topk_final(const float2* part, int nparts,
 }
 
 // ---------------------------------------------------------------------------
-// dequant (debug exports): one thread per 32-weight run
-// ---------------------------------------------------------------------------
-
-__global__ __launch_bounds__(NT) void dequant_q4k_kernel(const uint8_t* blocks, uint64_t nblocks, float* out) {
-  const uint64_t t = (uint64_t)blockIdx.x * NT + threadIdx.x;  // (block, group, half)
-  if (t >= nblocks * 8) return;
-  const uint64_t b = t >> 3;
-  const int g = (int)(t >> 1) & 3, hi = (int)t & 1;
-  const uint8_t* p = blocks + b * 144;
-  const float d = g4d::f16_bits_to_f32(p[0] | (p[1] << 8));
-  const float dmin = g4d::f16_bits_to_f32(p[2] | (p[3] << 8));
-  const uint8_t* s = p + 4;
-  const int j = 2 * g + hi;
-  int sc, m;
-  if (j < 4) {
-    sc = s[j] & 63;
-    m = s[j + 4] & 63;
-  } else {
-    sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
-    m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
-  }
-  const float d1 = d * (float)sc, m1 = dmin * (float)m;  // exact products
-  float* o = out + b * 256 + 64 * g + 32 * hi;
-  for (int l = 0; l < 32; ++l) {
-    const uint8_t q = p[16 + 32 * g + l];
-    const int qq = hi ? (q >> 4) : (q & 15);
-    // d1*q is exact, so the fused form rounds once, like the f64 reference
-    o[l] = __builtin_fmaf(d1, (float)qq, -m1);
-  }
-}
-
-__global__ __launch_bounds__(NT) void dequant_q6k_kernel(const uint8_t* blocks, uint64_t nblocks, float* out) {
-  const uint64_t t = (uint64_t)blockIdx.x * NT + threadIdx.x;  // (block, half, l)
-  if (t >= nblocks * 64) return;
-  const uint64_t b = t >> 6;
-  const int half = (int)(t >> 5) & 1, l = (int)t & 31;
-  const uint8_t* p = blocks + b * 210;
-  const float d = g4d::f16_bits_to_f32(p[208] | (p[209] << 8));
-  const uint8_t* ql = p + 64 * half;
-  const uint8_t qh = p[128 + 32 * half + l];
-  const int8_t* sc = (const int8_t*)(p + 192 + 8 * half);
-  const int is = l >> 4;
-  const int q1 = ((ql[l] & 15) | ((qh & 3) << 4)) - 32;
-  const int q2 = ((ql[l + 32] & 15) | (((qh >> 2) & 3) << 4)) - 32;
-  const int q3 = ((ql[l] >> 4) | (((qh >> 4) & 3) << 4)) - 32;
-  const int q4 = ((ql[l + 32] >> 4) | (((qh >> 6) & 3) << 4)) - 32;
-  float* o = out + b * 256 + 128 * half;
-  // d*sc*q needs <= 23 significant bits: exact in f32
-  o[l] = d * (float)sc[is] * (float)q1;
-  o[l + 32] = d * (float)sc[is + 2] * (float)q2;
-  o[l + 64] = d * (float)sc[is + 4] * (float)q3;
-  o[l + 96] = d * (float)sc[is + 6] * (float)q4;
-}
-
-// ---------------------------------------------------------------------------
 // seeded synthetic inputs (counter-based SplitMix64, Box-Muller in f64)
 // ---------------------------------------------------------------------------
 
@@ -595,26 +540,6 @@ int g4_topk256Batch(g4_ctx* ctx, const float* logits, float* result, uint32_t si
 
 int g4_topk256(g4_ctx* ctx, const float* logits, float* result, uint32_t size) {
   return g4_topk256Batch(ctx, logits, result, size, 1);
-}
-
-int g4_dequant_q4k(g4_ctx* ctx, const void* blocks, uint64_t nblocks, float* out) {
-  G4_ENTER(ctx);
-  G4_REQUIRE(blocks && out, "g4_dequant_q4k: null buffer");
-  if (!nblocks) return G4_OK;
-  hipLaunchKernelGGL(dequant_q4k_kernel, dim3(ceil_div(nblocks * 8, NT)), dim3(NT), 0, ctx->stream,
-                     (const uint8_t*)blocks, nblocks, out);
-  G4_LAUNCHED(ctx, "dequant_q4k");
-  return G4_OK;
-}
-
-int g4_dequant_q6k(g4_ctx* ctx, const void* blocks, uint64_t nblocks, float* out) {
-  G4_ENTER(ctx);
-  G4_REQUIRE(blocks && out, "g4_dequant_q6k: null buffer");
-  if (!nblocks) return G4_OK;
-  hipLaunchKernelGGL(dequant_q6k_kernel, dim3(ceil_div(nblocks * 64, NT)), dim3(NT), 0, ctx->stream,
-                     (const uint8_t*)blocks, nblocks, out);
-  G4_LAUNCHED(ctx, "dequant_q6k");
-  return G4_OK;
 }
 
 int g4_fill_q4k(g4_ctx* ctx, void* dst, uint64_t nblocks, uint64_t seed) {

@@ -28,6 +28,7 @@
 //    per launch (q/k/v), gate/up pairs with the GELU product epilogue.
 #include "g4_internal.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace {
@@ -116,7 +117,9 @@ __device__ __forceinline__ void digits4(const XView& xv, int vec, uint32_t e, fl
     *(uint32_t*)(xv.hi + off) = phi;
     *(uint32_t*)(xv.lo + off) = plo;
     if ((threadIdx.x & 7) == 0) {
-      xv.s[vec * (xv.K / 32) + e / 32] = am * (1.0f / XQ);
+      // a NaN or Inf input (sum not finite) makes the sub-block scale NaN,
+      // so the products carry it as the reference's f32 matvec does
+      xv.s[vec * (xv.K / 32) + e / 32] = __builtin_isfinite(sm) ? am * (1.0f / XQ) : __builtin_nanf("");
       xv.sum[vec * (xv.K / 32) + e / 32] = sm;
     }
     if ((threadIdx.x & 3) == 0) xv.c16[vec * (xv.K / 16) + e / 16] = make_int2(32 * shi, 32 * slo);
@@ -241,6 +244,24 @@ __device__ __forceinline__ void q4k_scales(uint32_t S0, uint32_t S1, uint32_t S2
   m_hi = (float)(mp >> 8);
 }
 
+// Q4_K 4-bit codes of one 32-bit word of qs (four weights of sub-blocks
+// 2g and 2g + 1 of group g, src/gguf.ts:188-207): the low nibbles belong to
+// sub-block 2g, the high nibbles to 2g + 1. Every Q4_K unit below extracts
+// its codes with these (g4_dequantPath checks them against the oracle).
+__device__ __forceinline__ uint32_t q4k_lo_codes(uint32_t w) { return w & 0x0f0f0f0fu; }
+__device__ __forceinline__ uint32_t q4k_hi_codes(uint32_t w) { return (w >> 4) & 0x0f0f0f0fu; }
+
+// Q6_K 6-bit codes (0..63, the value is code - 32) of run k of a half
+// (elements 128h + 32k + l .. l + 3, src/gguf.ts:344-361) from the words A =
+// ql[64h + l..], B = ql[64h + 32 + l..] and H = qh[32h + l..]; k is a
+// compile-time constant at every call.
+__device__ __forceinline__ uint32_t q6k_codes(int k, uint32_t A, uint32_t B, uint32_t H) {
+  if (k == 0) return (A & 0x0f0f0f0fu) | ((H << 4) & 0x30303030u);
+  if (k == 1) return (B & 0x0f0f0f0fu) | ((H << 2) & 0x30303030u);
+  if (k == 2) return ((A >> 4) & 0x0f0f0f0fu) | (H & 0x30303030u);
+  return ((B >> 4) & 0x0f0f0f0fu) | ((H >> 2) & 0x30303030u);
+}
+
 __device__ __forceinline__ int dot8(const uint32_t* q, const uint32_t* x) {
   int acc = 0;
 #pragma unroll
@@ -325,21 +346,45 @@ __device__ __forceinline__ void lds_piece(const uint8_t* p, uint32_t (&w)[4]) {
   w[3] = __builtin_amdgcn_alignbyte(a4, a3, sh);
 }
 
-// partial dot of quarter g of the Q4_K block at blk (LDS) with vector v
-__device__ __forceinline__ float q4_part(const XView& xv, const uint8_t* blk, int g, uint32_t b, int v) {
-  const uint4 hd = *(const uint4*)blk;
+// Q4_K unit g (a quarter block: sub-blocks 2g, 2g + 1) of a block in LDS:
+// the 16-byte header and the unit's 32 quant bytes (qs[32g..32g + 31]).
+__device__ __forceinline__ void q4_lds_unit(const uint8_t* blk, int g, uint4& hd, uint32_t (&qa)[8]) {
+  hd = *(const uint4*)blk;
   const uint4 q0 = *(const uint4*)(blk + 16 + 32 * g);
   const uint4 q1 = *(const uint4*)(blk + 32 + 32 * g);
+  qa[0] = q0.x; qa[1] = q0.y; qa[2] = q0.z; qa[3] = q0.w;
+  qa[4] = q1.x; qa[5] = q1.y; qa[6] = q1.z; qa[7] = q1.w;
+}
+
+// Q6_K unit g of a block in LDS (half h = g >> 1, l0 = 16 (g & 1)): the
+// 16-byte runs ql[64h + l0..], ql[64h + 32 + l0..], qh[32h + l0..], the
+// unit's scales sc[8h + (g & 1) + 2k] and d (src/gguf.ts:323-364).
+__device__ __forceinline__ void q6_lds_unit(const uint8_t* blk, int g, uint32_t (&A)[4], uint32_t (&B)[4],
+                                            uint32_t (&H)[4], int32_t (&scs)[4], float& dd) {
+  const int h = g >> 1, l0 = (g & 1) * 16;
+  lds_piece(blk + 64 * h + l0, A);
+  lds_piece(blk + 64 * h + 32 + l0, B);
+  lds_piece(blk + 128 + 32 * h + l0, H);
+  const int8_t* scp = (const int8_t*)(blk + 192 + 8 * h + (g & 1));
+#pragma unroll
+  for (int k = 0; k < 4; ++k) scs[k] = scp[2 * k];
+  dd = g4d::f16_bits_to_f32(*(const uint16_t*)(blk + 208));
+}
+
+// partial dot of quarter g of the Q4_K block at blk (LDS) with vector v
+__device__ __forceinline__ float q4_part(const XView& xv, const uint8_t* blk, int g, uint32_t b, int v) {
+  uint4 hd;
+  uint32_t qa[8];
+  q4_lds_unit(blk, g, hd, qa);
   const float d = g4d::f16_bits_to_f32(hd.x & 0xffffu);
   const float dmin = g4d::f16_bits_to_f32(hd.x >> 16);
   float sc_lo, sc_hi, m_lo, m_hi;
   q4k_scales(hd.y, hd.z, hd.w, g, sc_lo, sc_hi, m_lo, m_hi);
   uint32_t nl[8], nh[8];
-  const uint32_t qa[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    nl[k] = qa[k] & 0x0f0f0f0fu;
-    nh[k] = (qa[k] >> 4) & 0x0f0f0f0fu;
+    nl[k] = q4k_lo_codes(qa[k]);
+    nh[k] = q4k_hi_codes(qa[k]);
   }
   const uint32_t e0 = b * 256 + 64u * g;
   const int sub = (int)(e0 / 32);
@@ -367,19 +412,15 @@ __device__ __forceinline__ float q4_part(const XView& xv, const uint8_t* blk, in
 __device__ __forceinline__ float q6_part(const XView& xv, const uint8_t* blk, int u, uint32_t b, int v) {
   const int h = u >> 1, l0 = (u & 1) * 16;
   uint32_t A[4], B[4], H[4];
-  lds_piece(blk + 64 * h + l0, A);
-  lds_piece(blk + 64 * h + 32 + l0, B);
-  lds_piece(blk + 128 + 32 * h + l0, H);
-  const int8_t* scp = (const int8_t*)(blk + 192 + 8 * h + (u & 1));
-  const float dd = g4d::f16_bits_to_f32(*(const uint16_t*)(blk + 208));
+  int32_t scs[4];
+  float dd;
+  q6_lds_unit(blk, u, A, B, H, scs, dd);
   // run k covers elements 128h + 32k + l0 + [0,16) (src/gguf.ts:344-361)
   uint32_t q[4][4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    q[0][j] = (A[j] & 0x0f0f0f0fu) | ((H[j] << 4) & 0x30303030u);
-    q[1][j] = (B[j] & 0x0f0f0f0fu) | ((H[j] << 2) & 0x30303030u);
-    q[2][j] = ((A[j] >> 4) & 0x0f0f0f0fu) | (H[j] & 0x30303030u);
-    q[3][j] = ((B[j] >> 4) & 0x0f0f0f0fu) | ((H[j] >> 2) & 0x30303030u);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) q[k][j] = q6k_codes(k, A[j], B[j], H[j]);
   }
   float part = 0.f;
 #pragma unroll
@@ -399,7 +440,7 @@ __device__ __forceinline__ float q6_part(const XView& xv, const uint8_t* blk, in
     al = __builtin_amdgcn_sdot4((int)q[k][3], (int)tl.w, al, false);
     const int2 c = xv.c16[v * (xv.K / 16) + e / 16];
     const int I = (ah - c.x) * 256 + (al - c.y);
-    part += (float)scp[2 * k] * xv.s[v * (xv.K / 32) + e / 32] * (float)I;
+    part += (float)scs[k] * xv.s[v * (xv.K / 32) + e / 32] * (float)I;
   }
   return part * dd;
 }
@@ -802,7 +843,8 @@ __device__ __forceinline__ void mv_digitize(const MvPro<BPR, NWV, PRO>& P, uint8
       *(uint32_t*)(smem + X::HI + f) = ph;
       *(uint32_t*)(smem + X::LO + f) = pl;
       if ((lane & 7) == 0) {
-        ((float*)(smem + X::S))[f / 32] = am * (1.0f / XQ);
+        // non-finite input: a NaN scale carries it into every product
+        ((float*)(smem + X::S))[f / 32] = __builtin_isfinite(sm) ? am * (1.0f / XQ) : __builtin_nanf("");
         ((float*)(smem + X::SUM))[f / 32] = sm;
       }
       if ((lane & 3) == 0) ((int2*)(smem + X::C16))[f / 16] = make_int2(32 * shi, 32 * slo);
@@ -947,16 +989,15 @@ __device__ __forceinline__ void mv_unit_load(MvUnit<QT>& X, const uint8_t* smem,
 template <int QT>
 __device__ __forceinline__ float mv_unit_dot(const MvUnit<QT>& X, const uint8_t* blk, int g) {
   if constexpr (QT == 0) {
-    const uint4 hd = *(const uint4*)blk;
-    const uint4 q0 = *(const uint4*)(blk + 16 + 32 * g);
-    const uint4 q1 = *(const uint4*)(blk + 32 + 32 * g);
+    uint4 hd;
+    uint32_t qa[8];
+    q4_lds_unit(blk, g, hd, qa);
     float sc_lo, sc_hi, m_lo, m_hi;
     q4k_scales(hd.y, hd.z, hd.w, g, sc_lo, sc_hi, m_lo, m_hi);
-    const uint32_t qa[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
     int ah0 = 0, al0 = 0, ah1 = 0, al1 = 0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const uint32_t nl = qa[k] & 0x0f0f0f0fu, nh = (qa[k] >> 4) & 0x0f0f0f0fu;
+      const uint32_t nl = q4k_lo_codes(qa[k]), nh = q4k_hi_codes(qa[k]);
       ah0 = __builtin_amdgcn_sdot4((int)nl, (int)X.hi[k], ah0, false);
       al0 = __builtin_amdgcn_sdot4((int)nl, (int)X.lo[k], al0, false);
       ah1 = __builtin_amdgcn_sdot4((int)nh, (int)X.hi[8 + k], ah1, false);
@@ -967,29 +1008,22 @@ __device__ __forceinline__ float mv_unit_dot(const MvUnit<QT>& X, const uint8_t*
     const float i0 = (float)(ah0 * 256 + al0), i1 = (float)(ah1 * 256 + al1);
     return d * (sc_lo * X.s[0] * i0 + sc_hi * X.s[1] * i1) - dmin * (m_lo * X.s[2] + m_hi * X.s[3]);
   } else {
-    const int h = g >> 1, l0 = 16 * (g & 1);
     uint32_t A[4], B[4], H[4];
-    lds_piece(blk + 64 * h + l0, A);
-    lds_piece(blk + 64 * h + 32 + l0, B);
-    lds_piece(blk + 128 + 32 * h + l0, H);
-    const int8_t* scp = (const int8_t*)(blk + 192 + 8 * h + (g & 1));
-    const float dd = g4d::f16_bits_to_f32(*(const uint16_t*)(blk + 208));
+    int32_t scs[4];
+    float dd;
+    q6_lds_unit(blk, g, A, B, H, scs, dd);
     float part = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       int ah = 0, al = 0;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        uint32_t q;
-        if (k == 0) q = (A[j] & 0x0f0f0f0fu) | ((H[j] << 4) & 0x30303030u);
-        else if (k == 1) q = (B[j] & 0x0f0f0f0fu) | ((H[j] << 2) & 0x30303030u);
-        else if (k == 2) q = ((A[j] >> 4) & 0x0f0f0f0fu) | (H[j] & 0x30303030u);
-        else q = ((B[j] >> 4) & 0x0f0f0f0fu) | ((H[j] >> 2) & 0x30303030u);
+        const uint32_t q = q6k_codes(k, A[j], B[j], H[j]);
         ah = __builtin_amdgcn_sdot4((int)q, (int)X.hi[4 * k + j], ah, false);
         al = __builtin_amdgcn_sdot4((int)q, (int)X.lo[4 * k + j], al, false);
       }
       const int I = (ah - X.c[k].x) * 256 + (al - X.c[k].y);
-      part += (float)scp[2 * k] * X.s[k] * (float)I;
+      part += (float)scs[k] * X.s[k] * (float)I;
     }
     return part * dd;
   }
@@ -1018,21 +1052,29 @@ __device__ __forceinline__ void q4_unit_load(Q4Unit& w, __amdgpu_buffer_rsrc_t r
   w.q0 = bl16<POL>(r, o + 16 + 32 * g);
   w.q1 = bl16<POL>(r, o + 32 + 32 * g);
 }
+// The unit's header and 32 quant bytes as q4_lds_unit gives them.
+__device__ __forceinline__ void q4_unit_words(const Q4Unit& w, uint4& hd, uint32_t (&qa)[8]) {
+  hd = make_uint4(w.hd[0], w.hd[1], w.hd[2], w.hd[3]);
+  qa[0] = w.q0[0]; qa[1] = w.q0[1]; qa[2] = w.q0[2]; qa[3] = w.q0[3];
+  qa[4] = w.q1[0]; qa[5] = w.q1[1]; qa[6] = w.q1[2]; qa[7] = w.q1[3];
+}
 __device__ __forceinline__ float q4_unit_dot(const MvUnit<0>& X, const Q4Unit& w, int g) {
+  uint4 hd;
+  uint32_t qa[8];
+  q4_unit_words(w, hd, qa);
   float sc_lo, sc_hi, m_lo, m_hi;
-  q4k_scales(w.hd[1], w.hd[2], w.hd[3], g, sc_lo, sc_hi, m_lo, m_hi);
-  const uint32_t qa[8] = {w.q0[0], w.q0[1], w.q0[2], w.q0[3], w.q1[0], w.q1[1], w.q1[2], w.q1[3]};
+  q4k_scales(hd.y, hd.z, hd.w, g, sc_lo, sc_hi, m_lo, m_hi);
   int ah0 = 0, al0 = 0, ah1 = 0, al1 = 0;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    const uint32_t nl = qa[k] & 0x0f0f0f0fu, nh = (qa[k] >> 4) & 0x0f0f0f0fu;
+    const uint32_t nl = q4k_lo_codes(qa[k]), nh = q4k_hi_codes(qa[k]);
     ah0 = __builtin_amdgcn_sdot4((int)nl, (int)X.hi[k], ah0, false);
     al0 = __builtin_amdgcn_sdot4((int)nl, (int)X.lo[k], al0, false);
     ah1 = __builtin_amdgcn_sdot4((int)nh, (int)X.hi[8 + k], ah1, false);
     al1 = __builtin_amdgcn_sdot4((int)nh, (int)X.lo[8 + k], al1, false);
   }
-  const float d = g4d::f16_bits_to_f32(w.hd[0] & 0xffffu);
-  const float dmin = g4d::f16_bits_to_f32(w.hd[0] >> 16);
+  const float d = g4d::f16_bits_to_f32(hd.x & 0xffffu);
+  const float dmin = g4d::f16_bits_to_f32(hd.x >> 16);
   const float i0 = (float)(ah0 * 256 + al0), i1 = (float)(ah1 * 256 + al1);
   return d * (sc_lo * X.s[0] * i0 + sc_hi * X.s[1] * i1) - dmin * (m_lo * X.s[2] + m_hi * X.s[3]);
 }
@@ -1076,33 +1118,41 @@ __device__ __forceinline__ void q6_run(const u32x4a& v4, uint32_t v1, uint32_t s
   o[2] = __builtin_amdgcn_alignbyte(v4[3], v4[2], sh);
   o[3] = __builtin_amdgcn_alignbyte(v1, v4[3], sh);
 }
-__device__ __forceinline__ float q6_unit_dot(const MvUnit<1>& X, const Q6Unit& w) {
-  uint32_t A[4], B[4], H[4];
+// The unit's three runs shifted into place, its four scales and d, as
+// q6_lds_unit gives them for a block in LDS.
+__device__ __forceinline__ void q6_unit_unpack(const Q6Unit& w, uint32_t (&A)[4], uint32_t (&B)[4],
+                                               uint32_t (&H)[4], int32_t (&scs)[4], float& dd) {
   q6_run(w.a4, w.a1, w.sh, A);
   q6_run(w.b4, w.b1, w.sh, B);
   q6_run(w.h4, w.h1, w.sh, H);
   // the empty asm pins the byte extraction here, after the loads' wait
   uint32_t r0 = w.s0, r1 = w.s1, r2 = w.s2, r3 = w.s3, rd = w.d;
   asm volatile("" : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3), "+v"(rd));
-  const int32_t scs[4] = {(int32_t)(int8_t)r0, (int32_t)(int8_t)r1, (int32_t)(int8_t)r2, (int32_t)(int8_t)r3};
+  scs[0] = (int32_t)(int8_t)r0;
+  scs[1] = (int32_t)(int8_t)r1;
+  scs[2] = (int32_t)(int8_t)r2;
+  scs[3] = (int32_t)(int8_t)r3;
+  dd = g4d::f16_bits_to_f32(rd);
+}
+__device__ __forceinline__ float q6_unit_dot(const MvUnit<1>& X, const Q6Unit& w) {
+  uint32_t A[4], B[4], H[4];
+  int32_t scs[4];
+  float dd;
+  q6_unit_unpack(w, A, B, H, scs, dd);
   float part = 0.f;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     int ah = 0, al = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      uint32_t q;
-      if (k == 0) q = (A[j] & 0x0f0f0f0fu) | ((H[j] << 4) & 0x30303030u);
-      else if (k == 1) q = (B[j] & 0x0f0f0f0fu) | ((H[j] << 2) & 0x30303030u);
-      else if (k == 2) q = ((A[j] >> 4) & 0x0f0f0f0fu) | (H[j] & 0x30303030u);
-      else q = ((B[j] >> 4) & 0x0f0f0f0fu) | ((H[j] >> 2) & 0x30303030u);
+      const uint32_t q = q6k_codes(k, A[j], B[j], H[j]);
       ah = __builtin_amdgcn_sdot4((int)q, (int)X.hi[4 * k + j], ah, false);
       al = __builtin_amdgcn_sdot4((int)q, (int)X.lo[4 * k + j], al, false);
     }
     const int I = (ah - X.c[k].x) * 256 + (al - X.c[k].y);
     part += (float)scs[k] * X.s[k] * (float)I;
   }
-  return part * g4d::f16_bits_to_f32(rd);
+  return part * dd;
 }
 
 // Q6_K unit against D8 digits: each 16-element run (one int8 scale) is two
@@ -1135,23 +1185,16 @@ __device__ __forceinline__ void mv_unit_load8(MvUnit8& X, const uint8_t* smem, i
 }
 __device__ __forceinline__ float q6_unit_dot8(const MvUnit8& X, const Q6Unit& w) {
   uint32_t A[4], B[4], H[4];
-  q6_run(w.a4, w.a1, w.sh, A);
-  q6_run(w.b4, w.b1, w.sh, B);
-  q6_run(w.h4, w.h1, w.sh, H);
-  uint32_t r0 = w.s0, r1 = w.s1, r2 = w.s2, r3 = w.s3, rd = w.d;
-  asm volatile("" : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3), "+v"(rd));
-  const int32_t scs[4] = {(int32_t)(int8_t)r0, (int32_t)(int8_t)r1, (int32_t)(int8_t)r2, (int32_t)(int8_t)r3};
+  int32_t scs[4];
+  float dd;
+  q6_unit_unpack(w, A, B, H, scs, dd);
   float part = 0.f;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     int ah[2] = {0, 0}, al[2] = {0, 0};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      uint32_t q;
-      if (k == 0) q = (A[j] & 0x0f0f0f0fu) | ((H[j] << 4) & 0x30303030u);
-      else if (k == 1) q = (B[j] & 0x0f0f0f0fu) | ((H[j] << 2) & 0x30303030u);
-      else if (k == 2) q = ((A[j] >> 4) & 0x0f0f0f0fu) | (H[j] & 0x30303030u);
-      else q = ((B[j] >> 4) & 0x0f0f0f0fu) | ((H[j] >> 2) & 0x30303030u);
+      const uint32_t q = q6k_codes(k, A[j], B[j], H[j]);
       ah[j >> 1] = __builtin_amdgcn_sdot4((int)q, (int)X.hi[4 * k + j], ah[j >> 1], false);
       al[j >> 1] = __builtin_amdgcn_sdot4((int)q, (int)X.lo[4 * k + j], al[j >> 1], false);
     }
@@ -1159,7 +1202,7 @@ __device__ __forceinline__ float q6_unit_dot8(const MvUnit8& X, const Q6Unit& w)
     const int I1 = (ah[1] - X.c[2 * k + 1].x) * 256 + (al[1] - X.c[2 * k + 1].y);
     part += (float)scs[k] * (X.s[2 * k] * (float)I0 + X.s[2 * k + 1] * (float)I1);
   }
-  return part * g4d::f16_bits_to_f32(rd);
+  return part * dd;
 }
 
 // D8 digits of a gate/up launch's GELU outputs: the 8 rows of a group are
@@ -1175,12 +1218,14 @@ __device__ __forceinline__ void mv_d8_group(float v, bool real, uint32_t row, ui
   const int lo = ((q + 128) & 255) - 128;
   const int hi = (q - lo) >> 8;
   const int shi = (int)g4d::wave_sum_dpp((float)hi), slo = (int)g4d::wave_sum_dpp((float)lo);
+  // a NaN or Inf in the group makes its scale NaN (the products carry it)
+  const bool bad = __ballot(real && !__builtin_isfinite(v)) != 0;
   if (real) {
     d8[row] = (uint8_t)(hi & 255);
     d8[K + row] = (uint8_t)(lo & 255);
   }
   if (real && (threadIdx.x & 63) == 0) {  // the group's first row
-    ((float*)(d8 + 2 * (size_t)K))[row / 8] = am * (1.0f / XQ);
+    ((float*)(d8 + 2 * (size_t)K))[row / 8] = bad ? __builtin_nanf("") : am * (1.0f / XQ);
     ((int2*)(d8 + 2 * (size_t)K + 4 * (size_t)(K / 8)))[row / 8] = make_int2(32 * shi, 32 * slo);
   }
 }
@@ -1368,6 +1413,108 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
     if constexpr (NMAT == 1)
       if (segs.amx)
         mv_argmax_partial<NWV>(best, (g4d::Cand*)(smem + MvXA<BPR, PRO>::RED8), segs.amx + blockIdx.x);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Unpack check (the test export g4_dequantPath): weight values as the matvec
+// units see them. Each thread takes one unit (a quarter block), loads it
+// with the loader of a kernel family, extracts codes, scales, mins and d with
+// the same helpers the products use, and forms the reference's dequantized
+// value from them: Q4_K (d*sc)*q - dmin*m (src/gguf.ts:184-209), Q6_K
+// (d*sc)*(q - 32) (src/gguf.ts:336-364); the products are exact in f32 and
+// the result is rounded once, as the reference's f64 value stored to f32.
+// PATH 0: register units (q4_unit_load / q6_unit_load through a buffer
+// resource, q6_run; the one-tile mv_kernel). PATH 1: units of blocks staged
+// in LDS at their byte offsets (q4_lds_unit / q6_lds_unit with lds_piece;
+// the tile-walking mv_kernel and gemv_kernel).
+// ---------------------------------------------------------------------------
+constexpr int UC_BLOCKS = NT / 4;  // blocks per workgroup (4 units each)
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
+
+__device__ __forceinline__ void q4_unit_values(uint4 hd, const uint32_t (&qa)[8], int g, float* out) {
+  float sc_lo, sc_hi, m_lo, m_hi;
+  q4k_scales(hd.y, hd.z, hd.w, g, sc_lo, sc_hi, m_lo, m_hi);
+  const float d = g4d::f16_bits_to_f32(hd.x & 0xffffu), dmin = g4d::f16_bits_to_f32(hd.x >> 16);
+  const float d_lo = d * sc_lo, d_hi = d * sc_hi, n_lo = dmin * m_lo, n_hi = dmin * m_hi;  // exact
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t lo = q4k_lo_codes(qa[k]), hi = q4k_hi_codes(qa[k]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[64 * g + 4 * k + i] = d_lo * (float)byte_of(lo, i) - n_lo;
+      out[64 * g + 32 + 4 * k + i] = d_hi * (float)byte_of(hi, i) - n_hi;
+    }
+  }
+}
+
+__device__ __forceinline__ void q6_unit_values(const uint32_t (&A)[4], const uint32_t (&B)[4],
+                                               const uint32_t (&H)[4], const int32_t (&scs)[4], float dd, int g,
+                                               float* out) {
+  const int h = g >> 1, l0 = 16 * (g & 1);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float ds = dd * (float)scs[k];  // exact
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t c = q6k_codes(k, A[j], B[j], H[j]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[128 * h + 32 * k + l0 + 4 * j + i] = ds * (float)((int)byte_of(c, i) - 32);
+    }
+  }
+}
+
+template <int QT, int PATH>
+__global__ __launch_bounds__(NT) void unpack_check_kernel(const uint8_t* W, uint32_t nblocks, float* out) {
+  constexpr int BY = BlockOf<QT>::BYTES;
+  __shared__ __align__(16) uint8_t lds[PATH == 1 ? UC_BLOCKS * BY : 16];
+  const uint32_t b0 = blockIdx.x * (uint32_t)UC_BLOCKS;
+  const uint32_t b = b0 + threadIdx.x / 4;
+  const int g = threadIdx.x & 3;
+  float* o = out + (size_t)b * 256;
+  if constexpr (PATH == 0) {
+    if (b >= nblocks) return;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, (int)(nblocks * (uint32_t)BY), 0x00020000);
+    const uint32_t off = b * (uint32_t)BY;
+    if constexpr (QT == 0) {
+      Q4Unit w;
+      q4_unit_load<0>(w, rs, off, g);
+      uint4 hd;
+      uint32_t qa[8];
+      q4_unit_words(w, hd, qa);
+      q4_unit_values(hd, qa, g, o);
+    } else {
+      Q6Unit w;
+      q6_unit_load<0>(w, rs, off, W + off, g);
+      uint32_t A[4], B[4], H[4];
+      int32_t scs[4];
+      float dd;
+      q6_unit_unpack(w, A, B, H, scs, dd);
+      q6_unit_values(A, B, H, scs, dd, g, o);
+    }
+  } else {
+    // the workgroup's blocks, byte for byte at their offsets from the first
+    // (16-byte aligned: UC_BLOCKS * BY is a multiple of 16)
+    const uint32_t nb = min((uint32_t)UC_BLOCKS, nblocks - b0);
+    const uint16_t* src = (const uint16_t*)(W + (size_t)b0 * BY);
+    for (uint32_t i = threadIdx.x; i < nb * BY / 2; i += NT) ((uint16_t*)lds)[i] = src[i];
+    __syncthreads();
+    if (b >= nblocks) return;
+    const uint8_t* blk = lds + (threadIdx.x / 4) * BY;
+    if constexpr (QT == 0) {
+      uint4 hd;
+      uint32_t qa[8];
+      q4_lds_unit(blk, g, hd, qa);
+      q4_unit_values(hd, qa, g, o);
+    } else {
+      uint32_t A[4], B[4], H[4];
+      int32_t scs[4];
+      float dd;
+      q6_lds_unit(blk, g, A, B, H, scs, dd);
+      q6_unit_values(A, B, H, scs, dd, g, o);
+    }
   }
 }
 
@@ -1832,6 +1979,42 @@ int g4_matmulQuantBatch_q4k(g4_ctx* ctx, const float* input, const void* weight,
 int g4_matmulQuantBatch_q6k(g4_ctx* ctx, const float* input, const void* weight, float* output,
                             g4_matmul_params p, uint32_t batch) {
   return matmul_quant(ctx, __func__, 1, input, weight, output, p, batch);
+}
+
+// g4_dequantPath: values through the unpack of one kernel family. Paths 0
+// and 1 (the matvec units) here; path 2 (the matrix-core operands) in
+// k_batch.hip. Blocks go in launches of at most 2^24 (the buffer resource
+// addresses up to 4 GiB).
+int g4_dequantPath(g4_ctx* ctx, int wtype, int path, const void* blocks, uint64_t nblocks, float* out) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(blocks && out, "g4_dequantPath: null buffer");
+  G4_REQUIRE(wtype == 0 || wtype == 1, "g4_dequantPath: wtype must be 0 (Q4_K) or 1 (Q6_K)");
+  G4_REQUIRE(path >= 0 && path <= 2, "g4_dequantPath: path must be 0, 1 or 2");
+  G4_REQUIRE(((uintptr_t)blocks & 15) == 0, "g4_dequantPath: blocks must be 16-byte aligned");
+  if (!nblocks) return G4_OK;
+  if (path == 2) return g4_internal_operand_values(ctx, wtype, blocks, nblocks, out);
+  const size_t by = wtype == 0 ? 144 : 210;
+  constexpr uint64_t kChunk = 1u << 24;
+  for (uint64_t b0 = 0; b0 < nblocks; b0 += kChunk) {
+    const uint32_t nb = (uint32_t)std::min<uint64_t>(kChunk, nblocks - b0);
+    const uint8_t* w = (const uint8_t*)blocks + b0 * by;
+    float* o = out + b0 * 256;
+    const dim3 grid(ceil_div(nb, UC_BLOCKS));
+    if (wtype == 0 && path == 0) hipLaunchKernelGGL((unpack_check_kernel<0, 0>), grid, dim3(NT), 0, ctx->stream, w, nb, o);
+    else if (wtype == 0) hipLaunchKernelGGL((unpack_check_kernel<0, 1>), grid, dim3(NT), 0, ctx->stream, w, nb, o);
+    else if (path == 0) hipLaunchKernelGGL((unpack_check_kernel<1, 0>), grid, dim3(NT), 0, ctx->stream, w, nb, o);
+    else hipLaunchKernelGGL((unpack_check_kernel<1, 1>), grid, dim3(NT), 0, ctx->stream, w, nb, o);
+    G4_LAUNCHED(ctx, "unpack_check");
+  }
+  return G4_OK;
+}
+
+// The dequant debug exports run the one-vector matvec's register units.
+int g4_dequant_q4k(g4_ctx* ctx, const void* blocks, uint64_t nblocks, float* out) {
+  return g4_dequantPath(ctx, 0, 0, blocks, nblocks, out);
+}
+int g4_dequant_q6k(g4_ctx* ctx, const void* blocks, uint64_t nblocks, float* out) {
+  return g4_dequantPath(ctx, 1, 0, blocks, nblocks, out);
 }
 
 int g4_matmulQuant_f16(g4_ctx* ctx, const float* input, const uint16_t* weight, float* output,

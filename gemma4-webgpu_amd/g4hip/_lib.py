@@ -147,6 +147,9 @@ SIGNATURES = {
     "g4_attnScore": (_I, [_P, _P, _P, _P, AttnScoreParams]),
     "g4_softmax": (_I, [_P, _P, SoftmaxParams]),
     "g4_attnOutput": (_I, [_P, _P, _P, _P, AttnOutputParams]),
+    "g4_attnScore_dev": (_I, [_P, _P, _P, _P, AttnScoreParams, _P]),
+    "g4_softmax_dev": (_I, [_P, _P, SoftmaxParams, _P]),
+    "g4_attnOutput_dev": (_I, [_P, _P, _P, _P, AttnOutputParams, _P]),
     "g4_attnDecode_workspace_size": (_I, [AttnScoreParams, ctypes.POINTER(_SZ)]),
     "g4_attnDecode": (_I, [_P, _P, _P, _P, _P, AttnScoreParams, _P, _SZ]),
     "g4_attnDecode_dev": (_I, [_P, _P, _P, _P, _P, AttnScoreParams, _P, _SZ, _P]),
@@ -199,6 +202,7 @@ SIGNATURES = {
                                            ctypes.POINTER(_P), ctypes.POINTER(_U32), _I, _U32, _F, _F, _U32]),
     "g4_dequant_q4k": (_I, [_P, _P, _U64, _P]),
     "g4_dequant_q6k": (_I, [_P, _P, _U64, _P]),
+    "g4_dequantPath": (_I, [_P, _I, _I, _P, _U64, _P]),
     "g4_splitmix64": (_U64, [_U64, _U64]),
     "g4_fill_q4k": (_I, [_P, _P, _U64, _U64]),
     "g4_fill_q6k": (_I, [_P, _P, _U64, _U64]),

@@ -296,15 +296,29 @@ class Context:
                                             _p(position_dev)))
 
     def attnScore(self, q: Ptr, k_cache: Ptr, scores: Ptr, nqh: int, nkh: int, hd: int, seq_len: int,
-                  scale: float = 1.0, window: int = 0) -> None:
-        check(lib().g4_attnScore(self.h, _p(q), _p(k_cache), _p(scores),
-                                 AttnScoreParams(nqh, nkh, hd, seq_len, scale, window)))
+                  scale: float = 1.0, window: int = 0, position_dev: Ptr = None) -> None:
+        """With position_dev, seq_len = *position_dev + 1 on the device and the
+        `seq_len` argument is the maximum (g4_attnScore_dev)."""
+        p = AttnScoreParams(nqh, nkh, hd, seq_len, scale, window)
+        if position_dev is None:
+            check(lib().g4_attnScore(self.h, _p(q), _p(k_cache), _p(scores), p))
+        else:
+            check(lib().g4_attnScore_dev(self.h, _p(q), _p(k_cache), _p(scores), p, _p(position_dev)))
 
-    def softmax(self, scores: Ptr, num_heads: int, seq_len: int) -> None:
-        check(lib().g4_softmax(self.h, _p(scores), SoftmaxParams(num_heads, seq_len)))
+    def softmax(self, scores: Ptr, num_heads: int, seq_len: int, position_dev: Ptr = None) -> None:
+        p = SoftmaxParams(num_heads, seq_len)
+        if position_dev is None:
+            check(lib().g4_softmax(self.h, _p(scores), p))
+        else:
+            check(lib().g4_softmax_dev(self.h, _p(scores), p, _p(position_dev)))
 
-    def attnOutput(self, probs: Ptr, v_cache: Ptr, out: Ptr, nqh: int, nkh: int, hd: int, seq_len: int) -> None:
-        check(lib().g4_attnOutput(self.h, _p(probs), _p(v_cache), _p(out), AttnOutputParams(nqh, nkh, hd, seq_len)))
+    def attnOutput(self, probs: Ptr, v_cache: Ptr, out: Ptr, nqh: int, nkh: int, hd: int, seq_len: int,
+                   position_dev: Ptr = None) -> None:
+        p = AttnOutputParams(nqh, nkh, hd, seq_len)
+        if position_dev is None:
+            check(lib().g4_attnOutput(self.h, _p(probs), _p(v_cache), _p(out), p))
+        else:
+            check(lib().g4_attnOutput_dev(self.h, _p(probs), _p(v_cache), _p(out), p, _p(position_dev)))
 
     @staticmethod
     def attn_workspace_bytes(nqh: int, nkh: int, hd: int, seq_len: int, window: int = 0) -> int:
@@ -484,6 +498,11 @@ class Context:
 
     def dequant_q6k(self, blocks: Ptr, nblocks: int, out: Ptr) -> None:
         check(lib().g4_dequant_q6k(self.h, _p(blocks), nblocks, _p(out)))
+
+    def dequantPath(self, wtype: str, path: int, blocks: Ptr, nblocks: int, out: Ptr) -> None:
+        """Weight values through the unpack of one kernel family (0: register
+        units, 1: LDS units, 2: matrix-core operands)."""
+        check(lib().g4_dequantPath(self.h, {"q4k": 0, "q6k": 1}[wtype], path, _p(blocks), nblocks, _p(out)))
 
     def fill_q4k(self, dst: Ptr, nblocks: int, seed: int) -> None:
         check(lib().g4_fill_q4k(self.h, _p(dst), nblocks, seed))

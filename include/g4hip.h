@@ -89,7 +89,10 @@ int g4_event_elapsed_ms(g4_event* start, g4_event* end, float* ms);
 int g4_event_destroy(g4_event* ev);
 
 /* Graph capture of everything enqueued on the context stream between begin
- * and end; launch replays it on the context stream. */
+ * and end; launch replays it on the context stream. While capturing,
+ * g4_memset, g4_upload, g4_download(_async) and g4_stream_sync return
+ * G4_ERR_INVALID (a memset node or a synchronisation has no place in a
+ * replayed graph). */
 int g4_graph_begin(g4_ctx* ctx);
 int g4_graph_end(g4_ctx* ctx, g4_graph** graph);
 int g4_graph_launch(g4_ctx* ctx, g4_graph* graph);
@@ -150,6 +153,16 @@ int g4_softmax(g4_ctx* ctx, float* scores, g4_softmax_params p);
 typedef struct { uint32_t num_q_heads, num_kv_heads, head_dim, seq_len; } g4_attn_output_params;
 int g4_attnOutput(g4_ctx* ctx, const float* probs, const uint16_t* v_cache, float* output,
                   g4_attn_output_params p);
+/* The trio with seq_len = *position_dev + 1 read on the device (the per-forward
+ * seq_len patches of src/engine.ts:1496-1504, so the per-key sequence can be
+ * captured once and replayed): p.seq_len is the maximum the grid and the
+ * scores buffer were sized for, and the device value is clamped to it. The
+ * scores rows keep the reference's stride seq_len (the device value). */
+int g4_attnScore_dev(g4_ctx* ctx, const float* q, const uint16_t* k_cache, float* scores,
+                     g4_attn_score_params p, const uint32_t* position_dev);
+int g4_softmax_dev(g4_ctx* ctx, float* scores, g4_softmax_params p, const uint32_t* position_dev);
+int g4_attnOutput_dev(g4_ctx* ctx, const float* probs, const uint16_t* v_cache, float* output,
+                      g4_attn_output_params p, const uint32_t* position_dev);
 
 /* Fused split-K flash-decode: the attnScore -> softmax -> attnOutput trio in
  * one pass over the KV cache (same inputs and masking as the trio,
@@ -485,9 +498,22 @@ int g4_gateUpGeluBatch(g4_ctx* ctx, const float* x, const void* ops, const void*
 /* Debug / test exports                                                      */
 /* ------------------------------------------------------------------------ */
 
-/* Dequantize nblocks raw blocks to f32 (bit-exact vs src/gguf.ts:168-210 / :323-368). */
+/* Dequantize nblocks raw blocks to f32 (bit-exact vs src/gguf.ts:168-210 / :323-368),
+ * through the unpack of the one-vector matvec's register units (path 0 below). */
 int g4_dequant_q4k(g4_ctx* ctx, const void* blocks, uint64_t nblocks, float* out);
 int g4_dequant_q6k(g4_ctx* ctx, const void* blocks, uint64_t nblocks, float* out);
+/* The weight values as one kernel family of the hot path unpacks them
+ * (GGUFParser.dequantizeQ4_K / dequantizeQ6_K, src/gguf.ts:168-210 / :323-368,
+ * restated with the family's own loads and code/scale extraction; blocks is
+ * 16-byte aligned, one-block rows, wtype 0 = Q4_K, 1 = Q6_K):
+ *   path 0: register units of the one-vector matvec (buffer loads, byte shifts);
+ *   path 1: units read from blocks staged in LDS (the tile-walking matvec and
+ *           the 2-8 vector matvec);
+ *   path 2: the matrix-core operands of the M >= 16 matmul: Q4_K d*(sc*q) -
+ *           dmin*m as the reference; Q6_K d times sc*(q-32) rounded once to
+ *           f16 (exact for |sc*(q-32)| <= 2048).
+ * Paths 0 and 1 are bit-exact with the reference's f32 values. */
+int g4_dequantPath(g4_ctx* ctx, int wtype, int path, const void* blocks, uint64_t nblocks, float* out);
 
 /* Seeded synthetic inputs, generated on the device (counter-based SplitMix64;
  * block b of a stream draws words 32b.., element i of a normal stream words

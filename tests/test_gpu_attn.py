@@ -43,6 +43,52 @@ def test_trio(ctx, L, window):
     assert_close(out.download(np.float32), O.attention(q, k, v, nqh, nkh, hd, L, 1.0, window), what="trio")
 
 
+def test_trio_dev_graph_replay(ctx):
+    """The trio with seq_len read from the device (src/engine.ts:1496-1504
+    patches it per forward): one captured graph replayed at positions 40, 41,
+    42 (a device-side position advance ends each replay) gives the oracle's
+    attention at every length, with the scores rows at stride seq_len, and
+    memset / upload / download / stream sync are refused inside the capture."""
+    nqh, nkh, hd, max_len, window = 8, 1, 256, 64, 32
+    k, v = kv(91, max_len, nkh, hd)
+    q = unit_q(93, nqh, hd)
+    dq, dk, dv = ctx.from_numpy(q), ctx.from_numpy(k), ctx.from_numpy(v)
+    sc = ctx.zeros(nqh * max_len, np.float32)
+    out = ctx.empty(nqh * hd, np.float32)
+    pos = ctx.from_numpy(np.array([40], np.uint32))
+    ctx.graph_begin()
+    try:
+        ctx.attnScore(dq, dk, sc, nqh, nkh, hd, max_len, 1.0, window, position_dev=pos)
+        ctx.softmax(sc, nqh, max_len, position_dev=pos)
+        ctx.attnOutput(sc, dv, out, nqh, nkh, hd, max_len, position_dev=pos)
+        ctx.advancePosition(pos, 1)
+        for bad in (lambda: sc.zero(), lambda: pos.upload(np.array([1], np.uint32)),
+                    lambda: pos.download(np.uint32), lambda: ctx.sync()):
+            with pytest.raises(Exception, match="while a graph is being captured"):
+                bad()
+    finally:
+        g = ctx.graph_end()
+    try:
+        for p in (40, 41, 42):
+            ctx.graph_launch(g)
+            ctx.sync()
+            L = p + 1
+            got = out.download(np.float32)
+            assert_close(got, O.attention(q, k, v, nqh, nkh, hd, L, 1.0, window), what=f"dev trio L={L}")
+            probs = sc.download(np.float32)[:nqh * L].reshape(nqh, L)
+            assert np.allclose(probs.sum(axis=1), 1.0, rtol=1e-5)
+            assert np.all(probs[:, :L - window] == 0)          # masked rows: exp(-1e30 - max) = 0
+        assert int(pos.download(np.uint32)[0]) == 43
+    finally:
+        ctx.graph_destroy(g)
+    # a device position past the maximum is clamped to it
+    pos.upload(np.array([1000], np.uint32))
+    ctx.attnScore(dq, dk, sc, nqh, nkh, hd, max_len, 1.0, window, position_dev=pos)
+    ctx.softmax(sc, nqh, max_len, position_dev=pos)
+    ctx.attnOutput(sc, dv, out, nqh, nkh, hd, max_len, position_dev=pos)
+    assert_close(out.download(np.float32), O.attention(q, k, v, nqh, nkh, hd, max_len, 1.0, window), what="clamped")
+
+
 DECODE_CASES = [
     # (L, window, head_dim): short, E2B local (W=512), the config-3 contexts
     (1, 0, 256), (7, 0, 256), (64, 0, 256), (65, 0, 256), (600, 512, 256), (600, 0, 256),

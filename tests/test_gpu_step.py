@@ -53,7 +53,10 @@ def check_token(d, logits_gpu, what):
 
 def test_step_reference_and_fused_vs_oracle(ctx, dec):
     snap = snapshot(dec)
-    x_ref, logits_ref = oracle_step(dec, snap[0], [k.copy() for k in snap[1]], [v.copy() for v in snap[2]], POS)
+    kcs, vcs = [k.copy() for k in snap[1]], [v.copy() for v in snap[2]]
+    x_ref, logits_ref = oracle_step(dec, snap[0], kcs, vcs, POS)   # stores the oracle's rows at POS
+    kv = dec.s.kv_dim
+    row = slice(POS * kv, (POS + 1) * kv)
 
     dec.step_reference(POS)
     ctx.sync()
@@ -61,6 +64,7 @@ def test_step_reference_and_fused_vs_oracle(ctx, dec):
     lg = host(dec.logits, np.float32)
     assert_close(lg, logits_ref, what="per-key logits")
     check_token(dec, lg, "per-key token")
+    perkey_rows = [(host(L.k_cache, np.uint16)[row], host(L.v_cache, np.uint16)[row]) for L in dec.layers]
 
     restore(dec, snap)
     dec.set_position(POS)
@@ -71,12 +75,24 @@ def test_step_reference_and_fused_vs_oracle(ctx, dec):
     lg = host(dec.logits, np.float32)
     assert_close(lg, logits_ref, what="fused logits")
     check_token(dec, lg, "fused token")
-    # the KV rows written at POS are the same f16 bits on both paths
+    # the K/V rows written at POS: the fused path's f16 rows within one f16
+    # ulp of the per-key path's (the two round f32 values that differ in
+    # their last bits), both within the tolerance of the oracle's rows, and
+    # nothing else of the caches changed
     for il, L in enumerate(dec.layers):
-        row = slice(POS * dec.s.kv_dim, (POS + 1) * dec.s.kv_dim)
-        kf = host(L.k_cache, np.uint16)[row]
-        restore_k = snap[1][il][row]
-        assert not np.array_equal(kf, restore_k)
+        kall, vall = host(L.k_cache, np.uint16), host(L.v_cache, np.uint16)
+        for nm, fused, perkey, ref, before in (("k", kall, perkey_rows[il][0], kcs[il], snap[1][il]),
+                                               ("v", vall, perkey_rows[il][1], vcs[il], snap[2][il])):
+            f16 = fused[row].view(np.float16).astype(np.float32)
+            p16 = perkey.view(np.float16).astype(np.float32)
+            assert np.all(np.abs(f16 - p16) <= 2.0 ** -10 * np.maximum(np.abs(p16), 2.0 ** -14)), (nm, il)
+            want = ref[row].view(np.float16).astype(np.float32)
+            assert_close(f16, want, what=f"fused {nm} row layer {il}")
+            assert_close(p16, want, what=f"per-key {nm} row layer {il}")
+            assert not np.array_equal(fused[row], before[row])
+            other = np.ones(fused.size, bool)
+            other[row] = False
+            assert np.array_equal(fused[other], before[other])
     restore(dec, snap)
 
 

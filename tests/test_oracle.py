@@ -233,6 +233,51 @@ def test_matmul_closed_forms():
     assert np.allclose(O.matmul(x2, W6, 32, 1536, "q6k"), Wd6 @ x2, rtol=1e-6, atol=1e-6)
 
 
+def test_matmul_f16w_closed_forms():
+    """The f16-weight matvec (shaders/matmul_quant.wgsl:14,21-54: W is
+    array<f16>, f32 accumulate) on weights whose products are known exactly:
+    all ones -> sum(x); a permutation matrix -> the permuted x bit for bit;
+    powers of two down a diagonal -> x scaled exactly; f16 limits (65504,
+    the smallest subnormal) times power-of-two x; and linearity in x."""
+    rng = np.random.default_rng(21)
+    M, N = 7, 384
+    x = rng.standard_normal(N).astype(np.float32)
+    ones = np.full(M * N, 0x3C00, np.uint16)
+    assert np.allclose(O.matmul(x, ones, M, N, "f16"), x.astype(np.float64).sum(), rtol=1e-7, atol=1e-7)
+    perm = rng.permutation(N)
+    P = np.zeros((N, N), np.uint16)
+    P[np.arange(N), perm] = 0x3C00
+    y = O.matmul(x, P.reshape(-1), N, N, "f16")
+    assert np.array_equal(y.view(np.uint32), x[perm].view(np.uint32))
+    D = np.zeros((N, N), np.float16)
+    e = rng.integers(-14, 15, N)
+    D[np.arange(N), np.arange(N)] = np.float16(2.0) ** e.astype(np.float16)
+    y = O.matmul(x, D.view(np.uint16).reshape(-1), N, N, "f16")
+    assert np.array_equal(y, (x.astype(np.float64) * 2.0 ** e).astype(np.float32))
+    lim = np.array([0x7BFF, 0x0001, 0x8400, 0x3555], np.uint16)     # 65504, 2^-24, -2^-14, 0.33325...
+    xs = np.zeros(4, np.float32)
+    for i, h in enumerate(lim):
+        xs[:] = 0
+        xs[i] = 0.5
+        row = lim.reshape(1, 4)
+        want = float(np.uint16(h).view(np.float16)) * 0.5
+        assert O.matmul(xs, row.reshape(-1), 1, 4, "f16")[0] == np.float32(want)
+    # torch's float64 linear on the decoded weights (a library routine)
+    import torch
+    W = (rng.standard_normal((M, N)) * 0.05).astype(np.float16)
+    x2 = rng.standard_normal(N).astype(np.float32)
+    ref = torch.nn.functional.linear(torch.from_numpy(x2.astype(np.float64)),
+                                     torch.from_numpy(W.astype(np.float64))).numpy()
+    got = O.matmul(x2, W.view(np.uint16).reshape(-1), M, N, "f16")
+    assert np.allclose(got, ref, rtol=1e-6, atol=1e-7)
+    # a transposed operand (W^T x) would fail this
+    assert not np.allclose(got, (W.astype(np.float64).T[:M, :M] @ x2[:M]), rtol=1e-2)
+    # linearity
+    got3 = O.matmul((x2 + x).astype(np.float32), W.view(np.uint16).reshape(-1), M, N, "f16")
+    assert np.allclose(got3, got + O.matmul(x, W.view(np.uint16).reshape(-1), M, N, "f16"), rtol=1e-5,
+                       atol=1e-6)
+
+
 # --------------------------------------------------------------------------
 # norms, activations, RoPE: fixtures and library routines
 # --------------------------------------------------------------------------
@@ -304,6 +349,87 @@ def test_rope_against_transformers_rotate_half():
         sin = torch.from_numpy(np.sin(emb))[None, None]
         want = apply_rotary_pos_emb(torch.from_numpy(xn)[None], cos, sin, unsqueeze_dim=1)[0].numpy()
         assert np.allclose(got, want, rtol=1e-5, atol=1e-6), (hd, theta, pos)
+
+
+def _tf_inv_freq():
+    """transformers' own RoPE initialisers for Gemma 4 (default rope for the
+    sliding layers: theta 1e4, head_dim 256; proportional rope for the full
+    layers: theta 1e6, head_dim 512, partial_rotary_factor 0.25), read from
+    the rotary module's buffers."""
+    from transformers.models.gemma4.configuration_gemma4 import Gemma4TextConfig
+    from transformers.models.gemma4.modeling_gemma4 import Gemma4TextRotaryEmbedding
+
+    cfg = Gemma4TextConfig()
+    rp = cfg.rope_parameters
+    assert rp["sliding_attention"] == {"rope_type": "default", "rope_theta": 10000.0}
+    assert rp["full_attention"]["rope_type"] == "proportional"
+    assert rp["full_attention"]["partial_rotary_factor"] == 0.25
+    assert rp["full_attention"]["rope_theta"] == 1e6
+    rot = Gemma4TextRotaryEmbedding(cfg)
+    buf = dict(rot.named_buffers())
+    return rot, buf["sliding_attention_inv_freq"].numpy(), buf["full_attention_inv_freq"].numpy()
+
+
+def test_rope_freq_against_transformers_init():
+    """Every pair's frequency (src/engine.ts:522-537,
+    shaders/fused_per_head_norm_rope.wgsl:50-55) against transformers'
+    default and proportional initialisers: 1/theta^(2i/hd) for every pair of
+    a sliding layer (hd 256, theta 1e4); for a full layer (hd 512, theta 1e6)
+    the first 64 pairs rotate at 1/theta^(2i/512) and the other 192 are
+    frozen, which the reference gets from the GGUF rope_freqs divisor table
+    (1.0, then 1e30 = +Inf in f16)."""
+    _, inv_s, inv_f = _tf_inv_freq()
+    assert inv_s.shape == (128,) and inv_f.shape == (256,)
+    ones = np.ones(128, np.float16).view(np.uint16)
+    got_s = np.array([O.rope_freq(1e4, i, 256, 0, ones) for i in range(128)], np.float32)
+    # f64 pow rounded once vs torch's f32 pow: within 2 ulp
+    assert np.max(np.abs(got_s.view(np.int32) - inv_s.view(np.int32))) <= 1   # f64 vs f32 pow: 1 ulp
+    table = np.where(np.arange(256) < 64, 1.0, 1e30).astype(np.float32)
+    table16 = np.array([O.f32_to_f16_trunc(float(t)) for t in table], np.uint16)   # 1e30 -> +Inf
+    got_f = np.array([O.rope_freq(1e6, i, 512, 1, table16) for i in range(256)], np.float32)
+    assert np.array_equal(got_f[64:], inv_f[64:]) and np.all(inv_f[64:] == 0)
+    assert np.max(np.abs(got_f.view(np.int32) - inv_f.view(np.int32))) <= 1
+    # a plausible mistake: exponent i/hd instead of 2i/hd fails the check
+    wrong = np.array([1.0 / 1e4 ** (i / 256) for i in range(128)], np.float32)
+    assert not np.allclose(wrong, inv_s, rtol=1e-3)
+
+
+def test_rope_rotation_against_transformers_module():
+    """The whole per-head norm + RoPE at non-zero positions against
+    transformers: its rotary module's cos/sin for each layer type fed to its
+    apply_rotary_pos_emb, on the oracle's own normalised vector. torch forms
+    each frequency with an f32 pow, which differs from the oracle's by at
+    most 1 ulp (checked above); pairs whose frequencies are bit-equal are
+    held to 1e-5, the others to the angle difference position * |df| that
+    one ulp makes."""
+    import torch
+    from transformers.models.gemma4.modeling_gemma4 import apply_rotary_pos_emb
+
+    rot, inv_s, inv_f = _tf_inv_freq()
+    rng = np.random.default_rng(19)
+    for layer_type, hd, theta, div, inv in [("sliding_attention", 256, 1e4, 0, inv_s),
+                                            ("full_attention", 512, 1e6, 1, inv_f)]:
+        half = hd // 2
+        table = np.where(np.arange(half) < 64, 1.0, np.inf).astype(np.float16).view(np.uint16)
+        f = np.array([O.rope_freq(theta, i, hd, div, table) for i in range(half)], np.float32)
+        df = np.abs(f.astype(np.float64) - inv.astype(np.float64))
+        for pos in (1, 14, 511, 4095, 32767):
+            x = rng.standard_normal((8, hd)).astype(np.float32)
+            w = (rng.standard_normal(hd) * 0.1 + 1).astype(np.float16)
+            got = O.fused_per_head_norm_rope(x.reshape(-1), w.view(np.uint16), 8, hd, 1e-6, pos, theta, div,
+                                             table).reshape(8, hd)
+            xn = np.stack([O.rms_norm(x[h], w.view(np.uint16), 1e-6) for h in range(8)]).astype(np.float64)
+            with torch.no_grad():
+                cos, sin = rot(torch.zeros(1, 1, hd), torch.tensor([[pos]]), layer_type=layer_type)
+                want = apply_rotary_pos_emb(torch.from_numpy(xn)[None], cos.double(), sin.double(),
+                                            unsqueeze_dim=1)[0].numpy().reshape(8, hd)
+            assert cos.shape[-1] == hd
+            pair_mag = np.sqrt(xn[:, :half] ** 2 + xn[:, half:] ** 2)
+            tol = np.tile(1e-5 * pair_mag + 3e-6 + 1.01 * pos * df * pair_mag, (1, 2))
+            err = np.abs(got - want)
+            assert np.all(err <= tol), (layer_type, pos, float(np.max(err - tol)))
+            eq = np.tile(df == 0, 2)
+            assert np.allclose(got[:, eq], want[:, eq], rtol=1e-5, atol=3e-6), (layer_type, pos)
 
 
 def test_rope_closed_forms():
