@@ -23,7 +23,16 @@ struct g4_ctx {
   // so that no entry point allocates. Calls use it in stream order.
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
+  // Device address, on this context's device, of the static partials array
+  // of g4_attnDecode_noalloc (k_attn.hip), looked up once at g4_init; null
+  // (with the lookup's status in noalloc_status) when the lookup failed.
+  void* noalloc_scratch = nullptr;
+  int noalloc_status = 0;
 };
+
+// Looks up the device address of g4_attnDecode_noalloc's static partials
+// array on the current device (k_attn.hip); called by g4_init.
+void g4_internal_noalloc_init(g4_ctx* ctx);
 
 // Returns the context scratch buffer if it holds `bytes`.
 int g4_internal_scratch(g4_ctx* ctx, size_t bytes, void** out);

@@ -115,6 +115,7 @@ int g4_init(int device, g4_ctx** out) {
     delete ctx;
     return g4::hip_fail(nullptr, e, "hipMalloc(scratch)");
   }
+  g4_internal_noalloc_init(ctx);  // a failed lookup only disables g4_attnDecode_noalloc
   *out = ctx;
   return G4_OK;
 }

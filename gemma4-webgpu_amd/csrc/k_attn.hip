@@ -1747,7 +1747,27 @@ int paged_setup(const char* fn, const uint16_t* k_pool, const uint16_t* v_pool, 
   return G4_OK;
 }
 
+// Partials of g4_attnDecode_noalloc: a file-scope device array instead of a
+// caller workspace, for callers that cannot allocate (code under graph
+// capture, serving loops that forbid hipMalloc). Each GPU the library runs
+// on holds its own copy for the life of the process. Host code never passes
+// the array's name to a kernel (on the host it is a stand-in, not a device
+// address): g4_init looks up the device address on its device and keeps it
+// in the context. Every split writes its partial before the merge launch
+// reads it, so nothing in the array has to start at zero; calls on one GPU
+// share the array, so calls that overlap (other streams) race.
+constexpr size_t kNoAllocScratchBytes = 16u << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
 }  // namespace
+
+void g4_internal_noalloc_init(g4_ctx* ctx) {
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  ctx->noalloc_status = (int)e;
+  ctx->noalloc_scratch = e == hipSuccess ? ptr : nullptr;
+  if (e != hipSuccess) (void)hipGetLastError();  // leave no sticky error for the next call
+}
 
 extern "C" {
 
@@ -1809,6 +1829,23 @@ int g4_attnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_cache, const ui
                   g4_attn_score_params p, void* workspace, size_t workspace_bytes) {
   G4_ENTER(ctx);
   return dense_decode(ctx, __func__, q, k_cache, v_cache, output, p, workspace, workspace_bytes, nullptr);
+}
+
+int g4_attnDecode_noalloc(g4_ctx* ctx, const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                          float* output, g4_attn_score_params p) {
+  G4_ENTER(ctx);
+  if (!ctx->noalloc_scratch)
+    return g4::set_error(G4_ERR_HIP, "g4_attnDecode_noalloc: no device address for the static scratch (%s)",
+                         hipGetErrorString((hipError_t)ctx->noalloc_status));
+  size_t need = 0;
+  const int rc = g4_attnDecode_workspace_size(p, &need);
+  if (rc) return rc;
+  G4_REQUIRE(need <= kNoAllocScratchBytes,
+             "g4_attnDecode_noalloc: this shape needs %zu bytes of partials, more than the %zu-byte static "
+             "scratch (use g4_attnDecode with a workspace)",
+             need, kNoAllocScratchBytes);
+  return dense_decode(ctx, __func__, q, k_cache, v_cache, output, p, ctx->noalloc_scratch, kNoAllocScratchBytes,
+                      nullptr);
 }
 
 int g4_attnDecode_dev(g4_ctx* ctx, const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* output,

@@ -153,6 +153,7 @@ SIGNATURES = {
     "g4_attnDecode_workspace_size": (_I, [AttnScoreParams, ctypes.POINTER(_SZ)]),
     "g4_attnDecode": (_I, [_P, _P, _P, _P, _P, AttnScoreParams, _P, _SZ]),
     "g4_attnDecode_dev": (_I, [_P, _P, _P, _P, _P, AttnScoreParams, _P, _SZ, _P]),
+    "g4_attnDecode_noalloc": (_I, [_P, _P, _P, _P, _P, AttnScoreParams]),
     "g4_attnDecodeFused_workspace_size": (_I, [AttnFusedParams, ctypes.POINTER(_SZ)]),
     "g4_attnDecodeFused": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, AttnFusedParams, _P, _SZ, _P]),
     "g4_attnDecodeFusedWarm": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, AttnFusedParams, _P, _SZ, _P,

@@ -343,6 +343,13 @@ class Context:
             self.sync()
             ws.free()
 
+    def attnDecodeNoAlloc(self, q: Ptr, k_cache: Ptr, v_cache: Ptr, out: Ptr, nqh: int, nkh: int, hd: int,
+                          seq_len: int, scale: float = 1.0, window: int = 0) -> None:
+        """g4_attnDecode_noalloc: the partials in the library's static device
+        array; no workspace, nothing allocated."""
+        check(lib().g4_attnDecode_noalloc(self.h, _p(q), _p(k_cache), _p(v_cache), _p(out),
+                                          AttnScoreParams(nqh, nkh, hd, seq_len, scale, window)))
+
     @staticmethod
     def attn_fused_params(nqh, nkh, hd, max_seq_len, window=0, eps=1e-6, theta=1e4, apply_divisor=0,
                           scale=1.0) -> AttnFusedParams:

@@ -172,6 +172,16 @@ int g4_attnOutput_dev(g4_ctx* ctx, const float* probs, const uint16_t* v_cache, 
 int g4_attnDecode_workspace_size(g4_attn_score_params p, size_t* bytes);
 int g4_attnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                   float* output, g4_attn_score_params p, void* workspace, size_t workspace_bytes);
+/* g4_attnDecode without a workspace: the split-K partials go to a static
+ * 16 MiB device array of the library (each GPU holds one until the process
+ * ends), and the call allocates nothing. No counterpart in the reference; it
+ * is for callers that cannot allocate (code under graph capture, serving
+ * loops that forbid hipMalloc). Shapes whose g4_attnDecode_workspace_size
+ * exceeds 16 MiB (e.g. head_dim 512 beyond 32768 positions) return
+ * G4_ERR_INVALID. All calls on one GPU share the array: calls that overlap
+ * (on other streams) race. */
+int g4_attnDecode_noalloc(g4_ctx* ctx, const float* q, const uint16_t* k_cache,
+                          const uint16_t* v_cache, float* output, g4_attn_score_params p);
 /* seq_len = *position_dev + 1 read on the device; p.seq_len is the maximum
  * the workspace was sized for. */
 int g4_attnDecode_dev(g4_ctx* ctx, const float* q, const uint16_t* k_cache,
