@@ -255,7 +255,12 @@ void g4o_gelu_mul(const float* gate, const float* up, float* out, uint32_t n) {
     double t = k0 * x * (1.0 + k1 * x * x);
     if (t > 15.0) t = 15.0;
     if (t < -15.0) t = -15.0;
-    out[i] = (float)(0.5 * x * (1.0 + tanh(t)) * (double)up[i]);
+    /* The shader's tanh returns an f32 (shaders/gelu_mul.wgsl:14): carry
+     * it as that value (the f64 result rounded once), so that 1 + tanh(t)
+     * is exactly 0 where f32 tanh saturates at -1 (x below about -5.5), as
+     * in every f32 evaluation, rather than the ~1e-10 an f64 tanh leaves. */
+    const double th = (double)(float)tanh(t);
+    out[i] = (float)(0.5 * x * (1.0 + th) * (double)up[i]);
   }
 }
 

@@ -412,7 +412,8 @@ def np_rms_norm(x, w_f16, eps=1e-6):
 def np_gelu_mul(gate, up):
     x = np.asarray(gate, np.float64)
     t = np.clip(0.7978845608028654 * x * (1 + 0.044715 * x * x), -15, 15)
-    return (0.5 * x * (1 + np.tanh(t)) * np.asarray(up, np.float64)).astype(np.float32)
+    th = np.tanh(t).astype(np.float32).astype(np.float64)   # the shader's tanh is an f32 value
+    return (0.5 * x * (1 + th) * np.asarray(up, np.float64)).astype(np.float32)
 
 
 def rel_l2(a, b) -> float:

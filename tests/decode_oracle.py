@@ -6,6 +6,30 @@ import numpy as np
 import oracle as O
 
 
+def gelu_mul_f32(gate, up):
+    """shaders/gelu_mul.wgsl:10-16 evaluated in f32 operations in the shader's
+    order (tanh correctly rounded to f32): another faithful evaluation of the
+    reference, used to measure how sensitive a step is to the last bits of
+    the GELU (the oracle's gelu_mul forms the tanh argument in f64)."""
+    x = np.asarray(gate, np.float32)
+    f = np.float32
+    t = np.clip(f(0.7978845608028654) * x * (f(1.0) + f(0.044715) * x * x), f(-15.0), f(15.0))
+    th = np.tanh(t.astype(np.float64)).astype(np.float32)
+    return (f(0.5) * x * (f(1.0) + th) * np.asarray(up, np.float32)).astype(np.float32)
+
+
+def f16_toward_zero(x):
+    """f32 -> f16 bits rounded toward zero: one f16 ulp from round-to-nearest
+    wherever that rounded away from zero."""
+    x = np.asarray(x, np.float32)
+    with np.errstate(over="ignore"):
+        h = x.astype(np.float16)
+    bits = h.view(np.uint16).copy()
+    away = np.abs(h.astype(np.float32)) > np.abs(x)
+    bits[away] -= 1
+    return bits
+
+
 class HostModel:
     def __init__(self, dec):
         self.s = s = dec.s
@@ -19,10 +43,13 @@ class HostModel:
         self.final_norm = dec.final_norm.download(u16)
         self.lm_head = dec.lm_head.download(u8) if dec.lm_head is not None else None
 
-    def step(self, hidden, kcs, vcs, pos):
+    def step(self, hidden, kcs, vcs, pos, gelu=O.gelu_mul, row_toward_zero=False):
         """Decode position `pos`: kcs/vcs are this sequence's dense f16 caches
         (one per layer, >= pos + 1 rows), updated in place. Returns the new
-        hidden state and the softcapped logits (None without an LM head)."""
+        hidden state and the softcapped logits (None without an LM head).
+        `row_toward_zero` stores the new K/V rows rounded toward zero instead
+        of to nearest (a one-ulp change of the f16 cache, to measure how much
+        the step depends on the cache's resolution)."""
         s, x = self.s, hidden.copy()
         for il, W in enumerate(self.layers):
             glob = s.is_global(il)
@@ -38,13 +65,17 @@ class HostModel:
             k = O.fused_per_head_norm_rope(k, W["k_norm"], s.n_kv_heads, s.head_dim, s.eps, pos, theta, int(glob),
                                            self.table)
             O.kv_cache_store_f16(k, v, kcs[il], vcs[il], s.n_kv_heads, s.head_dim, pos)
+            if row_toward_zero:
+                row = slice(pos * s.kv_dim, (pos + 1) * s.kv_dim)
+                kcs[il][row] = f16_toward_zero(k)
+                vcs[il][row] = f16_toward_zero(v)
             a = O.attention(q, kcs[il], vcs[il], s.n_q_heads, s.n_kv_heads, s.head_dim, pos + 1, 1.0, window)
             o = O.matmul(a, W["wo"], s.hidden, s.q_dim, "q4k")
             h = O.fused_norm_add(o, W["post_attn_norm"], x, s.eps)
             n2 = O.rms_norm(h, W["pre_ffn_norm"], s.eps)
             g = O.matmul(n2, W["wgate"], s.ffn, s.hidden, "q4k")
             u = O.matmul(n2, W["wup"], s.ffn, s.hidden, "q4k")
-            dn = O.matmul(O.gelu_mul(g, u), W["wdown"], s.hidden, s.ffn, "q6k")
+            dn = O.matmul(gelu(g, u), W["wdown"], s.hidden, s.ffn, "q6k")
             x = O.fused_norm_add(dn, W["post_ffn_norm"], h, s.eps)
         if self.lm_head is None:
             return x, None

@@ -6,6 +6,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+import synth
 from gpu_util import assert_close
 
 pytestmark = pytest.mark.gpu
@@ -13,10 +14,14 @@ pytestmark = pytest.mark.gpu
 
 def _weights(wtype, seed, M, N):
     nb = M * N // 256
+    if wtype == "q6k_wide":
+        return synth.q6k_wide(seed, nb)
+    if wtype == "q4k_centered":
+        return synth.q4k_centered(seed, nb)
     return O.gen_q4k(seed, nb) if wtype == "q4k" else O.gen_q6k(seed, nb)
 
 
-@pytest.mark.parametrize("wtype,M,N,batch", [
+@pytest.mark.parametrize("gen,M,N,batch", [
     ("q4k", 2048, 1536, 32),   # E2B q projection at B=32
     ("q4k", 1536, 2048, 16),   # o projection
     ("q4k", 6144, 1536, 64),   # gate/up at B=64
@@ -24,9 +29,16 @@ def _weights(wtype, seed, M, N):
     ("q6k", 1536, 6144, 32),   # down projection
     ("q6k", 1000, 1536, 33),   # LM-head-like K, ragged
     ("q6k", 777, 12288, 16),   # wide FFN down, rows not a multiple of 16
+    # real GGUF scales span the int8 range: |sc * (q - 32)| up to 4096, where
+    # the f16 weight operand rounds once (2^-12 relative at most)
+    ("q6k_wide", 1536, 6144, 32),
+    ("q6k_wide", 1000, 1536, 33),
+    ("q6k_wide", 1536, 6144, 64),
+    ("q4k_centered", 2048, 1536, 32),
 ])
-def test_batched_matmul_matches_oracle(ctx, wtype, M, N, batch):
-    W = _weights(wtype, 60, M, N)
+def test_batched_matmul_matches_oracle(ctx, gen, M, N, batch):
+    wtype = gen[:3]
+    W = _weights(gen, 60, M, N)
     X = O.gen_normal_f32(61, batch * N, 0.0, 1.5).reshape(batch, N)
     X[batch // 2] *= 40.0  # one vector with a very different scale
     dY = ctx.empty(batch * M, np.float32)

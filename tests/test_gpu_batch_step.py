@@ -5,18 +5,25 @@
   two merge chunks and sum squares in different orders), within rel-L2 1e-3
   of the oracle, K/V rows appended only where the table says.
 * The whole step: every sequence against the oracle's single-sequence step on
-  its own dense caches. Attention at scale 1.0 over N(0,1) keys has scores
-  with a standard deviation near 16, so where two positions' scores are
-  within a fraction of a unit the softmax weights amplify the ~1e-5 relative
-  difference of the int8-activation q/k/v projections roughly 100-fold; the
-  composed step is therefore held to rel-L2 1e-2 and cosine 0.9999 (each
-  kernel meets 1e-3 on its own inputs in the stage-wise tests).
+  its own dense caches, at rel-L2 1e-3 / cosine 0.9999 (or, for the rare
+  sequence whose step is that sensitive to one f16 ulp of its newest K/V
+  row, the oracle's own movement under such a change): the 18 edge lengths
+  above, and the ragged serving shape of 32 sequences with lengths drawn from
+  U(128, 8192), once with the benchmark's weight generator and once with
+  real-model-like weights (zero-mean Q4_K, Q6_K scales over the whole int8
+  range, which the matrix-core weight operand rounds once above 2048).
+  With the benchmark's generator the Q4_K weights have a mean near +0.35, so
+  for sequences whose normalised FFN input sums negative every GELU input is
+  far below -5.5 and f32 tanh saturates: the product is exactly 0 (as in the
+  reference's f32 shader and the oracle, which carries tanh as an f32 value),
+  and the post-FFN RMSNorm then sees an all-zero vector.
 * HIP-graph replays equal eager steps bit for bit."""
 import numpy as np
 import pytest
 
 import oracle as O
-from decode_oracle import HostModel
+import synth
+from decode_oracle import HostModel, gelu_mul_f32
 from g4hip.decoder import BatchDecoder, E2BShape
 from gpu_util import assert_close, bits_equal
 
@@ -60,7 +67,12 @@ def _dense(d, pool, seq, n):
     return out.reshape(-1)
 
 
-STEP_REL = 1e-2
+STEP_REL = 1e-3
+# A sequence whose oracle step itself moves by more than STEP_REL when its
+# newest f16 K/V row is rounded toward zero instead of to nearest (one ulp of
+# the cache; a k that differs in its last f32 bits flips such ulps) is held
+# to that movement; likewise, times GELU_MARGIN, for the GELU's all-f32 form.
+GELU_MARGIN = 4.0
 
 
 def test_paged_attention_block_matches_dense_and_oracle(ctx, bdec):
@@ -173,7 +185,27 @@ def test_prologue_then_paged_decode_matches_fused_and_oracle(ctx, bdec):
 
 
 def test_batch_step_matches_oracle_per_sequence(ctx, bdec):
-    d, s, B = bdec, bdec.s, bdec.B
+    _step_vs_oracle(ctx, bdec, LENS)
+
+
+@pytest.mark.parametrize("weights", ["benchmark", "realistic"])
+def test_batch_step_serving_shape(ctx, weights):
+    """32 sequences, lengths ~ U(128, 8192) (seeded), a local and a global
+    layer, 16384-token vocabulary."""
+    lens = np.random.default_rng(2024).integers(128, 8193, 32)
+    shape = E2BShape(n_layers=2, global_layers=(1,), vocab=16384)
+    d = BatchDecoder(ctx, lens, shape, seed=17, reserve=4)
+    if weights == "realistic":
+        synth.make_realistic(d)
+    d.fill_kv(seed=18)
+    ctx.sync()
+    print(f"[batch step] B=32 {weights}: mean length {lens.mean():.0f}, {d.num_pages} pages", flush=True)
+    _step_vs_oracle(ctx, d, [int(x) for x in lens])
+    del d
+
+
+def _step_vs_oracle(ctx, d, LENS):
+    s, B = d.s, d.B
     hm = HostModel(d)
     hidden0 = d.hidden.download(np.float32).reshape(B, s.hidden)
     pools0 = _pools(d)
@@ -187,19 +219,38 @@ def test_batch_step_matches_oracle_per_sequence(ctx, bdec):
     TOK = d.tokens.download(np.uint32)
     pools1 = _pools(d)
     kv = s.kv_dim
+    refs, tol = [], []
     for b, L in enumerate(LENS):
         kcs = [_dense(d, k, b, L) for k, _ in pools0]
         vcs = [_dense(d, v, b, L) for _, v in pools0]
         x, logits = hm.step(hidden0[b], kcs, vcs, L)
-        assert_close(H[b], x, rel=STEP_REL, what=f"hidden seq {b} len {L}")
-        assert_close(LG[b], logits, rel=STEP_REL, what=f"logits seq {b} len {L}")
+        refs.append((x, logits, kcs, vcs))
+        # the step's own dependence on the f16 cache's resolution: the oracle
+        # against itself with its new K/V rows one ulp off (rounded toward
+        # zero), and on the last bits of the GELU (the shader's all-f32 form)
+        kz, vz = [_dense(d, k, b, L) for k, _ in pools0], [_dense(d, v, b, L) for _, v in pools0]
+        xz, lgz = hm.step(hidden0[b], kz, vz, L, row_toward_zero=True)
+        x32, lg32 = hm.step(hidden0[b], [k.copy() for k in kcs], [v.copy() for v in vcs], L, gelu=gelu_mul_f32)
+        tol.append(max(STEP_REL, O.rel_l2(xz, x), O.rel_l2(lgz, logits),
+                       GELU_MARGIN * O.rel_l2(x32, x), GELU_MARGIN * O.rel_l2(lg32, logits)))
+    rh = [O.rel_l2(H[b], r[0]) for b, r in enumerate(refs)]
+    rl = [O.rel_l2(LG[b], r[1]) for b, r in enumerate(refs)]
+    print(f"[batch step] B={B}: max rel-L2 hidden {max(rh):.2e} logits {max(rl):.2e}, "
+          f"median hidden {np.median(rh):.2e}; sequences whose own sensitivity sets the bound "
+          f"(seq, len, bound, error): "
+          f"{[(b, LENS[b], round(t, 5), round(rh[b], 5)) for b, t in enumerate(tol) if t > STEP_REL]}", flush=True)
+    for b, L in enumerate(LENS):
+        x, logits, kcs, vcs = refs[b]
+        assert_close(H[b], x, rel=tol[b], what=f"hidden seq {b} len {L}")
+        assert_close(LG[b], logits, rel=tol[b], what=f"logits seq {b} len {L}")
         assert TOK[b] == O.argmax(LG[b]), b
         r = d.pool_row(b, L)
         for il in range(s.n_layers):
             for got, ref, nm in ((pools1[il][0], kcs[il], "k"), (pools1[il][1], vcs[il], "v")):
                 row = got.reshape(-1, kv)[r].view(np.float16).astype(np.float32)
                 want = ref.reshape(-1, kv)[L].view(np.float16).astype(np.float32)
-                assert_close(row, want, rel=STEP_REL, what=f"{nm} row seq {b} layer {il}")
+                # layer 0's rows depend on the input only; later rows on the layers before
+                assert_close(row, want, rel=STEP_REL if il == 0 else tol[b], what=f"{nm} row seq {b} layer {il}")
     # nothing but the appended rows changed in the pools
     written = sorted(d.pool_row(b, L) for b, L in enumerate(LENS))
     for il in range(s.n_layers):

@@ -60,6 +60,7 @@ def test_step_reference_and_fused_vs_oracle(ctx, dec):
 
     dec.step_reference(POS)
     ctx.sync()
+    print(f"[step] per-key: hidden rel-L2 {O.rel_l2(host(dec.hidden, np.float32), x_ref):.2e}", flush=True)
     assert_close(host(dec.hidden, np.float32), x_ref, what="per-key hidden")
     lg = host(dec.logits, np.float32)
     assert_close(lg, logits_ref, what="per-key logits")
@@ -71,6 +72,7 @@ def test_step_reference_and_fused_vs_oracle(ctx, dec):
     dec.step_fused()
     ctx.sync()
     assert int(host(dec.pos, np.uint32)[0]) == POS + 1
+    print(f"[step] fused: hidden rel-L2 {O.rel_l2(host(dec.hidden, np.float32), x_ref):.2e}", flush=True)
     assert_close(host(dec.hidden, np.float32), x_ref, what="fused hidden")
     lg = host(dec.logits, np.float32)
     assert_close(lg, logits_ref, what="fused logits")

@@ -308,7 +308,16 @@ def test_gelu_against_fixture_and_torch(fx):
     # torch's tanh-approximate GELU (a library routine) on a wide range
     x = np.linspace(-40, 40, 20001).astype(np.float32)
     ref = torch.nn.functional.gelu(torch.from_numpy(x).double(), approximate="tanh").numpy()
-    assert np.allclose(O.gelu_mul(x, np.ones_like(x)), ref, rtol=1e-6, atol=1e-6)
+    got = O.gelu_mul(x, np.ones_like(x))
+    assert np.allclose(got, ref, rtol=1e-6, atol=1e-6)
+    # and torch's float32 evaluation where tanh saturates: the shader's tanh
+    # is an f32, so 1 + tanh(t) is 0 below x ~ -5.5 (f64 would leave ~1e-10)
+    ref32 = torch.nn.functional.gelu(torch.from_numpy(x), approximate="tanh").numpy()
+    sat = x < -5.5
+    assert np.all(got[sat] == 0) and np.all(ref32[sat] == 0)
+    near = (x > -5.5) & (x < -3)   # 1 + tanh(t) here is a multiple of 2^-24: within one such step
+    assert np.all(np.abs(got[near] - ref32[near]) <= np.abs(x[near]) * 2.0 ** -24 * 1.01)
+    assert np.array_equal(O.np_gelu_mul(x, np.ones_like(x)), got)
 
 
 def test_rms_norm_against_transformers():
