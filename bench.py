@@ -167,6 +167,39 @@ def gemv_cfg0(ctx, copies=101, rounds=5):
             "frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, "copies": copies}
 
 
+def stream_floor(ctx, nbytes=5339136, copies=101, rounds=5, wg_list=(256, 648, 1024, 2048)):
+    """The pure-streaming floor of one launch that reads `nbytes` (config 0's
+    5.34 MB by default) from HBM: g4_streamRead over `copies` rotated buffers
+    (> 2x the 256 MB last-level cache), timed like the config-0 GEMV."""
+    nb = (nbytes + 255) // 256 * 256
+    buf = ctx.alloc(nb * copies)  # contents are irrelevant to a read-only stream
+    sink = ctx.empty(65535, np.uint32)
+    ptrs = [buf.ptr + i * nb for i in range(copies)]
+    out = {}
+    for pol, name in ((1, "nontemporal"), (0, "plain")):
+        for nw in wg_list:
+            def one(i=0, pol=pol, nw=nw):
+                ctx.streamRead(ptrs[i % copies], nb, pol, nw, sink)
+            ms = time_launches(ctx, one, copies * rounds)
+            out[f"{name}_wg{nw}"] = {"us": round(ms * 1e3, 3), "gbps": round(nb / (ms * 1e-3) / 1e9, 1)}
+    buf.free()
+    best = min(out.values(), key=lambda v: v["us"])
+    return {"bytes": nb, "copies": copies, "launches": out, "best_us": best["us"], "best_gbps": best["gbps"],
+            "best_frac": round(best["gbps"] / HBM_PEAK_GBPS, 4)}
+
+
+def calibration_reads(ctx, nbytes=256 << 20):
+    """One 256 MiB read per cache policy (the streaming probe), for the HBM
+    byte counters' calibration under the profiler."""
+    buf = ctx.zeros(nbytes, np.uint8)
+    sink = ctx.empty(4096, np.uint32)
+    for pol in (0, 1, 2):
+        ctx.streamRead(buf, nbytes, pol, 4096, sink)
+    ctx.sync()
+    buf.free()
+    return {"bytes": nbytes, "policies": ["plain", "nontemporal", "device_scope"], "workgroups": 4096}
+
+
 def graph_us(ctx, body, reps):
     """Average us of one replay of a graph holding body()'s launches."""
     ctx.graph_begin()
@@ -362,13 +395,104 @@ def batch_decode(ctx, B, steps, warmup, seed=0, census=False):
     return res
 
 
-def cpu_baseline(tokens=5):
-    """Times the CPU oracle (plain C, 1 thread, f64 accumulation) on `tokens`
-    whole decode steps of the same workload: 35 E2B-shaped layers at context
-    START_POS + 1 (local layers windowed, every fifth global) plus the full
-    262144-row Q6_K LM head, softcap and argmax. One set of layer weights is
-    reused for all layers (the cost does not depend on the values); weight
-    generation is outside the timed region."""
+def _cpu_threads():
+    """Host threads this process may use (the box's CPU share, at most 16)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def node_q4k_gemv(seconds=4.0):
+    """Config 0 on the host as a TypeScript host would run it: the builder's
+    ES2019 restatement of GGUFParser.dequantizeQ4_K + the f32 dot of
+    matmul_quant (oracle/q4k_dot.js) under Node, one core, with the dequant
+    inside the timed loop and with the matrix pre-dequantized. Its output is
+    checked against the C oracle. None when node is absent."""
+    import shutil
+    import subprocess
+    import tempfile
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    node = shutil.which("node")
+    if node is None:
+        return None
+    M, K = 6144, 1536
+    W = O.gen_q4k(12345, M * K // 256)
+    x = O.gen_normal_f32(1, K)
+    with tempfile.TemporaryDirectory() as td:
+        fin, fout = os.path.join(td, "in.bin"), os.path.join(td, "out.bin")
+        with open(fin, "wb") as f:
+            f.write(np.array([M, K], np.uint32).tobytes())
+            f.write(W.tobytes())
+            f.write(x.tobytes())
+        r = subprocess.run([node, os.path.join(ROOT, "oracle", "q4k_dot.js"), fin, fout, str(seconds)],
+                           capture_output=True, text=True, check=True, timeout=20 * seconds + 60)
+        res = json.loads(r.stdout.strip().splitlines()[-1])
+        y = np.fromfile(fout, np.float32)
+    alg = M * K // 256 * 144 + K * 4 + M * 4
+    return {"shape": [M, K], "node": res["node"], "cores": 1,
+            "ms_dequant_in_loop": round(res["ms_dequant_dot"], 3),
+            "gbps_dequant_in_loop": round(alg / (res["ms_dequant_dot"] * 1e-3) / 1e9, 4),
+            "ms_predequantized_f32": round(res["ms_dot_predequantized"], 3),
+            "gemvs_timed": res["reps_dequant"] + res["reps_dot"],
+            "rel_l2_vs_oracle": float(O.rel_l2(y, O.matmul(x, W, M, K, "q4k")))}
+
+
+def torch_attention_cfg3(threads, seconds=0.5):
+    """Config 3 on the host: the builder's fp32 torch attention,
+    softmax(q k^T) v at scale 1.0 with the sliding-window mask, 8 query heads
+    over 1 KV head of dim 256, K/V held in f32 (the reference's cache type)."""
+    import torch
+
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(3)
+    res = {}
+    try:
+        for L in (512, 4096, 32768):
+            K = torch.randn(L, 256, generator=g)
+            V = torch.randn(L, 256, generator=g)
+            q = torch.randn(8, 256, generator=g)
+            for window in (0, 512):
+                if window and L <= window:
+                    continue
+                lo = L - window if window else 0
+
+                def attn():
+                    s = q @ K[lo:].T
+                    return torch.softmax(s, dim=-1) @ V[lo:]
+                attn()
+                n, t0 = 0, time.perf_counter()
+                while time.perf_counter() - t0 < seconds:
+                    attn()
+                    n += 1
+                us = (time.perf_counter() - t0) / n * 1e6
+                l_eff = L - lo
+                res[f"ctx{L}_{'window512' if window else 'global'}"] = {
+                    "us": round(us, 1), "gbps_f16_equiv": round(l_eff * 1024 / (us * 1e-6) / 1e9, 3)}
+    finally:
+        torch.set_num_threads(prev)
+    return res
+
+
+def oracle_step_rate(tokens=1):
+    """The C oracle (plain C, 1 thread, f64 accumulation) on whole decode
+    steps of the benchmark workload: 35 E2B-shaped layers at context
+    START_POS + 1 plus the 262144-row Q6_K LM head, softcap and argmax."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
@@ -406,10 +530,43 @@ def cpu_baseline(tokens=5):
         lg = O.logit_softcap(O.matmul(O.rms_norm(x, nw), Wh, s.vocab, H, "q6k"))
         O.argmax(lg)
     t = time.perf_counter() - t0
-    return {"value": tokens / t, "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": (f"CPU oracle (plain C, 1 thread, f64 accumulation): {tokens} whole decode steps "
-                       f"(35 E2B-shaped layers at context {L} + full 262144-row Q6_K LM head + softcap "
-                       f"+ argmax), {t:.1f} s of CPU work")}
+    return {"tok_s": round(tokens / t, 4), "tokens": tokens, "seconds": round(t, 2), "cores": 1}
+
+
+def cpu_baseline():
+    """The host-side baseline: config 0 (Q4_K dequant-dot) in Node on one
+    core, config 3 (fp32 torch attention) on one core and on the process's
+    host threads, and the C oracle's own step rate. `value` scales the
+    one-core figures to the headline unit: one token at batch 1 is 35 layers
+    of 22.34 MB of K-quant weights (dequant-dot at the Node rate; Q6_K bytes
+    priced like Q4_K) with the attention of the benchmark context (28 layers
+    over 512 positions, 7 over 513, torch on one core), plus the 330.3 MB LM
+    head."""
+    t0 = time.perf_counter()
+    g0 = node_q4k_gemv()
+    threads = _cpu_threads()
+    attn1 = torch_attention_cfg3(1)
+    attnT = torch_attention_cfg3(threads)
+    orc = oracle_step_rate(1)
+    s = E2BShape()
+    per_token_us = None
+    if g0 is not None:
+        bps = g0["gbps_dequant_in_loop"] * 1e9
+        w_us = (s.layer_weight_bytes() * s.n_layers + s.lm_head_bytes()) / bps * 1e6
+        n_glob = len(s.global_layers)
+        a_us = (s.n_layers - n_glob) * attn1["ctx4096_window512"]["us"] + n_glob * attn1["ctx512_global"]["us"]
+        per_token_us = w_us + a_us
+    value = round(1e6 / per_token_us, 5) if per_token_us else orc["tok_s"]
+    return {"value": value, "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": (f"config 0 ({g0['gemvs_timed'] if g0 else 0} Q4_K GEMVs 6144x1536, builder's ES2019 "
+                       f"dequantizeQ4_K + f32 dot under Node {g0['node'] if g0 else '(absent)'}, 1 core) and "
+                       f"config 3 (fp32 torch attention at 512/4096/32768 positions) scaled to one E2B token; "
+                       f"also the C oracle on {orc['tokens']} whole step(s); {time.perf_counter() - t0:.1f} s of "
+                       f"CPU work on {_cpu_model()}") if g0 else "node absent: C oracle whole steps only",
+            "q4k_gemv_config0_node": g0,
+            "attention_config3_torch": {"threads_1": attn1, f"threads_{threads}": attnT, "cpu": _cpu_model(),
+                                        "host_threads": threads},
+            "oracle_c_step": orc}
 
 
 def main():
@@ -419,7 +576,6 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--census-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=5)
     ap.add_argument("--no-warm", action="store_true",
                     help="attention launches do not read the next matvecs' weights into L2")
     ap.add_argument("--eager", action="store_true",
@@ -429,6 +585,11 @@ def main():
     ap.add_argument("--census-only", action="store_true",
                     help="time only the per-kernel census of the B=1 step (the launches a profiler should see)")
     ap.add_argument("--no-gemv0", action="store_true")
+    ap.add_argument("--gemv0-only", action="store_true",
+                    help="time only the config-0 GEMV over its rotated copies and the pure-streaming floor "
+                         "(the launches a profiler should see for config 0)")
+    ap.add_argument("--calib-only", action="store_true",
+                    help="one 256 MiB streaming read per cache policy, for the HBM counters' calibration")
     ap.add_argument("--batch-steps", type=int, default=30)
     ap.add_argument("--batch-warmup", type=int, default=5)
     ap.add_argument("--batch-sweep", default="1,8,32,64",
@@ -445,6 +606,13 @@ def main():
     ctx = g4hip.Context(0)
     info = ctx.info()
     log(f"device {info}")
+    if args.gemv0_only:
+        g0, fl = gemv_cfg0(ctx), stream_floor(ctx)
+        print(json.dumps({"q4k_gemv_config0": g0, "stream_floor": fl}), flush=True)
+        return
+    if args.calib_only:
+        print(json.dumps({"calibration": calibration_reads(ctx)}), flush=True)
+        return
     s = E2BShape()
     max_seq = START_POS + args.warmup + args.steps + 64
     max_seq = (max_seq + 255) // 256 * 256
@@ -507,6 +675,8 @@ def main():
                 "bytes_per_launch": bytes_launch, "us_per_launch": round(us_launch, 3)}
 
     g0 = {} if args.no_gemv0 else gemv_cfg0(ctx)
+    if g0:
+        g0["stream_floor"] = stream_floor(ctx, wg_list=(648, 2048))
     log(f"config-0 Q4_K GEMV: {g0}")
     attn3 = attention_cfg3(ctx)
     log(f"decode attention: {attn3}")
@@ -515,7 +685,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(tokens=args.cpu_tokens)
+        cpu = cpu_baseline()
         log(f"cpu baseline: {cpu}")
 
     line = {

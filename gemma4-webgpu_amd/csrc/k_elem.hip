@@ -304,6 +304,44 @@ __global__ __launch_bounds__(NT) void fill_normal_kernel(float* dst32, uint16_t*
   else dst16[i] = g4d::f32_to_f16_bits(v);
 }
 
+// ---------------------------------------------------------------------------
+// streaming-read probe (measurement export g4_streamRead): one pass over a
+// buffer with 16-byte loads, four in flight per thread, under one cache
+// policy; each workgroup writes the xor of what it read, so no load is dead.
+// ---------------------------------------------------------------------------
+typedef uint32_t sr_u4 __attribute__((ext_vector_type(4)));
+
+template <int POL>
+__global__ __launch_bounds__(NT) void stream_read_kernel(const uint8_t* src, uint32_t n16, uint32_t* sink) {
+  __shared__ uint32_t red[NT / 64];
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, (int)(n16 * 16u), 0x00020000);
+  const uint32_t stride = gridDim.x * NT;
+  uint32_t acc = 0;
+  uint32_t i = blockIdx.x * NT + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    sr_u4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, (i + u * stride) * 16u, 0, POL);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+  }
+  for (; i < n16; i += stride) {
+    const sr_u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, i * 16u, 0, POL);
+    acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t a = 0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) a ^= red[w];
+    sink[blockIdx.x] = a;
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -571,6 +609,24 @@ int g4_fill_normal_f32(g4_ctx* ctx, float* dst, uint64_t n, uint64_t seed, float
   hipLaunchKernelGGL(fill_normal_kernel, dim3(ceil_div(n, NT)), dim3(NT), 0, ctx->stream, dst, (uint16_t*)nullptr, n,
                      seed, mean, std);
   G4_LAUNCHED(ctx, "fill_normal_f32");
+  return G4_OK;
+}
+
+int g4_streamRead(g4_ctx* ctx, const void* src, uint64_t bytes, int policy, uint32_t nwgs, uint32_t* sink) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(src && sink, "g4_streamRead: null buffer");
+  G4_REQUIRE(((uintptr_t)src & 15) == 0 && bytes % 16 == 0 && bytes > 0 && bytes < (1ull << 32),
+             "g4_streamRead: src 16-byte aligned, bytes a multiple of 16 below 4 GiB");
+  G4_REQUIRE(nwgs >= 1 && nwgs <= 65535, "g4_streamRead: 1..65535 workgroups");
+  G4_REQUIRE(policy >= 0 && policy <= 2, "g4_streamRead: policy 0 (plain), 1 (non-temporal) or 2 (device scope)");
+  const uint32_t n16 = (uint32_t)(bytes / 16);
+  if (policy == 0)
+    hipLaunchKernelGGL(stream_read_kernel<0>, dim3(nwgs), dim3(NT), 0, ctx->stream, (const uint8_t*)src, n16, sink);
+  else if (policy == 1)
+    hipLaunchKernelGGL(stream_read_kernel<2>, dim3(nwgs), dim3(NT), 0, ctx->stream, (const uint8_t*)src, n16, sink);
+  else
+    hipLaunchKernelGGL(stream_read_kernel<16>, dim3(nwgs), dim3(NT), 0, ctx->stream, (const uint8_t*)src, n16, sink);
+  G4_LAUNCHED(ctx, "stream_read");
   return G4_OK;
 }
 

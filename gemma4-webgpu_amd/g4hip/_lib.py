@@ -204,6 +204,7 @@ SIGNATURES = {
     "g4_dequant_q4k": (_I, [_P, _P, _U64, _P]),
     "g4_dequant_q6k": (_I, [_P, _P, _U64, _P]),
     "g4_dequantPath": (_I, [_P, _I, _I, _P, _U64, _P]),
+    "g4_streamRead": (_I, [_P, _P, _U64, _I, _U32, _P]),
     "g4_splitmix64": (_U64, [_U64, _U64]),
     "g4_fill_q4k": (_I, [_P, _P, _U64, _U64]),
     "g4_fill_q6k": (_I, [_P, _P, _U64, _U64]),

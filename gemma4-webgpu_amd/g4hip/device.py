@@ -511,6 +511,11 @@ class Context:
         units, 1: LDS units, 2: matrix-core operands)."""
         check(lib().g4_dequantPath(self.h, {"q4k": 0, "q6k": 1}[wtype], path, _p(blocks), nblocks, _p(out)))
 
+    def streamRead(self, src: Ptr, nbytes: int, policy: int, nwgs: int, sink: Ptr) -> None:
+        """Measurement probe: one pass of 16-byte loads over nbytes (policy 0
+        plain, 1 non-temporal, 2 device scope)."""
+        check(lib().g4_streamRead(self.h, _p(src), nbytes, policy, nwgs, _p(sink)))
+
     def fill_q4k(self, dst: Ptr, nblocks: int, seed: int) -> None:
         check(lib().g4_fill_q4k(self.h, _p(dst), nblocks, seed))
 

@@ -525,6 +525,14 @@ int g4_dequant_q6k(g4_ctx* ctx, const void* blocks, uint64_t nblocks, float* out
  * Paths 0 and 1 are bit-exact with the reference's f32 values. */
 int g4_dequantPath(g4_ctx* ctx, int wtype, int path, const void* blocks, uint64_t nblocks, float* out);
 
+/* Measurement probe: reads bytes of src once with 16-byte loads (nwgs
+ * workgroups of 256 threads, 4 loads in flight per thread) under a cache
+ * policy (0 plain, 1 non-temporal as the one-matrix Q4_K matvec reads its
+ * weights, 2 device scope as the attention's partials are read) and writes
+ * one word per workgroup to sink[nwgs]. It times the pure-streaming floor of
+ * a launch and calibrates the HBM byte counters. */
+int g4_streamRead(g4_ctx* ctx, const void* src, uint64_t bytes, int policy, uint32_t nwgs, uint32_t* sink);
+
 /* Seeded synthetic inputs, generated on the device (counter-based SplitMix64;
  * block b of a stream draws words 32b.., element i of a normal stream words
  * 2i and 2i+1; Box-Muller in f64). */

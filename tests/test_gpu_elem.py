@@ -198,3 +198,17 @@ def test_embedding_lookup(ctx):
         assert not out.download(np.float32).any()
         with pytest.raises(Exception):
             ctx.embeddingLookup(d_tab, rows, out, H, rows)
+
+
+@pytest.mark.parametrize("policy", [0, 1, 2])
+def test_stream_read_probe_reads_every_word_once(ctx, policy):
+    """The streaming probe's workgroups together read every 16-byte chunk
+    once: the xor of their words is the xor of the buffer's words."""
+    rng = np.random.default_rng(policy)
+    words = rng.integers(0, 2 ** 32, 1 << 20, dtype=np.uint64).astype(np.uint32)
+    for nbytes, nwgs in ((words.nbytes, 300), (words.nbytes - 16 * 77, 1), (4096 + 16 * 3, 1000)):
+        buf = ctx.from_numpy(words)
+        sink = ctx.zeros(nwgs, np.uint32)
+        ctx.streamRead(buf, nbytes, policy, nwgs, sink)
+        got = np.bitwise_xor.reduce(sink.download(np.uint32))
+        assert got == np.bitwise_xor.reduce(words[:nbytes // 4]), (nbytes, nwgs)
