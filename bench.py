@@ -307,6 +307,19 @@ def lm_head_sampling(ctx, reps=10):
         res[f"M={M}"] = {"head_softcap_us": round(us_head, 2), "argmax_us": round(us_arg, 2),
                          "topk256_us": round(us_topk, 2), "head_bytes": nbytes,
                          "head_gbps": round(nbytes / (us_head * 1e-6) / 1e9, 1)}
+        if M == 1:
+            # the whole sampling step as the decode step runs it: final norm + LM
+            # head + softcap with the argmax / top-k candidates as the matvec's
+            # epilogue, then their reduction (two launches each)
+            w = ctx.empty(H, np.uint16)
+            ctx.fill_normal_f16(w, H, 43, 1.0, 0.1)
+            res["M=1"]["fused_argmax_us"] = round(graph_us(
+                ctx, lambda: ctx.normAddMatmulArgmax("q6k", x, w, None, None, None, W, lg, V, H, tok,
+                                                     softcap=30.0), reps), 2)
+            res["M=1"]["fused_topk256_us"] = round(graph_us(
+                ctx, lambda: ctx.normAddMatmulTopk("q6k", x, w, None, None, None, W, lg, V, H, tk,
+                                                   softcap=30.0), reps), 2)
+            w.free()
     W.free()
     return res
 

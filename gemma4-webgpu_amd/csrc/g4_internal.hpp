@@ -47,6 +47,11 @@ int g4_internal_argmax_final(g4_ctx* ctx, const void* parts, int nparts, uint32_
 // of g4_dequantPath).
 int g4_internal_operand_values(g4_ctx* ctx, int wtype, const void* blocks, uint64_t nblocks, float* out);
 
+// Second top-k stage (k_elem.hip): per batch row, each of the 256 residue
+// classes takes the best of its `nparts` candidates (Cand, laid out
+// [batch][256][nparts]) and result[r][512] receives (value, index bits).
+int g4_internal_topk_final(g4_ctx* ctx, const void* parts, int nparts, uint32_t batch, float* result);
+
 // Matrix-core matmul of `batch` activation vectors (k_batch.hip).
 int g4_internal_batch_matmul(g4_ctx* ctx, const char* fn, int qt, const float* x, const void* w, float* y,
                              uint32_t M, uint32_t N, uint32_t batch);

@@ -194,48 +194,76 @@ __global__ __launch_bounds__(64) void argmax_final(const Cand* part, int nparts,
   }
 }
 
-// topk256: residue class t of a slab of rows (row r = indices [256r, 256r+256)).
-// Within a class the first strict maximum wins, so slabs are merged in
-// ascending order with a strict '>' (shaders/topk256.wgsl:12-18).
-constexpr int kTopkSlabs = 128;
+// topk256 (shaders/topk256.wgsl:8-20): for each residue class t = i mod 256
+// the first strict maximum of the logits in class t, in index order, starting
+// from (-1e30, 0), so NaN and values <= -1e30 are never kept. Two stages:
+// slabs of the index range each keep their class maxima, then each class
+// takes the best slab candidate under `tk_better` (larger value, then
+// smaller index), which equals the in-order strict scan whatever the slab
+// order (slabs hold disjoint index ranges and never hold NaN).
+// Candidates are laid out [batch][256 classes][nparts], so a class's
+// candidates are contiguous for the second stage. The fused LM head
+// (k_gemv.hip) writes the same layout from its workgroups' stored rows.
+constexpr int kTopkSlabs = 256;
+constexpr int kTopkLoads = 8;   // loads a thread issues before comparing any
 
-__global__ __launch_bounds__(NT) void topk_partial(const float* logits, uint32_t n, float2* part) {
-  const uint32_t t = threadIdx.x;
-  logits += (size_t)blockIdx.y * n;
-  part += (size_t)blockIdx.y * gridDim.x * 256;
-  const uint32_t rows = (n + 255) / 256;
-  const uint32_t per = (rows + gridDim.x - 1) / gridDim.x;
-  const uint32_t r0 = blockIdx.x * per, r1 = min(rows, r0 + per);
-  float mx = -1e30f;
-  uint32_t idx = 0;
-  for (uint32_t r = r0; r < r1; ++r) {
-    const uint32_t i = r * 256 + t;
-    if (i < n) {
-      const float v = logits[i];
-      if (v > mx) {
-        mx = v;
-        idx = i;
-      }
-    }
-  }
-  part[(size_t)blockIdx.x * 256 + t] = make_float2(mx, __uint_as_float(idx));
+__device__ __forceinline__ bool tk_better(const Cand& a, const Cand& b) {
+  return a.v > b.v || (a.v == b.v && a.i < b.i);
 }
 
-__global__ __launch_bounds__(NT) void topk_final(const float2* part, int nparts, float* result) {
-  const uint32_t t = threadIdx.x;
-  part += (size_t)blockIdx.x * nparts * 256;
-  result += (size_t)blockIdx.x * 512;
-  float mx = -1e30f;
-  uint32_t idx = 0;
-  for (int s = 0; s < nparts; ++s) {
-    const float2 p = part[(size_t)s * 256 + t];
-    if (p.x > mx) {
-      mx = p.x;
-      idx = __float_as_uint(p.y);
+// stage 1: workgroup (s, b) scans rows [r0, r1) of 256 logits of batch row b
+__global__ __launch_bounds__(NT) void topk_partial(const float* logits, uint32_t n, Cand* part) {
+  const uint32_t t = threadIdx.x, ns = gridDim.x;
+  logits += (size_t)blockIdx.y * n;
+  part += (size_t)blockIdx.y * 256 * ns;
+  const uint32_t rows = (n + 255) / 256;
+  const uint32_t per = (rows + ns - 1) / ns;
+  const uint32_t r0 = blockIdx.x * per, r1 = min(rows, r0 + per);
+  Cand c{-1e30f, 0u};
+  for (uint32_t rb = r0; rb < r1; rb += kTopkLoads) {
+    float v[kTopkLoads];
+#pragma unroll
+    for (int k = 0; k < kTopkLoads; ++k) {  // clamped, unconditional loads
+      const uint32_t i = min((rb + (uint32_t)k) * 256u + t, n - 1);
+      v[k] = logits[i];
+    }
+#pragma unroll
+    for (int k = 0; k < kTopkLoads; ++k) {
+      const uint32_t i = (rb + (uint32_t)k) * 256u + t;
+      if (rb + (uint32_t)k < r1 && i < n && v[k] > c.v) c = Cand{v[k], i};
     }
   }
-  result[2 * t] = mx;
-  result[2 * t + 1] = __uint_as_float(idx);
+  part[(size_t)t * ns + blockIdx.x] = c;
+}
+
+// stage 2: 16 lanes per class, grid (16, batch); each lane reduces every
+// 16th candidate of its class (kTopkLoads loads in flight), then the 16
+// lanes combine. result[b][2t] = value, [2t + 1] = index bits.
+__global__ __launch_bounds__(NT) void topk_final(const Cand* part, int nparts, float* result) {
+  const uint32_t cls = blockIdx.x * (NT / 16) + threadIdx.x / 16, j = threadIdx.x % 16;
+  const Cand* p = part + ((size_t)blockIdx.y * 256 + cls) * nparts;
+  Cand c{-1e30f, 0u};
+  for (int k0 = (int)j; k0 < nparts; k0 += 16 * kTopkLoads) {
+    Cand d[kTopkLoads];
+#pragma unroll
+    for (int k = 0; k < kTopkLoads; ++k) {
+      const int i = k0 + 16 * k;
+      d[k] = i < nparts ? p[i] : Cand{-1e30f, 0u};
+    }
+#pragma unroll
+    for (int k = 0; k < kTopkLoads; ++k)
+      if (tk_better(d[k], c)) c = d[k];
+  }
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) {
+    const Cand d{__shfl_xor(c.v, o, 16), (uint32_t)__shfl_xor((int)c.i, o, 16)};
+    if (tk_better(d, c)) c = d;
+  }
+  if (j == 0) {
+    float* r = result + (size_t)blockIdx.y * 512;
+    r[2 * cls] = c.v;
+    r[2 * cls + 1] = __uint_as_float(c.i);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -563,18 +591,18 @@ int g4_topk256Batch(g4_ctx* ctx, const float* logits, float* result, uint32_t si
   G4_ENTER(ctx);
   G4_REQUIRE(logits && result, "g4_topk256: null buffer");
   G4_REQUIRE(batch >= 1 && batch <= 1024, "g4_topk256Batch: batch %u not in 1..1024", batch);
+  G4_REQUIRE(size > 0, "g4_topk256: empty logits");
   const uint32_t rows = (size + 255) / 256;
-  const unsigned want = ceil_div(rows, 8), cap = std::max(1u, 1024u / batch);
-  const int ns = want == 0 ? 1 : (int)std::min({want, (unsigned)kTopkSlabs, cap});
+  const unsigned want = ceil_div(rows, 4), cap = std::max(1u, 1024u / batch);
+  const int ns = (int)std::max(1u, std::min({want, (unsigned)kTopkSlabs, cap}));
   void* scratch = nullptr;
-  int rc = g4_internal_scratch(ctx, (size_t)batch * ns * 256 * sizeof(float2), &scratch);
+  int rc = g4_internal_scratch(ctx, (size_t)batch * ns * 256 * sizeof(Cand), &scratch);
   if (rc) return rc;
-  hipLaunchKernelGGL(topk_partial, dim3(ns, batch), dim3(NT), 0, ctx->stream, logits, size, (float2*)scratch);
+  hipLaunchKernelGGL(topk_partial, dim3(ns, batch), dim3(NT), 0, ctx->stream, logits, size, (Cand*)scratch);
   G4_LAUNCHED(ctx, "topk_partial");
-  hipLaunchKernelGGL(topk_final, dim3(batch), dim3(NT), 0, ctx->stream, (const float2*)scratch, ns, result);
-  G4_LAUNCHED(ctx, "topk_final");
-  return G4_OK;
+  return g4_internal_topk_final(ctx, scratch, ns, batch, result);
 }
+
 
 int g4_topk256(g4_ctx* ctx, const float* logits, float* result, uint32_t size) {
   return g4_topk256Batch(ctx, logits, result, size, 1);
@@ -641,6 +669,13 @@ int g4_fill_normal_f16(g4_ctx* ctx, uint16_t* dst, uint64_t n, uint64_t seed, fl
 }
 
 }  // extern "C"
+
+int g4_internal_topk_final(g4_ctx* ctx, const void* parts, int nparts, uint32_t batch, float* result) {
+  hipLaunchKernelGGL(topk_final, dim3(256 / (NT / 16), batch), dim3(NT), 0, ctx->stream, (const Cand*)parts, nparts,
+                     result);
+  G4_LAUNCHED(ctx, "topk_final");
+  return G4_OK;
+}
 
 int g4_internal_argmax_final(g4_ctx* ctx, const void* parts, int nparts, uint32_t batch, uint32_t* result,
                              uint32_t* adv, uint32_t delta) {

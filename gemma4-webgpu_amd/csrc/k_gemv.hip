@@ -519,6 +519,10 @@ struct GemvSegs {
   uint32_t rep;     // consecutive row tiles per workgroup
   g4d::Cand* amx;   // mv_kernel, one matrix: per-workgroup argmax candidate of the stored rows, or null
   uint8_t* d8;      // mv_kernel, gate/up pair: the outputs also as an MvD8 block (K = rows), or null
+  // mv_kernel, one matrix: per-workgroup top-k candidates (each residue
+  // class's first strict maximum among the stored rows), [256][tk_stride], or null
+  g4d::Cand* tk;
+  uint32_t tk_stride;
 };
 
 // EPI: 0 = store y, 1 = store softcap(y) (shaders/logit_softcap.wgsl).
@@ -1234,7 +1238,8 @@ __device__ __forceinline__ void mv_d8_group(float v, bool real, uint32_t row, ui
 // stores the tile's rows: y, softcap(y), or gelu(gate) * up for a pair.
 template <class T, int NTH, int NMAT>
 __device__ __forceinline__ void mv_reduce_store(const float* red, const GemvSeg& sg, uint32_t t, int tid, float cap,
-                                                bool track, g4d::Cand& best, uint8_t* d8 = nullptr) {
+                                                bool track, g4d::Cand& best, uint8_t* d8 = nullptr,
+                                                g4d::Cand* tkt = nullptr) {
   constexpr int U = NTH / T::TR;
   const int gl = tid % T::RG;
   for (int r = tid / T::RG; r < T::TR; r += NTH / T::RG) {  // uniform within a group
@@ -1261,6 +1266,9 @@ __device__ __forceinline__ void mv_reduce_store(const float* red, const GemvSeg&
       sg.Y[row] = v;
       const g4d::Cand d{v, row};
       if (track && g4d::better(d, best)) best = d;
+      // top-k classes: a tile's rows are distinct classes (TR <= 256) and
+      // tiles come in row order, so a strict '>' keeps the first maximum
+      if (tkt && v > tkt[row & 255u].v) tkt[row & 255u] = d;
     }
   }
 }
@@ -1280,6 +1288,14 @@ __device__ __forceinline__ void mv_argmax_partial(g4d::Cand c, g4d::Cand* sm, g4
       if (g4d::better(sm[k], b)) b = sm[k];
     *dst = b;
   }
+}
+
+// The workgroup's top-k class table (the first stage of shaders/topk256.wgsl
+// over the rows it stored) to column `wg` of the [256][tk_stride] candidates.
+template <int NTH>
+__device__ __forceinline__ void mv_topk_partial(const g4d::Cand* tkt, const GemvSegs& segs, uint32_t wg) {
+  lds_barrier();
+  for (int i = threadIdx.x; i < 256; i += NTH) segs.tk[(size_t)i * segs.tk_stride + wg] = tkt[i];
 }
 
 // NMAT = 1: y, or softcap(y) when cap > 0 (shaders/logit_softcap.wgsl), for
@@ -1308,6 +1324,12 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
   const uint32_t te = min(tiles, tb + segs.rep);
   const int tid = threadIdx.x;
   const int slot = tid / G::U, u = tid % G::U;
+  // top-k class table past the kernel's other LDS (ordered before its first
+  // use by the prologue's barriers)
+  g4d::Cand* const tkt =
+      (NMAT == 1 && segs.tk) ? (g4d::Cand*)(smem + mv_lds_bytes<QT, BPR, NWV, PRO, NMAT>(STAGED)) : nullptr;
+  if (tkt)
+    for (int i = tid; i < 256; i += NTH) tkt[i] = g4d::Cand{-1e30f, 0u};
   float* red = (float*)(smem + align16(MvXA<BPR, PRO>::END));
   uint8_t* const d8 = NMAT == 2 ? segs.d8 : nullptr;
 
@@ -1369,10 +1391,11 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
     }
     lds_barrier();
     g4d::Cand best{-1e30f, 0u};
-    mv_reduce_store<T, NTH, NMAT>(red, sg, tb, tid, cap, segs.amx != nullptr, best, d8);
+    mv_reduce_store<T, NTH, NMAT>(red, sg, tb, tid, cap, segs.amx != nullptr, best, d8, tkt);
     if constexpr (NMAT == 1)
       if (segs.amx)
         mv_argmax_partial<NWV>(best, (g4d::Cand*)(smem + MvXA<BPR, PRO>::RED8), segs.amx + blockIdx.x);
+    if (tkt) mv_topk_partial<NTH>(tkt, segs, blockIdx.x - sg.wg_begin);
     return;
   }
   if constexpr (STAGED && PRO != 3) {
@@ -1408,11 +1431,12 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
         red[m * T::TR * T::RS + slot * T::RS + u] = mv_unit_dot<QT>(X, blk, u & 3);
       }
       lds_barrier();
-      mv_reduce_store<T, NTH, NMAT>(red, sg, t, tid, cap, segs.amx != nullptr, best, d8);
+      mv_reduce_store<T, NTH, NMAT>(red, sg, t, tid, cap, segs.amx != nullptr, best, d8, tkt);
     }
     if constexpr (NMAT == 1)
       if (segs.amx)
         mv_argmax_partial<NWV>(best, (g4d::Cand*)(smem + MvXA<BPR, PRO>::RED8), segs.amx + blockIdx.x);
+    if (tkt) mv_topk_partial<NTH>(tkt, segs, blockIdx.x - sg.wg_begin);
   }
 }
 
@@ -1640,6 +1664,8 @@ struct LaunchReq {
   uint32_t amx_cap = 0;         // candidates `amx` holds
   uint32_t* wgs_out = nullptr;  // receives the workgroup count
   uint8_t* d8 = nullptr;        // gate/up pair: also write the outputs as an MvD8 block
+  g4d::Cand* tk = nullptr;      // one matrix: per-workgroup top-k class candidates [256][workgroups]
+  uint32_t tk_cap = 0;          // workgroups `tk` holds candidates for
 };
 
 constexpr uint32_t kMaxGemvWgs = 2048;  // beyond this a workgroup walks several row tiles
@@ -1742,13 +1768,18 @@ int mv_launch(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
   sg.n = q.nseg;
   sg.amx = q.amx;
   sg.d8 = q.d8;
+  sg.tk = NMAT == 1 ? q.tk : nullptr;
   if (PRO == 3 && sg.rep != 1)
     return g4::set_error(G4_ERR_UNSUPPORTED, "matvec: digit input needs one tile per workgroup (%u rows)", q.segs[0].M);
   if (q.wgs_out) *q.wgs_out = wgs;
   if (wgs == 0) return G4_OK;
   if (q.amx && wgs > q.amx_cap)
     return g4::set_error(G4_ERR_UNSUPPORTED, "matvec: %u workgroups exceed the %u argmax candidates", wgs, q.amx_cap);
-  const size_t lds = mv_lds_bytes<QT, BPR, NWV, PRO, NMAT>(sg.rep > 1);
+  if (sg.tk && (wgs > q.tk_cap || q.nseg != 1))
+    return g4::set_error(G4_ERR_UNSUPPORTED, "matvec: top-k candidates need one matrix and <= %u workgroups (%u)",
+                         q.tk_cap, wgs);
+  sg.tk_stride = wgs;
+  const size_t lds = mv_lds_bytes<QT, BPR, NWV, PRO, NMAT>(sg.rep > 1) + (sg.tk ? 256 * sizeof(g4d::Cand) : 0);
   // rep > 1 means more than 2 * num_cus tiles of the widest workgroup, which
   // mv_pick chooses for at least kMvFullWgs tiles: only the 12-wave
   // instances walk tiles
@@ -2161,6 +2192,38 @@ int g4_normAddMatmulArgmax(g4_ctx* ctx, int wtype, const float* x, const uint16_
   rc = launch_gemv(ctx, q);
   if (rc) return rc;  // (N is 1536 or 2048: every failure here sets its own message)
   return g4_internal_argmax_final(ctx, parts, (int)wgs, 1, result, positions, delta);
+}
+
+int g4_normAddMatmulTopk(g4_ctx* ctx, int wtype, const float* x, const uint16_t* w1, const float* residual,
+                         const uint16_t* w2, float* h_out, const void* weight, float* logits, uint32_t rows,
+                         uint32_t N, float eps, float softcap_cap, float* result) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(wtype == 0 || wtype == 1, "g4_normAddMatmulTopk: wtype must be 0 (Q4_K) or 1 (Q6_K)");
+  G4_REQUIRE(x && w1 && weight && logits && result && rows > 0, "g4_normAddMatmulTopk: null buffer or no rows");
+  G4_REQUIRE(!residual == !w2, "g4_normAddMatmulTopk: residual and w2 go together");
+  G4_REQUIRE(N == 1536 || N == 2048, "g4_normAddMatmulTopk: N=%u unsupported (1536 or 2048)", N);
+  G4_REQUIRE(((uintptr_t)x & 15) == 0 && (!residual || ((uintptr_t)residual & 15) == 0) &&
+                 (!h_out || ((uintptr_t)h_out & 15) == 0),
+             "g4_normAddMatmulTopk: activations must be 16-byte aligned");
+  G4_REQUIRE(((uintptr_t)w1 & 7) == 0 && ((uintptr_t)w2 & 7) == 0,
+             "g4_normAddMatmulTopk: norm weights must be 8-byte aligned");
+  int rc = check_w(__func__, wtype, weight);
+  if (rc) return rc;
+  // 256 candidates per workgroup: at most two workgroups per CU for a
+  // matrix walked tile by tile, one per tile below that
+  const uint32_t max_parts = 2 * (uint32_t)ctx->num_cus;
+  void* parts = nullptr;
+  rc = g4_internal_scratch(ctx, (size_t)256 * max_parts * sizeof(g4d::Cand), &parts);
+  if (rc) return rc;
+  GemvSeg seg{(const uint8_t*)weight, logits, rows, 0};
+  uint32_t wgs = 0;
+  LaunchReq q{wtype, &seg, 1, N, 1, residual ? 2 : 1, softcap_cap != 0.f ? 1 : 0, softcap_cap,
+              ProArgs{x, w1, residual, w2, h_out, eps}, 0, nullptr, 0, &wgs};
+  q.tk = (g4d::Cand*)parts;
+  q.tk_cap = max_parts;
+  rc = launch_gemv(ctx, q);
+  if (rc) return rc;
+  return g4_internal_topk_final(ctx, parts, (int)wgs, 1, result);
 }
 
 }  // extern "C"

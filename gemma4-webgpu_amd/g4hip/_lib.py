@@ -190,6 +190,7 @@ SIGNATURES = {
     "g4_normAddGateUpGeluDigits_q4k": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, MatmulParams, _F]),
     "g4_matmulQuantDigits_q6k": (_I, [_P, _P, _P, _P, MatmulParams]),
     "g4_normAddMatmulArgmax": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, _F, _F, _P, _P, _U32]),
+    "g4_normAddMatmulTopk": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, _F, _F, _P]),
     "g4_matmulSegmentsBatchPartial": (_I, [_P, _I, _P, _P, ctypes.POINTER(_P), ctypes.POINTER(_P),
                                            ctypes.POINTER(_U32), _I, _U32, _U32, _U32, _F,
                                            ctypes.POINTER(_U32)]),

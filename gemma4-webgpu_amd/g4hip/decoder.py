@@ -278,9 +278,10 @@ class Decoder(_SyntheticModel):
              (also written as the digit block the down launch reads)
           5. down matvec (Q6_K) over those digits
         then the last post-FFN norm-add + final rmsNorm + LM head + softcap in
-        one launch; with argmax sampling its workgroups also leave their
-        argmax candidates, which a one-workgroup launch reduces to the token
-        (and advances the position). With `warm`, each attention launch also
+        one launch; its workgroups also leave their argmax candidates (argmax
+        sampling), which a one-workgroup launch reduces to the token and the
+        position advance, or their per-residue top-k candidates (top-k
+        sampling), which a second launch reduces to the 256 pairs. With `warm`, each attention launch also
         reads the gate/up and down weights of its layer into the L2 caches
         (on the CUs the attention leaves idle).
         """
@@ -310,10 +311,8 @@ class Decoder(_SyntheticModel):
                                       self.hidden, self.lm_head, self.logits, s.vocab, s.hidden, self.token, s.eps,
                                       softcap=s.softcap, positions=self.pos if advance else None, delta=1)
                 return
-            c.normAddMatmulSegments("q6k", self.down, last.post_ffn_norm, self.hidden2, self.final_norm,
-                                    self.hidden, [self.lm_head], [self.logits], [s.vocab], s.hidden, s.eps,
-                                    softcap=s.softcap)
-            c.topk256(self.logits, self.topk, s.vocab)
+            c.normAddMatmulTopk("q6k", self.down, last.post_ffn_norm, self.hidden2, self.final_norm, self.hidden,
+                                 self.lm_head, self.logits, s.vocab, s.hidden, self.topk, s.eps, softcap=s.softcap)
         else:
             c.fusedNormAdd(self.down, last.post_ffn_norm, self.hidden2, self.hidden, s.hidden, s.eps)
         if advance:

@@ -236,6 +236,15 @@ class Context:
                                            _p(w2), _p(h_out), _p(weight), _p(logits), rows, N, eps, softcap,
                                            _p(result), _p(positions), delta))
 
+    def normAddMatmulTopk(self, wtype: str, x: Ptr, w1: Ptr, residual: Ptr, w2: Ptr, h_out: Ptr, weight: Ptr,
+                          logits: Ptr, rows: int, N: int, result: Ptr, eps: float = 1e-6,
+                          softcap: float = 0.0) -> None:
+        """normAddMatmulSegments over one matrix into `logits`, and result f32[512] = topk256(logits)
+        (per residue class, reference ties and NaN rule) from the matvec's own per-workgroup candidates."""
+        check(lib().g4_normAddMatmulTopk(self.h, {"q4k": 0, "q6k": 1}[wtype], _p(x), _p(w1), _p(residual),
+                                         _p(w2), _p(h_out), _p(weight), _p(logits), rows, N, eps, softcap,
+                                         _p(result)))
+
     def normAddMatmulSegmentsBatch(self, wtype: str, x: Ptr, w1: Ptr, residual: Ptr, w2: Ptr, h_out: Ptr,
                                    weights, outputs, rows, N: int, batch: int, eps: float = 1e-6,
                                    softcap: float = 0.0) -> None:

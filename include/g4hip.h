@@ -455,6 +455,19 @@ int g4_normAddMatmulArgmax(g4_ctx* ctx, int wtype, const float* x, const uint16_
                            float softcap_cap, uint32_t* result, uint32_t* positions,
                            uint32_t delta);
 
+/* The LM head with top-k sampling in two launches: g4_normAddMatmulSegments
+ * over one matrix (logits[rows], softcapped when softcap_cap != 0), whose
+ * workgroups also keep, for each residue class i mod 256, the first strict
+ * maximum among the rows they store, then the reduction of those candidates:
+ * result f32[512] = g4_topk256(logits, rows) (per class (max, bitcast index),
+ * ties, NaN and the (-1e30, 0) default as shaders/topk256.wgsl:8-20), without
+ * reading the logits back. Replaces src/engine.ts:1686-1701 + 1735-1740
+ * (final norm, LM head, softcap, topk256). */
+int g4_normAddMatmulTopk(g4_ctx* ctx, int wtype, const float* x, const uint16_t* w1,
+                         const float* residual, const uint16_t* w2, float* h_out,
+                         const void* weight, float* logits, uint32_t rows, uint32_t N, float eps,
+                         float softcap_cap, float* result);
+
 /* The same over `batch` activation vectors at once (ragged multi-sequence
  * decode: src/engine.ts:1546-1554 run once per sequence). x, residual and
  * h_out are [batch][N]; outputs[i] is [batch][rows[i]]. w1 == NULL skips the

@@ -292,6 +292,50 @@ def test_norm_add_matmul_argmax(ctx, M, scale, specials):
     assert p.download(np.uint32)[0] == 77 + 6
 
 
+@pytest.mark.parametrize("M,scale,specials", [(20000, 20.0, False), (3000, 20.0, False), (20000, 2000.0, False),
+                                              (3000, 2000.0, True), (262144, 20.0, False), (262144, 2000.0, False),
+                                              (300, 20.0, False)])
+def test_norm_add_matmul_topk(ctx, M, scale, specials):
+    """LM head + softcap with the top-k256 pairs taken from the matvec's own
+    per-workgroup residue-class candidates (src/engine.ts:1735-1740,
+    shaders/topk256.wgsl): the logits are those of normAddMatmulSegments bit
+    for bit and the 512 words equal the reference scan of them bit for bit,
+    with saturated ties (2000x final-norm weight), NaN rows (no softcap),
+    fewer rows than classes, and the full 262144-row head (workgroups walking
+    512 rows each). Twice in a row: every call restarts its class tables."""
+    N = 1536
+    W = O.gen_q6k(70, M * N // 256).reshape(M, -1).copy()
+    if specials:
+        W[5::97, 208:210] = np.frombuffer(struct.pack("<H", 0x7e00), np.uint8)  # d = NaN
+    W = W.reshape(-1)
+    x = O.gen_normal_f32(71, N, 0.0, 2.0)
+    res = O.gen_normal_f32(72, N, 0.0, 5.0)
+    w1 = O.gen_normal_f16(73, N, 1.0, 0.1)
+    w2 = O.gen_normal_f16(74, N, 1.0, 0.1)
+    w2s = (w2.view(np.float16).astype(np.float32) * scale).astype(np.float16).view(np.uint16)
+    cap = 0.0 if specials else 30.0
+    dx, dw1, dres, dw2, dW = (ctx.from_numpy(a) for a in (x, w1, res, w2s, W))
+    y_ref = ctx.empty(M, np.float32)
+    ctx.normAddMatmulSegments("q6k", dx, dw1, dres, dw2, None, [dW], [y_ref], [M], N, 1e-6, softcap=cap)
+    want = y_ref.download(np.float32)
+    y = ctx.empty(M, np.float32)
+    dh = ctx.empty(N, np.float32)
+    t = ctx.zeros(512, np.float32)
+    for call in range(2):
+        ctx.normAddMatmulTopk("q6k", dx, dw1, dres, dw2, dh, dW, y, M, N, t, 1e-6, softcap=cap)
+        got = y.download(np.float32)
+        assert bits_equal(got, want), call
+        assert bits_equal(t.download(np.float32), O.topk256(got)), call
+    if scale > 100 and not specials:
+        assert np.count_nonzero(got == np.float32(30.0)) > 8
+    if specials:
+        assert np.isnan(got).any()
+    # the standalone two-stage top-k over the written logits agrees
+    t2 = ctx.zeros(512, np.float32)
+    ctx.topk256(y, t2, M)
+    assert bits_equal(t2.download(np.float32), t.download(np.float32))
+
+
 def _check_digit_block(blk, x):
     """The digit block a gate/up launch writes for its outputs x: per 8
     elements, x ~ s * (256 hi + lo) to within one digit step (the scale is
