@@ -341,12 +341,13 @@ def batch_census(ctx, bd, reps=10):
                                                            bd.page_table, bd.seq_lens, bd.pro_params[il],
                                                            bd.rope_cs[bd.s.is_global(il)], bd.rope_rows),
         "attn_global": lambda il, L: (c.pagedAttnDecode(bd.q, L.k_cache, L.v_cache, bd.page_table, bd.seq_lens,
-                                                        bd.attn, bd.attn_params[il], bd.attn_ws)
+                                                        bd.attn, bd.attn_params[il], bd.attn_ws, ops=bd.aops)
                                       if s.is_global(il) else "skip"),
         "attn_window512": lambda il, L: (c.pagedAttnDecode(bd.q, L.k_cache, L.v_cache, bd.page_table, bd.seq_lens,
-                                                           bd.attn, bd.attn_params[il], bd.attn_ws)
+                                                           bd.attn, bd.attn_params[il], bd.attn_ws, ops=bd.aops)
                                          if not s.is_global(il) else "skip"),
-        "o": lambda il, L: c.matmulSegmentsBatchPartial("q4k", bd.attn, [L.wo], [bd.o_parts], [H], Q, B, bd.ks_q),
+        "o": lambda il, L: c.matmulSegmentsBatchPartial("q4k", bd.attn, [L.wo], [bd.o_parts], [H], Q, B, bd.ks_q,
+                                                        ops=bd.aops),
         "prep_ffn": lambda il, L: c.batchPrep(bd.o_parts, bd.ks_q, L.post_attn_norm, bd.hidden, L.pre_ffn_norm,
                                               bd.hidden2, bd.xn, H, B, s.eps, ops=bd.xops),
         "gate_up_gelu": lambda il, L: c.gateUpGeluBatch(bd.xn, L.wgate, L.wup, bd.act, I, H, B, ops=bd.xops),

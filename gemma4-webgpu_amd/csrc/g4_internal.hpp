@@ -276,6 +276,24 @@ __host__ __device__ __forceinline__ uint64_t splitmix64(uint64_t seed, uint64_t 
   return z ^ (z >> 31);
 }
 
+// Matrix-core operand blocks of the M >= 16 matmul (k_batch.hip), one per
+// super-block of K. Vectors are padded to the 16, 32 or 64 columns of the
+// MFMA tiles a launch uses (NTV tiles of 16 vectors):
+//   main  [t][s][h][lane] 16 B: f16 x 8 of vector 16t + lane%16 at
+//         k = 32s + 8(lane/16) .. +7; h = 0: x_hi, 1: x_lo of x * 2^e
+//   sums  [t][lane] 16 B: f16 slots 8(lane/16) .. +7 of vector 16t + lane%16;
+//         slot j is part j%4 of the sum over sub-block j/4 of x * 2^(e-6)
+//         (parts 0..2, part 3 zero)
+//   scale [t][16] f32: 2^-e per vector
+// where 2^e puts the vector's largest |x| in the super-block in [2^13, 2^14).
+__host__ __device__ constexpr uint32_t pad_batch(uint32_t b) { return b <= 16 ? 16 : (b <= 32 ? 32 : 64); }
+struct Ops {
+  static constexpr uint32_t MAIN_T = 8 * 2 * 1024;
+  __host__ __device__ static constexpr uint32_t sums_off(int ntv) { return (uint32_t)ntv * MAIN_T; }
+  __host__ __device__ static constexpr uint32_t scale_off(int ntv) { return (uint32_t)ntv * (MAIN_T + 1024); }
+  __host__ __device__ static constexpr uint32_t bytes(int ntv) { return (uint32_t)ntv * (MAIN_T + 1024 + 64); }
+};
+
 }  // namespace g4d
 
 inline unsigned ceil_div(uint64_t a, uint64_t b) { return (unsigned)((a + b - 1) / b); }

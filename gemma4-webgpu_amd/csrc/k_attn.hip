@@ -570,10 +570,56 @@ __device__ __forceinline__ void live_window(const LenArgs& a, uint32_t seq, uint
 
 // Splits past ceil(n / chunk) of a sequence are never read: the matrix-core
 // kernel does not launch workgroups for them.
+// The merged output of (sequence seq, head hq) also as the matrix-core
+// operand blocks of the o projection (g4d::Ops; K = nqh * HD, so the head's
+// HD dims are HD / 256 whole super-blocks): per super-block the exponent
+// from the block maximum, f16 hi / lo of y * 2^e, the 3-part sub-block sums
+// of y * 2^(e-6) and the scale 2^-e, what bprep_kernel writes for the same
+// values. Every thread of the workgroup calls it (`live`: a thread of group 0).
+template <int HD>
+__device__ __forceinline__ void merge_ops(float y, bool live, uint8_t* ops, int ntv, uint32_t seq, uint32_t hq,
+                                          uint32_t d) {
+  __shared__ float wmax_s[16];
+  const uint32_t tid = threadIdx.x;
+  const float wm = g4d::wave_max_dpp(fabsf(y));
+  if ((tid & 63) == 0) wmax_s[tid >> 6] = wm;
+  __syncthreads();
+  if (!live) return;
+  const uint32_t sbl = d >> 8, e = d & 255u;  // super-block of the head, element in it
+  const float am = fmaxf(fmaxf(wmax_s[4 * sbl], wmax_s[4 * sbl + 1]), fmaxf(wmax_s[4 * sbl + 2], wmax_s[4 * sbl + 3]));
+  int ex = 0;
+  (void)frexpf(am, &ex);
+  const int k = am > 0.f ? min(max(14 - ex, -120), 120) : 0;
+  const float xs = y * ldexpf(1.0f, k);
+  const _Float16 hi = (_Float16)xs, lo = (_Float16)(xs - (float)hi);
+  const uint32_t s = e >> 5, p = e & 31u, q = p >> 3, j = p & 7u;
+  const uint32_t kb = hq * (uint32_t)(HD / 256) + sbl, t = seq >> 4, c = seq & 15u;
+  uint8_t* base = ops + (size_t)kb * g4d::Ops::bytes(ntv);
+  uint8_t* mp = base + t * g4d::Ops::MAIN_T + s * 2048 + (c + 16u * q) * 16 + j * 2;
+  *(_Float16*)mp = hi;
+  *(_Float16*)(mp + 1024) = lo;
+  float sum = xs;  // over the sub-block: 32 consecutive lanes
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) sum += __shfl_xor(sum, o, 32);
+  if (p == 0) {
+    sum *= 0.015625f;  // * 2^-6
+    const _Float16 p0 = (_Float16)sum;
+    const float r1 = sum - (float)p0;
+    const _Float16 p1 = (_Float16)r1;
+    const _Float16 p2 = (_Float16)(r1 - (float)p1);
+    _Float16* sp = (_Float16*)(base + g4d::Ops::sums_off(ntv) + t * 1024 + (c + 16u * (s >> 1)) * 16 + (s & 1) * 8);
+    sp[0] = p0;
+    sp[1] = p1;
+    sp[2] = p2;
+    sp[3] = (_Float16)0.f;
+  }
+  if (e == 0) *(float*)(base + g4d::Ops::scale_off(ntv) + t * 64 + c * 4) = ldexpf(1.0f, -k);
+}
+
 template <int HD>
 __global__ __launch_bounds__(1024) void attn_merge_kernel(const float* ws, float* out, uint32_t nqh, uint32_t nkh,
                                                           uint32_t G, uint32_t nsplit, uint32_t num_seqs,
-                                                          LenArgs la, uint32_t chunk) {
+                                                          LenArgs la, uint32_t chunk, uint8_t* ops, int ntv) {
   constexpr int MG = 1024 / HD;  // split groups (thread g*HD + d owns column d of group g)
   __shared__ float gm_s[MG], gl_s[MG];
   __shared__ float go_s[MG > 1 ? (MG - 1) * HD : 1];
@@ -619,7 +665,7 @@ __global__ __launch_bounds__(1024) void attn_merge_kernel(const float* ws, float
   }
   if (grp > 0) go_s[(grp - 1) * HD + d] = acc;
   __syncthreads();
-  if (grp != 0) return;
+  if (grp != 0 && !ops) return;  // (uniform) the other groups only join the operand block's barrier
   float TM = -INFINITY;
 #pragma unroll
   for (int g = 0; g < MG; ++g) TM = fmaxf(TM, gm_s[g]);
@@ -630,7 +676,9 @@ __global__ __launch_bounds__(1024) void attn_merge_kernel(const float* ws, float
     tl += wg * gl_s[g];
     to += wg * (g == 0 ? acc : go_s[(g - 1) * HD + d]);
   }
-  out[((size_t)seq * nqh + hq) * HD + d] = tl > 0.f ? to / tl : 0.f;
+  const float y = tl > 0.f ? to / tl : 0.f;
+  if (grp == 0) out[((size_t)seq * nqh + hq) * HD + d] = y;
+  if (ops) merge_ops<HD>(grp == 0 ? y : 0.f, grp == 0, ops, ntv, seq, hq, d);
 }
 
 // ---------------------------------------------------------------------------
@@ -1576,20 +1624,21 @@ MqfPlan mqf_plan(const g4_attn_fused_params& p) {
 LenArgs len_args(const AttnArgs& a) { return LenArgs{a.seq_lens, a.pos_dev, a.seq_len, a.cap, a.window}; }
 
 int merge_launch(g4_ctx* ctx, const float* ws, float* out, uint32_t nqh, uint32_t nkh, uint32_t G, uint32_t hd,
-                 uint32_t nsplit, uint32_t num_seqs, const LenArgs& la, uint32_t chunk) {
+                 uint32_t nsplit, uint32_t num_seqs, const LenArgs& la, uint32_t chunk, uint8_t* ops = nullptr) {
+  const int ntv = (int)(g4d::pad_batch(num_seqs) / 16);
   const dim3 mg(nqh, num_seqs);
   switch (hd) {
     case 128:
       hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(1024), 0, ctx->stream, ws, out, nqh, nkh, G, nsplit,
-                         num_seqs, la, chunk);
+                         num_seqs, la, chunk, ops, ntv);
       break;
     case 256:
       hipLaunchKernelGGL(attn_merge_kernel<256>, mg, dim3(1024), 0, ctx->stream, ws, out, nqh, nkh, G, nsplit,
-                         num_seqs, la, chunk);
+                         num_seqs, la, chunk, ops, ntv);
       break;
     default:
       hipLaunchKernelGGL(attn_merge_kernel<512>, mg, dim3(1024), 0, ctx->stream, ws, out, nqh, nkh, G, nsplit,
-                         num_seqs, la, chunk);
+                         num_seqs, la, chunk, ops, ntv);
       break;
   }
   G4_LAUNCHED(ctx, "attn_merge");
@@ -1597,8 +1646,8 @@ int merge_launch(g4_ctx* ctx, const float* ws, float* out, uint32_t nqh, uint32_
 }
 
 int merge(g4_ctx* ctx, const AttnArgs& a, float* out, const SplitPlan& sp, uint32_t num_seqs, uint32_t G,
-          uint32_t hd) {
-  return merge_launch(ctx, a.ws, out, a.nqh, a.nkh, G, hd, sp.nsplit, num_seqs, len_args(a), sp.chunk);
+          uint32_t hd, uint8_t* ops = nullptr) {
+  return merge_launch(ctx, a.ws, out, a.nqh, a.nkh, G, hd, sp.nsplit, num_seqs, len_args(a), sp.chunk, ops);
 }
 
 // The matrix-core kernel serves 8 query heads per KV head at head_dim 256 and
@@ -1608,7 +1657,7 @@ bool mq_fits(uint32_t G, uint32_t hd, uint32_t num_seqs) { return G == 8 && hd =
 // Steps per workgroup from the largest window, sized for about four
 // workgroups per CU when every sequence is that long.
 int mq_decode(g4_ctx* ctx, const char* fn, const AttnArgs& base, bool paged, uint32_t num_seqs, float* out,
-              size_t ws_len) {
+              size_t ws_len, uint8_t* ops = nullptr) {
   const uint32_t eff = eff_len(base.cap, base.window);
   const uint64_t cus = ctx->num_cus > 0 ? (uint64_t)ctx->num_cus : 256;
   const uint64_t want = ((uint64_t)num_seqs * eff + 64 * 4 * cus - 1) / (64 * 4 * cus);
@@ -1637,7 +1686,7 @@ int mq_decode(g4_ctx* ctx, const char* fn, const AttnArgs& base, bool paged, uin
   if (paged) hipLaunchKernelGGL(mq_attn_kernel<true>, grid, dim3(NT), 0, ctx->stream, m);
   else hipLaunchKernelGGL(mq_attn_kernel<false>, grid, dim3(NT), 0, ctx->stream, m);
   G4_LAUNCHED(ctx, "attn_decode_mfma");
-  return merge_launch(ctx, base.ws, out, base.nqh, base.nkh, MQ_G, MQ_HD, max_chunks, num_seqs, m.len, chunk);
+  return merge_launch(ctx, base.ws, out, base.nqh, base.nkh, MQ_G, MQ_HD, max_chunks, num_seqs, m.len, chunk, ops);
 }
 
 int check_heads(const char* fn, uint32_t nqh, uint32_t nkh, uint32_t hd) {
@@ -2009,23 +2058,33 @@ int g4_pagedAttnDecode_workspace_size(g4_paged_attn_params p, size_t* bytes) {
   return G4_OK;
 }
 
-int g4_pagedAttnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
-                       const int32_t* page_table, const uint32_t* seq_lens, float* output, g4_paged_attn_params p,
-                       void* workspace, size_t workspace_bytes) {
+int g4_pagedAttnDecodeOps(g4_ctx* ctx, const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                          const int32_t* page_table, const uint32_t* seq_lens, float* output,
+                          g4_paged_attn_params p, void* workspace, size_t workspace_bytes, void* ops) {
   G4_ENTER(ctx);
   G4_REQUIRE(q && k_pool && v_pool && page_table && seq_lens && output && workspace,
              "g4_pagedAttnDecode: null buffer");
+  G4_REQUIRE(!ops || (p.head_dim % 256 == 0 && p.num_seqs <= 64 && ((uintptr_t)ops & 15) == 0),
+             "g4_pagedAttnDecodeOps: operand blocks need head_dim a multiple of 256, <= 64 sequences and a "
+             "16-byte aligned buffer");
   AttnArgs a{};
   SplitPlan sp{};
   int rc = paged_setup(__func__, k_pool, v_pool, page_table, seq_lens, p, workspace, workspace_bytes, a, sp);
   if (rc) return rc;
   a.q = q;
   if (mq_fits(p.num_q_heads / p.num_kv_heads, p.head_dim, p.num_seqs))
-    return mq_decode(ctx, __func__, a, true, p.num_seqs, output, workspace_bytes);
+    return mq_decode(ctx, __func__, a, true, p.num_seqs, output, workspace_bytes, (uint8_t*)ops);
   rc = launch_attn<true, false>(ctx, a, p.num_q_heads / p.num_kv_heads, p.head_dim, sp.cp,
                                 dim3(sp.nsplit, p.num_kv_heads, p.num_seqs));
   if (rc) return rc;
-  return merge(ctx, a, output, sp, p.num_seqs, p.num_q_heads / p.num_kv_heads, p.head_dim);
+  return merge(ctx, a, output, sp, p.num_seqs, p.num_q_heads / p.num_kv_heads, p.head_dim, (uint8_t*)ops);
+}
+
+int g4_pagedAttnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                       const int32_t* page_table, const uint32_t* seq_lens, float* output, g4_paged_attn_params p,
+                       void* workspace, size_t workspace_bytes) {
+  return g4_pagedAttnDecodeOps(ctx, q, k_pool, v_pool, page_table, seq_lens, output, p, workspace, workspace_bytes,
+                               nullptr);
 }
 
 int g4_pagedAttnDecodeFused_workspace_size(g4_paged_attn_fused_params p, size_t* bytes) {

@@ -50,22 +50,8 @@ constexpr int MNT = 256;   // matmul threads (4 waves)
 constexpr int PMAX = 12;   // partials added per pass of the prep loads (24 measured
                            // slower: passes over fewer chunks load clamped copies)
 
-// Vectors are padded to the 16, 32 or 64 columns of the MFMA tiles a launch uses.
-__host__ __device__ constexpr uint32_t pad_batch(uint32_t b) { return b <= 16 ? 16 : (b <= 32 ? 32 : 64); }
-
-// LDS operand block of one super-block for NTV tiles of 16 vectors:
-//   main  [t][s][h][lane] 16 B: f16 x 8 of vector 16t + lane%16 at
-//         k = 32s + 8(lane/16) .. +7; h = 0: x_hi, 1: x_lo
-//   sums  [t][lane] 16 B: f16 slots 8(lane/16) .. +7 of vector 16t + lane%16;
-//         slot j is part j%4 of the sum over sub-block j/4 of x * 2^(e-6)
-//         (parts 0..2, part 3 zero)
-//   scale [t][16] f32: 2^-e per vector
-struct Ops {
-  static constexpr uint32_t MAIN_T = 8 * 2 * 1024;
-  __host__ __device__ static constexpr uint32_t sums_off(int ntv) { return (uint32_t)ntv * MAIN_T; }
-  __host__ __device__ static constexpr uint32_t scale_off(int ntv) { return (uint32_t)ntv * (MAIN_T + 1024); }
-  __host__ __device__ static constexpr uint32_t bytes(int ntv) { return (uint32_t)ntv * (MAIN_T + 1024 + 64); }
-};
+using g4d::Ops;
+using g4d::pad_batch;
 
 __device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
   h2 v = {a, b};

@@ -162,6 +162,7 @@ SIGNATURES = {
     "g4_matmulWarmRegion": (_I, [_P, _I, _U32, _U32, _P, ctypes.POINTER(WarmRegion)]),
     "g4_pagedAttnDecode_workspace_size": (_I, [PagedAttnParams, ctypes.POINTER(_SZ)]),
     "g4_pagedAttnDecode": (_I, [_P, _P, _P, _P, _P, _P, _P, PagedAttnParams, _P, _SZ]),
+    "g4_pagedAttnDecodeOps": (_I, [_P, _P, _P, _P, _P, _P, _P, PagedAttnParams, _P, _SZ, _P]),
     "g4_pagedKvStore": (_I, [_P, _P, _P, _P, _P, _P, _P, PagedAttnParams]),
     "g4_pagedAttnDecodeFused_workspace_size": (_I, [PagedAttnFusedParams, ctypes.POINTER(_SZ)]),
     "g4_pagedAttnDecodeFused": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, PagedAttnFusedParams, _P,

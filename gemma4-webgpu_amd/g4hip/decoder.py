@@ -390,6 +390,9 @@ class BatchDecoder(_SyntheticModel):
         self.v_parts = ctx.empty(self.ks_h * B * s.kv_dim, f32)
         self.q = ctx.empty(B * s.q_dim, f32)           # q after q_norm + RoPE
         self.attn = ctx.empty(B * s.q_dim, f32)
+        # the attention output also as the o projection's operand blocks
+        # (written by the attention's merge when a head is whole super-blocks)
+        self.aops = ctx.empty(ctx.batch_operand_bytes(s.q_dim, B), np.uint8) if s.head_dim % 256 == 0 else None
         self.o_parts = ctx.empty(self.ks_q * B * s.hidden, f32)
         self.act = ctx.empty(B * s.ffn, f32)
         self.down_parts = ctx.empty(self.ks_f * B * s.hidden, f32)
@@ -446,7 +449,8 @@ class BatchDecoder(_SyntheticModel):
           1. [sum of the previous down chunks -> post-FFN norm-add ->] attn rmsNorm
           2. q/k/v projections (split-K partial sums)
           3. attention prologue: q/k norm + RoPE, v_norm, K/V append into the pages
-          4. paged split-K attention (+ merge)
+          4. paged split-K attention (+ merge, which also writes the o
+             projection's operand blocks)
           5. o projection (partial sums)
           6. post-attn norm-add -> pre-FFN rmsNorm
           7. gate/up -> GELU product
@@ -471,8 +475,9 @@ class BatchDecoder(_SyntheticModel):
                                 self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.pro_params[il],
                                 self.rope_cs[s.is_global(il)], self.rope_rows)
             c.pagedAttnDecode(self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.attn,
-                              self.attn_params[il], self.attn_ws)
-            no = c.matmulSegmentsBatchPartial("q4k", self.attn, [L.wo], [self.o_parts], [H], s.q_dim, B, self.ks_q)
+                              self.attn_params[il], self.attn_ws, ops=self.aops)
+            no = c.matmulSegmentsBatchPartial("q4k", self.attn, [L.wo], [self.o_parts], [H], s.q_dim, B, self.ks_q,
+                                              ops=self.aops)
             c.batchPrep(self.o_parts, no, L.post_attn_norm, self.hidden, L.pre_ffn_norm, self.hidden2, self.xn, H, B,
                         s.eps, ops=self.xops)
             c.gateUpGeluBatch(self.xn, L.wgate, L.wup, self.act, s.ffn, H, B, ops=self.xops)

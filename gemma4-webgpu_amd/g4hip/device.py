@@ -413,9 +413,14 @@ class Context:
         return int(n.value)
 
     def pagedAttnDecode(self, q: Ptr, k_pool: Ptr, v_pool: Ptr, page_table: Ptr, seq_lens: Ptr, out: Ptr,
-                        p: PagedAttnParams, workspace: Buffer) -> None:
-        check(lib().g4_pagedAttnDecode(self.h, _p(q), _p(k_pool), _p(v_pool), _p(page_table), _p(seq_lens),
-                                       _p(out), p, _p(workspace), workspace.nbytes))
+                        p: PagedAttnParams, workspace: Buffer, ops: Ptr = None) -> None:
+        """With `ops`, the output also as the o projection's operand blocks (g4_pagedAttnDecodeOps)."""
+        if ops is None:
+            check(lib().g4_pagedAttnDecode(self.h, _p(q), _p(k_pool), _p(v_pool), _p(page_table), _p(seq_lens),
+                                           _p(out), p, _p(workspace), workspace.nbytes))
+        else:
+            check(lib().g4_pagedAttnDecodeOps(self.h, _p(q), _p(k_pool), _p(v_pool), _p(page_table),
+                                              _p(seq_lens), _p(out), p, _p(workspace), workspace.nbytes, _p(ops)))
 
     def pagedKvStore(self, k_in: Ptr, v_in: Ptr, k_pool: Ptr, v_pool: Ptr, page_table: Ptr, seq_lens: Ptr,
                      p: PagedAttnParams) -> None:

@@ -268,6 +268,15 @@ int g4_pagedAttnDecode_workspace_size(g4_paged_attn_params p, size_t* bytes);
 int g4_pagedAttnDecode(g4_ctx* ctx, const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
                        const int32_t* page_table, const uint32_t* seq_lens, float* output,
                        g4_paged_attn_params p, void* workspace, size_t workspace_bytes);
+/* g4_pagedAttnDecode that also writes its output as the matrix-core operand
+ * blocks of the o projection (ops: g4_batchOperandBytes(num_q_heads *
+ * head_dim, num_seqs) bytes, 16-byte aligned), which g4_matmulSegmentsBatch-
+ * Partial takes so that its workgroups need not rebuild them (an MI355X
+ * hand-off with no reference counterpart). head_dim a multiple of 256,
+ * num_seqs <= 64; ops == NULL is g4_pagedAttnDecode. */
+int g4_pagedAttnDecodeOps(g4_ctx* ctx, const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                          const int32_t* page_table, const uint32_t* seq_lens, float* output,
+                          g4_paged_attn_params p, void* workspace, size_t workspace_bytes, void* ops);
 /* The per-layer attention block of a multi-sequence decode step in one launch
  * (per sequence, the block src/engine.ts:1562-1584 runs for one token):
  * sequence s decodes position seq_lens[s] - 1 (seq_lens already advanced,

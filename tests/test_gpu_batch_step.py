@@ -297,3 +297,57 @@ def test_paged_fused_rejects_bad_shapes(ctx, bdec):
     with pytest.raises(Exception, match="workspace"):
         ctx.pagedAttnDecodeFused(d.q, d.q, d.q, d.layers[0].q_norm, d.layers[0].k_norm, None, d.layers[0].k_cache,
                                  d.layers[0].v_cache, d.page_table, d.seq_lens, d.attn, p, small)
+
+
+def test_attention_writes_o_projection_operands(ctx, bdec):
+    """The paged attention's merge also writes its output as the o
+    projection's matrix-core operand blocks: the f16 hi/lo planes and the
+    scales equal what the prep kernel builds from the same f32 output, the
+    sub-block sums agree to f32 rounding, and the o projection from them
+    matches the one that converts the f32 activations itself."""
+    d, s, B = bdec, bdec.s, bdec.B
+    L = d.layers[1]
+    d.set_lengths(np.array(LENS, np.uint32) + 1)
+    ctx.pagedAttnDecode(d.q, L.k_cache, L.v_cache, d.page_table, d.seq_lens, d.attn, d.attn_params[1], d.attn_ws,
+                        ops=d.aops)
+    got_ops = d.aops.download(np.uint8)
+    ref_ops = ctx.zeros(d.aops.nbytes, np.uint8)
+    ctx.batchPrep(d.attn, 1, None, None, None, None, ctx.empty(B * s.q_dim, np.float32), s.q_dim, B, s.eps,
+                  ops=ref_ops)
+    want = ref_ops.download(np.uint8)
+    ntv = 2 if B > 16 else 1
+    blk = ntv * (8 * 2 * 1024 + 1024 + 64)
+    main, sums = ntv * 8 * 2 * 1024, ntv * 1024
+    g3, w3 = got_ops.reshape(-1, blk), want.reshape(-1, blk)
+    assert g3.shape[0] == s.q_dim // 256
+    live = np.zeros((ntv * 16,), bool)
+    live[:B] = True
+    # main planes: [t][s][h][lane] 16 B, lane = c + 16 q (vector 16 t + c)
+    gm = g3[:, :main].reshape(-1, ntv, 8, 2, 4, 16, 16)
+    wm = w3[:, :main].reshape(-1, ntv, 8, 2, 4, 16, 16)
+    lv = live.reshape(ntv, 16)
+    for t in range(ntv):
+        assert np.array_equal(gm[:, t][:, :, :, :, lv[t]], wm[:, t][:, :, :, :, lv[t]]), t
+    gs = g3[:, main + sums:].reshape(-1, ntv, 16, 4).view(np.float32)
+    ws_ = w3[:, main + sums:].reshape(-1, ntv, 16, 4).view(np.float32)
+    assert np.array_equal(gs[:, :, :, 0][:, lv], ws_[:, :, :, 0][:, lv])
+    # sums: [t][lane] 16 B, lane = c + 16 (s >> 1), 4 halves (3 parts + 0) per sub-block s
+    gsum = g3[:, main:main + sums].reshape(-1, ntv, 4, 16, 16).view(np.float16).reshape(-1, ntv, 4, 16, 2, 4)
+    wsum = w3[:, main:main + sums].reshape(-1, ntv, 4, 16, 16).view(np.float16).reshape(-1, ntv, 4, 16, 2, 4)
+    gsum = gsum.astype(np.float64).sum(-1)
+    wsum = wsum.astype(np.float64).sum(-1)
+    for t in range(ntv):
+        g_, w_ = gsum[:, t][:, :, lv[t]], wsum[:, t][:, :, lv[t]]
+        assert np.allclose(g_, w_, rtol=1e-6, atol=1e-6 * np.abs(w_).max()), t
+    a = ctx.empty(d.ks_q * B * s.hidden, np.float32)
+    b = ctx.empty(d.ks_q * B * s.hidden, np.float32)
+    na = ctx.matmulSegmentsBatchPartial("q4k", d.attn, [L.wo], [a], [s.hidden], s.q_dim, B, d.ks_q, ops=d.aops)
+    nb = ctx.matmulSegmentsBatchPartial("q4k", d.attn, [L.wo], [b], [s.hidden], s.q_dim, B, d.ks_q)
+    A = a.download(np.float32)[:na * B * s.hidden].reshape(na, B, -1).sum(0)
+    Bm = b.download(np.float32)[:nb * B * s.hidden].reshape(nb, B, -1).sum(0)
+    wo = L.wo.download(np.uint8)
+    X = d.attn.download(np.float32).reshape(B, -1)
+    for v in range(B):
+        assert_close(A[v], Bm[v], rel=1e-6, cos=0.99999999, what=f"o with operand blocks, seq {v}")
+        assert_close(A[v], O.matmul(X[v], wo, s.hidden, s.q_dim, "q4k"), what=f"o vs oracle, seq {v}")
+    d.set_lengths(np.array(LENS, np.uint32))
