@@ -409,6 +409,37 @@ def batch_decode(ctx, B, steps, warmup, seed=0, census=False):
     return res
 
 
+def decode_rate(ctx, shape, start, steps, warmup, embed=False, warm=True):
+    """Single-sequence tok/s of the fused step replayed as a HIP graph from
+    position `start` (KV pre-filled up to it). Returns the figures and the
+    decoder's launches per token."""
+    max_seq = (start + warmup + steps + 64 + 255) // 256 * 256
+    t0 = time.time()
+    d = Decoder(ctx, shape, max_seq=max_seq, seed=0, embed=embed)
+    d.fill_kv(start, seed=1)
+    d.set_position(start)
+    ctx.sync()
+    g = d.capture_fused("argmax", warm=warm)
+    for _ in range(warmup):
+        ctx.graph_launch(g)
+    ctx.sync()
+    a = ctx.record()
+    for _ in range(steps):
+        ctx.graph_launch(g)
+    b = ctx.record()
+    ms = ctx.elapsed_ms(a, b) / steps
+    ctx.sync()
+    end = int(d.pos.download(np.uint32)[0])
+    ctx.graph_destroy(g)
+    s = d.s
+    wbytes = s.weight_bytes() + s.lm_head_bytes()
+    res = {"tok_s": round(1000.0 / ms, 1), "us_per_token": round(ms * 1e3, 2), "positions": [start, end],
+           "weight_bytes_per_token": wbytes, "launches_per_token": d.launches_per_step_fused(),
+           "setup_s": round(time.time() - t0, 1)}
+    del d
+    return res
+
+
 def _cpu_threads():
     """Host threads this process may use (the box's CPU share, at most 16)."""
     try:
@@ -604,6 +635,12 @@ def main():
                          "(the launches a profiler should see for config 0)")
     ap.add_argument("--calib-only", action="store_true",
                     help="one 256 MiB streaming read per cache policy, for the HBM counters' calibration")
+    ap.add_argument("--positions", default="4096,32768",
+                    help="comma-separated start positions of extra B=1 decode runs ('' to skip)")
+    ap.add_argument("--pos-steps", type=int, default=100)
+    ap.add_argument("--pos-warmup", type=int, default=10)
+    ap.add_argument("--no-real-layout", action="store_true",
+                    help="skip the decode runs of Gemma-4-E2B's own layer layout")
     ap.add_argument("--batch-steps", type=int, default=30)
     ap.add_argument("--batch-warmup", type=int, default=5)
     ap.add_argument("--batch-sweep", default="1,8,32,64",
@@ -668,12 +705,27 @@ def main():
     if not args.eager:
         ctx.graph_destroy(graph)
 
+    # the same step from longer contexts, and Gemma-4-E2B's own layer layout
+    # (head dim 512 on the global layers, FFN 12288 and shared KV on layers
+    # 15..34) with the embedding lookup of the sampled token in the step
+    positions = {}
+    for start in [int(x) for x in args.positions.split(",") if x.strip()]:
+        positions[f"start{start}"] = decode_rate(ctx, E2BShape(), start, args.pos_steps, args.pos_warmup)
+        log(f"decode from position {start}: {positions[f'start{start}']}")
+    real = {}
+    if not args.no_real_layout:
+        for start in (START_POS, 4096):
+            real[f"start{start}"] = decode_rate(ctx, E2BShape.real(), start, args.pos_steps, args.pos_warmup,
+                                                embed=True)
+            log(f"real E2B layout from position {start}: {real[f'start{start}']}")
+
     batch = {}
     for B in [int(b) for b in args.batch_sweep.split(",") if b.strip()]:
         batch[f"B={B}"] = batch_decode(ctx, B, args.batch_steps, args.batch_warmup, census=(B == 32 and not
                                                                                               args.no_census))
     if args.no_census:
         print(json.dumps({"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": ms_step,
+                          "decode_from_position": positions, "real_e2b_layout": real,
                           "batch_decode": batch}), flush=True)
         return
     census = kernel_census(ctx, dec, args.census_reps)
@@ -725,6 +777,8 @@ def main():
         "cpu_baseline": cpu,
         "q4k_gemv_config0": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in g0.items()},
         "kernel_census_us": {k: round(per_step[k], 2) for k in per_step},
+        "decode_from_position": positions,
+        "real_e2b_layout": real,
         "batch_decode": batch,
         "attention_decode": attn3,
         "lm_head_sampling": head,

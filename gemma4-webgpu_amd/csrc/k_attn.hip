@@ -276,13 +276,16 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
   }
   float kx[FUSE ? KE : 1], vx[FUSE ? KE : 1], kwt[FUSE ? KE : 1], qwt[FUSE ? QE : 1];
   uint16_t rfb = 0;
+  // without k_in the layer reads a cache another layer has already written
+  // this position's row into: no row is formed, stored or patched
+  const bool own_row = !FUSE || a.k_in != nullptr;
   if constexpr (FUSE) {
 #pragma unroll
     for (int k = 0; k < KE; ++k) {
       const int i = tid + k * NT, ic = i < HD ? i : 0;
-      kx[k] = a.k_in[((size_t)seq * a.nkh + kvh) * HD + ic];
-      vx[k] = a.v_in[((size_t)seq * a.nkh + kvh) * HD + ic];
-      kwt[k] = g4d::f16_bits_to_f32(a.k_w[ic]);
+      kx[k] = own_row ? a.k_in[((size_t)seq * a.nkh + kvh) * HD + ic] : 0.f;
+      vx[k] = own_row ? a.v_in[((size_t)seq * a.nkh + kvh) * HD + ic] : 0.f;
+      kwt[k] = own_row ? g4d::f16_bits_to_f32(a.k_w[ic]) : 0.f;
     }
 #pragma unroll
     for (int k = 0; k < QE; ++k) qwt[k] = g4d::f16_bits_to_f32(a.q_w[(tid + k * NT) % HD]);
@@ -323,7 +326,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
     // angle in f32 (within 2 ulp of the rounded exact values).
     if (tid < HD / 2) cs_s[tid] = rope_cos_sin(a.theta, a.apply_divisor, rfb, tid, HD, pos);
     static_assert((G * HD) % NT == 0 && HD >= 256, "fused form: whole q heads per thread stride");
-    const bool owner = b1 == L;  // this chunk holds the current position
+    const bool owner = b1 == L && own_row;  // this chunk holds the current position and forms its row
     // Where the row is written. Paged: the page id must be in the pool and
     // the length unclamped; otherwise nothing is stored (the attention still
     // uses the row), as g4_pagedKvStore does for a bad table entry.
@@ -1089,7 +1092,11 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
   if (chunk >= nch) return;  // (uniform) past the live chunks
   const uint32_t c0 = chunk * CH, cend = min(n, c0 + CH), last = wstart + cend - 1;
   const uint32_t nst = (cend - c0 + MQ_STEP - 1) / MQ_STEP;
-  const bool owner = cend == n;  // this chunk ends at the current position
+  // this chunk ends at the current position and forms its row (without
+  // k_raw the layer reads a cache another layer has already written the
+  // row into: nothing is formed, stored or patched)
+  const bool own_row = a.k_raw != nullptr;
+  const bool owner = cend == n && own_row;
   // thread -> (head, 4 dims of each RoPE half) for q, the partial and the merge
   const int th = tid >> 5, td = 4 * (tid & 31);
 
@@ -1127,8 +1134,9 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
   const float* qg = a.q_raw + (size_t)(kvh * MQ_G + th) * MQ_HD + td;
   const float4 q0 = *(const float4*)qg, q1 = *(const float4*)(qg + MQ_HD / 2);
   const uint2 w0 = *(const uint2*)(a.q_w + td), w1 = *(const uint2*)(a.q_w + MQ_HD / 2 + td);
-  const float kx = a.k_raw[(size_t)kvh * MQ_HD + tid], vx = a.v_raw[(size_t)kvh * MQ_HD + tid];
-  const float kw = g4d::f16_bits_to_f32(a.k_w[tid]);
+  const float kx = own_row ? a.k_raw[(size_t)kvh * MQ_HD + tid] : 0.f;
+  const float vx = own_row ? a.v_raw[(size_t)kvh * MQ_HD + tid] : 0.f;
+  const float kw = own_row ? g4d::f16_bits_to_f32(a.k_w[tid]) : 0.f;
   const uint16_t rfb = a.rope_freqs[tid & (MQ_HD / 2 - 1)];
   const float2 cst =
       a.rope_cs ? a.rope_cs[(size_t)pos * (MQ_HD / 2) + (tid & (MQ_HD / 2 - 1))] : make_float2(1.f, 0.f);
@@ -1951,9 +1959,12 @@ int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, 
   G4_ENTER(ctx);
   G4_REQUIRE(!rope_cs || rope_rows >= p.max_seq_len, "g4_attnDecodeFusedWarm: RoPE table of %u rows < max_seq_len %u",
              rope_rows, p.max_seq_len);
-  G4_REQUIRE(q_raw && k_raw && v_raw && q_norm_w && k_norm_w && k_cache && v_cache && output && workspace &&
-                 position_dev,
+  G4_REQUIRE(q_raw && q_norm_w && k_cache && v_cache && output && workspace && position_dev,
              "g4_attnDecodeFused: null buffer");
+  // k_raw = v_raw = k_norm_w = null: the caches already hold this position's
+  // row (a layer reading its producer layer's cache)
+  G4_REQUIRE(k_raw ? (v_raw && k_norm_w) : (!v_raw && !k_norm_w),
+             "g4_attnDecodeFused: k_raw, v_raw and k_norm_w are all given or all null");
   G4_REQUIRE(nregions >= 0 && nregions <= kMaxWarm && (nregions == 0 || regions),
              "g4_attnDecodeFusedWarm: 0..%d warm regions", kMaxWarm);
   for (int i = 0; i < nregions; ++i) {
@@ -2096,9 +2107,10 @@ int g4_pagedAttnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw,
                             uint16_t* k_pool, uint16_t* v_pool, const int32_t* page_table, const uint32_t* seq_lens,
                             float* output, g4_paged_attn_fused_params p, void* workspace, size_t workspace_bytes) {
   G4_ENTER(ctx);
-  G4_REQUIRE(q_raw && k_raw && v_raw && q_norm_w && k_norm_w && k_pool && v_pool && page_table && seq_lens &&
-                 output && workspace,
+  G4_REQUIRE(q_raw && q_norm_w && k_pool && v_pool && page_table && seq_lens && output && workspace,
              "g4_pagedAttnDecodeFused: null buffer");
+  G4_REQUIRE(k_raw ? (v_raw && k_norm_w) : (!v_raw && !k_norm_w),
+             "g4_pagedAttnDecodeFused: k_raw, v_raw and k_norm_w are all given or all null");
   G4_REQUIRE(!p.apply_divisor || rope_freqs, "g4_pagedAttnDecodeFused: apply_divisor needs rope_freqs");
   const g4_paged_attn_params ap = fused_attn_part(p);
   AttnArgs a{};
@@ -2132,9 +2144,13 @@ int g4_pagedAttnPrologue(g4_ctx* ctx, const float* q_parts, const float* k_parts
   G4_ENTER(ctx);
   G4_REQUIRE(!rope_cs || rope_rows >= p.max_seq_len, "g4_pagedAttnPrologue: RoPE table of %u rows < max_seq_len %u",
              rope_rows, p.max_seq_len);
-  G4_REQUIRE(q_parts && k_parts && v_parts && q_norm_w && k_norm_w && q_out && k_pool && v_pool && page_table &&
-                 seq_lens && nparts >= 1,
+  G4_REQUIRE(q_parts && q_norm_w && q_out && page_table && seq_lens && nparts >= 1,
              "g4_pagedAttnPrologue: null buffer or no parts");
+  // k_parts = v_parts = null: q only (a layer reading its producer layer's
+  // pool appends no row); the pools and k_norm_w are then not used
+  const bool kv = k_parts != nullptr;
+  G4_REQUIRE(kv ? (v_parts && k_norm_w && k_pool && v_pool) : !v_parts,
+             "g4_pagedAttnPrologue: k_parts, v_parts, k_norm_w and the pools go together");
   G4_REQUIRE(((uintptr_t)rope_cs & 7) == 0, "g4_pagedAttnPrologue: rope_cs must be 8-byte aligned");
   G4_REQUIRE(!p.apply_divisor || rope_freqs, "g4_pagedAttnPrologue: apply_divisor needs rope_freqs");
   G4_REQUIRE(p.num_seqs > 0 && p.num_seqs <= 65535 && p.num_q_heads > 0 && p.num_kv_heads > 0,
@@ -2170,7 +2186,7 @@ int g4_pagedAttnPrologue(g4_ctx* ctx, const float* q_parts, const float* k_parts
   a.num_pages = p.num_pages;
   a.cap = p.max_seq_len;
   a.rope_cs = (const float2*)rope_cs;
-  hipLaunchKernelGGL(attn_prologue_kernel, dim3(p.num_q_heads + p.num_kv_heads, p.num_seqs), dim3(NT), 0,
+  hipLaunchKernelGGL(attn_prologue_kernel, dim3(p.num_q_heads + (kv ? p.num_kv_heads : 0u), p.num_seqs), dim3(NT), 0,
                      ctx->stream, a);
   G4_LAUNCHED(ctx, "attn_prologue");
   return G4_OK;

@@ -720,9 +720,10 @@ int mm_launch(g4_ctx* ctx, const MmArgs& a, uint32_t groups) {
   return G4_OK;
 }
 
-// Prebuilt operands come from the norm prologue, whose widths are 1536 and 2048.
+// Prebuilt operands come from the norm prologue (widths 1536 and 2048) and
+// from the attention's merge (the q widths 2048 and, head dim 512, 4096).
 template <int BPR>
-constexpr bool ops_width() { return BPR == 6 || BPR == 8; }
+constexpr bool ops_width() { return BPR == 6 || BPR == 8 || BPR == 16; }
 
 template <int QT, int BPR, int MODE>
 int mm_ntv(g4_ctx* ctx, const MmArgs& a, uint32_t groups) {

@@ -23,11 +23,24 @@ vectors through the matrix-core kernel (each weight tile read once per
 step), and attention reads each sequence's K/V from a paged f16 pool
 through a per-sequence page table.
 
-Shapes follow the layer the benchmark is quoted on: hidden 1536, 8 query heads
-and 1 KV head of dim 256, FFN 6144 (Q4_K q/k/v/o/gate/up, Q6_K down), tied
-Q6_K LM head [262144 x 1536], softcap 30; layers {4,9,...,34} attend globally
-(theta 1e6, proportional RoPE table), the rest use a 512-token window
-(theta 1e4) (src/config/gemma4-e2b.ts:16-63).
+Two layer layouts (src/config/gemma4-e2b.ts:16-63):
+
+* the default ``E2BShape()`` repeats the layer the benchmark is quoted on:
+  hidden 1536, 8 query heads and 1 KV head of dim 256, FFN 6144 (Q4_K
+  q/k/v/o/gate/up, Q6_K down), tied Q6_K LM head [262144 x 1536], softcap 30;
+  layers {4,9,...,34} attend globally (theta 1e6, proportional RoPE table),
+  the rest use a 512-token window (theta 1e4);
+* ``E2BShape.real()`` is Gemma-4-E2B's own layout on top of that: global
+  layers have head dim 512 (of whose 256 RoPE pairs the table rotates the
+  first 64), layers 15..34 have FFN 12288 and compute no K/V of their own:
+  each reads the cache of the last of layers 0..14 of its attention kind
+  (13 local, 14 global) (src/config/gemma4-e2b.ts:151-180,
+  src/engine.ts:1149-1152 and 1541-1583).
+
+With ``embed=True`` a step starts from the embedding row of the token the
+previous step sampled (src/engine.ts:1505-1514 and 1720-1725: the argmax
+result is copied into the embedding lookup's token): the device-side token
+feeds the next step without a host round trip.
 """
 from __future__ import annotations
 
@@ -47,8 +60,8 @@ class E2BShape:
     hidden: int = 1536
     n_q_heads: int = 8
     n_kv_heads: int = 1
-    head_dim: int = 256
-    ffn: int = 6144
+    head_dim: int = 256          # local layers (and global ones when head_dim_global is 0)
+    ffn: int = 6144              # layers below n_unshared (all layers when ffn_shared is 0)
     vocab: int = 262144
     n_layers: int = 35
     eps: float = 1e-6
@@ -57,23 +70,73 @@ class E2BShape:
     theta_global: float = 1e6
     softcap: float = 30.0
     global_layers: tuple = (4, 9, 14, 19, 24, 29, 34)
+    head_dim_global: int = 0     # head dim of the global layers (0: head_dim)
+    ffn_shared: int = 0          # FFN width of layers >= n_unshared (0: ffn)
+    n_unshared: int = 0          # layers >= n_unshared read a producer's KV cache (0: every layer owns its cache)
+
+    @classmethod
+    def real(cls, **kw) -> "E2BShape":
+        """Gemma-4-E2B's layer layout (src/config/gemma4-e2b.ts:16-63)."""
+        return cls(**{"head_dim_global": 512, "ffn_shared": 12288, "n_unshared": 15, **kw})
 
     @property
     def q_dim(self) -> int:
-        return self.n_q_heads * self.head_dim
+        """The widest layer's q width (buffer sizing)."""
+        return self.n_q_heads * self.max_head_dim
 
     @property
     def kv_dim(self) -> int:
-        return self.n_kv_heads * self.head_dim
+        return self.n_kv_heads * self.max_head_dim
+
+    @property
+    def max_head_dim(self) -> int:
+        return max(self.head_dim, self.head_dim_global)
+
+    @property
+    def max_ffn(self) -> int:
+        return max(self.ffn, self.ffn_shared)
 
     def is_global(self, il: int) -> bool:
         return il in self.global_layers
 
-    def layer_weight_bytes(self) -> int:
-        H, Q, KV, I = self.hidden, self.q_dim, self.kv_dim, self.ffn
-        q4 = (Q * H + 2 * KV * H + H * Q + 2 * I * H) // 256 * Q4K_BYTES
+    def hd(self, il: int) -> int:
+        """getHeadDim (src/types.ts:79-81)."""
+        return self.head_dim_global if self.is_global(il) and self.head_dim_global else self.head_dim
+
+    def q_dim_of(self, il: int) -> int:
+        return self.n_q_heads * self.hd(il)
+
+    def kv_dim_of(self, il: int) -> int:
+        return self.n_kv_heads * self.hd(il)
+
+    def ffn_of(self, il: int) -> int:
+        """getIntermediateSize (src/types.ts:84-86)."""
+        return self.ffn_shared if self.ffn_shared and self.n_unshared and il >= self.n_unshared else self.ffn
+
+    def producer(self, il: int) -> int:
+        """The layer whose KV cache layer `il` reads: itself below n_unshared,
+        else the last unshared layer of its attention kind
+        (computeKvProducerMap, src/config/gemma4-e2b.ts:159-180)."""
+        if not self.n_unshared or il < self.n_unshared:
+            return il
+        same = [j for j in range(min(self.n_unshared, self.n_layers)) if self.is_global(j) == self.is_global(il)]
+        if not same:
+            raise ValueError(f"layer {il}: no unshared layer of its attention kind")
+        return same[-1]
+
+    def is_producer(self, il: int) -> bool:
+        return self.producer(il) == il
+
+    def layer_weight_bytes(self, il: int = 0) -> int:
+        H, Q, KV, I = self.hidden, self.q_dim_of(il), self.kv_dim_of(il), self.ffn_of(il)
+        kv = 2 * KV * H if self.is_producer(il) else 0
+        q4 = (Q * H + kv + H * Q + 2 * I * H) // 256 * Q4K_BYTES
         q6 = (H * I) // 256 * Q6K_BYTES
         return q4 + q6
+
+    def weight_bytes(self) -> int:
+        """Bytes of every layer's matrices (the LM head apart)."""
+        return sum(self.layer_weight_bytes(il) for il in range(self.n_layers))
 
     def lm_head_bytes(self) -> int:
         return self.vocab * self.hidden // 256 * Q6K_BYTES
@@ -82,8 +145,8 @@ class E2BShape:
 @dataclass
 class LayerWeights:
     wq: Buffer
-    wk: Buffer
-    wv: Buffer
+    wk: Optional[Buffer]   # None in a layer that reads a producer's cache
+    wv: Optional[Buffer]
     wo: Buffer
     wgate: Buffer
     wup: Buffer
@@ -93,18 +156,19 @@ class LayerWeights:
     pre_ffn_norm: Buffer
     post_ffn_norm: Buffer
     q_norm: Buffer
-    k_norm: Buffer
-    k_cache: Buffer
+    k_norm: Optional[Buffer]
+    k_cache: Buffer        # the producer's cache in a layer that reads one
     v_cache: Buffer
 
 
 class _SyntheticModel:
     """Seeded synthetic E2B-shaped weights, generated on the device. Each
-    layer's k_cache / v_cache is whatever `kv(il)` returns (dense caches or
-    paged pools)."""
+    producer layer's k_cache / v_cache is whatever `kv(il)` returns (dense
+    caches or paged pools); a layer that reads a producer's cache holds that
+    producer's buffers and has no k/v projections or k_norm."""
 
     def _build_weights(self, ctx: Context, shape: Optional[E2BShape], n_layers: Optional[int], seed: int,
-                       lm_head: bool, kv) -> None:
+                       lm_head: bool, kv, embed: bool = False) -> None:
         self.ctx = ctx
         self.s = shape or E2BShape()
         if n_layers is not None:
@@ -114,19 +178,31 @@ class _SyntheticModel:
         self._tid = 0
         self.layers: List[LayerWeights] = []
         for il in range(s.n_layers):
-            kc, vc = kv(il)
+            Q, KV, I, hd = s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il), s.hd(il)
+            prod = s.is_producer(il)
+            if prod:
+                kc, vc = kv(il)
+            else:
+                src = self.layers[s.producer(il)]
+                kc, vc = src.k_cache, src.v_cache
             self.layers.append(LayerWeights(
-                wq=self._q4k(s.q_dim, s.hidden), wk=self._q4k(s.kv_dim, s.hidden), wv=self._q4k(s.kv_dim, s.hidden),
-                wo=self._q4k(s.hidden, s.q_dim), wgate=self._q4k(s.ffn, s.hidden), wup=self._q4k(s.ffn, s.hidden),
-                wdown=self._q6k(s.hidden, s.ffn),
+                wq=self._q4k(Q, s.hidden), wk=self._q4k(KV, s.hidden) if prod else None,
+                wv=self._q4k(KV, s.hidden) if prod else None,
+                wo=self._q4k(s.hidden, Q), wgate=self._q4k(I, s.hidden), wup=self._q4k(I, s.hidden),
+                wdown=self._q6k(s.hidden, I),
                 attn_norm=self._f16(s.hidden), post_attn_norm=self._f16(s.hidden), pre_ffn_norm=self._f16(s.hidden),
-                post_ffn_norm=self._f16(s.hidden), q_norm=self._f16(s.head_dim), k_norm=self._f16(s.head_dim),
+                post_ffn_norm=self._f16(s.hidden), q_norm=self._f16(hd), k_norm=self._f16(hd) if prod else None,
                 k_cache=kc, v_cache=vc))
         self.final_norm = self._f16(s.hidden)
         self.lm_head = self._q6k(s.vocab, s.hidden) if lm_head else None
-        # proportional RoPE divisor table: 1.0 on the first quarter of the pairs,
-        # 1e30 (+Inf in f16) after (src/engine.ts:522-537)
-        half = s.head_dim // 2
+        # the f16 token embedding table [vocab x hidden] (shaders/embedding_lookup.wgsl)
+        self.embedding = None
+        if embed:
+            self.embedding = ctx.empty(s.vocab * s.hidden, np.uint16)
+            ctx.fill_normal_f16(self.embedding, s.vocab * s.hidden, self._seed(), 0.0, 0.03)
+        # proportional RoPE divisor table over the global layers' pairs: 1.0 on
+        # the first quarter, 1e30 (+Inf in f16) after (src/engine.ts:522-537)
+        half = s.hd(s.global_layers[0]) // 2 if s.global_layers else s.head_dim // 2
         table = np.where(np.arange(half) < half // 4, 1.0, np.inf).astype(np.float16)
         self.rope_freqs = ctx.from_numpy(table.view(np.uint16))
 
@@ -152,9 +228,9 @@ class _SyntheticModel:
         s, out = self.s, {}
         self.rope_rows = rows
         for glob in (False, True):
-            t = self.ctx.empty(rows * s.head_dim, np.float32)
-            self.ctx.ropeTable(s.theta_global if glob else s.theta_local, int(glob), self.rope_freqs, s.head_dim,
-                               rows, t)
+            hd = (s.head_dim_global or s.head_dim) if glob else s.head_dim
+            t = self.ctx.empty(rows * hd, np.float32)
+            self.ctx.ropeTable(s.theta_global if glob else s.theta_local, int(glob), self.rope_freqs, hd, rows, t)
             out[glob] = t
         return out
 
@@ -166,25 +242,26 @@ class _SyntheticModel:
 
 class Decoder(_SyntheticModel):
     def __init__(self, ctx: Context, shape: Optional[E2BShape] = None, max_seq: int = 4096, seed: int = 0,
-                 n_layers: Optional[int] = None, lm_head: bool = True):
+                 n_layers: Optional[int] = None, lm_head: bool = True, embed: bool = False):
         self.max_seq = max_seq
-        kvn = max_seq * (shape or E2BShape()).kv_dim
         self._build_weights(ctx, shape, n_layers, seed, lm_head,
-                            lambda il: (ctx.zeros(kvn, np.uint16), ctx.zeros(kvn, np.uint16)))
+                            lambda il: (ctx.zeros(max_seq * self.s.kv_dim_of(il), np.uint16),
+                                        ctx.zeros(max_seq * self.s.kv_dim_of(il), np.uint16)), embed=embed)
         s = self.s
         f32 = np.float32
+        Q, I = s.q_dim, s.max_ffn
         self.hidden = ctx.empty(s.hidden, f32)
         self.hidden2 = ctx.empty(s.hidden, f32)
         self.normed = ctx.empty(s.hidden, f32)
-        self.q = ctx.empty(s.q_dim, f32)
+        self.q = ctx.empty(Q, f32)
         self.k = ctx.empty(s.kv_dim, f32)
         self.v = ctx.empty(s.kv_dim, f32)
-        self.attn = ctx.empty(s.q_dim, f32)
+        self.attn = ctx.empty(Q, f32)
         self.o = ctx.empty(s.hidden, f32)
-        self.gate = ctx.empty(s.ffn, f32)
-        self.up = ctx.empty(s.ffn, f32)
-        self.act = ctx.empty(s.ffn, f32)
-        self.act_digits = ctx.empty(ctx.digits_bytes(s.ffn), np.uint8)  # `act` as the down launch reads it
+        self.gate = ctx.empty(I, f32)
+        self.up = ctx.empty(I, f32)
+        self.act = ctx.empty(I, f32)
+        self.act_digits = ctx.empty(ctx.digits_bytes(I), np.uint8)  # `act` as the down launch reads it
         self.down = ctx.empty(s.hidden, f32)
         self.logits = ctx.empty(s.vocab, f32)
         self.scores = ctx.empty(s.n_q_heads * max_seq, f32)
@@ -195,10 +272,10 @@ class Decoder(_SyntheticModel):
         for il in range(s.n_layers):
             glob = s.is_global(il)
             self.attn_params.append(ctx.attn_fused_params(
-                s.n_q_heads, s.n_kv_heads, s.head_dim, max_seq, 0 if glob else s.window, s.eps,
+                s.n_q_heads, s.n_kv_heads, s.hd(il), max_seq, 0 if glob else s.window, s.eps,
                 s.theta_global if glob else s.theta_local, int(glob)))
-        ws = max(max(ctx.attn_workspace_bytes(s.n_q_heads, s.n_kv_heads, s.head_dim, max_seq, w)
-                     for w in (0, s.window)),
+        ws = max(max(ctx.attn_workspace_bytes(s.n_q_heads, s.n_kv_heads, s.hd(il), max_seq, w)
+                     for il in range(s.n_layers) for w in (0, s.window)),
                  max(ctx.attn_fused_workspace_bytes(p) for p in self.attn_params))
         # split-K partials + arrival counters; zeroed once, the kernels keep the counters zeroed
         self.attn_ws = ctx.zeros(ws, np.uint8)
@@ -206,50 +283,63 @@ class Decoder(_SyntheticModel):
         # launch, read into the L2 caches by that launch (the o projection's
         # 1.8 MB arrive in time on their own: measured no faster from L2)
         self.rope_cs = self._rope_tables(max_seq)
-        self.warm = [[ctx.matmulWarmRegion("q4k", s.ffn, s.hidden, L.wgate),
-                      ctx.matmulWarmRegion("q4k", s.ffn, s.hidden, L.wup),
-                      ctx.matmulWarmRegion("q6k", s.hidden, s.ffn, L.wdown)] for L in self.layers]
+        self.warm = [[ctx.matmulWarmRegion("q4k", s.ffn_of(il), s.hidden, L.wgate),
+                      ctx.matmulWarmRegion("q4k", s.ffn_of(il), s.hidden, L.wup),
+                      ctx.matmulWarmRegion("q6k", s.hidden, s.ffn_of(il), L.wdown)]
+                     for il, L in enumerate(self.layers)]
         ctx.fill_normal_f32(self.hidden, s.hidden, self._seed(), 0.0, 1.0)
         ctx.sync()
 
     def fill_kv(self, length: int, seed: int = 1) -> None:
-        """Synthetic cached K/V ~ N(0,1) for positions [0, length)."""
-        n = length * self.s.kv_dim
+        """Synthetic cached K/V ~ N(0,1) for positions [0, length) of every
+        cache (the producer layers')."""
         for il, L in enumerate(self.layers):
+            if not self.s.is_producer(il):
+                continue
+            n = length * self.s.kv_dim_of(il)
             self.ctx.fill_normal_f16(L.k_cache, n, splitmix64(seed, 2 * il), 0.0, 1.0)
             self.ctx.fill_normal_f16(L.v_cache, n, splitmix64(seed, 2 * il + 1), 0.0, 1.0)
 
     def set_position(self, pos: int) -> None:
         self.pos.upload(np.array([pos], np.uint32))
 
+    def set_token(self, token: int) -> None:
+        self.token.upload(np.array([token], np.uint32))
+
     # ---- the reference's per-key sequence ----------------------------------
     def step_reference(self, position: int, sample: str = "argmax") -> None:
         c, s = self.ctx, self.s
         seq_len = position + 1
+        if self.embedding is not None:
+            c.embeddingLookup(self.embedding, s.vocab, self.hidden, s.hidden, token_dev=self.token)
         for il, L in enumerate(self.layers):
             glob = s.is_global(il)
             theta = s.theta_global if glob else s.theta_local
             window = 0 if glob else s.window
+            hd, Q, KV, I = s.hd(il), s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il)
+            prod = s.is_producer(il)
             c.rmsNorm(self.hidden, L.attn_norm, self.normed, s.hidden, s.eps)
-            c.matmulQuant(self.normed, L.wq, self.q, s.q_dim, s.hidden)
-            c.matmulQuant(self.normed, L.wk, self.k, s.kv_dim, s.hidden)
-            c.matmulQuant(self.normed, L.wv, self.v, s.kv_dim, s.hidden)
-            c.perHeadRmsNormNoWeight(self.v, s.n_kv_heads, s.head_dim, s.eps)
-            c.fusedPerHeadNormRope(self.q, L.q_norm, s.n_q_heads, s.head_dim, s.eps, position, theta, int(glob),
+            c.matmulQuant(self.normed, L.wq, self.q, Q, s.hidden)
+            if prod:
+                c.matmulQuant(self.normed, L.wk, self.k, KV, s.hidden)
+                c.matmulQuant(self.normed, L.wv, self.v, KV, s.hidden)
+                c.perHeadRmsNormNoWeight(self.v, s.n_kv_heads, hd, s.eps)
+            c.fusedPerHeadNormRope(self.q, L.q_norm, s.n_q_heads, hd, s.eps, position, theta, int(glob),
                                    self.rope_freqs)
-            c.fusedPerHeadNormRope(self.k, L.k_norm, s.n_kv_heads, s.head_dim, s.eps, position, theta, int(glob),
-                                   self.rope_freqs)
-            c.kvCacheStore(self.k, self.v, L.k_cache, L.v_cache, s.n_kv_heads, s.head_dim, position, self.max_seq)
-            c.attnScore(self.q, L.k_cache, self.scores, s.n_q_heads, s.n_kv_heads, s.head_dim, seq_len, 1.0, window)
+            if prod:
+                c.fusedPerHeadNormRope(self.k, L.k_norm, s.n_kv_heads, hd, s.eps, position, theta, int(glob),
+                                       self.rope_freqs)
+                c.kvCacheStore(self.k, self.v, L.k_cache, L.v_cache, s.n_kv_heads, hd, position, self.max_seq)
+            c.attnScore(self.q, L.k_cache, self.scores, s.n_q_heads, s.n_kv_heads, hd, seq_len, 1.0, window)
             c.softmax(self.scores, s.n_q_heads, seq_len)
-            c.attnOutput(self.scores, L.v_cache, self.attn, s.n_q_heads, s.n_kv_heads, s.head_dim, seq_len)
-            c.matmulQuant(self.attn, L.wo, self.o, s.hidden, s.q_dim)
+            c.attnOutput(self.scores, L.v_cache, self.attn, s.n_q_heads, s.n_kv_heads, hd, seq_len)
+            c.matmulQuant(self.attn, L.wo, self.o, s.hidden, Q)
             c.fusedNormAdd(self.o, L.post_attn_norm, self.hidden, self.hidden2, s.hidden, s.eps)
             c.rmsNorm(self.hidden2, L.pre_ffn_norm, self.normed, s.hidden, s.eps)
-            c.matmulQuantMR4(self.normed, L.wgate, self.gate, s.ffn, s.hidden)
-            c.matmulQuantMR4(self.normed, L.wup, self.up, s.ffn, s.hidden)
-            c.geluMul(self.gate, self.up, self.act, s.ffn)
-            c.matmulQuant(self.act, L.wdown, self.down, s.hidden, s.ffn, "q6k")
+            c.matmulQuantMR4(self.normed, L.wgate, self.gate, I, s.hidden)
+            c.matmulQuantMR4(self.normed, L.wup, self.up, I, s.hidden)
+            c.geluMul(self.gate, self.up, self.act, I)
+            c.matmulQuant(self.act, L.wdown, self.down, s.hidden, I, "q6k")
             c.fusedNormAdd(self.down, L.post_ffn_norm, self.hidden2, self.hidden, s.hidden, s.eps)
         self._head(sample)
 
@@ -284,12 +374,21 @@ class Decoder(_SyntheticModel):
         sampling), which a second launch reduces to the 256 pairs. With `warm`, each attention launch also
         reads the gate/up and down weights of its layer into the L2 caches
         (on the CUs the attention leaves idle).
+        A layer that reads a producer's cache projects q only, and its
+        attention launch forms and stores no K/V row. With the embedding
+        table, an embedding lookup of the device-side token (the previous
+        step's sample) starts the step.
         """
         c, s = self.ctx, self.s
+        if self.embedding is not None:
+            c.embeddingLookup(self.embedding, s.vocab, self.hidden, s.hidden, token_dev=self.token)
         for il, L in enumerate(self.layers):
-            outs = [self.q, self.k, self.v]
-            ws = [L.wq, L.wk, L.wv]
-            rows = [s.q_dim, s.kv_dim, s.kv_dim]
+            Q, KV, I = s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il)
+            prod = s.is_producer(il)
+            if prod:
+                outs, ws, rows = [self.q, self.k, self.v], [L.wq, L.wk, L.wv], [Q, KV, KV]
+            else:
+                outs, ws, rows = [self.q], [L.wq], [Q]
             if il == 0:
                 c.normAddMatmulSegments("q4k", self.hidden, L.attn_norm, None, None, None, ws, outs, rows,
                                         s.hidden, s.eps)
@@ -297,13 +396,14 @@ class Decoder(_SyntheticModel):
                 prev = self.layers[il - 1]
                 c.normAddMatmulSegments("q4k", self.down, prev.post_ffn_norm, self.hidden2, L.attn_norm,
                                         self.hidden, ws, outs, rows, s.hidden, s.eps)
-            c.attnDecodeFusedWarm(self.q, self.k, self.v, L.q_norm, L.k_norm, self.rope_freqs, L.k_cache,
-                                  L.v_cache, self.attn, self.attn_params[il], self.attn_ws, self.pos,
-                                  self.warm[il] if warm else [], self.rope_cs[s.is_global(il)], self.rope_rows)
-            c.matmulQuant(self.attn, L.wo, self.o, s.hidden, s.q_dim)
+            c.attnDecodeFusedWarm(self.q, self.k if prod else None, self.v if prod else None, L.q_norm, L.k_norm,
+                                  self.rope_freqs, L.k_cache, L.v_cache, self.attn, self.attn_params[il],
+                                  self.attn_ws, self.pos, self.warm[il] if warm else [],
+                                  self.rope_cs[s.is_global(il)], self.rope_rows)
+            c.matmulQuant(self.attn, L.wo, self.o, s.hidden, Q)
             c.normAddGateUpGeluDigits_q4k(self.o, L.post_attn_norm, self.hidden, L.pre_ffn_norm, L.wgate, L.wup,
-                                          self.hidden2, self.act, self.act_digits, s.ffn, s.hidden, s.eps)
-            c.matmulQuantDigits_q6k(self.act_digits, L.wdown, self.down, s.hidden, s.ffn)
+                                          self.hidden2, self.act, self.act_digits, I, s.hidden, s.eps)
+            c.matmulQuantDigits_q6k(self.act_digits, L.wdown, self.down, s.hidden, I)
         last = self.layers[-1]
         if self.lm_head is not None:
             if sample == "argmax":
@@ -327,10 +427,15 @@ class Decoder(_SyntheticModel):
         return g
 
     def launches_per_step_fused(self) -> int:
-        """Kernel launches of step_fused with argmax sampling: 5 per layer, the
-        head with its argmax candidates (1) and their reduction, which also
-        advances the position (1)."""
-        return 5 * self.s.n_layers + 2
+        """Kernel launches of step_fused with argmax sampling: 5 per layer (6
+        where the attention takes a launch and a merge: head dim 512, or a
+        window longer than the one-launch plan's), the head with its argmax
+        candidates (1) and their reduction, which also advances the position
+        (1), and the embedding lookup when there is a table."""
+        s, n = self.s, 2 + (self.embedding is not None)
+        for il in range(s.n_layers):
+            n += 5 + (not self.ctx.attn_fused_single_launch(self.attn_params[il]))
+        return n
 
 
 class BatchDecoder(_SyntheticModel):
@@ -372,9 +477,10 @@ class BatchDecoder(_SyntheticModel):
             at += n
         self.page_table_host = table
         self.lens_host = lens.astype(np.uint32)
-        pool = self.num_pages * page_size * s0.kv_dim
+        rows = self.num_pages * page_size
         self._build_weights(ctx, shape, n_layers, seed, lm_head,
-                            lambda il: (ctx.zeros(pool, np.uint16), ctx.zeros(pool, np.uint16)))
+                            lambda il: (ctx.zeros(rows * self.s.kv_dim_of(il), np.uint16),
+                                        ctx.zeros(rows * self.s.kv_dim_of(il), np.uint16)))
         s, B, f32 = self.s, self.B, np.float32
         self.page_table = ctx.from_numpy(table)
         self.seq_lens = ctx.from_numpy(self.lens_host)
@@ -383,8 +489,8 @@ class BatchDecoder(_SyntheticModel):
         self.xn = ctx.empty(B * s.hidden, f32)        # normalised input of the next matmul
         self.xops = ctx.empty(ctx.batch_operand_bytes(s.hidden, B), np.uint8)  # its operand blocks
         self.ks_h = s.hidden // 256                    # most K chunks of a matmul over the hidden width
-        self.ks_q = s.q_dim // 256
-        self.ks_f = s.ffn // 256
+        self.ks_q = s.q_dim // 256                     # (over the widest layer's q / FFN width)
+        self.ks_f = s.max_ffn // 256
         self.q_parts = ctx.empty(self.ks_h * B * s.q_dim, f32)
         self.k_parts = ctx.empty(self.ks_h * B * s.kv_dim, f32)
         self.v_parts = ctx.empty(self.ks_h * B * s.kv_dim, f32)
@@ -394,7 +500,7 @@ class BatchDecoder(_SyntheticModel):
         # (written by the attention's merge when a head is whole super-blocks)
         self.aops = ctx.empty(ctx.batch_operand_bytes(s.q_dim, B), np.uint8) if s.head_dim % 256 == 0 else None
         self.o_parts = ctx.empty(self.ks_q * B * s.hidden, f32)
-        self.act = ctx.empty(B * s.ffn, f32)
+        self.act = ctx.empty(B * s.max_ffn, f32)
         self.down_parts = ctx.empty(self.ks_f * B * s.hidden, f32)
         self.logits = ctx.empty(B * s.vocab, f32) if lm_head else None
         self.tokens = ctx.zeros(B, np.uint32)
@@ -404,10 +510,10 @@ class BatchDecoder(_SyntheticModel):
             glob = s.is_global(il)
             window = 0 if glob else s.window
             self.pro_params.append(ctx.paged_fused_params(
-                B, s.n_q_heads, s.n_kv_heads, s.head_dim, page_size, self.max_pages, self.max_seq, self.num_pages,
+                B, s.n_q_heads, s.n_kv_heads, s.hd(il), page_size, self.max_pages, self.max_seq, self.num_pages,
                 window, s.eps, s.theta_global if glob else s.theta_local, int(glob)))
             self.attn_params.append(ctx.paged_params(
-                B, s.n_q_heads, s.n_kv_heads, s.head_dim, page_size, self.max_pages, self.max_seq, self.num_pages,
+                B, s.n_q_heads, s.n_kv_heads, s.hd(il), page_size, self.max_pages, self.max_seq, self.num_pages,
                 1.0, window))
         self.attn_ws = ctx.zeros(max(ctx.paged_workspace_bytes(p) for p in self.attn_params), np.uint8)
         self.rope_cs = self._rope_tables(self.max_seq)
@@ -415,9 +521,11 @@ class BatchDecoder(_SyntheticModel):
         ctx.sync()
 
     def fill_kv(self, seed: int = 1) -> None:
-        """Synthetic cached K/V ~ N(0,1) over every page of every pool."""
-        n = self.num_pages * self.page_size * self.s.kv_dim
+        """Synthetic cached K/V ~ N(0,1) over every page of every pool (the producer layers')."""
         for il, L in enumerate(self.layers):
+            if not self.s.is_producer(il):
+                continue
+            n = self.num_pages * self.page_size * self.s.kv_dim_of(il)
             self.ctx.fill_normal_f16(L.k_cache, n, splitmix64(seed, 2 * il), 0.0, 1.0)
             self.ctx.fill_normal_f16(L.v_cache, n, splitmix64(seed, 2 * il + 1), 0.0, 1.0)
 
@@ -441,7 +549,7 @@ class BatchDecoder(_SyntheticModel):
                 n = int(L) + 1
                 if not s.is_global(il):
                     n = min(n, s.window)
-                total += n * 2 * s.kv_dim * 2
+                total += n * 2 * s.kv_dim_of(il) * 2
         return total
 
     def step(self, sample: str = "argmax") -> None:
@@ -462,26 +570,34 @@ class BatchDecoder(_SyntheticModel):
         c.advanceSeqLens(self.seq_lens, B, 1)
         nd = 0
         for il, L in enumerate(self.layers):
+            Q, KV, I = s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il)
+            prod = s.is_producer(il)
             if il == 0:
                 c.batchPrep(self.hidden, 1, L.attn_norm, None, None, None, self.xn, H, B, s.eps, ops=self.xops)
             else:
                 prev = self.layers[il - 1]
                 c.batchPrep(self.down_parts, nd, prev.post_ffn_norm, self.hidden2, L.attn_norm, self.hidden,
                             self.xn, H, B, s.eps, ops=self.xops)
-            nq = c.matmulSegmentsBatchPartial("q4k", self.xn, [L.wq, L.wk, L.wv],
-                                              [self.q_parts, self.k_parts, self.v_parts],
-                                              [s.q_dim, s.kv_dim, s.kv_dim], H, B, self.ks_h, ops=self.xops)
-            c.pagedAttnPrologue(self.q_parts, self.k_parts, self.v_parts, nq, L.q_norm, L.k_norm, self.rope_freqs,
-                                self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.pro_params[il],
+            if prod:  # a layer reading a producer's pool projects q only and appends no row
+                nq = c.matmulSegmentsBatchPartial("q4k", self.xn, [L.wq, L.wk, L.wv],
+                                                  [self.q_parts, self.k_parts, self.v_parts],
+                                                  [Q, KV, KV], H, B, self.ks_h, ops=self.xops)
+            else:
+                nq = c.matmulSegmentsBatchPartial("q4k", self.xn, [L.wq], [self.q_parts], [Q], H, B, self.ks_h,
+                                                  ops=self.xops)
+            c.pagedAttnPrologue(self.q_parts, self.k_parts if prod else None, self.v_parts if prod else None, nq,
+                                L.q_norm, L.k_norm, self.rope_freqs, self.q, L.k_cache if prod else None,
+                                L.v_cache if prod else None, self.page_table, self.seq_lens, self.pro_params[il],
                                 self.rope_cs[s.is_global(il)], self.rope_rows)
+            ops = self.aops if s.hd(il) % 256 == 0 else None
             c.pagedAttnDecode(self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.attn,
-                              self.attn_params[il], self.attn_ws, ops=self.aops)
-            no = c.matmulSegmentsBatchPartial("q4k", self.attn, [L.wo], [self.o_parts], [H], s.q_dim, B, self.ks_q,
-                                              ops=self.aops)
+                              self.attn_params[il], self.attn_ws, ops=ops)
+            no = c.matmulSegmentsBatchPartial("q4k", self.attn, [L.wo], [self.o_parts], [H], Q, B, self.ks_q,
+                                              ops=ops)
             c.batchPrep(self.o_parts, no, L.post_attn_norm, self.hidden, L.pre_ffn_norm, self.hidden2, self.xn, H, B,
                         s.eps, ops=self.xops)
-            c.gateUpGeluBatch(self.xn, L.wgate, L.wup, self.act, s.ffn, H, B, ops=self.xops)
-            nd = c.matmulSegmentsBatchPartial("q6k", self.act, [L.wdown], [self.down_parts], [H], s.ffn, B,
+            c.gateUpGeluBatch(self.xn, L.wgate, L.wup, self.act, I, H, B, ops=self.xops)
+            nd = c.matmulSegmentsBatchPartial("q6k", self.act, [L.wdown], [self.down_parts], [H], I, B,
                                               self.ks_f)
         last = self.layers[-1]
         c.batchPrep(self.down_parts, nd, last.post_ffn_norm, self.hidden2, self.final_norm, self.hidden, self.xn, H,

@@ -370,6 +370,14 @@ class Context:
         check(lib().g4_attnDecodeFused_workspace_size(p, ctypes.byref(n)))
         return int(n.value)
 
+    @staticmethod
+    def attn_fused_single_launch(p: AttnFusedParams) -> bool:
+        """Whether g4_attnDecodeFused runs as one launch (the matrix-core plan:
+        head dim 256, at most 64 KV heads, a window of at most 65536
+        positions) rather than an attention launch and a merge launch."""
+        eff = min(p.max_seq_len, p.sliding_window) if p.sliding_window else p.max_seq_len
+        return p.head_dim == 256 and p.num_kv_heads <= 64 and eff <= 65536
+
     def attnDecodeFused(self, q_raw: Ptr, k_raw: Ptr, v_raw: Ptr, q_norm_w: Ptr, k_norm_w: Ptr, rope_freqs: Ptr,
                         k_cache: Ptr, v_cache: Ptr, out: Ptr, p: AttnFusedParams, workspace: Buffer,
                         position_dev: Ptr) -> None:

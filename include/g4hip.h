@@ -199,7 +199,12 @@ int g4_attnDecode_dev(g4_ctx* ctx, const float* q, const uint16_t* k_cache,
  * must be zeroed (g4_memset) before its first use, every call leaves the
  * counters zero, and one workspace may serve calls of different windows and
  * lengths (the layers of a step) as long as they do not overlap and no other
- * entry point writes into it in between. */
+ * entry point writes into it in between.
+ * A layer that reads another layer's KV cache (the consumer layers of
+ * src/engine.ts:1541-1583, which compute only q and attend over their
+ * producer's cache, src/engine.ts:1149-1152) passes k_raw = v_raw =
+ * k_norm_w = NULL and that cache: no row is formed or stored, and the row
+ * at *position_dev is read from the cache like every other. */
 typedef struct {
   uint32_t num_q_heads, num_kv_heads, head_dim, max_seq_len;
   float scale;
@@ -286,7 +291,8 @@ int g4_pagedAttnDecodeOps(g4_ctx* ctx, const float* q, const uint16_t* k_pool, c
  * page the table names (a page id outside [0, num_pages) stores nothing),
  * then split-K decode attention over the sequence's window. The workspace is
  * sized by g4_pagedAttnDecodeFused_workspace_size; calls that share it must
- * not overlap. */
+ * not overlap. k_raw = v_raw = k_norm_w = NULL: a consumer layer over its
+ * producer's pool, as for g4_attnDecodeFused. */
 typedef struct {
   uint32_t num_seqs, num_q_heads, num_kv_heads, head_dim;
   uint32_t page_size, max_pages, max_seq_len, num_pages;
@@ -310,7 +316,9 @@ int g4_pagedAttnDecodeFused(g4_ctx* ctx, const float* q_raw, const float* k_raw,
  * g4_pagedAttnDecode then attends. p.scale and p.sliding_window are unused.
  * rope_cs: a g4_ropeTable table for p.theta / p.apply_divisor of
  * rope_rows >= p.max_seq_len rows, or NULL to compute the RoPE angles per
- * call (same values). */
+ * call (same values). k_parts = v_parts = NULL: q only, for a consumer layer
+ * (src/engine.ts:1547-1574 skip the k/v projections, k_norm, v_norm and the
+ * store there); k_norm_w and the pools are then not read and may be NULL. */
 int g4_pagedAttnPrologue(g4_ctx* ctx, const float* q_parts, const float* k_parts,
                          const float* v_parts, uint32_t nparts, const uint16_t* q_norm_w,
                          const uint16_t* k_norm_w, const uint16_t* rope_freqs, float* q_out,
@@ -516,7 +524,9 @@ int g4_batchPrep(g4_ctx* ctx, const float* x_parts, uint32_t nparts, const uint1
  * receives [*ksplit][batch][rows[i]] partial sums (one chunk each) and must
  * hold max_ksplit * batch * rows[i] floats. The consumer adds the chunks in
  * order: g4_batchPrep, g4_pagedAttnPrologue. softcap_cap > 0 (tanh softcap
- * of the outputs) needs max_ksplit == 1. */
+ * of the outputs) needs max_ksplit == 1. Prebuilt `ops` are taken for N
+ * 1536, 2048 and 4096 (the norm prologue's and the attention merge's
+ * widths); other widths with ops are G4_ERR_UNSUPPORTED. */
 int g4_matmulSegmentsBatchPartial(g4_ctx* ctx, int wtype, const float* x, const void* ops,
                                   const void* const* weights, float* const* outputs,
                                   const uint32_t* rows, int nseg, uint32_t N, uint32_t batch,

@@ -31,6 +31,10 @@ def f16_toward_zero(x):
 
 
 class HostModel:
+    """A decoder's weights on the host. Layers that read a producer's cache
+    (no k/v projections) index the producer's entry of the cache lists the
+    step is given (src/engine.ts:1149-1152)."""
+
     def __init__(self, dec):
         self.s = s = dec.s
         u8, u16 = np.uint8, np.uint16
@@ -39,43 +43,54 @@ class HostModel:
         for L in dec.layers:
             self.layers.append({k: getattr(L, k).download(u8 if k.startswith("w") else u16)
                                 for k in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown", "attn_norm",
-                                          "post_attn_norm", "pre_ffn_norm", "post_ffn_norm", "q_norm", "k_norm")})
+                                          "post_attn_norm", "pre_ffn_norm", "post_ffn_norm", "q_norm", "k_norm")
+                                if getattr(L, k) is not None})
         self.final_norm = dec.final_norm.download(u16)
         self.lm_head = dec.lm_head.download(u8) if dec.lm_head is not None else None
+        self.embedding = getattr(dec, "embedding", None)  # device table: rows are fetched on demand
+
+    def embed(self, token: int):
+        """shaders/embedding_lookup.wgsl for one token (the oracle's embedding_lookup on its row)."""
+        H = self.s.hidden
+        row = self.embedding.download(np.uint16, H, offset=int(token) * H * 2)
+        return O.embedding_lookup(row.view(np.float16), H, 0)
 
     def step(self, hidden, kcs, vcs, pos, gelu=O.gelu_mul, row_toward_zero=False):
         """Decode position `pos`: kcs/vcs are this sequence's dense f16 caches
-        (one per layer, >= pos + 1 rows), updated in place. Returns the new
-        hidden state and the softcapped logits (None without an LM head).
-        `row_toward_zero` stores the new K/V rows rounded toward zero instead
-        of to nearest (a one-ulp change of the f16 cache, to measure how much
-        the step depends on the cache's resolution)."""
+        (one per layer, >= pos + 1 rows; a consumer layer's entry is not
+        used), updated in place. Returns the new hidden state and the
+        softcapped logits (None without an LM head). `row_toward_zero`
+        stores the new K/V rows rounded toward zero instead of to nearest (a
+        one-ulp change of the f16 cache, to measure how much the step depends
+        on the cache's resolution)."""
         s, x = self.s, hidden.copy()
         for il, W in enumerate(self.layers):
             glob = s.is_global(il)
             theta = s.theta_global if glob else s.theta_local
             window = 0 if glob else s.window
+            hd, Q, KV, I = s.hd(il), s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il)
+            src = s.producer(il)
             n = O.rms_norm(x, W["attn_norm"], s.eps)
-            q = O.matmul(n, W["wq"], s.q_dim, s.hidden, "q4k")
-            k = O.matmul(n, W["wk"], s.kv_dim, s.hidden, "q4k")
-            v = O.matmul(n, W["wv"], s.kv_dim, s.hidden, "q4k")
-            v = O.per_head_rms_norm_no_weight(v, s.n_kv_heads, s.head_dim, s.eps)
-            q = O.fused_per_head_norm_rope(q, W["q_norm"], s.n_q_heads, s.head_dim, s.eps, pos, theta, int(glob),
-                                           self.table)
-            k = O.fused_per_head_norm_rope(k, W["k_norm"], s.n_kv_heads, s.head_dim, s.eps, pos, theta, int(glob),
-                                           self.table)
-            O.kv_cache_store_f16(k, v, kcs[il], vcs[il], s.n_kv_heads, s.head_dim, pos)
-            if row_toward_zero:
-                row = slice(pos * s.kv_dim, (pos + 1) * s.kv_dim)
-                kcs[il][row] = f16_toward_zero(k)
-                vcs[il][row] = f16_toward_zero(v)
-            a = O.attention(q, kcs[il], vcs[il], s.n_q_heads, s.n_kv_heads, s.head_dim, pos + 1, 1.0, window)
-            o = O.matmul(a, W["wo"], s.hidden, s.q_dim, "q4k")
+            q = O.matmul(n, W["wq"], Q, s.hidden, "q4k")
+            q = O.fused_per_head_norm_rope(q, W["q_norm"], s.n_q_heads, hd, s.eps, pos, theta, int(glob), self.table)
+            if src == il:
+                k = O.matmul(n, W["wk"], KV, s.hidden, "q4k")
+                v = O.matmul(n, W["wv"], KV, s.hidden, "q4k")
+                v = O.per_head_rms_norm_no_weight(v, s.n_kv_heads, hd, s.eps)
+                k = O.fused_per_head_norm_rope(k, W["k_norm"], s.n_kv_heads, hd, s.eps, pos, theta, int(glob),
+                                               self.table)
+                O.kv_cache_store_f16(k, v, kcs[il], vcs[il], s.n_kv_heads, hd, pos)
+                if row_toward_zero:
+                    row = slice(pos * KV, (pos + 1) * KV)
+                    kcs[il][row] = f16_toward_zero(k)
+                    vcs[il][row] = f16_toward_zero(v)
+            a = O.attention(q, kcs[src], vcs[src], s.n_q_heads, s.n_kv_heads, hd, pos + 1, 1.0, window)
+            o = O.matmul(a, W["wo"], s.hidden, Q, "q4k")
             h = O.fused_norm_add(o, W["post_attn_norm"], x, s.eps)
             n2 = O.rms_norm(h, W["pre_ffn_norm"], s.eps)
-            g = O.matmul(n2, W["wgate"], s.ffn, s.hidden, "q4k")
-            u = O.matmul(n2, W["wup"], s.ffn, s.hidden, "q4k")
-            dn = O.matmul(gelu(g, u), W["wdown"], s.hidden, s.ffn, "q6k")
+            g = O.matmul(n2, W["wgate"], I, s.hidden, "q4k")
+            u = O.matmul(n2, W["wup"], I, s.hidden, "q4k")
+            dn = O.matmul(gelu(g, u), W["wdown"], s.hidden, I, "q6k")
             x = O.fused_norm_add(dn, W["post_ffn_norm"], h, s.eps)
         if self.lm_head is None:
             return x, None

@@ -56,10 +56,11 @@ def _restore(d, hidden, pools, lens):
     d.set_lengths(lens)
 
 
-def _dense(d, pool, seq, n):
-    """Sequence `seq`'s first n rows gathered from a pool, as a dense cache
-    with one spare row."""
-    kv = d.s.kv_dim
+def _dense(d, pool, seq, n, kv=None):
+    """Sequence `seq`'s first n rows gathered from a pool of rows of kv
+    values (default: the uniform layer's), as a dense cache with one spare
+    row."""
+    kv = kv or d.s.kv_dim
     P = pool.reshape(-1, kv)
     out = np.zeros((n + 1, kv), np.uint16)
     for t in range(n):
@@ -218,17 +219,19 @@ def _step_vs_oracle(ctx, d, LENS):
     LG = d.logits.download(np.float32).reshape(B, s.vocab)
     TOK = d.tokens.download(np.uint32)
     pools1 = _pools(d)
-    kv = s.kv_dim
+    kvs = [s.kv_dim_of(il) for il in range(s.n_layers)]
     refs, tol = [], []
     for b, L in enumerate(LENS):
-        kcs = [_dense(d, k, b, L) for k, _ in pools0]
-        vcs = [_dense(d, v, b, L) for _, v in pools0]
+        # (a layer reading a producer's pool has that pool here; the oracle reads the producer's entry)
+        kcs = [_dense(d, k, b, L, kvs[il]) for il, (k, _) in enumerate(pools0)]
+        vcs = [_dense(d, v, b, L, kvs[il]) for il, (_, v) in enumerate(pools0)]
         x, logits = hm.step(hidden0[b], kcs, vcs, L)
         refs.append((x, logits, kcs, vcs))
         # the step's own dependence on the f16 cache's resolution: the oracle
         # against itself with its new K/V rows one ulp off (rounded toward
         # zero), and on the last bits of the GELU (the shader's all-f32 form)
-        kz, vz = [_dense(d, k, b, L) for k, _ in pools0], [_dense(d, v, b, L) for _, v in pools0]
+        kz = [_dense(d, k, b, L, kvs[il]) for il, (k, _) in enumerate(pools0)]
+        vz = [_dense(d, v, b, L, kvs[il]) for il, (_, v) in enumerate(pools0)]
         xz, lgz = hm.step(hidden0[b], kz, vz, L, row_toward_zero=True)
         x32, lg32 = hm.step(hidden0[b], [k.copy() for k in kcs], [v.copy() for v in vcs], L, gelu=gelu_mul_f32)
         tol.append(max(STEP_REL, O.rel_l2(xz, x), O.rel_l2(lgz, logits),
@@ -246,16 +249,18 @@ def _step_vs_oracle(ctx, d, LENS):
         assert TOK[b] == O.argmax(LG[b]), b
         r = d.pool_row(b, L)
         for il in range(s.n_layers):
+            if not s.is_producer(il):
+                continue
             for got, ref, nm in ((pools1[il][0], kcs[il], "k"), (pools1[il][1], vcs[il], "v")):
-                row = got.reshape(-1, kv)[r].view(np.float16).astype(np.float32)
-                want = ref.reshape(-1, kv)[L].view(np.float16).astype(np.float32)
+                row = got.reshape(-1, kvs[il])[r].view(np.float16).astype(np.float32)
+                want = ref.reshape(-1, kvs[il])[L].view(np.float16).astype(np.float32)
                 # layer 0's rows depend on the input only; later rows on the layers before
                 assert_close(row, want, rel=STEP_REL if il == 0 else tol[b], what=f"{nm} row seq {b} layer {il}")
     # nothing but the appended rows changed in the pools
     written = sorted(d.pool_row(b, L) for b, L in enumerate(LENS))
     for il in range(s.n_layers):
         for before, after in ((pools0[il][0], pools1[il][0]), (pools0[il][1], pools1[il][1])):
-            diff = np.nonzero(np.any(before.reshape(-1, kv) != after.reshape(-1, kv), axis=1))[0]
+            diff = np.nonzero(np.any(before.reshape(-1, kvs[il]) != after.reshape(-1, kvs[il]), axis=1))[0]
             assert set(diff.tolist()) <= set(written)
     _restore(d, hidden0.reshape(-1), pools0, lens0)
 
