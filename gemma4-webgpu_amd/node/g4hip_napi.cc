@@ -1,0 +1,631 @@
+// N-API addon over libg4hip.so: the per-key dispatch contract of the
+// reference's WebGPU backend (src/engine.ts:1466-1651 encodeTransformerPass,
+// :1670-1846 sampleNextTokenSubmit) for a Node host.
+//
+// Device pointers, contexts, graphs and events travel to JavaScript as
+// BigInt handles; null/undefined stands for NULL. Each key takes the buffers
+// in the WGSL binding order of its shader and then a plain object whose
+// properties are the fields of the shader's Params struct, by name
+// (e.g. matmulQuant(ctx, input, weight, output, {M, N}, 'q4k')). A failing
+// call throws an Error whose `code` is the G4_ERR_* name of the status and
+// whose message is g4_last_error().
+#define NAPI_VERSION 6
+#include <node_api.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "g4hip.h"
+
+namespace {
+
+const char* status_name(int rc) {
+  switch (rc) {
+    case G4_ERR_INVALID: return "G4_ERR_INVALID";
+    case G4_ERR_HIP: return "G4_ERR_HIP";
+    case G4_ERR_DEVICE_LOST: return "G4_ERR_DEVICE_LOST";
+    case G4_ERR_OOM: return "G4_ERR_OOM";
+    case G4_ERR_UNSUPPORTED: return "G4_ERR_UNSUPPORTED";
+    case G4_ERR_NO_DEVICE: return "G4_ERR_NO_DEVICE";
+    default: return "G4_ERR_UNKNOWN";
+  }
+}
+
+// Argument errors found here (a wrong JS type) are thrown as TypeErrors and
+// the wrapper returns nullptr; `ok` turns false so no library call is made.
+struct Args {
+  napi_env env;
+  size_t argc = 0;
+  napi_value v[12];
+  bool ok = true;
+  Args(napi_env e, napi_callback_info info) : env(e) {
+    argc = 12;
+    if (napi_get_cb_info(env, info, &argc, v, nullptr, nullptr) != napi_ok) fail("bad call");
+  }
+  void fail(const char* msg) {
+    if (ok) napi_throw_type_error(env, "G4_ERR_ARG", msg);
+    ok = false;
+  }
+  bool present(size_t i) const {
+    if (i >= argc) return false;
+    napi_valuetype t;
+    napi_typeof(env, v[i], &t);
+    return t != napi_undefined && t != napi_null;
+  }
+  void* ptr(size_t i) {
+    if (!present(i)) return nullptr;
+    uint64_t p = 0;
+    bool lossless = false;
+    if (napi_get_value_bigint_uint64(env, v[i], &p, &lossless) != napi_ok || !lossless) {
+      fail("expected a BigInt device handle (or null)");
+      return nullptr;
+    }
+    return (void*)(uintptr_t)p;
+  }
+  uint32_t u32(size_t i) {
+    uint32_t u = 0;
+    if (i >= argc || napi_get_value_uint32(env, v[i], &u) != napi_ok) fail("expected a number");
+    return u;
+  }
+  uint64_t u64(size_t i) {
+    if (i >= argc) {
+      fail("missing argument");
+      return 0;
+    }
+    napi_valuetype t;
+    napi_typeof(env, v[i], &t);
+    if (t == napi_bigint) {
+      uint64_t u = 0;
+      bool lossless = false;
+      napi_get_value_bigint_uint64(env, v[i], &u, &lossless);
+      return u;
+    }
+    double d = 0;
+    if (napi_get_value_double(env, v[i], &d) != napi_ok || d < 0) fail("expected a non-negative number");
+    return (uint64_t)d;
+  }
+  float f32(size_t i) {
+    double d = 0;
+    if (i >= argc || napi_get_value_double(env, v[i], &d) != napi_ok) fail("expected a number");
+    return (float)d;
+  }
+  std::string str(size_t i) {
+    char buf[64] = {0};
+    size_t n = 0;
+    if (i >= argc || napi_get_value_string_utf8(env, v[i], buf, sizeof buf, &n) != napi_ok) fail("expected a string");
+    return std::string(buf, n);
+  }
+  // a named field of the Params object at argument i
+  napi_value field(size_t i, const char* name) {
+    napi_value out = nullptr;
+    bool has = false;
+    if (i >= argc || napi_has_named_property(env, v[i], name, &has) != napi_ok || !has) {
+      std::string m = std::string("params object lacks field '") + name + "'";
+      fail(m.c_str());
+      return nullptr;
+    }
+    napi_get_named_property(env, v[i], name, &out);
+    return out;
+  }
+  uint32_t fu32(size_t i, const char* name) {
+    napi_value f = field(i, name);
+    uint32_t u = 0;
+    if (f && napi_get_value_uint32(env, f, &u) != napi_ok) fail(name);
+    return u;
+  }
+  float ff32(size_t i, const char* name) {
+    napi_value f = field(i, name);
+    double d = 0;
+    if (f && napi_get_value_double(env, f, &d) != napi_ok) fail(name);
+    return (float)d;
+  }
+};
+
+napi_value undefined(napi_env env) {
+  napi_value u;
+  napi_get_undefined(env, &u);
+  return u;
+}
+
+napi_value done(napi_env env, int rc) {
+  if (rc != G4_OK) {
+    const char* msg = g4_last_error();
+    napi_throw_error(env, status_name(rc), msg && *msg ? msg : status_name(rc));
+    return nullptr;
+  }
+  return undefined(env);
+}
+
+napi_value bigint(napi_env env, const void* p) {
+  napi_value out;
+  napi_create_bigint_uint64(env, (uint64_t)(uintptr_t)p, &out);
+  return out;
+}
+
+napi_value number(napi_env env, double d) {
+  napi_value out;
+  napi_create_double(env, d, &out);
+  return out;
+}
+
+#define CTX(a, i) ((g4_ctx*)(a).ptr(i))
+#define F32P(a, i) ((float*)(a).ptr(i))
+#define U16P(a, i) ((uint16_t*)(a).ptr(i))
+#define U32P(a, i) ((uint32_t*)(a).ptr(i))
+#define CHECKED(a) \
+  if (!(a).ok) return nullptr
+
+// ---- lifecycle, memory, synchronisation --------------------------------
+
+napi_value Version(napi_env env, napi_callback_info) { return number(env, g4_version()); }
+
+napi_value LastError(napi_env env, napi_callback_info) {
+  napi_value s;
+  const char* m = g4_last_error();
+  napi_create_string_utf8(env, m ? m : "", NAPI_AUTO_LENGTH, &s);
+  return s;
+}
+
+// init(device) -> ctx
+napi_value Init(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  const uint32_t dev = a.present(0) ? a.u32(0) : 0;
+  CHECKED(a);
+  g4_ctx* ctx = nullptr;
+  const int rc = g4_init((int)dev, &ctx);
+  if (rc != G4_OK) return done(env, rc);
+  return bigint(env, ctx);
+}
+
+napi_value Destroy(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  CHECKED(a);
+  return done(env, g4_destroy(c));
+}
+
+// deviceInfo(ctx) -> {name, numCus, hbmBytes}
+napi_value DeviceInfo(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  CHECKED(a);
+  char name[256] = {0};
+  int cus = 0;
+  size_t hbm = 0;
+  const int rc = g4_device_info(c, name, sizeof name, &cus, &hbm);
+  if (rc != G4_OK) return done(env, rc);
+  napi_value o, s;
+  napi_create_object(env, &o);
+  napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &s);
+  napi_set_named_property(env, o, "name", s);
+  napi_set_named_property(env, o, "numCus", number(env, cus));
+  napi_set_named_property(env, o, "hbmBytes", number(env, (double)hbm));
+  return o;
+}
+
+// alloc(ctx, bytes) -> ptr
+napi_value Alloc(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const uint64_t n = a.u64(1);
+  CHECKED(a);
+  void* p = nullptr;
+  const int rc = g4_alloc(c, (size_t)n, &p);
+  if (rc != G4_OK) return done(env, rc);
+  return bigint(env, p);
+}
+
+napi_value Free(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  void* p = a.ptr(1);
+  CHECKED(a);
+  return done(env, g4_free(c, p));
+}
+
+// memset(ctx, ptr, value, bytes)
+napi_value Memset(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  void* p = a.ptr(1);
+  const uint32_t v = a.u32(2);
+  const uint64_t n = a.u64(3);
+  CHECKED(a);
+  return done(env, g4_memset(c, p, (int)v, (size_t)n));
+}
+
+// upload(ctx, dst, typedArrayOrBuffer, dstOffset = 0): writeBuffer
+napi_value Upload(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  void* dst = a.ptr(1);
+  const uint64_t off = a.present(3) ? a.u64(3) : 0;
+  CHECKED(a);
+  bool is_ta = false, is_buf = false;
+  void* data = nullptr;
+  size_t bytes = 0;
+  if (a.argc > 2) napi_is_typedarray(env, a.v[2], &is_ta);
+  if (is_ta) {
+    napi_typedarray_type t;
+    size_t len, boff;
+    napi_value ab;
+    napi_get_typedarray_info(env, a.v[2], &t, &len, &data, &ab, &boff);
+    napi_value bl;
+    uint32_t bpe = 1;
+    if (napi_get_named_property(env, a.v[2], "BYTES_PER_ELEMENT", &bl) == napi_ok) napi_get_value_uint32(env, bl, &bpe);
+    bytes = len * bpe;
+  } else {
+    if (a.argc > 2) napi_is_buffer(env, a.v[2], &is_buf);
+    if (!is_buf) {
+      a.fail("upload: expected a typed array or Buffer");
+      return nullptr;
+    }
+    napi_get_buffer_info(env, a.v[2], &data, &bytes);
+  }
+  return done(env, g4_upload(c, dst, data, bytes, (size_t)off));
+}
+
+// download(ctx, src, bytes, srcOffset = 0) -> Buffer (blocking readback)
+napi_value Download(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  void* src = a.ptr(1);
+  const uint64_t n = a.u64(2);
+  const uint64_t off = a.present(3) ? a.u64(3) : 0;
+  CHECKED(a);
+  void* data = nullptr;
+  napi_value buf;
+  if (napi_create_buffer(env, (size_t)n, &data, &buf) != napi_ok) {
+    a.fail("download: cannot allocate the host buffer");
+    return nullptr;
+  }
+  const int rc = g4_download(c, data, src, (size_t)n, (size_t)off);
+  if (rc != G4_OK) return done(env, rc);
+  return buf;
+}
+
+napi_value Sync(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  CHECKED(a);
+  return done(env, g4_stream_sync(c));
+}
+
+napi_value GraphBegin(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  CHECKED(a);
+  return done(env, g4_graph_begin(c));
+}
+
+napi_value GraphEnd(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  CHECKED(a);
+  g4_graph* g = nullptr;
+  const int rc = g4_graph_end(c, &g);
+  if (rc != G4_OK) return done(env, rc);
+  return bigint(env, g);
+}
+
+napi_value GraphLaunch(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  g4_graph* g = (g4_graph*)a.ptr(1);
+  CHECKED(a);
+  return done(env, g4_graph_launch(c, g));
+}
+
+napi_value GraphDestroy(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_graph* g = (g4_graph*)a.ptr(0);
+  CHECKED(a);
+  return done(env, g4_graph_destroy(g));
+}
+
+// fill(ctx, kind, dst, count, seed[, mean, std]): the library's seeded
+// synthetic generators ('q4k' / 'q6k': count blocks; 'f16' / 'f32': values)
+napi_value Fill(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const std::string kind = a.str(1);
+  void* dst = a.ptr(2);
+  const uint64_t n = a.u64(3), seed = a.u64(4);
+  const float mean = a.present(5) ? a.f32(5) : 0.f, sd = a.present(6) ? a.f32(6) : 1.f;
+  CHECKED(a);
+  if (kind == "q4k") return done(env, g4_fill_q4k(c, dst, n, seed));
+  if (kind == "q6k") return done(env, g4_fill_q6k(c, dst, n, seed));
+  if (kind == "f16") return done(env, g4_fill_normal_f16(c, (uint16_t*)dst, n, seed, mean, sd));
+  if (kind == "f32") return done(env, g4_fill_normal_f32(c, (float*)dst, n, seed, mean, sd));
+  a.fail("fill: kind must be 'q4k', 'q6k', 'f16' or 'f32'");
+  return nullptr;
+}
+
+// ---- kernel keys (src/shaders.ts:34-56) --------------------------------
+
+// matmulQuant(ctx, input, weight, output, {M, N}, wtype = 'q4k')
+napi_value MatmulQuant(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* x = F32P(a, 1);
+  const void* w = a.ptr(2);
+  float* y = F32P(a, 3);
+  const g4_matmul_params p{a.fu32(4, "M"), a.fu32(4, "N")};
+  const std::string t = a.present(5) ? a.str(5) : "q4k";
+  CHECKED(a);
+  if (t == "q4k") return done(env, g4_matmulQuant_q4k(c, x, w, y, p));
+  if (t == "q6k") return done(env, g4_matmulQuant_q6k(c, x, w, y, p));
+  if (t == "f16") return done(env, g4_matmulQuant_f16(c, x, (const uint16_t*)w, y, p));
+  a.fail("matmulQuant: wtype must be 'q4k', 'q6k' or 'f16'");
+  return nullptr;
+}
+
+// matmulQuantMR4(ctx, input, weight, output, {M, N})
+napi_value MatmulQuantMR4(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* x = F32P(a, 1);
+  const void* w = a.ptr(2);
+  float* y = F32P(a, 3);
+  const g4_matmul_params p{a.fu32(4, "M"), a.fu32(4, "N")};
+  CHECKED(a);
+  return done(env, g4_matmulQuantMR4_q4k(c, x, w, y, p));
+}
+
+// kvCacheStore(ctx, k_in, v_in, k_cache, v_cache, {num_kv_heads, head_dim, position, max_seq_len}[, positionDev])
+napi_value KvCacheStore(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* k = F32P(a, 1);
+  const float* v = F32P(a, 2);
+  uint16_t* kc = U16P(a, 3);
+  uint16_t* vc = U16P(a, 4);
+  const g4_kv_store_params p{a.fu32(5, "num_kv_heads"), a.fu32(5, "head_dim"), a.fu32(5, "position"),
+                             a.fu32(5, "max_seq_len")};
+  const uint32_t* pd = U32P(a, 6);
+  CHECKED(a);
+  return done(env, pd ? g4_kvCacheStore_dev(c, k, v, kc, vc, p, pd) : g4_kvCacheStore(c, k, v, kc, vc, p));
+}
+
+g4_attn_score_params score_params(Args& a, size_t i) {
+  return g4_attn_score_params{a.fu32(i, "num_q_heads"), a.fu32(i, "num_kv_heads"), a.fu32(i, "head_dim"),
+                              a.fu32(i, "seq_len"), a.ff32(i, "scale"), a.fu32(i, "sliding_window")};
+}
+
+// attnScore(ctx, q, k_cache, scores, {num_q_heads, num_kv_heads, head_dim, seq_len, scale, sliding_window}[, positionDev])
+napi_value AttnScore(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* q = F32P(a, 1);
+  const uint16_t* kc = U16P(a, 2);
+  float* sc = F32P(a, 3);
+  const g4_attn_score_params p = score_params(a, 4);
+  const uint32_t* pd = U32P(a, 5);
+  CHECKED(a);
+  return done(env, pd ? g4_attnScore_dev(c, q, kc, sc, p, pd) : g4_attnScore(c, q, kc, sc, p));
+}
+
+// softmax(ctx, scores, {num_heads, seq_len}[, positionDev])
+napi_value Softmax(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  float* sc = F32P(a, 1);
+  const g4_softmax_params p{a.fu32(2, "num_heads"), a.fu32(2, "seq_len")};
+  const uint32_t* pd = U32P(a, 3);
+  CHECKED(a);
+  return done(env, pd ? g4_softmax_dev(c, sc, p, pd) : g4_softmax(c, sc, p));
+}
+
+// attnOutput(ctx, probs, v_cache, output, {num_q_heads, num_kv_heads, head_dim, seq_len}[, positionDev])
+napi_value AttnOutput(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* pr = F32P(a, 1);
+  const uint16_t* vc = U16P(a, 2);
+  float* out = F32P(a, 3);
+  const g4_attn_output_params p{a.fu32(4, "num_q_heads"), a.fu32(4, "num_kv_heads"), a.fu32(4, "head_dim"),
+                                a.fu32(4, "seq_len")};
+  const uint32_t* pd = U32P(a, 5);
+  CHECKED(a);
+  return done(env, pd ? g4_attnOutput_dev(c, pr, vc, out, p, pd) : g4_attnOutput(c, pr, vc, out, p));
+}
+
+// attnDecodeWorkspaceSize({num_q_heads, ...attnScore params}) -> bytes
+napi_value AttnDecodeWorkspaceSize(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  const g4_attn_score_params p = score_params(a, 0);
+  CHECKED(a);
+  size_t n = 0;
+  const int rc = g4_attnDecode_workspace_size(p, &n);
+  if (rc != G4_OK) return done(env, rc);
+  return number(env, (double)n);
+}
+
+// attnDecode(ctx, q, k_cache, v_cache, output, {attnScore params}, workspace, workspaceBytes[, positionDev]):
+// the attnScore -> softmax -> attnOutput trio in one split-K pass
+napi_value AttnDecode(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* q = F32P(a, 1);
+  const uint16_t* kc = U16P(a, 2);
+  const uint16_t* vc = U16P(a, 3);
+  float* out = F32P(a, 4);
+  const g4_attn_score_params p = score_params(a, 5);
+  void* ws = a.ptr(6);
+  const uint64_t wsb = a.u64(7);
+  const uint32_t* pd = U32P(a, 8);
+  CHECKED(a);
+  return done(env, pd ? g4_attnDecode_dev(c, q, kc, vc, out, p, ws, (size_t)wsb, pd)
+                      : g4_attnDecode(c, q, kc, vc, out, p, ws, (size_t)wsb));
+}
+
+// perHeadRmsNormNoWeight(ctx, data, {num_heads, head_dim, eps})
+napi_value PerHeadRmsNormNoWeight(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  float* d = F32P(a, 1);
+  const g4_per_head_norm_params p{a.fu32(2, "num_heads"), a.fu32(2, "head_dim"), a.ff32(2, "eps"), 0u};
+  CHECKED(a);
+  return done(env, g4_perHeadRmsNormNoWeight(c, d, p));
+}
+
+// fusedPerHeadNormRope(ctx, data, weight, {num_heads, head_dim, eps, position, theta, apply_divisor},
+//                      rope_freqs[, positionDev])
+napi_value FusedPerHeadNormRope(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  float* d = F32P(a, 1);
+  const uint16_t* w = U16P(a, 2);
+  const g4_norm_rope_params p{a.fu32(3, "num_heads"), a.fu32(3, "head_dim"), a.ff32(3, "eps"),
+                              a.fu32(3, "position"),  a.ff32(3, "theta"),    a.fu32(3, "apply_divisor")};
+  const uint16_t* rf = U16P(a, 4);
+  const uint32_t* pd = U32P(a, 5);
+  CHECKED(a);
+  return done(env, pd ? g4_fusedPerHeadNormRope_dev(c, d, w, p, rf, pd) : g4_fusedPerHeadNormRope(c, d, w, p, rf));
+}
+
+// rmsNorm(ctx, input, weight, output, {hidden_size, eps})
+napi_value RmsNorm(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* x = F32P(a, 1);
+  const uint16_t* w = U16P(a, 2);
+  float* out = F32P(a, 3);
+  const g4_rms_norm_params p{a.fu32(4, "hidden_size"), a.ff32(4, "eps")};
+  CHECKED(a);
+  return done(env, g4_rmsNorm(c, x, w, out, p));
+}
+
+// fusedNormAdd(ctx, input, weight, residual, output, {size, eps})
+napi_value FusedNormAdd(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* x = F32P(a, 1);
+  const uint16_t* w = U16P(a, 2);
+  const float* r = F32P(a, 3);
+  float* out = F32P(a, 4);
+  const g4_norm_add_params p{a.fu32(5, "size"), a.ff32(5, "eps")};
+  CHECKED(a);
+  return done(env, g4_fusedNormAdd(c, x, w, r, out, p));
+}
+
+// geluMul(ctx, gate, up, output, size)
+napi_value GeluMul(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* g = F32P(a, 1);
+  const float* u = F32P(a, 2);
+  float* out = F32P(a, 3);
+  const uint32_t n = a.u32(4);
+  CHECKED(a);
+  return done(env, g4_geluMul(c, g, u, out, n));
+}
+
+// logitSoftcap(ctx, logits, {size, cap})
+napi_value LogitSoftcap(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  float* lg = F32P(a, 1);
+  const g4_softcap_params p{a.fu32(2, "size"), a.ff32(2, "cap")};
+  CHECKED(a);
+  return done(env, g4_logitSoftcap(c, lg, p));
+}
+
+// embeddingLookup(ctx, embedding, num_rows, output, {hidden_size, token_id}[, tokenDev])
+napi_value EmbeddingLookup(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const uint16_t* e = U16P(a, 1);
+  const uint32_t rows = a.u32(2);
+  float* out = F32P(a, 3);
+  const g4_embedding_params p{a.fu32(4, "hidden_size"), a.fu32(4, "token_id")};
+  const uint32_t* td = U32P(a, 5);
+  CHECKED(a);
+  return done(env, td ? g4_embeddingLookup_dev(c, e, rows, out, p, td) : g4_embeddingLookup(c, e, rows, out, p));
+}
+
+// argmax(ctx, logits, result, size)
+napi_value Argmax(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* lg = F32P(a, 1);
+  uint32_t* r = U32P(a, 2);
+  const uint32_t n = a.u32(3);
+  CHECKED(a);
+  return done(env, g4_argmax(c, lg, r, n));
+}
+
+// topk256(ctx, logits, result, size)
+napi_value Topk256(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* lg = F32P(a, 1);
+  float* r = F32P(a, 2);
+  const uint32_t n = a.u32(3);
+  CHECKED(a);
+  return done(env, g4_topk256(c, lg, r, n));
+}
+
+// advancePosition(ctx, positionDev, delta = 1)
+napi_value AdvancePosition(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  uint32_t* pd = U32P(a, 1);
+  const uint32_t d = a.present(2) ? a.u32(2) : 1u;
+  CHECKED(a);
+  return done(env, g4_advancePosition(c, pd, d));
+}
+
+struct Entry {
+  const char* name;
+  napi_callback fn;
+};
+
+const Entry kEntries[] = {
+    {"version", Version},
+    {"lastError", LastError},
+    {"init", Init},
+    {"destroy", Destroy},
+    {"deviceInfo", DeviceInfo},
+    {"alloc", Alloc},
+    {"free", Free},
+    {"memset", Memset},
+    {"upload", Upload},
+    {"download", Download},
+    {"sync", Sync},
+    {"graphBegin", GraphBegin},
+    {"graphEnd", GraphEnd},
+    {"graphLaunch", GraphLaunch},
+    {"graphDestroy", GraphDestroy},
+    {"fill", Fill},
+    {"matmulQuant", MatmulQuant},
+    {"matmulQuantMR4", MatmulQuantMR4},
+    {"kvCacheStore", KvCacheStore},
+    {"attnScore", AttnScore},
+    {"softmax", Softmax},
+    {"attnOutput", AttnOutput},
+    {"attnDecodeWorkspaceSize", AttnDecodeWorkspaceSize},
+    {"attnDecode", AttnDecode},
+    {"perHeadRmsNormNoWeight", PerHeadRmsNormNoWeight},
+    {"fusedPerHeadNormRope", FusedPerHeadNormRope},
+    {"rmsNorm", RmsNorm},
+    {"fusedNormAdd", FusedNormAdd},
+    {"geluMul", GeluMul},
+    {"logitSoftcap", LogitSoftcap},
+    {"embeddingLookup", EmbeddingLookup},
+    {"argmax", Argmax},
+    {"topk256", Topk256},
+    {"advancePosition", AdvancePosition},
+};
+
+}  // namespace
+
+NAPI_MODULE_INIT() {
+  for (const Entry& e : kEntries) {
+    napi_value fn;
+    napi_create_function(env, e.name, NAPI_AUTO_LENGTH, e.fn, nullptr, &fn);
+    napi_set_named_property(env, exports, e.name, fn);
+  }
+  return exports;
+}

@@ -1,0 +1,356 @@
+'use strict';
+// HipBackend: the decode step of the reference's WebGPU engine, dispatched key
+// by key on libg4hip through the N-API addon g4hip.node, for a Node host.
+//
+// Written in ES2019 (plain classes and functions, no TypeScript compiler);
+// device buffers are the addon's BigInt handles. The pass order, the
+// buffers each key binds and its Params follow
+//   src/engine.ts:1466-1651  encodeTransformerPass (embed, 35 layers, final norm)
+//   src/engine.ts:1670-1746  sampleNextTokenSubmit (LM head, softcap, argmax /
+//                            top-k, the sampled token fed to the next embed)
+// with the work-buffer names of src/types.ts:489-517 and the layer tensor
+// names of the GGUF (attn_q, ffn_down, ...). The per-layer-embedding passes
+// (ple1.*, ple2.*) are not part of this path and are not issued.
+//
+// Differences from the WebGPU backend, all at the boundary:
+//  - matrices are the raw GGUF block bytes (Q4_K, Q6_K for ffn_down and the
+//    tied LM head) rather than f16 rows; the f16 token table is still bound
+//    for the embedding lookup;
+//  - the KV caches are f16 (2 bytes per element);
+//  - dynamic fields (position, seq_len, token) are call arguments or, with a
+//    device position / token buffer, read by the kernels themselves, so a
+//    whole forward can be captured once (graphBegin/graphEnd) and replayed.
+
+const path = require('path');
+
+function loadAddon() {
+  return require(path.join(__dirname, 'g4hip.node'));
+}
+
+// computeKvProducerMap (src/config/gemma4-e2b.ts:159-180): a layer past the
+// unshared ones reads the cache of the last unshared layer of its kind.
+function kvProducerMap(numLayers, numUnshared, isSliding) {
+  let lastLocal = -1;
+  let lastGlobal = -1;
+  for (let i = 0; i < numUnshared; i++) {
+    if (isSliding[i]) lastLocal = i;
+    else lastGlobal = i;
+  }
+  const out = [];
+  for (let i = 0; i < numLayers; i++) {
+    if (i < numUnshared) out.push(i);
+    else out.push(isSliding[i] ? lastLocal : lastGlobal);
+  }
+  return out;
+}
+
+// The Gemma-4-E2B configuration (src/config/gemma4-e2b.ts:16-63); any field
+// may be overridden (a smaller model for tests: num_layers, num_unshared_layers,
+// global_layers, vocab_size, ...).
+function e2bConfig(overrides) {
+  const o = overrides || {};
+  const numLayers = o.num_layers !== undefined ? o.num_layers : 35;
+  const globals = o.global_layers || [4, 9, 14, 19, 24, 29, 34];
+  const numUnshared = o.num_unshared_layers !== undefined ? o.num_unshared_layers : 15;
+  const isSliding = [];
+  const inter = [];
+  for (let i = 0; i < numLayers; i++) {
+    isSliding.push(globals.indexOf(i) < 0);
+    inter.push(i < numUnshared ? (o.intermediate_unshared || 6144) : (o.intermediate_shared || 12288));
+  }
+  return {
+    hidden_size: o.hidden_size || 1536,
+    num_q_heads: o.num_q_heads || 8,
+    num_kv_heads: o.num_kv_heads || 1,
+    head_dim_local: o.head_dim_local || 256,
+    head_dim_global: o.head_dim_global || 512,
+    vocab_size: o.vocab_size || 262144,
+    num_layers: numLayers,
+    rms_norm_eps: o.rms_norm_eps || 1e-6,
+    rope_theta_global: o.rope_theta_global || 1e6,
+    rope_theta_swa: o.rope_theta_swa || 1e4,
+    sliding_window: o.sliding_window || 512,
+    attention_is_sliding: isSliding,
+    intermediate_sizes: inter,
+    num_unshared_layers: numUnshared,
+    kv_producer_for_layer: kvProducerMap(numLayers, numUnshared, isSliding),
+    final_logit_softcapping: o.final_logit_softcapping !== undefined ? o.final_logit_softcapping : 30.0,
+  };
+}
+
+// Per-layer selectors (src/types.ts:69-91).
+const isSwaLayer = (C, il) => C.attention_is_sliding[il];
+const ropeTheta = (C, il) => (isSwaLayer(C, il) ? C.rope_theta_swa : C.rope_theta_global);
+const headDim = (C, il) => (isSwaLayer(C, il) ? C.head_dim_local : C.head_dim_global);
+const intermediateSize = (C, il) => C.intermediate_sizes[il];
+const isKvProducer = (C, il) => C.kv_producer_for_layer[il] === il;
+
+const LAYER_TENSORS = ['attn_norm', 'attn_q', 'attn_k', 'attn_v', 'attn_q_norm', 'attn_k_norm', 'attn_output',
+  'post_attention_norm', 'ffn_norm', 'ffn_gate', 'ffn_up', 'ffn_down', 'post_ffw_norm'];
+
+class HipBackend {
+  // addon: the g4hip.node exports (or any object with the same functions);
+  // ctx: its context handle. opts.maxSeqLen (default 2048, the reference's
+  // context cap), opts.mr4ForFfn (gate/up through matmulQuantMR4, default
+  // true), opts.trace (an array that receives [passLabel, key] per dispatch).
+  constructor(addon, ctx, config, opts) {
+    const o = opts || {};
+    this.g = addon;
+    this.ctx = ctx;
+    this.config = config;
+    this.maxSeqLen = o.maxSeqLen || 2048;
+    this.mr4ForFfn = o.mr4ForFfn !== undefined ? o.mr4ForFfn : true;
+    this.trace = o.trace || null;
+    this.owned = [];
+    this.layers = [];      // per layer: {tensor name: handle}
+    this.globals = {};     // tokenEmbed (f16), lmHead (Q6_K), finalNorm, rope_freqs
+    this.workBuffers = {};
+    this.kvCaches = [];    // per layer: {k, v} (consumers hold their producer's)
+  }
+
+  static open(config, opts) {
+    const addon = loadAddon();
+    const ctx = addon.init((opts && opts.device) || 0);
+    return new HipBackend(addon, ctx, config, opts);
+  }
+
+  close() {
+    for (const p of this.owned) this.g.free(this.ctx, p);
+    this.owned = [];
+    this.g.destroy(this.ctx);
+  }
+
+  alloc(bytes) {
+    const p = this.g.alloc(this.ctx, bytes);
+    this.owned.push(p);
+    return p;
+  }
+
+  // Work buffers (src/engine.ts:1001-1064; src/types.ts:489-517) and the f16
+  // KV caches of the producer layers.
+  allocate() {
+    const C = this.config;
+    const H = C.hidden_size;
+    let maxHd = 0;
+    let maxI = 0;
+    for (let il = 0; il < C.num_layers; il++) {
+      maxHd = Math.max(maxHd, headDim(C, il));
+      maxI = Math.max(maxI, intermediateSize(C, il));
+    }
+    const Q = C.num_q_heads * maxHd;
+    const KV = C.num_kv_heads * maxHd;
+    const f4 = (n) => this.alloc(4 * n);
+    this.workBuffers = {
+      hidden: f4(H), residual: f4(H), normed: f4(H), q: f4(Q), k: f4(KV), v: f4(KV), attnOut: f4(Q),
+      attnProj: f4(H), attnScores: f4(C.num_q_heads * this.maxSeqLen), ffnGate: f4(maxI), ffnUp: f4(maxI),
+      ffnMul: f4(maxI), ffnDown: f4(H), logits: f4(C.vocab_size), argmaxResult: f4(1), topk256Result: f4(512),
+      position: f4(1),
+    };
+    this.g.memset(this.ctx, this.workBuffers.argmaxResult, 0, 4);
+    this.g.memset(this.ctx, this.workBuffers.position, 0, 4);
+    this.kvCaches = [];
+    for (let il = 0; il < C.num_layers; il++) {
+      if (C.kv_producer_for_layer[il] < 0) throw new Error('layer ' + il + ': no unshared layer of its attention kind');
+      if (isKvProducer(C, il)) {
+        const bytes = 2 * this.maxSeqLen * C.num_kv_heads * headDim(C, il);
+        const kv = { k: this.alloc(bytes), v: this.alloc(bytes) };
+        this.g.memset(this.ctx, kv.k, 0, bytes);
+        this.g.memset(this.ctx, kv.v, 0, bytes);
+        this.kvCaches.push(kv);
+      } else {
+        this.kvCaches.push(this.kvCaches[C.kv_producer_for_layer[il]]);
+      }
+    }
+  }
+
+  // Byte sizes of a layer's tensors (raw GGUF blocks, f16 norm weights).
+  layerTensorBytes(il) {
+    const C = this.config;
+    const H = C.hidden_size;
+    const hd = headDim(C, il);
+    const Q = C.num_q_heads * hd;
+    const KV = C.num_kv_heads * hd;
+    const I = intermediateSize(C, il);
+    const q4 = (m, n) => (m * n / 256) * 144;
+    const out = {
+      attn_norm: 2 * H, attn_q: q4(Q, H), attn_q_norm: 2 * hd, attn_output: q4(H, Q), post_attention_norm: 2 * H,
+      ffn_norm: 2 * H, ffn_gate: q4(I, H), ffn_up: q4(I, H), ffn_down: (H * I / 256) * 210, post_ffw_norm: 2 * H,
+    };
+    if (isKvProducer(C, il)) {
+      out.attn_k = q4(KV, H);
+      out.attn_v = q4(KV, H);
+      out.attn_k_norm = 2 * hd;
+    }
+    return out;
+  }
+
+  setLayerWeights(il, tensors) {
+    const need = Object.keys(this.layerTensorBytes(il));
+    for (const name of need) {
+      if (tensors[name] === undefined) throw new Error('layer ' + il + ': missing tensor ' + name);
+    }
+    this.layers[il] = tensors;
+  }
+
+  setGlobals(g) {
+    for (const name of ['tokenEmbed', 'lmHead', 'finalNorm', 'rope_freqs']) {
+      if (g[name] === undefined) throw new Error('missing global ' + name);
+    }
+    this.globals = g;
+  }
+
+  setKvCache(il, k, v) {
+    this.kvCaches[il] = { k: k, v: v };
+  }
+
+  _key(label, key) {
+    if (this.trace) this.trace.push([label, key]);
+  }
+
+  // The WebGPU engine's encodeTransformerPass for `position`. tokenId null:
+  // the embedding lookup reads the token the previous sample left on the
+  // device (src/engine.ts:1724-1727). positionDev true: position / seq_len
+  // are read from the device position counter, which sampleNextToken then
+  // advances (so the pass and the sample can be captured once and replayed).
+  encodeTransformerPass(tokenId, position, positionDev) {
+    const C = this.config;
+    const g = this.g;
+    const c = this.ctx;
+    const W = this.workBuffers;
+    const H = C.hidden_size;
+    const NQH = C.num_q_heads;
+    const NKH = C.num_kv_heads;
+    const eps = C.rms_norm_eps;
+    const seqLen = position + 1;
+    const pd = positionDev ? W.position : null;
+    const G = this.globals;
+
+    this._key('embed', 'embeddingLookup');
+    g.embeddingLookup(c, G.tokenEmbed, C.vocab_size, W.hidden,
+      { hidden_size: H, token_id: tokenId === null ? 0 : tokenId }, tokenId === null ? W.argmaxResult : null);
+
+    for (let il = 0; il < C.num_layers; il++) {
+      const L = this.layers[il];
+      const HD = headDim(C, il);
+      const I = intermediateSize(C, il);
+      const Q = NQH * HD;
+      const KV = NKH * HD;
+      const prod = isKvProducer(C, il);
+      const kv = this.kvCaches[C.kv_producer_for_layer[il]];
+      const own = this.kvCaches[il];
+      const theta = ropeTheta(C, il);
+      const applyDivisor = isSwaLayer(C, il) ? 0 : 1;
+      const window = isSwaLayer(C, il) ? C.sliding_window : 0;
+      // the caller's seq_len (or, from the device, the maximum the scores rows allow)
+      const sl = positionDev ? this.maxSeqLen : seqLen;
+
+      this._key('attn.rmsNorm', 'rmsNorm');
+      g.rmsNorm(c, W.hidden, L.attn_norm, W.normed, { hidden_size: H, eps: eps });
+      const lin = prod ? 'attn.linearQKV.producer' : 'attn.linearQ.consumer';
+      this._key(lin, 'matmulQuant');
+      g.matmulQuant(c, W.normed, L.attn_q, W.q, { M: Q, N: H }, 'q4k');
+      if (prod) {
+        this._key(lin, 'matmulQuant');
+        g.matmulQuant(c, W.normed, L.attn_k, W.k, { M: KV, N: H }, 'q4k');
+        this._key(lin, 'matmulQuant');
+        g.matmulQuant(c, W.normed, L.attn_v, W.v, { M: KV, N: H }, 'q4k');
+        this._key('attn.vNorm', 'perHeadRmsNormNoWeight');
+        g.perHeadRmsNormNoWeight(c, W.v, { num_heads: NKH, head_dim: HD, eps: eps });
+      }
+      const rope = prod ? 'attn.fusedNormRopeQK' : 'attn.fusedNormRopeQ';
+      const rp = (nh) => ({ num_heads: nh, head_dim: HD, eps: eps, position: position, theta: theta,
+        apply_divisor: applyDivisor });
+      this._key(rope, 'fusedPerHeadNormRope');
+      g.fusedPerHeadNormRope(c, W.q, L.attn_q_norm, rp(NQH), G.rope_freqs, pd);
+      if (prod) {
+        this._key(rope, 'fusedPerHeadNormRope');
+        g.fusedPerHeadNormRope(c, W.k, L.attn_k_norm, rp(NKH), G.rope_freqs, pd);
+        this._key('attn.kvCacheStore', 'kvCacheStore');
+        g.kvCacheStore(c, W.k, W.v, own.k, own.v,
+          { num_kv_heads: NKH, head_dim: HD, position: position, max_seq_len: this.maxSeqLen }, pd);
+      }
+      this._key('attn.attnScore', 'attnScore');
+      g.attnScore(c, W.q, kv.k, W.attnScores, { num_q_heads: NQH, num_kv_heads: NKH, head_dim: HD, seq_len: sl,
+        scale: 1.0, sliding_window: window }, pd);
+      this._key('attn.softmax', 'softmax');
+      g.softmax(c, W.attnScores, { num_heads: NQH, seq_len: sl }, pd);
+      this._key('attn.attnOutput', 'attnOutput');
+      g.attnOutput(c, W.attnScores, kv.v, W.attnOut, { num_q_heads: NQH, num_kv_heads: NKH, head_dim: HD,
+        seq_len: sl }, pd);
+      this._key('attn.linearOut', 'matmulQuant');
+      g.matmulQuant(c, W.attnOut, L.attn_output, W.attnProj, { M: H, N: Q }, 'q4k');
+      this._key('attn.postNormAdd', 'fusedNormAdd');
+      g.fusedNormAdd(c, W.attnProj, L.post_attention_norm, W.hidden, W.residual, { size: H, eps: eps });
+      this._key('ffn.rmsNorm', 'rmsNorm');
+      g.rmsNorm(c, W.residual, L.ffn_norm, W.normed, { hidden_size: H, eps: eps });
+      const mm = this.mr4ForFfn ? 'matmulQuantMR4' : 'matmulQuant';
+      this._key('ffn.linearGateUp', mm);
+      g[mm](c, W.normed, L.ffn_gate, W.ffnGate, { M: I, N: H }, 'q4k');
+      this._key('ffn.linearGateUp', mm);
+      g[mm](c, W.normed, L.ffn_up, W.ffnUp, { M: I, N: H }, 'q4k');
+      this._key('ffn.geluMul', 'geluMul');
+      g.geluMul(c, W.ffnGate, W.ffnUp, W.ffnMul, I);
+      this._key('ffn.linearDown', 'matmulQuant');
+      g.matmulQuant(c, W.ffnMul, L.ffn_down, W.ffnDown, { M: H, N: I }, 'q6k');
+      this._key('ffn.postNormAdd', 'fusedNormAdd');
+      g.fusedNormAdd(c, W.ffnDown, L.post_ffw_norm, W.residual, W.hidden, { size: H, eps: eps });
+    }
+    this._key('final.rmsNorm', 'rmsNorm');
+    g.rmsNorm(c, W.hidden, G.finalNorm, W.normed, { hidden_size: H, eps: eps });
+  }
+
+  // sampleNextTokenSubmit's GPU part: LM head, softcap, then argmax (greedy;
+  // the token stays in argmaxResult for the next embed) or top-k 256. With
+  // positionDev the device position counter is advanced by one.
+  sampleNextToken(greedy, positionDev) {
+    const C = this.config;
+    const g = this.g;
+    const c = this.ctx;
+    const W = this.workBuffers;
+    const V = C.vocab_size;
+    this._key('lmHead', 'matmulQuant');
+    g.matmulQuant(c, W.normed, this.globals.lmHead, W.logits, { M: V, N: C.hidden_size }, 'q6k');
+    if (C.final_logit_softcapping > 0) {
+      this._key('logitSoftcap', 'logitSoftcap');
+      g.logitSoftcap(c, W.logits, { size: V, cap: C.final_logit_softcapping });
+    }
+    if (greedy === false) {
+      this._key('sample.topk256', 'topk256');
+      g.topk256(c, W.logits, W.topk256Result, V);
+    } else {
+      this._key('sample.argmax', 'argmax');
+      g.argmax(c, W.logits, W.argmaxResult, V);
+    }
+    if (positionDev) g.advancePosition(c, W.position, 1);
+  }
+
+  // One greedy forward: returns nothing; readToken() reads the sample.
+  forward(tokenId, position) {
+    this.encodeTransformerPass(tokenId, position, false);
+    this.sampleNextToken(true, false);
+  }
+
+  setPosition(position) {
+    this.g.upload(this.ctx, this.workBuffers.position, new Uint32Array([position]));
+  }
+
+  readToken() {
+    return this.g.download(this.ctx, this.workBuffers.argmaxResult, 4).readUInt32LE(0);
+  }
+
+  readF32(name, count) {
+    const b = this.g.download(this.ctx, this.workBuffers[name], 4 * count);
+    return new Float32Array(b.buffer, b.byteOffset, count);
+  }
+}
+
+module.exports = {
+  HipBackend: HipBackend,
+  loadAddon: loadAddon,
+  e2bConfig: e2bConfig,
+  kvProducerMap: kvProducerMap,
+  headDim: headDim,
+  intermediateSize: intermediateSize,
+  isKvProducer: isKvProducer,
+  LAYER_TENSORS: LAYER_TENSORS,
+};

@@ -1,0 +1,76 @@
+'use strict';
+// GPU run of HipBackend through the N-API addon (driven by
+// tests/test_gpu_napi.py, which writes the model and checks the outputs
+// against the oracle): usage `node napi_forward.js <dir>`.
+//   <dir>/config.json  {overrides (e2bConfig), maxSeqLen, position, token}
+//   <dir>/<name>.bin   raw tensor bytes: L<il>.<tensor> per layer, kv<il>.k /
+//                      kv<il>.v (initial f16 caches of the producer layers),
+//                      tokenEmbed, lmHead, finalNorm, rope_freqs
+// Three greedy forwards: (1) token and position as arguments; (2) the token
+// the first one sampled, read on the device; (3) as (2) with the position
+// read on the device, captured once as a graph and replayed. Writes
+// <dir>/out.bin: per forward hidden f32[H], logits f32[V], token u32.
+const fs = require('fs');
+const path = require('path');
+
+const root = path.resolve(__dirname, '..', '..');
+const hb = require(path.join(root, 'gemma4-webgpu_amd', 'node', 'hip_backend.js'));
+
+const dir = process.argv[2];
+const cfg = JSON.parse(fs.readFileSync(path.join(dir, 'config.json'), 'utf8'));
+const C = hb.e2bConfig(cfg.overrides);
+const be = hb.HipBackend.open(C, { maxSeqLen: cfg.maxSeqLen });
+console.log('[napi] device', JSON.stringify(be.g.deviceInfo(be.ctx)));
+
+function upload(name) {
+  const data = fs.readFileSync(path.join(dir, name + '.bin'));
+  const p = be.alloc(data.length);
+  be.g.upload(be.ctx, p, data, 0);
+  return p;
+}
+
+be.allocate();
+for (let il = 0; il < C.num_layers; il++) {
+  const t = {};
+  for (const n of Object.keys(be.layerTensorBytes(il))) t[n] = upload('L' + il + '.' + n);
+  be.setLayerWeights(il, t);
+  if (hb.isKvProducer(C, il)) {
+    const k = fs.readFileSync(path.join(dir, 'kv' + il + '.k.bin'));
+    const v = fs.readFileSync(path.join(dir, 'kv' + il + '.v.bin'));
+    be.g.upload(be.ctx, be.kvCaches[il].k, k, 0);
+    be.g.upload(be.ctx, be.kvCaches[il].v, v, 0);
+  }
+}
+be.setGlobals({ tokenEmbed: upload('tokenEmbed'), lmHead: upload('lmHead'), finalNorm: upload('finalNorm'),
+  rope_freqs: upload('rope_freqs') });
+
+const H = C.hidden_size;
+const V = C.vocab_size;
+const outs = [];
+function collect(i) {
+  be.g.sync(be.ctx);
+  const tok = be.readToken();
+  console.log('[napi] forward ' + i + ': token ' + tok);
+  outs.push(Buffer.from(be.readF32('hidden', H).buffer.slice(0)), Buffer.from(be.readF32('logits', V).buffer.slice(0)),
+    Buffer.from(new Uint32Array([tok]).buffer));
+}
+
+const P = cfg.position;
+be.forward(cfg.token, P);
+collect(1);
+be.encodeTransformerPass(null, P + 1, false);
+be.sampleNextToken(true, false);
+collect(2);
+be.setPosition(P + 2);
+be.g.graphBegin(be.ctx);
+be.encodeTransformerPass(null, P + 2, true);
+be.sampleNextToken(true, true);
+const graph = be.g.graphEnd(be.ctx);
+be.g.graphLaunch(be.ctx, graph);
+collect(3);
+be.g.graphDestroy(graph);
+const pos = be.g.download(be.ctx, be.workBuffers.position, 4).readUInt32LE(0);
+if (pos !== P + 3) throw new Error('device position ' + pos + ', expected ' + (P + 3));
+fs.writeFileSync(path.join(dir, 'out.bin'), Buffer.concat(outs));
+be.close();
+console.log('[napi] done');

@@ -1,0 +1,197 @@
+'use strict';
+// CPU checks of the Node host side (no GPU needed): the N-API addon loads,
+// exports every key, maps library failures to JS Errors carrying the status
+// name and g4_last_error(); HipBackend issues the reference's pass order
+// (src/engine.ts:1505-1625 encodeTransformerPass, :1686-1746 the greedy
+// sample) with each layer's shapes, and the E2B KV producer map
+// (src/config/gemma4-e2b.ts:159-180). Exits non-zero on the first failure.
+const assert = require('assert');
+const path = require('path');
+
+const root = path.resolve(__dirname, '..', '..');
+const hb = require(path.join(root, 'gemma4-webgpu_amd', 'node', 'hip_backend.js'));
+
+function check(name, fn) {
+  fn();
+  console.log('ok ' + name);
+}
+
+const KEYS = ['version', 'lastError', 'init', 'destroy', 'deviceInfo', 'alloc', 'free', 'memset', 'upload',
+  'download', 'sync', 'graphBegin', 'graphEnd', 'graphLaunch', 'graphDestroy', 'fill', 'matmulQuant',
+  'matmulQuantMR4', 'kvCacheStore', 'attnScore', 'softmax', 'attnOutput', 'attnDecodeWorkspaceSize', 'attnDecode',
+  'perHeadRmsNormNoWeight', 'fusedPerHeadNormRope', 'rmsNorm', 'fusedNormAdd', 'geluMul', 'logitSoftcap',
+  'embeddingLookup', 'argmax', 'topk256', 'advancePosition'];
+
+const addon = hb.loadAddon();
+
+check('addon exports every key', () => {
+  assert.deepStrictEqual(Object.keys(addon).sort(), KEYS.slice().sort());
+  assert.strictEqual(addon.version(), 1);
+});
+
+check('init: a context, or without a device G4_ERR_NO_DEVICE with the library message', () => {
+  let err = null;
+  try {
+    const ctx = addon.init(0);
+    assert.strictEqual(typeof ctx, 'bigint');  // a machine with a GPU
+    assert.ok(addon.deviceInfo(ctx).numCus > 0);
+    addon.destroy(ctx);
+    return;
+  } catch (e) {
+    err = e;
+  }
+  assert.ok(err instanceof Error);
+  assert.strictEqual(err.code, 'G4_ERR_NO_DEVICE');
+  assert.ok(err.message.length > 0);
+  assert.strictEqual(err.message, addon.lastError());
+});
+
+check('null context: a key throws G4_ERR_INVALID', () => {
+  assert.throws(() => addon.rmsNorm(null, null, null, null, { hidden_size: 1536, eps: 1e-6 }),
+    (e) => e.code === 'G4_ERR_INVALID' && /null context/.test(e.message));
+});
+
+check('argument types are checked before any call', () => {
+  assert.throws(() => addon.rmsNorm(1, null, null, null, { hidden_size: 1536, eps: 1e-6 }),
+    (e) => e instanceof TypeError && e.code === 'G4_ERR_ARG');
+  assert.throws(() => addon.rmsNorm(null, null, null, null, { hidden_size: 1536 }),
+    (e) => e instanceof TypeError && /eps/.test(e.message));
+  assert.throws(() => addon.matmulQuant(null, null, null, null, { M: 8, N: 256 }, 'q5k'),
+    (e) => e instanceof TypeError);
+});
+
+check('workspace size query needs no device', () => {
+  const n = addon.attnDecodeWorkspaceSize({ num_q_heads: 8, num_kv_heads: 1, head_dim: 256, seq_len: 4096,
+    scale: 1.0, sliding_window: 0 });
+  assert.ok(n > 0);
+});
+
+check('E2B producer map', () => {
+  const C = hb.e2bConfig();
+  const want = [];
+  for (let i = 0; i < 35; i++) want.push(i < 15 ? i : ([19, 24, 29, 34].indexOf(i) >= 0 ? 14 : 13));
+  assert.deepStrictEqual(C.kv_producer_for_layer, want);
+  assert.strictEqual(hb.headDim(C, 4), 512);
+  assert.strictEqual(hb.headDim(C, 5), 256);
+  assert.strictEqual(hb.intermediateSize(C, 14), 6144);
+  assert.strictEqual(hb.intermediateSize(C, 15), 12288);
+});
+
+// A recording stand-in for the addon: every key logs its arguments.
+function mockAddon() {
+  const calls = [];
+  let next = 1;
+  const m = { calls: calls };
+  for (const k of KEYS) m[k] = function () { calls.push([k].concat(Array.prototype.slice.call(arguments))); };
+  m.alloc = () => next++;
+  m.init = () => 'ctx';
+  return m;
+}
+
+// The reference's passes for one layer (src/engine.ts:1544-1613, the
+// matmulQuantMR4 gate/up branch).
+function layerPasses(producer) {
+  const p = [['attn.rmsNorm', 'rmsNorm']];
+  if (producer) {
+    for (let i = 0; i < 3; i++) p.push(['attn.linearQKV.producer', 'matmulQuant']);
+    p.push(['attn.vNorm', 'perHeadRmsNormNoWeight']);
+    p.push(['attn.fusedNormRopeQK', 'fusedPerHeadNormRope'], ['attn.fusedNormRopeQK', 'fusedPerHeadNormRope']);
+    p.push(['attn.kvCacheStore', 'kvCacheStore']);
+  } else {
+    p.push(['attn.linearQ.consumer', 'matmulQuant'], ['attn.fusedNormRopeQ', 'fusedPerHeadNormRope']);
+  }
+  return p.concat([['attn.attnScore', 'attnScore'], ['attn.softmax', 'softmax'], ['attn.attnOutput', 'attnOutput'],
+    ['attn.linearOut', 'matmulQuant'], ['attn.postNormAdd', 'fusedNormAdd'], ['ffn.rmsNorm', 'rmsNorm'],
+    ['ffn.linearGateUp', 'matmulQuantMR4'], ['ffn.linearGateUp', 'matmulQuantMR4'], ['ffn.geluMul', 'geluMul'],
+    ['ffn.linearDown', 'matmulQuant'], ['ffn.postNormAdd', 'fusedNormAdd']]);
+}
+
+check('HipBackend replays the reference pass order with per-layer shapes', () => {
+  const C = hb.e2bConfig();
+  const m = mockAddon();
+  const trace = [];
+  const be = new hb.HipBackend(m, 'ctx', C, { maxSeqLen: 4096, trace: trace });
+  be.allocate();
+  const tensors = (il) => {
+    const t = {};
+    for (const n of Object.keys(be.layerTensorBytes(il))) t[n] = 'L' + il + '.' + n;
+    return t;
+  };
+  for (let il = 0; il < 35; il++) be.setLayerWeights(il, tensors(il));
+  be.setGlobals({ tokenEmbed: 'emb', lmHead: 'head', finalNorm: 'fnorm', rope_freqs: 'rf' });
+  m.calls.length = 0;
+  const pos = 700;
+  be.encodeTransformerPass(42, pos, false);
+  be.sampleNextToken(true, false);
+  let want = [['embed', 'embeddingLookup']];
+  for (let il = 0; il < 35; il++) want = want.concat(layerPasses(il < 15));
+  want = want.concat([['final.rmsNorm', 'rmsNorm'], ['lmHead', 'matmulQuant'], ['logitSoftcap', 'logitSoftcap'],
+    ['sample.argmax', 'argmax']]);
+  assert.deepStrictEqual(trace, want);
+  assert.deepStrictEqual(m.calls.map((c) => c[0]), want.map((w) => w[1]));
+
+  // per-layer shapes and bindings of the calls
+  let at = 1;
+  const W = be.workBuffers;
+  assert.deepStrictEqual(m.calls[0].slice(1, 6), ['ctx', 'emb', 262144, W.hidden, { hidden_size: 1536, token_id: 42 }]);
+  for (let il = 0; il < 35; il++) {
+    const n = layerPasses(il < 15).length;
+    const calls = m.calls.slice(at, at + n);
+    at += n;
+    const hd = [4, 9, 14, 19, 24, 29, 34].indexOf(il) >= 0 ? 512 : 256;
+    const glob = hd === 512;
+    const I = il < 15 ? 6144 : 12288;
+    const src = C.kv_producer_for_layer[il];
+    const by = (k) => calls.filter((c) => c[0] === k);
+    assert.deepStrictEqual(by('matmulQuant')[0].slice(3, 6), ['L' + il + '.attn_q', W.q, { M: 8 * hd, N: 1536 }]);
+    const rope = by('fusedPerHeadNormRope')[0][4];
+    assert.deepStrictEqual(rope, { num_heads: 8, head_dim: hd, eps: 1e-6, position: pos, theta: glob ? 1e6 : 1e4,
+      apply_divisor: glob ? 1 : 0 });
+    const score = by('attnScore')[0];
+    assert.strictEqual(score[3], be.kvCaches[src].k);
+    assert.deepStrictEqual(score[5], { num_q_heads: 8, num_kv_heads: 1, head_dim: hd, seq_len: pos + 1, scale: 1.0,
+      sliding_window: glob ? 0 : 512 });
+    assert.strictEqual(by('attnOutput')[0][3], be.kvCaches[src].v);
+    assert.deepStrictEqual(by('matmulQuantMR4')[0][5], { M: I, N: 1536 });
+    assert.deepStrictEqual(by('matmulQuant').slice(-1)[0].slice(3, 7),
+      ['L' + il + '.ffn_down', W.ffnDown, { M: 1536, N: I }, 'q6k']);
+    if (il < 15) {
+      const st = by('kvCacheStore')[0];
+      assert.deepStrictEqual(st.slice(4, 7), [be.kvCaches[il].k, be.kvCaches[il].v,
+        { num_kv_heads: 1, head_dim: hd, position: pos, max_seq_len: 4096 }]);
+    } else {
+      assert.strictEqual(by('kvCacheStore').length, 0);
+      assert.strictEqual(be.kvCaches[il], be.kvCaches[src]);
+    }
+  }
+});
+
+check('device-side token and position: the pass reads them, the sample advances the position', () => {
+  const bad = hb.e2bConfig({ num_layers: 2, num_unshared_layers: 1, global_layers: [1], vocab_size: 4096 });
+  assert.throws(() => new hb.HipBackend(mockAddon(), 'ctx', bad, {}).allocate(), /no unshared layer/);
+  const C = hb.e2bConfig({ num_layers: 3, num_unshared_layers: 2, global_layers: [1], vocab_size: 4096 });
+  const m = mockAddon();
+  const be = new hb.HipBackend(m, 'ctx', C, { maxSeqLen: 1024 });
+  be.allocate();
+  for (let il = 0; il < 3; il++) {
+    const t = {};
+    for (const n of Object.keys(be.layerTensorBytes(il))) t[n] = n;
+    be.setLayerWeights(il, t);
+  }
+  be.setGlobals({ tokenEmbed: 'emb', lmHead: 'head', finalNorm: 'fnorm', rope_freqs: 'rf' });
+  m.calls.length = 0;
+  be.encodeTransformerPass(null, 0, true);
+  be.sampleNextToken(true, true);
+  const W = be.workBuffers;
+  assert.strictEqual(m.calls[0][6], W.argmaxResult);            // embedding of the sampled token
+  for (const c of m.calls.filter((x) => ['attnScore', 'attnOutput'].indexOf(x[0]) >= 0)) {
+    assert.strictEqual(c[6], W.position);
+    assert.strictEqual(c[5].seq_len, 1024);                      // the bound, the device value is read
+  }
+  assert.strictEqual(m.calls.filter((x) => x[0] === 'kvCacheStore')[0][7], W.position);
+  const last = m.calls[m.calls.length - 1];
+  assert.deepStrictEqual(last, ['advancePosition', 'ctx', W.position, 1]);
+  assert.throws(() => be.setLayerWeights(0, {}), /missing tensor/);
+});
+
+console.log('all node CPU checks passed');
