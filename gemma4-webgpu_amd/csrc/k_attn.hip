@@ -684,6 +684,86 @@ __global__ __launch_bounds__(1024) void attn_merge_kernel(const float* ws, float
   if (ops) merge_ops<HD>(grp == 0 ? y : 0.f, grp == 0, ops, ntv, seq, hq, d);
 }
 
+// Merge of many chunk partials (long contexts): the grid also splits each
+// head's dims into slices of MW_D, so a head's partials are read by HD / MW_D
+// workgroups at once instead of one. Thread t holds chunk t's (m, l) and
+// thread (g, j) the o of dim d0 + j of chunks g, g + MW_G, ...; all of these
+// loads are issued together, then the maximum, the weights exp(m - M) (in
+// LDS) and the sums are formed, and the MW_G groups are added in LDS.
+// Chunks with l == 0 are skipped, as in attn_merge_kernel.
+constexpr uint32_t kMaxSplits = 1024;  // merge kernel limit; 64 * 1024 = 65536 positions
+constexpr int MW_D = 32;               // dims per workgroup
+constexpr int MW_G = 32;               // chunk groups
+constexpr int MW_NT = MW_D * MW_G;     // threads: one (m, l) each
+constexpr int MW_OU = (int)(kMaxSplits / MW_G);
+constexpr uint32_t kMergeWideMin = 64;  // fewer splits merge in attn_merge_kernel
+static_assert(MW_NT >= (int)kMaxSplits, "one chunk's (m, l) per thread");
+template <int HD>
+__global__ __launch_bounds__(MW_NT) void attn_merge_wide_kernel(const float* ws, float* out, uint32_t nqh,
+                                                               uint32_t nkh, uint32_t G, uint32_t nsplit,
+                                                               uint32_t num_seqs, LenArgs la, uint32_t chunk) {
+  __shared__ float w_s[kMaxSplits];  // weight of each chunk
+  __shared__ float red_s[2 * (MW_NT / 64)];
+  __shared__ float acc_s[MW_G * (MW_D + 1)];
+  const uint32_t hq = blockIdx.x, seq = blockIdx.y, d0 = blockIdx.z * MW_D;
+  const uint32_t kvh = hq / G, h = hq % G;
+  const size_t nparts = (size_t)num_seqs * nkh * nsplit * G;
+  const float* ws_m = ws;
+  const float* ws_l = ws + nparts;
+  const float* ws_o = ws + 2 * nparts;
+  const size_t base = ((size_t)seq * nkh + kvh) * nsplit * G + h;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  const uint32_t g = tid / MW_D, j = tid % MW_D;
+  // every planned chunk's partial is loaded without waiting for the live
+  // length (the workspace holds nsplit chunks); chunks past it are masked
+  // afterwards by selection, so stale values never enter a sum
+  float mc = -INFINITY, lc = 0.f;
+  if (tid < nsplit) {
+    mc = ws_m[base + (size_t)tid * G];
+    lc = ws_l[base + (size_t)tid * G];
+  }
+  float ov[MW_OU];
+#pragma unroll
+  for (int u = 0; u < MW_OU; ++u) {
+    const uint32_t c = g + (uint32_t)u * MW_G;
+    ov[u] = c < nsplit ? ws_o[(base + (size_t)c * G) * HD + d0 + j] : 0.f;
+  }
+  uint32_t wstart, n;
+  live_window(la, seq, wstart, n);
+  const uint32_t ns = min(nsplit, (n + chunk - 1) / chunk);
+#pragma unroll
+  for (int u = 0; u < MW_OU; ++u)
+    if (g + (uint32_t)u * MW_G >= ns) ov[u] = 0.f;
+  if (tid >= ns || !(lc > 0.f)) {
+    mc = -INFINITY;
+    lc = 0.f;
+  }
+  const float wm = g4d::wave_max_dpp(mc);
+  if (lane == 0) red_s[wv] = wm;
+  __syncthreads();
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < MW_NT / 64; ++w) M = fmaxf(M, red_s[w]);
+  const float wt = mc == -INFINITY ? 0.f : mq_exp(mc - M);
+  if (tid < kMaxSplits) w_s[tid] = wt;
+  const float wl = g4d::wave_sum_dpp(wt * lc);
+  if (lane == 0) red_s[MW_NT / 64 + wv] = wl;
+  __syncthreads();
+  float Ls = 0.f;
+#pragma unroll
+  for (int w = 0; w < MW_NT / 64; ++w) Ls += red_s[MW_NT / 64 + w];
+  float acc = 0.f;
+#pragma unroll
+  for (int u = 0; u < MW_OU; ++u) acc += w_s[g + u * MW_G] * ov[u];
+  acc_s[g * (MW_D + 1) + j] = acc;
+  __syncthreads();
+  if (g != 0) return;
+  float t = 0.f;
+#pragma unroll 8
+  for (int gg = 0; gg < MW_G; ++gg) t += acc_s[gg * (MW_D + 1) + j];
+  out[((size_t)seq * nqh + hq) * HD + d0 + j] = Ls > 0.f ? t / Ls : 0.f;
+}
+
 // ---------------------------------------------------------------------------
 // matrix-core split-K decode attention: 8 query heads per KV head, head_dim 256
 // ---------------------------------------------------------------------------
@@ -996,7 +1076,9 @@ typedef float mqf_f4 __attribute__((ext_vector_type(4)));
 constexpr int kScDevice = 16;  // cache policy operand: sc1 (device scope)
 // Merge tree: chunk partials are merged in groups of up to MQF_FAN by the
 // last workgroup of each group to arrive; with more than one group, the last
-// group merger merges the group partials. Two levels: MQF_FAN^2 chunks.
+// group merger merges the group partials (two levels: MQF_FAN^2 chunks). The
+// plan uses the tree for windows of up to MQF_FAN chunks (one level); longer
+// windows end in the merge launch (mqf_kernel<true>).
 constexpr uint32_t MQF_FAN = 16, MQF_CNT = 32;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(float* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, 0x00020000);
@@ -1064,6 +1146,10 @@ __device__ __forceinline__ void mqf_warm(const MqfArgs& a) {
   asm volatile("" ::"v"(acc));
 }
 
+// LONG (windows past MQF_FAN chunks): K/V rows are loaded non-temporally
+// (read once, measured faster at 32K positions) and the workgroups end after
+// storing their partials, which the merge launch that follows combines.
+template <bool LONG>
 __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
   if (blockIdx.x >= a.max_chunks) {  // (uniform) L2 warming workgroups
     if (blockIdx.y == 0) mqf_warm(a);
@@ -1108,7 +1194,8 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
       const uint32_t r = pc >> 5, col = (pc & 31) * 8;
       const uint32_t p = min(wstart + c0 + st * MQ_STEP + r, last);
       const uint16_t* base = i < 8 ? a.kc : a.vc;
-      pf[i] = *(const mu4*)(base + ((size_t)p * a.nkh + kvh) * MQ_HD + col);
+      const mu4* src = (const mu4*)(base + ((size_t)p * a.nkh + kvh) * MQ_HD + col);
+      pf[i] = LONG ? __builtin_nontemporal_load(src) : *src;
     }
   };
   auto store_step = [&]() {
@@ -1330,6 +1417,7 @@ __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
 #pragma unroll
     for (int h = 0; h < MQ_G; ++h) st_dev(r0, (uint32_t)(2 * nparts + (part0 + h) * MQ_HD + tid) * 4u, o[h]);
   }
+  if constexpr (LONG) return;  // the merge launch that follows combines the chunks
 
   // ---- merge tree: the last arriver of each group merges it in chunk order ----
   // thread (head th, dims td.. and td + 128..): one pass with a running maximum
@@ -1555,7 +1643,6 @@ __global__ __launch_bounds__(NT) void paged_store_kernel(const float* k_in, cons
 // host side
 // ---------------------------------------------------------------------------
 
-constexpr uint32_t kMaxSplits = 1024;  // merge kernel limit; 64 * 1024 = 65536 positions
 
 struct SplitPlan {
   int cp;           // 32-position blocks per split (1 or 2)
@@ -1607,25 +1694,33 @@ int launch_attn(g4_ctx* ctx, const AttnArgs& a, uint32_t G, uint32_t hd, int cp,
                        hd);
 }
 
-// Fused single-sequence plan: one 64-position step per workgroup up to
-// MQF_FAN^2 chunks (so a long context is read by as many CUs as it has
-// chunks), more steps beyond. The arrival counters sit in the first kMqfCnt
-// bytes of the workspace, at the same place whatever the plan, so that
-// layers of different windows can share one workspace; the chunk partials
-// follow, then the group partials.
+// Fused single-sequence plan: one 64-position step per workgroup. Up to
+// MQF_FAN chunks the last workgroup to arrive merges them in the launch
+// (one level of the merge tree); beyond, the workgroups store their
+// partials and end, and a merge launch combines them (two dependent
+// device-scope round trips per tree level cost more than a launch boundary,
+// and the merge launch spreads each head's partials over many workgroups).
+// Past kMaxSplits chunks a workgroup takes several steps. The arrival
+// counters sit in the first kMqfCnt bytes of the workspace, at the same
+// place whatever the plan, so that layers of different windows can share
+// one workspace; the chunk partials follow, then the group partials.
 constexpr uint32_t kMqfMaxKvHeads = 64;
 constexpr size_t kMqfCnt = (size_t)kMqfMaxKvHeads * MQF_CNT * sizeof(uint32_t);
 struct MqfPlan {
   uint32_t nstep, max_chunks;
+  bool partials;  // chunk partials + a merge launch
   size_t bytes_ws0, bytes;
 };
 MqfPlan mqf_plan(const g4_attn_fused_params& p) {
   MqfPlan m{};
   const uint32_t eff = std::max(eff_len(p.max_seq_len, p.sliding_window), 1u);
-  m.nstep = std::max(1u, ceil_div(eff, MQ_STEP * MQF_FAN * MQF_FAN));
+  m.partials = ceil_div(eff, MQ_STEP) > MQF_FAN;
+  // two steps per workgroup past 16K positions (fewer partials to merge;
+  // measured 1.2 us faster at 32K)
+  m.nstep = m.partials ? std::max(eff > 16384 ? 2u : 1u, ceil_div(eff, MQ_STEP * kMaxSplits)) : 1u;
   m.max_chunks = ceil_div(eff, MQ_STEP * m.nstep);
   m.bytes_ws0 = ws_bytes(1, p.num_kv_heads, m.max_chunks, MQ_G, MQ_HD);
-  m.bytes = kMqfCnt + m.bytes_ws0 + ws_bytes(1, p.num_kv_heads, MQF_FAN, MQ_G, MQ_HD);
+  m.bytes = kMqfCnt + m.bytes_ws0 + (m.partials ? 0 : ws_bytes(1, p.num_kv_heads, MQF_FAN, MQ_G, MQ_HD));
   return m;
 }
 
@@ -1633,6 +1728,25 @@ LenArgs len_args(const AttnArgs& a) { return LenArgs{a.seq_lens, a.pos_dev, a.se
 
 int merge_launch(g4_ctx* ctx, const float* ws, float* out, uint32_t nqh, uint32_t nkh, uint32_t G, uint32_t hd,
                  uint32_t nsplit, uint32_t num_seqs, const LenArgs& la, uint32_t chunk, uint8_t* ops = nullptr) {
+  if (!ops && nsplit >= kMergeWideMin && nsplit <= kMaxSplits) {
+    const dim3 wg(nqh, num_seqs, hd / MW_D);
+    switch (hd) {
+      case 128:
+        hipLaunchKernelGGL(attn_merge_wide_kernel<128>, wg, dim3(MW_D * MW_G), 0, ctx->stream, ws, out, nqh, nkh, G,
+                           nsplit, num_seqs, la, chunk);
+        break;
+      case 256:
+        hipLaunchKernelGGL(attn_merge_wide_kernel<256>, wg, dim3(MW_D * MW_G), 0, ctx->stream, ws, out, nqh, nkh, G,
+                           nsplit, num_seqs, la, chunk);
+        break;
+      default:
+        hipLaunchKernelGGL(attn_merge_wide_kernel<512>, wg, dim3(MW_D * MW_G), 0, ctx->stream, ws, out, nqh, nkh, G,
+                           nsplit, num_seqs, la, chunk);
+        break;
+    }
+    G4_LAUNCHED(ctx, "attn_merge_wide");
+    return G4_OK;
+  }
   const int ntv = (int)(g4d::pad_batch(num_seqs) / 16);
   const dim3 mg(nqh, num_seqs);
   switch (hd) {
@@ -2027,10 +2141,17 @@ int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, 
       m.wwgb[i] = (uint32_t)regions[i].wg_bytes;
       m.wnwg[i] = regions[i].nwgs;
     }
-    hipLaunchKernelGGL(mqf_kernel, dim3(mp.max_chunks + m.nwarm, p.num_kv_heads), dim3(NT),
-                       m.nwarm ? kWarmLds : 0, ctx->stream, m);
+    if (mp.partials)
+      hipLaunchKernelGGL(mqf_kernel<true>, dim3(mp.max_chunks + m.nwarm, p.num_kv_heads), dim3(NT),
+                         m.nwarm ? kWarmLds : 0, ctx->stream, m);
+    else
+      hipLaunchKernelGGL(mqf_kernel<false>, dim3(mp.max_chunks + m.nwarm, p.num_kv_heads), dim3(NT),
+                         m.nwarm ? kWarmLds : 0, ctx->stream, m);
     G4_LAUNCHED(ctx, "attn_decode_fused_mfma");
-    return G4_OK;
+    if (!mp.partials) return G4_OK;
+    const LenArgs la{nullptr, position_dev, p.max_seq_len, p.max_seq_len, p.sliding_window};
+    return merge_launch(ctx, m.ws, output, p.num_q_heads, p.num_kv_heads, MQ_G, MQ_HD, mp.max_chunks, 1, la,
+                        MQ_STEP * mp.nstep);
   }
   // (the two-launch form computes the RoPE per call: a table is not needed)
   const SplitPlan sp = plan_splits(eff_len(p.max_seq_len, p.sliding_window));
