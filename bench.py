@@ -440,6 +440,26 @@ def decode_rate(ctx, shape, start, steps, warmup, embed=False, warm=True):
     return res
 
 
+def prefill_rate(ctx, shape, T=512, B=64, reps=3):
+    """Batched prefill of one T-token prompt from position 0 (B tokens per
+    matrix-core step, T / B steps): prompt tokens/s."""
+    d = BatchDecoder(ctx, [0] * B, shape, reserve=T + 8, seed=0, shared_pages=True, embed=True)
+    ctx.sync()
+    toks = np.random.default_rng(5).integers(0, shape.vocab, T)
+    d.prefill(toks[:B], 0)  # warm-up
+    times = []
+    for _ in range(reps):
+        a = ctx.record()
+        d.prefill(toks, 0)
+        b = ctx.record()
+        times.append(ctx.elapsed_ms(a, b))
+    ms = min(times)
+    res = {"tokens": T, "chunk": B, "ms": round(ms, 3), "tok_s": round(T / ms * 1e3, 1),
+           "ms_per_chunk": round(ms / (T // B), 3)}
+    del d
+    return res
+
+
 def _cpu_threads():
     """Host threads this process may use (the box's CPU share, at most 16)."""
     try:
@@ -712,12 +732,16 @@ def main():
     for start in [int(x) for x in args.positions.split(",") if x.strip()]:
         positions[f"start{start}"] = decode_rate(ctx, E2BShape(), start, args.pos_steps, args.pos_warmup)
         log(f"decode from position {start}: {positions[f'start{start}']}")
+    prefill = {"uniform": prefill_rate(ctx, E2BShape())}
+    log(f"prefill: {prefill}")
     real = {}
     if not args.no_real_layout:
         for start in (START_POS, 4096):
             real[f"start{start}"] = decode_rate(ctx, E2BShape.real(), start, args.pos_steps, args.pos_warmup,
                                                 embed=True)
             log(f"real E2B layout from position {start}: {real[f'start{start}']}")
+        prefill["real_e2b_layout"] = prefill_rate(ctx, E2BShape.real())
+        log(f"prefill (real layout): {prefill['real_e2b_layout']}")
 
     batch = {}
     for B in [int(b) for b in args.batch_sweep.split(",") if b.strip()]:
@@ -726,7 +750,7 @@ def main():
     if args.no_census:
         print(json.dumps({"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": ms_step,
                           "decode_from_position": positions, "real_e2b_layout": real,
-                          "batch_decode": batch}), flush=True)
+                          "prefill": prefill, "batch_decode": batch}), flush=True)
         return
     census = kernel_census(ctx, dec, args.census_reps)
     for k, v in census.items():
@@ -779,6 +803,7 @@ def main():
         "kernel_census_us": {k: round(per_step[k], 2) for k in per_step},
         "decode_from_position": positions,
         "real_e2b_layout": real,
+        "prefill": prefill,
         "batch_decode": batch,
         "attention_decode": attn3,
         "lm_head_sampling": head,

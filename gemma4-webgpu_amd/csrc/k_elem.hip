@@ -443,10 +443,12 @@ int g4_geluMul(g4_ctx* ctx, const float* gate, const float* up, float* output, u
 // shaders/embedding_lookup.wgsl:9-13: one thread per hidden element; the row is
 // token * H, scaled by sqrt(H) in f32. The f16 row is read 8 halves (16 B) per
 // thread when H is a multiple of 8 and the table 16-byte aligned, else one.
+// blockIdx.y = output row: token_dev[y] (or `token` for the one-row host form).
 __global__ __launch_bounds__(NT) void embedding_lookup_kernel(const uint16_t* __restrict__ emb, uint32_t rows,
                                                               float* __restrict__ out, uint32_t H, uint32_t token,
                                                               const uint32_t* __restrict__ token_dev, int vec8) {
-  const uint32_t tok = token_dev ? *token_dev : token;
+  const uint32_t tok = token_dev ? token_dev[blockIdx.y] : token;
+  out += (size_t)blockIdx.y * H;
   const float scale = sqrtf(static_cast<float>(H));
   const uint32_t t = blockIdx.x * NT + threadIdx.x;
   if (vec8) {
@@ -474,14 +476,14 @@ __global__ __launch_bounds__(NT) void embedding_lookup_kernel(const uint16_t* __
 }
 
 static int embedding_lookup(g4_ctx* ctx, const uint16_t* emb, uint32_t rows, float* out, g4_embedding_params p,
-                            const uint32_t* token_dev) {
+                            const uint32_t* token_dev, uint32_t count = 1) {
   G4_REQUIRE(emb && out, "g4_embeddingLookup: null buffer");
-  if (!p.hidden_size) return G4_OK;
+  if (!p.hidden_size || !count) return G4_OK;
   const int vec8 = p.hidden_size % 8 == 0 && reinterpret_cast<uintptr_t>(emb) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(out) % 16 == 0;
   const uint32_t threads = vec8 ? p.hidden_size / 8 : p.hidden_size;
-  hipLaunchKernelGGL(embedding_lookup_kernel, dim3(ceil_div(threads, NT)), dim3(NT), 0, ctx->stream, emb, rows, out,
-                     p.hidden_size, p.token_id, token_dev, vec8);
+  hipLaunchKernelGGL(embedding_lookup_kernel, dim3(ceil_div(threads, NT), count), dim3(NT), 0, ctx->stream, emb, rows,
+                     out, p.hidden_size, p.token_id, token_dev, vec8);
   G4_LAUNCHED(ctx, "embedding_lookup");
   return G4_OK;
 }
@@ -498,6 +500,14 @@ int g4_embeddingLookup_dev(g4_ctx* ctx, const uint16_t* embedding, uint32_t num_
   G4_ENTER(ctx);
   G4_REQUIRE(token_dev, "g4_embeddingLookup_dev: null token");
   return embedding_lookup(ctx, embedding, num_rows, output, p, token_dev);
+}
+
+int g4_embeddingLookupBatch(g4_ctx* ctx, const uint16_t* embedding, uint32_t num_rows, float* output,
+                            uint32_t hidden_size, const uint32_t* tokens_dev, uint32_t count) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(tokens_dev, "g4_embeddingLookupBatch: null tokens");
+  G4_REQUIRE(count <= 65535, "g4_embeddingLookupBatch: %u rows > 65535", count);
+  return embedding_lookup(ctx, embedding, num_rows, output, g4_embedding_params{hidden_size, 0u}, tokens_dev, count);
 }
 
 int g4_logitSoftcap(g4_ctx* ctx, float* logits, g4_softcap_params p) {

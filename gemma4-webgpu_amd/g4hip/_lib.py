@@ -177,6 +177,7 @@ SIGNATURES = {
     "g4_logitSoftcap": (_I, [_P, _P, SoftcapParams]),
     "g4_embeddingLookup": (_I, [_P, _P, _U32, _P, EmbeddingParams]),
     "g4_embeddingLookup_dev": (_I, [_P, _P, _U32, _P, EmbeddingParams, _P]),
+    "g4_embeddingLookupBatch": (_I, [_P, _P, _U32, _P, _U32, _P, _U32]),
     "g4_advancePosition": (_I, [_P, _P, _U32]),
     "g4_argmax": (_I, [_P, _P, _P, _U32]),
     "g4_topk256": (_I, [_P, _P, _P, _U32]),

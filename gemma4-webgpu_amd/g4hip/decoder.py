@@ -458,29 +458,37 @@ class BatchDecoder(_SyntheticModel):
 
     def __init__(self, ctx: Context, context_lens, shape: Optional[E2BShape] = None, page_size: int = 16,
                  reserve: int = 64, seed: int = 0, n_layers: Optional[int] = None, lm_head: bool = True,
-                 page_seed: int = 7):
+                 page_seed: int = 7, shared_pages: bool = False, embed: bool = False):
+        """shared_pages: every row reads and appends through one page list
+        (the rows are tokens of one sequence: batched prefill). embed: an f16
+        token table; each step starts from the embedding of every row's
+        token in `tokens` (the previous step's sample, or the prompt)."""
         lens = np.asarray(context_lens, dtype=np.int64)
         if lens.ndim != 1 or lens.size == 0 or lens.size > 64 or np.any(lens < 0):
             raise ValueError("context_lens: 1..64 non-negative lengths")
         s0 = shape or E2BShape()
         self.B = int(lens.size)
         self.page_size = page_size
+        self.shared_pages = shared_pages
         self.max_seq = int(lens.max()) + reserve
         self.max_pages = -(-self.max_seq // page_size)
-        per_seq = [-(-(int(L) + reserve) // page_size) for L in lens]
+        per_seq = [self.max_pages] if shared_pages else [-(-(int(L) + reserve) // page_size) for L in lens]
         self.num_pages = int(sum(per_seq))
         order = np.random.default_rng(page_seed).permutation(self.num_pages).astype(np.int32)
         table = np.full((self.B, self.max_pages), -1, np.int32)
-        at = 0
-        for i, n in enumerate(per_seq):
-            table[i, :n] = order[at:at + n]
-            at += n
+        if shared_pages:
+            table[:, :] = order[None, :self.max_pages]
+        else:
+            at = 0
+            for i, n in enumerate(per_seq):
+                table[i, :n] = order[at:at + n]
+                at += n
         self.page_table_host = table
         self.lens_host = lens.astype(np.uint32)
         rows = self.num_pages * page_size
         self._build_weights(ctx, shape, n_layers, seed, lm_head,
                             lambda il: (ctx.zeros(rows * self.s.kv_dim_of(il), np.uint16),
-                                        ctx.zeros(rows * self.s.kv_dim_of(il), np.uint16)))
+                                        ctx.zeros(rows * self.s.kv_dim_of(il), np.uint16)), embed=embed)
         s, B, f32 = self.s, self.B, np.float32
         self.page_table = ctx.from_numpy(table)
         self.seq_lens = ctx.from_numpy(self.lens_host)
@@ -567,6 +575,8 @@ class BatchDecoder(_SyntheticModel):
         per-sequence argmax (or top-k 256)."""
         c, s, B = self.ctx, self.s, self.B
         H = s.hidden
+        if self.embedding is not None:
+            c.embeddingLookupBatch(self.embedding, s.vocab, self.hidden, H, self.tokens, B)
         c.advanceSeqLens(self.seq_lens, B, 1)
         nd = 0
         for il, L in enumerate(self.layers):
@@ -610,6 +620,44 @@ class BatchDecoder(_SyntheticModel):
             else:
                 c.topk256Batch(self.logits, self.topk, s.vocab, B)
         self.lens_host = self.lens_host + 1
+
+    def prefill(self, tokens, start: int = 0, sample: str = "argmax") -> int:
+        """Batched prefill of one sequence (a shared_pages decoder with an
+        embedding table): the prompt's tokens at positions start, start + 1,
+        ... go through the layers B at a time, each chunk one step of the
+        ragged path in which row r embeds its token, appends its K/V row at
+        its own position and attends to the positions up to it (the
+        prologue launch appends every row of the chunk before the attention
+        launch reads them, so the chunk is causal). The reference runs one
+        full forward per prompt token instead (src/engine.ts:1923-1938) and
+        samples from the last one (src/engine.ts:2014-2017). A short last
+        chunk repeats its last token and position in the spare rows
+        (identical rows, identical writes). Returns the row of the final
+        chunk that holds the prompt's last token: its logits and `tokens`
+        entry are the first sample."""
+        if not self.shared_pages or self.embedding is None:
+            raise ValueError("prefill needs a shared_pages decoder with an embedding table")
+        toks = np.asarray(tokens, np.uint32)
+        T, B = int(toks.size), self.B
+        if T == 0 or start + T > self.max_seq - 1:
+            raise ValueError(f"prefill: {T} tokens from {start} do not fit {self.max_seq} positions")
+        nch = -(-T // B)
+        n = T - (nch - 1) * B
+        pad = nch * B - T
+        # every chunk's tokens and lengths (before the step appends each row)
+        # uploaded once; the chunks then run back to back on the stream
+        ctok = np.concatenate([toks, np.repeat(toks[-1], pad)]).astype(np.uint32)
+        cpos = np.concatenate([start + np.arange(T), np.repeat(start + T - 1, pad)]).astype(np.uint32)
+        dtok, dpos = self.ctx.from_numpy(ctok), self.ctx.from_numpy(cpos)
+        for k in range(nch):
+            self.ctx.copy(self.tokens, dtok.offset(4 * B * k), 4 * B)
+            self.ctx.copy(self.seq_lens, dpos.offset(4 * B * k), 4 * B)
+            self.lens_host = cpos[B * k:B * (k + 1)].copy()
+            self.step(sample)
+        self.ctx.sync()
+        dtok.free()
+        dpos.free()
+        return n - 1
 
     def capture(self, sample: str = "argmax"):
         """The step as a HIP graph; each replay appends one token per sequence."""

@@ -502,6 +502,12 @@ class Context:
         else:
             check(lib().g4_embeddingLookup_dev(self.h, _p(embedding), num_rows, _p(out), p, _p(token_dev)))
 
+    def embeddingLookupBatch(self, embedding: Ptr, num_rows: int, out: Ptr, hidden_size: int, tokens_dev: Ptr,
+                             count: int) -> None:
+        """Row r of out [count][hidden_size] = the embedding of tokens_dev[r]."""
+        check(lib().g4_embeddingLookupBatch(self.h, _p(embedding), num_rows, _p(out), hidden_size, _p(tokens_dev),
+                                            count))
+
     def advancePosition(self, position_dev: Ptr, delta: int = 1) -> None:
         check(lib().g4_advancePosition(self.h, _p(position_dev), delta))
 

@@ -385,6 +385,14 @@ int g4_embeddingLookup(g4_ctx* ctx, const uint16_t* embedding, uint32_t num_rows
 int g4_embeddingLookup_dev(g4_ctx* ctx, const uint16_t* embedding, uint32_t num_rows, float* output,
                            g4_embedding_params p, const uint32_t* token_dev);
 
+/* `count` lookups at once: output row r [hidden_size] from tokens_dev[r] (a
+ * token >= num_rows writes a zero row). The embedding of every row of a
+ * multi-sequence step, or of every prompt token of a batched prefill
+ * (src/engine.ts:1923-1938 runs one embedding lookup per prompt token);
+ * count <= 65535. */
+int g4_embeddingLookupBatch(g4_ctx* ctx, const uint16_t* embedding, uint32_t num_rows, float* output,
+                            uint32_t hidden_size, const uint32_t* tokens_dev, uint32_t count);
+
 /* *position_dev += delta on the stream: the device-side step counter that lets
  * a captured decode graph be replayed token after token (the role of the
  * per-forward uniform patches, src/engine.ts:1487-1504). */
