@@ -326,10 +326,27 @@ def lm_head_sampling(ctx, reps=10):
 
 def batch_census(ctx, bd, reps=10):
     """Average us per launch kind of the ragged step, each kind captured over
-    all 35 layers (weights rotate through HBM as in the step)."""
+    all 35 layers (weights rotate through HBM as in the step). Algorithmic
+    bytes per launch: the weights once, the activations read (f32 or their
+    operand blocks) and the outputs written; the attention kinds read every
+    sequence's K/V window of one layer."""
     c, s, B = ctx, bd.s, bd.B
     H, Q, KV, I = s.hidden, s.q_dim, s.kv_dim, s.ffn
     Ls = bd.layers
+    q4 = lambda M, N: M * N // 256 * 144  # noqa: E731
+    q6 = lambda M, N: M * N // 256 * 210  # noqa: E731
+    n_glob = sum(1 for il in range(s.n_layers) if s.is_global(il))
+    kv_glob = sum(int(L) + 1 for L in bd.lens_host) * KV * 4
+    kv_loc = sum(min(int(L) + 1, s.window) for L in bd.lens_host) * KV * 4
+    act = lambda N: ctx.batch_operand_bytes(N, B)  # noqa: E731
+    nbytes = {
+        "qkv": q4(Q + 2 * KV, H) + act(H) + bd.ks_h * B * (Q + 2 * KV) * 4,
+        "attn_global": kv_glob + B * Q * 4 * 2,
+        "attn_window512": kv_loc + B * Q * 4 * 2,
+        "o": q4(H, Q) + act(Q) + bd.ks_q * B * H * 4,
+        "gate_up_gelu": 2 * q4(I, H) + act(H) + B * I * 4,
+        "down": q6(H, I) + B * I * 4 + bd.ks_f * B * H * 4,
+    }
     kinds = {
         "prep_attn": lambda il, L: c.batchPrep(bd.down_parts, bd.ks_f // 2, L.post_ffn_norm, bd.hidden2, L.attn_norm,
                                                bd.hidden, bd.xn, H, B, s.eps, ops=bd.xops),
@@ -364,9 +381,15 @@ def batch_census(ctx, bd, reps=10):
                     n[0] += 1
         us = graph_us(ctx, run, reps)
         out[name] = {"us_per_launch": round(us / n[0], 2), "per_step_us": round(us, 1), "launches": n[0]}
+        if name in nbytes:
+            gbps = nbytes[name] / (us / n[0] * 1e-6) / 1e9
+            out[name].update({"bytes": nbytes[name], "gbps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4)})
     us = graph_us(ctx, lambda: c.matmulSegmentsBatchPartial("q6k", bd.xn, [bd.lm_head], [bd.logits], [s.vocab], H,
                                                             B, 1, ops=bd.xops, softcap=s.softcap), max(3, reps // 2))
-    out["lm_head_softcap"] = {"us_per_launch": round(us, 2), "per_step_us": round(us, 1), "launches": 1}
+    nb = s.lm_head_bytes() + act(H) + B * s.vocab * 4
+    out["lm_head_softcap"] = {"us_per_launch": round(us, 2), "per_step_us": round(us, 1), "launches": 1, "bytes": nb,
+                              "gbps": round(nb / (us * 1e-6) / 1e9, 1),
+                              "frac": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
     return out
 
 
@@ -661,6 +684,9 @@ def main():
     ap.add_argument("--pos-warmup", type=int, default=10)
     ap.add_argument("--no-real-layout", action="store_true",
                     help="skip the decode runs of Gemma-4-E2B's own layer layout")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill runs")
+    ap.add_argument("--attn-only", action="store_true",
+                    help="time only the decode attention of config 3 (the launches a profiler should see)")
     ap.add_argument("--batch-steps", type=int, default=30)
     ap.add_argument("--batch-warmup", type=int, default=5)
     ap.add_argument("--batch-sweep", default="1,8,32,64",
@@ -683,6 +709,9 @@ def main():
         return
     if args.calib_only:
         print(json.dumps({"calibration": calibration_reads(ctx)}), flush=True)
+        return
+    if args.attn_only:
+        print(json.dumps({"attention_decode": attention_cfg3(ctx)}), flush=True)
         return
     s = E2BShape()
     max_seq = START_POS + args.warmup + args.steps + 64
@@ -732,7 +761,7 @@ def main():
     for start in [int(x) for x in args.positions.split(",") if x.strip()]:
         positions[f"start{start}"] = decode_rate(ctx, E2BShape(), start, args.pos_steps, args.pos_warmup)
         log(f"decode from position {start}: {positions[f'start{start}']}")
-    prefill = {"uniform": prefill_rate(ctx, E2BShape())}
+    prefill = {} if args.no_prefill else {"uniform": prefill_rate(ctx, E2BShape())}
     log(f"prefill: {prefill}")
     real = {}
     if not args.no_real_layout:
@@ -740,8 +769,9 @@ def main():
             real[f"start{start}"] = decode_rate(ctx, E2BShape.real(), start, args.pos_steps, args.pos_warmup,
                                                 embed=True)
             log(f"real E2B layout from position {start}: {real[f'start{start}']}")
-        prefill["real_e2b_layout"] = prefill_rate(ctx, E2BShape.real())
-        log(f"prefill (real layout): {prefill['real_e2b_layout']}")
+        if not args.no_prefill:
+            prefill["real_e2b_layout"] = prefill_rate(ctx, E2BShape.real())
+            log(f"prefill (real layout): {prefill['real_e2b_layout']}")
 
     batch = {}
     for B in [int(b) for b in args.batch_sweep.split(",") if b.strip()]:
