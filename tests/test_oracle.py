@@ -645,3 +645,43 @@ def test_embedding_lookup_pinned():
     # the row index, not the column, selects the token
     t = np.arange(4 * 16, dtype=np.float16).reshape(4, 16)
     assert O.embedding_lookup(t, 16, 2)[0] == 32 * 4
+
+
+def test_kv_cache_store_layout():
+    """shaders/kv_cache_store.wgsl:1-18: row `position` of [max_seq][nkh][hd],
+    K and V each rounded once to f16 (the f16 cache of this build; the
+    rounding is NumPy's IEEE half cast), every other row untouched."""
+    rng = np.random.default_rng(11)
+    nkh, hd, cap, pos = 2, 8, 5, 3
+    k = rng.standard_normal(nkh * hd).astype(np.float32)
+    v = rng.standard_normal(nkh * hd).astype(np.float32) * 1e3
+    kc = rng.integers(0, 1 << 16, cap * nkh * hd).astype(np.uint16)
+    vc = kc.copy()
+    k0, v0 = kc.copy(), vc.copy()
+    O.kv_cache_store_f16(k, v, kc, vc, nkh, hd, pos)
+    row = slice(pos * nkh * hd, (pos + 1) * nkh * hd)
+    assert np.array_equal(kc[row], k.astype(np.float16).view(np.uint16))
+    assert np.array_equal(vc[row], v.astype(np.float16).view(np.uint16))
+    other = np.ones(kc.size, bool)
+    other[row] = False
+    assert np.array_equal(kc[other], k0[other]) and np.array_equal(vc[other], v0[other])
+
+
+def test_node_q4k_dot_matches_oracle(tmp_path):
+    """oracle/q4k_dot.js (the CPU baseline's Node dequant-dot) against the C
+    oracle's Q4_K matvec on the same seeded blocks."""
+    import shutil
+    import subprocess
+    node = shutil.which("node")
+    if node is None:
+        pytest.skip("no node binary")
+    M, K = 64, 512
+    W = O.gen_q4k(21, M * K // 256)
+    x = O.gen_normal_f32(22, K)
+    fin, fout = tmp_path / "in.bin", tmp_path / "out.bin"
+    fin.write_bytes(np.array([M, K], np.uint32).tobytes() + W.tobytes() + x.tobytes())
+    js = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle", "q4k_dot.js")
+    subprocess.run([node, js, str(fin), str(fout), "0.01"], check=True, capture_output=True, timeout=60)
+    y = np.fromfile(fout, np.float32)
+    want = O.matmul(x, W, M, K, "q4k")
+    assert O.rel_l2(y, want) < 1e-6
