@@ -1542,6 +1542,51 @@ __global__ __launch_bounds__(NT) void unpack_check_kernel(const uint8_t* W, uint
   }
 }
 
+// Blocks to f16 rows (round to nearest even): each thread's quarter block
+// through the register unit of path 0 into LDS, then the workgroup's rows
+// leave as 16-byte stores. (The tied embedding table: the LM head reads the
+// blocks, the embedding lookup f16 rows, src/engine.ts:570-579.)
+template <int QT>
+__global__ __launch_bounds__(NT) void unpack_f16_kernel(const uint8_t* W, uint32_t nblocks, uint16_t* out) {
+  constexpr int BY = BlockOf<QT>::BYTES;
+  __shared__ __align__(16) float vals[UC_BLOCKS * 256];
+  const uint32_t b0 = blockIdx.x * (uint32_t)UC_BLOCKS;
+  const uint32_t b = b0 + threadIdx.x / 4;
+  const int g = threadIdx.x & 3;
+  if (b < nblocks) {
+    float* o = vals + (threadIdx.x / 4) * 256;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, (int)(nblocks * (uint32_t)BY), 0x00020000);
+    const uint32_t off = b * (uint32_t)BY;
+    if constexpr (QT == 0) {
+      Q4Unit w;
+      q4_unit_load<0>(w, rs, off, g);
+      uint4 hd;
+      uint32_t qa[8];
+      q4_unit_words(w, hd, qa);
+      q4_unit_values(hd, qa, g, o);
+    } else {
+      Q6Unit w;
+      q6_unit_load<0>(w, rs, off, W + off, g);
+      uint32_t A[4], B[4], H[4];
+      int32_t scs[4];
+      float dd;
+      q6_unit_unpack(w, A, B, H, scs, dd);
+      q6_unit_values(A, B, H, scs, dd, g, o);
+    }
+  }
+  __syncthreads();
+  const uint32_t nb = min((uint32_t)UC_BLOCKS, nblocks - b0);
+  for (uint32_t i = threadIdx.x; i < nb * 32; i += NT) {
+    const float* v = vals + 8 * i;
+    uint32_t h[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      h[j] = (uint32_t)g4d::f32_to_f16_bits(v[2 * j]) | ((uint32_t)g4d::f32_to_f16_bits(v[2 * j + 1]) << 16);
+    *(uint4*)(out + (size_t)b0 * 256 + 8 * (size_t)i) = make_uint4(h[0], h[1], h[2], h[3]);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Fallbacks: any N % 256 == 0 (one wave per row, float math) and f16 rows.
 // ---------------------------------------------------------------------------
@@ -2036,6 +2081,27 @@ int g4_dequantPath(g4_ctx* ctx, int wtype, int path, const void* blocks, uint64_
     else if (path == 0) hipLaunchKernelGGL((unpack_check_kernel<1, 0>), grid, dim3(NT), 0, ctx->stream, w, nb, o);
     else hipLaunchKernelGGL((unpack_check_kernel<1, 1>), grid, dim3(NT), 0, ctx->stream, w, nb, o);
     G4_LAUNCHED(ctx, "unpack_check");
+  }
+  return G4_OK;
+}
+
+int g4_dequantF16(g4_ctx* ctx, int wtype, const void* blocks, uint64_t nblocks, uint16_t* out) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(blocks && out, "g4_dequantF16: null buffer");
+  G4_REQUIRE(wtype == 0 || wtype == 1, "g4_dequantF16: wtype must be 0 (Q4_K) or 1 (Q6_K)");
+  G4_REQUIRE(((uintptr_t)blocks & 15) == 0 && ((uintptr_t)out & 15) == 0,
+             "g4_dequantF16: blocks and out must be 16-byte aligned");
+  const size_t by = wtype == 0 ? 144 : 210;
+  constexpr uint64_t kChunk = 1u << 24;
+  for (uint64_t b0 = 0; b0 < nblocks; b0 += kChunk) {
+    const uint32_t nb = (uint32_t)std::min<uint64_t>(kChunk, nblocks - b0);
+    const uint8_t* w = (const uint8_t*)blocks + b0 * by;
+    const dim3 grid(ceil_div(nb, UC_BLOCKS));
+    if (wtype == 0)
+      hipLaunchKernelGGL((unpack_f16_kernel<0>), grid, dim3(NT), 0, ctx->stream, w, nb, out + b0 * 256);
+    else
+      hipLaunchKernelGGL((unpack_f16_kernel<1>), grid, dim3(NT), 0, ctx->stream, w, nb, out + b0 * 256);
+    G4_LAUNCHED(ctx, "unpack_f16");
   }
   return G4_OK;
 }

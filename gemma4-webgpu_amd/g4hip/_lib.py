@@ -207,7 +207,25 @@ SIGNATURES = {
     "g4_dequant_q4k": (_I, [_P, _P, _U64, _P]),
     "g4_dequant_q6k": (_I, [_P, _P, _U64, _P]),
     "g4_dequantPath": (_I, [_P, _I, _I, _P, _U64, _P]),
+    "g4_dequantF16": (_I, [_P, _I, _P, _U64, _P]),
     "g4_streamRead": (_I, [_P, _P, _U64, _I, _U32, _P]),
+    "g4_gguf_open": (_I, [ctypes.c_char_p, _PP]),
+    "g4_gguf_open_memory": (_I, [_P, _SZ, _PP]),
+    "g4_gguf_close": (_I, [_P]),
+    "g4_gguf_info": (_I, [_P, ctypes.POINTER(_U32), ctypes.POINTER(_U64), ctypes.POINTER(_U64),
+                          ctypes.POINTER(_U64), ctypes.POINTER(_U32)]),
+    "g4_gguf_find_key": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
+    "g4_gguf_kv": (_I, [_P, _U64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_U32), ctypes.POINTER(_U32),
+                        ctypes.POINTER(_U64)]),
+    "g4_gguf_kv_number": (_I, [_P, _U64, _U64, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64),
+                               ctypes.POINTER(_U64)]),
+    "g4_gguf_kv_string": (_I, [_P, _U64, _U64, _PP, ctypes.POINTER(_U64)]),
+    "g4_gguf_find_tensor": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
+    "g4_gguf_tensor": (_I, [_P, _U64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_U32), ctypes.POINTER(_U64),
+                            ctypes.POINTER(_U32), ctypes.POINTER(_U64), ctypes.POINTER(_U64)]),
+    "g4_gguf_tensor_data": (_I, [_P, _U64, _PP]),
+    "g4_gguf_upload": (_I, [_P, _P, _U64, _P, _SZ]),
+    "g4_gguf_upload_f16": (_I, [_P, _P, _U64, _P, _SZ]),
     "g4_splitmix64": (_U64, [_U64, _U64]),
     "g4_fill_q4k": (_I, [_P, _P, _U64, _U64]),
     "g4_fill_q6k": (_I, [_P, _P, _U64, _U64]),

@@ -53,6 +53,10 @@ from .device import Buffer, Context, splitmix64
 
 Q4K_BYTES = 144
 Q6K_BYTES = 210
+BLOCK_BYTES = {"q4k": Q4K_BYTES, "q6k": Q6K_BYTES}
+# the layer matrices and their default formats (Q4_K, the down projection Q6_K)
+MATRICES = ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown")
+DEFAULT_TYPES = {"wq": "q4k", "wk": "q4k", "wv": "q4k", "wo": "q4k", "wgate": "q4k", "wup": "q4k", "wdown": "q6k"}
 
 
 @dataclass
@@ -159,16 +163,53 @@ class LayerWeights:
     k_norm: Optional[Buffer]
     k_cache: Buffer        # the producer's cache in a layer that reads one
     v_cache: Buffer
+    qt: dict = field(default_factory=lambda: dict(DEFAULT_TYPES))  # matrix -> "q4k" / "q6k"
+
+
+def q4km_types(s: "E2BShape"):
+    """A per-matrix format mix of the kind a Q4_K_M file holds: Q4_K
+    everywhere except the v projection and the down projection of the first
+    and last eighth of their layers and every third layer between, which are
+    Q6_K (the k-quant recipe's "more bits" layers)."""
+    prod = [il for il in range(s.n_layers) if s.is_producer(il)]
+
+    def more_bits(i: int, n: int) -> bool:
+        return i < n // 8 or i >= 7 * n // 8 or (i - n // 8) % 3 == 2
+
+    def qt(il: int, name: str) -> str:
+        if name == "wv" and il in prod and more_bits(prod.index(il), len(prod)):
+            return "q6k"
+        if name == "wdown" and more_bits(il, s.n_layers):
+            return "q6k"
+        return "q4k"
+    return qt
+
+
+def qkv_groups(L: "LayerWeights", outs, rows):
+    """The q/k/v matrices of a layer grouped by format, in order: [(type,
+    weights, outputs, rows)] (one launch per group)."""
+    names = ("wq", "wk", "wv")[:len(outs)]
+    groups = {}
+    for nm, o, r in zip(names, outs, rows):
+        groups.setdefault(L.qt[nm], ([], [], []))
+        g = groups[L.qt[nm]]
+        g[0].append(getattr(L, nm))
+        g[1].append(o)
+        g[2].append(r)
+    return [(t, *g) for t, g in groups.items()]
 
 
 class _SyntheticModel:
-    """Seeded synthetic E2B-shaped weights, generated on the device. Each
-    producer layer's k_cache / v_cache is whatever `kv(il)` returns (dense
-    caches or paged pools); a layer that reads a producer's cache holds that
-    producer's buffers and has no k/v projections or k_norm."""
+    """The model's weights on the device: seeded synthetic E2B-shaped weights
+    generated there, or a GGUF file's tensors (`gguf`). Each producer layer's
+    k_cache / v_cache is whatever `kv(il)` returns (dense caches or paged
+    pools); a layer that reads a producer's cache holds that producer's
+    buffers and has no k/v projections or k_norm. `wtypes(il, name)` picks
+    each synthetic matrix's format ("q4k" / "q6k"; default Q4_K with a Q6_K
+    down projection); a file's matrices keep the file's formats."""
 
     def _build_weights(self, ctx: Context, shape: Optional[E2BShape], n_layers: Optional[int], seed: int,
-                       lm_head: bool, kv, embed: bool = False) -> None:
+                       lm_head: bool, kv, embed: bool = False, wtypes=None, gguf=None) -> None:
         self.ctx = ctx
         self.s = shape or E2BShape()
         if n_layers is not None:
@@ -178,22 +219,19 @@ class _SyntheticModel:
         self._tid = 0
         self.layers: List[LayerWeights] = []
         for il in range(s.n_layers):
-            Q, KV, I, hd = s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il), s.hd(il)
             prod = s.is_producer(il)
             if prod:
                 kc, vc = kv(il)
             else:
                 src = self.layers[s.producer(il)]
                 kc, vc = src.k_cache, src.v_cache
-            self.layers.append(LayerWeights(
-                wq=self._q4k(Q, s.hidden), wk=self._q4k(KV, s.hidden) if prod else None,
-                wv=self._q4k(KV, s.hidden) if prod else None,
-                wo=self._q4k(s.hidden, Q), wgate=self._q4k(I, s.hidden), wup=self._q4k(I, s.hidden),
-                wdown=self._q6k(s.hidden, I),
-                attn_norm=self._f16(s.hidden), post_attn_norm=self._f16(s.hidden), pre_ffn_norm=self._f16(s.hidden),
-                post_ffn_norm=self._f16(s.hidden), q_norm=self._f16(hd), k_norm=self._f16(hd) if prod else None,
-                k_cache=kc, v_cache=vc))
+            w = self._file_layer(gguf, il) if gguf is not None else self._synthetic_layer(il, wtypes)
+            self.layers.append(LayerWeights(k_cache=kc, v_cache=vc, **w))
+        if gguf is not None:
+            self._file_globals(gguf, lm_head, embed)
+            return
         self.final_norm = self._f16(s.hidden)
+        self.lm_type = "q6k"
         self.lm_head = self._q6k(s.vocab, s.hidden) if lm_head else None
         # the f16 token embedding table [vocab x hidden] (shaders/embedding_lookup.wgsl)
         self.embedding = None
@@ -205,6 +243,87 @@ class _SyntheticModel:
         half = s.hd(s.global_layers[0]) // 2 if s.global_layers else s.head_dim // 2
         table = np.where(np.arange(half) < half // 4, 1.0, np.inf).astype(np.float16)
         self.rope_freqs = ctx.from_numpy(table.view(np.uint16))
+
+    def _synthetic_layer(self, il: int, wtypes) -> dict:
+        s = self.s
+        Q, KV, I, hd = s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il), s.hd(il)
+        prod = s.is_producer(il)
+        qt = {nm: (wtypes(il, nm) if wtypes else DEFAULT_TYPES[nm]) for nm in MATRICES}
+        mk = lambda nm, M, N: self._q4k(M, N) if qt[nm] == "q4k" else self._q6k(M, N)  # noqa: E731
+        return dict(
+            wq=mk("wq", Q, s.hidden), wk=mk("wk", KV, s.hidden) if prod else None,
+            wv=mk("wv", KV, s.hidden) if prod else None,
+            wo=mk("wo", s.hidden, Q), wgate=mk("wgate", I, s.hidden), wup=mk("wup", I, s.hidden),
+            wdown=mk("wdown", s.hidden, I),
+            attn_norm=self._f16(s.hidden), post_attn_norm=self._f16(s.hidden), pre_ffn_norm=self._f16(s.hidden),
+            post_ffn_norm=self._f16(s.hidden), q_norm=self._f16(hd), k_norm=self._f16(hd) if prod else None, qt=qt)
+
+    # ---- weights from a GGUF file ---------------------------------------------
+    # tensor names of a layer (src/engine.ts:59-70; blk.{i}.{name}.weight)
+    _FILE_MATRICES = {"wq": "attn_q", "wk": "attn_k", "wv": "attn_v", "wo": "attn_output", "wgate": "ffn_gate",
+                      "wup": "ffn_up", "wdown": "ffn_down"}
+    _FILE_NORMS = {"attn_norm": "attn_norm", "post_attn_norm": "post_attention_norm", "pre_ffn_norm": "ffn_norm",
+                   "post_ffn_norm": "post_ffw_norm", "q_norm": "attn_q_norm", "k_norm": "attn_k_norm"}
+
+    def _file_matrix(self, g, name: str, M: int, N: int):
+        from .gguf import MATVEC_TYPES, TYPE_NAMES
+        t = g.tensor(name)
+        if t.dims != (N, M):
+            raise ValueError(f"{name}: dims {t.dims}, the layout needs ({N}, {M})")
+        qt = MATVEC_TYPES.get(t.type)
+        if qt is None:
+            raise ValueError(f"{name}: {TYPE_NAMES.get(t.type, t.type)} matrices are not supported "
+                             "(the matvecs read Q4_K and Q6_K blocks)")
+        return g.upload(self.ctx, name), qt
+
+    def _file_vector(self, g, name: str, n: int):
+        t = g.tensor(name)
+        if t.n_elements != n:
+            raise ValueError(f"{name}: {t.n_elements} elements, the layout needs {n}")
+        return g.upload_f16(self.ctx, name)
+
+    def _file_layer(self, g, il: int) -> dict:
+        s = self.s
+        Q, KV, I, hd = s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il), s.hd(il)
+        prod = s.is_producer(il)
+        shapes = {"wq": (Q, s.hidden), "wk": (KV, s.hidden), "wv": (KV, s.hidden), "wo": (s.hidden, Q),
+                  "wgate": (I, s.hidden), "wup": (I, s.hidden), "wdown": (s.hidden, I)}
+        w, qt = {}, {}
+        for nm in MATRICES:
+            if nm in ("wk", "wv") and not prod:
+                w[nm], qt[nm] = None, DEFAULT_TYPES[nm]
+                continue
+            w[nm], qt[nm] = self._file_matrix(g, f"blk.{il}.{self._FILE_MATRICES[nm]}.weight", *shapes[nm])
+        if qt["wgate"] != "q4k" or qt["wup"] != "q4k":
+            raise ValueError(f"blk.{il}: gate/up must be Q4_K (the fused gate/up launch reads Q4_K)")
+        for nm, fn in self._FILE_NORMS.items():
+            if nm == "k_norm" and not prod:
+                w[nm] = None
+                continue
+            w[nm] = self._file_vector(g, f"blk.{il}.{fn}.weight", hd if nm in ("q_norm", "k_norm") else s.hidden)
+        w["qt"] = qt
+        return w
+
+    def _file_globals(self, g, lm_head: bool, embed: bool) -> None:
+        s, ctx = self.s, self.ctx
+        self.final_norm = self._file_vector(g, "output_norm.weight", s.hidden)
+        self.lm_head, self.lm_type, self.embedding = None, "q6k", None
+        if lm_head or embed:
+            name = "output.weight" if lm_head and "output.weight" in g else "token_embd.weight"
+            head, self.lm_type = self._file_matrix(g, name, s.vocab, s.hidden)
+            if lm_head:
+                self.lm_head = head
+            if embed:
+                # the tied table: the lookup reads f16 rows (src/engine.ts:599-600)
+                te, et = (head, self.lm_type) if name == "token_embd.weight" else \
+                    self._file_matrix(g, "token_embd.weight", s.vocab, s.hidden)
+                self.embedding = ctx.empty(s.vocab * s.hidden, np.uint16)
+                ctx.dequantF16(et, te, s.vocab * s.hidden // 256, self.embedding)
+                if not lm_head or te is not head:
+                    ctx.sync()
+                    te.free()
+        half = s.hd(s.global_layers[0]) // 2 if s.global_layers else s.head_dim // 2
+        self.rope_freqs = self._file_vector(g, "rope_freqs.weight", half)
 
     # ---- synthetic weights -------------------------------------------------
     def _seed(self) -> int:
@@ -242,11 +361,13 @@ class _SyntheticModel:
 
 class Decoder(_SyntheticModel):
     def __init__(self, ctx: Context, shape: Optional[E2BShape] = None, max_seq: int = 4096, seed: int = 0,
-                 n_layers: Optional[int] = None, lm_head: bool = True, embed: bool = False):
+                 n_layers: Optional[int] = None, lm_head: bool = True, embed: bool = False, wtypes=None,
+                 gguf=None):
         self.max_seq = max_seq
         self._build_weights(ctx, shape, n_layers, seed, lm_head,
                             lambda il: (ctx.zeros(max_seq * self.s.kv_dim_of(il), np.uint16),
-                                        ctx.zeros(max_seq * self.s.kv_dim_of(il), np.uint16)), embed=embed)
+                                        ctx.zeros(max_seq * self.s.kv_dim_of(il), np.uint16)), embed=embed,
+                            wtypes=wtypes, gguf=gguf)
         s = self.s
         f32 = np.float32
         Q, I = s.q_dim, s.max_ffn
@@ -285,7 +406,7 @@ class Decoder(_SyntheticModel):
         self.rope_cs = self._rope_tables(max_seq)
         self.warm = [[ctx.matmulWarmRegion("q4k", s.ffn_of(il), s.hidden, L.wgate),
                       ctx.matmulWarmRegion("q4k", s.ffn_of(il), s.hidden, L.wup),
-                      ctx.matmulWarmRegion("q6k", s.hidden, s.ffn_of(il), L.wdown)]
+                      ctx.matmulWarmRegion(L.qt["wdown"], s.hidden, s.ffn_of(il), L.wdown)]
                      for il, L in enumerate(self.layers)]
         ctx.fill_normal_f32(self.hidden, s.hidden, self._seed(), 0.0, 1.0)
         ctx.sync()
@@ -319,10 +440,10 @@ class Decoder(_SyntheticModel):
             hd, Q, KV, I = s.hd(il), s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il)
             prod = s.is_producer(il)
             c.rmsNorm(self.hidden, L.attn_norm, self.normed, s.hidden, s.eps)
-            c.matmulQuant(self.normed, L.wq, self.q, Q, s.hidden)
+            c.matmulQuant(self.normed, L.wq, self.q, Q, s.hidden, L.qt["wq"])
             if prod:
-                c.matmulQuant(self.normed, L.wk, self.k, KV, s.hidden)
-                c.matmulQuant(self.normed, L.wv, self.v, KV, s.hidden)
+                c.matmulQuant(self.normed, L.wk, self.k, KV, s.hidden, L.qt["wk"])
+                c.matmulQuant(self.normed, L.wv, self.v, KV, s.hidden, L.qt["wv"])
                 c.perHeadRmsNormNoWeight(self.v, s.n_kv_heads, hd, s.eps)
             c.fusedPerHeadNormRope(self.q, L.q_norm, s.n_q_heads, hd, s.eps, position, theta, int(glob),
                                    self.rope_freqs)
@@ -333,13 +454,13 @@ class Decoder(_SyntheticModel):
             c.attnScore(self.q, L.k_cache, self.scores, s.n_q_heads, s.n_kv_heads, hd, seq_len, 1.0, window)
             c.softmax(self.scores, s.n_q_heads, seq_len)
             c.attnOutput(self.scores, L.v_cache, self.attn, s.n_q_heads, s.n_kv_heads, hd, seq_len)
-            c.matmulQuant(self.attn, L.wo, self.o, s.hidden, Q)
+            c.matmulQuant(self.attn, L.wo, self.o, s.hidden, Q, L.qt["wo"])
             c.fusedNormAdd(self.o, L.post_attn_norm, self.hidden, self.hidden2, s.hidden, s.eps)
             c.rmsNorm(self.hidden2, L.pre_ffn_norm, self.normed, s.hidden, s.eps)
             c.matmulQuantMR4(self.normed, L.wgate, self.gate, I, s.hidden)
             c.matmulQuantMR4(self.normed, L.wup, self.up, I, s.hidden)
             c.geluMul(self.gate, self.up, self.act, I)
-            c.matmulQuant(self.act, L.wdown, self.down, s.hidden, I, "q6k")
+            c.matmulQuant(self.act, L.wdown, self.down, s.hidden, I, L.qt["wdown"])
             c.fusedNormAdd(self.down, L.post_ffn_norm, self.hidden2, self.hidden, s.hidden, s.eps)
         self._head(sample)
 
@@ -348,7 +469,7 @@ class Decoder(_SyntheticModel):
         if self.lm_head is None:
             return
         c.rmsNorm(self.hidden, self.final_norm, self.normed, s.hidden, s.eps)
-        c.matmulQuant(self.normed, self.lm_head, self.logits, s.vocab, s.hidden, "q6k")
+        c.matmulQuant(self.normed, self.lm_head, self.logits, s.vocab, s.hidden, self.lm_type)
         c.logitSoftcap(self.logits, s.vocab, s.softcap)
         if sample == "argmax":
             c.argmax(self.logits, self.token, s.vocab)
@@ -385,33 +506,36 @@ class Decoder(_SyntheticModel):
         for il, L in enumerate(self.layers):
             Q, KV, I = s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il)
             prod = s.is_producer(il)
-            if prod:
-                outs, ws, rows = [self.q, self.k, self.v], [L.wq, L.wk, L.wv], [Q, KV, KV]
-            else:
-                outs, ws, rows = [self.q], [L.wq], [Q]
-            if il == 0:
-                c.normAddMatmulSegments("q4k", self.hidden, L.attn_norm, None, None, None, ws, outs, rows,
-                                        s.hidden, s.eps)
-            else:
-                prev = self.layers[il - 1]
-                c.normAddMatmulSegments("q4k", self.down, prev.post_ffn_norm, self.hidden2, L.attn_norm,
-                                        self.hidden, ws, outs, rows, s.hidden, s.eps)
+            outs, rows = ([self.q, self.k, self.v], [Q, KV, KV]) if prod else ([self.q], [Q])
+            # one launch per weight format among q/k/v; a second launch
+            # recomputes the norm from the same inputs and writes no h_out
+            for gi, (qt, ws, go, gr) in enumerate(qkv_groups(L, outs, rows)):
+                if il == 0:
+                    c.normAddMatmulSegments(qt, self.hidden, L.attn_norm, None, None, None, ws, go, gr,
+                                            s.hidden, s.eps)
+                else:
+                    prev = self.layers[il - 1]
+                    c.normAddMatmulSegments(qt, self.down, prev.post_ffn_norm, self.hidden2, L.attn_norm,
+                                            None if gi else self.hidden, ws, go, gr, s.hidden, s.eps)
             c.attnDecodeFusedWarm(self.q, self.k if prod else None, self.v if prod else None, L.q_norm, L.k_norm,
                                   self.rope_freqs, L.k_cache, L.v_cache, self.attn, self.attn_params[il],
                                   self.attn_ws, self.pos, self.warm[il] if warm else [],
                                   self.rope_cs[s.is_global(il)], self.rope_rows)
-            c.matmulQuant(self.attn, L.wo, self.o, s.hidden, Q)
+            c.matmulQuant(self.attn, L.wo, self.o, s.hidden, Q, L.qt["wo"])
             c.normAddGateUpGeluDigits_q4k(self.o, L.post_attn_norm, self.hidden, L.pre_ffn_norm, L.wgate, L.wup,
                                           self.hidden2, self.act, self.act_digits, I, s.hidden, s.eps)
-            c.matmulQuantDigits_q6k(self.act_digits, L.wdown, self.down, s.hidden, I)
+            if L.qt["wdown"] == "q6k":
+                c.matmulQuantDigits_q6k(self.act_digits, L.wdown, self.down, s.hidden, I)
+            else:
+                c.matmulQuant(self.act, L.wdown, self.down, s.hidden, I, L.qt["wdown"])
         last = self.layers[-1]
         if self.lm_head is not None:
             if sample == "argmax":
-                c.normAddMatmulArgmax("q6k", self.down, last.post_ffn_norm, self.hidden2, self.final_norm,
+                c.normAddMatmulArgmax(self.lm_type, self.down, last.post_ffn_norm, self.hidden2, self.final_norm,
                                       self.hidden, self.lm_head, self.logits, s.vocab, s.hidden, self.token, s.eps,
                                       softcap=s.softcap, positions=self.pos if advance else None, delta=1)
                 return
-            c.normAddMatmulTopk("q6k", self.down, last.post_ffn_norm, self.hidden2, self.final_norm, self.hidden,
+            c.normAddMatmulTopk(self.lm_type, self.down, last.post_ffn_norm, self.hidden2, self.final_norm, self.hidden,
                                  self.lm_head, self.logits, s.vocab, s.hidden, self.topk, s.eps, softcap=s.softcap)
         else:
             c.fusedNormAdd(self.down, last.post_ffn_norm, self.hidden2, self.hidden, s.hidden, s.eps)
@@ -433,8 +557,9 @@ class Decoder(_SyntheticModel):
         candidates (1) and their reduction, which also advances the position
         (1), and the embedding lookup when there is a table."""
         s, n = self.s, 2 + (self.embedding is not None)
-        for il in range(s.n_layers):
+        for il, L in enumerate(self.layers):
             n += 5 + (not self.ctx.attn_fused_single_launch(self.attn_params[il]))
+            n += len(qkv_groups(L, [0, 0, 0][:3 if s.is_producer(il) else 1], [0, 0, 0])) - 1
         return n
 
 
@@ -458,7 +583,7 @@ class BatchDecoder(_SyntheticModel):
 
     def __init__(self, ctx: Context, context_lens, shape: Optional[E2BShape] = None, page_size: int = 16,
                  reserve: int = 64, seed: int = 0, n_layers: Optional[int] = None, lm_head: bool = True,
-                 page_seed: int = 7, shared_pages: bool = False, embed: bool = False):
+                 page_seed: int = 7, shared_pages: bool = False, embed: bool = False, wtypes=None, gguf=None):
         """shared_pages: every row reads and appends through one page list
         (the rows are tokens of one sequence: batched prefill). embed: an f16
         token table; each step starts from the embedding of every row's
@@ -488,7 +613,8 @@ class BatchDecoder(_SyntheticModel):
         rows = self.num_pages * page_size
         self._build_weights(ctx, shape, n_layers, seed, lm_head,
                             lambda il: (ctx.zeros(rows * self.s.kv_dim_of(il), np.uint16),
-                                        ctx.zeros(rows * self.s.kv_dim_of(il), np.uint16)), embed=embed)
+                                        ctx.zeros(rows * self.s.kv_dim_of(il), np.uint16)), embed=embed,
+                            wtypes=wtypes, gguf=gguf)
         s, B, f32 = self.s, self.B, np.float32
         self.page_table = ctx.from_numpy(table)
         self.seq_lens = ctx.from_numpy(self.lens_host)
@@ -588,13 +714,16 @@ class BatchDecoder(_SyntheticModel):
                 prev = self.layers[il - 1]
                 c.batchPrep(self.down_parts, nd, prev.post_ffn_norm, self.hidden2, L.attn_norm, self.hidden,
                             self.xn, H, B, s.eps, ops=self.xops)
-            if prod:  # a layer reading a producer's pool projects q only and appends no row
-                nq = c.matmulSegmentsBatchPartial("q4k", self.xn, [L.wq, L.wk, L.wv],
-                                                  [self.q_parts, self.k_parts, self.v_parts],
-                                                  [Q, KV, KV], H, B, self.ks_h, ops=self.xops)
-            else:
-                nq = c.matmulSegmentsBatchPartial("q4k", self.xn, [L.wq], [self.q_parts], [Q], H, B, self.ks_h,
-                                                  ops=self.xops)
+            # a layer reading a producer's pool projects q only and appends no row
+            outs = [self.q_parts, self.k_parts, self.v_parts] if prod else [self.q_parts]
+            nq = 0
+            for qt, ws, go, gr in qkv_groups(L, outs, [Q, KV, KV] if prod else [Q]):
+                # a later format's launch takes the first one's K split (the
+                # prologue adds one chunk count): its fewer rows never pick fewer
+                k = c.matmulSegmentsBatchPartial(qt, self.xn, ws, go, gr, H, B, nq or self.ks_h, ops=self.xops)
+                if nq and k != nq:
+                    raise RuntimeError(f"layer {il}: q/k/v launches split K {nq} and {k} ways")
+                nq = k
             c.pagedAttnPrologue(self.q_parts, self.k_parts if prod else None, self.v_parts if prod else None, nq,
                                 L.q_norm, L.k_norm, self.rope_freqs, self.q, L.k_cache if prod else None,
                                 L.v_cache if prod else None, self.page_table, self.seq_lens, self.pro_params[il],
@@ -602,18 +731,18 @@ class BatchDecoder(_SyntheticModel):
             ops = self.aops if s.hd(il) % 256 == 0 else None
             c.pagedAttnDecode(self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.attn,
                               self.attn_params[il], self.attn_ws, ops=ops)
-            no = c.matmulSegmentsBatchPartial("q4k", self.attn, [L.wo], [self.o_parts], [H], Q, B, self.ks_q,
+            no = c.matmulSegmentsBatchPartial(L.qt["wo"], self.attn, [L.wo], [self.o_parts], [H], Q, B, self.ks_q,
                                               ops=ops)
             c.batchPrep(self.o_parts, no, L.post_attn_norm, self.hidden, L.pre_ffn_norm, self.hidden2, self.xn, H, B,
                         s.eps, ops=self.xops)
             c.gateUpGeluBatch(self.xn, L.wgate, L.wup, self.act, I, H, B, ops=self.xops)
-            nd = c.matmulSegmentsBatchPartial("q6k", self.act, [L.wdown], [self.down_parts], [H], I, B,
+            nd = c.matmulSegmentsBatchPartial(L.qt["wdown"], self.act, [L.wdown], [self.down_parts], [H], I, B,
                                               self.ks_f)
         last = self.layers[-1]
         c.batchPrep(self.down_parts, nd, last.post_ffn_norm, self.hidden2, self.final_norm, self.hidden, self.xn, H,
                     B, s.eps, ops=self.xops)
         if self.lm_head is not None:
-            c.matmulSegmentsBatchPartial("q6k", self.xn, [self.lm_head], [self.logits], [s.vocab], H, B, 1,
+            c.matmulSegmentsBatchPartial(self.lm_type, self.xn, [self.lm_head], [self.logits], [s.vocab], H, B, 1,
                                          ops=self.xops, softcap=s.softcap)
             if sample == "argmax":
                 c.argmaxBatch(self.logits, self.tokens, s.vocab, B)
@@ -669,3 +798,30 @@ class BatchDecoder(_SyntheticModel):
             g = self.ctx.graph_end()
         self.lens_host = lens  # capture enqueues nothing
         return g
+
+
+def open_gguf(path_or_file, max_context_length: Optional[int] = None, n_layers: Optional[int] = None):
+    """(GGUFFile, configFromGGUF result, decoder layout) of a Gemma 4 GGUF;
+    the layout's vocabulary is the token table's row count."""
+    from .gguf import GGUFFile, config_from_gguf, shape_from_config
+    g = path_or_file if isinstance(path_or_file, GGUFFile) else GGUFFile(str(path_or_file))
+    cfg = config_from_gguf(g, max_context_length)
+    emb = g.find("token_embd.weight")
+    shape = shape_from_config(cfg, vocab=emb.dims[1] if emb is not None and len(emb.dims) == 2 else None)
+    if n_layers is not None:
+        shape.n_layers = n_layers
+    return g, cfg, shape
+
+
+def decoder_from_gguf(ctx: Context, path_or_file, max_seq: Optional[int] = None, batch=None, **kw):
+    """A Decoder (batch None) or BatchDecoder (batch = the context lengths)
+    holding a GGUF file's weights: the layer matrices as the file's Q4_K /
+    Q6_K blocks, norms and the RoPE table as f16, the tied token table as
+    the LM head's blocks and (embed=True, the default) the lookup's f16
+    rows. max_seq defaults to the file's context length capped at 2048 (as
+    configFromGGUF)."""
+    g, cfg, shape = open_gguf(path_or_file, max_seq, kw.pop("n_layers", None))
+    kw.setdefault("embed", True)
+    if batch is None:
+        return Decoder(ctx, shape, max_seq=max_seq or cfg["context_length"], gguf=g, **kw)
+    return BatchDecoder(ctx, batch, shape, gguf=g, **kw)

@@ -539,6 +539,10 @@ class Context:
         units, 1: LDS units, 2: matrix-core operands)."""
         check(lib().g4_dequantPath(self.h, {"q4k": 0, "q6k": 1}[wtype], path, _p(blocks), nblocks, _p(out)))
 
+    def dequantF16(self, wtype: str, blocks: Ptr, nblocks: int, out: Ptr) -> None:
+        """Blocks to f16 values (round to nearest even of the f32 dequant)."""
+        check(lib().g4_dequantF16(self.h, {"q4k": 0, "q6k": 1}[wtype], _p(blocks), nblocks, _p(out)))
+
     def streamRead(self, src: Ptr, nbytes: int, policy: int, nwgs: int, sink: Ptr) -> None:
         """Measurement probe: one pass of 16-byte loads over nbytes (policy 0
         plain, 1 non-temporal, 2 device scope)."""

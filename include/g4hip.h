@@ -565,6 +565,12 @@ int g4_dequant_q6k(g4_ctx* ctx, const void* blocks, uint64_t nblocks, float* out
  * Paths 0 and 1 are bit-exact with the reference's f32 values. */
 int g4_dequantPath(g4_ctx* ctx, int wtype, int path, const void* blocks, uint64_t nblocks, float* out);
 
+/* Q4_K (wtype 0) or Q6_K (1) blocks to f16 values, rounded to nearest even
+ * from the f32 values of g4_dequantPath's path 0 (tensorToF16,
+ * src/engine.ts:570-579, for the tied token embedding table the lookup
+ * reads). blocks and out 16-byte aligned; out holds nblocks * 256 values. */
+int g4_dequantF16(g4_ctx* ctx, int wtype, const void* blocks, uint64_t nblocks, uint16_t* out);
+
 /* Measurement probe: reads bytes of src once with 16-byte loads (nwgs
  * workgroups of 256 threads, 4 loads in flight per thread) under a cache
  * policy (0 plain, 1 non-temporal as the one-matrix Q4_K matvec reads its
@@ -572,6 +578,53 @@ int g4_dequantPath(g4_ctx* ctx, int wtype, int path, const void* blocks, uint64_
  * one word per workgroup to sink[nwgs]. It times the pure-streaming floor of
  * a launch and calibrates the HBM byte counters. */
 int g4_streamRead(g4_ctx* ctx, const void* src, uint64_t bytes, int policy, uint32_t nwgs, uint32_t* sink);
+
+/* GGUF v2/v3 model files (replaces GGUFParser, src/gguf.ts:75-101 header,
+ * :103-134 key/values, :136-160 tensor infos and data offset, :385-395 tensor
+ * sizes). The file is memory-mapped (g4_gguf_open) or read from caller memory
+ * that outlives the handle (g4_gguf_open_memory); only the header is parsed,
+ * every read bounds-checked: a malformed or truncated file is G4_ERR_INVALID
+ * with the reason in g4_last_error. The data section starts at the header's
+ * end rounded up to general.alignment (32 when absent, as src/gguf.ts:97).
+ * Value types are GGUF's (0 u8 ... 12 f64; 8 string, 9 array). Tensor types
+ * with known sizes: 0 F32, 1 F16, 8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K, 30 BF16;
+ * other types parse (nbytes 0) but have no data access. Strings returned are
+ * not NUL-terminated (use len); key and tensor names are. Returned pointers
+ * live until g4_gguf_close. The handle is read-only and may be shared by
+ * threads. */
+typedef struct g4_gguf g4_gguf;
+int g4_gguf_open(const char* path, g4_gguf** out);
+int g4_gguf_open_memory(const void* data, size_t bytes, g4_gguf** out);
+int g4_gguf_close(g4_gguf* g);
+int g4_gguf_info(const g4_gguf* g, uint32_t* version, uint64_t* tensor_count, uint64_t* kv_count,
+                 uint64_t* data_offset, uint32_t* alignment);
+/* *index = -1 when absent. */
+int g4_gguf_find_key(const g4_gguf* g, const char* key, int64_t* index);
+/* type = the value type; for arrays arr_type = the element type and count
+ * the element count (1 and 0 for scalars). */
+int g4_gguf_kv(const g4_gguf* g, uint64_t index, const char** key, uint32_t* type, uint32_t* arr_type,
+               uint64_t* count);
+/* A numeric scalar (element 0) or array element, as f64, i64 and u64. */
+int g4_gguf_kv_number(const g4_gguf* g, uint64_t index, uint64_t element, double* f, int64_t* i,
+                      uint64_t* u);
+/* A string (element 0) or string-array element. */
+int g4_gguf_kv_string(const g4_gguf* g, uint64_t index, uint64_t element, const char** s, uint64_t* len);
+int g4_gguf_find_tensor(const g4_gguf* g, const char* name, int64_t* index);
+/* dims[4] (GGUF order, dims[0] the contiguous one; unused dims 1); offset is
+ * relative to the data section. */
+int g4_gguf_tensor(const g4_gguf* g, uint64_t index, const char** name, uint32_t* n_dims, uint64_t* dims,
+                   uint32_t* type, uint64_t* offset, uint64_t* nbytes);
+/* Host address of the tensor's bytes inside the mapping. */
+int g4_gguf_tensor_data(const g4_gguf* g, uint64_t index, const void** data);
+/* Copies the tensor's GGUF bytes unchanged to device memory (the quantized
+ * blocks are what the matvecs read; the reference instead dequantizes every
+ * tensor to f16 at upload, src/engine.ts:570-593). Synchronous; not during
+ * graph capture. */
+int g4_gguf_upload(g4_ctx* ctx, const g4_gguf* g, uint64_t index, void* dst, size_t dst_bytes);
+/* An F32, F16 or BF16 tensor to f16 on the device, rounded to nearest even
+ * (src/engine.ts:570-579 for the norm weights, rope_freqs and other f32
+ * tensors). */
+int g4_gguf_upload_f16(g4_ctx* ctx, const g4_gguf* g, uint64_t index, uint16_t* dst, size_t dst_elems);
 
 /* Seeded synthetic inputs, generated on the device (counter-based SplitMix64;
  * block b of a stream draws words 32b.., element i of a normal stream words

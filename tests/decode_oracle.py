@@ -45,7 +45,9 @@ class HostModel:
                                 for k in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown", "attn_norm",
                                           "post_attn_norm", "pre_ffn_norm", "post_ffn_norm", "q_norm", "k_norm")
                                 if getattr(L, k) is not None})
+        self.qt = [dict(L.qt) for L in dec.layers]  # each matrix's format
         self.final_norm = dec.final_norm.download(u16)
+        self.lm_type = getattr(dec, "lm_type", "q6k")
         self.lm_head = dec.lm_head.download(u8) if dec.lm_head is not None else None
         self.embedding = getattr(dec, "embedding", None)  # device table: rows are fetched on demand
 
@@ -70,12 +72,13 @@ class HostModel:
             window = 0 if glob else s.window
             hd, Q, KV, I = s.hd(il), s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il)
             src = s.producer(il)
+            qt = self.qt[il]
             n = O.rms_norm(x, W["attn_norm"], s.eps)
-            q = O.matmul(n, W["wq"], Q, s.hidden, "q4k")
+            q = O.matmul(n, W["wq"], Q, s.hidden, qt["wq"])
             q = O.fused_per_head_norm_rope(q, W["q_norm"], s.n_q_heads, hd, s.eps, pos, theta, int(glob), self.table)
             if src == il:
-                k = O.matmul(n, W["wk"], KV, s.hidden, "q4k")
-                v = O.matmul(n, W["wv"], KV, s.hidden, "q4k")
+                k = O.matmul(n, W["wk"], KV, s.hidden, qt["wk"])
+                v = O.matmul(n, W["wv"], KV, s.hidden, qt["wv"])
                 v = O.per_head_rms_norm_no_weight(v, s.n_kv_heads, hd, s.eps)
                 k = O.fused_per_head_norm_rope(k, W["k_norm"], s.n_kv_heads, hd, s.eps, pos, theta, int(glob),
                                                self.table)
@@ -85,14 +88,14 @@ class HostModel:
                     kcs[il][row] = f16_toward_zero(k)
                     vcs[il][row] = f16_toward_zero(v)
             a = O.attention(q, kcs[src], vcs[src], s.n_q_heads, s.n_kv_heads, hd, pos + 1, 1.0, window)
-            o = O.matmul(a, W["wo"], s.hidden, Q, "q4k")
+            o = O.matmul(a, W["wo"], s.hidden, Q, qt["wo"])
             h = O.fused_norm_add(o, W["post_attn_norm"], x, s.eps)
             n2 = O.rms_norm(h, W["pre_ffn_norm"], s.eps)
-            g = O.matmul(n2, W["wgate"], I, s.hidden, "q4k")
-            u = O.matmul(n2, W["wup"], I, s.hidden, "q4k")
-            dn = O.matmul(gelu(g, u), W["wdown"], s.hidden, I, "q6k")
+            g = O.matmul(n2, W["wgate"], I, s.hidden, qt["wgate"])
+            u = O.matmul(n2, W["wup"], I, s.hidden, qt["wup"])
+            dn = O.matmul(gelu(g, u), W["wdown"], s.hidden, I, qt["wdown"])
             x = O.fused_norm_add(dn, W["post_ffn_norm"], h, s.eps)
         if self.lm_head is None:
             return x, None
         n = O.rms_norm(x, self.final_norm, s.eps)
-        return x, O.logit_softcap(O.matmul(n, self.lm_head, s.vocab, s.hidden, "q6k"), s.softcap)
+        return x, O.logit_softcap(O.matmul(n, self.lm_head, s.vocab, s.hidden, self.lm_type), s.softcap)
