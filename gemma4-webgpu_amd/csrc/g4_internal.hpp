@@ -120,6 +120,13 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+// tanh-GELU with the tanh argument clamped to +-15 (shaders/gelu_mul.wgsl:10-16).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  float t = 0.7978845608028654f * x * (1.0f + 0.044715f * x * x);
+  t = fminf(fmaxf(t, -15.0f), 15.0f);
+  return 0.5f * x * (1.0f + tanhf(t));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);

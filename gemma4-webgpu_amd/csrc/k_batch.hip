@@ -76,6 +76,7 @@ struct BPrepArgs {
   float eps;
   uint8_t* ops;  // optional: operand blocks [K/256][Ops::bytes(ntv)]
   int ntv;
+  const uint16_t* scale;  // mode 2: h = (residual + norm(x)) * f16 scale (NULL: 1)
 };
 
 __device__ __forceinline__ float4 mulw(float4 x, uint2 w, float s) {
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(PNT) void bprep_kernel(BPrepArgs a) {
     if constexpr (PRO >= 1) w1[p] = *(const uint2*)(a.w1 + fc);
     if constexpr (PRO == 2) {
       r[p] = *(const float4*)(a.residual + (size_t)v * K + fc);
-      w2[p] = *(const uint2*)(a.w2 + fc);
+      w2[p] = a.w2 ? *(const uint2*)(a.w2 + fc) : make_uint2(0, 0);
     }
   }
   for (uint32_t c0 = 1; c0 < a.nparts; c0 += PMAX) {  // chunks 1.. in order
@@ -142,10 +143,12 @@ __global__ __launch_bounds__(PNT) void bprep_kernel(BPrepArgs a) {
       for (int p = 0; p < XP; ++p) x[p] = mulw(x[p], w1[p], inv1);
     } else {
       float ss2 = 0.f;
+      const float sc = a.scale ? g4d::f16_bits_to_f32(*a.scale) : 1.0f;
 #pragma unroll
       for (int p = 0; p < XP; ++p) {
         const int f = 4 * tid + 4 * PNT * p;
-        x[p] = add4(r[p], mulw(x[p], w1[p], inv1));
+        const float4 h = add4(r[p], mulw(x[p], w1[p], inv1));
+        x[p] = make_float4(h.x * sc, h.y * sc, h.z * sc, h.w * sc);
         ss2 += f < K ? sq4(x[p]) : 0.f;
         if (a.h_out && f < K) *(float4*)(a.h_out + (size_t)v * K + f) = x[p];
       }
@@ -156,8 +159,9 @@ __global__ __launch_bounds__(PNT) void bprep_kernel(BPrepArgs a) {
 #pragma unroll
       for (int i = 0; i < PNT / 64; ++i) t2 += red[PNT / 64 + i];
       const float inv2 = __builtin_amdgcn_rsqf(t2 * (1.0f / (float)K) + a.eps);
+      if (a.w2)  // (no w2: out = h)
 #pragma unroll
-      for (int p = 0; p < XP; ++p) x[p] = mulw(x[p], w2[p], inv2);
+        for (int p = 0; p < XP; ++p) x[p] = mulw(x[p], w2[p], inv2);
     }
   }
 #pragma unroll
@@ -505,11 +509,7 @@ struct OpSrc<NTV, true> {
   }
 };
 
-__device__ __forceinline__ float gelu_tanh(float x) {  // shaders/gelu_mul.wgsl:10-16
-  float t = 0.7978845608028654f * x * (1.0f + 0.044715f * x * x);
-  t = fminf(fmaxf(t, -15.0f), 15.0f);
-  return 0.5f * x * (1.0f + tanhf(t));
-}
+using g4d::gelu_tanh;  // shaders/gelu_mul.wgsl:10-16
 
 __device__ __forceinline__ float epilogue(float y, float cap) {
   if (cap > 0.f) {
@@ -958,17 +958,29 @@ int g4_batchOperandBytes(uint32_t N, uint32_t batch, size_t* bytes) {
 int g4_batchPrep(g4_ctx* ctx, const float* x, uint32_t nparts, const uint16_t* w1, const float* residual,
                  const uint16_t* w2, float* h_out, float* out, void* ops, uint32_t N, uint32_t batch, float eps) {
   G4_ENTER(ctx);
+  G4_REQUIRE(!residual == !w2, "g4_batchPrep: residual and w2 go together");
+  return g4_batchPrepScale(ctx, x, nparts, w1, residual, nullptr, w2, h_out, out, ops, N, batch, eps);
+}
+
+int g4_batchPrepScale(g4_ctx* ctx, const float* x, uint32_t nparts, const uint16_t* w1, const float* residual,
+                      const uint16_t* out_scale, const uint16_t* w2, float* h_out, float* out, void* ops, uint32_t N,
+                      uint32_t batch, float eps) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(!out_scale || residual, "g4_batchPrepScale: out_scale needs the residual form");
+  G4_REQUIRE(!w2 || residual, "g4_batchPrepScale: w2 needs the residual form");
   G4_REQUIRE(x && out && nparts >= 1, "g4_batchPrep: null buffer or no parts");
   G4_REQUIRE(batch >= 1 && batch <= (ops ? 64u : 65535u), "g4_batchPrep: batch %u out of range", batch);
   G4_REQUIRE(N == 1536 || N == 2048, "g4_batchPrep: N=%u must be 1536 or 2048", N);
   G4_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)ops & 15) == 0,
              "g4_batchPrep: buffers must be 16-byte aligned");
   G4_REQUIRE(w1 || !residual, "g4_batchPrep: residual needs w1");
-  int rc = check_norms(__func__, w1, residual, w2, h_out);
-  if (rc) return rc;
+  G4_REQUIRE((!residual || ((uintptr_t)residual & 15) == 0) && (!h_out || ((uintptr_t)h_out & 15) == 0),
+             "g4_batchPrep: activations must be 16-byte aligned");
+  G4_REQUIRE((!w1 || ((uintptr_t)w1 & 7) == 0) && (!w2 || ((uintptr_t)w2 & 7) == 0),
+             "g4_batchPrep: norm weights must be 8-byte aligned");
   const int pro = !w1 ? 0 : (residual ? 2 : 1);
   const BPrepArgs p{x, nparts, batch, w1, residual, w2, h_out, out, eps, (uint8_t*)ops,
-                    (int)(pad_batch(batch) / 16)};
+                    (int)(pad_batch(batch) / 16), out_scale};
   return bprep_launch(ctx, N, pro, p);
 }
 

@@ -89,10 +89,7 @@ __global__ __launch_bounds__(NT) void head_norm_kernel(float* data, const uint16
 __global__ __launch_bounds__(NT) void gelu_mul_kernel(const float* gate, const float* up, float* out, uint32_t n) {
   const uint32_t i = blockIdx.x * NT + threadIdx.x;
   if (i >= n) return;
-  const float x = gate[i];
-  float t = 0.7978845608028654f * x * (1.0f + 0.044715f * x * x);
-  t = fminf(fmaxf(t, -15.0f), 15.0f);
-  out[i] = 0.5f * x * (1.0f + tanhf(t)) * up[i];
+  out[i] = g4d::gelu_tanh(gate[i]) * up[i];
 }
 
 __global__ void advance_kernel(uint32_t* p, uint32_t delta) {
@@ -297,6 +294,31 @@ __global__ __launch_bounds__(NT) void fill_q4k_kernel(uint8_t* dst, uint64_t nbl
   uint4* o = (uint4*)(dst + b * 144);
 #pragma unroll
   for (int k = 0; k < 9; ++k) o[k] = make_uint4(words[4 * k], words[4 * k + 1], words[4 * k + 2], words[4 * k + 3]);
+}
+
+// Q5_K blocks (176 B): d ~ |N(0, 2e-3)|, dmin ~ |N(0, 1e-3)| as f16, then
+// 12 scale/min bytes, 32 high-bit bytes and 128 nibble bytes uniform.
+__global__ __launch_bounds__(NT) void fill_q5k_kernel(uint8_t* dst, uint64_t nblocks, uint64_t seed) {
+  const uint64_t b = (uint64_t)blockIdx.x * NT + threadIdx.x;
+  if (b >= nblocks) return;
+  uint64_t w[26];
+#pragma unroll
+  for (int i = 0; i < 26; ++i) w[i] = g4d::splitmix64(seed, 32 * b + (uint64_t)i);
+  uint32_t words[44];
+  const uint16_t d = g4d::f32_to_f16_bits((float)(fabs(normal_from(w[0], w[1])) * 2e-3));
+  const uint16_t dm = g4d::f32_to_f16_bits((float)(fabs(normal_from(w[2], w[3])) * 1e-3));
+  words[0] = (uint32_t)d | ((uint32_t)dm << 16);
+  words[1] = (uint32_t)w[4];
+  words[2] = (uint32_t)(w[4] >> 32);
+  words[3] = (uint32_t)w[5];
+#pragma unroll
+  for (int k = 0; k < 20; ++k) {
+    words[4 + 2 * k] = (uint32_t)w[6 + k];
+    words[5 + 2 * k] = (uint32_t)(w[6 + k] >> 32);
+  }
+  uint4* o = (uint4*)(dst + b * 176);
+#pragma unroll
+  for (int k = 0; k < 11; ++k) o[k] = make_uint4(words[4 * k], words[4 * k + 1], words[4 * k + 2], words[4 * k + 3]);
 }
 
 __global__ __launch_bounds__(NT) void fill_q6k_kernel(uint8_t* dst, uint64_t nblocks, uint64_t seed) {
@@ -626,6 +648,17 @@ int g4_fill_q4k(g4_ctx* ctx, void* dst, uint64_t nblocks, uint64_t seed) {
   hipLaunchKernelGGL(fill_q4k_kernel, dim3(ceil_div(nblocks, NT)), dim3(NT), 0, ctx->stream, (uint8_t*)dst, nblocks,
                      seed);
   G4_LAUNCHED(ctx, "fill_q4k");
+  return G4_OK;
+}
+
+int g4_fill_q5k(g4_ctx* ctx, void* dst, uint64_t nblocks, uint64_t seed) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(dst, "g4_fill_q5k: null buffer");
+  G4_REQUIRE(((uintptr_t)dst & 15) == 0, "g4_fill_q5k: destination must be 16-byte aligned");
+  if (!nblocks) return G4_OK;
+  hipLaunchKernelGGL(fill_q5k_kernel, dim3(ceil_div(nblocks, NT)), dim3(NT), 0, ctx->stream, (uint8_t*)dst, nblocks,
+                     seed);
+  G4_LAUNCHED(ctx, "fill_q5k");
   return G4_OK;
 }
 

@@ -138,6 +138,7 @@ struct ProArgs {
   const uint16_t* w2;
   float* h_out;
   float eps;
+  const uint16_t* out_scale;  // mode 2: h = (residual + norm(x)) * f16 scale (NULL: 1)
 };
 
 // Thread t owns the float4s at flat element p*1024 + 4t (p < XP) of the
@@ -197,10 +198,12 @@ __device__ __forceinline__ void pro_finish(XRegs<NV, K>& R, const XView& xv, con
       for (int p = 0; p < XP; ++p) R.x[p] = mul_w(R.x[p], R.w1[p], inv1);
     } else {
       float ss2 = 0.f;
+      const float sc = a.out_scale ? g4d::f16_bits_to_f32(*a.out_scale) : 1.0f;
 #pragma unroll
       for (int p = 0; p < XP; ++p) {
         const float4 t = mul_w(R.x[p], R.w1[p], inv1);
-        const float4 h = make_float4(R.r[p].x + t.x, R.r[p].y + t.y, R.r[p].z + t.z, R.r[p].w + t.w);
+        const float4 h = make_float4((R.r[p].x + t.x) * sc, (R.r[p].y + t.y) * sc, (R.r[p].z + t.z) * sc,
+                                     (R.r[p].w + t.w) * sc);
         R.x[p] = h;
         ss2 += sumsq(h);
         const uint32_t f = (uint32_t)p * 1024 + 4 * threadIdx.x;
@@ -594,11 +597,7 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvSegs segs, ProArgs pa, uin
 
 // gate/up pair with the tanh-GELU product epilogue (shaders/gelu_mul.wgsl:10-16):
 // out[i] = gelu(gate[i]) * up[i]; both matrices are [M, BPR*256] Q4_K.
-__device__ __forceinline__ float gelu_tanh(float x) {
-  float t = 0.7978845608028654f * x * (1.0f + 0.044715f * x * x);
-  t = fminf(fmaxf(t, -15.0f), 15.0f);
-  return 0.5f * x * (1.0f + tanhf(t));
-}
+using g4d::gelu_tanh;
 
 // ---------------------------------------------------------------------------
 // M=1 matvec with register-resident activation digits
@@ -929,13 +928,15 @@ __device__ __forceinline__ void mv_pro_finish(MvPro<BPR, NWV, PRO>& P, uint8_t* 
         acc.w += r.w;
       }
       const float inv1 = mv_inv_rms<X::K>(acc.x, a.eps);
-      const float ss2 = fmaxf(acc.y + 2.0f * inv1 * acc.z + inv1 * inv1 * acc.w, 0.f);
+      // with an output scale s, h = s (r + t inv1) and sum(h^2) = s^2 times the above
+      const float sc = a.out_scale ? g4d::f16_bits_to_f32(*a.out_scale) : 1.0f;
+      const float ss2 = fmaxf(acc.y + 2.0f * inv1 * acc.z + inv1 * inv1 * acc.w, 0.f) * (sc * sc);
       const float inv2 = mv_inv_rms<X::K>(ss2, a.eps);
 #pragma unroll
       for (int p = 0; p < PP::XP; ++p) {
         const float4 t = ow[p];
-        const float4 h = make_float4(P.r[p].x + t.x * inv1, P.r[p].y + t.y * inv1, P.r[p].z + t.z * inv1,
-                                     P.r[p].w + t.w * inv1);
+        const float4 h = make_float4((P.r[p].x + t.x * inv1) * sc, (P.r[p].y + t.y * inv1) * sc,
+                                     (P.r[p].z + t.z * inv1) * sc, (P.r[p].w + t.w * inv1) * sc);
         if (a.h_out && blockIdx.x == 0 && PP::live(p)) *(float4*)(a.h_out + PP::elem(p)) = h;
         P.x[p] = mul_w(h, P.w2[p], inv2);
       }
@@ -2205,7 +2206,16 @@ int g4_matmulQuantDigits_q6k(g4_ctx* ctx, const void* digits, const void* weight
 int g4_normAddMatmulSegments(g4_ctx* ctx, int wtype, const float* x, const uint16_t* w1, const float* residual,
                              const uint16_t* w2, float* h_out, const void* const* weights, float* const* outputs,
                              const uint32_t* rows, int nseg, uint32_t N, float eps, float softcap_cap) {
+  return g4_normAddScaleMatmulSegments(ctx, wtype, x, w1, residual, nullptr, w2, h_out, weights, outputs, rows, nseg,
+                                       N, eps, softcap_cap);
+}
+
+int g4_normAddScaleMatmulSegments(g4_ctx* ctx, int wtype, const float* x, const uint16_t* w1, const float* residual,
+                                  const uint16_t* out_scale, const uint16_t* w2, float* h_out,
+                                  const void* const* weights, float* const* outputs, const uint32_t* rows, int nseg,
+                                  uint32_t N, float eps, float softcap_cap) {
   G4_ENTER(ctx);
+  G4_REQUIRE(!out_scale || residual, "g4_normAddScaleMatmulSegments: out_scale needs the residual form");
   G4_REQUIRE(wtype == 0 || wtype == 1, "g4_normAddMatmulSegments: wtype must be 0 (Q4_K) or 1 (Q6_K)");
   G4_REQUIRE(nseg >= 1 && nseg <= 4, "g4_normAddMatmulSegments: 1..4 segments");
   G4_REQUIRE(x && w1 && weights && outputs && rows, "g4_normAddMatmulSegments: null buffer");
@@ -2225,7 +2235,7 @@ int g4_normAddMatmulSegments(g4_ctx* ctx, int wtype, const float* x, const uint1
   }
   const int pro = residual ? 2 : 1;
   LaunchReq q{wtype, segs, nseg, N, 1, pro, softcap_cap != 0.f ? 1 : 0, softcap_cap,
-              ProArgs{x, w1, residual, w2, h_out, eps}, 0};
+              ProArgs{x, w1, residual, w2, h_out, eps, out_scale}, 0};
   return launch_gemv(ctx, q);
 }
 

@@ -1,0 +1,334 @@
+// k_ple.hip — Gemma 4 per-layer embeddings (PLE) on gfx950.
+//
+// The reference runs PLE as one f16 matmul and one single-workgroup
+// dispatch per layer before the layers (src/engine.ts:1516-1535) and five
+// passes inside every layer (src/engine.ts:1608-1616). Here:
+//  * stage 1 is one launch for every layer and every row of a batch: the
+//    per-layer table stays in its Q5_K blocks (176 B per 256 values, one
+//    block per (token, layer)); each workgroup unpacks its block, rounds the
+//    values to f16 as the reference's f16 upload does (src/engine.ts:626-700),
+//    and fuses the projection's RMSNorm and the 1/sqrt(2) blend;
+//  * the f16 matvecs (per_layer_model_proj, inp_gate, proj) keep the
+//    weights in registers, one wave per row, while the vectors (up to 8 at a
+//    time) are read from LDS as f32, so B vectors cost one weight read;
+//  * the inp_gate launch takes the post-FFN norm-add as its prologue (one
+//    vector) and gelu(gate) * ple_inputs as its epilogue; the tail's rmsNorm
+//    + skip-scale-add is the next launch's prologue (the scaled norm-add of
+//    g4_normAddScaleMatmulSegments / g4_batchPrepScale).
+#include "g4_internal.hpp"
+
+namespace {
+
+constexpr int PT = 256;       // threads per workgroup
+constexpr int PW = PT / 64;   // waves per workgroup
+constexpr uint32_t kQ5Bytes = 176;
+
+// vectors staged in LDS per pass (at most 48 KB of f32)
+template <int N>
+constexpr int vectors_per_pass() { return N <= 1536 ? 8 : 4; }
+
+// Q5_K value t (0..255) of one block (src/gguf.ts:218-257): group g = t/64
+// uses sub-block j = 2g + (t/32 odd); q = 4 bits of qs[32g + l] (low nibble
+// for the first 32, high for the second) + 16 * bit j of qh[l], l = t % 32;
+// value = d*sc(j)*q - dmin*m(j) with the Q4_K scale/min packing. d*sc*q has
+// at most 22 significant bits, so the fma rounds the exact value once, as
+// the reference's f64 evaluation stored to f32 does.
+__device__ __forceinline__ float q5k_value(const uint8_t* blk, int t) {
+  const int g = t >> 6, hi = (t >> 5) & 1, l = t & 31, j = 2 * g + hi;
+  const uint32_t dd = *(const uint32_t*)blk;
+  const uint8_t* s = blk + 4;
+  int sc, m;
+  if (j < 4) {
+    sc = s[j] & 63;
+    m = s[j + 4] & 63;
+  } else {
+    sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+    m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+  }
+  const int qs = blk[48 + 32 * g + l];
+  const int q = (hi ? (qs >> 4) : (qs & 15)) + (((blk[16 + l] >> j) & 1) << 4);
+  const float d = g4d::f16_bits_to_f32(dd & 0xffffu) * (float)sc;
+  const float mn = g4d::f16_bits_to_f32(dd >> 16) * (float)m;
+  return __builtin_fmaf(d, (float)q, -mn);
+}
+
+__device__ __forceinline__ float f16_round(float v) { return g4d::f16_bits_to_f32(g4d::f32_to_f16_bits(v)); }
+
+struct Stage1Args {
+  const float* projected;  // [count][L * 256]
+  const uint16_t* norm_w;  // [256]
+  const uint8_t* table;    // Q5_K blocks [rows][L]
+  const uint32_t* tokens;  // [count] (NULL: token)
+  uint32_t token, rows, L;
+  float* out;              // [count][L * 256]
+  float eps;
+};
+
+// shaders/ple_stage1_fuse.wgsl:14-37 for layer blockIdx.x of row blockIdx.y.
+// A token past the table reads as a zero row (the embedding lookup's rule).
+__global__ __launch_bounds__(PT) void ple_stage1_kernel(Stage1Args a) {
+  __shared__ float red[PW];
+  const uint32_t il = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const uint32_t tok = a.tokens ? a.tokens[b] : a.token;
+  const size_t base = ((size_t)b * a.L + il) * 256;
+  const float v = a.projected[base + t];
+  const float ss = g4d::block_sum<PW>(v * v, red);
+  const float rms = sqrtf(ss * (1.0f / 256.0f) + a.eps);
+  const float normed = (v / rms) * g4d::f16_bits_to_f32(a.norm_w[t]);
+  const float e = tok < a.rows ? f16_round(q5k_value(a.table + ((size_t)tok * a.L + il) * kQ5Bytes, (int)t)) : 0.f;
+  a.out[base + t] = (normed + e * 16.0f) * 0.70710678118654752f;  // sqrt(256) = 16
+}
+
+// Q5_K blocks to f16 (the reference's table values, src/engine.ts:626-700).
+__global__ __launch_bounds__(PT) void q5k_f16_kernel(const uint8_t* W, uint64_t nblocks, uint16_t* out) {
+  const uint64_t b = blockIdx.x;
+  if (b >= nblocks) return;
+  out[b * 256 + threadIdx.x] = g4d::f32_to_f16_bits(q5k_value(W + b * kQ5Bytes, (int)threadIdx.x));
+}
+
+// shaders/ple_gelu_mul.wgsl:11-20
+__global__ __launch_bounds__(PT) void ple_gelu_mul_kernel(const float* gate, const float* ple, float* out,
+                                                          uint32_t n) {
+  const uint32_t i = blockIdx.x * PT + threadIdx.x;
+  if (i < n) out[i] = g4d::gelu_tanh(gate[i]) * ple[i];
+}
+
+// shaders/ple_skip_scale_add.wgsl:14-20
+__global__ __launch_bounds__(PT) void ple_skip_scale_add_kernel(float* hidden, const float* post, const uint16_t* scale,
+                                                                uint32_t n) {
+  const uint32_t i = blockIdx.x * PT + threadIdx.x;
+  if (i < n) hidden[i] = (hidden[i] + post[i]) * g4d::f16_bits_to_f32(scale[0]);
+}
+
+// ---------------------------------------------------------------------------
+// f16 rows x f32 vectors
+// ---------------------------------------------------------------------------
+
+struct HmvArgs {
+  const uint16_t* W;  // [M][N] f16
+  uint32_t M;
+  const float* x;     // [B][N] (PRO 1: the post-FFN down vector)
+  uint32_t B;
+  float* y;           // [B][M]
+  // PRO 1 (B == 1): h = residual + x * w1 / rms(x) is the vector (h_out by workgroup 0)
+  const uint16_t* w1;
+  const float* residual;
+  float* h_out;
+  float eps;
+  // EPI 1: y = gelu(y) * ple[b * ple_stride + m]
+  const float* ple;
+  uint32_t ple_stride;
+};
+
+// One wave per row (rows blockIdx.x * PW + wave, then + gridDim.x * PW):
+// lane l holds row elements 8l + 512i (N = 1536: 3 x 16 B) or 4l (N = 256:
+// 8 B) in registers and multiplies them with each of up to HB vectors
+// staged in LDS; the 64 lane partials meet through DPP.
+template <int N, int PRO, int EPI>
+__global__ __launch_bounds__(PT) void hmv_kernel(HmvArgs a) {
+  static_assert(N == 256 || N % 512 == 0, "row width");
+  constexpr int EPL = N == 256 ? 4 : 8;                // f16 per lane per load
+  constexpr int NL = N == 256 ? 1 : N / 512;           // loads per lane
+  constexpr int HB = vectors_per_pass<N>();
+  __shared__ __align__(16) float xs[HB * N];
+  __shared__ float red[2 * PW];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // one pass holds every vector: staged once, before the rows
+  const bool once = PRO == 1 || a.B <= (uint32_t)HB;
+  if (PRO == 0 && once) {
+    for (uint32_t i = tid; i < a.B * N / 4; i += PT) ((float4*)xs)[i] = ((const float4*)a.x)[i];
+    __syncthreads();
+  }
+  if constexpr (PRO == 1) {
+    // the one vector: h = residual + x * w1 / rms(x)
+    float ss = 0.f;
+    for (int i = tid; i < N; i += PT) ss += a.x[i] * a.x[i];
+    ss = g4d::block_sum<PW>(ss, red);
+    const float inv = __builtin_amdgcn_rsqf(ss * (1.0f / (float)N) + a.eps);
+    for (int i = tid; i < N; i += PT) {
+      const float h = a.residual[i] + a.x[i] * g4d::f16_bits_to_f32(a.w1[i]) * inv;
+      xs[i] = h;
+      if (a.h_out && blockIdx.x == 0) a.h_out[i] = h;
+    }
+    __syncthreads();
+  }
+  for (uint32_t m0 = blockIdx.x * PW; m0 < a.M; m0 += gridDim.x * PW) {
+    const uint32_t m = m0 + wv;
+    const bool live = m < a.M;
+    // the row in registers (a wave past M reads row M - 1, stores nothing)
+    float w[NL][EPL];
+    const uint16_t* row = a.W + (size_t)min(m, a.M - 1) * N;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      if constexpr (EPL == 8) {
+        const uint4 u = *(const uint4*)(row + 512 * i + 8 * lane);
+        const uint32_t uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          w[i][2 * j] = g4d::f16_bits_to_f32(uu[j] & 0xffffu);
+          w[i][2 * j + 1] = g4d::f16_bits_to_f32(uu[j] >> 16);
+        }
+      } else {
+        const uint2 u = *(const uint2*)(row + 4 * lane);
+        w[i][0] = g4d::f16_bits_to_f32(u.x & 0xffffu);
+        w[i][1] = g4d::f16_bits_to_f32(u.x >> 16);
+        w[i][2] = g4d::f16_bits_to_f32(u.y & 0xffffu);
+        w[i][3] = g4d::f16_bits_to_f32(u.y >> 16);
+      }
+    }
+    for (uint32_t b0 = 0; b0 < a.B; b0 += HB) {
+      const uint32_t nb = min((uint32_t)HB, a.B - b0);
+      if (!once) {  // (uniform over the workgroup)
+        __syncthreads();  // the previous pass's reads are done
+        for (uint32_t i = tid; i < nb * N / 4; i += PT)
+          ((float4*)xs)[i] = ((const float4*)(a.x + (size_t)b0 * N))[i];
+        __syncthreads();
+      }
+      for (uint32_t v = 0; v < nb; ++v) {
+        const float* xv = xs + v * N;
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+          const float* xe = xv + (EPL == 8 ? 512 * i + 8 * lane : 4 * lane);
+          const float4 p = *(const float4*)xe;
+          acc += w[i][0] * p.x + w[i][1] * p.y + w[i][2] * p.z + w[i][3] * p.w;
+          if constexpr (EPL == 8) {
+            const float4 q = *(const float4*)(xe + 4);
+            acc += w[i][4] * q.x + w[i][5] * q.y + w[i][6] * q.z + w[i][7] * q.w;
+          }
+        }
+        acc = g4d::wave_sum_dpp(acc);
+        if (live && lane == 0) {
+          const uint32_t b = b0 + v;
+          float r = acc;
+          if constexpr (EPI == 1) r = g4d::gelu_tanh(acc) * a.ple[(size_t)b * a.ple_stride + m];
+          a.y[(size_t)b * a.M + m] = r;
+        }
+      }
+    }
+  }
+}
+
+template <int PRO, int EPI>
+int hmv_launch(g4_ctx* ctx, const HmvArgs& a, uint32_t N) {
+  // about four workgroups per CU, fewer when the rows run out
+  const uint32_t want = (uint32_t)(ctx->num_cus > 0 ? ctx->num_cus : 256) * 4;
+  const dim3 grid(std::min<uint32_t>(want, ceil_div(a.M, (uint32_t)PW)));
+  switch (N) {
+    case 256: hipLaunchKernelGGL((hmv_kernel<256, PRO, EPI>), grid, dim3(PT), 0, ctx->stream, a); break;
+    case 1536: hipLaunchKernelGGL((hmv_kernel<1536, PRO, EPI>), grid, dim3(PT), 0, ctx->stream, a); break;
+    case 2048: hipLaunchKernelGGL((hmv_kernel<2048, PRO, EPI>), grid, dim3(PT), 0, ctx->stream, a); break;
+    default: return g4::set_error(G4_ERR_UNSUPPORTED, "f16 matvec: N=%u (256, 1536 or 2048)", N);
+  }
+  G4_LAUNCHED(ctx, "hmv");
+  return G4_OK;
+}
+
+int check_hmv(const char* fn, const float* x, const uint16_t* w, const float* y, uint32_t M, uint32_t N,
+              uint32_t batch) {
+  G4_REQUIRE(x && w && y, "%s: null buffer", fn);
+  G4_REQUIRE(M > 0 && batch >= 1, "%s: empty shape M=%u batch=%u", fn, M, batch);
+  G4_REQUIRE(N == 256 || N == 1536 || N == 2048, "%s: N=%u (256, 1536 or 2048)", fn, N);
+  G4_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0, "%s: x and weights must be 16-byte aligned", fn);
+  return G4_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int g4_pleStage1Fuse(g4_ctx* ctx, const float* projected, const uint16_t* norm_w, const void* table_q5k,
+                     uint32_t table_rows, uint32_t token, const uint32_t* tokens_dev, float* ple_inputs,
+                     uint32_t num_layers, uint32_t per_layer_dim, float eps, uint32_t count) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(projected && norm_w && table_q5k && ple_inputs, "g4_pleStage1Fuse: null buffer");
+  G4_REQUIRE(per_layer_dim == 256, "g4_pleStage1Fuse: per_layer_dim %u (one Q5_K block per layer: 256)",
+             per_layer_dim);
+  G4_REQUIRE(num_layers >= 1 && num_layers <= 65535 && count >= 1 && count <= 65535,
+             "g4_pleStage1Fuse: %u layers, %u rows", num_layers, count);
+  G4_REQUIRE(tokens_dev || count == 1, "g4_pleStage1Fuse: several rows need tokens_dev");
+  G4_REQUIRE(tokens_dev || token < table_rows, "g4_pleStage1Fuse: token %u >= %u rows", token, table_rows);
+  G4_REQUIRE(((uintptr_t)table_q5k & 15) == 0, "g4_pleStage1Fuse: the table must be 16-byte aligned");
+  const Stage1Args a{projected, norm_w, (const uint8_t*)table_q5k, tokens_dev, token, table_rows, num_layers,
+                     ple_inputs, eps};
+  hipLaunchKernelGGL(ple_stage1_kernel, dim3(num_layers, count), dim3(PT), 0, ctx->stream, a);
+  G4_LAUNCHED(ctx, "ple_stage1");
+  return G4_OK;
+}
+
+int g4_pleGeluMul(g4_ctx* ctx, const float* gate, const float* ple_inputs, float* output, uint32_t layer_offset,
+                  uint32_t size) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(gate && ple_inputs && output, "g4_pleGeluMul: null buffer");
+  if (!size) return G4_OK;
+  hipLaunchKernelGGL(ple_gelu_mul_kernel, dim3(ceil_div(size, (uint32_t)PT)), dim3(PT), 0, ctx->stream, gate,
+                     ple_inputs + layer_offset, output, size);
+  G4_LAUNCHED(ctx, "ple_gelu_mul");
+  return G4_OK;
+}
+
+int g4_pleSkipScaleAdd(g4_ctx* ctx, float* hidden, const float* post_normed, const uint16_t* scale, uint32_t size) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(hidden && post_normed && scale, "g4_pleSkipScaleAdd: null buffer");
+  if (!size) return G4_OK;
+  hipLaunchKernelGGL(ple_skip_scale_add_kernel, dim3(ceil_div(size, (uint32_t)PT)), dim3(PT), 0, ctx->stream,
+                     hidden, post_normed, scale, size);
+  G4_LAUNCHED(ctx, "ple_skip_scale_add");
+  return G4_OK;
+}
+
+int g4_matmulF16(g4_ctx* ctx, const float* x, const uint16_t* weight, float* y, uint32_t M, uint32_t N,
+                 uint32_t batch) {
+  G4_ENTER(ctx);
+  int rc = check_hmv(__func__, x, weight, y, M, N, batch);
+  if (rc) return rc;
+  HmvArgs a{};
+  a.W = weight;
+  a.M = M;
+  a.x = x;
+  a.B = batch;
+  a.y = y;
+  return hmv_launch<0, 0>(ctx, a, N);
+}
+
+int g4_pleGate(g4_ctx* ctx, const float* x, const uint16_t* w1, const float* residual, float* h_out,
+               const uint16_t* w_gate, const float* ple_inputs, uint32_t ple_stride, uint32_t layer_offset,
+               float* out, uint32_t M, uint32_t N, float eps, uint32_t batch) {
+  G4_ENTER(ctx);
+  int rc = check_hmv(__func__, x, w_gate, out, M, N, batch);
+  if (rc) return rc;
+  G4_REQUIRE(ple_inputs, "g4_pleGate: null ple_inputs");
+  G4_REQUIRE(!w1 == !residual, "g4_pleGate: w1 and residual go together");
+  G4_REQUIRE(!w1 || batch == 1, "g4_pleGate: the norm-add prologue takes one vector");
+  G4_REQUIRE(!w1 || N != 256, "g4_pleGate: the norm-add prologue is over the hidden width");
+  HmvArgs a{};
+  a.W = w_gate;
+  a.M = M;
+  a.x = x;
+  a.B = batch;
+  a.y = out;
+  a.w1 = w1;
+  a.residual = residual;
+  a.h_out = h_out;
+  a.eps = eps;
+  a.ple = ple_inputs + layer_offset;
+  a.ple_stride = ple_stride;
+  return w1 ? hmv_launch<1, 1>(ctx, a, N) : hmv_launch<0, 1>(ctx, a, N);
+}
+
+int g4_dequantQ5K_F16(g4_ctx* ctx, const void* blocks, uint64_t nblocks, uint16_t* out) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(blocks && out, "g4_dequantQ5K_F16: null buffer");
+  G4_REQUIRE(((uintptr_t)blocks & 15) == 0, "g4_dequantQ5K_F16: blocks must be 16-byte aligned");
+  G4_REQUIRE(((uintptr_t)out & 1) == 0, "g4_dequantQ5K_F16: out must be 2-byte aligned");
+  constexpr uint64_t kChunk = 1u << 22;  // blocks per launch
+  for (uint64_t b0 = 0; b0 < nblocks; b0 += kChunk) {
+    const uint64_t nb = std::min<uint64_t>(kChunk, nblocks - b0);
+    hipLaunchKernelGGL(q5k_f16_kernel, dim3((uint32_t)nb), dim3(PT), 0, ctx->stream,
+                       (const uint8_t*)blocks + b0 * kQ5Bytes, nb, out + b0 * 256);
+    G4_LAUNCHED(ctx, "q5k_f16");
+  }
+  return G4_OK;
+}
+
+}  // extern "C"

@@ -226,6 +226,16 @@ SIGNATURES = {
     "g4_gguf_tensor_data": (_I, [_P, _U64, _PP]),
     "g4_gguf_upload": (_I, [_P, _P, _U64, _P, _SZ]),
     "g4_gguf_upload_f16": (_I, [_P, _P, _U64, _P, _SZ]),
+    "g4_normAddScaleMatmulSegments": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, ctypes.POINTER(_P), ctypes.POINTER(_P),
+                                           ctypes.POINTER(_U32), _I, _U32, _F, _F]),
+    "g4_batchPrepScale": (_I, [_P, _P, _U32, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, _F]),
+    "g4_pleStage1Fuse": (_I, [_P, _P, _P, _P, _U32, _U32, _P, _P, _U32, _U32, _F, _U32]),
+    "g4_pleGeluMul": (_I, [_P, _P, _P, _P, _U32, _U32]),
+    "g4_pleSkipScaleAdd": (_I, [_P, _P, _P, _P, _U32]),
+    "g4_matmulF16": (_I, [_P, _P, _P, _P, _U32, _U32, _U32]),
+    "g4_pleGate": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _P, _U32, _U32, _F, _U32]),
+    "g4_dequantQ5K_F16": (_I, [_P, _P, _U64, _P]),
+    "g4_fill_q5k": (_I, [_P, _P, _U64, _U64]),
     "g4_splitmix64": (_U64, [_U64, _U64]),
     "g4_fill_q4k": (_I, [_P, _P, _U64, _U64]),
     "g4_fill_q6k": (_I, [_P, _P, _U64, _U64]),

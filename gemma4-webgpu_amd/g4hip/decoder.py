@@ -77,11 +77,12 @@ class E2BShape:
     head_dim_global: int = 0     # head dim of the global layers (0: head_dim)
     ffn_shared: int = 0          # FFN width of layers >= n_unshared (0: ffn)
     n_unshared: int = 0          # layers >= n_unshared read a producer's KV cache (0: every layer owns its cache)
+    ple_dim: int = 0             # per-layer embedding width (0: no per-layer embeddings)
 
     @classmethod
     def real(cls, **kw) -> "E2BShape":
         """Gemma-4-E2B's layer layout (src/config/gemma4-e2b.ts:16-63)."""
-        return cls(**{"head_dim_global": 512, "ffn_shared": 12288, "n_unshared": 15, **kw})
+        return cls(**{"head_dim_global": 512, "ffn_shared": 12288, "n_unshared": 15, "ple_dim": 256, **kw})
 
     @property
     def q_dim(self) -> int:
@@ -145,6 +146,14 @@ class E2BShape:
     def lm_head_bytes(self) -> int:
         return self.vocab * self.hidden // 256 * Q6K_BYTES
 
+    def ple_bytes(self) -> int:
+        """Per-layer-embedding bytes one token reads: per_layer_model_proj
+        (f16), its table row (Q5_K), every layer's inp_gate and proj (f16)."""
+        if not self.ple_dim:
+            return 0
+        L, D, H = self.n_layers, self.ple_dim, self.hidden
+        return L * D * H * 2 + L * 176 + L * 2 * D * H * 2
+
 
 @dataclass
 class LayerWeights:
@@ -164,6 +173,12 @@ class LayerWeights:
     k_cache: Buffer        # the producer's cache in a layer that reads one
     v_cache: Buffer
     qt: dict = field(default_factory=lambda: dict(DEFAULT_TYPES))  # matrix -> "q4k" / "q6k"
+    # per-layer embedding stage (src/engine.ts:1608-1616): inp_gate [D x H],
+    # proj [H x D], post_norm [H] (f16) and layer_output_scale (f16 [1])
+    ple_gate: Optional[Buffer] = None
+    ple_proj: Optional[Buffer] = None
+    ple_post_norm: Optional[Buffer] = None
+    ple_scale: Optional[Buffer] = None
 
 
 def q4km_types(s: "E2BShape"):
@@ -233,6 +248,7 @@ class _SyntheticModel:
         self.final_norm = self._f16(s.hidden)
         self.lm_type = "q6k"
         self.lm_head = self._q6k(s.vocab, s.hidden) if lm_head else None
+        self._synthetic_ple_globals()
         # the f16 token embedding table [vocab x hidden] (shaders/embedding_lookup.wgsl)
         self.embedding = None
         if embed:
@@ -256,7 +272,31 @@ class _SyntheticModel:
             wo=mk("wo", s.hidden, Q), wgate=mk("wgate", I, s.hidden), wup=mk("wup", I, s.hidden),
             wdown=mk("wdown", s.hidden, I),
             attn_norm=self._f16(s.hidden), post_attn_norm=self._f16(s.hidden), pre_ffn_norm=self._f16(s.hidden),
-            post_ffn_norm=self._f16(s.hidden), q_norm=self._f16(hd), k_norm=self._f16(hd) if prod else None, qt=qt)
+            post_ffn_norm=self._f16(s.hidden), q_norm=self._f16(hd), k_norm=self._f16(hd) if prod else None, qt=qt,
+            **self._synthetic_ple_layer())
+
+    def _synthetic_ple_layer(self) -> dict:
+        s = self.s
+        if not s.ple_dim:
+            return {}
+        D, H = s.ple_dim, s.hidden
+        return dict(ple_gate=self._f16(D * H, 0.0, 0.03), ple_proj=self._f16(H * D, 0.0, 0.03),
+                    ple_post_norm=self._f16(H), ple_scale=self._f16(2, 0.8, 0.1))
+
+    def _synthetic_ple_globals(self) -> None:
+        """per_layer_model_proj [L*D x H], per_layer_proj_norm [D] (f16) and
+        the Q5_K per_layer_token_embd table [vocab x L blocks]."""
+        s, ctx = self.s, self.ctx
+        self.ple_model_proj = self.ple_proj_norm = self.ple_table = None
+        if not s.ple_dim:
+            return
+        if s.ple_dim != 256:
+            raise ValueError("per-layer embeddings need ple_dim 256 (one Q5_K block per layer)")
+        L, D, H = s.n_layers, s.ple_dim, s.hidden
+        self.ple_model_proj = self._f16(L * D * H, 0.0, 0.03)
+        self.ple_proj_norm = self._f16(D)
+        self.ple_table = ctx.alloc(s.vocab * L * 176)
+        ctx.fill_q5k(self.ple_table, s.vocab * L, self._seed())
 
     # ---- weights from a GGUF file ---------------------------------------------
     # tensor names of a layer (src/engine.ts:59-70; blk.{i}.{name}.weight)
@@ -302,7 +342,19 @@ class _SyntheticModel:
                 continue
             w[nm] = self._file_vector(g, f"blk.{il}.{fn}.weight", hd if nm in ("q_norm", "k_norm") else s.hidden)
         w["qt"] = qt
+        if s.ple_dim:  # src/engine.ts:63-69 (inp_gate, proj, post_norm, layer_output_scale)
+            D, H = s.ple_dim, s.hidden
+            w["ple_gate"] = self._file_f16_matrix(g, f"blk.{il}.inp_gate.weight", D, H)
+            w["ple_proj"] = self._file_f16_matrix(g, f"blk.{il}.proj.weight", H, D)
+            w["ple_post_norm"] = self._file_vector(g, f"blk.{il}.post_norm.weight", H)
+            w["ple_scale"] = self._file_vector(g, f"blk.{il}.layer_output_scale.weight", 1)
         return w
+
+    def _file_f16_matrix(self, g, name: str, M: int, N: int):
+        t = g.tensor(name)
+        if t.dims != (N, M):
+            raise ValueError(f"{name}: dims {t.dims}, the layout needs ({N}, {M})")
+        return g.upload_f16(self.ctx, name)
 
     def _file_globals(self, g, lm_head: bool, embed: bool) -> None:
         s, ctx = self.s, self.ctx
@@ -324,6 +376,18 @@ class _SyntheticModel:
                     te.free()
         half = s.hd(s.global_layers[0]) // 2 if s.global_layers else s.head_dim // 2
         self.rope_freqs = self._file_vector(g, "rope_freqs.weight", half)
+        self.ple_model_proj = self.ple_proj_norm = self.ple_table = None
+        if s.ple_dim:  # src/engine.ts:71-77, 599-625, 626-700
+            L, D = s.n_layers, s.ple_dim
+            if D != 256:
+                raise ValueError("per-layer embeddings need per_layer_input_dim 256")
+            self.ple_model_proj = self._file_f16_matrix(g, "per_layer_model_proj.weight", L * D, s.hidden)
+            self.ple_proj_norm = self._file_vector(g, "per_layer_proj_norm.weight", D)
+            t = g.tensor("per_layer_token_embd.weight")
+            if t.type != 13 or t.dims != (L * D, s.vocab):
+                raise ValueError(f"per_layer_token_embd.weight: {t.type_name} {t.dims}, the layout needs Q5_K "
+                                 f"({L * D}, {s.vocab})")
+            self.ple_table = g.upload(ctx, "per_layer_token_embd.weight")
 
     # ---- synthetic weights -------------------------------------------------
     def _seed(self) -> int:
@@ -353,9 +417,9 @@ class _SyntheticModel:
             out[glob] = t
         return out
 
-    def _f16(self, n: int) -> Buffer:
+    def _f16(self, n: int, mean: float = 1.0, std: float = 0.1) -> Buffer:
         b = self.ctx.empty(n, np.uint16)
-        self.ctx.fill_normal_f16(b, n, self._seed(), 1.0, 0.1)
+        self.ctx.fill_normal_f16(b, n, self._seed(), mean, std)
         return b
 
 
@@ -389,6 +453,15 @@ class Decoder(_SyntheticModel):
         self.token = ctx.zeros(1, np.uint32)
         self.topk = ctx.empty(512, f32)
         self.pos = ctx.zeros(1, np.uint32)
+        if s.ple_dim:
+            LD = s.n_layers * s.ple_dim
+            self.ple_projected = ctx.empty(LD, f32)   # per_layer_model_proj . embedding
+            self.ple_inputs = ctx.empty(LD, f32)      # stage 1 output, every layer's slice
+            self.ple_gate_out = ctx.empty(s.ple_dim, f32)
+            self.ple_gated = ctx.empty(s.ple_dim, f32)
+            self.ple_out = ctx.empty(s.hidden, f32)   # proj . gated
+            self.ple_normed = ctx.empty(s.hidden, f32)
+            self.hidden3 = ctx.empty(s.hidden, f32)   # the post-FFN residual the PLE tail adds to
         self.attn_params = []
         for il in range(s.n_layers):
             glob = s.is_global(il)
@@ -428,11 +501,22 @@ class Decoder(_SyntheticModel):
         self.token.upload(np.array([token], np.uint32))
 
     # ---- the reference's per-key sequence ----------------------------------
+    def _ple_stage1(self) -> None:
+        """PLE stage 1 (src/engine.ts:1516-1535) from the step's input vector
+        and the device-side token."""
+        c, s = self.ctx, self.s
+        L, D = s.n_layers, s.ple_dim
+        c.matmulF16(self.hidden, self.ple_model_proj, self.ple_projected, L * D, s.hidden)
+        c.pleStage1Fuse(self.ple_projected, self.ple_proj_norm, self.ple_table, s.vocab, self.ple_inputs, L, D,
+                        s.eps, tokens_dev=self.token)
+
     def step_reference(self, position: int, sample: str = "argmax") -> None:
         c, s = self.ctx, self.s
         seq_len = position + 1
         if self.embedding is not None:
             c.embeddingLookup(self.embedding, s.vocab, self.hidden, s.hidden, token_dev=self.token)
+        if s.ple_dim:
+            self._ple_stage1()
         for il, L in enumerate(self.layers):
             glob = s.is_global(il)
             theta = s.theta_global if glob else s.theta_local
@@ -462,6 +546,13 @@ class Decoder(_SyntheticModel):
             c.geluMul(self.gate, self.up, self.act, I)
             c.matmulQuant(self.act, L.wdown, self.down, s.hidden, I, L.qt["wdown"])
             c.fusedNormAdd(self.down, L.post_ffn_norm, self.hidden2, self.hidden, s.hidden, s.eps)
+            if s.ple_dim:  # PLE stage 2 (src/engine.ts:1608-1616)
+                D = s.ple_dim
+                c.matmulF16(self.hidden, L.ple_gate, self.ple_gate_out, D, s.hidden)
+                c.pleGeluMul(self.ple_gate_out, self.ple_inputs, self.ple_gated, il * D, D)
+                c.matmulF16(self.ple_gated, L.ple_proj, self.ple_out, s.hidden, D)
+                c.rmsNorm(self.ple_out, L.ple_post_norm, self.ple_normed, s.hidden, s.eps)
+                c.pleSkipScaleAdd(self.hidden, self.ple_normed, L.ple_scale, s.hidden)
         self._head(sample)
 
     def _head(self, sample: str) -> None:
@@ -503,6 +594,8 @@ class Decoder(_SyntheticModel):
         c, s = self.ctx, self.s
         if self.embedding is not None:
             c.embeddingLookup(self.embedding, s.vocab, self.hidden, s.hidden, token_dev=self.token)
+        if s.ple_dim:
+            self._ple_stage1()
         for il, L in enumerate(self.layers):
             Q, KV, I = s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il)
             prod = s.is_producer(il)
@@ -510,13 +603,18 @@ class Decoder(_SyntheticModel):
             # one launch per weight format among q/k/v; a second launch
             # recomputes the norm from the same inputs and writes no h_out
             for gi, (qt, ws, go, gr) in enumerate(qkv_groups(L, outs, rows)):
+                h_out = None if gi else self.hidden
                 if il == 0:
                     c.normAddMatmulSegments(qt, self.hidden, L.attn_norm, None, None, None, ws, go, gr,
                                             s.hidden, s.eps)
+                elif s.ple_dim:  # the previous layer's PLE tail: (h + norm(proj out)) * scale
+                    prev = self.layers[il - 1]
+                    c.normAddScaleMatmulSegments(qt, self.ple_out, prev.ple_post_norm, self.hidden3, prev.ple_scale,
+                                                 L.attn_norm, h_out, ws, go, gr, s.hidden, s.eps)
                 else:
                     prev = self.layers[il - 1]
                     c.normAddMatmulSegments(qt, self.down, prev.post_ffn_norm, self.hidden2, L.attn_norm,
-                                            None if gi else self.hidden, ws, go, gr, s.hidden, s.eps)
+                                            h_out, ws, go, gr, s.hidden, s.eps)
             c.attnDecodeFusedWarm(self.q, self.k if prod else None, self.v if prod else None, L.q_norm, L.k_norm,
                                   self.rope_freqs, L.k_cache, L.v_cache, self.attn, self.attn_params[il],
                                   self.attn_ws, self.pos, self.warm[il] if warm else [],
@@ -528,7 +626,28 @@ class Decoder(_SyntheticModel):
                 c.matmulQuantDigits_q6k(self.act_digits, L.wdown, self.down, s.hidden, I)
             else:
                 c.matmulQuant(self.act, L.wdown, self.down, s.hidden, I, L.qt["wdown"])
+            if s.ple_dim:
+                # post-FFN norm-add -> inp_gate -> gelu * ple_inputs, then proj
+                D = s.ple_dim
+                c.pleGate(self.down, L.post_ffn_norm, self.hidden2, self.hidden3, L.ple_gate, self.ple_inputs, 0,
+                          il * D, self.ple_gated, D, s.hidden, s.eps)
+                c.matmulF16(self.ple_gated, L.ple_proj, self.ple_out, s.hidden, D)
         last = self.layers[-1]
+        if s.ple_dim:
+            # the last PLE tail on its own (one vector), then the head normalises it
+            c.batchPrepScale(self.ple_out, 1, last.ple_post_norm, self.hidden3, last.ple_scale, None, self.hidden,
+                             self.normed, s.hidden, 1, s.eps)
+            if self.lm_head is not None:
+                if sample == "argmax":
+                    c.normAddMatmulArgmax(self.lm_type, self.hidden, self.final_norm, None, None, None, self.lm_head,
+                                          self.logits, s.vocab, s.hidden, self.token, s.eps, softcap=s.softcap,
+                                          positions=self.pos if advance else None, delta=1)
+                    return
+                c.normAddMatmulTopk(self.lm_type, self.hidden, self.final_norm, None, None, None, self.lm_head,
+                                    self.logits, s.vocab, s.hidden, self.topk, s.eps, softcap=s.softcap)
+            if advance:
+                c.advancePosition(self.pos, 1)
+            return
         if self.lm_head is not None:
             if sample == "argmax":
                 c.normAddMatmulArgmax(self.lm_type, self.down, last.post_ffn_norm, self.hidden2, self.final_norm,
@@ -557,6 +676,8 @@ class Decoder(_SyntheticModel):
         candidates (1) and their reduction, which also advances the position
         (1), and the embedding lookup when there is a table."""
         s, n = self.s, 2 + (self.embedding is not None)
+        if s.ple_dim:  # stage 1 (2), two per layer, the last tail (1)
+            n += 3 + 2 * s.n_layers
         for il, L in enumerate(self.layers):
             n += 5 + (not self.ctx.attn_fused_single_launch(self.attn_params[il]))
             n += len(qkv_groups(L, [0, 0, 0][:3 if s.is_producer(il) else 1], [0, 0, 0])) - 1
@@ -639,6 +760,13 @@ class BatchDecoder(_SyntheticModel):
         self.logits = ctx.empty(B * s.vocab, f32) if lm_head else None
         self.tokens = ctx.zeros(B, np.uint32)
         self.topk = ctx.empty(B * 512, f32)
+        if s.ple_dim:
+            LD = s.n_layers * s.ple_dim
+            self.ple_projected = ctx.empty(B * LD, f32)
+            self.ple_inputs = ctx.empty(B * LD, f32)
+            self.ple_gated = ctx.empty(B * s.ple_dim, f32)
+            self.ple_out = ctx.empty(B * s.hidden, f32)
+            self.hidden3 = ctx.empty(B * s.hidden, f32)
         self.pro_params, self.attn_params = [], []
         for il in range(s.n_layers):
             glob = s.is_global(il)
@@ -703,6 +831,11 @@ class BatchDecoder(_SyntheticModel):
         H = s.hidden
         if self.embedding is not None:
             c.embeddingLookupBatch(self.embedding, s.vocab, self.hidden, H, self.tokens, B)
+        if s.ple_dim:  # PLE stage 1 for every row (src/engine.ts:1516-1535)
+            LD = s.n_layers * s.ple_dim
+            c.matmulF16(self.hidden, self.ple_model_proj, self.ple_projected, LD, H, B)
+            c.pleStage1Fuse(self.ple_projected, self.ple_proj_norm, self.ple_table, s.vocab, self.ple_inputs,
+                            s.n_layers, s.ple_dim, s.eps, tokens_dev=self.tokens, count=B)
         c.advanceSeqLens(self.seq_lens, B, 1)
         nd = 0
         for il, L in enumerate(self.layers):
@@ -710,6 +843,10 @@ class BatchDecoder(_SyntheticModel):
             prod = s.is_producer(il)
             if il == 0:
                 c.batchPrep(self.hidden, 1, L.attn_norm, None, None, None, self.xn, H, B, s.eps, ops=self.xops)
+            elif s.ple_dim:  # the previous layer's PLE tail: (h + norm(proj out)) * scale
+                prev = self.layers[il - 1]
+                c.batchPrepScale(self.ple_out, 1, prev.ple_post_norm, self.hidden3, prev.ple_scale, L.attn_norm,
+                                 self.hidden, self.xn, H, B, s.eps, ops=self.xops)
             else:
                 prev = self.layers[il - 1]
                 c.batchPrep(self.down_parts, nd, prev.post_ffn_norm, self.hidden2, L.attn_norm, self.hidden,
@@ -738,9 +875,21 @@ class BatchDecoder(_SyntheticModel):
             c.gateUpGeluBatch(self.xn, L.wgate, L.wup, self.act, I, H, B, ops=self.xops)
             nd = c.matmulSegmentsBatchPartial(L.qt["wdown"], self.act, [L.wdown], [self.down_parts], [H], I, B,
                                               self.ks_f)
+            if s.ple_dim:
+                # post-FFN norm-add (h, no second norm) -> inp_gate -> gelu * ple_inputs -> proj
+                D = s.ple_dim
+                c.batchPrepScale(self.down_parts, nd, L.post_ffn_norm, self.hidden2, None, None, None, self.hidden3,
+                                 H, B, s.eps)
+                c.pleGate(self.hidden3, None, None, None, L.ple_gate, self.ple_inputs, s.n_layers * D, il * D,
+                          self.ple_gated, D, H, s.eps, batch=B)
+                c.matmulF16(self.ple_gated, L.ple_proj, self.ple_out, H, D, B)
         last = self.layers[-1]
-        c.batchPrep(self.down_parts, nd, last.post_ffn_norm, self.hidden2, self.final_norm, self.hidden, self.xn, H,
-                    B, s.eps, ops=self.xops)
+        if s.ple_dim:
+            c.batchPrepScale(self.ple_out, 1, last.ple_post_norm, self.hidden3, last.ple_scale, self.final_norm,
+                             self.hidden, self.xn, H, B, s.eps, ops=self.xops)
+        else:
+            c.batchPrep(self.down_parts, nd, last.post_ffn_norm, self.hidden2, self.final_norm, self.hidden, self.xn,
+                        H, B, s.eps, ops=self.xops)
         if self.lm_head is not None:
             c.matmulSegmentsBatchPartial(self.lm_type, self.xn, [self.lm_head], [self.logits], [s.vocab], H, B, 1,
                                          ops=self.xops, softcap=s.softcap)
@@ -808,6 +957,8 @@ def open_gguf(path_or_file, max_context_length: Optional[int] = None, n_layers: 
     cfg = config_from_gguf(g, max_context_length)
     emb = g.find("token_embd.weight")
     shape = shape_from_config(cfg, vocab=emb.dims[1] if emb is not None and len(emb.dims) == 2 else None)
+    # per-layer embeddings when the file carries their table (Gemma 4 E2B does)
+    shape.ple_dim = cfg["per_layer_input_dim"] if "per_layer_token_embd.weight" in g else 0
     if n_layers is not None:
         shape.n_layers = n_layers
     return g, cfg, shape

@@ -211,6 +211,18 @@ class Context:
         check(lib().g4_normAddMatmulSegments(self.h, {"q4k": 0, "q6k": 1}[wtype], _p(x), _p(w1), _p(residual),
                                              _p(w2), _p(h_out), W, Y, R, n, N, eps, softcap))
 
+    def normAddScaleMatmulSegments(self, wtype: str, x: Ptr, w1: Ptr, residual: Ptr, out_scale: Ptr, w2: Ptr,
+                                   h_out: Ptr, weights, outputs, rows, N: int, eps: float = 1e-6,
+                                   softcap: float = 0.0) -> None:
+        """h = (residual + norm(x)*w1) * out_scale[0] -> norm(h)*w2 -> y_i = W_i . x'."""
+        n = len(weights)
+        W = (ctypes.c_void_p * n)(*[_p(w).value for w in weights])
+        Y = (ctypes.c_void_p * n)(*[_p(y).value for y in outputs])
+        R = (ctypes.c_uint32 * n)(*rows)
+        check(lib().g4_normAddScaleMatmulSegments(self.h, {"q4k": 0, "q6k": 1}[wtype], _p(x), _p(w1),
+                                                  _p(residual), _p(out_scale), _p(w2), _p(h_out), W, Y, R, n, N,
+                                                  eps, softcap))
+
     def digits_bytes(self, K: int) -> int:
         n = ctypes.c_size_t(0)
         check(lib().g4_digitsBytes(K, ctypes.byref(n)))
@@ -288,6 +300,36 @@ class Context:
         `ops` (optional) receives the matrix-core operand blocks of out."""
         check(lib().g4_batchPrep(self.h, _p(x_parts), nparts, _p(w1), _p(residual), _p(w2), _p(h_out), _p(out),
                                  _p(ops), N, batch, eps))
+
+    def batchPrepScale(self, x_parts: Ptr, nparts: int, w1: Ptr, residual: Ptr, out_scale: Ptr, w2: Ptr,
+                       h_out: Ptr, out: Ptr, N: int, batch: int, eps: float = 1e-6, ops: Ptr = None) -> None:
+        """batchPrep with h = (residual + norm(x)*w1) * out_scale[0]; w2 None: out = h."""
+        check(lib().g4_batchPrepScale(self.h, _p(x_parts), nparts, _p(w1), _p(residual), _p(out_scale), _p(w2),
+                                      _p(h_out), _p(out), _p(ops), N, batch, eps))
+
+    # ---- per-layer embeddings (shaders/ple_*.wgsl) ----
+    def pleStage1Fuse(self, projected: Ptr, norm_w: Ptr, table: Ptr, table_rows: int, ple_inputs: Ptr,
+                      num_layers: int, per_layer_dim: int = 256, eps: float = 1e-6, token: int = 0,
+                      tokens_dev: Ptr = None, count: int = 1) -> None:
+        check(lib().g4_pleStage1Fuse(self.h, _p(projected), _p(norm_w), _p(table), table_rows, token,
+                                     _p(tokens_dev), _p(ple_inputs), num_layers, per_layer_dim, eps, count))
+
+    def pleGeluMul(self, gate: Ptr, ple_inputs: Ptr, out: Ptr, layer_offset: int, size: int) -> None:
+        check(lib().g4_pleGeluMul(self.h, _p(gate), _p(ple_inputs), _p(out), layer_offset, size))
+
+    def pleSkipScaleAdd(self, hidden: Ptr, post_normed: Ptr, scale: Ptr, size: int) -> None:
+        check(lib().g4_pleSkipScaleAdd(self.h, _p(hidden), _p(post_normed), _p(scale), size))
+
+    def matmulF16(self, x: Ptr, w: Ptr, y: Ptr, M: int, N: int, batch: int = 1) -> None:
+        check(lib().g4_matmulF16(self.h, _p(x), _p(w), _p(y), M, N, batch))
+
+    def pleGate(self, x: Ptr, w1: Ptr, residual: Ptr, h_out: Ptr, w_gate: Ptr, ple_inputs: Ptr, ple_stride: int,
+                layer_offset: int, out: Ptr, M: int, N: int, eps: float = 1e-6, batch: int = 1) -> None:
+        check(lib().g4_pleGate(self.h, _p(x), _p(w1), _p(residual), _p(h_out), _p(w_gate), _p(ple_inputs),
+                               ple_stride, layer_offset, _p(out), M, N, eps, batch))
+
+    def dequantQ5K_F16(self, blocks: Ptr, nblocks: int, out: Ptr) -> None:
+        check(lib().g4_dequantQ5K_F16(self.h, _p(blocks), nblocks, _p(out)))
 
     def gateUpGeluBatch(self, x: Ptr, w_gate: Ptr, w_up: Ptr, out: Ptr, M: int, N: int, batch: int,
                         ops: Ptr = None) -> None:
@@ -553,6 +595,9 @@ class Context:
 
     def fill_q6k(self, dst: Ptr, nblocks: int, seed: int) -> None:
         check(lib().g4_fill_q6k(self.h, _p(dst), nblocks, seed))
+
+    def fill_q5k(self, dst: Ptr, nblocks: int, seed: int) -> None:
+        check(lib().g4_fill_q5k(self.h, _p(dst), nblocks, seed))
 
     def fill_normal_f32(self, dst: Ptr, n: int, seed: int, mean: float = 0.0, std: float = 1.0) -> None:
         check(lib().g4_fill_normal_f32(self.h, _p(dst), n, seed, mean, std))

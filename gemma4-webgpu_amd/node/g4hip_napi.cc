@@ -545,6 +545,50 @@ napi_value EmbeddingLookup(napi_env env, napi_callback_info info) {
   return done(env, td ? g4_embeddingLookup_dev(c, e, rows, out, p, td) : g4_embeddingLookup(c, e, rows, out, p));
 }
 
+// ---- per-layer embeddings (shaders/ple_*.wgsl) --------------------------
+
+// pleStage1Fuse(ctx, projected, norm_weight, table_q5k, table_rows, ple_inputs,
+//               {num_layers, per_layer_dim, eps, token_id}[, tokenDev]): every
+// layer in one dispatch (the reference dispatches one workgroup per layer).
+napi_value PleStage1Fuse(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* proj = F32P(a, 1);
+  const uint16_t* w = U16P(a, 2);
+  const void* table = a.ptr(3);
+  const uint32_t rows = a.u32(4);
+  float* out = F32P(a, 5);
+  const uint32_t nl = a.fu32(6, "num_layers"), dim = a.fu32(6, "per_layer_dim"), tok = a.fu32(6, "token_id");
+  const float eps = a.ff32(6, "eps");
+  const uint32_t* td = U32P(a, 7);
+  CHECKED(a);
+  return done(env, g4_pleStage1Fuse(c, proj, w, table, rows, tok, td, out, nl, dim, eps, 1));
+}
+
+// pleGeluMul(ctx, gate, ple_inputs, output, {layer_offset, size})
+napi_value PleGeluMul(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* g = F32P(a, 1);
+  const float* ple = F32P(a, 2);
+  float* out = F32P(a, 3);
+  const uint32_t off = a.fu32(4, "layer_offset"), n = a.fu32(4, "size");
+  CHECKED(a);
+  return done(env, g4_pleGeluMul(c, g, ple, out, off, n));
+}
+
+// pleSkipScaleAdd(ctx, hidden, post_normed, scale, {size})
+napi_value PleSkipScaleAdd(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  float* h = F32P(a, 1);
+  const float* pn = F32P(a, 2);
+  const uint16_t* sc = U16P(a, 3);
+  const uint32_t n = a.fu32(4, "size");
+  CHECKED(a);
+  return done(env, g4_pleSkipScaleAdd(c, h, pn, sc, n));
+}
+
 // argmax(ctx, logits, result, size)
 napi_value Argmax(napi_env env, napi_callback_info info) {
   Args a(env, info);
@@ -617,6 +661,9 @@ const Entry kEntries[] = {
     {"argmax", Argmax},
     {"topk256", Topk256},
     {"advancePosition", AdvancePosition},
+    {"pleStage1Fuse", PleStage1Fuse},
+    {"pleGeluMul", PleGeluMul},
+    {"pleSkipScaleAdd", PleSkipScaleAdd},
 };
 
 }  // namespace

@@ -9,13 +9,16 @@
 //   src/engine.ts:1670-1746  sampleNextTokenSubmit (LM head, softcap, argmax /
 //                            top-k, the sampled token fed to the next embed)
 // with the work-buffer names of src/types.ts:489-517 and the layer tensor
-// names of the GGUF (attn_q, ffn_down, ...). The per-layer-embedding passes
-// (ple1.*, ple2.*) are not part of this path and are not issued.
+// names of the GGUF (attn_q, ffn_down, ...), including the per-layer-embedding
+// passes (ple1.* before the layers, src/engine.ts:1516-1535; ple2.* at the end
+// of each layer, src/engine.ts:1608-1616).
 //
 // Differences from the WebGPU backend, all at the boundary:
-//  - matrices are the raw GGUF block bytes (Q4_K, Q6_K for ffn_down and the
-//    tied LM head) rather than f16 rows; the f16 token table is still bound
-//    for the embedding lookup;
+//  - matrices are the raw GGUF block bytes in the file's own format per
+//    tensor (Q4_K or Q6_K: a Q4_K_M file mixes both) rather than f16 rows;
+//    the f16 token table is still bound for the embedding lookup, and the
+//    per-layer-embedding table stays in its Q5_K blocks (one 256-value block
+//    per token and layer), the stage-1 pass dispatching every layer at once;
 //  - the KV caches are f16 (2 bytes per element);
 //  - dynamic fields (position, seq_len, token) are call arguments or, with a
 //    device position / token buffer, read by the kernels themselves, so a
@@ -74,6 +77,7 @@ function e2bConfig(overrides) {
     intermediate_sizes: inter,
     num_unshared_layers: numUnshared,
     kv_producer_for_layer: kvProducerMap(numLayers, numUnshared, isSliding),
+    per_layer_input_dim: o.per_layer_input_dim !== undefined ? o.per_layer_input_dim : 256,
     final_logit_softcapping: o.final_logit_softcapping !== undefined ? o.final_logit_softcapping : 30.0,
   };
 }
@@ -87,6 +91,12 @@ const isKvProducer = (C, il) => C.kv_producer_for_layer[il] === il;
 
 const LAYER_TENSORS = ['attn_norm', 'attn_q', 'attn_k', 'attn_v', 'attn_q_norm', 'attn_k_norm', 'attn_output',
   'post_attention_norm', 'ffn_norm', 'ffn_gate', 'ffn_up', 'ffn_down', 'post_ffw_norm'];
+// per-layer-embedding tensors of a layer (f16), src/engine.ts:63-69
+const PLE_TENSORS = ['inp_gate', 'proj', 'post_norm', 'layer_output_scale'];
+// the matrices' block formats unless a layer says otherwise
+const DEFAULT_FORMATS = { attn_q: 'q4k', attn_k: 'q4k', attn_v: 'q4k', attn_output: 'q4k', ffn_gate: 'q4k',
+  ffn_up: 'q4k', ffn_down: 'q6k' };
+const BLOCK_BYTES = { q4k: 144, q6k: 210 };
 
 class HipBackend {
   // addon: the g4hip.node exports (or any object with the same functions);
@@ -103,7 +113,9 @@ class HipBackend {
     this.trace = o.trace || null;
     this.owned = [];
     this.layers = [];      // per layer: {tensor name: handle}
-    this.globals = {};     // tokenEmbed (f16), lmHead (Q6_K), finalNorm, rope_freqs
+    this.formats = [];     // per layer: {matrix name: 'q4k' | 'q6k'}
+    this.globals = {};     // tokenEmbed (f16), lmHead (+ lmHeadFormat), finalNorm, rope_freqs,
+                           // perLayerModelProj / perLayerProjNorm (f16), perLayerTable (Q5_K)
     this.workBuffers = {};
     this.kvCaches = [];    // per layer: {k, v} (consumers hold their producer's)
   }
@@ -146,6 +158,11 @@ class HipBackend {
       ffnMul: f4(maxI), ffnDown: f4(H), logits: f4(C.vocab_size), argmaxResult: f4(1), topk256Result: f4(512),
       position: f4(1),
     };
+    const D = C.per_layer_input_dim;
+    if (D > 0) {
+      Object.assign(this.workBuffers, { plePmProjected: f4(C.num_layers * D), pleInputs: f4(C.num_layers * D),
+        pleGate: f4(D), pleGated: f4(D), pleProjOut: f4(H), plePostNormed: f4(H) });
+    }
     this.g.memset(this.ctx, this.workBuffers.argmaxResult, 0, 4);
     this.g.memset(this.ctx, this.workBuffers.position, 0, 4);
     this.kvCaches = [];
@@ -163,38 +180,55 @@ class HipBackend {
     }
   }
 
-  // Byte sizes of a layer's tensors (raw GGUF blocks, f16 norm weights).
-  layerTensorBytes(il) {
+  // Byte sizes of a layer's tensors (raw GGUF blocks in `formats`, f16 norm
+  // and per-layer-embedding weights).
+  layerTensorBytes(il, formats) {
     const C = this.config;
+    const F = Object.assign({}, DEFAULT_FORMATS, formats || this.formats[il] || {});
     const H = C.hidden_size;
     const hd = headDim(C, il);
     const Q = C.num_q_heads * hd;
     const KV = C.num_kv_heads * hd;
     const I = intermediateSize(C, il);
-    const q4 = (m, n) => (m * n / 256) * 144;
+    const D = C.per_layer_input_dim;
+    const mat = (name, m, n) => (m * n / 256) * BLOCK_BYTES[F[name]];
     const out = {
-      attn_norm: 2 * H, attn_q: q4(Q, H), attn_q_norm: 2 * hd, attn_output: q4(H, Q), post_attention_norm: 2 * H,
-      ffn_norm: 2 * H, ffn_gate: q4(I, H), ffn_up: q4(I, H), ffn_down: (H * I / 256) * 210, post_ffw_norm: 2 * H,
+      attn_norm: 2 * H, attn_q: mat('attn_q', Q, H), attn_q_norm: 2 * hd, attn_output: mat('attn_output', H, Q),
+      post_attention_norm: 2 * H, ffn_norm: 2 * H, ffn_gate: mat('ffn_gate', I, H), ffn_up: mat('ffn_up', I, H),
+      ffn_down: mat('ffn_down', H, I), post_ffw_norm: 2 * H,
     };
     if (isKvProducer(C, il)) {
-      out.attn_k = q4(KV, H);
-      out.attn_v = q4(KV, H);
+      out.attn_k = mat('attn_k', KV, H);
+      out.attn_v = mat('attn_v', KV, H);
       out.attn_k_norm = 2 * hd;
     }
+    if (D > 0) Object.assign(out, { inp_gate: 2 * D * H, proj: 2 * H * D, post_norm: 2 * H, layer_output_scale: 2 });
     return out;
   }
 
-  setLayerWeights(il, tensors) {
-    const need = Object.keys(this.layerTensorBytes(il));
+  // formats: the block format of each matrix that is not the default
+  // (Q4_K, ffn_down Q6_K), e.g. {attn_v: 'q6k', ffn_down: 'q4k'}.
+  setLayerWeights(il, tensors, formats) {
+    const F = Object.assign({}, DEFAULT_FORMATS, formats || {});
+    for (const name of Object.keys(F)) {
+      if (BLOCK_BYTES[F[name]] === undefined) throw new Error('layer ' + il + ': ' + name + ' format ' + F[name]);
+    }
+    const need = Object.keys(this.layerTensorBytes(il, F));
     for (const name of need) {
       if (tensors[name] === undefined) throw new Error('layer ' + il + ': missing tensor ' + name);
     }
     this.layers[il] = tensors;
+    this.formats[il] = F;
   }
 
   setGlobals(g) {
-    for (const name of ['tokenEmbed', 'lmHead', 'finalNorm', 'rope_freqs']) {
+    const need = ['tokenEmbed', 'lmHead', 'finalNorm', 'rope_freqs'];
+    if (this.config.per_layer_input_dim > 0) need.push('perLayerModelProj', 'perLayerProjNorm', 'perLayerTable');
+    for (const name of need) {
       if (g[name] === undefined) throw new Error('missing global ' + name);
+    }
+    if (g.lmHeadFormat !== undefined && BLOCK_BYTES[g.lmHeadFormat] === undefined) {
+      throw new Error('lmHead format ' + g.lmHeadFormat);
     }
     this.globals = g;
   }
@@ -225,12 +259,25 @@ class HipBackend {
     const pd = positionDev ? W.position : null;
     const G = this.globals;
 
+    const tokDev = tokenId === null ? W.argmaxResult : null;
     this._key('embed', 'embeddingLookup');
     g.embeddingLookup(c, G.tokenEmbed, C.vocab_size, W.hidden,
-      { hidden_size: H, token_id: tokenId === null ? 0 : tokenId }, tokenId === null ? W.argmaxResult : null);
+      { hidden_size: H, token_id: tokenId === null ? 0 : tokenId }, tokDev);
+
+    const D = C.per_layer_input_dim;
+    if (D > 0) {
+      // PLE stage 1: per_layer_model_proj . embedding, then every layer's
+      // norm + table row + blend
+      this._key('ple1.pmProj', 'matmulQuant');
+      g.matmulQuant(c, W.hidden, G.perLayerModelProj, W.plePmProjected, { M: C.num_layers * D, N: H }, 'f16');
+      this._key('ple1.stage1Fuse', 'pleStage1Fuse');
+      g.pleStage1Fuse(c, W.plePmProjected, G.perLayerProjNorm, G.perLayerTable, C.vocab_size, W.pleInputs,
+        { num_layers: C.num_layers, per_layer_dim: D, eps: eps, token_id: tokenId === null ? 0 : tokenId }, tokDev);
+    }
 
     for (let il = 0; il < C.num_layers; il++) {
       const L = this.layers[il];
+      const F = this.formats[il] || DEFAULT_FORMATS;
       const HD = headDim(C, il);
       const I = intermediateSize(C, il);
       const Q = NQH * HD;
@@ -248,12 +295,12 @@ class HipBackend {
       g.rmsNorm(c, W.hidden, L.attn_norm, W.normed, { hidden_size: H, eps: eps });
       const lin = prod ? 'attn.linearQKV.producer' : 'attn.linearQ.consumer';
       this._key(lin, 'matmulQuant');
-      g.matmulQuant(c, W.normed, L.attn_q, W.q, { M: Q, N: H }, 'q4k');
+      g.matmulQuant(c, W.normed, L.attn_q, W.q, { M: Q, N: H }, F.attn_q);
       if (prod) {
         this._key(lin, 'matmulQuant');
-        g.matmulQuant(c, W.normed, L.attn_k, W.k, { M: KV, N: H }, 'q4k');
+        g.matmulQuant(c, W.normed, L.attn_k, W.k, { M: KV, N: H }, F.attn_k);
         this._key(lin, 'matmulQuant');
-        g.matmulQuant(c, W.normed, L.attn_v, W.v, { M: KV, N: H }, 'q4k');
+        g.matmulQuant(c, W.normed, L.attn_v, W.v, { M: KV, N: H }, F.attn_v);
         this._key('attn.vNorm', 'perHeadRmsNormNoWeight');
         g.perHeadRmsNormNoWeight(c, W.v, { num_heads: NKH, head_dim: HD, eps: eps });
       }
@@ -278,22 +325,37 @@ class HipBackend {
       g.attnOutput(c, W.attnScores, kv.v, W.attnOut, { num_q_heads: NQH, num_kv_heads: NKH, head_dim: HD,
         seq_len: sl }, pd);
       this._key('attn.linearOut', 'matmulQuant');
-      g.matmulQuant(c, W.attnOut, L.attn_output, W.attnProj, { M: H, N: Q }, 'q4k');
+      g.matmulQuant(c, W.attnOut, L.attn_output, W.attnProj, { M: H, N: Q }, F.attn_output);
       this._key('attn.postNormAdd', 'fusedNormAdd');
       g.fusedNormAdd(c, W.attnProj, L.post_attention_norm, W.hidden, W.residual, { size: H, eps: eps });
       this._key('ffn.rmsNorm', 'rmsNorm');
       g.rmsNorm(c, W.residual, L.ffn_norm, W.normed, { hidden_size: H, eps: eps });
-      const mm = this.mr4ForFfn ? 'matmulQuantMR4' : 'matmulQuant';
+      // (the 4-row kernel reads Q4_K only)
+      const mm = this.mr4ForFfn && F.ffn_gate === 'q4k' && F.ffn_up === 'q4k' ? 'matmulQuantMR4' : 'matmulQuant';
       this._key('ffn.linearGateUp', mm);
-      g[mm](c, W.normed, L.ffn_gate, W.ffnGate, { M: I, N: H }, 'q4k');
+      g[mm](c, W.normed, L.ffn_gate, W.ffnGate, { M: I, N: H }, F.ffn_gate);
       this._key('ffn.linearGateUp', mm);
-      g[mm](c, W.normed, L.ffn_up, W.ffnUp, { M: I, N: H }, 'q4k');
+      g[mm](c, W.normed, L.ffn_up, W.ffnUp, { M: I, N: H }, F.ffn_up);
       this._key('ffn.geluMul', 'geluMul');
       g.geluMul(c, W.ffnGate, W.ffnUp, W.ffnMul, I);
       this._key('ffn.linearDown', 'matmulQuant');
-      g.matmulQuant(c, W.ffnMul, L.ffn_down, W.ffnDown, { M: H, N: I }, 'q6k');
+      g.matmulQuant(c, W.ffnMul, L.ffn_down, W.ffnDown, { M: H, N: I }, F.ffn_down);
       this._key('ffn.postNormAdd', 'fusedNormAdd');
       g.fusedNormAdd(c, W.ffnDown, L.post_ffw_norm, W.residual, W.hidden, { size: H, eps: eps });
+
+      if (D > 0) {
+        // PLE stage 2 and layer_output_scale
+        this._key('ple2.linearInpGate', 'matmulQuant');
+        g.matmulQuant(c, W.hidden, L.inp_gate, W.pleGate, { M: D, N: H }, 'f16');
+        this._key('ple2.geluMul', 'pleGeluMul');
+        g.pleGeluMul(c, W.pleGate, W.pleInputs, W.pleGated, { layer_offset: il * D, size: D });
+        this._key('ple2.linearPostProj', 'matmulQuant');
+        g.matmulQuant(c, W.pleGated, L.proj, W.pleProjOut, { M: H, N: D }, 'f16');
+        this._key('ple2.rmsNorm', 'rmsNorm');
+        g.rmsNorm(c, W.pleProjOut, L.post_norm, W.plePostNormed, { hidden_size: H, eps: eps });
+        this._key('ple2.skipScaleAdd', 'pleSkipScaleAdd');
+        g.pleSkipScaleAdd(c, W.hidden, W.plePostNormed, L.layer_output_scale, { size: H });
+      }
     }
     this._key('final.rmsNorm', 'rmsNorm');
     g.rmsNorm(c, W.hidden, G.finalNorm, W.normed, { hidden_size: H, eps: eps });
@@ -309,7 +371,8 @@ class HipBackend {
     const W = this.workBuffers;
     const V = C.vocab_size;
     this._key('lmHead', 'matmulQuant');
-    g.matmulQuant(c, W.normed, this.globals.lmHead, W.logits, { M: V, N: C.hidden_size }, 'q6k');
+    g.matmulQuant(c, W.normed, this.globals.lmHead, W.logits, { M: V, N: C.hidden_size },
+      this.globals.lmHeadFormat || 'q6k');
     if (C.final_logit_softcapping > 0) {
       this._key('logitSoftcap', 'logitSoftcap');
       g.logitSoftcap(c, W.logits, { size: V, cap: C.final_logit_softcapping });
@@ -353,4 +416,6 @@ module.exports = {
   intermediateSize: intermediateSize,
   isKvProducer: isKvProducer,
   LAYER_TENSORS: LAYER_TENSORS,
+  PLE_TENSORS: PLE_TENSORS,
+  DEFAULT_FORMATS: DEFAULT_FORMATS,
 };

@@ -466,6 +466,17 @@ int g4_normAddMatmulSegments(g4_ctx* ctx, int wtype, const float* x, const uint1
                              const void* const* weights, float* const* outputs,
                              const uint32_t* rows, int nseg, uint32_t N, float eps,
                              float softcap_cap);
+/* The same with the residual form's sum scaled by the f16 scalar at
+ * out_scale before it is written to h_out and normalised by w2:
+ *   h = (residual + x * w1 / rms(x)) * out_scale[0];  x' = h * w2 / rms(h)
+ * (src/engine.ts:1611-1616: the per-layer-embedding tail's rmsNorm +
+ * pleSkipScaleAdd, shaders/ple_skip_scale_add.wgsl, ahead of the next
+ * layer's attention rmsNorm). out_scale NULL is g4_normAddMatmulSegments. */
+int g4_normAddScaleMatmulSegments(g4_ctx* ctx, int wtype, const float* x, const uint16_t* w1,
+                                  const float* residual, const uint16_t* out_scale, const uint16_t* w2,
+                                  float* h_out, const void* const* weights, float* const* outputs,
+                                  const uint32_t* rows, int nseg, uint32_t N, float eps,
+                                  float softcap_cap);
 /* The LM head with greedy sampling in two launches: g4_normAddMatmulSegments
  * over one matrix (logits[rows], softcapped when softcap_cap != 0), whose
  * workgroups also keep the argmax candidate of the rows they store, then the
@@ -526,6 +537,14 @@ int g4_batchOperandBytes(uint32_t N, uint32_t batch, size_t* bytes);
 int g4_batchPrep(g4_ctx* ctx, const float* x_parts, uint32_t nparts, const uint16_t* w1,
                  const float* residual, const uint16_t* w2, float* h_out, float* out, void* ops,
                  uint32_t N, uint32_t batch, float eps);
+/* g4_batchPrep with the residual form's sum scaled by the f16 scalar at
+ * out_scale (NULL: 1) before it is written to h_out and normalised:
+ * h = (residual + x * w1 / rms(x)) * out_scale[0] (the per-layer-embedding
+ * tail, src/engine.ts:1614-1616); and with w2 == NULL, out = h (no second
+ * norm: the input of the per-layer-embedding gate, src/engine.ts:1612). */
+int g4_batchPrepScale(g4_ctx* ctx, const float* x_parts, uint32_t nparts, const uint16_t* w1,
+                      const float* residual, const uint16_t* out_scale, const uint16_t* w2, float* h_out,
+                      float* out, void* ops, uint32_t N, uint32_t batch, float eps);
 /* x [batch][N] f32 (with `ops` from g4_batchPrep of the same x, or NULL)
  * times up to 4 matrices on the matrix cores, K split into
  * *ksplit <= max_ksplit chunks (chosen to fill the device); outputs[i]
@@ -578,6 +597,45 @@ int g4_dequantF16(g4_ctx* ctx, int wtype, const void* blocks, uint64_t nblocks, 
  * one word per workgroup to sink[nwgs]. It times the pure-streaming floor of
  * a launch and calibrates the HBM byte counters. */
 int g4_streamRead(g4_ctx* ctx, const void* src, uint64_t bytes, int policy, uint32_t nwgs, uint32_t* sink);
+
+/* ---- per-layer embeddings (Gemma 4 PLE) ----
+ *
+ * g4_pleStage1Fuse: shaders/ple_stage1_fuse.wgsl for every layer of `count`
+ * rows in one launch (replaces the per-layer dispatches of
+ * src/engine.ts:1529-1535). projected [count][num_layers*256] is
+ * per_layer_model_proj . embedding; table_q5k holds the per_layer_token_embd
+ * Q5_K blocks, table_rows x num_layers of them (row = token, one block =
+ * one layer's 256 values, src/engine.ts:626-700); each value is rounded to
+ * f16 as the reference's upload does. Row b's token is tokens_dev[b] (NULL:
+ * `token`, count 1); a token past the table reads a zero row.
+ *   ple_inputs[b][l*256 + t] = (p/rms_l * f32(norm_w[t]) + f16(table) * 16) / sqrt(2)
+ * per_layer_dim must be 256. */
+int g4_pleStage1Fuse(g4_ctx* ctx, const float* projected, const uint16_t* norm_w, const void* table_q5k,
+                     uint32_t table_rows, uint32_t token, const uint32_t* tokens_dev, float* ple_inputs,
+                     uint32_t num_layers, uint32_t per_layer_dim, float eps, uint32_t count);
+/* shaders/ple_gelu_mul.wgsl: output[i] = gelu(gate[i]) * ple_inputs[layer_offset + i]. */
+int g4_pleGeluMul(g4_ctx* ctx, const float* gate, const float* ple_inputs, float* output, uint32_t layer_offset,
+                  uint32_t size);
+/* shaders/ple_skip_scale_add.wgsl: hidden[i] = (hidden[i] + post_normed[i]) * f32(scale[0]). */
+int g4_pleSkipScaleAdd(g4_ctx* ctx, float* hidden, const float* post_normed, const uint16_t* scale,
+                       uint32_t size);
+/* y[b][m] = W[m] . x[b] for f16 rows W [M][N] (N 256, 1536 or 2048) and
+ * `batch` f32 vectors: the reference's matmulQuant on its f16 weights
+ * (shaders/matmul_quant.wgsl), as PLE runs it for per_layer_model_proj,
+ * inp_gate and proj (src/engine.ts:1521-1524, 1611, 1613). */
+int g4_matmulF16(g4_ctx* ctx, const float* x, const uint16_t* weight, float* y, uint32_t M, uint32_t N,
+                 uint32_t batch);
+/* The PLE gate (src/engine.ts:1606 + 1611-1612): with w1 (batch 1) the
+ * vector is h = residual + x * w1 / rms(x) (fusedNormAdd; written to h_out
+ * when non-NULL, which must not alias x or residual), else x [batch][N];
+ * out[b][m] = gelu(w_gate[m] . h_b) * ple_inputs[b * ple_stride +
+ * layer_offset + m]. */
+int g4_pleGate(g4_ctx* ctx, const float* x, const uint16_t* w1, const float* residual, float* h_out,
+               const uint16_t* w_gate, const float* ple_inputs, uint32_t ple_stride, uint32_t layer_offset,
+               float* out, uint32_t M, uint32_t N, float eps, uint32_t batch);
+/* Q5_K blocks to f16 values (src/gguf.ts:218-257 values rounded to nearest
+ * even, as the per-layer table is uploaded, src/engine.ts:626-700). */
+int g4_dequantQ5K_F16(g4_ctx* ctx, const void* blocks, uint64_t nblocks, uint16_t* out);
 
 /* GGUF v2/v3 model files (replaces GGUFParser, src/gguf.ts:75-101 header,
  * :103-134 key/values, :136-160 tensor infos and data offset, :385-395 tensor
@@ -632,6 +690,7 @@ int g4_gguf_upload_f16(g4_ctx* ctx, const g4_gguf* g, uint64_t index, uint16_t* 
 uint64_t g4_splitmix64(uint64_t seed, uint64_t idx);
 int g4_fill_q4k(g4_ctx* ctx, void* dst, uint64_t nblocks, uint64_t seed);
 int g4_fill_q6k(g4_ctx* ctx, void* dst, uint64_t nblocks, uint64_t seed);
+int g4_fill_q5k(g4_ctx* ctx, void* dst, uint64_t nblocks, uint64_t seed);
 int g4_fill_normal_f32(g4_ctx* ctx, float* dst, uint64_t n, uint64_t seed, float mean, float std);
 int g4_fill_normal_f16(g4_ctx* ctx, uint16_t* dst, uint64_t n, uint64_t seed, float mean,
                        float std);

@@ -173,6 +173,36 @@ void g4o_dequant_q6k(const uint8_t* blocks, size_t nblocks, float* out) {
   }
 }
 
+/* src/gguf.ts:218-257 (decodeQ5_KBlock). 176-byte block: f16 d @0, f16
+ * dmin @2, the 12 packed 6-bit scale/min bytes of Q4_K @4, qh[32] @16,
+ * qs[128] @48. Group g (values 64g .. 64g+63) uses sub-blocks 2g and 2g+1:
+ *   value 64g + l      = d*sc(2g)   * ((qs[32g+l] & 15) + 16*bit(qh[l], 2g))   - dmin*m(2g)
+ *   value 64g + 32 + l = d*sc(2g+1) * ((qs[32g+l] >> 4) + 16*bit(qh[l], 2g+1)) - dmin*m(2g+1)
+ * evaluated in f64 as the reference's JS numbers and stored as f32. */
+void g4o_dequant_q5k(const uint8_t* blocks, size_t nblocks, float* out) {
+  for (size_t b = 0; b < nblocks; ++b) {
+    const uint8_t* blk = blocks + b * 176;
+    const double d = g4o_f16_to_f32(rd16(blk));
+    const double dmin = g4o_f16_to_f32(rd16(blk + 2));
+    const uint8_t* s = blk + 4;
+    const uint8_t* qh = blk + 16;
+    const uint8_t* qs = blk + 48;
+    float* o = out + b * 256;
+    for (int g = 0; g < 4; ++g) {
+      int sc1, m1, sc2, m2;
+      g4o_q4k_scale_min(s, 2 * g, &sc1, &m1);
+      g4o_q4k_scale_min(s, 2 * g + 1, &sc2, &m2);
+      const double d1 = d * sc1, min1 = dmin * m1, d2 = d * sc2, min2 = dmin * m2;
+      for (int l = 0; l < 32; ++l) {
+        const int lo = (qs[32 * g + l] & 0x0f) + (((qh[l] >> (2 * g)) & 1) ? 16 : 0);
+        const int hi = (qs[32 * g + l] >> 4) + (((qh[l] >> (2 * g + 1)) & 1) ? 16 : 0);
+        o[64 * g + l] = (float)(d1 * lo - min1);
+        o[64 * g + 32 + l] = (float)(d2 * hi - min2);
+      }
+    }
+  }
+}
+
 /* ------------------------------------------------------------------------ */
 /* matvec: y[m] = sum_k W[m,k] * x[k]   (shaders/matmul_quant.wgsl:25-53)    */
 /* ------------------------------------------------------------------------ */
@@ -262,6 +292,31 @@ void g4o_gelu_mul(const float* gate, const float* up, float* out, uint32_t n) {
     const double th = (double)(float)tanh(t);
     out[i] = (float)(0.5 * x * (1.0 + th) * (double)up[i]);
   }
+}
+
+/* shaders/ple_stage1_fuse.wgsl:14-37 for every layer: with
+ * rms_l = sqrt(mean(projected[l*D .. l*D+D)^2) + eps),
+ *   ple_inputs[l*D + t] = (projected[l*D+t] / rms_l * f32(norm_w[t])
+ *                          + f32(embed_row[l*D+t]) * sqrt(D)) / sqrt(2),
+ * embed_row being the token's row of the per-layer table (f16 values). */
+void g4o_ple_stage1(const float* projected, const uint16_t* norm_w, const uint16_t* embed_row,
+                    float* ple_inputs, uint32_t num_layers, uint32_t dim, float eps) {
+  const double sq = sqrt((double)dim), inv2 = 1.0 / sqrt(2.0);
+  for (uint32_t l = 0; l < num_layers; ++l) {
+    const float* v = projected + (size_t)l * dim;
+    const double rms = sqrt(mean_sq(v, dim) + (double)eps);
+    for (uint32_t t = 0; t < dim; ++t) {
+      const double normed = (double)v[t] / rms * g4o_f16_to_f32(norm_w[t]);
+      const double emb = (double)g4o_f16_to_f32(embed_row[(size_t)l * dim + t]) * sq;
+      ple_inputs[(size_t)l * dim + t] = (float)((normed + emb) * inv2);
+    }
+  }
+}
+
+/* shaders/ple_skip_scale_add.wgsl:14-20: hidden = (hidden + post_normed) * f32(scale) */
+void g4o_ple_skip_scale_add(float* hidden, const float* post_normed, uint16_t scale, uint32_t n) {
+  const double s = g4o_f16_to_f32(scale);
+  for (uint32_t i = 0; i < n; ++i) hidden[i] = (float)(((double)hidden[i] + (double)post_normed[i]) * s);
 }
 
 /* shaders/per_head_rms_norm_no_weight.wgsl:14-37 (v_norm): per head

@@ -28,6 +28,7 @@ uint16_t g4o_f32_to_f16_trunc(float f); /* manual fallback, src/gguf.ts:439-471 
 void g4o_q4k_scale_min(const uint8_t scales12[12], int j, int* sc, int* m);
 void g4o_dequant_q4k(const uint8_t* blocks, size_t nblocks, float* out);
 void g4o_dequant_q6k(const uint8_t* blocks, size_t nblocks, float* out);
+void g4o_dequant_q5k(const uint8_t* blocks, size_t nblocks, float* out); /* src/gguf.ts:218-257 */
 
 /* ---- matvec (shaders/matmul_quant.wgsl:12-54; rows M, reduction N) ---- */
 void g4o_matmul_f32w(const float* x, const float* W, float* y, uint32_t M, uint32_t N);
@@ -65,6 +66,11 @@ void g4o_attention_paged(const float* q, const uint16_t* k_pool, const uint16_t*
                          const int32_t* page_table, uint32_t page_size, float* out, uint32_t nqh,
                          uint32_t nkh, uint32_t hd, uint32_t seq_len, float scale,
                          uint32_t window);
+
+/* ---- per-layer embeddings (shaders/ple_*.wgsl) ---- */
+void g4o_ple_stage1(const float* projected, const uint16_t* norm_w, const uint16_t* embed_row,
+                    float* ple_inputs, uint32_t num_layers, uint32_t dim, float eps);
+void g4o_ple_skip_scale_add(float* hidden, const float* post_normed, uint16_t scale, uint32_t n);
 
 /* ---- LM head tail ---- */
 void g4o_logit_softcap(float* logits, uint32_t n, float cap);

@@ -25,6 +25,7 @@ _LIB_PATH = os.path.join(_HERE, "libg4oracle.so")
 
 Q4K_BLOCK_BYTES = 144
 Q6K_BLOCK_BYTES = 210
+Q5K_BLOCK_BYTES = 176
 QK = 256
 
 
@@ -62,6 +63,9 @@ def _declare(L):
         "g4o_q4k_scale_min": (None, [_P, ctypes.c_int, _P, _P]),
         "g4o_dequant_q4k": (None, [_P, _SZ, _P]),
         "g4o_dequant_q6k": (None, [_P, _SZ, _P]),
+        "g4o_dequant_q5k": (None, [_P, _SZ, _P]),
+        "g4o_ple_stage1": (None, [_P, _P, _P, _P, _U32, _U32, _F]),
+        "g4o_ple_skip_scale_add": (None, [_P, _P, ctypes.c_uint16, _U32]),
         "g4o_matmul_f32w": (None, [_P, _P, _P, _U32, _U32]),
         "g4o_matmul_f16w": (None, [_P, _P, _P, _U32, _U32]),
         "g4o_matmul_q4k": (None, [_P, _P, _P, _U32, _U32]),
@@ -145,6 +149,15 @@ def dequant_q6k(blocks: np.ndarray) -> np.ndarray:
     return out
 
 
+def dequant_q5k(blocks: np.ndarray) -> np.ndarray:
+    b = _c(blocks, np.uint8).reshape(-1)
+    assert b.size % Q5K_BLOCK_BYTES == 0
+    n = b.size // Q5K_BLOCK_BYTES
+    out = np.empty(n * QK, np.float32)
+    lib().g4o_dequant_q5k(_p(b), n, _p(out))
+    return out
+
+
 def matmul(x: np.ndarray, W: np.ndarray, M: int, N: int, wtype: str) -> np.ndarray:
     """y[M] = W[M, N] . x[N] for wtype in {'f32', 'f16', 'q4k', 'q6k'}."""
     x = _c(x, np.float32)
@@ -191,6 +204,50 @@ def gelu_mul(gate, up):
     out = np.empty_like(g)
     lib().g4o_gelu_mul(_p(g), _p(u), _p(out), g.size)
     return out
+
+
+def ple_stage1(projected, norm_w_f16, embed_row_f16, num_layers, dim, eps=1e-6):
+    """shaders/ple_stage1_fuse.wgsl for every layer of one token."""
+    p = _c(projected, np.float32)
+    w = _c(norm_w_f16, np.uint16)
+    e = _c(embed_row_f16, np.uint16)
+    assert p.size == e.size == num_layers * dim and w.size == dim
+    out = np.empty(num_layers * dim, np.float32)
+    lib().g4o_ple_stage1(_p(p), _p(w), _p(e), _p(out), num_layers, dim, eps)
+    return out
+
+
+def ple_gelu_mul(gate, ple_inputs, layer_offset):
+    """shaders/ple_gelu_mul.wgsl: gelu(gate[i]) * ple_inputs[layer_offset + i]
+    (the GELU of gelu_mul)."""
+    g = _c(gate, np.float32)
+    return gelu_mul(g, _c(ple_inputs, np.float32)[layer_offset:layer_offset + g.size])
+
+
+def ple_skip_scale_add(hidden, post_normed, scale_f16):
+    h = _c(hidden, np.float32).copy()
+    n = _c(post_normed, np.float32)
+    lib().g4o_ple_skip_scale_add(_p(h), _p(n), int(scale_f16), h.size)
+    return h
+
+
+def ple_project(x0, model_proj_f16, proj_norm_f16, row_f16, num_layers, dim, eps=1e-6):
+    """PLE stage 1 for one token (src/engine.ts:1516-1535): the f16
+    per_layer_model_proj [L*D x H] times the step's input vector, then
+    shaders/ple_stage1_fuse.wgsl per layer with the token's table row (f16)."""
+    x0 = _c(x0, np.float32)
+    proj = matmul(x0, model_proj_f16, num_layers * dim, x0.size, "f16")
+    return ple_stage1(proj, proj_norm_f16, row_f16, num_layers, dim, eps)
+
+
+def ple_layer_tail(x, gate_f16, proj_f16, post_norm_f16, scale_f16, ple_slice, eps=1e-6):
+    """PLE stage 2 of one layer (src/engine.ts:1608-1616): inp_gate,
+    gelu * ple_inputs slice, proj, rmsNorm, skip-scale-add."""
+    x = _c(x, np.float32)
+    D, H = _c(ple_slice, np.float32).size, x.size
+    g = matmul(x, gate_f16, D, H, "f16")
+    po = matmul(gelu_mul(g, ple_slice), proj_f16, H, D, "f16")
+    return ple_skip_scale_add(x, rms_norm(po, post_norm_f16, eps), scale_f16)
 
 
 def per_head_rms_norm_no_weight(data, num_heads, head_dim, eps=1e-6):

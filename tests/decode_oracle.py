@@ -4,6 +4,7 @@ over weights downloaded once from a decoder's device buffers."""
 import numpy as np
 
 import oracle as O
+from g4hip.decoder import DEFAULT_TYPES
 
 
 def gelu_mul_f32(gate, up):
@@ -43,9 +44,16 @@ class HostModel:
         for L in dec.layers:
             self.layers.append({k: getattr(L, k).download(u8 if k.startswith("w") else u16)
                                 for k in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown", "attn_norm",
-                                          "post_attn_norm", "pre_ffn_norm", "post_ffn_norm", "q_norm", "k_norm")
-                                if getattr(L, k) is not None})
-        self.qt = [dict(L.qt) for L in dec.layers]  # each matrix's format
+                                          "post_attn_norm", "pre_ffn_norm", "post_ffn_norm", "q_norm", "k_norm",
+                                          "ple_gate", "ple_proj", "ple_post_norm", "ple_scale")
+                                if getattr(L, k, None) is not None})
+        # per-layer embeddings: the projection and its norm on the host, the
+        # Q5_K table's rows fetched per token
+        self.ple = None
+        if s.ple_dim:
+            self.ple = dict(model_proj=dec.ple_model_proj.download(u16), proj_norm=dec.ple_proj_norm.download(u16),
+                            table=dec.ple_table)
+        self.qt = [dict(getattr(L, "qt", DEFAULT_TYPES)) for L in dec.layers]  # each matrix's format
         self.final_norm = dec.final_norm.download(u16)
         self.lm_type = getattr(dec, "lm_type", "q6k")
         self.lm_head = dec.lm_head.download(u8) if dec.lm_head is not None else None
@@ -57,15 +65,28 @@ class HostModel:
         row = self.embedding.download(np.uint16, H, offset=int(token) * H * 2)
         return O.embedding_lookup(row.view(np.float16), H, 0)
 
-    def step(self, hidden, kcs, vcs, pos, gelu=O.gelu_mul, row_toward_zero=False):
+    def ple_inputs(self, x0, token: int):
+        """PLE stage 1 (src/engine.ts:1516-1535) for the step's input vector:
+        per_layer_model_proj . x0, then shaders/ple_stage1_fuse.wgsl per layer
+        over the token's table row, dequantized (src/gguf.ts:218-257) and
+        rounded to f16 as the reference uploads it."""
+        s = self.s
+        L, D = s.n_layers, s.ple_dim
+        blocks = self.ple["table"].download(np.uint8, L * 176, offset=int(token) * L * 176)
+        row = O.dequant_q5k(blocks).astype(np.float16).view(np.uint16)
+        return O.ple_project(x0, self.ple["model_proj"], self.ple["proj_norm"], row, L, D, s.eps)
+
+    def step(self, hidden, kcs, vcs, pos, gelu=O.gelu_mul, row_toward_zero=False, token=0):
         """Decode position `pos`: kcs/vcs are this sequence's dense f16 caches
         (one per layer, >= pos + 1 rows; a consumer layer's entry is not
         used), updated in place. Returns the new hidden state and the
         softcapped logits (None without an LM head). `row_toward_zero`
         stores the new K/V rows rounded toward zero instead of to nearest (a
         one-ulp change of the f16 cache, to measure how much the step depends
-        on the cache's resolution)."""
+        on the cache's resolution). `token` picks the per-layer-embedding
+        table row."""
         s, x = self.s, hidden.copy()
+        pin = self.ple_inputs(x, token) if self.ple is not None else None
         for il, W in enumerate(self.layers):
             glob = s.is_global(il)
             theta = s.theta_global if glob else s.theta_local
@@ -95,6 +116,10 @@ class HostModel:
             u = O.matmul(n2, W["wup"], I, s.hidden, qt["wup"])
             dn = O.matmul(gelu(g, u), W["wdown"], s.hidden, I, qt["wdown"])
             x = O.fused_norm_add(dn, W["post_ffn_norm"], h, s.eps)
+            if pin is not None:  # PLE stage 2 (src/engine.ts:1608-1616)
+                D = s.ple_dim
+                x = O.ple_layer_tail(x, W["ple_gate"], W["ple_proj"], W["ple_post_norm"], W["ple_scale"][0],
+                                     pin[il * D:(il + 1) * D], s.eps)
         if self.lm_head is None:
             return x, None
         n = O.rms_norm(x, self.final_norm, s.eps)

@@ -2,10 +2,13 @@
 // GPU run of HipBackend through the N-API addon (driven by
 // tests/test_gpu_napi.py, which writes the model and checks the outputs
 // against the oracle): usage `node napi_forward.js <dir>`.
-//   <dir>/config.json  {overrides (e2bConfig), maxSeqLen, position, token}
+//   <dir>/config.json  {overrides (e2bConfig), maxSeqLen, position, token,
+//                       formats (per layer: {matrix: 'q4k' | 'q6k'})}
 //   <dir>/<name>.bin   raw tensor bytes: L<il>.<tensor> per layer, kv<il>.k /
 //                      kv<il>.v (initial f16 caches of the producer layers),
-//                      tokenEmbed, lmHead, finalNorm, rope_freqs
+//                      tokenEmbed, lmHead, finalNorm, rope_freqs, and with
+//                      per-layer embeddings perLayerModelProj,
+//                      perLayerProjNorm, perLayerTable
 // Three greedy forwards: (1) token and position as arguments; (2) the token
 // the first one sampled, read on the device; (3) as (2) with the position
 // read on the device, captured once as a graph and replayed. Writes
@@ -31,9 +34,10 @@ function upload(name) {
 
 be.allocate();
 for (let il = 0; il < C.num_layers; il++) {
+  const f = (cfg.formats || [])[il] || {};
   const t = {};
-  for (const n of Object.keys(be.layerTensorBytes(il))) t[n] = upload('L' + il + '.' + n);
-  be.setLayerWeights(il, t);
+  for (const n of Object.keys(be.layerTensorBytes(il, f))) t[n] = upload('L' + il + '.' + n);
+  be.setLayerWeights(il, t, f);
   if (hb.isKvProducer(C, il)) {
     const k = fs.readFileSync(path.join(dir, 'kv' + il + '.k.bin'));
     const v = fs.readFileSync(path.join(dir, 'kv' + il + '.v.bin'));
@@ -41,8 +45,12 @@ for (let il = 0; il < C.num_layers; il++) {
     be.g.upload(be.ctx, be.kvCaches[il].v, v, 0);
   }
 }
-be.setGlobals({ tokenEmbed: upload('tokenEmbed'), lmHead: upload('lmHead'), finalNorm: upload('finalNorm'),
-  rope_freqs: upload('rope_freqs') });
+const globals = { tokenEmbed: upload('tokenEmbed'), lmHead: upload('lmHead'), finalNorm: upload('finalNorm'),
+  rope_freqs: upload('rope_freqs') };
+if (C.per_layer_input_dim > 0) {
+  for (const n of ['perLayerModelProj', 'perLayerProjNorm', 'perLayerTable']) globals[n] = upload(n);
+}
+be.setGlobals(globals);
 
 const H = C.hidden_size;
 const V = C.vocab_size;

@@ -20,7 +20,7 @@ const KEYS = ['version', 'lastError', 'init', 'destroy', 'deviceInfo', 'alloc', 
   'download', 'sync', 'graphBegin', 'graphEnd', 'graphLaunch', 'graphDestroy', 'fill', 'matmulQuant',
   'matmulQuantMR4', 'kvCacheStore', 'attnScore', 'softmax', 'attnOutput', 'attnDecodeWorkspaceSize', 'attnDecode',
   'perHeadRmsNormNoWeight', 'fusedPerHeadNormRope', 'rmsNorm', 'fusedNormAdd', 'geluMul', 'logitSoftcap',
-  'embeddingLookup', 'argmax', 'topk256', 'advancePosition'];
+  'embeddingLookup', 'argmax', 'topk256', 'advancePosition', 'pleStage1Fuse', 'pleGeluMul', 'pleSkipScaleAdd'];
 
 const addon = hb.loadAddon();
 
@@ -88,8 +88,8 @@ function mockAddon() {
   return m;
 }
 
-// The reference's passes for one layer (src/engine.ts:1544-1613, the
-// matmulQuantMR4 gate/up branch).
+// The reference's passes for one layer (src/engine.ts:1544-1616, the
+// matmulQuantMR4 gate/up branch, PLE stage 2 at the end).
 function layerPasses(producer) {
   const p = [['attn.rmsNorm', 'rmsNorm']];
   if (producer) {
@@ -103,8 +103,12 @@ function layerPasses(producer) {
   return p.concat([['attn.attnScore', 'attnScore'], ['attn.softmax', 'softmax'], ['attn.attnOutput', 'attnOutput'],
     ['attn.linearOut', 'matmulQuant'], ['attn.postNormAdd', 'fusedNormAdd'], ['ffn.rmsNorm', 'rmsNorm'],
     ['ffn.linearGateUp', 'matmulQuantMR4'], ['ffn.linearGateUp', 'matmulQuantMR4'], ['ffn.geluMul', 'geluMul'],
-    ['ffn.linearDown', 'matmulQuant'], ['ffn.postNormAdd', 'fusedNormAdd']]);
+    ['ffn.linearDown', 'matmulQuant'], ['ffn.postNormAdd', 'fusedNormAdd'],
+    ['ple2.linearInpGate', 'matmulQuant'], ['ple2.geluMul', 'pleGeluMul'], ['ple2.linearPostProj', 'matmulQuant'],
+    ['ple2.rmsNorm', 'rmsNorm'], ['ple2.skipScaleAdd', 'pleSkipScaleAdd']]);
 }
+
+const PLE_GLOBALS = { perLayerModelProj: 'pmp', perLayerProjNorm: 'ppn', perLayerTable: 'plt' };
 
 check('HipBackend replays the reference pass order with per-layer shapes', () => {
   const C = hb.e2bConfig();
@@ -118,12 +122,15 @@ check('HipBackend replays the reference pass order with per-layer shapes', () =>
     return t;
   };
   for (let il = 0; il < 35; il++) be.setLayerWeights(il, tensors(il));
-  be.setGlobals({ tokenEmbed: 'emb', lmHead: 'head', finalNorm: 'fnorm', rope_freqs: 'rf' });
+  assert.throws(() => be.setGlobals({ tokenEmbed: 'emb', lmHead: 'head', finalNorm: 'fnorm', rope_freqs: 'rf' }),
+    /perLayerModelProj/);
+  be.setGlobals(Object.assign({ tokenEmbed: 'emb', lmHead: 'head', finalNorm: 'fnorm', rope_freqs: 'rf' },
+    PLE_GLOBALS));
   m.calls.length = 0;
   const pos = 700;
   be.encodeTransformerPass(42, pos, false);
   be.sampleNextToken(true, false);
-  let want = [['embed', 'embeddingLookup']];
+  let want = [['embed', 'embeddingLookup'], ['ple1.pmProj', 'matmulQuant'], ['ple1.stage1Fuse', 'pleStage1Fuse']];
   for (let il = 0; il < 35; il++) want = want.concat(layerPasses(il < 15));
   want = want.concat([['final.rmsNorm', 'rmsNorm'], ['lmHead', 'matmulQuant'], ['logitSoftcap', 'logitSoftcap'],
     ['sample.argmax', 'argmax']]);
@@ -131,9 +138,13 @@ check('HipBackend replays the reference pass order with per-layer shapes', () =>
   assert.deepStrictEqual(m.calls.map((c) => c[0]), want.map((w) => w[1]));
 
   // per-layer shapes and bindings of the calls
-  let at = 1;
+  let at = 3;
   const W = be.workBuffers;
   assert.deepStrictEqual(m.calls[0].slice(1, 6), ['ctx', 'emb', 262144, W.hidden, { hidden_size: 1536, token_id: 42 }]);
+  assert.deepStrictEqual(m.calls[1].slice(1, 7), ['ctx', W.hidden, 'pmp', W.plePmProjected, { M: 35 * 256, N: 1536 },
+    'f16']);
+  assert.deepStrictEqual(m.calls[2].slice(1, 9), ['ctx', W.plePmProjected, 'ppn', 'plt', 262144, W.pleInputs,
+    { num_layers: 35, per_layer_dim: 256, eps: 1e-6, token_id: 42 }, null]);
   for (let il = 0; il < 35; il++) {
     const n = layerPasses(il < 15).length;
     const calls = m.calls.slice(at, at + n);
@@ -153,8 +164,17 @@ check('HipBackend replays the reference pass order with per-layer shapes', () =>
       sliding_window: glob ? 0 : 512 });
     assert.strictEqual(by('attnOutput')[0][3], be.kvCaches[src].v);
     assert.deepStrictEqual(by('matmulQuantMR4')[0][5], { M: I, N: 1536 });
-    assert.deepStrictEqual(by('matmulQuant').slice(-1)[0].slice(3, 7),
+    assert.deepStrictEqual(by('matmulQuant').filter((c) => c[3] === 'L' + il + '.ffn_down')[0].slice(3, 7),
       ['L' + il + '.ffn_down', W.ffnDown, { M: 1536, N: I }, 'q6k']);
+    const mqs = by('matmulQuant');
+    assert.deepStrictEqual(mqs[mqs.length - 2].slice(2, 7), [W.hidden, 'L' + il + '.inp_gate', W.pleGate,
+      { M: 256, N: 1536 }, 'f16']);
+    assert.deepStrictEqual(mqs[mqs.length - 1].slice(2, 7), [W.pleGated, 'L' + il + '.proj', W.pleProjOut,
+      { M: 1536, N: 256 }, 'f16']);
+    assert.deepStrictEqual(by('pleGeluMul')[0].slice(2, 6), [W.pleGate, W.pleInputs, W.pleGated,
+      { layer_offset: il * 256, size: 256 }]);
+    assert.deepStrictEqual(by('pleSkipScaleAdd')[0].slice(2, 6), [W.hidden, W.plePostNormed,
+      'L' + il + '.layer_output_scale', { size: 1536 }]);
     if (il < 15) {
       const st = by('kvCacheStore')[0];
       assert.deepStrictEqual(st.slice(4, 7), [be.kvCaches[il].k, be.kvCaches[il].v,
@@ -178,12 +198,15 @@ check('device-side token and position: the pass reads them, the sample advances 
     for (const n of Object.keys(be.layerTensorBytes(il))) t[n] = n;
     be.setLayerWeights(il, t);
   }
-  be.setGlobals({ tokenEmbed: 'emb', lmHead: 'head', finalNorm: 'fnorm', rope_freqs: 'rf' });
+  be.setGlobals(Object.assign({ tokenEmbed: 'emb', lmHead: 'head', finalNorm: 'fnorm', rope_freqs: 'rf' },
+    PLE_GLOBALS));
   m.calls.length = 0;
   be.encodeTransformerPass(null, 0, true);
   be.sampleNextToken(true, true);
   const W = be.workBuffers;
   assert.strictEqual(m.calls[0][6], W.argmaxResult);            // embedding of the sampled token
+  assert.strictEqual(m.calls[2][0], 'pleStage1Fuse');
+  assert.strictEqual(m.calls[2][8], W.argmaxResult);            // and its per-layer-embedding row
   for (const c of m.calls.filter((x) => ['attnScore', 'attnOutput'].indexOf(x[0]) >= 0)) {
     assert.strictEqual(c[6], W.position);
     assert.strictEqual(c[5].seq_len, 1024);                      // the bound, the device value is read
@@ -192,6 +215,41 @@ check('device-side token and position: the pass reads them, the sample advances 
   const last = m.calls[m.calls.length - 1];
   assert.deepStrictEqual(last, ['advancePosition', 'ctx', W.position, 1]);
   assert.throws(() => be.setLayerWeights(0, {}), /missing tensor/);
+});
+
+check('per-tensor block formats: sizes, wtypes, the LM head and the 4-row gate/up only for Q4_K', () => {
+  const C = hb.e2bConfig({ num_layers: 2, num_unshared_layers: 2, global_layers: [1], vocab_size: 4096,
+    per_layer_input_dim: 0 });
+  const m = mockAddon();
+  const be = new hb.HipBackend(m, 'ctx', C, { maxSeqLen: 1024 });
+  be.allocate();
+  const F = { attn_v: 'q6k', ffn_down: 'q4k' };
+  const sizes = be.layerTensorBytes(0, F);
+  assert.strictEqual(sizes.attn_v, 256 * 1536 / 256 * 210);
+  assert.strictEqual(sizes.ffn_down, 1536 * 6144 / 256 * 144);
+  assert.strictEqual(sizes.inp_gate, undefined);
+  const t = (il, f) => {
+    const o = {};
+    for (const n of Object.keys(be.layerTensorBytes(il, f))) o[n] = n + il;
+    return o;
+  };
+  be.setLayerWeights(0, t(0, F), F);
+  be.setLayerWeights(1, t(1, { ffn_gate: 'q6k' }), { ffn_gate: 'q6k' });
+  assert.throws(() => be.setLayerWeights(1, t(1), { attn_q: 'q5k' }), /format/);
+  be.setGlobals({ tokenEmbed: 'emb', lmHead: 'head', finalNorm: 'fnorm', rope_freqs: 'rf', lmHeadFormat: 'q4k' });
+  m.calls.length = 0;
+  be.forward(7, 3);
+  const mq = m.calls.filter((c) => c[0] === 'matmulQuant' || c[0] === 'matmulQuantMR4');
+  const fmt = (name) => mq.filter((c) => c[3] === name)[0];
+  assert.strictEqual(fmt('attn_v0')[6], 'q6k');
+  assert.strictEqual(fmt('attn_k0')[6], 'q4k');
+  assert.strictEqual(fmt('ffn_down0')[6], 'q4k');
+  assert.strictEqual(fmt('ffn_down1')[6], 'q6k');
+  assert.strictEqual(fmt('ffn_gate0')[0], 'matmulQuantMR4');
+  assert.strictEqual(fmt('ffn_gate1')[0], 'matmulQuant');
+  assert.strictEqual(fmt('ffn_gate1')[6], 'q6k');
+  assert.strictEqual(fmt('head')[6], 'q4k');
+  assert.strictEqual(m.calls.filter((c) => /^ple/.test(c[0])).length, 0);
 });
 
 console.log('all node CPU checks passed');

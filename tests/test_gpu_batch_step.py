@@ -209,6 +209,7 @@ def _step_vs_oracle(ctx, d, LENS):
     s, B = d.s, d.B
     hm = HostModel(d)
     hidden0 = d.hidden.download(np.float32).reshape(B, s.hidden)
+    tokens0 = d.tokens.download(np.uint32)  # (the per-layer-embedding rows)
     pools0 = _pools(d)
     lens0 = d.lens_host.copy()
 
@@ -225,15 +226,16 @@ def _step_vs_oracle(ctx, d, LENS):
         # (a layer reading a producer's pool has that pool here; the oracle reads the producer's entry)
         kcs = [_dense(d, k, b, L, kvs[il]) for il, (k, _) in enumerate(pools0)]
         vcs = [_dense(d, v, b, L, kvs[il]) for il, (_, v) in enumerate(pools0)]
-        x, logits = hm.step(hidden0[b], kcs, vcs, L)
+        x, logits = hm.step(hidden0[b], kcs, vcs, L, token=int(tokens0[b]))
         refs.append((x, logits, kcs, vcs))
         # the step's own dependence on the f16 cache's resolution: the oracle
         # against itself with its new K/V rows one ulp off (rounded toward
         # zero), and on the last bits of the GELU (the shader's all-f32 form)
         kz = [_dense(d, k, b, L, kvs[il]) for il, (k, _) in enumerate(pools0)]
         vz = [_dense(d, v, b, L, kvs[il]) for il, (_, v) in enumerate(pools0)]
-        xz, lgz = hm.step(hidden0[b], kz, vz, L, row_toward_zero=True)
-        x32, lg32 = hm.step(hidden0[b], [k.copy() for k in kcs], [v.copy() for v in vcs], L, gelu=gelu_mul_f32)
+        xz, lgz = hm.step(hidden0[b], kz, vz, L, row_toward_zero=True, token=int(tokens0[b]))
+        x32, lg32 = hm.step(hidden0[b], [k.copy() for k in kcs], [v.copy() for v in vcs], L, gelu=gelu_mul_f32,
+                            token=int(tokens0[b]))
         tol.append(max(STEP_REL, O.rel_l2(xz, x), O.rel_l2(lgz, logits),
                        GELU_MARGIN * O.rel_l2(x32, x), GELU_MARGIN * O.rel_l2(lg32, logits)))
     rh = [O.rel_l2(H[b], r[0]) for b, r in enumerate(refs)]

@@ -110,6 +110,15 @@ def test_dequant_f16(ctx, wtype):
 N_LAYERS, N_UNSHARED, GLOBALS, VOCAB = 4, 2, (1, 3), 4096
 
 
+def _q5k_blocks(seed: int, n: int) -> np.ndarray:
+    """Q5_K blocks: f16 d ~ |N(0, 2e-3)|, dmin ~ |N(0, 1e-3)|, the other bytes uniform."""
+    rng = np.random.default_rng(seed)
+    b = rng.integers(0, 256, (n, 176), dtype=np.uint8)
+    b[:, 0:2] = np.abs(rng.standard_normal(n) * 2e-3).astype(np.float16).view(np.uint8).reshape(n, 2)
+    b[:, 2:4] = np.abs(rng.standard_normal(n) * 1e-3).astype(np.float16).view(np.uint8).reshape(n, 2)
+    return b.reshape(-1)
+
+
 def _shape() -> E2BShape:
     return E2BShape.real(n_layers=N_LAYERS, n_unshared=N_UNSHARED, global_layers=GLOBALS, vocab=VOCAB)
 
@@ -142,6 +151,10 @@ def _model_file(path: str) -> str:
         seed[0] += 1
         w.tensor(name, (n,), T_F32, O.gen_normal_f32(seed[0], n, mean, std))
 
+    def f32mat(name, M, N):
+        seed[0] += 1
+        w.tensor(name, (N, M), T_F32, O.gen_normal_f32(seed[0], M * N, 0.0, 0.03))
+
     for il in range(N_LAYERS):
         H, Q, KV, I, hd = s.hidden, s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il), s.hd(il)
         p = f"blk.{il}."
@@ -160,6 +173,20 @@ def _model_file(path: str) -> str:
         mat(p + "ffn_down.weight", H, I, qt(il, "wdown"))
         vec(p + "post_ffw_norm.weight", H)
     vec("output_norm.weight", s.hidden)
+    # per-layer embeddings as the real file holds them: a BF16 projection,
+    # an F32 norm, the Q5_K table and F32 per-layer matrices
+    L, D = N_LAYERS, s.ple_dim
+    seed[0] += 1
+    pm = (O.gen_normal_f32(seed[0], L * D * s.hidden, 0.0, 0.03).view(np.uint32) >> 16).astype(np.uint16)
+    w.tensor("per_layer_model_proj.weight", (s.hidden, L * D), T_BF16, pm)
+    vec("per_layer_proj_norm.weight", D)
+    seed[0] += 1
+    w.tensor("per_layer_token_embd.weight", (L * D, VOCAB), T_Q5_K, _q5k_blocks(seed[0], VOCAB * L))
+    for il in range(N_LAYERS):
+        f32mat(f"blk.{il}.inp_gate.weight", D, s.hidden)
+        f32mat(f"blk.{il}.proj.weight", s.hidden, D)
+        vec(f"blk.{il}.post_norm.weight", s.hidden)
+        vec(f"blk.{il}.layer_output_scale.weight", 1, 0.8, 0.1)
     # the tied table (the LM head's blocks, the lookup's f16 rows)
     seed[0] += 1
     te = O.gen_q6k(seed[0], VOCAB * s.hidden // 256)
@@ -201,6 +228,18 @@ def test_decoder_holds_the_file(ctx, model_path):
     assert np.array_equal(_nan_canon(emb), _np_f16_bits(O.dequant_q6k(te)))
     rf = d.rope_freqs.download(np.uint16).view(np.float16)
     assert np.all(rf[:64] == 1.0) and np.all(np.isinf(rf[64:]))
+    # per-layer embeddings: BF16 / F32 tensors as f16, the Q5_K table as is
+    assert s.ple_dim == 256
+    pm = g.data("per_layer_model_proj.weight").view(np.uint16)
+    want = _np_f16_bits((pm.astype(np.uint32) << 16).view(np.float32))
+    assert np.array_equal(_nan_canon(d.ple_model_proj.download(np.uint16)), want)
+    assert np.array_equal(d.ple_table.download(np.uint8), g.data("per_layer_token_embd.weight"))
+    for il, L in enumerate(d.layers):
+        for nm, fn in (("ple_gate", "inp_gate"), ("ple_proj", "proj"), ("ple_post_norm", "post_norm")):
+            want = g.data(f"blk.{il}.{fn}.weight").view(np.float32).astype(np.float16).view(np.uint16)
+            assert np.array_equal(getattr(L, nm).download(np.uint16), want), (il, nm)
+        sc = g.data(f"blk.{il}.layer_output_scale.weight").view(np.float32).astype(np.float16).view(np.uint16)
+        assert L.ple_scale.download(np.uint16)[0] == sc[0]
     del d
 
 
@@ -216,16 +255,17 @@ def test_file_model_fused_step_with_token_feedback(ctx, model_path):
     kcs = [L.k_cache.download(np.uint16) for L in d.layers]
     vcs = [L.v_cache.download(np.uint16) for L in d.layers]
     # 5 per layer, + a merge launch on the two head-dim-512 layers, + the
-    # second q/k/v launch of layer 1 (Q6_K v), + embedding, head, argmax
+    # second q/k/v launch of layer 1 (Q6_K v), + embedding, head, argmax,
+    # + per-layer embeddings: stage 1 (2), 2 per layer, the last tail (1)
     assert d.layers[1].qt["wv"] == "q6k" and d.layers[1].qt["wq"] == "q4k"
-    assert d.launches_per_step_fused() == 5 * N_LAYERS + 2 + 1 + 3
+    assert d.launches_per_step_fused() == 5 * N_LAYERS + 2 + 1 + 3 + 3 + 2 * N_LAYERS
     g = d.capture_fused()
     try:
         tok = T0
         for i in range(2):
             ctx.graph_launch(g)
             ctx.sync()
-            x_ref, lg_ref = hm.step(hm.embed(tok), kcs, vcs, POS + i)
+            x_ref, lg_ref = hm.step(hm.embed(tok), kcs, vcs, POS + i, token=tok)
             lg = d.logits.download(np.float32)
             print(f"[gguf model] replay {i}: token {tok}, hidden rel-L2 "
                   f"{O.rel_l2(d.hidden.download(np.float32), x_ref):.2e}, logits {O.rel_l2(lg, lg_ref):.2e}",

@@ -2,7 +2,8 @@
 hip_backend.js) dispatching the reference's per-key pass order through the
 N-API addon, on a four-layer model with Gemma-4-E2B's layer kinds (layer 0
 local and 1 global own their caches; 2 local reads 0's, 3 global reads 1's;
-head dims 256 / 512, FFN 6144 / 12288) and a 4096-token vocabulary.
+head dims 256 / 512, FFN 6144 / 12288, per-layer embeddings) and a
+4096-token vocabulary, its matrices in a Q4_K_M-style mix of Q4_K and Q6_K.
 
 The model is written here from the oracle's seeded generators; the Node
 program (tests/node/napi_forward.js) uploads it and runs three greedy
@@ -23,7 +24,7 @@ import pytest
 
 import oracle as O
 from decode_oracle import HostModel
-from g4hip.decoder import E2BShape
+from g4hip.decoder import DEFAULT_TYPES, E2BShape, q4km_types
 from gpu_util import assert_close
 
 pytestmark = pytest.mark.gpu
@@ -63,18 +64,36 @@ def _model(shape):
     def f16(n, mean=1.0, std=0.1):
         return O.gen_normal_f16(nxt(), n, mean, std)
 
-    layers = []
+    fmt_of = q4km_types(s)
+    names = dict(wq="attn_q", wk="attn_k", wv="attn_v", wo="attn_output", wgate="ffn_gate", wup="ffn_up",
+                 wdown="ffn_down")
+    layers, formats = [], []
+    D = s.ple_dim
     for il in range(s.n_layers):
         hd, Q, KV, I, H = s.hd(il), s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il), s.hidden
         prod = s.is_producer(il)
-        t = {"attn_norm": f16(H), "attn_q": q4(Q, H), "attn_k": q4(KV, H) if prod else None,
-             "attn_v": q4(KV, H) if prod else None, "attn_q_norm": f16(hd), "attn_k_norm": f16(hd) if prod else None,
-             "attn_output": q4(H, Q), "post_attention_norm": f16(H), "ffn_norm": f16(H), "ffn_gate": q4(I, H),
-             "ffn_up": q4(I, H), "ffn_down": q6(H, I), "post_ffw_norm": f16(H)}
+        qt = {nm: fmt_of(il, nm) for nm in names}
+
+        def mat(nm, M, N):
+            return q4(M, N) if qt[nm] == "q4k" else q6(M, N)
+
+        t = {"attn_norm": f16(H), "attn_q": mat("wq", Q, H), "attn_k": mat("wk", KV, H) if prod else None,
+             "attn_v": mat("wv", KV, H) if prod else None, "attn_q_norm": f16(hd),
+             "attn_k_norm": f16(hd) if prod else None, "attn_output": mat("wo", H, Q), "post_attention_norm": f16(H),
+             "ffn_norm": f16(H), "ffn_gate": mat("wgate", I, H), "ffn_up": mat("wup", I, H),
+             "ffn_down": mat("wdown", H, I), "post_ffw_norm": f16(H)}
+        if D:
+            t.update({"inp_gate": f16(D * H, 0.0, 0.03), "proj": f16(H * D, 0.0, 0.03), "post_norm": f16(H),
+                      "layer_output_scale": f16(2, 0.8, 0.1)})
         for k, v in t.items():
             if v is not None:
                 files[f"L{il}.{k}"] = v
-        layers.append(SimpleNamespace(
+        formats.append({names[nm]: f for nm, f in qt.items() if f != DEFAULT_TYPES[nm]})
+        ple = {}
+        if D:
+            ple = dict(ple_gate=_Host(t["inp_gate"]), ple_proj=_Host(t["proj"]), ple_post_norm=_Host(t["post_norm"]),
+                       ple_scale=_Host(t["layer_output_scale"]))
+        layers.append(SimpleNamespace(qt=qt, **ple,
             wq=_Host(t["attn_q"]), wk=_Host(t["attn_k"]) if prod else None, wv=_Host(t["attn_v"]) if prod else None,
             wo=_Host(t["attn_output"]), wgate=_Host(t["ffn_gate"]), wup=_Host(t["ffn_up"]),
             wdown=_Host(t["ffn_down"]), attn_norm=_Host(t["attn_norm"]),
@@ -87,6 +106,17 @@ def _model(shape):
     half = s.head_dim_global // 2
     table = np.where(np.arange(half) < half // 4, 1.0, np.inf).astype(np.float16).view(np.uint16)
     files.update({"finalNorm": final_norm, "lmHead": lm_head, "tokenEmbed": emb, "rope_freqs": table})
+    ple_globals = {}
+    if D:
+        pmp, ppn = f16(s.n_layers * D * s.hidden, 0.0, 0.03), f16(D)
+        rng = np.random.default_rng(nxt())
+        tbl = rng.integers(0, 256, (s.vocab * s.n_layers, 176), dtype=np.uint8)
+        n = tbl.shape[0]
+        tbl[:, 0:2] = np.abs(rng.standard_normal(n) * 2e-3).astype(np.float16).view(np.uint8).reshape(n, 2)
+        tbl[:, 2:4] = np.abs(rng.standard_normal(n) * 1e-3).astype(np.float16).view(np.uint8).reshape(n, 2)
+        tbl = tbl.reshape(-1)
+        files.update({"perLayerModelProj": pmp, "perLayerProjNorm": ppn, "perLayerTable": tbl})
+        ple_globals = dict(ple_model_proj=_Host(pmp), ple_proj_norm=_Host(ppn), ple_table=_Host(tbl))
     kcs, vcs = [], []
     for il in range(s.n_layers):
         n = MAX_SEQ * s.kv_dim_of(il)
@@ -98,8 +128,8 @@ def _model(shape):
         kcs.append(k.copy())
         vcs.append(v.copy())
     dec = SimpleNamespace(s=s, rope_freqs=_Host(table), layers=layers, final_norm=_Host(final_norm),
-                          lm_head=_Host(lm_head), embedding=_Host(emb))
-    return files, HostModel(dec), kcs, vcs
+                          lm_head=_Host(lm_head), embedding=_Host(emb), **ple_globals)
+    return files, formats, HostModel(dec), kcs, vcs
 
 
 @pytest.mark.skipif(shutil.which("node") is None, reason="no node binary")
@@ -107,9 +137,10 @@ def test_node_backend_forwards_vs_oracle():
     addon = os.path.join(ROOT, "gemma4-webgpu_amd", "node", "g4hip.node")
     assert os.path.exists(addon), "g4hip.node is not built"
     shape = E2BShape.real(n_layers=4, n_unshared=2, global_layers=(1, 3), vocab=4096)
-    files, hm, kcs, vcs = _model(shape)
+    files, formats, hm, kcs, vcs = _model(shape)
+    assert any(formats), "the model mixes block formats"
     cfg = {"overrides": {"num_layers": 4, "num_unshared_layers": 2, "global_layers": [1, 3], "vocab_size": 4096},
-           "maxSeqLen": MAX_SEQ, "position": POS, "token": TOKEN}
+           "maxSeqLen": MAX_SEQ, "position": POS, "token": TOKEN, "formats": formats}
     with tempfile.TemporaryDirectory() as d:
         for name, arr in files.items():
             np.ascontiguousarray(arr).tofile(os.path.join(d, name + ".bin"))
@@ -130,7 +161,7 @@ def test_node_backend_forwards_vs_oracle():
         hidden = blk[:4 * H].view(np.float32)
         logits = blk[4 * H:4 * H + 4 * V].view(np.float32)
         got_tok = int(blk[4 * H + 4 * V:].view(np.uint32)[0])
-        x_ref, lg_ref = hm.step(hm.embed(tok), kcs, vcs, POS + i)
+        x_ref, lg_ref = hm.step(hm.embed(tok), kcs, vcs, POS + i, token=tok)
         print(f"[napi] forward {i + 1}: token in {tok}, hidden rel-L2 {O.rel_l2(hidden, x_ref):.2e}, "
               f"logits rel-L2 {O.rel_l2(logits, lg_ref):.2e}, sampled {got_tok}", flush=True)
         assert_close(hidden, x_ref, what=f"hidden forward {i + 1}")

@@ -58,7 +58,7 @@ def test_prefill_matches_sequential_forwards(ctx, kind, start):
     tok = int(d.tokens.download(np.uint32)[last])
     x = lg = None
     for t in range(T):
-        x, lg = hm.step(hm.embed(int(toks[t])), kcs, vcs, start + t)
+        x, lg = hm.step(hm.embed(int(toks[t])), kcs, vcs, start + t, token=int(toks[t]))
     print(f"[prefill] {kind} start {start}: last hidden rel-L2 {O.rel_l2(H, x):.2e}, logits {O.rel_l2(LG, lg):.2e}",
           flush=True)
     assert_close(H, x, what="last token hidden")

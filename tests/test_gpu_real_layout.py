@@ -46,14 +46,17 @@ def rdec(ctx):
 
 def _snapshot(d):
     return (d.hidden.download(np.float32), [L.k_cache.download(np.uint16) for L in d.layers],
-            [L.v_cache.download(np.uint16) for L in d.layers])
+            [L.v_cache.download(np.uint16) for L in d.layers], d.token.download(np.uint32))
 
 
 def _restore(d, snap):
+    """hidden state, caches and the device token (the per-layer-embedding row
+    a step reads; the previous step's sample overwrote it)."""
     d.hidden.upload(snap[0])
     for L, k, v in zip(d.layers, snap[1], snap[2]):
         L.k_cache.upload(k)
         L.v_cache.upload(v)
+    d.token.upload(snap[3])
 
 
 @pytest.mark.parametrize("layer", [2, 1])  # head dim 256 (one launch), 512 (launch + merge)
@@ -148,7 +151,7 @@ def test_embedding_token_feedback_graph(ctx):
         for i in range(2):
             ctx.graph_launch(g)
             ctx.sync()
-            x_ref, lg_ref = hm.step(hm.embed(tok), kcs, vcs, POS + i)
+            x_ref, lg_ref = hm.step(hm.embed(tok), kcs, vcs, POS + i, token=tok)
             lg = d.logits.download(np.float32)
             print(f"[embed feedback] replay {i}: token in {tok}, hidden rel-L2 "
                   f"{O.rel_l2(d.hidden.download(np.float32), x_ref):.2e}", flush=True)

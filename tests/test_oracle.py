@@ -685,3 +685,179 @@ def test_node_q4k_dot_matches_oracle(tmp_path):
     y = np.fromfile(fout, np.float32)
     want = O.matmul(x, W, M, K, "q4k")
     assert O.rel_l2(y, want) < 1e-6
+
+
+# ---- Q5_K and per-layer embeddings ----------------------------------------------
+
+def _q5k_from_q4k(q4: np.ndarray, qh: np.ndarray) -> np.ndarray:
+    """The Q5_K block with a Q4_K block's d, dmin, scales and nibbles and the
+    given high-bit bytes (layout: d, dmin, 12 scale bytes, qh[32], qs[128])."""
+    q4 = q4.reshape(-1, 144)
+    out = np.empty((q4.shape[0], 176), np.uint8)
+    out[:, :16] = q4[:, :16]
+    out[:, 16:48] = qh.reshape(-1, 32)
+    out[:, 48:] = q4[:, 16:]
+    return out.reshape(-1)
+
+
+def test_q5k_without_high_bits_is_q4k():
+    """qh = 0: the values are those of the Q4_K block with the same scales and
+    nibbles (the Q4_K oracle is pinned above against hand-computed blocks and
+    the reference's packing)."""
+    q4 = O.gen_q4k(77, 64)
+    q5 = _q5k_from_q4k(q4, np.zeros(64 * 32, np.uint8))
+    assert np.array_equal(O.dequant_q5k(q5).view(np.uint32), O.dequant_q4k(q4).view(np.uint32))
+
+
+def test_q5k_high_bit_positions():
+    """ggml's Q5_K layout (the one src/gguf.ts:235-255 reads): bit 2g of qh[l]
+    adds 16 to value 64g + l, bit 2g + 1 to value 64g + 32 + l. With d = 1,
+    every scale 1 and every min 0, a single set bit yields a single 16."""
+    blk = np.zeros(176, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[4:8] = 1          # sc(0..3) = 1, m(0..3) = 0
+    blk[12:16] = 1        # sc(4..7) = s[8..11] & 15 = 1, m(4..7) = s[8..11] >> 4 = 0
+    seen = set()
+    for l in range(32):
+        for bit in range(8):
+            b = blk.copy()
+            b[16 + l] = 1 << bit
+            v = O.dequant_q5k(b)
+            nz = np.flatnonzero(v)
+            want = 64 * (bit // 2) + 32 * (bit % 2) + l
+            assert nz.tolist() == [want] and v[want] == 16.0, (l, bit)
+            seen.add(want)
+    assert seen == set(range(256))
+
+
+def test_q5k_f64_single_rounding():
+    """d*sc*q - dmin*m evaluated once in f64 and stored as f32 equals the
+    correctly rounded f32 of the exact rational value (fractions), on random
+    blocks with d and dmin over the whole f16 range."""
+    from fractions import Fraction
+    rng = np.random.default_rng(13)
+    blk = rng.integers(0, 256, (24, 176), dtype=np.uint8)
+    d = np.abs(rng.standard_normal(24) * 10.0 ** rng.integers(-6, 3, 24)).astype(np.float16)
+    dm = np.abs(rng.standard_normal(24) * 10.0 ** rng.integers(-6, 3, 24)).astype(np.float16)
+    blk[:, 0:2] = d.view(np.uint8).reshape(24, 2)
+    blk[:, 2:4] = dm.view(np.uint8).reshape(24, 2)
+    got = O.dequant_q5k(blk.reshape(-1)).reshape(24, 256)
+    for b in range(24):
+        s = bytes(blk[b, 4:16])
+        for t in range(0, 256, 7):
+            g, hi, l = t // 64, (t // 32) % 2, t % 32
+            j = 2 * g + hi
+            sc, m = O.q4k_scale_min(s, j)
+            q = (blk[b, 48 + 32 * g + l] >> (4 * hi)) & 15
+            q += 16 * ((blk[b, 16 + l] >> j) & 1)
+            exact = Fraction(float(d[b])) * sc * int(q) - Fraction(float(dm[b])) * m
+            assert got[b, t] == np.float32(float(exact)), (b, t)
+
+
+def _tiny_gemma4(eps):
+    import torch
+    from transformers.models.gemma4.configuration_gemma4 import Gemma4TextConfig
+    from transformers.models.gemma4.modeling_gemma4 import Gemma4TextDecoderLayer, Gemma4TextModel
+
+    cfg = Gemma4TextConfig(vocab_size=64, hidden_size=32, intermediate_size=64, num_hidden_layers=3,
+                           num_attention_heads=2, num_key_value_heads=1, head_dim=16, hidden_size_per_layer_input=16,
+                           vocab_size_per_layer_input=64, rms_norm_eps=eps)
+    torch.manual_seed(0)
+    return cfg, Gemma4TextModel(cfg).double(), Gemma4TextDecoderLayer(cfg, 0).double()
+
+
+def test_ple_stage1_against_transformers():
+    """Gemma4TextModel.get_per_layer_inputs + project_per_layer_inputs (the
+    token row x sqrt(D), the projection, its RMSNorm, the 1/sqrt(2) blend)
+    against the oracle's stage 1 on the same f16 weights. transformers also
+    scales the projection by 1/sqrt(H) before the norm, which the reference
+    does not: with eps = 0 the norm removes that factor."""
+    import torch
+    cfg, m, _ = _tiny_gemma4(0.0)
+    L, D, H, V = 3, 16, 32, 64
+    rng = np.random.default_rng(14)
+    proj16 = (rng.standard_normal((L * D, H)) * 0.2).astype(np.float16)
+    norm16 = (rng.standard_normal(D) * 0.1 + 1).astype(np.float16)
+    table16 = (rng.standard_normal((V, L * D)) * 0.5).astype(np.float16)
+    x0 = rng.standard_normal(H).astype(np.float32)
+    tok = 37
+    with torch.no_grad():
+        m.per_layer_model_projection.weight.copy_(torch.from_numpy(proj16.astype(np.float64)))
+        m.per_layer_projection_norm.weight.copy_(torch.from_numpy(norm16.astype(np.float64)))
+        m.embed_tokens_per_layer.weight.copy_(torch.from_numpy(table16.astype(np.float64)))
+        ids = torch.tensor([[tok]])
+        pli = m.get_per_layer_inputs(ids, None)
+        want = m.project_per_layer_inputs(torch.from_numpy(x0.astype(np.float64))[None, None], pli)
+    want = want.numpy().reshape(-1)
+    got = O.ple_project(x0, proj16.view(np.uint16), norm16.view(np.uint16), table16[tok].view(np.uint16), L, D, 0.0)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6), np.abs(got - want).max()
+
+
+def test_ple_layer_tail_against_transformers():
+    """Gemma4TextDecoderLayer.forward with its attention and MLP returning
+    zeros (so the residual passes through both, as their norms of zero are
+    zero) runs transformers' per-layer-input tail on the input: gate, tanh
+    GELU, x per-layer input, projection, RMSNorm, residual add, x layer
+    scalar. The oracle's stage 2 must give the same on the same weights."""
+    import torch
+    cfg, _, lay = _tiny_gemma4(1e-6)
+
+    class Zero(torch.nn.Module):
+        def forward(self, hidden_states=None, *a, **k):
+            z = torch.zeros_like(hidden_states)
+            return (z, None) if k or a else z
+
+    lay.self_attn = Zero()
+    lay.mlp = Zero()
+    D, H = 16, 32
+    rng = np.random.default_rng(15)
+    gate16 = (rng.standard_normal((D, H)) * 0.3).astype(np.float16)
+    proj16 = (rng.standard_normal((H, D)) * 0.3).astype(np.float16)
+    post16 = (rng.standard_normal(H) * 0.1 + 1).astype(np.float16)
+    scale16 = np.float16(0.75)
+    x = rng.standard_normal(H).astype(np.float32) * 2
+    ple = rng.standard_normal(D).astype(np.float32)
+    with torch.no_grad():
+        lay.per_layer_input_gate.weight.copy_(torch.from_numpy(gate16.astype(np.float64)))
+        lay.per_layer_projection.weight.copy_(torch.from_numpy(proj16.astype(np.float64)))
+        lay.post_per_layer_input_norm.weight.copy_(torch.from_numpy(post16.astype(np.float64)))
+        lay.layer_scalar.copy_(torch.tensor([float(scale16)], dtype=torch.float64))
+        want = lay(torch.from_numpy(x.astype(np.float64))[None, None],
+                   per_layer_input=torch.from_numpy(ple.astype(np.float64))[None, None]).numpy().reshape(-1)
+    got = O.ple_layer_tail(x, gate16.view(np.uint16), proj16.view(np.uint16), post16.view(np.uint16),
+                           int(scale16.view(np.uint16)), ple, 1e-6)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6), np.abs(got - want).max()
+
+
+def test_ple_stage1_closed_forms():
+    """Per-layer slices: a layer's output depends on its own projection slice
+    and table slice only; projection zero leaves table * sqrt(D) / sqrt(2);
+    with eps 0 a constant slice c normalises to sign(c) * w."""
+    L, D = 4, 256
+    rng = np.random.default_rng(16)
+    w = (rng.standard_normal(D) * 0.1 + 1).astype(np.float16).view(np.uint16)
+    row = (rng.standard_normal(L * D) * 0.5).astype(np.float16)
+    out = O.ple_stage1(np.zeros(L * D, np.float32), w, row.view(np.uint16), L, D, 1e-6)
+    assert np.allclose(out, row.astype(np.float64) * 16 / np.sqrt(2), rtol=1e-6)
+    p = np.repeat(np.array([3.0, -0.5, 7.0, -2.0], np.float32), D)
+    out = O.ple_stage1(p, w, np.zeros(L * D, np.uint16), L, D, 0.0)
+    wf = w.view(np.float16).astype(np.float64)
+    for l, sgn in enumerate((1, -1, 1, -1)):
+        assert np.allclose(out[l * D:(l + 1) * D], sgn * wf / np.sqrt(2), rtol=1e-6)
+    perm = [2, 0, 3, 1]
+    pr = rng.standard_normal(L * D).astype(np.float32)
+    a = O.ple_stage1(pr, w, row.view(np.uint16), L, D, 1e-6).reshape(L, D)
+    b = O.ple_stage1(pr.reshape(L, D)[perm].reshape(-1), w, row.reshape(L, D)[perm].reshape(-1).view(np.uint16), L,
+                     D, 1e-6).reshape(L, D)
+    assert np.array_equal(a[perm], b)
+
+
+def test_ple_gelu_mul_and_skip_scale_add():
+    rng = np.random.default_rng(17)
+    g = rng.standard_normal(256).astype(np.float32)
+    ple = rng.standard_normal(3 * 256).astype(np.float32)
+    assert np.array_equal(O.ple_gelu_mul(g, ple, 256), O.gelu_mul(g, ple[256:512]))
+    h, n = rng.standard_normal(64).astype(np.float32), rng.standard_normal(64).astype(np.float32)
+    assert np.array_equal(O.ple_skip_scale_add(h, n, f16(1.0)), (h.astype(np.float64) + n).astype(np.float32))
+    assert np.array_equal(O.ple_skip_scale_add(h, n, f16(2.0)), (2 * (h.astype(np.float64) + n)).astype(np.float32))
+    assert not np.any(O.ple_skip_scale_add(h, n, f16(0.0)))
