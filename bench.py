@@ -455,7 +455,7 @@ def decode_rate(ctx, shape, start, steps, warmup, embed=False, warm=True):
     end = int(d.pos.download(np.uint32)[0])
     ctx.graph_destroy(g)
     s = d.s
-    wbytes = s.weight_bytes() + s.lm_head_bytes()
+    wbytes = s.weight_bytes() + s.lm_head_bytes() + s.ple_bytes()
     res = {"tok_s": round(1000.0 / ms, 1), "us_per_token": round(ms * 1e3, 2), "positions": [start, end],
            "weight_bytes_per_token": wbytes, "launches_per_token": d.launches_per_step_fused(),
            "setup_s": round(time.time() - t0, 1)}
@@ -769,6 +769,10 @@ def main():
             real[f"start{start}"] = decode_rate(ctx, E2BShape.real(), start, args.pos_steps, args.pos_warmup,
                                                 embed=True)
             log(f"real E2B layout from position {start}: {real[f'start{start}']}")
+        # the per-layer embeddings' share: the same step without them
+        real[f"start{START_POS}_no_ple"] = decode_rate(ctx, E2BShape.real(ple_dim=0), START_POS, args.pos_steps,
+                                                       args.pos_warmup, embed=True)
+        log(f"real E2B layout without per-layer embeddings: {real[f'start{START_POS}_no_ple']}")
         if not args.no_prefill:
             prefill["real_e2b_layout"] = prefill_rate(ctx, E2BShape.real())
             log(f"prefill (real layout): {prefill['real_e2b_layout']}")

@@ -72,10 +72,12 @@ __global__ __launch_bounds__(PT) void ple_stage1_kernel(Stage1Args a) {
   const uint32_t tok = a.tokens ? a.tokens[b] : a.token;
   const size_t base = ((size_t)b * a.L + il) * 256;
   const float v = a.projected[base + t];
+  const float w = g4d::f16_bits_to_f32(a.norm_w[t]);
+  // the table value first: its loads wait on the token, the norm's do not
+  const float e = tok < a.rows ? f16_round(q5k_value(a.table + ((size_t)tok * a.L + il) * kQ5Bytes, (int)t)) : 0.f;
   const float ss = g4d::block_sum<PW>(v * v, red);
   const float rms = sqrtf(ss * (1.0f / 256.0f) + a.eps);
-  const float normed = (v / rms) * g4d::f16_bits_to_f32(a.norm_w[t]);
-  const float e = tok < a.rows ? f16_round(q5k_value(a.table + ((size_t)tok * a.L + il) * kQ5Bytes, (int)t)) : 0.f;
+  const float normed = (v / rms) * w;
   a.out[base + t] = (normed + e * 16.0f) * 0.70710678118654752f;  // sqrt(256) = 16
 }
 
@@ -123,89 +125,113 @@ struct HmvArgs {
 // One wave per row (rows blockIdx.x * PW + wave, then + gridDim.x * PW):
 // lane l holds row elements 8l + 512i (N = 1536: 3 x 16 B) or 4l (N = 256:
 // 8 B) in registers and multiplies them with each of up to HB vectors
-// staged in LDS; the 64 lane partials meet through DPP.
-template <int N, int PRO, int EPI>
-__global__ __launch_bounds__(PT) void hmv_kernel(HmvArgs a) {
-  static_assert(N == 256 || N % 512 == 0, "row width");
-  constexpr int EPL = N == 256 ? 4 : 8;                // f16 per lane per load
-  constexpr int NL = N == 256 ? 1 : N / 512;           // loads per lane
-  constexpr int HB = vectors_per_pass<N>();
-  __shared__ __align__(16) float xs[HB * N];
-  __shared__ float red[2 * PW];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  // one pass holds every vector: staged once, before the rows
-  const bool once = PRO == 1 || a.B <= (uint32_t)HB;
-  if (PRO == 0 && once) {
-    for (uint32_t i = tid; i < a.B * N / 4; i += PT) ((float4*)xs)[i] = ((const float4*)a.x)[i];
-    __syncthreads();
-  }
-  if constexpr (PRO == 1) {
-    // the one vector: h = residual + x * w1 / rms(x)
-    float ss = 0.f;
-    for (int i = tid; i < N; i += PT) ss += a.x[i] * a.x[i];
-    ss = g4d::block_sum<PW>(ss, red);
-    const float inv = __builtin_amdgcn_rsqf(ss * (1.0f / (float)N) + a.eps);
-    for (int i = tid; i < N; i += PT) {
-      const float h = a.residual[i] + a.x[i] * g4d::f16_bits_to_f32(a.w1[i]) * inv;
-      xs[i] = h;
-      if (a.h_out && blockIdx.x == 0) a.h_out[i] = h;
-    }
-    __syncthreads();
-  }
-  for (uint32_t m0 = blockIdx.x * PW; m0 < a.M; m0 += gridDim.x * PW) {
-    const uint32_t m = m0 + wv;
-    const bool live = m < a.M;
-    // the row in registers (a wave past M reads row M - 1, stores nothing)
-    float w[NL][EPL];
-    const uint16_t* row = a.W + (size_t)min(m, a.M - 1) * N;
+// staged in LDS; the 64 lane partials meet through DPP and lane v stores
+// vector v's result. Every global load a result waits on is issued before
+// the first wait: the wave's first row and the next one (prefetched while a
+// row is multiplied), the prologue's vector, residual and norm weights, and
+// the epilogue's ple_inputs values.
+template <int N>
+struct HmvRow {
+  static constexpr int EPL = N == 256 ? 4 : 8;   // f16 per lane per load
+  static constexpr int NL = N == 256 ? 1 : N / 512;
+  uint4 u[NL];
+  __device__ void load(const uint16_t* W, uint32_t m, int lane) {
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       if constexpr (EPL == 8) {
-        const uint4 u = *(const uint4*)(row + 512 * i + 8 * lane);
-        const uint32_t uu[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          w[i][2 * j] = g4d::f16_bits_to_f32(uu[j] & 0xffffu);
-          w[i][2 * j + 1] = g4d::f16_bits_to_f32(uu[j] >> 16);
-        }
+        u[i] = *(const uint4*)(W + (size_t)m * N + 512 * i + 8 * lane);
       } else {
-        const uint2 u = *(const uint2*)(row + 4 * lane);
-        w[i][0] = g4d::f16_bits_to_f32(u.x & 0xffffu);
-        w[i][1] = g4d::f16_bits_to_f32(u.x >> 16);
-        w[i][2] = g4d::f16_bits_to_f32(u.y & 0xffffu);
-        w[i][3] = g4d::f16_bits_to_f32(u.y >> 16);
+        const uint2 v = *(const uint2*)(W + (size_t)m * N + 4 * lane);
+        u[i] = make_uint4(v.x, v.y, 0u, 0u);
       }
     }
+  }
+  // row . xv (the lane's elements), f32 products and sums
+  __device__ float dot(const float* xv, int lane) const {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const float* xe = xv + (EPL == 8 ? 512 * i + 8 * lane : 4 * lane);
+      const float4 p = *(const float4*)xe;
+      acc += g4d::f16_bits_to_f32(u[i].x & 0xffffu) * p.x + g4d::f16_bits_to_f32(u[i].x >> 16) * p.y +
+             g4d::f16_bits_to_f32(u[i].y & 0xffffu) * p.z + g4d::f16_bits_to_f32(u[i].y >> 16) * p.w;
+      if constexpr (EPL == 8) {
+        const float4 q = *(const float4*)(xe + 4);
+        acc += g4d::f16_bits_to_f32(u[i].z & 0xffffu) * q.x + g4d::f16_bits_to_f32(u[i].z >> 16) * q.y +
+               g4d::f16_bits_to_f32(u[i].w & 0xffffu) * q.z + g4d::f16_bits_to_f32(u[i].w >> 16) * q.w;
+      }
+    }
+    return acc;
+  }
+};
+
+template <int N, int PRO, int EPI>
+__global__ __launch_bounds__(PT) void hmv_kernel(HmvArgs a) {
+  static_assert(N == 256 || N % 512 == 0, "row width");
+  static_assert(PRO == 0 || N % PT == 0, "prologue width");
+  constexpr int HB = vectors_per_pass<N>();
+  constexpr int PE = PRO == 1 ? N / PT : 1;  // prologue elements per thread
+  __shared__ __align__(16) float xs[HB * N];
+  __shared__ float red[2 * PW];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t step = gridDim.x * PW;
+  uint32_t m0 = blockIdx.x * PW;
+  HmvRow<N> row, next;
+  if (m0 < a.M) row.load(a.W, min(m0 + wv, a.M - 1), lane);  // (a wave past M reads row M - 1, stores nothing)
+  // one pass holds every vector: staged once, before the rows
+  const bool once = PRO == 1 || a.B <= (uint32_t)HB;
+  if constexpr (PRO == 1) {
+    // the one vector: h = residual + x * w1 / rms(x)
+    float xr[PE], rr[PE], wr[PE];
+#pragma unroll
+    for (int k = 0; k < PE; ++k) {
+      xr[k] = a.x[tid + PT * k];
+      rr[k] = a.residual[tid + PT * k];
+      wr[k] = g4d::f16_bits_to_f32(a.w1[tid + PT * k]);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < PE; ++k) ss += xr[k] * xr[k];
+    ss = g4d::block_sum<PW>(ss, red);
+    const float inv = __builtin_amdgcn_rsqf(ss * (1.0f / (float)N) + a.eps);
+#pragma unroll
+    for (int k = 0; k < PE; ++k) {
+      const float h = rr[k] + xr[k] * wr[k] * inv;
+      xs[tid + PT * k] = h;
+      if (a.h_out && blockIdx.x == 0) a.h_out[tid + PT * k] = h;
+    }
+    __syncthreads();
+  } else if (once) {
+    for (uint32_t i = tid; i < a.B * N / 4; i += PT) ((float4*)xs)[i] = ((const float4*)a.x)[i];
+    __syncthreads();
+  }
+  for (; m0 < a.M; m0 += step) {
+    const uint32_t m = m0 + wv;
+    const bool live = m < a.M;
+    if (m0 + step < a.M) next.load(a.W, min(m0 + step + wv, a.M - 1), lane);
     for (uint32_t b0 = 0; b0 < a.B; b0 += HB) {
       const uint32_t nb = min((uint32_t)HB, a.B - b0);
+      // lane v's epilogue input, for vector b0 + v of this row
+      float pv = 0.f;
+      if (EPI == 1 && live && (uint32_t)lane < nb) pv = a.ple[(size_t)(b0 + lane) * a.ple_stride + m];
       if (!once) {  // (uniform over the workgroup)
         __syncthreads();  // the previous pass's reads are done
         for (uint32_t i = tid; i < nb * N / 4; i += PT)
           ((float4*)xs)[i] = ((const float4*)(a.x + (size_t)b0 * N))[i];
         __syncthreads();
       }
+      float mine = 0.f;
       for (uint32_t v = 0; v < nb; ++v) {
-        const float* xv = xs + v * N;
-        float acc = 0.f;
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-          const float* xe = xv + (EPL == 8 ? 512 * i + 8 * lane : 4 * lane);
-          const float4 p = *(const float4*)xe;
-          acc += w[i][0] * p.x + w[i][1] * p.y + w[i][2] * p.z + w[i][3] * p.w;
-          if constexpr (EPL == 8) {
-            const float4 q = *(const float4*)(xe + 4);
-            acc += w[i][4] * q.x + w[i][5] * q.y + w[i][6] * q.z + w[i][7] * q.w;
-          }
-        }
-        acc = g4d::wave_sum_dpp(acc);
-        if (live && lane == 0) {
-          const uint32_t b = b0 + v;
-          float r = acc;
-          if constexpr (EPI == 1) r = g4d::gelu_tanh(acc) * a.ple[(size_t)b * a.ple_stride + m];
-          a.y[(size_t)b * a.M + m] = r;
-        }
+        const float r = g4d::wave_sum_dpp(row.dot(xs + v * N, lane));
+        if ((uint32_t)lane == v) mine = r;
+      }
+      if (live && (uint32_t)lane < nb) {
+        float r = mine;
+        if constexpr (EPI == 1) r = g4d::gelu_tanh(mine) * pv;
+        a.y[(size_t)(b0 + lane) * a.M + m] = r;
       }
     }
+    row = next;
   }
 }
 
