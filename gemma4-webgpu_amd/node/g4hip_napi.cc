@@ -91,10 +91,15 @@ struct Args {
     return (float)d;
   }
   std::string str(size_t i) {
-    char buf[64] = {0};
     size_t n = 0;
-    if (i >= argc || napi_get_value_string_utf8(env, v[i], buf, sizeof buf, &n) != napi_ok) fail("expected a string");
-    return std::string(buf, n);
+    if (i >= argc || napi_get_value_string_utf8(env, v[i], nullptr, 0, &n) != napi_ok) {
+      fail("expected a string");
+      return std::string();
+    }
+    std::string out(n + 1, '\0');
+    napi_get_value_string_utf8(env, v[i], &out[0], n + 1, &n);
+    out.resize(n);
+    return out;
   }
   // a named field of the Params object at argument i
   napi_value field(size_t i, const char* name) {
@@ -621,6 +626,200 @@ napi_value AdvancePosition(napi_env env, napi_callback_info info) {
   return done(env, g4_advancePosition(c, pd, d));
 }
 
+// ---- GGUF files (GGUFParser, src/gguf.ts:75-101) ------------------------
+
+// ggufOpen(path) -> handle (the file stays mapped until ggufClose)
+napi_value GgufOpen(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  const std::string path = a.str(0);
+  CHECKED(a);
+  g4_gguf* g = nullptr;
+  const int rc = g4_gguf_open(path.c_str(), &g);
+  if (rc != G4_OK) return done(env, rc);
+  return bigint(env, g);
+}
+
+napi_value GgufClose(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_gguf* g = (g4_gguf*)a.ptr(0);
+  CHECKED(a);
+  return done(env, g4_gguf_close(g));
+}
+
+void set_num(napi_env env, napi_value o, const char* k, double d) {
+  napi_set_named_property(env, o, k, number(env, d));
+}
+
+// ggufInfo(handle) -> {version, tensorCount, kvCount, dataOffset, alignment}
+napi_value GgufInfo(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  const g4_gguf* g = (const g4_gguf*)a.ptr(0);
+  CHECKED(a);
+  uint32_t v = 0, al = 0;
+  uint64_t nt = 0, nkv = 0, off = 0;
+  const int rc = g4_gguf_info(g, &v, &nt, &nkv, &off, &al);
+  if (rc != G4_OK) return done(env, rc);
+  napi_value o;
+  napi_create_object(env, &o);
+  set_num(env, o, "version", v);
+  set_num(env, o, "tensorCount", (double)nt);
+  set_num(env, o, "kvCount", (double)nkv);
+  set_num(env, o, "dataOffset", (double)off);
+  set_num(env, o, "alignment", al);
+  return o;
+}
+
+// the reference's GGUFValue type names (src/gguf.ts:50-72)
+const char* value_type_name(uint32_t t) {
+  static const char* names[] = {"uint8", "int8", "uint16", "int16", "uint32", "int32", "float32",
+                                "bool", "string", "array", "uint64", "int64", "float64"};
+  return t < 13 ? names[t] : "unknown";
+}
+
+// one element as {type, value}: 64-bit integers as BigInt, the rest as Number /
+// Boolean / String
+napi_value gguf_value(napi_env env, const g4_gguf* g, uint64_t i, uint64_t e, uint32_t t, int* rc) {
+  napi_value o, val;
+  napi_create_object(env, &o);
+  napi_value tn;
+  napi_create_string_utf8(env, value_type_name(t), NAPI_AUTO_LENGTH, &tn);
+  napi_set_named_property(env, o, "type", tn);
+  if (t == 8) {
+    const char* s = nullptr;
+    uint64_t n = 0;
+    *rc = g4_gguf_kv_string(g, i, e, &s, &n);
+    if (*rc) return nullptr;
+    napi_create_string_utf8(env, s, (size_t)n, &val);
+  } else {
+    double f = 0;
+    int64_t iv = 0;
+    uint64_t u = 0;
+    *rc = g4_gguf_kv_number(g, i, e, &f, &iv, &u);
+    if (*rc) return nullptr;
+    if (t == 10) napi_create_bigint_uint64(env, u, &val);
+    else if (t == 11) napi_create_bigint_int64(env, iv, &val);
+    else if (t == 7) napi_get_boolean(env, u != 0, &val);
+    else napi_create_double(env, f, &val);
+  }
+  napi_set_named_property(env, o, "value", val);
+  return o;
+}
+
+// ggufMetadata(handle) -> {key: {type, value}} as GGUFParser's kv map
+// (arrays: value is an array of {type, value}; nested arrays: value null)
+napi_value GgufMetadata(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  const g4_gguf* g = (const g4_gguf*)a.ptr(0);
+  CHECKED(a);
+  uint64_t nkv = 0;
+  int rc = g4_gguf_info(g, nullptr, nullptr, &nkv, nullptr, nullptr);
+  if (rc != G4_OK) return done(env, rc);
+  napi_value out;
+  napi_create_object(env, &out);
+  for (uint64_t i = 0; i < nkv; ++i) {
+    const char* key = nullptr;
+    uint32_t t = 0, at = 0;
+    uint64_t n = 0;
+    rc = g4_gguf_kv(g, i, &key, &t, &at, &n);
+    if (rc != G4_OK) return done(env, rc);
+    napi_value entry;
+    if (t == 9) {
+      napi_create_object(env, &entry);
+      napi_value tn, arr;
+      napi_create_string_utf8(env, "array", NAPI_AUTO_LENGTH, &tn);
+      napi_set_named_property(env, entry, "type", tn);
+      if (at == 9) {
+        napi_get_null(env, &arr);
+      } else {
+        napi_create_array_with_length(env, (size_t)n, &arr);
+        for (uint64_t e = 0; e < n; ++e) {
+          napi_value el = gguf_value(env, g, i, e, at, &rc);
+          if (rc != G4_OK) return done(env, rc);
+          napi_set_element(env, arr, (uint32_t)e, el);
+        }
+      }
+      napi_set_named_property(env, entry, "value", arr);
+    } else {
+      entry = gguf_value(env, g, i, 0, t, &rc);
+      if (rc != G4_OK) return done(env, rc);
+    }
+    napi_set_named_property(env, out, key, entry);
+  }
+  return out;
+}
+
+// ggufTensors(handle) -> [{name, dims, type, offset, nbytes, index}] (GGUFTensor)
+napi_value GgufTensors(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  const g4_gguf* g = (const g4_gguf*)a.ptr(0);
+  CHECKED(a);
+  uint64_t nt = 0;
+  int rc = g4_gguf_info(g, nullptr, &nt, nullptr, nullptr, nullptr);
+  if (rc != G4_OK) return done(env, rc);
+  napi_value out;
+  napi_create_array_with_length(env, (size_t)nt, &out);
+  for (uint64_t i = 0; i < nt; ++i) {
+    const char* name = nullptr;
+    uint32_t nd = 0, t = 0;
+    uint64_t dims[4], off = 0, nb = 0;
+    rc = g4_gguf_tensor(g, i, &name, &nd, dims, &t, &off, &nb);
+    if (rc != G4_OK) return done(env, rc);
+    napi_value o, nm, dv;
+    napi_create_object(env, &o);
+    napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &nm);
+    napi_set_named_property(env, o, "name", nm);
+    napi_create_array_with_length(env, nd, &dv);
+    for (uint32_t d = 0; d < nd; ++d) napi_set_element(env, dv, d, number(env, (double)dims[d]));
+    napi_set_named_property(env, o, "dims", dv);
+    set_num(env, o, "type", t);
+    set_num(env, o, "offset", (double)off);
+    set_num(env, o, "nbytes", (double)nb);
+    set_num(env, o, "index", (double)i);
+    napi_set_element(env, out, (uint32_t)i, o);
+  }
+  return out;
+}
+
+// ggufUpload(ctx, handle, index, dst, dstBytes): the tensor's bytes as they are
+napi_value GgufUpload(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const g4_gguf* g = (const g4_gguf*)a.ptr(1);
+  const uint64_t idx = a.u64(2);
+  void* dst = a.ptr(3);
+  const uint64_t n = a.u64(4);
+  CHECKED(a);
+  return done(env, g4_gguf_upload(c, g, idx, dst, (size_t)n));
+}
+
+// ggufUploadF16(ctx, handle, index, dst, dstElems): F32 / F16 / BF16 as f16
+napi_value GgufUploadF16(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const g4_gguf* g = (const g4_gguf*)a.ptr(1);
+  const uint64_t idx = a.u64(2);
+  uint16_t* dst = U16P(a, 3);
+  const uint64_t n = a.u64(4);
+  CHECKED(a);
+  return done(env, g4_gguf_upload_f16(c, g, idx, dst, (size_t)n));
+}
+
+// dequantF16(ctx, 'q4k' | 'q6k', blocks, nblocks, out): blocks to f16 rows
+napi_value DequantF16(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const std::string t = a.str(1);
+  const void* b = a.ptr(2);
+  const uint64_t n = a.u64(3);
+  uint16_t* out = U16P(a, 4);
+  CHECKED(a);
+  if (t != "q4k" && t != "q6k") {
+    a.fail("dequantF16: wtype must be 'q4k' or 'q6k'");
+    return nullptr;
+  }
+  return done(env, g4_dequantF16(c, t == "q4k" ? 0 : 1, b, n, out));
+}
+
 struct Entry {
   const char* name;
   napi_callback fn;
@@ -664,6 +863,14 @@ const Entry kEntries[] = {
     {"pleStage1Fuse", PleStage1Fuse},
     {"pleGeluMul", PleGeluMul},
     {"pleSkipScaleAdd", PleSkipScaleAdd},
+    {"ggufOpen", GgufOpen},
+    {"ggufClose", GgufClose},
+    {"ggufInfo", GgufInfo},
+    {"ggufMetadata", GgufMetadata},
+    {"ggufTensors", GgufTensors},
+    {"ggufUpload", GgufUpload},
+    {"ggufUploadF16", GgufUploadF16},
+    {"dequantF16", DequantF16},
 };
 
 }  // namespace

@@ -82,6 +82,56 @@ function e2bConfig(overrides) {
   };
 }
 
+// configFromGGUF (src/config/gemma4-e2b.ts:70-148): the E2B baseline,
+// overridden by every gemma4.* key of the file's metadata (ggufMetadata:
+// {key: {type, value}}, arrays as lists of {type, value}).
+function configFromGGUF(kv, maxContextLength) {
+  if (!kv['gemma4.block_count'] && !kv['gemma4.embedding_length']) {
+    throw new Error('Not a Gemma 4 GGUF: no gemma4.* metadata keys found.');
+  }
+  const num = (k) => {
+    const e = kv[k];
+    if (!e || e.type === 'array' || e.value === null || e.value === undefined) return null;
+    return Number(e.value);
+  };
+  const arr = (k) => {
+    const e = kv[k];
+    return e && e.type === 'array' && e.value ? e.value.map((x) => x.value) : null;
+  };
+  const base = e2bConfig();
+  const C = Object.assign({}, base);
+  const set = (k, field) => {
+    const v = num(k);
+    if (v !== null) C[field] = v;
+  };
+  set('gemma4.embedding_length', 'hidden_size');
+  set('gemma4.block_count', 'num_layers');
+  set('gemma4.attention.head_count', 'num_q_heads');
+  set('gemma4.attention.head_count_kv', 'num_kv_heads');
+  const ctxLen = num('gemma4.context_length');
+  C.context_length = ctxLen !== null ? Math.min(ctxLen, maxContextLength || 2048) : 2048;
+  const ffn = arr('gemma4.feed_forward_length');
+  if (ffn) {
+    C.intermediate_sizes = ffn.map(Number);
+  } else {
+    const v = num('gemma4.feed_forward_length');
+    if (v !== null) C.intermediate_sizes = new Array(C.num_layers).fill(v);
+  }
+  set('gemma4.attention.key_length', 'head_dim_global');
+  set('gemma4.attention.key_length_swa', 'head_dim_local');
+  set('gemma4.rope.freq_base', 'rope_theta_global');
+  set('gemma4.rope.freq_base_swa', 'rope_theta_swa');
+  set('gemma4.attention.sliding_window', 'sliding_window');
+  const pat = arr('gemma4.attention.sliding_window_pattern');
+  if (pat) C.attention_is_sliding = pat.map(Boolean);
+  set('gemma4.embedding_length_per_layer_input', 'per_layer_input_dim');
+  set('gemma4.final_logit_softcapping', 'final_logit_softcapping');
+  const shared = num('gemma4.attention.shared_kv_layers');
+  if (shared !== null) C.num_unshared_layers = C.num_layers - shared;
+  C.kv_producer_for_layer = kvProducerMap(C.num_layers, C.num_unshared_layers, C.attention_is_sliding);
+  return C;
+}
+
 // Per-layer selectors (src/types.ts:69-91).
 const isSwaLayer = (C, il) => C.attention_is_sliding[il];
 const ropeTheta = (C, il) => (isSwaLayer(C, il) ? C.rope_theta_swa : C.rope_theta_global);
@@ -124,6 +174,100 @@ class HipBackend {
     const addon = loadAddon();
     const ctx = addon.init((opts && opts.device) || 0);
     return new HipBackend(addon, ctx, config, opts);
+  }
+
+  // A backend holding a GGUF file's weights (GGUFParser + the upload of
+  // src/engine.ts:547-625, without the f16 expansion): each layer matrix as
+  // the file's Q4_K / Q6_K blocks, norms and the per-layer-embedding
+  // matrices as f16, the tied token table as the LM head's blocks and the
+  // lookup's f16 rows, the per-layer table as its Q5_K blocks. opts as the
+  // constructor's, plus device and maxContextLength.
+  static fromGGUF(file, opts) {
+    const o = opts || {};
+    const addon = loadAddon();
+    const gg = addon.ggufOpen(file);
+    try {
+      const C = configFromGGUF(addon.ggufMetadata(gg), o.maxContextLength);
+      const tensors = {};
+      for (const t of addon.ggufTensors(gg)) tensors[t.name] = t;
+      const emb = tensors['token_embd.weight'];
+      if (!emb) throw new Error('GGUF has no token_embd.weight');
+      C.vocab_size = emb.dims[1];
+      if (!tensors['per_layer_token_embd.weight']) C.per_layer_input_dim = 0;
+      const ctx = addon.init(o.device || 0);
+      const be = new HipBackend(addon, ctx, C, Object.assign({ maxSeqLen: C.context_length }, o));
+      be.allocate();
+      be._loadGGUF(gg, tensors);
+      return be;
+    } finally {
+      addon.ggufClose(gg);
+    }
+  }
+
+  _loadGGUF(gg, tensors) {
+    const C = this.config;
+    const g = this.g;
+    const FMT = { 12: 'q4k', 14: 'q6k' };
+    const get = (name) => {
+      const t = tensors[name];
+      if (!t) throw new Error('GGUF has no tensor ' + name);
+      return t;
+    };
+    const raw = (name) => {
+      const t = get(name);
+      if (!t.nbytes) throw new Error(name + ': tensor type ' + t.type + ' has no known size');
+      const p = this.alloc(t.nbytes);
+      g.ggufUpload(this.ctx, gg, t.index, p, t.nbytes);
+      return p;
+    };
+    const f16 = (name) => {
+      const t = get(name);
+      let n = 1;
+      for (const d of t.dims) n *= d;
+      const p = this.alloc(2 * Math.max(n, 2));
+      g.ggufUploadF16(this.ctx, gg, t.index, p, Math.max(n, 2));
+      return p;
+    };
+    const matFormat = (name) => {
+      const f = FMT[get(name).type];
+      if (!f) throw new Error(name + ': tensor type ' + get(name).type + ' (the matvecs read Q4_K and Q6_K)');
+      return f;
+    };
+    const MATS = ['attn_q', 'attn_k', 'attn_v', 'attn_output', 'ffn_gate', 'ffn_up', 'ffn_down'];
+    const F16S = ['attn_norm', 'attn_q_norm', 'attn_k_norm', 'post_attention_norm', 'ffn_norm', 'post_ffw_norm',
+      'inp_gate', 'proj', 'post_norm', 'layer_output_scale'];
+    for (let il = 0; il < C.num_layers; il++) {
+      const prefix = 'blk.' + il + '.';
+      const formats = {};
+      for (const m of MATS) {
+        if (tensors[prefix + m + '.weight'] && (isKvProducer(C, il) || (m !== 'attn_k' && m !== 'attn_v'))) {
+          formats[m] = matFormat(prefix + m + '.weight');
+        }
+      }
+      const need = Object.keys(this.layerTensorBytes(il, formats));
+      const t = {};
+      for (const name of need) {
+        t[name] = F16S.indexOf(name) >= 0 ? f16(prefix + name + '.weight') : raw(prefix + name + '.weight');
+      }
+      this.setLayerWeights(il, t, formats);
+    }
+    const glob = { finalNorm: f16('output_norm.weight'), rope_freqs: f16('rope_freqs.weight') };
+    const headName = tensors['output.weight'] ? 'output.weight' : 'token_embd.weight';
+    glob.lmHead = raw(headName);
+    glob.lmHeadFormat = matFormat(headName);
+    // the tied table's f16 rows for the lookup, from the same blocks
+    const te = headName === 'token_embd.weight' ? glob.lmHead : raw('token_embd.weight');
+    glob.tokenEmbed = this.alloc(2 * C.vocab_size * C.hidden_size);
+    g.dequantF16(this.ctx, matFormat('token_embd.weight'), te, C.vocab_size * C.hidden_size / 256, glob.tokenEmbed);
+    if (C.per_layer_input_dim > 0) {
+      glob.perLayerModelProj = f16('per_layer_model_proj.weight');
+      glob.perLayerProjNorm = f16('per_layer_proj_norm.weight');
+      const ple = get('per_layer_token_embd.weight');
+      if (ple.type !== 13) throw new Error('per_layer_token_embd.weight: type ' + ple.type + ', expected Q5_K');
+      glob.perLayerTable = raw('per_layer_token_embd.weight');
+    }
+    this.setGlobals(glob);
+    g.sync(this.ctx);
   }
 
   close() {
@@ -411,6 +555,7 @@ module.exports = {
   HipBackend: HipBackend,
   loadAddon: loadAddon,
   e2bConfig: e2bConfig,
+  configFromGGUF: configFromGGUF,
   kvProducerMap: kvProducerMap,
   headDim: headDim,
   intermediateSize: intermediateSize,

@@ -3,7 +3,9 @@
 // tests/test_gpu_napi.py, which writes the model and checks the outputs
 // against the oracle): usage `node napi_forward.js <dir>`.
 //   <dir>/config.json  {overrides (e2bConfig), maxSeqLen, position, token,
-//                       formats (per layer: {matrix: 'q4k' | 'q6k'})}
+//                       formats (per layer: {matrix: 'q4k' | 'q6k'})}, or
+//                      {gguf (a model file: HipBackend.fromGGUF, zero
+//                       caches), maxSeqLen, position, token}
 //   <dir>/<name>.bin   raw tensor bytes: L<il>.<tensor> per layer, kv<il>.k /
 //                      kv<il>.v (initial f16 caches of the producer layers),
 //                      tokenEmbed, lmHead, finalNorm, rope_freqs, and with
@@ -21,8 +23,10 @@ const hb = require(path.join(root, 'gemma4-webgpu_amd', 'node', 'hip_backend.js'
 
 const dir = process.argv[2];
 const cfg = JSON.parse(fs.readFileSync(path.join(dir, 'config.json'), 'utf8'));
-const C = hb.e2bConfig(cfg.overrides);
-const be = hb.HipBackend.open(C, { maxSeqLen: cfg.maxSeqLen });
+// cfg.gguf: the model (weights and configuration) from a GGUF file, caches zero
+const be = cfg.gguf ? hb.HipBackend.fromGGUF(cfg.gguf, { maxSeqLen: cfg.maxSeqLen })
+  : hb.HipBackend.open(hb.e2bConfig(cfg.overrides), { maxSeqLen: cfg.maxSeqLen });
+const C = be.config;
 console.log('[napi] device', JSON.stringify(be.g.deviceInfo(be.ctx)));
 
 function upload(name) {
@@ -32,8 +36,8 @@ function upload(name) {
   return p;
 }
 
-be.allocate();
-for (let il = 0; il < C.num_layers; il++) {
+if (!cfg.gguf) be.allocate();
+for (let il = 0; il < C.num_layers && !cfg.gguf; il++) {
   const f = (cfg.formats || [])[il] || {};
   const t = {};
   for (const n of Object.keys(be.layerTensorBytes(il, f))) t[n] = upload('L' + il + '.' + n);
@@ -45,12 +49,14 @@ for (let il = 0; il < C.num_layers; il++) {
     be.g.upload(be.ctx, be.kvCaches[il].v, v, 0);
   }
 }
-const globals = { tokenEmbed: upload('tokenEmbed'), lmHead: upload('lmHead'), finalNorm: upload('finalNorm'),
-  rope_freqs: upload('rope_freqs') };
-if (C.per_layer_input_dim > 0) {
-  for (const n of ['perLayerModelProj', 'perLayerProjNorm', 'perLayerTable']) globals[n] = upload(n);
+if (!cfg.gguf) {
+  const globals = { tokenEmbed: upload('tokenEmbed'), lmHead: upload('lmHead'), finalNorm: upload('finalNorm'),
+    rope_freqs: upload('rope_freqs') };
+  if (C.per_layer_input_dim > 0) {
+    for (const n of ['perLayerModelProj', 'perLayerProjNorm', 'perLayerTable']) globals[n] = upload(n);
+  }
+  be.setGlobals(globals);
 }
-be.setGlobals(globals);
 
 const H = C.hidden_size;
 const V = C.vocab_size;

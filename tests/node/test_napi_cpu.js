@@ -20,7 +20,8 @@ const KEYS = ['version', 'lastError', 'init', 'destroy', 'deviceInfo', 'alloc', 
   'download', 'sync', 'graphBegin', 'graphEnd', 'graphLaunch', 'graphDestroy', 'fill', 'matmulQuant',
   'matmulQuantMR4', 'kvCacheStore', 'attnScore', 'softmax', 'attnOutput', 'attnDecodeWorkspaceSize', 'attnDecode',
   'perHeadRmsNormNoWeight', 'fusedPerHeadNormRope', 'rmsNorm', 'fusedNormAdd', 'geluMul', 'logitSoftcap',
-  'embeddingLookup', 'argmax', 'topk256', 'advancePosition', 'pleStage1Fuse', 'pleGeluMul', 'pleSkipScaleAdd'];
+  'embeddingLookup', 'argmax', 'topk256', 'advancePosition', 'pleStage1Fuse', 'pleGeluMul', 'pleSkipScaleAdd',
+  'ggufOpen', 'ggufClose', 'ggufInfo', 'ggufMetadata', 'ggufTensors', 'ggufUpload', 'ggufUploadF16', 'dequantF16'];
 
 const addon = hb.loadAddon();
 

@@ -16,6 +16,12 @@ built from one.
   replayed) and ragged step match the oracle composition over the same
   weights at rel-L2 1e-3 / cosine 0.9999, the sampled tokens bit-exact on
   the device's logits."""
+import json
+import os
+import shutil
+import subprocess
+import tempfile
+
 import numpy as np
 import pytest
 
@@ -306,3 +312,43 @@ def test_file_model_ragged_step(ctx, model_path):
     print(f"[gguf model] ragged step B={d.B}", flush=True)
     _step_vs_oracle(ctx, d, LENS)
     del d
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="no node binary")
+def test_node_backend_from_gguf(ctx, model_path):
+    """HipBackend.fromGGUF (the N-API addon's reader and uploads, the Node
+    backend's configFromGGUF) on the same file: three greedy forwards from
+    position 0 with zero caches against the oracle over the Python
+    decoder's copy of the file's weights."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    d = decoder_from_gguf(ctx, model_path, max_seq=1024)
+    ctx.sync()
+    hm = HostModel(d)
+    s = d.s
+    kcs = [np.zeros(1024 * s.kv_dim_of(il), np.uint16) for il in range(s.n_layers)]
+    vcs = [np.zeros(1024 * s.kv_dim_of(il), np.uint16) for il in range(s.n_layers)]
+    del d
+    with tempfile.TemporaryDirectory() as td:
+        with open(os.path.join(td, "config.json"), "w") as f:
+            json.dump({"gguf": model_path, "maxSeqLen": 1024, "position": 0, "token": 1234}, f)
+        print("[gguf node] running the Node forwards", flush=True)
+        r = subprocess.run(["node", os.path.join(root, "tests", "node", "napi_forward.js"), td], capture_output=True,
+                           text=True, timeout=240)
+        print(r.stdout, r.stderr, flush=True)
+        assert r.returncode == 0, r.stderr
+        out = np.fromfile(os.path.join(td, "out.bin"), np.uint8)
+    H, V = s.hidden, s.vocab
+    per = 4 * H + 4 * V + 4
+    assert out.size == 3 * per
+    tok = 1234
+    for i in range(3):
+        blk = out[i * per:(i + 1) * per]
+        hidden = blk[:4 * H].view(np.float32)
+        logits = blk[4 * H:4 * H + 4 * V].view(np.float32)
+        got = int(blk[4 * H + 4 * V:].view(np.uint32)[0])
+        x_ref, lg_ref = hm.step(hm.embed(tok), kcs, vcs, i, token=tok)
+        print(f"[gguf node] forward {i + 1}: token {tok}, hidden rel-L2 {O.rel_l2(hidden, x_ref):.2e}", flush=True)
+        assert_close(hidden, x_ref, what=f"hidden forward {i + 1}")
+        assert_close(logits, lg_ref, what=f"logits forward {i + 1}")
+        assert got == O.argmax(logits)
+        tok = got
