@@ -685,6 +685,9 @@ def main():
     ap.add_argument("--no-real-layout", action="store_true",
                     help="skip the decode runs of Gemma-4-E2B's own layer layout")
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill runs")
+    ap.add_argument("--real-eager-only", type=int, default=0, metavar="STEPS",
+                    help="run STEPS eager (not captured) fused steps of Gemma-4-E2B's layout with per-layer "
+                         "embeddings from position 512 and exit (for the kernel tracer)")
     ap.add_argument("--attn-only", action="store_true",
                     help="time only the decode attention of config 3 (the launches a profiler should see)")
     ap.add_argument("--batch-steps", type=int, default=30)
@@ -712,6 +715,20 @@ def main():
         return
     if args.attn_only:
         print(json.dumps({"attention_decode": attention_cfg3(ctx)}), flush=True)
+        return
+    if args.real_eager_only:
+        d = Decoder(ctx, E2BShape.real(), max_seq=1024, seed=0, embed=True)
+        d.fill_kv(START_POS, seed=1)
+        d.set_position(START_POS)
+        ctx.sync()
+        a = ctx.record()
+        for _ in range(args.real_eager_only):
+            d.step_fused("argmax")
+        b = ctx.record()
+        ctx.sync()
+        print(json.dumps({"real_eager": {"steps": args.real_eager_only,
+                                         "us_per_step": round(ctx.elapsed_ms(a, b) * 1e3 / args.real_eager_only, 1),
+                                         "launches_per_step": d.launches_per_step_fused()}}), flush=True)
         return
     s = E2BShape()
     max_seq = START_POS + args.warmup + args.steps + 64

@@ -266,5 +266,5 @@ def lib() -> ctypes.CDLL:
 def check(rc: int) -> int:
     if rc < 0:
         msg = lib().g4_last_error()
-        raise G4Error(rc, msg.decode() if msg else "")
+        raise G4Error(rc, msg.decode("utf-8", "replace") if msg else "")
     return rc

@@ -221,3 +221,42 @@ def test_config_overrides_and_errors():
     # a consumer layer with no unshared layer of its kind
     cfg = dict(num_layers=3, num_unshared_layers=1, attention_is_sliding=[True, False, True])
     assert kv_producer_map(cfg) == [0, -1, 0]
+
+
+def test_random_corruptions_parse_or_refuse():
+    """2000 random corruptions of a valid file (byte flips, 64-bit length
+    fields set to huge values, splices of the file into itself): each one
+    either parses, and then every key, string and tensor is readable, or is
+    refused with an error; none may crash the process or read outside the
+    buffer (the reader bounds-checks every access)."""
+    full = bytearray(_small_file())
+    rng = np.random.default_rng(2024)
+    parsed = refused = 0
+    for it in range(2000):
+        b = bytearray(full)
+        kind = it % 4
+        if kind == 0:
+            for _ in range(int(rng.integers(1, 6))):
+                b[int(rng.integers(0, len(b)))] = int(rng.integers(0, 256))
+        elif kind == 1:
+            at = int(rng.integers(0, len(b) - 8))
+            b[at:at + 8] = struct.pack("<Q", int(rng.integers(0, 2**63)))
+        elif kind == 2:
+            at = int(rng.integers(0, len(b) - 4))
+            b[at:at + 4] = struct.pack("<I", int(rng.integers(0, 2**32)))
+        else:
+            i, j = sorted(int(x) for x in rng.integers(0, len(b), 2))
+            b = b[:i] + b[j:] + b[i:j]
+        try:
+            g = GGUFFile(data=bytes(b))
+        except G4Error:
+            refused += 1
+            continue
+        parsed += 1
+        for k in g.kv:
+            g.kv[k]
+        for t in g.tensors:
+            if t.nbytes:
+                assert g.data(t.name).size == t.nbytes
+        g.close()
+    assert parsed > 0 and refused > 0
