@@ -124,9 +124,9 @@ struct HmvArgs {
 
 // One wave per row (rows blockIdx.x * PW + wave, then + gridDim.x * PW):
 // lane l holds row elements 8l + 512i (N = 1536: 3 x 16 B) or 4l (N = 256:
-// 8 B) in registers and multiplies them with each of up to HB vectors
-// staged in LDS; the 64 lane partials meet through DPP and lane v stores
-// vector v's result. Every global load a result waits on is issued before
+// 8 B) in registers and multiplies them with each of the up to HB vectors
+// of its workgroup row (blockIdx.y), staged in LDS; the 64 lane partials
+// meet through DPP and lane v stores vector v's result. Every global load a result waits on is issued before
 // the first wait: the wave's first row and the next one (prefetched while a
 // row is multiplied), the prologue's vector, residual and norm weights, and
 // the epilogue's ple_inputs values.
@@ -174,12 +174,14 @@ __global__ __launch_bounds__(PT) void hmv_kernel(HmvArgs a) {
   __shared__ __align__(16) float xs[HB * N];
   __shared__ float red[2 * PW];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const uint32_t step = gridDim.x * PW;
-  uint32_t m0 = blockIdx.x * PW;
+  const uint32_t step = gridDim.x * PW, m_first = blockIdx.x * PW;
+  if (m_first >= a.M) return;  // (uniform)
   HmvRow<N> row, next;
-  if (m0 < a.M) row.load(a.W, min(m0 + wv, a.M - 1), lane);  // (a wave past M reads row M - 1, stores nothing)
-  // one pass holds every vector: staged once, before the rows
-  const bool once = PRO == 1 || a.B <= (uint32_t)HB;
+  // workgroup row blockIdx.y takes vectors HB * blockIdx.y .. + HB (one pass:
+  // the vector groups run side by side, each reading the rows it needs)
+  const uint32_t b0 = blockIdx.y * (uint32_t)HB;
+  const uint32_t nb = min((uint32_t)HB, a.B - b0);
+  row.load(a.W, min(m_first + wv, a.M - 1), lane);  // (a wave past M reads row M - 1, stores nothing)
   if constexpr (PRO == 1) {
     // the one vector: h = residual + x * w1 / rms(x)
     float xr[PE], rr[PE], wr[PE];
@@ -200,36 +202,26 @@ __global__ __launch_bounds__(PT) void hmv_kernel(HmvArgs a) {
       xs[tid + PT * k] = h;
       if (a.h_out && blockIdx.x == 0) a.h_out[tid + PT * k] = h;
     }
-    __syncthreads();
-  } else if (once) {
-    for (uint32_t i = tid; i < a.B * N / 4; i += PT) ((float4*)xs)[i] = ((const float4*)a.x)[i];
-    __syncthreads();
+  } else {
+    for (uint32_t i = tid; i < nb * N / 4; i += PT) ((float4*)xs)[i] = ((const float4*)(a.x + (size_t)b0 * N))[i];
   }
-  for (; m0 < a.M; m0 += step) {
+  __syncthreads();
+  for (uint32_t m0 = m_first; m0 < a.M; m0 += step) {
     const uint32_t m = m0 + wv;
     const bool live = m < a.M;
     if (m0 + step < a.M) next.load(a.W, min(m0 + step + wv, a.M - 1), lane);
-    for (uint32_t b0 = 0; b0 < a.B; b0 += HB) {
-      const uint32_t nb = min((uint32_t)HB, a.B - b0);
-      // lane v's epilogue input, for vector b0 + v of this row
-      float pv = 0.f;
-      if (EPI == 1 && live && (uint32_t)lane < nb) pv = a.ple[(size_t)(b0 + lane) * a.ple_stride + m];
-      if (!once) {  // (uniform over the workgroup)
-        __syncthreads();  // the previous pass's reads are done
-        for (uint32_t i = tid; i < nb * N / 4; i += PT)
-          ((float4*)xs)[i] = ((const float4*)(a.x + (size_t)b0 * N))[i];
-        __syncthreads();
-      }
-      float mine = 0.f;
-      for (uint32_t v = 0; v < nb; ++v) {
-        const float r = g4d::wave_sum_dpp(row.dot(xs + v * N, lane));
-        if ((uint32_t)lane == v) mine = r;
-      }
-      if (live && (uint32_t)lane < nb) {
-        float r = mine;
-        if constexpr (EPI == 1) r = g4d::gelu_tanh(mine) * pv;
-        a.y[(size_t)(b0 + lane) * a.M + m] = r;
-      }
+    // lane v's epilogue input, for vector b0 + v of this row
+    float pv = 0.f;
+    if (EPI == 1 && live && (uint32_t)lane < nb) pv = a.ple[(size_t)(b0 + lane) * a.ple_stride + m];
+    float mine = 0.f;
+    for (uint32_t v = 0; v < nb; ++v) {
+      const float r = g4d::wave_sum_dpp(row.dot(xs + v * N, lane));
+      if ((uint32_t)lane == v) mine = r;
+    }
+    if (live && (uint32_t)lane < nb) {
+      float r = mine;
+      if constexpr (EPI == 1) r = g4d::gelu_tanh(mine) * pv;
+      a.y[(size_t)(b0 + lane) * a.M + m] = r;
     }
     row = next;
   }
@@ -237,9 +229,10 @@ __global__ __launch_bounds__(PT) void hmv_kernel(HmvArgs a) {
 
 template <int PRO, int EPI>
 int hmv_launch(g4_ctx* ctx, const HmvArgs& a, uint32_t N) {
-  // about four workgroups per CU, fewer when the rows run out
-  const uint32_t want = (uint32_t)(ctx->num_cus > 0 ? ctx->num_cus : 256) * 4;
-  const dim3 grid(std::min<uint32_t>(want, ceil_div(a.M, (uint32_t)PW)));
+  // about four workgroups per CU over the rows, times the vector groups
+  const uint32_t cus = (uint32_t)(ctx->num_cus > 0 ? ctx->num_cus : 256);
+  const uint32_t hb = N <= 1536 ? 8u : 4u;
+  const dim3 grid(std::min<uint32_t>(4 * cus, ceil_div(a.M, (uint32_t)PW)), ceil_div(a.B, hb));
   switch (N) {
     case 256: hipLaunchKernelGGL((hmv_kernel<256, PRO, EPI>), grid, dim3(PT), 0, ctx->stream, a); break;
     case 1536: hipLaunchKernelGGL((hmv_kernel<1536, PRO, EPI>), grid, dim3(PT), 0, ctx->stream, a); break;
@@ -253,7 +246,7 @@ int hmv_launch(g4_ctx* ctx, const HmvArgs& a, uint32_t N) {
 int check_hmv(const char* fn, const float* x, const uint16_t* w, const float* y, uint32_t M, uint32_t N,
               uint32_t batch) {
   G4_REQUIRE(x && w && y, "%s: null buffer", fn);
-  G4_REQUIRE(M > 0 && batch >= 1, "%s: empty shape M=%u batch=%u", fn, M, batch);
+  G4_REQUIRE(M > 0 && batch >= 1 && batch <= 65535, "%s: shape M=%u batch=%u (batch 1..65535)", fn, M, batch);
   G4_REQUIRE(N == 256 || N == 1536 || N == 2048, "%s: N=%u (256, 1536 or 2048)", fn, N);
   G4_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0, "%s: x and weights must be 16-byte aligned", fn);
   return G4_OK;
