@@ -46,6 +46,8 @@ int g4_internal_argmax_final(g4_ctx* ctx, const void* parts, int nparts, uint32_
 // Weight values through the matrix-core operands (k_batch.hip; the path 2
 // of g4_dequantPath).
 int g4_internal_operand_values(g4_ctx* ctx, int wtype, const void* blocks, uint64_t nblocks, float* out);
+// Q5_K (wtype 2) / Q8_0 (wtype 3) blocks to f16 (k_ple.hip), for g4_dequantF16.
+int g4_internal_dequant_f16_q58(g4_ctx* ctx, int wtype, const void* blocks, uint64_t nblocks, uint16_t* out);
 
 // Second top-k stage (k_elem.hip): per batch row, each of the 256 residue
 // classes takes the best of its `nparts` candidates (Cand, laid out
@@ -118,6 +120,16 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
 // Round to nearest even f32 -> f16 bits (the hardware conversion).
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// v as an f32 register value. The empty asm keeps the compiler from fusing
+// the fma that produced v with a later f32 -> f16 conversion into one
+// mixed-precision fma that rounds once: the reference rounds to f32 first
+// (a Float32Array store) and then to f16, and the two can differ by one f16
+// ulp.
+__device__ __forceinline__ float as_f32(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
 }
 
 // tanh-GELU with the tanh argument clamped to +-15 (shaders/gelu_mul.wgsl:10-16).

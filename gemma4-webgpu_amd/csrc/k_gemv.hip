@@ -2089,9 +2089,11 @@ int g4_dequantPath(g4_ctx* ctx, int wtype, int path, const void* blocks, uint64_
 int g4_dequantF16(g4_ctx* ctx, int wtype, const void* blocks, uint64_t nblocks, uint16_t* out) {
   G4_ENTER(ctx);
   G4_REQUIRE(blocks && out, "g4_dequantF16: null buffer");
-  G4_REQUIRE(wtype == 0 || wtype == 1, "g4_dequantF16: wtype must be 0 (Q4_K) or 1 (Q6_K)");
+  G4_REQUIRE(wtype >= 0 && wtype <= 3, "g4_dequantF16: wtype must be 0 (Q4_K), 1 (Q6_K), 2 (Q5_K) or 3 (Q8_0)");
   G4_REQUIRE(((uintptr_t)blocks & 15) == 0 && ((uintptr_t)out & 15) == 0,
              "g4_dequantF16: blocks and out must be 16-byte aligned");
+  if (!nblocks) return G4_OK;
+  if (wtype >= 2) return g4_internal_dequant_f16_q58(ctx, wtype, blocks, nblocks, out);
   const size_t by = wtype == 0 ? 144 : 210;
   constexpr uint64_t kChunk = 1u << 24;
   for (uint64_t b0 = 0; b0 < nblocks; b0 += kChunk) {

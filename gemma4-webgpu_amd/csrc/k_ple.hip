@@ -23,16 +23,18 @@ constexpr int PT = 256;       // threads per workgroup
 constexpr int PW = PT / 64;   // waves per workgroup
 constexpr uint32_t kQ5Bytes = 176;
 
-// vectors staged in LDS per pass (at most 48 KB of f32)
+// vectors staged in LDS per workgroup (at most 48 KB of f32)
 template <int N>
-constexpr int vectors_per_pass() { return N <= 1536 ? 8 : 4; }
+constexpr int vectors_per_pass() { return N <= 1536 ? 8 : N <= 2048 ? 4 : N <= 4096 ? 2 : 1; }
+inline uint32_t vectors_per_pass_of(uint32_t N) { return N <= 1536 ? 8 : N <= 2048 ? 4 : N <= 4096 ? 2 : 1; }
 
 // Q5_K value t (0..255) of one block (src/gguf.ts:218-257): group g = t/64
 // uses sub-block j = 2g + (t/32 odd); q = 4 bits of qs[32g + l] (low nibble
 // for the first 32, high for the second) + 16 * bit j of qh[l], l = t % 32;
 // value = d*sc(j)*q - dmin*m(j) with the Q4_K scale/min packing. d*sc*q has
 // at most 22 significant bits, so the fma rounds the exact value once, as
-// the reference's f64 evaluation stored to f32 does.
+// the reference's f64 evaluation stored to f32 does; as_f32 keeps that f32
+// rounding when the caller rounds on to f16.
 __device__ __forceinline__ float q5k_value(const uint8_t* blk, int t) {
   const int g = t >> 6, hi = (t >> 5) & 1, l = t & 31, j = 2 * g + hi;
   const uint32_t dd = *(const uint32_t*)blk;
@@ -49,7 +51,7 @@ __device__ __forceinline__ float q5k_value(const uint8_t* blk, int t) {
   const int q = (hi ? (qs >> 4) : (qs & 15)) + (((blk[16 + l] >> j) & 1) << 4);
   const float d = g4d::f16_bits_to_f32(dd & 0xffffu) * (float)sc;
   const float mn = g4d::f16_bits_to_f32(dd >> 16) * (float)m;
-  return __builtin_fmaf(d, (float)q, -mn);
+  return g4d::as_f32(__builtin_fmaf(d, (float)q, -mn));
 }
 
 __device__ __forceinline__ float f16_round(float v) { return g4d::f16_bits_to_f32(g4d::f32_to_f16_bits(v)); }
@@ -86,6 +88,23 @@ __global__ __launch_bounds__(PT) void q5k_f16_kernel(const uint8_t* W, uint64_t 
   const uint64_t b = blockIdx.x;
   if (b >= nblocks) return;
   out[b * 256 + threadIdx.x] = g4d::f32_to_f16_bits(q5k_value(W + b * kQ5Bytes, (int)threadIdx.x));
+}
+
+// Q8_0 blocks (34 B: f16 d, 32 int8) to f16 (src/gguf.ts:115-131: q * d,
+// exact in f32, then rounded to f16 as the reference's upload does); thread
+// t of a workgroup takes value t of its 8 blocks.
+__global__ __launch_bounds__(PT) void q8_0_f16_kernel(const uint8_t* W, uint64_t nblocks, uint16_t* out) {
+  const uint64_t e = (uint64_t)blockIdx.x * PT + threadIdx.x, b = e / 32;
+  if (b >= nblocks) return;
+  const uint8_t* blk = W + b * 34;
+  const uint32_t dbits = (uint32_t)blk[0] | ((uint32_t)blk[1] << 8);
+  const int32_t q = (int8_t)blk[2 + e % 32];
+  // The product is exact in f32; one rounding to f16. The compiler turns
+  // the multiply into fma(d, q, +0), which loses the sign of a zero product
+  // (d = 0, q < 0 gives -0 in the reference's f64 product), so the sign is
+  // set from the operands.
+  const uint16_t h = g4d::f32_to_f16_bits(g4d::f16_bits_to_f32(dbits) * (float)q);
+  out[e] = (uint16_t)((h & 0x7fffu) | (((dbits >> 15) ^ (uint32_t)(q < 0)) << 15));
 }
 
 // shaders/ple_gelu_mul.wgsl:11-20
@@ -209,7 +228,8 @@ __global__ __launch_bounds__(PT) void hmv_kernel(HmvArgs a) {
   for (uint32_t m0 = m_first; m0 < a.M; m0 += step) {
     const uint32_t m = m0 + wv;
     const bool live = m < a.M;
-    if (m0 + step < a.M) next.load(a.W, min(m0 + step + wv, a.M - 1), lane);
+    // (rows past 4096 wide are not prefetched: two of them would not fit the registers)
+    if (N <= 4096 && m0 + step < a.M) next.load(a.W, min(m0 + step + wv, a.M - 1), lane);
     // lane v's epilogue input, for vector b0 + v of this row
     float pv = 0.f;
     if (EPI == 1 && live && (uint32_t)lane < nb) pv = a.ple[(size_t)(b0 + lane) * a.ple_stride + m];
@@ -223,7 +243,11 @@ __global__ __launch_bounds__(PT) void hmv_kernel(HmvArgs a) {
       if constexpr (EPI == 1) r = g4d::gelu_tanh(mine) * pv;
       a.y[(size_t)(b0 + lane) * a.M + m] = r;
     }
-    row = next;
+    if constexpr (N <= 4096) {
+      row = next;
+    } else if (m0 + step < a.M) {
+      row.load(a.W, min(m0 + step + wv, a.M - 1), lane);
+    }
   }
 }
 
@@ -231,13 +255,15 @@ template <int PRO, int EPI>
 int hmv_launch(g4_ctx* ctx, const HmvArgs& a, uint32_t N) {
   // about four workgroups per CU over the rows, times the vector groups
   const uint32_t cus = (uint32_t)(ctx->num_cus > 0 ? ctx->num_cus : 256);
-  const uint32_t hb = N <= 1536 ? 8u : 4u;
-  const dim3 grid(std::min<uint32_t>(4 * cus, ceil_div(a.M, (uint32_t)PW)), ceil_div(a.B, hb));
+  const dim3 grid(std::min<uint32_t>(4 * cus, ceil_div(a.M, (uint32_t)PW)), ceil_div(a.B, vectors_per_pass_of(N)));
   switch (N) {
     case 256: hipLaunchKernelGGL((hmv_kernel<256, PRO, EPI>), grid, dim3(PT), 0, ctx->stream, a); break;
     case 1536: hipLaunchKernelGGL((hmv_kernel<1536, PRO, EPI>), grid, dim3(PT), 0, ctx->stream, a); break;
     case 2048: hipLaunchKernelGGL((hmv_kernel<2048, PRO, EPI>), grid, dim3(PT), 0, ctx->stream, a); break;
-    default: return g4::set_error(G4_ERR_UNSUPPORTED, "f16 matvec: N=%u (256, 1536 or 2048)", N);
+    case 4096: hipLaunchKernelGGL((hmv_kernel<4096, PRO, EPI>), grid, dim3(PT), 0, ctx->stream, a); break;
+    case 6144: hipLaunchKernelGGL((hmv_kernel<6144, PRO, EPI>), grid, dim3(PT), 0, ctx->stream, a); break;
+    case 12288: hipLaunchKernelGGL((hmv_kernel<12288, PRO, EPI>), grid, dim3(PT), 0, ctx->stream, a); break;
+    default: return g4::set_error(G4_ERR_UNSUPPORTED, "f16 matvec: N=%u (256, 1536, 2048, 4096, 6144, 12288)", N);
   }
   G4_LAUNCHED(ctx, "hmv");
   return G4_OK;
@@ -247,12 +273,39 @@ int check_hmv(const char* fn, const float* x, const uint16_t* w, const float* y,
               uint32_t batch) {
   G4_REQUIRE(x && w && y, "%s: null buffer", fn);
   G4_REQUIRE(M > 0 && batch >= 1 && batch <= 65535, "%s: shape M=%u batch=%u (batch 1..65535)", fn, M, batch);
-  G4_REQUIRE(N == 256 || N == 1536 || N == 2048, "%s: N=%u (256, 1536 or 2048)", fn, N);
+  G4_REQUIRE(N == 256 || N == 1536 || N == 2048 || N == 4096 || N == 6144 || N == 12288,
+             "%s: N=%u (256, 1536, 2048, 4096, 6144 or 12288)", fn, N);
   G4_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0, "%s: x and weights must be 16-byte aligned", fn);
   return G4_OK;
 }
 
 }  // namespace
+
+// Q5_K (wtype 2) and Q8_0 (wtype 3) blocks to f16 for g4_dequantF16
+// (k_gemv.hip handles Q4_K and Q6_K): nblocks blocks of 256 (Q5_K) or 32
+// (Q8_0) values.
+int g4_internal_dequant_f16_q58(g4_ctx* ctx, int wtype, const void* blocks, uint64_t nblocks, uint16_t* out) {
+  constexpr uint64_t kChunk = 1u << 22;  // workgroups per launch
+  if (wtype == 2) {
+    for (uint64_t b0 = 0; b0 < nblocks; b0 += kChunk) {
+      const uint64_t nb = std::min<uint64_t>(kChunk, nblocks - b0);
+      hipLaunchKernelGGL(q5k_f16_kernel, dim3((uint32_t)nb), dim3(PT), 0, ctx->stream,
+                         (const uint8_t*)blocks + b0 * kQ5Bytes, nb, out + b0 * 256);
+      G4_LAUNCHED(ctx, "q5k_f16");
+    }
+    return G4_OK;
+  }
+  // Q8_0: 8 blocks (256 values) per workgroup
+  const uint64_t groups = (nblocks + 7) / 8;
+  for (uint64_t g0 = 0; g0 < groups; g0 += kChunk) {
+    const uint64_t ng = std::min<uint64_t>(kChunk, groups - g0);
+    const uint64_t nb = std::min<uint64_t>(ng * 8, nblocks - g0 * 8);
+    hipLaunchKernelGGL(q8_0_f16_kernel, dim3((uint32_t)ng), dim3(PT), 0, ctx->stream,
+                       (const uint8_t*)blocks + g0 * 8 * 34, nb, out + g0 * 8 * 32);
+    G4_LAUNCHED(ctx, "q8_0_f16");
+  }
+  return G4_OK;
+}
 
 extern "C" {
 
@@ -319,7 +372,7 @@ int g4_pleGate(g4_ctx* ctx, const float* x, const uint16_t* w1, const float* res
   G4_REQUIRE(ple_inputs, "g4_pleGate: null ple_inputs");
   G4_REQUIRE(!w1 == !residual, "g4_pleGate: w1 and residual go together");
   G4_REQUIRE(!w1 || batch == 1, "g4_pleGate: the norm-add prologue takes one vector");
-  G4_REQUIRE(!w1 || N != 256, "g4_pleGate: the norm-add prologue is over the hidden width");
+  G4_REQUIRE(!w1 || N == 1536 || N == 2048, "g4_pleGate: the norm-add prologue is over the hidden width");
   HmvArgs a{};
   a.W = w_gate;
   a.M = M;
@@ -333,21 +386,6 @@ int g4_pleGate(g4_ctx* ctx, const float* x, const uint16_t* w1, const float* res
   a.ple = ple_inputs + layer_offset;
   a.ple_stride = ple_stride;
   return w1 ? hmv_launch<1, 1>(ctx, a, N) : hmv_launch<0, 1>(ctx, a, N);
-}
-
-int g4_dequantQ5K_F16(g4_ctx* ctx, const void* blocks, uint64_t nblocks, uint16_t* out) {
-  G4_ENTER(ctx);
-  G4_REQUIRE(blocks && out, "g4_dequantQ5K_F16: null buffer");
-  G4_REQUIRE(((uintptr_t)blocks & 15) == 0, "g4_dequantQ5K_F16: blocks must be 16-byte aligned");
-  G4_REQUIRE(((uintptr_t)out & 1) == 0, "g4_dequantQ5K_F16: out must be 2-byte aligned");
-  constexpr uint64_t kChunk = 1u << 22;  // blocks per launch
-  for (uint64_t b0 = 0; b0 < nblocks; b0 += kChunk) {
-    const uint64_t nb = std::min<uint64_t>(kChunk, nblocks - b0);
-    hipLaunchKernelGGL(q5k_f16_kernel, dim3((uint32_t)nb), dim3(PT), 0, ctx->stream,
-                       (const uint8_t*)blocks + b0 * kQ5Bytes, nb, out + b0 * 256);
-    G4_LAUNCHED(ctx, "q5k_f16");
-  }
-  return G4_OK;
 }
 
 }  // extern "C"

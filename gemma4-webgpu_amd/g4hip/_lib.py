@@ -234,7 +234,6 @@ SIGNATURES = {
     "g4_pleSkipScaleAdd": (_I, [_P, _P, _P, _P, _U32]),
     "g4_matmulF16": (_I, [_P, _P, _P, _P, _U32, _U32, _U32]),
     "g4_pleGate": (_I, [_P, _P, _P, _P, _P, _P, _P, _U32, _U32, _P, _U32, _U32, _F, _U32]),
-    "g4_dequantQ5K_F16": (_I, [_P, _P, _U64, _P]),
     "g4_fill_q5k": (_I, [_P, _P, _U64, _U64]),
     "g4_splitmix64": (_U64, [_U64, _U64]),
     "g4_fill_q4k": (_I, [_P, _P, _U64, _U64]),

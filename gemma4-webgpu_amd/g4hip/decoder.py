@@ -265,7 +265,7 @@ class _SyntheticModel:
         Q, KV, I, hd = s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il), s.hd(il)
         prod = s.is_producer(il)
         qt = {nm: (wtypes(il, nm) if wtypes else DEFAULT_TYPES[nm]) for nm in MATRICES}
-        mk = lambda nm, M, N: self._q4k(M, N) if qt[nm] == "q4k" else self._q6k(M, N)  # noqa: E731
+        mk = lambda nm, M, N: {"q4k": self._q4k, "q6k": self._q6k, "f16": self._f16w}[qt[nm]](M, N)  # noqa: E731
         return dict(
             wq=mk("wq", Q, s.hidden), wk=mk("wk", KV, s.hidden) if prod else None,
             wv=mk("wv", KV, s.hidden) if prod else None,
@@ -311,10 +311,21 @@ class _SyntheticModel:
         if t.dims != (N, M):
             raise ValueError(f"{name}: dims {t.dims}, the layout needs ({N}, {M})")
         qt = MATVEC_TYPES.get(t.type)
-        if qt is None:
-            raise ValueError(f"{name}: {TYPE_NAMES.get(t.type, t.type)} matrices are not supported "
-                             "(the matvecs read Q4_K and Q6_K blocks)")
-        return g.upload(self.ctx, name), qt
+        if qt is not None:
+            return g.upload(self.ctx, name), qt
+        # other formats become the reference's own f16 rows (tensorToF16,
+        # src/engine.ts:570-579) and run through the f16 matvec
+        if t.type in (0, 1, 30):
+            return g.upload_f16(self.ctx, name), "f16"
+        if t.type in (8, 13):
+            raw = g.upload(self.ctx, name)
+            out = self.ctx.empty(M * N, np.uint16)
+            nblk = M * N // (32 if t.type == 8 else 256)
+            self.ctx.dequantF16("q8_0" if t.type == 8 else "q5k", raw, nblk, out)
+            self.ctx.sync()
+            raw.free()
+            return out, "f16"
+        raise ValueError(f"{name}: {TYPE_NAMES.get(t.type, t.type)} matrices are not supported")
 
     def _file_vector(self, g, name: str, n: int):
         t = g.tensor(name)
@@ -334,8 +345,6 @@ class _SyntheticModel:
                 w[nm], qt[nm] = None, DEFAULT_TYPES[nm]
                 continue
             w[nm], qt[nm] = self._file_matrix(g, f"blk.{il}.{self._FILE_MATRICES[nm]}.weight", *shapes[nm])
-        if qt["wgate"] != "q4k" or qt["wup"] != "q4k":
-            raise ValueError(f"blk.{il}: gate/up must be Q4_K (the fused gate/up launch reads Q4_K)")
         for nm, fn in self._FILE_NORMS.items():
             if nm == "k_norm" and not prod:
                 w[nm] = None
@@ -369,11 +378,14 @@ class _SyntheticModel:
                 # the tied table: the lookup reads f16 rows (src/engine.ts:599-600)
                 te, et = (head, self.lm_type) if name == "token_embd.weight" else \
                     self._file_matrix(g, "token_embd.weight", s.vocab, s.hidden)
-                self.embedding = ctx.empty(s.vocab * s.hidden, np.uint16)
-                ctx.dequantF16(et, te, s.vocab * s.hidden // 256, self.embedding)
-                if not lm_head or te is not head:
-                    ctx.sync()
-                    te.free()
+                if et == "f16":  # already the f16 rows
+                    self.embedding = te
+                else:
+                    self.embedding = ctx.empty(s.vocab * s.hidden, np.uint16)
+                    ctx.dequantF16(et, te, s.vocab * s.hidden // 256, self.embedding)
+                    if not lm_head or te is not head:
+                        ctx.sync()
+                        te.free()
         half = s.hd(s.global_layers[0]) // 2 if s.global_layers else s.head_dim // 2
         self.rope_freqs = self._file_vector(g, "rope_freqs.weight", half)
         self.ple_model_proj = self.ple_proj_norm = self.ple_table = None
@@ -399,6 +411,11 @@ class _SyntheticModel:
         b = self.ctx.alloc(nb * Q4K_BYTES)
         self.ctx.fill_q4k(b, nb, self._seed())
         return b
+
+    def _f16w(self, M: int, N: int) -> Buffer:
+        """f16 rows ~ N(0, 0.03) (a matrix the file stores in a format the
+        matvecs do not read as blocks)."""
+        return self._f16(M * N, 0.0, 0.03)
 
     def _q6k(self, M: int, N: int) -> Buffer:
         nb = M * N // 256
@@ -477,9 +494,10 @@ class Decoder(_SyntheticModel):
         # launch, read into the L2 caches by that launch (the o projection's
         # 1.8 MB arrive in time on their own: measured no faster from L2)
         self.rope_cs = self._rope_tables(max_seq)
-        self.warm = [[ctx.matmulWarmRegion("q4k", s.ffn_of(il), s.hidden, L.wgate),
-                      ctx.matmulWarmRegion("q4k", s.ffn_of(il), s.hidden, L.wup),
-                      ctx.matmulWarmRegion(L.qt["wdown"], s.hidden, s.ffn_of(il), L.wdown)]
+        self.warm = [([ctx.matmulWarmRegion("q4k", s.ffn_of(il), s.hidden, L.wgate),
+                       ctx.matmulWarmRegion("q4k", s.ffn_of(il), s.hidden, L.wup)] if self._ffn_fused(L) else []) +
+                     ([ctx.matmulWarmRegion(L.qt["wdown"], s.hidden, s.ffn_of(il), L.wdown)]
+                      if L.qt["wdown"] != "f16" else [])
                      for il, L in enumerate(self.layers)]
         ctx.fill_normal_f32(self.hidden, s.hidden, self._seed(), 0.0, 1.0)
         ctx.sync()
@@ -541,8 +559,11 @@ class Decoder(_SyntheticModel):
             c.matmulQuant(self.attn, L.wo, self.o, s.hidden, Q, L.qt["wo"])
             c.fusedNormAdd(self.o, L.post_attn_norm, self.hidden, self.hidden2, s.hidden, s.eps)
             c.rmsNorm(self.hidden2, L.pre_ffn_norm, self.normed, s.hidden, s.eps)
-            c.matmulQuantMR4(self.normed, L.wgate, self.gate, I, s.hidden)
-            c.matmulQuantMR4(self.normed, L.wup, self.up, I, s.hidden)
+            for w, y, nm in ((L.wgate, self.gate, "wgate"), (L.wup, self.up, "wup")):
+                if L.qt[nm] == "q4k":
+                    c.matmulQuantMR4(self.normed, w, y, I, s.hidden)
+                else:
+                    c.matmulQuant(self.normed, w, y, I, s.hidden, L.qt[nm])
             c.geluMul(self.gate, self.up, self.act, I)
             c.matmulQuant(self.act, L.wdown, self.down, s.hidden, I, L.qt["wdown"])
             c.fusedNormAdd(self.down, L.post_ffn_norm, self.hidden2, self.hidden, s.hidden, s.eps)
@@ -568,6 +589,30 @@ class Decoder(_SyntheticModel):
             c.topk256(self.logits, self.topk, s.vocab)
 
     # ---- the fused MI355X step ----------------------------------------------
+    def _layer_input(self, il: int):
+        """The prologue that forms layer il's normalised input: (x, w1,
+        residual, scale, w2). Layer 0 normalises the step's input; later
+        layers add the previous layer's post-FFN output (or, with per-layer
+        embeddings, its PLE tail) to the residual stream first."""
+        L = self.layers[il]
+        if il == 0:
+            return self.hidden, L.attn_norm, None, None, None
+        prev = self.layers[il - 1]
+        if self.s.ple_dim:  # (h + norm(proj out)) * layer_output_scale
+            return self.ple_out, prev.ple_post_norm, self.hidden3, prev.ple_scale, L.attn_norm
+        return self.down, prev.post_ffn_norm, self.hidden2, None, L.attn_norm
+
+    def _mv(self, qt: str, x, w, y, M: int, N: int) -> None:
+        if qt == "f16":
+            self.ctx.matmulF16(x, w, y, M, N)
+        else:
+            self.ctx.matmulQuant(x, w, y, M, N, qt)
+
+    @staticmethod
+    def _ffn_fused(L) -> bool:
+        """gate/up in one launch (Q4_K pair; the digit hand-off when down is Q6_K)."""
+        return L.qt["wgate"] == "q4k" and L.qt["wup"] == "q4k"
+
     def step_fused(self, sample: str = "argmax", advance: bool = True, warm: bool = True) -> None:
         """One token at position *pos (device), then pos += 1 on the device.
 
@@ -590,74 +635,88 @@ class Decoder(_SyntheticModel):
         attention launch forms and stores no K/V row. With the embedding
         table, an embedding lookup of the device-side token (the previous
         step's sample) starts the step.
+
+        Matrices held as f16 rows (a file's Q5_K, Q8_0, F16, BF16 or F32
+        matrices) take the f16 matvec: their group's norm is formed by a
+        launch of its own, and an f16 gate or up makes the FFN unfused
+        (norm launch, two matvecs, GELU product); an f16 LM head is followed
+        by the softcap and the argmax / top-k launches.
         """
         c, s = self.ctx, self.s
+        H = s.hidden
         if self.embedding is not None:
-            c.embeddingLookup(self.embedding, s.vocab, self.hidden, s.hidden, token_dev=self.token)
+            c.embeddingLookup(self.embedding, s.vocab, self.hidden, H, token_dev=self.token)
         if s.ple_dim:
             self._ple_stage1()
         for il, L in enumerate(self.layers):
             Q, KV, I = s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il)
             prod = s.is_producer(il)
             outs, rows = ([self.q, self.k, self.v], [Q, KV, KV]) if prod else ([self.q], [Q])
-            # one launch per weight format among q/k/v; a second launch
+            x, w1, res, scale, w2 = self._layer_input(il)
+            # one launch per weight format among q/k/v; a later launch
             # recomputes the norm from the same inputs and writes no h_out
             for gi, (qt, ws, go, gr) in enumerate(qkv_groups(L, outs, rows)):
-                h_out = None if gi else self.hidden
-                if il == 0:
-                    c.normAddMatmulSegments(qt, self.hidden, L.attn_norm, None, None, None, ws, go, gr,
-                                            s.hidden, s.eps)
-                elif s.ple_dim:  # the previous layer's PLE tail: (h + norm(proj out)) * scale
-                    prev = self.layers[il - 1]
-                    c.normAddScaleMatmulSegments(qt, self.ple_out, prev.ple_post_norm, self.hidden3, prev.ple_scale,
-                                                 L.attn_norm, h_out, ws, go, gr, s.hidden, s.eps)
+                h_out = None if gi or il == 0 else self.hidden
+                if qt == "f16":
+                    c.batchPrepScale(x, 1, w1, res, scale, w2, h_out, self.normed, H, 1, s.eps)
+                    for w, y, r in zip(ws, go, gr):
+                        c.matmulF16(self.normed, w, y, r, H)
                 else:
-                    prev = self.layers[il - 1]
-                    c.normAddMatmulSegments(qt, self.down, prev.post_ffn_norm, self.hidden2, L.attn_norm,
-                                            h_out, ws, go, gr, s.hidden, s.eps)
+                    c.normAddScaleMatmulSegments(qt, x, w1, res, scale, w2, h_out, ws, go, gr, H, s.eps)
             c.attnDecodeFusedWarm(self.q, self.k if prod else None, self.v if prod else None, L.q_norm, L.k_norm,
                                   self.rope_freqs, L.k_cache, L.v_cache, self.attn, self.attn_params[il],
                                   self.attn_ws, self.pos, self.warm[il] if warm else [],
                                   self.rope_cs[s.is_global(il)], self.rope_rows)
-            c.matmulQuant(self.attn, L.wo, self.o, s.hidden, Q, L.qt["wo"])
-            c.normAddGateUpGeluDigits_q4k(self.o, L.post_attn_norm, self.hidden, L.pre_ffn_norm, L.wgate, L.wup,
-                                          self.hidden2, self.act, self.act_digits, I, s.hidden, s.eps)
-            if L.qt["wdown"] == "q6k":
-                c.matmulQuantDigits_q6k(self.act_digits, L.wdown, self.down, s.hidden, I)
+            self._mv(L.qt["wo"], self.attn, L.wo, self.o, H, Q)
+            if self._ffn_fused(L):
+                c.normAddGateUpGeluDigits_q4k(self.o, L.post_attn_norm, self.hidden, L.pre_ffn_norm, L.wgate, L.wup,
+                                              self.hidden2, self.act, self.act_digits, I, H, s.eps)
             else:
-                c.matmulQuant(self.act, L.wdown, self.down, s.hidden, I, L.qt["wdown"])
+                c.batchPrepScale(self.o, 1, L.post_attn_norm, self.hidden, None, L.pre_ffn_norm, self.hidden2,
+                                 self.normed, H, 1, s.eps)
+                self._mv(L.qt["wgate"], self.normed, L.wgate, self.gate, I, H)
+                self._mv(L.qt["wup"], self.normed, L.wup, self.up, I, H)
+                c.geluMul(self.gate, self.up, self.act, I)
+            if L.qt["wdown"] == "q6k" and self._ffn_fused(L):
+                c.matmulQuantDigits_q6k(self.act_digits, L.wdown, self.down, H, I)
+            else:
+                self._mv(L.qt["wdown"], self.act, L.wdown, self.down, H, I)
             if s.ple_dim:
                 # post-FFN norm-add -> inp_gate -> gelu * ple_inputs, then proj
                 D = s.ple_dim
                 c.pleGate(self.down, L.post_ffn_norm, self.hidden2, self.hidden3, L.ple_gate, self.ple_inputs, 0,
-                          il * D, self.ple_gated, D, s.hidden, s.eps)
-                c.matmulF16(self.ple_gated, L.ple_proj, self.ple_out, s.hidden, D)
+                          il * D, self.ple_gated, D, H, s.eps)
+                c.matmulF16(self.ple_gated, L.ple_proj, self.ple_out, H, D)
         last = self.layers[-1]
         if s.ple_dim:
             # the last PLE tail on its own (one vector), then the head normalises it
             c.batchPrepScale(self.ple_out, 1, last.ple_post_norm, self.hidden3, last.ple_scale, None, self.hidden,
-                             self.normed, s.hidden, 1, s.eps)
-            if self.lm_head is not None:
-                if sample == "argmax":
-                    c.normAddMatmulArgmax(self.lm_type, self.hidden, self.final_norm, None, None, None, self.lm_head,
-                                          self.logits, s.vocab, s.hidden, self.token, s.eps, softcap=s.softcap,
-                                          positions=self.pos if advance else None, delta=1)
-                    return
-                c.normAddMatmulTopk(self.lm_type, self.hidden, self.final_norm, None, None, None, self.lm_head,
-                                    self.logits, s.vocab, s.hidden, self.topk, s.eps, softcap=s.softcap)
-            if advance:
-                c.advancePosition(self.pos, 1)
-            return
-        if self.lm_head is not None:
-            if sample == "argmax":
-                c.normAddMatmulArgmax(self.lm_type, self.down, last.post_ffn_norm, self.hidden2, self.final_norm,
-                                      self.hidden, self.lm_head, self.logits, s.vocab, s.hidden, self.token, s.eps,
-                                      softcap=s.softcap, positions=self.pos if advance else None, delta=1)
-                return
-            c.normAddMatmulTopk(self.lm_type, self.down, last.post_ffn_norm, self.hidden2, self.final_norm, self.hidden,
-                                 self.lm_head, self.logits, s.vocab, s.hidden, self.topk, s.eps, softcap=s.softcap)
+                             self.normed, H, 1, s.eps)
+            x, w1, res, w2, h_out = self.hidden, self.final_norm, None, None, None
         else:
-            c.fusedNormAdd(self.down, last.post_ffn_norm, self.hidden2, self.hidden, s.hidden, s.eps)
+            x, w1, res, w2, h_out = self.down, last.post_ffn_norm, self.hidden2, self.final_norm, self.hidden
+        if self.lm_head is None:
+            if not s.ple_dim:
+                c.fusedNormAdd(self.down, last.post_ffn_norm, self.hidden2, self.hidden, H, s.eps)
+        elif self.lm_type == "f16":
+            c.batchPrepScale(x, 1, w1, res, None, w2, h_out, self.normed, H, 1, s.eps)
+            c.matmulF16(self.normed, self.lm_head, self.logits, s.vocab, H)
+            c.logitSoftcap(self.logits, s.vocab, s.softcap)
+            if sample == "argmax":
+                if advance:
+                    c.argmaxAdvance(self.logits, self.token, s.vocab, 1, self.pos, 1)
+                    return
+                c.argmax(self.logits, self.token, s.vocab)
+            else:
+                c.topk256(self.logits, self.topk, s.vocab)
+        elif sample == "argmax":
+            c.normAddMatmulArgmax(self.lm_type, x, w1, res, w2, h_out, self.lm_head, self.logits, s.vocab, H,
+                                  self.token, s.eps, softcap=s.softcap, positions=self.pos if advance else None,
+                                  delta=1)
+            return
+        else:
+            c.normAddMatmulTopk(self.lm_type, x, w1, res, w2, h_out, self.lm_head, self.logits, s.vocab, H,
+                                self.topk, s.eps, softcap=s.softcap)
         if advance:
             c.advancePosition(self.pos, 1)
 
@@ -674,13 +733,20 @@ class Decoder(_SyntheticModel):
         where the attention takes a launch and a merge: head dim 512, or a
         window longer than the one-launch plan's), the head with its argmax
         candidates (1) and their reduction, which also advances the position
-        (1), and the embedding lookup when there is a table."""
+        (1), and the embedding lookup when there is a table; with per-layer
+        embeddings 2 before the layers, 2 per layer and the last tail; more
+        where a layer's matrices mix formats or are f16 rows."""
         s, n = self.s, 2 + (self.embedding is not None)
         if s.ple_dim:  # stage 1 (2), two per layer, the last tail (1)
             n += 3 + 2 * s.n_layers
+        if self.lm_head is not None and self.lm_type == "f16":  # norm, matvec, softcap, two argmax stages
+            n += 3
         for il, L in enumerate(self.layers):
-            n += 5 + (not self.ctx.attn_fused_single_launch(self.attn_params[il]))
-            n += len(qkv_groups(L, [0, 0, 0][:3 if s.is_producer(il) else 1], [0, 0, 0])) - 1
+            n += 4 + (not self.ctx.attn_fused_single_launch(self.attn_params[il]))
+            for qt, ws, _, _ in qkv_groups(L, [0, 0, 0][:3 if s.is_producer(il) else 1], [0, 0, 0]):
+                n += 1 + (len(ws) if qt == "f16" else 0)
+            if not self._ffn_fused(L):
+                n += 3  # norm, second matvec, GELU product
         return n
 
 
@@ -757,6 +823,9 @@ class BatchDecoder(_SyntheticModel):
         self.o_parts = ctx.empty(self.ks_q * B * s.hidden, f32)
         self.act = ctx.empty(B * s.max_ffn, f32)
         self.down_parts = ctx.empty(self.ks_f * B * s.hidden, f32)
+        if any(not (L.qt["wgate"] == "q4k" and L.qt["wup"] == "q4k") for L in self.layers):
+            self.gate_b = ctx.empty(B * s.max_ffn, f32)  # gate and up of a layer that does not pair them
+            self.up_b = ctx.empty(B * s.max_ffn, f32)
         self.logits = ctx.empty(B * s.vocab, f32) if lm_head else None
         self.tokens = ctx.zeros(B, np.uint32)
         self.topk = ctx.empty(B * 512, f32)
@@ -853,8 +922,14 @@ class BatchDecoder(_SyntheticModel):
                             self.xn, H, B, s.eps, ops=self.xops)
             # a layer reading a producer's pool projects q only and appends no row
             outs = [self.q_parts, self.k_parts, self.v_parts] if prod else [self.q_parts]
-            nq = 0
-            for qt, ws, go, gr in qkv_groups(L, outs, [Q, KV, KV] if prod else [Q]):
+            groups = qkv_groups(L, outs, [Q, KV, KV] if prod else [Q])
+            # f16 rows write whole sums (one chunk), so the block formats then split K once too
+            nq = 1 if any(g[0] == "f16" for g in groups) else 0
+            for qt, ws, go, gr in groups:
+                if qt == "f16":
+                    for w, y, r in zip(ws, go, gr):
+                        c.matmulF16(self.xn, w, y, r, H, B)
+                    continue
                 # a later format's launch takes the first one's K split (the
                 # prologue adds one chunk count): its fewer rows never pick fewer
                 k = c.matmulSegmentsBatchPartial(qt, self.xn, ws, go, gr, H, B, nq or self.ks_h, ops=self.xops)
@@ -868,13 +943,16 @@ class BatchDecoder(_SyntheticModel):
             ops = self.aops if s.hd(il) % 256 == 0 else None
             c.pagedAttnDecode(self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.attn,
                               self.attn_params[il], self.attn_ws, ops=ops)
-            no = c.matmulSegmentsBatchPartial(L.qt["wo"], self.attn, [L.wo], [self.o_parts], [H], Q, B, self.ks_q,
-                                              ops=ops)
+            no = self._mm_batch(L.qt["wo"], self.attn, L.wo, self.o_parts, H, Q, self.ks_q, ops)
             c.batchPrep(self.o_parts, no, L.post_attn_norm, self.hidden, L.pre_ffn_norm, self.hidden2, self.xn, H, B,
                         s.eps, ops=self.xops)
-            c.gateUpGeluBatch(self.xn, L.wgate, L.wup, self.act, I, H, B, ops=self.xops)
-            nd = c.matmulSegmentsBatchPartial(L.qt["wdown"], self.act, [L.wdown], [self.down_parts], [H], I, B,
-                                              self.ks_f)
+            if L.qt["wgate"] == "q4k" and L.qt["wup"] == "q4k":
+                c.gateUpGeluBatch(self.xn, L.wgate, L.wup, self.act, I, H, B, ops=self.xops)
+            else:  # gate and up apart (whole sums), then the GELU product
+                self._mm_batch(L.qt["wgate"], self.xn, L.wgate, self.gate_b, I, H, 1, self.xops)
+                self._mm_batch(L.qt["wup"], self.xn, L.wup, self.up_b, I, H, 1, self.xops)
+                c.geluMul(self.gate_b, self.up_b, self.act, B * I)
+            nd = self._mm_batch(L.qt["wdown"], self.act, L.wdown, self.down_parts, H, I, self.ks_f, None)
             if s.ple_dim:
                 # post-FFN norm-add (h, no second norm) -> inp_gate -> gelu * ple_inputs -> proj
                 D = s.ple_dim
@@ -891,13 +969,26 @@ class BatchDecoder(_SyntheticModel):
             c.batchPrep(self.down_parts, nd, last.post_ffn_norm, self.hidden2, self.final_norm, self.hidden, self.xn,
                         H, B, s.eps, ops=self.xops)
         if self.lm_head is not None:
-            c.matmulSegmentsBatchPartial(self.lm_type, self.xn, [self.lm_head], [self.logits], [s.vocab], H, B, 1,
-                                         ops=self.xops, softcap=s.softcap)
+            if self.lm_type == "f16":
+                c.matmulF16(self.xn, self.lm_head, self.logits, s.vocab, H, B)
+                c.logitSoftcap(self.logits, B * s.vocab, s.softcap)
+            else:
+                c.matmulSegmentsBatchPartial(self.lm_type, self.xn, [self.lm_head], [self.logits], [s.vocab], H, B,
+                                             1, ops=self.xops, softcap=s.softcap)
             if sample == "argmax":
                 c.argmaxBatch(self.logits, self.tokens, s.vocab, B)
             else:
                 c.topk256Batch(self.logits, self.topk, s.vocab, B)
         self.lens_host = self.lens_host + 1
+
+    def _mm_batch(self, qt: str, x, w, y, M: int, N: int, max_ksplit: int, ops) -> int:
+        """y = W . x for the B rows: f16 rows through the f16 matvec (one
+        chunk), block formats split-K into at most max_ksplit chunks. Returns
+        the chunk count."""
+        if qt == "f16":
+            self.ctx.matmulF16(x, w, y, M, N, self.B)
+            return 1
+        return self.ctx.matmulSegmentsBatchPartial(qt, x, [w], [y], [M], N, self.B, max_ksplit, ops=ops)
 
     def prefill(self, tokens, start: int = 0, sample: str = "argmax") -> int:
         """Batched prefill of one sequence (a shared_pages decoder with an

@@ -328,8 +328,6 @@ class Context:
         check(lib().g4_pleGate(self.h, _p(x), _p(w1), _p(residual), _p(h_out), _p(w_gate), _p(ple_inputs),
                                ple_stride, layer_offset, _p(out), M, N, eps, batch))
 
-    def dequantQ5K_F16(self, blocks: Ptr, nblocks: int, out: Ptr) -> None:
-        check(lib().g4_dequantQ5K_F16(self.h, _p(blocks), nblocks, _p(out)))
 
     def gateUpGeluBatch(self, x: Ptr, w_gate: Ptr, w_up: Ptr, out: Ptr, M: int, N: int, batch: int,
                         ops: Ptr = None) -> None:
@@ -582,8 +580,10 @@ class Context:
         check(lib().g4_dequantPath(self.h, {"q4k": 0, "q6k": 1}[wtype], path, _p(blocks), nblocks, _p(out)))
 
     def dequantF16(self, wtype: str, blocks: Ptr, nblocks: int, out: Ptr) -> None:
-        """Blocks to f16 values (round to nearest even of the f32 dequant)."""
-        check(lib().g4_dequantF16(self.h, {"q4k": 0, "q6k": 1}[wtype], _p(blocks), nblocks, _p(out)))
+        """Blocks ("q4k", "q6k", "q5k": 256 values; "q8_0": 32) to f16 values
+        (round to nearest even of the f32 dequant)."""
+        check(lib().g4_dequantF16(self.h, {"q4k": 0, "q6k": 1, "q5k": 2, "q8_0": 3}[wtype], _p(blocks), nblocks,
+                                  _p(out)))
 
     def streamRead(self, src: Ptr, nbytes: int, policy: int, nwgs: int, sink: Ptr) -> None:
         """Measurement probe: one pass of 16-byte loads over nbytes (policy 0

@@ -804,7 +804,8 @@ napi_value GgufUploadF16(napi_env env, napi_callback_info info) {
   return done(env, g4_gguf_upload_f16(c, g, idx, dst, (size_t)n));
 }
 
-// dequantF16(ctx, 'q4k' | 'q6k', blocks, nblocks, out): blocks to f16 rows
+// dequantF16(ctx, 'q4k' | 'q6k' | 'q5k' | 'q8_0', blocks, nblocks, out):
+// blocks (256 values; Q8_0: 32) to f16 rows
 napi_value DequantF16(napi_env env, napi_callback_info info) {
   Args a(env, info);
   g4_ctx* c = CTX(a, 0);
@@ -813,11 +814,12 @@ napi_value DequantF16(napi_env env, napi_callback_info info) {
   const uint64_t n = a.u64(3);
   uint16_t* out = U16P(a, 4);
   CHECKED(a);
-  if (t != "q4k" && t != "q6k") {
-    a.fail("dequantF16: wtype must be 'q4k' or 'q6k'");
+  const int w = t == "q4k" ? 0 : t == "q6k" ? 1 : t == "q5k" ? 2 : t == "q8_0" ? 3 : -1;
+  if (w < 0) {
+    a.fail("dequantF16: wtype must be 'q4k', 'q6k', 'q5k' or 'q8_0'");
     return nullptr;
   }
-  return done(env, g4_dequantF16(c, t == "q4k" ? 0 : 1, b, n, out));
+  return done(env, g4_dequantF16(c, w, b, n, out));
 }
 
 struct Entry {

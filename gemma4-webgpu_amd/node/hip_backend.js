@@ -146,7 +146,8 @@ const PLE_TENSORS = ['inp_gate', 'proj', 'post_norm', 'layer_output_scale'];
 // the matrices' block formats unless a layer says otherwise
 const DEFAULT_FORMATS = { attn_q: 'q4k', attn_k: 'q4k', attn_v: 'q4k', attn_output: 'q4k', ffn_gate: 'q4k',
   ffn_up: 'q4k', ffn_down: 'q6k' };
-const BLOCK_BYTES = { q4k: 144, q6k: 210 };
+// bytes per 256 values: Q4_K / Q6_K blocks, or f16 rows
+const BLOCK_BYTES = { q4k: 144, q6k: 210, f16: 512 };
 
 class HipBackend {
   // addon: the g4hip.node exports (or any object with the same functions);
@@ -163,7 +164,7 @@ class HipBackend {
     this.trace = o.trace || null;
     this.owned = [];
     this.layers = [];      // per layer: {tensor name: handle}
-    this.formats = [];     // per layer: {matrix name: 'q4k' | 'q6k'}
+    this.formats = [];     // per layer: {matrix name: 'q4k' | 'q6k' | 'f16'}
     this.globals = {};     // tokenEmbed (f16), lmHead (+ lmHeadFormat), finalNorm, rope_freqs,
                            // perLayerModelProj / perLayerProjNorm (f16), perLayerTable (Q5_K)
     this.workBuffers = {};
@@ -177,11 +178,13 @@ class HipBackend {
   }
 
   // A backend holding a GGUF file's weights (GGUFParser + the upload of
-  // src/engine.ts:547-625, without the f16 expansion): each layer matrix as
-  // the file's Q4_K / Q6_K blocks, norms and the per-layer-embedding
-  // matrices as f16, the tied token table as the LM head's blocks and the
-  // lookup's f16 rows, the per-layer table as its Q5_K blocks. opts as the
-  // constructor's, plus device and maxContextLength.
+  // src/engine.ts:547-625): each layer matrix as the file's Q4_K / Q6_K
+  // blocks, and a matrix in another format (F32, F16, BF16, Q5_K, Q8_0) as
+  // the reference's f16 rows (tensorToF16, src/engine.ts:570-579); norms and
+  // the per-layer-embedding matrices as f16, the tied token table as the LM
+  // head's blocks (or rows) and the lookup's f16 rows, the per-layer table as
+  // its Q5_K blocks. opts as the constructor's, plus device and
+  // maxContextLength.
   static fromGGUF(file, opts) {
     const o = opts || {};
     const addon = loadAddon();
@@ -228,10 +231,33 @@ class HipBackend {
       g.ggufUploadF16(this.ctx, gg, t.index, p, Math.max(n, 2));
       return p;
     };
+    // GGUF types held as f16 rows: F32, F16, BF16 converted on upload;
+    // Q8_0 and Q5_K dequantized on the device
+    const ROWS = { 0: null, 1: null, 30: null, 8: ['q8_0', 32], 13: ['q5k', 256] };
     const matFormat = (name) => {
-      const f = FMT[get(name).type];
-      if (!f) throw new Error(name + ': tensor type ' + get(name).type + ' (the matvecs read Q4_K and Q6_K)');
-      return f;
+      const ty = get(name).type;
+      if (FMT[ty]) return FMT[ty];
+      if (ROWS[ty] !== undefined) return 'f16';
+      throw new Error(name + ': tensor type ' + ty + ' (Q4_K, Q6_K, Q5_K, Q8_0, F16, BF16 or F32 matrices)');
+    };
+    const matrix = (name) => {
+      const t = get(name);
+      if (FMT[t.type]) return raw(name);
+      const dq = ROWS[t.type];
+      if (dq === undefined) matFormat(name);  // throws
+      if (dq === null) return f16(name);
+      let n = 1;
+      for (const d of t.dims) n *= d;
+      const tmp = g.alloc(this.ctx, t.nbytes);
+      try {
+        g.ggufUpload(this.ctx, gg, t.index, tmp, t.nbytes);
+        const p = this.alloc(2 * n);
+        g.dequantF16(this.ctx, dq[0], tmp, n / dq[1], p);
+        g.sync(this.ctx);
+        return p;
+      } finally {
+        g.free(this.ctx, tmp);
+      }
     };
     const MATS = ['attn_q', 'attn_k', 'attn_v', 'attn_output', 'ffn_gate', 'ffn_up', 'ffn_down'];
     const F16S = ['attn_norm', 'attn_q_norm', 'attn_k_norm', 'post_attention_norm', 'ffn_norm', 'post_ffw_norm',
@@ -247,18 +273,23 @@ class HipBackend {
       const need = Object.keys(this.layerTensorBytes(il, formats));
       const t = {};
       for (const name of need) {
-        t[name] = F16S.indexOf(name) >= 0 ? f16(prefix + name + '.weight') : raw(prefix + name + '.weight');
+        t[name] = F16S.indexOf(name) >= 0 ? f16(prefix + name + '.weight') : matrix(prefix + name + '.weight');
       }
       this.setLayerWeights(il, t, formats);
     }
     const glob = { finalNorm: f16('output_norm.weight'), rope_freqs: f16('rope_freqs.weight') };
     const headName = tensors['output.weight'] ? 'output.weight' : 'token_embd.weight';
-    glob.lmHead = raw(headName);
+    glob.lmHead = matrix(headName);
     glob.lmHeadFormat = matFormat(headName);
-    // the tied table's f16 rows for the lookup, from the same blocks
-    const te = headName === 'token_embd.weight' ? glob.lmHead : raw('token_embd.weight');
-    glob.tokenEmbed = this.alloc(2 * C.vocab_size * C.hidden_size);
-    g.dequantF16(this.ctx, matFormat('token_embd.weight'), te, C.vocab_size * C.hidden_size / 256, glob.tokenEmbed);
+    // the tied table's f16 rows for the lookup, from the same blocks (or rows)
+    const te = headName === 'token_embd.weight' ? glob.lmHead : matrix('token_embd.weight');
+    const teFormat = matFormat('token_embd.weight');
+    if (teFormat === 'f16') {
+      glob.tokenEmbed = te;
+    } else {
+      glob.tokenEmbed = this.alloc(2 * C.vocab_size * C.hidden_size);
+      g.dequantF16(this.ctx, teFormat, te, C.vocab_size * C.hidden_size / 256, glob.tokenEmbed);
+    }
     if (C.per_layer_input_dim > 0) {
       glob.perLayerModelProj = f16('per_layer_model_proj.weight');
       glob.perLayerProjNorm = f16('per_layer_proj_norm.weight');

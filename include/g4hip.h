@@ -584,10 +584,13 @@ int g4_dequant_q6k(g4_ctx* ctx, const void* blocks, uint64_t nblocks, float* out
  * Paths 0 and 1 are bit-exact with the reference's f32 values. */
 int g4_dequantPath(g4_ctx* ctx, int wtype, int path, const void* blocks, uint64_t nblocks, float* out);
 
-/* Q4_K (wtype 0) or Q6_K (1) blocks to f16 values, rounded to nearest even
- * from the f32 values of g4_dequantPath's path 0 (tensorToF16,
- * src/engine.ts:570-579, for the tied token embedding table the lookup
- * reads). blocks and out 16-byte aligned; out holds nblocks * 256 values. */
+/* Blocks to f16 values, each the reference's f32 dequantized value rounded
+ * to nearest even (tensorToF16, src/engine.ts:570-579): wtype 0 Q4_K and 1
+ * Q6_K (the f32 values of g4_dequantPath's path 0; the tied token table the
+ * lookup reads), 2 Q5_K (src/gguf.ts:218-257; the per-layer table's values
+ * and Q5_K matrices), 3 Q8_0 (src/gguf.ts:115-131; nblocks of 32 values).
+ * blocks and out 16-byte aligned; out holds nblocks * 256 values (Q8_0:
+ * nblocks * 32). */
 int g4_dequantF16(g4_ctx* ctx, int wtype, const void* blocks, uint64_t nblocks, uint16_t* out);
 
 /* Measurement probe: reads bytes of src once with 16-byte loads (nwgs
@@ -619,7 +622,8 @@ int g4_pleGeluMul(g4_ctx* ctx, const float* gate, const float* ple_inputs, float
 /* shaders/ple_skip_scale_add.wgsl: hidden[i] = (hidden[i] + post_normed[i]) * f32(scale[0]). */
 int g4_pleSkipScaleAdd(g4_ctx* ctx, float* hidden, const float* post_normed, const uint16_t* scale,
                        uint32_t size);
-/* y[b][m] = W[m] . x[b] for f16 rows W [M][N] (N 256, 1536 or 2048) and
+/* y[b][m] = W[m] . x[b] for f16 rows W [M][N] (N 256, 1536, 2048, 4096, 6144
+ * or 12288) and
  * `batch` f32 vectors: the reference's matmulQuant on its f16 weights
  * (shaders/matmul_quant.wgsl), as PLE runs it for per_layer_model_proj,
  * inp_gate and proj (src/engine.ts:1521-1524, 1611, 1613). */
@@ -633,9 +637,6 @@ int g4_matmulF16(g4_ctx* ctx, const float* x, const uint16_t* weight, float* y, 
 int g4_pleGate(g4_ctx* ctx, const float* x, const uint16_t* w1, const float* residual, float* h_out,
                const uint16_t* w_gate, const float* ple_inputs, uint32_t ple_stride, uint32_t layer_offset,
                float* out, uint32_t M, uint32_t N, float eps, uint32_t batch);
-/* Q5_K blocks to f16 values (src/gguf.ts:218-257 values rounded to nearest
- * even, as the per-layer table is uploaded, src/engine.ts:626-700). */
-int g4_dequantQ5K_F16(g4_ctx* ctx, const void* blocks, uint64_t nblocks, uint16_t* out);
 
 /* GGUF v2/v3 model files (replaces GGUFParser, src/gguf.ts:75-101 header,
  * :103-134 key/values, :136-160 tensor infos and data offset, :385-395 tensor

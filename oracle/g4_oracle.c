@@ -173,6 +173,16 @@ void g4o_dequant_q6k(const uint8_t* blocks, size_t nblocks, float* out) {
   }
 }
 
+/* src/gguf.ts:115-131 (dequantizeQ8_0): 34-byte blocks, f16 d then 32
+ * int8 q; value = q * d (exact in f32: 8 x 11 significant bits). */
+void g4o_dequant_q8_0(const uint8_t* blocks, size_t nblocks, float* out) {
+  for (size_t b = 0; b < nblocks; ++b) {
+    const uint8_t* blk = blocks + b * 34;
+    const double d = g4o_f16_to_f32(rd16(blk));
+    for (int i = 0; i < 32; ++i) out[b * 32 + i] = (float)((double)(int8_t)blk[2 + i] * d);
+  }
+}
+
 /* src/gguf.ts:218-257 (decodeQ5_KBlock). 176-byte block: f16 d @0, f16
  * dmin @2, the 12 packed 6-bit scale/min bytes of Q4_K @4, qh[32] @16,
  * qs[128] @48. Group g (values 64g .. 64g+63) uses sub-blocks 2g and 2g+1:

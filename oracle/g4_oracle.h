@@ -29,6 +29,7 @@ void g4o_q4k_scale_min(const uint8_t scales12[12], int j, int* sc, int* m);
 void g4o_dequant_q4k(const uint8_t* blocks, size_t nblocks, float* out);
 void g4o_dequant_q6k(const uint8_t* blocks, size_t nblocks, float* out);
 void g4o_dequant_q5k(const uint8_t* blocks, size_t nblocks, float* out); /* src/gguf.ts:218-257 */
+void g4o_dequant_q8_0(const uint8_t* blocks, size_t nblocks, float* out); /* src/gguf.ts:115-131 */
 
 /* ---- matvec (shaders/matmul_quant.wgsl:12-54; rows M, reduction N) ---- */
 void g4o_matmul_f32w(const float* x, const float* W, float* y, uint32_t M, uint32_t N);

@@ -64,6 +64,7 @@ def _declare(L):
         "g4o_dequant_q4k": (None, [_P, _SZ, _P]),
         "g4o_dequant_q6k": (None, [_P, _SZ, _P]),
         "g4o_dequant_q5k": (None, [_P, _SZ, _P]),
+        "g4o_dequant_q8_0": (None, [_P, _SZ, _P]),
         "g4o_ple_stage1": (None, [_P, _P, _P, _P, _U32, _U32, _F]),
         "g4o_ple_skip_scale_add": (None, [_P, _P, ctypes.c_uint16, _U32]),
         "g4o_matmul_f32w": (None, [_P, _P, _P, _U32, _U32]),
@@ -156,6 +157,40 @@ def dequant_q5k(blocks: np.ndarray) -> np.ndarray:
     out = np.empty(n * QK, np.float32)
     lib().g4o_dequant_q5k(_p(b), n, _p(out))
     return out
+
+
+def dequant_q8_0(blocks: np.ndarray) -> np.ndarray:
+    b = _c(blocks, np.uint8).reshape(-1)
+    assert b.size % 34 == 0
+    n = b.size // 34
+    out = np.empty(n * 32, np.float32)
+    lib().g4o_dequant_q8_0(_p(b), n, _p(out))
+    return out
+
+
+def dequant_f16_rows(raw: np.ndarray, ggml_type: int) -> np.ndarray:
+    """A GGUF tensor's values as the reference uploads them (tensorToF16,
+    src/engine.ts:570-579): dequantized to f32 (src/gguf.ts:370-381), then
+    f16 bits rounded to nearest even (the Float16Array path)."""
+    raw = _c(raw, np.uint8).reshape(-1)
+    if ggml_type == 0:
+        f = raw.view(np.float32)
+    elif ggml_type == 1:
+        return raw.view(np.uint16).copy()
+    elif ggml_type == 30:
+        f = (raw.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    elif ggml_type == 8:
+        f = dequant_q8_0(raw)
+    elif ggml_type == 12:
+        f = dequant_q4k(raw)
+    elif ggml_type == 13:
+        f = dequant_q5k(raw)
+    elif ggml_type == 14:
+        f = dequant_q6k(raw)
+    else:
+        raise ValueError(f"tensor type {ggml_type}")
+    with np.errstate(over="ignore", invalid="ignore"):
+        return f.astype(np.float16).view(np.uint16)
 
 
 def matmul(x: np.ndarray, W: np.ndarray, M: int, N: int, wtype: str) -> np.ndarray:

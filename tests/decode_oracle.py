@@ -54,9 +54,15 @@ class HostModel:
             self.ple = dict(model_proj=dec.ple_model_proj.download(u16), proj_norm=dec.ple_proj_norm.download(u16),
                             table=dec.ple_table)
         self.qt = [dict(getattr(L, "qt", DEFAULT_TYPES)) for L in dec.layers]  # each matrix's format
+        for W, qt in zip(self.layers, self.qt):  # f16 rows as f16 bits
+            for k, t in qt.items():
+                if t == "f16" and k in W:
+                    W[k] = W[k].view(np.uint16)
         self.final_norm = dec.final_norm.download(u16)
         self.lm_type = getattr(dec, "lm_type", "q6k")
         self.lm_head = dec.lm_head.download(u8) if dec.lm_head is not None else None
+        if self.lm_head is not None and self.lm_type == "f16":
+            self.lm_head = self.lm_head.view(np.uint16)
         self.embedding = getattr(dec, "embedding", None)  # device table: rows are fetched on demand
 
     def embed(self, token: int):

@@ -218,16 +218,17 @@ check('device-side token and position: the pass reads them, the sample advances 
   assert.throws(() => be.setLayerWeights(0, {}), /missing tensor/);
 });
 
-check('per-tensor block formats: sizes, wtypes, the LM head and the 4-row gate/up only for Q4_K', () => {
+check('per-tensor formats: sizes, wtypes, f16 rows, the LM head and the 4-row gate/up only for Q4_K', () => {
   const C = hb.e2bConfig({ num_layers: 2, num_unshared_layers: 2, global_layers: [1], vocab_size: 4096,
     per_layer_input_dim: 0 });
   const m = mockAddon();
   const be = new hb.HipBackend(m, 'ctx', C, { maxSeqLen: 1024 });
   be.allocate();
-  const F = { attn_v: 'q6k', ffn_down: 'q4k' };
+  const F = { attn_v: 'q6k', ffn_down: 'q4k', attn_output: 'f16' };
   const sizes = be.layerTensorBytes(0, F);
   assert.strictEqual(sizes.attn_v, 256 * 1536 / 256 * 210);
   assert.strictEqual(sizes.ffn_down, 1536 * 6144 / 256 * 144);
+  assert.strictEqual(sizes.attn_output, 2 * 1536 * 2048);
   assert.strictEqual(sizes.inp_gate, undefined);
   const t = (il, f) => {
     const o = {};
@@ -243,6 +244,8 @@ check('per-tensor block formats: sizes, wtypes, the LM head and the 4-row gate/u
   const mq = m.calls.filter((c) => c[0] === 'matmulQuant' || c[0] === 'matmulQuantMR4');
   const fmt = (name) => mq.filter((c) => c[3] === name)[0];
   assert.strictEqual(fmt('attn_v0')[6], 'q6k');
+  assert.strictEqual(fmt('attn_output0')[6], 'f16');
+  assert.strictEqual(fmt('attn_output1')[6], 'q4k');
   assert.strictEqual(fmt('attn_k0')[6], 'q4k');
   assert.strictEqual(fmt('ffn_down0')[6], 'q4k');
   assert.strictEqual(fmt('ffn_down1')[6], 'q6k');

@@ -100,15 +100,40 @@ def test_upload_bytes_and_f16(ctx, tmp_path):
         g.upload(ctx, "x32", dst=small)
 
 
-@pytest.mark.parametrize("wtype", ["q4k", "q6k"])
+def _report_mismatch(got: np.ndarray, want: np.ndarray, raw: np.ndarray, block_bytes: int, per_block: int,
+                     what: str) -> None:
+    bad = np.flatnonzero(_nan_canon(got) != _nan_canon(want))
+    if bad.size:
+        print(f"[{what}] {bad.size} of {got.size} values differ", flush=True)
+        for i in bad[:8]:
+            b = int(i) // per_block
+            print(f"  value {i} (block {b}): got {got[i]:#06x} want {want[i]:#06x}, block head "
+                  f"{raw[b * block_bytes:b * block_bytes + 4].tolist()}", flush=True)
+    assert bad.size == 0, what
+
+
+@pytest.mark.parametrize("wtype", ["q4k", "q6k", "q8_0"])
 def test_dequant_f16(ctx, wtype):
     nb = 3000
-    blocks = O.gen_q4k(11, nb) if wtype == "q4k" else O.gen_q6k(12, nb)
-    ref = (O.dequant_q4k if wtype == "q4k" else O.dequant_q6k)(blocks)
+    if wtype == "q8_0":
+        blocks = _q8_0_blocks(13, nb * 8)
+        # d over the f16 range (subnormal, largest, negative, zero) and q = -128
+        blocks.reshape(-1, 34)[:8, 0:2] = np.array([0x0001, 0x03ff, 0x0400, 0x7bff, 0x0000, 0x8400, 0xbc00, 0x1234],
+                                                   np.uint16).view(np.uint8).reshape(8, 2)
+        blocks.reshape(-1, 34)[:8, 2] = 0x80
+        ref = O.dequant_q8_0(blocks)
+        n = nb * 8
+    else:
+        blocks = O.gen_q4k(11, nb) if wtype == "q4k" else O.gen_q6k(12, nb)
+        ref = (O.dequant_q4k if wtype == "q4k" else O.dequant_q6k)(blocks)
+        n = nb
     out = ctx.empty(nb * 256, np.uint16)
-    ctx.dequantF16(wtype, ctx.from_numpy(blocks), nb, out)
+    ctx.dequantF16(wtype, ctx.from_numpy(blocks), n, out)
     got = out.download(np.uint16)
-    assert np.array_equal(_nan_canon(got), _np_f16_bits(ref))
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = ref.astype(np.float16).view(np.uint16)
+    _report_mismatch(got, want, blocks, 34 if wtype == "q8_0" else (144 if wtype == "q4k" else 210),
+                     32 if wtype == "q8_0" else 256, f"dequant {wtype}")
 
 
 # ---- a small Gemma-4-E2B-layout model in a file --------------------------------
@@ -129,9 +154,64 @@ def _shape() -> E2BShape:
     return E2BShape.real(n_layers=N_LAYERS, n_unshared=N_UNSHARED, global_layers=GLOBALS, vocab=VOCAB)
 
 
-def _model_file(path: str) -> str:
+def _q5k_matrix_blocks(seed: int, n: int) -> np.ndarray:
+    """Q5_K blocks of a zero-mean matrix: d ~ |N(0, 5e-4)| and dmin = 15.5 d,
+    the mean of d*sc*q over q, so that the sub-block offsets cancel on
+    average (a biased matrix would make the test model ill-conditioned:
+    its products would hinge on sums of the activations)."""
+    b = _q5k_blocks(seed, n).reshape(n, 176)
+    rng = np.random.default_rng(seed + 1)
+    d = np.abs(rng.standard_normal(n) * 5e-4).astype(np.float16)
+    b[:, 0:2] = d.view(np.uint8).reshape(n, 2)
+    b[:, 2:4] = (d.astype(np.float32) * 15.5).astype(np.float16).view(np.uint8).reshape(n, 2)
+    return b.reshape(-1)
+
+
+def _q8_0_blocks(seed: int, n: int) -> np.ndarray:
+    """Q8_0 blocks: f16 d ~ |N(0, 1e-3)|, 32 uniform int8."""
+    rng = np.random.default_rng(seed)
+    b = rng.integers(0, 256, (n, 34), dtype=np.uint8)
+    b[:, 0:2] = np.abs(rng.standard_normal(n) * 1e-3).astype(np.float16).view(np.uint8).reshape(n, 2)
+    return b.reshape(-1)
+
+
+def _q4k_zero_mean(blocks: np.ndarray) -> np.ndarray:
+    """Q4_K blocks with dmin = 7.5 d (the mean of d*sc*q over q): the
+    sub-block offsets cancel on average, as in a trained matrix."""
+    b = blocks.reshape(-1, 144).copy()
+    d = b[:, 0:2].copy().view(np.float16).reshape(-1)
+    b[:, 2:4] = (d.astype(np.float32) * 7.5).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    return b.reshape(-1)
+
+
+def _matrix_bytes(t: int, seed: int, M: int, N: int, zero_mean: bool = False) -> np.ndarray:
+    """An M x N matrix of GGUF type t from the seeded generators."""
+    if t == T_Q4_K:
+        b = O.gen_q4k(seed, M * N // 256)
+        return _q4k_zero_mean(b) if zero_mean else b
+    if t == T_Q6_K:
+        return O.gen_q6k(seed, M * N // 256)
+    if t == T_Q5_K:
+        return _q5k_matrix_blocks(seed, M * N // 256)
+    if t == T_Q8_0:
+        return _q8_0_blocks(seed, M * N // 32)
+    f = O.gen_normal_f32(seed, M * N, 0.0, 0.03)
+    if t == T_F32:
+        return f
+    if t == T_F16:
+        return f.astype(np.float16)
+    return (f.view(np.uint32) >> 16).astype(np.uint16)  # BF16
+
+
+def _model_file(path: str, fmt=None, head_type: int = T_Q6_K, q_norm: float = 1.0, zero_mean: bool = False) -> str:
+    """fmt(il, name) -> GGUF type of each layer matrix (default: the
+    Q4_K_M-style mix with Q4_K gate/up); q_norm is the mean of the q-norm
+    weights (the attention scores scale with it); zero_mean makes the Q4_K
+    matrices zero-mean."""
     s = _shape()
-    qt = q4km_types(s)
+    if fmt is None:
+        qt = q4km_types(s)
+        fmt = lambda il, nm: {"q4k": T_Q4_K, "q6k": T_Q6_K}[qt(il, nm) if nm not in ("wgate", "wup") else "q4k"]  # noqa
     w = GGUFWriter()
     w.kv("general.architecture", STR, "gemma4")
     w.kv("gemma4.embedding_length", U32, s.hidden).kv("gemma4.block_count", U32, N_LAYERS)
@@ -148,10 +228,7 @@ def _model_file(path: str) -> str:
 
     def mat(name, M, N, t):
         seed[0] += 1
-        if t == "q4k":
-            w.tensor(name, (N, M), T_Q4_K, O.gen_q4k(seed[0], M * N // 256))
-        else:
-            w.tensor(name, (N, M), T_Q6_K, O.gen_q6k(seed[0], M * N // 256))
+        w.tensor(name, (N, M), t, _matrix_bytes(t, seed[0], M, N, zero_mean))
 
     def vec(name, n, mean=1.0, std=0.1):
         seed[0] += 1
@@ -165,18 +242,18 @@ def _model_file(path: str) -> str:
         H, Q, KV, I, hd = s.hidden, s.q_dim_of(il), s.kv_dim_of(il), s.ffn_of(il), s.hd(il)
         p = f"blk.{il}."
         vec(p + "attn_norm.weight", H)
-        mat(p + "attn_q.weight", Q, H, qt(il, "wq"))
+        mat(p + "attn_q.weight", Q, H, fmt(il, "wq"))
         if s.is_producer(il):
-            mat(p + "attn_k.weight", KV, H, qt(il, "wk"))
-            mat(p + "attn_v.weight", KV, H, qt(il, "wv"))
+            mat(p + "attn_k.weight", KV, H, fmt(il, "wk"))
+            mat(p + "attn_v.weight", KV, H, fmt(il, "wv"))
             vec(p + "attn_k_norm.weight", hd)
-        vec(p + "attn_q_norm.weight", hd)
-        mat(p + "attn_output.weight", H, Q, qt(il, "wo"))
+        vec(p + "attn_q_norm.weight", hd, q_norm, 0.1 * q_norm)
+        mat(p + "attn_output.weight", H, Q, fmt(il, "wo"))
         vec(p + "post_attention_norm.weight", H)
         vec(p + "ffn_norm.weight", H)
-        mat(p + "ffn_gate.weight", I, H, "q4k")
-        mat(p + "ffn_up.weight", I, H, "q4k")
-        mat(p + "ffn_down.weight", H, I, qt(il, "wdown"))
+        mat(p + "ffn_gate.weight", I, H, fmt(il, "wgate"))
+        mat(p + "ffn_up.weight", I, H, fmt(il, "wup"))
+        mat(p + "ffn_down.weight", H, I, fmt(il, "wdown"))
         vec(p + "post_ffw_norm.weight", H)
     vec("output_norm.weight", s.hidden)
     # per-layer embeddings as the real file holds them: a BF16 projection,
@@ -195,8 +272,7 @@ def _model_file(path: str) -> str:
         vec(f"blk.{il}.layer_output_scale.weight", 1, 0.8, 0.1)
     # the tied table (the LM head's blocks, the lookup's f16 rows)
     seed[0] += 1
-    te = O.gen_q6k(seed[0], VOCAB * s.hidden // 256)
-    w.tensor("token_embd.weight", (s.hidden, VOCAB), T_Q6_K, te)
+    w.tensor("token_embd.weight", (s.hidden, VOCAB), head_type, _matrix_bytes(head_type, seed[0], VOCAB, s.hidden))
     w.tensor("rope_freqs.weight", (256,), T_F32, np.where(np.arange(256) < 64, 1.0, 1e30).astype(np.float32))
     return w.write(path)
 
@@ -314,10 +390,9 @@ def test_file_model_ragged_step(ctx, model_path):
     del d
 
 
-@pytest.mark.skipif(shutil.which("node") is None, reason="no node binary")
-def test_node_backend_from_gguf(ctx, model_path):
+def _node_from_gguf(ctx, model_path):
     """HipBackend.fromGGUF (the N-API addon's reader and uploads, the Node
-    backend's configFromGGUF) on the same file: three greedy forwards from
+    backend's configFromGGUF) on a file: three greedy forwards from
     position 0 with zero caches against the oracle over the Python
     decoder's copy of the file's weights."""
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -352,3 +427,124 @@ def test_node_backend_from_gguf(ctx, model_path):
         assert_close(logits, lg_ref, what=f"logits forward {i + 1}")
         assert got == O.argmax(logits)
         tok = got
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="no node binary")
+def test_node_backend_from_gguf(ctx, model_path):
+    _node_from_gguf(ctx, model_path)
+
+
+# A file whose matrices are in every format the reference loads: the layers
+# mix Q8_0, Q5_K, F16, BF16 and F32 matrices with Q4_K / Q6_K ones (a Q5_K
+# gate makes layer 1's FFN unfused; layer 2's gate and up are both F16), and
+# the tied table is Q8_0. The formats the matvecs do not read as blocks are
+# held as the reference's f16 rows (tensorToF16, src/engine.ts:570-579).
+# Its embedding rows are small next to the layers' outputs, so the residual
+# stream does not hide the layers' errors. To keep the model well
+# conditioned, the q-norm weights (mean 0.25) hold the attention scores at a
+# standard deviation of about 4 over the N(0, 1) caches (with mean 1, about
+# 16: a softmax whose near-ties amplify any rounding), and the Q4_K and Q5_K
+# matrices are zero-mean (a common offset on every row makes the products
+# hinge on sums of the activations).
+_FORMATS = {
+    0: {"wq": T_Q8_0, "wk": T_Q5_K, "wv": T_F16, "wo": T_BF16, "wgate": T_Q4_K, "wup": T_Q4_K, "wdown": T_Q8_0},
+    1: {"wq": T_Q4_K, "wk": T_Q4_K, "wv": T_Q6_K, "wo": T_F32, "wgate": T_Q5_K, "wup": T_Q4_K, "wdown": T_Q6_K},
+    2: {"wq": T_F16, "wo": T_Q4_K, "wgate": T_F16, "wup": T_F16, "wdown": T_Q4_K},
+}
+
+
+@pytest.fixture(scope="module")
+def formats_path(tmp_path_factory):
+    fmt = lambda il, nm: _FORMATS.get(il, {}).get(nm, T_Q6_K if nm == "wdown" else T_Q4_K)  # noqa: E731
+    return _model_file(str(tmp_path_factory.mktemp("gguf") / "formats.gguf"), fmt, head_type=T_Q8_0, q_norm=0.25,
+                       zero_mean=True)
+
+
+def test_every_format_as_f16_rows(ctx, formats_path):
+    g = GGUFFile(formats_path)
+    d = decoder_from_gguf(ctx, g, max_seq=1024)
+    names = dict(wq="attn_q", wk="attn_k", wv="attn_v", wo="attn_output", wgate="ffn_gate", wup="ffn_up",
+                 wdown="ffn_down")
+    for il, L in enumerate(d.layers):
+        for nm, fn in names.items():
+            b = getattr(L, nm)
+            if b is None:
+                continue
+            t = g.tensor(f"blk.{il}.{fn}.weight")
+            if t.type in (T_Q4_K, T_Q6_K):
+                assert L.qt[nm] == {T_Q4_K: "q4k", T_Q6_K: "q6k"}[t.type]
+                assert np.array_equal(b.download(np.uint8, t.nbytes), g.data(t.name))
+            else:
+                assert L.qt[nm] == "f16", (il, nm)
+                got = b.download(np.uint16, t.n_elements)
+                bb, per = {T_Q8_0: (34, 32), T_Q5_K: (176, 256)}.get(t.type, (2, 1))
+                _report_mismatch(got, O.dequant_f16_rows(g.data(t.name), t.type), g.data(t.name), bb, per,
+                                 f"layer {il} {nm} {t.type_name}")
+    te = g.tensor("token_embd.weight")
+    assert d.lm_type == "f16" and d.embedding is d.lm_head
+    assert np.array_equal(d.lm_head.download(np.uint16), O.dequant_f16_rows(g.data(te.name), te.type))
+    del d
+
+
+def test_every_format_fused_step(ctx, formats_path):
+    POS = 600
+    d = decoder_from_gguf(ctx, formats_path, max_seq=1024)
+    d.fill_kv(POS, seed=34)
+    d.set_token(77)
+    d.set_position(POS)
+    ctx.sync()
+    hm = HostModel(d)
+    kcs = [L.k_cache.download(np.uint16) for L in d.layers]
+    vcs = [L.v_cache.download(np.uint16) for L in d.layers]
+    # embedding, head (norm, matvec, softcap, two argmax stages); PLE 3 + 2 per layer;
+    # layer 0: one f16 q/k/v group (norm + 3 matvecs), attention, o, fused FFN (2);
+    # layer 1: a Q4_K (q, k) and a Q6_K (v) launch, attention + merge, o, unfused FFN
+    # (norm, gate, up, GELU product, down); layer 2: f16 q (norm + matvec), attention,
+    # o, unfused FFN; layer 3: q, attention + merge, o, fused FFN
+    assert d.launches_per_step_fused() == 1 + 5 + (3 + 2 * N_LAYERS) + 8 + 10 + 9 + 6
+    g = d.capture_fused()
+    try:
+        tok = 77
+        for i in range(2):
+            ctx.graph_launch(g)
+            ctx.sync()
+            x_ref, lg_ref = hm.step(hm.embed(tok), kcs, vcs, POS + i, token=tok)
+            lg = d.logits.download(np.float32)
+            print(f"[gguf formats] replay {i}: hidden rel-L2 {O.rel_l2(d.hidden.download(np.float32), x_ref):.2e}",
+                  flush=True)
+            assert_close(d.hidden.download(np.float32), x_ref, what=f"hidden replay {i}")
+            assert_close(lg, lg_ref, what=f"logits replay {i}")
+            new = int(d.token.download(np.uint32)[0])
+            assert new == O.argmax(lg)
+            tok = new
+        assert int(d.pos.download(np.uint32)[0]) == POS + 2
+    finally:
+        ctx.graph_destroy(g)
+    # the reference-order step on the same weights
+    d.set_token(5)
+    d.set_position(POS)
+    x0 = d.hidden.download(np.float32)
+    d.fill_kv(POS, seed=34)
+    ctx.sync()
+    kcs = [L.k_cache.download(np.uint16) for L in d.layers]
+    vcs = [L.v_cache.download(np.uint16) for L in d.layers]
+    d.step_reference(POS)
+    ctx.sync()
+    x_ref, lg_ref = hm.step(hm.embed(5), kcs, vcs, POS, token=5)
+    assert_close(d.hidden.download(np.float32), x_ref, what="per-key hidden")
+    assert_close(d.logits.download(np.float32), lg_ref, what="per-key logits")
+    del d
+
+
+def test_every_format_ragged_step(ctx, formats_path):
+    LENS = [9, 650, 200]
+    d = decoder_from_gguf(ctx, formats_path, batch=LENS, embed=False, reserve=8, seed=3)
+    d.fill_kv(seed=35)
+    ctx.sync()
+    _step_vs_oracle(ctx, d, LENS)
+    del d
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="no node binary")
+def test_every_format_node_backend(ctx, formats_path):
+    _node_from_gguf(ctx, formats_path)

@@ -7,8 +7,8 @@ matmul_quant.wgsl over f16 weights; src/engine.ts:1516-1535, 1608-1616).
 * stage 1 over every layer of several rows (device tokens, a token past the
   table), pleGeluMul and pleSkipScaleAdd at rel-L2 1e-6 (f32 arithmetic in
   another order);
-* the f16 matvec over 1..13 vectors and row counts that do not fill a
-  workgroup, the gate with and without its norm-add prologue, the scaled
+* the f16 matvec over 1..13 vectors, every row length it takes (256 to
+  12288) and row counts that do not fill a workgroup, the gate with and without its norm-add prologue, the scaled
   norm-add prologue of the quantized matvec and of the batch prologue, at
   rel-L2 1e-3 / cosine 0.9999 (the matvec's tolerance).
 """
@@ -43,7 +43,7 @@ def test_q5k_to_f16_bit_exact(ctx):
     for name, blocks in (("host", host), ("generated", dev.download(np.uint8))):
         n = blocks.size // 176
         out = ctx.empty(n * 256, np.uint16)
-        ctx.dequantQ5K_F16(ctx.from_numpy(blocks), n, out)
+        ctx.dequantF16("q5k", ctx.from_numpy(blocks), n, out)
         with np.errstate(over="ignore", invalid="ignore"):
             want = O.dequant_q5k(blocks).astype(np.float16).view(np.uint16)
         got = out.download(np.uint16)
@@ -93,7 +93,8 @@ def test_gelu_mul_and_skip_scale_add(ctx):
                  what="skip scale add")
 
 
-@pytest.mark.parametrize("M,N", [(256, 1536), (1536, 256), (1001, 1536), (77, 2048), (4480, 1536)])
+@pytest.mark.parametrize("M,N", [(256, 1536), (1536, 256), (1001, 1536), (77, 2048), (4480, 1536), (1536, 4096),
+                                 (333, 6144), (1536, 12288)])
 @pytest.mark.parametrize("batch", [1, 3, 8, 13])
 def test_matmul_f16(ctx, M, N, batch):
     rng = np.random.default_rng(M + N + batch)

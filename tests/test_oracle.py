@@ -861,3 +861,36 @@ def test_ple_gelu_mul_and_skip_scale_add():
     assert np.array_equal(O.ple_skip_scale_add(h, n, f16(1.0)), (h.astype(np.float64) + n).astype(np.float32))
     assert np.array_equal(O.ple_skip_scale_add(h, n, f16(2.0)), (2 * (h.astype(np.float64) + n)).astype(np.float32))
     assert not np.any(O.ple_skip_scale_add(h, n, f16(0.0)))
+
+
+def test_q8_0_known_answers():
+    """src/gguf.ts:115-131: q * d per 32-value block; known blocks, and the
+    int8 sign of every byte value."""
+    blk = np.zeros(2 * 34, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    blk[2:34] = np.arange(-16, 16, dtype=np.int8).view(np.uint8)
+    blk[34:36] = np.frombuffer(np.float16(-3.0).tobytes(), np.uint8)
+    blk[36:68] = np.array([-128, 127, 0, 1] * 8, np.int8).view(np.uint8)
+    v = O.dequant_q8_0(blk)
+    assert np.array_equal(v[:32], np.arange(-16, 16) * 0.5)
+    assert np.array_equal(v[32:], np.array([384.0, -381.0, 0.0, -3.0] * 8, np.float32))
+    # every q with d = 1: the value is the signed byte
+    blocks = np.zeros((8, 34), np.uint8)
+    blocks[:, 0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blocks[:, 2:] = np.arange(256, dtype=np.uint8).reshape(8, 32)
+    assert np.array_equal(O.dequant_q8_0(blocks.reshape(-1)), np.arange(256, dtype=np.uint8).view(np.int8))
+
+
+def test_dequant_f16_rows_per_type():
+    """The f16 rows of every tensor type, against the pinned dequants and
+    NumPy's IEEE half: F16 unchanged, BF16 through its f32 high half."""
+    rng = np.random.default_rng(40)
+    f32 = rng.standard_normal(64).astype(np.float32)
+    assert np.array_equal(O.dequant_f16_rows(f32.view(np.uint8), 0), f32.astype(np.float16).view(np.uint16))
+    h = rng.standard_normal(64).astype(np.float16)
+    assert np.array_equal(O.dequant_f16_rows(h.view(np.uint8), 1), h.view(np.uint16))
+    bf = (f32.view(np.uint32) >> 16).astype(np.uint16)
+    want = (bf.astype(np.uint32) << 16).view(np.float32).astype(np.float16).view(np.uint16)
+    assert np.array_equal(O.dequant_f16_rows(bf.view(np.uint8), 30), want)
+    q4 = O.gen_q4k(41, 4)
+    assert np.array_equal(O.dequant_f16_rows(q4, 12), O.dequant_q4k(q4).astype(np.float16).view(np.uint16))
