@@ -339,13 +339,18 @@ def batch_census(ctx, bd, reps=10):
     kv_glob = sum(int(L) + 1 for L in bd.lens_host) * KV * 4
     kv_loc = sum(min(int(L) + 1, s.window) for L in bd.lens_host) * KV * 4
     act = lambda N: ctx.batch_operand_bytes(N, B)  # noqa: E731
+    sub = lambda K: ctx.batch_sub_operand_bytes(K, B)  # noqa: E731
+    # the gate/up launch hands its product to the down projection as
+    # sub-block-scaled operand blocks (every layer of this shape)
+    handoff = bd.dops is not None
+    ks_down = (I // 768) if handoff else bd.ks_f
     nbytes = {
         "qkv": q4(Q + 2 * KV, H) + act(H) + bd.ks_h * B * (Q + 2 * KV) * 4,
         "attn_global": kv_glob + B * Q * 4 * 2,
         "attn_window512": kv_loc + B * Q * 4 * 2,
         "o": q4(H, Q) + act(Q) + bd.ks_q * B * H * 4,
-        "gate_up_gelu": 2 * q4(I, H) + act(H) + B * I * 4,
-        "down": q6(H, I) + B * I * 4 + bd.ks_f * B * H * 4,
+        "gate_up_gelu": 2 * q4(I, H) + act(H) + (sub(I) if handoff else B * I * 4),
+        "down": q6(H, I) + (sub(I) if handoff else B * I * 4) + ks_down * B * H * 4,
     }
     kinds = {
         "prep_attn": lambda il, L: c.batchPrep(bd.down_parts, bd.ks_f // 2, L.post_ffn_norm, bd.hidden2, L.attn_norm,
@@ -367,9 +372,12 @@ def batch_census(ctx, bd, reps=10):
                                                         ops=bd.aops),
         "prep_ffn": lambda il, L: c.batchPrep(bd.o_parts, bd.ks_q, L.post_attn_norm, bd.hidden, L.pre_ffn_norm,
                                               bd.hidden2, bd.xn, H, B, s.eps, ops=bd.xops),
-        "gate_up_gelu": lambda il, L: c.gateUpGeluBatch(bd.xn, L.wgate, L.wup, bd.act, I, H, B, ops=bd.xops),
-        "down": lambda il, L: c.matmulSegmentsBatchPartial("q6k", bd.act, [L.wdown], [bd.down_parts], [H], I, B,
-                                                           bd.ks_f),
+        "gate_up_gelu": lambda il, L: (c.gateUpGeluBatchOps(bd.xn, bd.xops, L.wgate, L.wup, None, bd.dops, I, H, B)
+                                       if handoff else c.gateUpGeluBatch(bd.xn, L.wgate, L.wup, bd.act, I, H, B,
+                                                                         ops=bd.xops)),
+        "down": lambda il, L: (c.matmulSubBatchPartial(bd.dops, L.wdown, bd.down_parts, H, I, B, ks_down)
+                               if handoff else c.matmulSegmentsBatchPartial("q6k", bd.act, [L.wdown],
+                                                                            [bd.down_parts], [H], I, B, bd.ks_f)),
     }
     out = {}
     for name, body in kinds.items():

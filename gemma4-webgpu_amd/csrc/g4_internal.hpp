@@ -312,6 +312,17 @@ struct Ops {
   __host__ __device__ static constexpr uint32_t scale_off(int ntv) { return (uint32_t)ntv * (MAIN_T + 1024); }
   __host__ __device__ static constexpr uint32_t bytes(int ntv) { return (uint32_t)ntv * (MAIN_T + 1024 + 64); }
 };
+// Sub-block-scaled operand blocks (the gate/up launch's product, written for
+// a Q6_K down projection): main as above, but every 32-element sub-block has
+// its own 2^e (largest |x| of the vector's sub-block in [2^13, 2^14)), so
+// the workgroup that owns 32 rows of the product can write them alone; no
+// sums (Q6_K has no min term).
+//   scale [t][s][16] f32: 2^-e of vector 16t + lane%16, sub-block s
+struct OpsSub {
+  static constexpr uint32_t MAIN_T = Ops::MAIN_T;
+  __host__ __device__ static constexpr uint32_t scale_off(int ntv) { return (uint32_t)ntv * MAIN_T; }
+  __host__ __device__ static constexpr uint32_t bytes(int ntv) { return (uint32_t)ntv * (MAIN_T + 512); }
+};
 
 }  // namespace g4d
 

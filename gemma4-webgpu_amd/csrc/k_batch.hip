@@ -51,6 +51,7 @@ constexpr int PMAX = 12;   // partials added per pass of the prep loads (24 meas
                            // slower: passes over fewer chunks load clamped copies)
 
 using g4d::Ops;
+using g4d::OpsSub;
 using g4d::pad_batch;
 
 __device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
@@ -246,9 +247,10 @@ struct MmArgs {
   uint32_t B;
   float cap;       // softcap when > 0 (ksplit == 1)
   const float* x;        // [B][K] activations
-  const uint8_t* ops;    // OPS: their operand blocks [K/256][Ops::bytes(NTV)]
+  const uint8_t* ops;    // OPK 1: their operand blocks [K/256][Ops::bytes(NTV)]; OPK 2: [K/256][OpsSub::bytes(NTV)]
   uint32_t K;
   uint32_t ksplit, kc;  // K in ksplit chunks of kc super-blocks
+  uint8_t* ops_out;     // MODE 1: the product's sub-block-scaled operand blocks (or null)
 };
 
 // 8 bytes at a 2-byte aligned address: three aligned dwords, funnel-shifted.
@@ -486,19 +488,21 @@ __device__ __forceinline__ void cp_store(const u32x4 (&cp)[NCP], u32x4* lds, int
   }
 }
 
-// The operand source of one launch: built from f32 activations (OPS false)
-// or copied from blocks a prep launch built (OPS true).
-template <int NTV, bool OPS>
+// The operand source of one launch: built from f32 activations (OPK 0),
+// copied from blocks a prep launch built (OPK 1) or from the sub-block-scaled
+// blocks a gate/up launch wrote (OPK 2).
+template <int NTV, int OPK>
 struct OpSrc;
 template <int NTV>
-struct OpSrc<NTV, false> {
+struct OpSrc<NTV, 0> {
   Raw<NTV> r;
   __device__ __forceinline__ void load(const MmArgs& a, uint32_t kb, int tid) { raw_load<NTV>(r, a.x, a.B, a.K, kb, tid); }
   __device__ __forceinline__ void store(uint8_t* lds, const MmArgs& a, int tid) { raw_store<NTV>(r, lds, a.B, tid); }
 };
-template <int NTV>
-struct OpSrc<NTV, true> {
-  static constexpr uint32_t NPC = Ops::bytes(NTV) / 16;
+template <int NTV, int OPK>
+struct OpSrc {
+  static_assert(OPK == 1 || OPK == 2, "copied operand blocks");
+  static constexpr uint32_t NPC = (OPK == 1 ? Ops::bytes(NTV) : OpsSub::bytes(NTV)) / 16;
   static constexpr int NCP = (int)((NPC + MNT - 1) / MNT);
   u32x4 cp[NCP];
   __device__ __forceinline__ void load(const MmArgs& a, uint32_t kb, int tid) {
@@ -521,9 +525,13 @@ __device__ __forceinline__ float epilogue(float y, float cap) {
 
 // MODE 0: a row group is 64 rows of one segment. MODE 1 (gate/up): segments
 // 0 and 1 have the same rows; a row group is 32 rows of both, waves 0-1 gate,
-// waves 2-3 up, and the output (segment 0's Y) is gelu(gate) * up.
-template <int QT, int BPR, int NTV, int MODE, bool OPS>
+// waves 2-3 up, and the output (segment 0's Y) is gelu(gate) * up; with
+// ops_out the workgroup also writes its 32 rows of the product as one
+// sub-block of the sub-block-scaled operand blocks a Q6_K down projection
+// reads (OPK 2).
+template <int QT, int BPR, int NTV, int MODE, int OPK>
 __global__ __launch_bounds__(MNT) void mmf_kernel(MmArgs a) {
+  static_assert(OPK != 2 || (QT == 1 && MODE == 0), "sub-block-scaled operands: Q6_K matmuls");
   __shared__ __align__(16) uint8_t lds[Ops::bytes(NTV) + 16];  // + the copy's sink slot
 
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q = l >> 4;
@@ -546,7 +554,7 @@ __global__ __launch_bounds__(MNT) void mmf_kernel(MmArgs a) {
   }
   const uint32_t kb0 = chunk * a.kc;
 
-  OpSrc<NTV, OPS> src;
+  OpSrc<NTV, OPK> src;
   WRegs<QT> wr, wn;
   src.load(a, kb0, tid);
   load_w<BPR>(wr, W, M, rbase, kb0, l);
@@ -565,6 +573,31 @@ __global__ __launch_bounds__(MNT) void mmf_kernel(MmArgs a) {
     load_w<BPR>(wn, W, M, rbase, kn, l);
 
     f4 C[NTV], Cm[NTV];
+    if constexpr (OPK == 2) {
+      // each sub-block's products scaled by its own 2^-e, then d
+      const float* scs = (const float*)(lds + OpsSub::scale_off(NTV));
+#pragma unroll
+      for (int t = 0; t < NTV; ++t) C[t] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const h8 A = a_operand(wr, s, q);
+#pragma unroll
+        for (int t = 0; t < NTV; ++t) {
+          const u32x4 bh = lv[(t * Ops::MAIN_T + s * 2048) / 16 + l];
+          const u32x4 bl = lv[(t * Ops::MAIN_T + s * 2048 + 1024) / 16 + l];
+          f4 z = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bh), f4{0.f, 0.f, 0.f, 0.f}, 0, 0,
+                                                        0);
+          z = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bl), z, 0, 0, 0);
+          const float fs = scs[t * 128 + s * 16 + (l & 15)];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) C[t][i] += fs * z[i];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < NTV; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] += g4d::f16_bits_to_f32(wr.dd[i]) * C[t][i];
+    } else {
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const h8 A = a_operand(wr, s, q);
@@ -601,6 +634,7 @@ __global__ __launch_bounds__(MNT) void mmf_kernel(MmArgs a) {
         }
       }
     }
+    }
     __syncthreads();  // every wave is done with this block's operands
     if (more) {
       src.store(lds, a, tid);
@@ -618,6 +652,7 @@ __global__ __launch_bounds__(MNT) void mmf_kernel(MmArgs a) {
       for (int t = 0; t < NTV; ++t) xfer[((w - 2) * NTV + t) * 64 + l] = acc[t];
     }
     __syncthreads();
+    f4 y[NTV];  // the product (0 for padded vectors and rows past M)
     if (w < 2) {
 #pragma unroll
       for (int t = 0; t < NTV; ++t) {
@@ -626,8 +661,49 @@ __global__ __launch_bounds__(MNT) void mmf_kernel(MmArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint32_t row = rbase + 4u * q + i;
-          if (row < M && v < a.B) a.s[0].Y[(size_t)v * M + row] = gelu_tanh(acc[t][i]) * up[i];
+          const bool live = row < M && v < a.B;
+          y[t][i] = live ? gelu_tanh(acc[t][i]) * up[i] : 0.f;
+          if (live && a.s[0].Y) a.s[0].Y[(size_t)v * M + row] = y[t][i];
         }
+      }
+    }
+    if (!a.ops_out) return;  // (uniform)
+    // The workgroup's 32 rows are sub-block g % 8 of super-block g / 8 of
+    // the product: per vector, the largest |y| over them (lanes of one column
+    // in each gate wave, then the two waves) sets its 2^e.
+    float* mx = (float*)(lds + NTV * 2048);  // [2 waves][NTV][16]
+    if (w < 2) {
+#pragma unroll
+      for (int t = 0; t < NTV; ++t) {
+        float m = fmaxf(fmaxf(fabsf(y[t][0]), fabsf(y[t][1])), fmaxf(fabsf(y[t][2]), fabsf(y[t][3])));
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        if (q == 0) mx[(w * NTV + t) * 16 + l] = m;
+      }
+    }
+    __syncthreads();
+    if (w < 2) {
+      const uint32_t sb = g & 7u, c = (uint32_t)(l & 15);
+      uint8_t* base = a.ops_out + (size_t)(g >> 3) * OpsSub::bytes(NTV);
+      const uint32_t qq = 2u * (uint32_t)w + (uint32_t)(q >> 1);  // 8-element group of rows 16w + 4q ..
+#pragma unroll
+      for (int t = 0; t < NTV; ++t) {
+        const float am = fmaxf(mx[t * 16 + c], mx[(NTV + t) * 16 + c]);
+        int ex = 0;
+        (void)frexpf(am, &ex);
+        const int k = am > 0.f ? min(max(14 - ex, -120), 120) : 0;
+        const float sc = ldexpf(1.0f, k);
+        _Float16 hi[4], lo[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float xs = y[t][i] * sc;
+          hi[i] = (_Float16)xs;
+          lo[i] = (_Float16)(xs - (float)hi[i]);
+        }
+        uint8_t* slot = base + t * Ops::MAIN_T + sb * 2048 + (c + 16u * qq) * 16 + (q & 1) * 8;
+        *(uint2*)slot = make_uint2(pack_h2(hi[0], hi[1]), pack_h2(hi[2], hi[3]));
+        *(uint2*)(slot + 1024) = make_uint2(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));
+        if (w == 0 && q == 0) *(float*)(base + OpsSub::scale_off(NTV) + t * 512 + sb * 64 + c * 4) = ldexpf(1.0f, -k);
       }
     }
     return;
@@ -713,9 +789,9 @@ bool mm_supported(uint32_t bpr) {
   return bpr == 4 || bpr == 6 || bpr == 8 || bpr == 12 || bpr == 16 || bpr == 24 || bpr == 32 || bpr == 48;
 }
 
-template <int QT, int BPR, int NTV, int MODE, bool OPS>
+template <int QT, int BPR, int NTV, int MODE, int OPK>
 int mm_launch(g4_ctx* ctx, const MmArgs& a, uint32_t groups) {
-  hipLaunchKernelGGL((mmf_kernel<QT, BPR, NTV, MODE, OPS>), dim3(groups * a.ksplit), dim3(MNT), 0, ctx->stream, a);
+  hipLaunchKernelGGL((mmf_kernel<QT, BPR, NTV, MODE, OPK>), dim3(groups * a.ksplit), dim3(MNT), 0, ctx->stream, a);
   G4_LAUNCHED(ctx, "mm");
   return G4_OK;
 }
@@ -730,15 +806,23 @@ int mm_ntv(g4_ctx* ctx, const MmArgs& a, uint32_t groups) {
   const uint32_t Bp = pad_batch(a.B);
   if constexpr (ops_width<BPR>()) {
     if (a.ops) {
-      if (Bp == 16) return mm_launch<QT, BPR, 1, MODE, true>(ctx, a, groups);
-      if (Bp == 32) return mm_launch<QT, BPR, 2, MODE, true>(ctx, a, groups);
-      return mm_launch<QT, BPR, 4, MODE, true>(ctx, a, groups);
+      if (Bp == 16) return mm_launch<QT, BPR, 1, MODE, 1>(ctx, a, groups);
+      if (Bp == 32) return mm_launch<QT, BPR, 2, MODE, 1>(ctx, a, groups);
+      return mm_launch<QT, BPR, 4, MODE, 1>(ctx, a, groups);
     }
   }
   if (a.ops) return G4_ERR_UNSUPPORTED;
-  if (Bp == 16) return mm_launch<QT, BPR, 1, MODE, false>(ctx, a, groups);
-  if (Bp == 32) return mm_launch<QT, BPR, 2, MODE, false>(ctx, a, groups);
-  return mm_launch<QT, BPR, 4, MODE, false>(ctx, a, groups);
+  if (Bp == 16) return mm_launch<QT, BPR, 1, MODE, 0>(ctx, a, groups);
+  if (Bp == 32) return mm_launch<QT, BPR, 2, MODE, 0>(ctx, a, groups);
+  return mm_launch<QT, BPR, 4, MODE, 0>(ctx, a, groups);
+}
+// A Q6_K matmul over sub-block-scaled operand blocks (the FFN widths).
+template <int BPR>
+int mm_sub_ntv(g4_ctx* ctx, const MmArgs& a, uint32_t groups) {
+  const uint32_t Bp = pad_batch(a.B);
+  if (Bp == 16) return mm_launch<1, BPR, 1, 0, 2>(ctx, a, groups);
+  if (Bp == 32) return mm_launch<1, BPR, 2, 0, 2>(ctx, a, groups);
+  return mm_launch<1, BPR, 4, 0, 2>(ctx, a, groups);
 }
 
 template <int QT>
@@ -777,9 +861,11 @@ int check_x(const char* fn, const float* x, uint32_t N, uint32_t B) {
 
 // One matmul launch over up to four matrices sharing the input x [B][N] (or
 // the gate/up pair). ksplit > 1 leaves partial sums in Y[i] [ksplit][B][rows[i]].
+// sub: ops are sub-block-scaled blocks (a Q6_K matmul of width 6144 or
+// 12288); ops_out: the gate/up pair also writes its product's blocks.
 int mm_run(g4_ctx* ctx, const char* fn, int qt, const float* x, const uint8_t* ops, const uint8_t* const* W,
            float* const* Y, const uint32_t* rows, int nseg, uint32_t N, uint32_t B, float cap, bool gelu,
-           uint32_t ksplit) {
+           uint32_t ksplit, bool sub = false, uint8_t* ops_out = nullptr) {
   const uint32_t bpr = N / 256;
   uint32_t groups = 0;
   MmArgs a{};
@@ -796,8 +882,15 @@ int mm_run(g4_ctx* ctx, const char* fn, int qt, const float* x, const uint8_t* o
   a.K = N;
   a.ksplit = ksplit;
   a.kc = bpr / ksplit;
+  a.ops_out = ops_out;
   int rc;
-  if (gelu) {
+  if (sub) {
+    switch (bpr) {
+      case 24: rc = mm_sub_ntv<24>(ctx, a, groups); break;
+      case 48: rc = mm_sub_ntv<48>(ctx, a, groups); break;
+      default: rc = G4_ERR_UNSUPPORTED;
+    }
+  } else if (gelu) {
     switch (bpr) {
       case 6: rc = mm_ntv<0, 6, 1>(ctx, a, groups); break;
       case 8: rc = mm_ntv<0, 8, 1>(ctx, a, groups); break;
@@ -1020,6 +1113,50 @@ int g4_gateUpGeluBatch(g4_ctx* ctx, const float* x, const void* ops, const void*
   float* Y[2] = {out, out};
   const uint32_t rows[2] = {p.M, p.M};
   return mm_run(ctx, __func__, 0, x, (const uint8_t*)ops, W, Y, rows, 2, p.N, batch, 0.f, true, 1);
+}
+
+int g4_batchSubOperandBytes(uint32_t K, uint32_t batch, size_t* bytes) {
+  G4_REQUIRE(bytes && (K == 6144 || K == 12288) && batch >= 1 && batch <= 64, "g4_batchSubOperandBytes: bad shape");
+  *bytes = (size_t)(K / 256) * OpsSub::bytes((int)(pad_batch(batch) / 16));
+  return G4_OK;
+}
+
+int g4_gateUpGeluBatchOps(g4_ctx* ctx, const float* x, const void* ops, const void* w_gate, const void* w_up,
+                          float* out, void* down_ops, g4_matmul_params p, uint32_t batch) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(w_gate && w_up && ops && down_ops && p.M > 0, "g4_gateUpGeluBatchOps: null buffer or empty");
+  G4_REQUIRE(p.N == 1536 || p.N == 2048, "g4_gateUpGeluBatchOps: N=%u must be 1536 or 2048", p.N);
+  G4_REQUIRE(p.M == 6144 || p.M == 12288, "g4_gateUpGeluBatchOps: M=%u must be 6144 or 12288", p.M);
+  G4_REQUIRE(((uintptr_t)w_gate & 15) == 0 && ((uintptr_t)w_up & 15) == 0 && ((uintptr_t)ops & 15) == 0 &&
+                 ((uintptr_t)down_ops & 15) == 0,
+             "g4_gateUpGeluBatchOps: weights and operands must be 16-byte aligned");
+  int rc = check_x(__func__, x, p.N, batch);
+  if (rc) return rc;
+  const uint8_t* W[2] = {(const uint8_t*)w_gate, (const uint8_t*)w_up};
+  float* Y[2] = {out, out};
+  const uint32_t rows[2] = {p.M, p.M};
+  return mm_run(ctx, __func__, 0, x, (const uint8_t*)ops, W, Y, rows, 2, p.N, batch, 0.f, true, 1, false,
+                (uint8_t*)down_ops);
+}
+
+int g4_matmulSubBatchPartial(g4_ctx* ctx, const void* ops, const void* weight, float* out, uint32_t M, uint32_t K,
+                             uint32_t batch, uint32_t max_ksplit, uint32_t* ksplit) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(ops && weight && out && ksplit && M > 0 && max_ksplit >= 1,
+             "g4_matmulSubBatchPartial: null buffer, no rows or max_ksplit 0");
+  G4_REQUIRE(K == 6144 || K == 12288, "g4_matmulSubBatchPartial: K=%u must be 6144 or 12288", K);
+  G4_REQUIRE(batch >= 1 && batch <= 64, "g4_matmulSubBatchPartial: batch %u outside 1..64", batch);
+  G4_REQUIRE(((uintptr_t)ops & 15) == 0 && ((uintptr_t)weight & 3) == 0,
+             "g4_matmulSubBatchPartial: operands 16-byte, weights 4-byte aligned");
+  const uint8_t* W[1] = {(const uint8_t*)weight};
+  float* Y[1] = {out};
+  const uint32_t rows[1] = {M};
+  const uint32_t ks = pick_ksplit(ctx, total_groups(rows, 1), K / 256, max_ksplit);
+  // (x is not read: the operands are the blocks)
+  const int rc = mm_run(ctx, __func__, 1, (const float*)ops, (const uint8_t*)ops, W, Y, rows, 1, K, batch, 0.f,
+                        false, ks, true);
+  if (rc == G4_OK) *ksplit = ks;
+  return rc;
 }
 
 }  // extern "C"

@@ -199,6 +199,9 @@ SIGNATURES = {
     "g4_batchOperandBytes": (_I, [_U32, _U32, ctypes.POINTER(_SZ)]),
     "g4_batchPrep": (_I, [_P, _P, _U32, _P, _P, _P, _P, _P, _P, _U32, _U32, _F]),
     "g4_gateUpGeluBatch": (_I, [_P, _P, _P, _P, _P, _P, MatmulParams, _U32]),
+    "g4_batchSubOperandBytes": (_I, [_U32, _U32, ctypes.POINTER(_SZ)]),
+    "g4_gateUpGeluBatchOps": (_I, [_P, _P, _P, _P, _P, _P, _P, MatmulParams, _U32]),
+    "g4_matmulSubBatchPartial": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, ctypes.POINTER(_U32)]),
     "g4_pagedAttnPrologue": (_I, [_P, _P, _P, _P, _U32, _P, _P, _P, _P, _P, _P, _P, _P, PagedAttnFusedParams,
                                   _P, _U32]),
     "g4_normAddGateUpGeluBatch": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, MatmulParams, _F, _U32]),

@@ -823,6 +823,10 @@ class BatchDecoder(_SyntheticModel):
         self.o_parts = ctx.empty(self.ks_q * B * s.hidden, f32)
         self.act = ctx.empty(B * s.max_ffn, f32)
         self.down_parts = ctx.empty(self.ks_f * B * s.hidden, f32)
+        # the FFN product handed to the down projection as sub-block-scaled
+        # operand blocks (a Q4_K gate/up pair over a Q6_K down)
+        self.dops = (ctx.empty(ctx.batch_sub_operand_bytes(s.max_ffn, B), np.uint8)
+                     if any(self._ffn_handoff(il) for il in range(s.n_layers)) else None)
         if any(not (L.qt["wgate"] == "q4k" and L.qt["wup"] == "q4k") for L in self.layers):
             self.gate_b = ctx.empty(B * s.max_ffn, f32)  # gate and up of a layer that does not pair them
             self.up_b = ctx.empty(B * s.max_ffn, f32)
@@ -946,13 +950,19 @@ class BatchDecoder(_SyntheticModel):
             no = self._mm_batch(L.qt["wo"], self.attn, L.wo, self.o_parts, H, Q, self.ks_q, ops)
             c.batchPrep(self.o_parts, no, L.post_attn_norm, self.hidden, L.pre_ffn_norm, self.hidden2, self.xn, H, B,
                         s.eps, ops=self.xops)
-            if L.qt["wgate"] == "q4k" and L.qt["wup"] == "q4k":
-                c.gateUpGeluBatch(self.xn, L.wgate, L.wup, self.act, I, H, B, ops=self.xops)
-            else:  # gate and up apart (whole sums), then the GELU product
-                self._mm_batch(L.qt["wgate"], self.xn, L.wgate, self.gate_b, I, H, 1, self.xops)
-                self._mm_batch(L.qt["wup"], self.xn, L.wup, self.up_b, I, H, 1, self.xops)
-                c.geluMul(self.gate_b, self.up_b, self.act, B * I)
-            nd = self._mm_batch(L.qt["wdown"], self.act, L.wdown, self.down_parts, H, I, self.ks_f, None)
+            if self._ffn_handoff(il):
+                # the product goes to the down projection as operand blocks only;
+                # K in chunks of 3 super-blocks (one workgroup per CU)
+                c.gateUpGeluBatchOps(self.xn, self.xops, L.wgate, L.wup, None, self.dops, I, H, B)
+                nd = c.matmulSubBatchPartial(self.dops, L.wdown, self.down_parts, H, I, B, I // 768)
+            else:
+                if L.qt["wgate"] == "q4k" and L.qt["wup"] == "q4k":
+                    c.gateUpGeluBatch(self.xn, L.wgate, L.wup, self.act, I, H, B, ops=self.xops)
+                else:  # gate and up apart (whole sums), then the GELU product
+                    self._mm_batch(L.qt["wgate"], self.xn, L.wgate, self.gate_b, I, H, 1, self.xops)
+                    self._mm_batch(L.qt["wup"], self.xn, L.wup, self.up_b, I, H, 1, self.xops)
+                    c.geluMul(self.gate_b, self.up_b, self.act, B * I)
+                nd = self._mm_batch(L.qt["wdown"], self.act, L.wdown, self.down_parts, H, I, self.ks_f, None)
             if s.ple_dim:
                 # post-FFN norm-add (h, no second norm) -> inp_gate -> gelu * ple_inputs -> proj
                 D = s.ple_dim
@@ -980,6 +990,14 @@ class BatchDecoder(_SyntheticModel):
             else:
                 c.topk256Batch(self.logits, self.topk, s.vocab, B)
         self.lens_host = self.lens_host + 1
+
+    def _ffn_handoff(self, il: int) -> bool:
+        """Layer il's gate/up launch hands its product to the down projection
+        as sub-block-scaled operand blocks: a Q4_K gate/up pair, a Q6_K down,
+        FFN width 6144 or 12288."""
+        L = self.layers[il]
+        return (L.qt["wgate"] == "q4k" and L.qt["wup"] == "q4k" and L.qt["wdown"] == "q6k"
+                and self.s.ffn_of(il) in (6144, 12288))
 
     def _mm_batch(self, qt: str, x, w, y, M: int, N: int, max_ksplit: int, ops) -> int:
         """y = W . x for the B rows: f16 rows through the f16 matvec (one

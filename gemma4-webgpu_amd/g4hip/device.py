@@ -334,6 +334,27 @@ class Context:
         check(lib().g4_gateUpGeluBatch(self.h, _p(x), _p(ops), _p(w_gate), _p(w_up), _p(out), MatmulParams(M, N),
                                        batch))
 
+    @staticmethod
+    def batch_sub_operand_bytes(K: int, batch: int) -> int:
+        n = ctypes.c_size_t(0)
+        check(lib().g4_batchSubOperandBytes(K, batch, ctypes.byref(n)))
+        return int(n.value)
+
+    def gateUpGeluBatchOps(self, x: Ptr, ops: Ptr, w_gate: Ptr, w_up: Ptr, out: Ptr, down_ops: Ptr, M: int, N: int,
+                           batch: int) -> None:
+        """gateUpGeluBatch that also writes the product's sub-block-scaled operand blocks (down_ops)."""
+        check(lib().g4_gateUpGeluBatchOps(self.h, _p(x), _p(ops), _p(w_gate), _p(w_up), _p(out), _p(down_ops),
+                                          MatmulParams(M, N), batch))
+
+    def matmulSubBatchPartial(self, ops: Ptr, weight: Ptr, out: Ptr, M: int, K: int, batch: int,
+                              max_ksplit: int) -> int:
+        """Q6_K weight [M][K] times the vectors of sub-block-scaled operand blocks; out gets
+        [ksplit][batch][M] partial sums. Returns ksplit (<= max_ksplit)."""
+        ks = ctypes.c_uint32(0)
+        check(lib().g4_matmulSubBatchPartial(self.h, _p(ops), _p(weight), _p(out), M, K, batch, max_ksplit,
+                                             ctypes.byref(ks)))
+        return int(ks.value)
+
     # ---- attention (kv_cache_store / attn_score / softmax / attn_output) ----
     def kvCacheStore(self, k_in: Ptr, v_in: Ptr, k_cache: Ptr, v_cache: Ptr, num_kv_heads: int, head_dim: int,
                      position: int, max_seq_len: int, position_dev: Ptr = None) -> None:

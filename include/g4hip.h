@@ -562,6 +562,22 @@ int g4_matmulSegmentsBatchPartial(g4_ctx* ctx, int wtype, const float* x, const 
  * normalised; `ops` as above). */
 int g4_gateUpGeluBatch(g4_ctx* ctx, const float* x, const void* ops, const void* w_gate,
                        const void* w_up, float* out, g4_matmul_params p, uint32_t batch);
+/* The FFN's hand-off at batch sizes 1..64 (the batched counterpart of
+ * g4_normAddGateUpGeluDigits_q4k; src/engine.ts:1594-1601 runs gate, up,
+ * geluMul and down as four dispatches per token): g4_gateUpGeluBatch (Q4_K
+ * gate and up, p.M 6144 or 12288; `out` may be NULL) that also writes its
+ * product as sub-block-scaled operand blocks (down_ops,
+ * g4_batchSubOperandBytes(p.M, batch) bytes: each 32 consecutive values of
+ * a vector scaled by their own power of two, split into f16 hi + lo), which
+ * g4_matmulSubBatchPartial multiplies by a Q6_K down projection
+ * (shaders/matmul_quant.wgsl over Q6_K, src/gguf.ts:323-368) without
+ * rebuilding them from f32 values: out [*ksplit][batch][M] partial sums as
+ * g4_matmulSegmentsBatchPartial's (max_ksplit * batch * M floats). */
+int g4_batchSubOperandBytes(uint32_t K, uint32_t batch, size_t* bytes);
+int g4_gateUpGeluBatchOps(g4_ctx* ctx, const float* x, const void* ops, const void* w_gate,
+                          const void* w_up, float* out, void* down_ops, g4_matmul_params p, uint32_t batch);
+int g4_matmulSubBatchPartial(g4_ctx* ctx, const void* ops, const void* weight, float* out, uint32_t M,
+                             uint32_t K, uint32_t batch, uint32_t max_ksplit, uint32_t* ksplit);
 
 /* ------------------------------------------------------------------------ */
 /* Debug / test exports                                                      */

@@ -134,6 +134,61 @@ def test_batched_gate_up_gelu(ctx, B):
         assert_close(A[b], ref, what=f"gelu(gate)*up seq {b}")
 
 
+def _decode_sub_operands(raw: np.ndarray, M: int, B: int) -> np.ndarray:
+    """Values [16 * ntv][M] of sub-block-scaled operand blocks: per super-block
+    and 16-vector tile, f16 hi / lo at [sub-block][hi|lo][8-group][vector][8]
+    (16384 B per tile), then the f32 2^-e at [tile][sub-block][vector]."""
+    ntv = (16 if B <= 16 else 32 if B <= 32 else 64) // 16
+    main_t, nsb = 16384, M // 256
+    blk = raw.reshape(nsb, ntv * (main_t + 512))
+    hl = blk[:, :ntv * main_t].copy().view(np.float16).reshape(nsb, ntv, 8, 2, 4, 16, 8).astype(np.float64)
+    fs = blk[:, ntv * main_t:].copy().view(np.float32).reshape(nsb, ntv, 8, 16).astype(np.float64)
+    val = (hl[:, :, :, 0] + hl[:, :, :, 1]) * fs[:, :, :, None, :, None]  # (kb, t, s, qq, c, e)
+    return val.transpose(1, 4, 0, 2, 3, 5).reshape(16 * ntv, M)
+
+
+@pytest.mark.parametrize("B,M", [(5, 6144), (32, 6144), (64, 6144), (16, 12288)])
+def test_ffn_handoff_operands(ctx, B, M):
+    """The gate/up launch's product as sub-block-scaled operand blocks: the
+    f32 product equals the plain launch's, the blocks hold it to 2^-19 of the
+    largest |value| of each 32-value sub-block (f16 hi + lo), padded vectors
+    are zero, and the Q6_K down projection over them (split K, int8 scales
+    over their whole range) matches the oracle's matvec of the product."""
+    N = 1536
+    Wg = O.gen_q4k(110, M * N // 256)
+    Wu = O.gen_q4k(111, M * N // 256)
+    Wd = synth.q6k_wide(112, N * M // 256)
+    X = O.gen_normal_f32(113, B * N, 0.0, 2.0).reshape(B, N)
+    X[B // 2] *= 30.0
+    w1 = O.gen_normal_f16(114, N, 1.0, 0.1)
+    xn = ctx.empty(B * N, np.float32)
+    xops = ctx.empty(ctx.batch_operand_bytes(N, B), np.uint8)
+    ctx.batchPrep(ctx.from_numpy(X), 1, ctx.from_numpy(w1), None, None, None, xn, N, B, ops=xops)
+    dWg, dWu, dWd = ctx.from_numpy(Wg), ctx.from_numpy(Wu), ctx.from_numpy(Wd)
+    a_ref = ctx.empty(B * M, np.float32)
+    ctx.gateUpGeluBatch(xn, dWg, dWu, a_ref, M, N, B, ops=xops)
+    a2 = ctx.empty(B * M, np.float32)
+    dops = ctx.empty(ctx.batch_sub_operand_bytes(M, B), np.uint8)
+    ctx.gateUpGeluBatchOps(xn, xops, dWg, dWu, a2, dops, M, N, B)
+    A = a_ref.download(np.float32).reshape(B, M)
+    assert np.array_equal(a2.download(np.float32).reshape(B, M), A)
+    dec = _decode_sub_operands(dops.download(np.uint8), M, B)
+    assert np.all(dec[B:] == 0)
+    sub_max = np.abs(A.astype(np.float64)).reshape(B, M // 32, 32).max(axis=2, keepdims=True)
+    err = np.abs(dec[:B] - A).reshape(B, M // 32, 32)
+    assert np.all(err <= sub_max * 2.0 ** -19), float((err / np.maximum(sub_max, 1e-30)).max())
+    ks_max = M // 768
+    parts = ctx.empty(ks_max * B * N, np.float32)
+    ks = ctx.matmulSubBatchPartial(dops, dWd, parts, N, M, B, ks_max)
+    assert 1 <= ks <= ks_max and (M // 256) % ks == 0
+    P = parts.download(np.float32)[:ks * B * N].reshape(ks, B, N)
+    Y = P[0].copy()
+    for k in range(1, ks):
+        Y += P[k]
+    for b in range(B):
+        assert_close(Y[b], O.matmul(A[b], Wd, N, M, "q6k"), what=f"down over the hand-off, vector {b}")
+
+
 @pytest.mark.parametrize("B", [3, 32])
 def test_batch_prep_adds_partials_then_norms(ctx, B):
     """fusedNormAdd -> rmsNorm over x given as 3 chunks added in order."""
