@@ -1772,14 +1772,19 @@ int merge(g4_ctx* ctx, const AttnArgs& a, float* out, const SplitPlan& sp, uint3
   return merge_launch(ctx, a.ws, out, a.nqh, a.nkh, G, hd, sp.nsplit, num_seqs, len_args(a), sp.chunk, ops);
 }
 
-// The matrix-core kernel serves 8 query heads per KV head at head_dim 256 and
-// up to 64 sequences (its chunk numbering runs in one wave).
+// The matrix-core kernel serves the paged batch: 8 query heads per KV head at
+// head_dim 256 and up to 64 sequences (its chunk numbering runs in one wave).
+// One dense sequence takes the VALU form (attn_kernel), measured faster on
+// its own at every context of the single-sequence shape (8 query heads,
+// 1 KV head x 256: 9.0 against 11.8 us at 512 positions, 11.2 against
+// 13.9 at 4096, 20.7 against 21.5 at 32768); in the decode step the fused
+// form (mqf_kernel) keeps the matrix cores.
 bool mq_fits(uint32_t G, uint32_t hd, uint32_t num_seqs) { return G == 8 && hd == 256 && num_seqs <= 64; }
 
 // Steps per workgroup from the largest window, sized for about four
 // workgroups per CU when every sequence is that long.
-int mq_decode(g4_ctx* ctx, const char* fn, const AttnArgs& base, bool paged, uint32_t num_seqs, float* out,
-              size_t ws_len, uint8_t* ops = nullptr) {
+int mq_decode(g4_ctx* ctx, const char* fn, const AttnArgs& base, uint32_t num_seqs, float* out, size_t ws_len,
+              uint8_t* ops = nullptr) {
   const uint32_t eff = eff_len(base.cap, base.window);
   const uint64_t cus = ctx->num_cus > 0 ? (uint64_t)ctx->num_cus : 256;
   const uint64_t want = ((uint64_t)num_seqs * eff + 64 * 4 * cus - 1) / (64 * 4 * cus);
@@ -1805,8 +1810,7 @@ int mq_decode(g4_ctx* ctx, const char* fn, const AttnArgs& base, bool paged, uin
   m.max_chunks = max_chunks;
   m.ws = base.ws;
   const dim3 grid(num_seqs * max_chunks, base.nkh);
-  if (paged) hipLaunchKernelGGL(mq_attn_kernel<true>, grid, dim3(NT), 0, ctx->stream, m);
-  else hipLaunchKernelGGL(mq_attn_kernel<false>, grid, dim3(NT), 0, ctx->stream, m);
+  hipLaunchKernelGGL(mq_attn_kernel<true>, grid, dim3(NT), 0, ctx->stream, m);
   G4_LAUNCHED(ctx, "attn_decode_mfma");
   return merge_launch(ctx, base.ws, out, base.nqh, base.nkh, MQ_G, MQ_HD, max_chunks, num_seqs, m.len, chunk, ops);
 }
@@ -1860,7 +1864,6 @@ int dense_decode(g4_ctx* ctx, const char* fn, const float* q, const uint16_t* kc
   G4_REQUIRE(ws_len >= need, "%s: workspace %zu bytes < %zu required", fn, ws_len, need);
   const AttnArgs a = dense_args(q, kc, vc, p.num_q_heads, p.num_kv_heads, p.seq_len, p.scale, p.sliding_window,
                                 sp, ws, pos_dev);
-  if (mq_fits(G, p.head_dim, 1)) return mq_decode(ctx, fn, a, false, 1, out, ws_len);
   rc = launch_attn<false, false>(ctx, a, G, p.head_dim, sp.cp, dim3(sp.nsplit, p.num_kv_heads, 1));
   if (rc) return rc;
   return merge(ctx, a, out, sp, 1, G, p.head_dim);
@@ -2205,7 +2208,7 @@ int g4_pagedAttnDecodeOps(g4_ctx* ctx, const float* q, const uint16_t* k_pool, c
   if (rc) return rc;
   a.q = q;
   if (mq_fits(p.num_q_heads / p.num_kv_heads, p.head_dim, p.num_seqs))
-    return mq_decode(ctx, __func__, a, true, p.num_seqs, output, workspace_bytes, (uint8_t*)ops);
+    return mq_decode(ctx, __func__, a, p.num_seqs, output, workspace_bytes, (uint8_t*)ops);
   rc = launch_attn<true, false>(ctx, a, p.num_q_heads / p.num_kv_heads, p.head_dim, sp.cp,
                                 dim3(sp.nsplit, p.num_kv_heads, p.num_seqs));
   if (rc) return rc;
