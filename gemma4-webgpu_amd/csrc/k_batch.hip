@@ -607,6 +607,11 @@ __global__ __launch_bounds__(MNT * KG) void mmf_kernel(MmArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[t][i] += g4d::f16_bits_to_f32(wr.dd[i]) * C[t][i];
     } else {
+    // the x_hi and x_lo products accumulate apart: two independent MFMA
+    // chains per tile instead of one (a dependent MFMA waits for its
+    // predecessor's result; waves of the batched LM head spent 55 % of their
+    // cycles waiting to issue with one chain)
+    f4 Cl[NTV];
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const h8 A = a_operand(wr, s, q);
@@ -614,11 +619,14 @@ __global__ __launch_bounds__(MNT * KG) void mmf_kernel(MmArgs a) {
       for (int t = 0; t < NTV; ++t) {
         const u32x4 bh = lv[(t * Ops::MAIN_T + s * 2048) / 16 + l];
         const u32x4 bl = lv[(t * Ops::MAIN_T + s * 2048 + 1024) / 16 + l];
-        const f4 z = s == 0 ? f4{0.f, 0.f, 0.f, 0.f} : C[t];
-        C[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bh), z, 0, 0, 0);
-        C[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bl), C[t], 0, 0, 0);
+        const f4 zh = s == 0 ? f4{0.f, 0.f, 0.f, 0.f} : C[t];
+        const f4 zl = s == 0 ? f4{0.f, 0.f, 0.f, 0.f} : Cl[t];
+        C[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bh), zh, 0, 0, 0);
+        Cl[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bl), zl, 0, 0, 0);
       }
     }
+#pragma unroll
+    for (int t = 0; t < NTV; ++t) C[t] += Cl[t];
     if constexpr (QT == 0) {
       const h8 Am = min_operand(wr, q);
 #pragma unroll
