@@ -548,6 +548,22 @@ def node_q4k_gemv(seconds=4.0):
             "rel_l2_vs_oracle": float(O.rel_l2(y, O.matmul(x, W, M, K, "q4k")))}
 
 
+def node_step_rate(start=START_POS, steps=100, warmup=10):
+    """The fused step from a Node host: gemma4-webgpu_amd/node/bench_step.js
+    builds the model of `value` (same shape, weights generated on the device,
+    KV filled to `start`) through HipBackend over the N-API addon, captures
+    HipBackend.encodeFusedStep once and replays it. None when node or the
+    addon is absent."""
+    import shutil
+    import subprocess
+    node = shutil.which("node")
+    if node is None or not os.path.exists(os.path.join(ROOT, "gemma4-webgpu_amd", "node", "g4hip.node")):
+        return None
+    r = subprocess.run([node, os.path.join(ROOT, "gemma4-webgpu_amd", "node", "bench_step.js"), str(start),
+                        str(steps), str(warmup)], capture_output=True, text=True, check=True, timeout=600)
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def torch_attention_cfg3(threads, seconds=0.5):
     """Config 3 on the host: the builder's fp32 torch attention,
     softmax(q k^T) v at scale 1.0 with the sliding-window mask, 8 query heads
@@ -693,6 +709,8 @@ def main():
     ap.add_argument("--no-real-layout", action="store_true",
                     help="skip the decode runs of Gemma-4-E2B's own layer layout")
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill runs")
+    ap.add_argument("--no-node-step", action="store_true",
+                    help="skip the fused step's rate from a Node host (gemma4-webgpu_amd/node/bench_step.js)")
     ap.add_argument("--real-eager-only", type=int, default=0, metavar="STEPS",
                     help="run STEPS eager (not captured) fused steps of Gemma-4-E2B's layout with per-layer "
                          "embeddings from position 512 and exit (for the kernel tracer)")
@@ -802,6 +820,9 @@ def main():
             prefill["real_e2b_layout"] = prefill_rate(ctx, E2BShape.real())
             log(f"prefill (real layout): {prefill['real_e2b_layout']}")
 
+    node_step = None if args.no_node_step else node_step_rate(START_POS, args.pos_steps, args.pos_warmup)
+    log(f"fused step from Node: {node_step}")
+
     batch = {}
     for B in [int(b) for b in args.batch_sweep.split(",") if b.strip()]:
         batch[f"B={B}"] = batch_decode(ctx, B, args.batch_steps, args.batch_warmup, census=(B == 32 and not
@@ -809,7 +830,7 @@ def main():
     if args.no_census:
         print(json.dumps({"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": ms_step,
                           "decode_from_position": positions, "real_e2b_layout": real,
-                          "prefill": prefill, "batch_decode": batch}), flush=True)
+                          "node_fused_step": node_step, "prefill": prefill, "batch_decode": batch}), flush=True)
         return
     census = kernel_census(ctx, dec, args.census_reps)
     for k, v in census.items():
@@ -862,6 +883,7 @@ def main():
         "kernel_census_us": {k: round(per_step[k], 2) for k in per_step},
         "decode_from_position": positions,
         "real_e2b_layout": real,
+        "node_fused_step": node_step,
         "prefill": prefill,
         "batch_decode": batch,
         "attention_decode": attn3,

@@ -822,6 +822,346 @@ napi_value DequantF16(napi_env env, napi_callback_info info) {
   return done(env, g4_dequantF16(c, w, b, n, out));
 }
 
+// ---- the MI355X decode step (Decoder.step_fused in g4hip/decoder.py) -----
+// Keys with no counterpart among the reference's kernel keys: a host that
+// captures the whole step as a graph issues these instead of the per-key
+// sequence. Buffers travel in a plain object by name (BigInt or null).
+
+void* fptr(Args& a, size_t i, const char* name) {
+  napi_value f = nullptr;
+  bool has = false;
+  if (i >= a.argc || napi_has_named_property(a.env, a.v[i], name, &has) != napi_ok || !has) return nullptr;
+  napi_get_named_property(a.env, a.v[i], name, &f);
+  napi_valuetype t;
+  napi_typeof(a.env, f, &t);
+  if (t == napi_undefined || t == napi_null) return nullptr;
+  uint64_t p = 0;
+  bool lossless = false;
+  if (napi_get_value_bigint_uint64(a.env, f, &p, &lossless) != napi_ok || !lossless) {
+    std::string m = std::string("field '") + name + "' must be a BigInt device handle (or null)";
+    a.fail(m.c_str());
+    return nullptr;
+  }
+  return (void*)(uintptr_t)p;
+}
+
+// an array of up to `maxn` BigInt handles (kind 0) or numbers (kind 1) at argument i
+int array_at(Args& a, size_t i, void** ptrs, uint32_t* nums, int maxn, int kind) {
+  bool is = false;
+  if (i >= a.argc || napi_is_array(a.env, a.v[i], &is) != napi_ok || !is) {
+    a.fail("expected an array");
+    return 0;
+  }
+  uint32_t n = 0;
+  napi_get_array_length(a.env, a.v[i], &n);
+  if (n < 1 || (int)n > maxn) {
+    a.fail("array length out of range");
+    return 0;
+  }
+  for (uint32_t k = 0; k < n; ++k) {
+    napi_value e;
+    napi_get_element(a.env, a.v[i], k, &e);
+    if (kind == 0) {
+      uint64_t p = 0;
+      bool lossless = false;
+      if (napi_get_value_bigint_uint64(a.env, e, &p, &lossless) != napi_ok || !lossless) {
+        a.fail("expected BigInt device handles");
+        return 0;
+      }
+      ptrs[k] = (void*)(uintptr_t)p;
+    } else if (napi_get_value_uint32(a.env, e, &nums[k]) != napi_ok) {
+      a.fail("expected numbers");
+      return 0;
+    }
+  }
+  return (int)n;
+}
+
+g4_attn_fused_params fused_params(Args& a, size_t i) {
+  g4_attn_fused_params p{};
+  p.num_q_heads = a.fu32(i, "num_q_heads");
+  p.num_kv_heads = a.fu32(i, "num_kv_heads");
+  p.head_dim = a.fu32(i, "head_dim");
+  p.max_seq_len = a.fu32(i, "max_seq_len");
+  p.scale = a.ff32(i, "scale");
+  p.sliding_window = a.fu32(i, "sliding_window");
+  p.eps = a.ff32(i, "eps");
+  p.theta = a.ff32(i, "theta");
+  p.apply_divisor = a.fu32(i, "apply_divisor");
+  return p;
+}
+
+int wtype_of(Args& a, size_t i) {
+  const std::string t = a.str(i);
+  if (t == "q4k") return 0;
+  if (t == "q6k") return 1;
+  a.fail("wtype must be 'q4k' or 'q6k'");
+  return -1;
+}
+
+// digitsBytes(K) -> bytes of a digit block over K activations
+napi_value DigitsBytes(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  const uint32_t K = a.u32(0);
+  CHECKED(a);
+  size_t n = 0;
+  const int rc = g4_digitsBytes(K, &n);
+  if (rc != G4_OK) return done(env, rc);
+  return number(env, (double)n);
+}
+
+// attnFusedWorkspaceSize(params) -> bytes (zero them once; the kernels keep their counters zero)
+napi_value AttnFusedWorkspaceSize(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  const g4_attn_fused_params p = fused_params(a, 0);
+  CHECKED(a);
+  size_t n = 0;
+  const int rc = g4_attnDecodeFused_workspace_size(p, &n);
+  if (rc != G4_OK) return done(env, rc);
+  return number(env, (double)n);
+}
+
+// ropeTable(ctx, theta, applyDivisor, ropeFreqs, headDim, rows, table)
+napi_value RopeTable(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float theta = a.f32(1);
+  const uint32_t ad = a.u32(2);
+  const uint16_t* rf = U16P(a, 3);
+  const uint32_t hd = a.u32(4), rows = a.u32(5);
+  float* t = F32P(a, 6);
+  CHECKED(a);
+  return done(env, g4_ropeTable(c, theta, ad, rf, hd, rows, t));
+}
+
+// matmulWarmRegion(ctx, wtype, M, N, weight) -> {base, totalBytes, wgBytes, nwgs}:
+// the bytes each workgroup of the one-vector matvec over W [M x N] reads
+napi_value MatmulWarmRegion(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const int wt = wtype_of(a, 1);
+  const uint32_t M = a.u32(2), N = a.u32(3);
+  const void* w = a.ptr(4);
+  CHECKED(a);
+  g4_warm_region r{};
+  const int rc = g4_matmulWarmRegion(c, wt, M, N, w, &r);
+  if (rc != G4_OK) return done(env, rc);
+  napi_value o;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "base", bigint(env, r.base));
+  napi_set_named_property(env, o, "totalBytes", number(env, (double)r.total_bytes));
+  napi_set_named_property(env, o, "wgBytes", number(env, (double)r.wg_bytes));
+  napi_set_named_property(env, o, "nwgs", number(env, r.nwgs));
+  return o;
+}
+
+// up to 4 regions from an array of matmulWarmRegion objects at argument i
+int regions_at(Args& a, size_t i, g4_warm_region* out) {
+  if (!a.present(i)) return 0;
+  bool is = false;
+  uint32_t n = 0;
+  if (napi_is_array(a.env, a.v[i], &is) != napi_ok || !is || napi_get_array_length(a.env, a.v[i], &n) != napi_ok ||
+      n > 4) {
+    a.fail("regions: an array of at most 4 matmulWarmRegion objects");
+    return 0;
+  }
+  for (uint32_t k = 0; k < n; ++k) {
+    napi_value e, f;
+    napi_get_element(a.env, a.v[i], k, &e);
+    uint64_t p = 0;
+    bool lossless = false;
+    double d = 0;
+    if (napi_get_named_property(a.env, e, "base", &f) != napi_ok ||
+        napi_get_value_bigint_uint64(a.env, f, &p, &lossless) != napi_ok || !lossless) {
+      a.fail("region base must be a BigInt");
+      return 0;
+    }
+    out[k].base = (const void*)(uintptr_t)p;
+    napi_get_named_property(a.env, e, "totalBytes", &f);
+    napi_get_value_double(a.env, f, &d);
+    out[k].total_bytes = (uint64_t)d;
+    napi_get_named_property(a.env, e, "wgBytes", &f);
+    napi_get_value_double(a.env, f, &d);
+    out[k].wg_bytes = (uint64_t)d;
+    napi_get_named_property(a.env, e, "nwgs", &f);
+    napi_get_value_double(a.env, f, &d);
+    out[k].nwgs = (uint32_t)d;
+    out[k].reserved = 0;
+  }
+  return (int)n;
+}
+
+// attnDecodeFused(ctx, {q, k, v, qNorm, kNorm, ropeFreqs, kCache, vCache, out,
+//   workspace, position, ropeCs}, params, workspaceBytes, ropeRows[, regions]):
+// the fused attention block at the device position; its idle workgroups read
+// `regions` (matmulWarmRegion of the launches that follow) into the L2 caches
+napi_value AttnDecodeFused(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* q = (const float*)fptr(a, 1, "q");
+  const float* k = (const float*)fptr(a, 1, "k");
+  const float* v = (const float*)fptr(a, 1, "v");
+  const uint16_t* qn = (const uint16_t*)fptr(a, 1, "qNorm");
+  const uint16_t* kn = (const uint16_t*)fptr(a, 1, "kNorm");
+  const uint16_t* rf = (const uint16_t*)fptr(a, 1, "ropeFreqs");
+  uint16_t* kc = (uint16_t*)fptr(a, 1, "kCache");
+  uint16_t* vc = (uint16_t*)fptr(a, 1, "vCache");
+  float* out = (float*)fptr(a, 1, "out");
+  void* ws = fptr(a, 1, "workspace");
+  const uint32_t* pos = (const uint32_t*)fptr(a, 1, "position");
+  const float* cs = (const float*)fptr(a, 1, "ropeCs");
+  const g4_attn_fused_params p = fused_params(a, 2);
+  const uint64_t wsb = a.u64(3);
+  const uint32_t rows = a.present(4) ? a.u32(4) : 0;
+  g4_warm_region reg[4] = {};
+  const int nreg = regions_at(a, 5, reg);
+  CHECKED(a);
+  return done(env, g4_attnDecodeFusedWarm(c, q, k, v, qn, kn, rf, kc, vc, out, p, ws, (size_t)wsb, pos,
+                                          nreg ? reg : nullptr, nreg, cs, rows));
+}
+
+// normAddScaleMatmulSegments(ctx, wtype, {x, w1, residual, scale, w2, hOut},
+//   weights[], outputs[], rows[], N, eps)
+napi_value NormAddScaleMatmulSegments(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const int wt = wtype_of(a, 1);
+  const float* x = (const float*)fptr(a, 2, "x");
+  const uint16_t* w1 = (const uint16_t*)fptr(a, 2, "w1");
+  const float* res = (const float*)fptr(a, 2, "residual");
+  const uint16_t* sc = (const uint16_t*)fptr(a, 2, "scale");
+  const uint16_t* w2 = (const uint16_t*)fptr(a, 2, "w2");
+  float* h = (float*)fptr(a, 2, "hOut");
+  void* W[4] = {};
+  void* Y[4] = {};
+  uint32_t R[4] = {};
+  const int n = array_at(a, 3, W, nullptr, 4, 0);
+  const int ny = array_at(a, 4, Y, nullptr, 4, 0);
+  const int nr = array_at(a, 5, nullptr, R, 4, 1);
+  const uint32_t N = a.u32(6);
+  const float eps = a.f32(7);
+  CHECKED(a);
+  if (n != ny || n != nr) {
+    a.fail("weights, outputs and rows differ in length");
+    return nullptr;
+  }
+  return done(env, g4_normAddScaleMatmulSegments(c, wt, x, w1, res, sc, w2, h, W, (float* const*)Y, R, n, N, eps,
+                                                 0.f));
+}
+
+// normAddGateUpGeluDigits(ctx, {o, wPost, residual, wPre, wGate, wUp, hOut, out, digits}, {M, N}, eps)
+napi_value NormAddGateUpGeluDigits(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* o = (const float*)fptr(a, 1, "o");
+  const uint16_t* wpo = (const uint16_t*)fptr(a, 1, "wPost");
+  const float* res = (const float*)fptr(a, 1, "residual");
+  const uint16_t* wpr = (const uint16_t*)fptr(a, 1, "wPre");
+  const void* wg = fptr(a, 1, "wGate");
+  const void* wu = fptr(a, 1, "wUp");
+  float* h = (float*)fptr(a, 1, "hOut");
+  float* out = (float*)fptr(a, 1, "out");
+  void* dg = fptr(a, 1, "digits");
+  g4_matmul_params p{a.fu32(2, "M"), a.fu32(2, "N")};
+  const float eps = a.f32(3);
+  CHECKED(a);
+  return done(env, g4_normAddGateUpGeluDigits_q4k(c, o, wpo, res, wpr, wg, wu, h, out, dg, p, eps));
+}
+
+// matmulQuantDigits(ctx, digits, weight, output, {M, N}): Q6_K over a digit block
+napi_value MatmulQuantDigits(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const void* dg = a.ptr(1);
+  const void* w = a.ptr(2);
+  float* y = F32P(a, 3);
+  g4_matmul_params p{a.fu32(4, "M"), a.fu32(4, "N")};
+  CHECKED(a);
+  return done(env, g4_matmulQuantDigits_q6k(c, dg, w, y, p));
+}
+
+// normAddMatmulArgmax(ctx, wtype, {x, w1, residual, w2, hOut, weight, logits, result, positions},
+//   rows, N, eps, softcap, delta): the LM head with its argmax candidates
+napi_value NormAddMatmulArgmax(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const int wt = wtype_of(a, 1);
+  const float* x = (const float*)fptr(a, 2, "x");
+  const uint16_t* w1 = (const uint16_t*)fptr(a, 2, "w1");
+  const float* res = (const float*)fptr(a, 2, "residual");
+  const uint16_t* w2 = (const uint16_t*)fptr(a, 2, "w2");
+  float* h = (float*)fptr(a, 2, "hOut");
+  const void* w = fptr(a, 2, "weight");
+  float* lg = (float*)fptr(a, 2, "logits");
+  uint32_t* r = (uint32_t*)fptr(a, 2, "result");
+  uint32_t* pos = (uint32_t*)fptr(a, 2, "positions");
+  const uint32_t rows = a.u32(3), N = a.u32(4);
+  const float eps = a.f32(5), cap = a.f32(6);
+  const uint32_t delta = a.u32(7);
+  CHECKED(a);
+  return done(env, g4_normAddMatmulArgmax(c, wt, x, w1, res, w2, h, w, lg, rows, N, eps, cap, r, pos, delta));
+}
+
+// pleGate(ctx, {x, w1, residual, hOut, wGate, pleInputs, out}, {M, N, ple_stride, layer_offset, batch}, eps)
+napi_value PleGate(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* x = (const float*)fptr(a, 1, "x");
+  const uint16_t* w1 = (const uint16_t*)fptr(a, 1, "w1");
+  const float* res = (const float*)fptr(a, 1, "residual");
+  float* h = (float*)fptr(a, 1, "hOut");
+  const uint16_t* wg = (const uint16_t*)fptr(a, 1, "wGate");
+  const float* pin = (const float*)fptr(a, 1, "pleInputs");
+  float* out = (float*)fptr(a, 1, "out");
+  const uint32_t M = a.fu32(2, "M"), N = a.fu32(2, "N"), st = a.fu32(2, "ple_stride");
+  const uint32_t off = a.fu32(2, "layer_offset"), b = a.fu32(2, "batch");
+  const float eps = a.f32(3);
+  CHECKED(a);
+  return done(env, g4_pleGate(c, x, w1, res, h, wg, pin, st, off, out, M, N, eps, b));
+}
+
+// matmulF16(ctx, x, weight, y, {M, N, batch}): f16 rows times f32 vectors
+napi_value MatmulF16(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* x = F32P(a, 1);
+  const uint16_t* w = U16P(a, 2);
+  float* y = F32P(a, 3);
+  const uint32_t M = a.fu32(4, "M"), N = a.fu32(4, "N"), b = a.fu32(4, "batch");
+  CHECKED(a);
+  return done(env, g4_matmulF16(c, x, w, y, M, N, b));
+}
+
+// batchPrepScale(ctx, {x, w1, residual, scale, w2, hOut, out}, {nparts, N, batch}, eps)
+napi_value BatchPrepScale(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* x = (const float*)fptr(a, 1, "x");
+  const uint16_t* w1 = (const uint16_t*)fptr(a, 1, "w1");
+  const float* res = (const float*)fptr(a, 1, "residual");
+  const uint16_t* sc = (const uint16_t*)fptr(a, 1, "scale");
+  const uint16_t* w2 = (const uint16_t*)fptr(a, 1, "w2");
+  float* h = (float*)fptr(a, 1, "hOut");
+  float* out = (float*)fptr(a, 1, "out");
+  const uint32_t np = a.fu32(2, "nparts"), N = a.fu32(2, "N"), b = a.fu32(2, "batch");
+  const float eps = a.f32(3);
+  CHECKED(a);
+  return done(env, g4_batchPrepScale(c, x, np, w1, res, sc, w2, h, out, nullptr, N, b, eps));
+}
+
+// argmaxAdvance(ctx, logits, result, size, positions, delta): argmax, then *positions += delta
+napi_value ArgmaxAdvance(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* lg = F32P(a, 1);
+  uint32_t* r = U32P(a, 2);
+  const uint32_t n = a.u32(3);
+  uint32_t* pos = U32P(a, 4);
+  const uint32_t d = a.u32(5);
+  CHECKED(a);
+  return done(env, g4_argmaxAdvance(c, lg, r, n, 1, pos, d));
+}
+
 struct Entry {
   const char* name;
   napi_callback fn;
@@ -873,6 +1213,19 @@ const Entry kEntries[] = {
     {"ggufUpload", GgufUpload},
     {"ggufUploadF16", GgufUploadF16},
     {"dequantF16", DequantF16},
+    {"digitsBytes", DigitsBytes},
+    {"attnFusedWorkspaceSize", AttnFusedWorkspaceSize},
+    {"ropeTable", RopeTable},
+    {"matmulWarmRegion", MatmulWarmRegion},
+    {"attnDecodeFused", AttnDecodeFused},
+    {"normAddScaleMatmulSegments", NormAddScaleMatmulSegments},
+    {"normAddGateUpGeluDigits", NormAddGateUpGeluDigits},
+    {"matmulQuantDigits", MatmulQuantDigits},
+    {"normAddMatmulArgmax", NormAddMatmulArgmax},
+    {"pleGate", PleGate},
+    {"matmulF16", MatmulF16},
+    {"batchPrepScale", BatchPrepScale},
+    {"argmaxAdvance", ArgmaxAdvance},
 };
 
 }  // namespace

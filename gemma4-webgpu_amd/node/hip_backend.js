@@ -562,6 +562,201 @@ class HipBackend {
     if (positionDev) g.advancePosition(c, W.position, 1);
   }
 
+  // ---- the MI355X decode step -------------------------------------------
+  // The fused launch sequence of g4hip/decoder.py Decoder.step_fused (greedy
+  // sampling): per layer a q/k/v launch per weight format that also forms
+  // the layer's normalised input (the previous layer's post-FFN or
+  // per-layer-embedding tail as its prologue), the attention block in one
+  // launch (q/k norm + RoPE from a per-position table, v norm, KV row store,
+  // split-K attention and merge), o, gate/up + GELU (writing the product as
+  // the digit block a Q6_K down launch reads), down, and with per-layer
+  // embeddings the gate (post-FFN norm-add prologue, GELU x ple epilogue) and
+  // proj; then the LM head with its argmax candidates and the reduction that
+  // also advances the device position. The embedding lookup and per-layer
+  // stage 1 read the token the previous step sampled (argmaxResult), the
+  // attention reads the device position: the step is captured once
+  // (captureFusedStep) and replayed token after token. Its results equal the
+  // key-by-key pass within the matvec tolerance (rel-L2 1e-3).
+  prepareFusedStep() {
+    if (this.fused) return this.fused;
+    const C = this.config;
+    const g = this.g;
+    const c = this.ctx;
+    const G = this.globals;
+    const rows = this.maxSeqLen;
+    let maxI = 0;
+    for (let il = 0; il < C.num_layers; il++) maxI = Math.max(maxI, intermediateSize(C, il));
+    const params = [];
+    let ws = 0;
+    for (let il = 0; il < C.num_layers; il++) {
+      const swa = isSwaLayer(C, il);
+      const p = { num_q_heads: C.num_q_heads, num_kv_heads: C.num_kv_heads, head_dim: headDim(C, il),
+        max_seq_len: rows, scale: 1.0, sliding_window: swa ? C.sliding_window : 0, eps: C.rms_norm_eps,
+        theta: ropeTheta(C, il), apply_divisor: swa ? 0 : 1 };
+      params.push(p);
+      ws = Math.max(ws, g.attnFusedWorkspaceSize(p));
+    }
+    const workspace = this.alloc(ws);
+    g.memset(c, workspace, 0, ws);  // the arrival counters start (and stay) zero
+    const rope = {};
+    for (const glob of [false, true]) {
+      const hd = glob ? C.head_dim_global : C.head_dim_local;
+      const t = this.alloc(4 * rows * hd);
+      g.ropeTable(c, glob ? C.rope_theta_global : C.rope_theta_swa, glob ? 1 : 0, G.rope_freqs, hd, rows, t);
+      rope[glob] = t;
+    }
+    // the gate/up and down weights each attention launch reads into the L2
+    // caches on the CUs it leaves idle (block formats only)
+    const warm = [];
+    for (let il = 0; il < C.num_layers; il++) {
+      const L = this.layers[il];
+      const F = this.formats[il] || DEFAULT_FORMATS;
+      const I = intermediateSize(C, il);
+      const H = C.hidden_size;
+      const r = [];
+      if (F.ffn_gate === 'q4k' && F.ffn_up === 'q4k') {
+        r.push(g.matmulWarmRegion(c, 'q4k', I, H, L.ffn_gate), g.matmulWarmRegion(c, 'q4k', I, H, L.ffn_up));
+      }
+      if (F.ffn_down !== 'f16') r.push(g.matmulWarmRegion(c, F.ffn_down, H, I, L.ffn_down));
+      warm.push(r);
+    }
+    const bytes = g.digitsBytes(maxI);
+    this.fused = { params: params, workspace: workspace, workspaceBytes: ws, rope: rope, warm: warm,
+      actDigits: this.alloc(bytes), pleResidual: this.alloc(4 * C.hidden_size) };
+    g.sync(c);
+    return this.fused;
+  }
+
+  _mv(fmt, x, w, y, M, N) {
+    if (fmt === 'f16') this.g.matmulF16(this.ctx, x, w, y, { M: M, N: N, batch: 1 });
+    else this.g.matmulQuant(this.ctx, x, w, y, { M: M, N: N }, fmt);
+  }
+
+  encodeFusedStep() {
+    const C = this.config;
+    const g = this.g;
+    const c = this.ctx;
+    const W = this.workBuffers;
+    const G = this.globals;
+    const Fz = this.prepareFusedStep();
+    const H = C.hidden_size;
+    const V = C.vocab_size;
+    const D = C.per_layer_input_dim;
+    const eps = C.rms_norm_eps;
+    g.embeddingLookup(c, G.tokenEmbed, V, W.hidden, { hidden_size: H, token_id: 0 }, W.argmaxResult);
+    if (D > 0) {
+      g.matmulF16(c, W.hidden, G.perLayerModelProj, W.plePmProjected, { M: C.num_layers * D, N: H, batch: 1 });
+      g.pleStage1Fuse(c, W.plePmProjected, G.perLayerProjNorm, G.perLayerTable, V, W.pleInputs,
+        { num_layers: C.num_layers, per_layer_dim: D, eps: eps, token_id: 0 }, W.argmaxResult);
+    }
+    for (let il = 0; il < C.num_layers; il++) {
+      const L = this.layers[il];
+      const F = this.formats[il] || DEFAULT_FORMATS;
+      const HD = headDim(C, il);
+      const Q = C.num_q_heads * HD;
+      const KV = C.num_kv_heads * HD;
+      const I = intermediateSize(C, il);
+      const prod = isKvProducer(C, il);
+      const kv = this.kvCaches[C.kv_producer_for_layer[il]];
+      // the prologue that forms this layer's normalised input
+      let pro;
+      if (il === 0) {
+        pro = { x: W.hidden, w1: L.attn_norm, residual: null, scale: null, w2: null };
+      } else {
+        const P = this.layers[il - 1];
+        pro = D > 0 ? { x: W.pleProjOut, w1: P.post_norm, residual: Fz.pleResidual, scale: P.layer_output_scale,
+          w2: L.attn_norm } : { x: W.ffnDown, w1: P.post_ffw_norm, residual: W.residual, scale: null,
+          w2: L.attn_norm };
+      }
+      // one q/k/v launch per weight format, in order of first appearance; a
+      // later one recomputes the norm and writes no residual
+      const mats = prod ? [['attn_q', W.q, Q], ['attn_k', W.k, KV], ['attn_v', W.v, KV]] : [['attn_q', W.q, Q]];
+      const groups = [];
+      for (const [name, y, r] of mats) {
+        let grp = groups.find((x) => x.fmt === F[name]);
+        if (!grp) {
+          grp = { fmt: F[name], w: [], y: [], r: [] };
+          groups.push(grp);
+        }
+        grp.w.push(L[name]);
+        grp.y.push(y);
+        grp.r.push(r);
+      }
+      groups.forEach((grp, gi) => {
+        const hOut = gi > 0 || il === 0 ? null : W.hidden;
+        if (grp.fmt === 'f16') {
+          g.batchPrepScale(c, Object.assign({ hOut: hOut, out: W.normed }, pro), { nparts: 1, N: H, batch: 1 }, eps);
+          grp.w.forEach((w, k) => g.matmulF16(c, W.normed, w, grp.y[k], { M: grp.r[k], N: H, batch: 1 }));
+        } else {
+          g.normAddScaleMatmulSegments(c, grp.fmt, Object.assign({ hOut: hOut }, pro), grp.w, grp.y, grp.r, H, eps);
+        }
+      });
+      g.attnDecodeFused(c, { q: W.q, k: prod ? W.k : null, v: prod ? W.v : null, qNorm: L.attn_q_norm,
+        kNorm: prod ? L.attn_k_norm : null, ropeFreqs: G.rope_freqs, kCache: kv.k, vCache: kv.v, out: W.attnOut,
+        workspace: Fz.workspace, position: W.position, ropeCs: Fz.rope[!isSwaLayer(C, il)] },
+      Fz.params[il], Fz.workspaceBytes, this.maxSeqLen, Fz.warm[il]);
+      this._mv(F.attn_output, W.attnOut, L.attn_output, W.attnProj, H, Q);
+      const pair = F.ffn_gate === 'q4k' && F.ffn_up === 'q4k';
+      if (pair) {
+        g.normAddGateUpGeluDigits(c, { o: W.attnProj, wPost: L.post_attention_norm, residual: W.hidden,
+          wPre: L.ffn_norm, wGate: L.ffn_gate, wUp: L.ffn_up, hOut: W.residual, out: W.ffnMul, digits: Fz.actDigits },
+        { M: I, N: H }, eps);
+      } else {
+        g.batchPrepScale(c, { x: W.attnProj, w1: L.post_attention_norm, residual: W.hidden, w2: L.ffn_norm,
+          hOut: W.residual, out: W.normed }, { nparts: 1, N: H, batch: 1 }, eps);
+        this._mv(F.ffn_gate, W.normed, L.ffn_gate, W.ffnGate, I, H);
+        this._mv(F.ffn_up, W.normed, L.ffn_up, W.ffnUp, I, H);
+        g.geluMul(c, W.ffnGate, W.ffnUp, W.ffnMul, I);
+      }
+      if (pair && F.ffn_down === 'q6k') g.matmulQuantDigits(c, Fz.actDigits, L.ffn_down, W.ffnDown, { M: H, N: I });
+      else this._mv(F.ffn_down, W.ffnMul, L.ffn_down, W.ffnDown, H, I);
+      if (D > 0) {
+        g.pleGate(c, { x: W.ffnDown, w1: L.post_ffw_norm, residual: W.residual, hOut: Fz.pleResidual,
+          wGate: L.inp_gate, pleInputs: W.pleInputs, out: W.pleGated },
+        { M: D, N: H, ple_stride: 0, layer_offset: il * D, batch: 1 }, eps);
+        g.matmulF16(c, W.pleGated, L.proj, W.pleProjOut, { M: H, N: D, batch: 1 });
+      }
+    }
+    const last = this.layers[C.num_layers - 1];
+    let head;
+    if (D > 0) {  // the last per-layer-embedding tail, then the head normalises it
+      g.batchPrepScale(c, { x: W.pleProjOut, w1: last.post_norm, residual: Fz.pleResidual,
+        scale: last.layer_output_scale, hOut: W.hidden, out: W.normed }, { nparts: 1, N: H, batch: 1 }, eps);
+      head = { x: W.hidden, w1: G.finalNorm, residual: null, w2: null, hOut: null };
+    } else {
+      head = { x: W.ffnDown, w1: last.post_ffw_norm, residual: W.residual, w2: G.finalNorm, hOut: W.hidden };
+    }
+    const fmt = G.lmHeadFormat || 'q6k';
+    const cap = C.final_logit_softcapping;
+    if (fmt === 'f16') {
+      g.batchPrepScale(c, Object.assign({ out: W.normed }, head), { nparts: 1, N: H, batch: 1 }, eps);
+      g.matmulF16(c, W.normed, G.lmHead, W.logits, { M: V, N: H, batch: 1 });
+      if (cap > 0) g.logitSoftcap(c, W.logits, { size: V, cap: cap });
+      g.argmaxAdvance(c, W.logits, W.argmaxResult, V, W.position, 1);
+    } else {
+      g.normAddMatmulArgmax(c, fmt, Object.assign({ weight: G.lmHead, logits: W.logits, result: W.argmaxResult,
+        positions: W.position }, head), V, H, eps, cap, 1);
+    }
+  }
+
+  // The fused step captured as a graph (replay with g.graphLaunch; destroy
+  // with g.graphDestroy).
+  captureFusedStep() {
+    this.prepareFusedStep();
+    this.g.graphBegin(this.ctx);
+    try {
+      this.encodeFusedStep();
+    } catch (e) {
+      this.g.graphEnd(this.ctx);
+      throw e;
+    }
+    return this.g.graphEnd(this.ctx);
+  }
+
+  setToken(token) {
+    this.g.upload(this.ctx, this.workBuffers.argmaxResult, new Uint32Array([token]));
+  }
+
   // One greedy forward: returns nothing; readToken() reads the sample.
   forward(tokenId, position) {
     this.encodeTransformerPass(tokenId, position, false);

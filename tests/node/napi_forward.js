@@ -13,7 +13,9 @@
 //                      perLayerProjNorm, perLayerTable
 // Three greedy forwards: (1) token and position as arguments; (2) the token
 // the first one sampled, read on the device; (3) as (2) with the position
-// read on the device, captured once as a graph and replayed. Writes
+// read on the device, captured once as a graph and replayed. With
+// cfg.fused: three steps of the fused MI355X step (encodeFusedStep twice,
+// then captureFusedStep replayed once). Writes
 // <dir>/out.bin: per forward hidden f32[H], logits f32[V], token u32.
 const fs = require('fs');
 const path = require('path');
@@ -70,6 +72,27 @@ function collect(i) {
 }
 
 const P = cfg.position;
+if (cfg.fused) {
+  // the fused MI355X step: twice eagerly (the second from the token the first
+  // sampled, both at the device position the steps advance), then captured
+  // once and replayed
+  be.setToken(cfg.token);
+  be.setPosition(P);
+  be.encodeFusedStep();
+  collect(1);
+  be.encodeFusedStep();
+  collect(2);
+  const fg = be.captureFusedStep();
+  be.g.graphLaunch(be.ctx, fg);
+  collect(3);
+  be.g.graphDestroy(fg);
+  const fpos = be.g.download(be.ctx, be.workBuffers.position, 4).readUInt32LE(0);
+  if (fpos !== P + 3) throw new Error('device position ' + fpos + ', expected ' + (P + 3));
+  fs.writeFileSync(path.join(dir, 'out.bin'), Buffer.concat(outs));
+  be.close();
+  console.log('[napi] done (fused step)');
+  process.exit(0);
+}
 be.forward(cfg.token, P);
 collect(1);
 be.encodeTransformerPass(null, P + 1, false);

@@ -21,7 +21,11 @@ const KEYS = ['version', 'lastError', 'init', 'destroy', 'deviceInfo', 'alloc', 
   'matmulQuantMR4', 'kvCacheStore', 'attnScore', 'softmax', 'attnOutput', 'attnDecodeWorkspaceSize', 'attnDecode',
   'perHeadRmsNormNoWeight', 'fusedPerHeadNormRope', 'rmsNorm', 'fusedNormAdd', 'geluMul', 'logitSoftcap',
   'embeddingLookup', 'argmax', 'topk256', 'advancePosition', 'pleStage1Fuse', 'pleGeluMul', 'pleSkipScaleAdd',
-  'ggufOpen', 'ggufClose', 'ggufInfo', 'ggufMetadata', 'ggufTensors', 'ggufUpload', 'ggufUploadF16', 'dequantF16'];
+  'ggufOpen', 'ggufClose', 'ggufInfo', 'ggufMetadata', 'ggufTensors', 'ggufUpload', 'ggufUploadF16', 'dequantF16',
+  'digitsBytes', 'attnFusedWorkspaceSize', 'ropeTable', 'matmulWarmRegion', 'attnDecodeFused',
+  'normAddScaleMatmulSegments',
+  'normAddGateUpGeluDigits', 'matmulQuantDigits', 'normAddMatmulArgmax', 'pleGate', 'matmulF16', 'batchPrepScale',
+  'argmaxAdvance'];
 
 const addon = hb.loadAddon();
 
@@ -86,6 +90,18 @@ function mockAddon() {
   for (const k of KEYS) m[k] = function () { calls.push([k].concat(Array.prototype.slice.call(arguments))); };
   m.alloc = () => next++;
   m.init = () => 'ctx';
+  m.digitsBytes = function () {
+    calls.push(['digitsBytes'].concat(Array.prototype.slice.call(arguments)));
+    return 4096;
+  };
+  m.matmulWarmRegion = function (ctx, wtype, M, N, w) {
+    calls.push(['matmulWarmRegion', ctx, wtype, M, N, w]);
+    return { base: w, totalBytes: M * N, wgBytes: 1024, nwgs: 8 };
+  };
+  m.attnFusedWorkspaceSize = function (p) {
+    calls.push(['attnFusedWorkspaceSize', p]);
+    return 1024 + p.head_dim;
+  };
   return m;
 }
 
@@ -254,6 +270,68 @@ check('per-tensor formats: sizes, wtypes, f16 rows, the LM head and the 4-row ga
   assert.strictEqual(fmt('ffn_gate1')[6], 'q6k');
   assert.strictEqual(fmt('head')[6], 'q4k');
   assert.strictEqual(m.calls.filter((c) => /^ple/.test(c[0])).length, 0);
+});
+
+check('the fused step: launch order, prologue chaining, format groups, PLE and the head', () => {
+  const C = hb.e2bConfig({ num_layers: 4, num_unshared_layers: 2, global_layers: [1, 3], vocab_size: 4096 });
+  const m = mockAddon();
+  const be = new hb.HipBackend(m, 'ctx', C, { maxSeqLen: 1024 });
+  be.allocate();
+  const t = (il, f) => {
+    const o = {};
+    for (const n of Object.keys(be.layerTensorBytes(il, f))) o[n] = n + il;
+    return o;
+  };
+  const F1 = { attn_v: 'q6k', ffn_gate: 'f16' };  // layer 1: two q/k/v launches, unfused FFN
+  be.setLayerWeights(0, t(0), {});
+  be.setLayerWeights(1, t(1, F1), F1);
+  be.setLayerWeights(2, t(2), {});
+  be.setLayerWeights(3, t(3), { ffn_down: 'q4k' });
+  be.setGlobals(Object.assign({ tokenEmbed: 'emb', lmHead: 'head', finalNorm: 'fnorm', rope_freqs: 'rf' },
+    PLE_GLOBALS));
+  m.calls.length = 0;
+  be.encodeFusedStep();
+  const keys = m.calls.map((x) => x[0]);
+  assert.strictEqual(keys.filter((k) => k === 'attnFusedWorkspaceSize').length, 4);
+  assert.strictEqual(keys.filter((k) => k === 'ropeTable').length, 2);
+  const step = keys.filter((k) => ['alloc', 'memset', 'sync', 'attnFusedWorkspaceSize', 'ropeTable',
+    'digitsBytes', 'matmulWarmRegion'].indexOf(k) < 0);
+  const layer = (qkv, ffn, down) => qkv.concat(['attnDecodeFused', 'matmulQuant'], ffn, [down], ['pleGate', 'matmulF16']);
+  const want = ['embeddingLookup', 'matmulF16', 'pleStage1Fuse']
+    .concat(layer(['normAddScaleMatmulSegments'], ['normAddGateUpGeluDigits'], 'matmulQuantDigits'))
+    .concat(layer(['normAddScaleMatmulSegments', 'normAddScaleMatmulSegments'],
+      ['batchPrepScale', 'matmulF16', 'matmulQuant', 'geluMul'], 'matmulQuant'))
+    .concat(layer(['normAddScaleMatmulSegments'], ['normAddGateUpGeluDigits'], 'matmulQuantDigits'))
+    .concat(layer(['normAddScaleMatmulSegments'], ['normAddGateUpGeluDigits'], 'matmulQuant'))
+    .concat(['batchPrepScale', 'normAddMatmulArgmax']);
+  assert.deepStrictEqual(step, want);
+  const nas = m.calls.filter((x) => x[0] === 'normAddScaleMatmulSegments');
+  // layer 0 normalises the embedding and writes no residual; layer 1's first
+  // launch adds the previous PLE tail and writes the residual, its second
+  // (the Q6_K v) recomputes the norm and writes none
+  assert.strictEqual(nas[0][3].x, be.workBuffers.hidden);
+  assert.strictEqual(nas[0][3].hOut, null);
+  assert.strictEqual(nas[1][3].x, be.workBuffers.pleProjOut);
+  assert.strictEqual(nas[1][3].scale, 'layer_output_scale0');
+  assert.strictEqual(nas[1][3].hOut, be.workBuffers.hidden);
+  assert.deepStrictEqual([nas[1][2], nas[1][4]], ['q4k', ['attn_q1', 'attn_k1']]);
+  assert.deepStrictEqual([nas[2][2], nas[2][4], nas[2][3].hOut], ['q6k', ['attn_v1'], null]);
+  // consumer layers (2, 3) project q only and read their producer's cache
+  assert.deepStrictEqual(nas[3][4], ['attn_q2']);
+  const att = m.calls.filter((x) => x[0] === 'attnDecodeFused');
+  assert.strictEqual(att[2][2].k, null);
+  assert.strictEqual(att[2][2].kCache, be.kvCaches[0].k);
+  assert.strictEqual(att[3][2].kCache, be.kvCaches[1].k);
+  assert.strictEqual(att[1][3].sliding_window, 0);
+  assert.strictEqual(att[1][3].head_dim, 512);
+  assert.strictEqual(att[0][3].sliding_window, 512);
+  // L2 warming: layer 0 the gate/up pair and the down, layer 1 (f16 gate) the down only
+  assert.deepStrictEqual(att[0][6].map((r) => r.base), ['ffn_gate0', 'ffn_up0', 'ffn_down0']);
+  assert.deepStrictEqual(att[1][6].map((r) => r.base), ['ffn_down1']);
+  const head = m.calls.filter((x) => x[0] === 'normAddMatmulArgmax')[0];
+  assert.strictEqual(head[2], 'q6k');
+  assert.strictEqual(head[3].positions, be.workBuffers.position);
+  assert.strictEqual(head[3].result, be.workBuffers.argmaxResult);
 });
 
 console.log('all node CPU checks passed');

@@ -390,7 +390,7 @@ def test_file_model_ragged_step(ctx, model_path):
     del d
 
 
-def _node_from_gguf(ctx, model_path):
+def _node_from_gguf(ctx, model_path, fused=False):
     """HipBackend.fromGGUF (the N-API addon's reader and uploads, the Node
     backend's configFromGGUF) on a file: three greedy forwards from
     position 0 with zero caches against the oracle over the Python
@@ -405,7 +405,7 @@ def _node_from_gguf(ctx, model_path):
     del d
     with tempfile.TemporaryDirectory() as td:
         with open(os.path.join(td, "config.json"), "w") as f:
-            json.dump({"gguf": model_path, "maxSeqLen": 1024, "position": 0, "token": 1234}, f)
+            json.dump({"gguf": model_path, "maxSeqLen": 1024, "position": 0, "token": 1234, "fused": fused}, f)
         print("[gguf node] running the Node forwards", flush=True)
         r = subprocess.run(["node", os.path.join(root, "tests", "node", "napi_forward.js"), td], capture_output=True,
                            text=True, timeout=240)
@@ -430,8 +430,9 @@ def _node_from_gguf(ctx, model_path):
 
 
 @pytest.mark.skipif(shutil.which("node") is None, reason="no node binary")
-def test_node_backend_from_gguf(ctx, model_path):
-    _node_from_gguf(ctx, model_path)
+@pytest.mark.parametrize("fused", [False, True], ids=["key_by_key", "fused_step"])
+def test_node_backend_from_gguf(ctx, model_path, fused):
+    _node_from_gguf(ctx, model_path, fused)
 
 
 # A file whose matrices are in every format the reference loads: the layers
@@ -546,5 +547,6 @@ def test_every_format_ragged_step(ctx, formats_path):
 
 
 @pytest.mark.skipif(shutil.which("node") is None, reason="no node binary")
-def test_every_format_node_backend(ctx, formats_path):
-    _node_from_gguf(ctx, formats_path)
+@pytest.mark.parametrize("fused", [False, True], ids=["key_by_key", "fused_step"])
+def test_every_format_node_backend(ctx, formats_path, fused):
+    _node_from_gguf(ctx, formats_path, fused)

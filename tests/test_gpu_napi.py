@@ -11,7 +11,8 @@ forwards: token and position as arguments, then the sampled token read on
 the device, then that with the position read on the device from a captured
 graph. Each forward's hidden state and logits are checked against the
 oracle's step at rel-L2 1e-3 / cosine 0.9999, and its token is the argmax
-of its logits (bit-exact)."""
+of its logits (bit-exact). The same three steps run again through the fused
+MI355X step (HipBackend.encodeFusedStep / captureFusedStep)."""
 import json
 import os
 import shutil
@@ -133,14 +134,15 @@ def _model(shape):
 
 
 @pytest.mark.skipif(shutil.which("node") is None, reason="no node binary")
-def test_node_backend_forwards_vs_oracle():
+@pytest.mark.parametrize("fused", [False, True], ids=["key_by_key", "fused_step"])
+def test_node_backend_forwards_vs_oracle(fused):
     addon = os.path.join(ROOT, "gemma4-webgpu_amd", "node", "g4hip.node")
     assert os.path.exists(addon), "g4hip.node is not built"
     shape = E2BShape.real(n_layers=4, n_unshared=2, global_layers=(1, 3), vocab=4096)
     files, formats, hm, kcs, vcs = _model(shape)
     assert any(formats), "the model mixes block formats"
     cfg = {"overrides": {"num_layers": 4, "num_unshared_layers": 2, "global_layers": [1, 3], "vocab_size": 4096},
-           "maxSeqLen": MAX_SEQ, "position": POS, "token": TOKEN, "formats": formats}
+           "maxSeqLen": MAX_SEQ, "position": POS, "token": TOKEN, "formats": formats, "fused": fused}
     with tempfile.TemporaryDirectory() as d:
         for name, arr in files.items():
             np.ascontiguousarray(arr).tofile(os.path.join(d, name + ".bin"))
