@@ -19,8 +19,11 @@
 #include <algorithm>
 
 #include "g4_internal.hpp"
+#include "mqf_core.hpp"
 
 namespace {
+
+using namespace g4mqf;
 
 constexpr int NT = 256;
 constexpr float kMasked = -1e30f;
@@ -193,28 +196,6 @@ __device__ __forceinline__ float group_sum(float v) {
 // and V rows of the chunk. Loads are unconditional at clamped positions (rows
 // past the chunk are masked in the scores), so no branch or loop surrounds a
 // load: the compiler then waits for exactly the loads each step consumes.
-// exp(x) = 2^(x log2 e) on the hardware exp2 (v_exp_f32, 1 ulp): the
-// softmax and merge weights are exponents of differences <= 0, where the
-// product's rounding (|x| ulp of log2 e) stays below 1e-5 relative; a
-// library expf is some 15 instructions on the merge's critical path.
-__device__ __forceinline__ float mq_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504f); }
-
-// RoPE of position `pos` for the pair (i, i + hd/2): the frequency is the
-// correctly rounded f32 of 1/theta^(2i/hd) (divided in f32 by the f16
-// divisor when apply_divisor), the angle the f32 product, as
-// shaders/fused_per_head_norm_rope.wgsl:50-55 forms them; cos/sin of that
-// angle in f32 (within 2 ulp of the rounded exact values). The table kernel
-// and the in-launch path share it, so a precomputed table is bit-identical.
-__device__ __forceinline__ float2 rope_cos_sin(float theta, uint32_t apply_divisor, uint16_t divisor_bits, uint32_t i,
-                                               uint32_t hd, uint32_t pos) {
-  float f = (float)(1.0 / pow((double)theta, (double)(2 * i) / (double)hd));
-  if (apply_divisor) f = f / g4d::f16_bits_to_f32(divisor_bits);
-  const float ang = (float)pos * f;
-  float sn, cn;
-  sincosf(ang, &sn, &cn);
-  return make_float2(cn, sn);
-}
-
 template <int G, int HD, int CP, bool PAGED, bool FUSE>
 __global__ __launch_bounds__(NT) void attn_kernel(AttnArgs a) {
   constexpr int P = 32 * CP;        // positions of a chunk
@@ -783,15 +764,6 @@ __global__ __launch_bounds__(MW_NT) void attn_merge_wide_kernel(const float* ws,
 //    positions x 16 dims of V; 16 dim tiles.
 // At the end the four waves' (m, l, o) are combined in LDS and one partial
 // per head is written for attn_merge_kernel.
-typedef _Float16 mh8 __attribute__((ext_vector_type(8)));
-typedef _Float16 mh4 __attribute__((ext_vector_type(4)));
-typedef float mf4 __attribute__((ext_vector_type(4)));
-typedef uint32_t mu4 __attribute__((ext_vector_type(4)));
-
-constexpr int MQ_STEP = 64;  // positions per step
-constexpr int MQ_RS = 264;   // LDS row stride in halves (528 B)
-constexpr int MQ_G = 8, MQ_HD = 256;
-constexpr int kDppRor8 = 0x128;  // row_ror:8 within 16 lanes
 
 struct MqArgs {
   const float* q;  // [num_seqs][nqh][256]
@@ -1018,480 +990,12 @@ __global__ __launch_bounds__(NT, 2) void mq_attn_kernel(MqArgs a) {
   }
 }
 
-// Fused single-sequence form over a dense cache (the one-token decode step),
-// the whole attention block of src/engine.ts:1556-1584 in one launch:
-//  * every workgroup applies q_norm + RoPE to q once, cooperatively (thread t
-//    owns head t / 32 and the RoPE pairs (d, d + 128), d = 4 (t % 32) + 0..3),
-//    and stages the MFMA B operand (q hi / lo columns) in LDS;
-//  * the workgroup that owns the current position forms that position's K/V
-//    row (k_norm + RoPE, weightless v_norm), writes it to the caches and
-//    patches it into its LDS tile;
-//  * each workgroup writes one (m, l, o) partial per head; the last one to
-//    arrive (arrival counter per KV head, reset for the next call) merges
-//    the chunks in chunk order.
-// With one sequence the grid is a few dozen workgroups, so latency is the
-// instruction count of one wave's path: the per-thread work outside the
-// MFMA loop is kept to a handful of vector operations.
-constexpr int kMaxWarm = 4;
-// Dynamic LDS a warming launch adds to each workgroup's static ~75 KB: past
-// half of the CU's 160 KB, so one workgroup per CU (unused otherwise).
-constexpr size_t kWarmLds = 16384;
-struct MqfArgs {
-  const float* q_raw;  // [nqh][256]
-  const float* k_raw;  // [nkh][256]
-  const float* v_raw;
-  const uint16_t* q_w;
-  const uint16_t* k_w;
-  const uint16_t* rope_freqs;
-  float theta;
-  uint32_t apply_divisor;
-  float eps;
-  uint16_t* kc;  // [cap][nkh][256]
-  uint16_t* vc;
-  const uint32_t* pos_dev;
-  uint32_t cap, nqh, nkh;
-  float scale;
-  uint32_t window;
-  uint32_t nstep, max_chunks;
-  float* ws;      // chunk partials [nkh][max_chunks][8] (m, l, o)
-  float* ws1;     // group partials [nkh][MQF_FAN][8] (m, l, o)
-  uint32_t* cnt;  // [nkh][MQF_CNT] arrivals (groups, then the top), zero between calls
-  float* out;     // [nqh][256]
-  // L2 warming: workgroups max_chunks.. of row 0 read the weights of the
-  // launches that follow (see mqf_warm)
-  const uint8_t* wbase[kMaxWarm];
-  uint32_t wtotal[kMaxWarm];  // bytes of the matrix (reads past it return 0)
-  uint32_t wwgb[kMaxWarm];    // bytes each consuming workgroup reads
-  uint32_t wnwg[kMaxWarm];    // consuming workgroups
-  uint32_t nwarm_regions, nwarm;  // regions; warming workgroups (a multiple of 8)
-  const float2* rope_cs;          // [cap][128] (cos, sin) of every position (g4_ropeTable), or null
-};
-
-constexpr int MQF_QS = 264;  // LDS stride of a q column (halves)
-
-// Device-scope (agent) loads and stores through a buffer resource: written
-// through / read past the XCD-local L2, so they are coherent across XCDs
-// without a write-back or invalidation of the whole L2. Offsets in bytes.
-typedef float mqf_f4 __attribute__((ext_vector_type(4)));
-constexpr int kScDevice = 16;  // cache policy operand: sc1 (device scope)
-// Merge tree: chunk partials are merged in groups of up to MQF_FAN by the
-// last workgroup of each group to arrive; with more than one group, the last
-// group merger merges the group partials (two levels: MQF_FAN^2 chunks). The
-// plan uses the tree for windows of up to MQF_FAN chunks (one level); longer
-// windows end in the merge launch (mqf_kernel<true>).
-constexpr uint32_t MQF_FAN = 16, MQF_CNT = 32;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(float* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ void st_dev(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, kScDevice);
-}
-__device__ __forceinline__ void st_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off, const float4& v) {
-  __builtin_amdgcn_raw_buffer_store_b128(mqf_f4{v.x, v.y, v.z, v.w}, r, off, 0, kScDevice);
-}
-__device__ __forceinline__ float ld_dev(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kScDevice));
-}
-__device__ __forceinline__ float4 ld_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const mqf_f4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kScDevice);
-  return make_float4(v.x, v.y, v.z, v.w);
-}
-
-// Brings the weights of the launches that follow into the L2 of the XCD
-// that will read them. Workgroups are dispatched to the 8 XCDs in turn
-// (linear id mod 8), in this launch and in the consuming ones, so consuming
-// workgroup j reads through the L2 of XCD j % 8: warming workgroup p (at
-// linear id max_chunks + p, XCD c) reads the tiles of consuming workgroups
-// j = c + 8 (p / 8 + R i), R = nwarm / 8. These workgroups run on the CUs
-// the attention leaves idle; the loads go through a buffer resource sized to
-// each matrix, so a partial last tile reads zeros past its end.
-__device__ __forceinline__ void mqf_warm(const MqfArgs& a) {
-  const uint32_t p = blockIdx.x - a.max_chunks;
-  const uint32_t c = blockIdx.x & 7u, r = p >> 3, R = a.nwarm >> 3;
-  const uint32_t t = threadIdx.x;
-  // regions past nwarm_regions have no records (their loads return 0)
-  __amdgpu_buffer_rsrc_t rs[kMaxWarm];
-  uint32_t wgb[kMaxWarm], nwg[kMaxWarm], maxwg = 0;
-#pragma unroll
-  for (int g = 0; g < kMaxWarm; ++g) {
-    const bool on = (uint32_t)g < a.nwarm_regions;
-    rs[g] = __builtin_amdgcn_make_buffer_rsrc((void*)a.wbase[g], (short)0, on ? (int)a.wtotal[g] : 0, 0x00020000);
-    wgb[g] = on ? a.wwgb[g] : 0u;
-    nwg[g] = on ? a.wnwg[g] : 0u;
-    maxwg = max(maxwg, nwg[g]);
-  }
-  constexpr uint32_t kStep = 64u * NT * 8u;  // bytes one round of 8 loads covers
-  uint32_t acc = 0;
-  // one region's round at a time, the workgroups' first rounds staggered:
-  // a burst of every region at once queued ahead of the attention's own
-  // memory traffic and slowed it by 1 us
-  for (uint32_t k = 0; k < (p & 3u); ++k) __builtin_amdgcn_s_sleep(16);
-  for (uint32_t j = c + 8u * r; j < maxwg; j += 8u * R) {
-#pragma unroll
-    for (int g = 0; g < kMaxWarm; ++g) {
-      for (uint32_t o = 0; o < wgb[g]; o += kStep) {
-        uint32_t v[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          // one dword per 64-byte line brings the line into the cache
-          const uint32_t off = o + (64u * NT) * (uint32_t)k + 64u * t;
-          const bool in = j < nwg[g] && off < wgb[g];
-          v[k] = __builtin_amdgcn_raw_buffer_load_b32(rs[g], in ? j * wgb[g] + off : 0xfffffff0u, 0, 0);
-        }
-#pragma unroll
-        for (int k = 0; k < 8; ++k) acc ^= v[k];
-      }
-    }
-  }
-  asm volatile("" ::"v"(acc));
-}
-
-// LONG (windows past MQF_FAN chunks): K/V rows are loaded non-temporally
-// (read once, measured faster at 32K positions) and the workgroups end after
-// storing their partials, which the merge launch that follows combines.
+// The fused block as a launch of its own (blockIdx.y = KV head).
 template <bool LONG>
 __global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
-  if (blockIdx.x >= a.max_chunks) {  // (uniform) L2 warming workgroups
-    if (blockIdx.y == 0) mqf_warm(a);
-    return;
-  }
-  // K and V tiles; after the last step, the waves' o rows [4 waves][256 dims][16 rows]
-  __shared__ __align__(16) _Float16 kvt[2 * MQ_STEP * MQ_RS];
-  __shared__ __align__(16) _Float16 qs[16 * MQF_QS];  // B operand: column c = head c % 8, hi (c < 8) / lo
-  __shared__ float2 cs_s[MQ_HD / 2];
-  __shared__ float red_s[8];
-  __shared__ float kn_s[MQ_HD];
-  __shared__ __align__(16) uint16_t cur_s[2 * MQ_HD];  // the current row: k (roped), v; f16
-  __shared__ float ml_s[2 * 4 * MQ_G];                 // per (wave, head) m, then l
-  __shared__ __align__(16) float wt_s[4 * MQ_G];       // per (wave, head) weight
-  __shared__ uint32_t s_last;
-  _Float16* const kt = kvt;
-  _Float16* const vt = kvt + MQ_STEP * MQ_RS;
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q = l >> 4, c = l & 15;
-  const uint32_t kvh = blockIdx.y, chunk = blockIdx.x;
-  const uint32_t CH = MQ_STEP * a.nstep;
-  const uint32_t L = min(*a.pos_dev + 1, a.cap);
-  const uint32_t pos = L - 1;  // the position being decoded
-  const uint32_t wstart = (a.window != 0 && L > a.window) ? L - a.window : 0;
-  const uint32_t n = L - wstart;
-  const uint32_t nch = (n + CH - 1) / CH;
-  if (chunk >= nch) return;  // (uniform) past the live chunks
-  const uint32_t c0 = chunk * CH, cend = min(n, c0 + CH), last = wstart + cend - 1;
-  const uint32_t nst = (cend - c0 + MQ_STEP - 1) / MQ_STEP;
-  // this chunk ends at the current position and forms its row (without
-  // k_raw the layer reads a cache another layer has already written the
-  // row into: nothing is formed, stored or patched)
-  const bool own_row = a.k_raw != nullptr;
-  const bool owner = cend == n && own_row;
-  // thread -> (head, 4 dims of each RoPE half) for q, the partial and the merge
-  const int th = tid >> 5, td = 4 * (tid & 31);
-
-  mu4 pf[16];
-  auto load_step = [&](uint32_t st) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const uint32_t pc = (uint32_t)tid + 256u * (uint32_t)(i & 7);
-      const uint32_t r = pc >> 5, col = (pc & 31) * 8;
-      const uint32_t p = min(wstart + c0 + st * MQ_STEP + r, last);
-      const uint16_t* base = i < 8 ? a.kc : a.vc;
-      const mu4* src = (const mu4*)(base + ((size_t)p * a.nkh + kvh) * MQ_HD + col);
-      pf[i] = LONG ? __builtin_nontemporal_load(src) : *src;
-    }
-  };
-  auto store_step = [&]() {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const uint32_t pc = (uint32_t)tid + 256u * (uint32_t)(i & 7);
-      const uint32_t r = pc >> 5, col = (pc & 31) * 8;
-      *(mu4*)((i < 8 ? kt : vt) + r * MQ_RS + col) = pf[i];
-    }
-  };
-  // the owner's last step: rows from the current position on (the clamped
-  // rows repeat it) take the row formed here, not the cache's stale one
-  auto patch = [&](uint32_t st) {
-    const uint32_t r0 = last - (wstart + c0 + st * MQ_STEP);
-    for (uint32_t e = (uint32_t)tid; e < (MQ_STEP - r0) * 32; e += NT) {
-      const uint32_t r = r0 + e / 32, col = (e % 32) * 8;
-      *(mu4*)(kt + r * MQ_RS + col) = *(const mu4*)(cur_s + col);
-      *(mu4*)(vt + r * MQ_RS + col) = *(const mu4*)(cur_s + MQ_HD + col);
-    }
-  };
-
-  // ---- every load of the prologue, then the first step's rows ----
-  const float* qg = a.q_raw + (size_t)(kvh * MQ_G + th) * MQ_HD + td;
-  const float4 q0 = *(const float4*)qg, q1 = *(const float4*)(qg + MQ_HD / 2);
-  const uint2 w0 = *(const uint2*)(a.q_w + td), w1 = *(const uint2*)(a.q_w + MQ_HD / 2 + td);
-  const float kx = own_row ? a.k_raw[(size_t)kvh * MQ_HD + tid] : 0.f;
-  const float vx = own_row ? a.v_raw[(size_t)kvh * MQ_HD + tid] : 0.f;
-  const float kw = own_row ? g4d::f16_bits_to_f32(a.k_w[tid]) : 0.f;
-  const uint16_t rfb = a.rope_freqs[tid & (MQ_HD / 2 - 1)];
-  const float2 cst =
-      a.rope_cs ? a.rope_cs[(size_t)pos * (MQ_HD / 2) + (tid & (MQ_HD / 2 - 1))] : make_float2(1.f, 0.f);
-  __builtin_amdgcn_sched_barrier(0);
-  load_step(0);
-  __builtin_amdgcn_sched_barrier(0);
-
-  // RoPE of this position (rope_cos_sin), from the table when there is one:
-  // the frequency's f64 pow and a large-argument sincos are some 380 VALU
-  // instructions of the prologue's critical path
-  if (tid < MQ_HD / 2) cs_s[tid] = a.rope_cs ? cst : rope_cos_sin(a.theta, a.apply_divisor, rfb, tid, MQ_HD, pos);
-  const float sk = g4d::wave_sum_dpp(kx * kx), sv = g4d::wave_sum_dpp(vx * vx);
-  if (l == 0) {
-    red_s[w] = sk;
-    red_s[4 + w] = sv;
-  }
-  // q: the head's sum of squares over its 32 threads (two DPP rows)
-  float qss = (q0.x * q0.x + q0.y * q0.y) + (q0.z * q0.z + q0.w * q0.w) + (q1.x * q1.x + q1.y * q1.y) +
-              (q1.z * q1.z + q1.w * q1.w);
-  qss = g4d::sum16(qss);
-  qss = g4d::xsum16(qss);
-  const float invq = __builtin_amdgcn_rsqf(qss * (1.0f / (float)MQ_HD) + a.eps);
-  __syncthreads();
-  const float invk =
-      __builtin_amdgcn_rsqf(((red_s[0] + red_s[1]) + (red_s[2] + red_s[3])) * (1.0f / (float)MQ_HD) + a.eps);
-  const float invv =
-      __builtin_amdgcn_rsqf(((red_s[4] + red_s[5]) + (red_s[6] + red_s[7])) * (1.0f / (float)MQ_HD) + a.eps);
-  kn_s[tid] = kx * kw * invk;
-  cur_s[MQ_HD + tid] = g4d::f32_to_f16_bits(vx * invv);
-  {
-    const float x0[4] = {q0.x, q0.y, q0.z, q0.w}, x1[4] = {q1.x, q1.y, q1.z, q1.w};
-    const uint32_t wa[4] = {w0.x & 0xffffu, w0.x >> 16, w0.y & 0xffffu, w0.y >> 16};
-    const uint32_t wb[4] = {w1.x & 0xffffu, w1.x >> 16, w1.y & 0xffffu, w1.y >> 16};
-    mh4 h0, l0, h1, l1;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float2 cs = cs_s[td + e];
-      const float y0 = x0[e] * g4d::f16_bits_to_f32(wa[e]) * invq;
-      const float y1 = x1[e] * g4d::f16_bits_to_f32(wb[e]) * invq;
-      const float r0 = y0 * cs.x - y1 * cs.y, r1 = y0 * cs.y + y1 * cs.x;
-      h0[e] = (_Float16)r0;
-      l0[e] = (_Float16)(r0 - (float)h0[e]);
-      h1[e] = (_Float16)r1;
-      l1[e] = (_Float16)(r1 - (float)h1[e]);
-    }
-    *(mh4*)(qs + th * MQF_QS + td) = h0;
-    *(mh4*)(qs + (th + 8) * MQF_QS + td) = l0;
-    *(mh4*)(qs + th * MQF_QS + MQ_HD / 2 + td) = h1;
-    *(mh4*)(qs + (th + 8) * MQF_QS + MQ_HD / 2 + td) = l1;
-  }
-  __syncthreads();
-  if (tid < MQ_HD / 2) {
-    const float2 cs = cs_s[tid];
-    const float x0 = kn_s[tid], x1 = kn_s[tid + MQ_HD / 2];
-    cur_s[tid] = g4d::f32_to_f16_bits(x0 * cs.x - x1 * cs.y);
-    cur_s[tid + MQ_HD / 2] = g4d::f32_to_f16_bits(x0 * cs.y + x1 * cs.x);
-  }
-  store_step();
-  __syncthreads();
-  if (owner) {
-    a.kc[((size_t)pos * a.nkh + kvh) * MQ_HD + tid] = cur_s[tid];
-    a.vc[((size_t)pos * a.nkh + kvh) * MQ_HD + tid] = cur_s[MQ_HD + tid];
-    if (nst == 1) patch(0);
-  }
-  mh8 qb[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) qb[j] = *(const mh8*)(qs + c * MQF_QS + 32 * j + 8 * q);
-  __syncthreads();
-
-  mf4 O[16];
-#pragma unroll
-  for (int dt = 0; dt < 16; ++dt) O[dt] = mf4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;  // of head c % 8
-
-  for (uint32_t st = 0; st < nst; ++st) {
-    const bool more = st + 1 < nst;
-    if (more) load_step(st + 1);
-    mf4 S = mf4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const mh8 A = *(const mh8*)(kt + (16 * w + c) * MQ_RS + 32 * j + 8 * q);
-      S = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, qb[j], S, 0, 0, 0);
-    }
-    float sc[4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float v = S[i] + g4d::dpp<kDppRor8>(S[i]);
-      const uint32_t off = c0 + st * MQ_STEP + 16u * w + 4u * q + i;
-      sc[i] = off < cend ? v * a.scale : -INFINITY;
-      mx = fmaxf(mx, sc[i]);
-    }
-    mx = g4d::xmax16(mx);
-    mx = g4d::xmax32(mx);
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = m_new == -INFINITY ? 1.f : mq_exp(m_run - m_new);
-    float p[4], ps = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      p[i] = sc[i] == -INFINITY ? 0.f : mq_exp(sc[i] - m_new);
-      ps += p[i];
-    }
-    ps = g4d::xsum16(ps);
-    ps = g4d::xsum32(ps);
-    l_run = l_run * alpha + ps;
-    m_run = m_new;
-    float ar[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float a0 = g4d::lane_value(alpha, i), a1 = g4d::lane_value(alpha, 4 + i);
-      ar[i] = (q & 1) ? a1 : a0;
-    }
-    mh4 P;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const _Float16 hi = (_Float16)p[i];
-      P[i] = c < 8 ? hi : (_Float16)(p[i] - (float)hi);
-    }
-#pragma unroll
-    for (int dt = 0; dt < 16; ++dt) {
-      mh4 Bv;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) Bv[i] = vt[(16 * w + 4 * q + i) * MQ_RS + 16 * dt + c];
-      mf4 o = O[dt];
-      if (st > 0) {  // (uniform) the first step's O is zero
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] *= ar[i];
-      }
-      O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(P, Bv, o, 0, 0, 0);
-    }
-    __syncthreads();
-    if (more) {
-      store_step();
-      if (owner && st + 2 == nst) {  // (uniform) the patched rows are stored rows: order the two writes
-        __syncthreads();
-        patch(st + 1);
-      }
-      __syncthreads();
-    }
-  }
-
-  // ---- the four waves, then this chunk's partial ----
-  // O row 4q + i of lane (q, c) is head (4q + i) % 8 (the p_hi rows for
-  // q < 2, the p_lo rows for q >= 2) at dim 16 dt + c.
-  float* ow = (float*)kvt;
-#pragma unroll
-  for (int dt = 0; dt < 16; ++dt) *(mf4*)(ow + ((w * MQ_HD) + 16 * dt + c) * 16 + 4 * q) = O[dt];
-  if (q == 0 && c < MQ_G) {
-    ml_s[w * MQ_G + c] = m_run;
-    ml_s[4 * MQ_G + w * MQ_G + c] = l_run;
-  }
-  __syncthreads();
-  const size_t nparts = (size_t)a.nkh * a.max_chunks * MQ_G;
-  // chunk partials: m [nparts], l [nparts], o [nparts][256] (f32)
-  const __amdgpu_buffer_rsrc_t r0 = dev_rsrc(a.ws, (uint32_t)(nparts * (MQ_HD + 2) * sizeof(float)));
-  const size_t part0 = ((size_t)kvh * a.max_chunks + chunk) * MQ_G;
-  if (tid < MQ_G) {  // thread h: the head's weight per wave and the chunk's (m, l)
-    float m4[4], M = -INFINITY;
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww) {
-      m4[ww] = ml_s[ww * MQ_G + tid];
-      M = fmaxf(M, m4[ww]);
-    }
-    float Ls = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww) {
-      const float wt = m4[ww] == -INFINITY ? 0.f : mq_exp(m4[ww] - M);
-      wt_s[ww * MQ_G + tid] = wt;
-      Ls += wt * ml_s[4 * MQ_G + ww * MQ_G + tid];
-    }
-    st_dev(r0, (uint32_t)(part0 + tid) * 4u, M);
-    st_dev(r0, (uint32_t)(nparts + part0 + tid) * 4u, Ls);
-  }
-  __syncthreads();
-  {  // thread = dim: o[h] = sum over waves of wt * (hi row + lo row)
-    float o[MQ_G];
-#pragma unroll
-    for (int h = 0; h < MQ_G; ++h) o[h] = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww) {
-      const float* r = ow + (ww * MQ_HD + tid) * 16;
-      const mf4 h03 = *(const mf4*)r, h47 = *(const mf4*)(r + 4), l03 = *(const mf4*)(r + 8),
-                l47 = *(const mf4*)(r + 12);
-      const mf4 w03 = *(const mf4*)(wt_s + ww * MQ_G), w47 = *(const mf4*)(wt_s + ww * MQ_G + 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        o[i] += w03[i] * (h03[i] + l03[i]);
-        o[4 + i] += w47[i] * (h47[i] + l47[i]);
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < MQ_G; ++h) st_dev(r0, (uint32_t)(2 * nparts + (part0 + h) * MQ_HD + tid) * 4u, o[h]);
-  }
-  if constexpr (LONG) return;  // the merge launch that follows combines the chunks
-
-  // ---- merge tree: the last arriver of each group merges it in chunk order ----
-  // thread (head th, dims td.. and td + 128..): one pass with a running maximum
-  auto merge = [&](__amdgpu_buffer_rsrc_t r, size_t stride, size_t first, uint32_t count, float& M, float& Ls,
-                   float4& o0, float4& o1) {
-    M = -INFINITY;
-    Ls = 0.f;
-    o0 = make_float4(0.f, 0.f, 0.f, 0.f);
-    o1 = o0;
-#pragma unroll 4
-    for (uint32_t s2 = 0; s2 < count; ++s2) {
-      const size_t pp = first + (size_t)s2 * MQ_G + th;
-      const float m = ld_dev(r, (uint32_t)pp * 4u), lv = ld_dev(r, (uint32_t)(stride + pp) * 4u);
-      const uint32_t ob = (uint32_t)(2 * stride + pp * MQ_HD + td) * 4u;
-      const float4 a0 = ld_dev4(r, ob);
-      const float4 a1 = ld_dev4(r, ob + MQ_HD / 2 * 4u);
-      const float Mn = fmaxf(M, m);
-      const float fo = M == -INFINITY ? 0.f : mq_exp(M - Mn);
-      const float fn = m == -INFINITY ? 0.f : mq_exp(m - Mn);
-      Ls = Ls * fo + lv * fn;
-      o0.x = o0.x * fo + a0.x * fn; o0.y = o0.y * fo + a0.y * fn;
-      o0.z = o0.z * fo + a0.z * fn; o0.w = o0.w * fo + a0.w * fn;
-      o1.x = o1.x * fo + a1.x * fn; o1.y = o1.y * fo + a1.y * fn;
-      o1.z = o1.z * fo + a1.z * fn; o1.w = o1.w * fo + a1.w * fn;
-      M = Mn;
-    }
-  };
-  // The partials are written and read with device-scope accesses (written
-  // through / read past the XCD-local L2), so an arrival needs only its own
-  // stores complete, not a write-back or invalidation of the whole L2.
-  auto arrive = [&](uint32_t* c, uint32_t fanin) -> bool {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_s_waitcnt(0);  // every store of this thread has completed
-    __syncthreads();
-    if (tid == 0)
-      s_last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == fanin - 1 ? 1u : 0u;
-    __syncthreads();
-    if (!s_last) return false;
-    if (tid == 0) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // all arrivals are in
-    return true;
-  };
-  auto write_out = [&](float Ls, const float4& o0, const float4& o1) {
-    const float li = Ls > 0.f ? 1.0f / Ls : 0.f;
-    float* dst = a.out + ((size_t)kvh * MQ_G + th) * MQ_HD + td;
-    *(float4*)dst = make_float4(o0.x * li, o0.y * li, o0.z * li, o0.w * li);
-    *(float4*)(dst + MQ_HD / 2) = make_float4(o1.x * li, o1.y * li, o1.z * li, o1.w * li);
-  };
-  uint32_t* cnt = a.cnt + (size_t)kvh * MQF_CNT;
-  const uint32_t ng = (nch + MQF_FAN - 1) / MQF_FAN, g = chunk / MQF_FAN;
-  if (!arrive(cnt + g, min(MQF_FAN, nch - g * MQF_FAN))) return;
-  float M, Ls;
-  float4 o0, o1;
-  merge(r0, nparts, ((size_t)kvh * a.max_chunks + g * MQF_FAN) * MQ_G,
-        min(MQF_FAN, nch - g * MQF_FAN), M, Ls, o0, o1);
-  if (ng == 1) {
-    write_out(Ls, o0, o1);
-    return;
-  }
-  const size_t nparts1 = (size_t)a.nkh * MQF_FAN * MQ_G;
-  const __amdgpu_buffer_rsrc_t r1 = dev_rsrc(a.ws1, (uint32_t)(nparts1 * (MQ_HD + 2) * sizeof(float)));
-  {
-    const size_t pp = ((size_t)kvh * MQF_FAN + g) * MQ_G + th;
-    if ((tid & 31) == 0) {
-      st_dev(r1, (uint32_t)pp * 4u, M);
-      st_dev(r1, (uint32_t)(nparts1 + pp) * 4u, Ls);
-    }
-    const uint32_t ob = (uint32_t)(2 * nparts1 + pp * MQ_HD + td) * 4u;
-    st_dev4(r1, ob, o0);
-    st_dev4(r1, ob + MQ_HD / 2 * 4u, o1);
-  }
-  if (!arrive(cnt + MQF_CNT - 1, ng)) return;
-  merge(r1, nparts1, (size_t)kvh * MQF_FAN * MQ_G, ng, M, Ls, o0, o1);
-  write_out(Ls, o0, o1);
+  mqf_body<LONG, false>(a, blockIdx.x, blockIdx.y, blockIdx.x);
 }
+
 
 // RoPE table: (cos, sin) of every position and pair, rope_cos_sin's values.
 __global__ __launch_bounds__(NT) void rope_table_kernel(float2* out, float theta, uint32_t apply_divisor,
@@ -1701,11 +1205,10 @@ int launch_attn(g4_ctx* ctx, const AttnArgs& a, uint32_t G, uint32_t hd, int cp,
 // device-scope round trips per tree level cost more than a launch boundary,
 // and the merge launch spreads each head's partials over many workgroups).
 // Past kMaxSplits chunks a workgroup takes several steps. The arrival
-// counters sit in the first kMqfCnt bytes of the workspace, at the same
-// place whatever the plan, so that layers of different windows can share
-// one workspace; the chunk partials follow, then the group partials.
-constexpr uint32_t kMqfMaxKvHeads = 64;
-constexpr size_t kMqfCnt = (size_t)kMqfMaxKvHeads * MQF_CNT * sizeof(uint32_t);
+// counters and the q/k/v flags sit in the first kMqfCnt bytes of the
+// workspace, at the same place whatever the plan, so that layers of
+// different windows can share one workspace; the chunk partials follow,
+// then the group partials.
 struct MqfPlan {
   uint32_t nstep, max_chunks;
   bool partials;  // chunk partials + a merge launch
@@ -1821,6 +1324,103 @@ int check_heads(const char* fn, uint32_t nqh, uint32_t nkh, uint32_t hd) {
   G4_REQUIRE(hd == 128 || hd == 256 || hd == 512, "%s: head_dim %u not in {128, 256, 512}", fn, hd);
   return G4_OK;
 }
+
+}  // namespace
+
+namespace g4mqf {
+int mqf_check(g4_ctx* ctx, const char* fn, const float* q_raw, const float* k_raw, const float* v_raw,
+              const uint16_t* q_norm_w, const uint16_t* k_norm_w, const uint16_t* rope_freqs, uint16_t* k_cache,
+              uint16_t* v_cache, float* output, const g4_attn_fused_params& p, void* workspace,
+              const uint32_t* position_dev, const g4_warm_region* regions, int nregions, const float* rope_cs,
+              uint32_t rope_rows) {
+  (void)ctx;
+  G4_REQUIRE(!rope_cs || rope_rows >= p.max_seq_len, "g4_attnDecodeFusedWarm: RoPE table of %u rows < max_seq_len %u",
+             rope_rows, p.max_seq_len);
+  G4_REQUIRE(q_raw && q_norm_w && k_cache && v_cache && output && workspace && position_dev,
+             "g4_attnDecodeFused: null buffer");
+  // k_raw = v_raw = k_norm_w = null: the caches already hold this position's
+  // row (a layer reading its producer layer's cache)
+  G4_REQUIRE(k_raw ? (v_raw && k_norm_w) : (!v_raw && !k_norm_w),
+             "g4_attnDecodeFused: k_raw, v_raw and k_norm_w are all given or all null");
+  G4_REQUIRE(nregions >= 0 && nregions <= kMaxWarm && (nregions == 0 || regions),
+             "g4_attnDecodeFusedWarm: 0..%d warm regions", kMaxWarm);
+  for (int i = 0; i < nregions; ++i) {
+    const g4_warm_region& r = regions[i];
+    // (below 4 GiB - 4 KiB: the kernel's out-of-range reads use offset 0xfffffff0)
+    G4_REQUIRE(r.base && r.total_bytes > 0 && r.total_bytes <= 0xfffff000ull && r.wg_bytes > 0 && r.nwgs > 0 &&
+                   r.wg_bytes * (uint64_t)r.nwgs <= 0xfffff000ull,
+               "g4_attnDecodeFusedWarm: region %d empty or beyond 4 GiB - 4 KiB", i);
+  }
+  G4_REQUIRE(!p.apply_divisor || rope_freqs, "g4_attnDecodeFused: apply_divisor needs rope_freqs");
+  G4_REQUIRE(((uintptr_t)k_cache & 15) == 0 && ((uintptr_t)v_cache & 15) == 0 && ((uintptr_t)workspace & 15) == 0,
+             "g4_attnDecodeFused: KV caches and workspace must be 16-byte aligned");
+  int rc = check_heads(fn, p.num_q_heads, p.num_kv_heads, p.head_dim);
+  if (rc) return rc;
+  G4_REQUIRE(p.max_seq_len > 0, "g4_attnDecodeFused: max_seq_len must be >= 1");
+  G4_REQUIRE(p.num_q_heads == 8 * p.num_kv_heads && (p.head_dim == 256 || p.head_dim == 512),
+             "g4_attnDecodeFused: built for 8 query heads per kv head and head_dim 256/512");
+  return G4_OK;
+}
+
+int mqf_prepare(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float* v_raw, const uint16_t* q_norm_w,
+                const uint16_t* k_norm_w, const uint16_t* rope_freqs, uint16_t* k_cache, uint16_t* v_cache,
+                float* output, const g4_attn_fused_params& p, void* workspace, size_t workspace_bytes,
+                const uint32_t* position_dev, const g4_warm_region* regions, int nregions, const float* rope_cs,
+                uint32_t busy_extra, bool& applies, MqfLaunch& L) {
+  applies = p.head_dim == MQ_HD && p.num_q_heads == MQ_G * p.num_kv_heads && p.num_kv_heads <= kMqfMaxKvHeads &&
+            ((uintptr_t)q_norm_w & 15) == 0 && eff_len(p.max_seq_len, p.sliding_window) <= 4 * MQ_STEP * MQF_FAN * MQF_FAN;
+  if (!applies) return G4_OK;
+  const MqfPlan mp = mqf_plan(p);
+  G4_REQUIRE(workspace_bytes >= mp.bytes, "g4_attnDecodeFused: workspace %zu bytes < %zu required", workspace_bytes,
+             mp.bytes);
+  MqfArgs& m = L.m;
+  m = MqfArgs{};
+  m.q_raw = q_raw;
+  m.k_raw = k_raw;
+  m.v_raw = v_raw;
+  m.q_w = q_norm_w;
+  m.k_w = k_norm_w;
+  m.rope_freqs = rope_freqs ? rope_freqs : q_norm_w;  // read unconditionally, used only with the divisor
+  m.theta = p.theta;
+  m.apply_divisor = p.apply_divisor;
+  m.eps = p.eps;
+  m.kc = k_cache;
+  m.vc = v_cache;
+  m.pos_dev = position_dev;
+  m.cap = p.max_seq_len;
+  m.nqh = p.num_q_heads;
+  m.nkh = p.num_kv_heads;
+  m.scale = p.scale;
+  m.window = p.sliding_window;
+  m.nstep = mp.nstep;
+  m.max_chunks = mp.max_chunks;
+  m.ws = (float*)((uint8_t*)workspace + kMqfCnt);
+  m.ws1 = (float*)((uint8_t*)workspace + kMqfCnt + mp.bytes_ws0);
+  m.cnt = (uint32_t*)workspace;
+  m.out = output;
+  m.rope_cs = (const float2*)rope_cs;
+  // warming workgroups on the CUs the attention leaves idle, a multiple
+  // of 8 so that every XCD gets as many. A launch that warms asks for
+  // kWarmLds more LDS per workgroup, so no two of its workgroups share a
+  // CU: a warming workgroup next to an attention one slowed it by 1 us.
+  const uint32_t busy = mp.max_chunks * p.num_kv_heads + busy_extra;
+  const uint32_t idle = (uint32_t)ctx->num_cus > busy ? (uint32_t)ctx->num_cus - busy : 0u;
+  m.nwarm = nregions ? idle / 8u * 8u : 0u;
+  m.nwarm_regions = m.nwarm ? (uint32_t)nregions : 0u;
+  for (int i = 0; i < (int)m.nwarm_regions; ++i) {
+    m.wbase[i] = (const uint8_t*)regions[i].base;
+    m.wtotal[i] = (uint32_t)regions[i].total_bytes;
+    m.wwgb[i] = (uint32_t)regions[i].wg_bytes;
+    m.wnwg[i] = regions[i].nwgs;
+  }
+  m.flags = (uint32_t*)((uint8_t*)workspace + kMqfCntOnly);
+  m.nflags = 0;
+  L.partials = mp.partials;
+  return G4_OK;
+}
+}  // namespace g4mqf
+
+namespace {
 
 int check_plan(const char* fn, const SplitPlan& sp) {
   G4_REQUIRE(sp.nsplit <= kMaxSplits, "%s: %u positions exceed the %u-position limit of one decode call", fn,
@@ -2074,87 +1674,28 @@ int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, 
                            const g4_warm_region* regions, int nregions, const float* rope_cs,
                            uint32_t rope_rows) {
   G4_ENTER(ctx);
-  G4_REQUIRE(!rope_cs || rope_rows >= p.max_seq_len, "g4_attnDecodeFusedWarm: RoPE table of %u rows < max_seq_len %u",
-             rope_rows, p.max_seq_len);
-  G4_REQUIRE(q_raw && q_norm_w && k_cache && v_cache && output && workspace && position_dev,
-             "g4_attnDecodeFused: null buffer");
-  // k_raw = v_raw = k_norm_w = null: the caches already hold this position's
-  // row (a layer reading its producer layer's cache)
-  G4_REQUIRE(k_raw ? (v_raw && k_norm_w) : (!v_raw && !k_norm_w),
-             "g4_attnDecodeFused: k_raw, v_raw and k_norm_w are all given or all null");
-  G4_REQUIRE(nregions >= 0 && nregions <= kMaxWarm && (nregions == 0 || regions),
-             "g4_attnDecodeFusedWarm: 0..%d warm regions", kMaxWarm);
-  for (int i = 0; i < nregions; ++i) {
-    const g4_warm_region& r = regions[i];
-    // (below 4 GiB - 4 KiB: the kernel's out-of-range reads use offset 0xfffffff0)
-    G4_REQUIRE(r.base && r.total_bytes > 0 && r.total_bytes <= 0xfffff000ull && r.wg_bytes > 0 && r.nwgs > 0 &&
-                   r.wg_bytes * (uint64_t)r.nwgs <= 0xfffff000ull,
-               "g4_attnDecodeFusedWarm: region %d empty or beyond 4 GiB - 4 KiB", i);
-  }
-  G4_REQUIRE(!p.apply_divisor || rope_freqs, "g4_attnDecodeFused: apply_divisor needs rope_freqs");
-  G4_REQUIRE(((uintptr_t)k_cache & 15) == 0 && ((uintptr_t)v_cache & 15) == 0 && ((uintptr_t)workspace & 15) == 0,
-             "g4_attnDecodeFused: KV caches and workspace must be 16-byte aligned");
-  int rc = check_heads(__func__, p.num_q_heads, p.num_kv_heads, p.head_dim);
+  int rc = mqf_check(ctx, "g4_attnDecodeFusedWarm", q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs, k_cache,
+                     v_cache, output, p, workspace, position_dev, regions, nregions, rope_cs, rope_rows);
   if (rc) return rc;
-  G4_REQUIRE(p.max_seq_len > 0, "g4_attnDecodeFused: max_seq_len must be >= 1");
   const uint32_t G = p.num_q_heads / p.num_kv_heads;
-  G4_REQUIRE(G == 8 && (p.head_dim == 256 || p.head_dim == 512),
-             "g4_attnDecodeFused: built for 8 query heads per kv head and head_dim 256/512");
-  if (p.head_dim == MQ_HD && p.num_kv_heads <= kMqfMaxKvHeads && ((uintptr_t)q_norm_w & 15) == 0 &&
-      eff_len(p.max_seq_len, p.sliding_window) <= 4 * MQ_STEP * MQF_FAN * MQF_FAN) {
-    const MqfPlan mp = mqf_plan(p);
-    G4_REQUIRE(workspace_bytes >= mp.bytes, "g4_attnDecodeFused: workspace %zu bytes < %zu required",
-               workspace_bytes, mp.bytes);
-    MqfArgs m{};
-    m.q_raw = q_raw;
-    m.k_raw = k_raw;
-    m.v_raw = v_raw;
-    m.q_w = q_norm_w;
-    m.k_w = k_norm_w;
-    m.rope_freqs = rope_freqs ? rope_freqs : q_norm_w;  // read unconditionally, used only with the divisor
-    m.theta = p.theta;
-    m.apply_divisor = p.apply_divisor;
-    m.eps = p.eps;
-    m.kc = k_cache;
-    m.vc = v_cache;
-    m.pos_dev = position_dev;
-    m.cap = p.max_seq_len;
-    m.nqh = p.num_q_heads;
-    m.nkh = p.num_kv_heads;
-    m.scale = p.scale;
-    m.window = p.sliding_window;
-    m.nstep = mp.nstep;
-    m.max_chunks = mp.max_chunks;
-    m.ws = (float*)((uint8_t*)workspace + kMqfCnt);
-    m.ws1 = (float*)((uint8_t*)workspace + kMqfCnt + mp.bytes_ws0);
-    m.cnt = (uint32_t*)workspace;
-    m.out = output;
-    m.rope_cs = (const float2*)rope_cs;
-    // warming workgroups on the CUs the attention leaves idle, a multiple
-    // of 8 so that every XCD gets as many. A launch that warms asks for
-    // kWarmLds more LDS per workgroup, so no two of its workgroups share a
-    // CU: a warming workgroup next to an attention one slowed it by 1 us.
-    const uint32_t busy = mp.max_chunks * p.num_kv_heads;
-    const uint32_t idle = (uint32_t)ctx->num_cus > busy ? (uint32_t)ctx->num_cus - busy : 0u;
-    m.nwarm = nregions ? idle / 8u * 8u : 0u;
-    m.nwarm_regions = m.nwarm ? (uint32_t)nregions : 0u;
-    for (int i = 0; i < (int)m.nwarm_regions; ++i) {
-      m.wbase[i] = (const uint8_t*)regions[i].base;
-      m.wtotal[i] = (uint32_t)regions[i].total_bytes;
-      m.wwgb[i] = (uint32_t)regions[i].wg_bytes;
-      m.wnwg[i] = regions[i].nwgs;
-    }
-    if (mp.partials)
-      hipLaunchKernelGGL(mqf_kernel<true>, dim3(mp.max_chunks + m.nwarm, p.num_kv_heads), dim3(NT),
+  bool one_launch = false;
+  MqfLaunch L{};
+  rc = mqf_prepare(ctx, q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs, k_cache, v_cache, output, p, workspace,
+                   workspace_bytes, position_dev, regions, nregions, rope_cs, 0, one_launch, L);
+  if (rc) return rc;
+  if (one_launch) {
+    const MqfArgs& m = L.m;
+    if (L.partials)
+      hipLaunchKernelGGL(mqf_kernel<true>, dim3(m.max_chunks + m.nwarm, p.num_kv_heads), dim3(NT),
                          m.nwarm ? kWarmLds : 0, ctx->stream, m);
     else
-      hipLaunchKernelGGL(mqf_kernel<false>, dim3(mp.max_chunks + m.nwarm, p.num_kv_heads), dim3(NT),
+      hipLaunchKernelGGL(mqf_kernel<false>, dim3(m.max_chunks + m.nwarm, p.num_kv_heads), dim3(NT),
                          m.nwarm ? kWarmLds : 0, ctx->stream, m);
     G4_LAUNCHED(ctx, "attn_decode_fused_mfma");
-    if (!mp.partials) return G4_OK;
+    if (!L.partials) return G4_OK;
     const LenArgs la{nullptr, position_dev, p.max_seq_len, p.max_seq_len, p.sliding_window};
-    return merge_launch(ctx, m.ws, output, p.num_q_heads, p.num_kv_heads, MQ_G, MQ_HD, mp.max_chunks, 1, la,
-                        MQ_STEP * mp.nstep);
+    return merge_launch(ctx, m.ws, output, p.num_q_heads, p.num_kv_heads, MQ_G, MQ_HD, m.max_chunks, 1, la,
+                        MQ_STEP * m.nstep);
   }
   // (the two-launch form computes the RoPE per call: a table is not needed)
   const SplitPlan sp = plan_splits(eff_len(p.max_seq_len, p.sliding_window));

@@ -27,6 +27,7 @@
 //    RMSNorm) prologue, softcap epilogue, several matrices sharing one input
 //    per launch (q/k/v), gate/up pairs with the GELU product epilogue.
 #include "g4_internal.hpp"
+#include "mqf_core.hpp"
 
 #include <algorithm>
 #include <type_traits>
@@ -1237,7 +1238,9 @@ __device__ __forceinline__ void mv_d8_group(float v, bool real, uint32_t row, ui
 
 // Adds each row's U unit partials (RG lanes per row, then a butterfly) and
 // stores the tile's rows: y, softcap(y), or gelu(gate) * up for a pair.
-template <class T, int NTH, int NMAT>
+// DEV: the rows are stored at device scope (written through to the point of
+// coherence), for readers in other workgroups of the same launch.
+template <class T, int NTH, int NMAT, bool DEV = false>
 __device__ __forceinline__ void mv_reduce_store(const float* red, const GemvSeg& sg, uint32_t t, int tid, float cap,
                                                 bool track, g4d::Cand& best, uint8_t* d8 = nullptr,
                                                 g4d::Cand* tkt = nullptr) {
@@ -1264,7 +1267,8 @@ __device__ __forceinline__ void mv_reduce_store(const float* red, const GemvSeg&
         if (d8) mv_d8_group(v, real, row, sg.M, d8);
     } else if (real) {
       const float v = cap > 0.f ? softcap(y[0], cap) : y[0];
-      sg.Y[row] = v;
+      if constexpr (DEV) __hip_atomic_store(sg.Y + row, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else sg.Y[row] = v;
       const g4d::Cand d{v, row};
       if (track && g4d::better(d, best)) best = d;
       // top-k classes: a tile's rows are distinct classes (TR <= 256) and
@@ -1307,13 +1311,14 @@ __device__ __forceinline__ void mv_topk_partial(const g4d::Cand* tkt, const Gemv
 // tiles per CU, the LM head); the other instances hold the one-tile path
 // only. (Bounding the staged instance to two 12-wave workgroups per CU,
 // 80 VGPRs, spilled the tile loop to scratch: 199 us instead of 82.)
-template <int QT, int BPR, int NWV, int PRO, int NMAT, bool STAGED>
-__global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8_t* w_up, ProArgs pa, float cap) {
+template <int QT, int BPR, int NWV, int PRO, int NMAT, bool STAGED, bool DEV = false>
+__device__ __forceinline__ void mv_body(const GemvSegs& segs, const uint8_t* w_up, const ProArgs& pa, float cap,
+                                        uint8_t* smem) {
   using G = MvGeom<BPR, NWV>;
   using T = MvTile<QT, BPR, NWV>;
   constexpr int NTH = G::NTH;
   static_assert(PRO != 3 || (QT == 1 && NMAT == 1), "D8 input: one Q6_K matrix");
-  extern __shared__ __align__(16) uint8_t smem[];
+  static_assert(!DEV || (!STAGED && NMAT == 1), "device-scope rows: one tile of one matrix");
   int si = 0;
 #pragma unroll
   for (int i = 1; i < 4; ++i)
@@ -1392,7 +1397,7 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
     }
     lds_barrier();
     g4d::Cand best{-1e30f, 0u};
-    mv_reduce_store<T, NTH, NMAT>(red, sg, tb, tid, cap, segs.amx != nullptr, best, d8, tkt);
+    mv_reduce_store<T, NTH, NMAT, DEV>(red, sg, tb, tid, cap, segs.amx != nullptr, best, d8, tkt);
     if constexpr (NMAT == 1)
       if (segs.amx)
         mv_argmax_partial<NWV>(best, (g4d::Cand*)(smem + MvXA<BPR, PRO>::RED8), segs.amx + blockIdx.x);
@@ -1439,6 +1444,12 @@ __global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8
         mv_argmax_partial<NWV>(best, (g4d::Cand*)(smem + MvXA<BPR, PRO>::RED8), segs.amx + blockIdx.x);
     if (tkt) mv_topk_partial<NTH>(tkt, segs, blockIdx.x - sg.wg_begin);
   }
+}
+
+template <int QT, int BPR, int NWV, int PRO, int NMAT, bool STAGED>
+__global__ __launch_bounds__(64 * NWV) void mv_kernel(GemvSegs segs, const uint8_t* w_up, ProArgs pa, float cap) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  mv_body<QT, BPR, NWV, PRO, NMAT, STAGED>(segs, w_up, pa, cap, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -1846,6 +1857,38 @@ int mv_launch(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
                      w_up, q.pa, q.epi ? q.cap : 0.f);
   G4_LAUNCHED(ctx, "mv");
   return G4_OK;
+}
+
+// The q/k/v matvec and the attention block in one launch (one sequence,
+// one KV head, a window of at most MQF_FAN chunks). Workgroups [0, nmv) are
+// the one-tile matvec (Q4_K rows of 1536, MNWV waves: the width the matvec's
+// own launch would take, so the rows are the same bit for bit) with its norm
+// prologue; they store their rows at device scope and then each sets its
+// flag.
+// Workgroups nmv.. are the attention block's chunk and L2-warming
+// workgroups (the first 256 threads; the other two waves end at once).
+// A chunk workgroup reads the position and requests its K/V rows at
+// once, and waits for the flags only before it reads q/k/v, so the window's
+// load overlaps the matvec instead of following a launch boundary. The
+// matvec workgroups come first in the grid and wait on nothing: in-order
+// dispatch lets them finish whatever the residency, and the wait is bounded.
+constexpr int kQkvNwv = 6;  // workgroup width (waves): the wider of the two parts
+template <int PRO, int MNWV>
+__global__ __launch_bounds__(64 * kQkvNwv) void qkv_attn_kernel(GemvSegs segs, ProArgs pa, g4mqf::MqfArgs a,
+                                                                 uint32_t nmv) {
+  static_assert(MNWV <= kQkvNwv && 64 * kQkvNwv >= g4mqf::MQ_NT, "both parts fit the workgroup");
+  extern __shared__ __align__(16) uint8_t smem[];
+  if (blockIdx.x < nmv) {  // (uniform)
+    if (threadIdx.x >= 64u * MNWV) return;  // (uniform per wave)
+    mv_body<0, 6, MNWV, PRO, 1, false, true>(segs, nullptr, pa, 0.f, smem);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);  // every row store of this thread is acknowledged
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(a.flags + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  if (threadIdx.x >= (unsigned)g4mqf::MQ_NT) return;  // (uniform per wave)
+  g4mqf::mqf_body<false, true>(a, blockIdx.x - nmv, 0u, blockIdx.x);
 }
 
 // workgroup widths in waves for a row of BPR super-blocks (slots must tile it)
@@ -2302,6 +2345,87 @@ int g4_normAddMatmulTopk(g4_ctx* ctx, int wtype, const float* x, const uint16_t*
   rc = launch_gemv(ctx, q);
   if (rc) return rc;
   return g4_internal_topk_final(ctx, parts, (int)wgs, 1, result);
+}
+
+int g4_qkvAttnDecodeFusedWarm(g4_ctx* ctx, const float* x, const uint16_t* w1, const float* residual,
+                              const uint16_t* out_scale, const uint16_t* w2, float* h_out,
+                              const void* const* weights, float* const* outputs, int nseg, uint32_t N, float eps,
+                              const uint16_t* q_norm_w, const uint16_t* k_norm_w, const uint16_t* rope_freqs,
+                              uint16_t* k_cache, uint16_t* v_cache, float* output, g4_attn_fused_params p,
+                              void* workspace, size_t workspace_bytes, const uint32_t* position_dev,
+                              const g4_warm_region* regions, int nregions, const float* rope_cs,
+                              uint32_t rope_rows) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(nseg == 1 || nseg == 3, "g4_qkvAttnDecodeFusedWarm: nseg must be 1 (q) or 3 (q, k, v)");
+  G4_REQUIRE(weights && outputs, "g4_qkvAttnDecodeFusedWarm: null buffer");
+  const uint32_t rows[3] = {p.num_q_heads * p.head_dim, p.num_kv_heads * p.head_dim, p.num_kv_heads * p.head_dim};
+  const float* q_raw = outputs[0];
+  const float* k_raw = nseg == 3 ? outputs[1] : nullptr;
+  const float* v_raw = nseg == 3 ? outputs[2] : nullptr;
+  int rc = g4mqf::mqf_check(ctx, "g4_qkvAttnDecodeFusedWarm", q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs,
+                            k_cache, v_cache, output, p, workspace, position_dev, regions, nregions, rope_cs,
+                            rope_rows);
+  if (rc) return rc;
+  // the matvec's own checks (g4_normAddScaleMatmulSegments)
+  G4_REQUIRE(x && w1, "g4_qkvAttnDecodeFusedWarm: null buffer");
+  G4_REQUIRE(!out_scale || residual, "g4_qkvAttnDecodeFusedWarm: out_scale needs the residual form");
+  G4_REQUIRE(!residual == !w2, "g4_qkvAttnDecodeFusedWarm: residual and w2 go together");
+  G4_REQUIRE(N == 1536 || N == 2048, "g4_qkvAttnDecodeFusedWarm: N=%u unsupported (1536 or 2048)", N);
+  G4_REQUIRE(((uintptr_t)x & 15) == 0 && (!residual || ((uintptr_t)residual & 15) == 0) &&
+                 (!h_out || ((uintptr_t)h_out & 15) == 0),
+             "g4_qkvAttnDecodeFusedWarm: activations must be 16-byte aligned");
+  G4_REQUIRE(((uintptr_t)w1 & 7) == 0 && ((uintptr_t)w2 & 7) == 0,
+             "g4_qkvAttnDecodeFusedWarm: norm weights must be 8-byte aligned");
+  for (int i = 0; i < nseg; ++i) {
+    G4_REQUIRE(weights[i] && outputs[i], "g4_qkvAttnDecodeFusedWarm: segment %d empty", i);
+    rc = check_w(__func__, 0, weights[i]);
+    if (rc) return rc;
+  }
+  // the one-launch form: Q4_K rows of 1536 at the width the matvec's own
+  // launch takes (6 or 3 waves), one KV head, a window merged in the
+  // launch, a flag per matvec workgroup
+  GemvSegs sg{};
+  for (int i = 0; i < nseg; ++i) sg.s[i] = GemvSeg{(const uint8_t*)weights[i], outputs[i], rows[i], 0};
+  const int mnwv = mv_pick(6, sg.s, nseg);
+  const uint32_t tr = 16u * (uint32_t)mnwv / 6u;  // rows per tile
+  uint32_t nmv = 0;
+  for (int i = 0; i < nseg; ++i) {
+    sg.s[i].wg_begin = nmv;
+    nmv += ceil_div(rows[i], tr);
+  }
+  bool applies = false;
+  g4mqf::MqfLaunch L{};
+  if (N == 1536 && (mnwv == 6 || mnwv == 3) && p.num_kv_heads == 1 && nmv <= g4mqf::kMaxFlags) {
+    rc = g4mqf::mqf_prepare(ctx, q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs, k_cache, v_cache, output, p,
+                            workspace, workspace_bytes, position_dev, regions, nregions, rope_cs, nmv, applies, L);
+    if (rc) return rc;
+    applies = applies && !L.partials;
+  }
+  if (!applies) {  // two launches, the same results
+    rc = g4_normAddScaleMatmulSegments(ctx, 0, x, w1, residual, out_scale, w2, h_out, weights, outputs, rows, nseg,
+                                       N, eps, 0.f);
+    if (rc) return rc;
+    return g4_attnDecodeFusedWarm(ctx, q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs, k_cache, v_cache,
+                                  output, p, workspace, workspace_bytes, position_dev, regions, nregions, rope_cs,
+                                  rope_rows);
+  }
+  sg.n = nseg;
+  sg.rep = 1;
+  L.m.nflags = nmv;
+  const ProArgs pa{x, w1, residual, w2, h_out, eps, out_scale};
+  const dim3 grid(nmv + L.m.max_chunks + L.m.nwarm), block(64 * kQkvNwv);
+  auto launch = [&](auto kern, size_t lds) {
+    int r = claim_lds((const void*)kern, ctx, lds);
+    if (r) return r;
+    hipLaunchKernelGGL(kern, grid, block, lds, ctx->stream, sg, pa, L.m, nmv);
+    G4_LAUNCHED(ctx, "qkv_attn_fused");
+    return G4_OK;
+  };
+  if (residual)
+    return mnwv == 6 ? launch(qkv_attn_kernel<2, 6>, mv_lds_bytes<0, 6, 6, 2, 1>(false))
+                     : launch(qkv_attn_kernel<2, 3>, mv_lds_bytes<0, 6, 3, 2, 1>(false));
+  return mnwv == 6 ? launch(qkv_attn_kernel<1, 6>, mv_lds_bytes<0, 6, 6, 1, 1>(false))
+                   : launch(qkv_attn_kernel<1, 3>, mv_lds_bytes<0, 6, 3, 1, 1>(false));
 }
 
 }  // extern "C"

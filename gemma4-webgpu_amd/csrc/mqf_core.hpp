@@ -1,0 +1,610 @@
+// mqf_core.hpp — the fused single-sequence decode attention block on the
+// matrix cores (q/k norm + RoPE, v_norm, KV row store, split-K attention and
+// its in-launch merge), shared by k_attn.hip (g4_attnDecodeFused*) and
+// k_gemv.hip (the launch that also runs the q/k/v matvec).
+#pragma once
+#include "g4_internal.hpp"
+
+namespace g4mqf {
+
+constexpr int MQ_NT = 256;  // threads of an attention workgroup
+
+// exp(x) = 2^(x log2 e) on the hardware exp2 (v_exp_f32, 1 ulp): the
+// softmax and merge weights are exponents of differences <= 0, where the
+// product's rounding (|x| ulp of log2 e) stays below 1e-5 relative; a
+// library expf is some 15 instructions on the merge's critical path.
+__device__ __forceinline__ float mq_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504f); }
+
+// RoPE of position `pos` for the pair (i, i + hd/2): the frequency is the
+// correctly rounded f32 of 1/theta^(2i/hd) (divided in f32 by the f16
+// divisor when apply_divisor), the angle the f32 product, as
+// shaders/fused_per_head_norm_rope.wgsl:50-55 forms them; cos/sin of that
+// angle in f32 (within 2 ulp of the rounded exact values). The table kernel
+// and the in-launch path share it, so a precomputed table is bit-identical.
+__device__ __forceinline__ float2 rope_cos_sin(float theta, uint32_t apply_divisor, uint16_t divisor_bits, uint32_t i,
+                                               uint32_t hd, uint32_t pos) {
+  float f = (float)(1.0 / pow((double)theta, (double)(2 * i) / (double)hd));
+  if (apply_divisor) f = f / g4d::f16_bits_to_f32(divisor_bits);
+  const float ang = (float)pos * f;
+  float sn, cn;
+  sincosf(ang, &sn, &cn);
+  return make_float2(cn, sn);
+}
+
+typedef _Float16 mh8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mh4 __attribute__((ext_vector_type(4)));
+typedef float mf4 __attribute__((ext_vector_type(4)));
+typedef uint32_t mu4 __attribute__((ext_vector_type(4)));
+
+constexpr int MQ_STEP = 64;  // positions per step
+constexpr int MQ_RS = 264;   // LDS row stride in halves (528 B)
+constexpr int MQ_G = 8, MQ_HD = 256;
+constexpr int kDppRor8 = 0x128;  // row_ror:8 within 16 lanes
+
+// Fused single-sequence form over a dense cache (the one-token decode step),
+// the whole attention block of src/engine.ts:1556-1584 in one launch:
+//  * every workgroup applies q_norm + RoPE to q once, cooperatively (thread t
+//    owns head t / 32 and the RoPE pairs (d, d + 128), d = 4 (t % 32) + 0..3),
+//    and stages the MFMA B operand (q hi / lo columns) in LDS;
+//  * the workgroup that owns the current position forms that position's K/V
+//    row (k_norm + RoPE, weightless v_norm), writes it to the caches and
+//    patches it into its LDS tile;
+//  * each workgroup writes one (m, l, o) partial per head; the last one to
+//    arrive (arrival counter per KV head, reset for the next call) merges
+//    the chunks in chunk order.
+// With one sequence the grid is a few dozen workgroups, so latency is the
+// instruction count of one wave's path: the per-thread work outside the
+// MFMA loop is kept to a handful of vector operations.
+constexpr int kMaxWarm = 4;
+// Dynamic LDS a warming launch adds to each workgroup's static ~75 KB: past
+// half of the CU's 160 KB, so one workgroup per CU (unused otherwise).
+constexpr size_t kWarmLds = 16384;
+struct MqfArgs {
+  const float* q_raw;  // [nqh][256]
+  const float* k_raw;  // [nkh][256]
+  const float* v_raw;
+  const uint16_t* q_w;
+  const uint16_t* k_w;
+  const uint16_t* rope_freqs;
+  float theta;
+  uint32_t apply_divisor;
+  float eps;
+  uint16_t* kc;  // [cap][nkh][256]
+  uint16_t* vc;
+  const uint32_t* pos_dev;
+  uint32_t cap, nqh, nkh;
+  float scale;
+  uint32_t window;
+  uint32_t nstep, max_chunks;
+  float* ws;      // chunk partials [nkh][max_chunks][8] (m, l, o)
+  float* ws1;     // group partials [nkh][MQF_FAN][8] (m, l, o)
+  uint32_t* cnt;  // [nkh][MQF_CNT] arrivals (groups, then the top), zero between calls
+  float* out;     // [nqh][256]
+  // L2 warming: workgroups max_chunks.. of row 0 read the weights of the
+  // launches that follow (see mqf_warm)
+  const uint8_t* wbase[kMaxWarm];
+  uint32_t wtotal[kMaxWarm];  // bytes of the matrix (reads past it return 0)
+  uint32_t wwgb[kMaxWarm];    // bytes each consuming workgroup reads
+  uint32_t wnwg[kMaxWarm];    // consuming workgroups
+  uint32_t nwarm_regions, nwarm;  // regions; warming workgroups (a multiple of 8)
+  const float2* rope_cs;          // [cap][128] (cos, sin) of every position (g4_ropeTable), or null
+  // the launch that also runs the q/k/v matvec (mqf_body<false, true>):
+  // one flag per matvec workgroup, set when its rows are stored, cleared by
+  // the merger
+  uint32_t* flags;
+  uint32_t nflags;
+};
+
+constexpr int MQF_QS = 264;  // LDS stride of a q column (halves)
+
+// Device-scope (agent) loads and stores through a buffer resource: written
+// through / read past the XCD-local L2, so they are coherent across XCDs
+// without a write-back or invalidation of the whole L2. Offsets in bytes.
+typedef float mqf_f4 __attribute__((ext_vector_type(4)));
+constexpr int kScDevice = 16;  // cache policy operand: sc1 (device scope)
+// Merge tree: chunk partials are merged in groups of up to MQF_FAN by the
+// last workgroup of each group to arrive; with more than one group, the last
+// group merger merges the group partials (two levels: MQF_FAN^2 chunks). The
+// plan uses the tree for windows of up to MQF_FAN chunks (one level); longer
+// windows end in the merge launch (mqf_kernel<true>).
+constexpr uint32_t MQF_FAN = 16, MQF_CNT = 32;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(float* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void st_dev(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, kScDevice);
+}
+__device__ __forceinline__ void st_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off, const float4& v) {
+  __builtin_amdgcn_raw_buffer_store_b128(mqf_f4{v.x, v.y, v.z, v.w}, r, off, 0, kScDevice);
+}
+__device__ __forceinline__ float ld_dev(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kScDevice));
+}
+__device__ __forceinline__ float4 ld_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const mqf_f4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kScDevice);
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
+// The q/k/v flags of a launch that also runs the matvec. The wait is bounded
+// (kFlagSpin polls, each a device-scope round trip, about 0.1 s in all) so
+// that every workgroup ends even if a flag never comes; the matvec
+// workgroups precede the attention ones in the grid and wait on nothing, so
+// in-order dispatch always lets them finish.
+constexpr uint32_t kFlagSpin = 1u << 16;
+constexpr uint32_t kMaxFlags = 256;
+// The workgroup's MQ_NT threads (4 waves; a wider launch's other waves have
+// ended) poll one flag each; the vote goes through LDS, one word per wave.
+__device__ __forceinline__ void mqf_wait_flags(const MqfArgs& a, int tid) {
+  __shared__ uint32_t s_ok[MQ_NT / 64];
+  // flags past nflags read as 0 through the resource: they count as set
+  const __amdgpu_buffer_rsrc_t fr = dev_rsrc((float*)a.flags, a.nflags * 4u);
+  for (uint32_t it = 0;; ++it) {
+    const uint32_t f = __builtin_amdgcn_raw_buffer_load_b32(fr, (uint32_t)tid * 4u, 0, kScDevice);
+    const bool set = (uint32_t)tid >= a.nflags || f != 0u;
+    const uint64_t votes = __ballot(set);
+    if ((tid & 63) == 0) s_ok[tid >> 6] = votes == ~0ull ? 1u : 0u;
+    __syncthreads();
+    bool all = true;
+#pragma unroll
+    for (int w = 0; w < MQ_NT / 64; ++w) all = all && s_ok[w] != 0u;
+    __syncthreads();  // every wave has read the votes before the next round writes them
+    if (all || it >= kFlagSpin) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+__device__ __forceinline__ void mqf_clear_flags(const MqfArgs& a, int tid) {
+  const __amdgpu_buffer_rsrc_t fr = dev_rsrc((float*)a.flags, a.nflags * 4u);
+  for (uint32_t i = (uint32_t)tid; i < a.nflags; i += MQ_NT)
+    __builtin_amdgcn_raw_buffer_store_b32(0u, fr, i * 4u, 0, kScDevice);
+}
+
+// Workspace head: the arrival counters ([kv head][MQF_CNT]), then the q/k/v
+// flags; zero between calls.
+constexpr uint32_t kMqfMaxKvHeads = 64;
+constexpr size_t kMqfCntOnly = (size_t)kMqfMaxKvHeads * MQF_CNT * sizeof(uint32_t);
+constexpr size_t kMqfCnt = kMqfCntOnly + kMaxFlags * sizeof(uint32_t);
+
+struct MqfLaunch {
+  MqfArgs m;
+  bool partials;  // chunk partials + the merge launch
+};
+// Host side (k_attn.hip). mqf_check: the argument checks of
+// g4_attnDecodeFusedWarm (messages name `fn`).
+int mqf_check(g4_ctx* ctx, const char* fn, const float* q_raw, const float* k_raw, const float* v_raw,
+              const uint16_t* q_norm_w, const uint16_t* k_norm_w, const uint16_t* rope_freqs, uint16_t* k_cache,
+              uint16_t* v_cache, float* output, const g4_attn_fused_params& p, void* workspace,
+              const uint32_t* position_dev, const g4_warm_region* regions, int nregions, const float* rope_cs,
+              uint32_t rope_rows);
+// mqf_prepare: after those checks, sets
+// `applies` when the one-launch matrix-core form serves p and then fills L
+// (workspace plan, warming workgroups on the CUs left idle by the attention
+// and `busy_extra` other workgroups of the same launch). m.flags points at
+// the workspace's flags, m.nflags is 0.
+int mqf_prepare(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float* v_raw, const uint16_t* q_norm_w,
+                const uint16_t* k_norm_w, const uint16_t* rope_freqs, uint16_t* k_cache, uint16_t* v_cache,
+                float* output, const g4_attn_fused_params& p, void* workspace, size_t workspace_bytes,
+                const uint32_t* position_dev, const g4_warm_region* regions, int nregions, const float* rope_cs,
+                uint32_t busy_extra, bool& applies, MqfLaunch& L);
+
+// Brings the weights of the launches that follow into the L2 of the XCD
+// that will read them. Workgroups are dispatched to the 8 XCDs in turn
+// (linear id mod 8), in this launch and in the consuming ones, so consuming
+// workgroup j reads through the L2 of XCD j % 8: warming workgroup p (at
+// linear id max_chunks + p, XCD c) reads the tiles of consuming workgroups
+// j = c + 8 (p / 8 + R i), R = nwarm / 8. These workgroups run on the CUs
+// the attention leaves idle; the loads go through a buffer resource sized to
+// each matrix, so a partial last tile reads zeros past its end.
+__device__ __forceinline__ void mqf_warm(const MqfArgs& a, uint32_t p, uint32_t c) {
+  const uint32_t r = p >> 3, R = a.nwarm >> 3;
+  const uint32_t t = threadIdx.x;
+  // regions past nwarm_regions have no records (their loads return 0)
+  __amdgpu_buffer_rsrc_t rs[kMaxWarm];
+  uint32_t wgb[kMaxWarm], nwg[kMaxWarm], maxwg = 0;
+#pragma unroll
+  for (int g = 0; g < kMaxWarm; ++g) {
+    const bool on = (uint32_t)g < a.nwarm_regions;
+    rs[g] = __builtin_amdgcn_make_buffer_rsrc((void*)a.wbase[g], (short)0, on ? (int)a.wtotal[g] : 0, 0x00020000);
+    wgb[g] = on ? a.wwgb[g] : 0u;
+    nwg[g] = on ? a.wnwg[g] : 0u;
+    maxwg = max(maxwg, nwg[g]);
+  }
+  constexpr uint32_t kStep = 64u * MQ_NT * 8u;  // bytes one round of 8 loads covers
+  uint32_t acc = 0;
+  // one region's round at a time, the workgroups' first rounds staggered:
+  // a burst of every region at once queued ahead of the attention's own
+  // memory traffic and slowed it by 1 us
+  for (uint32_t k = 0; k < (p & 3u); ++k) __builtin_amdgcn_s_sleep(16);
+  for (uint32_t j = c + 8u * r; j < maxwg; j += 8u * R) {
+#pragma unroll
+    for (int g = 0; g < kMaxWarm; ++g) {
+      for (uint32_t o = 0; o < wgb[g]; o += kStep) {
+        uint32_t v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          // one dword per 64-byte line brings the line into the cache
+          const uint32_t off = o + (64u * MQ_NT) * (uint32_t)k + 64u * t;
+          const bool in = j < nwg[g] && off < wgb[g];
+          v[k] = __builtin_amdgcn_raw_buffer_load_b32(rs[g], in ? j * wgb[g] + off : 0xfffffff0u, 0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc ^= v[k];
+      }
+    }
+  }
+  asm volatile("" ::"v"(acc));
+}
+
+// LONG (windows past MQF_FAN chunks): K/V rows are loaded non-temporally
+// (read once, measured faster at 32K positions) and the workgroups end after
+// storing their partials, which the merge launch that follows combines.
+template <bool LONG, bool FUSED>
+__device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t kvh, uint32_t lin) {
+  static_assert(!(LONG && FUSED), "the fused matvec form merges in the launch");
+  if (bx >= a.max_chunks) {  // (uniform) L2 warming workgroups
+    if (kvh == 0) mqf_warm(a, bx - a.max_chunks, lin & 7u);
+    return;
+  }
+  // K and V tiles; after the last step, the waves' o rows [4 waves][256 dims][16 rows]
+  __shared__ __align__(16) _Float16 kvt[2 * MQ_STEP * MQ_RS];
+  __shared__ __align__(16) _Float16 qs[16 * MQF_QS];  // B operand: column c = head c % 8, hi (c < 8) / lo
+  __shared__ float2 cs_s[MQ_HD / 2];
+  __shared__ float red_s[8];
+  __shared__ float kn_s[MQ_HD];
+  __shared__ __align__(16) uint16_t cur_s[2 * MQ_HD];  // the current row: k (roped), v; f16
+  __shared__ float ml_s[2 * 4 * MQ_G];                 // per (wave, head) m, then l
+  __shared__ __align__(16) float wt_s[4 * MQ_G];       // per (wave, head) weight
+  __shared__ uint32_t s_last;
+  _Float16* const kt = kvt;
+  _Float16* const vt = kvt + MQ_STEP * MQ_RS;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q = l >> 4, c = l & 15;
+  const uint32_t chunk = bx;
+  const uint32_t CH = MQ_STEP * a.nstep;
+  const uint32_t L = min(*a.pos_dev + 1, a.cap);
+  const uint32_t pos = L - 1;  // the position being decoded
+  const uint32_t wstart = (a.window != 0 && L > a.window) ? L - a.window : 0;
+  const uint32_t n = L - wstart;
+  const uint32_t nch = (n + CH - 1) / CH;
+  if (chunk >= nch) return;  // (uniform) past the live chunks
+  const uint32_t c0 = chunk * CH, cend = min(n, c0 + CH), last = wstart + cend - 1;
+  const uint32_t nst = (cend - c0 + MQ_STEP - 1) / MQ_STEP;
+  // this chunk ends at the current position and forms its row (without
+  // k_raw the layer reads a cache another layer has already written the
+  // row into: nothing is formed, stored or patched)
+  const bool own_row = a.k_raw != nullptr;
+  const bool owner = cend == n && own_row;
+  // thread -> (head, 4 dims of each RoPE half) for q, the partial and the merge
+  const int th = tid >> 5, td = 4 * (tid & 31);
+
+  mu4 pf[16];
+  auto load_step = [&](uint32_t st) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t pc = (uint32_t)tid + 256u * (uint32_t)(i & 7);
+      const uint32_t r = pc >> 5, col = (pc & 31) * 8;
+      const uint32_t p = min(wstart + c0 + st * MQ_STEP + r, last);
+      const uint16_t* base = i < 8 ? a.kc : a.vc;
+      const mu4* src = (const mu4*)(base + ((size_t)p * a.nkh + kvh) * MQ_HD + col);
+      pf[i] = LONG ? __builtin_nontemporal_load(src) : *src;
+    }
+  };
+  auto store_step = [&]() {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t pc = (uint32_t)tid + 256u * (uint32_t)(i & 7);
+      const uint32_t r = pc >> 5, col = (pc & 31) * 8;
+      *(mu4*)((i < 8 ? kt : vt) + r * MQ_RS + col) = pf[i];
+    }
+  };
+  // the owner's last step: rows from the current position on (the clamped
+  // rows repeat it) take the row formed here, not the cache's stale one
+  auto patch = [&](uint32_t st) {
+    const uint32_t r0 = last - (wstart + c0 + st * MQ_STEP);
+    for (uint32_t e = (uint32_t)tid; e < (MQ_STEP - r0) * 32; e += MQ_NT) {
+      const uint32_t r = r0 + e / 32, col = (e % 32) * 8;
+      *(mu4*)(kt + r * MQ_RS + col) = *(const mu4*)(cur_s + col);
+      *(mu4*)(vt + r * MQ_RS + col) = *(const mu4*)(cur_s + MQ_HD + col);
+    }
+  };
+
+  // ---- every load of the prologue, then the first step's rows ----
+  // (FUSED: q, k and v come from the matvec workgroups of the same launch;
+  // the K/V rows and the weights are requested first, then q/k/v are read at
+  // device scope once every matvec workgroup has flagged its rows stored)
+  const size_t qoff = (size_t)(kvh * MQ_G + th) * MQ_HD + td;
+  float4 q0, q1;
+  float kx, vx;
+  if constexpr (!FUSED) {
+    const float* qg = a.q_raw + qoff;
+    q0 = *(const float4*)qg;
+    q1 = *(const float4*)(qg + MQ_HD / 2);
+  }
+  const uint2 w0 = *(const uint2*)(a.q_w + td), w1 = *(const uint2*)(a.q_w + MQ_HD / 2 + td);
+  if constexpr (!FUSED) {
+    kx = own_row ? a.k_raw[(size_t)kvh * MQ_HD + tid] : 0.f;
+    vx = own_row ? a.v_raw[(size_t)kvh * MQ_HD + tid] : 0.f;
+  }
+  const float kw = own_row ? g4d::f16_bits_to_f32(a.k_w[tid]) : 0.f;
+  const uint16_t rfb = a.rope_freqs[tid & (MQ_HD / 2 - 1)];
+  const float2 cst =
+      a.rope_cs ? a.rope_cs[(size_t)pos * (MQ_HD / 2) + (tid & (MQ_HD / 2 - 1))] : make_float2(1.f, 0.f);
+  __builtin_amdgcn_sched_barrier(0);
+  load_step(0);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (FUSED) {
+    mqf_wait_flags(a, tid);
+    const __amdgpu_buffer_rsrc_t rq = dev_rsrc((float*)a.q_raw, a.nqh * MQ_HD * 4u);
+    q0 = ld_dev4(rq, (uint32_t)qoff * 4u);
+    q1 = ld_dev4(rq, (uint32_t)(qoff + MQ_HD / 2) * 4u);
+    // (k_raw / v_raw are null in a layer without its own row: reads of an
+    // empty resource return 0)
+    const __amdgpu_buffer_rsrc_t rk = dev_rsrc((float*)a.k_raw, own_row ? a.nkh * MQ_HD * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rv = dev_rsrc((float*)a.v_raw, own_row ? a.nkh * MQ_HD * 4u : 0u);
+    kx = ld_dev(rk, (kvh * MQ_HD + (uint32_t)tid) * 4u);
+    vx = ld_dev(rv, (kvh * MQ_HD + (uint32_t)tid) * 4u);
+  }
+
+  // RoPE of this position (rope_cos_sin), from the table when there is one:
+  // the frequency's f64 pow and a large-argument sincos are some 380 VALU
+  // instructions of the prologue's critical path
+  if (tid < MQ_HD / 2) cs_s[tid] = a.rope_cs ? cst : rope_cos_sin(a.theta, a.apply_divisor, rfb, tid, MQ_HD, pos);
+  const float sk = g4d::wave_sum_dpp(kx * kx), sv = g4d::wave_sum_dpp(vx * vx);
+  if (l == 0) {
+    red_s[w] = sk;
+    red_s[4 + w] = sv;
+  }
+  // q: the head's sum of squares over its 32 threads (two DPP rows)
+  float qss = (q0.x * q0.x + q0.y * q0.y) + (q0.z * q0.z + q0.w * q0.w) + (q1.x * q1.x + q1.y * q1.y) +
+              (q1.z * q1.z + q1.w * q1.w);
+  qss = g4d::sum16(qss);
+  qss = g4d::xsum16(qss);
+  const float invq = __builtin_amdgcn_rsqf(qss * (1.0f / (float)MQ_HD) + a.eps);
+  __syncthreads();
+  const float invk =
+      __builtin_amdgcn_rsqf(((red_s[0] + red_s[1]) + (red_s[2] + red_s[3])) * (1.0f / (float)MQ_HD) + a.eps);
+  const float invv =
+      __builtin_amdgcn_rsqf(((red_s[4] + red_s[5]) + (red_s[6] + red_s[7])) * (1.0f / (float)MQ_HD) + a.eps);
+  kn_s[tid] = kx * kw * invk;
+  cur_s[MQ_HD + tid] = g4d::f32_to_f16_bits(vx * invv);
+  {
+    const float x0[4] = {q0.x, q0.y, q0.z, q0.w}, x1[4] = {q1.x, q1.y, q1.z, q1.w};
+    const uint32_t wa[4] = {w0.x & 0xffffu, w0.x >> 16, w0.y & 0xffffu, w0.y >> 16};
+    const uint32_t wb[4] = {w1.x & 0xffffu, w1.x >> 16, w1.y & 0xffffu, w1.y >> 16};
+    mh4 h0, l0, h1, l1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float2 cs = cs_s[td + e];
+      const float y0 = x0[e] * g4d::f16_bits_to_f32(wa[e]) * invq;
+      const float y1 = x1[e] * g4d::f16_bits_to_f32(wb[e]) * invq;
+      const float r0 = y0 * cs.x - y1 * cs.y, r1 = y0 * cs.y + y1 * cs.x;
+      h0[e] = (_Float16)r0;
+      l0[e] = (_Float16)(r0 - (float)h0[e]);
+      h1[e] = (_Float16)r1;
+      l1[e] = (_Float16)(r1 - (float)h1[e]);
+    }
+    *(mh4*)(qs + th * MQF_QS + td) = h0;
+    *(mh4*)(qs + (th + 8) * MQF_QS + td) = l0;
+    *(mh4*)(qs + th * MQF_QS + MQ_HD / 2 + td) = h1;
+    *(mh4*)(qs + (th + 8) * MQF_QS + MQ_HD / 2 + td) = l1;
+  }
+  __syncthreads();
+  if (tid < MQ_HD / 2) {
+    const float2 cs = cs_s[tid];
+    const float x0 = kn_s[tid], x1 = kn_s[tid + MQ_HD / 2];
+    cur_s[tid] = g4d::f32_to_f16_bits(x0 * cs.x - x1 * cs.y);
+    cur_s[tid + MQ_HD / 2] = g4d::f32_to_f16_bits(x0 * cs.y + x1 * cs.x);
+  }
+  store_step();
+  __syncthreads();
+  if (owner) {
+    a.kc[((size_t)pos * a.nkh + kvh) * MQ_HD + tid] = cur_s[tid];
+    a.vc[((size_t)pos * a.nkh + kvh) * MQ_HD + tid] = cur_s[MQ_HD + tid];
+    if (nst == 1) patch(0);
+  }
+  mh8 qb[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) qb[j] = *(const mh8*)(qs + c * MQF_QS + 32 * j + 8 * q);
+  __syncthreads();
+
+  mf4 O[16];
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) O[dt] = mf4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;  // of head c % 8
+
+  for (uint32_t st = 0; st < nst; ++st) {
+    const bool more = st + 1 < nst;
+    if (more) load_step(st + 1);
+    mf4 S = mf4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const mh8 A = *(const mh8*)(kt + (16 * w + c) * MQ_RS + 32 * j + 8 * q);
+      S = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, qb[j], S, 0, 0, 0);
+    }
+    float sc[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = S[i] + g4d::dpp<kDppRor8>(S[i]);
+      const uint32_t off = c0 + st * MQ_STEP + 16u * w + 4u * q + i;
+      sc[i] = off < cend ? v * a.scale : -INFINITY;
+      mx = fmaxf(mx, sc[i]);
+    }
+    mx = g4d::xmax16(mx);
+    mx = g4d::xmax32(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = m_new == -INFINITY ? 1.f : mq_exp(m_run - m_new);
+    float p[4], ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = sc[i] == -INFINITY ? 0.f : mq_exp(sc[i] - m_new);
+      ps += p[i];
+    }
+    ps = g4d::xsum16(ps);
+    ps = g4d::xsum32(ps);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+    float ar[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a0 = g4d::lane_value(alpha, i), a1 = g4d::lane_value(alpha, 4 + i);
+      ar[i] = (q & 1) ? a1 : a0;
+    }
+    mh4 P;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const _Float16 hi = (_Float16)p[i];
+      P[i] = c < 8 ? hi : (_Float16)(p[i] - (float)hi);
+    }
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) {
+      mh4 Bv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Bv[i] = vt[(16 * w + 4 * q + i) * MQ_RS + 16 * dt + c];
+      mf4 o = O[dt];
+      if (st > 0) {  // (uniform) the first step's O is zero
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] *= ar[i];
+      }
+      O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(P, Bv, o, 0, 0, 0);
+    }
+    __syncthreads();
+    if (more) {
+      store_step();
+      if (owner && st + 2 == nst) {  // (uniform) the patched rows are stored rows: order the two writes
+        __syncthreads();
+        patch(st + 1);
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---- the four waves, then this chunk's partial ----
+  // O row 4q + i of lane (q, c) is head (4q + i) % 8 (the p_hi rows for
+  // q < 2, the p_lo rows for q >= 2) at dim 16 dt + c.
+  float* ow = (float*)kvt;
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) *(mf4*)(ow + ((w * MQ_HD) + 16 * dt + c) * 16 + 4 * q) = O[dt];
+  if (q == 0 && c < MQ_G) {
+    ml_s[w * MQ_G + c] = m_run;
+    ml_s[4 * MQ_G + w * MQ_G + c] = l_run;
+  }
+  __syncthreads();
+  const size_t nparts = (size_t)a.nkh * a.max_chunks * MQ_G;
+  // chunk partials: m [nparts], l [nparts], o [nparts][256] (f32)
+  const __amdgpu_buffer_rsrc_t r0 = dev_rsrc(a.ws, (uint32_t)(nparts * (MQ_HD + 2) * sizeof(float)));
+  const size_t part0 = ((size_t)kvh * a.max_chunks + chunk) * MQ_G;
+  if (tid < MQ_G) {  // thread h: the head's weight per wave and the chunk's (m, l)
+    float m4[4], M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      m4[ww] = ml_s[ww * MQ_G + tid];
+      M = fmaxf(M, m4[ww]);
+    }
+    float Ls = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float wt = m4[ww] == -INFINITY ? 0.f : mq_exp(m4[ww] - M);
+      wt_s[ww * MQ_G + tid] = wt;
+      Ls += wt * ml_s[4 * MQ_G + ww * MQ_G + tid];
+    }
+    st_dev(r0, (uint32_t)(part0 + tid) * 4u, M);
+    st_dev(r0, (uint32_t)(nparts + part0 + tid) * 4u, Ls);
+  }
+  __syncthreads();
+  {  // thread = dim: o[h] = sum over waves of wt * (hi row + lo row)
+    float o[MQ_G];
+#pragma unroll
+    for (int h = 0; h < MQ_G; ++h) o[h] = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float* r = ow + (ww * MQ_HD + tid) * 16;
+      const mf4 h03 = *(const mf4*)r, h47 = *(const mf4*)(r + 4), l03 = *(const mf4*)(r + 8),
+                l47 = *(const mf4*)(r + 12);
+      const mf4 w03 = *(const mf4*)(wt_s + ww * MQ_G), w47 = *(const mf4*)(wt_s + ww * MQ_G + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[i] += w03[i] * (h03[i] + l03[i]);
+        o[4 + i] += w47[i] * (h47[i] + l47[i]);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < MQ_G; ++h) st_dev(r0, (uint32_t)(2 * nparts + (part0 + h) * MQ_HD + tid) * 4u, o[h]);
+  }
+  if constexpr (LONG) return;  // the merge launch that follows combines the chunks
+
+  // ---- merge tree: the last arriver of each group merges it in chunk order ----
+  // thread (head th, dims td.. and td + 128..): one pass with a running maximum
+  auto merge = [&](__amdgpu_buffer_rsrc_t r, size_t stride, size_t first, uint32_t count, float& M, float& Ls,
+                   float4& o0, float4& o1) {
+    M = -INFINITY;
+    Ls = 0.f;
+    o0 = make_float4(0.f, 0.f, 0.f, 0.f);
+    o1 = o0;
+#pragma unroll 4
+    for (uint32_t s2 = 0; s2 < count; ++s2) {
+      const size_t pp = first + (size_t)s2 * MQ_G + th;
+      const float m = ld_dev(r, (uint32_t)pp * 4u), lv = ld_dev(r, (uint32_t)(stride + pp) * 4u);
+      const uint32_t ob = (uint32_t)(2 * stride + pp * MQ_HD + td) * 4u;
+      const float4 a0 = ld_dev4(r, ob);
+      const float4 a1 = ld_dev4(r, ob + MQ_HD / 2 * 4u);
+      const float Mn = fmaxf(M, m);
+      const float fo = M == -INFINITY ? 0.f : mq_exp(M - Mn);
+      const float fn = m == -INFINITY ? 0.f : mq_exp(m - Mn);
+      Ls = Ls * fo + lv * fn;
+      o0.x = o0.x * fo + a0.x * fn; o0.y = o0.y * fo + a0.y * fn;
+      o0.z = o0.z * fo + a0.z * fn; o0.w = o0.w * fo + a0.w * fn;
+      o1.x = o1.x * fo + a1.x * fn; o1.y = o1.y * fo + a1.y * fn;
+      o1.z = o1.z * fo + a1.z * fn; o1.w = o1.w * fo + a1.w * fn;
+      M = Mn;
+    }
+  };
+  // The partials are written and read with device-scope accesses (written
+  // through / read past the XCD-local L2), so an arrival needs only its own
+  // stores complete, not a write-back or invalidation of the whole L2.
+  auto arrive = [&](uint32_t* c, uint32_t fanin) -> bool {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);  // every store of this thread has completed
+    __syncthreads();
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == fanin - 1 ? 1u : 0u;
+    __syncthreads();
+    if (!s_last) return false;
+    if (tid == 0) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // all arrivals are in
+    return true;
+  };
+  auto write_out = [&](float Ls, const float4& o0, const float4& o1) {
+    const float li = Ls > 0.f ? 1.0f / Ls : 0.f;
+    float* dst = a.out + ((size_t)kvh * MQ_G + th) * MQ_HD + td;
+    *(float4*)dst = make_float4(o0.x * li, o0.y * li, o0.z * li, o0.w * li);
+    *(float4*)(dst + MQ_HD / 2) = make_float4(o1.x * li, o1.y * li, o1.z * li, o1.w * li);
+  };
+  uint32_t* cnt = a.cnt + (size_t)kvh * MQF_CNT;
+  const uint32_t ng = (nch + MQF_FAN - 1) / MQF_FAN, g = chunk / MQF_FAN;
+  if (!arrive(cnt + g, min(MQF_FAN, nch - g * MQF_FAN))) return;
+  float M, Ls;
+  float4 o0, o1;
+  merge(r0, nparts, ((size_t)kvh * a.max_chunks + g * MQF_FAN) * MQ_G,
+        min(MQF_FAN, nch - g * MQF_FAN), M, Ls, o0, o1);
+  if (ng == 1) {
+    if constexpr (FUSED) mqf_clear_flags(a, tid);
+    write_out(Ls, o0, o1);
+    return;
+  }
+  const size_t nparts1 = (size_t)a.nkh * MQF_FAN * MQ_G;
+  const __amdgpu_buffer_rsrc_t r1 = dev_rsrc(a.ws1, (uint32_t)(nparts1 * (MQ_HD + 2) * sizeof(float)));
+  {
+    const size_t pp = ((size_t)kvh * MQF_FAN + g) * MQ_G + th;
+    if ((tid & 31) == 0) {
+      st_dev(r1, (uint32_t)pp * 4u, M);
+      st_dev(r1, (uint32_t)(nparts1 + pp) * 4u, Ls);
+    }
+    const uint32_t ob = (uint32_t)(2 * nparts1 + pp * MQ_HD + td) * 4u;
+    st_dev4(r1, ob, o0);
+    st_dev4(r1, ob + MQ_HD / 2 * 4u, o1);
+  }
+  if (!arrive(cnt + MQF_CNT - 1, ng)) return;
+  merge(r1, nparts1, (size_t)kvh * MQF_FAN * MQ_G, ng, M, Ls, o0, o1);
+  if constexpr (FUSED) mqf_clear_flags(a, tid);
+  write_out(Ls, o0, o1);
+}
+
+}  // namespace g4mqf

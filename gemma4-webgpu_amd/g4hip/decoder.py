@@ -445,6 +445,7 @@ class Decoder(_SyntheticModel):
                  n_layers: Optional[int] = None, lm_head: bool = True, embed: bool = False, wtypes=None,
                  gguf=None):
         self.max_seq = max_seq
+        self.fuse_qkv = True  # step_fused: q/k/v and the attention in one launch where the shape allows
         self._build_weights(ctx, shape, n_layers, seed, lm_head,
                             lambda il: (ctx.zeros(max_seq * self.s.kv_dim_of(il), np.uint16),
                                         ctx.zeros(max_seq * self.s.kv_dim_of(il), np.uint16)), embed=embed,
@@ -608,6 +609,11 @@ class Decoder(_SyntheticModel):
         else:
             self.ctx.matmulQuant(x, w, y, M, N, qt)
 
+    def _qkv_fused(self, groups) -> bool:
+        """q/k/v through qkvAttnDecodeFusedWarm: every one of them Q4_K (one
+        group), unless `fuse_qkv` is off."""
+        return self.fuse_qkv and len(groups) == 1 and groups[0][0] == "q4k"
+
     @staticmethod
     def _ffn_fused(L) -> bool:
         """gate/up in one launch (Q4_K pair; the digit hand-off when down is Q6_K)."""
@@ -653,20 +659,28 @@ class Decoder(_SyntheticModel):
             prod = s.is_producer(il)
             outs, rows = ([self.q, self.k, self.v], [Q, KV, KV]) if prod else ([self.q], [Q])
             x, w1, res, scale, w2 = self._layer_input(il)
-            # one launch per weight format among q/k/v; a later launch
-            # recomputes the norm from the same inputs and writes no h_out
-            for gi, (qt, ws, go, gr) in enumerate(qkv_groups(L, outs, rows)):
-                h_out = None if gi or il == 0 else self.hidden
-                if qt == "f16":
-                    c.batchPrepScale(x, 1, w1, res, scale, w2, h_out, self.normed, H, 1, s.eps)
-                    for w, y, r in zip(ws, go, gr):
-                        c.matmulF16(self.normed, w, y, r, H)
-                else:
-                    c.normAddScaleMatmulSegments(qt, x, w1, res, scale, w2, h_out, ws, go, gr, H, s.eps)
-            c.attnDecodeFusedWarm(self.q, self.k if prod else None, self.v if prod else None, L.q_norm, L.k_norm,
-                                  self.rope_freqs, L.k_cache, L.v_cache, self.attn, self.attn_params[il],
-                                  self.attn_ws, self.pos, self.warm[il] if warm else [],
-                                  self.rope_cs[s.is_global(il)], self.rope_rows)
+            groups = qkv_groups(L, outs, rows)
+            warm_il = self.warm[il] if warm else []
+            if self._qkv_fused(groups):  # q/k/v and the attention block: one launch where the shape allows
+                c.qkvAttnDecodeFusedWarm(x, w1, res, scale, w2, None if il == 0 else self.hidden, groups[0][1], outs,
+                                         H, s.eps, L.q_norm, L.k_norm, self.rope_freqs, L.k_cache, L.v_cache,
+                                         self.attn, self.attn_params[il], self.attn_ws, self.pos, warm_il,
+                                         self.rope_cs[s.is_global(il)], self.rope_rows)
+            else:
+                # one launch per weight format among q/k/v; a later launch
+                # recomputes the norm from the same inputs and writes no h_out
+                for gi, (qt, ws, go, gr) in enumerate(groups):
+                    h_out = None if gi or il == 0 else self.hidden
+                    if qt == "f16":
+                        c.batchPrepScale(x, 1, w1, res, scale, w2, h_out, self.normed, H, 1, s.eps)
+                        for w, y, r in zip(ws, go, gr):
+                            c.matmulF16(self.normed, w, y, r, H)
+                    else:
+                        c.normAddScaleMatmulSegments(qt, x, w1, res, scale, w2, h_out, ws, go, gr, H, s.eps)
+                c.attnDecodeFusedWarm(self.q, self.k if prod else None, self.v if prod else None, L.q_norm,
+                                      L.k_norm, self.rope_freqs, L.k_cache, L.v_cache, self.attn,
+                                      self.attn_params[il], self.attn_ws, self.pos, warm_il,
+                                      self.rope_cs[s.is_global(il)], self.rope_rows)
             self._mv(L.qt["wo"], self.attn, L.wo, self.o, H, Q)
             if self._ffn_fused(L):
                 c.normAddGateUpGeluDigits_q4k(self.o, L.post_attn_norm, self.hidden, L.pre_ffn_norm, L.wgate, L.wup,
@@ -742,8 +756,12 @@ class Decoder(_SyntheticModel):
         if self.lm_head is not None and self.lm_type == "f16":  # norm, matvec, softcap, two argmax stages
             n += 3
         for il, L in enumerate(self.layers):
+            groups = qkv_groups(L, [0, 0, 0][:3 if s.is_producer(il) else 1], [0, 0, 0])
+            if self._qkv_fused(groups) and self.ctx.qkv_attn_single_launch(self.attn_params[il], s.hidden):
+                n += 4
+                continue
             n += 4 + (not self.ctx.attn_fused_single_launch(self.attn_params[il]))
-            for qt, ws, _, _ in qkv_groups(L, [0, 0, 0][:3 if s.is_producer(il) else 1], [0, 0, 0]):
+            for qt, ws, _, _ in groups:
                 n += 1 + (len(ws) if qt == "f16" else 0)
             if not self._ffn_fused(L):
                 n += 3  # norm, second matvec, GELU product

@@ -439,6 +439,13 @@ class Context:
         eff = min(p.max_seq_len, p.sliding_window) if p.sliding_window else p.max_seq_len
         return p.head_dim == 256 and p.num_kv_heads <= 64 and eff <= 65536
 
+    @staticmethod
+    def qkv_attn_single_launch(p: AttnFusedParams, N: int) -> bool:
+        """Whether g4_qkvAttnDecodeFusedWarm runs as one launch: hidden 1536,
+        one KV head of dim 256, a window of at most 1024 positions."""
+        eff = min(p.max_seq_len, p.sliding_window) if p.sliding_window else p.max_seq_len
+        return N == 1536 and p.head_dim == 256 and p.num_kv_heads == 1 and p.num_q_heads == 8 and eff <= 1024
+
     def attnDecodeFused(self, q_raw: Ptr, k_raw: Ptr, v_raw: Ptr, q_norm_w: Ptr, k_norm_w: Ptr, rope_freqs: Ptr,
                         k_cache: Ptr, v_cache: Ptr, out: Ptr, p: AttnFusedParams, workspace: Buffer,
                         position_dev: Ptr) -> None:
@@ -465,6 +472,22 @@ class Context:
         check(lib().g4_attnDecodeFusedWarm(self.h, _p(q_raw), _p(k_raw), _p(v_raw), _p(q_norm_w), _p(k_norm_w),
                                            _p(rope_freqs), _p(k_cache), _p(v_cache), _p(out), p, _p(workspace),
                                            workspace.nbytes, _p(position_dev), arr, n, _p(rope_cs), rope_rows))
+
+    def qkvAttnDecodeFusedWarm(self, x: Ptr, w1: Ptr, residual: Ptr, out_scale: Ptr, w2: Ptr, h_out: Ptr,
+                               weights, outputs, N: int, eps: float, q_norm_w: Ptr, k_norm_w: Ptr, rope_freqs: Ptr,
+                               k_cache: Ptr, v_cache: Ptr, out: Ptr, p: AttnFusedParams, workspace: Buffer,
+                               position_dev: Ptr, regions, rope_cs: Ptr = None, rope_rows: int = 0) -> None:
+        """normAddScaleMatmulSegments('q4k', ...) into `outputs` (q, or q/k/v), then attnDecodeFusedWarm
+        over them; one launch where the shape allows (g4_qkvAttnDecodeFusedWarm)."""
+        n = len(weights)
+        W = (ctypes.c_void_p * n)(*[_p(w).value for w in weights])
+        Y = (ctypes.c_void_p * n)(*[_p(y).value for y in outputs])
+        nr = len(regions)
+        arr = (WarmRegion * max(nr, 1))(*regions)
+        check(lib().g4_qkvAttnDecodeFusedWarm(self.h, _p(x), _p(w1), _p(residual), _p(out_scale), _p(w2), _p(h_out),
+                                              W, Y, n, N, eps, _p(q_norm_w), _p(k_norm_w), _p(rope_freqs),
+                                              _p(k_cache), _p(v_cache), _p(out), p, _p(workspace), workspace.nbytes,
+                                              _p(position_dev), arr, nr, _p(rope_cs), rope_rows))
 
     def ropeTable(self, theta: float, apply_divisor: int, rope_freqs: Ptr, head_dim: int, rows: int,
                   table: Ptr) -> None:

@@ -247,6 +247,28 @@ int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, 
                            size_t workspace_bytes, const uint32_t* position_dev,
                            const g4_warm_region* regions, int nregions, const float* rope_cs,
                            uint32_t rope_rows);
+/* The q/k/v projections and the attention block of one layer
+ * (src/engine.ts:1550-1584: the Q4_K q/k/v matvecs over the attention
+ * rmsNorm of the residual stream, then the block g4_attnDecodeFusedWarm
+ * runs): g4_normAddScaleMatmulSegments(wtype Q4_K, x .. eps, weights,
+ * outputs, rows = q_dim / kv_dim / kv_dim, nseg, no softcap) followed by
+ * g4_attnDecodeFusedWarm(outputs[0], outputs[1], outputs[2] (null when
+ * nseg = 1, a layer reading its producer's cache), ...). Results are those
+ * of the two calls, bit for bit; outputs[] receive q/k/v as well.
+ * When N = 1536, one KV head and a window of at most 1024 positions, both
+ * run as one launch: the attention workgroups load their K/V rows while the
+ * matvec workgroups run, and read q/k/v once these flag them stored (an
+ * MI355X fusion with no reference counterpart); other shapes make the two
+ * launches. The workspace is g4_attnDecodeFused's, zeroed before its first
+ * use; calls that share a workspace must not overlap. */
+int g4_qkvAttnDecodeFusedWarm(g4_ctx* ctx, const float* x, const uint16_t* w1, const float* residual,
+                              const uint16_t* out_scale, const uint16_t* w2, float* h_out,
+                              const void* const* weights, float* const* outputs, int nseg, uint32_t N, float eps,
+                              const uint16_t* q_norm_w, const uint16_t* k_norm_w, const uint16_t* rope_freqs,
+                              uint16_t* k_cache, uint16_t* v_cache, float* output, g4_attn_fused_params p,
+                              void* workspace, size_t workspace_bytes, const uint32_t* position_dev,
+                              const g4_warm_region* regions, int nregions, const float* rope_cs,
+                              uint32_t rope_rows);
 /* RoPE table of shaders/fused_per_head_norm_rope.wgsl:50-55: for position
  * t < rows and pair i < head_dim/2, table[2 (t head_dim/2 + i)] = cos and
  * [.. + 1] = sin of t * freq_i, freq_i = 1/theta^(2i/head_dim) (divided by

@@ -27,7 +27,7 @@ import pytest
 
 import oracle as O
 from decode_oracle import HostModel
-from g4hip.decoder import E2BShape, decoder_from_gguf, q4km_types
+from g4hip.decoder import E2BShape, decoder_from_gguf, q4km_types, qkv_groups
 from g4hip.gguf import GGUFFile
 from gguf_writer import BOOL, F32, GGUFWriter, I32, STR, U32
 from gpu_util import assert_close
@@ -338,9 +338,15 @@ def test_file_model_fused_step_with_token_feedback(ctx, model_path):
     vcs = [L.v_cache.download(np.uint16) for L in d.layers]
     # 5 per layer, + a merge launch on the two head-dim-512 layers, + the
     # second q/k/v launch of layer 1 (Q6_K v), + embedding, head, argmax,
-    # + per-layer embeddings: stage 1 (2), 2 per layer, the last tail (1)
+    # + per-layer embeddings: stage 1 (2), 2 per layer, the last tail (1),
+    # - one on each layer whose Q4_K q/k/v share the attention's launch
+    # (the two head-dim-256 layers with Q4_K q/k/v)
     assert d.layers[1].qt["wv"] == "q6k" and d.layers[1].qt["wq"] == "q4k"
-    assert d.launches_per_step_fused() == 5 * N_LAYERS + 2 + 1 + 3 + 3 + 2 * N_LAYERS
+    shared = [il for il in range(N_LAYERS)
+              if d._qkv_fused(qkv_groups(d.layers[il], [0, 0, 0], [0, 0, 0]))
+              and ctx.qkv_attn_single_launch(d.attn_params[il], d.s.hidden)]
+    assert len(shared) == 2
+    assert d.launches_per_step_fused() == 5 * N_LAYERS + 2 + 1 + 3 + 3 + 2 * N_LAYERS - len(shared)
     g = d.capture_fused()
     try:
         tok = T0
