@@ -1049,6 +1049,49 @@ napi_value NormAddScaleMatmulSegments(napi_env env, napi_callback_info info) {
                                                  0.f));
 }
 
+// qkvAttnDecodeFused(ctx, {x, w1, residual, scale, w2, hOut}, weights[], outputs[], N, eps,
+//   {qNorm, kNorm, ropeFreqs, kCache, vCache, out, workspace, position, ropeCs}, params, workspaceBytes,
+//   ropeRows[, regions]): the Q4_K q (or q/k/v) matvecs and the attention
+// block over them, in one launch where the shape allows
+napi_value QkvAttnDecodeFused(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* x = (const float*)fptr(a, 1, "x");
+  const uint16_t* w1 = (const uint16_t*)fptr(a, 1, "w1");
+  const float* res = (const float*)fptr(a, 1, "residual");
+  const uint16_t* sc = (const uint16_t*)fptr(a, 1, "scale");
+  const uint16_t* w2 = (const uint16_t*)fptr(a, 1, "w2");
+  float* h = (float*)fptr(a, 1, "hOut");
+  void* W[4] = {};
+  void* Y[4] = {};
+  const int n = array_at(a, 2, W, nullptr, 3, 0);
+  const int ny = array_at(a, 3, Y, nullptr, 3, 0);
+  const uint32_t N = a.u32(4);
+  const float eps = a.f32(5);
+  const uint16_t* qn = (const uint16_t*)fptr(a, 6, "qNorm");
+  const uint16_t* kn = (const uint16_t*)fptr(a, 6, "kNorm");
+  const uint16_t* rf = (const uint16_t*)fptr(a, 6, "ropeFreqs");
+  uint16_t* kc = (uint16_t*)fptr(a, 6, "kCache");
+  uint16_t* vc = (uint16_t*)fptr(a, 6, "vCache");
+  float* out = (float*)fptr(a, 6, "out");
+  void* ws = fptr(a, 6, "workspace");
+  const uint32_t* pos = (const uint32_t*)fptr(a, 6, "position");
+  const float* cs = (const float*)fptr(a, 6, "ropeCs");
+  const g4_attn_fused_params p = fused_params(a, 7);
+  const uint64_t wsb = a.u64(8);
+  const uint32_t rows = a.u32(9);
+  g4_warm_region reg[4] = {};
+  const int nreg = regions_at(a, 10, reg);
+  CHECKED(a);
+  if (n != ny) {
+    a.fail("weights and outputs differ in length");
+    return nullptr;
+  }
+  return done(env, g4_qkvAttnDecodeFusedWarm(c, x, w1, res, sc, w2, h, W, (float* const*)Y, n, N, eps, qn, kn, rf,
+                                             kc, vc, out, p, ws, (size_t)wsb, pos, nreg ? reg : nullptr, nreg, cs,
+                                             rows));
+}
+
 // normAddGateUpGeluDigits(ctx, {o, wPost, residual, wPre, wGate, wUp, hOut, out, digits}, {M, N}, eps)
 napi_value NormAddGateUpGeluDigits(napi_env env, napi_callback_info info) {
   Args a(env, info);
@@ -1219,6 +1262,7 @@ const Entry kEntries[] = {
     {"matmulWarmRegion", MatmulWarmRegion},
     {"attnDecodeFused", AttnDecodeFused},
     {"normAddScaleMatmulSegments", NormAddScaleMatmulSegments},
+    {"qkvAttnDecodeFused", QkvAttnDecodeFused},
     {"normAddGateUpGeluDigits", NormAddGateUpGeluDigits},
     {"matmulQuantDigits", MatmulQuantDigits},
     {"normAddMatmulArgmax", NormAddMatmulArgmax},

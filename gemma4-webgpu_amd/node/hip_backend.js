@@ -632,6 +632,23 @@ class HipBackend {
     else this.g.matmulQuant(this.ctx, x, w, y, { M: M, N: N }, fmt);
   }
 
+  // one q/k/v launch per weight format, in order of first appearance; a
+  // later one recomputes the norm and writes no residual
+  _qkvGroups(groups, il, pro, H, eps) {
+    const g = this.g;
+    const c = this.ctx;
+    const W = this.workBuffers;
+    groups.forEach((grp, gi) => {
+      const hOut = gi > 0 || il === 0 ? null : W.hidden;
+      if (grp.fmt === 'f16') {
+        g.batchPrepScale(c, Object.assign({ hOut: hOut, out: W.normed }, pro), { nparts: 1, N: H, batch: 1 }, eps);
+        grp.w.forEach((w, k) => g.matmulF16(c, W.normed, w, grp.y[k], { M: grp.r[k], N: H, batch: 1 }));
+      } else {
+        g.normAddScaleMatmulSegments(c, grp.fmt, Object.assign({ hOut: hOut }, pro), grp.w, grp.y, grp.r, H, eps);
+      }
+    });
+  }
+
   encodeFusedStep() {
     const C = this.config;
     const g = this.g;
@@ -668,8 +685,7 @@ class HipBackend {
           w2: L.attn_norm } : { x: W.ffnDown, w1: P.post_ffw_norm, residual: W.residual, scale: null,
           w2: L.attn_norm };
       }
-      // one q/k/v launch per weight format, in order of first appearance; a
-      // later one recomputes the norm and writes no residual
+      // q/k/v grouped by weight format, in order of first appearance
       const mats = prod ? [['attn_q', W.q, Q], ['attn_k', W.k, KV], ['attn_v', W.v, KV]] : [['attn_q', W.q, Q]];
       const groups = [];
       for (const [name, y, r] of mats) {
@@ -682,19 +698,18 @@ class HipBackend {
         grp.y.push(y);
         grp.r.push(r);
       }
-      groups.forEach((grp, gi) => {
-        const hOut = gi > 0 || il === 0 ? null : W.hidden;
-        if (grp.fmt === 'f16') {
-          g.batchPrepScale(c, Object.assign({ hOut: hOut, out: W.normed }, pro), { nparts: 1, N: H, batch: 1 }, eps);
-          grp.w.forEach((w, k) => g.matmulF16(c, W.normed, w, grp.y[k], { M: grp.r[k], N: H, batch: 1 }));
-        } else {
-          g.normAddScaleMatmulSegments(c, grp.fmt, Object.assign({ hOut: hOut }, pro), grp.w, grp.y, grp.r, H, eps);
-        }
-      });
-      g.attnDecodeFused(c, { q: W.q, k: prod ? W.k : null, v: prod ? W.v : null, qNorm: L.attn_q_norm,
-        kNorm: prod ? L.attn_k_norm : null, ropeFreqs: G.rope_freqs, kCache: kv.k, vCache: kv.v, out: W.attnOut,
-        workspace: Fz.workspace, position: W.position, ropeCs: Fz.rope[!isSwaLayer(C, il)] },
-      Fz.params[il], Fz.workspaceBytes, this.maxSeqLen, Fz.warm[il]);
+      const attnBufs = { qNorm: L.attn_q_norm, kNorm: prod ? L.attn_k_norm : null, ropeFreqs: G.rope_freqs,
+        kCache: kv.k, vCache: kv.v, out: W.attnOut, workspace: Fz.workspace, position: W.position,
+        ropeCs: Fz.rope[!isSwaLayer(C, il)] };
+      if (groups.length === 1 && groups[0].fmt === 'q4k') {
+        // q/k/v and the attention block: one launch where the shape allows
+        g.qkvAttnDecodeFused(c, Object.assign({ hOut: il === 0 ? null : W.hidden }, pro), groups[0].w, groups[0].y,
+          H, eps, attnBufs, Fz.params[il], Fz.workspaceBytes, this.maxSeqLen, Fz.warm[il]);
+      } else {
+        this._qkvGroups(groups, il, pro, H, eps);
+        g.attnDecodeFused(c, Object.assign({ q: W.q, k: prod ? W.k : null, v: prod ? W.v : null }, attnBufs),
+          Fz.params[il], Fz.workspaceBytes, this.maxSeqLen, Fz.warm[il]);
+      }
       this._mv(F.attn_output, W.attnOut, L.attn_output, W.attnProj, H, Q);
       const pair = F.ffn_gate === 'q4k' && F.ffn_up === 'q4k';
       if (pair) {

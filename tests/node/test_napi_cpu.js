@@ -23,7 +23,7 @@ const KEYS = ['version', 'lastError', 'init', 'destroy', 'deviceInfo', 'alloc', 
   'embeddingLookup', 'argmax', 'topk256', 'advancePosition', 'pleStage1Fuse', 'pleGeluMul', 'pleSkipScaleAdd',
   'ggufOpen', 'ggufClose', 'ggufInfo', 'ggufMetadata', 'ggufTensors', 'ggufUpload', 'ggufUploadF16', 'dequantF16',
   'digitsBytes', 'attnFusedWorkspaceSize', 'ropeTable', 'matmulWarmRegion', 'attnDecodeFused',
-  'normAddScaleMatmulSegments',
+  'normAddScaleMatmulSegments', 'qkvAttnDecodeFused',
   'normAddGateUpGeluDigits', 'matmulQuantDigits', 'normAddMatmulArgmax', 'pleGate', 'matmulF16', 'batchPrepScale',
   'argmaxAdvance'];
 
@@ -296,38 +296,48 @@ check('the fused step: launch order, prologue chaining, format groups, PLE and t
   assert.strictEqual(keys.filter((k) => k === 'ropeTable').length, 2);
   const step = keys.filter((k) => ['alloc', 'memset', 'sync', 'attnFusedWorkspaceSize', 'ropeTable',
     'digitsBytes', 'matmulWarmRegion'].indexOf(k) < 0);
-  const layer = (qkv, ffn, down) => qkv.concat(['attnDecodeFused', 'matmulQuant'], ffn, [down], ['pleGate', 'matmulF16']);
+  // layers whose q/k/v are all Q4_K issue them with the attention
+  // (qkvAttnDecodeFused); layer 1 (a Q6_K v) makes two q/k/v launches and
+  // the attention's own
+  const tail = (ffn, down) => ['matmulQuant'].concat(ffn, [down], ['pleGate', 'matmulF16']);
   const want = ['embeddingLookup', 'matmulF16', 'pleStage1Fuse']
-    .concat(layer(['normAddScaleMatmulSegments'], ['normAddGateUpGeluDigits'], 'matmulQuantDigits'))
-    .concat(layer(['normAddScaleMatmulSegments', 'normAddScaleMatmulSegments'],
-      ['batchPrepScale', 'matmulF16', 'matmulQuant', 'geluMul'], 'matmulQuant'))
-    .concat(layer(['normAddScaleMatmulSegments'], ['normAddGateUpGeluDigits'], 'matmulQuantDigits'))
-    .concat(layer(['normAddScaleMatmulSegments'], ['normAddGateUpGeluDigits'], 'matmulQuant'))
+    .concat(['qkvAttnDecodeFused'], tail(['normAddGateUpGeluDigits'], 'matmulQuantDigits'))
+    .concat(['normAddScaleMatmulSegments', 'normAddScaleMatmulSegments', 'attnDecodeFused'],
+      tail(['batchPrepScale', 'matmulF16', 'matmulQuant', 'geluMul'], 'matmulQuant'))
+    .concat(['qkvAttnDecodeFused'], tail(['normAddGateUpGeluDigits'], 'matmulQuantDigits'))
+    .concat(['qkvAttnDecodeFused'], tail(['normAddGateUpGeluDigits'], 'matmulQuant'))
     .concat(['batchPrepScale', 'normAddMatmulArgmax']);
   assert.deepStrictEqual(step, want);
+  // qkvAttnDecodeFused(ctx, pro, weights, outputs, N, eps, buffers, params, wsBytes, ropeRows, regions)
+  const qa = m.calls.filter((x) => x[0] === 'qkvAttnDecodeFused');
+  // layer 0 normalises the embedding and writes no residual
+  assert.strictEqual(qa[0][2].x, be.workBuffers.hidden);
+  assert.strictEqual(qa[0][2].hOut, null);
+  assert.deepStrictEqual(qa[0][3], ['attn_q0', 'attn_k0', 'attn_v0']);
+  assert.deepStrictEqual(qa[0][4], [be.workBuffers.q, be.workBuffers.k, be.workBuffers.v]);
   const nas = m.calls.filter((x) => x[0] === 'normAddScaleMatmulSegments');
-  // layer 0 normalises the embedding and writes no residual; layer 1's first
-  // launch adds the previous PLE tail and writes the residual, its second
-  // (the Q6_K v) recomputes the norm and writes none
-  assert.strictEqual(nas[0][3].x, be.workBuffers.hidden);
-  assert.strictEqual(nas[0][3].hOut, null);
-  assert.strictEqual(nas[1][3].x, be.workBuffers.pleProjOut);
-  assert.strictEqual(nas[1][3].scale, 'layer_output_scale0');
-  assert.strictEqual(nas[1][3].hOut, be.workBuffers.hidden);
-  assert.deepStrictEqual([nas[1][2], nas[1][4]], ['q4k', ['attn_q1', 'attn_k1']]);
-  assert.deepStrictEqual([nas[2][2], nas[2][4], nas[2][3].hOut], ['q6k', ['attn_v1'], null]);
+  // layer 1's first launch adds the previous PLE tail and writes the
+  // residual, its second (the Q6_K v) recomputes the norm and writes none
+  assert.strictEqual(nas[0][3].x, be.workBuffers.pleProjOut);
+  assert.strictEqual(nas[0][3].scale, 'layer_output_scale0');
+  assert.strictEqual(nas[0][3].hOut, be.workBuffers.hidden);
+  assert.deepStrictEqual([nas[0][2], nas[0][4]], ['q4k', ['attn_q1', 'attn_k1']]);
+  assert.deepStrictEqual([nas[1][2], nas[1][4], nas[1][3].hOut], ['q6k', ['attn_v1'], null]);
   // consumer layers (2, 3) project q only and read their producer's cache
-  assert.deepStrictEqual(nas[3][4], ['attn_q2']);
+  assert.deepStrictEqual([qa[1][3], qa[1][4]], [['attn_q2'], [be.workBuffers.q]]);
+  assert.strictEqual(qa[1][2].hOut, be.workBuffers.hidden);
+  assert.strictEqual(qa[1][7].kNorm, null);
+  assert.strictEqual(qa[1][7].kCache, be.kvCaches[0].k);
+  assert.strictEqual(qa[2][7].kCache, be.kvCaches[1].k);
   const att = m.calls.filter((x) => x[0] === 'attnDecodeFused');
-  assert.strictEqual(att[2][2].k, null);
-  assert.strictEqual(att[2][2].kCache, be.kvCaches[0].k);
-  assert.strictEqual(att[3][2].kCache, be.kvCaches[1].k);
-  assert.strictEqual(att[1][3].sliding_window, 0);
-  assert.strictEqual(att[1][3].head_dim, 512);
-  assert.strictEqual(att[0][3].sliding_window, 512);
+  assert.strictEqual(att.length, 1);
+  assert.strictEqual(att[0][2].k, be.workBuffers.k);
+  assert.strictEqual(att[0][3].sliding_window, 0);
+  assert.strictEqual(att[0][3].head_dim, 512);
+  assert.strictEqual(qa[0][8].sliding_window, 512);
   // L2 warming: layer 0 the gate/up pair and the down, layer 1 (f16 gate) the down only
-  assert.deepStrictEqual(att[0][6].map((r) => r.base), ['ffn_gate0', 'ffn_up0', 'ffn_down0']);
-  assert.deepStrictEqual(att[1][6].map((r) => r.base), ['ffn_down1']);
+  assert.deepStrictEqual(qa[0][11].map((r) => r.base), ['ffn_gate0', 'ffn_up0', 'ffn_down0']);
+  assert.deepStrictEqual(att[0][6].map((r) => r.base), ['ffn_down1']);
   const head = m.calls.filter((x) => x[0] === 'normAddMatmulArgmax')[0];
   assert.strictEqual(head[2], 'q6k');
   assert.strictEqual(head[3].positions, be.workBuffers.position);
