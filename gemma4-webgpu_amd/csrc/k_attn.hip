@@ -1205,7 +1205,7 @@ int launch_attn(g4_ctx* ctx, const AttnArgs& a, uint32_t G, uint32_t hd, int cp,
 // device-scope round trips per tree level cost more than a launch boundary,
 // and the merge launch spreads each head's partials over many workgroups).
 // Past kMaxSplits chunks a workgroup takes several steps. The arrival
-// counters and the q/k/v flags sit in the first kMqfCnt bytes of the
+// counters and the staged q/k/v sit in the first kMqfCnt bytes of the
 // workspace, at the same place whatever the plan, so that layers of
 // different windows can share one workspace; the chunk partials follow,
 // then the group partials.
@@ -1413,8 +1413,8 @@ int mqf_prepare(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float
     m.wwgb[i] = (uint32_t)regions[i].wg_bytes;
     m.wnwg[i] = regions[i].nwgs;
   }
-  m.flags = (uint32_t*)((uint8_t*)workspace + kMqfCntOnly);
-  m.nflags = 0;
+  m.stage = (uint64_t*)((uint8_t*)workspace + kMqfCntOnly);
+  m.nstage = 0;
   L.partials = mp.partials;
   return G4_OK;
 }

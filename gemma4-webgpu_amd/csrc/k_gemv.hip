@@ -516,6 +516,7 @@ struct GemvSeg {
   float* Y;
   uint32_t M;
   uint32_t wg_begin;  // first workgroup of this segment
+  uint64_t* stage;    // DEV rows: also staged as (1 << 32 | f32 bits) pairs here, [M]
 };
 struct GemvSegs {
   GemvSeg s[4];
@@ -1238,8 +1239,9 @@ __device__ __forceinline__ void mv_d8_group(float v, bool real, uint32_t row, ui
 
 // Adds each row's U unit partials (RG lanes per row, then a butterfly) and
 // stores the tile's rows: y, softcap(y), or gelu(gate) * up for a pair.
-// DEV: the rows are stored at device scope (written through to the point of
-// coherence), for readers in other workgroups of the same launch.
+// DEV: each row is also staged as a (tag 1, value) pair in one device-scope
+// 8-byte store (written through to the point of coherence), for readers in
+// other workgroups of the same launch.
 template <class T, int NTH, int NMAT, bool DEV = false>
 __device__ __forceinline__ void mv_reduce_store(const float* red, const GemvSeg& sg, uint32_t t, int tid, float cap,
                                                 bool track, g4d::Cand& best, uint8_t* d8 = nullptr,
@@ -1267,8 +1269,10 @@ __device__ __forceinline__ void mv_reduce_store(const float* red, const GemvSeg&
         if (d8) mv_d8_group(v, real, row, sg.M, d8);
     } else if (real) {
       const float v = cap > 0.f ? softcap(y[0], cap) : y[0];
-      if constexpr (DEV) __hip_atomic_store(sg.Y + row, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      else sg.Y[row] = v;
+      sg.Y[row] = v;
+      if constexpr (DEV)
+        __hip_atomic_store(sg.stage + row, g4mqf::kStaged | __float_as_uint(v), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
       const g4d::Cand d{v, row};
       if (track && g4d::better(d, best)) best = d;
       // top-k classes: a tile's rows are distinct classes (TR <= 256) and
@@ -1863,12 +1867,12 @@ int mv_launch(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
 // one KV head, a window of at most MQF_FAN chunks). Workgroups [0, nmv) are
 // the one-tile matvec (Q4_K rows of 1536, MNWV waves: the width the matvec's
 // own launch would take, so the rows are the same bit for bit) with its norm
-// prologue; they store their rows at device scope and then each sets its
-// flag.
+// prologue; each row is also staged, with its tag, in one device-scope
+// store.
 // Workgroups nmv.. are the attention block's chunk and L2-warming
 // workgroups (the first 256 threads; the other two waves end at once).
 // A chunk workgroup reads the position and requests its K/V rows at
-// once, and waits for the flags only before it reads q/k/v, so the window's
+// once, and polls the staged q/k/v only before its prologue, so the window's
 // load overlaps the matvec instead of following a launch boundary. The
 // matvec workgroups come first in the grid and wait on nothing: in-order
 // dispatch lets them finish whatever the residency, and the wait is bounded.
@@ -1881,10 +1885,6 @@ __global__ __launch_bounds__(64 * kQkvNwv) void qkv_attn_kernel(GemvSegs segs, P
   if (blockIdx.x < nmv) {  // (uniform)
     if (threadIdx.x >= 64u * MNWV) return;  // (uniform per wave)
     mv_body<0, 6, MNWV, PRO, 1, false, true>(segs, nullptr, pa, 0.f, smem);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_s_waitcnt(0);  // every row store of this thread is acknowledged
-    __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_store(a.flags + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   if (threadIdx.x >= (unsigned)g4mqf::MQ_NT) return;  // (uniform per wave)
@@ -2395,7 +2395,7 @@ int g4_qkvAttnDecodeFusedWarm(g4_ctx* ctx, const float* x, const uint16_t* w1, c
   }
   bool applies = false;
   g4mqf::MqfLaunch L{};
-  if (N == 1536 && (mnwv == 6 || mnwv == 3) && p.num_kv_heads == 1 && nmv <= g4mqf::kMaxFlags) {
+  if (N == 1536 && (mnwv == 6 || mnwv == 3) && p.num_kv_heads == 1 && rows[0] + 2 * rows[1] <= g4mqf::kMaxStage) {
     rc = g4mqf::mqf_prepare(ctx, q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs, k_cache, v_cache, output, p,
                             workspace, workspace_bytes, position_dev, regions, nregions, rope_cs, nmv, applies, L);
     if (rc) return rc;
@@ -2411,7 +2411,9 @@ int g4_qkvAttnDecodeFusedWarm(g4_ctx* ctx, const float* x, const uint16_t* w1, c
   }
   sg.n = nseg;
   sg.rep = 1;
-  L.m.nflags = nmv;
+  // staged q/k/v: q at 0, k at nqh * hd, v at (nqh + nkh) * hd
+  L.m.nstage = rows[0] + 2 * rows[1];
+  for (int i = 0; i < nseg; ++i) sg.s[i].stage = L.m.stage + (i == 0 ? 0 : rows[0] + (size_t)(i - 1) * rows[1]);
   const ProArgs pa{x, w1, residual, w2, h_out, eps, out_scale};
   const dim3 grid(nmv + L.m.max_chunks + L.m.nwarm), block(64 * kQkvNwv);
   auto launch = [&](auto kern, size_t lds) {

@@ -89,10 +89,11 @@ struct MqfArgs {
   uint32_t nwarm_regions, nwarm;  // regions; warming workgroups (a multiple of 8)
   const float2* rope_cs;          // [cap][128] (cos, sin) of every position (g4_ropeTable), or null
   // the launch that also runs the q/k/v matvec (mqf_body<false, true>):
-  // one flag per matvec workgroup, set when its rows are stored, cleared by
-  // the merger
-  uint32_t* flags;
-  uint32_t nflags;
+  // q, k and v staged as (tag << 32 | f32 bits) pairs, tag 1 once the matvec
+  // stored the value, reset to 0 by the merger ([nqh][256] q, [nkh][256] k,
+  // then v)
+  uint64_t* stage;
+  uint32_t nstage;
 };
 
 constexpr int MQF_QS = 264;  // LDS stride of a q column (halves)
@@ -125,22 +126,42 @@ __device__ __forceinline__ float4 ld_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off
   return make_float4(v.x, v.y, v.z, v.w);
 }
 
-// The q/k/v flags of a launch that also runs the matvec. The wait is bounded
-// (kFlagSpin polls, each a device-scope round trip, about 0.1 s in all) so
-// that every workgroup ends even if a flag never comes; the matvec
-// workgroups precede the attention ones in the grid and wait on nothing, so
-// in-order dispatch always lets them finish.
-constexpr uint32_t kFlagSpin = 1u << 16;
-constexpr uint32_t kMaxFlags = 256;
-// The workgroup's MQ_NT threads (4 waves; a wider launch's other waves have
-// ended) poll one flag each; the vote goes through LDS, one word per wave.
-__device__ __forceinline__ void mqf_wait_flags(const MqfArgs& a, int tid) {
+// The staged q/k/v of a launch that also runs the matvec. A value and its
+// tag travel in one 8-byte device-scope store and load, so a pair read with
+// tag 1 holds the stored value: the attention polls the values it needs
+// until every one carries the tag, with no separate flag to wait for. The
+// wait is bounded (kStageSpin polls, each a device-scope round trip, about
+// 0.1 s in all) so that every workgroup ends even if a value never comes;
+// the matvec workgroups precede the attention ones in the grid and wait on
+// nothing, so in-order dispatch always lets them finish.
+constexpr uint32_t kStageSpin = 1u << 16;
+constexpr uint32_t kMaxStage = 4096;  // staged values: nqh * 256 + 2 * nkh * 256
+constexpr uint64_t kStaged = 1ull << 32;
+__device__ __forceinline__ uint64_t stage_ld(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float stage_val(uint64_t e) { return __uint_as_float((uint32_t)e); }
+// The MQ_NT threads (4 waves; a wider launch's other waves have ended) each
+// poll their 8 q values and (own_row) one k and one v value; the vote goes
+// through LDS, one word per wave.
+__device__ __forceinline__ void mqf_wait_stage(const MqfArgs& a, int tid, size_t qoff, uint32_t kvh, bool own_row,
+                                               float4& q0, float4& q1, float& kx, float& vx) {
   __shared__ uint32_t s_ok[MQ_NT / 64];
-  // flags past nflags read as 0 through the resource: they count as set
-  const __amdgpu_buffer_rsrc_t fr = dev_rsrc((float*)a.flags, a.nflags * 4u);
+  const uint64_t* sq = a.stage + qoff;
+  const uint64_t* sk = a.stage + (size_t)a.nqh * MQ_HD + (size_t)kvh * MQ_HD + tid;
+  const uint64_t* sv = sk + (size_t)a.nkh * MQ_HD;
   for (uint32_t it = 0;; ++it) {
-    const uint32_t f = __builtin_amdgcn_raw_buffer_load_b32(fr, (uint32_t)tid * 4u, 0, kScDevice);
-    const bool set = (uint32_t)tid >= a.nflags || f != 0u;
+    uint64_t e[10];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      e[i] = stage_ld(sq + i);
+      e[4 + i] = stage_ld(sq + MQ_HD / 2 + i);
+    }
+    e[8] = own_row ? stage_ld(sk) : kStaged;
+    e[9] = own_row ? stage_ld(sv) : kStaged;
+    bool set = true;
+#pragma unroll
+    for (int i = 0; i < 10; ++i) set = set && (e[i] >> 32) == 1u;
     const uint64_t votes = __ballot(set);
     if ((tid & 63) == 0) s_ok[tid >> 6] = votes == ~0ull ? 1u : 0u;
     __syncthreads();
@@ -148,21 +169,26 @@ __device__ __forceinline__ void mqf_wait_flags(const MqfArgs& a, int tid) {
 #pragma unroll
     for (int w = 0; w < MQ_NT / 64; ++w) all = all && s_ok[w] != 0u;
     __syncthreads();  // every wave has read the votes before the next round writes them
-    if (all || it >= kFlagSpin) return;
+    if (all || it >= kStageSpin) {
+      q0 = make_float4(stage_val(e[0]), stage_val(e[1]), stage_val(e[2]), stage_val(e[3]));
+      q1 = make_float4(stage_val(e[4]), stage_val(e[5]), stage_val(e[6]), stage_val(e[7]));
+      kx = own_row ? stage_val(e[8]) : 0.f;
+      vx = own_row ? stage_val(e[9]) : 0.f;
+      return;
+    }
     __builtin_amdgcn_s_sleep(1);
   }
 }
-__device__ __forceinline__ void mqf_clear_flags(const MqfArgs& a, int tid) {
-  const __amdgpu_buffer_rsrc_t fr = dev_rsrc((float*)a.flags, a.nflags * 4u);
-  for (uint32_t i = (uint32_t)tid; i < a.nflags; i += MQ_NT)
-    __builtin_amdgcn_raw_buffer_store_b32(0u, fr, i * 4u, 0, kScDevice);
+__device__ __forceinline__ void mqf_clear_stage(const MqfArgs& a, int tid) {
+  for (uint32_t i = (uint32_t)tid; i < a.nstage; i += MQ_NT)
+    __hip_atomic_store(a.stage + i, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Workspace head: the arrival counters ([kv head][MQF_CNT]), then the q/k/v
-// flags; zero between calls.
+// Workspace head: the arrival counters ([kv head][MQF_CNT]), then the staged
+// q/k/v; zero between calls.
 constexpr uint32_t kMqfMaxKvHeads = 64;
 constexpr size_t kMqfCntOnly = (size_t)kMqfMaxKvHeads * MQF_CNT * sizeof(uint32_t);
-constexpr size_t kMqfCnt = kMqfCntOnly + kMaxFlags * sizeof(uint32_t);
+constexpr size_t kMqfCnt = kMqfCntOnly + kMaxStage * sizeof(uint64_t);
 
 struct MqfLaunch {
   MqfArgs m;
@@ -178,8 +204,8 @@ int mqf_check(g4_ctx* ctx, const char* fn, const float* q_raw, const float* k_ra
 // mqf_prepare: after those checks, sets
 // `applies` when the one-launch matrix-core form serves p and then fills L
 // (workspace plan, warming workgroups on the CUs left idle by the attention
-// and `busy_extra` other workgroups of the same launch). m.flags points at
-// the workspace's flags, m.nflags is 0.
+// and `busy_extra` other workgroups of the same launch). m.stage points at
+// the workspace's staged q/k/v, m.nstage is 0.
 int mqf_prepare(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float* v_raw, const uint16_t* q_norm_w,
                 const uint16_t* k_norm_w, const uint16_t* rope_freqs, uint16_t* k_cache, uint16_t* v_cache,
                 float* output, const g4_attn_fused_params& p, void* workspace, size_t workspace_bytes,
@@ -308,8 +334,8 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
 
   // ---- every load of the prologue, then the first step's rows ----
   // (FUSED: q, k and v come from the matvec workgroups of the same launch;
-  // the K/V rows and the weights are requested first, then q/k/v are read at
-  // device scope once every matvec workgroup has flagged its rows stored)
+  // the K/V rows and the weights are requested first, then the staged q/k/v
+  // are polled until every value this thread needs is there)
   const size_t qoff = (size_t)(kvh * MQ_G + th) * MQ_HD + td;
   float4 q0, q1;
   float kx, vx;
@@ -330,18 +356,7 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   __builtin_amdgcn_sched_barrier(0);
   load_step(0);
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (FUSED) {
-    mqf_wait_flags(a, tid);
-    const __amdgpu_buffer_rsrc_t rq = dev_rsrc((float*)a.q_raw, a.nqh * MQ_HD * 4u);
-    q0 = ld_dev4(rq, (uint32_t)qoff * 4u);
-    q1 = ld_dev4(rq, (uint32_t)(qoff + MQ_HD / 2) * 4u);
-    // (k_raw / v_raw are null in a layer without its own row: reads of an
-    // empty resource return 0)
-    const __amdgpu_buffer_rsrc_t rk = dev_rsrc((float*)a.k_raw, own_row ? a.nkh * MQ_HD * 4u : 0u);
-    const __amdgpu_buffer_rsrc_t rv = dev_rsrc((float*)a.v_raw, own_row ? a.nkh * MQ_HD * 4u : 0u);
-    kx = ld_dev(rk, (kvh * MQ_HD + (uint32_t)tid) * 4u);
-    vx = ld_dev(rv, (kvh * MQ_HD + (uint32_t)tid) * 4u);
-  }
+  if constexpr (FUSED) mqf_wait_stage(a, tid, qoff, kvh, own_row, q0, q1, kx, vx);
 
   // RoPE of this position (rope_cos_sin), from the table when there is one:
   // the frequency's f64 pow and a large-argument sincos are some 380 VALU
@@ -585,7 +600,7 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   merge(r0, nparts, ((size_t)kvh * a.max_chunks + g * MQF_FAN) * MQ_G,
         min(MQF_FAN, nch - g * MQF_FAN), M, Ls, o0, o1);
   if (ng == 1) {
-    if constexpr (FUSED) mqf_clear_flags(a, tid);
+    if constexpr (FUSED) mqf_clear_stage(a, tid);
     write_out(Ls, o0, o1);
     return;
   }
@@ -603,7 +618,7 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   }
   if (!arrive(cnt + MQF_CNT - 1, ng)) return;
   merge(r1, nparts1, (size_t)kvh * MQF_FAN * MQ_G, ng, M, Ls, o0, o1);
-  if constexpr (FUSED) mqf_clear_flags(a, tid);
+  if constexpr (FUSED) mqf_clear_stage(a, tid);
   write_out(Ls, o0, o1);
 }
 
