@@ -257,9 +257,9 @@ int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, 
  * of the two calls, bit for bit; outputs[] receive q/k/v as well.
  * When N = 1536, one KV head and a window of at most 1024 positions, both
  * run as one launch: the attention workgroups load their K/V rows while the
- * matvec workgroups run, and read q/k/v once these flag them stored (an
- * MI355X fusion with no reference counterpart); other shapes make the two
- * launches. The workspace is g4_attnDecodeFused's, zeroed before its first
+ * matvec workgroups run, and poll q/k/v, which the matvec also stages with
+ * a tag in the workspace (an MI355X fusion with no reference counterpart);
+ * other shapes make the two launches. The workspace is g4_attnDecodeFused's, zeroed before its first
  * use; calls that share a workspace must not overlap. */
 int g4_qkvAttnDecodeFusedWarm(g4_ctx* ctx, const float* x, const uint16_t* w1, const float* residual,
                               const uint16_t* out_scale, const uint16_t* w2, float* h_out,
