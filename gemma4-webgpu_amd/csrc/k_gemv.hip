@@ -2383,7 +2383,7 @@ int g4_qkvAttnDecodeFusedWarm(g4_ctx* ctx, const float* x, const uint16_t* w1, c
   }
   // the one-launch form: Q4_K rows of 1536 at the width the matvec's own
   // launch takes (6 or 3 waves), one KV head, a window merged in the
-  // launch, a flag per matvec workgroup
+  // launch, q/k/v staged in the workspace (at most kMaxStage values)
   GemvSegs sg{};
   for (int i = 0; i < nseg; ++i) sg.s[i] = GemvSeg{(const uint8_t*)weights[i], outputs[i], rows[i], 0};
   const int mnwv = mv_pick(6, sg.s, nseg);
