@@ -2381,8 +2381,11 @@ int g4_qkvAttnDecodeFusedWarm(g4_ctx* ctx, const float* x, const uint16_t* w1, c
     rc = check_w(__func__, 0, weights[i]);
     if (rc) return rc;
   }
-  // the one-launch form: Q4_K rows of 1536 at the width the matvec's own
-  // launch takes (6 or 3 waves), one KV head, a window merged in the
+  // the one-launch form: q, k and v (a layer reading its producer's cache
+  // projects q only, over 256 workgroups of 3 waves that would leave no CU
+  // to the attention or its L2 warming: it keeps the two launches), Q4_K
+  // rows of 1536 at the width the matvec's own launch takes, one KV head, a
+  // window merged in the
   // launch, q/k/v staged in the workspace (at most kMaxStage values)
   GemvSegs sg{};
   for (int i = 0; i < nseg; ++i) sg.s[i] = GemvSeg{(const uint8_t*)weights[i], outputs[i], rows[i], 0};
@@ -2395,7 +2398,7 @@ int g4_qkvAttnDecodeFusedWarm(g4_ctx* ctx, const float* x, const uint16_t* w1, c
   }
   bool applies = false;
   g4mqf::MqfLaunch L{};
-  if (N == 1536 && (mnwv == 6 || mnwv == 3) && p.num_kv_heads == 1 && rows[0] + 2 * rows[1] <= g4mqf::kMaxStage) {
+  if (N == 1536 && mnwv == 6 && nseg == 3 && p.num_kv_heads == 1 && rows[0] + 2 * rows[1] <= g4mqf::kMaxStage) {
     rc = g4mqf::mqf_prepare(ctx, q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs, k_cache, v_cache, output, p,
                             workspace, workspace_bytes, position_dev, regions, nregions, rope_cs, nmv, applies, L);
     if (rc) return rc;

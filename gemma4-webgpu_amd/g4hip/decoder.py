@@ -757,7 +757,8 @@ class Decoder(_SyntheticModel):
             n += 3
         for il, L in enumerate(self.layers):
             groups = qkv_groups(L, [0, 0, 0][:3 if s.is_producer(il) else 1], [0, 0, 0])
-            if self._qkv_fused(groups) and self.ctx.qkv_attn_single_launch(self.attn_params[il], s.hidden):
+            if self._qkv_fused(groups) and self.ctx.qkv_attn_single_launch(self.attn_params[il], s.hidden,
+                                                                          3 if s.is_producer(il) else 1):
                 n += 4
                 continue
             n += 4 + (not self.ctx.attn_fused_single_launch(self.attn_params[il]))

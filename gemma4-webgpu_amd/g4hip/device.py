@@ -440,11 +440,13 @@ class Context:
         return p.head_dim == 256 and p.num_kv_heads <= 64 and eff <= 65536
 
     @staticmethod
-    def qkv_attn_single_launch(p: AttnFusedParams, N: int) -> bool:
-        """Whether g4_qkvAttnDecodeFusedWarm runs as one launch: hidden 1536,
-        one KV head of dim 256, a window of at most 1024 positions."""
+    def qkv_attn_single_launch(p: AttnFusedParams, N: int, nseg: int = 3) -> bool:
+        """Whether g4_qkvAttnDecodeFusedWarm runs as one launch: q, k and v
+        (nseg 3), hidden 1536, one KV head of dim 256, a window of at most 1024
+        positions."""
         eff = min(p.max_seq_len, p.sliding_window) if p.sliding_window else p.max_seq_len
-        return N == 1536 and p.head_dim == 256 and p.num_kv_heads == 1 and p.num_q_heads == 8 and eff <= 1024
+        return (nseg == 3 and N == 1536 and p.head_dim == 256 and p.num_kv_heads == 1 and p.num_q_heads == 8
+                and eff <= 1024)
 
     def attnDecodeFused(self, q_raw: Ptr, k_raw: Ptr, v_raw: Ptr, q_norm_w: Ptr, k_norm_w: Ptr, rope_freqs: Ptr,
                         k_cache: Ptr, v_cache: Ptr, out: Ptr, p: AttnFusedParams, workspace: Buffer,

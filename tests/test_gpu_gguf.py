@@ -340,12 +340,12 @@ def test_file_model_fused_step_with_token_feedback(ctx, model_path):
     # second q/k/v launch of layer 1 (Q6_K v), + embedding, head, argmax,
     # + per-layer embeddings: stage 1 (2), 2 per layer, the last tail (1),
     # - one on each layer whose Q4_K q/k/v share the attention's launch
-    # (the two head-dim-256 layers with Q4_K q/k/v)
+    # (layer 0, the head-dim-256 producer with Q4_K q/k/v)
     assert d.layers[1].qt["wv"] == "q6k" and d.layers[1].qt["wq"] == "q4k"
     shared = [il for il in range(N_LAYERS)
               if d._qkv_fused(qkv_groups(d.layers[il], [0, 0, 0], [0, 0, 0]))
-              and ctx.qkv_attn_single_launch(d.attn_params[il], d.s.hidden)]
-    assert len(shared) == 2
+              and ctx.qkv_attn_single_launch(d.attn_params[il], d.s.hidden, 3 if d.s.is_producer(il) else 1)]
+    assert shared == [0]
     assert d.launches_per_step_fused() == 5 * N_LAYERS + 2 + 1 + 3 + 3 + 2 * N_LAYERS - len(shared)
     g = d.capture_fused()
     try:

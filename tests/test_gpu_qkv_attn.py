@@ -6,8 +6,9 @@ bit for bit: the attention output, q/k/v, the new residual and the caches.
 Both calls are pinned against the oracle by their own tests.
 
 Cases: a producer layer with the norm-add prologue, layer 0's plain rmsNorm,
-a layer reading its producer's cache (q only), windows merged in the launch
-(one launch) and a global window past 1024 positions (two launches), each
+a layer reading its producer's cache (q only: two launches), windows merged
+in the launch (one launch) and a global window past 1024 positions (two
+launches), each
 called three times on one workspace (the flags the launch sets must be clear
 again for the next call), and with a per-layer output scale.
 """
@@ -73,9 +74,9 @@ def test_qkv_attn_matches_two_calls(ctx, pos, window, cap, form):
     w2 = None if form == "first" else dev["w2"]
     scale = dev["scale"] if form == "scaled" else None
     kn = None if form == "consumer" else dev["kn"]
-    one = ctx.qkv_attn_single_launch(p, H)
+    one = ctx.qkv_attn_single_launch(p, H, nseg)
     print(f"[qkv+attn] pos={pos} window={window} cap={cap} {form}: one launch {one}", flush=True)
-    assert one == (cap <= 1024)
+    assert one == (cap <= 1024 and nseg == 3)
     results = []
     ws_two = ctx.zeros(ctx.attn_fused_workspace_bytes(p), np.uint8)
     ws_one = ctx.zeros(ctx.attn_fused_workspace_bytes(p), np.uint8)
