@@ -38,19 +38,25 @@ uint32_t scalar_size(uint32_t t) {
   }
 }
 
-// Bytes of a tensor of `n` elements (src/gguf.ts:385-395); 0 for a type the
-// reference does not load.
-uint64_t type_bytes(uint32_t type, uint64_t n) {
+// Bytes of a tensor of `n` elements (src/gguf.ts:385-395) in *bytes; 0 for
+// a type the reference does not load. False when the size does not fit 64
+// bits (a file whose dims describe more bytes than any file holds).
+bool type_bytes(uint32_t type, uint64_t n, uint64_t* bytes) {
+  uint64_t per = 0;  // bytes per element of the unblocked types
   switch (type) {
-    case 0: return n * 4;                     // F32
-    case 1: return n * 2;                     // F16
-    case 8: return n % 32 ? 0 : n / 32 * 34;  // Q8_0
-    case 12: return n % 256 ? 0 : n / 256 * 144;  // Q4_K
-    case 13: return n % 256 ? 0 : n / 256 * 176;  // Q5_K
-    case 14: return n % 256 ? 0 : n / 256 * 210;  // Q6_K
-    case 30: return n * 2;                    // BF16
-    default: return 0;
+    case 0: per = 4; break;   // F32
+    case 1: per = 2; break;   // F16
+    case 30: per = 2; break;  // BF16
+    // block types: n / block x block bytes stays below n
+    case 8: *bytes = n % 32 ? 0 : n / 32 * 34; return true;      // Q8_0
+    case 12: *bytes = n % 256 ? 0 : n / 256 * 144; return true;  // Q4_K
+    case 13: *bytes = n % 256 ? 0 : n / 256 * 176; return true;  // Q5_K
+    case 14: *bytes = n % 256 ? 0 : n / 256 * 210; return true;  // Q6_K
+    default: *bytes = 0; return true;
   }
+  if (n > UINT64_MAX / per) return false;
+  *bytes = n * per;
+  return true;
 }
 
 struct Kv {
@@ -233,7 +239,8 @@ int parse(g4_gguf* g) {
     t.type = r.get<uint32_t>();
     t.offset = r.get<uint64_t>();
     G4_REQUIRE(r.ok, "g4_gguf: tensor info %llu truncated", (unsigned long long)i);
-    t.nbytes = type_bytes(t.type, n);
+    G4_REQUIRE(type_bytes(t.type, n, &t.nbytes), "g4_gguf: tensor %s: %llu elements of type %u overflow 64-bit bytes",
+               t.name.c_str(), (unsigned long long)n, t.type);
     g->tensor_index[t.name] = i;
   }
   g->data_offset = (r.pos + g->alignment - 1) / g->alignment * g->alignment;

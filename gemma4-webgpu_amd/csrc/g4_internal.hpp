@@ -28,6 +28,16 @@ struct g4_ctx {
   // (with the lookup's status in noalloc_status) when the lookup failed.
   void* noalloc_scratch = nullptr;
   int noalloc_status = 0;
+  // Kernel status word in pinned host memory that kernels write through its
+  // device address: nonzero once a bounded in-kernel wait of a launch on
+  // this context expired (that launch's outputs are NaN). Checked by every
+  // entry point and after every synchronisation; cleared by g4_clear_stall.
+  volatile uint32_t* status = nullptr;
+  uint32_t* status_dev = nullptr;
+  // g4_test_stage_wait: poll limit of the q/k/v hand-off (0 = the built-in
+  // one) and whether the q/k/v + attention launch leaves out its matvec
+  uint32_t test_spin = 0;
+  bool test_skip_matvec = false;
 };
 
 // Looks up the device address of g4_attnDecode_noalloc's static partials
@@ -61,6 +71,7 @@ int g4_internal_batch_matmul(g4_ctx* ctx, const char* fn, int qt, const float* x
 struct g4_event {
   hipEvent_t ev = nullptr;
   int device = 0;
+  const volatile uint32_t* status = nullptr;  // the recording context's kernel status word
 };
 
 struct g4_graph {
@@ -78,6 +89,8 @@ int hip_fail(g4_ctx* ctx, hipError_t e, const char* what);
 int enter(g4_ctx* ctx, const char* fn);
 // Checks the launch that was just enqueued.
 int check_launch(g4_ctx* ctx, const char* kernel);
+// G4_ERR_STALLED when a kernel status word reports an expired wait.
+int check_status(const volatile uint32_t* status, const char* fn);
 
 }  // namespace g4
 

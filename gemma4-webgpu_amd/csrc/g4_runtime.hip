@@ -7,6 +7,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <vector>
+
 #include "g4_internal.hpp"
 
 namespace {
@@ -49,9 +51,21 @@ int hip_fail(g4_ctx* ctx, hipError_t e, const char* what) {
   return set_error(G4_ERR_HIP, "%s failed: %s", what, hipGetErrorString(e));
 }
 
+int check_status(const volatile uint32_t* status, const char* fn) {
+  if (status && *status != 0u)
+    return set_error(G4_ERR_STALLED,
+                     "%s: a bounded wait inside a kernel expired (status 0x%x): the q/k/v hand-off of a "
+                     "g4_qkvAttnDecodeFusedWarm launch never completed and that launch wrote NaN; "
+                     "g4_clear_stall, then zero its attention workspace",
+                     fn, (unsigned)*status);
+  return G4_OK;
+}
+
 int enter(g4_ctx* ctx, const char* fn) {
   if (!ctx) return set_error(G4_ERR_INVALID, "%s: null context", fn);
   if (ctx->lost) return set_error(G4_ERR_DEVICE_LOST, "%s: device was lost earlier", fn);
+  int rc = check_status(ctx->status, fn);
+  if (rc) return rc;
   hipError_t e = hipSetDevice(ctx->device);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
   return G4_OK;
@@ -115,6 +129,20 @@ int g4_init(int device, g4_ctx** out) {
     delete ctx;
     return g4::hip_fail(nullptr, e, "hipMalloc(scratch)");
   }
+  // the kernel status word: pinned, coherent host memory that kernels
+  // write through its device address
+  void* st = nullptr;
+  e = hipHostMalloc(&st, 256, hipHostMallocMapped | hipHostMallocCoherent);
+  if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&ctx->status_dev, st, 0);
+  if (e != hipSuccess) {
+    if (st) (void)hipHostFree(st);
+    (void)hipFree(ctx->scratch);
+    (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+    return g4::hip_fail(nullptr, e, "hipHostMalloc(status)");
+  }
+  memset(st, 0, 256);
+  ctx->status = (volatile uint32_t*)st;
   g4_internal_noalloc_init(ctx);  // a failed lookup only disables g4_attnDecode_noalloc
   *out = ctx;
   return G4_OK;
@@ -125,6 +153,7 @@ int g4_destroy(g4_ctx* ctx) {
   (void)hipSetDevice(ctx->device);
   if (!ctx->lost) (void)hipStreamSynchronize(ctx->own_stream);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
+  if (ctx->status) (void)hipHostFree((void*)ctx->status);
   (void)hipStreamDestroy(ctx->own_stream);
   delete ctx;
   return G4_OK;
@@ -185,7 +214,7 @@ int g4_upload(g4_ctx* ctx, void* dst, const void* src, size_t bytes, size_t dst_
   G4_HIP(ctx, hipMemcpyAsync((char*)dst + dst_offset, src, bytes, hipMemcpyHostToDevice,
                              ctx->stream));
   G4_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  return G4_OK;
+  return g4::check_status(ctx->status, __func__);
 }
 
 int g4_download(g4_ctx* ctx, void* dst, const void* src, size_t bytes, size_t src_offset) {
@@ -196,7 +225,7 @@ int g4_download(g4_ctx* ctx, void* dst, const void* src, size_t bytes, size_t sr
   G4_HIP(ctx, hipMemcpyAsync(dst, (const char*)src + src_offset, bytes, hipMemcpyDeviceToHost,
                              ctx->stream));
   G4_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  return G4_OK;
+  return g4::check_status(ctx->status, __func__);
 }
 
 int g4_download_async(g4_ctx* ctx, void* dst, const void* src, size_t bytes, size_t src_offset,
@@ -222,6 +251,19 @@ int g4_stream_sync(g4_ctx* ctx) {
   G4_ENTER(ctx);
   G4_NOT_CAPTURING(ctx, "g4_stream_sync");
   G4_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return g4::check_status(ctx->status, __func__);
+}
+
+int g4_clear_stall(g4_ctx* ctx) {
+  if (!ctx) return g4::set_error(G4_ERR_INVALID, "g4_clear_stall: null context");
+  if (ctx->status) *ctx->status = 0u;
+  return G4_OK;
+}
+
+int g4_test_stage_wait(g4_ctx* ctx, uint32_t spin_limit, int skip_matvec) {
+  G4_ENTER(ctx);
+  ctx->test_spin = spin_limit;
+  ctx->test_skip_matvec = skip_matvec != 0;
   return G4_OK;
 }
 
@@ -230,6 +272,7 @@ int g4_event_record(g4_ctx* ctx, g4_event** ev) {
   G4_REQUIRE(ev, "g4_event_record: null out");
   g4_event* e = new g4_event();
   e->device = ctx->device;
+  e->status = ctx->status;
   hipError_t he = hipEventCreate(&e->ev);
   if (he != hipSuccess) {
     delete e;
@@ -249,7 +292,10 @@ int g4_event_query(g4_event* ev) {
   if (!ev) return g4::set_error(G4_ERR_INVALID, "g4_event_query: null event");
   (void)hipSetDevice(ev->device);
   hipError_t e = hipEventQuery(ev->ev);
-  if (e == hipSuccess) return 1;
+  if (e == hipSuccess) {
+    const int rc = g4::check_status(ev->status, "g4_event_query");
+    return rc ? rc : 1;
+  }
   if (e == hipErrorNotReady) return 0;
   return g4::hip_fail(nullptr, e, "hipEventQuery");
 }
@@ -259,7 +305,7 @@ int g4_event_wait(g4_event* ev) {
   (void)hipSetDevice(ev->device);
   hipError_t e = hipEventSynchronize(ev->ev);
   if (e != hipSuccess) return g4::hip_fail(nullptr, e, "hipEventSynchronize");
-  return G4_OK;
+  return g4::check_status(ev->status, "g4_event_wait");
 }
 
 int g4_event_elapsed_ms(g4_event* a, g4_event* b, float* ms) {
@@ -310,6 +356,26 @@ int g4_graph_launch(g4_ctx* ctx, g4_graph* graph) {
   G4_ENTER(ctx);
   G4_REQUIRE(graph && graph->exec, "g4_graph_launch: null graph");
   G4_HIP(ctx, hipGraphLaunch(graph->exec, ctx->stream));
+  return G4_OK;
+}
+
+int g4_graph_kernel_nodes(g4_graph* graph, size_t* count) {
+  if (!graph || !graph->graph || !count) return g4::set_error(G4_ERR_INVALID, "g4_graph_kernel_nodes: null");
+  *count = 0;
+  size_t n = 0;
+  hipError_t e = hipGraphGetNodes(graph->graph, nullptr, &n);
+  if (e != hipSuccess) return g4::hip_fail(nullptr, e, "hipGraphGetNodes");
+  std::vector<hipGraphNode_t> nodes(n);
+  if (n) {
+    e = hipGraphGetNodes(graph->graph, nodes.data(), &n);
+    if (e != hipSuccess) return g4::hip_fail(nullptr, e, "hipGraphGetNodes");
+  }
+  for (size_t i = 0; i < n; ++i) {
+    hipGraphNodeType t;
+    e = hipGraphNodeGetType(nodes[i], &t);
+    if (e != hipSuccess) return g4::hip_fail(nullptr, e, "hipGraphNodeGetType");
+    if (t == hipGraphNodeTypeKernel) ++*count;
+  }
   return G4_OK;
 }
 

@@ -1415,6 +1415,8 @@ int mqf_prepare(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float
   }
   m.stage = (uint64_t*)((uint8_t*)workspace + kMqfCntOnly);
   m.nstage = 0;
+  m.spin = ctx->test_spin ? ctx->test_spin : kStageSpin;
+  m.status = ctx->status_dev;
   L.partials = mp.partials;
   return G4_OK;
 }

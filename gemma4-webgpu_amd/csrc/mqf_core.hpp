@@ -94,6 +94,8 @@ struct MqfArgs {
   // then v)
   uint64_t* stage;
   uint32_t nstage;
+  uint32_t spin;       // polls before the wait for the staged values gives up
+  uint32_t* status;    // the context's kernel status word (pinned host memory)
 };
 
 constexpr int MQF_QS = 264;  // LDS stride of a q column (halves)
@@ -133,8 +135,13 @@ __device__ __forceinline__ float4 ld_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off
 // wait is bounded (kStageSpin polls, each a device-scope round trip, about
 // 0.1 s in all) so that every workgroup ends even if a value never comes;
 // the matvec workgroups precede the attention ones in the grid and wait on
-// nothing, so in-order dispatch always lets them finish.
+// nothing, so in-order dispatch always lets them finish. A wait that
+// expires is not silent: the workgroup takes NaN for every value, stores a
+// partial whose maximum is +Inf (so every merge that includes it yields NaN
+// whatever the order), and sets the kernel status word, which the host
+// reports as G4_ERR_STALLED.
 constexpr uint32_t kStageSpin = 1u << 16;
+constexpr uint32_t kStatusStageWait = 1u;  // status bit: the q/k/v hand-off wait expired
 constexpr uint32_t kMaxStage = 4096;  // staged values: nqh * 256 + 2 * nkh * 256
 constexpr uint64_t kStaged = 1ull << 32;
 __device__ __forceinline__ uint64_t stage_ld(const uint64_t* p) {
@@ -143,8 +150,9 @@ __device__ __forceinline__ uint64_t stage_ld(const uint64_t* p) {
 __device__ __forceinline__ float stage_val(uint64_t e) { return __uint_as_float((uint32_t)e); }
 // The MQ_NT threads (4 waves; a wider launch's other waves have ended) each
 // poll their 8 q values and (own_row) one k and one v value; the vote goes
-// through LDS, one word per wave.
-__device__ __forceinline__ void mqf_wait_stage(const MqfArgs& a, int tid, size_t qoff, uint32_t kvh, bool own_row,
+// through LDS, one word per wave. Returns true (uniform over the
+// workgroup) when the wait expired, with every value NaN.
+__device__ __forceinline__ bool mqf_wait_stage(const MqfArgs& a, int tid, size_t qoff, uint32_t kvh, bool own_row,
                                                float4& q0, float4& q1, float& kx, float& vx) {
   __shared__ uint32_t s_ok[MQ_NT / 64];
   const uint64_t* sq = a.stage + qoff;
@@ -169,12 +177,21 @@ __device__ __forceinline__ void mqf_wait_stage(const MqfArgs& a, int tid, size_t
 #pragma unroll
     for (int w = 0; w < MQ_NT / 64; ++w) all = all && s_ok[w] != 0u;
     __syncthreads();  // every wave has read the votes before the next round writes them
-    if (all || it >= kStageSpin) {
+    if (all) {
       q0 = make_float4(stage_val(e[0]), stage_val(e[1]), stage_val(e[2]), stage_val(e[3]));
       q1 = make_float4(stage_val(e[4]), stage_val(e[5]), stage_val(e[6]), stage_val(e[7]));
       kx = own_row ? stage_val(e[8]) : 0.f;
       vx = own_row ? stage_val(e[9]) : 0.f;
-      return;
+      return false;
+    }
+    if (it >= a.spin) {  // (uniform) expired: poison, and report it to the host
+      const float nan = __builtin_nanf("");
+      q0 = make_float4(nan, nan, nan, nan);
+      q1 = q0;
+      kx = nan;
+      vx = nan;
+      if (tid == 0) __hip_atomic_store(a.status, kStatusStageWait, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      return true;
     }
     __builtin_amdgcn_s_sleep(1);
   }
@@ -339,6 +356,7 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   const size_t qoff = (size_t)(kvh * MQ_G + th) * MQ_HD + td;
   float4 q0, q1;
   float kx, vx;
+  bool stalled = false;  // (uniform) FUSED: the wait for q/k/v expired
   if constexpr (!FUSED) {
     const float* qg = a.q_raw + qoff;
     q0 = *(const float4*)qg;
@@ -356,7 +374,7 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   __builtin_amdgcn_sched_barrier(0);
   load_step(0);
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (FUSED) mqf_wait_stage(a, tid, qoff, kvh, own_row, q0, q1, kx, vx);
+  if constexpr (FUSED) stalled = mqf_wait_stage(a, tid, qoff, kvh, own_row, q0, q1, kx, vx);
 
   // RoPE of this position (rope_cos_sin), from the table when there is one:
   // the frequency's f64 pow and a large-argument sincos are some 380 VALU
@@ -521,7 +539,8 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
       wt_s[ww * MQ_G + tid] = wt;
       Ls += wt * ml_s[4 * MQ_G + ww * MQ_G + tid];
     }
-    st_dev(r0, (uint32_t)(part0 + tid) * 4u, M);
+    // a stalled chunk's +Inf maximum turns every merge that includes it into NaN
+    st_dev(r0, (uint32_t)(part0 + tid) * 4u, stalled ? INFINITY : M);
     st_dev(r0, (uint32_t)(nparts + part0 + tid) * 4u, Ls);
   }
   __syncthreads();

@@ -15,6 +15,7 @@ ERRORS = {
     -4: "G4_ERR_OOM",
     -5: "G4_ERR_UNSUPPORTED",
     -6: "G4_ERR_NO_DEVICE",
+    -7: "G4_ERR_STALLED",
 }
 
 
@@ -127,6 +128,9 @@ SIGNATURES = {
     "g4_download_async": (_I, [_P, _P, _P, _SZ, _SZ, _PP]),
     "g4_copy_d2d": (_I, [_P, _P, _P, _SZ]),
     "g4_stream_sync": (_I, [_P]),
+    "g4_clear_stall": (_I, [_P]),
+    "g4_graph_kernel_nodes": (_I, [_P, ctypes.POINTER(ctypes.c_size_t)]),
+    "g4_test_stage_wait": (_I, [_P, _U32, _I]),
     "g4_event_record": (_I, [_P, _PP]),
     "g4_event_query": (_I, [_P]),
     "g4_event_wait": (_I, [_P]),

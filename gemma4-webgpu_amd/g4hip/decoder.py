@@ -759,11 +759,11 @@ class Decoder(_SyntheticModel):
             groups = qkv_groups(L, [0, 0, 0][:3 if s.is_producer(il) else 1], [0, 0, 0])
             if self._qkv_fused(groups) and self.ctx.qkv_attn_single_launch(self.attn_params[il], s.hidden,
                                                                           3 if s.is_producer(il) else 1):
-                n += 4
-                continue
-            n += 4 + (not self.ctx.attn_fused_single_launch(self.attn_params[il]))
-            for qt, ws, _, _ in groups:
-                n += 1 + (len(ws) if qt == "f16" else 0)
+                n += 4  # q/k/v with the attention block, o, gate/up, down
+            else:
+                n += 4 + (not self.ctx.attn_fused_single_launch(self.attn_params[il]))
+                for qt, ws, _, _ in groups:
+                    n += 1 + (len(ws) if qt == "f16" else 0)
             if not self._ffn_fused(L):
                 n += 3  # norm, second matvec, GELU product
         return n
@@ -906,7 +906,7 @@ class BatchDecoder(_SyntheticModel):
                 total += n * 2 * s.kv_dim_of(il) * 2
         return total
 
-    def step(self, sample: str = "argmax") -> None:
+    def step(self, sample: str = "argmax", probe=None) -> None:
         """One token for every sequence. Per layer:
           1. [sum of the previous down chunks -> post-FFN norm-add ->] attn rmsNorm
           2. q/k/v projections (split-K partial sums)
@@ -918,7 +918,15 @@ class BatchDecoder(_SyntheticModel):
           7. gate/up -> GELU product
           8. down projection (Q6_K, partial sums)
         then the last norm-add + final rmsNorm, the LM head + softcap, and the
-        per-sequence argmax (or top-k 256)."""
+        per-sequence argmax (or top-k 256).
+
+        probe (tests): called as probe(stage, il, chunks) once the stage's
+        launches are enqueued, so that a test can read the stage's buffers:
+        "prep" (layer il's normalised input `xn` and residual `hidden`; il =
+        n_layers for the final norm), "attn" (roped `q`, the appended K/V
+        rows, `attn`), "ffn_in" (`hidden2` and `xn` after the post-attention
+        norm-add), "ffn" (the down projection's `chunks` partial sums in
+        `down_parts`), "head" (`logits`). Not for captured steps."""
         c, s, B = self.ctx, self.s, self.B
         H = s.hidden
         if self.embedding is not None:
@@ -943,6 +951,8 @@ class BatchDecoder(_SyntheticModel):
                 prev = self.layers[il - 1]
                 c.batchPrep(self.down_parts, nd, prev.post_ffn_norm, self.hidden2, L.attn_norm, self.hidden,
                             self.xn, H, B, s.eps, ops=self.xops)
+            if probe:
+                probe("prep", il, 0)
             # a layer reading a producer's pool projects q only and appends no row
             outs = [self.q_parts, self.k_parts, self.v_parts] if prod else [self.q_parts]
             groups = qkv_groups(L, outs, [Q, KV, KV] if prod else [Q])
@@ -966,9 +976,13 @@ class BatchDecoder(_SyntheticModel):
             ops = self.aops if s.hd(il) % 256 == 0 else None
             c.pagedAttnDecode(self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.attn,
                               self.attn_params[il], self.attn_ws, ops=ops)
+            if probe:
+                probe("attn", il, 0)
             no = self._mm_batch(L.qt["wo"], self.attn, L.wo, self.o_parts, H, Q, self.ks_q, ops)
             c.batchPrep(self.o_parts, no, L.post_attn_norm, self.hidden, L.pre_ffn_norm, self.hidden2, self.xn, H, B,
                         s.eps, ops=self.xops)
+            if probe:
+                probe("ffn_in", il, 0)
             if self._ffn_handoff(il):
                 # the product goes to the down projection as operand blocks only;
                 # K in chunks of 3 super-blocks (one workgroup per CU)
@@ -982,6 +996,8 @@ class BatchDecoder(_SyntheticModel):
                     self._mm_batch(L.qt["wup"], self.xn, L.wup, self.up_b, I, H, 1, self.xops)
                     c.geluMul(self.gate_b, self.up_b, self.act, B * I)
                 nd = self._mm_batch(L.qt["wdown"], self.act, L.wdown, self.down_parts, H, I, self.ks_f, None)
+            if probe:
+                probe("ffn", il, nd)
             if s.ple_dim:
                 # post-FFN norm-add (h, no second norm) -> inp_gate -> gelu * ple_inputs -> proj
                 D = s.ple_dim
@@ -997,6 +1013,8 @@ class BatchDecoder(_SyntheticModel):
         else:
             c.batchPrep(self.down_parts, nd, last.post_ffn_norm, self.hidden2, self.final_norm, self.hidden, self.xn,
                         H, B, s.eps, ops=self.xops)
+        if probe:
+            probe("prep", s.n_layers, 0)
         if self.lm_head is not None:
             if self.lm_type == "f16":
                 c.matmulF16(self.xn, self.lm_head, self.logits, s.vocab, H, B)
@@ -1008,6 +1026,8 @@ class BatchDecoder(_SyntheticModel):
                 c.argmaxBatch(self.logits, self.tokens, s.vocab, B)
             else:
                 c.topk256Batch(self.logits, self.topk, s.vocab, B)
+            if probe:
+                probe("head", s.n_layers, 0)
         self.lens_host = self.lens_host + 1
 
     def _ffn_handoff(self, il: int) -> bool:

@@ -148,6 +148,15 @@ class Context:
     def sync(self) -> None:
         check(lib().g4_stream_sync(self.h))
 
+    def clear_stall(self) -> None:
+        """Acknowledges a G4_ERR_STALLED (the kernel status word)."""
+        check(lib().g4_clear_stall(self.h))
+
+    def test_stage_wait(self, spin_limit: int, skip_matvec: bool) -> None:
+        """Test hook: poll limit of the q/k/v hand-off and whether the one
+        q/k/v + attention launch leaves out its matvec workgroups."""
+        check(lib().g4_test_stage_wait(self.h, spin_limit, 1 if skip_matvec else 0))
+
     # ---- events / graphs ----
     def record(self) -> ctypes.c_void_p:
         ev = ctypes.c_void_p()
@@ -167,6 +176,13 @@ class Context:
 
     def graph_begin(self) -> None:
         check(lib().g4_graph_begin(self.h))
+
+    @staticmethod
+    def graph_kernel_nodes(g) -> int:
+        """Kernel launches one replay of the captured graph issues."""
+        n = ctypes.c_size_t()
+        check(lib().g4_graph_kernel_nodes(g, ctypes.byref(n)))
+        return int(n.value)
 
     def graph_end(self) -> ctypes.c_void_p:
         g = ctypes.c_void_p()

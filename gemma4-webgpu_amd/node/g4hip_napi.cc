@@ -28,6 +28,7 @@ const char* status_name(int rc) {
     case G4_ERR_OOM: return "G4_ERR_OOM";
     case G4_ERR_UNSUPPORTED: return "G4_ERR_UNSUPPORTED";
     case G4_ERR_NO_DEVICE: return "G4_ERR_NO_DEVICE";
+    case G4_ERR_STALLED: return "G4_ERR_STALLED";
     default: return "G4_ERR_UNKNOWN";
   }
 }

@@ -15,6 +15,14 @@
  *    g4_last_error() returns a thread-local message for the last failure.
  *  - A device fault makes the context sticky-lost: every later call on it
  *    returns G4_ERR_DEVICE_LOST (mirrors `device.lost`, src/engine.ts:385-388).
+ *  - A launch whose workgroups hand values to each other inside the launch
+ *    (g4_qkvAttnDecodeFusedWarm) waits for them a bounded number of polls.
+ *    If a wait expires, the launch still ends, its outputs are NaN, and the
+ *    context's kernel status word is set: every later call, and the
+ *    synchronisation that follows the launch (g4_stream_sync, g4_download,
+ *    g4_event_wait / g4_event_query), returns G4_ERR_STALLED until
+ *    g4_clear_stall. The reference has no in-launch hand-off and so no
+ *    counterpart; it is reported as device loss is, at the next call.
  *  - Kernels are enqueued on the context's stream and return immediately;
  *    they never allocate (callers own every buffer, src/engine.ts:1001-1064).
  *  - Weights are raw GGUF block bytes (Q4_K: 144 B / 256 weights, Q6_K: 210 B /
@@ -46,6 +54,8 @@ extern "C" {
 #define G4_ERR_OOM (-4)          /* device allocation failed */
 #define G4_ERR_UNSUPPORTED (-5)  /* shape the kernels do not handle */
 #define G4_ERR_NO_DEVICE (-6)    /* no HIP device / wrong architecture */
+#define G4_ERR_STALLED (-7)      /* sticky until g4_clear_stall: a bounded wait inside a
+                                    kernel expired, and that launch wrote NaN outputs */
 
 typedef struct g4_ctx g4_ctx;
 typedef struct g4_event g4_event;
@@ -81,7 +91,14 @@ int g4_download_async(g4_ctx* ctx, void* dst, const void* src, size_t bytes, siz
                       g4_event** ev);
 int g4_copy_d2d(g4_ctx* ctx, void* dst, const void* src, size_t bytes);
 int g4_stream_sync(g4_ctx* ctx);
+/* Clears the kernel status word after a G4_ERR_STALLED (no counterpart in
+ * the reference, see Conventions). The launch that stalled may still have
+ * left staged values in its attention workspace: zero that workspace
+ * (g4_memset) before the next g4_qkvAttnDecodeFusedWarm on it. */
+int g4_clear_stall(g4_ctx* ctx);
 
+/* An event reports its context's G4_ERR_STALLED once complete, so it is
+ * destroyed before the context that recorded it. */
 int g4_event_record(g4_ctx* ctx, g4_event** ev);
 int g4_event_query(g4_event* ev); /* 1 = complete, 0 = pending, <0 error */
 int g4_event_wait(g4_event* ev);
@@ -97,6 +114,9 @@ int g4_graph_begin(g4_ctx* ctx);
 int g4_graph_end(g4_ctx* ctx, g4_graph** graph);
 int g4_graph_launch(g4_ctx* ctx, g4_graph* graph);
 int g4_graph_destroy(g4_graph* graph);
+/* Kernel nodes of a captured graph (diagnostics, no reference counterpart:
+ * the launches one replay issues). */
+int g4_graph_kernel_nodes(g4_graph* graph, size_t* count);
 
 /* ------------------------------------------------------------------------ */
 /* Kernel entry points (one per SHADERS key, src/shaders.ts:34-56)           */
@@ -260,7 +280,11 @@ int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, 
  * matvec workgroups run, and poll q/k/v, which the matvec also stages with
  * a tag in the workspace (an MI355X fusion with no reference counterpart);
  * other shapes make the two launches. The workspace is g4_attnDecodeFused's, zeroed before its first
- * use; calls that share a workspace must not overlap. */
+ * use; calls that share a workspace must not overlap. The attention
+ * workgroups of the one launch poll for q/k/v at most 2^16 times (about
+ * 0.1 s); if that expires, the launch writes NaN to `output` (and to the
+ * K/V row it stores) and the call's stall is reported as G4_ERR_STALLED
+ * (Conventions). */
 int g4_qkvAttnDecodeFusedWarm(g4_ctx* ctx, const float* x, const uint16_t* w1, const float* residual,
                               const uint16_t* out_scale, const uint16_t* w2, float* h_out,
                               const void* const* weights, float* const* outputs, int nseg, uint32_t N, float eps,
@@ -269,6 +293,13 @@ int g4_qkvAttnDecodeFusedWarm(g4_ctx* ctx, const float* x, const uint16_t* w1, c
                               void* workspace, size_t workspace_bytes, const uint32_t* position_dev,
                               const g4_warm_region* regions, int nregions, const float* rope_cs,
                               uint32_t rope_rows);
+/* Test hook with no reference counterpart, for tests of the stall report:
+ * the following one-launch g4_qkvAttnDecodeFusedWarm calls on this context
+ * poll at most `spin_limit` times (0 restores the built-in limit) and, when
+ * skip_matvec is nonzero, launch no matvec workgroups, so that nothing
+ * stages q/k/v and every attention workgroup's wait expires (every kernel
+ * still ends). (0, 0) restores normal operation. */
+int g4_test_stage_wait(g4_ctx* ctx, uint32_t spin_limit, int skip_matvec);
 /* RoPE table of shaders/fused_per_head_norm_rope.wgsl:50-55: for position
  * t < rows and pair i < head_dim/2, table[2 (t head_dim/2 + i)] = cos and
  * [.. + 1] = sin of t * freq_i, freq_i = 1/theta^(2i/head_dim) (divided by

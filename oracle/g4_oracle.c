@@ -217,15 +217,6 @@ void g4o_dequant_q5k(const uint8_t* blocks, size_t nblocks, float* out) {
 /* matvec: y[m] = sum_k W[m,k] * x[k]   (shaders/matmul_quant.wgsl:25-53)    */
 /* ------------------------------------------------------------------------ */
 
-void g4o_matmul_f32w(const float* x, const float* W, float* y, uint32_t M, uint32_t N) {
-  for (uint32_t m = 0; m < M; ++m) {
-    const float* row = W + (size_t)m * N;
-    double acc = 0.0;
-    for (uint32_t k = 0; k < N; ++k) acc += (double)row[k] * (double)x[k];
-    y[m] = (float)acc;
-  }
-}
-
 /* The reference's own weight format: f16 rows (shaders/matmul_quant.wgsl:14). */
 void g4o_matmul_f16w(const float* x, const uint16_t* W, float* y, uint32_t M, uint32_t N) {
   for (uint32_t m = 0; m < M; ++m) {

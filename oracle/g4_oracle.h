@@ -32,7 +32,6 @@ void g4o_dequant_q5k(const uint8_t* blocks, size_t nblocks, float* out); /* src/
 void g4o_dequant_q8_0(const uint8_t* blocks, size_t nblocks, float* out); /* src/gguf.ts:115-131 */
 
 /* ---- matvec (shaders/matmul_quant.wgsl:12-54; rows M, reduction N) ---- */
-void g4o_matmul_f32w(const float* x, const float* W, float* y, uint32_t M, uint32_t N);
 void g4o_matmul_f16w(const float* x, const uint16_t* W, float* y, uint32_t M, uint32_t N);
 void g4o_matmul_q4k(const float* x, const uint8_t* W, float* y, uint32_t M, uint32_t N);
 void g4o_matmul_q6k(const float* x, const uint8_t* W, float* y, uint32_t M, uint32_t N);

@@ -67,7 +67,6 @@ def _declare(L):
         "g4o_dequant_q8_0": (None, [_P, _SZ, _P]),
         "g4o_ple_stage1": (None, [_P, _P, _P, _P, _U32, _U32, _F]),
         "g4o_ple_skip_scale_add": (None, [_P, _P, ctypes.c_uint16, _U32]),
-        "g4o_matmul_f32w": (None, [_P, _P, _P, _U32, _U32]),
         "g4o_matmul_f16w": (None, [_P, _P, _P, _U32, _U32]),
         "g4o_matmul_q4k": (None, [_P, _P, _P, _U32, _U32]),
         "g4o_matmul_q6k": (None, [_P, _P, _P, _U32, _U32]),
@@ -194,13 +193,10 @@ def dequant_f16_rows(raw: np.ndarray, ggml_type: int) -> np.ndarray:
 
 
 def matmul(x: np.ndarray, W: np.ndarray, M: int, N: int, wtype: str) -> np.ndarray:
-    """y[M] = W[M, N] . x[N] for wtype in {'f32', 'f16', 'q4k', 'q6k'}."""
+    """y[M] = W[M, N] . x[N] for wtype in {'f16', 'q4k', 'q6k'}."""
     x = _c(x, np.float32)
     y = np.empty(M, np.float32)
-    if wtype == "f32":
-        W = _c(W, np.float32)
-        lib().g4o_matmul_f32w(_p(x), _p(W), _p(y), M, N)
-    elif wtype == "f16":
+    if wtype == "f16":
         W = _c(W, np.uint16)
         lib().g4o_matmul_f16w(_p(x), _p(W), _p(y), M, N)
     elif wtype == "q4k":

@@ -139,6 +139,11 @@ def test_corrupt_headers_are_refused():
     bad.append(_patch(full, hdr + 4, "<Q", 0))        # a zero dim
     bad.append(_patch(full, hdr + 16, "<Q", t.offset + 4))  # misaligned offset
     bad.append(_patch(full, hdr + 16, "<Q", 1 << 40))  # data past the end
+    # element counts whose byte size wraps 64 bits to a few bytes (F32 x 4, F16 / BF16 x 2)
+    bad.append(_patch(full, hdr + 4, "<Q", (1 << 62) + 1))
+    bad.append(_patch(full, hdr + 4, "<Q", 1 << 62))
+    for t16 in (1, 30):
+        bad.append(_patch(_patch(full, hdr + 12, "<I", t16), hdr + 4, "<Q", (1 << 63) + 1))
     for i, b in enumerate(bad):
         with pytest.raises(G4Error):
             GGUFFile(data=b)

@@ -133,7 +133,7 @@ def test_attn_decode_dev_position(ctx):
         assert_close(out.download(np.float32), O.attention(q, k, v, nqh, nkh, hd, pos + 1), what=f"pos={pos}")
 
 
-@pytest.mark.parametrize("B,window", [(4, 0), (32, 0), (32, 512)])
+@pytest.mark.parametrize("B,window", [(4, 0), (32, 0), (32, 512), (64, 0), (64, 512)])
 def test_paged_ragged(ctx, B, window):
     nqh, nkh, hd, P = 8, 1, 256, 16
     rng = np.random.default_rng(B + window)

@@ -348,6 +348,7 @@ def test_file_model_fused_step_with_token_feedback(ctx, model_path):
     assert shared == [0]
     assert d.launches_per_step_fused() == 5 * N_LAYERS + 2 + 1 + 3 + 3 + 2 * N_LAYERS - len(shared)
     g = d.capture_fused()
+    assert ctx.graph_kernel_nodes(g) == d.launches_per_step_fused()
     try:
         tok = T0
         for i in range(2):
@@ -510,6 +511,7 @@ def test_every_format_fused_step(ctx, formats_path):
     # o, unfused FFN; layer 3: q, attention + merge, o, fused FFN
     assert d.launches_per_step_fused() == 1 + 5 + (3 + 2 * N_LAYERS) + 8 + 10 + 9 + 6
     g = d.capture_fused()
+    assert ctx.graph_kernel_nodes(g) == d.launches_per_step_fused()
     try:
         tok = 77
         for i in range(2):

@@ -11,7 +11,8 @@ device's logits (bit-exact) and a maximum of the oracle's up to the logits'
 tolerance. Cases: a 40-token prompt in chunks of 16 (the last one short),
 from position 0 and after 600 cached positions (past the 512 window), on a
 local + global layer pair and on Gemma-4-E2B's layer kinds (head dim 512
-globals, layers reading a producer's cache)."""
+globals, layers reading a producer's cache); and a 100-token prompt in the
+benchmark's 64-row chunks (one whole chunk, then a short one)."""
 import numpy as np
 import pytest
 
@@ -22,8 +23,7 @@ from gpu_util import assert_close
 
 pytestmark = pytest.mark.gpu
 
-B = 16
-T = 40
+CHUNKS = [(16, 40), (64, 100)]  # (rows per chunk, prompt tokens)
 
 
 def _shape(kind):
@@ -32,9 +32,10 @@ def _shape(kind):
     return E2BShape.real(n_layers=4, n_unshared=2, global_layers=(1, 3), vocab=4096)
 
 
+@pytest.mark.parametrize("B,T", CHUNKS)
 @pytest.mark.parametrize("kind", ["uniform", "real"])
 @pytest.mark.parametrize("start", [0, 600])
-def test_prefill_matches_sequential_forwards(ctx, kind, start):
+def test_prefill_matches_sequential_forwards(ctx, kind, start, B, T):
     s = _shape(kind)
     d = BatchDecoder(ctx, [0] * B, s, seed=31, reserve=start + T + 8, shared_pages=True, embed=True)
     d.fill_kv(seed=32)

@@ -387,6 +387,76 @@ def test_gate_up_digits_then_down(ctx, I):
         assert_close(y.download(np.float32), O.matmul(x, Wd, N, I, "q6k"), what=f"down over digits I={I}")
 
 
+NON_FINITE = [float("nan"), float("inf"), float("-inf")]
+
+
+def _non_finite_like_reference(got, ref, what):
+    """A non-finite input reaches every row, as in the reference's f32
+    matvec (shaders/matmul_quant.wgsl:38-47): NaN where the reference has
+    NaN, and NaN or the reference's signed infinity where it has one (the
+    input's 32-element sub-block carries it as a NaN scale, so an infinity
+    arrives as NaN; the norm that reads the result would turn it into NaN in
+    the reference as well)."""
+    assert not np.any(np.isfinite(ref)), f"{what}: the oracle has finite rows"
+    assert not np.any(np.isfinite(got)), f"{what}: {np.count_nonzero(np.isfinite(got))} finite rows"
+    assert np.all(np.isnan(got[np.isnan(ref)])), what
+    inf = np.isinf(got)
+    assert np.array_equal(got[inf], ref[inf]), what
+
+
+@pytest.mark.parametrize("wtype,M,N", [("q4k", 6144, 1536), ("q4k", 1536, 2048), ("q6k", 1536, 6144),
+                                       ("q6k", 8192, 1536)])
+@pytest.mark.parametrize("special", NON_FINITE)
+def test_matmul_quant_non_finite_input(ctx, wtype, M, N, special):
+    """The one-vector launches with a NaN / +Inf / -Inf activation element,
+    then a finite vector through the same buffers (nothing non-finite stays
+    behind)."""
+    nb = M * N // 256
+    W = O.gen_q4k(M + N + 5, nb) if wtype == "q4k" else O.gen_q6k(M + N + 5, nb)
+    x = O.gen_normal_f32(N + 1, N)
+    xb = x.copy()
+    xb[N // 3 + 5] = special
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = O.matmul(xb, W, M, N, wtype)
+    dW, dy = ctx.from_numpy(W), ctx.empty(M, np.float32)
+    dx = ctx.from_numpy(xb)
+    ctx.matmulQuant(dx, dW, dy, M, N, wtype)
+    _non_finite_like_reference(dy.download(np.float32), ref, f"{wtype} {M}x{N} x={special}")
+    dx.upload(x)
+    ctx.matmulQuant(dx, dW, dy, M, N, wtype)
+    assert_close(dy.download(np.float32), O.matmul(x, W, M, N, wtype), what=f"{wtype} {M}x{N} after {special}")
+
+
+@pytest.mark.parametrize("special", NON_FINITE)
+def test_norm_prologue_and_digit_hand_off_non_finite(ctx, special):
+    """The rmsNorm-prologue matvec and the FFN whose GELU product reaches the
+    Q6_K down launch as digits: one non-finite element of the input makes
+    every output row NaN, as the reference's rms_norm (mean of squares
+    non-finite) does before its matvec."""
+    N, M, I = 1536, 2048, 6144
+    W = O.gen_q4k(50, M * N // 256)
+    nw = O.gen_normal_f16(51, N, 1.0, 0.1)
+    x = O.gen_normal_f32(52, N, 0.0, 2.0)
+    x[700] = special
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = O.matmul(O.rms_norm(x, nw, 1e-6), W, M, N, "q4k")
+    y = ctx.empty(M, np.float32)
+    ctx.rmsNormMatmul_q4k(ctx.from_numpy(x), ctx.from_numpy(nw), ctx.from_numpy(W), y, M, N, 1e-6)
+    got = y.download(np.float32)
+    assert np.all(np.isnan(got)) and np.all(np.isnan(ref)), special
+    Wg, Wu, Wd = O.gen_q4k(53, I * N // 256), O.gen_q4k(54, I * N // 256), O.gen_q6k(55, N * I // 256)
+    res = O.gen_normal_f32(56, N)
+    w_post, w_pre = O.gen_normal_f16(57, N, 1.0, 0.1), O.gen_normal_f16(58, N, 1.0, 0.1)
+    args = [ctx.from_numpy(a) for a in (x, w_post, res, w_pre, Wg, Wu)]
+    act = ctx.empty(I, np.float32)
+    dig = ctx.zeros(ctx.digits_bytes(I), np.uint8)
+    ctx.normAddGateUpGeluDigits_q4k(*args, ctx.empty(N, np.float32), act, dig, I, N, 1e-6)
+    down = ctx.empty(N, np.float32)
+    ctx.matmulQuantDigits_q6k(dig, ctx.from_numpy(Wd), down, N, I)
+    assert np.all(np.isnan(act.download(np.float32))), special
+    assert np.all(np.isnan(down.download(np.float32))), special
+
+
 def test_digit_entries_reject_bad_shapes(ctx):
     """Shapes the digit hand-off does not cover fail with an error, not a launch."""
     N, I = 2048, 6144

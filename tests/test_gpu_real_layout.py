@@ -145,6 +145,7 @@ def test_embedding_token_feedback_graph(ctx):
     kcs = [L.k_cache.download(np.uint16) for L in d.layers]
     vcs = [L.v_cache.download(np.uint16) for L in d.layers]
     g = d.capture_fused()
+    assert ctx.graph_kernel_nodes(g) == d.launches_per_step_fused()
     try:
         x_prev = None
         tok = T0

@@ -6,7 +6,7 @@ import pytest
 
 import oracle as O
 from decode_oracle import HostModel
-from g4hip.decoder import Decoder, E2BShape
+from g4hip.decoder import Decoder, E2BShape, qkv_groups
 from gpu_util import assert_close, bits_equal
 
 pytestmark = pytest.mark.gpu
@@ -109,6 +109,7 @@ def test_graph_replay_matches_eager(ctx, dec):
     restore(dec, snap)
     dec.set_position(POS)
     g = dec.capture_fused()
+    assert ctx.graph_kernel_nodes(g) == dec.launches_per_step_fused()
     try:
         for i in range(3):
             ctx.graph_launch(g)
@@ -122,3 +123,50 @@ def test_graph_replay_matches_eager(ctx, dec):
     finally:
         ctx.graph_destroy(g)
         restore(dec, snap)
+
+
+# Layer format mixes of the fused step (wtypes(il, name)): Q4_K q/k/v in one
+# launch with the attention block over an FFN that is not one gate/up launch
+# (an f16 gate; a Q6_K up), and q/k/v split over two formats.
+MIXES = {
+    "qkv_one_launch_f16_gate": lambda il, nm: "f16" if nm == "wgate" else ("q6k" if nm == "wdown" else "q4k"),
+    "qkv_one_launch_q6k_up": lambda il, nm: "q6k" if nm in ("wup", "wdown") else "q4k",
+    "q6k_v": lambda il, nm: "q6k" if nm in ("wv", "wdown") else "q4k",
+}
+
+
+@pytest.mark.parametrize("mix", sorted(MIXES))
+def test_fused_step_layer_mixes(ctx, mix):
+    """The fused step of each mix against the oracle (hidden, logits, token),
+    and the kernel launches of its captured graph against
+    launches_per_step_fused."""
+    shape = E2BShape(n_layers=N_LAYERS, global_layers=(1,), vocab=16384)
+    d = Decoder(ctx, shape, max_seq=MAX_SEQ, seed=5, wtypes=MIXES[mix])
+    d.fill_kv(POS, seed=6)
+    ctx.sync()
+    # layer 0 (local, its own K/V) takes the one q/k/v + attention launch unless v is Q6_K
+    one = (d._qkv_fused(qkv_groups(d.layers[0], [0, 0, 0], [0, 0, 0]))
+           and ctx.qkv_attn_single_launch(d.attn_params[0], shape.hidden, 3))
+    assert one == (mix != "q6k_v"), mix
+    snap = snapshot(d)
+    kcs, vcs = [k.copy() for k in snap[1]], [v.copy() for v in snap[2]]
+    x_ref, logits_ref = oracle_step(d, snap[0], kcs, vcs, POS)
+    d.set_position(POS)
+    d.step_fused()
+    ctx.sync()
+    print(f"[step mix] {mix}: hidden rel-L2 {O.rel_l2(host(d.hidden, np.float32), x_ref):.2e}", flush=True)
+    assert_close(host(d.hidden, np.float32), x_ref, what=f"{mix} hidden")
+    lg = host(d.logits, np.float32)
+    assert_close(lg, logits_ref, what=f"{mix} logits")
+    check_token(d, lg, f"{mix} token")
+    restore(d, snap)
+    d.set_position(POS)
+    g = d.capture_fused()
+    try:
+        assert ctx.graph_kernel_nodes(g) == d.launches_per_step_fused(), mix
+        ctx.graph_launch(g)
+        ctx.sync()
+        assert_close(host(d.hidden, np.float32), x_ref, what=f"{mix} hidden (graph)")
+    finally:
+        ctx.graph_destroy(g)
+    del d
