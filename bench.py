@@ -62,11 +62,15 @@ def kernel_census(ctx, dec: Decoder, reps: int):
     through HBM as in a real step, and no host launch overhead is timed),
     replayed `reps` times between HIP events on the library's stream.
     Algorithmic bytes: weights + activations read/written by one launch.
-    The attention is timed as the step runs it (RoPE cos/sin from the
-    per-theta table) but without the L2 warming the step's attention
-    launches also do (the warming reads the next matvecs' weights, which
-    those matvecs' own launches are charged for), and the matvecs with cold
-    weights."""
+    `qkv_attn` is the launch every layer of the step issues: the q/k/v
+    matvec with its norm prologue and the attention block (RoPE cos/sin from
+    the per-theta table, the new K/V row stored) in one launch, with the L2
+    warming of the step (the warming's reads are the next matvecs' weights,
+    which those matvecs' own launches are charged for, so they are not in
+    its algorithmic bytes). `qkv_normadd_matvec` and `attn_fused` time the
+    two halves as separate launches (the two-launch form the step falls
+    back to for other shapes): reported, not issued by this step
+    (per_step 0). The matvecs run with cold weights."""
     s, c = dec.s, ctx
     dec.set_position(START_POS)
     Ls = dec.layers
@@ -79,32 +83,39 @@ def kernel_census(ctx, dec: Decoder, reps: int):
     kv_avg = ((nl - n_glob) * L_loc + n_glob * L_glob) * KV * 2 * 2 // nl  # f16 K + V rows read
     dig = ctx.digits_bytes(I)  # the GELU product as the down launch's digit block
 
+    qkv_bytes = q4(Q + 2 * KV, H) + 5 * H * 4 + (Q + 2 * KV) * 4
     kinds = {
-        # name: (per-layer body, launches per body, algorithmic bytes per launch)
+        # name: (per-layer body, launches per step of this kind, algorithmic bytes per launch)
+        "qkv_attn": (
+            lambda il, L: c.qkvAttnDecodeFusedWarm(
+                dec.down, L.post_ffn_norm, dec.hidden2, None, L.attn_norm, dec.hidden, [L.wq, L.wk, L.wv],
+                [dec.q, dec.k, dec.v], H, s.eps, L.q_norm, L.k_norm, dec.rope_freqs, L.k_cache, L.v_cache, dec.attn,
+                dec.attn_params[il], dec.attn_ws, dec.pos, dec.warm[il], dec.rope_cs[s.is_global(il)], dec.rope_rows),
+            nl, qkv_bytes + kv_avg + 2 * KV * 2 + Q * 4),
         "qkv_normadd_matvec": (
             lambda il, L: c.normAddMatmulSegments(
                 "q4k", dec.down, L.post_ffn_norm, dec.hidden2, L.attn_norm, dec.hidden, [L.wq, L.wk, L.wv],
                 [dec.q, dec.k, dec.v], [Q, KV, KV], H, s.eps),
-            1, q4(Q + 2 * KV, H) + 5 * H * 4 + (Q + 2 * KV) * 4),
+            0, qkv_bytes),
         "attn_fused": (
             lambda il, L: c.attnDecodeFusedWarm(dec.q, dec.k, dec.v, L.q_norm, L.k_norm, dec.rope_freqs, L.k_cache,
                                                 L.v_cache, dec.attn, dec.attn_params[il], dec.attn_ws, dec.pos, [],
                                                 dec.rope_cs[s.is_global(il)], dec.rope_rows),
-            1, kv_avg + (Q + 2 * KV) * 4 + Q * 4),
+            0, kv_avg + (Q + 2 * KV) * 4 + 2 * KV * 2 + Q * 4),
         "o_matvec": (
             lambda il, L: c.matmulQuant(dec.attn, L.wo, dec.o, H, Q),
-            1, q4(H, Q) + Q * 4 + H * 4),
+            nl, q4(H, Q) + Q * 4 + H * 4),
         "gateup_gelu": (
             lambda il, L: c.normAddGateUpGeluDigits_q4k(dec.o, L.post_attn_norm, dec.hidden, L.pre_ffn_norm,
                                                         L.wgate, L.wup, dec.hidden2, dec.act, dec.act_digits, I, H,
                                                         s.eps),
-            1, 2 * q4(I, H) + 4 * H * 4 + I * 4 + dig),
+            nl, 2 * q4(I, H) + 4 * H * 4 + I * 4 + dig),
         "down_matvec_q6k": (
             lambda il, L: c.matmulQuantDigits_q6k(dec.act_digits, L.wdown, dec.down, H, I),
-            1, q6(H, I) + dig + H * 4),
+            nl, q6(H, I) + dig + H * 4),
     }
     out = {}
-    for name, (body, launches, nbytes) in kinds.items():
+    for name, (body, per_step, nbytes) in kinds.items():
         ctx.graph_begin()
         try:
             for il, L in enumerate(Ls):
@@ -113,7 +124,7 @@ def kernel_census(ctx, dec: Decoder, reps: int):
             g = ctx.graph_end()
         us = time_launches(ctx, lambda _i=0: ctx.graph_launch(g), reps) * 1e3 / nl
         ctx.graph_destroy(g)
-        out[name] = {"us": us, "per_step": nl, "bytes": nbytes, "gbps": nbytes / (us * 1e-6) / 1e9}
+        out[name] = {"us": us, "per_step": per_step, "bytes": nbytes, "gbps": nbytes / (us * 1e-6) / 1e9}
     # LM head with the final norm-add, softcap and the argmax candidates,
     # then their reduction, as the step runs them (330 MB: larger than the
     # 256 MB last-level cache, so no rotation is needed)
@@ -835,9 +846,10 @@ def main():
     census = kernel_census(ctx, dec, args.census_reps)
     for k, v in census.items():
         log(f"  {k}: {v}")
-    # dominant kernel = largest time per step
+    # dominant kernel = the launch kind with the largest time per step among
+    # those the step issues (per_step > 0)
     per_step = {k: v["us"] * v["per_step"] for k, v in census.items()}
-    dom = max(per_step, key=lambda k: per_step[k])
+    dom = max((k for k in per_step if census[k]["per_step"] > 0), key=lambda k: per_step[k])
     bytes_launch, us_launch = census[dom]["bytes"], census[dom]["us"]
     achieved = bytes_launch / (us_launch * 1e-6) / 1e9
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
@@ -880,7 +892,9 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "q4k_gemv_config0": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in g0.items()},
-        "kernel_census_us": {k: round(per_step[k], 2) for k in per_step},
+        "kernel_census": {k: {"us_per_launch": round(v["us"], 3), "launches_per_step": v["per_step"],
+                              "us_per_step": round(per_step[k], 2), "bytes_per_launch": v["bytes"],
+                              "gbps": round(v["gbps"], 1)} for k, v in census.items()},
         "decode_from_position": positions,
         "real_e2b_layout": real,
         "node_fused_step": node_step,

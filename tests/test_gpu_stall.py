@@ -12,11 +12,13 @@ no matvec workgroups, so nothing is ever staged): every kernel still ends
 normally. Each test runs on a context of its own so that the sticky status
 cannot reach other tests.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
 import g4hip
-from g4hip._lib import G4Error
+from g4hip._lib import G4Error, lib
 from gpu_util import bits_equal
 from test_gpu_qkv_attn import H, HD, NQH, _setup
 
@@ -26,13 +28,22 @@ STALLED = -7
 POS, WINDOW, CAP = 700, 512, 1024
 
 
-def _call(ctx, host, dev, W, table, rope, p, regions, ws):
+def _prepare(ctx, host, dev, W, table, rope, p, regions, ws):
+    """Buffers of one call (uploaded now), and the launch, which enqueues only."""
     dk, dv = ctx.from_numpy(host["k"]), ctx.from_numpy(host["v"])
     q, k, v = (ctx.empty(n, np.float32) for n in (NQH * HD, HD, HD))
     h_out, out = ctx.empty(H, np.float32), ctx.empty(NQH * HD, np.float32)
     pdev = ctx.from_numpy(np.array([POS], np.uint32))
-    ctx.qkvAttnDecodeFusedWarm(dev["x"], dev["w1"], dev["res"], None, dev["w2"], h_out, W[:3], [q, k, v], H, 1e-6,
-                               dev["qn"], dev["kn"], table, dk, dv, out, p, ws, pdev, regions, rope, CAP)
+
+    def launch():
+        ctx.qkvAttnDecodeFusedWarm(dev["x"], dev["w1"], dev["res"], None, dev["w2"], h_out, W[:3], [q, k, v], H,
+                                   1e-6, dev["qn"], dev["kn"], table, dk, dv, out, p, ws, pdev, regions, rope, CAP)
+    return launch, out, dk, dv
+
+
+def _call(ctx, *S):
+    launch, out, dk, dv = _prepare(ctx, *S)
+    launch()
     return out, dk, dv
 
 
@@ -90,20 +101,33 @@ def test_expired_hand_off_is_reported_and_poisons(own_ctx):
 
 
 def test_expired_hand_off_is_reported_by_events(own_ctx):
+    """An event recorded behind the stalled launch reports the stall once it
+    completes (g4_event_wait, g4_event_query). A 2 GiB fill ahead of the
+    launch keeps the stream busy well past the host's record call, so the
+    record itself precedes the stall."""
     ctx = own_ctx
     S = _setup(ctx, 12, POS, WINDOW, CAP)
     ws = ctx.zeros(ctx.attn_fused_workspace_bytes(S[5]), np.uint8)
+    busy = ctx.empty(1 << 29, np.float32)
+    launch, out, _, _ = _prepare(ctx, *S, ws)
+    ctx.sync()
     ctx.test_stage_wait(64, True)
-    _call(ctx, *S, ws)
-    ev = ctx.record()
-    from g4hip._lib import lib
-
-    rc = lib().g4_event_wait(ev)
-    assert rc == STALLED
-    ctx.destroy_event(ev)
+    ctx.fill_normal_f32(busy, 1 << 29, 3, 0.0, 1.0)
+    launch()
+    ev = ctypes.c_void_p()
+    rc = lib().g4_event_record(ctx.h, ctypes.byref(ev))
+    if rc == 0:
+        assert lib().g4_event_wait(ev) == STALLED
+        assert lib().g4_event_query(ev) == STALLED
+        ctx.destroy_event(ev)
+    else:  # the stream drained before the record: the record reports it
+        assert rc == STALLED
+    print(f"[stall] reported by {'g4_event_wait' if rc == 0 else 'g4_event_record'}", flush=True)
     ctx.clear_stall()
+    assert np.all(np.isnan(out.download(np.float32)))
     ctx.test_stage_wait(0, False)
     ctx.sync()
+    busy.free()
     for w in S[2]:
         w.free()
 
