@@ -667,13 +667,30 @@ struct MvXA {
   static constexpr size_t END = RED8 + 256;
 };
 
+// A one-matrix workgroup that walks several tiles (the LM head) reads them
+// straight into LDS (global -> LDS loads, no registers) into a ring of
+// kRing tile buffers, so that two tiles are in flight while the third is
+// multiplied. Lane l of wave w writes the 16-byte chunk 64 w + l of each
+// round of NTH chunks, so a buffer spans whole waves' 1024-byte pieces.
+constexpr int kRing = 3;
+template <int QT, int BPR, int NWV>
+struct MvRing {
+  using T = MvTile<QT, BPR, NWV>;
+  static constexpr uint32_t CH = (T::TB + 15) / 16;               // 16-byte chunks of a tile
+  static constexpr uint32_t BUF = (CH + 63) / 64 * 1024;          // bytes of one ring buffer
+  static constexpr int LPT = T::LPT;                              // rounds of loads per tile
+  static constexpr uint32_t LAST = (uint32_t)(LPT - 1) * 64 * NWV;  // first chunk of the last round
+};
+
 // A workgroup with one tile reads its weight units straight into registers;
-// one that walks several tiles stages them through LDS (`staged`).
+// one that walks several tiles stages them through LDS (`staged`): the
+// ring of MvRing buffers for one matrix, one register-staged tile per
+// matrix for a pair.
 template <int QT, int BPR, int NWV, int PRO, int NMAT>
 __host__ __device__ constexpr size_t mv_lds_bytes(bool staged) {
   using T = MvTile<QT, BPR, NWV>;
   return align16(MvXA<BPR, PRO>::END) + NMAT * align16((size_t)T::TR * T::RS * 4) +
-         (staged ? NMAT * (size_t)T::LDS_T : 0);
+         (staged ? (NMAT == 1 ? kRing * (size_t)MvRing<QT, BPR, NWV>::BUF : NMAT * (size_t)T::LDS_T) : 0);
 }
 
 template <class T, int NTH>
@@ -690,6 +707,48 @@ __device__ __forceinline__ void mv_stage_store(uint8_t* lds, uint32_t nbytes, co
     const uint32_t off = (uint32_t)(i * NTH + threadIdx.x) * 16u;
     if (off < T::LDS_T) *(u32x4a*)(lds + chunk_off(off, nbytes)) = st.r[i];
   }
+}
+
+// Issues the global -> LDS loads of a tile of nbytes at src into the ring
+// buffer at buf: round i's chunk 64 w + l of wave w, lane l, goes to byte
+// 16 (i NTH + 64 w + l) of the buffer; a chunk past the tile (lanes of the
+// last round, or a short last tile) reads the tile's last 16 bytes, which
+// land past the bytes any row reads. A wave issues a round only if some of
+// its chunks are in the full tile, so it issues the same count for every
+// tile (mv_ring_rounds).
+template <int QT, int BPR, int NWV>
+__device__ __forceinline__ void mv_ring_load(const uint8_t* src, uint32_t nbytes, uint8_t* buf, int w, int l) {
+  using R = MvRing<QT, BPR, NWV>;
+  constexpr int NTH = 64 * NWV;
+#pragma unroll
+  for (int i = 0; i < R::LPT; ++i) {
+    const uint32_t c0 = (uint32_t)(i * NTH + 64 * w);  // (uniform per wave)
+    if (i == R::LPT - 1 && c0 >= R::CH) break;
+    const uint32_t off = chunk_off((c0 + (uint32_t)l) * 16u, nbytes);
+    __builtin_amdgcn_global_load_lds((const void*)(src + off),
+                                     (__attribute__((address_space(3))) void*)(buf + 16u * c0), 16, 0, 0);
+  }
+}
+// Loads one tile issues in wave w: R::LPT, or one less where the last
+// round has no chunk of the tile for it.
+template <int QT, int BPR, int NWV>
+__device__ __forceinline__ bool mv_ring_short(int w) {
+  using R = MvRing<QT, BPR, NWV>;
+  return R::LAST + 64u * (uint32_t)w >= R::CH;
+}
+// Workgroup barrier of the LDS ring: waits for this wave's LDS operations
+// only. lds_barrier's release fence on LDS also waits for every global ->
+// LDS load in flight (they write LDS), which would drain the two tiles the
+// ring keeps in flight; the loads of the tile about to be read are waited
+// for explicitly (wait_vmcnt) before this barrier. The memory clobber keeps
+// the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// s_waitcnt for vector memory count <= n (the other counters left free).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 template <int QT, int BPR, int NWV>
@@ -1315,6 +1374,18 @@ __device__ __forceinline__ void mv_topk_partial(const g4d::Cand* tkt, const Gemv
 // tiles per CU, the LM head); the other instances hold the one-tile path
 // only. (Bounding the staged instance to two 12-wave workgroups per CU,
 // 80 VGPRs, spilled the tile loop to scratch: 199 us instead of 82.)
+// One ring step: the loads of tile t + 2 into `nxt` (when `more`), then
+// this thread's unit product of tile t from `cur`. The two buffers are
+// different ring slots, which the restrict qualifiers tell the compiler, so
+// it adds no wait for the new loads before the products' LDS reads (the
+// caller waits for tile t's own loads explicitly).
+template <int QT, int BPR, int NWV>
+__device__ __forceinline__ void mv_ring_step(bool more, const uint8_t* src, uint32_t nbytes, uint8_t* __restrict__ nxt,
+                                             const uint8_t* __restrict__ cur, const MvUnit<QT>& X,
+                                             float* __restrict__ red, int w, int l, int g) {
+  if (more) mv_ring_load<QT, BPR, NWV>(src, nbytes, nxt, w, l);
+  *red = mv_unit_dot<QT>(X, cur, g);
+}
 template <int QT, int BPR, int NWV, int PRO, int NMAT, bool STAGED, bool DEV = false>
 __device__ __forceinline__ void mv_body(const GemvSegs& segs, const uint8_t* w_up, const ProArgs& pa, float cap,
                                         uint8_t* smem) {
@@ -1408,9 +1479,50 @@ __device__ __forceinline__ void mv_body(const GemvSegs& segs, const uint8_t* w_u
     if (tkt) mv_topk_partial<NTH>(tkt, segs, blockIdx.x - sg.wg_begin);
     return;
   }
-  if constexpr (STAGED && PRO != 3) {
-    // several tiles: coalesced loads of the next tile into registers while
-    // this one is multiplied out of LDS
+  if constexpr (STAGED && PRO != 3 && NMAT == 1) {
+    // several tiles of one matrix: a ring of kRing LDS buffers filled by
+    // global -> LDS loads, tiles t + 1 and t + 2 in flight while tile t is
+    // multiplied. A wave's loads complete in issue order, so once it has
+    // at most one tile's loads outstanding (vmcnt <= its per-tile count;
+    // the row stores after them only make the wait stricter) its share of
+    // tile t is in LDS; the barrier that follows makes the whole tile
+    // visible. Buffer (t + 2) % kRing held tile t - 1, whose products every
+    // wave finished before the barrier ahead of the last reduction.
+    using R = MvRing<QT, BPR, NWV>;
+    uint8_t* ring = smem + align16(MvXA<BPR, PRO>::END) + align16((size_t)T::TR * T::RS * 4);
+    const int w = tid >> 6, l = tid & 63;
+    const bool short_wave = mv_ring_short<QT, BPR, NWV>(w);
+    mv_ring_load<QT, BPR, NWV>(W[0] + (size_t)tb * T::TB, mv_tile_bytes<QT, BPR, NWV>(sg.M, tb), ring, w, l);
+    if (tb + 1 < te)
+      mv_ring_load<QT, BPR, NWV>(W[0] + (size_t)(tb + 1) * T::TB, mv_tile_bytes<QT, BPR, NWV>(sg.M, tb + 1),
+                                 ring + R::BUF, w, l);
+    __builtin_amdgcn_sched_barrier(0);  // every weight load is issued before the activations are used
+    mv_pro_finish<BPR, NWV, PRO>(P, smem, pa);
+    MvUnit<QT> X;
+    mv_unit_load<QT, BPR>(X, smem, u);
+    g4d::Cand best{-1e30f, 0u};
+    uint32_t cur = 0;  // ring buffer of tile t
+    for (uint32_t t = tb; t < te; ++t) {
+      if (t + 1 < te) {  // (uniform) tile t + 1 stays in flight
+        if (short_wave) wait_vmcnt<R::LPT - 1>();
+        else wait_vmcnt<R::LPT>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      ring_barrier();  // tile t in LDS for every wave; tile t - 1 reduced
+      const uint32_t nxt = cur >= kRing - 2 ? cur + 2 - kRing : cur + 2;
+      mv_ring_step<QT, BPR, NWV>(t + 2 < te, W[0] + (size_t)(t + 2) * T::TB, mv_tile_bytes<QT, BPR, NWV>(sg.M, t + 2),
+                                 ring + nxt * R::BUF, ring + cur * R::BUF + slot * T::RB + (u >> 2) * T::BYTES, X,
+                                 red + slot * T::RS + u, w, l, u & 3);
+      ring_barrier();
+      mv_reduce_store<T, NTH, NMAT>(red, sg, t, tid, cap, segs.amx != nullptr, best, d8, tkt);
+      cur = cur + 1 == kRing ? 0u : cur + 1;
+    }
+    if (segs.amx) mv_argmax_partial<NWV>(best, (g4d::Cand*)(smem + MvXA<BPR, PRO>::RED8), segs.amx + blockIdx.x);
+    if (tkt) mv_topk_partial<NTH>(tkt, segs, blockIdx.x - sg.wg_begin);
+  } else if constexpr (STAGED && PRO != 3) {
+    // several tiles of a pair: coalesced loads of the next tile into
+    // registers while this one is multiplied out of LDS
     uint8_t* tl = smem + align16(MvXA<BPR, PRO>::END) + NMAT * align16((size_t)T::TR * T::RS * 4);
     // (Two tiles in flight per workgroup, in two register sets, measured
     // 85 us for the LM head against 82 with one.)

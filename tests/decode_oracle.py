@@ -82,7 +82,7 @@ class HostModel:
         row = O.dequant_q5k(blocks).astype(np.float16).view(np.uint16)
         return O.ple_project(x0, self.ple["model_proj"], self.ple["proj_norm"], row, L, D, s.eps)
 
-    def step(self, hidden, kcs, vcs, pos, gelu=O.gelu_mul, row_toward_zero=False, token=0):
+    def step(self, hidden, kcs, vcs, pos, gelu=O.gelu_mul, row_toward_zero=False, token=0, rows=None):
         """Decode position `pos`: kcs/vcs are this sequence's dense f16 caches
         (one per layer, >= pos + 1 rows; a consumer layer's entry is not
         used), updated in place. Returns the new hidden state and the
@@ -90,7 +90,8 @@ class HostModel:
         stores the new K/V rows rounded toward zero instead of to nearest (a
         one-ulp change of the f16 cache, to measure how much the step depends
         on the cache's resolution). `token` picks the per-layer-embedding
-        table row."""
+        table row. `rows`, a dict, receives each producer layer's new K and V
+        rows in f32, before the cache's f16 rounding."""
         s, x = self.s, hidden.copy()
         pin = self.ple_inputs(x, token) if self.ple is not None else None
         for il, W in enumerate(self.layers):
@@ -110,6 +111,8 @@ class HostModel:
                 k = O.fused_per_head_norm_rope(k, W["k_norm"], s.n_kv_heads, hd, s.eps, pos, theta, int(glob),
                                                self.table)
                 O.kv_cache_store_f16(k, v, kcs[il], vcs[il], s.n_kv_heads, hd, pos)
+                if rows is not None:
+                    rows[il] = (np.asarray(k, np.float32).copy(), np.asarray(v, np.float32).copy())
                 if row_toward_zero:
                     row = slice(pos * KV, (pos + 1) * KV)
                     kcs[il][row] = f16_toward_zero(k)
