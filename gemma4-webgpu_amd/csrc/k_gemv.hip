@@ -131,7 +131,13 @@ __device__ __forceinline__ void digits4(const XView& xv, int vec, uint32_t e, fl
 // 2 = h = residual + o * w1 / rms(o); x = h * w2 / rms(h)
 // (shaders/fused_norm_add.wgsl then shaders/rms_norm.wgsl); h is written to
 // h_out by workgroup 0 when h_out is non-null; 3 (one-vector matvec, Q6_K)
-// = x already digitised by the launch that produced it (MvD8 block at x).
+// = x already digitised by the launch that produced it (MvD8 block at x);
+// 4 (one-vector matvec) = mode 2 with o given as kHeadParts vectors of K
+// (the o projection's per-head shares, [kHeadParts][K] at x), added in
+// order.
+constexpr int kHeadParts = 8;  // prologue mode 4: shares of o, one per query head
+__host__ __device__ constexpr bool pro_add(int pro) { return pro == 2 || pro == 4; }  // residual-add + norm
+
 struct ProArgs {
   const float* x;         // [NV][K] (mode 2: o)
   const uint16_t* w1;
@@ -827,9 +833,9 @@ struct MvPro {
   static constexpr int PTH = 64 * PW;
   static constexpr int XP = (K + 4 * PTH - 1) / (4 * PTH);
   float4 x[XP];
-  float4 r[PRO == 2 ? XP : 1];
+  float4 r[pro_add(PRO) ? XP : 1];
   uint2 w1[PRO >= 1 ? XP : 1];
-  uint2 w2[PRO == 2 ? XP : 1];
+  uint2 w2[pro_add(PRO) ? XP : 1];
   // Every workgroup reads the whole vector; starting each one at a different
   // sub-block spreads these broadcast reads over the L2 channels instead of
   // all workgroups asking for the same lines at the same moment.
@@ -854,9 +860,20 @@ __device__ __forceinline__ void mv_pro_load(MvPro<BPR, NWV, PRO>& P, const ProAr
 #pragma unroll
   for (int p = 0; p < PP::XP; ++p) {
     const int fc = PP::live(p) ? PP::elem(p) : 0;
-    P.x[p] = *(const float4*)(a.x + fc);
+    if constexpr (PRO == 4) {
+      float4 part[kHeadParts];
+#pragma unroll
+      for (int i = 0; i < kHeadParts; ++i) part[i] = *(const float4*)(a.x + (size_t)i * PP::K + fc);
+      float4 v = part[0];
+#pragma unroll
+      for (int i = 1; i < kHeadParts; ++i) v = make_float4(v.x + part[i].x, v.y + part[i].y, v.z + part[i].z,
+                                                           v.w + part[i].w);
+      P.x[p] = v;
+    } else {
+      P.x[p] = *(const float4*)(a.x + fc);
+    }
     if constexpr (PRO >= 1) P.w1[p] = *(const uint2*)(a.w1 + fc);
-    if constexpr (PRO == 2) {
+    if constexpr (pro_add(PRO)) {
       P.r[p] = *(const float4*)(a.residual + fc);
       P.w2[p] = *(const uint2*)(a.w2 + fc);
     }
@@ -952,7 +969,7 @@ __device__ __forceinline__ void mv_pro_finish(MvPro<BPR, NWV, PRO>& P, uint8_t* 
 #pragma unroll
       for (int p = 0; p < PP::XP; ++p) P.x[p] = mul_w(P.x[p], P.w1[p], inv1);
     }
-  } else if constexpr (PRO == 2) {
+  } else if constexpr (pro_add(PRO)) {
     // h = r + t, t = (o * w1) * inv1. Both norms come out of one block
     // reduction: sum(o^2), and sum(h^2) expanded as
     // sum(r^2) + 2 inv1 sum(r (o w1)) + inv1^2 sum((o w1)^2).
@@ -1989,7 +2006,7 @@ int mv_launch(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
 // matvec workgroups come first in the grid and wait on nothing: in-order
 // dispatch lets them finish whatever the residency, and the wait is bounded.
 constexpr int kQkvNwv = 6;  // workgroup width (waves): the wider of the two parts
-template <int PRO, int MNWV>
+template <int PRO, int MNWV, bool MERGE>
 __global__ __launch_bounds__(64 * kQkvNwv) void qkv_attn_kernel(GemvSegs segs, ProArgs pa, g4mqf::MqfArgs a,
                                                                  uint32_t nmv) {
   static_assert(MNWV <= kQkvNwv && 64 * kQkvNwv >= g4mqf::MQ_NT, "both parts fit the workgroup");
@@ -2000,7 +2017,95 @@ __global__ __launch_bounds__(64 * kQkvNwv) void qkv_attn_kernel(GemvSegs segs, P
     return;
   }
   if (threadIdx.x >= (unsigned)g4mqf::MQ_NT) return;  // (uniform per wave)
-  g4mqf::mqf_body<false, true>(a, blockIdx.x - nmv, 0u, blockIdx.x);
+  g4mqf::mqf_body<false, true, MERGE>(a, blockIdx.x - nmv, 0u, blockIdx.x);
+}
+
+// The attention's chunk merge and the o projection, split by head
+// (g4_attnHeadsMatmul_q4k). The q/k/v + attention launch without its merge
+// leaves per chunk c and head h the partial (m, l, o[256]): the chunk's
+// running maximum, its softmax denominator and its unnormalised output.
+// Workgroup (tile, h) merges head h over the live chunks (weights
+// exp(m_c - max), as the in-launch merger), digitises the head's 256
+// outputs exactly as the o matvec's prologue digitises those elements (one
+// scale per 32), multiplies them with super-block h of 32 rows of W_o and
+// writes out[h][row]: the head's share of o = sum_h out[h]. The next launch
+// (the gate/up prologue, PRO 4) adds the shares in head order. Workgroups
+// also clear the staged q/k/v the attention's merger used to clear.
+struct HeadsArgs {
+  const float* ws;       // chunk partials: m [nparts], l [nparts], o [nparts][256]
+  uint32_t nparts;       // max_chunks * 8 (one KV head)
+  uint32_t max_chunks, chunk;  // chunk length in positions
+  uint32_t window, cap;
+  const uint32_t* pos_dev;
+  const uint8_t* W;      // [M][nqh * 256] Q4_K
+  float* out;            // [nqh][M]
+  uint32_t M;
+  uint64_t* stage;       // staged q/k/v to clear
+  uint32_t nstage;
+};
+constexpr int kHeadsRows = 32;  // rows per workgroup: 4 units of 64 weights per row, 2 waves
+
+__global__ __launch_bounds__(4 * kHeadsRows) void attn_heads_kernel(HeadsArgs a) {
+  __shared__ __align__(16) uint8_t smem[align16(MvX<1>::END)];
+  const int tid = threadIdx.x, u = tid & 3, slot = tid >> 2;
+  const uint32_t h = blockIdx.y, nh = gridDim.y;
+  const uint32_t row = min(blockIdx.x * (uint32_t)kHeadsRows + (uint32_t)slot, a.M - 1);
+  // this unit's weights first: 48 bytes of super-block h of the row
+  const uint32_t rb = nh * 144u;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.W, (short)0, (int)(uint32_t)min((uint64_t)a.M * rb, (uint64_t)0xffffffffu), 0x00020000);
+  Q4Unit wu;
+  q4_unit_load<2>(wu, rs, row * rb + h * 144u, u);
+  // the staged q/k/v of the attention launch, cleared for the next one
+  {
+    const uint32_t lin = blockIdx.y * gridDim.x + blockIdx.x, nwg = gridDim.x * gridDim.y;
+    for (uint32_t i = lin * 4u * kHeadsRows + (uint32_t)tid; i < a.nstage; i += nwg * 4u * kHeadsRows)
+      a.stage[i] = 0ull;
+  }
+  if (tid < 64) {  // (uniform per wave) wave 0 merges and digitises the head
+    const uint32_t L = min(*a.pos_dev + 1, a.cap);
+    const uint32_t wstart = (a.window != 0 && L > a.window) ? L - a.window : 0;
+    const uint32_t nch = (L - wstart + a.chunk - 1) / a.chunk;
+    using PP = MvPro<1, 1, 0>;
+    PP P;
+    const int e = PP::elem(0);  // this lane's 4 outputs
+    // every chunk slot is read at a clamped index (a dead chunk's partial
+    // is stale) and weighted 0 past the live ones
+    float m[g4mqf::MQF_FAN], lv[g4mqf::MQF_FAN];
+    float4 o[g4mqf::MQF_FAN];
+#pragma unroll
+    for (uint32_t c = 0; c < g4mqf::MQF_FAN; ++c) {
+      const uint32_t pc = (min(c, nch - 1) * 8u + h);
+      m[c] = a.ws[pc];
+      lv[c] = a.ws[a.nparts + pc];
+      o[c] = *(const float4*)(a.ws + 2 * (size_t)a.nparts + (size_t)pc * 256 + e);
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (uint32_t c = 0; c < g4mqf::MQF_FAN; ++c) M = c < nch ? fmaxf(M, m[c]) : M;
+    float Ls = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (uint32_t c = 0; c < g4mqf::MQF_FAN; ++c) {
+      // a stalled chunk's +Inf maximum makes every weight NaN (0 * Inf or Inf - Inf)
+      const float wc = (c >= nch || m[c] == -INFINITY) ? 0.f : g4mqf::mq_exp(m[c] - M);
+      Ls += wc * lv[c];
+      acc.x += wc * o[c].x;
+      acc.y += wc * o[c].y;
+      acc.z += wc * o[c].z;
+      acc.w += wc * o[c].w;
+    }
+    const float li = Ls > 0.f ? 1.0f / Ls : 0.f;  // (NaN stays NaN through acc)
+    P.x[0] = make_float4(acc.x * li, acc.y * li, acc.z * li, acc.w * li);
+    mv_digitize<1, 1, 0>(P, smem);
+  }
+  lds_barrier();
+  MvUnit<0> X;
+  mv_unit_load<0, 1>(X, smem, u);
+  float v = q4_unit_dot(X, wu, u);
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  if (u == 0 && blockIdx.x * (uint32_t)kHeadsRows + (uint32_t)slot < a.M) a.out[(size_t)h * a.M + row] = v;
 }
 
 // workgroup widths in waves for a row of BPR super-blocks (slots must tile it)
@@ -2168,6 +2273,100 @@ MvShape mv_shape(const g4_ctx* ctx, uint32_t M, uint32_t bpr) {
   s.rep = ceil_div(t, 2u * (uint32_t)ctx->num_cus);  // as mv_launch
   s.wgs = ceil_div(t, s.rep);
   return s;
+}
+
+int qkv_attn(g4_ctx* ctx, const char* fn, bool merge, const float* x, const uint16_t* w1, const float* residual,
+                              const uint16_t* out_scale, const uint16_t* w2, float* h_out,
+                              const void* const* weights, float* const* outputs, int nseg, uint32_t N, float eps,
+                              const uint16_t* q_norm_w, const uint16_t* k_norm_w, const uint16_t* rope_freqs,
+                              uint16_t* k_cache, uint16_t* v_cache, float* output, g4_attn_fused_params p,
+                              void* workspace, size_t workspace_bytes, const uint32_t* position_dev,
+                              const g4_warm_region* regions, int nregions, const float* rope_cs,
+                              uint32_t rope_rows) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(nseg == 1 || nseg == 3, "%s: nseg must be 1 (q) or 3 (q, k, v)", fn);
+  G4_REQUIRE(weights && outputs, "%s: null buffer", fn);
+  const uint32_t rows[3] = {p.num_q_heads * p.head_dim, p.num_kv_heads * p.head_dim, p.num_kv_heads * p.head_dim};
+  const float* q_raw = outputs[0];
+  const float* k_raw = nseg == 3 ? outputs[1] : nullptr;
+  const float* v_raw = nseg == 3 ? outputs[2] : nullptr;
+  int rc = g4mqf::mqf_check(ctx, fn, q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs,
+                            k_cache, v_cache, output, p, workspace, position_dev, regions, nregions, rope_cs,
+                            rope_rows);
+  if (rc) return rc;
+  // the matvec's own checks (g4_normAddScaleMatmulSegments)
+  G4_REQUIRE(x && w1, "%s: null buffer", fn);
+  G4_REQUIRE(!out_scale || residual, "%s: out_scale needs the residual form", fn);
+  G4_REQUIRE(!residual == !w2, "%s: residual and w2 go together", fn);
+  G4_REQUIRE(N == 1536 || N == 2048, "%s: N=%u unsupported (1536 or 2048)", fn, N);
+  G4_REQUIRE(((uintptr_t)x & 15) == 0 && (!residual || ((uintptr_t)residual & 15) == 0) &&
+                 (!h_out || ((uintptr_t)h_out & 15) == 0),
+             "%s: activations must be 16-byte aligned", fn);
+  G4_REQUIRE(((uintptr_t)w1 & 7) == 0 && ((uintptr_t)w2 & 7) == 0,
+             "%s: norm weights must be 8-byte aligned", fn);
+  for (int i = 0; i < nseg; ++i) {
+    G4_REQUIRE(weights[i] && outputs[i], "%s: segment %d empty", fn, i);
+    rc = check_w(fn, 0, weights[i]);
+    if (rc) return rc;
+  }
+  // the one-launch form: q, k and v (a layer reading its producer's cache
+  // projects q only, over 256 workgroups of 3 waves that would leave no CU
+  // to the attention or its L2 warming: it keeps the two launches), Q4_K
+  // rows of 1536 at the width the matvec's own launch takes, one KV head, a
+  // window merged in the
+  // launch, q/k/v staged in the workspace (at most kMaxStage values)
+  GemvSegs sg{};
+  for (int i = 0; i < nseg; ++i) sg.s[i] = GemvSeg{(const uint8_t*)weights[i], outputs[i], rows[i], 0};
+  const int mnwv = mv_pick(6, sg.s, nseg);
+  const uint32_t tr = 16u * (uint32_t)mnwv / 6u;  // rows per tile
+  uint32_t nmv = 0;
+  for (int i = 0; i < nseg; ++i) {
+    sg.s[i].wg_begin = nmv;
+    nmv += ceil_div(rows[i], tr);
+  }
+  bool applies = false;
+  g4mqf::MqfLaunch L{};
+  if (N == 1536 && mnwv == 6 && nseg == 3 && p.num_kv_heads == 1 && rows[0] + 2 * rows[1] <= g4mqf::kMaxStage) {
+    rc = g4mqf::mqf_prepare(ctx, q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs, k_cache, v_cache, output, p,
+                            workspace, workspace_bytes, position_dev, regions, nregions, rope_cs, nmv, applies, L);
+    if (rc) return rc;
+    applies = applies && !L.partials;
+  }
+  if (!applies) {  // two launches, the same results
+    if (!merge)
+      return g4::set_error(G4_ERR_UNSUPPORTED,
+                           "%s: the shape does not take the one q/k/v + attention launch with its merge left out", fn);
+    rc = g4_normAddScaleMatmulSegments(ctx, 0, x, w1, residual, out_scale, w2, h_out, weights, outputs, rows, nseg,
+                                       N, eps, 0.f);
+    if (rc) return rc;
+    return g4_attnDecodeFusedWarm(ctx, q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs, k_cache, v_cache,
+                                  output, p, workspace, workspace_bytes, position_dev, regions, nregions, rope_cs,
+                                  rope_rows);
+  }
+  sg.n = nseg;
+  sg.rep = 1;
+  // staged q/k/v: q at 0, k at nqh * hd, v at (nqh + nkh) * hd
+  L.m.nstage = rows[0] + 2 * rows[1];
+  for (int i = 0; i < nseg; ++i) sg.s[i].stage = L.m.stage + (i == 0 ? 0 : rows[0] + (size_t)(i - 1) * rows[1]);
+  const ProArgs pa{x, w1, residual, w2, h_out, eps, out_scale};
+  // g4_test_stage_wait can leave the matvec workgroups out (nothing is
+  // staged, so every attention workgroup's bounded wait expires)
+  const uint32_t nmv_run = ctx->test_skip_matvec ? 0u : nmv;
+  const dim3 grid(nmv_run + L.m.max_chunks + L.m.nwarm), block(64 * kQkvNwv);
+  auto launch = [&](auto kern, size_t lds) {
+    int r = claim_lds((const void*)kern, ctx, lds);
+    if (r) return r;
+    hipLaunchKernelGGL(kern, grid, block, lds, ctx->stream, sg, pa, L.m, nmv_run);
+    G4_LAUNCHED(ctx, "qkv_attn_fused");
+    return G4_OK;
+  };
+  // (the one launch takes 6-wave matvec workgroups: mnwv == 6 above)
+  if (merge) {
+    if (residual) return launch(qkv_attn_kernel<2, 6, true>, mv_lds_bytes<0, 6, 6, 2, 1>(false));
+    return launch(qkv_attn_kernel<1, 6, true>, mv_lds_bytes<0, 6, 6, 1, 1>(false));
+  }
+  if (residual) return launch(qkv_attn_kernel<2, 6, false>, mv_lds_bytes<0, 6, 6, 2, 1>(false));
+  return launch(qkv_attn_kernel<1, 6, false>, mv_lds_bytes<0, 6, 6, 1, 1>(false));
 }
 
 }  // namespace
@@ -2467,83 +2666,80 @@ int g4_qkvAttnDecodeFusedWarm(g4_ctx* ctx, const float* x, const uint16_t* w1, c
                               void* workspace, size_t workspace_bytes, const uint32_t* position_dev,
                               const g4_warm_region* regions, int nregions, const float* rope_cs,
                               uint32_t rope_rows) {
+  return qkv_attn(ctx, __func__, true, x, w1, residual, out_scale, w2, h_out, weights, outputs, nseg, N, eps, q_norm_w,
+                  k_norm_w, rope_freqs, k_cache, v_cache, output, p, workspace, workspace_bytes, position_dev, regions,
+                  nregions, rope_cs, rope_rows);
+}
+
+int g4_qkvAttnDecodePartials(g4_ctx* ctx, const float* x, const uint16_t* w1, const float* residual,
+                             const uint16_t* out_scale, const uint16_t* w2, float* h_out, const void* const* weights,
+                             float* const* outputs, int nseg, uint32_t N, float eps, const uint16_t* q_norm_w,
+                             const uint16_t* k_norm_w, const uint16_t* rope_freqs, uint16_t* k_cache,
+                             uint16_t* v_cache, g4_attn_fused_params p, void* workspace, size_t workspace_bytes,
+                             const uint32_t* position_dev, const g4_warm_region* regions, int nregions,
+                             const float* rope_cs, uint32_t rope_rows) {
+  // (the chunk workgroups write no output: a non-null placeholder for the checks)
+  float* no_output = outputs ? outputs[0] : nullptr;
+  return qkv_attn(ctx, __func__, false, x, w1, residual, out_scale, w2, h_out, weights, outputs, nseg, N, eps,
+                  q_norm_w, k_norm_w, rope_freqs, k_cache, v_cache, no_output, p, workspace, workspace_bytes,
+                  position_dev, regions, nregions, rope_cs, rope_rows);
+}
+
+int g4_attnHeadsMatmul_q4k(g4_ctx* ctx, void* workspace, size_t workspace_bytes, g4_attn_fused_params p,
+                           const uint32_t* position_dev, const void* weight, float* output, uint32_t M) {
   G4_ENTER(ctx);
-  G4_REQUIRE(nseg == 1 || nseg == 3, "g4_qkvAttnDecodeFusedWarm: nseg must be 1 (q) or 3 (q, k, v)");
-  G4_REQUIRE(weights && outputs, "g4_qkvAttnDecodeFusedWarm: null buffer");
-  const uint32_t rows[3] = {p.num_q_heads * p.head_dim, p.num_kv_heads * p.head_dim, p.num_kv_heads * p.head_dim};
-  const float* q_raw = outputs[0];
-  const float* k_raw = nseg == 3 ? outputs[1] : nullptr;
-  const float* v_raw = nseg == 3 ? outputs[2] : nullptr;
-  int rc = g4mqf::mqf_check(ctx, "g4_qkvAttnDecodeFusedWarm", q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs,
-                            k_cache, v_cache, output, p, workspace, position_dev, regions, nregions, rope_cs,
-                            rope_rows);
+  G4_REQUIRE(workspace && position_dev && weight && output && M > 0, "g4_attnHeadsMatmul_q4k: null buffer or no rows");
+  G4_REQUIRE(p.num_kv_heads == 1 && p.num_q_heads == g4mqf::MQ_G && p.head_dim == g4mqf::MQ_HD,
+             "g4_attnHeadsMatmul_q4k: built for 8 query heads of 256 over one KV head");
+  G4_REQUIRE(p.max_seq_len > 0, "g4_attnHeadsMatmul_q4k: max_seq_len must be >= 1");
+  G4_REQUIRE(((uintptr_t)workspace & 15) == 0 && ((uintptr_t)output & 15) == 0,
+             "g4_attnHeadsMatmul_q4k: workspace and output must be 16-byte aligned");
+  int rc = check_w(__func__, 0, weight);
   if (rc) return rc;
-  // the matvec's own checks (g4_normAddScaleMatmulSegments)
-  G4_REQUIRE(x && w1, "g4_qkvAttnDecodeFusedWarm: null buffer");
-  G4_REQUIRE(!out_scale || residual, "g4_qkvAttnDecodeFusedWarm: out_scale needs the residual form");
-  G4_REQUIRE(!residual == !w2, "g4_qkvAttnDecodeFusedWarm: residual and w2 go together");
-  G4_REQUIRE(N == 1536 || N == 2048, "g4_qkvAttnDecodeFusedWarm: N=%u unsupported (1536 or 2048)", N);
-  G4_REQUIRE(((uintptr_t)x & 15) == 0 && (!residual || ((uintptr_t)residual & 15) == 0) &&
-                 (!h_out || ((uintptr_t)h_out & 15) == 0),
-             "g4_qkvAttnDecodeFusedWarm: activations must be 16-byte aligned");
-  G4_REQUIRE(((uintptr_t)w1 & 7) == 0 && ((uintptr_t)w2 & 7) == 0,
-             "g4_qkvAttnDecodeFusedWarm: norm weights must be 8-byte aligned");
-  for (int i = 0; i < nseg; ++i) {
-    G4_REQUIRE(weights[i] && outputs[i], "g4_qkvAttnDecodeFusedWarm: segment %d empty", i);
-    rc = check_w(__func__, 0, weights[i]);
-    if (rc) return rc;
-  }
-  // the one-launch form: q, k and v (a layer reading its producer's cache
-  // projects q only, over 256 workgroups of 3 waves that would leave no CU
-  // to the attention or its L2 warming: it keeps the two launches), Q4_K
-  // rows of 1536 at the width the matvec's own launch takes, one KV head, a
-  // window merged in the
-  // launch, q/k/v staged in the workspace (at most kMaxStage values)
-  GemvSegs sg{};
-  for (int i = 0; i < nseg; ++i) sg.s[i] = GemvSeg{(const uint8_t*)weights[i], outputs[i], rows[i], 0};
-  const int mnwv = mv_pick(6, sg.s, nseg);
-  const uint32_t tr = 16u * (uint32_t)mnwv / 6u;  // rows per tile
-  uint32_t nmv = 0;
-  for (int i = 0; i < nseg; ++i) {
-    sg.s[i].wg_begin = nmv;
-    nmv += ceil_div(rows[i], tr);
-  }
   bool applies = false;
   g4mqf::MqfLaunch L{};
-  if (N == 1536 && mnwv == 6 && nseg == 3 && p.num_kv_heads == 1 && rows[0] + 2 * rows[1] <= g4mqf::kMaxStage) {
-    rc = g4mqf::mqf_prepare(ctx, q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs, k_cache, v_cache, output, p,
-                            workspace, workspace_bytes, position_dev, regions, nregions, rope_cs, nmv, applies, L);
-    if (rc) return rc;
-    applies = applies && !L.partials;
-  }
-  if (!applies) {  // two launches, the same results
-    rc = g4_normAddScaleMatmulSegments(ctx, 0, x, w1, residual, out_scale, w2, h_out, weights, outputs, rows, nseg,
-                                       N, eps, 0.f);
-    if (rc) return rc;
-    return g4_attnDecodeFusedWarm(ctx, q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs, k_cache, v_cache,
-                                  output, p, workspace, workspace_bytes, position_dev, regions, nregions, rope_cs,
-                                  rope_rows);
-  }
-  sg.n = nseg;
-  sg.rep = 1;
-  // staged q/k/v: q at 0, k at nqh * hd, v at (nqh + nkh) * hd
-  L.m.nstage = rows[0] + 2 * rows[1];
-  for (int i = 0; i < nseg; ++i) sg.s[i].stage = L.m.stage + (i == 0 ? 0 : rows[0] + (size_t)(i - 1) * rows[1]);
-  const ProArgs pa{x, w1, residual, w2, h_out, eps, out_scale};
-  // g4_test_stage_wait can leave the matvec workgroups out (nothing is
-  // staged, so every attention workgroup's bounded wait expires)
-  const uint32_t nmv_run = ctx->test_skip_matvec ? 0u : nmv;
-  const dim3 grid(nmv_run + L.m.max_chunks + L.m.nwarm), block(64 * kQkvNwv);
-  auto launch = [&](auto kern, size_t lds) {
-    int r = claim_lds((const void*)kern, ctx, lds);
-    if (r) return r;
-    hipLaunchKernelGGL(kern, grid, block, lds, ctx->stream, sg, pa, L.m, nmv_run);
-    G4_LAUNCHED(ctx, "qkv_attn_fused");
-    return G4_OK;
-  };
-  // (the one launch takes 6-wave matvec workgroups: mnwv == 6 above)
-  if (residual) return launch(qkv_attn_kernel<2, 6>, mv_lds_bytes<0, 6, 6, 2, 1>(false));
-  return launch(qkv_attn_kernel<1, 6>, mv_lds_bytes<0, 6, 6, 1, 1>(false));
+  uint16_t dummy_w[8] __attribute__((aligned(16))) = {0};  // (plan only: no norm weight is read here)
+  rc = g4mqf::mqf_prepare(ctx, nullptr, nullptr, nullptr, dummy_w, nullptr, nullptr, nullptr, nullptr, output, p,
+                          workspace, workspace_bytes, position_dev, nullptr, 0, nullptr, 0, applies, L);
+  if (rc) return rc;
+  G4_REQUIRE(applies && !L.partials && L.m.max_chunks <= g4mqf::MQF_FAN,
+             "g4_attnHeadsMatmul_q4k: the window takes the long attention form, whose chunks another launch merges");
+  HeadsArgs a{};
+  a.ws = L.m.ws;
+  a.nparts = L.m.max_chunks * g4mqf::MQ_G;
+  a.max_chunks = L.m.max_chunks;
+  a.chunk = g4mqf::MQ_STEP * L.m.nstep;
+  a.window = p.sliding_window;
+  a.cap = p.max_seq_len;
+  a.pos_dev = position_dev;
+  a.W = (const uint8_t*)weight;
+  a.out = output;
+  a.M = M;
+  a.stage = L.m.stage;
+  a.nstage = p.num_q_heads * p.head_dim + 2 * p.num_kv_heads * p.head_dim;
+  const dim3 grid(ceil_div(M, (uint32_t)kHeadsRows), p.num_q_heads);
+  hipLaunchKernelGGL(attn_heads_kernel, grid, dim3(4 * kHeadsRows), 0, ctx->stream, a);
+  G4_LAUNCHED(ctx, "attn_heads");
+  return G4_OK;
+}
+
+int g4_normAddPartsGateUpGeluDigits_q4k(g4_ctx* ctx, const float* o_parts, const uint16_t* w_post,
+                                        const float* residual, const uint16_t* w_pre, const void* w_gate,
+                                        const void* w_up, float* h_out, float* out, void* digits, g4_matmul_params p,
+                                        float eps) {
+  G4_ENTER(ctx);
+  int rc = check_mm(__func__, o_parts, w_gate, out, p);
+  if (rc) return rc;
+  G4_REQUIRE(w_post && residual && w_pre && w_up && digits, "g4_normAddPartsGateUpGeluDigits_q4k: null buffer");
+  G4_REQUIRE(p.N == 1536, "g4_normAddPartsGateUpGeluDigits_q4k: N=%u unsupported (1536)", p.N);
+  G4_REQUIRE(p.M % 256 == 0, "g4_normAddPartsGateUpGeluDigits_q4k: M=%u must be a multiple of 256", p.M);
+  G4_REQUIRE(((uintptr_t)w_post & 7) == 0 && ((uintptr_t)w_pre & 7) == 0,
+             "g4_normAddPartsGateUpGeluDigits_q4k: norm weights must be 8-byte aligned");
+  G4_REQUIRE(((uintptr_t)w_gate & 15) == 0 && ((uintptr_t)w_up & 15) == 0 && ((uintptr_t)residual & 15) == 0 &&
+                 ((uintptr_t)digits & 15) == 0 && (!h_out || ((uintptr_t)h_out & 15) == 0),
+             "g4_normAddPartsGateUpGeluDigits_q4k: weights, residual, h_out and digits must be 16-byte aligned");
+  const ProArgs pa{o_parts, w_post, residual, w_pre, h_out, eps};
+  return launch_gateup<6, 4>(ctx, (const uint8_t*)w_gate, (const uint8_t*)w_up, out, p.M, pa, (uint8_t*)digits);
 }
 
 }  // extern "C"

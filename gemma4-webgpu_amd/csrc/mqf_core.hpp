@@ -280,9 +280,13 @@ __device__ __forceinline__ void mqf_warm(const MqfArgs& a, uint32_t p, uint32_t 
 // LONG (windows past MQF_FAN chunks): K/V rows are loaded non-temporally
 // (read once, measured faster at 32K positions) and the workgroups end after
 // storing their partials, which the merge launch that follows combines.
-template <bool LONG, bool FUSED>
+// FUSED && !MERGE: the launch that also runs the q/k/v matvec, whose
+// workgroups end after storing their partials; the o projection's launch
+// merges them per head (attn_heads_kernel) and clears the staged q/k/v.
+template <bool LONG, bool FUSED, bool MERGE = !LONG>
 __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t kvh, uint32_t lin) {
-  static_assert(!(LONG && FUSED), "the fused matvec form merges in the launch");
+  static_assert(!(LONG && FUSED), "the fused matvec form merges in the launch or in the o projection");
+  static_assert(!(LONG && MERGE), "the long form merges in a launch of its own");
   if (bx >= a.max_chunks) {  // (uniform) L2 warming workgroups
     if (kvh == 0) mqf_warm(a, bx - a.max_chunks, lin & 7u);
     return;
@@ -563,7 +567,7 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
 #pragma unroll
     for (int h = 0; h < MQ_G; ++h) st_dev(r0, (uint32_t)(2 * nparts + (part0 + h) * MQ_HD + tid) * 4u, o[h]);
   }
-  if constexpr (LONG) return;  // the merge launch that follows combines the chunks
+  if constexpr (!MERGE) return;  // a later launch combines the chunks
 
   // ---- merge tree: the last arriver of each group merges it in chunk order ----
   // thread (head th, dims td.. and td + 128..): one pass with a running maximum

@@ -165,6 +165,11 @@ SIGNATURES = {
     "g4_qkvAttnDecodeFusedWarm": (_I, [_P, _P, _P, _P, _P, _P, _P, ctypes.POINTER(_P), ctypes.POINTER(_P), _I, _U32,
                                        _F, _P, _P, _P, _P, _P, _P, AttnFusedParams, _P, _SZ, _P,
                                        ctypes.POINTER(WarmRegion), _I, _P, _U32]),
+    "g4_qkvAttnDecodePartials": (_I, [_P, _P, _P, _P, _P, _P, _P, ctypes.POINTER(_P), ctypes.POINTER(_P), _I, _U32,
+                                      _F, _P, _P, _P, _P, _P, AttnFusedParams, _P, _SZ, _P,
+                                      ctypes.POINTER(WarmRegion), _I, _P, _U32]),
+    "g4_attnHeadsMatmul_q4k": (_I, [_P, _P, _SZ, AttnFusedParams, _P, _P, _P, _U32]),
+    "g4_normAddPartsGateUpGeluDigits_q4k": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, MatmulParams, _F]),
     "g4_ropeTable": (_I, [_P, _F, _U32, _P, _U32, _U32, _P]),
     "g4_matmulWarmRegion": (_I, [_P, _I, _U32, _U32, _P, ctypes.POINTER(WarmRegion)]),
     "g4_pagedAttnDecode_workspace_size": (_I, [PagedAttnParams, ctypes.POINTER(_SZ)]),

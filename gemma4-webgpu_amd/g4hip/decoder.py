@@ -446,6 +446,9 @@ class Decoder(_SyntheticModel):
                  gguf=None):
         self.max_seq = max_seq
         self.fuse_qkv = True  # step_fused: q/k/v and the attention in one launch where the shape allows
+        # step_fused: where q/k/v take that launch, its chunk merge moves into
+        # the o projection (per head) and the gate/up prologue adds the heads
+        self.heads_o = True
         self._build_weights(ctx, shape, n_layers, seed, lm_head,
                             lambda il: (ctx.zeros(max_seq * self.s.kv_dim_of(il), np.uint16),
                                         ctx.zeros(max_seq * self.s.kv_dim_of(il), np.uint16)), embed=embed,
@@ -461,6 +464,7 @@ class Decoder(_SyntheticModel):
         self.v = ctx.empty(s.kv_dim, f32)
         self.attn = ctx.empty(Q, f32)
         self.o = ctx.empty(s.hidden, f32)
+        self.o_parts = ctx.empty(s.n_q_heads * s.hidden, f32)  # the o projection's per-head shares
         self.gate = ctx.empty(I, f32)
         self.up = ctx.empty(I, f32)
         self.act = ctx.empty(I, f32)
@@ -619,6 +623,17 @@ class Decoder(_SyntheticModel):
         """gate/up in one launch (Q4_K pair; the digit hand-off when down is Q6_K)."""
         return L.qt["wgate"] == "q4k" and L.qt["wup"] == "q4k"
 
+    def _heads_path(self, il: int, groups) -> bool:
+        """Layer il runs q/k/v + attention without the merge, the per-head
+        merge + o projection, and the gate/up over the head shares: its q/k/v
+        take the one launch (own K/V, Q4_K, hidden 1536, one KV head of 256,
+        window <= 1024), its o is Q4_K over 8 heads and its gate/up is one
+        Q4_K launch."""
+        s, L = self.s, self.layers[il]
+        return (self.heads_o and s.is_producer(il) and self._qkv_fused(groups) and L.qt["wo"] == "q4k"
+                and self._ffn_fused(L) and s.n_q_heads == 8
+                and self.ctx.qkv_attn_single_launch(self.attn_params[il], s.hidden, 3))
+
     def step_fused(self, sample: str = "argmax", advance: bool = True, warm: bool = True) -> None:
         """One token at position *pos (device), then pos += 1 on the device.
 
@@ -630,6 +645,10 @@ class Decoder(_SyntheticModel):
           4. post-attn norm-add -> pre-FFN rmsNorm -> gate/up matvecs -> GELU product
              (also written as the digit block the down launch reads)
           5. down matvec (Q6_K) over those digits
+        Where the shape allows (_heads_path), four: 1 and 2 in one launch
+        whose attention workgroups store their chunk partials and end; the
+        per-head chunk merge with the o projection by head (8 shares of o);
+        4 with the shares added in head order; 5.
         then the last post-FFN norm-add + final rmsNorm + LM head + softcap in
         one launch; its workgroups also leave their argmax candidates (argmax
         sampling), which a one-workgroup launch reduces to the token and the
@@ -661,6 +680,23 @@ class Decoder(_SyntheticModel):
             x, w1, res, scale, w2 = self._layer_input(il)
             groups = qkv_groups(L, outs, rows)
             warm_il = self.warm[il] if warm else []
+            if self._heads_path(il, groups):
+                # q/k/v + attention (chunk partials), per-head merge + o, gate/up over the shares, down
+                c.qkvAttnDecodePartials(x, w1, res, scale, w2, None if il == 0 else self.hidden, groups[0][1], outs,
+                                        H, s.eps, L.q_norm, L.k_norm, self.rope_freqs, L.k_cache, L.v_cache,
+                                        self.attn_params[il], self.attn_ws, self.pos, warm_il,
+                                        self.rope_cs[s.is_global(il)], self.rope_rows)
+                c.attnHeadsMatmul_q4k(self.attn_ws, self.attn_params[il], self.pos, L.wo, self.o_parts, H)
+                c.normAddPartsGateUpGeluDigits_q4k(self.o_parts, L.post_attn_norm, self.hidden, L.pre_ffn_norm,
+                                                   L.wgate, L.wup, self.hidden2, self.act, self.act_digits, I, H,
+                                                   s.eps)
+                if L.qt["wdown"] == "q6k":
+                    c.matmulQuantDigits_q6k(self.act_digits, L.wdown, self.down, H, I)
+                else:
+                    self._mv(L.qt["wdown"], self.act, L.wdown, self.down, H, I)
+                if s.ple_dim:
+                    self._ple_tail(il, L)
+                continue
             if self._qkv_fused(groups):  # q/k/v and the attention block: one launch where the shape allows
                 c.qkvAttnDecodeFusedWarm(x, w1, res, scale, w2, None if il == 0 else self.hidden, groups[0][1], outs,
                                          H, s.eps, L.q_norm, L.k_norm, self.rope_freqs, L.k_cache, L.v_cache,
@@ -696,11 +732,7 @@ class Decoder(_SyntheticModel):
             else:
                 self._mv(L.qt["wdown"], self.act, L.wdown, self.down, H, I)
             if s.ple_dim:
-                # post-FFN norm-add -> inp_gate -> gelu * ple_inputs, then proj
-                D = s.ple_dim
-                c.pleGate(self.down, L.post_ffn_norm, self.hidden2, self.hidden3, L.ple_gate, self.ple_inputs, 0,
-                          il * D, self.ple_gated, D, H, s.eps)
-                c.matmulF16(self.ple_gated, L.ple_proj, self.ple_out, H, D)
+                self._ple_tail(il, L)
         last = self.layers[-1]
         if s.ple_dim:
             # the last PLE tail on its own (one vector), then the head normalises it
@@ -733,6 +765,15 @@ class Decoder(_SyntheticModel):
                                 self.topk, s.eps, softcap=s.softcap)
         if advance:
             c.advancePosition(self.pos, 1)
+
+    def _ple_tail(self, il: int, L) -> None:
+        """Post-FFN norm-add -> inp_gate -> gelu * ple_inputs, then proj (the
+        layer's per-layer-embedding tail, src/engine.ts:1608-1616)."""
+        c, s = self.ctx, self.s
+        D = s.ple_dim
+        c.pleGate(self.down, L.post_ffn_norm, self.hidden2, self.hidden3, L.ple_gate, self.ple_inputs, 0, il * D,
+                  self.ple_gated, D, s.hidden, s.eps)
+        c.matmulF16(self.ple_gated, L.ple_proj, self.ple_out, s.hidden, D)
 
     def capture_fused(self, sample: str = "argmax", warm: bool = True):
         self.ctx.graph_begin()

@@ -507,6 +507,36 @@ class Context:
                                               _p(k_cache), _p(v_cache), _p(out), p, _p(workspace), workspace.nbytes,
                                               _p(position_dev), arr, nr, _p(rope_cs), rope_rows))
 
+    def qkvAttnDecodePartials(self, x: Ptr, w1: Ptr, residual: Ptr, out_scale: Ptr, w2: Ptr, h_out: Ptr,
+                              weights, outputs, N: int, eps: float, q_norm_w: Ptr, k_norm_w: Ptr, rope_freqs: Ptr,
+                              k_cache: Ptr, v_cache: Ptr, p: AttnFusedParams, workspace: Buffer,
+                              position_dev: Ptr, regions, rope_cs: Ptr = None, rope_rows: int = 0) -> None:
+        """The one q/k/v + attention launch with its chunk merge left to
+        attnHeadsMatmul_q4k (g4_qkvAttnDecodePartials)."""
+        n = len(weights)
+        W = (ctypes.c_void_p * n)(*[_p(w).value for w in weights])
+        Y = (ctypes.c_void_p * n)(*[_p(y).value for y in outputs])
+        nr = len(regions)
+        arr = (WarmRegion * max(nr, 1))(*regions)
+        check(lib().g4_qkvAttnDecodePartials(self.h, _p(x), _p(w1), _p(residual), _p(out_scale), _p(w2), _p(h_out),
+                                             W, Y, n, N, eps, _p(q_norm_w), _p(k_norm_w), _p(rope_freqs),
+                                             _p(k_cache), _p(v_cache), p, _p(workspace), workspace.nbytes,
+                                             _p(position_dev), arr, nr, _p(rope_cs), rope_rows))
+
+    def attnHeadsMatmul_q4k(self, workspace: Buffer, p: AttnFusedParams, position_dev: Ptr, weight: Ptr, out: Ptr,
+                            M: int) -> None:
+        """Per-head chunk merge + o projection: out[h][M] = W_o[:, 256h:256h+256] . merged head h."""
+        check(lib().g4_attnHeadsMatmul_q4k(self.h, _p(workspace), workspace.nbytes, p, _p(position_dev), _p(weight),
+                                           _p(out), M))
+
+    def normAddPartsGateUpGeluDigits_q4k(self, o_parts: Ptr, w_post: Ptr, residual: Ptr, w_pre: Ptr, w_gate: Ptr,
+                                         w_up: Ptr, h_out: Ptr, out: Ptr, digits: Ptr, M: int, N: int,
+                                         eps: float = 1e-6) -> None:
+        """normAddGateUpGeluDigits_q4k with o given as 8 per-head shares [8][N], added in head order."""
+        check(lib().g4_normAddPartsGateUpGeluDigits_q4k(self.h, _p(o_parts), _p(w_post), _p(residual), _p(w_pre),
+                                                        _p(w_gate), _p(w_up), _p(h_out), _p(out), _p(digits),
+                                                        MatmulParams(M, N), eps))
+
     def ropeTable(self, theta: float, apply_divisor: int, rope_freqs: Ptr, head_dim: int, rows: int,
                   table: Ptr) -> None:
         """table[t][i] = (cos, sin) of position t's RoPE angle for pair i (rows x head_dim/2 float2)."""

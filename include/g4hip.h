@@ -293,6 +293,39 @@ int g4_qkvAttnDecodeFusedWarm(g4_ctx* ctx, const float* x, const uint16_t* w1, c
                               void* workspace, size_t workspace_bytes, const uint32_t* position_dev,
                               const g4_warm_region* regions, int nregions, const float* rope_cs,
                               uint32_t rope_rows);
+/* g4_qkvAttnDecodeFusedWarm's one launch with the attention's chunk merge
+ * left out: the attention workgroups end after storing their chunk partials
+ * (m, l, o) in the workspace, and g4_attnHeadsMatmul_q4k merges them in the
+ * o projection's launch. Only shapes that take the one launch (N = 1536,
+ * Q4_K q/k/v, one KV head of 256, a window of at most 1024 positions);
+ * others return G4_ERR_UNSUPPORTED. Leaves the staged q/k/v in the
+ * workspace: the next call on it must be g4_attnHeadsMatmul_q4k, which
+ * clears them. An MI355X split of src/engine.ts:1550-1584 with no reference
+ * counterpart. */
+int g4_qkvAttnDecodePartials(g4_ctx* ctx, const float* x, const uint16_t* w1, const float* residual,
+                             const uint16_t* out_scale, const uint16_t* w2, float* h_out, const void* const* weights,
+                             float* const* outputs, int nseg, uint32_t N, float eps, const uint16_t* q_norm_w,
+                             const uint16_t* k_norm_w, const uint16_t* rope_freqs, uint16_t* k_cache,
+                             uint16_t* v_cache, g4_attn_fused_params p, void* workspace, size_t workspace_bytes,
+                             const uint32_t* position_dev, const g4_warm_region* regions, int nregions,
+                             const float* rope_cs, uint32_t rope_rows);
+/* The attention output projection of src/engine.ts:1585-1589
+ * (matmulQuant of attn_output by W_o, Q4_K [M][8 * 256]) over the chunk
+ * partials g4_qkvAttnDecodePartials left in the workspace, split by head:
+ * output[h][M] = W_o[:, 256 h .. 256 h + 255] . o_h, o_h the attention
+ * output of head h (its chunks merged as attn_output.wgsl sums over all
+ * positions). o = sum over h of output[h], which
+ * g4_normAddPartsGateUpGeluDigits_q4k adds in head order. Also clears the
+ * workspace's staged q/k/v. */
+int g4_attnHeadsMatmul_q4k(g4_ctx* ctx, void* workspace, size_t workspace_bytes, g4_attn_fused_params p,
+                           const uint32_t* position_dev, const void* weight, float* output, uint32_t M);
+/* g4_normAddGateUpGeluDigits_q4k with o given as 8 per-head shares
+ * o_parts[8][N] (g4_attnHeadsMatmul_q4k's output), added in head order
+ * before the post-attention norm-add (src/engine.ts:1590-1602). */
+int g4_normAddPartsGateUpGeluDigits_q4k(g4_ctx* ctx, const float* o_parts, const uint16_t* w_post,
+                                        const float* residual, const uint16_t* w_pre, const void* w_gate,
+                                        const void* w_up, float* h_out, float* out, void* digits, g4_matmul_params p,
+                                        float eps);
 /* Test hook with no reference counterpart, for tests of the stall report:
  * the following one-launch g4_qkvAttnDecodeFusedWarm calls on this context
  * poll at most `spin_limit` times (0 restores the built-in limit) and, when

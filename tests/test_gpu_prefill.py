@@ -6,7 +6,8 @@ same weights and cache.
 
 Checked at rel-L2 1e-3 / cosine 0.9999: the last token's hidden state and
 logits; every K/V row the prompt appended (f16) against the oracle's f32 row
-of its own position before rounding; the first sampled token is the argmax of the
+of its own position before rounding (rows behind a saturated FFN: see
+GELU_MARGIN); the first sampled token is the argmax of the
 device's logits (bit-exact) and a maximum of the oracle's up to the logits'
 tolerance. Cases: a 40-token prompt in chunks of 16 (the last one short),
 from position 0 and after 600 cached positions (past the 512 window), on a
@@ -17,13 +18,19 @@ import numpy as np
 import pytest
 
 import oracle as O
-from decode_oracle import HostModel
+from decode_oracle import HostModel, gelu_mul_f32
 from g4hip.decoder import BatchDecoder, E2BShape
-from gpu_util import assert_close, assert_f16_row_close
+from gpu_util import assert_close
 
 pytestmark = pytest.mark.gpu
 
 CHUNKS = [(16, 40), (64, 100)]  # (rows per chunk, prompt tokens)
+# A row whose layer input went through an FFN in tanh's saturation (the
+# benchmark weights' +0.35 mean makes some tokens' GELU inputs all large and
+# negative, where the reference's f32 GELU is cancellation) is held to
+# GELU_MARGIN x the distance between the oracle's rows with its GELU and
+# with the all-f32 evaluation of the shader, when that exceeds 1e-3.
+GELU_MARGIN = 4.0
 
 
 def _shape(kind):
@@ -58,16 +65,21 @@ def test_prefill_matches_sequential_forwards(ctx, kind, start, B, T):
     LG = d.logits.download(np.float32).reshape(B, s.vocab)[last]
     tok = int(d.tokens.download(np.uint32)[last])
     x = lg = None
-    rows = []  # per prompt token: {layer: (k, v)} in f32
+    rows, rows32 = [], []  # per prompt token: {layer: (k, v)} in f32, with the oracle's and the all-f32 GELU
+    kc32, vc32 = [k.copy() for k in kcs], [v.copy() for v in vcs]
     for t in range(T):
         rows.append({})
+        rows32.append({})
         x, lg = hm.step(hm.embed(int(toks[t])), kcs, vcs, start + t, token=int(toks[t]), rows=rows[-1])
+        hm.step(hm.embed(int(toks[t])), kc32, vc32, start + t, token=int(toks[t]), rows=rows32[-1],
+                gelu=gelu_mul_f32)
     print(f"[prefill] {kind} start {start}: last hidden rel-L2 {O.rel_l2(H, x):.2e}, logits {O.rel_l2(LG, lg):.2e}",
           flush=True)
     assert_close(H, x, what="last token hidden")
     assert_close(LG, lg, what="last token logits")
     assert tok == O.argmax(LG)
     assert lg[tok] >= lg.max() - 1e-3 * np.abs(lg).max()
+    loose = []
     for il, L in enumerate(d.layers):
         if not s.is_producer(il):
             continue
@@ -75,5 +87,11 @@ def test_prefill_matches_sequential_forwards(ctx, kind, start, B, T):
         for j, (nm, pool) in enumerate((("k", L.k_cache.download(np.uint16)), ("v", L.v_cache.download(np.uint16)))):
             prow = pool.reshape(-1, kv)
             for t in range(start, start + T):
-                assert_f16_row_close(prow[d.pool_row(0, t)], rows[t - start][il][j], what=f"{nm} row {t} layer {il}")
+                want = rows[t - start][il][j]
+                bound = max(1e-3, GELU_MARGIN * O.rel_l2(rows32[t - start][il][j], want))
+                if bound > 1e-3:
+                    loose.append((t, il, nm, round(bound, 5)))
+                g = prow[d.pool_row(0, t)].view(np.float16).astype(np.float32)
+                assert_close(g, want, rel=bound, what=f"{nm} row {t} layer {il}")
+    print(f"[prefill] rows held to the GELU's own spread (position, layer, k/v, bound): {loose}", flush=True)
     del d
