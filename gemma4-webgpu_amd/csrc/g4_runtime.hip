@@ -240,6 +240,22 @@ int g4_download_async(g4_ctx* ctx, void* dst, const void* src, size_t bytes, siz
   return g4_event_record(ctx, ev);
 }
 
+int g4_host_alloc(g4_ctx* ctx, size_t bytes, void** host) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(host, "g4_host_alloc: null out");
+  *host = nullptr;
+  G4_REQUIRE(bytes > 0, "g4_host_alloc: zero bytes");
+  G4_HIP(ctx, hipHostMalloc(host, bytes, hipHostMallocDefault));
+  return G4_OK;
+}
+
+int g4_host_free(void* host) {
+  if (!host) return G4_OK;
+  const hipError_t e = hipHostFree(host);
+  if (e != hipSuccess) return g4::hip_fail(nullptr, e, "hipHostFree");
+  return G4_OK;
+}
+
 int g4_copy_d2d(g4_ctx* ctx, void* dst, const void* src, size_t bytes) {
   G4_ENTER(ctx);
   G4_REQUIRE((dst && src) || bytes == 0, "g4_copy_d2d: null pointer");

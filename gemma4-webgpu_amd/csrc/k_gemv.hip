@@ -132,11 +132,17 @@ __device__ __forceinline__ void digits4(const XView& xv, int vec, uint32_t e, fl
 // (shaders/fused_norm_add.wgsl then shaders/rms_norm.wgsl); h is written to
 // h_out by workgroup 0 when h_out is non-null; 3 (one-vector matvec, Q6_K)
 // = x already digitised by the launch that produced it (MvD8 block at x);
-// 4 (one-vector matvec) = mode 2 with o given as kHeadParts vectors of K
-// (the o projection's per-head shares, [kHeadParts][K] at x), added in
-// order.
-constexpr int kHeadParts = 8;  // prologue mode 4: shares of o, one per query head
+// 4 (one-vector matvec) = mode 2 with o given as kOShares vectors of K
+// (the o projection's shares by group of heads, [kOShares][K] at x),
+// added in order.
 __host__ __device__ constexpr bool pro_add(int pro) { return pro == 2 || pro == 4; }  // residual-add + norm
+// The o projection split by groups of heads (attn_heads_kernel): fewer,
+// wider groups trade the chunk partials each of its workgroups reads (8 KB
+// per head) against the shares every gate/up workgroup reads ahead of its
+// weights (6 KB each at hidden 1536).
+constexpr int kHeadsPerWg = 2;
+constexpr int kOShares = 8 / kHeadsPerWg;
+static_assert(kOShares == G4_O_SHARES, "the ABI states the share count");
 
 struct ProArgs {
   const float* x;         // [NV][K] (mode 2: o)
@@ -861,13 +867,13 @@ __device__ __forceinline__ void mv_pro_load(MvPro<BPR, NWV, PRO>& P, const ProAr
   for (int p = 0; p < PP::XP; ++p) {
     const int fc = PP::live(p) ? PP::elem(p) : 0;
     if constexpr (PRO == 4) {
-      float4 part[kHeadParts];
+      float4 part[kOShares];
 #pragma unroll
-      for (int i = 0; i < kHeadParts; ++i) part[i] = *(const float4*)(a.x + (size_t)i * PP::K + fc);
+      for (int i = 0; i < kOShares; ++i) part[i] = *(const float4*)(a.x + (size_t)i * PP::K + fc);
       float4 v = part[0];
 #pragma unroll
-      for (int i = 1; i < kHeadParts; ++i) v = make_float4(v.x + part[i].x, v.y + part[i].y, v.z + part[i].z,
-                                                           v.w + part[i].w);
+      for (int i = 1; i < kOShares; ++i) v = make_float4(v.x + part[i].x, v.y + part[i].y, v.z + part[i].z,
+                                                         v.w + part[i].w);
       P.x[p] = v;
     } else {
       P.x[p] = *(const float4*)(a.x + fc);
@@ -2024,61 +2030,65 @@ __global__ __launch_bounds__(64 * kQkvNwv) void qkv_attn_kernel(GemvSegs segs, P
 // (g4_attnHeadsMatmul_q4k). The q/k/v + attention launch without its merge
 // leaves per chunk c and head h the partial (m, l, o[256]): the chunk's
 // running maximum, its softmax denominator and its unnormalised output.
-// Workgroup (tile, h) merges head h over the live chunks (weights
-// exp(m_c - max), as the in-launch merger), digitises the head's 256
-// outputs exactly as the o matvec's prologue digitises those elements (one
-// scale per 32), multiplies them with super-block h of 32 rows of W_o and
-// writes out[h][row]: the head's share of o = sum_h out[h]. The next launch
-// (the gate/up prologue, PRO 4) adds the shares in head order. Workgroups
-// also clear the staged q/k/v the attention's merger used to clear.
+// Workgroup (tile, group) merges the kHeadsPerWg heads of its group over the
+// live chunks (weights exp(m_c - max), as the in-launch merger), digitises
+// their outputs exactly as the o matvec's prologue digitises those elements
+// (one scale per 32), multiplies them with the group's super-blocks of
+// kHeadsRows rows of W_o and writes out[group][row]: that group's share of
+// o = sum over groups of out[group]. The next launch (the gate/up prologue,
+// PRO 4) adds the kOShares shares in group order. Workgroups also clear the
+// staged q/k/v the attention's merger used to clear.
+constexpr int kHeadsRows = 32;  // rows per workgroup; 4 units of 64 weights per row and head
+
 struct HeadsArgs {
   const float* ws;       // chunk partials: m [nparts], l [nparts], o [nparts][256]
   uint32_t nparts;       // max_chunks * 8 (one KV head)
   uint32_t max_chunks, chunk;  // chunk length in positions
   uint32_t window, cap;
   const uint32_t* pos_dev;
-  const uint8_t* W;      // [M][nqh * 256] Q4_K
-  float* out;            // [nqh][M]
+  const uint8_t* W;      // [M][8 * 256] Q4_K
+  float* out;            // [kOShares][M]
   uint32_t M;
   uint64_t* stage;       // staged q/k/v to clear
   uint32_t nstage;
 };
-constexpr int kHeadsRows = 32;  // rows per workgroup: 4 units of 64 weights per row, 2 waves
 
-__global__ __launch_bounds__(4 * kHeadsRows) void attn_heads_kernel(HeadsArgs a) {
-  __shared__ __align__(16) uint8_t smem[align16(MvX<1>::END)];
-  const int tid = threadIdx.x, u = tid & 3, slot = tid >> 2;
-  const uint32_t h = blockIdx.y, nh = gridDim.y;
+__global__ __launch_bounds__(4 * kHeadsRows * kHeadsPerWg) void attn_heads_kernel(HeadsArgs a) {
+  constexpr int HPW = kHeadsPerWg, NTH = 4 * kHeadsRows * HPW, U = 4 * HPW;  // U: units per row
+  __shared__ __align__(16) uint8_t smem[align16(MvX<HPW>::END)];
+  const int tid = threadIdx.x, u = tid % U, slot = tid / U;
+  const uint32_t grp = blockIdx.y;
   const uint32_t row = min(blockIdx.x * (uint32_t)kHeadsRows + (uint32_t)slot, a.M - 1);
-  // this unit's weights first: 48 bytes of super-block h of the row
-  const uint32_t rb = nh * 144u;
+  // this unit's weights first: 48 bytes of super-block (head) HPW grp + u / 4 of the row
+  const uint32_t rb = 8u * 144u;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)a.W, (short)0, (int)(uint32_t)min((uint64_t)a.M * rb, (uint64_t)0xffffffffu), 0x00020000);
   Q4Unit wu;
-  q4_unit_load<2>(wu, rs, row * rb + h * 144u, u);
+  q4_unit_load<2>(wu, rs, row * rb + (HPW * grp + (uint32_t)(u >> 2)) * 144u, u & 3);
   // the staged q/k/v of the attention launch, cleared for the next one
   {
     const uint32_t lin = blockIdx.y * gridDim.x + blockIdx.x, nwg = gridDim.x * gridDim.y;
-    for (uint32_t i = lin * 4u * kHeadsRows + (uint32_t)tid; i < a.nstage; i += nwg * 4u * kHeadsRows)
+    for (uint32_t i = lin * (uint32_t)NTH + (uint32_t)tid; i < a.nstage; i += nwg * (uint32_t)NTH)
       a.stage[i] = 0ull;
   }
-  if (tid < 64) {  // (uniform per wave) wave 0 merges and digitises the head
+  using PP = MvPro<HPW, HPW, 0>;  // HPW waves, 4 outputs per lane: the group's 256 HPW outputs
+  if (PP::active()) {             // (uniform per wave)
     const uint32_t L = min(*a.pos_dev + 1, a.cap);
     const uint32_t wstart = (a.window != 0 && L > a.window) ? L - a.window : 0;
     const uint32_t nch = (L - wstart + a.chunk - 1) / a.chunk;
-    using PP = MvPro<1, 1, 0>;
     PP P;
-    const int e = PP::elem(0);  // this lane's 4 outputs
+    const int e = PP::elem(0);  // this lane's 4 outputs: head HPW grp + e / 256, dims e % 256 ..
+    const uint32_t h = HPW * grp + (uint32_t)(e >> 8), d = (uint32_t)(e & 255);
     // every chunk slot is read at a clamped index (a dead chunk's partial
     // is stale) and weighted 0 past the live ones
     float m[g4mqf::MQF_FAN], lv[g4mqf::MQF_FAN];
     float4 o[g4mqf::MQF_FAN];
 #pragma unroll
     for (uint32_t c = 0; c < g4mqf::MQF_FAN; ++c) {
-      const uint32_t pc = (min(c, nch - 1) * 8u + h);
+      const uint32_t pc = min(c, nch - 1) * 8u + h;
       m[c] = a.ws[pc];
       lv[c] = a.ws[a.nparts + pc];
-      o[c] = *(const float4*)(a.ws + 2 * (size_t)a.nparts + (size_t)pc * 256 + e);
+      o[c] = *(const float4*)(a.ws + 2 * (size_t)a.nparts + (size_t)pc * 256 + d);
     }
     float M = -INFINITY;
 #pragma unroll
@@ -2087,7 +2097,7 @@ __global__ __launch_bounds__(4 * kHeadsRows) void attn_heads_kernel(HeadsArgs a)
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (uint32_t c = 0; c < g4mqf::MQF_FAN; ++c) {
-      // a stalled chunk's +Inf maximum makes every weight NaN (0 * Inf or Inf - Inf)
+      // a stalled chunk's +Inf maximum makes the weights NaN (Inf - Inf)
       const float wc = (c >= nch || m[c] == -INFINITY) ? 0.f : g4mqf::mq_exp(m[c] - M);
       Ls += wc * lv[c];
       acc.x += wc * o[c].x;
@@ -2097,15 +2107,13 @@ __global__ __launch_bounds__(4 * kHeadsRows) void attn_heads_kernel(HeadsArgs a)
     }
     const float li = Ls > 0.f ? 1.0f / Ls : 0.f;  // (NaN stays NaN through acc)
     P.x[0] = make_float4(acc.x * li, acc.y * li, acc.z * li, acc.w * li);
-    mv_digitize<1, 1, 0>(P, smem);
+    mv_digitize<HPW, HPW, 0>(P, smem);
   }
   lds_barrier();
   MvUnit<0> X;
-  mv_unit_load<0, 1>(X, smem, u);
-  float v = q4_unit_dot(X, wu, u);
-  v += dpp<kDppXor1>(v);
-  v += dpp<kDppXor2>(v);
-  if (u == 0 && blockIdx.x * (uint32_t)kHeadsRows + (uint32_t)slot < a.M) a.out[(size_t)h * a.M + row] = v;
+  mv_unit_load<0, HPW>(X, smem, u);
+  const float v = g4d::group_sum<U>(q4_unit_dot(X, wu, u & 3));
+  if (u == 0 && blockIdx.x * (uint32_t)kHeadsRows + (uint32_t)slot < a.M) a.out[(size_t)grp * a.M + row] = v;
 }
 
 // workgroup widths in waves for a row of BPR super-blocks (slots must tile it)
@@ -2717,8 +2725,8 @@ int g4_attnHeadsMatmul_q4k(g4_ctx* ctx, void* workspace, size_t workspace_bytes,
   a.M = M;
   a.stage = L.m.stage;
   a.nstage = p.num_q_heads * p.head_dim + 2 * p.num_kv_heads * p.head_dim;
-  const dim3 grid(ceil_div(M, (uint32_t)kHeadsRows), p.num_q_heads);
-  hipLaunchKernelGGL(attn_heads_kernel, grid, dim3(4 * kHeadsRows), 0, ctx->stream, a);
+  const dim3 grid(ceil_div(M, (uint32_t)kHeadsRows), p.num_q_heads / kHeadsPerWg);
+  hipLaunchKernelGGL(attn_heads_kernel, grid, dim3(4 * kHeadsRows * kHeadsPerWg), 0, ctx->stream, a);
   G4_LAUNCHED(ctx, "attn_heads");
   return G4_OK;
 }

@@ -8,6 +8,7 @@ _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libg4hip.so")
 
 G4_OK = 0
+O_SHARES = 4  # G4_O_SHARES: shares of o g4_attnHeadsMatmul_q4k writes
 ERRORS = {
     -1: "G4_ERR_INVALID",
     -2: "G4_ERR_HIP",
@@ -129,6 +130,8 @@ SIGNATURES = {
     "g4_copy_d2d": (_I, [_P, _P, _P, _SZ]),
     "g4_stream_sync": (_I, [_P]),
     "g4_clear_stall": (_I, [_P]),
+    "g4_host_alloc": (_I, [_P, _SZ, ctypes.POINTER(_P)]),
+    "g4_host_free": (_I, [_P]),
     "g4_graph_kernel_nodes": (_I, [_P, ctypes.POINTER(ctypes.c_size_t)]),
     "g4_test_stage_wait": (_I, [_P, _U32, _I]),
     "g4_event_record": (_I, [_P, _PP]),

@@ -49,6 +49,7 @@ from typing import List, Optional
 
 import numpy as np
 
+from ._lib import O_SHARES
 from .device import Buffer, Context, splitmix64
 
 Q4K_BYTES = 144
@@ -464,7 +465,8 @@ class Decoder(_SyntheticModel):
         self.v = ctx.empty(s.kv_dim, f32)
         self.attn = ctx.empty(Q, f32)
         self.o = ctx.empty(s.hidden, f32)
-        self.o_parts = ctx.empty(s.n_q_heads * s.hidden, f32)  # the o projection's per-head shares
+        # the o projection's shares by groups of heads (O_SHARES of them; room for one per head)
+        self.o_parts = ctx.empty(max(O_SHARES, s.n_q_heads) * s.hidden, f32)
         self.gate = ctx.empty(I, f32)
         self.up = ctx.empty(I, f32)
         self.act = ctx.empty(I, f32)

@@ -525,14 +525,15 @@ class Context:
 
     def attnHeadsMatmul_q4k(self, workspace: Buffer, p: AttnFusedParams, position_dev: Ptr, weight: Ptr, out: Ptr,
                             M: int) -> None:
-        """Per-head chunk merge + o projection: out[h][M] = W_o[:, 256h:256h+256] . merged head h."""
+        """Chunk merge + o projection by group of heads: out[g][M] = sum over the group's heads h of
+        W_o[:, 256h:256h+256] . merged head h (O_SHARES groups of 8 / O_SHARES heads)."""
         check(lib().g4_attnHeadsMatmul_q4k(self.h, _p(workspace), workspace.nbytes, p, _p(position_dev), _p(weight),
                                            _p(out), M))
 
     def normAddPartsGateUpGeluDigits_q4k(self, o_parts: Ptr, w_post: Ptr, residual: Ptr, w_pre: Ptr, w_gate: Ptr,
                                          w_up: Ptr, h_out: Ptr, out: Ptr, digits: Ptr, M: int, N: int,
                                          eps: float = 1e-6) -> None:
-        """normAddGateUpGeluDigits_q4k with o given as 8 per-head shares [8][N], added in head order."""
+        """normAddGateUpGeluDigits_q4k with o given as O_SHARES shares [O_SHARES][N], added in order."""
         check(lib().g4_normAddPartsGateUpGeluDigits_q4k(self.h, _p(o_parts), _p(w_post), _p(residual), _p(w_pre),
                                                         _p(w_gate), _p(w_up), _p(h_out), _p(out), _p(digits),
                                                         MatmulParams(M, N), eps))

@@ -291,6 +291,124 @@ napi_value Download(napi_env env, napi_callback_info info) {
   return buf;
 }
 
+// downloadAsync(ctx, src, bytes, srcOffset = 0) -> Promise<Buffer>: the
+// readback of src/engine.ts:1772-1787 (mapAsync) without blocking the event
+// loop. The copy lands in pinned host memory (g4_host_alloc) behind the work
+// already enqueued; a worker thread of the libuv pool waits on its event,
+// and the promise resolves on the event loop with a Buffer over that memory
+// (freed with the Buffer) or rejects with the library's error (code =
+// G4_ERR_* name). Depth-2 pipelining submits the next step before awaiting.
+struct Readback {
+  napi_async_work work = nullptr;
+  napi_deferred deferred = nullptr;
+  g4_event* ev = nullptr;
+  void* host = nullptr;
+  size_t bytes = 0;
+  int rc = G4_OK;
+  std::string err;
+};
+
+void readback_wait(napi_env, void* data) {  // worker thread: no N-API calls here
+  Readback* r = (Readback*)data;
+  r->rc = g4_event_wait(r->ev);
+  if (r->rc != G4_OK) r->err = g4_last_error();
+}
+
+void free_pinned(napi_env, void* data, void*) { g4_host_free(data); }
+
+void readback_done(napi_env env, napi_status status, void* data) {
+  Readback* r = (Readback*)data;
+  g4_event_destroy(r->ev);
+  if (status == napi_ok && r->rc == G4_OK) {
+    napi_value buf;
+    if (napi_create_external_buffer(env, r->bytes, r->host, free_pinned, nullptr, &buf) == napi_ok) {
+      napi_resolve_deferred(env, r->deferred, buf);
+    } else {
+      g4_host_free(r->host);
+      napi_value msg, e;
+      napi_create_string_utf8(env, "downloadAsync: cannot wrap the host buffer", NAPI_AUTO_LENGTH, &msg);
+      napi_create_error(env, nullptr, msg, &e);
+      napi_reject_deferred(env, r->deferred, e);
+    }
+  } else {
+    g4_host_free(r->host);
+    const int rc = r->rc != G4_OK ? r->rc : G4_ERR_INVALID;
+    napi_value code, msg, e;
+    napi_create_string_utf8(env, status_name(rc), NAPI_AUTO_LENGTH, &code);
+    napi_create_string_utf8(env, r->err.empty() ? status_name(rc) : r->err.c_str(), NAPI_AUTO_LENGTH, &msg);
+    napi_create_error(env, code, msg, &e);
+    napi_reject_deferred(env, r->deferred, e);
+  }
+  napi_delete_async_work(env, r->work);
+  delete r;
+}
+
+napi_value DownloadAsync(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  void* src = a.ptr(1);
+  const uint64_t n = a.u64(2);
+  const uint64_t off = a.present(3) ? a.u64(3) : 0;
+  CHECKED(a);
+  if (n == 0) {
+    a.fail("downloadAsync: zero bytes");
+    return nullptr;
+  }
+  Readback* r = new Readback();
+  r->bytes = (size_t)n;
+  int rc = g4_host_alloc(c, r->bytes, &r->host);
+  if (rc == G4_OK) rc = g4_download_async(c, r->host, src, r->bytes, (size_t)off, &r->ev);
+  if (rc != G4_OK) {
+    g4_host_free(r->host);
+    delete r;
+    return done(env, rc);
+  }
+  napi_value promise, name;
+  napi_create_promise(env, &r->deferred, &promise);
+  napi_create_string_utf8(env, "g4hip.downloadAsync", NAPI_AUTO_LENGTH, &name);
+  napi_create_async_work(env, nullptr, name, readback_wait, readback_done, r, &r->work);
+  napi_queue_async_work(env, r->work);
+  return promise;
+}
+
+// eventRecord(ctx) -> handle; eventQuery(ev) -> true once complete (throws on
+// a failure, G4_ERR_STALLED included); eventWait(ev); eventDestroy(ev): for
+// hosts that poll instead of awaiting a promise.
+napi_value EventRecord(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  CHECKED(a);
+  g4_event* ev = nullptr;
+  const int rc = g4_event_record(c, &ev);
+  if (rc != G4_OK) return done(env, rc);
+  return bigint(env, ev);
+}
+
+napi_value EventQuery(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_event* ev = (g4_event*)a.ptr(0);
+  CHECKED(a);
+  const int rc = g4_event_query(ev);
+  if (rc < 0) return done(env, rc);
+  napi_value out;
+  napi_get_boolean(env, rc == 1, &out);
+  return out;
+}
+
+napi_value EventWait(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_event* ev = (g4_event*)a.ptr(0);
+  CHECKED(a);
+  return done(env, g4_event_wait(ev));
+}
+
+napi_value EventDestroy(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_event* ev = (g4_event*)a.ptr(0);
+  CHECKED(a);
+  return done(env, g4_event_destroy(ev));
+}
+
 napi_value Sync(napi_env env, napi_callback_info info) {
   Args a(env, info);
   g4_ctx* c = CTX(a, 0);
@@ -1222,6 +1340,11 @@ const Entry kEntries[] = {
     {"memset", Memset},
     {"upload", Upload},
     {"download", Download},
+    {"downloadAsync", DownloadAsync},
+    {"eventRecord", EventRecord},
+    {"eventQuery", EventQuery},
+    {"eventWait", EventWait},
+    {"eventDestroy", EventDestroy},
     {"sync", Sync},
     {"graphBegin", GraphBegin},
     {"graphEnd", GraphEnd},

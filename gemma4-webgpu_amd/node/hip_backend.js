@@ -302,6 +302,10 @@ class HipBackend {
   }
 
   close() {
+    if (this.fusedGraph) {
+      this.g.graphDestroy(this.fusedGraph);
+      this.fusedGraph = null;
+    }
     for (const p of this.owned) this.g.free(this.ctx, p);
     this.owned = [];
     this.g.destroy(this.ctx);
@@ -784,6 +788,46 @@ class HipBackend {
 
   readToken() {
     return this.g.download(this.ctx, this.workBuffers.argmaxResult, 4).readUInt32LE(0);
+  }
+
+  // The sampled token as a Promise: the copy is enqueued behind the work
+  // already submitted and completes off the event loop (mapAsync,
+  // src/engine.ts:1772-1787).
+  readTokenAsync() {
+    return this.g.downloadAsync(this.ctx, this.workBuffers.argmaxResult, 4).then((b) => b.readUInt32LE(0));
+  }
+
+  // Greedy generation from `token` at `position` with the captured fused
+  // step, pipelined as src/engine.ts:2041-2124 does: step N + 1 is submitted
+  // before step N's token is awaited (depth 2 by default), each step reading
+  // the previous step's token and position on the device. Stops after
+  // maxTokens, at the last position the cache holds, or at a token in
+  // opts.stopTokens, which is not returned (isHardStop, :2092-2101; a step
+  // already in flight behind it completes and its token is dropped).
+  // Resolves to the generated tokens in order.
+  async generate(token, position, maxTokens, opts) {
+    const o = opts || {};
+    const depth = Math.max(1, o.depth || 2);
+    const stop = new Set(o.stopTokens || []);
+    const steps = Math.max(0, Math.min(maxTokens, this.maxSeqLen - 1 - position));
+    if (!this.fusedGraph) this.fusedGraph = this.captureFusedStep();
+    this.setToken(token);
+    this.setPosition(position);
+    const out = [];
+    const inflight = [];
+    let stopped = false;
+    const take = (t) => {
+      if (stopped) return;
+      if (stop.has(t)) stopped = true;
+      else out.push(t);
+    };
+    for (let i = 0; i < steps && !stopped; i++) {
+      this.g.graphLaunch(this.ctx, this.fusedGraph);
+      inflight.push(this.readTokenAsync());
+      if (inflight.length >= depth) take(await inflight.shift());
+    }
+    while (inflight.length) take(await inflight.shift());
+    return out;
   }
 
   readF32(name, count) {

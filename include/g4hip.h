@@ -90,6 +90,11 @@ int g4_download(g4_ctx* ctx, void* dst, const void* src, size_t bytes, size_t sr
 int g4_download_async(g4_ctx* ctx, void* dst, const void* src, size_t bytes, size_t src_offset,
                       g4_event** ev);
 int g4_copy_d2d(g4_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Pinned (page-locked) host memory, the destination g4_download_async needs
+ * to complete without blocking the caller (the mapAsync staging buffer of
+ * src/engine.ts:1772-1787). g4_host_free takes what g4_host_alloc returned. */
+int g4_host_alloc(g4_ctx* ctx, size_t bytes, void** host);
+int g4_host_free(void* host);
 int g4_stream_sync(g4_ctx* ctx);
 /* Clears the kernel status word after a G4_ERR_STALLED (no counterpart in
  * the reference, see Conventions). The launch that stalled may still have
@@ -311,16 +316,18 @@ int g4_qkvAttnDecodePartials(g4_ctx* ctx, const float* x, const uint16_t* w1, co
                              const float* rope_cs, uint32_t rope_rows);
 /* The attention output projection of src/engine.ts:1585-1589
  * (matmulQuant of attn_output by W_o, Q4_K [M][8 * 256]) over the chunk
- * partials g4_qkvAttnDecodePartials left in the workspace, split by head:
- * output[h][M] = W_o[:, 256 h .. 256 h + 255] . o_h, o_h the attention
- * output of head h (its chunks merged as attn_output.wgsl sums over all
- * positions). o = sum over h of output[h], which
- * g4_normAddPartsGateUpGeluDigits_q4k adds in head order. Also clears the
+ * partials g4_qkvAttnDecodePartials left in the workspace, split into
+ * G4_O_SHARES groups of 8 / G4_O_SHARES heads:
+ * output[g][M] = sum over the group's heads h of W_o[:, 256 h .. 256 h + 255] . o_h,
+ * o_h the attention output of head h (its chunks merged as attn_output.wgsl
+ * sums over all positions). o = sum over g of output[g], which
+ * g4_normAddPartsGateUpGeluDigits_q4k adds in group order. Also clears the
  * workspace's staged q/k/v. */
+#define G4_O_SHARES 4
 int g4_attnHeadsMatmul_q4k(g4_ctx* ctx, void* workspace, size_t workspace_bytes, g4_attn_fused_params p,
                            const uint32_t* position_dev, const void* weight, float* output, uint32_t M);
-/* g4_normAddGateUpGeluDigits_q4k with o given as 8 per-head shares
- * o_parts[8][N] (g4_attnHeadsMatmul_q4k's output), added in head order
+/* g4_normAddGateUpGeluDigits_q4k with o given as G4_O_SHARES shares
+ * o_parts[G4_O_SHARES][N] (g4_attnHeadsMatmul_q4k's output), added in order
  * before the post-attention norm-add (src/engine.ts:1590-1602). */
 int g4_normAddPartsGateUpGeluDigits_q4k(g4_ctx* ctx, const float* o_parts, const uint16_t* w_post,
                                         const float* residual, const uint16_t* w_pre, const void* w_gate,

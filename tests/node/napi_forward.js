@@ -17,6 +17,8 @@
 // cfg.fused: three steps of the fused MI355X step (encodeFusedStep twice,
 // then captureFusedStep replayed once). Writes
 // <dir>/out.bin: per forward hidden f32[H], logits f32[V], token u32.
+// With cfg.generate = n: HipBackend.generate's pipelined greedy loop for n
+// tokens at depth 2 and again at depth 1; out.bin: the u32 tokens of both.
 const fs = require('fs');
 const path = require('path');
 
@@ -72,7 +74,23 @@ function collect(i) {
 }
 
 const P = cfg.position;
-if (cfg.fused) {
+if (cfg.generate) {
+  // greedy generation with the pipelined loop (depth 2: step N + 1 submitted
+  // before step N's token is awaited), then again from the same token and
+  // position with depth 1; out.bin: u32 tokens of both runs
+  (async () => {
+    const t2 = await be.generate(cfg.token, P, cfg.generate, { depth: 2 });
+    const t1 = await be.generate(cfg.token, P, cfg.generate, { depth: 1 });
+    console.log('[napi] generate depth 2: ' + t2.join(' ') + '; depth 1: ' + t1.join(' '));
+    fs.writeFileSync(path.join(dir, 'out.bin'), Buffer.from(new Uint32Array(t2.concat(t1)).buffer));
+    be.close();
+    console.log('[napi] done (generate)');
+    process.exit(0);
+  })().catch((e) => {
+    console.error(e);
+    process.exit(1);
+  });
+} else if (cfg.fused) {
   // the fused MI355X step: twice eagerly (the second from the token the first
   // sampled, both at the device position the steps advance), then captured
   // once and replayed
@@ -93,6 +111,7 @@ if (cfg.fused) {
   console.log('[napi] done (fused step)');
   process.exit(0);
 }
+if (!cfg.generate && !cfg.fused) {
 be.forward(cfg.token, P);
 collect(1);
 be.encodeTransformerPass(null, P + 1, false);
@@ -111,3 +130,4 @@ if (pos !== P + 3) throw new Error('device position ' + pos + ', expected ' + (P
 fs.writeFileSync(path.join(dir, 'out.bin'), Buffer.concat(outs));
 be.close();
 console.log('[napi] done');
+}

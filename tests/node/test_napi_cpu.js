@@ -17,7 +17,7 @@ function check(name, fn) {
 }
 
 const KEYS = ['version', 'lastError', 'init', 'destroy', 'deviceInfo', 'alloc', 'free', 'memset', 'upload',
-  'download', 'sync', 'graphBegin', 'graphEnd', 'graphLaunch', 'graphDestroy', 'fill', 'matmulQuant',
+  'download', 'downloadAsync', 'eventRecord', 'eventQuery', 'eventWait', 'eventDestroy', 'sync', 'graphBegin', 'graphEnd', 'graphLaunch', 'graphDestroy', 'fill', 'matmulQuant',
   'matmulQuantMR4', 'kvCacheStore', 'attnScore', 'softmax', 'attnOutput', 'attnDecodeWorkspaceSize', 'attnDecode',
   'perHeadRmsNormNoWeight', 'fusedPerHeadNormRope', 'rmsNorm', 'fusedNormAdd', 'geluMul', 'logitSoftcap',
   'embeddingLookup', 'argmax', 'topk256', 'advancePosition', 'pleStage1Fuse', 'pleGeluMul', 'pleSkipScaleAdd',
@@ -345,3 +345,68 @@ check('the fused step: launch order, prologue chaining, format groups, PLE and t
 });
 
 console.log('all node CPU checks passed');
+
+// generate(): step N + 1 is submitted before step N's token is awaited
+// (src/engine.ts:2041-2124 depth 2); each readback resolves on a later turn
+// of the event loop, as a real one completes off the loop.
+async function checkPipelinedGenerate() {
+  const C = hb.e2bConfig();
+  const m = mockAddon();
+  const be = new hb.HipBackend(m, 'ctx', C, { maxSeqLen: 4096 });
+  be.allocate();
+  be.fusedGraph = 'graph';  // (capture is checked by the fused-step checks)
+  const log = [];
+  let n = 0;
+  m.graphLaunch = (ctx, g) => {
+    assert.strictEqual(g, 'graph');
+    log.push('launch');
+  };
+  const tokenAt = (i) => (i === 2 ? 1 : 100 + i);
+  m.downloadAsync = (ctx, src, bytes) => {
+    assert.strictEqual(src, be.workBuffers.argmaxResult);
+    assert.strictEqual(bytes, 4);
+    const i = n++;
+    log.push('read' + i);
+    return new Promise((resolve) => setImmediate(() => {
+      log.push('done' + i);
+      const b = Buffer.alloc(4);
+      b.writeUInt32LE(tokenAt(i), 0);
+      resolve(b);
+    }));
+  };
+  let toks = await be.generate(7, 600, 4);
+  assert.deepStrictEqual(toks, [100, 101, 1, 103]);
+  assert.deepStrictEqual(log, ['launch', 'read0', 'launch', 'read1', 'done0', 'launch', 'read2', 'done1', 'launch',
+    'read3', 'done2', 'done3']);
+  const uploads = m.calls.filter((c) => c[0] === 'upload');
+  assert.deepStrictEqual(Array.from(uploads[uploads.length - 2][3]), [7]);    // the first token
+  assert.deepStrictEqual(Array.from(uploads[uploads.length - 1][3]), [600]);  // its position
+  console.log('ok generate pipelines depth 2');
+  // a stop token: not returned; the step in flight behind it completes, its token is dropped
+  log.length = 0;
+  n = 0;
+  toks = await be.generate(7, 600, 10, { stopTokens: [1] });
+  assert.deepStrictEqual(toks, [100, 101]);
+  assert.deepStrictEqual(log, ['launch', 'read0', 'launch', 'read1', 'done0', 'launch', 'read2', 'done1', 'launch',
+    'read3', 'done2', 'done3']);
+  console.log('ok generate stops at a stop token');
+  // depth 1: each token is awaited before the next step is submitted
+  log.length = 0;
+  n = 0;
+  toks = await be.generate(7, 600, 2, { depth: 1 });
+  assert.deepStrictEqual(toks, [100, 101]);
+  assert.deepStrictEqual(log, ['launch', 'read0', 'done0', 'launch', 'read1', 'done1']);
+  console.log('ok generate depth 1');
+  // no step past the cache's last position
+  log.length = 0;
+  n = 0;
+  toks = await be.generate(7, 4093, 10);
+  assert.deepStrictEqual(toks, [100, 101]);
+  assert.strictEqual(log.filter((e) => e === 'launch').length, 2);
+  console.log('ok generate stops at the cache capacity');
+}
+
+checkPipelinedGenerate().catch((e) => {
+  console.error(e);
+  process.exit(1);
+});

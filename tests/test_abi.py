@@ -90,3 +90,12 @@ def test_splitmix64_matches_oracle():
 
     for seed, idx in [(0, 0), (1234567, 3), (2 ** 63 + 5, 10 ** 12)]:
         assert g4hip.device.splitmix64(seed, idx) == O.splitmix64(seed, idx)
+
+
+def test_header_constants_match_the_python_host():
+    """Status codes and the o projection's share count, as the header defines them."""
+    text = open(HEADER).read()
+    defs = dict(re.findall(r"^#define\s+(G4_\w+)\s+\(?(-?\d+)\)?", text, re.M))
+    assert int(defs["G4_O_SHARES"]) == _lib.O_SHARES
+    for code, name in _lib.ERRORS.items():
+        assert int(defs[name]) == code, name

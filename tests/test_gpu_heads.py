@@ -2,15 +2,16 @@
 
 g4_qkvAttnDecodePartials runs the q/k/v matvec and the attention block in
 one launch whose attention workgroups end after storing their chunk partials;
-g4_attnHeadsMatmul_q4k merges each head's chunks and multiplies the head's
-256 input columns of W_o (out[h] = W_o[:, 256h:256h+256] . o_h); and
-g4_normAddPartsGateUpGeluDigits_q4k adds the 8 shares in head order before
+g4_attnHeadsMatmul_q4k merges each head's chunks and multiplies the heads of
+each group with their input columns of W_o (out[g] = sum over the group's
+heads h of W_o[:, 256h:256h+256] . o_h); and
+g4_normAddPartsGateUpGeluDigits_q4k adds the O_SHARES shares in order before
 the post-attention norm-add (src/engine.ts:1550-1602 is the sequence these
 three launches compute).
 
-Checked against the oracle at rel-L2 1e-3 / cosine 0.9999: every head's
-share against the oracle's matvec of that head's attention output, and their
-sum against the oracle's o projection; q/k/v and the stored K/V rows equal
+Checked against the oracle at rel-L2 1e-3 / cosine 0.9999: every share
+against the oracle's matvec of its heads' attention output, and their sum
+against the oracle's o projection; q/k/v and the stored K/V rows equal
 the one-launch form with the merge (g4_qkvAttnDecodeFusedWarm) bit for bit;
 the gate/up over the shares equals the gate/up over their in-order f32 sum
 bit for bit. Repeated calls on one workspace (the heads launch clears the
@@ -22,7 +23,7 @@ import pytest
 
 import g4hip
 import oracle as O
-from g4hip._lib import G4Error
+from g4hip._lib import O_SHARES, G4Error
 from gpu_util import assert_close, bits_equal
 from test_gpu_qkv_attn import H, HD, NQH, _setup
 
@@ -34,9 +35,13 @@ def _wo(ctx, seed):
     return W, ctx.from_numpy(W)
 
 
-def _head_blocks(W, h):
-    """Super-block h of every row of W_o [H][8 * 256] (Q4_K): the head's columns."""
-    return np.ascontiguousarray(W.reshape(H, NQH, 144)[:, h, :]).reshape(-1)
+HPS = NQH // O_SHARES  # heads per share
+
+
+def _group_blocks(W, g):
+    """Super-blocks HPS g .. HPS g + HPS - 1 of every row of W_o [H][8 * 256]
+    (Q4_K): the columns of the heads of share g."""
+    return np.ascontiguousarray(W.reshape(H, NQH, 144)[:, HPS * g:HPS * (g + 1), :]).reshape(-1)
 
 
 def _run(ctx, S, ws, dwo, pos, cap, partials):
@@ -46,11 +51,11 @@ def _run(ctx, S, ws, dwo, pos, cap, partials):
     h_out = ctx.empty(H, np.float32)
     pdev = ctx.from_numpy(np.array([pos], np.uint32))
     if partials:
-        parts = ctx.empty(NQH * H, np.float32)
+        parts = ctx.empty(O_SHARES * H, np.float32)
         ctx.qkvAttnDecodePartials(dev["x"], dev["w1"], dev["res"], None, dev["w2"], h_out, W[:3], [q, k, v], H, 1e-6,
                                   dev["qn"], dev["kn"], table, dk, dv, p, ws, pdev, regions, rope, cap)
         ctx.attnHeadsMatmul_q4k(ws, p, pdev, dwo, parts, H)
-        return {"parts": parts.download(np.float32).reshape(NQH, H), "k": dk.download(np.uint16),
+        return {"parts": parts.download(np.float32).reshape(O_SHARES, H), "k": dk.download(np.uint16),
                 "v": dv.download(np.uint16), "q": q.download(np.float32), "h": h_out.download(np.float32)}
     out = ctx.empty(NQH * HD, np.float32)
     ctx.qkvAttnDecodeFusedWarm(dev["x"], dev["w1"], dev["res"], None, dev["w2"], h_out, W[:3], [q, k, v], H, 1e-6,
@@ -74,13 +79,13 @@ def test_heads_match_oracle_and_merged_form(ctx, pos, window, cap):
         got = _run(ctx, S, ws_p, dwo, pos, cap, True)
         for key in ("q", "k", "v", "h"):
             assert bits_equal(got[key], merged[key]), (rep, key)
-        for h in range(NQH):
-            assert_close(got["parts"][h], O.matmul(attn[h], _head_blocks(W, h), H, HD, "q4k"),
-                         what=f"head {h} share, pos {pos} window {window}")
+        for g in range(O_SHARES):
+            assert_close(got["parts"][g], O.matmul(attn[HPS * g:HPS * (g + 1)].reshape(-1), _group_blocks(W, g), H,
+                                                   HPS * HD, "q4k"), what=f"share {g}, pos {pos} window {window}")
         total = got["parts"].astype(np.float32)
         acc = total[0].copy()
-        for h in range(1, NQH):
-            acc = (acc + total[h]).astype(np.float32)
+        for g in range(1, O_SHARES):
+            acc = (acc + total[g]).astype(np.float32)
         assert_close(acc, O.matmul(merged["attn"], W, H, NQH * HD, "q4k"), what=f"o, pos {pos} window {window}")
     for w in S[2]:
         w.free()
@@ -88,10 +93,10 @@ def test_heads_match_oracle_and_merged_form(ctx, pos, window, cap):
 
 def test_gate_up_over_shares_equals_over_their_sum(ctx):
     I = 6144
-    parts = O.gen_normal_f32(61, NQH * H, 0.0, 0.3).reshape(NQH, H)
+    parts = O.gen_normal_f32(61, O_SHARES * H, 0.0, 0.3).reshape(O_SHARES, H)
     acc = parts[0].copy()
-    for h in range(1, NQH):
-        acc = (acc + parts[h]).astype(np.float32)
+    for g in range(1, O_SHARES):
+        acc = (acc + parts[g]).astype(np.float32)
     res = O.gen_normal_f32(62, H)
     w_post, w_pre = O.gen_normal_f16(63, H, 1.0, 0.1), O.gen_normal_f16(64, H, 1.0, 0.1)
     Wg, Wu = O.gen_q4k(65, I * H // 256), O.gen_q4k(66, I * H // 256)
@@ -126,7 +131,7 @@ def test_heads_after_expired_hand_off_are_nan():
         host, dev, W, table, rope, p, regions = S
         _, dwo = _wo(ctx, 32)
         ws = ctx.zeros(ctx.attn_fused_workspace_bytes(p), np.uint8)
-        parts = ctx.empty(NQH * H, np.float32)
+        parts = ctx.empty(O_SHARES * H, np.float32)
         pdev = ctx.from_numpy(np.array([pos], np.uint32))
         qkv = [ctx.empty(NQH * HD, np.float32), ctx.empty(HD, np.float32), ctx.empty(HD, np.float32)]
         dk, dv = ctx.from_numpy(host["k"]), ctx.from_numpy(host["v"])
@@ -165,6 +170,6 @@ def test_partials_entry_rejects_shapes_without_the_one_launch(ctx):
                                   p, ws, pdev, regions, rope, cap)
     _, dwo = _wo(ctx, 42)
     with pytest.raises(G4Error, match="long attention form"):
-        ctx.attnHeadsMatmul_q4k(ws, p, pdev, dwo, ctx.empty(NQH * H, np.float32), H)
+        ctx.attnHeadsMatmul_q4k(ws, p, pdev, dwo, ctx.empty(O_SHARES * H, np.float32), H)
     for w in S[2]:
         w.free()

@@ -171,3 +171,37 @@ def test_node_backend_forwards_vs_oracle(fused):
         assert got_tok == O.argmax(logits)
         assert lg_ref[got_tok] >= lg_ref.max() - 1e-3 * np.abs(lg_ref).max()
         tok = got_tok
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="no node binary")
+def test_node_backend_pipelined_generate_vs_oracle():
+    """HipBackend.generate on the GPU: the reference's depth-2 loop
+    (src/engine.ts:2041-2124: step N + 1 submitted before step N's token is
+    read back, asynchronously) gives the same tokens as the depth-1 loop, and
+    each token is a maximum of the oracle's logits for the step that the
+    previous token starts (within the logits' tolerance)."""
+    N = 6
+    shape = E2BShape.real(n_layers=4, n_unshared=2, global_layers=(1, 3), vocab=4096)
+    files, formats, hm, kcs, vcs = _model(shape)
+    cfg = {"overrides": {"num_layers": 4, "num_unshared_layers": 2, "global_layers": [1, 3], "vocab_size": 4096},
+           "maxSeqLen": MAX_SEQ, "position": POS, "token": TOKEN, "formats": formats, "generate": N}
+    with tempfile.TemporaryDirectory() as d:
+        for name, arr in files.items():
+            np.ascontiguousarray(arr).tofile(os.path.join(d, name + ".bin"))
+        with open(os.path.join(d, "config.json"), "w") as f:
+            json.dump(cfg, f)
+        print("[napi] running the Node generate loop", flush=True)
+        r = subprocess.run(["node", os.path.join(ROOT, "tests", "node", "napi_forward.js"), d], capture_output=True,
+                           text=True, timeout=240)
+        print(r.stdout, r.stderr, flush=True)
+        assert r.returncode == 0, r.stderr
+        toks = np.fromfile(os.path.join(d, "out.bin"), np.uint32)
+    assert toks.size == 2 * N
+    assert np.array_equal(toks[:N], toks[N:]), "depth 2 and depth 1 differ"
+    tok = TOKEN
+    for i in range(N):
+        _, lg = hm.step(hm.embed(tok), kcs, vcs, POS + i, token=tok)
+        got = int(toks[i])
+        print(f"[napi] generate step {i}: in {tok}, out {got}, oracle argmax {O.argmax(lg)}", flush=True)
+        assert lg[got] >= lg.max() - 1e-3 * np.abs(lg).max(), i
+        tok = got
