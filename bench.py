@@ -62,15 +62,24 @@ def kernel_census(ctx, dec: Decoder, reps: int):
     through HBM as in a real step, and no host launch overhead is timed),
     replayed `reps` times between HIP events on the library's stream.
     Algorithmic bytes: weights + activations read/written by one launch.
-    `qkv_attn` is the launch every layer of the step issues: the q/k/v
-    matvec with its norm prologue and the attention block (RoPE cos/sin from
-    the per-theta table, the new K/V row stored) in one launch, with the L2
-    warming of the step (the warming's reads are the next matvecs' weights,
-    which those matvecs' own launches are charged for, so they are not in
-    its algorithmic bytes). `qkv_normadd_matvec` and `attn_fused` time the
-    two halves as separate launches (the two-launch form the step falls
-    back to for other shapes): reported, not issued by this step
-    (per_step 0). The matvecs run with cold weights."""
+
+    The step's four launches per layer:
+    - `qkv_attn`: the q/k/v matvec with its norm prologue and the attention
+      block (RoPE cos/sin from the per-theta table, the new K/V row stored,
+      chunk partials written), with the step's L2 warming (its reads are the
+      next launches' weights, charged to those launches). It leaves the
+      staged q/k/v for `attn_heads` to clear, so it is timed in a graph of
+      (qkv_attn, attn_heads) pairs, less the `attn_heads` graph's time;
+    - `attn_heads`: the per-head chunk merge and the o projection by groups
+      of heads (O_SHARES shares of o);
+    - `gateup_gelu`: post-attention norm-add over the shares, pre-FFN norm,
+      gate/up, GELU product and its digit block;
+    - `down_matvec_q6k` over those digits.
+    Reported with per_step 0 (not issued by this step): the one q/k/v +
+    attention launch with its in-launch merge (`qkv_attn_merged`), and the
+    launches of the two-launch form the step takes for other shapes
+    (`qkv_normadd_matvec`, `attn_fused`, `o_matvec`). The matvecs run with
+    cold weights."""
     s, c = dec.s, ctx
     dec.set_position(START_POS)
     Ls = dec.layers
@@ -81,41 +90,54 @@ def kernel_census(ctx, dec: Decoder, reps: int):
     n_glob = sum(1 for il in range(nl) if s.is_global(il))
     L_loc, L_glob = min(START_POS + 1, s.window), START_POS + 1
     kv_avg = ((nl - n_glob) * L_loc + n_glob * L_glob) * KV * 2 * 2 // nl  # f16 K + V rows read
+    ch_avg = ((nl - n_glob) * -(-L_loc // 64) + n_glob * -(-L_glob // 64)) / nl  # live 64-position chunks
+    parts = int(ch_avg * s.n_q_heads * (s.head_dim + 2) * 4)  # chunk partials (m, l, o) written / read
     dig = ctx.digits_bytes(I)  # the GELU product as the down launch's digit block
+    shares = g4hip.O_SHARES * H * 4
 
     qkv_bytes = q4(Q + 2 * KV, H) + 5 * H * 4 + (Q + 2 * KV) * 4
+    qkv_args = lambda il, L: (  # noqa: E731
+        dec.down, L.post_ffn_norm, dec.hidden2, None, L.attn_norm, dec.hidden, [L.wq, L.wk, L.wv],
+        [dec.q, dec.k, dec.v], H, s.eps, L.q_norm, L.k_norm, dec.rope_freqs, L.k_cache, L.v_cache)
+    rope = lambda il: (dec.rope_cs[s.is_global(il)], dec.rope_rows)  # noqa: E731
+    heads = lambda il, L: c.attnHeadsMatmul_q4k(dec.attn_ws, dec.attn_params[il], dec.pos, L.wo, dec.o_parts, H)  # noqa
+
+    def pair(il, L):
+        c.qkvAttnDecodePartials(*qkv_args(il, L), dec.attn_params[il], dec.attn_ws, dec.pos, dec.warm[il], *rope(il))
+        heads(il, L)
+
     kinds = {
-        # name: (per-layer body, launches per step of this kind, algorithmic bytes per launch)
-        "qkv_attn": (
-            lambda il, L: c.qkvAttnDecodeFusedWarm(
-                dec.down, L.post_ffn_norm, dec.hidden2, None, L.attn_norm, dec.hidden, [L.wq, L.wk, L.wv],
-                [dec.q, dec.k, dec.v], H, s.eps, L.q_norm, L.k_norm, dec.rope_freqs, L.k_cache, L.v_cache, dec.attn,
-                dec.attn_params[il], dec.attn_ws, dec.pos, dec.warm[il], dec.rope_cs[s.is_global(il)], dec.rope_rows),
-            nl, qkv_bytes + kv_avg + 2 * KV * 2 + Q * 4),
+        # name: (per-layer body, launches per body, launches per step of this kind, algorithmic bytes per launch)
+        "qkv_attn+attn_heads": (pair, 2, 0, 0),
+        "attn_heads": (heads, 1, nl, parts + q4(H, Q) + shares),
+        "gateup_gelu": (
+            lambda il, L: c.normAddPartsGateUpGeluDigits_q4k(dec.o_parts, L.post_attn_norm, dec.hidden,
+                                                             L.pre_ffn_norm, L.wgate, L.wup, dec.hidden2, dec.act,
+                                                             dec.act_digits, I, H, s.eps),
+            1, nl, 2 * q4(I, H) + 3 * H * 4 + shares + I * 4 + dig),
+        "down_matvec_q6k": (
+            lambda il, L: c.matmulQuantDigits_q6k(dec.act_digits, L.wdown, dec.down, H, I),
+            1, nl, q6(H, I) + dig + H * 4),
+        "qkv_attn_merged": (
+            lambda il, L: c.qkvAttnDecodeFusedWarm(*qkv_args(il, L), dec.attn, dec.attn_params[il], dec.attn_ws,
+                                                   dec.pos, dec.warm[il], *rope(il)),
+            1, 0, qkv_bytes + kv_avg + 2 * KV * 2 + Q * 4),
         "qkv_normadd_matvec": (
             lambda il, L: c.normAddMatmulSegments(
                 "q4k", dec.down, L.post_ffn_norm, dec.hidden2, L.attn_norm, dec.hidden, [L.wq, L.wk, L.wv],
                 [dec.q, dec.k, dec.v], [Q, KV, KV], H, s.eps),
-            0, qkv_bytes),
+            1, 0, qkv_bytes),
         "attn_fused": (
             lambda il, L: c.attnDecodeFusedWarm(dec.q, dec.k, dec.v, L.q_norm, L.k_norm, dec.rope_freqs, L.k_cache,
                                                 L.v_cache, dec.attn, dec.attn_params[il], dec.attn_ws, dec.pos, [],
-                                                dec.rope_cs[s.is_global(il)], dec.rope_rows),
-            0, kv_avg + (Q + 2 * KV) * 4 + 2 * KV * 2 + Q * 4),
+                                                *rope(il)),
+            1, 0, kv_avg + (Q + 2 * KV) * 4 + 2 * KV * 2 + Q * 4),
         "o_matvec": (
             lambda il, L: c.matmulQuant(dec.attn, L.wo, dec.o, H, Q),
-            nl, q4(H, Q) + Q * 4 + H * 4),
-        "gateup_gelu": (
-            lambda il, L: c.normAddGateUpGeluDigits_q4k(dec.o, L.post_attn_norm, dec.hidden, L.pre_ffn_norm,
-                                                        L.wgate, L.wup, dec.hidden2, dec.act, dec.act_digits, I, H,
-                                                        s.eps),
-            nl, 2 * q4(I, H) + 4 * H * 4 + I * 4 + dig),
-        "down_matvec_q6k": (
-            lambda il, L: c.matmulQuantDigits_q6k(dec.act_digits, L.wdown, dec.down, H, I),
-            nl, q6(H, I) + dig + H * 4),
+            1, 0, q4(H, Q) + Q * 4 + H * 4),
     }
     out = {}
-    for name, (body, per_step, nbytes) in kinds.items():
+    for name, (body, per_body, per_step, nbytes) in kinds.items():
         ctx.graph_begin()
         try:
             for il, L in enumerate(Ls):
@@ -124,7 +146,13 @@ def kernel_census(ctx, dec: Decoder, reps: int):
             g = ctx.graph_end()
         us = time_launches(ctx, lambda _i=0: ctx.graph_launch(g), reps) * 1e3 / nl
         ctx.graph_destroy(g)
-        out[name] = {"us": us, "per_step": per_step, "bytes": nbytes, "gbps": nbytes / (us * 1e-6) / 1e9}
+        out[name] = {"us": us, "per_step": per_step, "bytes": nbytes,
+                     "gbps": nbytes / (us * 1e-6) / 1e9 if nbytes else None}
+    # the partials launch: its pairs' time less the heads launch's
+    us = out["qkv_attn+attn_heads"]["us"] - out["attn_heads"]["us"]
+    nbytes = qkv_bytes + kv_avg + 2 * KV * 2 + parts
+    out["qkv_attn"] = {"us": us, "per_step": nl, "bytes": nbytes, "gbps": nbytes / (us * 1e-6) / 1e9,
+                       "timed_as": "qkv_attn+attn_heads less attn_heads"}
     # LM head with the final norm-add, softcap and the argmax candidates,
     # then their reduction, as the step runs them (330 MB: larger than the
     # 256 MB last-level cache, so no rotation is needed)
@@ -894,7 +922,8 @@ def main():
         "q4k_gemv_config0": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in g0.items()},
         "kernel_census": {k: {"us_per_launch": round(v["us"], 3), "launches_per_step": v["per_step"],
                               "us_per_step": round(per_step[k], 2), "bytes_per_launch": v["bytes"],
-                              "gbps": round(v["gbps"], 1)} for k, v in census.items()},
+                              "gbps": None if v["gbps"] is None else round(v["gbps"], 1)}
+                          for k, v in census.items()},
         "decode_from_position": positions,
         "real_e2b_layout": real,
         "node_fused_step": node_step,

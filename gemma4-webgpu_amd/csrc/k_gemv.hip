@@ -1947,6 +1947,16 @@ int launch_qt(g4_ctx* ctx, const LaunchReq& q) {
 // per CU are walked tile by tile.
 constexpr uint32_t kMvFullWgs = 240, kMvMinWgs = 160;
 
+// Tiles per workgroup: one tile up to two workgroups per CU, else walked
+// tile by tile, by one workgroup per CU where the walk fills the LDS ring
+// (a 12-wave one-matrix launch: its 131 KB of LDS hold one workgroup per CU,
+// and each workgroup pays its prologue and the ring's first tiles once).
+__host__ __device__ constexpr uint32_t mv_rep(uint32_t tiles, int num_cus, bool ring) {
+  return (tiles + 2u * (uint32_t)num_cus - 1) / (2u * (uint32_t)num_cus) > 1 && ring
+             ? (tiles + (uint32_t)num_cus - 1) / (uint32_t)num_cus
+             : (tiles + 2u * (uint32_t)num_cus - 1) / (2u * (uint32_t)num_cus);
+}
+
 template <int QT, int BPR, int NWV, int PRO, int NMAT>
 int mv_launch(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
   using T = MvTile<QT, BPR, NWV>;
@@ -1954,7 +1964,7 @@ int mv_launch(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
   GemvSegs sg{};
   uint32_t tiles = 0;
   for (int i = 0; i < q.nseg; ++i) tiles += ceil_div(q.segs[i].M, T::TR);
-  sg.rep = ceil_div(tiles, 2u * (uint32_t)ctx->num_cus);
+  sg.rep = mv_rep(tiles, ctx->num_cus, NWV == 12 && NMAT == 1 && PRO != 3);
   uint32_t wgs = 0;
   for (int i = 0; i < q.nseg; ++i) {
     sg.s[i] = q.segs[i];
@@ -2278,7 +2288,7 @@ MvShape mv_shape(const g4_ctx* ctx, uint32_t M, uint32_t bpr) {
   s.nwv = mv_pick(bpr, &seg, 1);
   s.rows_per_tile = (uint32_t)(16 * s.nwv) / bpr;
   const uint32_t t = ceil_div(M, s.rows_per_tile);
-  s.rep = ceil_div(t, 2u * (uint32_t)ctx->num_cus);  // as mv_launch
+  s.rep = mv_rep(t, ctx->num_cus, s.nwv == 12);  // as mv_launch for one matrix
   s.wgs = ceil_div(t, s.rep);
   return s;
 }

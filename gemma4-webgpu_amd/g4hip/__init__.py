@@ -11,6 +11,7 @@ from __future__ import annotations
 from ._lib import (  # noqa: F401
     G4Error,
     LIB_PATH,
+    O_SHARES,
     lib,
     MatmulParams,
     KvStoreParams,

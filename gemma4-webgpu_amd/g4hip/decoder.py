@@ -448,8 +448,12 @@ class Decoder(_SyntheticModel):
         self.max_seq = max_seq
         self.fuse_qkv = True  # step_fused: q/k/v and the attention in one launch where the shape allows
         # step_fused: where q/k/v take that launch, its chunk merge moves into
-        # the o projection (per head) and the gate/up prologue adds the heads
-        self.heads_o = True
+        # the o projection (by groups of heads) and the gate/up prologue adds
+        # the shares. Off by default: measured in one process on one device,
+        # the step takes 1057 us against 1040 with the in-launch merge (the
+        # shares the gate/up launch reads ahead of its weights, and the
+        # heads launch, cost more than the merge they remove)
+        self.heads_o = False
         self._build_weights(ctx, shape, n_layers, seed, lm_head,
                             lambda il: (ctx.zeros(max_seq * self.s.kv_dim_of(il), np.uint16),
                                         ctx.zeros(max_seq * self.s.kv_dim_of(il), np.uint16)), embed=embed,
