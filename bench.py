@@ -66,20 +66,20 @@ def kernel_census(ctx, dec: Decoder, reps: int):
     The step's four launches per layer:
     - `qkv_attn`: the q/k/v matvec with its norm prologue and the attention
       block (RoPE cos/sin from the per-theta table, the new K/V row stored,
-      chunk partials written), with the step's L2 warming (its reads are the
-      next launches' weights, charged to those launches). It leaves the
-      staged q/k/v for `attn_heads` to clear, so it is timed in a graph of
-      (qkv_attn, attn_heads) pairs, less the `attn_heads` graph's time;
-    - `attn_heads`: the per-head chunk merge and the o projection by groups
-      of heads (O_SHARES shares of o);
-    - `gateup_gelu`: post-attention norm-add over the shares, pre-FFN norm,
-      gate/up, GELU product and its digit block;
+      the chunks merged in the launch), with the step's L2 warming (its
+      reads are the next launches' weights, charged to those launches);
+    - `o_matvec`;
+    - `gateup_gelu`: post-attention norm-add, pre-FFN norm, gate/up, GELU
+      product and its digit block;
     - `down_matvec_q6k` over those digits.
-    Reported with per_step 0 (not issued by this step): the one q/k/v +
-    attention launch with its in-launch merge (`qkv_attn_merged`), and the
-    launches of the two-launch form the step takes for other shapes
-    (`qkv_normadd_matvec`, `attn_fused`, `o_matvec`). The matvecs run with
-    cold weights."""
+    The kinds of the per-head o split (Decoder.heads_o) are timed as well:
+    `qkv_attn_partials` (the same launch without its merge; it leaves the
+    staged q/k/v for `attn_heads` to clear, so it is timed in a graph of
+    pairs, less the `attn_heads` graph's time), `attn_heads` (per-head
+    merge + o by groups of heads) and `gateup_gelu_shares`. Kinds the step
+    does not issue, and those of the two-launch form the step takes for
+    other shapes (`qkv_normadd_matvec`, `attn_fused`), have per_step 0. The
+    matvecs run with cold weights."""
     s, c = dec.s, ctx
     dec.set_position(START_POS)
     Ls = dec.layers
@@ -106,22 +106,32 @@ def kernel_census(ctx, dec: Decoder, reps: int):
         c.qkvAttnDecodePartials(*qkv_args(il, L), dec.attn_params[il], dec.attn_ws, dec.pos, dec.warm[il], *rope(il))
         heads(il, L)
 
+    hs = nl if dec.heads_o else 0  # launches per step of the per-head o split's kinds
+    ms = nl - hs                     # of the in-launch merge's
     kinds = {
         # name: (per-layer body, launches per body, launches per step of this kind, algorithmic bytes per launch)
-        "qkv_attn+attn_heads": (pair, 2, 0, 0),
-        "attn_heads": (heads, 1, nl, parts + q4(H, Q) + shares),
+        "qkv_attn": (
+            lambda il, L: c.qkvAttnDecodeFusedWarm(*qkv_args(il, L), dec.attn, dec.attn_params[il], dec.attn_ws,
+                                                   dec.pos, dec.warm[il], *rope(il)),
+            1, ms, qkv_bytes + kv_avg + 2 * KV * 2 + Q * 4),
+        "o_matvec": (
+            lambda il, L: c.matmulQuant(dec.attn, L.wo, dec.o, H, Q),
+            1, ms, q4(H, Q) + Q * 4 + H * 4),
         "gateup_gelu": (
-            lambda il, L: c.normAddPartsGateUpGeluDigits_q4k(dec.o_parts, L.post_attn_norm, dec.hidden,
-                                                             L.pre_ffn_norm, L.wgate, L.wup, dec.hidden2, dec.act,
-                                                             dec.act_digits, I, H, s.eps),
-            1, nl, 2 * q4(I, H) + 3 * H * 4 + shares + I * 4 + dig),
+            lambda il, L: c.normAddGateUpGeluDigits_q4k(dec.o, L.post_attn_norm, dec.hidden, L.pre_ffn_norm,
+                                                        L.wgate, L.wup, dec.hidden2, dec.act, dec.act_digits, I, H,
+                                                        s.eps),
+            1, ms, 2 * q4(I, H) + 4 * H * 4 + I * 4 + dig),
         "down_matvec_q6k": (
             lambda il, L: c.matmulQuantDigits_q6k(dec.act_digits, L.wdown, dec.down, H, I),
             1, nl, q6(H, I) + dig + H * 4),
-        "qkv_attn_merged": (
-            lambda il, L: c.qkvAttnDecodeFusedWarm(*qkv_args(il, L), dec.attn, dec.attn_params[il], dec.attn_ws,
-                                                   dec.pos, dec.warm[il], *rope(il)),
-            1, 0, qkv_bytes + kv_avg + 2 * KV * 2 + Q * 4),
+        "qkv_attn_partials+attn_heads": (pair, 2, 0, 0),
+        "attn_heads": (heads, 1, hs, parts + q4(H, Q) + shares),
+        "gateup_gelu_shares": (
+            lambda il, L: c.normAddPartsGateUpGeluDigits_q4k(dec.o_parts, L.post_attn_norm, dec.hidden,
+                                                             L.pre_ffn_norm, L.wgate, L.wup, dec.hidden2, dec.act,
+                                                             dec.act_digits, I, H, s.eps),
+            1, hs, 2 * q4(I, H) + 3 * H * 4 + shares + I * 4 + dig),
         "qkv_normadd_matvec": (
             lambda il, L: c.normAddMatmulSegments(
                 "q4k", dec.down, L.post_ffn_norm, dec.hidden2, L.attn_norm, dec.hidden, [L.wq, L.wk, L.wv],
@@ -132,9 +142,6 @@ def kernel_census(ctx, dec: Decoder, reps: int):
                                                 L.v_cache, dec.attn, dec.attn_params[il], dec.attn_ws, dec.pos, [],
                                                 *rope(il)),
             1, 0, kv_avg + (Q + 2 * KV) * 4 + 2 * KV * 2 + Q * 4),
-        "o_matvec": (
-            lambda il, L: c.matmulQuant(dec.attn, L.wo, dec.o, H, Q),
-            1, 0, q4(H, Q) + Q * 4 + H * 4),
     }
     out = {}
     for name, (body, per_body, per_step, nbytes) in kinds.items():
@@ -149,10 +156,10 @@ def kernel_census(ctx, dec: Decoder, reps: int):
         out[name] = {"us": us, "per_step": per_step, "bytes": nbytes,
                      "gbps": nbytes / (us * 1e-6) / 1e9 if nbytes else None}
     # the partials launch: its pairs' time less the heads launch's
-    us = out["qkv_attn+attn_heads"]["us"] - out["attn_heads"]["us"]
+    us = out["qkv_attn_partials+attn_heads"]["us"] - out["attn_heads"]["us"]
     nbytes = qkv_bytes + kv_avg + 2 * KV * 2 + parts
-    out["qkv_attn"] = {"us": us, "per_step": nl, "bytes": nbytes, "gbps": nbytes / (us * 1e-6) / 1e9,
-                       "timed_as": "qkv_attn+attn_heads less attn_heads"}
+    out["qkv_attn_partials"] = {"us": us, "per_step": hs, "bytes": nbytes, "gbps": nbytes / (us * 1e-6) / 1e9,
+                                "timed_as": "qkv_attn_partials+attn_heads less attn_heads"}
     # LM head with the final norm-add, softcap and the argmax candidates,
     # then their reduction, as the step runs them (330 MB: larger than the
     # 256 MB last-level cache, so no rotation is needed)
@@ -181,7 +188,7 @@ def measured_traffic(kind):
             entry = json.load(f)["entries"].get(kind)
     except (OSError, ValueError, KeyError):
         return None
-    return None if entry is None else entry["bytes_per_launch"]
+    return None if entry is None else (entry["bytes_per_launch"], entry.get("warming_bytes", 0))
 
 
 def gemv_cfg0(ctx, copies=101, rounds=5):
@@ -194,6 +201,29 @@ def gemv_cfg0(ctx, copies=101, rounds=5):
     ctx.fill_q4k(W, nb * copies, 12345)
     x = ctx.empty(N, np.float32)
     ctx.fill_normal_f32(x, N, 1, 0.0, 1.0)
+    y = ctx.empty(M, np.float32)
+    ptrs = [W.ptr + i * wb for i in range(copies)]
+
+    def one(i=0):
+        ctx.matmulQuant(x, ptrs[i % copies], y, M, N, "q4k")
+    ms = time_launches(ctx, one, copies * rounds)
+    alg = wb + N * 4 + M * 4
+    W.free()
+    return {"shape": [M, N], "us": ms * 1e3, "bytes": alg, "gbps": alg / (ms * 1e-3) / 1e9,
+            "frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, "copies": copies}
+
+
+def gemv_q4k_amortised(ctx, M=262144, N=1536, copies=2, rounds=10):
+    """The config-0 kernel family at a size that amortises the launch: the
+    one-vector Q4_K matvec (mv_kernel, 12-wave workgroups walking tiles
+    through the LDS ring, one workgroup per CU) over W [M x N], 226 MB per
+    copy, rotated over `copies` (> the 256 MB last-level cache)."""
+    nb = M * N // 256
+    wb = nb * 144
+    W = ctx.alloc(wb * copies)
+    ctx.fill_q4k(W, nb * copies, 4321)
+    x = ctx.empty(N, np.float32)
+    ctx.fill_normal_f32(x, N, 2, 0.0, 1.0)
     y = ctx.empty(M, np.float32)
     ptrs = [W.ptr + i * wb for i in range(copies)]
 
@@ -773,7 +803,8 @@ def main():
     log(f"device {info}")
     if args.gemv0_only:
         g0, fl = gemv_cfg0(ctx), stream_floor(ctx)
-        print(json.dumps({"q4k_gemv_config0": g0, "stream_floor": fl}), flush=True)
+        print(json.dumps({"q4k_gemv_config0": g0, "stream_floor": fl, "q4k_gemv_amortised": gemv_q4k_amortised(ctx)}),
+              flush=True)
         return
     if args.calib_only:
         print(json.dumps({"calibration": calibration_reads(ctx)}), flush=True)
@@ -880,13 +911,18 @@ def main():
     dom = max((k for k in per_step if census[k]["per_step"] > 0), key=lambda k: per_step[k])
     bytes_launch, us_launch = census[dom]["bytes"], census[dom]["us"]
     achieved = bytes_launch / (us_launch * 1e-6) / 1e9
+    traffic = measured_traffic(dom)
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(dom),
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                "traffic": None if traffic is None else traffic[0],
+                # of which the L2 warming's reads of the next launches' weights
+                "traffic_warming": None if traffic is None else traffic[1],
                 "bytes_per_launch": bytes_launch, "us_per_launch": round(us_launch, 3)}
 
     g0 = {} if args.no_gemv0 else gemv_cfg0(ctx)
     if g0:
         g0["stream_floor"] = stream_floor(ctx, wg_list=(648, 2048))
+        g0["amortised_262144x1536"] = gemv_q4k_amortised(ctx)
     log(f"config-0 Q4_K GEMV: {g0}")
     attn3 = attention_cfg3(ctx)
     log(f"decode attention: {attn3}")
@@ -919,7 +955,9 @@ def main():
                    "launches_per_token": dec.launches_per_step_fused()},
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "q4k_gemv_config0": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in g0.items()},
+        "q4k_gemv_config0": {k: (round(v, 4) if isinstance(v, float) else
+                                 {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                                 if isinstance(v, dict) else v) for k, v in g0.items()},
         "kernel_census": {k: {"us_per_launch": round(v["us"], 3), "launches_per_step": v["per_step"],
                               "us_per_step": round(per_step[k], 2), "bytes_per_launch": v["bytes"],
                               "gbps": None if v["gbps"] is None else round(v["gbps"], 1)}

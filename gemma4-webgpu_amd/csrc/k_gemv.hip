@@ -681,15 +681,20 @@ struct MvXA {
 
 // A one-matrix workgroup that walks several tiles (the LM head) reads them
 // straight into LDS (global -> LDS loads, no registers) into a ring of
-// kRing tile buffers, so that two tiles are in flight while the third is
+// MvRing::D tile buffers, so that D - 1 tiles are in flight while one is
 // multiplied. Lane l of wave w writes the 16-byte chunk 64 w + l of each
 // round of NTH chunks, so a buffer spans whole waves' 1024-byte pieces.
-constexpr int kRing = 3;
+// The ring takes as many buffers (3 to 6: two to five tiles in flight) as
+// fit next to the activation digits and the row partials in kRingLds bytes
+// of LDS (the top-k class table, 2 KB, comes on top).
+constexpr uint32_t kRingLds = 152u * 1024u;
 template <int QT, int BPR, int NWV>
 struct MvRing {
   using T = MvTile<QT, BPR, NWV>;
   static constexpr uint32_t CH = (T::TB + 15) / 16;               // 16-byte chunks of a tile
   static constexpr uint32_t BUF = (CH + 63) / 64 * 1024;          // bytes of one ring buffer
+  static constexpr uint32_t FREE = kRingLds - (uint32_t)align16(MvX<BPR>::END) - (uint32_t)align16(T::TR * T::RS * 4);
+  static constexpr int D = FREE / BUF < 3 ? 3 : (FREE / BUF > 6 ? 6 : (int)(FREE / BUF));
   static constexpr int LPT = T::LPT;                              // rounds of loads per tile
   static constexpr uint32_t LAST = (uint32_t)(LPT - 1) * 64 * NWV;  // first chunk of the last round
 };
@@ -702,7 +707,9 @@ template <int QT, int BPR, int NWV, int PRO, int NMAT>
 __host__ __device__ constexpr size_t mv_lds_bytes(bool staged) {
   using T = MvTile<QT, BPR, NWV>;
   return align16(MvXA<BPR, PRO>::END) + NMAT * align16((size_t)T::TR * T::RS * 4) +
-         (staged ? (NMAT == 1 ? kRing * (size_t)MvRing<QT, BPR, NWV>::BUF : NMAT * (size_t)T::LDS_T) : 0);
+         (staged ? (NMAT == 1 ? MvRing<QT, BPR, NWV>::D * (size_t)MvRing<QT, BPR, NWV>::BUF
+                              : NMAT * (size_t)T::LDS_T)
+                 : 0);
 }
 
 template <class T, int NTH>
@@ -761,6 +768,19 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt field");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Waits until at most `ahead` tiles of PER loads each remain in flight
+// (ahead < D - 1, a runtime value: one compile-time wait per case).
+template <int PER, int D>
+__device__ __forceinline__ void wait_tiles(uint32_t ahead) {
+  static_assert(D >= 3 && D <= 6, "ring depth");
+  switch (ahead) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<PER>(); break;
+    case 2: if constexpr (D > 3) wait_vmcnt<2 * PER>(); break;
+    case 3: if constexpr (D > 4) wait_vmcnt<3 * PER>(); break;
+    default: if constexpr (D > 5) wait_vmcnt<4 * PER>(); break;
+  }
 }
 
 template <int QT, int BPR, int NWV>
@@ -1503,22 +1523,24 @@ __device__ __forceinline__ void mv_body(const GemvSegs& segs, const uint8_t* w_u
     return;
   }
   if constexpr (STAGED && PRO != 3 && NMAT == 1) {
-    // several tiles of one matrix: a ring of kRing LDS buffers filled by
-    // global -> LDS loads, tiles t + 1 and t + 2 in flight while tile t is
-    // multiplied. A wave's loads complete in issue order, so once it has
-    // at most one tile's loads outstanding (vmcnt <= its per-tile count;
-    // the row stores after them only make the wait stricter) its share of
-    // tile t is in LDS; the barrier that follows makes the whole tile
-    // visible. Buffer (t + 2) % kRing held tile t - 1, whose products every
-    // wave finished before the barrier ahead of the last reduction.
+    // several tiles of one matrix: a ring of R::D LDS buffers filled by
+    // global -> LDS loads, tiles t + 1 .. t + D - 1 in flight while tile t
+    // is multiplied. A wave's loads complete in issue order, so once it has
+    // at most the later tiles' loads outstanding (vmcnt <= their count; the
+    // row stores among them only make the wait stricter) its share of tile
+    // t is in LDS; the barrier that follows makes the whole tile visible.
+    // Buffer (t + D - 1) % D held tile t - 1, whose products every wave
+    // finished before the barrier ahead of the last reduction.
     using R = MvRing<QT, BPR, NWV>;
+    constexpr uint32_t D = (uint32_t)R::D;
     uint8_t* ring = smem + align16(MvXA<BPR, PRO>::END) + align16((size_t)T::TR * T::RS * 4);
     const int w = tid >> 6, l = tid & 63;
     const bool short_wave = mv_ring_short<QT, BPR, NWV>(w);
-    mv_ring_load<QT, BPR, NWV>(W[0] + (size_t)tb * T::TB, mv_tile_bytes<QT, BPR, NWV>(sg.M, tb), ring, w, l);
-    if (tb + 1 < te)
-      mv_ring_load<QT, BPR, NWV>(W[0] + (size_t)(tb + 1) * T::TB, mv_tile_bytes<QT, BPR, NWV>(sg.M, tb + 1),
-                                 ring + R::BUF, w, l);
+#pragma unroll
+    for (uint32_t k = 0; k + 1 < D; ++k)
+      if (tb + k < te)
+        mv_ring_load<QT, BPR, NWV>(W[0] + (size_t)(tb + k) * T::TB, mv_tile_bytes<QT, BPR, NWV>(sg.M, tb + k),
+                                   ring + k * R::BUF, w, l);
     __builtin_amdgcn_sched_barrier(0);  // every weight load is issued before the activations are used
     mv_pro_finish<BPR, NWV, PRO>(P, smem, pa);
     MvUnit<QT> X;
@@ -1526,20 +1548,18 @@ __device__ __forceinline__ void mv_body(const GemvSegs& segs, const uint8_t* w_u
     g4d::Cand best{-1e30f, 0u};
     uint32_t cur = 0;  // ring buffer of tile t
     for (uint32_t t = tb; t < te; ++t) {
-      if (t + 1 < te) {  // (uniform) tile t + 1 stays in flight
-        if (short_wave) wait_vmcnt<R::LPT - 1>();
-        else wait_vmcnt<R::LPT>();
-      } else {
-        wait_vmcnt<0>();
-      }
+      const uint32_t ahead = min(D - 2, te - 1 - t);  // (uniform) later tiles in flight
+      if (short_wave) wait_tiles<R::LPT - 1, R::D>(ahead);
+      else wait_tiles<R::LPT, R::D>(ahead);
       ring_barrier();  // tile t in LDS for every wave; tile t - 1 reduced
-      const uint32_t nxt = cur >= kRing - 2 ? cur + 2 - kRing : cur + 2;
-      mv_ring_step<QT, BPR, NWV>(t + 2 < te, W[0] + (size_t)(t + 2) * T::TB, mv_tile_bytes<QT, BPR, NWV>(sg.M, t + 2),
-                                 ring + nxt * R::BUF, ring + cur * R::BUF + slot * T::RB + (u >> 2) * T::BYTES, X,
-                                 red + slot * T::RS + u, w, l, u & 3);
+      const uint32_t nxt = cur == 0 ? D - 1 : cur - 1;  // tile t - 1's buffer
+      mv_ring_step<QT, BPR, NWV>(t + D - 1 < te, W[0] + (size_t)(t + D - 1) * T::TB,
+                                 mv_tile_bytes<QT, BPR, NWV>(sg.M, t + D - 1), ring + nxt * R::BUF,
+                                 ring + cur * R::BUF + slot * T::RB + (u >> 2) * T::BYTES, X, red + slot * T::RS + u,
+                                 w, l, u & 3);
       ring_barrier();
       mv_reduce_store<T, NTH, NMAT>(red, sg, t, tid, cap, segs.amx != nullptr, best, d8, tkt);
-      cur = cur + 1 == kRing ? 0u : cur + 1;
+      cur = cur + 1 == D ? 0u : cur + 1;
     }
     if (segs.amx) mv_argmax_partial<NWV>(best, (g4d::Cand*)(smem + MvXA<BPR, PRO>::RED8), segs.amx + blockIdx.x);
     if (tkt) mv_topk_partial<NTH>(tkt, segs, blockIdx.x - sg.wg_begin);

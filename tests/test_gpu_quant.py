@@ -88,6 +88,12 @@ MATVEC_CASES = [
     ("q6k", 8192, 1536),
     ("q6k", 77, 1536),
     ("q6k", 40, 2560),
+    # past two workgroups per CU of tiles: one workgroup per CU walks its
+    # tiles through the LDS ring (5 buffers for Q4_K, 3 for Q6_K), with a
+    # last partial tile
+    ("q4k", 65536, 1536),
+    ("q6k", 65536, 1536),
+    ("q4k", 65531, 2048),
 ]
 
 
