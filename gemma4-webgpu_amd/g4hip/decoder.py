@@ -953,7 +953,7 @@ class BatchDecoder(_SyntheticModel):
                 total += n * 2 * s.kv_dim_of(il) * 2
         return total
 
-    def step(self, sample: str = "argmax", probe=None) -> None:
+    def step(self, sample: str = "argmax", probe=None, head: bool = True) -> None:
         """One token for every sequence. Per layer:
           1. [sum of the previous down chunks -> post-FFN norm-add ->] attn rmsNorm
           2. q/k/v projections (split-K partial sums)
@@ -973,7 +973,11 @@ class BatchDecoder(_SyntheticModel):
         n_layers for the final norm), "attn" (roped `q`, the appended K/V
         rows, `attn`), "ffn_in" (`hidden2` and `xn` after the post-attention
         norm-add), "ffn" (the down projection's `chunks` partial sums in
-        `down_parts`), "head" (`logits`). Not for captured steps."""
+        `down_parts`), "head" (`logits`). Not for captured steps.
+
+        head=False stops after the layers (no final norm, LM head or sample):
+        a prefill chunk whose logits nobody reads (the reference's prefill
+        forwards run no LM head either, src/engine.ts:1896-1900)."""
         c, s, B = self.ctx, self.s, self.B
         H = s.hidden
         if self.embedding is not None:
@@ -1053,6 +1057,9 @@ class BatchDecoder(_SyntheticModel):
                 c.pleGate(self.hidden3, None, None, None, L.ple_gate, self.ple_inputs, s.n_layers * D, il * D,
                           self.ple_gated, D, H, s.eps, batch=B)
                 c.matmulF16(self.ple_gated, L.ple_proj, self.ple_out, H, D, B)
+        if not head:
+            self.lens_host = self.lens_host + 1
+            return
         last = self.layers[-1]
         if s.ple_dim:
             c.batchPrepScale(self.ple_out, 1, last.ple_post_norm, self.hidden3, last.ple_scale, self.final_norm,
@@ -1094,7 +1101,7 @@ class BatchDecoder(_SyntheticModel):
             return 1
         return self.ctx.matmulSegmentsBatchPartial(qt, x, [w], [y], [M], N, self.B, max_ksplit, ops=ops)
 
-    def prefill(self, tokens, start: int = 0, sample: str = "argmax") -> int:
+    def prefill(self, tokens, start: int = 0, sample: str = "argmax", probe=None) -> int:
         """Batched prefill of one sequence (a shared_pages decoder with an
         embedding table): the prompt's tokens at positions start, start + 1,
         ... go through the layers B at a time, each chunk one step of the
@@ -1103,11 +1110,13 @@ class BatchDecoder(_SyntheticModel):
         prologue launch appends every row of the chunk before the attention
         launch reads them, so the chunk is causal). The reference runs one
         full forward per prompt token instead (src/engine.ts:1923-1938) and
-        samples from the last one (src/engine.ts:2014-2017). A short last
+        samples from the last one (src/engine.ts:2014-2017); as there, only
+        the last chunk runs the LM head. A short last
         chunk repeats its last token and position in the spare rows
         (identical rows, identical writes). Returns the row of the final
         chunk that holds the prompt's last token: its logits and `tokens`
-        entry are the first sample."""
+        entry are the first sample. probe (tests): passed to every chunk's
+        step."""
         if not self.shared_pages or self.embedding is None:
             raise ValueError("prefill needs a shared_pages decoder with an embedding table")
         toks = np.asarray(tokens, np.uint32)
@@ -1126,7 +1135,7 @@ class BatchDecoder(_SyntheticModel):
             self.ctx.copy(self.tokens, dtok.offset(4 * B * k), 4 * B)
             self.ctx.copy(self.seq_lens, dpos.offset(4 * B * k), 4 * B)
             self.lens_host = cpos[B * k:B * (k + 1)].copy()
-            self.step(sample)
+            self.step(sample, probe=probe, head=k == nch - 1)
         self.ctx.sync()
         dtok.free()
         dpos.free()

@@ -672,8 +672,9 @@ napi_value EmbeddingLookup(napi_env env, napi_callback_info info) {
 // ---- per-layer embeddings (shaders/ple_*.wgsl) --------------------------
 
 // pleStage1Fuse(ctx, projected, norm_weight, table_q5k, table_rows, ple_inputs,
-//               {num_layers, per_layer_dim, eps, token_id}[, tokenDev]): every
-// layer in one dispatch (the reference dispatches one workgroup per layer).
+//               {num_layers, per_layer_dim, eps, token_id}[, tokenDev[, count]]):
+// every layer in one dispatch (the reference dispatches one workgroup per
+// layer); with tokenDev and count, the rows of count tokens at once.
 napi_value PleStage1Fuse(napi_env env, napi_callback_info info) {
   Args a(env, info);
   g4_ctx* c = CTX(a, 0);
@@ -685,8 +686,9 @@ napi_value PleStage1Fuse(napi_env env, napi_callback_info info) {
   const uint32_t nl = a.fu32(6, "num_layers"), dim = a.fu32(6, "per_layer_dim"), tok = a.fu32(6, "token_id");
   const float eps = a.ff32(6, "eps");
   const uint32_t* td = U32P(a, 7);
+  const uint32_t count = a.present(8) ? a.u32(8) : 1;
   CHECKED(a);
-  return done(env, g4_pleStage1Fuse(c, proj, w, table, rows, tok, td, out, nl, dim, eps, 1));
+  return done(env, g4_pleStage1Fuse(c, proj, w, table, rows, tok, td, out, nl, dim, eps, count));
 }
 
 // pleGeluMul(ctx, gate, ple_inputs, output, {layer_offset, size})
@@ -1305,10 +1307,11 @@ napi_value BatchPrepScale(napi_env env, napi_callback_info info) {
   const uint16_t* w2 = (const uint16_t*)fptr(a, 1, "w2");
   float* h = (float*)fptr(a, 1, "hOut");
   float* out = (float*)fptr(a, 1, "out");
+  void* ops = fptr(a, 1, "ops");
   const uint32_t np = a.fu32(2, "nparts"), N = a.fu32(2, "N"), b = a.fu32(2, "batch");
   const float eps = a.f32(3);
   CHECKED(a);
-  return done(env, g4_batchPrepScale(c, x, np, w1, res, sc, w2, h, out, nullptr, N, b, eps));
+  return done(env, g4_batchPrepScale(c, x, np, w1, res, sc, w2, h, out, ops, N, b, eps));
 }
 
 // argmaxAdvance(ctx, logits, result, size, positions, delta): argmax, then *positions += delta
@@ -1322,6 +1325,259 @@ napi_value ArgmaxAdvance(napi_env env, napi_callback_info info) {
   const uint32_t d = a.u32(5);
   CHECKED(a);
   return done(env, g4_argmaxAdvance(c, lg, r, n, 1, pos, d));
+}
+
+// ---- the ragged multi-sequence step and the batched prefill --------------
+// (BatchDecoder.step / prefill in g4hip/decoder.py.) The reference runs one
+// forward per sequence and per prompt token (src/engine.ts:1923-1938); these
+// keys take `batch` rows at once over paged K/V pools (pages of page_size
+// rows [num_kv_heads][head_dim], a page table per row, the row lengths on the
+// device). Paged params travel as plain objects with the C structs' fields.
+
+g4_paged_attn_params paged_params(Args& a, size_t i) {
+  g4_paged_attn_params p{};
+  p.num_seqs = a.fu32(i, "num_seqs");
+  p.num_q_heads = a.fu32(i, "num_q_heads");
+  p.num_kv_heads = a.fu32(i, "num_kv_heads");
+  p.head_dim = a.fu32(i, "head_dim");
+  p.page_size = a.fu32(i, "page_size");
+  p.max_pages = a.fu32(i, "max_pages");
+  p.max_seq_len = a.fu32(i, "max_seq_len");
+  p.num_pages = a.fu32(i, "num_pages");
+  p.scale = a.ff32(i, "scale");
+  p.sliding_window = a.fu32(i, "sliding_window");
+  return p;
+}
+
+g4_paged_attn_fused_params paged_fused_params(Args& a, size_t i) {
+  const g4_paged_attn_params b = paged_params(a, i);
+  g4_paged_attn_fused_params p{};
+  p.num_seqs = b.num_seqs;
+  p.num_q_heads = b.num_q_heads;
+  p.num_kv_heads = b.num_kv_heads;
+  p.head_dim = b.head_dim;
+  p.page_size = b.page_size;
+  p.max_pages = b.max_pages;
+  p.max_seq_len = b.max_seq_len;
+  p.num_pages = b.num_pages;
+  p.scale = b.scale;
+  p.sliding_window = b.sliding_window;
+  p.eps = a.ff32(i, "eps");
+  p.theta = a.ff32(i, "theta");
+  p.apply_divisor = a.fu32(i, "apply_divisor");
+  return p;
+}
+
+napi_value size_result(napi_env env, int rc, size_t n) {
+  if (rc != G4_OK) return done(env, rc);
+  return number(env, (double)n);
+}
+
+// batchOperandBytes(N, batch) / batchSubOperandBytes(K, batch) -> bytes of the
+// matrix-core operand blocks of `batch` vectors of N (K) values
+napi_value BatchOperandBytes(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  const uint32_t N = a.u32(0), b = a.u32(1);
+  CHECKED(a);
+  size_t n = 0;
+  const int rc = g4_batchOperandBytes(N, b, &n);
+  return size_result(env, rc, n);
+}
+napi_value BatchSubOperandBytes(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  const uint32_t K = a.u32(0), b = a.u32(1);
+  CHECKED(a);
+  size_t n = 0;
+  const int rc = g4_batchSubOperandBytes(K, b, &n);
+  return size_result(env, rc, n);
+}
+
+// pagedAttnWorkspaceSize(params) -> bytes of pagedAttnDecode's split-K workspace
+napi_value PagedAttnWorkspaceSize(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  const g4_paged_attn_params p = paged_params(a, 0);
+  CHECKED(a);
+  size_t n = 0;
+  const int rc = g4_pagedAttnDecode_workspace_size(p, &n);
+  return size_result(env, rc, n);
+}
+
+// copy(ctx, dst, src, bytes): a device-to-device copy on the stream
+napi_value Copy(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  void* d = a.ptr(1);
+  const void* s = a.ptr(2);
+  const uint64_t n = a.u64(3);
+  CHECKED(a);
+  return done(env, g4_copy_d2d(c, d, s, n));
+}
+
+// embeddingLookupBatch(ctx, embedding, num_rows, output, {hidden_size}, tokensDev, count)
+napi_value EmbeddingLookupBatch(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const uint16_t* e = U16P(a, 1);
+  const uint32_t rows = a.u32(2);
+  float* out = F32P(a, 3);
+  const uint32_t H = a.fu32(4, "hidden_size");
+  const uint32_t* td = U32P(a, 5);
+  const uint32_t n = a.u32(6);
+  CHECKED(a);
+  return done(env, g4_embeddingLookupBatch(c, e, rows, out, H, td, n));
+}
+
+// advanceSeqLens(ctx, seqLens, numSeqs, delta)
+napi_value AdvanceSeqLens(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  uint32_t* sl = U32P(a, 1);
+  const uint32_t n = a.u32(2), d = a.u32(3);
+  CHECKED(a);
+  return done(env, g4_advanceSeqLens(c, sl, n, d));
+}
+
+// batchPrep(ctx, {x, w1, residual, w2, hOut, out, ops}, {nparts, N, batch}, eps)
+napi_value BatchPrep(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* x = (const float*)fptr(a, 1, "x");
+  const uint16_t* w1 = (const uint16_t*)fptr(a, 1, "w1");
+  const float* res = (const float*)fptr(a, 1, "residual");
+  const uint16_t* w2 = (const uint16_t*)fptr(a, 1, "w2");
+  float* h = (float*)fptr(a, 1, "hOut");
+  float* out = (float*)fptr(a, 1, "out");
+  void* ops = fptr(a, 1, "ops");
+  const uint32_t np = a.fu32(2, "nparts"), N = a.fu32(2, "N"), b = a.fu32(2, "batch");
+  const float eps = a.f32(3);
+  CHECKED(a);
+  return done(env, g4_batchPrep(c, x, np, w1, res, w2, h, out, ops, N, b, eps));
+}
+
+// matmulSegmentsBatchPartial(ctx, wtype, {x, ops}, weights, outputs, rows,
+//   {N, batch, max_ksplit}[, softcap]) -> the chunk count K was split into
+napi_value MatmulSegmentsBatchPartial(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const int wt = wtype_of(a, 1);
+  const float* x = (const float*)fptr(a, 2, "x");
+  const void* ops = fptr(a, 2, "ops");
+  void* W[4] = {};
+  void* Y[4] = {};
+  uint32_t R[4] = {};
+  const int n = array_at(a, 3, W, nullptr, 4, 0);
+  const int ny = array_at(a, 4, Y, nullptr, 4, 0);
+  const int nr = array_at(a, 5, nullptr, R, 4, 1);
+  const uint32_t N = a.fu32(6, "N"), b = a.fu32(6, "batch"), mk = a.fu32(6, "max_ksplit");
+  const float cap = a.present(7) ? a.f32(7) : 0.f;
+  CHECKED(a);
+  if (n != ny || n != nr) {
+    a.fail("weights, outputs and rows differ in length");
+    return nullptr;
+  }
+  uint32_t ks = 0;
+  const int rc = g4_matmulSegmentsBatchPartial(c, wt, x, ops, W, (float* const*)Y, R, n, N, b, mk, cap, &ks);
+  return size_result(env, rc, ks);
+}
+
+// pagedAttnPrologue(ctx, {qParts, kParts, vParts, qNorm, kNorm, ropeFreqs, qOut,
+//   kPool, vPool, pageTable, seqLens, ropeCs}, nparts, pagedFusedParams, ropeRows)
+napi_value PagedAttnPrologue(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* qp = (const float*)fptr(a, 1, "qParts");
+  const float* kp = (const float*)fptr(a, 1, "kParts");
+  const float* vp = (const float*)fptr(a, 1, "vParts");
+  const uint16_t* qn = (const uint16_t*)fptr(a, 1, "qNorm");
+  const uint16_t* kn = (const uint16_t*)fptr(a, 1, "kNorm");
+  const uint16_t* rf = (const uint16_t*)fptr(a, 1, "ropeFreqs");
+  float* qo = (float*)fptr(a, 1, "qOut");
+  uint16_t* kc = (uint16_t*)fptr(a, 1, "kPool");
+  uint16_t* vc = (uint16_t*)fptr(a, 1, "vPool");
+  const int32_t* pt = (const int32_t*)fptr(a, 1, "pageTable");
+  const uint32_t* sl = (const uint32_t*)fptr(a, 1, "seqLens");
+  const float* cs = (const float*)fptr(a, 1, "ropeCs");
+  const uint32_t np = a.u32(2);
+  const g4_paged_attn_fused_params p = paged_fused_params(a, 3);
+  const uint32_t rows = a.u32(4);
+  CHECKED(a);
+  return done(env, g4_pagedAttnPrologue(c, qp, kp, vp, np, qn, kn, rf, qo, kc, vc, pt, sl, p, cs, rows));
+}
+
+// pagedAttnDecode(ctx, {q, kPool, vPool, pageTable, seqLens, out, workspace, ops},
+//   pagedParams, workspaceBytes): ops also receives the output as the o
+//   projection's operand blocks (null: the attention alone)
+napi_value PagedAttnDecode(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* q = (const float*)fptr(a, 1, "q");
+  const uint16_t* kc = (const uint16_t*)fptr(a, 1, "kPool");
+  const uint16_t* vc = (const uint16_t*)fptr(a, 1, "vPool");
+  const int32_t* pt = (const int32_t*)fptr(a, 1, "pageTable");
+  const uint32_t* sl = (const uint32_t*)fptr(a, 1, "seqLens");
+  float* out = (float*)fptr(a, 1, "out");
+  void* ws = fptr(a, 1, "workspace");
+  void* ops = fptr(a, 1, "ops");
+  const g4_paged_attn_params p = paged_params(a, 2);
+  const uint64_t wsb = a.u64(3);
+  CHECKED(a);
+  return done(env, ops ? g4_pagedAttnDecodeOps(c, q, kc, vc, pt, sl, out, p, ws, wsb, ops)
+                       : g4_pagedAttnDecode(c, q, kc, vc, pt, sl, out, p, ws, wsb));
+}
+
+// gateUpGeluBatch(ctx, {x, ops, wGate, wUp, out, downOps}, {M, N}, batch): the
+// Q4_K gate/up pair and the GELU product over `batch` rows; with downOps the
+// product is also written as the down projection's sub-block-scaled operand
+// blocks (out may then be null)
+napi_value GateUpGeluBatch(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* x = (const float*)fptr(a, 1, "x");
+  const void* ops = fptr(a, 1, "ops");
+  const void* wg = fptr(a, 1, "wGate");
+  const void* wu = fptr(a, 1, "wUp");
+  float* out = (float*)fptr(a, 1, "out");
+  void* dops = fptr(a, 1, "downOps");
+  const g4_matmul_params p{a.fu32(2, "M"), a.fu32(2, "N")};
+  const uint32_t b = a.u32(3);
+  CHECKED(a);
+  return done(env, dops ? g4_gateUpGeluBatchOps(c, x, ops, wg, wu, out, dops, p, b)
+                        : g4_gateUpGeluBatch(c, x, ops, wg, wu, out, p, b));
+}
+
+// matmulSubBatchPartial(ctx, downOps, weight, out, {M, K, batch, max_ksplit})
+//   -> the chunk count (the Q6_K down projection over gateUpGeluBatch's blocks)
+napi_value MatmulSubBatchPartial(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const void* ops = a.ptr(1);
+  const void* w = a.ptr(2);
+  float* out = F32P(a, 3);
+  const uint32_t M = a.fu32(4, "M"), K = a.fu32(4, "K"), b = a.fu32(4, "batch"), mk = a.fu32(4, "max_ksplit");
+  CHECKED(a);
+  uint32_t ks = 0;
+  const int rc = g4_matmulSubBatchPartial(c, ops, w, out, M, K, b, mk, &ks);
+  return size_result(env, rc, ks);
+}
+
+// argmaxBatch(ctx, logits, result, size, batch) / topk256Batch(...): per row
+napi_value ArgmaxBatch(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* lg = F32P(a, 1);
+  uint32_t* r = U32P(a, 2);
+  const uint32_t n = a.u32(3), b = a.u32(4);
+  CHECKED(a);
+  return done(env, g4_argmaxBatch(c, lg, r, n, b));
+}
+napi_value Topk256Batch(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  g4_ctx* c = CTX(a, 0);
+  const float* lg = F32P(a, 1);
+  float* r = F32P(a, 2);
+  const uint32_t n = a.u32(3), b = a.u32(4);
+  CHECKED(a);
+  return done(env, g4_topk256Batch(c, lg, r, n, b));
 }
 
 struct Entry {
@@ -1394,6 +1650,20 @@ const Entry kEntries[] = {
     {"matmulF16", MatmulF16},
     {"batchPrepScale", BatchPrepScale},
     {"argmaxAdvance", ArgmaxAdvance},
+    {"batchOperandBytes", BatchOperandBytes},
+    {"batchSubOperandBytes", BatchSubOperandBytes},
+    {"pagedAttnWorkspaceSize", PagedAttnWorkspaceSize},
+    {"copy", Copy},
+    {"embeddingLookupBatch", EmbeddingLookupBatch},
+    {"advanceSeqLens", AdvanceSeqLens},
+    {"batchPrep", BatchPrep},
+    {"matmulSegmentsBatchPartial", MatmulSegmentsBatchPartial},
+    {"pagedAttnPrologue", PagedAttnPrologue},
+    {"pagedAttnDecode", PagedAttnDecode},
+    {"gateUpGeluBatch", GateUpGeluBatch},
+    {"matmulSubBatchPartial", MatmulSubBatchPartial},
+    {"argmaxBatch", ArgmaxBatch},
+    {"topk256Batch", Topk256Batch},
 };
 
 }  // namespace

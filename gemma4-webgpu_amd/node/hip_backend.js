@@ -306,6 +306,7 @@ class HipBackend {
       this.g.graphDestroy(this.fusedGraph);
       this.fusedGraph = null;
     }
+    this._freeBatch();
     for (const p of this.owned) this.g.free(this.ctx, p);
     this.owned = [];
     this.g.destroy(this.ctx);
@@ -348,7 +349,9 @@ class HipBackend {
     for (let il = 0; il < C.num_layers; il++) {
       if (C.kv_producer_for_layer[il] < 0) throw new Error('layer ' + il + ': no unshared layer of its attention kind');
       if (isKvProducer(C, il)) {
-        const bytes = 2 * this.maxSeqLen * C.num_kv_heads * headDim(C, il);
+        // rows rounded up to whole pages of 16, so that the batched prefill's
+        // paged keys address the same cache through an identity page table
+        const bytes = 2 * Math.ceil(this.maxSeqLen / 16) * 16 * C.num_kv_heads * headDim(C, il);
         const kv = { k: this.alloc(bytes), v: this.alloc(bytes) };
         this.g.memset(this.ctx, kv.k, 0, bytes);
         this.g.memset(this.ctx, kv.v, 0, bytes);
@@ -412,6 +415,7 @@ class HipBackend {
     this.globals = g;
   }
 
+  // k, v: [maxSeqLen rounded up to a multiple of 16][num_kv_heads][head_dim] f16
   setKvCache(il, k, v) {
     this.kvCaches[il] = { k: k, v: v };
   }
@@ -828,6 +832,290 @@ class HipBackend {
     }
     while (inflight.length) take(await inflight.shift());
     return out;
+  }
+
+  // ---- batched prefill ---------------------------------------------------
+  // The ragged multi-sequence step of g4hip/decoder.py (BatchDecoder.step)
+  // over `rows` rows that are tokens of this backend's one sequence: the
+  // paged keys over an identity page table, so that the pool of pages of 16
+  // rows IS the decode step's [maxSeqLen][num_kv_heads][head_dim] cache and
+  // the fused step continues from what the prefill appended.
+  _prepareBatch(B) {
+    if (this.batch && this.batch.B === B) return this.batch;
+    this._freeBatch();
+    const C = this.config;
+    const g = this.g;
+    const c = this.ctx;
+    const H = C.hidden_size;
+    const V = C.vocab_size;
+    const D = C.per_layer_input_dim;
+    const NL = C.num_layers;
+    if (B < 1 || B > 64) throw new Error('prefill rows: 1..64');
+    let maxHd = 0;
+    let maxI = 0;
+    for (let il = 0; il < NL; il++) {
+      maxHd = Math.max(maxHd, headDim(C, il));
+      maxI = Math.max(maxI, intermediateSize(C, il));
+    }
+    const Q = C.num_q_heads * maxHd;
+    const KV = C.num_kv_heads * maxHd;
+    const own = [];
+    const al = (bytes) => {
+      const p = g.alloc(c, bytes);
+      own.push(p);
+      return p;
+    };
+    const f4 = (n) => al(4 * n);
+    const pageSize = 16;
+    const pages = Math.ceil(this.maxSeqLen / pageSize);
+    const ident = new Int32Array(B * pages);
+    for (let r = 0; r < B; r++) for (let p = 0; p < pages; p++) ident[r * pages + p] = p;
+    const F = (il) => this.formats[il] || DEFAULT_FORMATS;
+    const handoff = (il) => F(il).ffn_gate === 'q4k' && F(il).ffn_up === 'q4k' && F(il).ffn_down === 'q6k' &&
+      (intermediateSize(C, il) === 6144 || intermediateSize(C, il) === 12288);
+    let anyHandoff = false;
+    let anyUnpaired = false;
+    for (let il = 0; il < NL; il++) {
+      anyHandoff = anyHandoff || handoff(il);
+      anyUnpaired = anyUnpaired || !(F(il).ffn_gate === 'q4k' && F(il).ffn_up === 'q4k');
+    }
+    const b = { B: B, own: own, pageSize: pageSize, pages: pages, handoff: handoff,
+      pageTable: al(4 * B * pages), seqLens: al(4 * B), tokens: al(4 * B),
+      hidden: f4(B * H), hidden2: f4(B * H), xn: f4(B * H), xops: al(g.batchOperandBytes(H, B)),
+      ksH: H / 256, ksQ: Q / 256, ksF: maxI / 256,
+      q: f4(B * Q), attn: f4(B * Q), act: f4(B * maxI), logits: f4(B * V) };
+    g.upload(c, b.pageTable, ident);
+    Object.assign(b, { qParts: f4(b.ksH * B * Q), kParts: f4(b.ksH * B * KV), vParts: f4(b.ksH * B * KV),
+      oParts: f4(b.ksQ * B * H), downParts: f4(b.ksF * B * H) });
+    // the attention output also as the o projection's operand blocks (heads
+    // of whole super-blocks)
+    b.aops = C.head_dim_local % 256 === 0 ? al(g.batchOperandBytes(Q, B)) : null;
+    b.dops = anyHandoff ? al(g.batchSubOperandBytes(maxI, B)) : null;
+    if (anyUnpaired) Object.assign(b, { gate: f4(B * maxI), up: f4(B * maxI) });
+    if (D > 0) {
+      Object.assign(b, { pleProjected: f4(B * NL * D), pleInputs: f4(B * NL * D), pleGated: f4(B * D),
+        pleOut: f4(B * H), hidden3: f4(B * H) });
+    }
+    b.pro = [];
+    b.attnParams = [];
+    let ws = 0;
+    for (let il = 0; il < NL; il++) {
+      const swa = isSwaLayer(C, il);
+      const p = { num_seqs: B, num_q_heads: C.num_q_heads, num_kv_heads: C.num_kv_heads, head_dim: headDim(C, il),
+        page_size: pageSize, max_pages: pages, max_seq_len: this.maxSeqLen, num_pages: pages, scale: 1.0,
+        sliding_window: swa ? C.sliding_window : 0 };
+      b.attnParams.push(p);
+      b.pro.push(Object.assign({ eps: C.rms_norm_eps, theta: ropeTheta(C, il), apply_divisor: swa ? 0 : 1 }, p));
+      ws = Math.max(ws, g.pagedAttnWorkspaceSize(p));
+    }
+    b.workspace = al(ws);
+    b.workspaceBytes = ws;
+    g.memset(c, b.workspace, 0, ws);
+    g.sync(c);
+    this.batch = b;
+    return b;
+  }
+
+  _freeBatch() {
+    if (!this.batch) return;
+    for (const p of this.batch.own) this.g.free(this.ctx, p);
+    this.batch = null;
+  }
+
+  // y = W . x for the batch rows: f16 rows through the f16 matvec (one
+  // chunk), block formats split-K into at most maxKsplit chunks; returns the
+  // chunk count
+  _mmBatch(fmt, x, ops, w, y, M, N, maxKsplit) {
+    const b = this.batch;
+    if (fmt === 'f16') {
+      this.g.matmulF16(this.ctx, x, w, y, { M: M, N: N, batch: b.B });
+      return 1;
+    }
+    return this.g.matmulSegmentsBatchPartial(this.ctx, fmt, { x: x, ops: ops }, [w], [y], [M],
+      { N: N, batch: b.B, max_ksplit: maxKsplit });
+  }
+
+  // One chunk: every row embeds its token (tokens) and appends its K/V row
+  // at position seqLens - 1 after the advance, then attends to the positions
+  // up to it (the prologue launch appends every row before the attention
+  // launch reads them). head: the final norm, LM head, softcap and argmax
+  // per row.
+  _encodeBatchStep(head) {
+    const C = this.config;
+    const g = this.g;
+    const c = this.ctx;
+    const G = this.globals;
+    const Fz = this.prepareFusedStep();
+    const b = this.batch;
+    const B = b.B;
+    const H = C.hidden_size;
+    const V = C.vocab_size;
+    const D = C.per_layer_input_dim;
+    const NL = C.num_layers;
+    const eps = C.rms_norm_eps;
+    const dims = { nparts: 1, N: H, batch: B };
+    g.embeddingLookupBatch(c, G.tokenEmbed, V, b.hidden, { hidden_size: H }, b.tokens, B);
+    if (D > 0) {
+      g.matmulF16(c, b.hidden, G.perLayerModelProj, b.pleProjected, { M: NL * D, N: H, batch: B });
+      g.pleStage1Fuse(c, b.pleProjected, G.perLayerProjNorm, G.perLayerTable, V, b.pleInputs,
+        { num_layers: NL, per_layer_dim: D, eps: eps, token_id: 0 }, b.tokens, B);
+    }
+    g.advanceSeqLens(c, b.seqLens, B, 1);
+    let nd = 0;
+    for (let il = 0; il < NL; il++) {
+      const L = this.layers[il];
+      const F = this.formats[il] || DEFAULT_FORMATS;
+      const HD = headDim(C, il);
+      const Q = C.num_q_heads * HD;
+      const KV = C.num_kv_heads * HD;
+      const I = intermediateSize(C, il);
+      const prod = isKvProducer(C, il);
+      const kv = this.kvCaches[C.kv_producer_for_layer[il]];
+      if (il === 0) {
+        g.batchPrep(c, { x: b.hidden, w1: L.attn_norm, out: b.xn, ops: b.xops }, dims, eps);
+      } else if (D > 0) {  // the previous layer's per-layer-embedding tail
+        const P = this.layers[il - 1];
+        g.batchPrepScale(c, { x: b.pleOut, w1: P.post_norm, residual: b.hidden3, scale: P.layer_output_scale,
+          w2: L.attn_norm, hOut: b.hidden, out: b.xn, ops: b.xops }, dims, eps);
+      } else {
+        const P = this.layers[il - 1];
+        g.batchPrep(c, { x: b.downParts, w1: P.post_ffw_norm, residual: b.hidden2, w2: L.attn_norm, hOut: b.hidden,
+          out: b.xn, ops: b.xops }, { nparts: nd, N: H, batch: B }, eps);
+      }
+      // q/k/v grouped by weight format (a consumer layer projects q only); f16
+      // rows write whole sums, so the block formats then split K once too
+      const mats = prod ? [['attn_q', b.qParts, Q], ['attn_k', b.kParts, KV], ['attn_v', b.vParts, KV]]
+        : [['attn_q', b.qParts, Q]];
+      const groups = [];
+      for (const [name, y, r] of mats) {
+        let grp = groups.find((x) => x.fmt === F[name]);
+        if (!grp) {
+          grp = { fmt: F[name], w: [], y: [], r: [] };
+          groups.push(grp);
+        }
+        grp.w.push(L[name]);
+        grp.y.push(y);
+        grp.r.push(r);
+      }
+      let nq = groups.some((x) => x.fmt === 'f16') ? 1 : 0;
+      for (const grp of groups) {
+        if (grp.fmt === 'f16') {
+          grp.w.forEach((w, k) => g.matmulF16(c, b.xn, w, grp.y[k], { M: grp.r[k], N: H, batch: B }));
+          continue;
+        }
+        const k = g.matmulSegmentsBatchPartial(c, grp.fmt, { x: b.xn, ops: b.xops }, grp.w, grp.y, grp.r,
+          { N: H, batch: B, max_ksplit: nq || b.ksH });
+        if (nq && k !== nq) throw new Error('layer ' + il + ': q/k/v launches split K ' + nq + ' and ' + k + ' ways');
+        nq = k;
+      }
+      g.pagedAttnPrologue(c, { qParts: b.qParts, kParts: prod ? b.kParts : null, vParts: prod ? b.vParts : null,
+        qNorm: L.attn_q_norm, kNorm: prod ? L.attn_k_norm : null, ropeFreqs: G.rope_freqs, qOut: b.q,
+        kPool: prod ? kv.k : null, vPool: prod ? kv.v : null, pageTable: b.pageTable, seqLens: b.seqLens,
+        ropeCs: Fz.rope[!isSwaLayer(C, il)] }, nq, b.pro[il], this.maxSeqLen);
+      const ops = HD % 256 === 0 ? b.aops : null;
+      g.pagedAttnDecode(c, { q: b.q, kPool: kv.k, vPool: kv.v, pageTable: b.pageTable, seqLens: b.seqLens,
+        out: b.attn, workspace: b.workspace, ops: ops }, b.attnParams[il], b.workspaceBytes);
+      const no = this._mmBatch(F.attn_output, b.attn, ops, L.attn_output, b.oParts, H, Q, b.ksQ);
+      g.batchPrep(c, { x: b.oParts, w1: L.post_attention_norm, residual: b.hidden, w2: L.ffn_norm, hOut: b.hidden2,
+        out: b.xn, ops: b.xops }, { nparts: no, N: H, batch: B }, eps);
+      if (b.handoff(il)) {
+        // the product goes to the down projection as operand blocks only; K
+        // in chunks of 3 super-blocks
+        g.gateUpGeluBatch(c, { x: b.xn, ops: b.xops, wGate: L.ffn_gate, wUp: L.ffn_up, out: null,
+          downOps: b.dops }, { M: I, N: H }, B);
+        nd = g.matmulSubBatchPartial(c, b.dops, L.ffn_down, b.downParts, { M: H, K: I, batch: B,
+          max_ksplit: I / 768 });
+      } else {
+        if (F.ffn_gate === 'q4k' && F.ffn_up === 'q4k') {
+          g.gateUpGeluBatch(c, { x: b.xn, ops: b.xops, wGate: L.ffn_gate, wUp: L.ffn_up, out: b.act },
+            { M: I, N: H }, B);
+        } else {  // gate and up apart (whole sums), then the GELU product
+          this._mmBatch(F.ffn_gate, b.xn, b.xops, L.ffn_gate, b.gate, I, H, 1);
+          this._mmBatch(F.ffn_up, b.xn, b.xops, L.ffn_up, b.up, I, H, 1);
+          g.geluMul(c, b.gate, b.up, b.act, B * I);
+        }
+        nd = this._mmBatch(F.ffn_down, b.act, null, L.ffn_down, b.downParts, H, I, b.ksF);
+      }
+      if (D > 0) {
+        // post-FFN norm-add (h, no second norm) -> inp_gate -> gelu * ple_inputs -> proj
+        g.batchPrepScale(c, { x: b.downParts, w1: L.post_ffw_norm, residual: b.hidden2, out: b.hidden3 },
+          { nparts: nd, N: H, batch: B }, eps);
+        g.pleGate(c, { x: b.hidden3, wGate: L.inp_gate, pleInputs: b.pleInputs, out: b.pleGated },
+          { M: D, N: H, ple_stride: NL * D, layer_offset: il * D, batch: B }, eps);
+        g.matmulF16(c, b.pleGated, L.proj, b.pleOut, { M: H, N: D, batch: B });
+      }
+    }
+    if (!head) return;
+    const last = this.layers[NL - 1];
+    if (D > 0) {
+      g.batchPrepScale(c, { x: b.pleOut, w1: last.post_norm, residual: b.hidden3, scale: last.layer_output_scale,
+        w2: G.finalNorm, hOut: b.hidden, out: b.xn, ops: b.xops }, dims, eps);
+    } else {
+      g.batchPrep(c, { x: b.downParts, w1: last.post_ffw_norm, residual: b.hidden2, w2: G.finalNorm,
+        hOut: b.hidden, out: b.xn, ops: b.xops }, { nparts: nd, N: H, batch: B }, eps);
+    }
+    const fmt = G.lmHeadFormat || 'q6k';
+    const cap = C.final_logit_softcapping;
+    if (fmt === 'f16') {
+      g.matmulF16(c, b.xn, G.lmHead, b.logits, { M: V, N: H, batch: B });
+      if (cap > 0) g.logitSoftcap(c, b.logits, { size: B * V, cap: cap });
+    } else {
+      g.matmulSegmentsBatchPartial(c, fmt, { x: b.xn, ops: b.xops }, [G.lmHead], [b.logits], [V],
+        { N: H, batch: B, max_ksplit: 1 }, cap > 0 ? cap : 0);
+    }
+    g.argmaxBatch(c, b.logits, b.tokens, V, B);
+  }
+
+  // The prompt `tokens` at positions start, start + 1, ... through the
+  // batched step, opts.rows (default 64) tokens per chunk. The reference
+  // runs one forward per prompt token (src/engine.ts:1923-1938) and the LM
+  // head once after the last (getFirstTokenAfterPrefill, :1951-1959); here
+  // each chunk is one ragged step whose row r is token start + 64k + r, and
+  // only the last chunk runs the LM head. A short last chunk repeats its
+  // last token and position in the spare rows (identical rows, identical
+  // writes). Leaves the greedy sample of the last token where the fused
+  // step reads its token and start + T in the position counter, so
+  // generate(sample, start + T, ...) continues; returns that sample.
+  prefill(tokens, start, opts) {
+    const o = opts || {};
+    const T = tokens.length;
+    const pos0 = start || 0;
+    if (T === 0 || pos0 + T > this.maxSeqLen - 1) {
+      throw new Error('prefill: ' + T + ' tokens from ' + pos0 + ' do not fit ' + this.maxSeqLen + ' positions');
+    }
+    const B = Math.min(o.rows || 64, T);
+    const b = this._prepareBatch(B);
+    const g = this.g;
+    const c = this.ctx;
+    const nch = Math.ceil(T / B);
+    // every chunk's tokens and lengths before the step's advance, uploaded once
+    const tok = new Uint32Array(nch * B);
+    const len = new Uint32Array(nch * B);
+    for (let i = 0; i < nch * B; i++) {
+      const t = Math.min(i, T - 1);
+      tok[i] = tokens[t];
+      len[i] = pos0 + t;
+    }
+    const dtok = g.alloc(c, 4 * nch * B);
+    const dlen = g.alloc(c, 4 * nch * B);
+    try {
+      g.upload(c, dtok, tok);
+      g.upload(c, dlen, len);
+      for (let k = 0; k < nch; k++) {
+        g.copy(c, b.tokens, dtok + BigInt(4 * B * k), 4 * B);
+        g.copy(c, b.seqLens, dlen + BigInt(4 * B * k), 4 * B);
+        this._encodeBatchStep(k === nch - 1);
+      }
+      // the prompt's last token is row (T - 1) - (nch - 1) B of the last chunk
+      const last = T - 1 - (nch - 1) * B;
+      g.copy(c, this.workBuffers.argmaxResult, b.tokens + BigInt(4 * last), 4);
+      this.setPosition(pos0 + T);
+      g.sync(c);
+    } finally {
+      g.free(c, dtok);
+      g.free(c, dlen);
+    }
+    return this.readToken();
   }
 
   readF32(name, count) {

@@ -19,6 +19,10 @@
 // <dir>/out.bin: per forward hidden f32[H], logits f32[V], token u32.
 // With cfg.generate = n: HipBackend.generate's pipelined greedy loop for n
 // tokens at depth 2 and again at depth 1; out.bin: the u32 tokens of both.
+// With cfg.prefill = [tokens]: HipBackend.prefill of those tokens from
+// `position` in chunks of cfg.rows, then one fused step from its sample;
+// out.bin: the sample u32, every producer layer's K then V rows of the
+// prompt's positions (f16), and the step's hidden, logits and token.
 const fs = require('fs');
 const path = require('path');
 
@@ -74,6 +78,25 @@ function collect(i) {
 }
 
 const P = cfg.position;
+if (cfg.prefill) {
+  const T = cfg.prefill.length;
+  const first = be.prefill(cfg.prefill, P, { rows: cfg.rows });
+  console.log('[napi] prefill of ' + T + ' tokens in chunks of ' + cfg.rows + ': sample ' + first);
+  const pos = be.g.download(be.ctx, be.workBuffers.position, 4).readUInt32LE(0);
+  if (pos !== P + T) throw new Error('device position ' + pos + ', expected ' + (P + T));
+  outs.push(Buffer.from(new Uint32Array([first]).buffer));
+  for (let il = 0; il < C.num_layers; il++) {
+    if (!hb.isKvProducer(C, il)) continue;
+    const row = 2 * C.num_kv_heads * hb.headDim(C, il);
+    for (const which of ['k', 'v']) outs.push(be.g.download(be.ctx, be.kvCaches[il][which], row * T, row * P));
+  }
+  be.encodeFusedStep();
+  collect(1);
+  fs.writeFileSync(path.join(dir, 'out.bin'), Buffer.concat(outs));
+  be.close();
+  console.log('[napi] done (prefill)');
+  process.exit(0);
+}
 if (cfg.generate) {
   // greedy generation with the pipelined loop (depth 2: step N + 1 submitted
   // before step N's token is awaited), then again from the same token and

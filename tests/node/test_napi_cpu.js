@@ -25,7 +25,9 @@ const KEYS = ['version', 'lastError', 'init', 'destroy', 'deviceInfo', 'alloc', 
   'digitsBytes', 'attnFusedWorkspaceSize', 'ropeTable', 'matmulWarmRegion', 'attnDecodeFused',
   'normAddScaleMatmulSegments', 'qkvAttnDecodeFused',
   'normAddGateUpGeluDigits', 'matmulQuantDigits', 'normAddMatmulArgmax', 'pleGate', 'matmulF16', 'batchPrepScale',
-  'argmaxAdvance'];
+  'argmaxAdvance', 'batchOperandBytes', 'batchSubOperandBytes', 'pagedAttnWorkspaceSize', 'copy',
+  'embeddingLookupBatch', 'advanceSeqLens', 'batchPrep', 'matmulSegmentsBatchPartial', 'pagedAttnPrologue',
+  'pagedAttnDecode', 'gateUpGeluBatch', 'matmulSubBatchPartial', 'argmaxBatch', 'topk256Batch'];
 
 const addon = hb.loadAddon();
 
@@ -88,7 +90,7 @@ function mockAddon() {
   let next = 1;
   const m = { calls: calls };
   for (const k of KEYS) m[k] = function () { calls.push([k].concat(Array.prototype.slice.call(arguments))); };
-  m.alloc = () => next++;
+  m.alloc = () => BigInt(4096 * next++);
   m.init = () => 'ctx';
   m.digitsBytes = function () {
     calls.push(['digitsBytes'].concat(Array.prototype.slice.call(arguments)));
@@ -101,6 +103,22 @@ function mockAddon() {
   m.attnFusedWorkspaceSize = function (p) {
     calls.push(['attnFusedWorkspaceSize', p]);
     return 1024 + p.head_dim;
+  };
+  m.batchOperandBytes = (N, b) => N * b;
+  m.batchSubOperandBytes = (K, b) => 2 * K * b;
+  m.pagedAttnWorkspaceSize = (p) => 64 * p.head_dim;
+  // the K split of a batched matmul: the most the caller allows, at most 6
+  m.matmulSegmentsBatchPartial = function () {
+    calls.push(['matmulSegmentsBatchPartial'].concat(Array.prototype.slice.call(arguments)));
+    return Math.min(6, arguments[6].max_ksplit);
+  };
+  m.matmulSubBatchPartial = function () {
+    calls.push(['matmulSubBatchPartial'].concat(Array.prototype.slice.call(arguments)));
+    return arguments[4].max_ksplit;
+  };
+  m.download = function () {
+    calls.push(['download'].concat(Array.prototype.slice.call(arguments)));
+    return Buffer.alloc(arguments[2]);
   };
   return m;
 }
@@ -342,6 +360,70 @@ check('the fused step: launch order, prologue chaining, format groups, PLE and t
   assert.strictEqual(head[2], 'q6k');
   assert.strictEqual(head[3].positions, be.workBuffers.position);
   assert.strictEqual(head[3].result, be.workBuffers.argmaxResult);
+});
+
+check('prefill: the batched step over the decode caches, LM head on the last chunk only', () => {
+  const C = hb.e2bConfig();
+  const m = mockAddon();
+  const be = new hb.HipBackend(m, 'ctx', C, { maxSeqLen: 1000 });
+  be.allocate();
+  for (let il = 0; il < C.num_layers; il++) {
+    const t = {};
+    for (const n of Object.keys(be.layerTensorBytes(il))) t[n] = n + il;
+    be.setLayerWeights(il, t);
+  }
+  be.setGlobals(Object.assign({ tokenEmbed: 'emb', lmHead: 'head', finalNorm: 'fn', rope_freqs: 'rf' },
+    PLE_GLOBALS));
+  const toks = [];
+  for (let i = 0; i < 20; i++) toks.push(1000 + i);
+  m.calls.length = 0;
+  be.prefill(toks, 600, { rows: 8 });
+  const b = be.batch;
+  const of = (k) => m.calls.filter((x) => x[0] === k);
+  assert.strictEqual(b.B, 8);
+  assert.strictEqual(b.pages, 63);  // 1000 positions in pages of 16
+  // the identity page table, one list per row
+  const table = of('upload').find((x) => x[2] === b.pageTable)[3];
+  assert.strictEqual(table.length, 8 * 63);
+  for (let r = 0; r < 8; r++) for (let p = 0; p < 63; p++) assert.strictEqual(table[r * 63 + p], p);
+  // chunk tokens and lengths: 20 tokens, the last chunk's spare rows repeat token 19 at position 619
+  const up = of('upload').filter((x) => x[3] instanceof Uint32Array && x[3].length === 24);
+  assert.deepStrictEqual(Array.from(up[0][3]), toks.concat([1019, 1019, 1019, 1019]));
+  const lens = [];
+  for (let i = 0; i < 24; i++) lens.push(600 + Math.min(i, 19));
+  assert.deepStrictEqual(Array.from(up[1][3]), lens);
+  const copies = of('copy');
+  assert.deepStrictEqual(copies.slice(0, 6).map((x) => [x[2], x[3] - up[x[2] === b.tokens ? 0 : 1][2], x[4]]),
+    [[b.tokens, 0n, 32], [b.seqLens, 0n, 32], [b.tokens, 32n, 32], [b.seqLens, 32n, 32], [b.tokens, 64n, 32],
+      [b.seqLens, 64n, 32]]);
+  // the first sample: row 3 of the last chunk, where the fused step reads its token
+  assert.deepStrictEqual(copies[6].slice(2), [be.workBuffers.argmaxResult, b.tokens + 12n, 4]);
+  assert.deepStrictEqual(Array.from(of('upload').pop()[3]), [620]);  // the position after the prompt
+  assert.strictEqual(of('embeddingLookupBatch').length, 3);
+  assert.strictEqual(of('advanceSeqLens').length, 3);
+  assert.strictEqual(of('argmaxBatch').length, 1);
+  assert.strictEqual(of('pagedAttnDecode').length, 3 * C.num_layers);
+  // a consumer layer projects q only and attends over its producer's cache
+  const pro = of('pagedAttnPrologue');
+  const dec = of('pagedAttnDecode');
+  for (let il = 0; il < C.num_layers; il++) {
+    const src = C.kv_producer_for_layer[il];
+    const p = pro[il][2];
+    assert.strictEqual(p.kPool, il === src ? be.kvCaches[il].k : null);
+    assert.strictEqual(p.kParts, il === src ? b.kParts : null);
+    assert.strictEqual(dec[il][2].kPool, be.kvCaches[src].k);
+    assert.strictEqual(pro[il][4].max_seq_len, 1000);
+    assert.strictEqual(pro[il][4].num_pages, 63);
+    assert.strictEqual(pro[il][4].head_dim, hb.headDim(C, il));
+    assert.strictEqual(pro[il][3], 6);  // the q/k/v launch's K split
+  }
+  // Q4_K gate/up over a Q6_K down: the product handed over as operand blocks
+  const gu = of('gateUpGeluBatch');
+  assert.strictEqual(gu.length, 3 * C.num_layers);
+  assert.ok(gu.every((x) => x[2].downOps === b.dops && x[2].out === null));
+  assert.strictEqual(of('matmulSubBatchPartial')[0][5].max_ksplit, 8);  // 6144 / 768
+  be.close();
+  assert.strictEqual(be.batch, null);
 });
 
 console.log('all node CPU checks passed');

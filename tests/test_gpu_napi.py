@@ -205,3 +205,67 @@ def test_node_backend_pipelined_generate_vs_oracle():
         print(f"[napi] generate step {i}: in {tok}, out {got}, oracle argmax {O.argmax(lg)}", flush=True)
         assert lg[got] >= lg.max() - 1e-3 * np.abs(lg).max(), i
         tok = got
+
+
+def _run_node(cfg, files):
+    with tempfile.TemporaryDirectory() as d:
+        for name, arr in files.items():
+            np.ascontiguousarray(arr).tofile(os.path.join(d, name + ".bin"))
+        with open(os.path.join(d, "config.json"), "w") as f:
+            json.dump(cfg, f)
+        r = subprocess.run(["node", os.path.join(ROOT, "tests", "node", "napi_forward.js"), d], capture_output=True,
+                           text=True, timeout=240)
+        print(r.stdout, r.stderr, flush=True)
+        assert r.returncode == 0, r.stderr
+        return np.fromfile(os.path.join(d, "out.bin"), np.uint8)
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="no node binary")
+@pytest.mark.parametrize("rows,T", [(8, 20), (64, 70)])
+def test_node_backend_batched_prefill_vs_oracle(rows, T):
+    """HipBackend.prefill on the GPU: the prompt through the batched step,
+    `rows` tokens per chunk (the last one short), over the backend's own
+    caches (an identity page table), against the reference's prefill of one
+    forward per token (src/engine.ts:1923-1938; here the oracle's steps
+    from position 600, past the 512 window). Every K/V row the prompt
+    appended (f16) is checked against the oracle's f32 row of its position,
+    the sample is a maximum of the oracle's logits for the last token, and
+    the fused step that follows (from the sample, at position 600 + T, over
+    the prefilled caches) matches the oracle's step."""
+    shape = E2BShape.real(n_layers=4, n_unshared=2, global_layers=(1, 3), vocab=4096)
+    files, formats, hm, kcs, vcs = _model(shape)
+    toks = np.random.default_rng(T).integers(0, shape.vocab, T).astype(np.uint32)
+    cfg = {"overrides": {"num_layers": 4, "num_unshared_layers": 2, "global_layers": [1, 3], "vocab_size": 4096},
+           "maxSeqLen": MAX_SEQ, "position": POS, "token": 0, "formats": formats, "prefill": toks.tolist(),
+           "rows": rows}
+    print(f"[napi] prefill of {T} tokens in chunks of {rows}", flush=True)
+    out = _run_node(cfg, files)
+    first = int(out[:4].view(np.uint32)[0])
+    at = 4
+    got_rows = {}
+    for il in range(shape.n_layers):
+        if not shape.is_producer(il):
+            continue
+        n = 2 * shape.kv_dim_of(il) * T
+        got_rows[il] = [out[at + j * n:at + (j + 1) * n].view(np.float16).astype(np.float32).reshape(T, -1)
+                        for j in range(2)]
+        at += 2 * n
+    H, V = shape.hidden, shape.vocab
+    hidden = out[at:at + 4 * H].view(np.float32)
+    logits = out[at + 4 * H:at + 4 * H + 4 * V].view(np.float32)
+    step_tok = int(out[at + 4 * H + 4 * V:].view(np.uint32)[0])
+    lg = None
+    for t in range(T):
+        want = {}
+        _, lg = hm.step(hm.embed(int(toks[t])), kcs, vcs, POS + t, token=int(toks[t]), rows=want)
+        for il, (k, v) in got_rows.items():
+            assert_close(k[t], want[il][0], what=f"k row {POS + t} layer {il}")
+            assert_close(v[t], want[il][1], what=f"v row {POS + t} layer {il}")
+    print(f"[napi] prefill sample {first}, oracle argmax {O.argmax(lg)}", flush=True)
+    assert lg[first] >= lg.max() - 1e-3 * np.abs(lg).max()
+    x_ref, lg_ref = hm.step(hm.embed(first), kcs, vcs, POS + T, token=first)
+    print(f"[napi] step after prefill: hidden rel-L2 {O.rel_l2(hidden, x_ref):.2e}, logits rel-L2 "
+          f"{O.rel_l2(logits, lg_ref):.2e}", flush=True)
+    assert_close(hidden, x_ref, what="hidden of the step after prefill")
+    assert_close(logits, lg_ref, what="logits of the step after prefill")
+    assert step_tok == O.argmax(logits)
