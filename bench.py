@@ -282,7 +282,8 @@ def graph_us(ctx, body, reps):
 
 
 def attention_cfg3(ctx, reps=3):
-    """Decode attention: 8 query heads, 1 KV head, head_dim 256, f16 K/V ~
+    """Decode attention: 8 query heads, 1 KV head, head_dim 256 (and the
+    fused block at head_dim 512, `hd512_*`), f16 K/V ~
     N(0,1), one sequence, contexts 512 / 4096 / 32768, globally (no window)
     and with the 512-position window; `us` is attention alone (normed q in),
     `fused_block_us` the whole block (q/k norm + RoPE, v_norm, KV store,
@@ -342,6 +343,43 @@ def attention_cfg3(ctx, reps=3):
             fws.free()
             ws.free()
     for b in (k, v, k_raw, v_raw, q_w, k_w, table):
+        b.free()
+    # the fused block at head dim 512 (Gemma-4-E2B's global layers: no
+    # window, theta 1e6 with the divisor table), K/V rotated over 604 MB
+    hd = 512
+    k = ctx.empty(P * hd, np.uint16)
+    v = ctx.empty(P * hd, np.uint16)
+    ctx.fill_normal_f16(k, P * hd, 41, 0.0, 1.0)
+    ctx.fill_normal_f16(v, P * hd, 42, 0.0, 1.0)
+    q = ctx.empty(nqh * hd, np.float32)
+    ctx.fill_normal_f32(q, nqh * hd, 43, 0.0, 1.0)
+    out = ctx.empty(nqh * hd, np.float32)
+    k_raw = ctx.empty(hd, np.float32)
+    v_raw = ctx.empty(hd, np.float32)
+    ctx.fill_normal_f32(k_raw, hd, 44, 0.0, 1.0)
+    ctx.fill_normal_f32(v_raw, hd, 45, 0.0, 1.0)
+    q_w = ctx.empty(hd, np.uint16)
+    k_w = ctx.empty(hd, np.uint16)
+    ctx.fill_normal_f16(q_w, hd, 46, 1.0, 0.1)
+    ctx.fill_normal_f16(k_w, hd, 47, 1.0, 0.1)
+    table = ctx.from_numpy(np.where(np.arange(hd // 2) < hd // 8, 1.0, np.inf).astype(np.float16).view(np.uint16))
+    for L in (513, 4096):
+        fp = ctx.attn_fused_params(nqh, nkh, hd, L, 0, 1e-6, 1e6, 1)
+        fws = ctx.zeros(ctx.attn_fused_workspace_bytes(fp), np.uint8)
+        pdev = ctx.from_numpy(np.array([L - 1], np.uint32))
+        n_rot = P // L
+
+        def fused512():
+            for r in range(n_rot):
+                off = r * L * hd * 2
+                ctx.attnDecodeFused(q, k_raw, v_raw, q_w, k_w, table, k.offset(off), v.offset(off), out, fp, fws,
+                                    pdev)
+        us_f = graph_us(ctx, fused512, reps) / n_rot
+        nbytes = L * 2048 + 2 * nqh * hd * 4
+        res[f"hd512_ctx{L}_global"] = {"fused_block_us": round(us_f, 2), "bytes": nbytes,
+                                       "fused_block_gbps": round(nbytes / (us_f * 1e-6) / 1e9, 1)}
+        fws.free()
+    for b in (k, v, q, out, k_raw, v_raw, q_w, k_w, table):
         b.free()
     return res
 

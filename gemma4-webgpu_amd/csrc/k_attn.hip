@@ -990,10 +990,11 @@ __global__ __launch_bounds__(NT, 2) void mq_attn_kernel(MqArgs a) {
   }
 }
 
-// The fused block as a launch of its own (blockIdx.y = KV head).
-template <bool LONG>
-__global__ __launch_bounds__(NT, 2) void mqf_kernel(MqfArgs a) {
-  mqf_body<LONG, false>(a, blockIdx.x, blockIdx.y, blockIdx.x);
+// The fused block as a launch of its own (blockIdx.y = KV head), for head
+// dim 256 (256 threads) or 512 (512 threads).
+template <bool LONG, int HD>
+__global__ __launch_bounds__(HD, 512 / HD) void mqf_kernel(MqfArgs a) {
+  mqf_body<LONG, false, !LONG, HD>(a, blockIdx.x, blockIdx.y, blockIdx.x);
 }
 
 
@@ -1210,7 +1211,7 @@ int launch_attn(g4_ctx* ctx, const AttnArgs& a, uint32_t G, uint32_t hd, int cp,
 // different windows can share one workspace; the chunk partials follow,
 // then the group partials.
 struct MqfPlan {
-  uint32_t nstep, max_chunks;
+  uint32_t nstep, max_chunks;  // 64-position steps per workgroup, workgroups
   bool partials;  // chunk partials + a merge launch
   size_t bytes_ws0, bytes;
 };
@@ -1222,8 +1223,9 @@ MqfPlan mqf_plan(const g4_attn_fused_params& p) {
   // measured 1.2 us faster at 32K)
   m.nstep = m.partials ? std::max(eff > 16384 ? 2u : 1u, ceil_div(eff, MQ_STEP * kMaxSplits)) : 1u;
   m.max_chunks = ceil_div(eff, MQ_STEP * m.nstep);
-  m.bytes_ws0 = ws_bytes(1, p.num_kv_heads, m.max_chunks, MQ_G, MQ_HD);
-  m.bytes = kMqfCnt + m.bytes_ws0 + (m.partials ? 0 : ws_bytes(1, p.num_kv_heads, MQF_FAN, MQ_G, MQ_HD));
+  const uint32_t hd = p.head_dim == 512 ? 512u : (uint32_t)MQ_HD;
+  m.bytes_ws0 = ws_bytes(1, p.num_kv_heads, m.max_chunks, MQ_G, hd);
+  m.bytes = kMqfCnt + m.bytes_ws0 + (m.partials ? 0 : ws_bytes(1, p.num_kv_heads, MQF_FAN, MQ_G, hd));
   return m;
 }
 
@@ -1367,7 +1369,8 @@ int mqf_prepare(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float
                 float* output, const g4_attn_fused_params& p, void* workspace, size_t workspace_bytes,
                 const uint32_t* position_dev, const g4_warm_region* regions, int nregions, const float* rope_cs,
                 uint32_t busy_extra, bool& applies, MqfLaunch& L) {
-  applies = p.head_dim == MQ_HD && p.num_q_heads == MQ_G * p.num_kv_heads && p.num_kv_heads <= kMqfMaxKvHeads &&
+  applies = (p.head_dim == 256 || p.head_dim == 512) && p.num_q_heads == MQ_G * p.num_kv_heads &&
+            p.num_kv_heads <= kMqfMaxKvHeads &&
             ((uintptr_t)q_norm_w & 15) == 0 && eff_len(p.max_seq_len, p.sliding_window) <= 4 * MQ_STEP * MQF_FAN * MQF_FAN;
   if (!applies) return G4_OK;
   const MqfPlan mp = mqf_plan(p);
@@ -1687,16 +1690,19 @@ int g4_attnDecodeFusedWarm(g4_ctx* ctx, const float* q_raw, const float* k_raw, 
   if (rc) return rc;
   if (one_launch) {
     const MqfArgs& m = L.m;
-    if (L.partials)
-      hipLaunchKernelGGL(mqf_kernel<true>, dim3(m.max_chunks + m.nwarm, p.num_kv_heads), dim3(NT),
-                         m.nwarm ? kWarmLds : 0, ctx->stream, m);
-    else
-      hipLaunchKernelGGL(mqf_kernel<false>, dim3(m.max_chunks + m.nwarm, p.num_kv_heads), dim3(NT),
-                         m.nwarm ? kWarmLds : 0, ctx->stream, m);
+    const dim3 grid(m.max_chunks + m.nwarm, p.num_kv_heads);
+    if (p.head_dim == 512) {  // (its LDS already keeps one workgroup per CU)
+      if (L.partials) hipLaunchKernelGGL((mqf_kernel<true, 512>), grid, dim3(512), 0, ctx->stream, m);
+      else hipLaunchKernelGGL((mqf_kernel<false, 512>), grid, dim3(512), 0, ctx->stream, m);
+    } else {
+      const size_t lds = m.nwarm ? kWarmLds : 0;
+      if (L.partials) hipLaunchKernelGGL((mqf_kernel<true, 256>), grid, dim3(NT), lds, ctx->stream, m);
+      else hipLaunchKernelGGL((mqf_kernel<false, 256>), grid, dim3(NT), lds, ctx->stream, m);
+    }
     G4_LAUNCHED(ctx, "attn_decode_fused_mfma");
     if (!L.partials) return G4_OK;
     const LenArgs la{nullptr, position_dev, p.max_seq_len, p.max_seq_len, p.sliding_window};
-    return merge_launch(ctx, m.ws, output, p.num_q_heads, p.num_kv_heads, MQ_G, MQ_HD, m.max_chunks, 1, la,
+    return merge_launch(ctx, m.ws, output, p.num_q_heads, p.num_kv_heads, MQ_G, p.head_dim, m.max_chunks, 1, la,
                         MQ_STEP * m.nstep);
   }
   // (the two-launch form computes the RoPE per call: a table is not needed)

@@ -2364,7 +2364,8 @@ int qkv_attn(g4_ctx* ctx, const char* fn, bool merge, const float* x, const uint
   }
   bool applies = false;
   g4mqf::MqfLaunch L{};
-  if (N == 1536 && mnwv == 6 && nseg == 3 && p.num_kv_heads == 1 && rows[0] + 2 * rows[1] <= g4mqf::kMaxStage) {
+  if (N == 1536 && mnwv == 6 && nseg == 3 && p.num_kv_heads == 1 && p.head_dim == g4mqf::MQ_HD &&
+      rows[0] + 2 * rows[1] <= g4mqf::kMaxStage) {
     rc = g4mqf::mqf_prepare(ctx, q_raw, k_raw, v_raw, q_norm_w, k_norm_w, rope_freqs, k_cache, v_cache, output, p,
                             workspace, workspace_bytes, position_dev, regions, nregions, rope_cs, nmv, applies, L);
     if (rc) return rc;

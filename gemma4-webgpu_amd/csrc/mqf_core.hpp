@@ -36,10 +36,27 @@ typedef _Float16 mh4 __attribute__((ext_vector_type(4)));
 typedef float mf4 __attribute__((ext_vector_type(4)));
 typedef uint32_t mu4 __attribute__((ext_vector_type(4)));
 
-constexpr int MQ_STEP = 64;  // positions per step
+constexpr int MQ_STEP = 64;  // positions per step (head dim 256)
 constexpr int MQ_RS = 264;   // LDS row stride in halves (528 B)
 constexpr int MQ_G = 8, MQ_HD = 256;
 constexpr int kDppRor8 = 0x128;  // row_ror:8 within 16 lanes
+
+// The block's shape per head dim: one thread per dim of a K/V row, so
+// 256 threads (4 waves) at head dim 256 and 512 (8 waves) at 512. A step is
+// 64 positions in 16-position row tiles; wave w takes row tile w % 4 and the
+// 256 dims from 256 (w / 4) on, so every wave multiplies 16 positions x 256
+// dims at either head dim. In the prologue and the merge a head's values
+// are spread over HD / 8 threads, 4 dims of each RoPE half per thread.
+template <int HD>
+struct MqShape {
+  static_assert(HD == 256 || HD == 512, "head dim 256 or 512");
+  static constexpr int NT = HD;        // threads
+  static constexpr int NW = NT / 64;   // waves
+  static constexpr int NH = HD / 256;  // 256-dim halves of a row
+  static constexpr int RS = HD + 8;    // K/V row stride in LDS (halves)
+  static constexpr int QS = HD + 8;    // q column stride in LDS (halves)
+  static constexpr int TPH = HD / 8;   // threads per head in the prologue and the merge
+};
 
 // Fused single-sequence form over a dense cache (the one-token decode step),
 // the whole attention block of src/engine.ts:1556-1584 in one launch:
@@ -60,8 +77,8 @@ constexpr int kMaxWarm = 4;
 // half of the CU's 160 KB, so one workgroup per CU (unused otherwise).
 constexpr size_t kWarmLds = 16384;
 struct MqfArgs {
-  const float* q_raw;  // [nqh][256]
-  const float* k_raw;  // [nkh][256]
+  const float* q_raw;  // [nqh][head dim]
+  const float* k_raw;  // [nkh][head dim]
   const float* v_raw;
   const uint16_t* q_w;
   const uint16_t* k_w;
@@ -69,17 +86,17 @@ struct MqfArgs {
   float theta;
   uint32_t apply_divisor;
   float eps;
-  uint16_t* kc;  // [cap][nkh][256]
+  uint16_t* kc;  // [cap][nkh][head dim]
   uint16_t* vc;
   const uint32_t* pos_dev;
   uint32_t cap, nqh, nkh;
   float scale;
   uint32_t window;
-  uint32_t nstep, max_chunks;
+  uint32_t nstep, max_chunks;  // steps per chunk (of the head dim's step), chunks
   float* ws;      // chunk partials [nkh][max_chunks][8] (m, l, o)
   float* ws1;     // group partials [nkh][MQF_FAN][8] (m, l, o)
   uint32_t* cnt;  // [nkh][MQF_CNT] arrivals (groups, then the top), zero between calls
-  float* out;     // [nqh][256]
+  float* out;     // [nqh][head dim]
   // L2 warming: workgroups max_chunks.. of row 0 read the weights of the
   // launches that follow (see mqf_warm)
   const uint8_t* wbase[kMaxWarm];
@@ -87,7 +104,7 @@ struct MqfArgs {
   uint32_t wwgb[kMaxWarm];    // bytes each consuming workgroup reads
   uint32_t wnwg[kMaxWarm];    // consuming workgroups
   uint32_t nwarm_regions, nwarm;  // regions; warming workgroups (a multiple of 8)
-  const float2* rope_cs;          // [cap][128] (cos, sin) of every position (g4_ropeTable), or null
+  const float2* rope_cs;          // [cap][head dim / 2] (cos, sin) of every position (g4_ropeTable), or null
   // the launch that also runs the q/k/v matvec (mqf_body<false, true>):
   // q, k and v staged as (tag << 32 | f32 bits) pairs, tag 1 once the matvec
   // stored the value, reset to 0 by the merger ([nqh][256] q, [nkh][256] k,
@@ -237,6 +254,7 @@ int mqf_prepare(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float
 // j = c + 8 (p / 8 + R i), R = nwarm / 8. These workgroups run on the CUs
 // the attention leaves idle; the loads go through a buffer resource sized to
 // each matrix, so a partial last tile reads zeros past its end.
+template <int NT = MQ_NT>
 __device__ __forceinline__ void mqf_warm(const MqfArgs& a, uint32_t p, uint32_t c) {
   const uint32_t r = p >> 3, R = a.nwarm >> 3;
   const uint32_t t = threadIdx.x;
@@ -251,7 +269,7 @@ __device__ __forceinline__ void mqf_warm(const MqfArgs& a, uint32_t p, uint32_t 
     nwg[g] = on ? a.wnwg[g] : 0u;
     maxwg = max(maxwg, nwg[g]);
   }
-  constexpr uint32_t kStep = 64u * MQ_NT * 8u;  // bytes one round of 8 loads covers
+  constexpr uint32_t kStep = 64u * NT * 8u;  // bytes one round of 8 loads covers
   uint32_t acc = 0;
   // one region's round at a time, the workgroups' first rounds staggered:
   // a burst of every region at once queued ahead of the attention's own
@@ -265,7 +283,7 @@ __device__ __forceinline__ void mqf_warm(const MqfArgs& a, uint32_t p, uint32_t 
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           // one dword per 64-byte line brings the line into the cache
-          const uint32_t off = o + (64u * MQ_NT) * (uint32_t)k + 64u * t;
+          const uint32_t off = o + (64u * NT) * (uint32_t)k + 64u * t;
           const bool in = j < nwg[g] && off < wgb[g];
           v[k] = __builtin_amdgcn_raw_buffer_load_b32(rs[g], in ? j * wgb[g] + off : 0xfffffff0u, 0, 0);
         }
@@ -283,27 +301,37 @@ __device__ __forceinline__ void mqf_warm(const MqfArgs& a, uint32_t p, uint32_t 
 // FUSED && !MERGE: the launch that also runs the q/k/v matvec, whose
 // workgroups end after storing their partials; the o projection's launch
 // merges them per head (attn_heads_kernel) and clears the staged q/k/v.
-template <bool LONG, bool FUSED, bool MERGE = !LONG>
+// HD: the head dim (MqShape: HD threads); the matvec hand-off is built for 256.
+template <bool LONG, bool FUSED, bool MERGE = !LONG, int HD = MQ_HD>
 __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t kvh, uint32_t lin) {
   static_assert(!(LONG && FUSED), "the fused matvec form merges in the launch or in the o projection");
   static_assert(!(LONG && MERGE), "the long form merges in a launch of its own");
+  static_assert(!FUSED || HD == MQ_HD, "the q/k/v hand-off is built for head dim 256");
+  using Sh = MqShape<HD>;
+  constexpr int NT = Sh::NT, NW = Sh::NW, RS = Sh::RS, QS = Sh::QS, TPH = Sh::TPH;
+  constexpr int PR = HD / 8;  // 16-byte pieces of a K/V row
   if (bx >= a.max_chunks) {  // (uniform) L2 warming workgroups
-    if (kvh == 0) mqf_warm(a, bx - a.max_chunks, lin & 7u);
+    if (kvh == 0) mqf_warm<NT>(a, bx - a.max_chunks, lin & 7u);
     return;
   }
-  // K and V tiles; after the last step, the waves' o rows [4 waves][256 dims][16 rows]
-  __shared__ __align__(16) _Float16 kvt[2 * MQ_STEP * MQ_RS];
-  __shared__ __align__(16) _Float16 qs[16 * MQF_QS];  // B operand: column c = head c % 8, hi (c < 8) / lo
-  __shared__ float2 cs_s[MQ_HD / 2];
-  __shared__ float red_s[8];
-  __shared__ float kn_s[MQ_HD];
-  __shared__ __align__(16) uint16_t cur_s[2 * MQ_HD];  // the current row: k (roped), v; f16
-  __shared__ float ml_s[2 * 4 * MQ_G];                 // per (wave, head) m, then l
-  __shared__ __align__(16) float wt_s[4 * MQ_G];       // per (wave, head) weight
+  // K and V tiles; after the last step, the waves' o rows [NW waves][256 dims][16 rows]
+  __shared__ __align__(16) _Float16 kvt[2 * MQ_STEP * RS];
+  static_assert(2 * MQ_STEP * RS * 2 >= NW * 256 * 16 * 4, "the o rows fit in the K/V tiles");
+  // B operand: column c = head c % 8, hi (c < 8) / lo; once the waves hold
+  // it in registers, the space takes their partial scores (head dim 512)
+  __shared__ __align__(16) _Float16 qs[16 * QS];
+  static_assert(16 * QS * 2 >= NW * 64 * 16, "the scores fit in the q operand's space");
+  __shared__ float2 cs_s[HD / 2];
+  __shared__ float red_s[2 * NW];
+  __shared__ float kn_s[HD];
+  __shared__ __align__(16) uint16_t cur_s[2 * HD];  // the current row: k (roped), v; f16
+  __shared__ float ml_s[2 * NW * MQ_G];             // per (wave, head) m, then l
+  __shared__ __align__(16) float wt_s[4 * MQ_G];    // per (row tile, head) weight
   __shared__ uint32_t s_last;
   _Float16* const kt = kvt;
-  _Float16* const vt = kvt + MQ_STEP * MQ_RS;
+  _Float16* const vt = kvt + MQ_STEP * RS;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q = l >> 4, c = l & 15;
+  const int rt = w & 3, dh = w >> 2;  // this wave's row tile and 256-dim half
   const uint32_t chunk = bx;
   const uint32_t CH = MQ_STEP * a.nstep;
   const uint32_t L = min(*a.pos_dev + 1, a.cap);
@@ -320,36 +348,38 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   const bool own_row = a.k_raw != nullptr;
   const bool owner = cend == n && own_row;
   // thread -> (head, 4 dims of each RoPE half) for q, the partial and the merge
-  const int th = tid >> 5, td = 4 * (tid & 31);
+  const int th = tid / TPH, td = 4 * (tid % TPH);
 
+  // a step's K rows, then its V rows: piece pc = tid + NT (i % 8) is row
+  // pc / PR, 16 bytes at column 8 (pc % PR)
   mu4 pf[16];
   auto load_step = [&](uint32_t st) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const uint32_t pc = (uint32_t)tid + 256u * (uint32_t)(i & 7);
-      const uint32_t r = pc >> 5, col = (pc & 31) * 8;
+      const uint32_t pc = (uint32_t)tid + (uint32_t)NT * (uint32_t)(i & 7);
+      const uint32_t r = pc / PR, col = (pc % PR) * 8;
       const uint32_t p = min(wstart + c0 + st * MQ_STEP + r, last);
       const uint16_t* base = i < 8 ? a.kc : a.vc;
-      const mu4* src = (const mu4*)(base + ((size_t)p * a.nkh + kvh) * MQ_HD + col);
+      const mu4* src = (const mu4*)(base + ((size_t)p * a.nkh + kvh) * HD + col);
       pf[i] = LONG ? __builtin_nontemporal_load(src) : *src;
     }
   };
   auto store_step = [&]() {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const uint32_t pc = (uint32_t)tid + 256u * (uint32_t)(i & 7);
-      const uint32_t r = pc >> 5, col = (pc & 31) * 8;
-      *(mu4*)((i < 8 ? kt : vt) + r * MQ_RS + col) = pf[i];
+      const uint32_t pc = (uint32_t)tid + (uint32_t)NT * (uint32_t)(i & 7);
+      const uint32_t r = pc / PR, col = (pc % PR) * 8;
+      *(mu4*)((i < 8 ? kt : vt) + r * RS + col) = pf[i];
     }
   };
   // the owner's last step: rows from the current position on (the clamped
   // rows repeat it) take the row formed here, not the cache's stale one
   auto patch = [&](uint32_t st) {
     const uint32_t r0 = last - (wstart + c0 + st * MQ_STEP);
-    for (uint32_t e = (uint32_t)tid; e < (MQ_STEP - r0) * 32; e += MQ_NT) {
-      const uint32_t r = r0 + e / 32, col = (e % 32) * 8;
-      *(mu4*)(kt + r * MQ_RS + col) = *(const mu4*)(cur_s + col);
-      *(mu4*)(vt + r * MQ_RS + col) = *(const mu4*)(cur_s + MQ_HD + col);
+    for (uint32_t e = (uint32_t)tid; e < (MQ_STEP - r0) * PR; e += NT) {
+      const uint32_t r = r0 + e / PR, col = (e % PR) * 8;
+      *(mu4*)(kt + r * RS + col) = *(const mu4*)(cur_s + col);
+      *(mu4*)(vt + r * RS + col) = *(const mu4*)(cur_s + HD + col);
     }
   };
 
@@ -357,24 +387,23 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   // (FUSED: q, k and v come from the matvec workgroups of the same launch;
   // the K/V rows and the weights are requested first, then the staged q/k/v
   // are polled until every value this thread needs is there)
-  const size_t qoff = (size_t)(kvh * MQ_G + th) * MQ_HD + td;
+  const size_t qoff = (size_t)(kvh * MQ_G + th) * HD + td;
   float4 q0, q1;
   float kx, vx;
   bool stalled = false;  // (uniform) FUSED: the wait for q/k/v expired
   if constexpr (!FUSED) {
     const float* qg = a.q_raw + qoff;
     q0 = *(const float4*)qg;
-    q1 = *(const float4*)(qg + MQ_HD / 2);
+    q1 = *(const float4*)(qg + HD / 2);
   }
-  const uint2 w0 = *(const uint2*)(a.q_w + td), w1 = *(const uint2*)(a.q_w + MQ_HD / 2 + td);
+  const uint2 w0 = *(const uint2*)(a.q_w + td), w1 = *(const uint2*)(a.q_w + HD / 2 + td);
   if constexpr (!FUSED) {
-    kx = own_row ? a.k_raw[(size_t)kvh * MQ_HD + tid] : 0.f;
-    vx = own_row ? a.v_raw[(size_t)kvh * MQ_HD + tid] : 0.f;
+    kx = own_row ? a.k_raw[(size_t)kvh * HD + tid] : 0.f;
+    vx = own_row ? a.v_raw[(size_t)kvh * HD + tid] : 0.f;
   }
   const float kw = own_row ? g4d::f16_bits_to_f32(a.k_w[tid]) : 0.f;
-  const uint16_t rfb = a.rope_freqs[tid & (MQ_HD / 2 - 1)];
-  const float2 cst =
-      a.rope_cs ? a.rope_cs[(size_t)pos * (MQ_HD / 2) + (tid & (MQ_HD / 2 - 1))] : make_float2(1.f, 0.f);
+  const uint16_t rfb = a.rope_freqs[tid & (HD / 2 - 1)];
+  const float2 cst = a.rope_cs ? a.rope_cs[(size_t)pos * (HD / 2) + (tid & (HD / 2 - 1))] : make_float2(1.f, 0.f);
   __builtin_amdgcn_sched_barrier(0);
   load_step(0);
   __builtin_amdgcn_sched_barrier(0);
@@ -383,25 +412,30 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   // RoPE of this position (rope_cos_sin), from the table when there is one:
   // the frequency's f64 pow and a large-argument sincos are some 380 VALU
   // instructions of the prologue's critical path
-  if (tid < MQ_HD / 2) cs_s[tid] = a.rope_cs ? cst : rope_cos_sin(a.theta, a.apply_divisor, rfb, tid, MQ_HD, pos);
+  if (tid < HD / 2) cs_s[tid] = a.rope_cs ? cst : rope_cos_sin(a.theta, a.apply_divisor, rfb, tid, HD, pos);
   const float sk = g4d::wave_sum_dpp(kx * kx), sv = g4d::wave_sum_dpp(vx * vx);
   if (l == 0) {
     red_s[w] = sk;
-    red_s[4 + w] = sv;
+    red_s[NW + w] = sv;
   }
-  // q: the head's sum of squares over its 32 threads (two DPP rows)
+  // q: the head's sum of squares over its TPH threads (DPP rows, then the
+  // half-wave swap, then at head dim 512 the wave's two halves)
   float qss = (q0.x * q0.x + q0.y * q0.y) + (q0.z * q0.z + q0.w * q0.w) + (q1.x * q1.x + q1.y * q1.y) +
               (q1.z * q1.z + q1.w * q1.w);
   qss = g4d::sum16(qss);
   qss = g4d::xsum16(qss);
-  const float invq = __builtin_amdgcn_rsqf(qss * (1.0f / (float)MQ_HD) + a.eps);
+  if constexpr (TPH == 64) qss = g4d::xsum32(qss);
+  const float invq = __builtin_amdgcn_rsqf(qss * (1.0f / (float)HD) + a.eps);
   __syncthreads();
-  const float invk =
-      __builtin_amdgcn_rsqf(((red_s[0] + red_s[1]) + (red_s[2] + red_s[3])) * (1.0f / (float)MQ_HD) + a.eps);
-  const float invv =
-      __builtin_amdgcn_rsqf(((red_s[4] + red_s[5]) + (red_s[6] + red_s[7])) * (1.0f / (float)MQ_HD) + a.eps);
+  float skk = (red_s[0] + red_s[1]) + (red_s[2] + red_s[3]), svv = (red_s[NW] + red_s[NW + 1]) + (red_s[NW + 2] + red_s[NW + 3]);
+  if constexpr (NW == 8) {
+    skk += (red_s[4] + red_s[5]) + (red_s[6] + red_s[7]);
+    svv += (red_s[12] + red_s[13]) + (red_s[14] + red_s[15]);
+  }
+  const float invk = __builtin_amdgcn_rsqf(skk * (1.0f / (float)HD) + a.eps);
+  const float invv = __builtin_amdgcn_rsqf(svv * (1.0f / (float)HD) + a.eps);
   kn_s[tid] = kx * kw * invk;
-  cur_s[MQ_HD + tid] = g4d::f32_to_f16_bits(vx * invv);
+  cur_s[HD + tid] = g4d::f32_to_f16_bits(vx * invv);
   {
     const float x0[4] = {q0.x, q0.y, q0.z, q0.w}, x1[4] = {q1.x, q1.y, q1.z, q1.w};
     const uint32_t wa[4] = {w0.x & 0xffffu, w0.x >> 16, w0.y & 0xffffu, w0.y >> 16};
@@ -418,29 +452,30 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
       h1[e] = (_Float16)r1;
       l1[e] = (_Float16)(r1 - (float)h1[e]);
     }
-    *(mh4*)(qs + th * MQF_QS + td) = h0;
-    *(mh4*)(qs + (th + 8) * MQF_QS + td) = l0;
-    *(mh4*)(qs + th * MQF_QS + MQ_HD / 2 + td) = h1;
-    *(mh4*)(qs + (th + 8) * MQF_QS + MQ_HD / 2 + td) = l1;
+    *(mh4*)(qs + th * QS + td) = h0;
+    *(mh4*)(qs + (th + 8) * QS + td) = l0;
+    *(mh4*)(qs + th * QS + HD / 2 + td) = h1;
+    *(mh4*)(qs + (th + 8) * QS + HD / 2 + td) = l1;
   }
   __syncthreads();
-  if (tid < MQ_HD / 2) {
+  if (tid < HD / 2) {
     const float2 cs = cs_s[tid];
-    const float x0 = kn_s[tid], x1 = kn_s[tid + MQ_HD / 2];
+    const float x0 = kn_s[tid], x1 = kn_s[tid + HD / 2];
     cur_s[tid] = g4d::f32_to_f16_bits(x0 * cs.x - x1 * cs.y);
-    cur_s[tid + MQ_HD / 2] = g4d::f32_to_f16_bits(x0 * cs.y + x1 * cs.x);
+    cur_s[tid + HD / 2] = g4d::f32_to_f16_bits(x0 * cs.y + x1 * cs.x);
   }
   store_step();
   __syncthreads();
   if (owner) {
-    a.kc[((size_t)pos * a.nkh + kvh) * MQ_HD + tid] = cur_s[tid];
-    a.vc[((size_t)pos * a.nkh + kvh) * MQ_HD + tid] = cur_s[MQ_HD + tid];
+    a.kc[((size_t)pos * a.nkh + kvh) * HD + tid] = cur_s[tid];
+    a.vc[((size_t)pos * a.nkh + kvh) * HD + tid] = cur_s[HD + tid];
     if (nst == 1) patch(0);
   }
   mh8 qb[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) qb[j] = *(const mh8*)(qs + c * MQF_QS + 32 * j + 8 * q);
+  for (int j = 0; j < 8; ++j) qb[j] = *(const mh8*)(qs + c * QS + 256 * dh + 32 * j + 8 * q);
   __syncthreads();
+  float* const sx = (float*)qs;  // (head dim 512) the waves' partial scores
 
   mf4 O[16];
 #pragma unroll
@@ -453,15 +488,24 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
     mf4 S = mf4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const mh8 A = *(const mh8*)(kt + (16 * w + c) * MQ_RS + 32 * j + 8 * q);
+      const mh8 A = *(const mh8*)(kt + (16 * rt + c) * RS + 256 * dh + 32 * j + 8 * q);
       S = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, qb[j], S, 0, 0, 0);
+    }
+    if constexpr (NW == 8) {
+      // a row tile's scores over its two dim halves, added in the same order
+      // in both of its waves (so both hold the same scores)
+      *(mf4*)(sx + (w * 64 + l) * 4) = S;
+      __syncthreads();
+      const mf4 s0 = *(const mf4*)(sx + (rt * 64 + l) * 4), s1 = *(const mf4*)(sx + ((4 + rt) * 64 + l) * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) S[i] = s0[i] + s1[i];
     }
     float sc[4];
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float v = S[i] + g4d::dpp<kDppRor8>(S[i]);
-      const uint32_t off = c0 + st * MQ_STEP + 16u * w + 4u * q + i;
+      const uint32_t off = c0 + st * MQ_STEP + 16u * rt + 4u * q + i;
       sc[i] = off < cend ? v * a.scale : -INFINITY;
       mx = fmaxf(mx, sc[i]);
     }
@@ -495,7 +539,7 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
     for (int dt = 0; dt < 16; ++dt) {
       mh4 Bv;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) Bv[i] = vt[(16 * w + 4 * q + i) * MQ_RS + 16 * dt + c];
+      for (int i = 0; i < 4; ++i) Bv[i] = vt[(16 * rt + 4 * q + i) * RS + 256 * dh + 16 * dt + c];
       mf4 o = O[dt];
       if (st > 0) {  // (uniform) the first step's O is zero
 #pragma unroll
@@ -514,22 +558,23 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
     }
   }
 
-  // ---- the four waves, then this chunk's partial ----
+  // ---- the waves, then this chunk's partial ----
   // O row 4q + i of lane (q, c) is head (4q + i) % 8 (the p_hi rows for
-  // q < 2, the p_lo rows for q >= 2) at dim 16 dt + c.
+  // q < 2, the p_lo rows for q >= 2) at dim 256 dh + 16 dt + c; wave w's
+  // 256 dims go to block w of ow.
   float* ow = (float*)kvt;
 #pragma unroll
-  for (int dt = 0; dt < 16; ++dt) *(mf4*)(ow + ((w * MQ_HD) + 16 * dt + c) * 16 + 4 * q) = O[dt];
+  for (int dt = 0; dt < 16; ++dt) *(mf4*)(ow + ((w * 256) + 16 * dt + c) * 16 + 4 * q) = O[dt];
   if (q == 0 && c < MQ_G) {
     ml_s[w * MQ_G + c] = m_run;
-    ml_s[4 * MQ_G + w * MQ_G + c] = l_run;
+    ml_s[NW * MQ_G + w * MQ_G + c] = l_run;
   }
   __syncthreads();
   const size_t nparts = (size_t)a.nkh * a.max_chunks * MQ_G;
-  // chunk partials: m [nparts], l [nparts], o [nparts][256] (f32)
-  const __amdgpu_buffer_rsrc_t r0 = dev_rsrc(a.ws, (uint32_t)(nparts * (MQ_HD + 2) * sizeof(float)));
+  // chunk partials: m [nparts], l [nparts], o [nparts][HD] (f32)
+  const __amdgpu_buffer_rsrc_t r0 = dev_rsrc(a.ws, (uint32_t)(nparts * (HD + 2) * sizeof(float)));
   const size_t part0 = ((size_t)kvh * a.max_chunks + chunk) * MQ_G;
-  if (tid < MQ_G) {  // thread h: the head's weight per wave and the chunk's (m, l)
+  if (tid < MQ_G) {  // thread h: the head's weight per row tile and the chunk's (m, l)
     float m4[4], M = -INFINITY;
 #pragma unroll
     for (int ww = 0; ww < 4; ++ww) {
@@ -541,20 +586,21 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
     for (int ww = 0; ww < 4; ++ww) {
       const float wt = m4[ww] == -INFINITY ? 0.f : mq_exp(m4[ww] - M);
       wt_s[ww * MQ_G + tid] = wt;
-      Ls += wt * ml_s[4 * MQ_G + ww * MQ_G + tid];
+      Ls += wt * ml_s[NW * MQ_G + ww * MQ_G + tid];
     }
     // a stalled chunk's +Inf maximum turns every merge that includes it into NaN
     st_dev(r0, (uint32_t)(part0 + tid) * 4u, stalled ? INFINITY : M);
     st_dev(r0, (uint32_t)(nparts + part0 + tid) * 4u, Ls);
   }
   __syncthreads();
-  {  // thread = dim: o[h] = sum over waves of wt * (hi row + lo row)
+  {  // thread = dim: o[h] = sum over row tiles of wt * (hi row + lo row)
     float o[MQ_G];
 #pragma unroll
     for (int h = 0; h < MQ_G; ++h) o[h] = 0.f;
+    const int e = tid >> 8, d = tid & 255;  // dim half, dim within it
 #pragma unroll
     for (int ww = 0; ww < 4; ++ww) {
-      const float* r = ow + (ww * MQ_HD + tid) * 16;
+      const float* r = ow + ((e * 4 + ww) * 256 + d) * 16;
       const mf4 h03 = *(const mf4*)r, h47 = *(const mf4*)(r + 4), l03 = *(const mf4*)(r + 8),
                 l47 = *(const mf4*)(r + 12);
       const mf4 w03 = *(const mf4*)(wt_s + ww * MQ_G), w47 = *(const mf4*)(wt_s + ww * MQ_G + 4);
@@ -565,12 +611,12 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
       }
     }
 #pragma unroll
-    for (int h = 0; h < MQ_G; ++h) st_dev(r0, (uint32_t)(2 * nparts + (part0 + h) * MQ_HD + tid) * 4u, o[h]);
+    for (int h = 0; h < MQ_G; ++h) st_dev(r0, (uint32_t)(2 * nparts + (part0 + h) * HD + tid) * 4u, o[h]);
   }
   if constexpr (!MERGE) return;  // a later launch combines the chunks
 
   // ---- merge tree: the last arriver of each group merges it in chunk order ----
-  // thread (head th, dims td.. and td + 128..): one pass with a running maximum
+  // thread (head th, dims td.. and HD / 2 + td..): one pass with a running maximum
   auto merge = [&](__amdgpu_buffer_rsrc_t r, size_t stride, size_t first, uint32_t count, float& M, float& Ls,
                    float4& o0, float4& o1) {
     M = -INFINITY;
@@ -581,9 +627,9 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
     for (uint32_t s2 = 0; s2 < count; ++s2) {
       const size_t pp = first + (size_t)s2 * MQ_G + th;
       const float m = ld_dev(r, (uint32_t)pp * 4u), lv = ld_dev(r, (uint32_t)(stride + pp) * 4u);
-      const uint32_t ob = (uint32_t)(2 * stride + pp * MQ_HD + td) * 4u;
+      const uint32_t ob = (uint32_t)(2 * stride + pp * HD + td) * 4u;
       const float4 a0 = ld_dev4(r, ob);
-      const float4 a1 = ld_dev4(r, ob + MQ_HD / 2 * 4u);
+      const float4 a1 = ld_dev4(r, ob + HD / 2 * 4u);
       const float Mn = fmaxf(M, m);
       const float fo = M == -INFINITY ? 0.f : mq_exp(M - Mn);
       const float fn = m == -INFINITY ? 0.f : mq_exp(m - Mn);
@@ -598,46 +644,46 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   // The partials are written and read with device-scope accesses (written
   // through / read past the XCD-local L2), so an arrival needs only its own
   // stores complete, not a write-back or invalidation of the whole L2.
-  auto arrive = [&](uint32_t* c, uint32_t fanin) -> bool {
+  auto arrive = [&](uint32_t* cp, uint32_t fanin) -> bool {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_s_waitcnt(0);  // every store of this thread has completed
     __syncthreads();
     if (tid == 0)
-      s_last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == fanin - 1 ? 1u : 0u;
+      s_last = __hip_atomic_fetch_add(cp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == fanin - 1 ? 1u : 0u;
     __syncthreads();
     if (!s_last) return false;
-    if (tid == 0) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // all arrivals are in
+    if (tid == 0) __hip_atomic_store(cp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // all arrivals are in
     return true;
   };
   auto write_out = [&](float Ls, const float4& o0, const float4& o1) {
     const float li = Ls > 0.f ? 1.0f / Ls : 0.f;
-    float* dst = a.out + ((size_t)kvh * MQ_G + th) * MQ_HD + td;
+    float* dst = a.out + ((size_t)kvh * MQ_G + th) * HD + td;
     *(float4*)dst = make_float4(o0.x * li, o0.y * li, o0.z * li, o0.w * li);
-    *(float4*)(dst + MQ_HD / 2) = make_float4(o1.x * li, o1.y * li, o1.z * li, o1.w * li);
+    *(float4*)(dst + HD / 2) = make_float4(o1.x * li, o1.y * li, o1.z * li, o1.w * li);
   };
   uint32_t* cnt = a.cnt + (size_t)kvh * MQF_CNT;
   const uint32_t ng = (nch + MQF_FAN - 1) / MQF_FAN, g = chunk / MQF_FAN;
   if (!arrive(cnt + g, min(MQF_FAN, nch - g * MQF_FAN))) return;
   float M, Ls;
   float4 o0, o1;
-  merge(r0, nparts, ((size_t)kvh * a.max_chunks + g * MQF_FAN) * MQ_G,
-        min(MQF_FAN, nch - g * MQF_FAN), M, Ls, o0, o1);
+  merge(r0, nparts, ((size_t)kvh * a.max_chunks + g * MQF_FAN) * MQ_G, min(MQF_FAN, nch - g * MQF_FAN), M, Ls, o0,
+        o1);
   if (ng == 1) {
     if constexpr (FUSED) mqf_clear_stage(a, tid);
     write_out(Ls, o0, o1);
     return;
   }
   const size_t nparts1 = (size_t)a.nkh * MQF_FAN * MQ_G;
-  const __amdgpu_buffer_rsrc_t r1 = dev_rsrc(a.ws1, (uint32_t)(nparts1 * (MQ_HD + 2) * sizeof(float)));
+  const __amdgpu_buffer_rsrc_t r1 = dev_rsrc(a.ws1, (uint32_t)(nparts1 * (HD + 2) * sizeof(float)));
   {
     const size_t pp = ((size_t)kvh * MQF_FAN + g) * MQ_G + th;
-    if ((tid & 31) == 0) {
+    if ((tid % TPH) == 0) {
       st_dev(r1, (uint32_t)pp * 4u, M);
       st_dev(r1, (uint32_t)(nparts1 + pp) * 4u, Ls);
     }
-    const uint32_t ob = (uint32_t)(2 * nparts1 + pp * MQ_HD + td) * 4u;
+    const uint32_t ob = (uint32_t)(2 * nparts1 + pp * HD + td) * 4u;
     st_dev4(r1, ob, o0);
-    st_dev4(r1, ob + MQ_HD / 2 * 4u, o1);
+    st_dev4(r1, ob + HD / 2 * 4u, o1);
   }
   if (!arrive(cnt + MQF_CNT - 1, ng)) return;
   merge(r1, nparts1, (size_t)kvh * MQF_FAN * MQ_G, ng, M, Ls, o0, o1);

@@ -790,9 +790,10 @@ class Decoder(_SyntheticModel):
         return g
 
     def launches_per_step_fused(self) -> int:
-        """Kernel launches of step_fused with argmax sampling: 5 per layer (6
-        where the attention takes a launch and a merge: head dim 512, or a
-        window longer than the one-launch plan's), the head with its argmax
+        """Kernel launches of step_fused with argmax sampling: 5 per layer (4
+        where the q/k/v matvec and the attention share one launch; 6 where
+        the attention takes a launch and a merge: a window longer than 1024
+        positions), the head with its argmax
         candidates (1) and their reduction, which also advances the position
         (1), and the embedding lookup when there is a table; with per-layer
         embeddings 2 before the layers, 2 per layer and the last tail; more

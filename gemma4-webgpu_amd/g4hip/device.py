@@ -449,11 +449,13 @@ class Context:
 
     @staticmethod
     def attn_fused_single_launch(p: AttnFusedParams) -> bool:
-        """Whether g4_attnDecodeFused runs as one launch (the matrix-core plan:
-        head dim 256, at most 64 KV heads, a window of at most 65536
-        positions) rather than an attention launch and a merge launch."""
+        """Whether g4_attnDecodeFused runs as one launch (the matrix-core plan
+        with its merge in the launch: head dim 256 or 512, 8 query heads per
+        KV head, at most 64 KV heads, a window of at most 1024 positions)
+        rather than an attention launch and a merge launch."""
         eff = min(p.max_seq_len, p.sliding_window) if p.sliding_window else p.max_seq_len
-        return p.head_dim == 256 and p.num_kv_heads <= 64 and eff <= 65536
+        return (p.head_dim in (256, 512) and p.num_q_heads == 8 * p.num_kv_heads and p.num_kv_heads <= 64
+                and eff <= 1024)
 
     @staticmethod
     def qkv_attn_single_launch(p: AttnFusedParams, N: int, nseg: int = 3) -> bool:

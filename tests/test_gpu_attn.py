@@ -192,10 +192,21 @@ FUSED_CASES = [
     (700, 0, 256, 1e6, 1),
     (3000, 0, 256, 1e6, 1),
     (900, 0, 512, 1e6, 1),
+    # head dim 512 (Gemma-4-E2B's global layers): steps of 32 positions, two
+    # per chunk; the first position, step and chunk edges, the benchmark's
+    # context, a window, the merge launch past 16 chunks
+    (0, 0, 512, 1e6, 1),
+    (31, 0, 512, 1e6, 1),
+    (32, 0, 512, 1e6, 1),
+    (64, 0, 512, 1e6, 1),
+    (512, 0, 512, 1e6, 1),
+    (700, 512, 512, 1e4, 0),
+    (1100, 0, 512, 1e6, 1),
     # long contexts: chunk partials merged in groups, then the groups
     (20000, 0, 256, 1e6, 1),
     (32767, 0, 256, 1e6, 1),
     (32767, 512, 256, 1e4, 0),
+    (32767, 0, 512, 1e6, 1),
 ]
 
 
@@ -273,14 +284,14 @@ def test_attn_decode_fused_shared_workspace(ctx):
             assert_close(out.download(np.float32), c["ref"], what=f"shared ws round {rnd} pos={pos} hd={hd}")
 
 
-@pytest.mark.parametrize("pos,window", [(700, 512), (3000, 0), (20, 512)])
-def test_attn_decode_fused_warm_matches(ctx, pos, window):
+@pytest.mark.parametrize("pos,window,hd", [(700, 512, 256), (3000, 0, 256), (20, 512, 256), (900, 0, 512)])
+def test_attn_decode_fused_warm_matches(ctx, pos, window, hd):
     """The launch that also reads the following matvecs' weights into the L2
     caches and takes the RoPE cos/sin from a precomputed table computes
     exactly what the plain one does (output and caches bit for bit); the warm
     regions describe the matvec launches' own tiling, with sizes that are
     not multiples of a tile (a partial last tile reads past no matrix end)."""
-    hd, theta, div = 256, (1e6 if window == 0 else 1e4), int(window == 0)
+    theta, div = (1e6 if window == 0 else 1e4), int(window == 0)
     c = _fused_inputs(pos, window, hd, theta, div)
     p = ctx.attn_fused_params(c["nqh"], c["nkh"], hd, c["cap"], window, 1e-6, theta, div)
     ws = ctx.zeros(ctx.attn_fused_workspace_bytes(p), np.uint8)

@@ -336,8 +336,8 @@ def test_file_model_fused_step_with_token_feedback(ctx, model_path):
     hm = HostModel(d)
     kcs = [L.k_cache.download(np.uint16) for L in d.layers]
     vcs = [L.v_cache.download(np.uint16) for L in d.layers]
-    # 5 per layer, + a merge launch on the two head-dim-512 layers, + the
-    # second q/k/v launch of layer 1 (Q6_K v), + embedding, head, argmax,
+    # 5 per layer (the head-dim-512 layers' attention merges in its launch),
+    # + the second q/k/v launch of layer 1 (Q6_K v), + embedding, head, argmax,
     # + per-layer embeddings: stage 1 (2), 2 per layer, the last tail (1),
     # - one on each layer whose Q4_K q/k/v share the attention's launch
     # (layer 0, the head-dim-256 producer with Q4_K q/k/v)
@@ -346,7 +346,7 @@ def test_file_model_fused_step_with_token_feedback(ctx, model_path):
               if d._qkv_fused(qkv_groups(d.layers[il], [0, 0, 0], [0, 0, 0]))
               and ctx.qkv_attn_single_launch(d.attn_params[il], d.s.hidden, 3 if d.s.is_producer(il) else 1)]
     assert shared == [0]
-    assert d.launches_per_step_fused() == 5 * N_LAYERS + 2 + 1 + 3 + 3 + 2 * N_LAYERS - len(shared)
+    assert d.launches_per_step_fused() == 5 * N_LAYERS + 1 + 3 + 3 + 2 * N_LAYERS - len(shared)
     g = d.capture_fused()
     assert ctx.graph_kernel_nodes(g) == d.launches_per_step_fused()
     try:
@@ -506,10 +506,11 @@ def test_every_format_fused_step(ctx, formats_path):
     vcs = [L.v_cache.download(np.uint16) for L in d.layers]
     # embedding, head (norm, matvec, softcap, two argmax stages); PLE 3 + 2 per layer;
     # layer 0: one f16 q/k/v group (norm + 3 matvecs), attention, o, fused FFN (2);
-    # layer 1: a Q4_K (q, k) and a Q6_K (v) launch, attention + merge, o, unfused FFN
-    # (norm, gate, up, GELU product, down); layer 2: f16 q (norm + matvec), attention,
-    # o, unfused FFN; layer 3: q, attention + merge, o, fused FFN
-    assert d.launches_per_step_fused() == 1 + 5 + (3 + 2 * N_LAYERS) + 8 + 10 + 9 + 6
+    # layer 1: a Q4_K (q, k) and a Q6_K (v) launch, attention (head dim 512, its
+    # merge in the launch), o, unfused FFN (norm, gate, up, GELU product, down);
+    # layer 2: f16 q (norm + matvec), attention, o, unfused FFN; layer 3: q,
+    # attention (head dim 512), o, fused FFN
+    assert d.launches_per_step_fused() == 1 + 5 + (3 + 2 * N_LAYERS) + 8 + 9 + 9 + 5
     g = d.capture_fused()
     assert ctx.graph_kernel_nodes(g) == d.launches_per_step_fused()
     try:

@@ -7,8 +7,8 @@ A six-layer model keeps every case and the oracle quick: layers 0 (local),
 1 (global) and 2 (local) own their caches; 3 and 5 (local) read layer 2's,
 4 (global) reads layer 1's.
 
-* the shared-cache forms of the fused attention (head dim 256: the one-launch
-  plan; 512: launch + merge) and of the paged prologue equal the unfused
+* the shared-cache forms of the fused attention (the one-launch matrix-core
+  plan at head dims 256 and 512) and of the paged prologue equal the unfused
   path on the same inputs and leave the caches untouched;
 * the per-key sequence and the fused step against the oracle's step, the
   fused step's K/V rows only in the producers' caches;
@@ -59,7 +59,7 @@ def _restore(d, snap):
     d.token.upload(snap[3])
 
 
-@pytest.mark.parametrize("layer", [2, 1])  # head dim 256 (one launch), 512 (launch + merge)
+@pytest.mark.parametrize("layer", [2, 1])  # head dim 256, 512
 def test_fused_attention_over_a_producer_cache(ctx, rdec, layer):
     """k_raw = v_raw = k_norm_w = NULL: q_norm + RoPE and attention over the
     cache as it is, equal to fusedPerHeadNormRope + attnDecode over it
