@@ -232,8 +232,13 @@ def gemv_q4k_amortised(ctx, M=262144, N=1536, copies=2, rounds=10):
     ms = time_launches(ctx, one, copies * rounds)
     alg = wb + N * 4 + M * 4
     W.free()
+    # the pure-streaming rate of the same bytes (the probe read of the same
+    # rotation), so that the matvec's rate reads against what a launch of
+    # this size can stream at all
+    fl = stream_floor(ctx, nbytes=wb, copies=copies, rounds=rounds, wg_list=(1024, 2048, 4096))
     return {"shape": [M, N], "us": ms * 1e3, "bytes": alg, "gbps": alg / (ms * 1e-3) / 1e9,
-            "frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, "copies": copies}
+            "frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, "copies": copies,
+            "stream_floor": {k: fl[k] for k in ("launches", "best_us", "best_gbps", "best_frac")}}
 
 
 def stream_floor(ctx, nbytes=5339136, copies=101, rounds=5, wg_list=(256, 648, 1024, 2048)):
