@@ -459,7 +459,9 @@ def batch_census(ctx, bd, reps=10):
     nbytes = {
         "qkv": q4(Q + 2 * KV, H) + act(H) + bd.ks_h * B * (Q + 2 * KV) * 4,
         "attn_global": kv_glob + B * Q * 4 * 2,
-        "attn_window512": kv_loc + B * Q * 4 * 2,
+        # (the one-launch block also reads the q/k/v partials and writes the K/V row)
+        "attn_window512": kv_loc + B * Q * 4 * 2 + (bd.ks_h * B * (Q + 2 * KV) * 4 + B * KV * 4
+                                                    if bd.block_attn else 0),
         "o": q4(H, Q) + act(Q) + bd.ks_q * B * H * 4,
         "gate_up_gelu": 2 * q4(I, H) + act(H) + (sub(I) if handoff else B * I * 4),
         "down": q6(H, I) + (sub(I) if handoff else B * I * 4) + ks_down * B * H * 4,
@@ -470,16 +472,29 @@ def batch_census(ctx, bd, reps=10):
         "qkv": lambda il, L: c.matmulSegmentsBatchPartial("q4k", bd.xn, [L.wq, L.wk, L.wv],
                                                           [bd.q_parts, bd.k_parts, bd.v_parts], [Q, KV, KV], H, B,
                                                           bd.ks_h, ops=bd.xops),
-        "attn_prologue": lambda il, L: c.pagedAttnPrologue(bd.q_parts, bd.k_parts, bd.v_parts, bd.ks_h, L.q_norm,
-                                                           L.k_norm, bd.rope_freqs, bd.q, L.k_cache, L.v_cache,
-                                                           bd.page_table, bd.seq_lens, bd.pro_params[il],
-                                                           bd.rope_cs[bd.s.is_global(il)], bd.rope_rows),
+        # the prologue as a launch of its own: every layer, or (with the
+        # one-launch block) the global layers, whose windows the block's
+        # in-launch merge does not cover
+        "attn_prologue": lambda il, L: (c.pagedAttnPrologue(bd.q_parts, bd.k_parts, bd.v_parts, bd.ks_h, L.q_norm,
+                                                            L.k_norm, bd.rope_freqs, bd.q, L.k_cache, L.v_cache,
+                                                            bd.page_table, bd.seq_lens, bd.pro_params[il],
+                                                            bd.rope_cs[bd.s.is_global(il)], bd.rope_rows)
+                                        if s.is_global(il) or not bd.block_attn else "skip"),
         "attn_global": lambda il, L: (c.pagedAttnDecode(bd.q, L.k_cache, L.v_cache, bd.page_table, bd.seq_lens,
                                                         bd.attn, bd.attn_params[il], bd.attn_ws, ops=bd.aops)
                                       if s.is_global(il) else "skip"),
-        "attn_window512": lambda il, L: (c.pagedAttnDecode(bd.q, L.k_cache, L.v_cache, bd.page_table, bd.seq_lens,
-                                                           bd.attn, bd.attn_params[il], bd.attn_ws, ops=bd.aops)
-                                         if not s.is_global(il) else "skip"),
+        # the window-512 layers: prologue, attention and merge in one launch
+        # (g4_pagedAttnBlock), or the paged decode alone
+        "attn_window512": lambda il, L: (("skip" if s.is_global(il) else
+                                          c.pagedAttnBlock(bd.q_parts, bd.k_parts, bd.v_parts, bd.ks_h, L.q_norm,
+                                                           L.k_norm, bd.rope_freqs, None, L.k_cache, L.v_cache,
+                                                           bd.page_table, bd.seq_lens, bd.attn, bd.pro_params[il],
+                                                           bd.block_ws, ops=bd.aops,
+                                                           rope_cs=bd.rope_cs[False], rope_rows=bd.rope_rows))
+                                         if bd.block_attn else
+                                         (c.pagedAttnDecode(bd.q, L.k_cache, L.v_cache, bd.page_table, bd.seq_lens,
+                                                            bd.attn, bd.attn_params[il], bd.attn_ws, ops=bd.aops)
+                                          if not s.is_global(il) else "skip")),
         "o": lambda il, L: c.matmulSegmentsBatchPartial("q4k", bd.attn, [L.wo], [bd.o_parts], [H], Q, B, bd.ks_q,
                                                         ops=bd.aops),
         "prep_ffn": lambda il, L: c.batchPrep(bd.o_parts, bd.ks_q, L.post_attn_norm, bd.hidden, L.pre_ffn_norm,

@@ -990,6 +990,12 @@ __global__ __launch_bounds__(NT, 2) void mq_attn_kernel(MqArgs a) {
   }
 }
 
+// The paged batch's whole attention block in one launch (g4_pagedAttnBlock):
+// workgroup (chunk, sequence, KV head).
+__global__ __launch_bounds__(NT, 2) void pmqf_kernel(MqfArgs a) {
+  mqf_body<false, false, true, MQ_HD, true>(a, blockIdx.x, blockIdx.z, blockIdx.x, blockIdx.y);
+}
+
 // The fused block as a launch of its own (blockIdx.y = KV head), for head
 // dim 256 (256 threads) or 512 (512 threads).
 template <bool LONG, int HD>
@@ -1420,6 +1426,7 @@ int mqf_prepare(g4_ctx* ctx, const float* q_raw, const float* k_raw, const float
   m.nstage = 0;
   m.spin = ctx->test_spin ? ctx->test_spin : kStageSpin;
   m.status = ctx->status_dev;
+  m.num_seqs = 1;
   L.partials = mp.partials;
   return G4_OK;
 }
@@ -1862,6 +1869,122 @@ int g4_pagedAttnPrologue(g4_ctx* ctx, const float* q_parts, const float* k_parts
   hipLaunchKernelGGL(attn_prologue_kernel, dim3(p.num_q_heads + (kv ? p.num_kv_heads : 0u), p.num_seqs), dim3(NT), 0,
                      ctx->stream, a);
   G4_LAUNCHED(ctx, "attn_prologue");
+  return G4_OK;
+}
+
+// g4_pagedAttnBlock: the one-launch plan (pmqf_kernel) when the window takes
+// at most MQF_FAN chunks of MQ_STEP positions at head dim 256, else
+// g4_pagedAttnPrologue then g4_pagedAttnDecodeOps. Workspace: the arrival
+// counters [num_seqs][nkh][MQF_CNT] (zero between calls), then the chunk
+// partials, or q_out (when the caller gives none) and the decode's
+// workspace.
+namespace {
+size_t block_cnt_bytes(const g4_paged_attn_fused_params& p) {
+  return ((size_t)p.num_seqs * p.num_kv_heads * g4mqf::MQF_CNT * sizeof(uint32_t) + 255) / 256 * 256;
+}
+bool block_one_launch(const g4_paged_attn_fused_params& p, uint32_t nparts) {
+  const uint32_t eff = std::max(eff_len(p.max_seq_len, p.sliding_window), 1u);
+  return p.head_dim == MQ_HD && p.num_q_heads == MQ_G * p.num_kv_heads && p.num_seqs <= 64 &&
+         nparts <= (uint32_t)g4mqf::kMaxParts && ceil_div(eff, MQ_STEP) <= g4mqf::MQF_FAN;
+}
+}  // namespace
+
+int g4_pagedAttnBlock_workspace_size(g4_paged_attn_fused_params p, uint32_t nparts, size_t* bytes) {
+  G4_REQUIRE(bytes, "g4_pagedAttnBlock_workspace_size: null out");
+  size_t dec = 0;
+  int rc = g4_pagedAttnDecode_workspace_size(fused_attn_part(p), &dec);
+  if (rc) return rc;
+  const size_t qo = ((size_t)p.num_seqs * p.num_q_heads * p.head_dim * sizeof(float) + 255) / 256 * 256;
+  size_t body = qo + dec;
+  if (block_one_launch(p, nparts)) {
+    const uint32_t eff = std::max(eff_len(p.max_seq_len, p.sliding_window), 1u);
+    body = std::max(body, ws_bytes(p.num_seqs, p.num_kv_heads, ceil_div(eff, MQ_STEP), MQ_G, MQ_HD));
+  }
+  *bytes = block_cnt_bytes(p) + body;
+  return G4_OK;
+}
+
+int g4_pagedAttnBlock(g4_ctx* ctx, const float* q_parts, const float* k_parts, const float* v_parts, uint32_t nparts,
+                      const uint16_t* q_norm_w, const uint16_t* k_norm_w, const uint16_t* rope_freqs, float* q_out,
+                      uint16_t* k_pool, uint16_t* v_pool, const int32_t* page_table, const uint32_t* seq_lens,
+                      float* output, void* ops, g4_paged_attn_fused_params p, void* workspace,
+                      size_t workspace_bytes, const float* rope_cs, uint32_t rope_rows) {
+  G4_ENTER(ctx);
+  G4_REQUIRE(output && workspace && k_pool && v_pool, "g4_pagedAttnBlock: null buffer");
+  G4_REQUIRE(((uintptr_t)workspace & 15) == 0, "g4_pagedAttnBlock: the workspace must be 16-byte aligned");
+  G4_REQUIRE(!ops || (p.head_dim % 256 == 0 && p.num_seqs <= 64 && ((uintptr_t)ops & 15) == 0),
+             "g4_pagedAttnBlock: operand blocks need head_dim a multiple of 256, <= 64 sequences and a 16-byte "
+             "aligned buffer");
+  size_t need = 0;
+  int rc = g4_pagedAttnBlock_workspace_size(p, nparts, &need);
+  if (rc) return rc;
+  G4_REQUIRE(workspace_bytes >= need, "g4_pagedAttnBlock: workspace %zu bytes < %zu required", workspace_bytes, need);
+  const size_t cb = block_cnt_bytes(p);
+  uint8_t* body = (uint8_t*)workspace + cb;
+  if (!block_one_launch(p, nparts) || ((uintptr_t)q_norm_w & 15) != 0) {
+    float* qo = q_out;
+    size_t used = 0;
+    if (!qo) {
+      qo = (float*)body;
+      used = ((size_t)p.num_seqs * p.num_q_heads * p.head_dim * sizeof(float) + 255) / 256 * 256;
+    }
+    rc = g4_pagedAttnPrologue(ctx, q_parts, k_parts, v_parts, nparts, q_norm_w, k_norm_w, rope_freqs, qo, k_pool,
+                              v_pool, page_table, seq_lens, p, rope_cs, rope_rows);
+    if (rc) return rc;
+    return g4_pagedAttnDecodeOps(ctx, qo, k_pool, v_pool, page_table, seq_lens, output, fused_attn_part(p),
+                                 body + used, workspace_bytes - cb - used, ops);
+  }
+  // the prologue's argument rules, then the one launch
+  G4_REQUIRE(!rope_cs || rope_rows >= p.max_seq_len, "g4_pagedAttnBlock: RoPE table of %u rows < max_seq_len %u",
+             rope_rows, p.max_seq_len);
+  G4_REQUIRE(q_parts && q_norm_w && page_table && seq_lens && nparts >= 1, "g4_pagedAttnBlock: null buffer or no parts");
+  const bool kv = k_parts != nullptr;
+  G4_REQUIRE(kv ? (v_parts && k_norm_w) : !v_parts, "g4_pagedAttnBlock: k_parts, v_parts and k_norm_w go together");
+  G4_REQUIRE(((uintptr_t)rope_cs & 7) == 0, "g4_pagedAttnBlock: rope_cs must be 8-byte aligned");
+  G4_REQUIRE(!p.apply_divisor || rope_freqs, "g4_pagedAttnBlock: apply_divisor needs rope_freqs");
+  G4_REQUIRE(p.num_seqs > 0 && p.page_size > 0 && p.max_pages > 0 && p.num_pages > 0 && p.max_seq_len > 0 &&
+                 (uint64_t)p.max_seq_len <= (uint64_t)p.page_size * p.max_pages,
+             "g4_pagedAttnBlock: max_seq_len %u exceeds the page table (%u x %u)", p.max_seq_len, p.max_pages,
+             p.page_size);
+  G4_REQUIRE(((uintptr_t)q_parts & 15) == 0 && ((uintptr_t)k_pool & 15) == 0 && ((uintptr_t)v_pool & 15) == 0,
+             "g4_pagedAttnBlock: q partials and pools must be 16-byte aligned");
+  const uint32_t eff = std::max(eff_len(p.max_seq_len, p.sliding_window), 1u);
+  MqfArgs m{};
+  m.q_raw = q_parts;
+  m.k_raw = k_parts;
+  m.v_raw = v_parts;
+  m.q_w = q_norm_w;
+  m.k_w = k_norm_w;
+  m.rope_freqs = rope_freqs ? rope_freqs : q_norm_w;  // read unconditionally, used only with the divisor
+  m.theta = p.theta;
+  m.apply_divisor = p.apply_divisor;
+  m.eps = p.eps;
+  m.kc = k_pool;
+  m.vc = v_pool;
+  m.cap = p.max_seq_len;
+  m.nqh = p.num_q_heads;
+  m.nkh = p.num_kv_heads;
+  m.scale = p.scale;
+  m.window = p.sliding_window;
+  m.nstep = 1;
+  m.max_chunks = ceil_div(eff, MQ_STEP);
+  m.ws = (float*)body;
+  m.cnt = (uint32_t*)workspace;
+  m.out = output;
+  m.rope_cs = (const float2*)rope_cs;
+  m.status = ctx->status_dev;
+  m.page_table = page_table;
+  m.seq_lens = seq_lens;
+  m.page_size = p.page_size;
+  m.max_pages = p.max_pages;
+  m.num_pages = p.num_pages;
+  m.num_seqs = p.num_seqs;
+  m.nparts = nparts;
+  m.q_out = q_out;
+  m.ops = (uint8_t*)ops;
+  m.ntv = (int)(g4d::pad_batch(p.num_seqs) / 16);
+  hipLaunchKernelGGL(pmqf_kernel, dim3(m.max_chunks, p.num_seqs, p.num_kv_heads), dim3(NT), 0, ctx->stream, m);
+  G4_LAUNCHED(ctx, "paged_attn_block");
   return G4_OK;
 }
 

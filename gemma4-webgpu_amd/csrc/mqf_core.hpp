@@ -113,9 +113,23 @@ struct MqfArgs {
   uint32_t nstage;
   uint32_t spin;       // polls before the wait for the staged values gives up
   uint32_t* status;    // the context's kernel status word (pinned host memory)
+  // the paged batch (mqf_body<..., PAGED>, sequence `seq`): q_raw / k_raw /
+  // v_raw are the q/k/v projections' nparts split-K partial sums
+  // ([nparts][num_seqs][heads * 256], added in chunk order), the K/V rows
+  // live in pages of the pools, the lengths (already advanced) in seq_lens;
+  // out is [num_seqs][nqh][256]; q_out (or null) receives q after q_norm +
+  // RoPE, ops (or null) the output as the o projection's operand blocks
+  const int32_t* page_table;
+  const uint32_t* seq_lens;
+  uint32_t page_size, max_pages, num_pages;
+  uint32_t num_seqs, nparts;  // (num_seqs 1 for the dense forms)
+  float* q_out;
+  uint8_t* ops;
+  int ntv;
 };
 
 constexpr int MQF_QS = 264;  // LDS stride of a q column (halves)
+constexpr int kMaxParts = 8;  // split-K partials the paged block adds (the hidden width's super-blocks)
 
 // Device-scope (agent) loads and stores through a buffer resource: written
 // through / read past the XCD-local L2, so they are coherent across XCDs
@@ -295,6 +309,59 @@ __device__ __forceinline__ void mqf_warm(const MqfArgs& a, uint32_t p, uint32_t 
   asm volatile("" ::"v"(acc));
 }
 
+// The paged merger's output as the o projection's matrix-core operand
+// blocks (the layout g4d::Ops and merge_ops write: per super-block of K and
+// tile of 16 vectors, the f16 hi / lo of y * 2^k with k from the largest
+// |y| of the super-block, the 3-part f16 sums of each 32-value sub-block
+// times 2^-6, and 2^-k). Thread (head th, dims td.. and 128 + td..) holds
+// ov[0] and ov[1] of head hq = 8 kvh + th; head dim 256, so one head is one
+// super-block.
+__device__ __forceinline__ void mqf_write_ops(uint8_t* ops, int ntv, uint32_t seq, uint32_t hq, int td,
+                                              const float4& y0, const float4& y1) {
+  float am = fmaxf(fmaxf(fmaxf(fabsf(y0.x), fabsf(y0.y)), fmaxf(fabsf(y0.z), fabsf(y0.w))),
+                   fmaxf(fmaxf(fabsf(y1.x), fabsf(y1.y)), fmaxf(fabsf(y1.z), fabsf(y1.w))));
+  am = g4d::max16(am);
+  am = g4d::xmax16(am);  // the head's 32 threads
+  int ex = 0;
+  (void)frexpf(am, &ex);
+  const int k = am > 0.f ? min(max(14 - ex, -120), 120) : 0;
+  const float sc = ldexpf(1.0f, k);
+  const uint32_t t = seq >> 4, c = seq & 15u;
+  uint8_t* base = ops + (size_t)hq * g4d::Ops::bytes(ntv);
+  const float ys[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+  float part[2] = {0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t e = (uint32_t)((i < 4 ? 0 : 128) + td + (i & 3));
+    const float xs = ys[i] * sc;
+    const _Float16 hi = (_Float16)xs, lo = (_Float16)(xs - (float)hi);
+    const uint32_t sb = e >> 5, p = e & 31u, q = p >> 3, j = p & 7u;
+    uint8_t* mp = base + t * g4d::Ops::MAIN_T + sb * 2048 + (c + 16u * q) * 16 + j * 2;
+    *(_Float16*)mp = hi;
+    *(_Float16*)(mp + 1024) = lo;
+    part[i >> 2] += xs;
+  }
+  // a sub-block's 32 values are 8 consecutive threads' 4 (per half)
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float sum = g4d::sum8(part[h]) * 0.015625f;  // * 2^-6
+    const uint32_t sb = (uint32_t)(h * 4) + ((uint32_t)td >> 5);
+    if ((td & 31) == 0) {
+      const _Float16 p0 = (_Float16)sum;
+      const float r1 = sum - (float)p0;
+      const _Float16 p1 = (_Float16)r1;
+      const _Float16 p2 = (_Float16)(r1 - (float)p1);
+      _Float16* sp =
+          (_Float16*)(base + g4d::Ops::sums_off(ntv) + t * 1024 + (c + 16u * (sb >> 1)) * 16 + (sb & 1) * 8);
+      sp[0] = p0;
+      sp[1] = p1;
+      sp[2] = p2;
+      sp[3] = (_Float16)0.f;
+    }
+  }
+  if (td == 0) *(float*)(base + g4d::Ops::scale_off(ntv) + t * 64 + c * 4) = ldexpf(1.0f, -k);
+}
+
 // LONG (windows past MQF_FAN chunks): K/V rows are loaded non-temporally
 // (read once, measured faster at 32K positions) and the workgroups end after
 // storing their partials, which the merge launch that follows combines.
@@ -302,11 +369,15 @@ __device__ __forceinline__ void mqf_warm(const MqfArgs& a, uint32_t p, uint32_t 
 // workgroups end after storing their partials; the o projection's launch
 // merges them per head (attn_heads_kernel) and clears the staged q/k/v.
 // HD: the head dim (MqShape: HD threads); the matvec hand-off is built for 256.
-template <bool LONG, bool FUSED, bool MERGE = !LONG, int HD = MQ_HD>
-__device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t kvh, uint32_t lin) {
+// PAGED: sequence `seq` of a paged batch (the MqfArgs fields above), its
+// q/k/v from split-K partial sums, merged in the launch.
+template <bool LONG, bool FUSED, bool MERGE = !LONG, int HD = MQ_HD, bool PAGED = false>
+__device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t kvh, uint32_t lin,
+                                         uint32_t seq = 0) {
   static_assert(!(LONG && FUSED), "the fused matvec form merges in the launch or in the o projection");
   static_assert(!(LONG && MERGE), "the long form merges in a launch of its own");
   static_assert(!FUSED || HD == MQ_HD, "the q/k/v hand-off is built for head dim 256");
+  static_assert(!PAGED || (HD == MQ_HD && MERGE && !FUSED && !LONG), "the paged block: head dim 256, merged");
   using Sh = MqShape<HD>;
   constexpr int NT = Sh::NT, NW = Sh::NW, RS = Sh::RS, QS = Sh::QS, TPH = Sh::TPH;
   constexpr int PR = HD / 8;  // 16-byte pieces of a K/V row
@@ -334,8 +405,8 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   const int rt = w & 3, dh = w >> 2;  // this wave's row tile and 256-dim half
   const uint32_t chunk = bx;
   const uint32_t CH = MQ_STEP * a.nstep;
-  const uint32_t L = min(*a.pos_dev + 1, a.cap);
-  const uint32_t pos = L - 1;  // the position being decoded
+  const uint32_t L = PAGED ? min(a.seq_lens[seq], a.cap) : min(*a.pos_dev + 1, a.cap);
+  const uint32_t pos = L - 1;  // the position being decoded (PAGED: L == 0 has no chunk)
   const uint32_t wstart = (a.window != 0 && L > a.window) ? L - a.window : 0;
   const uint32_t n = L - wstart;
   const uint32_t nch = (n + CH - 1) / CH;
@@ -349,6 +420,15 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   const bool owner = cend == n && own_row;
   // thread -> (head, 4 dims of each RoPE half) for q, the partial and the merge
   const int th = tid / TPH, td = 4 * (tid % TPH);
+  // the cache row of position p (PAGED: its page, clamped to the pool)
+  auto crow = [&](uint32_t p) -> size_t {
+    if constexpr (PAGED) {
+      int32_t pg = a.page_table[(size_t)seq * a.max_pages + p / a.page_size];
+      pg = pg < 0 ? 0 : (pg >= (int32_t)a.num_pages ? (int32_t)a.num_pages - 1 : pg);
+      return (size_t)pg * a.page_size + p % a.page_size;
+    }
+    return p;
+  };
 
   // a step's K rows, then its V rows: piece pc = tid + NT (i % 8) is row
   // pc / PR, 16 bytes at column 8 (pc % PR)
@@ -360,7 +440,7 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
       const uint32_t r = pc / PR, col = (pc % PR) * 8;
       const uint32_t p = min(wstart + c0 + st * MQ_STEP + r, last);
       const uint16_t* base = i < 8 ? a.kc : a.vc;
-      const mu4* src = (const mu4*)(base + ((size_t)p * a.nkh + kvh) * HD + col);
+      const mu4* src = (const mu4*)(base + (crow(p) * a.nkh + kvh) * HD + col);
       pf[i] = LONG ? __builtin_nontemporal_load(src) : *src;
     }
   };
@@ -391,13 +471,50 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   float4 q0, q1;
   float kx, vx;
   bool stalled = false;  // (uniform) FUSED: the wait for q/k/v expired
-  if constexpr (!FUSED) {
+  if constexpr (PAGED) {  // the split-K partial sums, added in chunk order
+    // (up to kMaxParts partials; every load is issued before the first add)
+    const size_t qs_stride = (size_t)a.num_seqs * a.nqh * HD;
+    const float* qg = a.q_raw + (size_t)seq * a.nqh * HD + qoff;
+    float4 u[kMaxParts], v[kMaxParts];
+#pragma unroll
+    for (int k = 0; k < kMaxParts; ++k) {
+      const size_t o = (size_t)min((uint32_t)k, a.nparts - 1) * qs_stride;
+      u[k] = *(const float4*)(qg + o);
+      v[k] = *(const float4*)(qg + o + HD / 2);
+    }
+    q0 = make_float4(0.f, 0.f, 0.f, 0.f);
+    q1 = q0;
+#pragma unroll
+    for (int k = 0; k < kMaxParts; ++k)
+      if ((uint32_t)k < a.nparts) {
+        q0.x += u[k].x; q0.y += u[k].y; q0.z += u[k].z; q0.w += u[k].w;
+        q1.x += v[k].x; q1.y += v[k].y; q1.z += v[k].z; q1.w += v[k].w;
+      }
+  } else if constexpr (!FUSED) {
     const float* qg = a.q_raw + qoff;
     q0 = *(const float4*)qg;
     q1 = *(const float4*)(qg + HD / 2);
   }
   const uint2 w0 = *(const uint2*)(a.q_w + td), w1 = *(const uint2*)(a.q_w + HD / 2 + td);
-  if constexpr (!FUSED) {
+  if constexpr (PAGED) {
+    const size_t kv_stride = (size_t)a.num_seqs * a.nkh * HD;
+    const size_t ko = ((size_t)seq * a.nkh + kvh) * HD + tid;
+    float ku[kMaxParts], vu[kMaxParts];
+#pragma unroll
+    for (int k = 0; k < kMaxParts; ++k) {
+      const size_t o = (size_t)min((uint32_t)k, a.nparts - 1) * kv_stride + ko;
+      ku[k] = own_row ? a.k_raw[o] : 0.f;
+      vu[k] = own_row ? a.v_raw[o] : 0.f;
+    }
+    kx = 0.f;
+    vx = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxParts; ++k)
+      if ((uint32_t)k < a.nparts) {
+        kx += ku[k];
+        vx += vu[k];
+      }
+  } else if constexpr (!FUSED) {
     kx = own_row ? a.k_raw[(size_t)kvh * HD + tid] : 0.f;
     vx = own_row ? a.v_raw[(size_t)kvh * HD + tid] : 0.f;
   }
@@ -451,6 +568,13 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
       l0[e] = (_Float16)(r0 - (float)h0[e]);
       h1[e] = (_Float16)r1;
       l1[e] = (_Float16)(r1 - (float)h1[e]);
+      if constexpr (PAGED) {  // the roped q, as g4_pagedAttnPrologue writes it (chunk 0's copy)
+        if (a.q_out && chunk == 0) {
+          float* qo = a.q_out + ((size_t)seq * a.nqh + kvh * MQ_G + th) * HD + td + e;
+          qo[0] = r0;
+          qo[HD / 2] = r1;
+        }
+      }
     }
     *(mh4*)(qs + th * QS + td) = h0;
     *(mh4*)(qs + (th + 8) * QS + td) = l0;
@@ -467,8 +591,15 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   store_step();
   __syncthreads();
   if (owner) {
-    a.kc[((size_t)pos * a.nkh + kvh) * HD + tid] = cur_s[tid];
-    a.vc[((size_t)pos * a.nkh + kvh) * HD + tid] = cur_s[HD + tid];
+    bool store = true;
+    if constexpr (PAGED) {  // as the prologue: only into a page of the pool
+      const int32_t pg = a.page_table[(size_t)seq * a.max_pages + pos / a.page_size];
+      store = pg >= 0 && pg < (int32_t)a.num_pages;
+    }
+    if (store) {
+      a.kc[(crow(pos) * a.nkh + kvh) * HD + tid] = cur_s[tid];
+      a.vc[(crow(pos) * a.nkh + kvh) * HD + tid] = cur_s[HD + tid];
+    }
     if (nst == 1) patch(0);
   }
   mh8 qb[8];
@@ -570,10 +701,11 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
     ml_s[NW * MQ_G + w * MQ_G + c] = l_run;
   }
   __syncthreads();
-  const size_t nparts = (size_t)a.nkh * a.max_chunks * MQ_G;
+  const size_t nparts = (size_t)a.num_seqs * a.nkh * a.max_chunks * MQ_G;
   // chunk partials: m [nparts], l [nparts], o [nparts][HD] (f32)
   const __amdgpu_buffer_rsrc_t r0 = dev_rsrc(a.ws, (uint32_t)(nparts * (HD + 2) * sizeof(float)));
-  const size_t part0 = ((size_t)kvh * a.max_chunks + chunk) * MQ_G;
+  const size_t skh = (size_t)seq * a.nkh + kvh;  // (sequence, KV head)
+  const size_t part0 = (skh * a.max_chunks + chunk) * MQ_G;
   if (tid < MQ_G) {  // thread h: the head's weight per row tile and the chunk's (m, l)
     float m4[4], M = -INFINITY;
 #pragma unroll
@@ -657,22 +789,26 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   };
   auto write_out = [&](float Ls, const float4& o0, const float4& o1) {
     const float li = Ls > 0.f ? 1.0f / Ls : 0.f;
-    float* dst = a.out + ((size_t)kvh * MQ_G + th) * HD + td;
-    *(float4*)dst = make_float4(o0.x * li, o0.y * li, o0.z * li, o0.w * li);
-    *(float4*)(dst + HD / 2) = make_float4(o1.x * li, o1.y * li, o1.z * li, o1.w * li);
+    float* dst = a.out + (skh * MQ_G + th) * HD + td;
+    const float4 y0 = make_float4(o0.x * li, o0.y * li, o0.z * li, o0.w * li);
+    const float4 y1 = make_float4(o1.x * li, o1.y * li, o1.z * li, o1.w * li);
+    *(float4*)dst = y0;
+    *(float4*)(dst + HD / 2) = y1;
+    if constexpr (PAGED)
+      if (a.ops) mqf_write_ops(a.ops, a.ntv, seq, (uint32_t)(kvh * MQ_G + th), td, y0, y1);
   };
-  uint32_t* cnt = a.cnt + (size_t)kvh * MQF_CNT;
+  uint32_t* cnt = a.cnt + skh * MQF_CNT;
   const uint32_t ng = (nch + MQF_FAN - 1) / MQF_FAN, g = chunk / MQF_FAN;
   if (!arrive(cnt + g, min(MQF_FAN, nch - g * MQF_FAN))) return;
   float M, Ls;
   float4 o0, o1;
-  merge(r0, nparts, ((size_t)kvh * a.max_chunks + g * MQF_FAN) * MQ_G, min(MQF_FAN, nch - g * MQF_FAN), M, Ls, o0,
-        o1);
+  merge(r0, nparts, (skh * a.max_chunks + g * MQF_FAN) * MQ_G, min(MQF_FAN, nch - g * MQF_FAN), M, Ls, o0, o1);
   if (ng == 1) {
     if constexpr (FUSED) mqf_clear_stage(a, tid);
     write_out(Ls, o0, o1);
     return;
   }
+  if constexpr (PAGED) return;  // (the host keeps the paged block to one merge level)
   const size_t nparts1 = (size_t)a.nkh * MQF_FAN * MQ_G;
   const __amdgpu_buffer_rsrc_t r1 = dev_rsrc(a.ws1, (uint32_t)(nparts1 * (HD + 2) * sizeof(float)));
   {

@@ -219,6 +219,9 @@ SIGNATURES = {
     "g4_matmulSubBatchPartial": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, ctypes.POINTER(_U32)]),
     "g4_pagedAttnPrologue": (_I, [_P, _P, _P, _P, _U32, _P, _P, _P, _P, _P, _P, _P, _P, PagedAttnFusedParams,
                                   _P, _U32]),
+    "g4_pagedAttnBlock_workspace_size": (_I, [PagedAttnFusedParams, _U32, ctypes.POINTER(_SZ)]),
+    "g4_pagedAttnBlock": (_I, [_P, _P, _P, _P, _U32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, PagedAttnFusedParams,
+                               _P, _SZ, _P, _U32]),
     "g4_normAddGateUpGeluBatch": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, MatmulParams, _F, _U32]),
     "g4_normAddMatmulSegmentsBatch": (_I, [_P, _I, _P, _P, _P, _P, _P, ctypes.POINTER(_P),
                                            ctypes.POINTER(_P), ctypes.POINTER(_U32), _I, _U32, _F, _F, _U32]),

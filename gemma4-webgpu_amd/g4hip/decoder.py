@@ -917,7 +917,14 @@ class BatchDecoder(_SyntheticModel):
             self.attn_params.append(ctx.paged_params(
                 B, s.n_q_heads, s.n_kv_heads, s.hd(il), page_size, self.max_pages, self.max_seq, self.num_pages,
                 1.0, window))
+        # the attention block of each layer in one launch (g4_pagedAttnBlock),
+        # except where the rows share pages (prefill), whose prologue must
+        # append every row before the attention reads any
+        # (its own workspace: its arrival counters stay zero between calls)
+        self.block_attn = not shared_pages
         self.attn_ws = ctx.zeros(max(ctx.paged_workspace_bytes(p) for p in self.attn_params), np.uint8)
+        self.block_ws = ctx.zeros(max(ctx.paged_block_workspace_bytes(p, self.ks_h) for p in self.pro_params),
+                                  np.uint8)
         self.rope_cs = self._rope_tables(self.max_seq)
         ctx.fill_normal_f32(self.hidden, B * s.hidden, self._seed(), 0.0, 1.0)
         ctx.sync()
@@ -1021,13 +1028,19 @@ class BatchDecoder(_SyntheticModel):
                 if nq and k != nq:
                     raise RuntimeError(f"layer {il}: q/k/v launches split K {nq} and {k} ways")
                 nq = k
-            c.pagedAttnPrologue(self.q_parts, self.k_parts if prod else None, self.v_parts if prod else None, nq,
-                                L.q_norm, L.k_norm, self.rope_freqs, self.q, L.k_cache if prod else None,
-                                L.v_cache if prod else None, self.page_table, self.seq_lens, self.pro_params[il],
-                                self.rope_cs[s.is_global(il)], self.rope_rows)
             ops = self.aops if s.hd(il) % 256 == 0 else None
-            c.pagedAttnDecode(self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.attn,
-                              self.attn_params[il], self.attn_ws, ops=ops)
+            if self.block_attn:  # prologue and attention in one launch where the window allows
+                c.pagedAttnBlock(self.q_parts, self.k_parts if prod else None, self.v_parts if prod else None, nq,
+                                 L.q_norm, L.k_norm, self.rope_freqs, self.q, L.k_cache, L.v_cache, self.page_table,
+                                 self.seq_lens, self.attn, self.pro_params[il], self.block_ws, ops=ops,
+                                 rope_cs=self.rope_cs[s.is_global(il)], rope_rows=self.rope_rows)
+            else:
+                c.pagedAttnPrologue(self.q_parts, self.k_parts if prod else None, self.v_parts if prod else None, nq,
+                                    L.q_norm, L.k_norm, self.rope_freqs, self.q, L.k_cache if prod else None,
+                                    L.v_cache if prod else None, self.page_table, self.seq_lens, self.pro_params[il],
+                                    self.rope_cs[s.is_global(il)], self.rope_rows)
+                c.pagedAttnDecode(self.q, L.k_cache, L.v_cache, self.page_table, self.seq_lens, self.attn,
+                                  self.attn_params[il], self.attn_ws, ops=ops)
             if probe:
                 probe("attn", il, 0)
             no = self._mm_batch(L.qt["wo"], self.attn, L.wo, self.o_parts, H, Q, self.ks_q, ops)

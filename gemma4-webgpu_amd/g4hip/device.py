@@ -599,6 +599,23 @@ class Context:
                                          _p(k_norm_w), _p(rope_freqs), _p(q_out), _p(k_pool), _p(v_pool),
                                          _p(page_table), _p(seq_lens), p, _p(rope_cs), rope_rows))
 
+    @staticmethod
+    def paged_block_workspace_bytes(p: PagedAttnFusedParams, nparts: int) -> int:
+        n = ctypes.c_size_t()
+        check(lib().g4_pagedAttnBlock_workspace_size(p, nparts, ctypes.byref(n)))
+        return int(n.value)
+
+    def pagedAttnBlock(self, q_parts: Ptr, k_parts: Ptr, v_parts: Ptr, nparts: int, q_norm_w: Ptr, k_norm_w: Ptr,
+                       rope_freqs: Ptr, q_out: Ptr, k_pool: Ptr, v_pool: Ptr, page_table: Ptr, seq_lens: Ptr,
+                       out: Ptr, p: PagedAttnFusedParams, workspace: Buffer, ops: Ptr = None, rope_cs: Ptr = None,
+                       rope_rows: int = 0) -> None:
+        """pagedAttnPrologue + pagedAttnDecode(Ops) in one launch where the window allows
+        (g4_pagedAttnBlock); workspace: paged_block_workspace_bytes, zeroed once."""
+        check(lib().g4_pagedAttnBlock(self.h, _p(q_parts), _p(k_parts), _p(v_parts), nparts, _p(q_norm_w),
+                                      _p(k_norm_w), _p(rope_freqs), _p(q_out), _p(k_pool), _p(v_pool),
+                                      _p(page_table), _p(seq_lens), _p(out), _p(ops), p, _p(workspace),
+                                      workspace.nbytes, _p(rope_cs), rope_rows))
+
     def advanceSeqLens(self, seq_lens: Ptr, num_seqs: int, delta: int = 1) -> None:
         check(lib().g4_advanceSeqLens(self.h, _p(seq_lens), num_seqs, delta))
 

@@ -418,6 +418,30 @@ int g4_pagedAttnPrologue(g4_ctx* ctx, const float* q_parts, const float* k_parts
                          uint16_t* k_pool, uint16_t* v_pool, const int32_t* page_table,
                          const uint32_t* seq_lens, g4_paged_attn_fused_params p,
                          const float* rope_cs, uint32_t rope_rows);
+/* g4_pagedAttnPrologue followed by g4_pagedAttnDecodeOps (the per-layer
+ * attention block of a multi-sequence step, src/engine.ts:1556-1584 per
+ * sequence) in one launch where the window takes at most 16 chunks of 64
+ * positions (sliding windows up to 1024, or a cache of at most 1024
+ * positions), head_dim 256, 8 query heads per KV head, <= 64 sequences and
+ * nparts <= 8: every workgroup sums its sequence's q (and k/v) partials,
+ * forms q_norm + RoPE, the chunk that ends at the sequence's position forms
+ * and appends its K/V row, each chunk attends, and the last chunk of each
+ * sequence to arrive merges them and writes the output (and, with ops, the
+ * o projection's operand blocks). Other shapes make the two calls. q_out
+ * (or NULL) receives q after q_norm + RoPE as the prologue writes it. The
+ * row a sequence appends is read by that sequence only in this launch: a
+ * batch whose rows share pages (the rows of one prompt, a batched prefill)
+ * takes the two calls, whose first appends every row before the second
+ * reads any. workspace: g4_pagedAttnBlock_workspace_size bytes, 16-byte
+ * aligned, zero before the first call (calls leave its arrival counters
+ * zero; calls sharing it must not overlap). An MI355X launch fusion with
+ * no counterpart in the reference. */
+int g4_pagedAttnBlock_workspace_size(g4_paged_attn_fused_params p, uint32_t nparts, size_t* bytes);
+int g4_pagedAttnBlock(g4_ctx* ctx, const float* q_parts, const float* k_parts, const float* v_parts, uint32_t nparts,
+                      const uint16_t* q_norm_w, const uint16_t* k_norm_w, const uint16_t* rope_freqs, float* q_out,
+                      uint16_t* k_pool, uint16_t* v_pool, const int32_t* page_table, const uint32_t* seq_lens,
+                      float* output, void* ops, g4_paged_attn_fused_params p, void* workspace,
+                      size_t workspace_bytes, const float* rope_cs, uint32_t rope_rows);
 /* seq_lens[s] += delta for s < num_seqs, on the stream (the device-side
  * length counters a captured multi-sequence step replays with). */
 int g4_advanceSeqLens(g4_ctx* ctx, uint32_t* seq_lens, uint32_t num_seqs, uint32_t delta);

@@ -187,6 +187,92 @@ def test_prologue_then_paged_decode_matches_fused_and_oracle(ctx, bdec):
     d.set_lengths(np.array(LENS, np.uint32))
 
 
+def _ops_values(ops, B, nblk):
+    """The activations an operand-block buffer encodes: (hi + lo) * 2^-k per
+    super-block and vector, [nblk][B][256]."""
+    ntv = 2 if B > 16 else 1
+    blk = ntv * (8 * 2 * 1024 + 1024 + 64)
+    main, sums = ntv * 8 * 2 * 1024, ntv * 1024
+    g = ops.reshape(-1, blk)[:nblk]
+    # main planes [t][s][hi/lo][q][lane 16 B = c + 16 q]: element 32 s + 8 q + j of vector 16 t + c
+    m = g[:, :main].reshape(nblk, ntv, 8, 2, 4, 16, 8, 2).view(np.float16)[..., 0].astype(np.float64)
+    sc = g[:, main + sums:].reshape(nblk, ntv, 16, 4).view(np.float32)[..., 0].astype(np.float64)
+    vals = (m[:, :, :, 0] + m[:, :, :, 1])  # [blk][t][s][q][c][j]
+    vals = vals.transpose(0, 1, 4, 2, 3, 5).reshape(nblk, ntv * 16, 256) * sc.reshape(nblk, ntv * 16, 1)
+    return vals[:, :B]
+
+
+def test_paged_block_matches_two_launches(ctx, bdec):
+    """g4_pagedAttnBlock (the prologue over split-K partials, the K/V append,
+    the attention and its merge in one launch) against the prologue and
+    the paged decode it replaces: the same attention output and roped q
+    (within the f32 rounding of the norms' sums, 1e-5), the same appended
+    rows to one f16 ulp, operand blocks that encode its own output, the o
+    projection from them; a second call on the same workspace (whose
+    arrival counters each call leaves zero) repeats the first bit for bit.
+    The local layer (window 512, 8 chunks) and the global one (1004
+    positions, 16 chunks) both take the one launch here."""
+    d, s, B = bdec, bdec.s, bdec.B
+    kv = s.kv_dim
+    rng = np.random.default_rng(41)
+    Q = rng.normal(0, 2, (B, s.q_dim)).astype(np.float32)
+    K = rng.normal(0, 2, (B, kv)).astype(np.float32)
+    V = rng.normal(0, 2, (B, kv)).astype(np.float32)
+    parts = [ctx.from_numpy(np.concatenate([0.25 * A, 0.75 * A])) for A in (Q, K, V)]
+    nblk = s.q_dim // 256
+    for il, L in enumerate(d.layers):
+        assert ctx.paged_block_workspace_bytes(d.pro_params[il], 2) <= d.block_ws.nbytes
+        k0, v0 = L.k_cache.download(np.uint16), L.v_cache.download(np.uint16)
+        d.set_lengths(np.array(LENS, np.uint32) + 1)
+        ctx.pagedAttnPrologue(parts[0], parts[1], parts[2], 2, L.q_norm, L.k_norm, d.rope_freqs, d.q, L.k_cache,
+                              L.v_cache, d.page_table, d.seq_lens, d.pro_params[il])
+        ctx.pagedAttnDecode(d.q, L.k_cache, L.v_cache, d.page_table, d.seq_lens, d.attn, d.attn_params[il],
+                            d.attn_ws, ops=d.aops)
+        A0, Q0 = d.attn.download(np.float32).reshape(B, -1), d.q.download(np.float32).reshape(B, -1)
+        kp0, vp0 = L.k_cache.download(np.uint16).reshape(-1, kv), L.v_cache.download(np.uint16).reshape(-1, kv)
+        runs = []
+        for rep in range(2):
+            L.k_cache.upload(k0)
+            L.v_cache.upload(v0)
+            d.attn.upload(np.zeros(B * s.q_dim, np.float32))
+            d.q.upload(np.zeros(B * s.q_dim, np.float32))
+            ctx.pagedAttnBlock(parts[0], parts[1], parts[2], 2, L.q_norm, L.k_norm, d.rope_freqs, d.q, L.k_cache,
+                               L.v_cache, d.page_table, d.seq_lens, d.attn, d.pro_params[il], d.block_ws,
+                               ops=d.aops)
+            ctx.sync()
+            runs.append((d.attn.download(np.float32), d.q.download(np.float32), L.k_cache.download(np.uint16),
+                         L.v_cache.download(np.uint16), d.aops.download(np.uint8)))
+        for a, b in zip(*runs):
+            assert bits_equal(a, b), f"layer {il}: the second call differs"
+        A1, Q1 = runs[0][0].reshape(B, -1), runs[0][1].reshape(B, -1)
+        kp1, vp1 = runs[0][2].reshape(-1, kv), runs[0][3].reshape(-1, kv)
+        for b, pos in enumerate(LENS):
+            assert_close(A1[b], A0[b], rel=1e-5, cos=0.9999999, what=f"block vs two launches layer {il} seq {b}")
+            assert_close(Q1[b], Q0[b], rel=1e-5, cos=0.9999999, what=f"roped q layer {il} seq {b}")
+            r = d.pool_row(b, pos)
+            for got, want in ((kp1[r], kp0[r]), (vp1[r], vp0[r])):
+                g16, w16 = got.view(np.float16).astype(np.float32), want.view(np.float16).astype(np.float32)
+                assert np.all(np.abs(g16 - w16) <= 2.0 ** -10 * np.maximum(np.abs(w16), 2.0 ** -14)), (il, b)
+        # every other row of the pools is untouched
+        rows = {d.pool_row(b, pos) for b, pos in enumerate(LENS)}
+        other = np.array([i not in rows for i in range(kp0.shape[0])])
+        assert np.array_equal(kp1[other], k0.reshape(-1, kv)[other]) and np.array_equal(vp1[other],
+                                                                                         v0.reshape(-1, kv)[other])
+        # the operand blocks encode the block's own output
+        enc = _ops_values(runs[0][4], B, nblk)
+        for b in range(B):
+            assert_close(enc[:, b].reshape(-1), A1[b], rel=1e-6, cos=0.99999999, what=f"operand blocks seq {b}")
+        a_ = ctx.empty(d.ks_q * B * s.hidden, np.float32)
+        na = ctx.matmulSegmentsBatchPartial("q4k", d.attn, [L.wo], [a_], [s.hidden], s.q_dim, B, d.ks_q, ops=d.aops)
+        OP = a_.download(np.float32)[:na * B * s.hidden].reshape(na, B, -1).sum(0)
+        wo = L.wo.download(np.uint8)
+        for b in range(B):
+            assert_close(OP[b], O.matmul(A1[b], wo, s.hidden, s.q_dim, "q4k"), what=f"o from the block's blocks {b}")
+        L.k_cache.upload(k0)
+        L.v_cache.upload(v0)
+    d.set_lengths(np.array(LENS, np.uint32))
+
+
 def test_batch_step_stages_match_oracle_edge_lengths(ctx, bdec):
     _stages_vs_oracle(ctx, bdec, LENS)
 
