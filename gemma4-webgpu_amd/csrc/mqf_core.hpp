@@ -331,15 +331,22 @@ __device__ __forceinline__ void mqf_write_ops(uint8_t* ops, int ntv, uint32_t se
   const float ys[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
   float part[2] = {0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t e = (uint32_t)((i < 4 ? 0 : 128) + td + (i & 3));
-    const float xs = ys[i] * sc;
-    const _Float16 hi = (_Float16)xs, lo = (_Float16)(xs - (float)hi);
+  for (int h = 0; h < 2; ++h) {
+    // dims e .. e + 3 (e a multiple of 4): four consecutive f16 of one lane's
+    // 16 bytes, one 8-byte store for the hi plane and one for the lo
+    const uint32_t e = (uint32_t)(h * 128 + td);
     const uint32_t sb = e >> 5, p = e & 31u, q = p >> 3, j = p & 7u;
+    mh4 hi, lo;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float xs = ys[4 * h + i] * sc;
+      hi[i] = (_Float16)xs;
+      lo[i] = (_Float16)(xs - (float)hi[i]);
+      part[h] += xs;
+    }
     uint8_t* mp = base + t * g4d::Ops::MAIN_T + sb * 2048 + (c + 16u * q) * 16 + j * 2;
-    *(_Float16*)mp = hi;
-    *(_Float16*)(mp + 1024) = lo;
-    part[i >> 2] += xs;
+    *(mh4*)mp = hi;
+    *(mh4*)(mp + 1024) = lo;
   }
   // a sub-block's 32 values are 8 consecutive threads' 4 (per half)
 #pragma unroll
