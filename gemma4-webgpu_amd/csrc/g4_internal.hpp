@@ -146,10 +146,18 @@ __device__ __forceinline__ float as_f32(float v) {
 }
 
 // tanh-GELU with the tanh argument clamped to +-15 (shaders/gelu_mul.wgsl:10-16).
+// tanh(t) = 2 / (1 + e^(-2t)) - 1: the quotient carries the few-ulp error of
+// the hardware exp and reciprocal relative to itself, so the final f32
+// subtraction rounds to the correctly rounded tanh except within ~1e-11 of
+// a rounding boundary; 1 + tanh(t) is then formed in f32 as the shader forms
+// it (exactly 0, or a multiple of 2^-24, where tanh is near -1). The
+// library tanhf's exact evaluation cost the gate/up epilogue more than a
+// microsecond per launch.
 __device__ __forceinline__ float gelu_tanh(float x) {
   float t = 0.7978845608028654f * x * (1.0f + 0.044715f * x * x);
   t = fminf(fmaxf(t, -15.0f), 15.0f);
-  return 0.5f * x * (1.0f + tanhf(t));
+  const float th = 2.0f * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * t)) - 1.0f;
+  return 0.5f * x * (1.0f + th);
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -779,11 +779,14 @@ struct MqArgs {
   float* ws;
 };
 
+constexpr int kMqPages = 96;  // page-table entries of a chunk held in LDS (1024 positions of 16-row pages)
+
 template <bool PAGED>
 __global__ __launch_bounds__(NT, 2) void mq_attn_kernel(MqArgs a) {
   __shared__ __align__(16) _Float16 kt[MQ_STEP * MQ_RS];
   __shared__ __align__(16) _Float16 vt[MQ_STEP * MQ_RS];
   __shared__ uint32_t s_seq, s_chunk;
+  __shared__ int32_t s_pg[kMqPages];
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, q = l >> 4, c = l & 15;
   const uint32_t kvh = blockIdx.y;
   const uint32_t CH = MQ_STEP * a.nstep;
@@ -821,10 +824,27 @@ __global__ __launch_bounds__(NT, 2) void mq_attn_kernel(MqArgs a) {
   const uint32_t last = wstart + cend - 1; // last live position of the chunk
   const uint32_t nst = (cend - c0 + MQ_STEP - 1) / MQ_STEP;
 
+  // PAGED: the chunk's page-table entries, clamped to the pool, in LDS (when
+  // they fit), so that a step's row loads do not wait on a page-table load
+  const uint32_t fpg = PAGED ? (wstart + c0) / a.page_size : 0u;
+  const uint32_t npg = PAGED ? last / a.page_size - fpg + 1 : 0u;
+  const bool pg_lds = PAGED && npg <= (uint32_t)kMqPages;  // (uniform)
+  if constexpr (PAGED) {
+    if (pg_lds && (uint32_t)tid < npg) {
+      const int32_t pg = a.page_table[(size_t)seq * a.max_pages + fpg + tid];
+      s_pg[tid] = pg < 0 ? 0 : (pg >= (int32_t)a.num_pages ? (int32_t)a.num_pages - 1 : pg);
+    }
+    __syncthreads();
+  }
   auto row_of = [&](uint32_t pos) -> size_t {
     if constexpr (PAGED) {
-      int32_t pg = a.page_table[(size_t)seq * a.max_pages + pos / a.page_size];
-      pg = pg < 0 ? 0 : (pg >= (int32_t)a.num_pages ? (int32_t)a.num_pages - 1 : pg);
+      int32_t pg;
+      if (pg_lds) {
+        pg = s_pg[pos / a.page_size - fpg];
+      } else {
+        pg = a.page_table[(size_t)seq * a.max_pages + pos / a.page_size];
+        pg = pg < 0 ? 0 : (pg >= (int32_t)a.num_pages ? (int32_t)a.num_pages - 1 : pg);
+      }
       return (size_t)pg * a.page_size + pos % a.page_size;
     }
     return pos;

@@ -34,6 +34,8 @@
 //    matmul that follows, so that its workgroups copy them instead of each
 //    building them again (the LM head's 4096 workgroups read the same
 //    activations).
+#include <utility>
+
 #include "g4_internal.hpp"
 
 namespace {
@@ -523,95 +525,18 @@ __device__ __forceinline__ float epilogue(float y, float cap) {
   return y;
 }
 
-// MODE 0: a row group is 64 rows of one segment. MODE 1 (gate/up): segments
-// 0 and 1 have the same rows; a row group is 32 rows of both, waves 0-1 gate,
-// waves 2-3 up, and the output (segment 0's Y) is gelu(gate) * up; with
-// ops_out the workgroup also writes its 32 rows of the product as one
-// sub-block of the sub-block-scaled operand blocks a Q6_K down projection
-// reads (OPK 2).
-//
-// KG = 2: the workgroup is two groups of four waves that take the even and
-// the odd blocks of the K chunk (kc even), each through its own LDS operand
-// buffer, and add their sums through LDS before the epilogue, which group 0
-// runs (group 1 passes the same barriers).
-template <int QT, int BPR, int NTV, int MODE, int OPK, int KG = 1>
-__global__ __launch_bounds__(MNT * KG) void mmf_kernel(MmArgs a) {
-  static_assert(OPK != 2 || (QT == 1 && MODE == 0), "sub-block-scaled operands: Q6_K matmuls");
-  static_assert(KG == 1 || KG == 2, "one or two K groups");
-  constexpr uint32_t LB = Ops::bytes(NTV) + 16;  // + the copy's sink slot
-  __shared__ __align__(16) uint8_t lds_all[KG * LB];
-
-  const int kg = KG == 1 ? 0 : (int)(threadIdx.x / MNT);
-  uint8_t* const lds = lds_all + kg * LB;
-  const int tid = (int)(threadIdx.x % MNT), w = tid >> 6, l = tid & 63, q = l >> 4;
-  const uint32_t g = blockIdx.x / a.ksplit, chunk = blockIdx.x % a.ksplit;
-  int si = 0;
-  uint32_t rbase;
-  const uint8_t* W;
-  uint32_t M;
-  if constexpr (MODE == 0) {
-#pragma unroll
-    for (int i = 1; i < 4; ++i)
-      if (i < a.n && g >= a.s[i].g_begin) si = i;
-    W = a.s[si].W;
-    M = a.s[si].M;
-    rbase = (g - a.s[si].g_begin) * 64 + 16u * w;
-  } else {
-    W = a.s[w >> 1].W;
-    M = a.s[0].M;
-    rbase = g * 32 + 16u * (w & 1);
-  }
-  const uint32_t kb0 = chunk * a.kc + (uint32_t)kg, nkb = a.kc / KG;  // this group's blocks: kb0 + KG j
-
-  OpSrc<NTV, OPK> src;
-  WRegs<QT> wr, wn;
-  src.load(a, kb0, tid);
-  load_w<BPR>(wr, W, M, rbase, kb0, l);
-  src.store(lds, a, tid);
-  __syncthreads();
-
-  f4 acc[NTV];
-#pragma unroll
-  for (int t = 0; t < NTV; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+// Products of one super-block: the weights of this lane's 16-row tile in wr,
+// the block's operands in LDS at lds; acc[t] gains the tile's sums for
+// vectors 16t .. 16t + 15.
+template <int QT, int NTV, int OPK>
+__device__ __forceinline__ void mm_block(const WRegs<QT>& wr, const uint8_t* lds, f4 (&acc)[NTV], int l, int q) {
   const u32x4* lv = (const u32x4*)lds;
-
-  for (uint32_t j = 0; j < nkb; ++j) {
-    const bool more = j + 1 < nkb;
-    const uint32_t kn = kb0 + KG * (j + (more ? 1u : 0u));
-    src.load(a, kn, tid);  // the next block is in flight during this one
-    load_w<BPR>(wn, W, M, rbase, kn, l);
-
-    f4 C[NTV], Cm[NTV];
-    if constexpr (OPK == 2) {
-      // each sub-block's products scaled by its own 2^-e, then d
-      const float* scs = (const float*)(lds + OpsSub::scale_off(NTV));
+  f4 C[NTV], Cl[NTV], Cm[NTV];
+  if constexpr (OPK == 2) {
+    // each sub-block's products scaled by its own 2^-e, then d
+    const float* scs = (const float*)(lds + OpsSub::scale_off(NTV));
 #pragma unroll
-      for (int t = 0; t < NTV; ++t) C[t] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const h8 A = a_operand(wr, s, q);
-#pragma unroll
-        for (int t = 0; t < NTV; ++t) {
-          const u32x4 bh = lv[(t * Ops::MAIN_T + s * 2048) / 16 + l];
-          const u32x4 bl = lv[(t * Ops::MAIN_T + s * 2048 + 1024) / 16 + l];
-          f4 z = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bh), f4{0.f, 0.f, 0.f, 0.f}, 0, 0,
-                                                        0);
-          z = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bl), z, 0, 0, 0);
-          const float fs = scs[t * 128 + s * 16 + (l & 15)];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) C[t][i] += fs * z[i];
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < NTV; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[t][i] += g4d::f16_bits_to_f32(wr.dd[i]) * C[t][i];
-    } else {
-    // the x_hi and x_lo products accumulate apart: two independent MFMA
-    // chains per tile instead of one (a dependent MFMA waits for its
-    // predecessor's result; waves of the batched LM head spent 55 % of their
-    // cycles waiting to issue with one chain)
-    f4 Cl[NTV];
+    for (int t = 0; t < NTV; ++t) C[t] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const h8 A = a_operand(wr, s, q);
@@ -619,60 +544,115 @@ __global__ __launch_bounds__(MNT * KG) void mmf_kernel(MmArgs a) {
       for (int t = 0; t < NTV; ++t) {
         const u32x4 bh = lv[(t * Ops::MAIN_T + s * 2048) / 16 + l];
         const u32x4 bl = lv[(t * Ops::MAIN_T + s * 2048 + 1024) / 16 + l];
-        const f4 zh = s == 0 ? f4{0.f, 0.f, 0.f, 0.f} : C[t];
-        const f4 zl = s == 0 ? f4{0.f, 0.f, 0.f, 0.f} : Cl[t];
-        C[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bh), zh, 0, 0, 0);
-        Cl[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bl), zl, 0, 0, 0);
+        f4 z = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bh), f4{0.f, 0.f, 0.f, 0.f}, 0, 0,
+                                                      0);
+        z = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bl), z, 0, 0, 0);
+        const float fs = scs[t * 128 + s * 16 + (l & 15)];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) C[t][i] += fs * z[i];
       }
     }
 #pragma unroll
-    for (int t = 0; t < NTV; ++t) C[t] += Cl[t];
-    if constexpr (QT == 0) {
-      const h8 Am = min_operand(wr, q);
+    for (int t = 0; t < NTV; ++t)
 #pragma unroll
-      for (int t = 0; t < NTV; ++t) {
-        const u32x4 bm = lv[(Ops::sums_off(NTV) + t * 1024) / 16 + l];
-        Cm[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Am, __builtin_bit_cast(h8, bm), f4{0.f, 0.f, 0.f, 0.f}, 0,
-                                                        0, 0);
-      }
-    }
-    const float* scl = (const float*)(lds + Ops::scale_off(NTV));
+      for (int i = 0; i < 4; ++i) acc[t][i] += g4d::f16_bits_to_f32(wr.dd[i]) * C[t][i];
+    return;
+  }
+  // the x_hi and x_lo products accumulate apart: two independent MFMA
+  // chains per tile instead of one (a dependent MFMA waits for its
+  // predecessor's result; waves of the batched LM head spent 55 % of their
+  // cycles waiting to issue with one chain)
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const h8 A = a_operand(wr, s, q);
 #pragma unroll
     for (int t = 0; t < NTV; ++t) {
-      const float fs = scl[t * 16 + (l & 15)];
+      const u32x4 bh = lv[(t * Ops::MAIN_T + s * 2048) / 16 + l];
+      const u32x4 bl = lv[(t * Ops::MAIN_T + s * 2048 + 1024) / 16 + l];
+      const f4 zh = s == 0 ? f4{0.f, 0.f, 0.f, 0.f} : C[t];
+      const f4 zl = s == 0 ? f4{0.f, 0.f, 0.f, 0.f} : Cl[t];
+      C[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bh), zh, 0, 0, 0);
+      Cl[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8, bl), zl, 0, 0, 0);
+    }
+  }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if constexpr (QT == 0) {
-          const float d = g4d::f16_bits_to_f32(wr.dd[i] & 0xffffu);
-          const float dm = g4d::f16_bits_to_f32(wr.dd[i] >> 16) * 64.0f;
-          acc[t][i] += fs * (d * C[t][i] - dm * Cm[t][i]);
-        } else {
-          acc[t][i] += fs * g4d::f16_bits_to_f32(wr.dd[i]) * C[t][i];
-        }
+  for (int t = 0; t < NTV; ++t) C[t] += Cl[t];
+  if constexpr (QT == 0) {
+    const h8 Am = min_operand(wr, q);
+#pragma unroll
+    for (int t = 0; t < NTV; ++t) {
+      const u32x4 bm = lv[(Ops::sums_off(NTV) + t * 1024) / 16 + l];
+      Cm[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Am, __builtin_bit_cast(h8, bm), f4{0.f, 0.f, 0.f, 0.f}, 0, 0,
+                                                      0);
+    }
+  }
+  const float* scl = (const float*)(lds + Ops::scale_off(NTV));
+#pragma unroll
+  for (int t = 0; t < NTV; ++t) {
+    const float fs = scl[t * 16 + (l & 15)];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (QT == 0) {
+        const float d = g4d::f16_bits_to_f32(wr.dd[i] & 0xffffu);
+        const float dm = g4d::f16_bits_to_f32(wr.dd[i] >> 16) * 64.0f;
+        acc[t][i] += fs * (d * C[t][i] - dm * Cm[t][i]);
+      } else {
+        acc[t][i] += fs * g4d::f16_bits_to_f32(wr.dd[i]) * C[t][i];
       }
     }
-    }
-    __syncthreads();  // every wave is done with this block's operands
-    if (more) {
-      src.store(lds, a, tid);
-      __syncthreads();
-    }
-    wr = wn;
   }
-  if constexpr (KG == 2) {  // group 1's sums into group 0's (its operand buffer is free)
-    f4* xk = (f4*)(lds_all + LB);
-    if (kg == 1) {
+}
+
+// Row coordinates of a workgroup: segment, first row of this wave's tile.
+struct MmRows {
+  int si;
+  uint32_t rbase, M;
+  const uint8_t* W;
+};
+template <int MODE>
+__device__ __forceinline__ MmRows mm_rows(const MmArgs& a, uint32_t g, int w) {
+  MmRows r;
+  r.si = 0;
+  if constexpr (MODE == 0) {
 #pragma unroll
-      for (int t = 0; t < NTV; ++t) xk[(w * NTV + t) * 64 + l] = acc[t];
+    for (int i = 1; i < 4; ++i)
+      if (i < a.n && g >= a.s[i].g_begin) r.si = i;
+    r.W = a.s[r.si].W;
+    r.M = a.s[r.si].M;
+    r.rbase = (g - a.s[r.si].g_begin) * 64 + 16u * w;
+  } else {
+    r.W = (w >> 1) ? a.s[1].W : a.s[0].W;  // (no dynamic index into the kernel arguments)
+    r.M = a.s[0].M;
+    r.rbase = g * 32 + 16u * (w & 1);
+  }
+  return r;
+}
+
+// Outputs of a workgroup once every wave's sums are in acc: the sums of
+// groups 1 .. KG - 1 go through LDS at x1 into group 0's, then MODE 0 stores rows (or
+// partial sums) with the softcap, MODE 1 the gate/up product and its
+// operand blocks. lds_all is free scratch for every wave (callers order it
+// after their last operand reads with a barrier).
+template <int NTV, int MODE, int KG>
+__device__ __forceinline__ void mm_epilogue(const MmArgs& a, f4 (&acc)[NTV], uint8_t* lds_all, uint8_t* x1, int kg,
+                                            int w, int l, int q, uint32_t g, uint32_t chunk, int si, uint32_t rbase,
+                                            uint32_t M) {
+  if constexpr (KG > 1) {  // the other groups' sums into group 0's, in group order
+    f4* xk = (f4*)x1;
+    if (kg > 0) {
+#pragma unroll
+      for (int t = 0; t < NTV; ++t) xk[(((kg - 1) * 4 + w) * NTV + t) * 64 + l] = acc[t];
     }
     __syncthreads();
     if (kg == 0) {
 #pragma unroll
-      for (int t = 0; t < NTV; ++t) {
-        const f4 o = xk[(w * NTV + t) * 64 + l];
+      for (int o = 0; o < KG - 1; ++o)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[t][i] += o[i];
-      }
+        for (int t = 0; t < NTV; ++t) {
+          const f4 v = xk[((o * 4 + w) * NTV + t) * 64 + l];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[t][i] += v[i];
+        }
     }
   }
   const bool out_group = kg == 0;
@@ -762,6 +742,94 @@ __global__ __launch_bounds__(MNT * KG) void mmf_kernel(MmArgs a) {
   }
 }
 
+template <typename F, int... J>
+__device__ __forceinline__ void static_for_seq(F&& f, std::integer_sequence<int, J...>) {
+  (f(std::integral_constant<int, J>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
+
+// MODE 0: a row group is 64 rows of one segment. MODE 1 (gate/up): segments
+// 0 and 1 have the same rows; a row group is 32 rows of both, waves 0-1 gate,
+// waves 2-3 up, and the output (segment 0's Y) is gelu(gate) * up; with
+// ops_out the workgroup also writes its 32 rows of the product as one
+// sub-block of the sub-block-scaled operand blocks a Q6_K down projection
+// reads (OPK 2).
+//
+// KG > 1: the workgroup is KG groups of four waves; group g takes blocks
+// g, g + KG, ... of the K chunk (kc a multiple of KG), each group through its
+// own LDS operand buffer, and the groups add their sums through LDS before
+// the epilogue, which group 0 runs (the others pass the same barriers).
+//
+// NKB > 0: each group walks exactly NKB blocks (kc = KG NKB, host-checked),
+// unrolled: the weights of blocks j + 1 and j + 2 are in flight, each in
+// registers of its own, while block j is multiplied (a loop that carries
+// the next block's weights into the current block's registers waits for
+// them at the end of every iteration). NKB = 0: a loop over kc / KG blocks
+// with one block in flight.
+template <int QT, int BPR, int NTV, int MODE, int OPK, int KG = 1, int NKB = 0>
+__global__ __launch_bounds__(MNT * KG) void mmf_kernel(MmArgs a) {
+  static_assert(OPK != 2 || (QT == 1 && MODE == 0), "sub-block-scaled operands: Q6_K matmuls");
+  static_assert(KG >= 1 && KG <= 3, "one to three K groups");
+  constexpr uint32_t LB = Ops::bytes(NTV) + 16;  // + the copy's sink slot
+  static_assert(KG == 1 || LB >= (uint32_t)(KG - 1) * 4u * NTV * 1024u, "other groups' sums fit in group 1's buffer");
+  __shared__ __align__(16) uint8_t lds_all[KG * LB];
+
+  const int kg = KG == 1 ? 0 : (int)(threadIdx.x / MNT);
+  uint8_t* const lds = lds_all + kg * LB;
+  const int tid = (int)(threadIdx.x % MNT), w = tid >> 6, l = tid & 63, q = l >> 4;
+  const uint32_t g = blockIdx.x / a.ksplit, chunk = blockIdx.x % a.ksplit;
+  const MmRows rw = mm_rows<MODE>(a, g, w);
+  const uint32_t kb0 = chunk * a.kc + (uint32_t)kg;  // this group's blocks: kb0 + KG j
+
+  f4 acc[NTV];
+#pragma unroll
+  for (int t = 0; t < NTV; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+  OpSrc<NTV, OPK> src;
+  if constexpr (NKB > 0) {
+    WRegs<QT> wr[NKB];
+    src.load(a, kb0, tid);
+    load_w<BPR>(wr[0], rw.W, rw.M, rw.rbase, kb0, l);
+    if constexpr (NKB > 1) load_w<BPR>(wr[1], rw.W, rw.M, rw.rbase, kb0 + KG, l);
+    src.store(lds, a, tid);
+    __syncthreads();
+    static_for<NKB>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      if constexpr (j + 1 < NKB) src.load(a, kb0 + KG * (j + 1), tid);  // the next block's operands
+      if constexpr (j + 2 < NKB) load_w<BPR>(wr[j + 2], rw.W, rw.M, rw.rbase, kb0 + KG * (j + 2), l);
+      mm_block<QT, NTV, OPK>(wr[j], lds, acc, l, q);
+      __syncthreads();  // every wave is done with this block's operands
+      if constexpr (j + 1 < NKB) {
+        src.store(lds, a, tid);
+        __syncthreads();
+      }
+    });
+  } else {
+    const uint32_t nkb = a.kc / KG;
+    WRegs<QT> wr, wn;
+    src.load(a, kb0, tid);
+    load_w<BPR>(wr, rw.W, rw.M, rw.rbase, kb0, l);
+    src.store(lds, a, tid);
+    __syncthreads();
+    for (uint32_t j = 0; j < nkb; ++j) {
+      const bool more = j + 1 < nkb;
+      const uint32_t kn = kb0 + KG * (j + (more ? 1u : 0u));
+      src.load(a, kn, tid);  // the next block is in flight during this one
+      load_w<BPR>(wn, rw.W, rw.M, rw.rbase, kn, l);
+      mm_block<QT, NTV, OPK>(wr, lds, acc, l, q);
+      __syncthreads();  // every wave is done with this block's operands
+      if (more) {
+        src.store(lds, a, tid);
+        __syncthreads();
+      }
+      wr = wn;
+    }
+  }
+  mm_epilogue<NTV, MODE, KG>(a, acc, lds_all, lds_all + LB, kg, w, l, q, g, chunk, rw.si, rw.rbase, rw.M);
+}
+
 // ---------------------------------------------------------------------------
 // Unpack check of the matrix-core operands (path 2 of the test export
 // g4_dequantPath): one wave per 16 blocks, each block a one-block row, lanes
@@ -824,16 +892,62 @@ bool mm_supported(uint32_t bpr) {
   return bpr == 4 || bpr == 6 || bpr == 8 || bpr == 12 || bpr == 16 || bpr == 24 || bpr == 32 || bpr == 48;
 }
 
+constexpr uint32_t kLdsBytes = 160 * 1024;
+
+// Unrolled walks (NKB > 0) for prebuilt operands: every count of blocks per
+// group the launches take (KG 1: kc 1 .. 6; gate/up, KG 2: 3 or 4; KG 3: 1 or
+// 2); anything else, and rebuilt operands, loops.
+template <int KG, int OPK>
+constexpr bool nkb_unrolled(int n) {
+  return OPK != 0 && (KG == 1 ? (n >= 1 && n <= 6 && n != 5) : KG == 2 ? (n == 3 || n == 4) : (n == 1 || n == 2));
+}
+
+template <int QT, int BPR, int NTV, int MODE, int OPK, int KG>
+void mm_launch_kg(g4_ctx* ctx, const MmArgs& a, uint32_t groups, bool unroll) {
+  const dim3 grid(groups * a.ksplit), block(KG * MNT);
+  switch (unroll ? a.kc / KG : 0u) {
+#define G4_MM_NKB(n)                                                                                      \
+  case n:                                                                                                 \
+    if constexpr (BPR % (KG * n) == 0 && nkb_unrolled<KG, OPK>(n)) {                                      \
+      hipLaunchKernelGGL((mmf_kernel<QT, BPR, NTV, MODE, OPK, KG, n>), grid, block, 0, ctx->stream, a); \
+      return;                                                                                             \
+    }                                                                                                     \
+    break;
+    G4_MM_NKB(1)
+    G4_MM_NKB(2)
+    G4_MM_NKB(3)
+    G4_MM_NKB(4)
+    G4_MM_NKB(6)
+#undef G4_MM_NKB
+    default:
+      break;
+  }
+  hipLaunchKernelGGL((mmf_kernel<QT, BPR, NTV, MODE, OPK, KG, 0>), grid, block, 0, ctx->stream, a);
+}
+
+// K groups per workgroup: the gate/up pair (one workgroup per CU, a whole K
+// each) takes two; launches of about one workgroup per CU or fewer take
+// three where kc allows (a wave per SIMD leaves the latency of every MFMA
+// and operand read exposed; 12 waves share one CU's work three ways).
+//
+// The unrolled walk holds a register set per block: it is taken by launches
+// of about one workgroup per CU or fewer (latency-bound), and with 64-vector
+// operands only where the walk is short or the gate/up pair's (longer walks
+// spill; the batched LM head, 4096 workgroups, keeps its occupancy with the
+// loop).
 template <int QT, int BPR, int NTV, int MODE, int OPK>
 int mm_launch(g4_ctx* ctx, const MmArgs& a, uint32_t groups) {
-  // the gate/up pair (one workgroup per CU, a whole K each): two K groups
-  // (measured at B=32 13.6 -> 13.2 us, at B=64 21.0 -> 20.2 us)
-  if (MODE == 1 && a.kc % 2 == 0)
-    hipLaunchKernelGGL((mmf_kernel<QT, BPR, NTV, MODE, OPK, 2>), dim3(groups * a.ksplit), dim3(2 * MNT), 0,
-                       ctx->stream, a);
-  else
-    hipLaunchKernelGGL((mmf_kernel<QT, BPR, NTV, MODE, OPK, 1>), dim3(groups * a.ksplit), dim3(MNT), 0,
-                       ctx->stream, a);
+  constexpr uint32_t LB = Ops::bytes(NTV) + 16;
+  const uint32_t cus = (uint32_t)(ctx->num_cus > 0 ? ctx->num_cus : 256);
+  const bool few = groups * a.ksplit <= cus;
+  if (MODE == 1 && a.kc % 2 == 0) {
+    mm_launch_kg<QT, BPR, NTV, MODE, OPK, 2>(ctx, a, groups, few);
+  } else if (few && a.kc % 3 == 0 && 3 * LB <= kLdsBytes) {
+    if constexpr (3 * LB <= kLdsBytes)
+      mm_launch_kg<QT, BPR, NTV, MODE, OPK, 3>(ctx, a, groups, NTV <= 2 || a.kc / 3 <= 2);
+  } else {
+    mm_launch_kg<QT, BPR, NTV, MODE, OPK, 1>(ctx, a, groups, few && (NTV <= 2 || a.kc <= 2));
+  }
   G4_LAUNCHED(ctx, "mm");
   return G4_OK;
 }
