@@ -7,6 +7,7 @@
 
 namespace g4mqf {
 
+
 constexpr int MQ_NT = 256;  // threads of an attention workgroup
 
 // exp(x) = 2^(x log2 e) on the hardware exp2 (v_exp_f32, 1 ulp): the
@@ -440,14 +441,35 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   // a step's K rows, then its V rows: piece pc = tid + NT (i % 8) is row
   // pc / PR, 16 bytes at column 8 (pc % PR)
   mu4 pf[16];
+  // PAGED: the page of each row this thread loads in the first step,
+  // requested before any other load of the launch (the rows' loads wait for
+  // it; the q/k/v partials, issued after it, then arrive meanwhile)
+  int32_t pg0[8];
+  if constexpr (PAGED) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t r = ((uint32_t)tid + (uint32_t)NT * (uint32_t)i) / PR;
+      const uint32_t p = min(wstart + c0 + r, last);
+      pg0[i] = a.page_table[(size_t)seq * a.max_pages + p / a.page_size];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
   auto load_step = [&](uint32_t st) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const uint32_t pc = (uint32_t)tid + (uint32_t)NT * (uint32_t)(i & 7);
       const uint32_t r = pc / PR, col = (pc % PR) * 8;
       const uint32_t p = min(wstart + c0 + st * MQ_STEP + r, last);
+      size_t row;
+      if (PAGED && st == 0) {
+        const int32_t pg = pg0[i & 7];
+        row = (size_t)(pg < 0 ? 0 : (pg >= (int32_t)a.num_pages ? (int32_t)a.num_pages - 1 : pg)) * a.page_size +
+              p % a.page_size;
+      } else {
+        row = crow(p);
+      }
       const uint16_t* base = i < 8 ? a.kc : a.vc;
-      const mu4* src = (const mu4*)(base + (crow(p) * a.nkh + kvh) * HD + col);
+      const mu4* src = (const mu4*)(base + (row * a.nkh + kvh) * HD + col);
       pf[i] = LONG ? __builtin_nontemporal_load(src) : *src;
     }
   };
@@ -478,60 +500,80 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   float4 q0, q1;
   float kx, vx;
   bool stalled = false;  // (uniform) FUSED: the wait for q/k/v expired
-  if constexpr (PAGED) {  // the split-K partial sums, added in chunk order
-    // (up to kMaxParts partials; every load is issued before the first add)
+  // PAGED: the split-K partial sums (up to kMaxParts partials), added in
+  // chunk order once the first step's rows are requested
+  float4 u[PAGED ? kMaxParts : 1], v[PAGED ? kMaxParts : 1];
+  float ku[PAGED ? kMaxParts : 1], vu[PAGED ? kMaxParts : 1];
+  if constexpr (PAGED) {
     const size_t qs_stride = (size_t)a.num_seqs * a.nqh * HD;
     const float* qg = a.q_raw + (size_t)seq * a.nqh * HD + qoff;
-    float4 u[kMaxParts], v[kMaxParts];
 #pragma unroll
     for (int k = 0; k < kMaxParts; ++k) {
       const size_t o = (size_t)min((uint32_t)k, a.nparts - 1) * qs_stride;
       u[k] = *(const float4*)(qg + o);
       v[k] = *(const float4*)(qg + o + HD / 2);
     }
-    q0 = make_float4(0.f, 0.f, 0.f, 0.f);
-    q1 = q0;
-#pragma unroll
-    for (int k = 0; k < kMaxParts; ++k)
-      if ((uint32_t)k < a.nparts) {
-        q0.x += u[k].x; q0.y += u[k].y; q0.z += u[k].z; q0.w += u[k].w;
-        q1.x += v[k].x; q1.y += v[k].y; q1.z += v[k].z; q1.w += v[k].w;
-      }
   } else if constexpr (!FUSED) {
     const float* qg = a.q_raw + qoff;
     q0 = *(const float4*)qg;
     q1 = *(const float4*)(qg + HD / 2);
   }
   const uint2 w0 = *(const uint2*)(a.q_w + td), w1 = *(const uint2*)(a.q_w + HD / 2 + td);
+  // The k/v loads are unconditional (from the q input, no smaller, when the
+  // layer forms no row) and selected only where they are used: a load under
+  // a branch is waited for where the branch joins, and with it every load
+  // issued before it.
+  const float* const kr = own_row ? a.k_raw : a.q_raw;
+  const float* const vr = own_row ? a.v_raw : a.q_raw;
   if constexpr (PAGED) {
     const size_t kv_stride = (size_t)a.num_seqs * a.nkh * HD;
     const size_t ko = ((size_t)seq * a.nkh + kvh) * HD + tid;
-    float ku[kMaxParts], vu[kMaxParts];
 #pragma unroll
     for (int k = 0; k < kMaxParts; ++k) {
       const size_t o = (size_t)min((uint32_t)k, a.nparts - 1) * kv_stride + ko;
-      ku[k] = own_row ? a.k_raw[o] : 0.f;
-      vu[k] = own_row ? a.v_raw[o] : 0.f;
+      ku[k] = kr[o];
+      vu[k] = vr[o];
     }
+  } else if constexpr (!FUSED) {
+    kx = kr[(size_t)kvh * HD + tid];
+    vx = vr[(size_t)kvh * HD + tid];
+  }
+  // (raw bits, from the q norm's weights when there is no row: converting
+  // here would wait for every load issued so far)
+  const uint16_t kwb = (own_row ? a.k_w : a.q_w)[tid];
+  const uint16_t rfb = a.rope_freqs[tid & (HD / 2 - 1)];
+  // the table row through a buffer resource of no records when there is no
+  // table: the load stays unconditional (reads past a resource return 0;
+  // the value is then unused) and a plain global load, not a flat one
+  const __amdgpu_buffer_rsrc_t csr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.rope_cs, (short)0, a.rope_cs ? (int)0xffffffff : 0, 0x00020000);
+  const auto csw = __builtin_amdgcn_raw_buffer_load_b64(
+      csr, (uint32_t)(((size_t)pos * (HD / 2) + (tid & (HD / 2 - 1))) * sizeof(float2)), 0, 0);
+  const float2 cst = make_float2(__uint_as_float(csw[0]), __uint_as_float(csw[1]));
+  __builtin_amdgcn_sched_barrier(0);
+  load_step(0);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (FUSED) stalled = mqf_wait_stage(a, tid, qoff, kvh, own_row, q0, q1, kx, vx);
+  if constexpr (PAGED) {
+    q0 = make_float4(0.f, 0.f, 0.f, 0.f);
+    q1 = q0;
     kx = 0.f;
     vx = 0.f;
 #pragma unroll
     for (int k = 0; k < kMaxParts; ++k)
       if ((uint32_t)k < a.nparts) {
+        q0.x += u[k].x; q0.y += u[k].y; q0.z += u[k].z; q0.w += u[k].w;
+        q1.x += v[k].x; q1.y += v[k].y; q1.z += v[k].z; q1.w += v[k].w;
         kx += ku[k];
         vx += vu[k];
       }
-  } else if constexpr (!FUSED) {
-    kx = own_row ? a.k_raw[(size_t)kvh * HD + tid] : 0.f;
-    vx = own_row ? a.v_raw[(size_t)kvh * HD + tid] : 0.f;
   }
-  const float kw = own_row ? g4d::f16_bits_to_f32(a.k_w[tid]) : 0.f;
-  const uint16_t rfb = a.rope_freqs[tid & (HD / 2 - 1)];
-  const float2 cst = a.rope_cs ? a.rope_cs[(size_t)pos * (HD / 2) + (tid & (HD / 2 - 1))] : make_float2(1.f, 0.f);
-  __builtin_amdgcn_sched_barrier(0);
-  load_step(0);
-  __builtin_amdgcn_sched_barrier(0);
-  if constexpr (FUSED) stalled = mqf_wait_stage(a, tid, qoff, kvh, own_row, q0, q1, kx, vx);
+  if constexpr (!FUSED) {
+    if (!own_row) {
+      kx = 0.f;
+      vx = 0.f;
+    }
+  }
 
   // RoPE of this position (rope_cos_sin), from the table when there is one:
   // the frequency's f64 pow and a large-argument sincos are some 380 VALU
@@ -558,7 +600,7 @@ __device__ __forceinline__ void mqf_body(const MqfArgs& a, uint32_t bx, uint32_t
   }
   const float invk = __builtin_amdgcn_rsqf(skk * (1.0f / (float)HD) + a.eps);
   const float invv = __builtin_amdgcn_rsqf(svv * (1.0f / (float)HD) + a.eps);
-  kn_s[tid] = kx * kw * invk;
+  kn_s[tid] = own_row ? kx * g4d::f16_bits_to_f32(kwb) * invk : 0.f;
   cur_s[HD + tid] = g4d::f32_to_f16_bits(vx * invv);
   {
     const float x0[4] = {q0.x, q0.y, q0.z, q0.w}, x1[4] = {q1.x, q1.y, q1.z, q1.w};
