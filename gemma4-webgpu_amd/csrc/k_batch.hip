@@ -103,6 +103,12 @@ __global__ __launch_bounds__(PNT) void bprep_kernel(BPrepArgs a) {
   const size_t vstride = (size_t)a.B * K;
   float4 x[XP], r[PRO == 2 ? XP : 1];
   uint2 w1[PRO >= 1 ? XP : 1], w2[PRO == 2 ? XP : 1];
+  // (w2 read unconditionally, from w1 when there is none: a load under a
+  // branch is waited for where the branch joins, before the partials below
+  // are even requested)
+  const uint16_t* const w2p = a.w2 ? a.w2 : a.w1;
+  // (likewise the output scale: requested with the rest, not after the first norm)
+  const uint16_t scb = PRO == 2 ? (a.scale ? a.scale : a.w1)[0] : (uint16_t)0;
 #pragma unroll
   for (int p = 0; p < XP; ++p) {
     const int f = 4 * tid + 4 * PNT * p, fc = f < K ? f : 0;
@@ -110,7 +116,7 @@ __global__ __launch_bounds__(PNT) void bprep_kernel(BPrepArgs a) {
     if constexpr (PRO >= 1) w1[p] = *(const uint2*)(a.w1 + fc);
     if constexpr (PRO == 2) {
       r[p] = *(const float4*)(a.residual + (size_t)v * K + fc);
-      w2[p] = a.w2 ? *(const uint2*)(a.w2 + fc) : make_uint2(0, 0);
+      w2[p] = *(const uint2*)(w2p + fc);
     }
   }
   for (uint32_t c0 = 1; c0 < a.nparts; c0 += PMAX) {  // chunks 1.. in order
@@ -146,7 +152,7 @@ __global__ __launch_bounds__(PNT) void bprep_kernel(BPrepArgs a) {
       for (int p = 0; p < XP; ++p) x[p] = mulw(x[p], w1[p], inv1);
     } else {
       float ss2 = 0.f;
-      const float sc = a.scale ? g4d::f16_bits_to_f32(*a.scale) : 1.0f;
+      const float sc = a.scale ? g4d::f16_bits_to_f32(scb) : 1.0f;
 #pragma unroll
       for (int p = 0; p < XP; ++p) {
         const int f = 4 * tid + 4 * PNT * p;
@@ -255,14 +261,6 @@ struct MmArgs {
   uint8_t* ops_out;     // MODE 1: the product's sub-block-scaled operand blocks (or null)
 };
 
-// 8 bytes at a 2-byte aligned address: three aligned dwords, funnel-shifted.
-__device__ __forceinline__ uint2 ld8_a2(const uint8_t* p) {
-  const uintptr_t ad = (uintptr_t)p;
-  const u32x3a w = *(const u32x3a*)(p - (ad & 3));
-  const uint32_t sh = (uint32_t)(ad & 3);
-  return make_uint2(__builtin_amdgcn_alignbyte(w.y, w.x, sh), __builtin_amdgcn_alignbyte(w.z, w.y, sh));
-}
-
 // Weight registers of one 16-row tile and super-block. A side (row lane%16,
 // k-group q = lane/16): codes and sub-block scales; D side (rows 4q + i): d
 // (Q4_K: d | dmin << 16).
@@ -279,9 +277,28 @@ template <> struct WRegs<1> {
   uint32_t dd[4];
 };
 
+// What load_w leaves in registers: the weights as loaded. Q4_K blocks are
+// 16-byte aligned and load straight into WRegs; a Q6_K block (210 bytes) may
+// sit 2 bytes off a dword, so its pieces are loaded as the aligned dwords
+// around them and shifted into place by w_decode where they are used (a
+// shift at the load would wait for the load there, also for the weights of
+// a block that is only prefetched).
+template <int QT>
+struct WLoad;
+template <> struct WLoad<0> {
+  WRegs<0> r;
+};
+template <> struct WLoad<1> {
+  u32x3a ql[4], qh[2];
+  uint32_t s0, s1, s2, s3, s4;  // the dwords around the 16 scale bytes
+  uint32_t dd[4];
+  uint32_t sh;                  // the block's byte offset within its dword (0 or 2)
+};
+
 template <int BPR>
-__device__ __forceinline__ void load_w(WRegs<0>& r, const uint8_t* W, uint32_t M, uint32_t rbase, uint32_t kb,
+__device__ __forceinline__ void load_w(WLoad<0>& ld, const uint8_t* W, uint32_t M, uint32_t rbase, uint32_t kb,
                                        int l) {
+  WRegs<0>& r = ld.r;
   constexpr int BY = 144;
   const int q = l >> 4;
   const uint32_t ra = min(rbase + (uint32_t)(l & 15), M - 1);
@@ -297,33 +314,52 @@ __device__ __forceinline__ void load_w(WRegs<0>& r, const uint8_t* W, uint32_t M
 }
 
 template <int BPR>
-__device__ __forceinline__ void load_w(WRegs<1>& r, const uint8_t* W, uint32_t M, uint32_t rbase, uint32_t kb,
+__device__ __forceinline__ void load_w(WLoad<1>& r, const uint8_t* W, uint32_t M, uint32_t rbase, uint32_t kb,
                                        int l) {
   constexpr int BY = 210;
   const int q = l >> 4;
   const uint32_t ra = min(rbase + (uint32_t)(l & 15), M - 1);
   const uint8_t* blk = W + ((size_t)ra * BPR + kb) * BY;
+  // every piece sits at a multiple of 8 bytes into the block: one shift for all
+  r.sh = (uint32_t)((uintptr_t)blk & 3);
+  const uint8_t* b4 = blk - r.sh;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    r.ql[2 * h] = ld8_a2(blk + 64 * h + 8 * q);
-    r.ql[2 * h + 1] = ld8_a2(blk + 64 * h + 32 + 8 * q);
-    r.qh[h] = ld8_a2(blk + 128 + 32 * h + 8 * q);
+    r.ql[2 * h] = *(const u32x3a*)(b4 + 64 * h + 8 * q);
+    r.ql[2 * h + 1] = *(const u32x3a*)(b4 + 64 * h + 32 + 8 * q);
+    r.qh[h] = *(const u32x3a*)(b4 + 128 + 32 * h + 8 * q);
   }
-  // sc[16] at bytes 192..207 from aligned dwords inside the 210-byte block:
-  // four from the dword holding byte 192 and a fifth (bytes 206..209) that is
-  // only needed when the block is 2 mod 4
-  const uintptr_t ad = (uintptr_t)(blk + 192);
-  const uint32_t sh = (uint32_t)(ad & 3);
-  const uint32_t* p4 = (const uint32_t*)(blk + 192 - sh);
-  const uint32_t x0 = p4[0], x1 = p4[1], x2 = p4[2], x3 = p4[3];
-  const uint32_t x4 = *(const uint32_t*)((const uint8_t*)p4 + 12 + 2 * sh);
-  r.sc = make_uint4(__builtin_amdgcn_alignbyte(x1, x0, sh), __builtin_amdgcn_alignbyte(x2, x1, sh),
-                    __builtin_amdgcn_alignbyte(x3, x2, sh), __builtin_amdgcn_alignbyte(x4, x3, sh));
+  // sc[16] at bytes 192..207: four dwords from the one holding byte 192 and
+  // a fifth (bytes 206..209) that only a block at 2 mod 4 needs
+  const uint32_t* p4 = (const uint32_t*)(b4 + 192);
+  r.s0 = p4[0];
+  r.s1 = p4[1];
+  r.s2 = p4[2];
+  r.s3 = p4[3];
+  r.s4 = *(const uint32_t*)((const uint8_t*)p4 + 12 + 2 * r.sh);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t rd = min(rbase + 4u * q + i, M - 1);
     r.dd[i] = *(const uint16_t*)(W + ((size_t)rd * BPR + kb) * BY + 208);
   }
+}
+
+__device__ __forceinline__ const WRegs<0>& w_decode(const WLoad<0>& ld) { return ld.r; }
+__device__ __forceinline__ WRegs<1> w_decode(const WLoad<1>& ld) {
+  WRegs<1> r;
+  const uint32_t sh = ld.sh;
+  auto piece = [&](const u32x3a& w) {
+    return make_uint2(__builtin_amdgcn_alignbyte(w.y, w.x, sh), __builtin_amdgcn_alignbyte(w.z, w.y, sh));
+  };
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.ql[i] = piece(ld.ql[i]);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) r.qh[h] = piece(ld.qh[h]);
+  r.sc = make_uint4(__builtin_amdgcn_alignbyte(ld.s1, ld.s0, sh), __builtin_amdgcn_alignbyte(ld.s2, ld.s1, sh),
+                    __builtin_amdgcn_alignbyte(ld.s3, ld.s2, sh), __builtin_amdgcn_alignbyte(ld.s4, ld.s3, sh));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.dd[i] = ld.dd[i];
+  return r;
 }
 
 // f16 pairs (1024 + b_i, 1024 + b_j) from two bytes of `codes`: v_perm_b32
@@ -770,7 +806,10 @@ __device__ __forceinline__ void static_for(F&& f) {
 // them at the end of every iteration). NKB = 0: a loop over kc / KG blocks
 // with one block in flight.
 template <int QT, int BPR, int NTV, int MODE, int OPK, int KG = 1, int NKB = 0>
-__global__ __launch_bounds__(MNT * KG) void mmf_kernel(MmArgs a) {
+__global__ __launch_bounds__(MNT * KG)
+// (64-vector tiles over copied operands, one group: two waves per SIMD, the
+// batched LM head's occupancy, rather than the one its free allocation gives)
+__attribute__((amdgpu_waves_per_eu(NTV == 4 && OPK == 1 && KG == 1 ? 2 : 1))) void mmf_kernel(MmArgs a) {
   static_assert(OPK != 2 || (QT == 1 && MODE == 0), "sub-block-scaled operands: Q6_K matmuls");
   static_assert(KG >= 1 && KG <= 3, "one to three K groups");
   constexpr uint32_t LB = Ops::bytes(NTV) + 16;  // + the copy's sink slot
@@ -789,7 +828,7 @@ __global__ __launch_bounds__(MNT * KG) void mmf_kernel(MmArgs a) {
   for (int t = 0; t < NTV; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
   OpSrc<NTV, OPK> src;
   if constexpr (NKB > 0) {
-    WRegs<QT> wr[NKB];
+    WLoad<QT> wr[NKB];
     src.load(a, kb0, tid);
     load_w<BPR>(wr[0], rw.W, rw.M, rw.rbase, kb0, l);
     if constexpr (NKB > 1) load_w<BPR>(wr[1], rw.W, rw.M, rw.rbase, kb0 + KG, l);
@@ -799,7 +838,7 @@ __global__ __launch_bounds__(MNT * KG) void mmf_kernel(MmArgs a) {
       constexpr int j = decltype(jc)::value;
       if constexpr (j + 1 < NKB) src.load(a, kb0 + KG * (j + 1), tid);  // the next block's operands
       if constexpr (j + 2 < NKB) load_w<BPR>(wr[j + 2], rw.W, rw.M, rw.rbase, kb0 + KG * (j + 2), l);
-      mm_block<QT, NTV, OPK>(wr[j], lds, acc, l, q);
+      mm_block<QT, NTV, OPK>(w_decode(wr[j]), lds, acc, l, q);
       __syncthreads();  // every wave is done with this block's operands
       if constexpr (j + 1 < NKB) {
         src.store(lds, a, tid);
@@ -807,24 +846,51 @@ __global__ __launch_bounds__(MNT * KG) void mmf_kernel(MmArgs a) {
       }
     });
   } else {
+    // two register sets in turn (unrolled by two, so that no copy of the next
+    // block's weights waits for them at the end of an iteration)
     const uint32_t nkb = a.kc / KG;
-    WRegs<QT> wr, wn;
+    WLoad<QT> wa, wb;
     src.load(a, kb0, tid);
-    load_w<BPR>(wr, rw.W, rw.M, rw.rbase, kb0, l);
+    load_w<BPR>(wa, rw.W, rw.M, rw.rbase, kb0, l);
     src.store(lds, a, tid);
     __syncthreads();
-    for (uint32_t j = 0; j < nkb; ++j) {
-      const bool more = j + 1 < nkb;
-      const uint32_t kn = kb0 + KG * (j + (more ? 1u : 0u));
-      src.load(a, kn, tid);  // the next block is in flight during this one
-      load_w<BPR>(wn, rw.W, rw.M, rw.rbase, kn, l);
-      mm_block<QT, NTV, OPK>(wr, lds, acc, l, q);
+    auto step = [&](const WLoad<QT>& cur, WLoad<QT>& nxt, uint32_t j) {
+      const bool more = j + 1 < nkb;  // (uniform)
+      if (more) {  // the next block is in flight during this one
+        src.load(a, kb0 + KG * (j + 1), tid);
+        load_w<BPR>(nxt, rw.W, rw.M, rw.rbase, kb0 + KG * (j + 1), l);
+      }
+      mm_block<QT, NTV, OPK>(w_decode(cur), lds, acc, l, q);
       __syncthreads();  // every wave is done with this block's operands
       if (more) {
         src.store(lds, a, tid);
         __syncthreads();
       }
-      wr = wn;
+    };
+    if constexpr (NTV <= 2) {
+      for (uint32_t j = 0; j < nkb; j += 2) {
+        step(wa, wb, j);
+        if (j + 1 < nkb) step(wb, wa, j + 1);
+      }
+    } else {
+      // 64-vector tiles: one decoded set, the next block's weights decoded
+      // into it after this block's products (a second undecoded set costs a
+      // wave per SIMD of occupancy here)
+      WRegs<QT> wr = w_decode(wa);
+      for (uint32_t j = 0; j < nkb; ++j) {
+        const bool more = j + 1 < nkb;  // (uniform)
+        if (more) {
+          src.load(a, kb0 + KG * (j + 1), tid);
+          load_w<BPR>(wb, rw.W, rw.M, rw.rbase, kb0 + KG * (j + 1), l);
+        }
+        mm_block<QT, NTV, OPK>(wr, lds, acc, l, q);
+        __syncthreads();  // every wave is done with this block's operands
+        if (more) {
+          src.store(lds, a, tid);
+          __syncthreads();
+          wr = w_decode(wb);
+        }
+      }
     }
   }
   mm_epilogue<NTV, MODE, KG>(a, acc, lds_all, lds_all + LB, kg, w, l, q, g, chunk, rw.si, rw.rbase, rw.M);
@@ -844,8 +910,9 @@ template <int QT>
 __global__ __launch_bounds__(64) void operand_check_kernel(const uint8_t* W, uint32_t nblocks, float* out) {
   const int l = threadIdx.x, q = l >> 4;
   const uint32_t rbase = blockIdx.x * 16u;
-  WRegs<QT> wr;
-  load_w<1>(wr, W, nblocks, rbase, 0, l);
+  WLoad<QT> wl;
+  load_w<1>(wl, W, nblocks, rbase, 0, l);
+  const auto& wr = w_decode(wl);
   const uint32_t row = rbase + (uint32_t)(l & 15);
   if (row >= nblocks) return;
   float* o = out + (size_t)row * 256;
@@ -892,14 +959,16 @@ bool mm_supported(uint32_t bpr) {
   return bpr == 4 || bpr == 6 || bpr == 8 || bpr == 12 || bpr == 16 || bpr == 24 || bpr == 32 || bpr == 48;
 }
 
-constexpr uint32_t kLdsBytes = 160 * 1024;
-
-// Unrolled walks (NKB > 0) for prebuilt operands: every count of blocks per
-// group the launches take (KG 1: kc 1 .. 6; gate/up, KG 2: 3 or 4; KG 3: 1 or
-// 2); anything else, and rebuilt operands, loops.
-template <int KG, int OPK>
+// Unrolled walks (NKB > 0) for prebuilt operands, where their register sets
+// fit without spilling: KG 1 up to 4 blocks (2 with 64-vector tiles), the
+// gate/up pair's KG 2 over 3 or 4 (3 with 64-vector tiles), KG 3 over 1 or 2
+// (at most 32-vector tiles); anything else, and rebuilt operands, loops.
+template <int KG, int OPK, int NTV>
 constexpr bool nkb_unrolled(int n) {
-  return OPK != 0 && (KG == 1 ? (n >= 1 && n <= 6 && n != 5) : KG == 2 ? (n == 3 || n == 4) : (n == 1 || n == 2));
+  if (OPK == 0) return false;
+  if (KG == 1) return n >= 1 && n <= (NTV <= 2 ? 4 : 2);
+  if (KG == 2) return n == 3 || (n == 4 && NTV <= 2);
+  return NTV <= 2 && (n == 1 || n == 2);
 }
 
 template <int QT, int BPR, int NTV, int MODE, int OPK, int KG>
@@ -908,7 +977,7 @@ void mm_launch_kg(g4_ctx* ctx, const MmArgs& a, uint32_t groups, bool unroll) {
   switch (unroll ? a.kc / KG : 0u) {
 #define G4_MM_NKB(n)                                                                                      \
   case n:                                                                                                 \
-    if constexpr (BPR % (KG * n) == 0 && nkb_unrolled<KG, OPK>(n)) {                                      \
+    if constexpr (BPR % (KG * n) == 0 && nkb_unrolled<KG, OPK, NTV>(n)) {                                 \
       hipLaunchKernelGGL((mmf_kernel<QT, BPR, NTV, MODE, OPK, KG, n>), grid, block, 0, ctx->stream, a); \
       return;                                                                                             \
     }                                                                                                     \
@@ -922,7 +991,11 @@ void mm_launch_kg(g4_ctx* ctx, const MmArgs& a, uint32_t groups, bool unroll) {
     default:
       break;
   }
-  hipLaunchKernelGGL((mmf_kernel<QT, BPR, NTV, MODE, OPK, KG, 0>), grid, block, 0, ctx->stream, a);
+  if constexpr (KG == 3) {  // (three groups only unrolled: the loop's registers spill at 12 waves)
+    mm_launch_kg<QT, BPR, NTV, MODE, OPK, 1>(ctx, a, groups, false);
+  } else {
+    hipLaunchKernelGGL((mmf_kernel<QT, BPR, NTV, MODE, OPK, KG, 0>), grid, block, 0, ctx->stream, a);
+  }
 }
 
 // K groups per workgroup: the gate/up pair (one workgroup per CU, a whole K
@@ -937,14 +1010,12 @@ void mm_launch_kg(g4_ctx* ctx, const MmArgs& a, uint32_t groups, bool unroll) {
 // loop).
 template <int QT, int BPR, int NTV, int MODE, int OPK>
 int mm_launch(g4_ctx* ctx, const MmArgs& a, uint32_t groups) {
-  constexpr uint32_t LB = Ops::bytes(NTV) + 16;
   const uint32_t cus = (uint32_t)(ctx->num_cus > 0 ? ctx->num_cus : 256);
   const bool few = groups * a.ksplit <= cus;
   if (MODE == 1 && a.kc % 2 == 0) {
-    mm_launch_kg<QT, BPR, NTV, MODE, OPK, 2>(ctx, a, groups, few);
-  } else if (few && a.kc % 3 == 0 && 3 * LB <= kLdsBytes) {
-    if constexpr (3 * LB <= kLdsBytes)
-      mm_launch_kg<QT, BPR, NTV, MODE, OPK, 3>(ctx, a, groups, NTV <= 2 || a.kc / 3 <= 2);
+    if constexpr (MODE == 1) mm_launch_kg<QT, BPR, NTV, MODE, OPK, 2>(ctx, a, groups, few);
+  } else if (NTV <= 2 && few && a.kc % 3 == 0 && (a.kc == 3 || a.kc == 6)) {
+    if constexpr (NTV <= 2) mm_launch_kg<QT, BPR, NTV, MODE, OPK, 3>(ctx, a, groups, true);
   } else {
     mm_launch_kg<QT, BPR, NTV, MODE, OPK, 1>(ctx, a, groups, few && (NTV <= 2 || a.kc <= 2));
   }
