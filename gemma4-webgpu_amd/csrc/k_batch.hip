@@ -807,9 +807,11 @@ __device__ __forceinline__ void static_for(F&& f) {
 // with one block in flight.
 template <int QT, int BPR, int NTV, int MODE, int OPK, int KG = 1, int NKB = 0>
 __global__ __launch_bounds__(MNT * KG)
-// (64-vector tiles over copied operands, one group: two waves per SIMD, the
-// batched LM head's occupancy, rather than the one its free allocation gives)
-__attribute__((amdgpu_waves_per_eu(NTV == 4 && OPK == 1 && KG == 1 ? 2 : 1))) void mmf_kernel(MmArgs a) {
+// (the looping walk over copied operands, one group, as the batched LM head
+// takes it: three waves per SIMD with 32-vector tiles, two with 64, rather
+// than the two and one its free allocation gives)
+__attribute__((amdgpu_waves_per_eu(OPK == 1 && KG == 1 && NKB == 0 ? (NTV <= 2 ? 3 : 2) : 1))) void mmf_kernel(
+    MmArgs a) {
   static_assert(OPK != 2 || (QT == 1 && MODE == 0), "sub-block-scaled operands: Q6_K matmuls");
   static_assert(KG >= 1 && KG <= 3, "one to three K groups");
   constexpr uint32_t LB = Ops::bytes(NTV) + 16;  // + the copy's sink slot
