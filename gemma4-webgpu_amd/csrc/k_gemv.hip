@@ -2156,8 +2156,12 @@ template <int BPR> struct MvWaves {
 };
 
 // The workgroup width of a one-vector launch over row segments of
-// 256*bpr-wide rows (the rule stated above kMvFullWgs).
-int mv_pick(uint32_t bpr, const GemvSeg* segs, int nseg) {
+// 256*bpr-wide rows (the rule stated above kMvFullWgs). Between one and two
+// tiles per CU the widest workgroup leaves some CUs two tiles and others
+// one: the next width is taken when its tiles spread evenly enough that the
+// busiest CU streams fewer bytes (e.g. 2 x 12288 rows of 1536: 384 tiles of
+// 12 waves, 128 CUs with two; 512 tiles of 9 waves, two on every CU).
+int mv_pick(uint32_t bpr, const GemvSeg* segs, int nseg, int num_cus) {
   const MvWaveSet w = mv_waves(bpr);
   auto tiles = [&](int nwv) {
     const uint32_t slots = (uint32_t)(16 * nwv) / bpr;  // 64 nwv threads over 4 bpr units per row
@@ -2165,7 +2169,13 @@ int mv_pick(uint32_t bpr, const GemvSeg* segs, int nseg) {
     for (int i = 0; i < nseg; ++i) t += ceil_div(segs[i].M, slots);
     return t;
   };
-  if (tiles(w.A) >= kMvFullWgs) return w.A;
+  const uint32_t cus = (uint32_t)(num_cus > 0 ? num_cus : 256);
+  if (tiles(w.A) >= kMvFullWgs) {
+    const uint32_t ta = tiles(w.A), tb = tiles(w.B);
+    if (ta > cus && tb <= 2 * cus && ceil_div(tb, cus) * (uint32_t)w.B < ceil_div(ta, cus) * (uint32_t)w.A)
+      return w.B;
+    return w.A;
+  }
   if (tiles(w.B) >= kMvFullWgs) return w.B;
   if (tiles(w.C) >= kMvMinWgs) return w.C;
   return w.D;
@@ -2174,7 +2184,7 @@ int mv_pick(uint32_t bpr, const GemvSeg* segs, int nseg) {
 template <int QT, int BPR, int PRO, int NMAT>
 int mv_rows(g4_ctx* ctx, const LaunchReq& q, const uint8_t* w_up) {
   using Wv = MvWaves<BPR>;
-  const int nwv = mv_pick(BPR, q.segs, q.nseg);
+  const int nwv = mv_pick(BPR, q.segs, q.nseg, ctx->num_cus);
   if (nwv == Wv::A) return mv_launch<QT, BPR, Wv::A, PRO, NMAT>(ctx, q, w_up);
   if (nwv == Wv::B) return mv_launch<QT, BPR, Wv::B, PRO, NMAT>(ctx, q, w_up);
   if (nwv == Wv::C) return mv_launch<QT, BPR, Wv::C, PRO, NMAT>(ctx, q, w_up);
@@ -2305,7 +2315,7 @@ struct MvShape {
 MvShape mv_shape(const g4_ctx* ctx, uint32_t M, uint32_t bpr) {
   const GemvSeg seg{nullptr, nullptr, M, 0};
   MvShape s{};
-  s.nwv = mv_pick(bpr, &seg, 1);
+  s.nwv = mv_pick(bpr, &seg, 1, ctx->num_cus);
   s.rows_per_tile = (uint32_t)(16 * s.nwv) / bpr;
   const uint32_t t = ceil_div(M, s.rows_per_tile);
   s.rep = mv_rep(t, ctx->num_cus, s.nwv == 12);  // as mv_launch for one matrix
@@ -2355,7 +2365,7 @@ int qkv_attn(g4_ctx* ctx, const char* fn, bool merge, const float* x, const uint
   // launch, q/k/v staged in the workspace (at most kMaxStage values)
   GemvSegs sg{};
   for (int i = 0; i < nseg; ++i) sg.s[i] = GemvSeg{(const uint8_t*)weights[i], outputs[i], rows[i], 0};
-  const int mnwv = mv_pick(6, sg.s, nseg);
+  const int mnwv = mv_pick(6, sg.s, nseg, ctx->num_cus);
   const uint32_t tr = 16u * (uint32_t)mnwv / 6u;  // rows per tile
   uint32_t nmv = 0;
   for (int i = 0; i < nseg; ++i) {
