@@ -744,8 +744,10 @@ __device__ __forceinline__ void mv_ring_load(const uint8_t* src, uint32_t nbytes
     const uint32_t c0 = (uint32_t)(i * NTH + 64 * w);  // (uniform per wave)
     if (i == R::LPT - 1 && c0 >= R::CH) break;
     const uint32_t off = chunk_off((c0 + (uint32_t)l) * 16u, nbytes);
+    // non-temporal: each weight byte is read once per pass (the amortised
+    // 262144 x 1536 Q4_K matvec: 45-46 -> 39-40 us, 61-63 -> 72-73 % of HBM)
     __builtin_amdgcn_global_load_lds((const void*)(src + off),
-                                     (__attribute__((address_space(3))) void*)(buf + 16u * c0), 16, 0, 0);
+                                     (__attribute__((address_space(3))) void*)(buf + 16u * c0), 16, 0, 2);
   }
 }
 // Loads one tile issues in wave w: R::LPT, or one less where the last
